@@ -1,0 +1,238 @@
+/*
+ * undertow_hip.h -- C ABI of the MI355X (gfx950) backend for undertow's
+ * MTP draft+verify decode step.
+ *
+ * Every entry point is plain C: integer status codes, plain pointers and
+ * sizes.  Pointers named *_dev are device (HBM) addresses; every other
+ * pointer is host memory that is only read (or written) during the call.
+ * Work is enqueued on the context's HIP stream; entry points that return
+ * host-visible results synchronise that stream before returning.
+ *
+ * Each declaration names the reference routine (mohitmishra786/undertow,
+ * Rust) whose semantics it reproduces and whose call site a Rust binding in
+ * undertow-quant / adapters/undertow-deepseek-moe would route through it.
+ *
+ * Threading: a ut_ctx (one HIP stream) belongs to one thread at a time and
+ * is not internally synchronised.  ut_qtensor / ut_expert_table / ut_model
+ * handles are immutable after set-up and may be shared by contexts on the
+ * same device.  Sessions are per thread, like the reference's
+ * InferenceSession (adapters/undertow-deepseek-moe/src/model.rs:407-445).
+ */
+#ifndef UNDERTOW_HIP_H
+#define UNDERTOW_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- status */
+/* Replaces the reference's panics (assert_eq! in QTensor::matmul,
+ * undertow-quant/src/qtensor.rs:283-284) and EngineError variants
+ * (undertow-core/src/error.rs:6-37).  No exception or abort crosses the ABI;
+ * ut_last_error() gives the message of the last failure on a context. */
+enum {
+    UT_OK = 0,
+    UT_ERR_ARG = -1,              /* null handle / pointer, bad enum value */
+    UT_ERR_SHAPE = -2,            /* x / out length does not match the tensor */
+    UT_ERR_FORMAT = -3,           /* payload size matches neither int8 nor int4 */
+    UT_ERR_OOM = -4,              /* device or host allocation failed */
+    UT_ERR_HIP = -5,              /* a HIP runtime call failed */
+    UT_ERR_BAD_EXPERT = -6,       /* expert id out of range or not loaded */
+    UT_ERR_CONTEXT_OVERFLOW = -7, /* EngineError::ContextOverflow */
+    UT_ERR_BAD_TOKEN = -8,        /* token id >= vocab_size */
+    UT_ERR_NOT_FOUND = -9,        /* a required tensor was never set */
+    UT_ERR_STATE = -10            /* call out of order (e.g. no MTP head) */
+};
+
+/* QuantFormat (undertow-quant/src/qtensor.rs:17-21).  UT_FMT_INFER asks
+ * ut_qtensor_upload to deduce int8/int4 from the payload size, as
+ * read_qtensor does (undertow-io/src/reader.rs:421-430). */
+enum { UT_FMT_INFER = -1, UT_FMT_F32 = 0, UT_FMT_INT8 = 1, UT_FMT_INT4 = 2 };
+
+typedef struct ut_ctx ut_ctx;
+typedef struct ut_qtensor ut_qtensor;
+typedef struct ut_expert_table ut_expert_table;
+typedef struct ut_model ut_model;
+typedef struct ut_session ut_session;
+
+/* --------------------------------------------------------------- context */
+/* No reference counterpart (the reference has no device): owns one HIP
+ * stream on `device` and a scratch arena reused across calls. */
+int32_t     ut_ctx_create(int32_t device, ut_ctx **out);
+void        ut_ctx_destroy(ut_ctx *ctx);
+const char *ut_last_error(const ut_ctx *ctx);
+/* Run subsequent work on `stream` (a hipStream_t of the same device, e.g.
+ * torch.cuda.current_stream().cuda_stream); NULL restores the own stream. */
+int32_t     ut_ctx_set_stream(ut_ctx *ctx, void *stream);
+void       *ut_ctx_stream(ut_ctx *ctx);
+int32_t     ut_ctx_synchronize(ut_ctx *ctx);
+/* Per-kernel timing with HIP events on the context stream (bench tooling):
+ * while enabled, every kernel the library launches is bracketed by events;
+ * ut_ctx_kernel_time() reports launches and total milliseconds of the
+ * kernels whose name starts with `prefix`. */
+int32_t     ut_ctx_enable_timing(ut_ctx *ctx, int32_t on);
+int32_t     ut_ctx_kernel_time(ut_ctx *ctx, const char *prefix, int64_t *launches,
+                               double *total_ms);
+
+/* --------------------------------------------------------------- QTensor */
+/* QTensor::from_quantized (undertow-quant/src/qtensor.rs:85-138) /
+ * read_qtensor (undertow-io/src/reader.rs:403-444): copies the payload
+ * (f32 data, int8 codes, or int4 rows of ceil(in/2) bytes, low nibble =
+ * even index) and per-output-row scales to HBM.  Validates payload_len
+ * against QuantFormat::payload_bytes (qtensor.rs:43-49) and
+ * scales_len == out_dim (int formats; ignored for f32). */
+int32_t ut_qtensor_upload(ut_ctx *ctx, int32_t fmt, const void *payload, int64_t payload_len,
+                          const float *scales, int64_t scales_len, int64_t out_dim,
+                          int64_t in_dim, ut_qtensor **out);
+void    ut_qtensor_free(ut_qtensor *qt);
+/* QTensor::format / out_dim / in_dim / nbytes (qtensor.rs:215-248). */
+int32_t ut_qtensor_format(const ut_qtensor *qt);
+int64_t ut_qtensor_out_dim(const ut_qtensor *qt);
+int64_t ut_qtensor_in_dim(const ut_qtensor *qt);
+int64_t ut_qtensor_nbytes(const ut_qtensor *qt);
+/* QTensor::dequantize (qtensor.rs:265-272): out[o,i] = fl(scale[o]*q[o,i])
+ * (bit-exact), f32 tensors copied.  out_dev holds out_dim*in_dim floats. */
+int32_t ut_qtensor_dequantize(ut_ctx *ctx, const ut_qtensor *qt, float *out_dev);
+/* QTensor::matmul(&self, out, x, seq) (qtensor.rs:281-319):
+ * out[s,o] = scale[o] * sum_i x[s,i]*q[o,i], x [seq,in] and out [seq,out]
+ * row-major f32.  x_len / out_len are element counts, checked like the
+ * reference's assert_eq!s.  Each output row's value does not depend on seq
+ * (the reference's "threading never changes numerics"). */
+int32_t ut_qtensor_matmul(ut_ctx *ctx, const ut_qtensor *qt, float *out_dev, int64_t out_len,
+                          const float *x_dev, int64_t x_len, int64_t seq);
+/* QTensor::add_scaled_row (qtensor.rs:516-543): acc[i] += (factor*scale[row])*q[row,i]. */
+int32_t ut_qtensor_add_scaled_row(ut_ctx *ctx, const ut_qtensor *qt, int64_t row, float factor,
+                                  float *acc_dev);
+
+/* ---------------------------------------------------------------- router */
+/* RouterAdapter::route (undertow-core/src/adapter.rs:99-114) as
+ * DeepseekSigmoidRouter::route (adapters/undertow-deepseek-moe/src/
+ * router.rs:58-113) over `rows` rows of gate logits [rows, n_experts]:
+ * sigmoid, + correction bias (bias_dev may be NULL) for selection only,
+ * group limitation by the sum of each group's top-2, top-k by
+ * topk_indices (undertow-core/src/router.rs:136-163, lowest index first on
+ * ties), weights = sigmoid normalised (norm_topk_prob) and scaled.
+ * Writes ids [rows, top_k] int32 and weights [rows, top_k] in choice order. */
+int32_t ut_route(ut_ctx *ctx, const float *logits_dev, const float *bias_dev, int64_t rows,
+                 int64_t n_experts, int32_t top_k, int32_t n_group, int32_t topk_group,
+                 int32_t norm_topk_prob, float routed_scaling_factor, int32_t *ids_dev,
+                 float *weights_dev);
+
+/* ----------------------------------------------------------- expert block */
+/* Device-side counterpart of the expert store (TieredStore::get_expert,
+ * undertow-core/src/store.rs:142-162; ResidentStore :167-229): per expert
+ * the gate/up [inter, hidden] and down [hidden, inter] QTensors.  The table
+ * borrows the QTensor handles; they must outlive it. */
+int32_t ut_expert_table_create(ut_ctx *ctx, int64_t n_experts, int64_t hidden, int64_t inter,
+                               ut_expert_table **out);
+int32_t ut_expert_table_set(ut_expert_table *tbl, int64_t expert, const ut_qtensor *gate,
+                            const ut_qtensor *up, const ut_qtensor *down);
+void    ut_expert_table_free(ut_expert_table *tbl);
+/* The routed-expert body of moe_forward (adapters/undertow-deepseek-moe/
+ * src/model.rs:210-281) for `rows` rows already routed on device:
+ * out[s] = sum_c weights[s,c] * down(silu(gate x_s) * up x_s) over the
+ * choices c in router order (out is overwritten, i.e. starts at zero).
+ * Each unique expert's weights are read once for all rows that chose it.
+ * Experts must all share one format (int4 or int8). */
+int32_t ut_moe_experts(ut_ctx *ctx, const ut_expert_table *tbl, const int32_t *ids_dev,
+                       const float *weights_dev, int64_t rows, int32_t top_k, const float *x_dev,
+                       float *out_dev);
+
+/* ------------------------------------------------------ sample / verify */
+/* argmax (undertow-core/src/sample.rs:353-361) per row: first index of the
+ * maximum; NaN never wins; returns 0 when row[0] is NaN. */
+int32_t ut_argmax_rows(ut_ctx *ctx, const float *logits_dev, int64_t rows, int64_t vocab,
+                       int32_t *idx_dev);
+
+/* ------------------------------------------------------------ attention */
+/* The absorbed score/softmax/context loops of mla_forward_cached
+ * (adapters/undertow-deepseek-moe/src/attention.rs:214-234) for R query
+ * rows x H heads: row s sees n_ctx = pos_base + s + 1 cache positions,
+ * score_t = (qabs.latent_t + q_rope.krot_t) * scale, fp32 softmax,
+ * clat = sum_t p_t latent_t.  qabs [R,H,L], q_rope [R,H,P], latent [T,L],
+ * krot [T,P] (T >= pos_base + R), clat [R,H,L]; all f32. */
+int32_t ut_mla_attend(ut_ctx *ctx, const float *qabs_dev, const float *q_rope_dev,
+                      const float *latent_dev, const float *krot_dev, int64_t R, int64_t H,
+                      int64_t L, int64_t P, int64_t pos_base, float scale, float *clat_dev);
+
+/* ---------------------------------------------------------------- model */
+/* DeepseekConfig fields the forward pass reads (adapters/undertow-deepseek-
+ * moe/src/config.rs:30-85).  q_lora_rank == 0 selects the direct q_proj. */
+typedef struct {
+    int64_t vocab_size, hidden_size, intermediate_size, moe_intermediate_size;
+    int64_t num_hidden_layers, first_k_dense_replace, num_attention_heads;
+    int64_t n_routed_experts, num_experts_per_tok, n_shared_experts;
+    int64_t n_group, topk_group;
+    int32_t norm_topk_prob;
+    float routed_scaling_factor;
+    int64_t q_lora_rank, kv_lora_rank, qk_nope_head_dim, qk_rope_head_dim, v_head_dim;
+    float rms_norm_eps, rope_theta;
+    int32_t mtp;                      /* 1: load the MTP module at layer index num_hidden_layers */
+    int64_t max_position_embeddings;  /* context capacity of a session */
+} ut_model_config;
+
+/* load_model_with (adapters/undertow-deepseek-moe/src/loader.rs:181-302),
+ * split into create / set_tensor / finalize so a host loader streams
+ * tensors straight from its shards.  Tensor names are the checkpoint's
+ * (model.layers.N.self_attn.q_a_proj.weight, ...).  set_tensor takes a 2-D
+ * matrix [d0, d1] in any format (fmt UT_FMT_INFER: int8/int4 from the
+ * payload size, as read_qtensor) or a 1-D f32 vector (d1 == 1 and
+ * scales == NULL).  finalize checks that every tensor the config needs is
+ * present with the right shape (UT_ERR_NOT_FOUND / UT_ERR_SHAPE). */
+int32_t ut_model_create(ut_ctx *ctx, const ut_model_config *cfg, ut_model **out);
+int32_t ut_model_set_tensor(ut_model *m, const char *name, int32_t fmt, const void *payload,
+                            int64_t nbytes, const float *scales, int64_t d0, int64_t d1);
+int32_t ut_model_finalize(ut_model *m);
+/* Benchmark support, no reference counterpart: fills every tensor of the
+ * config on device from a counter-based generator (int4 experts and int8
+ * dense matrices with codes uniform over the format's range and per-row
+ * scales |N(0,std)|/qmax; norms 1 +- 0.1; router gate f32 N(0,std); bias
+ * ramp -0.1..0.1) and finalizes.  expert_fmt / dense_fmt: UT_FMT_INT4 or
+ * UT_FMT_INT8. */
+int32_t ut_model_synthesize(ut_model *m, uint64_t seed, float init_std, int32_t expert_fmt,
+                            int32_t dense_fmt);
+int64_t ut_model_device_bytes(const ut_model *m);
+void    ut_model_free(ut_model *m);
+
+/* InferenceSession (model.rs:407-564).  path: 0 = Auto, 1 = Absorbed,
+ * 2 = Reconstruct (attention.rs:97-103); this backend runs the absorbed
+ * form for every path (the reference's two paths agree to < 1e-4,
+ * attention.rs:362-422). */
+int32_t ut_session_create(ut_model *m, int32_t path, ut_session **out);
+void    ut_session_free(ut_session *s);
+/* InferenceSession::prefill (model.rs:447-547): runs ids[0..n) through the
+ * model, extends the KV cache.  logits_host [n, vocab] may be NULL;
+ * argmax_host [n] (per-row argmax computed on device) may be NULL.
+ * Errors: UT_ERR_ARG (n == 0), UT_ERR_CONTEXT_OVERFLOW, UT_ERR_BAD_TOKEN. */
+int32_t ut_session_prefill(ut_session *s, const int32_t *ids, int64_t n, float *logits_host,
+                           int32_t *argmax_host);
+/* InferenceSession::truncate (model.rs:556-564). */
+int32_t ut_session_truncate(ut_session *s, int64_t len);
+int64_t ut_session_position(const ut_session *s);
+
+/* undertow_core::generate with a greedy sampler (undertow-core/src/
+ * model.rs:139-185) on a fresh session: writes up to max_new tokens to
+ * out, returns the count (< max_new when the context is full) or a
+ * negative status. */
+int64_t ut_generate_greedy(ut_model *m, const int32_t *prompt, int64_t n, int64_t max_new,
+                           int32_t *out);
+/* generate_greedy_mtp -> speculative_loop (adapters/undertow-deepseek-moe/
+ * src/mtp.rs:176-191,263-314) with the native MTP head (draft_logits,
+ * mtp.rs:74-133).  depth 1 is the reference: draft one token, verify
+ * [next, draft] as a 2-row prefill, accept iff argmax(row 0) == draft.
+ * depth 2..3 (no reference counterpart) chains the MTP module on its own
+ * last hidden state, verifies depth+1 rows and accepts the longest matching
+ * prefix; the main KV rolls back to the last verified position and the MTP
+ * module is only fed verified positions, so the output always equals
+ * ut_generate_greedy.  Returns the produced count; drafted / accepted
+ * count draft tokens. */
+int64_t ut_generate_mtp(ut_model *m, const int32_t *prompt, int64_t n, int64_t max_new,
+                        int32_t depth, int32_t *out, int64_t *drafted, int64_t *accepted);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* UNDERTOW_HIP_H */

@@ -1,0 +1,143 @@
+"""QTensor::matmul / dequantize on the GPU vs the CPU oracle.
+
+Bars:
+  - dequantized weights bit-exact: fl(scale * q) (qtensor.rs:265-272);
+  - int formats: bit-exact against the closed form of the GPU arithmetic
+    (tests/qgen.py) -- this pins the digitisation and the dot8/dot4 lanes;
+  - all formats: within the reference's own SIMD-vs-scalar bound,
+    1e-4 * max(|oracle|, 1) (undertow-quant/src/avx512.rs:335-366), of the
+    scalar oracle (kernels.rs:21-81);
+  - a row's value does not depend on seq (qtensor.rs:274-280): bitwise equal
+    for M = 1..5.
+Shapes: the reference's odd SIMD test shapes, BASELINE config-2 expert
+shapes, and the dense projection shapes of configs 1 and 4.
+"""
+import numpy as np
+import pytest
+
+from conftest import dev, host
+from oracle import oracle as O
+from qgen import F32, INT4, INT8, codes, gemv_closed_form, rand_qtensor
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(1, 1), (3, 16), (5, 17), (8, 64), (7, 130), (16, 256), (2, 31),  # avx512.rs:335-366
+          (96, 256), (256, 512), (64, 128), (2048, 7168), (7168, 2048), (192, 96), (1536, 7168)]
+FMTS = [INT4, INT8, F32]
+
+
+def upload(ctx, fmt, payload, scales, o, i):
+    import undertow_amd as U
+    return U.QTensor(ctx, fmt, payload, scales, o, i)
+
+
+def run_matmul(ctx, qt, x):
+    import torch
+    seq, i = x.shape
+    out = torch.full((seq, qt.out_dim), float("nan"), device="cuda:0")
+    xd = dev(x)
+    qt.matmul(out, xd, seq)
+    return host(out)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("o,i", SHAPES)
+def test_matmul_matches_oracle(ctx, fmt, o, i):
+    rng = np.random.default_rng(o * 1000 + i + fmt)
+    payload, scales = rand_qtensor(rng, fmt, o, i)
+    qt = upload(ctx, fmt, payload, scales, o, i)
+    x = rng.standard_normal((3, i)).astype(np.float32)
+    got = run_matmul(ctx, qt, x)
+    want = O.matmul(fmt, payload, scales, o, i, x)
+    assert np.isfinite(got).all()
+    tol = 1e-4 * np.maximum(np.abs(want), 1.0)
+    assert (np.abs(got - want) <= tol).all(), np.abs(got - want).max()
+    if fmt != F32:
+        exact = gemv_closed_form(fmt, payload, scales, o, i, x)
+        assert np.array_equal(got, exact)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("o,i", [(2048, 7168), (7168, 2048), (130, 64), (5, 17)])
+def test_rows_do_not_depend_on_seq(ctx, fmt, o, i):
+    rng = np.random.default_rng(7)
+    payload, scales = rand_qtensor(rng, fmt, o, i)
+    qt = upload(ctx, fmt, payload, scales, o, i)
+    x = rng.standard_normal((5, i)).astype(np.float32)
+    full = run_matmul(ctx, qt, x)
+    for m in range(1, 6):
+        part = run_matmul(ctx, qt, x[:m])
+        assert np.array_equal(part, full[:m]), m
+    for s in range(5):
+        assert np.array_equal(run_matmul(ctx, qt, x[s:s + 1])[0], full[s])
+
+
+@pytest.mark.parametrize("fmt", [INT4, INT8, F32])
+@pytest.mark.parametrize("o,i", [(5, 17), (2048, 7168), (33, 96)])
+def test_dequantize_bit_exact(ctx, fmt, o, i):
+    rng = np.random.default_rng(11)
+    payload, scales = rand_qtensor(rng, fmt, o, i)
+    qt = upload(ctx, fmt, payload, scales, o, i)
+    got = host(qt.dequantize())
+    want = O.dequantize(fmt, payload, scales, o, i)
+    assert np.array_equal(got, want)
+    if fmt != F32:
+        closed = (scales[:, None] * codes(fmt, payload, o, i).astype(np.float32)).astype(np.float32)
+        assert np.array_equal(got, closed)
+
+
+def test_oracle_quantized_checkpoint_tensors(ctx):
+    """Weights produced by the restated quantizer (qtensor.rs:142-213)."""
+    rng = np.random.default_rng(3)
+    w = rng.standard_normal((96, 256)).astype(np.float32) * 0.05
+    x = rng.standard_normal((2, 256)).astype(np.float32)
+    for fmt in (INT8, INT4):
+        q, s = O.quantize(w, fmt)
+        qt = upload(ctx, fmt, q, s, 96, 256)
+        got = run_matmul(ctx, qt, x)
+        want = O.matmul(fmt, q, s, 96, 256, x)
+        assert np.abs(got - want).max() <= 1e-5
+
+
+def test_zero_and_extreme_rows(ctx):
+    o, i = 64, 256
+    rng = np.random.default_rng(5)
+    payload, scales = rand_qtensor(rng, INT4, o, i)
+    qt = upload(ctx, INT4, payload, scales, o, i)
+    x = np.zeros((4, i), np.float32)
+    x[1, 3] = 1e-30                      # a tiny row
+    x[2] = rng.standard_normal(i) * 3e4  # a large row
+    x[3, :] = rng.standard_normal(i)
+    x[3, 0] = 1e6                        # one dominant element
+    got = run_matmul(ctx, qt, x)
+    assert (got[0] == 0).all()
+    want = O.matmul(INT4, payload, scales, o, i, x)
+    assert np.array_equal(got, gemv_closed_form(INT4, payload, scales, o, i, x))
+    assert (np.abs(got - want) <= 1e-4 * np.maximum(np.abs(want), 1e-30)).all()
+
+
+def test_non_finite_activation_gives_nan(ctx):
+    o, i = 16, 64
+    rng = np.random.default_rng(6)
+    payload, scales = rand_qtensor(rng, INT8, o, i)
+    qt = upload(ctx, INT8, payload, scales, o, i)
+    x = rng.standard_normal((2, i)).astype(np.float32)
+    x[1, 5] = np.inf
+    got = run_matmul(ctx, qt, x)
+    assert np.isfinite(got[0]).all() and np.isnan(got[1]).all()
+
+
+def test_shape_mismatch_raises(ctx):
+    import torch
+    import undertow_amd as U
+    rng = np.random.default_rng(1)
+    payload, scales = rand_qtensor(rng, INT4, 8, 64)
+    qt = upload(ctx, INT4, payload, scales, 8, 64)
+    x = torch.zeros(2 * 63, device="cuda:0")
+    out = torch.zeros(2 * 8, device="cuda:0")
+    with pytest.raises(U.ShapeError):
+        qt.matmul(out, x, 2)
+    with pytest.raises(U.UtError):
+        U.QTensor(ctx, INT4, payload[:, :-1], scales, 8, 64)  # payload size mismatch
+    q = U.QTensor(ctx, U.INFER, payload, scales, 8, 64)
+    assert q.format == INT4

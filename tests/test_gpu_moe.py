@@ -1,0 +1,188 @@
+"""Router top-k, routed-expert block, argmax and MLA attention on the GPU vs the oracle.
+
+Bars: top-k indices and argmax bit-exact whenever the
+top-2 gap exceeds 1e-3; expert outputs within 1e-4 * max(|oracle|, 1)
+(the reference's SIMD-vs-scalar bound, avx512.rs:335-366); attention within
+1e-5 of the oracle's sequential f32 loops.
+"""
+import numpy as np
+import pytest
+
+from conftest import dev, host
+from oracle import oracle as O
+from qgen import F32, INT4, INT8, rand_qtensor
+
+pytestmark = pytest.mark.gpu
+
+
+# ------------------------------------------------------------------ router
+@pytest.mark.parametrize("E,k,ng,tg", [(256, 8, 8, 4), (8, 2, 4, 2), (16, 4, 4, 2), (64, 6, 1, 1),
+                                       (8, 2, 1, 1), (4, 2, 4, 2)])
+@pytest.mark.parametrize("bias", [False, True])
+def test_route_matches_oracle(ctx, E, k, ng, tg, bias):
+    import undertow_amd as U
+    rng = np.random.default_rng(E * 10 + k)
+    rows = 9
+    logits = rng.standard_normal((rows, E)).astype(np.float32)
+    b = (-0.1 + 0.2 * np.arange(E) / max(E - 1, 1)).astype(np.float32) if bias else None
+    ids, w = U.route(ctx, dev(logits), None if b is None else dev(b), k, ng, tg, True, 2.5)
+    ids, w = host(ids), host(w)
+    for r in range(rows):
+        oid, ow = O.route(logits[r], b, k, ng, tg, True, 2.5)
+        assert ids[r].tolist() == oid.tolist()
+        assert np.abs(w[r] - ow).max() <= 1e-6
+
+
+def test_route_reference_kats(ctx):
+    """router.rs:132-186 restated: group limitation picks [0, 6, 1, 7]."""
+    import undertow_amd as U
+    logits = np.array([[2.0, 1.9, 3.0, -5.0, -1.0, -1.0, 2.0, 1.8]], np.float32)
+    ids, _ = U.route(ctx, dev(logits), None, 4, 4, 2, False, 1.0)
+    assert host(ids)[0].tolist() == [0, 6, 1, 7]
+    ids, w = U.route(ctx, dev(np.array([[1.0, 0.0, 0.9]], np.float32)),
+                     dev(np.array([0, 0, 0.5], np.float32)), 1, 1, 1, False, 1.0)
+    assert host(ids)[0].tolist() == [2]
+    assert abs(host(w)[0, 0] - 1 / (1 + np.exp(-0.9))) < 1e-6
+
+
+def test_route_ties_pick_lowest_index(ctx):
+    import undertow_amd as U
+    logits = np.zeros((1, 32), np.float32)
+    ids, _ = U.route(ctx, dev(logits), None, 8, 1, 1, True, 1.0)
+    assert host(ids)[0].tolist() == list(range(8))
+
+
+# ------------------------------------------------------------------ argmax
+def test_argmax_rows(ctx):
+    import undertow_amd as U
+    rng = np.random.default_rng(2)
+    rows = [rng.standard_normal(129280).astype(np.float32) for _ in range(3)]
+    rows.append(np.array([np.nan, 5.0, 1.0] + [0.0] * 61, np.float32))
+    rows.append(np.array([1.0, np.nan, 2.0, 2.0] + [-np.inf] * 60, np.float32))
+    t = np.full((3, 129280), -np.inf, np.float32)
+    t[0, 77] = 3.0
+    t[0, 99999] = 3.0  # tie: first index wins
+    t[1, :] = np.nan
+    t[1, 0] = 0.5      # v[0] finite, rest NaN -> 0
+    t[2, 129279] = 1.0
+    for r in rows[:3]:
+        got = host(U.argmax_rows(ctx, dev(r[None])))[0]
+        assert got == O.argmax(r)
+    for r in rows[3:]:
+        assert host(U.argmax_rows(ctx, dev(r[None])))[0] == O.argmax(r)
+    got = host(U.argmax_rows(ctx, dev(t)))
+    assert got.tolist() == [O.argmax(t[i]) for i in range(3)] == [77, 0, 129279]
+
+
+# ------------------------------------------------------------- expert block
+def make_experts(ctx, rng, fmt, E, H, I):
+    import undertow_amd as U
+    tbl = U.ExpertTable(ctx, E, H, I)
+    host_w = []
+    for e in range(E):
+        g = rand_qtensor(rng, fmt, I, H)
+        u = rand_qtensor(rng, fmt, I, H)
+        d = rand_qtensor(rng, fmt, H, I)
+        tbl.set(e, U.QTensor(ctx, fmt, *g, I, H), U.QTensor(ctx, fmt, *u, I, H),
+                U.QTensor(ctx, fmt, *d, H, I))
+        host_w.append((g, u, d))
+    return tbl, host_w
+
+
+def oracle_moe(fmt, H, I, host_w, ids, w, x):
+    E = len(host_w)
+
+    def payload(j):
+        return np.concatenate([np.asarray(hw[j][0]).reshape(-1).view(np.uint8) for hw in host_w])
+
+    def scales(j, rows):
+        if fmt == F32:
+            return np.zeros(E * rows, np.float32)
+        return np.concatenate([np.asarray(hw[j][1]).reshape(-1) for hw in host_w])
+
+    return O.moe_experts(fmt, H, I, payload(0), scales(0, I), payload(1), scales(1, I),
+                         payload(2), scales(2, H), ids.astype(np.int64), w, x)
+
+
+@pytest.mark.parametrize("fmt", [INT4, INT8])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 6])
+def test_moe_experts_small(ctx, fmt, M):
+    rng = np.random.default_rng(40 + M + fmt)
+    E, H, I, k = 8, 256, 128, 2
+    tbl, host_w = make_experts(ctx, rng, fmt, E, H, I)
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(M)]).astype(np.int32)
+    ids[0] = [3, 5]
+    if M > 1:
+        ids[1] = [5, 0]  # shared expert across rows
+    w = rng.random((M, k)).astype(np.float32)
+    x = rng.standard_normal((M, H)).astype(np.float32)
+    got = host(tbl.moe_experts(dev(ids), dev(w), dev(x)))
+    want = oracle_moe(fmt, H, I, host_w, ids, w, x)
+    tol = 1e-4 * np.maximum(np.abs(want), 1.0)
+    assert (np.abs(got - want) <= tol).all(), np.abs(got - want).max()
+    # per-row values do not depend on the other rows
+    for s in range(M):
+        one = host(tbl.moe_experts(dev(ids[s:s + 1]), dev(w[s:s + 1]), dev(x[s:s + 1])))
+        assert np.array_equal(one[0], got[s])
+
+
+def test_moe_experts_f32_weights(ctx):
+    import undertow_amd as U
+    rng = np.random.default_rng(9)
+    E, H, I, k, M = 4, 64, 32, 2, 2
+    tbl, host_w = make_experts(ctx, rng, F32, E, H, I)
+    ids = np.array([[1, 3], [3, 0]], np.int32)
+    w = rng.random((M, k)).astype(np.float32)
+    x = rng.standard_normal((M, H)).astype(np.float32)
+    got = host(tbl.moe_experts(dev(ids), dev(w), dev(x)))
+    want = oracle_moe(F32, H, I, host_w, ids, w, x)
+    assert np.abs(got - want).max() <= 1e-5 * max(1.0, np.abs(want).max())
+
+
+def test_moe_experts_deepseek_shape(ctx):
+    """hidden 7168, inter 2048, top-8 of 16 loaded experts."""
+    rng = np.random.default_rng(1234)
+    E, H, I, k = 16, 7168, 2048, 8
+    tbl, host_w = make_experts(ctx, rng, INT4, E, H, I)
+    for M in (1, 2, 4):
+        ids = np.stack([rng.permutation(E)[:k] for _ in range(M)]).astype(np.int32)
+        w = rng.random((M, k)).astype(np.float32)
+        x = rng.standard_normal((M, H)).astype(np.float32)
+        got = host(tbl.moe_experts(dev(ids), dev(w), dev(x)))
+        want = oracle_moe(INT4, H, I, host_w, ids, w, x)
+        tol = 1e-4 * np.maximum(np.abs(want), 1.0)
+        assert (np.abs(got - want) <= tol).all(), (M, np.abs(got - want).max())
+
+
+def test_moe_bad_expert_is_reported(ctx):
+    import undertow_amd as U
+    rng = np.random.default_rng(3)
+    tbl, _ = make_experts(ctx, rng, INT8, 4, 64, 32)
+    ids = np.array([[1, 9]], np.int32)
+    with pytest.raises(U.UtError) as ei:
+        tbl.moe_experts(dev(ids), dev(np.ones((1, 2), np.float32)),
+                        dev(np.ones((1, 64), np.float32)))
+    assert ei.value.code == U.runtime.UT_ERR_BAD_EXPERT
+
+
+# --------------------------------------------------------------- attention
+@pytest.mark.parametrize("R,H,L,P,T", [(1, 4, 64, 16, 5), (2, 4, 64, 16, 40), (4, 8, 16, 8, 300),
+                                       (2, 128, 512, 64, 1024), (1, 128, 512, 64, 600),
+                                       (3, 6, 32, 8, 17)])
+def test_mla_attend_matches_oracle(ctx, R, H, L, P, T):
+    import undertow_amd as U
+    rng = np.random.default_rng(R * 100 + T)
+    qabs = rng.standard_normal((R, H, L)).astype(np.float32)
+    qr = rng.standard_normal((R, H, P)).astype(np.float32)
+    lat = rng.standard_normal((T, L)).astype(np.float32)
+    kr = rng.standard_normal((T, P)).astype(np.float32)
+    pos_base = T - R
+    scale = float(1 / np.sqrt(192.0))
+    got = host(U.mla_attend(ctx, dev(qabs), dev(qr), dev(lat), dev(kr), pos_base, scale))
+    want = O.mla_attend(qabs, qr, lat, kr, pos_base, scale)
+    assert np.abs(got - want).max() <= 1e-5 * max(1.0, np.abs(want).max())
+    # row independence: row s alone at pos_base + s sees the same context
+    for s in range(R):
+        one = host(U.mla_attend(ctx, dev(qabs[s:s + 1]), dev(qr[s:s + 1]), dev(lat), dev(kr),
+                                pos_base + s, scale))
+        assert np.array_equal(one[0], got[s])

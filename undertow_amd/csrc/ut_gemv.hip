@@ -1,0 +1,349 @@
+// ut_gemv.hip -- QTensor::matmul on gfx950 (undertow-quant/src/qtensor.rs:
+// 281-493 and the kernels it dispatches to, kernels.rs:21-81 /
+// avx512.rs:197-267): activation digitisation, the fast skinny GEMV
+// (int4 / int8 / f32 weights, 1..4 activation rows per pass) and a generic
+// kernel for shapes the fast one does not take.
+#include "ut_gemv_core.h"
+#include "ut_moe.h"
+
+namespace ut {
+
+// ------------------------------------------------------- digitisation ---
+size_t xdigits_bytes(int64_t M, int64_t K, int flags) {
+    size_t b = ((size_t)M * 4 + 255) & ~size_t(255);
+    int64_t K8 = (K + 7) / 8, K4 = (K + 3) / 4;
+    if (flags & XD_DIG4) b += (((size_t)M * 6 * K8 * 4) + 255) & ~size_t(255);
+    if (flags & XD_DIG8) b += (((size_t)M * 3 * K4 * 4) + 255) & ~size_t(255);
+    if (flags & XD_XT) b += (((size_t)M * K * 4) + 255) & ~size_t(255);
+    return b;
+}
+
+XDigits xdigits_view(void *base, int64_t M, int64_t K, int flags) {
+    XDigits d;
+    d.M = M;
+    d.K = K;
+    char *p = (char *)base;
+    d.exps = (int32_t *)p;
+    p += ((size_t)M * 4 + 255) & ~size_t(255);
+    int64_t K8 = (K + 7) / 8, K4 = (K + 3) / 4;
+    if (flags & XD_DIG4) { d.dig4 = (uint32_t *)p; p += (((size_t)M * 6 * K8 * 4) + 255) & ~size_t(255); }
+    if (flags & XD_DIG8) { d.dig8 = (uint32_t *)p; p += (((size_t)M * 3 * K4 * 4) + 255) & ~size_t(255); }
+    if (flags & XD_XT) { d.xt = (int32_t *)p; }
+    return d;
+}
+
+int xdigit_flags_for(int32_t fmt, int64_t K) {
+    if (fmt == UT_FMT_INT4) return (K % 32 == 0) ? XD_DIG4 : XD_XT;
+    if (fmt == UT_FMT_INT8) return (K % 16 == 0) ? XD_DIG8 : XD_XT;
+    return 0;
+}
+
+// One workgroup per activation row.  x~ = rint(x * 2^(22-E)) with
+// max|x| < 2^E (frexp), so |x~| <= 2^22 and six balanced base-16 digits
+// (or three base-256 digits) represent it exactly.
+__global__ __launch_bounds__(256) void k_digitize(const float *__restrict__ x, int64_t ldx,
+                                                  int64_t K, const uint32_t *__restrict__ rowmax,
+                                                  int32_t nparts, int32_t *__restrict__ exps,
+                                                  uint32_t *__restrict__ dig4,
+                                                  uint32_t *__restrict__ dig8,
+                                                  int32_t *__restrict__ xt,
+                                                  const int32_t *__restrict__ slot_count,
+                                                  int rows_per_slot) {
+    const int64_t m = blockIdx.x;
+    if (slot_count && (int)(m / rows_per_slot) >= *slot_count) return;
+    const float *xr = x + m * ldx;
+    __shared__ uint32_t red[256];
+    uint32_t mx = 0;
+    if (rowmax) {
+        for (int i = threadIdx.x; i < nparts; i += 256) mx = max(mx, rowmax[m * nparts + i]);
+    } else {
+        for (int64_t k = threadIdx.x; k < K; k += 256) mx = max(mx, __float_as_uint(fabsf(xr[k])));
+    }
+    red[threadIdx.x] = mx;
+    __syncthreads();
+    for (int off = 128; off > 0; off >>= 1) {
+        if (threadIdx.x < off) red[threadIdx.x] = max(red[threadIdx.x], red[threadIdx.x + off]);
+        __syncthreads();
+    }
+    mx = red[0];
+    // non-finite rows (|x| bits >= +inf) produce NaN outputs downstream
+    const bool bad = mx >= 0x7f800000u;
+    int E = 0;
+    if (!bad && mx != 0) (void)frexpf(__uint_as_float(mx), &E);
+    const int sh = 22 - E;
+    if (threadIdx.x == 0) exps[m] = bad ? INT32_MIN : E - 22;
+    auto xq = [&](int64_t k) -> int32_t {
+        if (bad || k >= K) return 0;
+        return (int32_t)rintf(ldexpf(xr[k], sh));
+    };
+    if (dig4) {
+        const int64_t K8 = (K + 7) / 8;
+        for (int64_t c = threadIdx.x; c < K8; c += 256) {
+            uint32_t w[6] = {0, 0, 0, 0, 0, 0};
+            for (int j = 0; j < 8; j++) {
+                int32_t v = xq(8 * c + j);
+#pragma unroll
+                for (int p = 0; p < 6; p++) {
+                    int32_t d = ((v + 8) & 15) - 8;  // balanced digit in [-8, 7]
+                    v = (v - d) >> 4;
+                    w[p] |= (uint32_t)(d & 15) << (4 * j);
+                }
+            }
+#pragma unroll
+            for (int p = 0; p < 6; p++) dig4[(m * 6 + p) * K8 + c] = w[p];
+        }
+    }
+    if (dig8) {
+        const int64_t K4 = (K + 3) / 4;
+        for (int64_t c = threadIdx.x; c < K4; c += 256) {
+            uint32_t w[3] = {0, 0, 0};
+            for (int j = 0; j < 4; j++) {
+                int32_t v = xq(4 * c + j);
+#pragma unroll
+                for (int p = 0; p < 3; p++) {
+                    int32_t d = ((v + 128) & 255) - 128;  // balanced digit in [-128, 127]
+                    v = (v - d) >> 8;
+                    w[p] |= (uint32_t)(d & 255) << (8 * j);
+                }
+            }
+#pragma unroll
+            for (int p = 0; p < 3; p++) dig8[(m * 3 + p) * K4 + c] = w[p];
+        }
+    }
+    if (xt) {
+        for (int64_t k = threadIdx.x; k < K; k += 256) xt[m * K + k] = xq(k);
+    }
+}
+
+int32_t launch_digitize(ut_ctx *ctx, const float *x, int64_t ldx, int64_t M, int64_t K,
+                        const uint32_t *rowmax_bits, XDigits xd, int flags) {
+    return launch_digitize_parts(ctx, x, ldx, M, K, rowmax_bits, 1, xd, flags);
+}
+
+int32_t launch_digitize_parts(ut_ctx *ctx, const float *x, int64_t ldx, int64_t M, int64_t K,
+                              const uint32_t *rowmax_parts, int32_t nparts, XDigits xd,
+                              int flags) {
+    return launch_digitize_slots(ctx, x, ldx, M, K, rowmax_parts, nparts, xd, flags, nullptr, 1);
+}
+
+int32_t launch_digitize_slots(ut_ctx *ctx, const float *x, int64_t ldx, int64_t M, int64_t K,
+                              const uint32_t *rowmax_parts, int32_t nparts, XDigits xd,
+                              int flags, const int32_t *slot_count, int rows_per_slot) {
+    if (M <= 0) return UT_OK;
+    int tok = timing_begin(ctx, "digitize");
+    hipLaunchKernelGGL(k_digitize, dim3((unsigned)M), dim3(256), 0, ctx->stream, x, ldx, K,
+                       rowmax_parts, nparts, xd.exps, (flags & XD_DIG4) ? xd.dig4 : nullptr,
+                       (flags & XD_DIG8) ? xd.dig8 : nullptr, (flags & XD_XT) ? xd.xt : nullptr,
+                       slot_count, rows_per_slot);
+    timing_end(ctx, tok);
+    return launch_check(ctx, "k_digitize");
+}
+
+// --------------------------------------------------------- fast GEMV ---
+struct PlainArgs {
+    const uint8_t *w;
+    const float *scales;
+    int64_t O, K, row_bytes;
+    XSrc x;
+    const int32_t *exps;
+    float *out;
+    int64_t ldo;
+    int accumulate;
+};
+
+// 64 output rows per workgroup: wave w, row group g, slot r -> row
+// blockIdx.x*64 + w*16 + g*4 + r.
+template <int FMT, int M>
+__global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
+    __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
+    const int64_t row0 = (int64_t)blockIdx.x * 64 + wave * 16 + g * 4;
+    const uint8_t *rows[kGemvRows];
+#pragma unroll
+    for (int r = 0; r < kGemvRows; r++) {
+        int64_t row = row0 + r < a.O ? row0 + r : a.O - 1;
+        rows[r] = a.w + row * a.row_bytes;
+    }
+    CoreOut<FMT, M> res;
+    gemv_core<FMT, M>(rows, a.K, a.x, lds, res);
+#pragma unroll
+    for (int r = 0; r < kGemvRows; r++)
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            const int64_t row = row0 + r;
+            if (s == 4 * r + m && row < a.O) {
+                float v = core_value<FMT, M>(res, r, m, a.exps, a.scales, row);
+                float *o = a.out + m * a.ldo + row;
+                *o = a.accumulate ? __fadd_rn(*o, v) : v;
+            }
+        }
+}
+
+// ------------------------------------------------------ generic GEMV ---
+// One wave per output row; any K and alignment.  Integer formats sum
+// x~ * q exactly (so the result equals the fast kernel's bit for bit);
+// f32 sums in a fixed lane order.
+__global__ __launch_bounds__(64) void k_gemv_generic(int32_t fmt, const uint8_t *__restrict__ w,
+                                                     const float *__restrict__ scales, int64_t O,
+                                                     int64_t K, int64_t row_bytes,
+                                                     const int32_t *__restrict__ xt,
+                                                     const int32_t *__restrict__ exps,
+                                                     const float *__restrict__ xf, int64_t ldx,
+                                                     int64_t M, float *__restrict__ out,
+                                                     int64_t ldo, int accumulate) {
+    const int64_t row = blockIdx.x;
+    const int lane = threadIdx.x;
+    const uint8_t *wr = w + row * row_bytes;
+    for (int64_t m = 0; m < M; m++) {
+        float v;
+        if (fmt == UT_FMT_F32) {
+            float acc = 0.0f;
+            for (int64_t k = lane; k < K; k += 64)
+                acc = __builtin_fmaf(((const float *)wr)[k], xf[m * ldx + k], acc);
+            for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+            v = __shfl(acc, 0, 64);
+        } else {
+            int64_t S = 0;
+            for (int64_t k = lane; k < K; k += 64) {
+                int q;
+                if (fmt == UT_FMT_INT8) q = (int8_t)wr[k];
+                else {
+                    uint8_t b = wr[k >> 1];
+                    int nib = (k & 1) ? (b >> 4) : (b & 0xF);
+                    q = (nib ^ 8) - 8;
+                }
+                S += (int64_t)xt[m * K + k] * q;
+            }
+            for (int off = 32; off >= 1; off >>= 1) {
+                int lo = __shfl_xor((int)(uint32_t)(uint64_t)S, off, 64);
+                int hi = __shfl_xor((int)(uint32_t)((uint64_t)S >> 32), off, 64);
+                S += (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint64_t)(uint32_t)lo);
+            }
+            v = int_total_to_f32(S, exps[m], scales[row]);
+        }
+        if (lane == 0) {
+            float *o = out + m * ldo + row;
+            *o = accumulate ? __fadd_rn(*o, v) : v;
+        }
+    }
+}
+
+static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+// Whether the fast kernel takes this weight (16-byte aligned rows).
+static bool fast_ok(const ut_qtensor *w) {
+    if (!aligned16(w->payload)) return false;
+    if (w->fmt == UT_FMT_INT4) return w->in_dim % 32 == 0;
+    if (w->fmt == UT_FMT_INT8) return w->in_dim % 16 == 0;
+    return w->in_dim % 4 == 0;
+}
+
+template <int FMT>
+static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrows) {
+    const ut_qtensor *w = ga.w;
+    PlainArgs a;
+    a.w = (const uint8_t *)w->payload;
+    a.scales = w->scales;
+    a.O = w->out_dim;
+    a.K = w->in_dim;
+    a.row_bytes = w->row_bytes;
+    a.out = ga.out + m0 * ga.ldo;
+    a.ldo = ga.ldo;
+    a.accumulate = ga.accumulate;
+    if constexpr (FMT == UT_FMT_F32) {
+        a.x.xf = ga.xf + m0 * w->in_dim;
+        a.x.ldx = w->in_dim;
+        a.x.dig = nullptr;
+        a.x.KW = 0;
+        a.exps = nullptr;
+        if (!aligned16(a.x.xf)) return UT_ERR_ARG;
+    } else {
+        constexpr int PL = FmtTraits<FMT>::kPlanes;
+        const int64_t KW = (w->in_dim + FmtTraits<FMT>::kColsPerWord - 1) / FmtTraits<FMT>::kColsPerWord;
+        a.x.dig = (FMT == UT_FMT_INT4 ? ga.xd.dig4 : ga.xd.dig8) + m0 * PL * KW;
+        a.x.KW = KW;
+        a.x.xf = nullptr;
+        a.x.ldx = 0;
+        a.exps = ga.xd.exps + m0;
+    }
+    dim3 grid((unsigned)((w->out_dim + 63) / 64));
+    const char *name = FMT == UT_FMT_INT4 ? "gemv_int4" : FMT == UT_FMT_INT8 ? "gemv_int8" : "gemv_f32";
+    int tok = timing_begin(ctx, name);
+    switch (mrows) {
+    case 1: hipLaunchKernelGGL((k_gemv<FMT, 1>), grid, dim3(kGemvThreads), 0, ctx->stream, a); break;
+    case 2: hipLaunchKernelGGL((k_gemv<FMT, 2>), grid, dim3(kGemvThreads), 0, ctx->stream, a); break;
+    case 3: hipLaunchKernelGGL((k_gemv<FMT, 3>), grid, dim3(kGemvThreads), 0, ctx->stream, a); break;
+    default: hipLaunchKernelGGL((k_gemv<FMT, 4>), grid, dim3(kGemvThreads), 0, ctx->stream, a); break;
+    }
+    timing_end(ctx, tok);
+    return launch_check(ctx, name);
+}
+
+int32_t gemv(ut_ctx *ctx, const GemvArgs &ga) {
+    const ut_qtensor *w = ga.w;
+    if (ga.M <= 0) return UT_OK;
+    if (fast_ok(w) && (w->fmt == UT_FMT_F32 ? aligned16(ga.xf) && (w->in_dim % 4 == 0) : true)) {
+        for (int64_t m0 = 0; m0 < ga.M; m0 += 4) {
+            int mrows = (int)((ga.M - m0) < 4 ? (ga.M - m0) : 4);
+            int32_t rc;
+            if (w->fmt == UT_FMT_INT4) rc = launch_fast<UT_FMT_INT4>(ctx, ga, m0, mrows);
+            else if (w->fmt == UT_FMT_INT8) rc = launch_fast<UT_FMT_INT8>(ctx, ga, m0, mrows);
+            else rc = launch_fast<UT_FMT_F32>(ctx, ga, m0, mrows);
+            if (rc) return rc;
+        }
+        return UT_OK;
+    }
+    if (w->fmt != UT_FMT_F32 && !ga.xd.xt) {
+        set_error(ctx, "generic GEMV needs x~ (XD_XT) digits");
+        return UT_ERR_ARG;
+    }
+    int tok = timing_begin(ctx, "gemv_generic");
+    hipLaunchKernelGGL(k_gemv_generic, dim3((unsigned)w->out_dim), dim3(64), 0, ctx->stream, w->fmt,
+                       (const uint8_t *)w->payload, w->scales, w->out_dim, w->in_dim, w->row_bytes,
+                       ga.xd.xt, ga.xd.exps, ga.xf, w->in_dim, ga.M, ga.out, ga.ldo, ga.accumulate);
+    timing_end(ctx, tok);
+    return launch_check(ctx, "k_gemv_generic");
+}
+
+}  // namespace ut
+
+using namespace ut;
+
+extern "C" int32_t ut_qtensor_matmul(ut_ctx *ctx, const ut_qtensor *qt, float *out_dev,
+                                     int64_t out_len, const float *x_dev, int64_t x_len,
+                                     int64_t seq) {
+    if (!ctx || !qt || !out_dev || !x_dev || seq < 0) {
+        set_error(ctx, "ut_qtensor_matmul: bad argument");
+        return UT_ERR_ARG;
+    }
+    // the reference's assert_eq!s (qtensor.rs:283-284)
+    if (x_len != seq * qt->in_dim) {
+        set_error(ctx, "x shape: %lld != %lld*%lld", (long long)x_len, (long long)seq,
+                  (long long)qt->in_dim);
+        return UT_ERR_SHAPE;
+    }
+    if (out_len != seq * qt->out_dim) {
+        set_error(ctx, "out shape: %lld != %lld*%lld", (long long)out_len, (long long)seq,
+                  (long long)qt->out_dim);
+        return UT_ERR_SHAPE;
+    }
+    if (seq == 0) return UT_OK;
+    GemvArgs ga;
+    ga.w = qt;
+    ga.M = seq;
+    ga.out = out_dev;
+    ga.ldo = qt->out_dim;
+    if (qt->fmt == UT_FMT_F32) {
+        ga.xf = x_dev;
+        return gemv(ctx, ga);
+    }
+    int flags = xdigit_flags_for(qt->fmt, qt->in_dim);
+    if (!fast_ok(qt)) flags = XD_XT;
+    ScratchPlan plan;
+    plan.add(xdigits_bytes(seq, qt->in_dim, flags));
+    std::vector<void *> ptrs;
+    UT_TRY(scratch_acquire(ctx, plan, ptrs));
+    ga.xd = xdigits_view(ptrs[0], seq, qt->in_dim, flags);
+    UT_TRY(launch_digitize(ctx, x_dev, qt->in_dim, seq, qt->in_dim, nullptr, ga.xd, flags));
+    return gemv(ctx, ga);
+}

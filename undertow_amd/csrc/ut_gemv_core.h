@@ -1,0 +1,225 @@
+// ut_gemv_core.h -- device core of the quantized skinny GEMV on gfx950.
+//
+// Work split of one 256-thread workgroup (4 waves of 64 lanes):
+//   lane l of a wave: row group g = l >> 4 (0..3), sub-lane s = l & 15.
+//   Each lane owns R = 4 weight rows (caller-chosen row pointers) and walks
+//   K in steps; per step the 16 sub-lanes of a row group read 16
+//   consecutive 16-byte pieces of each of its rows (a 256-byte coalesced
+//   run per row per load instruction: 128-bit nibble / byte / float loads).
+//   Activations for a K chunk are staged once per workgroup in LDS and read
+//   back with 128-bit LDS loads, each reused across the lane's 4 rows.
+//
+// Arithmetic:
+//   int4: v_dot8c_i32_i4 of the raw weight word (8 signed nibbles, low
+//         nibble = even column, exactly the checkpoint's packing) with one
+//         word of balanced base-16 activation digits; 6 digit planes.
+//   int8: v_dot4c_i32_i8 of 4 weight bytes with base-256 digits; 3 planes.
+//   The per-plane int32 sums are exact; the lane total
+//   S = sum_p acc_p * base^p is formed in int64 and summed across the 16
+//   sub-lanes exactly.  The weights are never dequantized to floats: the
+//   per-row scale is applied once, out = fl(fl(S * 2^e) * scale[row]),
+//   the same formula for every tiling, row count and reduction order.
+//   f32:  fused multiply-add in a fixed order per lane, then a fixed
+//         butterfly; the value for (row slot r, activation row m) is always
+//         read from sub-lane 4*r + m, so it does not depend on M.
+#pragma once
+
+#include "ut_internal.h"
+
+namespace ut {
+
+constexpr int kGemvThreads = 256;
+constexpr int kGemvRows = 4;         // weight rows per lane
+constexpr int kLdsWords = 6144;      // 24 KiB of staged activations per WG
+
+template <int FMT> struct FmtTraits;
+template <> struct FmtTraits<UT_FMT_INT4> {
+    static constexpr int kPlanes = 6;       // digit planes of x~
+    static constexpr int kColsPerWord = 8;  // columns per 32-bit digit word
+    static constexpr int kStepCols = 512;   // 16 lanes x 32 columns
+    static constexpr int kBytesPerCol2 = 1; // 2 * bytes per column
+};
+template <> struct FmtTraits<UT_FMT_INT8> {
+    static constexpr int kPlanes = 3;
+    static constexpr int kColsPerWord = 4;
+    static constexpr int kStepCols = 256;   // 16 lanes x 16 columns
+    static constexpr int kBytesPerCol2 = 2;
+};
+template <> struct FmtTraits<UT_FMT_F32> {
+    static constexpr int kPlanes = 1;       // the f32 value itself
+    static constexpr int kColsPerWord = 1;
+    static constexpr int kStepCols = 64;    // 16 lanes x 4 columns
+    static constexpr int kBytesPerCol2 = 8;
+};
+
+// Columns of one staged chunk: as many as fit kLdsWords for M rows.
+template <int FMT, int M>
+__host__ __device__ constexpr int gemv_chunk_cols() {
+    using T = FmtTraits<FMT>;
+    // words per column per row = planes / cols_per_word
+    int cols = kLdsWords * T::kColsPerWord / (M * T::kPlanes);
+    return cols / T::kStepCols * T::kStepCols;
+}
+
+// Activations of one GEMV: digits (int formats) or f32 values.
+struct XSrc {
+    const uint32_t *dig;  // [M][planes][KW] words (int formats)
+    int64_t KW;           // words per plane row
+    const float *xf;      // [M][ldx] (f32)
+    int64_t ldx;
+};
+
+__device__ inline int64_t shfl_xor_i64(int64_t v, int off) {
+    int lo = __shfl_xor((int)(uint32_t)(uint64_t)v, off, 16);
+    int hi = __shfl_xor((int)(uint32_t)((uint64_t)v >> 32), off, 16);
+    return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint64_t)(uint32_t)lo);
+}
+
+// Result of the core for lane (g, s): the totals of every (r, m), identical
+// on all 16 sub-lanes for int formats; for f32 read them from sub-lane 4r+m.
+template <int FMT, int M> struct CoreOut {
+    int64_t S[kGemvRows][M];
+    float F[kGemvRows][M];
+};
+
+// rows[r]: byte pointer of row r (already clamped to a valid row).
+// K: columns (K % (2*16/bytes) alignment is the caller's contract: int4
+// K % 32 == 0, int8 K % 16 == 0, f32 K % 4 == 0, rows 16-byte aligned).
+template <int FMT, int M>
+__device__ __forceinline__ void gemv_core(const uint8_t *const rows[kGemvRows], int64_t K,
+                                          const XSrc &x, uint32_t *lds, CoreOut<FMT, M> &res) {
+    using T = FmtTraits<FMT>;
+    constexpr int KC = gemv_chunk_cols<FMT, M>();
+    constexpr int PL = T::kPlanes;
+    constexpr int LANE_COLS = T::kStepCols / 16;              // columns per lane per step
+    const int tid = threadIdx.x;
+    const int s = tid & 15;
+
+    int32_t acc[kGemvRows][M][PL];
+    float facc[kGemvRows][M];
+#pragma unroll
+    for (int r = 0; r < kGemvRows; r++)
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            facc[r][m] = 0.0f;
+#pragma unroll
+            for (int p = 0; p < PL; p++) acc[r][m][p] = 0;
+        }
+
+    for (int64_t kc = 0; kc < K; kc += KC) {
+        const int kcn = (int)((K - kc) < KC ? (K - kc) : KC);
+        __syncthreads();
+        // ---- stage the chunk's activations
+        if constexpr (FMT == UT_FMT_F32) {
+            const int n4 = kcn / 4;  // float4 per row
+            for (int i = tid; i < M * n4; i += kGemvThreads) {
+                int m = i / n4, c = i - m * n4;
+                float4 v = *(const float4 *)(x.xf + m * x.ldx + kc + 4 * c);
+                *(float4 *)(lds + m * KC + 4 * c) = *(const float4 *)&v;
+            }
+        } else {
+            const int wpr = kcn / T::kColsPerWord;   // words per plane row in the chunk
+            const int n4 = wpr / 4;
+            const int64_t w0 = kc / T::kColsPerWord;
+            constexpr int LW = KC / T::kColsPerWord;  // LDS words per plane row
+            for (int i = tid; i < M * PL * n4; i += kGemvThreads) {
+                int mp = i / n4, c = i - mp * n4;
+                uint4 v = *(const uint4 *)(x.dig + (int64_t)mp * x.KW + w0 + 4 * c);
+                *(uint4 *)(lds + mp * LW + 4 * c) = v;
+            }
+        }
+        __syncthreads();
+        // ---- stream the weights
+        for (int c0 = s * LANE_COLS; c0 < kcn; c0 += T::kStepCols) {
+            uint4 wv[kGemvRows];
+            const int64_t boff = (kc + c0) * T::kBytesPerCol2 / 2;
+#pragma unroll
+            for (int r = 0; r < kGemvRows; r++) wv[r] = *(const uint4 *)(rows[r] + boff);
+            if constexpr (FMT == UT_FMT_F32) {
+#pragma unroll
+                for (int m = 0; m < M; m++) {
+                    const float4 xv = *(const float4 *)(lds + m * KC + c0);
+#pragma unroll
+                    for (int r = 0; r < kGemvRows; r++) {
+                        const float4 wf = *(const float4 *)&wv[r];
+                        float a = facc[r][m];
+                        a = __builtin_fmaf(wf.x, xv.x, a);
+                        a = __builtin_fmaf(wf.y, xv.y, a);
+                        a = __builtin_fmaf(wf.z, xv.z, a);
+                        a = __builtin_fmaf(wf.w, xv.w, a);
+                        facc[r][m] = a;
+                    }
+                }
+            } else {
+                constexpr int LW = KC / T::kColsPerWord;
+                const int wc = c0 / T::kColsPerWord;  // first word of this lane's columns
+#pragma unroll
+                for (int m = 0; m < M; m++) {
+#pragma unroll
+                    for (int p = 0; p < PL; p++) {
+                        const uint4 xv = *(const uint4 *)(lds + (m * PL + p) * LW + wc);
+#pragma unroll
+                        for (int r = 0; r < kGemvRows; r++) {
+                            int a = acc[r][m][p];
+                            if constexpr (FMT == UT_FMT_INT4) {
+                                a = __builtin_amdgcn_sdot8((int)wv[r].x, (int)xv.x, a, false);
+                                a = __builtin_amdgcn_sdot8((int)wv[r].y, (int)xv.y, a, false);
+                                a = __builtin_amdgcn_sdot8((int)wv[r].z, (int)xv.z, a, false);
+                                a = __builtin_amdgcn_sdot8((int)wv[r].w, (int)xv.w, a, false);
+                            } else {
+                                a = __builtin_amdgcn_sdot4((int)wv[r].x, (int)xv.x, a, false);
+                                a = __builtin_amdgcn_sdot4((int)wv[r].y, (int)xv.y, a, false);
+                                a = __builtin_amdgcn_sdot4((int)wv[r].z, (int)xv.z, a, false);
+                                a = __builtin_amdgcn_sdot4((int)wv[r].w, (int)xv.w, a, false);
+                            }
+                            acc[r][m][p] = a;
+                        }
+                    }
+                }
+            }
+        }
+    }
+
+    // ---- reduce across the 16 sub-lanes of the row group
+#pragma unroll
+    for (int r = 0; r < kGemvRows; r++)
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            if constexpr (FMT == UT_FMT_F32) {
+                float v = facc[r][m];
+#pragma unroll
+                for (int off = 8; off >= 1; off >>= 1) v += __shfl_xor(v, off, 16);
+                res.F[r][m] = v;
+                res.S[r][m] = 0;
+            } else {
+                constexpr int SH = FMT == UT_FMT_INT4 ? 4 : 8;
+                int64_t t = 0;
+#pragma unroll
+                for (int p = PL - 1; p >= 0; p--) t = t * (1 << SH) + (int64_t)acc[r][m][p];
+#pragma unroll
+                for (int off = 8; off >= 1; off >>= 1) t += shfl_xor_i64(t, off);
+                res.S[r][m] = t;
+                res.F[r][m] = 0.0f;
+            }
+        }
+}
+
+// Converts an exact integer total to the reference's f32 row value:
+// fl(fl(S * 2^e) * scale).  e == INT32_MIN marks a non-finite activation row.
+__device__ __forceinline__ float int_total_to_f32(int64_t S, int32_t e, float scale) {
+    if (e == INT32_MIN) return __int_as_float(0x7fc00000);
+    float v = (float)ldexp((double)S, e);
+    return __fmul_rn(v, scale);
+}
+
+// Value of (r, m) from the core result: for f32 read sub-lane 4r+m (callers
+// run this on that lane), for int formats every sub-lane holds it.
+template <int FMT, int M>
+__device__ __forceinline__ float core_value(const CoreOut<FMT, M> &res, int r, int m,
+                                            const int32_t *exps, const float *scales,
+                                            int64_t row) {
+    if constexpr (FMT == UT_FMT_F32) return res.F[r][m];
+    else return int_total_to_f32(res.S[r][m], exps[m], scales[row]);
+}
+
+}  // namespace ut

@@ -1,0 +1,157 @@
+// ut_internal.h -- shared host/device definitions of the gfx950 backend.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+#include <vector>
+
+#include "../../include/undertow_hip.h"
+
+namespace ut {
+
+// ------------------------------------------------------------- errors ---
+// Failures are reported as status codes; the message is kept on the ctx.
+void set_error(ut_ctx *ctx, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+
+#define UT_CHECK_HIP(ctx, expr)                                                     \
+    do {                                                                            \
+        hipError_t e_ = (expr);                                                     \
+        if (e_ != hipSuccess) {                                                     \
+            ::ut::set_error((ctx), "%s failed: %s (%s:%d)", #expr,                 \
+                            hipGetErrorString(e_), __FILE__, __LINE__);             \
+            return UT_ERR_HIP;                                                      \
+        }                                                                           \
+    } while (0)
+
+#define UT_TRY(expr)                    \
+    do {                                \
+        int32_t rc_ = (expr);           \
+        if (rc_ != UT_OK) return rc_;   \
+    } while (0)
+
+// ------------------------------------------------------------ context ---
+struct KernelStat {
+    std::string name;
+    int64_t launches = 0;
+    double total_ms = 0.0;
+};
+
+struct PendingTiming {
+    int stat;
+    hipEvent_t start, stop;
+};
+
+struct DeviceBuffer {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+};
+
+}  // namespace ut
+
+struct ut_ctx {
+    int device = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    std::string err;
+    // Scratch arena: one device allocation, carved per call.  All work runs
+    // on one stream, so a later call may reuse what an earlier one used.
+    ut::DeviceBuffer scratch;
+    // Pinned host staging for small device->host results.
+    void *pinned = nullptr;
+    size_t pinned_bytes = 0;
+    // Kernel timing (bench tooling).
+    bool timing = false;
+    std::vector<ut::KernelStat> stats;
+    std::vector<ut::PendingTiming> pending;
+    int multiprocessors = 256;
+};
+
+struct ut_qtensor {
+    int32_t fmt = UT_FMT_F32;
+    int64_t out_dim = 0, in_dim = 0;
+    int64_t row_bytes = 0;     // payload bytes per output row
+    void *payload = nullptr;   // device
+    float *scales = nullptr;   // device, out_dim floats (int formats)
+    bool owns = true;          // false: views into a model arena
+    int device = 0;
+};
+
+namespace ut {
+
+// Scratch carving: returns device pointers into ctx->scratch, growing it
+// (after a stream sync) when needed.  Each carve is 256-byte aligned.
+struct ScratchPlan {
+    std::vector<size_t> sizes;
+    size_t add(size_t bytes) {
+        sizes.push_back((bytes + 255) & ~size_t(255));
+        return sizes.size() - 1;
+    }
+};
+int32_t scratch_acquire(ut_ctx *ctx, const ScratchPlan &plan, std::vector<void *> &ptrs);
+int32_t pinned_acquire(ut_ctx *ctx, size_t bytes, void **ptr);
+
+// Kernel timing hooks: call timing_begin before a launch and timing_end
+// after it; both are no-ops unless timing is enabled on the ctx.
+int timing_begin(ut_ctx *ctx, const char *name);
+void timing_end(ut_ctx *ctx, int token);
+int32_t launch_check(ut_ctx *ctx, const char *name);
+
+int64_t payload_bytes(int32_t fmt, int64_t out_dim, int64_t in_dim);
+
+// ---------------------------------------------------- activation digits ---
+// Integer form of an f32 activation row used by the quantized GEMVs:
+//   x~[k] = rint(x[k] * 2^(22 - E)),  E = exponent with max|x| < 2^E,
+// so |x~| <= 2^22.  The quantized products then accumulate exactly in
+// integers: S = sum_k x~[k] q[k], and out = fl(fl(S * 2^(E-22)) * scale).
+// The same S results for any tiling, reduction order or row count.
+//
+// Layout of one digitised batch (rows m < M, K columns, K8 = ceil(K/8),
+// K4 = ceil(K/4)):
+//   exps  [M]            int32: E - 22 (INT32_MIN when the row is non-finite)
+//   dig4  [M][6][K8]     uint32: balanced base-16 digits d_p in [-8,7] of x~,
+//                        nibble j of word c8 = digit of column 8*c8 + j
+//   dig8  [M][3][K4]     uint32: balanced base-256 digits in [-128,127],
+//                        byte j of word c4 = digit of column 4*c4 + j
+//   xt    [M][K]         int32: x~ itself (generic kernels)
+struct XDigits {
+    int32_t *exps = nullptr;
+    uint32_t *dig4 = nullptr;
+    uint32_t *dig8 = nullptr;
+    int32_t *xt = nullptr;
+    int64_t M = 0, K = 0;
+};
+enum { XD_DIG4 = 1, XD_DIG8 = 2, XD_XT = 4 };
+size_t xdigits_bytes(int64_t M, int64_t K, int flags);
+// Carves an XDigits view out of `base` (device memory of xdigits_bytes()).
+XDigits xdigits_view(void *base, int64_t M, int64_t K, int flags);
+// Digitise x [M, K] (row stride ldx floats).  rowmax_bits: optional
+// precomputed max|x| per row (float bits, as atomicMax'd by a producer).
+int32_t launch_digitize(ut_ctx *ctx, const float *x, int64_t ldx, int64_t M, int64_t K,
+                        const uint32_t *rowmax_bits, XDigits xd, int flags);
+// Same with the row maxima given as nparts partial maxima per row
+// ([M][nparts] float bits), reduced by the kernel.
+int32_t launch_digitize_parts(ut_ctx *ctx, const float *x, int64_t ldx, int64_t M, int64_t K,
+                              const uint32_t *rowmax_parts, int32_t nparts, XDigits xd,
+                              int flags);
+
+// Flags a GEMV needs for a weight of this format and shape.
+int xdigit_flags_for(int32_t fmt, int64_t K);
+
+// ---------------------------------------------------------- GEMV core ---
+// out[m, o] (row stride ldo) for one quantized matrix, all rows o < O.
+// x is given digitised (int formats) or as f32 (fmt F32).
+struct GemvArgs {
+    const ut_qtensor *w = nullptr;
+    const float *xf = nullptr;  // f32 activations [M, K] (F32 weights)
+    XDigits xd;                 // digitised activations (int weights)
+    int64_t M = 0;
+    float *out = nullptr;
+    int64_t ldo = 0;
+    int accumulate = 0;         // out += result instead of out = result
+};
+int32_t gemv(ut_ctx *ctx, const GemvArgs &a);
+
+}  // namespace ut

@@ -1,0 +1,70 @@
+// ut_moe.h -- internal interface of the expert block and router kernels.
+#pragma once
+
+#include "ut_internal.h"
+
+namespace ut {
+
+// Device arrays of per-expert pointers (indexed by expert id).
+struct ExpertPtrs {
+    const uint8_t *const *gate_w = nullptr;
+    const uint8_t *const *up_w = nullptr;
+    const uint8_t *const *down_w = nullptr;
+    const float *const *gate_s = nullptr;
+    const float *const *up_s = nullptr;
+    const float *const *down_s = nullptr;
+};
+
+struct MoePlan {
+    int32_t *count;        // number of slots used
+    int32_t *uniq;         // [slots] expert id per slot
+    int32_t *choice_slot;  // [M*k] slot of each (row, choice), -1 when invalid
+};
+
+// One pass of the expert block over M <= 4 rows (all on device).
+struct MoeCall {
+    int fmt = UT_FMT_INT4;
+    ExpertPtrs tbl;
+    int64_t E = 0, H = 0, I = 0;
+    int M = 1, k = 1;
+    const int32_t *ids = nullptr;      // [M, k]
+    const float *weights = nullptr;    // [M, k]
+    const float *x = nullptr;          // [M, H]
+    const XDigits *x_digits = nullptr; // optional: x already digitised
+    float *out = nullptr;              // [M, ldo]
+    int64_t ldo = 0;
+    int accumulate = 0;
+    int extra_slot = -1;  // >= 0: expert id always appended as the last slot, added with weight 1
+    int32_t *err_flag = nullptr;
+};
+
+struct ScratchLayout {
+    size_t total = 0;
+    size_t count = 0, uniq = 0, choice = 0, xd = 0, h = 0, hmax = 0, hd = 0, d = 0;
+    int xflags = 0, hflags = 0;
+    int64_t ntiles = 0;
+};
+
+inline int64_t moe_slots(int M, int64_t k, int64_t E, int extra) {
+    int64_t s = (int64_t)M * k;
+    if (s > E) s = E;
+    return s + (extra >= 0 ? 1 : 0);
+}
+ScratchLayout moe_layout(int64_t M, int64_t k, int64_t slots, int64_t H, int64_t I, int fmt);
+size_t moe_scratch_bytes(int64_t M, int64_t k, int64_t slots, int64_t H, int64_t I, int fmt);
+bool moe_shape_ok(int fmt, int64_t H, int64_t I);
+// scratch: device memory of moe_layout(...).total bytes for this call's
+// (M, k, slots); slots from moe_slots().
+int32_t moe_pass(ut_ctx *ctx, const MoeCall &c, void *scratch);
+
+int32_t launch_route(ut_ctx *ctx, const float *logits, const float *bias, int64_t rows,
+                     int64_t E, int32_t k, int32_t n_group, int32_t topk_group, int32_t norm,
+                     float scale, int32_t *ids, float *weights);
+
+// Digitise rows of x in slot groups of rows_per_slot rows; groups at or past
+// *slot_count are skipped.
+int32_t launch_digitize_slots(ut_ctx *ctx, const float *x, int64_t ldx, int64_t M, int64_t K,
+                              const uint32_t *rowmax_parts, int32_t nparts, XDigits xd,
+                              int flags, const int32_t *slot_count, int rows_per_slot);
+
+}  // namespace ut

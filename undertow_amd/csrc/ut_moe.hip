@@ -1,0 +1,590 @@
+// ut_moe.hip -- the routed-expert block of moe_forward on gfx950
+// (adapters/undertow-deepseek-moe/src/model.rs:195-286) and the DeepSeek
+// sigmoid router (router.rs:58-113, undertow-core/src/router.rs:136-163).
+//
+// One pass over M <= 4 token rows:
+//   k_route        one workgroup per row: sigmoid, bias, group limitation,
+//                  top-k by rank (value desc, lowest index first), weights
+//   k_moe_plan     unique experts in first-appearance order -> slots
+//   k_digitize     activation digits of x (shared by every expert)
+//   k_moe_gate_up  grid (I/32, slots): gate and up rows of one expert in the
+//                  same lanes, h = silu(g)*u written per (slot, row), plus
+//                  per-workgroup max|h| partials
+//   k_digitize     digits of h per (slot, row)
+//   k_moe_down     grid (H/64, slots): d = down(h) per (slot, row)
+//   k_moe_combine  out[s] = sum_c w[s,c]*d[slot(s,c), s] in router order
+// Every expert's weights are read once per pass whatever rows chose it;
+// the row dimension rides along in the same instructions.
+#include "ut_gemv_core.h"
+#include "ut_moe.h"
+
+namespace ut {
+
+// ------------------------------------------------------------- router ---
+__device__ __forceinline__ bool ranks_before(float a, int ia, float b, int ib) {
+    // `a` precedes `b` in topk_indices order: larger value, or equal value
+    // and lower index.
+    return a > b || (a == b && ia < ib);
+}
+
+__global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
+                                               const float *__restrict__ bias, int E, int k,
+                                               int n_group, int topk_group, int norm,
+                                               float scale, int32_t *__restrict__ ids,
+                                               float *__restrict__ weights) {
+    extern __shared__ float sm[];
+    float *sc = sm;           // sigmoid scores
+    float *corr = sm + E;     // corrected (selection) scores, then masked
+    float *gsc = sm + 2 * E;  // group scores
+    __shared__ int s_ids[64];
+    __shared__ int s_group_ok[64];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const float *lg = logits + (int64_t)row * E;
+    if (tid < 64) s_ids[tid] = 0;
+    for (int e = tid; e < E; e += blockDim.x) {
+        float s = 1.0f / (1.0f + expf(-lg[e]));  // sigmoid (undertow-quant/src/lib.rs:116)
+        sc[e] = s;
+        corr[e] = bias ? __fadd_rn(s, bias[e]) : s;
+    }
+    __syncthreads();
+    const bool limit = n_group > 1 && topk_group < n_group;
+    if (limit) {
+        const int gs = E / n_group;
+        // group score = sum of the group's top-2 (in topk order: best first)
+        for (int g = tid; g < n_group; g += blockDim.x) {
+            const float *v = corr + g * gs;
+            int b0 = 0;
+            for (int i = 1; i < gs; i++) if (v[i] > v[b0]) b0 = i;
+            float s = 0.0f + v[b0];
+            if (gs > 1) {
+                int b1 = b0 == 0 ? 1 : 0;
+                for (int i = 0; i < gs; i++)
+                    if (i != b0 && ranks_before(v[i], i, v[b1], b1)) b1 = i;
+                s = s + v[b1];
+            }
+            gsc[g] = s;
+        }
+        __syncthreads();
+        for (int g = tid; g < n_group; g += blockDim.x) {
+            int rank = 0;
+            for (int j = 0; j < n_group; j++) rank += ranks_before(gsc[j], j, gsc[g], g);
+            s_group_ok[g] = rank < topk_group;
+        }
+        __syncthreads();
+        for (int e = tid; e < E; e += blockDim.x) {
+            int g = e / gs;
+            bool ok = g < n_group && s_group_ok[g];
+            if (!ok) corr[e] = -INFINITY;
+        }
+        __syncthreads();
+    }
+    const int keff = k < E ? k : E;
+    for (int e = tid; e < E; e += blockDim.x) {
+        const float v = corr[e];
+        int rank = 0;
+        for (int j = 0; j < E; j++) rank += ranks_before(corr[j], j, v, e);
+        if (rank < keff) s_ids[rank] = e;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float w[64];
+        float denom = 0.0f;
+        for (int j = 0; j < keff; j++) { w[j] = sc[s_ids[j]]; denom = denom + w[j]; }
+        denom = denom + 1e-20f;
+        for (int j = 0; j < keff; j++) {
+            float v = norm ? w[j] / denom : w[j];
+            ids[(int64_t)row * k + j] = s_ids[j];
+            weights[(int64_t)row * k + j] = __fmul_rn(v, scale);
+        }
+        for (int j = keff; j < k; j++) {  // k > E: no expert (contributes nothing)
+            ids[(int64_t)row * k + j] = -1;
+            weights[(int64_t)row * k + j] = 0.0f;
+        }
+    }
+}
+
+int32_t launch_route(ut_ctx *ctx, const float *logits, const float *bias, int64_t rows,
+                     int64_t E, int32_t k, int32_t n_group, int32_t topk_group, int32_t norm,
+                     float scale, int32_t *ids, float *weights) {
+    if (rows <= 0) return UT_OK;
+    size_t shmem = (size_t)(2 * E + (n_group > 0 ? n_group : 1)) * sizeof(float);
+    int tok = timing_begin(ctx, "route");
+    hipLaunchKernelGGL(k_route, dim3((unsigned)rows), dim3(256), shmem, ctx->stream, logits, bias,
+                       (int)E, (int)k, (int)n_group, (int)topk_group, (int)norm, scale, ids,
+                       weights);
+    timing_end(ctx, tok);
+    return launch_check(ctx, "k_route");
+}
+
+// --------------------------------------------------------------- plan ---
+// Slots in first-appearance order over (row, choice) -- the order in which
+// moe_forward groups rows by expert (model.rs:219-233).  Invalid ids (out of
+// range or not loaded) set the sticky error flag and contribute nothing.
+__global__ void k_moe_plan(const int32_t *__restrict__ ids, int M, int k, int E,
+                           const uint8_t *const *__restrict__ gate_tbl, int extra_slot,
+                           MoePlan plan, int32_t *__restrict__ err_flag) {
+    if (threadIdx.x != 0) return;
+    int U = 0;
+    for (int s = 0; s < M; s++) {
+        for (int c = 0; c < k; c++) {
+            int e = ids[s * k + c];
+            int slot = -1;
+            if (e < 0 || e >= E || gate_tbl[e] == nullptr) {
+                if (e != -1 && err_flag) *err_flag = 1;
+            } else {
+                for (int u = 0; u < U; u++)
+                    if (plan.uniq[u] == e) { slot = u; break; }
+                if (slot < 0) { slot = U; plan.uniq[U++] = e; }
+            }
+            plan.choice_slot[s * k + c] = slot;
+        }
+    }
+    if (extra_slot >= 0) plan.uniq[U++] = extra_slot;  // a dense MLP run as one more slot
+    *plan.count = U;
+}
+
+// --------------------------------------------------------- gate / up ---
+struct GateUpArgs {
+    ExpertPtrs tbl;
+    const int32_t *uniq;
+    const int32_t *count;
+    int64_t H, I, row_bytes;  // gate/up are [I, H]
+    XSrc x;                   // digits (or f32) of x, shared by all slots
+    const int32_t *exps;
+    float *h;                 // [slots][M][I]
+    uint32_t *hmax_parts;     // [slots][M][ntiles] float bits
+    int ntiles;
+};
+
+// 32 h-rows per workgroup: wave w, row group g -> h rows o = tile*32 +
+// w*8 + g*2 + j (j = 0, 1); slots r = j read gate row o, r = 2 + j up row o.
+template <int FMT, int M>
+__global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up(GateUpArgs a) {
+    const int u = blockIdx.y;
+    if (u >= *a.count) return;
+    __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
+    __shared__ uint32_t wg_max[4];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
+    if (tid < 4) wg_max[tid] = 0;
+    const int e = a.uniq[u];
+    const uint8_t *gw = a.tbl.gate_w[e], *uw = a.tbl.up_w[e];
+    const float *gsc = a.tbl.gate_s[e], *usc = a.tbl.up_s[e];
+    const int64_t obase = (int64_t)blockIdx.x * 32 + wave * 8 + g * 2;
+    const uint8_t *rows[kGemvRows];
+#pragma unroll
+    for (int r = 0; r < kGemvRows; r++) {
+        int64_t o = obase + (r & 1);
+        if (o >= a.I) o = a.I - 1;
+        rows[r] = (r < 2 ? gw : uw) + o * a.row_bytes;
+    }
+    CoreOut<FMT, M> res;
+    gemv_core<FMT, M>(rows, a.H, a.x, lds, res);
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            const int64_t o = obase + j;
+            // f32: gate value lives on sub-lane 4j+m, up value on 4(2+j)+m
+            float gv, uv;
+            if constexpr (FMT == UT_FMT_F32) {
+                float up_here = res.F[2 + j][m];
+                uv = __shfl(up_here, (lane & ~15) | (4 * (2 + j) + m), 64);
+                gv = res.F[j][m];
+            }
+            if (s == 4 * j + m && o < a.I) {
+                if constexpr (FMT != UT_FMT_F32) {
+                    gv = int_total_to_f32(res.S[j][m], a.exps[m], gsc[o]);
+                    uv = int_total_to_f32(res.S[2 + j][m], a.exps[m], usc[o]);
+                }
+                // silu(g) * u (undertow-quant/src/lib.rs:121; model.rs:241-247)
+                float sg = gv / (1.0f + expf(-gv));
+                float hv = __fmul_rn(sg, uv);
+                a.h[((int64_t)u * M + m) * a.I + o] = hv;
+                atomicMax(&wg_max[m], __float_as_uint(fabsf(hv)));
+            }
+        }
+    __syncthreads();
+    if (tid < M) a.hmax_parts[((int64_t)u * M + tid) * a.ntiles + blockIdx.x] = wg_max[tid];
+}
+
+// --------------------------------------------------------------- down ---
+struct DownArgs {
+    ExpertPtrs tbl;
+    const int32_t *uniq;
+    const int32_t *count;
+    int64_t H, I, row_bytes;  // down is [H, I]
+    XSrc x;                   // digits of h: slot u's rows start at u*M
+    int64_t x_slot_stride;    // words (or floats) between slots
+    const int32_t *exps;      // [slots*M]
+    float *d;                 // [slots][M][H]
+};
+
+template <int FMT, int M>
+__global__ __launch_bounds__(kGemvThreads) void k_moe_down(DownArgs a) {
+    const int u = blockIdx.y;
+    if (u >= *a.count) return;
+    __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
+    const int e = a.uniq[u];
+    const uint8_t *dw = a.tbl.down_w[e];
+    const float *dsc = a.tbl.down_s[e];
+    const int64_t row0 = (int64_t)blockIdx.x * 64 + wave * 16 + g * 4;
+    const uint8_t *rows[kGemvRows];
+#pragma unroll
+    for (int r = 0; r < kGemvRows; r++) {
+        int64_t o = row0 + r < a.H ? row0 + r : a.H - 1;
+        rows[r] = dw + o * a.row_bytes;
+    }
+    XSrc xs = a.x;
+    if constexpr (FMT == UT_FMT_F32) xs.xf = a.x.xf + u * a.x_slot_stride;
+    else xs.dig = a.x.dig + u * a.x_slot_stride;
+    CoreOut<FMT, M> res;
+    gemv_core<FMT, M>(rows, a.I, xs, lds, res);
+#pragma unroll
+    for (int r = 0; r < kGemvRows; r++)
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            const int64_t o = row0 + r;
+            if (s == 4 * r + m && o < a.H) {
+                float v = core_value<FMT, M>(res, r, m, a.exps + u * M, dsc, o);
+                a.d[((int64_t)u * M + m) * a.H + o] = v;
+            }
+        }
+}
+
+// ------------------------------------------------------------ combine ---
+// out[s, o] = sum_c w[s,c] * d[slot(s,c), s, o], in router choice order from
+// zero (model.rs:268-281: moe_out starts zeroed; the reference adds
+// w*d per choice).  extra >= 0: then += d[extra, s, o] (a dense MLP slot,
+// MlpWeights::forward_add, model.rs:282-284).  accumulate: out += result.
+__global__ void k_moe_combine(const int32_t *__restrict__ choice_slot,
+                              const float *__restrict__ weights, const float *__restrict__ d,
+                              int M, int k, int64_t H, const int32_t *__restrict__ count,
+                              int extra, float *__restrict__ out, int64_t ldo, int accumulate) {
+    const int s = blockIdx.y;
+    const int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (o >= H) return;
+    float acc = 0.0f;
+    for (int c = 0; c < k; c++) {
+        int slot = choice_slot[s * k + c];
+        if (slot < 0) continue;
+        acc = __fadd_rn(acc, __fmul_rn(weights[s * k + c], d[((int64_t)slot * M + s) * H + o]));
+    }
+    if (extra) {
+        int slot = *count - 1;
+        acc = __fadd_rn(acc, d[((int64_t)slot * M + s) * H + o]);
+    }
+    float *po = out + s * ldo + o;
+    *po = accumulate ? __fadd_rn(*po, acc) : acc;
+}
+
+// ------------------------------------------------------------- driver ---
+size_t moe_scratch_bytes(int64_t M, int64_t k, int64_t slots, int64_t H, int64_t I, int fmt) {
+    ScratchLayout L = moe_layout(M, k, slots, H, I, fmt);
+    return L.total;
+}
+
+ScratchLayout moe_layout(int64_t M, int64_t k, int64_t slots, int64_t H, int64_t I, int fmt) {
+    ScratchLayout L;
+    auto take = [&](size_t bytes) { size_t off = L.total; L.total += (bytes + 255) & ~size_t(255); return off; };
+    const int xflags = fmt == UT_FMT_F32 ? 0 : xdigit_flags_for(fmt, H);
+    const int hflags = fmt == UT_FMT_F32 ? 0 : xdigit_flags_for(fmt, I);
+    const int64_t ntiles = (I + 31) / 32;
+    L.count = take(4);
+    L.uniq = take((size_t)slots * 4);
+    L.choice = take((size_t)M * k * 4);
+    L.xd = take(fmt == UT_FMT_F32 ? 0 : xdigits_bytes(M, H, xflags));
+    L.h = take((size_t)slots * M * I * 4);
+    L.hmax = take((size_t)slots * M * ntiles * 4);
+    L.hd = take(fmt == UT_FMT_F32 ? 0 : xdigits_bytes(slots * M, I, hflags));
+    L.d = take((size_t)slots * M * H * 4);
+    L.xflags = xflags;
+    L.hflags = hflags;
+    L.ntiles = ntiles;
+    return L;
+}
+
+template <int FMT, int M>
+static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L, char *base,
+                          int64_t slots) {
+    MoePlan plan;
+    plan.count = (int32_t *)(base + L.count);
+    plan.uniq = (int32_t *)(base + L.uniq);
+    plan.choice_slot = (int32_t *)(base + L.choice);
+    int tok = timing_begin(ctx, "moe_plan");
+    hipLaunchKernelGGL(k_moe_plan, dim3(1), dim3(64), 0, ctx->stream, c.ids, M, c.k, (int)c.E,
+                       c.tbl.gate_w, c.extra_slot, plan, c.err_flag);
+    timing_end(ctx, tok);
+    UT_TRY(launch_check(ctx, "k_moe_plan"));
+
+    XSrc xs{};
+    const int32_t *xexps = nullptr;
+    if constexpr (FMT == UT_FMT_F32) {
+        xs.xf = c.x;
+        xs.ldx = c.H;
+    } else {
+        XDigits xd = xdigits_view(base + L.xd, M, c.H, L.xflags);
+        if (c.x_digits) xd = *c.x_digits;  // caller already digitised x
+        else UT_TRY(launch_digitize(ctx, c.x, c.H, M, c.H, nullptr, xd, L.xflags));
+        xs.dig = FMT == UT_FMT_INT4 ? xd.dig4 : xd.dig8;
+        xs.KW = (c.H + FmtTraits<FMT>::kColsPerWord - 1) / FmtTraits<FMT>::kColsPerWord;
+        xexps = xd.exps;
+    }
+    float *h = (float *)(base + L.h);
+    uint32_t *hmax = (uint32_t *)(base + L.hmax);
+    {
+        GateUpArgs a;
+        a.tbl = c.tbl;
+        a.uniq = plan.uniq;
+        a.count = plan.count;
+        a.H = c.H;
+        a.I = c.I;
+        a.row_bytes = payload_bytes(FMT, 1, c.H);
+        a.x = xs;
+        a.exps = xexps;
+        a.h = h;
+        a.hmax_parts = hmax;
+        a.ntiles = (int)L.ntiles;
+        tok = timing_begin(ctx, FMT == UT_FMT_INT4 ? "moe_gate_up_int4" : FMT == UT_FMT_INT8 ? "moe_gate_up_int8" : "moe_gate_up_f32");
+        hipLaunchKernelGGL((k_moe_gate_up<FMT, M>), dim3((unsigned)L.ntiles, (unsigned)slots),
+                           dim3(kGemvThreads), 0, ctx->stream, a);
+        timing_end(ctx, tok);
+        UT_TRY(launch_check(ctx, "k_moe_gate_up"));
+    }
+    XSrc hs{};
+    const int32_t *hexps = nullptr;
+    int64_t hstride = 0;
+    if constexpr (FMT == UT_FMT_F32) {
+        hs.xf = h;
+        hs.ldx = c.I;
+        hstride = M * c.I;
+    } else {
+        XDigits hd = xdigits_view(base + L.hd, slots * M, c.I, L.hflags);
+        UT_TRY(launch_digitize_slots(ctx, h, c.I, slots * M, c.I, hmax, (int)L.ntiles, hd,
+                                     L.hflags, plan.count, M));
+        constexpr int PL = FmtTraits<FMT>::kPlanes;
+        const int64_t KW = (c.I + FmtTraits<FMT>::kColsPerWord - 1) / FmtTraits<FMT>::kColsPerWord;
+        hs.dig = FMT == UT_FMT_INT4 ? hd.dig4 : hd.dig8;
+        hs.KW = KW;
+        hstride = (int64_t)M * PL * KW;
+        hexps = hd.exps;
+    }
+    float *d = (float *)(base + L.d);
+    {
+        DownArgs a;
+        a.tbl = c.tbl;
+        a.uniq = plan.uniq;
+        a.count = plan.count;
+        a.H = c.H;
+        a.I = c.I;
+        a.row_bytes = payload_bytes(FMT, 1, c.I);
+        a.x = hs;
+        a.x_slot_stride = hstride;
+        a.exps = hexps;
+        a.d = d;
+        tok = timing_begin(ctx, FMT == UT_FMT_INT4 ? "moe_down_int4" : FMT == UT_FMT_INT8 ? "moe_down_int8" : "moe_down_f32");
+        hipLaunchKernelGGL((k_moe_down<FMT, M>), dim3((unsigned)((c.H + 63) / 64), (unsigned)slots),
+                           dim3(kGemvThreads), 0, ctx->stream, a);
+        timing_end(ctx, tok);
+        UT_TRY(launch_check(ctx, "k_moe_down"));
+    }
+    tok = timing_begin(ctx, "moe_combine");
+    hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((c.H + 255) / 256), (unsigned)M), dim3(256),
+                       0, ctx->stream, plan.choice_slot, c.weights, d, M, c.k, c.H, plan.count,
+                       c.extra_slot >= 0 ? 1 : 0, c.out, c.ldo, c.accumulate);
+    timing_end(ctx, tok);
+    return launch_check(ctx, "k_moe_combine");
+}
+
+template <int FMT>
+static int32_t moe_pass_fmt(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L, char *base,
+                            int64_t slots) {
+    switch (c.M) {
+    case 1: return moe_pass_t<FMT, 1>(ctx, c, L, base, slots);
+    case 2: return moe_pass_t<FMT, 2>(ctx, c, L, base, slots);
+    case 3: return moe_pass_t<FMT, 3>(ctx, c, L, base, slots);
+    default: return moe_pass_t<FMT, 4>(ctx, c, L, base, slots);
+    }
+}
+
+bool moe_shape_ok(int fmt, int64_t H, int64_t I) {
+    if (fmt == UT_FMT_INT4) return H % 32 == 0 && I % 32 == 0;
+    if (fmt == UT_FMT_INT8) return H % 16 == 0 && I % 16 == 0;
+    return H % 4 == 0 && I % 4 == 0;
+}
+
+int32_t moe_pass(ut_ctx *ctx, const MoeCall &c, void *scratch) {
+    if (c.M < 1 || c.M > 4) {
+        set_error(ctx, "moe_pass: M=%d outside 1..4", c.M);
+        return UT_ERR_ARG;
+    }
+    if (!moe_shape_ok(c.fmt, c.H, c.I)) {
+        set_error(ctx, "moe: hidden %lld / inter %lld not supported for format %d", (long long)c.H,
+                  (long long)c.I, c.fmt);
+        return UT_ERR_SHAPE;
+    }
+    const int64_t slots = moe_slots(c.M, c.k, c.E, c.extra_slot);
+    ScratchLayout L = moe_layout(c.M, c.k, slots, c.H, c.I, c.fmt);
+    char *base = (char *)scratch;
+    if (c.fmt == UT_FMT_INT4) return moe_pass_fmt<UT_FMT_INT4>(ctx, c, L, base, slots);
+    if (c.fmt == UT_FMT_INT8) return moe_pass_fmt<UT_FMT_INT8>(ctx, c, L, base, slots);
+    return moe_pass_fmt<UT_FMT_F32>(ctx, c, L, base, slots);
+}
+
+}  // namespace ut
+
+using namespace ut;
+
+struct ut_expert_table {
+    ut_ctx *ctx = nullptr;
+    int64_t n = 0, hidden = 0, inter = 0;
+    int32_t fmt = -1;
+    std::vector<const ut_qtensor *> gate, up, down;
+    // device arrays: gate_w, up_w, down_w (uint8_t*), gate_s, up_s, down_s (float*)
+    void *dev = nullptr;
+    ExpertPtrs ptrs{};
+    int device = 0;
+};
+
+extern "C" {
+
+int32_t ut_route(ut_ctx *ctx, const float *logits_dev, const float *bias_dev, int64_t rows,
+                 int64_t n_experts, int32_t top_k, int32_t n_group, int32_t topk_group,
+                 int32_t norm_topk_prob, float routed_scaling_factor, int32_t *ids_dev,
+                 float *weights_dev) {
+    if (!ctx || !logits_dev || !ids_dev || !weights_dev || rows < 0 || n_experts <= 0 ||
+        top_k <= 0 || top_k > 64 || n_group < 0 || n_group > 64 || topk_group < 0) {
+        set_error(ctx, "ut_route: bad argument (top_k must be 1..64, n_group <= 64)");
+        return UT_ERR_ARG;
+    }
+    if (n_experts > 4096) {
+        set_error(ctx, "ut_route: n_experts %lld > 4096", (long long)n_experts);
+        return UT_ERR_ARG;
+    }
+    return launch_route(ctx, logits_dev, bias_dev, rows, n_experts, top_k, n_group, topk_group,
+                        norm_topk_prob, routed_scaling_factor, ids_dev, weights_dev);
+}
+
+int32_t ut_expert_table_create(ut_ctx *ctx, int64_t n_experts, int64_t hidden, int64_t inter,
+                               ut_expert_table **out) {
+    if (!ctx || !out || n_experts <= 0 || hidden <= 0 || inter <= 0) return UT_ERR_ARG;
+    *out = nullptr;
+    ut_expert_table *t = new (std::nothrow) ut_expert_table();
+    if (!t) return UT_ERR_OOM;
+    t->ctx = ctx;
+    t->n = n_experts;
+    t->hidden = hidden;
+    t->inter = inter;
+    t->device = ctx->device;
+    t->gate.assign(n_experts, nullptr);
+    t->up.assign(n_experts, nullptr);
+    t->down.assign(n_experts, nullptr);
+    size_t bytes = (size_t)n_experts * sizeof(void *) * 6;
+    if (hipMalloc(&t->dev, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        delete t;
+        return UT_ERR_OOM;
+    }
+    if (hipMemset(t->dev, 0, bytes) != hipSuccess) {
+        (void)hipFree(t->dev);
+        delete t;
+        return UT_ERR_HIP;
+    }
+    void **p = (void **)t->dev;
+    t->ptrs.gate_w = (const uint8_t *const *)(p);
+    t->ptrs.up_w = (const uint8_t *const *)(p + n_experts);
+    t->ptrs.down_w = (const uint8_t *const *)(p + 2 * n_experts);
+    t->ptrs.gate_s = (const float *const *)(p + 3 * n_experts);
+    t->ptrs.up_s = (const float *const *)(p + 4 * n_experts);
+    t->ptrs.down_s = (const float *const *)(p + 5 * n_experts);
+    *out = t;
+    return UT_OK;
+}
+
+int32_t ut_expert_table_set(ut_expert_table *t, int64_t e, const ut_qtensor *gate,
+                            const ut_qtensor *up, const ut_qtensor *down) {
+    if (!t || !gate || !up || !down) return UT_ERR_ARG;
+    ut_ctx *ctx = t->ctx;
+    if (e < 0 || e >= t->n) {
+        set_error(ctx, "expert %lld out of range %lld", (long long)e, (long long)t->n);
+        return UT_ERR_BAD_EXPERT;
+    }
+    if (gate->out_dim != t->inter || gate->in_dim != t->hidden || up->out_dim != t->inter ||
+        up->in_dim != t->hidden || down->out_dim != t->hidden || down->in_dim != t->inter) {
+        set_error(ctx, "expert %lld: shapes do not match [%lld,%lld]/[%lld,%lld]", (long long)e,
+                  (long long)t->inter, (long long)t->hidden, (long long)t->hidden,
+                  (long long)t->inter);
+        return UT_ERR_SHAPE;
+    }
+    if (gate->fmt != up->fmt || gate->fmt != down->fmt || (t->fmt >= 0 && gate->fmt != t->fmt)) {
+        set_error(ctx, "expert %lld: all experts of a table must share one format", (long long)e);
+        return UT_ERR_FORMAT;
+    }
+    t->fmt = gate->fmt;
+    t->gate[e] = gate;
+    t->up[e] = up;
+    t->down[e] = down;
+    void *vals[6] = {gate->payload, up->payload, down->payload, gate->scales, up->scales,
+                     down->scales};
+    void **p = (void **)t->dev;
+    for (int i = 0; i < 6; i++)
+        UT_CHECK_HIP(ctx, hipMemcpy(p + i * t->n + e, &vals[i], sizeof(void *), hipMemcpyHostToDevice));
+    return UT_OK;
+}
+
+void ut_expert_table_free(ut_expert_table *t) {
+    if (!t) return;
+    (void)hipSetDevice(t->device);
+    if (t->dev) (void)hipFree(t->dev);
+    delete t;
+}
+
+int32_t ut_moe_experts(ut_ctx *ctx, const ut_expert_table *tbl, const int32_t *ids_dev,
+                       const float *weights_dev, int64_t rows, int32_t top_k, const float *x_dev,
+                       float *out_dev) {
+    if (!ctx || !tbl || !ids_dev || !weights_dev || !x_dev || !out_dev || rows < 0 || top_k <= 0) {
+        set_error(ctx, "ut_moe_experts: bad argument");
+        return UT_ERR_ARG;
+    }
+    if (tbl->fmt < 0) {
+        set_error(ctx, "ut_moe_experts: empty expert table");
+        return UT_ERR_BAD_EXPERT;
+    }
+    if (rows == 0) return UT_OK;
+    const int64_t maxM = 4;
+    const int64_t slots = moe_slots((int)maxM, top_k, tbl->n, -1);
+    ScratchPlan plan;
+    plan.add(moe_layout(maxM, top_k, slots, tbl->hidden, tbl->inter, tbl->fmt).total);
+    plan.add(4);  // error flag
+    std::vector<void *> ptrs;
+    UT_TRY(scratch_acquire(ctx, plan, ptrs));
+    int32_t *flag = (int32_t *)ptrs[1];
+    UT_CHECK_HIP(ctx, hipMemsetAsync(flag, 0, 4, ctx->stream));
+    for (int64_t s0 = 0; s0 < rows; s0 += maxM) {
+        MoeCall c;
+        c.fmt = tbl->fmt;
+        c.tbl = tbl->ptrs;
+        c.E = tbl->n;
+        c.H = tbl->hidden;
+        c.I = tbl->inter;
+        c.M = (int)((rows - s0) < maxM ? (rows - s0) : maxM);
+        c.k = top_k;
+        c.ids = ids_dev + s0 * top_k;
+        c.weights = weights_dev + s0 * top_k;
+        c.x = x_dev + s0 * tbl->hidden;
+        c.out = out_dev + s0 * tbl->hidden;
+        c.ldo = tbl->hidden;
+        c.err_flag = flag;
+        UT_TRY(moe_pass(ctx, c, ptrs[0]));
+    }
+    int32_t hflag = 0;
+    UT_CHECK_HIP(ctx, hipMemcpyAsync(&hflag, flag, 4, hipMemcpyDeviceToHost, ctx->stream));
+    UT_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (hflag) {
+        set_error(ctx, "ut_moe_experts: an expert id is out of range or not loaded");
+        return UT_ERR_BAD_EXPERT;
+    }
+    return UT_OK;
+}
+
+}  // extern "C"

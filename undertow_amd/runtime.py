@@ -1,0 +1,427 @@
+"""ctypes binding of libundertow_hip.so (the C ABI in include/undertow_hip.h).
+
+Host-side mirror of the reference's interfaces for the decode hot path:
+``QTensor`` (undertow-quant/src/qtensor.rs), the DeepSeek router
+(adapters/undertow-deepseek-moe/src/router.rs), the expert store
+(undertow-core/src/store.rs), ``argmax`` (undertow-core/src/sample.rs) and
+the model / session / MTP loop (adapters/undertow-deepseek-moe/src/
+{model,mtp}.rs).  Device buffers are torch tensors on the HIP device; the
+library runs on torch's current stream so ordering with torch work is
+automatic.
+
+There is no CPU fallback: every call goes through the HIP library, and a
+missing library raises ``RuntimeError``.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+from typing import Optional
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "lib" / "libundertow_hip.so"
+
+F32, INT8, INT4, INFER = 0, 1, 2, -1
+
+UT_OK = 0
+UT_ERR_ARG = -1
+UT_ERR_SHAPE = -2
+UT_ERR_FORMAT = -3
+UT_ERR_OOM = -4
+UT_ERR_HIP = -5
+UT_ERR_BAD_EXPERT = -6
+UT_ERR_CONTEXT_OVERFLOW = -7
+UT_ERR_BAD_TOKEN = -8
+UT_ERR_NOT_FOUND = -9
+UT_ERR_STATE = -10
+
+
+class UtError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+class ShapeError(UtError, AssertionError):
+    """The reference panics (assert_eq!) on a shape mismatch."""
+
+
+class ContextOverflow(UtError):
+    """EngineError::ContextOverflow (undertow-core/src/error.rs)."""
+
+
+_vp = C.c_void_p
+_i32 = C.c_int32
+_i64 = C.c_int64
+_f32 = C.c_float
+
+# (name, restype, argtypes) for every symbol the header declares.
+_SIGS = [
+    ("ut_ctx_create", _i32, [_i32, C.POINTER(_vp)]),
+    ("ut_ctx_destroy", None, [_vp]),
+    ("ut_last_error", C.c_char_p, [_vp]),
+    ("ut_ctx_set_stream", _i32, [_vp, _vp]),
+    ("ut_ctx_stream", _vp, [_vp]),
+    ("ut_ctx_synchronize", _i32, [_vp]),
+    ("ut_ctx_enable_timing", _i32, [_vp, _i32]),
+    ("ut_ctx_kernel_time", _i32, [_vp, C.c_char_p, C.POINTER(_i64), C.POINTER(C.c_double)]),
+    ("ut_qtensor_upload", _i32, [_vp, _i32, _vp, _i64, _vp, _i64, _i64, _i64, C.POINTER(_vp)]),
+    ("ut_qtensor_free", None, [_vp]),
+    ("ut_qtensor_format", _i32, [_vp]),
+    ("ut_qtensor_out_dim", _i64, [_vp]),
+    ("ut_qtensor_in_dim", _i64, [_vp]),
+    ("ut_qtensor_nbytes", _i64, [_vp]),
+    ("ut_qtensor_dequantize", _i32, [_vp, _vp, _vp]),
+    ("ut_qtensor_matmul", _i32, [_vp, _vp, _vp, _i64, _vp, _i64, _i64]),
+    ("ut_qtensor_add_scaled_row", _i32, [_vp, _vp, _i64, _f32, _vp]),
+    ("ut_route", _i32, [_vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _i32, _f32, _vp, _vp]),
+    ("ut_expert_table_create", _i32, [_vp, _i64, _i64, _i64, C.POINTER(_vp)]),
+    ("ut_expert_table_set", _i32, [_vp, _i64, _vp, _vp, _vp]),
+    ("ut_expert_table_free", None, [_vp]),
+    ("ut_moe_experts", _i32, [_vp, _vp, _vp, _vp, _i64, _i32, _vp, _vp]),
+    ("ut_argmax_rows", _i32, [_vp, _vp, _i64, _i64, _vp]),
+    ("ut_mla_attend", _i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _vp]),
+    ("ut_model_create", _i32, [_vp, _vp, C.POINTER(_vp)]),
+    ("ut_model_set_tensor", _i32, [_vp, C.c_char_p, _i32, _vp, _i64, _vp, _i64, _i64]),
+    ("ut_model_finalize", _i32, [_vp]),
+    ("ut_model_synthesize", _i32, [_vp, C.c_uint64, _f32, _i32, _i32]),
+    ("ut_model_device_bytes", _i64, [_vp]),
+    ("ut_model_free", None, [_vp]),
+    ("ut_session_create", _i32, [_vp, _i32, C.POINTER(_vp)]),
+    ("ut_session_free", None, [_vp]),
+    ("ut_session_prefill", _i32, [_vp, _vp, _i64, _vp, _vp]),
+    ("ut_session_truncate", _i32, [_vp, _i64]),
+    ("ut_session_position", _i64, [_vp]),
+    ("ut_generate_greedy", _i64, [_vp, _vp, _i64, _i64, _vp]),
+    ("ut_generate_mtp", _i64, [_vp, _vp, _i64, _i64, _i32, _vp, C.POINTER(_i64), C.POINTER(_i64)]),
+]
+
+EXPORTED = [s[0] for s in _SIGS]
+
+_lib = None
+
+
+def lib():
+    """Load the built library (raises when it was never built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build the HIP backend first "
+                "(python -c 'import __graft_entry__ as g; g.build()')")
+        L = C.CDLL(str(LIB_PATH))
+        for name, res, args in _SIGS:
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+class ModelConfig(C.Structure):
+    """ut_model_config: the DeepseekConfig fields the forward pass reads."""
+
+    _fields_ = [
+        ("vocab_size", _i64), ("hidden_size", _i64), ("intermediate_size", _i64),
+        ("moe_intermediate_size", _i64), ("num_hidden_layers", _i64),
+        ("first_k_dense_replace", _i64), ("num_attention_heads", _i64),
+        ("n_routed_experts", _i64), ("num_experts_per_tok", _i64), ("n_shared_experts", _i64),
+        ("n_group", _i64), ("topk_group", _i64),
+        ("norm_topk_prob", _i32), ("routed_scaling_factor", _f32),
+        ("q_lora_rank", _i64), ("kv_lora_rank", _i64), ("qk_nope_head_dim", _i64),
+        ("qk_rope_head_dim", _i64), ("v_head_dim", _i64),
+        ("rms_norm_eps", _f32), ("rope_theta", _f32),
+        ("mtp", _i32), ("max_position_embeddings", _i64),
+    ]
+
+    @classmethod
+    def from_dict(cls, d: dict) -> "ModelConfig":
+        c = cls()
+        for k, _ in cls._fields_:
+            if k in d:
+                setattr(c, k, d[k])
+        return c
+
+
+def _ptr(t) -> Optional[int]:
+    """Device address of a torch tensor (or None)."""
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def _torch():
+    import torch
+    return torch
+
+
+class Context:
+    """A ut_ctx bound to torch's current stream on `device`."""
+
+    def __init__(self, device: int = 0, bind_torch_stream: bool = True):
+        h = _vp()
+        rc = lib().ut_ctx_create(device, C.byref(h))
+        if rc != UT_OK:
+            raise UtError(rc, f"ut_ctx_create({device}) failed")
+        self._h = h
+        self.device = device
+        if bind_torch_stream:
+            torch = _torch()
+            s = torch.cuda.current_stream(device).cuda_stream
+            self.check(lib().ut_ctx_set_stream(self._h, s))
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h and _lib is not None:
+            _lib.ut_ctx_destroy(h)
+            self._h = None
+
+    @property
+    def handle(self):
+        return self._h
+
+    def last_error(self) -> str:
+        return lib().ut_last_error(self._h).decode()
+
+    def check(self, rc: int) -> int:
+        if rc < 0:
+            msg = self.last_error()
+            if rc == UT_ERR_SHAPE:
+                raise ShapeError(rc, msg)
+            if rc == UT_ERR_CONTEXT_OVERFLOW:
+                raise ContextOverflow(rc, msg)
+            raise UtError(rc, msg)
+        return rc
+
+    def synchronize(self) -> None:
+        self.check(lib().ut_ctx_synchronize(self._h))
+
+    def enable_timing(self, on: bool) -> None:
+        self.check(lib().ut_ctx_enable_timing(self._h, int(on)))
+
+    def kernel_time(self, prefix: str):
+        n = _i64()
+        ms = C.c_double()
+        self.check(lib().ut_ctx_kernel_time(self._h, prefix.encode(), C.byref(n), C.byref(ms)))
+        return n.value, ms.value
+
+
+class QTensor:
+    """Device QTensor (undertow-quant/src/qtensor.rs:53-71)."""
+
+    def __init__(self, ctx: Context, fmt: int, payload: np.ndarray, scales, out_dim: int,
+                 in_dim: int):
+        payload = np.ascontiguousarray(payload)
+        sc = None if scales is None else np.ascontiguousarray(scales, np.float32)
+        h = _vp()
+        rc = lib().ut_qtensor_upload(ctx.handle, fmt, payload.ctypes.data, payload.nbytes,
+                                     None if sc is None else sc.ctypes.data,
+                                     0 if sc is None else sc.size, out_dim, in_dim, C.byref(h))
+        ctx.check(rc)
+        self._h = h
+        self.ctx = ctx
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h and _lib is not None:
+            _lib.ut_qtensor_free(h)
+            self._h = None
+
+    @property
+    def handle(self):
+        return self._h
+
+    @property
+    def format(self) -> int:
+        return lib().ut_qtensor_format(self._h)
+
+    @property
+    def out_dim(self) -> int:
+        return lib().ut_qtensor_out_dim(self._h)
+
+    @property
+    def in_dim(self) -> int:
+        return lib().ut_qtensor_in_dim(self._h)
+
+    @property
+    def nbytes(self) -> int:
+        return lib().ut_qtensor_nbytes(self._h)
+
+    def dequantize(self):
+        torch = _torch()
+        out = torch.empty((self.out_dim, self.in_dim), dtype=torch.float32,
+                          device=f"cuda:{self.ctx.device}")
+        self.ctx.check(lib().ut_qtensor_dequantize(self.ctx.handle, self._h, _ptr(out)))
+        return out
+
+    def matmul(self, out, x, seq: int) -> None:
+        """QTensor::matmul(&self, out, x, seq): out [seq,out_dim] <- x [seq,in_dim]."""
+        self.ctx.check(lib().ut_qtensor_matmul(self.ctx.handle, self._h, _ptr(out), out.numel(),
+                                               _ptr(x), x.numel(), seq))
+
+    def matvec(self, out, x) -> None:
+        self.matmul(out, x, 1)
+
+    def add_scaled_row(self, row: int, factor: float, acc) -> None:
+        self.ctx.check(lib().ut_qtensor_add_scaled_row(self.ctx.handle, self._h, row, factor,
+                                                       _ptr(acc)))
+
+
+def route(ctx: Context, logits, bias, top_k: int, n_group: int, topk_group: int,
+          norm_topk_prob: bool, routed_scaling_factor: float):
+    """DeepseekSigmoidRouter::route per row of logits [rows, E] -> (ids, weights)."""
+    torch = _torch()
+    rows, E = logits.shape
+    ids = torch.empty((rows, top_k), dtype=torch.int32, device=logits.device)
+    w = torch.empty((rows, top_k), dtype=torch.float32, device=logits.device)
+    ctx.check(lib().ut_route(ctx.handle, _ptr(logits), _ptr(bias), rows, E, top_k, n_group,
+                             topk_group, int(norm_topk_prob), routed_scaling_factor, _ptr(ids),
+                             _ptr(w)))
+    return ids, w
+
+
+def argmax_rows(ctx: Context, logits):
+    torch = _torch()
+    rows, V = logits.shape
+    idx = torch.empty(rows, dtype=torch.int32, device=logits.device)
+    ctx.check(lib().ut_argmax_rows(ctx.handle, _ptr(logits), rows, V, _ptr(idx)))
+    return idx
+
+
+def mla_attend(ctx: Context, qabs, q_rope, latent, krot, pos_base: int, scale: float):
+    torch = _torch()
+    R, H, L = qabs.shape
+    P = q_rope.shape[2]
+    out = torch.empty((R, H, L), dtype=torch.float32, device=qabs.device)
+    ctx.check(lib().ut_mla_attend(ctx.handle, _ptr(qabs), _ptr(q_rope), _ptr(latent), _ptr(krot),
+                                  R, H, L, P, pos_base, scale, _ptr(out)))
+    return out
+
+
+class ExpertTable:
+    """Device expert store for one MoE layer (keeps its QTensors alive)."""
+
+    def __init__(self, ctx: Context, n_experts: int, hidden: int, inter: int):
+        h = _vp()
+        ctx.check(lib().ut_expert_table_create(ctx.handle, n_experts, hidden, inter, C.byref(h)))
+        self._h = h
+        self.ctx = ctx
+        self._keep = {}
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h and _lib is not None:
+            _lib.ut_expert_table_free(h)
+            self._h = None
+
+    def set(self, e: int, gate: QTensor, up: QTensor, down: QTensor) -> None:
+        self.ctx.check(lib().ut_expert_table_set(self._h, e, gate.handle, up.handle, down.handle))
+        self._keep[e] = (gate, up, down)
+
+    def moe_experts(self, ids, weights, x):
+        torch = _torch()
+        rows, k = ids.shape
+        out = torch.empty_like(x)
+        self.ctx.check(lib().ut_moe_experts(self.ctx.handle, self._h, _ptr(ids), _ptr(weights),
+                                            rows, k, _ptr(x), _ptr(out)))
+        return out
+
+
+class Model:
+    """DeepseekMoeModel on device (adapters/undertow-deepseek-moe/src/model.rs)."""
+
+    def __init__(self, ctx: Context, cfg: dict):
+        self.ctx = ctx
+        self.cfg = dict(cfg)
+        self._cfg = ModelConfig.from_dict(cfg)
+        h = _vp()
+        ctx.check(lib().ut_model_create(ctx.handle, C.byref(self._cfg), C.byref(h)))
+        self._h = h
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h and _lib is not None:
+            _lib.ut_model_free(h)
+            self._h = None
+
+    def set_tensor(self, name: str, fmt: int, payload: np.ndarray, scales, shape) -> None:
+        payload = np.ascontiguousarray(payload)
+        sc = None if scales is None else np.ascontiguousarray(scales, np.float32)
+        d0 = shape[0]
+        d1 = shape[1] if len(shape) == 2 else 1
+        self.ctx.check(lib().ut_model_set_tensor(self._h, name.encode(), fmt, payload.ctypes.data,
+                                                 payload.nbytes,
+                                                 None if sc is None else sc.ctypes.data, d0, d1))
+
+    def finalize(self) -> None:
+        self.ctx.check(lib().ut_model_finalize(self._h))
+
+    def synthesize(self, seed: int, init_std: float = 0.02, expert_fmt: int = INT4,
+                   dense_fmt: int = INT8) -> None:
+        self.ctx.check(lib().ut_model_synthesize(self._h, seed, init_std, expert_fmt, dense_fmt))
+
+    @property
+    def device_bytes(self) -> int:
+        return lib().ut_model_device_bytes(self._h)
+
+    def session(self, path: int = 0) -> "Session":
+        return Session(self, path)
+
+    def forward(self, ids) -> np.ndarray:
+        return self.session().prefill(ids)
+
+    def generate_greedy(self, prompt, max_new: int) -> list:
+        p = np.ascontiguousarray(prompt, np.int32)
+        out = np.zeros(max(max_new, 1), np.int32)
+        n = lib().ut_generate_greedy(self._h, p.ctypes.data, p.size, max_new, out.ctypes.data)
+        self.ctx.check(int(n))
+        return out[:n].tolist()
+
+    def generate_mtp(self, prompt, max_new: int, depth: int = 1):
+        p = np.ascontiguousarray(prompt, np.int32)
+        out = np.zeros(max(max_new, 1), np.int32)
+        d, a = _i64(), _i64()
+        n = lib().ut_generate_mtp(self._h, p.ctypes.data, p.size, max_new, depth,
+                                  out.ctypes.data, C.byref(d), C.byref(a))
+        self.ctx.check(int(n))
+        return out[:n].tolist(), d.value, a.value
+
+
+class Session:
+    """InferenceSession (model.rs:407-564) on device."""
+
+    def __init__(self, model: Model, path: int = 0):
+        self.model = model
+        h = _vp()
+        model.ctx.check(lib().ut_session_create(model._h, path, C.byref(h)))
+        self._h = h
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h and _lib is not None:
+            _lib.ut_session_free(h)
+            self._h = None
+
+    def prefill(self, ids, want_logits: bool = True):
+        ids = np.ascontiguousarray(ids, np.int32)
+        V = self.model.cfg["vocab_size"]
+        logits = np.zeros((ids.size, V), np.float32) if want_logits else None
+        am = np.zeros(max(ids.size, 1), np.int32)
+        rc = lib().ut_session_prefill(self._h, ids.ctypes.data, ids.size,
+                                      None if logits is None else logits.ctypes.data,
+                                      am.ctypes.data)
+        self.model.ctx.check(rc)
+        self.last_argmax = am[:ids.size].tolist()
+        return logits
+
+    def decode(self, tok: int):
+        return self.prefill([tok])[0]
+
+    def truncate(self, n: int) -> None:
+        self.model.ctx.check(lib().ut_session_truncate(self._h, n))
+
+    @property
+    def position(self) -> int:
+        return int(lib().ut_session_position(self._h))
