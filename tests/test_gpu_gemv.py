@@ -113,7 +113,9 @@ def test_zero_and_extreme_rows(ctx):
     assert (got[0] == 0).all()
     want = O.matmul(INT4, payload, scales, o, i, x)
     assert np.array_equal(got, gemv_closed_form(INT4, payload, scales, o, i, x))
-    assert (np.abs(got - want) <= 1e-4 * np.maximum(np.abs(want), 1e-30)).all()
+    # f32 rounding (the oracle's and ours) is relative to the row's magnitude
+    row_mag = np.abs(want).max(axis=1, keepdims=True)
+    assert (np.abs(got - want) <= 1e-5 * row_mag).all()
 
 
 def test_non_finite_activation_gives_nan(ctx):

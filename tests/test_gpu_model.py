@@ -1,0 +1,137 @@
+"""The decode step end to end on the GPU: the reference's transformers golden
+(oracle-tiny), BASELINE config 1 against the CPU oracle, greedy and MTP streams.
+
+Bars: logits within 1e-3 max-abs and 1e-4 mean-abs of
+the oracle; argmax exact wherever the top-2 gap exceeds 1e-3; greedy token
+streams identical; MTP output identical to plain greedy (mtp.rs losslessness,
+undertow-bench/tests/pipeline.rs:298-338).
+"""
+import json
+
+import numpy as np
+import pytest
+
+from models import C1, checkpoint, gpu_model, prompt_ids
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def gap_ok(logits):
+    s = np.sort(logits, axis=-1)
+    return (s[..., -1] - s[..., -2]) > 1e-3
+
+
+@pytest.fixture(scope="module")
+def ref(golden_dir):
+    return json.loads((golden_dir / "oracle-tiny" / "reference.json").read_text())
+
+
+def test_tiny_f32_matches_transformers_golden(ctx, ref):
+    """undertow-bench/tests/oracle.rs:47-84 against the GPU path."""
+    m = gpu_model(ctx, checkpoint())
+    logits = m.forward(ref["full_ids"])
+    tl = np.asarray(ref["tf_logits"], np.float32)
+    err = np.abs(logits - tl)
+    assert err.max() < 1e-3, err.max()
+    assert logits.argmax(1).tolist() == ref["tf_pred"]
+    max_new = len(ref["full_ids"]) - len(ref["prompt_ids"])
+    assert ref["prompt_ids"] + m.generate_greedy(ref["prompt_ids"], max_new) == ref["full_ids"]
+
+
+@pytest.mark.parametrize("fmt", ["f32", "int8", "int4"])
+def test_tiny_matches_oracle(ctx, ref, fmt):
+    ck = checkpoint(fmt=fmt)
+    m = gpu_model(ctx, ck)
+    om = O.Model(ck)
+    ids = ref["full_ids"]
+    got = m.forward(ids)
+    want = om.forward(ids)
+    err = np.abs(got - want)
+    assert err.max() <= 1e-3 and err.mean() <= 1e-4, (err.max(), err.mean())
+    ok = gap_ok(want)
+    assert (got.argmax(1)[ok] == want.argmax(1)[ok]).all()
+    assert m.generate_greedy(ref["prompt_ids"], 16) == om.greedy_decode(ref["prompt_ids"], 16)[len(ref["prompt_ids"]):]
+
+
+@pytest.fixture(scope="module")
+def c1(ctx):
+    ck = checkpoint(C1, fmt="int4")
+    return ck, gpu_model(ctx, ck), O.Model(ck)
+
+
+def test_c1_logits_match_oracle(c1):
+    ck, m, om = c1
+    prompt = prompt_ids(16, C1["vocab_size"])
+    got, want = m.forward(prompt), om.forward(prompt)
+    err = np.abs(got - want)
+    assert err.max() <= 1e-3 and err.mean() <= 1e-4, (err.max(), err.mean())
+    ok = gap_ok(want)
+    assert (got.argmax(1)[ok] == want.argmax(1)[ok]).all()
+
+
+def test_c1_greedy_stream_identical(c1):
+    ck, m, om = c1
+    prompt = prompt_ids(16, C1["vocab_size"])
+    want = om.greedy_decode(prompt, 64)[16:]
+    assert m.generate_greedy(prompt, 64) == want
+
+
+def test_c1_mtp_matches_oracle_and_greedy(c1):
+    ck, m, om = c1
+    prompt = prompt_ids(16, C1["vocab_size"])
+    toks, drafted, accepted = m.generate_mtp(prompt, 64, depth=1)
+    otoks, od, oa = om.generate_mtp(prompt, 64)
+    assert toks == otoks == m.generate_greedy(prompt, 64)
+    assert (drafted, accepted) == (od, oa)
+
+
+@pytest.mark.parametrize("depth", [2, 3])
+def test_c1_mtp_deeper_drafts_are_lossless(c1, depth):
+    ck, m, om = c1
+    prompt = prompt_ids(16, C1["vocab_size"])
+    toks, drafted, accepted = m.generate_mtp(prompt, 48, depth=depth)
+    assert toks == m.generate_greedy(prompt, 48)
+    assert drafted > 0 and 0 <= accepted <= drafted
+
+
+def test_incremental_decode_matches_one_shot(c1):
+    """pipeline.rs:100-136: incremental == full prefill (argmax exact, < 1e-3)."""
+    ck, m, om = c1
+    ids = prompt_ids(24, C1["vocab_size"], seed=9)
+    full = m.forward(ids)
+    s = m.session()
+    inc = [s.prefill(ids[:10])[-1]]
+    for t in ids[10:]:
+        inc.append(s.decode(t))
+    inc = np.stack(inc)
+    assert np.abs(inc - full[9:]).max() < 1e-3
+    assert (inc.argmax(1) == full[9:].argmax(1)).all()
+
+
+def test_truncate_then_refill_matches(c1):
+    """pipeline.rs:200-223."""
+    ck, m, om = c1
+    ids = prompt_ids(20, C1["vocab_size"], seed=11)
+    s = m.session()
+    a = s.prefill(ids)
+    s.truncate(12)
+    assert s.position == 12
+    b = s.prefill(ids[12:])
+    assert np.array_equal(a[12:], b)
+
+
+def test_context_overflow_and_bad_token(ctx):
+    import undertow_amd as U
+    ck = checkpoint({"max_position_embeddings": 32})
+    m = gpu_model(ctx, ck)
+    s = m.session()
+    s.prefill(list(range(30)))
+    with pytest.raises(U.ContextOverflow):
+        s.prefill([1, 2, 3])
+    with pytest.raises(U.UtError) as ei:
+        m.session().prefill([5, 999999])
+    assert ei.value.code == U.runtime.UT_ERR_BAD_TOKEN
+    # generation stops cleanly at the context end (pipeline.rs:450-459)
+    out = m.generate_greedy(list(range(28)), 10)
+    assert len(out) == 5

@@ -305,6 +305,29 @@ int32_t gemv(ut_ctx *ctx, const GemvArgs &ga) {
     return launch_check(ctx, "k_gemv_generic");
 }
 
+size_t matmul_digit_bytes(int64_t M, int64_t K) {
+    return xdigits_bytes(M, K, XD_DIG4 | XD_DIG8 | XD_XT);
+}
+
+int32_t matmul_dev(ut_ctx *ctx, const ut_qtensor *w, const float *x, int64_t M, float *out,
+                   int64_t ldo, int accumulate, void *digit_scratch) {
+    if (M <= 0) return UT_OK;
+    GemvArgs ga;
+    ga.w = w;
+    ga.M = M;
+    ga.out = out;
+    ga.ldo = ldo;
+    ga.accumulate = accumulate;
+    if (w->fmt == UT_FMT_F32) {
+        ga.xf = x;
+        return gemv(ctx, ga);
+    }
+    int flags = fast_ok(w) ? xdigit_flags_for(w->fmt, w->in_dim) : XD_XT;
+    ga.xd = xdigits_view(digit_scratch, M, w->in_dim, flags);
+    UT_TRY(launch_digitize(ctx, x, w->in_dim, M, w->in_dim, nullptr, ga.xd, flags));
+    return gemv(ctx, ga);
+}
+
 }  // namespace ut
 
 using namespace ut;

@@ -154,4 +154,10 @@ struct GemvArgs {
 };
 int32_t gemv(ut_ctx *ctx, const GemvArgs &a);
 
+// out[M, ldo] (+)= x[M, K] * w^T with x f32 on device: digitises x into
+// digit_scratch (matmul_digit_bytes(M, K) bytes) when w is quantized.
+size_t matmul_digit_bytes(int64_t M, int64_t K);
+int32_t matmul_dev(ut_ctx *ctx, const ut_qtensor *w, const float *x, int64_t M, float *out,
+                   int64_t ldo, int accumulate, void *digit_scratch);
+
 }  // namespace ut

@@ -1,23 +1,890 @@
-// ut_model.hip -- DeepSeek model / session / MTP loop on device (in progress).
-#include "ut_internal.h"
+// ut_model.hip -- the DeepSeek model, inference session and MTP
+// draft+verify loop on one HIP stream (adapters/undertow-deepseek-moe/src/
+// {loader,model,attention,mtp}.rs).
+//
+// All activations, the compressed KV caches and the hidden states kept for
+// the MTP head stay in HBM.  Per step the host only sends token ids and
+// reads back argmax ids (a few ints) to make the accept decision.
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <unordered_map>
+
+#include "ut_mla.h"
+#include "ut_moe.h"
+#include "ut_ops.h"
+#include "ut_sample.h"
 
 using namespace ut;
 
-struct ut_model { ut_ctx *ctx; };
-struct ut_session { ut_model *m; };
+namespace {
+
+struct DevTensor {
+    ut_qtensor *qt = nullptr;  // matrices
+    float *vec = nullptr;      // 1-D f32 vectors
+    int64_t d0 = 0, d1 = 0;
+};
+
+// One MLP (dense FFN, shared expert) as a one-slot expert table, so the
+// fused gate/up + down kernels serve it too.
+struct MlpW {
+    const ut_qtensor *gate = nullptr, *up = nullptr, *down = nullptr;
+    void *dev = nullptr;  // 6 device pointers
+    ExpertPtrs ptrs{};
+    int fmt = UT_FMT_F32;
+    int64_t inter = 0;
+};
+
+struct LayerW {
+    const float *input_norm = nullptr, *post_norm = nullptr;
+    bool lora = false;
+    const ut_qtensor *q_a = nullptr, *q_b = nullptr, *q_proj = nullptr, *kv_a = nullptr,
+                     *kv_b = nullptr, *o_proj = nullptr;
+    const float *q_a_norm = nullptr, *kv_a_norm = nullptr;
+    bool dense = false;
+    MlpW mlp;                        // dense FFN
+    const ut_qtensor *gate = nullptr;  // router [E, H] f32
+    const float *bias = nullptr;
+    bool has_shared = false;
+    MlpW shared;
+    void *experts_dev = nullptr;     // 6*E device pointers
+    ExpertPtrs experts{};
+    int expert_fmt = UT_FMT_F32;
+};
+
+struct KvCache {
+    float *latent = nullptr;  // [cap, kv_lora]
+    float *krot = nullptr;    // [cap, rope]
+    int64_t len = 0;
+};
+
+}  // namespace
+
+struct ut_model {
+    ut_ctx *ctx = nullptr;
+    ut_model_config c{};
+    std::unordered_map<std::string, DevTensor> tensors;
+    std::vector<LayerW> layers;
+    LayerW mtp_layer;
+    bool has_mtp = false;
+    const ut_qtensor *embed = nullptr, *lm_head = nullptr, *eh_proj = nullptr, *mtp_head = nullptr;
+    const float *final_norm = nullptr, *enorm = nullptr, *hnorm = nullptr, *mtp_norm = nullptr;
+    float2 *rope_table = nullptr;  // [max_pos][rope/2]
+    int32_t *zeros = nullptr;      // [4] expert id 0 (MLP as a one-slot table)
+    float *ones = nullptr;         // [4] weight 1
+    bool finalized = false;
+    std::vector<void *> device_allocs;
+    int64_t device_bytes = 0;
+    int device = 0;
+};
+
+namespace {
+
+struct Workspace {
+    int64_t rows = 0;
+    void *base = nullptr;
+    size_t bytes = 0;
+    float *x = nullptr, *normed = nullptr, *attn = nullptr, *moe_out = nullptr;
+    float *qa = nullptr, *qa_n = nullptr, *q = nullptr, *comp = nullptr;
+    float *qabs = nullptr, *qrope = nullptr, *clat = nullptr, *ctxv = nullptr;
+    float *logits = nullptr, *emb = nullptr, *cat = nullptr;
+    float *rlogits = nullptr, *rw = nullptr;
+    int32_t *rids = nullptr, *ids = nullptr, *am = nullptr, *err = nullptr;
+    void *digits = nullptr, *moe = nullptr, *mla = nullptr, *argm = nullptr;
+};
+
+}  // namespace
+
+struct ut_session {
+    ut_model *m = nullptr;
+    int32_t path = 0;
+    int64_t pos = 0;
+    std::vector<KvCache> kv;
+    KvCache mtp_kv;
+    int64_t mtp_fed = 0;
+    std::vector<int32_t> tokens;
+    float *hidden = nullptr;  // [cap, H] pre-final-norm hidden states (MTP input)
+    void *kv_alloc = nullptr;
+    Workspace ws;
+    int64_t cap = 0;
+};
+
+namespace {
+
+int64_t hd(const ut_model *m) { return m->c.hidden_size; }
+
+int32_t dev_alloc(ut_model *m, size_t bytes, void **p) {
+    if (hipMalloc(p, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        set_error(m->ctx, "device allocation of %zu bytes failed", bytes);
+        return UT_ERR_OOM;
+    }
+    m->device_allocs.push_back(*p);
+    m->device_bytes += (int64_t)bytes;
+    return UT_OK;
+}
+
+const DevTensor *find(const ut_model *m, const std::string &name) {
+    auto it = m->tensors.find(name);
+    return it == m->tensors.end() ? nullptr : &it->second;
+}
+
+int32_t get_qt(ut_model *m, const std::string &name, int64_t o, int64_t i, const ut_qtensor **out) {
+    const DevTensor *t = find(m, name);
+    if (!t || !t->qt) {
+        set_error(m->ctx, "missing tensor %s", name.c_str());
+        return UT_ERR_NOT_FOUND;
+    }
+    if (t->qt->out_dim != o || t->qt->in_dim != i) {
+        set_error(m->ctx, "tensor %s has shape [%lld, %lld], expected [%lld, %lld]", name.c_str(),
+                  (long long)t->qt->out_dim, (long long)t->qt->in_dim, (long long)o, (long long)i);
+        return UT_ERR_SHAPE;
+    }
+    *out = t->qt;
+    return UT_OK;
+}
+
+int32_t get_vec(ut_model *m, const std::string &name, int64_t n, const float **out) {
+    const DevTensor *t = find(m, name);
+    if (!t || !t->vec) {
+        set_error(m->ctx, "missing tensor %s", name.c_str());
+        return UT_ERR_NOT_FOUND;
+    }
+    if (t->d0 * t->d1 != n) {
+        set_error(m->ctx, "tensor %s has %lld elements, expected %lld", name.c_str(),
+                  (long long)(t->d0 * t->d1), (long long)n);
+        return UT_ERR_SHAPE;
+    }
+    *out = t->vec;
+    return UT_OK;
+}
+
+int32_t make_mlp(ut_model *m, const std::string &prefix, int64_t inter, MlpW *w) {
+    const int64_t H = hd(m);
+    UT_TRY(get_qt(m, prefix + "gate_proj.weight", inter, H, &w->gate));
+    UT_TRY(get_qt(m, prefix + "up_proj.weight", inter, H, &w->up));
+    UT_TRY(get_qt(m, prefix + "down_proj.weight", H, inter, &w->down));
+    if (w->gate->fmt != w->up->fmt || w->gate->fmt != w->down->fmt) {
+        set_error(m->ctx, "%s: gate/up/down must share one format", prefix.c_str());
+        return UT_ERR_FORMAT;
+    }
+    w->fmt = w->gate->fmt;
+    w->inter = inter;
+    if (!moe_shape_ok(w->fmt, H, inter)) {
+        set_error(m->ctx, "%s: hidden %lld / inter %lld unsupported for format %d", prefix.c_str(),
+                  (long long)H, (long long)inter, w->fmt);
+        return UT_ERR_SHAPE;
+    }
+    UT_TRY(dev_alloc(m, 6 * sizeof(void *), &w->dev));
+    const void *vals[6] = {w->gate->payload, w->up->payload, w->down->payload, w->gate->scales,
+                           w->up->scales, w->down->scales};
+    UT_CHECK_HIP(m->ctx, hipMemcpy(w->dev, vals, sizeof vals, hipMemcpyHostToDevice));
+    void **p = (void **)w->dev;
+    w->ptrs.gate_w = (const uint8_t *const *)(p + 0);
+    w->ptrs.up_w = (const uint8_t *const *)(p + 1);
+    w->ptrs.down_w = (const uint8_t *const *)(p + 2);
+    w->ptrs.gate_s = (const float *const *)(p + 3);
+    w->ptrs.up_s = (const float *const *)(p + 4);
+    w->ptrs.down_s = (const float *const *)(p + 5);
+    return UT_OK;
+}
+
+// load_layer (adapters/undertow-deepseek-moe/src/loader.rs:67-174)
+int32_t load_layer(ut_model *m, int64_t li, bool dense, LayerW *L) {
+    const ut_model_config &c = m->c;
+    const int64_t H = c.hidden_size, heads = c.num_attention_heads;
+    const int64_t qh = c.qk_nope_head_dim + c.qk_rope_head_dim;
+    const std::string p = "model.layers." + std::to_string(li) + ".";
+    UT_TRY(get_vec(m, p + "input_layernorm.weight", H, &L->input_norm));
+    UT_TRY(get_vec(m, p + "post_attention_layernorm.weight", H, &L->post_norm));
+    if (c.q_lora_rank > 0) {
+        L->lora = true;
+        UT_TRY(get_qt(m, p + "self_attn.q_a_proj.weight", c.q_lora_rank, H, &L->q_a));
+        UT_TRY(get_vec(m, p + "self_attn.q_a_layernorm.weight", c.q_lora_rank, &L->q_a_norm));
+        UT_TRY(get_qt(m, p + "self_attn.q_b_proj.weight", heads * qh, c.q_lora_rank, &L->q_b));
+    } else {
+        UT_TRY(get_qt(m, p + "self_attn.q_proj.weight", heads * qh, H, &L->q_proj));
+    }
+    UT_TRY(get_qt(m, p + "self_attn.kv_a_proj_with_mqa.weight", c.kv_lora_rank + c.qk_rope_head_dim,
+                  H, &L->kv_a));
+    UT_TRY(get_vec(m, p + "self_attn.kv_a_layernorm.weight", c.kv_lora_rank, &L->kv_a_norm));
+    UT_TRY(get_qt(m, p + "self_attn.kv_b_proj.weight", heads * (c.qk_nope_head_dim + c.v_head_dim),
+                  c.kv_lora_rank, &L->kv_b));
+    UT_TRY(get_qt(m, p + "self_attn.o_proj.weight", H, heads * c.v_head_dim, &L->o_proj));
+    L->dense = dense;
+    if (dense) {
+        UT_TRY(make_mlp(m, p + "mlp.", c.intermediate_size, &L->mlp));
+        return UT_OK;
+    }
+    const int64_t E = c.n_routed_experts;
+    UT_TRY(get_qt(m, p + "mlp.gate.weight", E, H, &L->gate));
+    if (L->gate->fmt != UT_FMT_F32) {
+        set_error(m->ctx, "%smlp.gate.weight must stay f32", p.c_str());
+        return UT_ERR_FORMAT;
+    }
+    if (find(m, p + "mlp.gate.e_score_correction_bias"))
+        UT_TRY(get_vec(m, p + "mlp.gate.e_score_correction_bias", E, &L->bias));
+    if (c.n_shared_experts > 0) {
+        L->has_shared = true;
+        UT_TRY(make_mlp(m, p + "mlp.shared_experts.", c.n_shared_experts * c.moe_intermediate_size,
+                        &L->shared));
+    }
+    UT_TRY(dev_alloc(m, (size_t)E * 6 * sizeof(void *), &L->experts_dev));
+    std::vector<const void *> vals((size_t)E * 6, nullptr);
+    const int64_t I = c.moe_intermediate_size;
+    int fmt = -1;
+    for (int64_t e = 0; e < E; e++) {
+        const std::string ep = p + "mlp.experts." + std::to_string(e) + ".";
+        const ut_qtensor *g, *u, *d;
+        UT_TRY(get_qt(m, ep + "gate_proj.weight", I, H, &g));
+        UT_TRY(get_qt(m, ep + "up_proj.weight", I, H, &u));
+        UT_TRY(get_qt(m, ep + "down_proj.weight", H, I, &d));
+        if (fmt < 0) fmt = g->fmt;
+        if (g->fmt != fmt || u->fmt != fmt || d->fmt != fmt) {
+            set_error(m->ctx, "layer %lld: experts must share one format", (long long)li);
+            return UT_ERR_FORMAT;
+        }
+        vals[0 * E + e] = g->payload;
+        vals[1 * E + e] = u->payload;
+        vals[2 * E + e] = d->payload;
+        vals[3 * E + e] = g->scales;
+        vals[4 * E + e] = u->scales;
+        vals[5 * E + e] = d->scales;
+    }
+    L->expert_fmt = fmt;
+    if (!moe_shape_ok(fmt, H, I)) {
+        set_error(m->ctx, "experts: hidden %lld / inter %lld unsupported for format %d",
+                  (long long)H, (long long)I, fmt);
+        return UT_ERR_SHAPE;
+    }
+    UT_CHECK_HIP(m->ctx, hipMemcpy(L->experts_dev, vals.data(), vals.size() * sizeof(void *),
+                                   hipMemcpyHostToDevice));
+    void **pp = (void **)L->experts_dev;
+    L->experts.gate_w = (const uint8_t *const *)(pp + 0 * E);
+    L->experts.up_w = (const uint8_t *const *)(pp + 1 * E);
+    L->experts.down_w = (const uint8_t *const *)(pp + 2 * E);
+    L->experts.gate_s = (const float *const *)(pp + 3 * E);
+    L->experts.up_s = (const float *const *)(pp + 4 * E);
+    L->experts.down_s = (const float *const *)(pp + 5 * E);
+    return UT_OK;
+}
+
+// --------------------------------------------------------- workspace ---
+int64_t max_inter(const ut_model *m) {
+    int64_t I = m->c.moe_intermediate_size * (m->c.n_shared_experts > 0 ? m->c.n_shared_experts : 1);
+    if (m->c.intermediate_size > I) I = m->c.intermediate_size;
+    if (m->c.moe_intermediate_size > I) I = m->c.moe_intermediate_size;
+    return I;
+}
+
+int32_t ws_reserve(ut_session *s, int64_t rows) {
+    Workspace &w = s->ws;
+    if (rows <= w.rows) return UT_OK;
+    ut_model *m = s->m;
+    const ut_model_config &c = m->c;
+    ut_ctx *ctx = m->ctx;
+    const int64_t H = c.hidden_size, heads = c.num_attention_heads;
+    const int64_t qh = c.qk_nope_head_dim + c.qk_rope_head_dim, Lr = c.kv_lora_rank;
+    const int64_t R = rows < 4 ? 4 : rows;
+    const int64_t E = c.n_routed_experts, k = c.num_experts_per_tok;
+    int64_t kmax = 2 * H;
+    for (int64_t v : {c.q_lora_rank, heads * c.v_head_dim, max_inter(m), Lr})
+        if (v > kmax) kmax = v;
+    int fmt_hint = UT_FMT_INT4;  // layout sizes are largest for the digit formats
+    const int64_t slots_routed = moe_slots(4, k, E, -1);
+    size_t moe_bytes = moe_layout(4, k, slots_routed, H, c.moe_intermediate_size, fmt_hint).total;
+    for (int f : {UT_FMT_INT8, UT_FMT_F32}) {
+        size_t b = moe_layout(4, k, slots_routed, H, c.moe_intermediate_size, f).total;
+        if (b > moe_bytes) moe_bytes = b;
+    }
+    for (int f : {UT_FMT_INT4, UT_FMT_INT8, UT_FMT_F32}) {
+        size_t b = moe_layout(4, 1, 1, H, max_inter(m), f).total;
+        if (b > moe_bytes) moe_bytes = b;
+    }
+    ScratchPlan plan;
+    auto F = [&](int64_t n) { return plan.add((size_t)n * 4); };
+    size_t ix = F(R * H), inorm = F(R * H), iattn = F(R * H), imoe = F(R * H);
+    size_t iqa = F(R * (c.q_lora_rank > 0 ? c.q_lora_rank : 1)), iqan = F(R * (c.q_lora_rank > 0 ? c.q_lora_rank : 1));
+    size_t iq = F(R * heads * qh), icomp = F(R * (Lr + c.qk_rope_head_dim));
+    size_t iqabs = F(R * heads * Lr), iqrope = F(R * heads * c.qk_rope_head_dim + 1);
+    size_t iclat = F(R * heads * Lr), ictx = F(R * heads * c.v_head_dim);
+    size_t ilog = F(R * c.vocab_size), iemb = F(R * H), icat = F(R * 2 * H);
+    size_t irl = F(4 * E), irw = F(4 * k), irid = F(4 * k), iids = F(R), iam = F(R), ierr = F(1);
+    size_t idig = plan.add(matmul_digit_bytes(R, kmax));
+    size_t imoes = plan.add(moe_bytes);
+    size_t imla = plan.add(mla_scratch_bytes(R, heads, Lr, s->cap));
+    size_t iarg = plan.add(argmax_scratch_bytes(R, c.vocab_size) + 256);
+    size_t total = 0;
+    for (size_t b : plan.sizes) total += b;
+    if (w.base) {
+        UT_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        UT_CHECK_HIP(ctx, hipFree(w.base));
+        w.base = nullptr;
+    }
+    if (hipMalloc(&w.base, total) != hipSuccess) {
+        (void)hipGetLastError();
+        set_error(ctx, "workspace allocation of %zu bytes failed", total);
+        w.rows = 0;
+        return UT_ERR_OOM;
+    }
+    w.bytes = total;
+    std::vector<char *> p;
+    char *q = (char *)w.base;
+    for (size_t b : plan.sizes) { p.push_back(q); q += b; }
+    w.x = (float *)p[ix]; w.normed = (float *)p[inorm]; w.attn = (float *)p[iattn];
+    w.moe_out = (float *)p[imoe]; w.qa = (float *)p[iqa]; w.qa_n = (float *)p[iqan];
+    w.q = (float *)p[iq]; w.comp = (float *)p[icomp]; w.qabs = (float *)p[iqabs];
+    w.qrope = (float *)p[iqrope]; w.clat = (float *)p[iclat]; w.ctxv = (float *)p[ictx];
+    w.logits = (float *)p[ilog]; w.emb = (float *)p[iemb]; w.cat = (float *)p[icat];
+    w.rlogits = (float *)p[irl]; w.rw = (float *)p[irw]; w.rids = (int32_t *)p[irid];
+    w.ids = (int32_t *)p[iids]; w.am = (int32_t *)p[iam]; w.err = (int32_t *)p[ierr];
+    w.digits = p[idig]; w.moe = p[imoes]; w.mla = p[imla]; w.argm = p[iarg];
+    w.rows = R;
+    UT_CHECK_HIP(ctx, hipMemsetAsync(w.err, 0, 4, ctx->stream));
+    return UT_OK;
+}
+
+// ------------------------------------------------------------ forward ---
+int32_t mm(ut_session *s, const ut_qtensor *w, const float *x, int64_t M, float *out, int64_t ldo,
+           int accumulate = 0) {
+    return matmul_dev(s->m->ctx, w, x, M, out, ldo, accumulate, s->ws.digits);
+}
+
+// An MLP (dense FFN or shared expert) over rows, added into out
+// (MlpWeights::forward_add, model.rs:43-58).
+int32_t mlp_add(ut_session *s, const MlpW &w, const float *x, int64_t rows, float *out) {
+    ut_model *m = s->m;
+    for (int64_t s0 = 0; s0 < rows; s0 += 4) {
+        MoeCall c;
+        c.fmt = w.fmt;
+        c.tbl = w.ptrs;
+        c.E = 1;
+        c.H = hd(m);
+        c.I = w.inter;
+        c.M = (int)(rows - s0 < 4 ? rows - s0 : 4);
+        c.k = 1;
+        c.ids = m->zeros;
+        c.weights = m->ones;
+        c.x = x + s0 * c.H;
+        c.out = out + s0 * c.H;
+        c.ldo = c.H;
+        c.accumulate = 1;
+        c.err_flag = s->ws.err;
+        UT_TRY(moe_pass(m->ctx, c, s->ws.moe));
+    }
+    return UT_OK;
+}
+
+// moe_forward (model.rs:195-286): router, routed experts in choice order,
+// then the shared expert, into out (overwritten).
+int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, int64_t rows, float *out) {
+    ut_model *m = s->m;
+    const ut_model_config &c = m->c;
+    const int64_t H = c.hidden_size, E = c.n_routed_experts;
+    const int k = (int)c.num_experts_per_tok;
+    for (int64_t s0 = 0; s0 < rows; s0 += 4) {
+        const int M = (int)(rows - s0 < 4 ? rows - s0 : 4);
+        // f32 gate matmul (lib.rs:128) + route (router.rs:58)
+        UT_TRY(mm(s, L.gate, x + s0 * H, M, s->ws.rlogits, E));
+        UT_TRY(launch_route(m->ctx, s->ws.rlogits, L.bias, M, E, k, (int)c.n_group,
+                            (int)c.topk_group, c.norm_topk_prob, c.routed_scaling_factor,
+                            s->ws.rids, s->ws.rw));
+        MoeCall mc;
+        mc.fmt = L.expert_fmt;
+        mc.tbl = L.experts;
+        mc.E = E;
+        mc.H = H;
+        mc.I = c.moe_intermediate_size;
+        mc.M = M;
+        mc.k = k;
+        mc.ids = s->ws.rids;
+        mc.weights = s->ws.rw;
+        mc.x = x + s0 * H;
+        mc.out = out + s0 * H;
+        mc.ldo = H;
+        mc.accumulate = 0;
+        mc.err_flag = s->ws.err;
+        UT_TRY(moe_pass(m->ctx, mc, s->ws.moe));
+    }
+    if (L.has_shared) UT_TRY(mlp_add(s, L.shared, x, rows, out));
+    return UT_OK;
+}
+
+// mla_forward_cached, absorbed form (attention.rs:123-279).  x: normed rows.
+int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, int64_t rows, KvCache &kv,
+                    float *out) {
+    ut_model *m = s->m;
+    ut_ctx *ctx = m->ctx;
+    const ut_model_config &c = m->c;
+    Workspace &w = s->ws;
+    const int64_t heads = c.num_attention_heads, nope = c.qk_nope_head_dim,
+                  rope = c.qk_rope_head_dim, vh = c.v_head_dim, Lr = c.kv_lora_rank;
+    const int64_t qh = nope + rope;
+    const float scale = 1.0f / sqrtf((float)qh);  // config.rs:142-144
+    const int64_t pos_base = kv.len;
+    if (L.lora) {
+        UT_TRY(mm(s, L.q_a, x, rows, w.qa, c.q_lora_rank));
+        UT_TRY(launch_rmsnorm(ctx, w.qa, c.q_lora_rank, L.q_a_norm, c.q_lora_rank, c.rms_norm_eps,
+                              rows, w.qa_n, c.q_lora_rank));
+        UT_TRY(mm(s, L.q_b, w.qa_n, rows, w.q, heads * qh));
+    } else {
+        UT_TRY(mm(s, L.q_proj, x, rows, w.q, heads * qh));
+    }
+    const int64_t half = rope / 2;
+    UT_TRY(launch_rope(ctx, w.q + nope, rows, heads, heads * qh, qh, rope, pos_base, m->rope_table,
+                       half));
+    UT_TRY(mm(s, L.kv_a, x, rows, w.comp, Lr + rope));
+    UT_TRY(launch_rmsnorm(ctx, w.comp, Lr + rope, L.kv_a_norm, Lr, c.rms_norm_eps, rows,
+                          kv.latent + pos_base * Lr, Lr));
+    UT_CHECK_HIP(ctx, hipMemcpy2DAsync(kv.krot + pos_base * rope, rope * 4, w.comp + Lr,
+                                       (Lr + rope) * 4, rope * 4, rows, hipMemcpyDeviceToDevice,
+                                       ctx->stream));
+    UT_TRY(launch_rope(ctx, kv.krot + pos_base * rope, rows, 1, rope, rope, rope, pos_base,
+                       m->rope_table, half));
+    kv.len = pos_base + rows;
+    UT_TRY(launch_absorb_q(ctx, L.kv_b, w.q, rows, heads, nope, rope, vh, w.qabs, w.qrope));
+    UT_TRY(launch_mla_attend(ctx, w.qabs, w.qrope, kv.latent, kv.krot, rows, heads, Lr, rope,
+                             pos_base, scale, w.clat, w.mla));
+    UT_TRY(launch_absorb_v(ctx, L.kv_b, w.clat, rows, heads, nope, vh, w.ctxv));
+    return mm(s, L.o_proj, w.ctxv, rows, out, c.hidden_size);
+}
+
+// run_layer (model.rs:127-183) / the per-layer body of prefill (:470-526).
+int32_t run_layer(ut_session *s, const LayerW &L, float *x, int64_t rows, KvCache &kv) {
+    ut_model *m = s->m;
+    ut_ctx *ctx = m->ctx;
+    const ut_model_config &c = m->c;
+    const int64_t H = c.hidden_size;
+    Workspace &w = s->ws;
+    UT_TRY(launch_rmsnorm(ctx, x, H, L.input_norm, H, c.rms_norm_eps, rows, w.normed, H));
+    UT_TRY(mla_forward(s, L, w.normed, rows, kv, w.attn));
+    UT_TRY(launch_add(ctx, x, w.attn, rows * H));
+    UT_TRY(launch_rmsnorm(ctx, x, H, L.post_norm, H, c.rms_norm_eps, rows, w.normed, H));
+    if (L.dense) return mlp_add(s, L.mlp, w.normed, rows, x);
+    UT_TRY(moe_forward(s, L, w.normed, rows, w.moe_out));
+    return launch_add(ctx, x, w.moe_out, rows * H);
+}
+
+int32_t check_flags(ut_session *s) {
+    // called after a stream sync: the sticky expert-id error flag
+    ut_ctx *ctx = s->m->ctx;
+    int32_t f = 0;
+    UT_CHECK_HIP(ctx, hipMemcpy(&f, s->ws.err, 4, hipMemcpyDeviceToHost));
+    if (f) {
+        set_error(ctx, "a routed expert id was out of range or not loaded");
+        return UT_ERR_BAD_EXPERT;
+    }
+    return UT_OK;
+}
+
+int32_t upload_ids(ut_session *s, const int32_t *ids, int64_t n) {
+    ut_ctx *ctx = s->m->ctx;
+    void *pin = nullptr;
+    UT_TRY(pinned_acquire(ctx, (size_t)n * 4, &pin));
+    // the pinned buffer may still feed an earlier copy: order behind the stream
+    UT_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    memcpy(pin, ids, (size_t)n * 4);
+    UT_CHECK_HIP(ctx, hipMemcpyAsync(s->ws.ids, pin, (size_t)n * 4, hipMemcpyHostToDevice, ctx->stream));
+    return UT_OK;
+}
+
+// InferenceSession::prefill (model.rs:447-547) into ws.logits / ws.am.
+int32_t prefill_dev(ut_session *s, const int32_t *ids, int64_t n) {
+    ut_model *m = s->m;
+    ut_ctx *ctx = m->ctx;
+    const ut_model_config &c = m->c;
+    if (n <= 0) {
+        set_error(ctx, "empty prompt");
+        return UT_ERR_ARG;
+    }
+    if (s->pos + n > s->cap) {
+        set_error(ctx, "context overflow: %lld + %lld > %lld", (long long)s->pos, (long long)n,
+                  (long long)s->cap);
+        return UT_ERR_CONTEXT_OVERFLOW;
+    }
+    for (int64_t i = 0; i < n; i++)
+        if (ids[i] < 0 || ids[i] >= c.vocab_size) {
+            set_error(ctx, "token id %d out of vocab (%lld)", ids[i], (long long)c.vocab_size);
+            return UT_ERR_BAD_TOKEN;
+        }
+    UT_TRY(ws_reserve(s, n));
+    Workspace &w = s->ws;
+    const int64_t H = c.hidden_size, V = c.vocab_size;
+    UT_TRY(upload_ids(s, ids, n));
+    UT_TRY(launch_embed(ctx, m->embed, w.ids, n, w.x, H));
+    for (size_t li = 0; li < m->layers.size(); li++) UT_TRY(run_layer(s, m->layers[li], w.x, n, s->kv[li]));
+    if (m->has_mtp)
+        UT_CHECK_HIP(ctx, hipMemcpyAsync(s->hidden + s->pos * H, w.x, (size_t)n * H * 4,
+                                         hipMemcpyDeviceToDevice, ctx->stream));
+    s->pos += n;
+    s->tokens.insert(s->tokens.end(), ids, ids + n);
+    UT_TRY(launch_rmsnorm(ctx, w.x, H, m->final_norm, H, c.rms_norm_eps, n, w.normed, H));
+    UT_TRY(mm(s, m->lm_head, w.normed, n, w.logits, V));
+    return launch_argmax(ctx, w.logits, n, V, V, w.am, w.argm);
+}
+
+int32_t read_argmax(ut_session *s, int64_t n, int32_t *out) {
+    ut_ctx *ctx = s->m->ctx;
+    void *pin = nullptr;
+    UT_TRY(pinned_acquire(ctx, (size_t)n * 4, &pin));
+    UT_CHECK_HIP(ctx, hipMemcpyAsync(pin, s->ws.am, (size_t)n * 4, hipMemcpyDeviceToHost, ctx->stream));
+    UT_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    UT_TRY(check_flags(s));
+    memcpy(out, pin, (size_t)n * 4);
+    return UT_OK;
+}
+
+void truncate_session(ut_session *s, int64_t len) {
+    // model.rs:556-564, LayerKvCache::truncate (attention.rs:89-93)
+    for (auto &kv : s->kv)
+        if (len < kv.len) kv.len = len;
+    if (len < s->pos) s->pos = len;
+    if ((int64_t)s->tokens.size() > s->pos) s->tokens.resize((size_t)s->pos);
+}
+
+// draft_logits (mtp.rs:74-133): feed positions fed..pos-1 to the MTP layer,
+// return the argmax of the head's logits for the last one.  chain_hidden:
+// when non-null, run one more chained draft row on (emb(next), hidden =
+// chain_hidden) at position pos (depth > 1; the caller rolls the MTP cache
+// back afterwards).
+int32_t draft_rows(ut_session *s, const std::vector<int32_t> &next_tokens, const float *hidden_rows,
+                   int64_t rows, int32_t *draft_out) {
+    ut_model *m = s->m;
+    ut_ctx *ctx = m->ctx;
+    const ut_model_config &c = m->c;
+    Workspace &w = s->ws;
+    const int64_t H = c.hidden_size, V = c.vocab_size;
+    UT_TRY(ws_reserve(s, rows));
+    UT_TRY(upload_ids(s, next_tokens.data(), rows));
+    UT_TRY(launch_embed(ctx, m->embed, w.ids, rows, w.emb, H));
+    UT_TRY(launch_rmsnorm(ctx, w.emb, H, m->enorm, H, c.rms_norm_eps, rows, w.cat, 2 * H));
+    UT_TRY(launch_rmsnorm(ctx, hidden_rows, H, m->hnorm, H, c.rms_norm_eps, rows, w.cat + H, 2 * H));
+    UT_TRY(mm(s, m->eh_proj, w.cat, rows, w.x, H));
+    UT_TRY(run_layer(s, m->mtp_layer, w.x, rows, s->mtp_kv));
+    UT_TRY(launch_rmsnorm(ctx, w.x + (rows - 1) * H, H, m->mtp_norm, H, c.rms_norm_eps, 1,
+                          w.normed, H));
+    UT_TRY(mm(s, m->mtp_head, w.normed, 1, w.logits, V));
+    UT_TRY(launch_argmax(ctx, w.logits, 1, V, V, w.am, w.argm));
+    return read_argmax(s, 1, draft_out);
+}
+
+}  // namespace
 
 extern "C" {
-int32_t ut_model_create(ut_ctx *ctx, const ut_model_config *, ut_model **out) { if (out) *out = nullptr; set_error(ctx, "not implemented"); return UT_ERR_STATE; }
-int32_t ut_model_set_tensor(ut_model *, const char *, int32_t, const void *, int64_t, const float *, int64_t, int64_t) { return UT_ERR_STATE; }
-int32_t ut_model_finalize(ut_model *) { return UT_ERR_STATE; }
-int32_t ut_model_synthesize(ut_model *, uint64_t, float, int32_t, int32_t) { return UT_ERR_STATE; }
-int64_t ut_model_device_bytes(const ut_model *) { return 0; }
-void ut_model_free(ut_model *) {}
-int32_t ut_session_create(ut_model *, int32_t, ut_session **out) { if (out) *out = nullptr; return UT_ERR_STATE; }
-void ut_session_free(ut_session *) {}
-int32_t ut_session_prefill(ut_session *, const int32_t *, int64_t, float *, int32_t *) { return UT_ERR_STATE; }
-int32_t ut_session_truncate(ut_session *, int64_t) { return UT_ERR_STATE; }
-int64_t ut_session_position(const ut_session *) { return UT_ERR_STATE; }
-int64_t ut_generate_greedy(ut_model *, const int32_t *, int64_t, int64_t, int32_t *) { return UT_ERR_STATE; }
-int64_t ut_generate_mtp(ut_model *, const int32_t *, int64_t, int64_t, int32_t, int32_t *, int64_t *, int64_t *) { return UT_ERR_STATE; }
+
+int32_t ut_model_create(ut_ctx *ctx, const ut_model_config *cfg, ut_model **out) {
+    if (!ctx || !cfg || !out) return UT_ERR_ARG;
+    *out = nullptr;
+    const ut_model_config &c = *cfg;
+    // DeepseekConfig::validate essentials (config.rs:154-216)
+    if (c.vocab_size <= 0 || c.hidden_size <= 0 || c.num_hidden_layers < 0 ||
+        c.num_attention_heads <= 0 || c.kv_lora_rank <= 0 || c.qk_rope_head_dim <= 0 ||
+        c.qk_rope_head_dim % 2 != 0 || c.qk_nope_head_dim <= 0 || c.v_head_dim <= 0 ||
+        c.max_position_embeddings <= 0 || c.num_experts_per_tok <= 0 ||
+        c.num_experts_per_tok > 64 || c.n_group < 0 || c.n_group > 64 ||
+        (c.n_routed_experts > 0 && c.n_routed_experts > 4096) ||
+        (c.first_k_dense_replace < c.num_hidden_layers && c.n_routed_experts <= 0)) {
+        set_error(ctx, "invalid model config");
+        return UT_ERR_ARG;
+    }
+    ut_model *m = new (std::nothrow) ut_model();
+    if (!m) return UT_ERR_OOM;
+    m->ctx = ctx;
+    m->c = c;
+    m->device = ctx->device;
+    *out = m;
+    return UT_OK;
 }
+
+int32_t ut_model_set_tensor(ut_model *m, const char *name, int32_t fmt, const void *payload,
+                            int64_t nbytes, const float *scales, int64_t d0, int64_t d1) {
+    if (!m || !name || !payload || d0 <= 0 || d1 <= 0) {
+        if (m) set_error(m->ctx, "ut_model_set_tensor: bad argument");
+        return UT_ERR_ARG;
+    }
+    if (m->finalized) {
+        set_error(m->ctx, "model already finalized");
+        return UT_ERR_STATE;
+    }
+    DevTensor t;
+    t.d0 = d0;
+    t.d1 = d1;
+    if (d1 == 1 && !scales && (fmt == UT_FMT_F32 || fmt == UT_FMT_INFER)) {
+        if (nbytes != d0 * 4) {
+            set_error(m->ctx, "%s: %lld bytes for a %lld-vector", name, (long long)nbytes, (long long)d0);
+            return UT_ERR_FORMAT;
+        }
+        void *p = nullptr;
+        UT_TRY(dev_alloc(m, (size_t)nbytes, &p));
+        UT_CHECK_HIP(m->ctx, hipMemcpy(p, payload, (size_t)nbytes, hipMemcpyHostToDevice));
+        t.vec = (float *)p;
+    } else {
+        ut_qtensor *q = nullptr;
+        UT_TRY(ut_qtensor_upload(m->ctx, fmt, payload, nbytes, scales, scales ? d0 : 0, d0, d1, &q));
+        m->device_bytes += ut_qtensor_nbytes(q);
+        t.qt = q;
+    }
+    auto it = m->tensors.find(name);
+    if (it != m->tensors.end()) {
+        if (it->second.qt) ut_qtensor_free(it->second.qt);
+        it->second = t;
+    } else {
+        m->tensors.emplace(name, t);
+    }
+    return UT_OK;
+}
+
+int32_t ut_model_finalize(ut_model *m) {
+    if (!m) return UT_ERR_ARG;
+    if (m->finalized) return UT_OK;
+    ut_ctx *ctx = m->ctx;
+    const ut_model_config &c = m->c;
+    const int64_t H = c.hidden_size;
+    UT_CHECK_HIP(ctx, hipSetDevice(m->device));
+    UT_TRY(get_qt(m, "model.embed_tokens.weight", c.vocab_size, H, &m->embed));
+    UT_TRY(get_qt(m, "lm_head.weight", c.vocab_size, H, &m->lm_head));
+    UT_TRY(get_vec(m, "model.norm.weight", H, &m->final_norm));
+    m->layers.assign((size_t)c.num_hidden_layers, LayerW());
+    for (int64_t li = 0; li < c.num_hidden_layers; li++)
+        UT_TRY(load_layer(m, li, li < c.first_k_dense_replace, &m->layers[li]));
+    const std::string p = "model.layers." + std::to_string(c.num_hidden_layers) + ".";
+    if (c.mtp && find(m, p + "eh_proj.weight")) {
+        // MTP head (loader.rs:201-229): its layer is an MoE layer keyed at
+        // index num_hidden_layers
+        m->has_mtp = true;
+        UT_TRY(get_qt(m, p + "eh_proj.weight", H, 2 * H, &m->eh_proj));
+        UT_TRY(get_vec(m, p + "enorm.weight", H, &m->enorm));
+        UT_TRY(get_vec(m, p + "hnorm.weight", H, &m->hnorm));
+        UT_TRY(load_layer(m, c.num_hidden_layers, false, &m->mtp_layer));
+        UT_TRY(get_vec(m, p + "shared_head.norm.weight", H, &m->mtp_norm));
+        UT_TRY(get_qt(m, p + "shared_head.head.weight", c.vocab_size, H, &m->mtp_head));
+    }
+    // RoPE table with the host libm (attention.rs:110-113):
+    // inv_j = theta^(-2j/dim), ang = pos*inv_j, (cos, sin)
+    const int64_t rope = c.qk_rope_head_dim, half = rope / 2, P = c.max_position_embeddings;
+    std::vector<float2> tab((size_t)(P * half));
+    for (int64_t j = 0; j < half; j++) {
+        const float inv = powf(c.rope_theta, -2.0f * (float)j / (float)rope);
+        for (int64_t pos = 0; pos < P; pos++) {
+            const float ang = (float)pos * inv;
+            tab[(size_t)(pos * half + j)] = make_float2(cosf(ang), sinf(ang));
+        }
+    }
+    void *tp = nullptr;
+    UT_TRY(dev_alloc(m, tab.size() * sizeof(float2), &tp));
+    UT_CHECK_HIP(ctx, hipMemcpy(tp, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice));
+    m->rope_table = (float2 *)tp;
+    void *z = nullptr, *o = nullptr;
+    UT_TRY(dev_alloc(m, 16, &z));
+    UT_TRY(dev_alloc(m, 16, &o));
+    const int32_t zs[4] = {0, 0, 0, 0};
+    const float os[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+    UT_CHECK_HIP(ctx, hipMemcpy(z, zs, 16, hipMemcpyHostToDevice));
+    UT_CHECK_HIP(ctx, hipMemcpy(o, os, 16, hipMemcpyHostToDevice));
+    m->zeros = (int32_t *)z;
+    m->ones = (float *)o;
+    m->finalized = true;
+    return UT_OK;
+}
+
+int64_t ut_model_device_bytes(const ut_model *m) { return m ? m->device_bytes : UT_ERR_ARG; }
+
+void ut_model_free(ut_model *m) {
+    if (!m) return;
+    (void)hipSetDevice(m->device);
+    if (m->ctx) (void)hipStreamSynchronize(m->ctx->stream);
+    for (auto &kv : m->tensors)
+        if (kv.second.qt) ut_qtensor_free(kv.second.qt);
+    for (void *p : m->device_allocs) (void)hipFree(p);
+    delete m;
+}
+
+int32_t ut_session_create(ut_model *m, int32_t path, ut_session **out) {
+    if (!m || !out) return UT_ERR_ARG;
+    *out = nullptr;
+    if (!m->finalized) {
+        set_error(m->ctx, "model not finalized");
+        return UT_ERR_STATE;
+    }
+    if (path < 0 || path > 2) {
+        set_error(m->ctx, "bad attention path %d", path);
+        return UT_ERR_ARG;
+    }
+    ut_session *s = new (std::nothrow) ut_session();
+    if (!s) return UT_ERR_OOM;
+    s->m = m;
+    s->path = path;
+    s->cap = m->c.max_position_embeddings;
+    const ut_model_config &c = m->c;
+    const int64_t nl = c.num_hidden_layers + (m->has_mtp ? 1 : 0);
+    const size_t per = (size_t)s->cap * (c.kv_lora_rank + c.qk_rope_head_dim) * 4;
+    const size_t hid = m->has_mtp ? (size_t)s->cap * c.hidden_size * 4 : 0;
+    if (hipMalloc(&s->kv_alloc, per * nl + hid + 256) != hipSuccess) {
+        (void)hipGetLastError();
+        set_error(m->ctx, "KV cache allocation failed");
+        delete s;
+        return UT_ERR_OOM;
+    }
+    char *p = (char *)s->kv_alloc;
+    s->kv.resize((size_t)c.num_hidden_layers);
+    auto carve = [&](KvCache &kv) {
+        kv.latent = (float *)p;
+        kv.krot = (float *)(p + (size_t)s->cap * c.kv_lora_rank * 4);
+        kv.len = 0;
+        p += per;
+    };
+    for (auto &kv : s->kv) carve(kv);
+    if (m->has_mtp) {
+        carve(s->mtp_kv);
+        s->hidden = (float *)p;
+    }
+    int32_t rc = ws_reserve(s, 4);
+    if (rc) {
+        ut_session_free(s);
+        return rc;
+    }
+    *out = s;
+    return UT_OK;
+}
+
+void ut_session_free(ut_session *s) {
+    if (!s) return;
+    (void)hipSetDevice(s->m->device);
+    (void)hipStreamSynchronize(s->m->ctx->stream);
+    if (s->ws.base) (void)hipFree(s->ws.base);
+    if (s->kv_alloc) (void)hipFree(s->kv_alloc);
+    delete s;
+}
+
+int32_t ut_session_prefill(ut_session *s, const int32_t *ids, int64_t n, float *logits_host,
+                           int32_t *argmax_host) {
+    if (!s || (!ids && n > 0)) return UT_ERR_ARG;
+    ut_ctx *ctx = s->m->ctx;
+    UT_TRY(prefill_dev(s, ids, n));
+    if (logits_host) {
+        UT_CHECK_HIP(ctx, hipMemcpyAsync(logits_host, s->ws.logits,
+                                         (size_t)n * s->m->c.vocab_size * 4,
+                                         hipMemcpyDeviceToHost, ctx->stream));
+    }
+    std::vector<int32_t> am((size_t)n);
+    UT_TRY(read_argmax(s, n, am.data()));
+    if (argmax_host) memcpy(argmax_host, am.data(), (size_t)n * 4);
+    return UT_OK;
+}
+
+int32_t ut_session_truncate(ut_session *s, int64_t len) {
+    if (!s || len < 0) return UT_ERR_ARG;
+    truncate_session(s, len);
+    return UT_OK;
+}
+
+int64_t ut_session_position(const ut_session *s) { return s ? s->pos : UT_ERR_ARG; }
+
+int64_t ut_generate_greedy(ut_model *m, const int32_t *prompt, int64_t n, int64_t max_new,
+                           int32_t *out) {
+    // undertow_core::generate, greedy (core/model.rs:139-185)
+    if (!m || !prompt || (max_new > 0 && !out) || max_new < 0) return UT_ERR_ARG;
+    ut_session *s = nullptr;
+    UT_TRY(ut_session_create(m, 0, &s));
+    std::vector<int32_t> am((size_t)n);
+    int32_t rc = prefill_dev(s, prompt, n);
+    if (rc == UT_OK) rc = read_argmax(s, n, am.data());
+    if (rc) { ut_session_free(s); return rc; }
+    int32_t next = am[(size_t)n - 1];
+    int64_t produced = 0;
+    while (produced < max_new) {
+        out[produced++] = next;
+        if (produced == max_new) break;
+        rc = prefill_dev(s, &next, 1);
+        if (rc == UT_ERR_CONTEXT_OVERFLOW) break;  // clean stop at the context end
+        if (rc == UT_OK) rc = read_argmax(s, 1, &next);
+        if (rc) { ut_session_free(s); return rc; }
+    }
+    ut_session_free(s);
+    return produced;
+}
+
+int64_t ut_generate_mtp(ut_model *m, const int32_t *prompt, int64_t n, int64_t max_new,
+                        int32_t depth, int32_t *out, int64_t *drafted, int64_t *accepted) {
+    // speculative_loop (mtp.rs:263-314) with the native draft head
+    if (!m || !prompt || (max_new > 0 && !out) || max_new < 0) return UT_ERR_ARG;
+    if (depth < 1 || depth > 3) {
+        set_error(m->ctx, "MTP depth %d outside 1..3", depth);
+        return UT_ERR_ARG;
+    }
+    if (!m->has_mtp) {
+        set_error(m->ctx, "model has no MTP head; use plain generation");
+        return UT_ERR_STATE;
+    }
+    if (drafted) *drafted = 0;
+    if (accepted) *accepted = 0;
+    if (max_new == 0) return 0;
+    ut_ctx *ctx = m->ctx;
+    const int64_t H = m->c.hidden_size;
+    ut_session *s = nullptr;
+    UT_TRY(ut_session_create(m, 0, &s));
+    std::vector<int32_t> am((size_t)(n > depth + 1 ? n : depth + 1));
+    int32_t rc = prefill_dev(s, prompt, n);
+    if (rc == UT_OK) rc = read_argmax(s, n, am.data());
+    if (rc) { ut_session_free(s); return rc; }
+    int32_t next = am[(size_t)n - 1];
+    int64_t produced = 0, nd = 0, na = 0;
+    std::vector<int32_t> toks, drafts;
+    for (;;) {
+        out[produced++] = next;
+        if (produced >= max_new) break;
+        // ---- draft: feed verified positions fed..pos-1 (mtp.rs:84-121)
+        const int64_t pos = s->pos, fed = s->mtp_fed, pending = pos - fed;
+        toks.clear();
+        for (int64_t i = fed; i < pos; i++) toks.push_back(i + 1 < pos ? s->tokens[(size_t)i + 1] : next);
+        int32_t d = 0;
+        rc = draft_rows(s, toks, s->hidden + fed * H, pending, &d);
+        if (rc) break;
+        s->mtp_fed = pos;
+        drafts.assign(1, d);
+        // ---- chained drafts (depth > 1): MTP layer on its own last hidden state
+        for (int32_t j = 1; j < depth && rc == UT_OK; j++) {
+            // the MTP layer's output row for the last fed position is in ws.x
+            // (hidden input staged in ws.attn, which is free between layers)
+            const int64_t last = (j == 1 ? pending : 1) - 1;
+            UT_CHECK_HIP(ctx, hipMemcpyAsync(s->ws.attn, s->ws.x + last * H, (size_t)H * 4,
+                                             hipMemcpyDeviceToDevice, ctx->stream));
+            toks.assign(1, drafts.back());
+            rc = draft_rows(s, toks, s->ws.attn, 1, &d);
+            drafts.push_back(d);
+        }
+        s->mtp_kv.len = s->mtp_fed;  // speculative MTP rows are never kept
+        if (rc) break;
+        nd += (int64_t)drafts.size();
+        // ---- verify [next, d1..dk] in one prefill
+        const int64_t pos_before = s->pos;
+        toks.assign(1, next);
+        toks.insert(toks.end(), drafts.begin(), drafts.end());
+        rc = prefill_dev(s, toks.data(), (int64_t)toks.size());
+        if (rc == UT_ERR_CONTEXT_OVERFLOW) { rc = UT_OK; break; }
+        if (rc == UT_OK) rc = read_argmax(s, (int64_t)toks.size(), am.data());
+        if (rc) break;
+        int64_t a = 0;
+        bool full = false;
+        while (a < (int64_t)drafts.size() && am[(size_t)a] == drafts[(size_t)a]) {
+            a++;
+            na++;
+            out[produced++] = drafts[(size_t)a - 1];
+            if (produced >= max_new) { full = true; break; }
+        }
+        if (full) break;
+        next = am[(size_t)a];
+        if (a < (int64_t)drafts.size()) truncate_session(s, pos_before + 1 + a);
+    }
+    if (drafted) *drafted = nd;
+    if (accepted) *accepted = na;
+    ut_session_free(s);
+    return rc ? rc : produced;
+}
+
+int32_t ut_model_synthesize(ut_model *m, uint64_t, float, int32_t, int32_t) {
+    if (m) set_error(m->ctx, "ut_model_synthesize: not available yet");
+    return UT_ERR_STATE;
+}
+
+}  // extern "C"
