@@ -68,6 +68,8 @@ const char *ut_last_error(const ut_ctx *ctx);
  * torch.cuda.current_stream().cuda_stream); NULL restores the own stream. */
 int32_t     ut_ctx_set_stream(ut_ctx *ctx, void *stream);
 void       *ut_ctx_stream(ut_ctx *ctx);
+/* Waits for the context's stream; also reports errors detected on device
+ * since the last call (UT_ERR_BAD_EXPERT). */
 int32_t     ut_ctx_synchronize(ut_ctx *ctx);
 /* Per-kernel timing with HIP events on the context stream (bench tooling):
  * while enabled, every kernel the library launches is bracketed by events;
@@ -80,6 +82,7 @@ int32_t     ut_ctx_kernel_time(ut_ctx *ctx, const char *prefix, int64_t *launche
 /* --------------------------------------------------------------- QTensor */
 /* QTensor::from_quantized (undertow-quant/src/qtensor.rs:85-138) /
  * read_qtensor (undertow-io/src/reader.rs:403-444): copies the payload
+ * (host or device memory)
  * (f32 data, int8 codes, or int4 rows of ceil(in/2) bytes, low nibble =
  * even index) and per-output-row scales to HBM.  Validates payload_len
  * against QuantFormat::payload_bytes (qtensor.rs:43-49) and
@@ -136,7 +139,10 @@ void    ut_expert_table_free(ut_expert_table *tbl);
  * out[s] = sum_c weights[s,c] * down(silu(gate x_s) * up x_s) over the
  * choices c in router order (out is overwritten, i.e. starts at zero).
  * Each unique expert's weights are read once for all rows that chose it.
- * Experts must all share one format (int4 or int8). */
+ * Experts must all share one format (int4 or int8).  Expert ids are
+ * validated on device without a host round trip: an id out of range or not
+ * loaded contributes nothing, and UT_ERR_BAD_EXPERT is returned by the next
+ * ut_ctx_synchronize() on this context. */
 int32_t ut_moe_experts(ut_ctx *ctx, const ut_expert_table *tbl, const int32_t *ids_dev,
                        const float *weights_dev, int64_t rows, int32_t top_k, const float *x_dev,
                        float *out_dev);

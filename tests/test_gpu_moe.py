@@ -159,10 +159,13 @@ def test_moe_bad_expert_is_reported(ctx):
     rng = np.random.default_rng(3)
     tbl, _ = make_experts(ctx, rng, INT8, 4, 64, 32)
     ids = np.array([[1, 9]], np.int32)
+    out = tbl.moe_experts(dev(ids), dev(np.ones((1, 2), np.float32)),
+                          dev(np.ones((1, 64), np.float32)))
     with pytest.raises(U.UtError) as ei:
-        tbl.moe_experts(dev(ids), dev(np.ones((1, 2), np.float32)),
-                        dev(np.ones((1, 64), np.float32)))
+        ctx.synchronize()
     assert ei.value.code == U.runtime.UT_ERR_BAD_EXPERT
+    assert np.isfinite(host(out)).all()
+    ctx.synchronize()  # the flag is cleared once reported
 
 
 # --------------------------------------------------------------- attention

@@ -67,6 +67,9 @@ struct ut_ctx {
     std::vector<ut::KernelStat> stats;
     std::vector<ut::PendingTiming> pending;
     int multiprocessors = 256;
+    // Sticky device-side error flag (invalid expert ids), reported by the
+    // next ut_ctx_synchronize().
+    int32_t *dev_err = nullptr;
 };
 
 struct ut_qtensor {
@@ -98,6 +101,9 @@ int32_t pinned_acquire(ut_ctx *ctx, size_t bytes, void **ptr);
 int timing_begin(ut_ctx *ctx, const char *name);
 void timing_end(ut_ctx *ctx, int token);
 int32_t launch_check(ut_ctx *ctx, const char *name);
+// The context's device error flag (allocated on first use) and its check.
+int32_t device_error_flag(ut_ctx *ctx, int32_t **flag);
+int32_t check_device_error(ut_ctx *ctx);
 
 int64_t payload_bytes(int32_t fmt, int64_t out_dim, int64_t in_dim);
 

@@ -113,6 +113,13 @@ namespace {
 
 int64_t hd(const ut_model *m) { return m->c.hidden_size; }
 
+uint64_t mix_host(uint64_t seed, uint64_t i) {
+    uint64_t z = seed * 0x9e3779b97f4a7c15ull + i + 1;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
 int32_t dev_alloc(ut_model *m, size_t bytes, void **p) {
     if (hipMalloc(p, bytes) != hipSuccess) {
         (void)hipGetLastError();
@@ -568,6 +575,168 @@ int32_t draft_rows(ut_session *s, const std::vector<int32_t> &next_tokens, const
     return read_argmax(s, 1, draft_out);
 }
 
+// ---------------------------------------------------------- synthesis ---
+// Counter-based generator (splitmix64 of seed, tensor index, element index):
+// every element is a pure function of its coordinates, so any launch shape
+// produces the same model.
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z += 0x9e3779b97f4a7c15ull;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+__device__ __forceinline__ float u01(uint64_t h) {  // (0, 1)
+    return ((float)(h >> 40) + 0.5f) * (1.0f / 16777216.0f);
+}
+
+__device__ __forceinline__ float normal01(uint64_t key, uint64_t i) {
+    const uint64_t h = mix64(key ^ mix64(i));
+    const float u1 = u01(h), u2 = u01(mix64(h));
+    return sqrtf(-2.0f * logf(u1)) * cosf(6.283185307f * u2);
+}
+
+// kind 0: int4 payload bytes (all 16 codes uniform); 1: int8 codes uniform in
+// [-127, 127]; 2: per-row scales |N(0,std)|/qmax; 3: f32 N(0, std);
+// 4: norm weights 1 + (u - 0.5) * 0.2; 5: bias ramp -0.1 + 0.2 i/(n-1).
+__global__ void k_synth(void *dst, int64_t n, int kind, uint64_t key, float a, float b) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        switch (kind) {
+        case 0: ((uint8_t *)dst)[i] = (uint8_t)(mix64(key ^ mix64(i)) >> 56); break;
+        case 1: ((int8_t *)dst)[i] = (int8_t)((int)((mix64(key ^ mix64(i)) >> 32) % 255u) - 127); break;
+        case 2: ((float *)dst)[i] = fabsf(normal01(key, i)) * a / b; break;
+        case 3: ((float *)dst)[i] = normal01(key, i) * a; break;
+        case 4: ((float *)dst)[i] = 1.0f + (u01(mix64(key ^ mix64(i))) - 0.5f) * 0.2f; break;
+        default: ((float *)dst)[i] = -0.1f + 0.2f * (float)i / (n > 1 ? (float)(n - 1) : 1.0f); break;
+        }
+    }
+}
+
+struct SynthItem {
+    std::string name;
+    int kind;  // 0 matrix, 1 norm vector, 2 bias vector
+    int cls;   // matrices: 0 f32 (router gate), 1 dense, 2 expert
+    int64_t d0, d1;
+};
+
+void synth_layer_list(const ut_model_config &c, int64_t li, bool dense, std::vector<SynthItem> &v) {
+    const int64_t H = c.hidden_size, heads = c.num_attention_heads;
+    const int64_t qh = c.qk_nope_head_dim + c.qk_rope_head_dim;
+    const std::string p = "model.layers." + std::to_string(li) + ".";
+    v.push_back({p + "input_layernorm.weight", 1, 0, H, 1});
+    v.push_back({p + "post_attention_layernorm.weight", 1, 0, H, 1});
+    if (c.q_lora_rank > 0) {
+        v.push_back({p + "self_attn.q_a_proj.weight", 0, 1, c.q_lora_rank, H});
+        v.push_back({p + "self_attn.q_a_layernorm.weight", 1, 0, c.q_lora_rank, 1});
+        v.push_back({p + "self_attn.q_b_proj.weight", 0, 1, heads * qh, c.q_lora_rank});
+    } else {
+        v.push_back({p + "self_attn.q_proj.weight", 0, 1, heads * qh, H});
+    }
+    v.push_back({p + "self_attn.kv_a_proj_with_mqa.weight", 0, 1, c.kv_lora_rank + c.qk_rope_head_dim, H});
+    v.push_back({p + "self_attn.kv_a_layernorm.weight", 1, 0, c.kv_lora_rank, 1});
+    v.push_back({p + "self_attn.kv_b_proj.weight", 0, 1, heads * (c.qk_nope_head_dim + c.v_head_dim), c.kv_lora_rank});
+    v.push_back({p + "self_attn.o_proj.weight", 0, 1, H, heads * c.v_head_dim});
+    if (dense) {
+        v.push_back({p + "mlp.gate_proj.weight", 0, 1, c.intermediate_size, H});
+        v.push_back({p + "mlp.up_proj.weight", 0, 1, c.intermediate_size, H});
+        v.push_back({p + "mlp.down_proj.weight", 0, 1, H, c.intermediate_size});
+        return;
+    }
+    const int64_t E = c.n_routed_experts, I = c.moe_intermediate_size;
+    v.push_back({p + "mlp.gate.weight", 0, 0, E, H});
+    v.push_back({p + "mlp.gate.e_score_correction_bias", 2, 0, E, 1});
+    for (int64_t e = 0; e < E; e++) {
+        const std::string ep = p + "mlp.experts." + std::to_string(e) + ".";
+        v.push_back({ep + "gate_proj.weight", 0, 2, I, H});
+        v.push_back({ep + "up_proj.weight", 0, 2, I, H});
+        v.push_back({ep + "down_proj.weight", 0, 2, H, I});
+    }
+    if (c.n_shared_experts > 0) {
+        const int64_t si = c.n_shared_experts * I;
+        v.push_back({p + "mlp.shared_experts.gate_proj.weight", 0, 1, si, H});
+        v.push_back({p + "mlp.shared_experts.up_proj.weight", 0, 1, si, H});
+        v.push_back({p + "mlp.shared_experts.down_proj.weight", 0, 1, H, si});
+    }
+}
+
+int32_t synthesize_all(ut_model *m, uint64_t seed, float std, int expert_fmt, int dense_fmt) {
+    const ut_model_config &c = m->c;
+    ut_ctx *ctx = m->ctx;
+    const int64_t H = c.hidden_size, L = c.num_hidden_layers;
+    std::vector<SynthItem> items;
+    items.push_back({"model.embed_tokens.weight", 0, 1, c.vocab_size, H});
+    for (int64_t li = 0; li < L; li++) synth_layer_list(c, li, li < c.first_k_dense_replace, items);
+    items.push_back({"model.norm.weight", 1, 0, H, 1});
+    items.push_back({"lm_head.weight", 0, 1, c.vocab_size, H});
+    if (c.mtp) {
+        const std::string p = "model.layers." + std::to_string(L) + ".";
+        synth_layer_list(c, L, false, items);
+        items.push_back({p + "enorm.weight", 1, 0, H, 1});
+        items.push_back({p + "hnorm.weight", 1, 0, H, 1});
+        items.push_back({p + "eh_proj.weight", 0, 1, H, 2 * H});
+        items.push_back({p + "shared_head.norm.weight", 1, 0, H, 1});
+        items.push_back({p + "shared_head.head.weight", 0, 1, c.vocab_size, H});
+    }
+    // one arena for everything, 256-byte aligned pieces
+    auto al = [](int64_t b) { return (b + 255) & ~int64_t(255); };
+    int64_t total = 0;
+    for (auto &it : items) {
+        if (it.kind != 0) { total += al(it.d0 * 4); continue; }
+        int fmt = it.cls == 0 ? UT_FMT_F32 : it.cls == 1 ? dense_fmt : expert_fmt;
+        total += al(payload_bytes(fmt, it.d0, it.d1)) + (fmt == UT_FMT_F32 ? 0 : al(it.d0 * 4));
+    }
+    void *arena = nullptr;
+    UT_TRY(dev_alloc(m, (size_t)total, &arena));
+    char *p = (char *)arena;
+    uint64_t idx = 0;
+    auto fill = [&](void *dst, int64_t n, int kind, float a, float b) -> int32_t {
+        const uint64_t key = mix_host(seed, idx++);
+        int64_t blocks = (n + 255) / 256;
+        if (blocks > 16384) blocks = 16384;
+        hipLaunchKernelGGL(k_synth, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, dst, n,
+                           kind, key, a, b);
+        return launch_check(ctx, "k_synth");
+    };
+    for (auto &it : items) {
+        DevTensor t;
+        t.d0 = it.d0;
+        t.d1 = it.d1;
+        if (it.kind != 0) {
+            UT_TRY(fill(p, it.d0, it.kind == 1 ? 4 : 5, 0.0f, 0.0f));
+            t.vec = (float *)p;
+            p += al(it.d0 * 4);
+        } else {
+            const int fmt = it.cls == 0 ? UT_FMT_F32 : it.cls == 1 ? dense_fmt : expert_fmt;
+            ut_qtensor *q = new (std::nothrow) ut_qtensor();
+            if (!q) return UT_ERR_OOM;
+            q->fmt = fmt;
+            q->out_dim = it.d0;
+            q->in_dim = it.d1;
+            q->row_bytes = payload_bytes(fmt, 1, it.d1);
+            q->owns = false;
+            q->device = m->device;
+            q->payload = p;
+            const int64_t pb = payload_bytes(fmt, it.d0, it.d1);
+            if (fmt == UT_FMT_F32) {
+                UT_TRY(fill(p, it.d0 * it.d1, 3, std, 1.0f));
+            } else {
+                UT_TRY(fill(p, pb, fmt == UT_FMT_INT4 ? 0 : 1, 0.0f, 0.0f));
+            }
+            p += al(pb);
+            if (fmt != UT_FMT_F32) {
+                q->scales = (float *)p;
+                UT_TRY(fill(p, it.d0, 2, std, fmt == UT_FMT_INT4 ? 7.0f : 127.0f));
+                p += al(it.d0 * 4);
+            }
+            t.qt = q;
+        }
+        m->tensors.emplace(it.name, t);
+    }
+    UT_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return UT_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -882,9 +1051,20 @@ int64_t ut_generate_mtp(ut_model *m, const int32_t *prompt, int64_t n, int64_t m
     return rc ? rc : produced;
 }
 
-int32_t ut_model_synthesize(ut_model *m, uint64_t, float, int32_t, int32_t) {
-    if (m) set_error(m->ctx, "ut_model_synthesize: not available yet");
-    return UT_ERR_STATE;
+int32_t ut_model_synthesize(ut_model *m, uint64_t seed, float init_std, int32_t expert_fmt,
+                            int32_t dense_fmt) {
+    if (!m) return UT_ERR_ARG;
+    if (m->finalized || !m->tensors.empty()) {
+        set_error(m->ctx, "ut_model_synthesize needs a fresh model");
+        return UT_ERR_STATE;
+    }
+    if ((expert_fmt != UT_FMT_INT4 && expert_fmt != UT_FMT_INT8) ||
+        (dense_fmt != UT_FMT_INT4 && dense_fmt != UT_FMT_INT8)) {
+        set_error(m->ctx, "synthesize: formats must be int4 or int8");
+        return UT_ERR_ARG;
+    }
+    UT_TRY(synthesize_all(m, seed, init_std, expert_fmt, dense_fmt));
+    return ut_model_finalize(m);
 }
 
 }  // extern "C"

@@ -555,11 +555,10 @@ int32_t ut_moe_experts(ut_ctx *ctx, const ut_expert_table *tbl, const int32_t *i
     const int64_t slots = moe_slots((int)maxM, top_k, tbl->n, -1);
     ScratchPlan plan;
     plan.add(moe_layout(maxM, top_k, slots, tbl->hidden, tbl->inter, tbl->fmt).total);
-    plan.add(4);  // error flag
     std::vector<void *> ptrs;
     UT_TRY(scratch_acquire(ctx, plan, ptrs));
-    int32_t *flag = (int32_t *)ptrs[1];
-    UT_CHECK_HIP(ctx, hipMemsetAsync(flag, 0, 4, ctx->stream));
+    int32_t *flag = nullptr;
+    UT_TRY(device_error_flag(ctx, &flag));
     for (int64_t s0 = 0; s0 < rows; s0 += maxM) {
         MoeCall c;
         c.fmt = tbl->fmt;
@@ -576,13 +575,6 @@ int32_t ut_moe_experts(ut_ctx *ctx, const ut_expert_table *tbl, const int32_t *i
         c.ldo = tbl->hidden;
         c.err_flag = flag;
         UT_TRY(moe_pass(ctx, c, ptrs[0]));
-    }
-    int32_t hflag = 0;
-    UT_CHECK_HIP(ctx, hipMemcpyAsync(&hflag, flag, 4, hipMemcpyDeviceToHost, ctx->stream));
-    UT_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
-    if (hflag) {
-        set_error(ctx, "ut_moe_experts: an expert id is out of range or not loaded");
-        return UT_ERR_BAD_EXPERT;
     }
     return UT_OK;
 }

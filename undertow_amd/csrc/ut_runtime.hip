@@ -92,6 +92,9 @@ static void timing_collect(ut_ctx *ctx, bool wait) {
 }
 
 int timing_begin(ut_ctx *ctx, const char *name) {
+    // every launch goes through here: drop error state left by unrelated
+    // earlier calls so launch_check() reports this launch only
+    (void)hipGetLastError();
     if (!ctx->timing) return -1;
     int idx = -1;
     for (size_t i = 0; i < ctx->stats.size(); i++)
@@ -115,6 +118,29 @@ int timing_begin(ut_ctx *ctx, const char *name) {
 void timing_end(ut_ctx *ctx, int token) {
     if (token < 0 || !ctx->timing || (size_t)token >= ctx->pending.size()) return;
     (void)hipEventRecord(ctx->pending[token].stop, ctx->stream);
+}
+
+int32_t device_error_flag(ut_ctx *ctx, int32_t **flag) {
+    if (!ctx->dev_err) {
+        if (hipMalloc((void **)&ctx->dev_err, 4) != hipSuccess) {
+            (void)hipGetLastError();
+            set_error(ctx, "error flag allocation failed");
+            return UT_ERR_OOM;
+        }
+        UT_CHECK_HIP(ctx, hipMemset(ctx->dev_err, 0, 4));
+    }
+    *flag = ctx->dev_err;
+    return UT_OK;
+}
+
+int32_t check_device_error(ut_ctx *ctx) {
+    if (!ctx->dev_err) return UT_OK;
+    int32_t f = 0;
+    UT_CHECK_HIP(ctx, hipMemcpy(&f, ctx->dev_err, 4, hipMemcpyDeviceToHost));
+    if (!f) return UT_OK;
+    UT_CHECK_HIP(ctx, hipMemset(ctx->dev_err, 0, 4));
+    set_error(ctx, "an expert id was out of range or not loaded (reported by a kernel)");
+    return UT_ERR_BAD_EXPERT;
 }
 
 int32_t launch_check(ut_ctx *ctx, const char *name) {
@@ -214,6 +240,7 @@ void ut_ctx_destroy(ut_ctx *ctx) {
         (void)hipEventDestroy(p.stop);
     }
     if (ctx->scratch.ptr) (void)hipFree(ctx->scratch.ptr);
+    if (ctx->dev_err) (void)hipFree(ctx->dev_err);
     if (ctx->pinned) (void)hipHostFree(ctx->pinned);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
@@ -237,7 +264,7 @@ void *ut_ctx_stream(ut_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
 int32_t ut_ctx_synchronize(ut_ctx *ctx) {
     if (!ctx) return UT_ERR_ARG;
     UT_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
-    return UT_OK;
+    return check_device_error(ctx);
 }
 
 int32_t ut_ctx_enable_timing(ut_ctx *ctx, int32_t on) {
@@ -310,9 +337,10 @@ int32_t ut_qtensor_upload(ut_ctx *ctx, int32_t fmt, const void *payload, int64_t
                   (long long)in_dim);
         return UT_ERR_OOM;
     }
-    hipError_t e = hipMemcpy(q->payload, payload, (size_t)payload_len, hipMemcpyHostToDevice);
+    // hipMemcpyDefault: the source may be host or device memory
+    hipError_t e = hipMemcpy(q->payload, payload, (size_t)payload_len, hipMemcpyDefault);
     if (e == hipSuccess && q->scales)
-        e = hipMemcpy(q->scales, scales, (size_t)out_dim * 4, hipMemcpyHostToDevice);
+        e = hipMemcpy(q->scales, scales, (size_t)out_dim * 4, hipMemcpyDefault);
     if (e != hipSuccess) {
         ut_qtensor_free(q);
         set_error(ctx, "upload failed: %s", hipGetErrorString(e));
@@ -369,6 +397,7 @@ int32_t ut_qtensor_add_scaled_row(ut_ctx *ctx, const ut_qtensor *qt, int64_t row
     }
     unsigned blocks = (unsigned)((qt->in_dim + 255) / 256);
     if (blocks > 1024) blocks = 1024;
+    (void)hipGetLastError();
     hipLaunchKernelGGL(k_add_scaled_row, dim3(blocks), dim3(256), 0, ctx->stream, qt->fmt,
                        (const uint8_t *)qt->payload, qt->scales, qt->in_dim, qt->row_bytes, row,
                        factor, acc_dev);

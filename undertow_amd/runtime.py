@@ -211,14 +211,24 @@ class Context:
 class QTensor:
     """Device QTensor (undertow-quant/src/qtensor.rs:53-71)."""
 
-    def __init__(self, ctx: Context, fmt: int, payload: np.ndarray, scales, out_dim: int,
-                 in_dim: int):
-        payload = np.ascontiguousarray(payload)
-        sc = None if scales is None else np.ascontiguousarray(scales, np.float32)
+    def __init__(self, ctx: Context, fmt: int, payload, scales, out_dim: int, in_dim: int):
+        """payload / scales: numpy arrays (host) or contiguous torch tensors (device)."""
         h = _vp()
-        rc = lib().ut_qtensor_upload(ctx.handle, fmt, payload.ctypes.data, payload.nbytes,
-                                     None if sc is None else sc.ctypes.data,
-                                     0 if sc is None else sc.size, out_dim, in_dim, C.byref(h))
+        if hasattr(payload, "data_ptr"):
+            p_ptr, p_len = payload.data_ptr(), payload.numel() * payload.element_size()
+            s_ptr = None if scales is None else scales.data_ptr()
+            s_len = 0 if scales is None else scales.numel()
+            keep = (payload, scales)
+        else:
+            payload = np.ascontiguousarray(payload)
+            sc = None if scales is None else np.ascontiguousarray(scales, np.float32)
+            p_ptr, p_len = payload.ctypes.data, payload.nbytes
+            s_ptr = None if sc is None else sc.ctypes.data
+            s_len = 0 if sc is None else sc.size
+            keep = (payload, sc)
+        rc = lib().ut_qtensor_upload(ctx.handle, fmt, p_ptr, p_len, s_ptr, s_len, out_dim, in_dim,
+                                     C.byref(h))
+        del keep
         ctx.check(rc)
         self._h = h
         self.ctx = ctx
