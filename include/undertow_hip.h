@@ -64,8 +64,11 @@ typedef struct ut_session ut_session;
 int32_t     ut_ctx_create(int32_t device, ut_ctx **out);
 void        ut_ctx_destroy(ut_ctx *ctx);
 const char *ut_last_error(const ut_ctx *ctx);
-/* Run subsequent work on `stream` (a hipStream_t of the same device, e.g.
- * torch.cuda.current_stream().cuda_stream); NULL restores the own stream. */
+/* Run subsequent work on `stream`, a hipStream_t of the same device (e.g.
+ * torch.cuda.current_stream().cuda_stream); NULL is the null stream.  The
+ * context's own stream is what ut_ctx_stream() returns right after
+ * ut_ctx_create().  Free sessions before their model and models before
+ * their context. */
 int32_t     ut_ctx_set_stream(ut_ctx *ctx, void *stream);
 void       *ut_ctx_stream(ut_ctx *ctx);
 /* Waits for the context's stream; also reports errors detected on device

@@ -151,28 +151,31 @@ struct PlainArgs {
     int accumulate;
 };
 
-// 64 output rows per workgroup: wave w, row group g, slot r -> row
-// blockIdx.x*64 + w*16 + g*4 + r.
+// 16*R output rows per workgroup (R = 4 rows per lane at M <= 2, else 2):
+// wave w, row group g, slot r -> row blockIdx.x*16R + w*4R + g*R + r.
+template <int M> constexpr int plain_rows() { return M <= 2 ? 4 : 2; }
+
 template <int FMT, int M>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
+    constexpr int R = plain_rows<M>();
     __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
-    const int64_t row0 = (int64_t)blockIdx.x * 64 + wave * 16 + g * 4;
-    const uint8_t *rows[kGemvRows];
+    const int64_t row0 = (int64_t)blockIdx.x * (16 * R) + wave * (4 * R) + g * R;
+    const uint8_t *rows[R];
 #pragma unroll
-    for (int r = 0; r < kGemvRows; r++) {
+    for (int r = 0; r < R; r++) {
         int64_t row = row0 + r < a.O ? row0 + r : a.O - 1;
         rows[r] = a.w + row * a.row_bytes;
     }
-    CoreOut<FMT, M> res;
-    gemv_core<FMT, M>(rows, a.K, a.x, lds, res);
+    CoreOut<FMT, M, R> res;
+    gemv_core<FMT, M, R>(rows, a.K, a.x, lds, res);
 #pragma unroll
-    for (int r = 0; r < kGemvRows; r++)
+    for (int r = 0; r < R; r++)
 #pragma unroll
         for (int m = 0; m < M; m++) {
             const int64_t row = row0 + r;
             if (s == 4 * r + m && row < a.O) {
-                float v = core_value<FMT, M>(res, r, m, a.exps, a.scales, row);
+                float v = core_value<FMT, M, R>(res, r, m, a.exps, a.scales, row);
                 float *o = a.out + m * a.ldo + row;
                 *o = a.accumulate ? __fadd_rn(*o, v) : v;
             }
@@ -266,7 +269,8 @@ static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrow
         a.x.ldx = 0;
         a.exps = ga.xd.exps + m0;
     }
-    dim3 grid((unsigned)((w->out_dim + 63) / 64));
+    const int rows_per_wg = 16 * (mrows <= 2 ? 4 : 2);
+    dim3 grid((unsigned)((w->out_dim + rows_per_wg - 1) / rows_per_wg));
     const char *name = FMT == UT_FMT_INT4 ? "gemv_int4" : FMT == UT_FMT_INT8 ? "gemv_int8" : "gemv_f32";
     int tok = timing_begin(ctx, name);
     switch (mrows) {

@@ -77,28 +77,35 @@ __device__ inline int64_t shfl_xor_i64(int64_t v, int off) {
 
 // Result of the core for lane (g, s): the totals of every (r, m), identical
 // on all 16 sub-lanes for int formats; for f32 read them from sub-lane 4r+m.
-template <int FMT, int M> struct CoreOut {
-    int64_t S[kGemvRows][M];
-    float F[kGemvRows][M];
+template <int FMT, int M, int R = kGemvRows> struct CoreOut {
+    int64_t S[R][M];
+    float F[R][M];
 };
 
 // rows[r]: byte pointer of row r (already clamped to a valid row).
-// K: columns (K % (2*16/bytes) alignment is the caller's contract: int4
-// K % 32 == 0, int8 K % 16 == 0, f32 K % 4 == 0, rows 16-byte aligned).
-template <int FMT, int M>
-__device__ __forceinline__ void gemv_core(const uint8_t *const rows[kGemvRows], int64_t K,
-                                          const XSrc &x, uint32_t *lds, CoreOut<FMT, M> &res) {
+// K: columns (the caller's contract: int4 K % 32 == 0, int8 K % 16 == 0,
+// f32 K % 4 == 0, rows 16-byte aligned).
+//
+// The K loop is software-pipelined two steps deep: the weights of steps
+// t+1 and t+2 are in flight while step t computes, and the first loads are
+// issued before the first activation chunk is staged, so the LDS barrier
+// does not drain the memory pipe.
+template <int FMT, int M, int R = kGemvRows>
+__device__ __forceinline__ void gemv_core(const uint8_t *const rows[R], int64_t K, const XSrc &x,
+                                          uint32_t *lds, CoreOut<FMT, M, R> &res) {
     using T = FmtTraits<FMT>;
     constexpr int KC = gemv_chunk_cols<FMT, M>();
     constexpr int PL = T::kPlanes;
-    constexpr int LANE_COLS = T::kStepCols / 16;              // columns per lane per step
+    constexpr int STEP = T::kStepCols;                 // columns per step (16 sub-lanes)
+    constexpr int LANE_COLS = STEP / 16;               // columns per lane per step
+    constexpr int LW = KC / T::kColsPerWord;           // LDS words per plane row
     const int tid = threadIdx.x;
     const int s = tid & 15;
 
-    int32_t acc[kGemvRows][M][PL];
-    float facc[kGemvRows][M];
+    int32_t acc[R][M][PL];
+    float facc[R][M];
 #pragma unroll
-    for (int r = 0; r < kGemvRows; r++)
+    for (int r = 0; r < R; r++)
 #pragma unroll
         for (int m = 0; m < M; m++) {
             facc[r][m] = 0.0f;
@@ -106,22 +113,25 @@ __device__ __forceinline__ void gemv_core(const uint8_t *const rows[kGemvRows], 
             for (int p = 0; p < PL; p++) acc[r][m][p] = 0;
         }
 
-    for (int64_t kc = 0; kc < K; kc += KC) {
-        const int kcn = (int)((K - kc) < KC ? (K - kc) : KC);
+    auto load = [&](uint4 (&w)[R], int64_t col) {
+        if (col < K) {
+            const int64_t boff = col * T::kBytesPerCol2 / 2;
+#pragma unroll
+            for (int r = 0; r < R; r++) w[r] = *(const uint4 *)(rows[r] + boff);
+        }
+    };
+    auto stage = [&](int64_t kc, int kcn) {
         __syncthreads();
-        // ---- stage the chunk's activations
         if constexpr (FMT == UT_FMT_F32) {
             const int n4 = kcn / 4;  // float4 per row
             for (int i = tid; i < M * n4; i += kGemvThreads) {
                 int m = i / n4, c = i - m * n4;
                 float4 v = *(const float4 *)(x.xf + m * x.ldx + kc + 4 * c);
-                *(float4 *)(lds + m * KC + 4 * c) = *(const float4 *)&v;
+                *(float4 *)(lds + m * KC + 4 * c) = v;
             }
         } else {
-            const int wpr = kcn / T::kColsPerWord;   // words per plane row in the chunk
-            const int n4 = wpr / 4;
+            const int n4 = kcn / T::kColsPerWord / 4;  // uint4 per plane row
             const int64_t w0 = kc / T::kColsPerWord;
-            constexpr int LW = KC / T::kColsPerWord;  // LDS words per plane row
             for (int i = tid; i < M * PL * n4; i += kGemvThreads) {
                 int mp = i / n4, c = i - mp * n4;
                 uint4 v = *(const uint4 *)(x.dig + (int64_t)mp * x.KW + w0 + 4 * c);
@@ -129,60 +139,85 @@ __device__ __forceinline__ void gemv_core(const uint8_t *const rows[kGemvRows], 
             }
         }
         __syncthreads();
-        // ---- stream the weights
-        for (int c0 = s * LANE_COLS; c0 < kcn; c0 += T::kStepCols) {
-            uint4 wv[kGemvRows];
-            const int64_t boff = (kc + c0) * T::kBytesPerCol2 / 2;
+    };
+    auto compute = [&](const uint4 (&wv)[R], int c0) {  // c0: column within the chunk
+        if constexpr (FMT == UT_FMT_F32) {
 #pragma unroll
-            for (int r = 0; r < kGemvRows; r++) wv[r] = *(const uint4 *)(rows[r] + boff);
-            if constexpr (FMT == UT_FMT_F32) {
+            for (int m = 0; m < M; m++) {
+                const float4 xv = *(const float4 *)(lds + m * KC + c0);
 #pragma unroll
-                for (int m = 0; m < M; m++) {
-                    const float4 xv = *(const float4 *)(lds + m * KC + c0);
-#pragma unroll
-                    for (int r = 0; r < kGemvRows; r++) {
-                        const float4 wf = *(const float4 *)&wv[r];
-                        float a = facc[r][m];
-                        a = __builtin_fmaf(wf.x, xv.x, a);
-                        a = __builtin_fmaf(wf.y, xv.y, a);
-                        a = __builtin_fmaf(wf.z, xv.z, a);
-                        a = __builtin_fmaf(wf.w, xv.w, a);
-                        facc[r][m] = a;
-                    }
+                for (int r = 0; r < R; r++) {
+                    const float4 wf = *(const float4 *)&wv[r];
+                    float a = facc[r][m];
+                    a = __builtin_fmaf(wf.x, xv.x, a);
+                    a = __builtin_fmaf(wf.y, xv.y, a);
+                    a = __builtin_fmaf(wf.z, xv.z, a);
+                    a = __builtin_fmaf(wf.w, xv.w, a);
+                    facc[r][m] = a;
                 }
-            } else {
-                constexpr int LW = KC / T::kColsPerWord;
-                const int wc = c0 / T::kColsPerWord;  // first word of this lane's columns
+            }
+        } else {
+            const int wc = c0 / T::kColsPerWord;  // first word of this lane's columns
 #pragma unroll
-                for (int m = 0; m < M; m++) {
+            for (int m = 0; m < M; m++) {
 #pragma unroll
-                    for (int p = 0; p < PL; p++) {
-                        const uint4 xv = *(const uint4 *)(lds + (m * PL + p) * LW + wc);
+                for (int p = 0; p < PL; p++) {
+                    const uint4 xv = *(const uint4 *)(lds + (m * PL + p) * LW + wc);
 #pragma unroll
-                        for (int r = 0; r < kGemvRows; r++) {
-                            int a = acc[r][m][p];
-                            if constexpr (FMT == UT_FMT_INT4) {
-                                a = __builtin_amdgcn_sdot8((int)wv[r].x, (int)xv.x, a, false);
-                                a = __builtin_amdgcn_sdot8((int)wv[r].y, (int)xv.y, a, false);
-                                a = __builtin_amdgcn_sdot8((int)wv[r].z, (int)xv.z, a, false);
-                                a = __builtin_amdgcn_sdot8((int)wv[r].w, (int)xv.w, a, false);
-                            } else {
-                                a = __builtin_amdgcn_sdot4((int)wv[r].x, (int)xv.x, a, false);
-                                a = __builtin_amdgcn_sdot4((int)wv[r].y, (int)xv.y, a, false);
-                                a = __builtin_amdgcn_sdot4((int)wv[r].z, (int)xv.z, a, false);
-                                a = __builtin_amdgcn_sdot4((int)wv[r].w, (int)xv.w, a, false);
-                            }
-                            acc[r][m][p] = a;
+                    for (int r = 0; r < R; r++) {
+                        int a = acc[r][m][p];
+                        if constexpr (FMT == UT_FMT_INT4) {
+                            a = __builtin_amdgcn_sdot8((int)wv[r].x, (int)xv.x, a, false);
+                            a = __builtin_amdgcn_sdot8((int)wv[r].y, (int)xv.y, a, false);
+                            a = __builtin_amdgcn_sdot8((int)wv[r].z, (int)xv.z, a, false);
+                            a = __builtin_amdgcn_sdot8((int)wv[r].w, (int)xv.w, a, false);
+                        } else {
+                            a = __builtin_amdgcn_sdot4((int)wv[r].x, (int)xv.x, a, false);
+                            a = __builtin_amdgcn_sdot4((int)wv[r].y, (int)xv.y, a, false);
+                            a = __builtin_amdgcn_sdot4((int)wv[r].z, (int)xv.z, a, false);
+                            a = __builtin_amdgcn_sdot4((int)wv[r].w, (int)xv.w, a, false);
                         }
+                        acc[r][m][p] = a;
                     }
                 }
             }
+        }
+    };
+
+    const int64_t nsteps = (K + STEP - 1) / STEP;
+    const int64_t lane_col = (int64_t)s * LANE_COLS;
+    uint4 wa[R], wb[R];
+    load(wa, lane_col);
+    load(wb, lane_col + STEP);
+    int64_t kc = 0, chunk_end = 0;
+    for (int64_t t = 0; t < nsteps; t += 2) {
+        // step t (buffer a)
+        if (t * STEP >= chunk_end) {
+            kc = t * STEP;
+            const int kcn = (int)((K - kc) < KC ? (K - kc) : KC);
+            chunk_end = kc + kcn;
+            stage(kc, kcn);
+        }
+        const int64_t ca = t * STEP + lane_col;
+        if (ca < K) compute(wa, (int)(ca - kc));
+        load(wa, ca + 2 * STEP);
+        // step t+1 (buffer b)
+        if (t + 1 < nsteps) {
+            if ((t + 1) * STEP >= chunk_end) {
+                kc = (t + 1) * STEP;
+                const int kcn = (int)((K - kc) < KC ? (K - kc) : KC);
+                chunk_end = kc + kcn;
+                stage(kc, kcn);
+            }
+            const int64_t cb = (t + 1) * STEP + lane_col;
+            if (cb < K) compute(wb, (int)(cb - kc));
+            load(wb, cb + 2 * STEP);
         }
     }
 
     // ---- reduce across the 16 sub-lanes of the row group
 #pragma unroll
-    for (int r = 0; r < kGemvRows; r++)
+    for (int r = 0; r < R; r++)
 #pragma unroll
         for (int m = 0; m < M; m++) {
             if constexpr (FMT == UT_FMT_F32) {
@@ -214,8 +249,8 @@ __device__ __forceinline__ float int_total_to_f32(int64_t S, int32_t e, float sc
 
 // Value of (r, m) from the core result: for f32 read sub-lane 4r+m (callers
 // run this on that lane), for int formats every sub-lane holds it.
-template <int FMT, int M>
-__device__ __forceinline__ float core_value(const CoreOut<FMT, M> &res, int r, int m,
+template <int FMT, int M, int R>
+__device__ __forceinline__ float core_value(const CoreOut<FMT, M, R> &res, int r, int m,
                                             const int32_t *exps, const float *scales,
                                             int64_t row) {
     if constexpr (FMT == UT_FMT_F32) return res.F[r][m];

@@ -5,6 +5,8 @@
 
 namespace ut {
 
+constexpr int kGateUpRowsPerWG = 16;  // h rows per gate/up workgroup
+
 // Device arrays of per-expert pointers (indexed by expert id).
 struct ExpertPtrs {
     const uint8_t *const *gate_w = nullptr;

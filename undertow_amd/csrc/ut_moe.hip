@@ -7,11 +7,11 @@
 //                  top-k by rank (value desc, lowest index first), weights
 //   k_moe_plan     unique experts in first-appearance order -> slots
 //   k_digitize     activation digits of x (shared by every expert)
-//   k_moe_gate_up  grid (I/32, slots): gate and up rows of one expert in the
+//   k_moe_gate_up  grid (I/16, slots): gate and up rows of one expert in the
 //                  same lanes, h = silu(g)*u written per (slot, row), plus
 //                  per-workgroup max|h| partials
 //   k_digitize     digits of h per (slot, row)
-//   k_moe_down     grid (H/64, slots): d = down(h) per (slot, row)
+//   k_moe_down     grid (H/64 or H/32, slots): d = down(h) per (slot, row)
 //   k_moe_combine  out[s] = sum_c w[s,c]*d[slot(s,c), s] in router order
 // Every expert's weights are read once per pass whatever rows chose it;
 // the row dimension rides along in the same instructions.
@@ -156,8 +156,9 @@ struct GateUpArgs {
     int ntiles;
 };
 
-// 32 h-rows per workgroup: wave w, row group g -> h rows o = tile*32 +
-// w*8 + g*2 + j (j = 0, 1); slots r = j read gate row o, r = 2 + j up row o.
+// 16 h-rows per workgroup: wave w, row group g -> h row o = tile*16 +
+// w*4 + g; row slot 0 reads gate row o, slot 1 up row o, so both land in the
+// same lanes and h = silu(g)*u is formed in registers.
 template <int FMT, int M>
 __global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up(GateUpArgs a) {
     const int u = blockIdx.y;
@@ -169,40 +170,31 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up(GateUpArgs a) {
     const int e = a.uniq[u];
     const uint8_t *gw = a.tbl.gate_w[e], *uw = a.tbl.up_w[e];
     const float *gsc = a.tbl.gate_s[e], *usc = a.tbl.up_s[e];
-    const int64_t obase = (int64_t)blockIdx.x * 32 + wave * 8 + g * 2;
-    const uint8_t *rows[kGemvRows];
+    const int64_t o = (int64_t)blockIdx.x * kGateUpRowsPerWG + wave * 4 + g;
+    const int64_t oc = o < a.I ? o : a.I - 1;
+    const uint8_t *rows[2] = {gw + oc * a.row_bytes, uw + oc * a.row_bytes};
+    CoreOut<FMT, M, 2> res;
+    gemv_core<FMT, M, 2>(rows, a.H, a.x, lds, res);
 #pragma unroll
-    for (int r = 0; r < kGemvRows; r++) {
-        int64_t o = obase + (r & 1);
-        if (o >= a.I) o = a.I - 1;
-        rows[r] = (r < 2 ? gw : uw) + o * a.row_bytes;
-    }
-    CoreOut<FMT, M> res;
-    gemv_core<FMT, M>(rows, a.H, a.x, lds, res);
-#pragma unroll
-    for (int j = 0; j < 2; j++)
-#pragma unroll
-        for (int m = 0; m < M; m++) {
-            const int64_t o = obase + j;
-            // f32: gate value lives on sub-lane 4j+m, up value on 4(2+j)+m
-            float gv, uv;
-            if constexpr (FMT == UT_FMT_F32) {
-                float up_here = res.F[2 + j][m];
-                uv = __shfl(up_here, (lane & ~15) | (4 * (2 + j) + m), 64);
-                gv = res.F[j][m];
-            }
-            if (s == 4 * j + m && o < a.I) {
-                if constexpr (FMT != UT_FMT_F32) {
-                    gv = int_total_to_f32(res.S[j][m], a.exps[m], gsc[o]);
-                    uv = int_total_to_f32(res.S[2 + j][m], a.exps[m], usc[o]);
-                }
-                // silu(g) * u (undertow-quant/src/lib.rs:121; model.rs:241-247)
-                float sg = gv / (1.0f + expf(-gv));
-                float hv = __fmul_rn(sg, uv);
-                a.h[((int64_t)u * M + m) * a.I + o] = hv;
-                atomicMax(&wg_max[m], __float_as_uint(fabsf(hv)));
-            }
+    for (int m = 0; m < M; m++) {
+        // f32: the gate value lives on sub-lane m, the up value on 4 + m
+        float gv = 0.0f, uv = 0.0f;
+        if constexpr (FMT == UT_FMT_F32) {
+            uv = __shfl(res.F[1][m], (lane & ~15) | (4 + m), 64);
+            gv = res.F[0][m];
         }
+        if (s == m && o < a.I) {
+            if constexpr (FMT != UT_FMT_F32) {
+                gv = int_total_to_f32(res.S[0][m], a.exps[m], gsc[o]);
+                uv = int_total_to_f32(res.S[1][m], a.exps[m], usc[o]);
+            }
+            // silu(g) * u (undertow-quant/src/lib.rs:121; model.rs:241-247)
+            float sg = gv / (1.0f + expf(-gv));
+            float hv = __fmul_rn(sg, uv);
+            a.h[((int64_t)u * M + m) * a.I + o] = hv;
+            atomicMax(&wg_max[m], __float_as_uint(fabsf(hv)));
+        }
+    }
     __syncthreads();
     if (tid < M) a.hmax_parts[((int64_t)u * M + tid) * a.ntiles + blockIdx.x] = wg_max[tid];
 }
@@ -219,8 +211,12 @@ struct DownArgs {
     float *d;                 // [slots][M][H]
 };
 
+// Rows per lane: 4 at M <= 2 (more activation reuse), 2 above (registers).
+template <int M> constexpr int down_rows() { return M <= 2 ? 4 : 2; }
+
 template <int FMT, int M>
 __global__ __launch_bounds__(kGemvThreads) void k_moe_down(DownArgs a) {
+    constexpr int R = down_rows<M>();
     const int u = blockIdx.y;
     if (u >= *a.count) return;
     __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
@@ -228,25 +224,25 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_down(DownArgs a) {
     const int e = a.uniq[u];
     const uint8_t *dw = a.tbl.down_w[e];
     const float *dsc = a.tbl.down_s[e];
-    const int64_t row0 = (int64_t)blockIdx.x * 64 + wave * 16 + g * 4;
-    const uint8_t *rows[kGemvRows];
+    const int64_t row0 = (int64_t)blockIdx.x * (16 * R) + wave * (4 * R) + g * R;
+    const uint8_t *rows[R];
 #pragma unroll
-    for (int r = 0; r < kGemvRows; r++) {
+    for (int r = 0; r < R; r++) {
         int64_t o = row0 + r < a.H ? row0 + r : a.H - 1;
         rows[r] = dw + o * a.row_bytes;
     }
     XSrc xs = a.x;
     if constexpr (FMT == UT_FMT_F32) xs.xf = a.x.xf + u * a.x_slot_stride;
     else xs.dig = a.x.dig + u * a.x_slot_stride;
-    CoreOut<FMT, M> res;
-    gemv_core<FMT, M>(rows, a.I, xs, lds, res);
+    CoreOut<FMT, M, R> res;
+    gemv_core<FMT, M, R>(rows, a.I, xs, lds, res);
 #pragma unroll
-    for (int r = 0; r < kGemvRows; r++)
+    for (int r = 0; r < R; r++)
 #pragma unroll
         for (int m = 0; m < M; m++) {
             const int64_t o = row0 + r;
             if (s == 4 * r + m && o < a.H) {
-                float v = core_value<FMT, M>(res, r, m, a.exps + u * M, dsc, o);
+                float v = core_value<FMT, M, R>(res, r, m, a.exps + u * M, dsc, o);
                 a.d[((int64_t)u * M + m) * a.H + o] = v;
             }
         }
@@ -289,7 +285,7 @@ ScratchLayout moe_layout(int64_t M, int64_t k, int64_t slots, int64_t H, int64_t
     auto take = [&](size_t bytes) { size_t off = L.total; L.total += (bytes + 255) & ~size_t(255); return off; };
     const int xflags = fmt == UT_FMT_F32 ? 0 : xdigit_flags_for(fmt, H);
     const int hflags = fmt == UT_FMT_F32 ? 0 : xdigit_flags_for(fmt, I);
-    const int64_t ntiles = (I + 31) / 32;
+    const int64_t ntiles = (I + kGateUpRowsPerWG - 1) / kGateUpRowsPerWG;
     L.count = take(4);
     L.uniq = take((size_t)slots * 4);
     L.choice = take((size_t)M * k * 4);
@@ -383,7 +379,8 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
         a.exps = hexps;
         a.d = d;
         tok = timing_begin(ctx, FMT == UT_FMT_INT4 ? "moe_down_int4" : FMT == UT_FMT_INT8 ? "moe_down_int8" : "moe_down_f32");
-        hipLaunchKernelGGL((k_moe_down<FMT, M>), dim3((unsigned)((c.H + 63) / 64), (unsigned)slots),
+        constexpr int DR = 16 * down_rows<M>();
+        hipLaunchKernelGGL((k_moe_down<FMT, M>), dim3((unsigned)((c.H + DR - 1) / DR), (unsigned)slots),
                            dim3(kGemvThreads), 0, ctx->stream, a);
         timing_end(ctx, tok);
         UT_TRY(launch_check(ctx, "k_moe_down"));

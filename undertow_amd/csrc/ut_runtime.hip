@@ -250,7 +250,7 @@ const char *ut_last_error(const ut_ctx *ctx) { return ctx ? ctx->err.c_str() : "
 
 int32_t ut_ctx_set_stream(ut_ctx *ctx, void *stream) {
     if (!ctx) return UT_ERR_ARG;
-    hipStream_t s = stream ? (hipStream_t)stream : ctx->own_stream;
+    hipStream_t s = (hipStream_t)stream;  // NULL: the device's null stream
     if (s != ctx->stream) {
         // order the switch: work on the old stream completes first
         UT_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));

@@ -15,6 +15,7 @@ missing library raises ``RuntimeError``.
 from __future__ import annotations
 
 import ctypes as C
+import weakref
 from pathlib import Path
 from typing import Optional
 
@@ -167,12 +168,18 @@ class Context:
             raise UtError(rc, f"ut_ctx_create({device}) failed")
         self._h = h
         self.device = device
+        self._models = weakref.WeakSet()
+        self.own_stream = lib().ut_ctx_stream(self._h)
         if bind_torch_stream:
             torch = _torch()
-            s = torch.cuda.current_stream(device).cuda_stream
+            s = torch.cuda.current_stream(device).cuda_stream  # 0: the null stream
             self.check(lib().ut_ctx_set_stream(self._h, s))
 
     def __del__(self):
+        # children first: finalizers of objects in a reference cycle run in
+        # any order, and a model or session must not outlive its context
+        for m in list(getattr(self, "_models", ())):
+            m._release()
         h = getattr(self, "_h", None)
         if h and _lib is not None:
             _lib.ut_ctx_destroy(h)
@@ -349,12 +356,19 @@ class Model:
         h = _vp()
         ctx.check(lib().ut_model_create(ctx.handle, C.byref(self._cfg), C.byref(h)))
         self._h = h
+        self._sessions = weakref.WeakSet()
+        ctx._models.add(self)
 
-    def __del__(self):
+    def _release(self):
+        for s in list(getattr(self, "_sessions", ())):
+            s._release()
         h = getattr(self, "_h", None)
         if h and _lib is not None:
             _lib.ut_model_free(h)
-            self._h = None
+        self._h = None
+
+    def __del__(self):
+        self._release()
 
     def set_tensor(self, name: str, fmt: int, payload: np.ndarray, scales, shape) -> None:
         payload = np.ascontiguousarray(payload)
@@ -407,12 +421,16 @@ class Session:
         h = _vp()
         model.ctx.check(lib().ut_session_create(model._h, path, C.byref(h)))
         self._h = h
+        model._sessions.add(self)
 
-    def __del__(self):
+    def _release(self):
         h = getattr(self, "_h", None)
         if h and _lib is not None:
             _lib.ut_session_free(h)
-            self._h = None
+        self._h = None
+
+    def __del__(self):
+        self._release()
 
     def prefill(self, ids, want_logits: bool = True):
         ids = np.ascontiguousarray(ids, np.int32)
