@@ -67,8 +67,8 @@ const char *ut_last_error(const ut_ctx *ctx);
 /* Run subsequent work on `stream`, a hipStream_t of the same device (e.g.
  * torch.cuda.current_stream().cuda_stream); NULL is the null stream.  The
  * context's own stream is what ut_ctx_stream() returns right after
- * ut_ctx_create().  Free sessions before their model and models before
- * their context. */
+ * ut_ctx_create().  Handles may be released in any order: a session keeps
+ * its model alive and a model its context until they are released. */
 int32_t     ut_ctx_set_stream(ut_ctx *ctx, void *stream);
 void       *ut_ctx_stream(ut_ctx *ctx);
 /* Waits for the context's stream; also reports errors detected on device

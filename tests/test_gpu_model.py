@@ -135,3 +135,20 @@ def test_context_overflow_and_bad_token(ctx):
     # generation stops cleanly at the context end (pipeline.rs:450-459)
     out = m.generate_greedy(list(range(28)), 10)
     assert len(out) == 5
+
+
+def test_handles_release_in_any_order():
+    """Sessions keep their model and models their context alive, so handles
+    can be released in any order (Python finalizers of a reference cycle)."""
+    import undertow_amd as U
+    c = U.Context(0)
+    m = gpu_model(c, checkpoint())
+    s = m.session()
+    L = U.lib()
+    L.ut_model_free(m._h)
+    m._h = None
+    L.ut_ctx_destroy(c._h)
+    c._h = None
+    logits = s.prefill([1, 2, 3])  # model and context are still alive
+    assert np.isfinite(logits).all()
+    s._release()

@@ -70,6 +70,9 @@ struct ut_ctx {
     // Sticky device-side error flag (invalid expert ids), reported by the
     // next ut_ctx_synchronize().
     int32_t *dev_err = nullptr;
+    // Handle lifetime: models hold a reference on their context and
+    // sessions on their model, so the handles may be released in any order.
+    int refs = 1;
 };
 
 struct ut_qtensor {
@@ -101,6 +104,8 @@ int32_t pinned_acquire(ut_ctx *ctx, size_t bytes, void **ptr);
 int timing_begin(ut_ctx *ctx, const char *name);
 void timing_end(ut_ctx *ctx, int token);
 int32_t launch_check(ut_ctx *ctx, const char *name);
+void ctx_retain(ut_ctx *ctx);
+void ctx_release(ut_ctx *ctx);
 // The context's device error flag (allocated on first use) and its check.
 int32_t device_error_flag(ut_ctx *ctx, int32_t **flag);
 int32_t check_device_error(ut_ctx *ctx);

@@ -76,6 +76,7 @@ struct ut_model {
     std::vector<void *> device_allocs;
     int64_t device_bytes = 0;
     int device = 0;
+    int refs = 1;  // the creator + one per live session
 };
 
 namespace {
@@ -761,6 +762,7 @@ int32_t ut_model_create(ut_ctx *ctx, const ut_model_config *cfg, ut_model **out)
     m->ctx = ctx;
     m->c = c;
     m->device = ctx->device;
+    ctx_retain(ctx);
     *out = m;
     return UT_OK;
 }
@@ -859,13 +861,15 @@ int32_t ut_model_finalize(ut_model *m) {
 int64_t ut_model_device_bytes(const ut_model *m) { return m ? m->device_bytes : UT_ERR_ARG; }
 
 void ut_model_free(ut_model *m) {
-    if (!m) return;
+    if (!m || --m->refs > 0) return;  // live sessions keep the model
     (void)hipSetDevice(m->device);
-    if (m->ctx) (void)hipStreamSynchronize(m->ctx->stream);
+    (void)hipStreamSynchronize(m->ctx->stream);
     for (auto &kv : m->tensors)
         if (kv.second.qt) ut_qtensor_free(kv.second.qt);
     for (void *p : m->device_allocs) (void)hipFree(p);
+    ut_ctx *ctx = m->ctx;
     delete m;
+    ctx_release(ctx);
 }
 
 int32_t ut_session_create(ut_model *m, int32_t path, ut_session **out) {
@@ -882,6 +886,7 @@ int32_t ut_session_create(ut_model *m, int32_t path, ut_session **out) {
     ut_session *s = new (std::nothrow) ut_session();
     if (!s) return UT_ERR_OOM;
     s->m = m;
+    m->refs++;
     s->path = path;
     s->cap = m->c.max_position_embeddings;
     const ut_model_config &c = m->c;
@@ -922,7 +927,9 @@ void ut_session_free(ut_session *s) {
     (void)hipStreamSynchronize(s->m->ctx->stream);
     if (s->ws.base) (void)hipFree(s->ws.base);
     if (s->kv_alloc) (void)hipFree(s->kv_alloc);
+    ut_model *m = s->m;
     delete s;
+    ut_model_free(m);  // drops the session's reference
 }
 
 int32_t ut_session_prefill(ut_session *s, const int32_t *ids, int64_t n, float *logits_host,

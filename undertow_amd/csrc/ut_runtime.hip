@@ -231,8 +231,14 @@ int32_t ut_ctx_create(int32_t device, ut_ctx **out) {
     return UT_OK;
 }
 
-void ut_ctx_destroy(ut_ctx *ctx) {
-    if (!ctx) return;
+void ut_ctx_destroy(ut_ctx *ctx) { ctx_release(ctx); }
+
+}  // extern "C"
+
+void ut::ctx_retain(ut_ctx *ctx) { ctx->refs++; }
+
+void ut::ctx_release(ut_ctx *ctx) {
+    if (!ctx || --ctx->refs > 0) return;
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     for (auto &p : ctx->pending) {
@@ -245,6 +251,8 @@ void ut_ctx_destroy(ut_ctx *ctx) {
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
 }
+
+extern "C" {
 
 const char *ut_last_error(const ut_ctx *ctx) { return ctx ? ctx->err.c_str() : "null context"; }
 

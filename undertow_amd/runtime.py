@@ -15,7 +15,6 @@ missing library raises ``RuntimeError``.
 from __future__ import annotations
 
 import ctypes as C
-import weakref
 from pathlib import Path
 from typing import Optional
 
@@ -168,7 +167,6 @@ class Context:
             raise UtError(rc, f"ut_ctx_create({device}) failed")
         self._h = h
         self.device = device
-        self._models = weakref.WeakSet()
         self.own_stream = lib().ut_ctx_stream(self._h)
         if bind_torch_stream:
             torch = _torch()
@@ -176,10 +174,8 @@ class Context:
             self.check(lib().ut_ctx_set_stream(self._h, s))
 
     def __del__(self):
-        # children first: finalizers of objects in a reference cycle run in
-        # any order, and a model or session must not outlive its context
-        for m in list(getattr(self, "_models", ())):
-            m._release()
+        # the library reference-counts contexts, models and sessions, so
+        # finalizers may run in any order (objects in a reference cycle)
         h = getattr(self, "_h", None)
         if h and _lib is not None:
             _lib.ut_ctx_destroy(h)
@@ -356,12 +352,8 @@ class Model:
         h = _vp()
         ctx.check(lib().ut_model_create(ctx.handle, C.byref(self._cfg), C.byref(h)))
         self._h = h
-        self._sessions = weakref.WeakSet()
-        ctx._models.add(self)
 
     def _release(self):
-        for s in list(getattr(self, "_sessions", ())):
-            s._release()
         h = getattr(self, "_h", None)
         if h and _lib is not None:
             _lib.ut_model_free(h)
@@ -421,7 +413,6 @@ class Session:
         h = _vp()
         model.ctx.check(lib().ut_session_create(model._h, path, C.byref(h)))
         self._h = h
-        model._sessions.add(self)
 
     def _release(self):
         h = getattr(self, "_h", None)
