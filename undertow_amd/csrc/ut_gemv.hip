@@ -41,44 +41,88 @@ int xdigit_flags_for(int32_t fmt, int64_t K) {
 // One workgroup per activation row.  x~ = rint(x * 2^(22-E)) with
 // max|x| < 2^E (frexp), so |x~| <= 2^22 and six balanced base-16 digits
 // (or three base-256 digits) represent it exactly.
-__global__ __launch_bounds__(256) void k_digitize(const float *__restrict__ x, int64_t ldx,
-                                                  int64_t K, const uint32_t *__restrict__ rowmax,
-                                                  int32_t nparts, int32_t *__restrict__ exps,
-                                                  uint32_t *__restrict__ dig4,
-                                                  uint32_t *__restrict__ dig8,
-                                                  int32_t *__restrict__ xt,
-                                                  const int32_t *__restrict__ slot_count,
-                                                  int rows_per_slot) {
-    const int64_t m = blockIdx.x;
-    if (slot_count && (int)(m / rows_per_slot) >= *slot_count) return;
-    const float *xr = x + m * ldx;
-    __shared__ uint32_t red[256];
-    uint32_t mx = 0;
-    if (rowmax) {
-        for (int i = threadIdx.x; i < nparts; i += 256) mx = max(mx, rowmax[m * nparts + i]);
-    } else {
-        for (int64_t k = threadIdx.x; k < K; k += 256) mx = max(mx, __float_as_uint(fabsf(xr[k])));
-    }
-    red[threadIdx.x] = mx;
+//
+// With norm_w set, the row is first rms-normalised exactly as
+// undertow-quant/src/lib.rs:91-100 (mean of squares in f64,
+// r = 1/sqrt((float)ms + eps), v = (x*r)*w) and the normalised row is what
+// gets digitised (and optionally written out as f32): one launch instead of
+// a norm kernel plus a digitise kernel per consumer.
+constexpr int kRowLds = 16384;  // rows up to this width are staged in LDS
+
+struct RowDigArgs {
+    const float *x;
+    int64_t ldx, K;
+    const float *norm_w;
+    float eps;
+    float *out;
+    int64_t ldo;
+    const uint32_t *rowmax;  // optional [rows][nparts] max|x| bits
+    int32_t nparts;
+    const int32_t *slot_count;
+    int rows_per_slot;
+    int32_t *exps;
+    uint32_t *dig4, *dig8;
+    int32_t *xt;
+};
+
+template <typename T, typename Op>
+__device__ __forceinline__ T block_reduce(T v, Op op, T *red4) {
+    for (int off = 32; off >= 1; off >>= 1) v = op(v, __shfl_xor(v, off, 64));
+    if ((threadIdx.x & 63) == 0) red4[threadIdx.x >> 6] = v;
     __syncthreads();
-    for (int off = 128; off > 0; off >>= 1) {
-        if (threadIdx.x < off) red[threadIdx.x] = max(red[threadIdx.x], red[threadIdx.x + off]);
-        __syncthreads();
+    T r = op(op(red4[0], red4[1]), op(red4[2], red4[3]));
+    __syncthreads();
+    return r;
+}
+
+__global__ __launch_bounds__(256) void k_rowdig(RowDigArgs a) {
+    extern __shared__ float row[];
+    __shared__ double redd[4];
+    __shared__ uint32_t redu[4];
+    const int64_t m = blockIdx.x;
+    if (a.slot_count && (int)(m / a.rows_per_slot) >= *a.slot_count) return;
+    const int tid = threadIdx.x;
+    const int64_t K = a.K;
+    const float *xr = a.x + m * a.ldx;
+    const bool staged = K <= kRowLds;
+    float r = 1.0f;
+    if (a.norm_w) {
+        double acc = 0.0;
+        for (int64_t i = tid; i < K; i += 256) {
+            const double v = (double)xr[i];
+            acc += v * v;
+        }
+        acc = block_reduce(acc, [](double p, double q) { return p + q; }, redd);
+        r = 1.0f / sqrtf(__fadd_rn((float)(acc / (double)K), a.eps));
     }
-    mx = red[0];
+    auto val = [&](int64_t i) -> float {
+        return a.norm_w ? __fmul_rn(__fmul_rn(xr[i], r), a.norm_w[i]) : xr[i];
+    };
+    uint32_t mx = 0;
+    for (int64_t i = tid; i < K; i += 256) {
+        const float v = val(i);
+        if (staged) row[i] = v;
+        if (a.out) a.out[m * a.ldo + i] = v;
+        mx = max(mx, __float_as_uint(fabsf(v)));
+    }
+    if (a.rowmax) {
+        mx = 0;
+        for (int i = tid; i < a.nparts; i += 256) mx = max(mx, a.rowmax[m * a.nparts + i]);
+    }
+    mx = block_reduce(mx, [](uint32_t p, uint32_t q) { return p > q ? p : q; }, redu);
     // non-finite rows (|x| bits >= +inf) produce NaN outputs downstream
     const bool bad = mx >= 0x7f800000u;
     int E = 0;
     if (!bad && mx != 0) (void)frexpf(__uint_as_float(mx), &E);
     const int sh = 22 - E;
-    if (threadIdx.x == 0) exps[m] = bad ? INT32_MIN : E - 22;
+    if (tid == 0) a.exps[m] = bad ? INT32_MIN : E - 22;
     auto xq = [&](int64_t k) -> int32_t {
         if (bad || k >= K) return 0;
-        return (int32_t)rintf(ldexpf(xr[k], sh));
+        return (int32_t)rintf(ldexpf(staged ? row[k] : val(k), sh));
     };
-    if (dig4) {
+    if (a.dig4) {
         const int64_t K8 = (K + 7) / 8;
-        for (int64_t c = threadIdx.x; c < K8; c += 256) {
+        for (int64_t c = tid; c < K8; c += 256) {
             uint32_t w[6] = {0, 0, 0, 0, 0, 0};
             for (int j = 0; j < 8; j++) {
                 int32_t v = xq(8 * c + j);
@@ -90,12 +134,12 @@ __global__ __launch_bounds__(256) void k_digitize(const float *__restrict__ x, i
                 }
             }
 #pragma unroll
-            for (int p = 0; p < 6; p++) dig4[(m * 6 + p) * K8 + c] = w[p];
+            for (int p = 0; p < 6; p++) a.dig4[(m * 6 + p) * K8 + c] = w[p];
         }
     }
-    if (dig8) {
+    if (a.dig8) {
         const int64_t K4 = (K + 3) / 4;
-        for (int64_t c = threadIdx.x; c < K4; c += 256) {
+        for (int64_t c = tid; c < K4; c += 256) {
             uint32_t w[3] = {0, 0, 0};
             for (int j = 0; j < 4; j++) {
                 int32_t v = xq(4 * c + j);
@@ -107,12 +151,21 @@ __global__ __launch_bounds__(256) void k_digitize(const float *__restrict__ x, i
                 }
             }
 #pragma unroll
-            for (int p = 0; p < 3; p++) dig8[(m * 3 + p) * K4 + c] = w[p];
+            for (int p = 0; p < 3; p++) a.dig8[(m * 3 + p) * K4 + c] = w[p];
         }
     }
-    if (xt) {
-        for (int64_t k = threadIdx.x; k < K; k += 256) xt[m * K + k] = xq(k);
+    if (a.xt) {
+        for (int64_t k = tid; k < K; k += 256) a.xt[m * K + k] = xq(k);
     }
+}
+
+static int32_t launch_rowdig(ut_ctx *ctx, const RowDigArgs &a, int64_t M, const char *name) {
+    if (M <= 0) return UT_OK;
+    const size_t shmem = a.K <= kRowLds ? (size_t)a.K * 4 : 0;
+    int tok = timing_begin(ctx, name);
+    hipLaunchKernelGGL(k_rowdig, dim3((unsigned)M), dim3(256), shmem, ctx->stream, a);
+    timing_end(ctx, tok);
+    return launch_check(ctx, "k_rowdig");
 }
 
 int32_t launch_digitize(ut_ctx *ctx, const float *x, int64_t ldx, int64_t M, int64_t K,
@@ -129,14 +182,37 @@ int32_t launch_digitize_parts(ut_ctx *ctx, const float *x, int64_t ldx, int64_t 
 int32_t launch_digitize_slots(ut_ctx *ctx, const float *x, int64_t ldx, int64_t M, int64_t K,
                               const uint32_t *rowmax_parts, int32_t nparts, XDigits xd,
                               int flags, const int32_t *slot_count, int rows_per_slot) {
-    if (M <= 0) return UT_OK;
-    int tok = timing_begin(ctx, "digitize");
-    hipLaunchKernelGGL(k_digitize, dim3((unsigned)M), dim3(256), 0, ctx->stream, x, ldx, K,
-                       rowmax_parts, nparts, xd.exps, (flags & XD_DIG4) ? xd.dig4 : nullptr,
-                       (flags & XD_DIG8) ? xd.dig8 : nullptr, (flags & XD_XT) ? xd.xt : nullptr,
-                       slot_count, rows_per_slot);
-    timing_end(ctx, tok);
-    return launch_check(ctx, "k_digitize");
+    RowDigArgs a{};
+    a.x = x;
+    a.ldx = ldx;
+    a.K = K;
+    a.rowmax = rowmax_parts;
+    a.nparts = nparts;
+    a.slot_count = slot_count;
+    a.rows_per_slot = rows_per_slot;
+    a.exps = xd.exps;
+    a.dig4 = (flags & XD_DIG4) ? xd.dig4 : nullptr;
+    a.dig8 = (flags & XD_DIG8) ? xd.dig8 : nullptr;
+    a.xt = (flags & XD_XT) ? xd.xt : nullptr;
+    return launch_rowdig(ctx, a, M, "digitize");
+}
+
+int32_t launch_rmsnorm_digitize(ut_ctx *ctx, const float *x, int64_t ldx, int64_t M, int64_t K,
+                                const float *w, float eps, float *out, int64_t ldo, XDigits xd,
+                                int flags) {
+    RowDigArgs a{};
+    a.x = x;
+    a.ldx = ldx;
+    a.K = K;
+    a.norm_w = w;
+    a.eps = eps;
+    a.out = out;
+    a.ldo = ldo;
+    a.exps = xd.exps;
+    a.dig4 = (flags & XD_DIG4) ? xd.dig4 : nullptr;
+    a.dig8 = (flags & XD_DIG8) ? xd.dig8 : nullptr;
+    a.xt = (flags & XD_XT) ? xd.xt : nullptr;
+    return launch_rowdig(ctx, a, M, "rmsnorm_digitize");
 }
 
 // --------------------------------------------------------- fast GEMV ---
@@ -311,6 +387,26 @@ int32_t gemv(ut_ctx *ctx, const GemvArgs &ga) {
 
 size_t matmul_digit_bytes(int64_t M, int64_t K) {
     return xdigits_bytes(M, K, XD_DIG4 | XD_DIG8 | XD_XT);
+}
+
+int32_t matmul_digits(ut_ctx *ctx, const ut_qtensor *w, const float *x, const XDigits &xd,
+                      int64_t M, float *out, int64_t ldo, int accumulate) {
+    GemvArgs ga;
+    ga.w = w;
+    ga.M = M;
+    ga.out = out;
+    ga.ldo = ldo;
+    ga.accumulate = accumulate;
+    ga.xf = x;
+    ga.xd = xd;
+    if (w->fmt != UT_FMT_F32) {
+        const bool need4 = w->fmt == UT_FMT_INT4 && fast_ok(w), need8 = w->fmt == UT_FMT_INT8 && fast_ok(w);
+        if ((need4 && !xd.dig4) || (need8 && !xd.dig8) || (!fast_ok(w) && !xd.xt)) {
+            set_error(ctx, "matmul_digits: activation digits of the wrong form");
+            return UT_ERR_ARG;
+        }
+    }
+    return gemv(ctx, ga);
 }
 
 int32_t matmul_dev(ut_ctx *ctx, const ut_qtensor *w, const float *x, int64_t M, float *out,

@@ -136,6 +136,17 @@ struct XDigits {
 };
 enum { XD_DIG4 = 1, XD_DIG8 = 2, XD_XT = 4 };
 size_t xdigits_bytes(int64_t M, int64_t K, int flags);
+// The rows s0.. of a digitised batch.
+inline XDigits xdigits_rows(const XDigits &d, int64_t s0) {
+    XDigits r = d;
+    const int64_t K8 = (d.K + 7) / 8, K4 = (d.K + 3) / 4;
+    r.exps = d.exps ? d.exps + s0 : nullptr;
+    r.dig4 = d.dig4 ? d.dig4 + s0 * 6 * K8 : nullptr;
+    r.dig8 = d.dig8 ? d.dig8 + s0 * 3 * K4 : nullptr;
+    r.xt = d.xt ? d.xt + s0 * d.K : nullptr;
+    r.M = d.M - s0;
+    return r;
+}
 // Carves an XDigits view out of `base` (device memory of xdigits_bytes()).
 XDigits xdigits_view(void *base, int64_t M, int64_t K, int flags);
 // Digitise x [M, K] (row stride ldx floats).  rowmax_bits: optional
@@ -147,6 +158,12 @@ int32_t launch_digitize(ut_ctx *ctx, const float *x, int64_t ldx, int64_t M, int
 int32_t launch_digitize_parts(ut_ctx *ctx, const float *x, int64_t ldx, int64_t M, int64_t K,
                               const uint32_t *rowmax_parts, int32_t nparts, XDigits xd,
                               int flags);
+
+// rmsnorm (undertow-quant/src/lib.rs:91-100) of each row fused with its
+// digitisation; out (optional) receives the normalised f32 row.
+int32_t launch_rmsnorm_digitize(ut_ctx *ctx, const float *x, int64_t ldx, int64_t M, int64_t K,
+                                const float *w, float eps, float *out, int64_t ldo, XDigits xd,
+                                int flags);
 
 // Flags a GEMV needs for a weight of this format and shape.
 int xdigit_flags_for(int32_t fmt, int64_t K);
@@ -168,6 +185,10 @@ int32_t gemv(ut_ctx *ctx, const GemvArgs &a);
 // out[M, ldo] (+)= x[M, K] * w^T with x f32 on device: digitises x into
 // digit_scratch (matmul_digit_bytes(M, K) bytes) when w is quantized.
 size_t matmul_digit_bytes(int64_t M, int64_t K);
+// Same with x already digitised (xd must hold the form the weight needs;
+// x is read only for f32 weights).
+int32_t matmul_digits(ut_ctx *ctx, const ut_qtensor *w, const float *x, const XDigits &xd,
+                      int64_t M, float *out, int64_t ldo, int accumulate);
 int32_t matmul_dev(ut_ctx *ctx, const ut_qtensor *w, const float *x, int64_t M, float *out,
                    int64_t ldo, int accumulate, void *digit_scratch);
 

@@ -3,10 +3,9 @@
 // rows x H heads over the shared latent cache, split-T flash decoding.
 //
 //   k_mla_split    grid (R*H/HG, nsplit): a workgroup takes HG heads of one
-//                  query row and one 256-position slice of the cache; each
-//                  thread scores one position against the HG queries (the
-//                  cache row is read once for all HG heads), then the slice's
-//                  max / sum / unnormalised context are written out.
+//                  query row and one 64-position slice of the cache; a lane
+//                  scores one position against HG/4 queries, then the
+//                  slice's max / sum / unnormalised context are written out.
 //   k_mla_combine  merges the slices: M = max m_j, L = sum l_j e^(m_j-M),
 //                  clat = sum o_j e^(m_j-M) / L.
 // Row s sees n_ctx = pos_base + s + 1 positions.  Slice boundaries depend
@@ -18,8 +17,12 @@
 
 namespace ut {
 
-constexpr int kMlaSlice = 256;
+constexpr int kMlaSlice = 64;
 
+// Workgroup = HG heads of one query row x one 64-position slice.
+// Scores: wave w takes heads w, w+4, ... (HG/4 of them), lane = position;
+// the slice max / sum per head are wave reductions.  Context: thread t takes
+// latent columns t, t+256, ... for all HG heads over the slice.
 template <int HG>
 __global__ __launch_bounds__(256) void k_mla_split(const float *__restrict__ qabs,
                                                    const float *__restrict__ qrope,
@@ -30,71 +33,70 @@ __global__ __launch_bounds__(256) void k_mla_split(const float *__restrict__ qab
                                                    float *__restrict__ part_l,
                                                    float *__restrict__ part_o, int nsplit) {
     extern __shared__ float sm[];
-    float *q = sm;                         // [HG][L + P]
-    float *p = sm + HG * (L + P);          // [HG][kMlaSlice]
-    __shared__ float red[HG][8];
+    constexpr int HW = HG >= 4 ? HG / 4 : 1;  // heads per wave
+    const int QW = L + P;
+    float *q = sm;                  // [HG][L + P]
+    float *p = sm + HG * QW;        // [HG][kMlaSlice]
     const int groups = H / HG;
     const int r = blockIdx.x / groups, h0 = (blockIdx.x % groups) * HG;
-    const int j = blockIdx.y, tid = threadIdx.x;
+    const int j = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int64_t n_ctx = pos_base + r + 1;
     const int64_t t0 = (int64_t)j * kMlaSlice;
-    const int QW = L + P;
     for (int i = tid; i < HG * QW; i += 256) {
         int hh = i / QW, d = i - hh * QW;
         int64_t qi = ((int64_t)r * H + h0 + hh);
         q[i] = d < L ? qabs[qi * L + d] : qrope[qi * P + (d - L)];
     }
     __syncthreads();
-    const int64_t pos = t0 + tid;
-    const bool live = pos < n_ctx;
-    float sc[HG];
-#pragma unroll
-    for (int hh = 0; hh < HG; hh++) sc[hh] = 0.0f;
-    if (live) {
-        const float *lr = latent + pos * L;
-        for (int d = 0; d < L; d++) {
-            float kv = lr[d];
-#pragma unroll
-            for (int hh = 0; hh < HG; hh++) sc[hh] = __fadd_rn(sc[hh], __fmul_rn(q[hh * QW + d], kv));
-        }
-        const float *kr = krot + pos * P;
-        for (int d = 0; d < P; d++) {
-            float kv = kr[d];
-#pragma unroll
-            for (int hh = 0; hh < HG; hh++)
-                sc[hh] = __fadd_rn(sc[hh], __fmul_rn(q[hh * QW + L + d], kv));
-        }
-    }
-    // slice max per head
-    const int wave = tid >> 6, lane = tid & 63;
-    float mx[HG];
-#pragma unroll
-    for (int hh = 0; hh < HG; hh++) {
-        sc[hh] = live ? __fmul_rn(sc[hh], scale) : -INFINITY;
-        float v = sc[hh];
-        for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-        if (lane == 0) red[hh][wave] = v;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int hh = 0; hh < HG; hh++)
-        mx[hh] = fmaxf(fmaxf(red[hh][0], red[hh][1]), fmaxf(red[hh][2], red[hh][3]));
-    __syncthreads();
-#pragma unroll
-    for (int hh = 0; hh < HG; hh++) {
-        float e = live ? expf(sc[hh] - mx[hh]) : 0.0f;
-        p[hh * kMlaSlice + tid] = e;
-        float v = e;
-        for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-        if (lane == 0) red[hh][4 + wave] = v;
-    }
-    __syncthreads();
     const int64_t pb = ((int64_t)r * H + h0) * nsplit + j;  // part index of head h0
-    if (tid < HG) {
-        part_m[pb + (int64_t)tid * nsplit] = mx[tid];
-        part_l[pb + (int64_t)tid * nsplit] =
-            (red[tid][4] + red[tid][5]) + (red[tid][6] + red[tid][7]);
+    if (wave < HG) {
+        const int64_t pos = t0 + lane;
+        const bool live = pos < n_ctx;
+        float sc[HW];
+#pragma unroll
+        for (int k = 0; k < HW; k++) sc[k] = 0.0f;
+        if (live) {
+            // score = sum_i q_i*lat_i + sum_i qr_i*krot_i, sequential adds
+            const float *lr = latent + pos * L;
+            for (int d = 0; d < L; d += 4) {
+                const float4 kv = *(const float4 *)(lr + d);
+#pragma unroll
+                for (int k = 0; k < HW; k++) {
+                    const float *qq = q + (wave + 4 * k) * QW + d;
+                    float a = sc[k];
+                    a = __fadd_rn(a, __fmul_rn(qq[0], kv.x));
+                    a = __fadd_rn(a, __fmul_rn(qq[1], kv.y));
+                    a = __fadd_rn(a, __fmul_rn(qq[2], kv.z));
+                    a = __fadd_rn(a, __fmul_rn(qq[3], kv.w));
+                    sc[k] = a;
+                }
+            }
+            const float *kr = krot + pos * P;
+            for (int d = 0; d < P; d++) {
+                const float kv = kr[d];
+#pragma unroll
+                for (int k = 0; k < HW; k++)
+                    sc[k] = __fadd_rn(sc[k], __fmul_rn(q[(wave + 4 * k) * QW + L + d], kv));
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < HW; k++) {
+            const int hh = wave + 4 * k;
+            if (hh >= HG) break;
+            const float v = live ? __fmul_rn(sc[k], scale) : -INFINITY;
+            float mx = v;
+            for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+            const float e = live ? expf(v - mx) : 0.0f;
+            p[hh * kMlaSlice + lane] = e;
+            float sum = e;
+            for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+            if (lane == 0) {
+                part_m[pb + (int64_t)hh * nsplit] = mx;
+                part_l[pb + (int64_t)hh * nsplit] = sum;
+            }
+        }
     }
+    __syncthreads();
     // unnormalised context over the slice
     const int64_t tn = n_ctx - t0 < kMlaSlice ? n_ctx - t0 : kMlaSlice;
     for (int d = tid; d < L; d += 256) {
@@ -102,7 +104,7 @@ __global__ __launch_bounds__(256) void k_mla_split(const float *__restrict__ qab
 #pragma unroll
         for (int hh = 0; hh < HG; hh++) o[hh] = 0.0f;
         for (int64_t t = 0; t < tn; t++) {
-            float kv = latent[(t0 + t) * L + d];
+            const float kv = latent[(t0 + t) * L + d];
 #pragma unroll
             for (int hh = 0; hh < HG; hh++) o[hh] = __builtin_fmaf(p[hh * kMlaSlice + t], kv, o[hh]);
         }
@@ -148,6 +150,10 @@ int32_t launch_mla_attend(ut_ctx *ctx, const float *qabs, const float *qrope, co
     float *pm = (float *)scratch;
     float *pl = (float *)((char *)scratch + ((n * 4 + 255) & ~size_t(255)));
     float *po = (float *)((char *)pl + ((n * 4 + 255) & ~size_t(255)));
+    if (L % 4 != 0) {
+        set_error(ctx, "mla: latent width %lld must be a multiple of 4", (long long)L);
+        return UT_ERR_SHAPE;
+    }
     int HG = 8;
     while (HG > 1 && H % HG != 0) HG >>= 1;
     const size_t shmem = (size_t)HG * (L + P + kMlaSlice) * 4;

@@ -92,6 +92,7 @@ struct Workspace {
     float *rlogits = nullptr, *rw = nullptr;
     int32_t *rids = nullptr, *ids = nullptr, *am = nullptr, *err = nullptr;
     void *digits = nullptr, *moe = nullptr, *mla = nullptr, *argm = nullptr;
+    void *digA = nullptr, *digB = nullptr;  // activation digits shared by consumers
 };
 
 }  // namespace
@@ -111,6 +112,8 @@ struct ut_session {
 };
 
 namespace {
+
+constexpr int64_t kMlaRowsPerCall = 16;
 
 int64_t hd(const ut_model *m) { return m->c.hidden_size; }
 
@@ -319,8 +322,10 @@ int32_t ws_reserve(ut_session *s, int64_t rows) {
     size_t ilog = F(R * c.vocab_size), iemb = F(R * H), icat = F(R * 2 * H);
     size_t irl = F(4 * E), irw = F(4 * k), irid = F(4 * k), iids = F(R), iam = F(R), ierr = F(1);
     size_t idig = plan.add(matmul_digit_bytes(R, kmax));
+    size_t idA = plan.add(matmul_digit_bytes(R, kmax));
+    size_t idB = plan.add(matmul_digit_bytes(R, kmax));
     size_t imoes = plan.add(moe_bytes);
-    size_t imla = plan.add(mla_scratch_bytes(R, heads, Lr, s->cap));
+    size_t imla = plan.add(mla_scratch_bytes(R < kMlaRowsPerCall ? R : kMlaRowsPerCall, heads, Lr, s->cap));
     size_t iarg = plan.add(argmax_scratch_bytes(R, c.vocab_size) + 256);
     size_t total = 0;
     for (size_t b : plan.sizes) total += b;
@@ -347,6 +352,7 @@ int32_t ws_reserve(ut_session *s, int64_t rows) {
     w.rlogits = (float *)p[irl]; w.rw = (float *)p[irw]; w.rids = (int32_t *)p[irid];
     w.ids = (int32_t *)p[iids]; w.am = (int32_t *)p[iam]; w.err = (int32_t *)p[ierr];
     w.digits = p[idig]; w.moe = p[imoes]; w.mla = p[imla]; w.argm = p[iarg];
+    w.digA = p[idA]; w.digB = p[idB];
     w.rows = R;
     UT_CHECK_HIP(ctx, hipMemsetAsync(w.err, 0, 4, ctx->stream));
     return UT_OK;
@@ -358,9 +364,37 @@ int32_t mm(ut_session *s, const ut_qtensor *w, const float *x, int64_t M, float 
     return matmul_dev(s->m->ctx, w, x, M, out, ldo, accumulate, s->ws.digits);
 }
 
+// Digit forms the given weights need from one shared activation.
+int dig_flags(std::initializer_list<const ut_qtensor *> ws) {
+    int f = 0;
+    for (const ut_qtensor *w : ws) {
+        if (!w || w->fmt == UT_FMT_F32) continue;
+        const bool fast = (w->fmt == UT_FMT_INT4 ? w->in_dim % 32 == 0 : w->in_dim % 16 == 0) &&
+                          ((uintptr_t)w->payload & 15) == 0;
+        f |= fast ? xdigit_flags_for(w->fmt, w->in_dim) : XD_XT;
+    }
+    return f;
+}
+
+int dig_flags_fmt(int fmt, int64_t K) {
+    if (fmt == UT_FMT_F32) return 0;
+    return xdigit_flags_for(fmt, K);
+}
+
+// rmsnorm rows of x into out (f32) and into digits in `buf` for consumers
+// needing `flags`.
+int32_t norm_dig(ut_session *s, const float *x, int64_t ldx, const float *w, int64_t n,
+                 int64_t rows, float *out, int64_t ldo, void *buf, int flags, XDigits *xd) {
+    const ut_model_config &c = s->m->c;
+    *xd = xdigits_view(buf, rows, n, flags);
+    return launch_rmsnorm_digitize(s->m->ctx, x, ldx, rows, n, w, c.rms_norm_eps, out, ldo, *xd,
+                                   flags);
+}
+
 // An MLP (dense FFN or shared expert) over rows, added into out
-// (MlpWeights::forward_add, model.rs:43-58).
-int32_t mlp_add(ut_session *s, const MlpW &w, const float *x, int64_t rows, float *out) {
+// (MlpWeights::forward_add, model.rs:43-58).  xd: digits of x.
+int32_t mlp_add(ut_session *s, const MlpW &w, const float *x, const XDigits &xd, int64_t rows,
+                float *out) {
     ut_model *m = s->m;
     for (int64_t s0 = 0; s0 < rows; s0 += 4) {
         MoeCall c;
@@ -374,6 +408,8 @@ int32_t mlp_add(ut_session *s, const MlpW &w, const float *x, int64_t rows, floa
         c.ids = m->zeros;
         c.weights = m->ones;
         c.x = x + s0 * c.H;
+        XDigits xr = xdigits_rows(xd, s0);
+        if (w.fmt != UT_FMT_F32) c.x_digits = &xr;
         c.out = out + s0 * c.H;
         c.ldo = c.H;
         c.accumulate = 1;
@@ -384,19 +420,24 @@ int32_t mlp_add(ut_session *s, const MlpW &w, const float *x, int64_t rows, floa
 }
 
 // moe_forward (model.rs:195-286): router, routed experts in choice order,
-// then the shared expert, into out (overwritten).
-int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, int64_t rows, float *out) {
+// then the shared expert, into out (overwritten).  x: normed rows (f32, for
+// the f32 router gate) with digits xd.
+int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigits &xd,
+                    int64_t rows, float *out) {
     ut_model *m = s->m;
     const ut_model_config &c = m->c;
     const int64_t H = c.hidden_size, E = c.n_routed_experts;
     const int k = (int)c.num_experts_per_tok;
     for (int64_t s0 = 0; s0 < rows; s0 += 4) {
         const int M = (int)(rows - s0 < 4 ? rows - s0 : 4);
-        // f32 gate matmul (lib.rs:128) + route (router.rs:58)
+        // f32 gate matmul (lib.rs:128), then route (router.rs:58) + slot plan
         UT_TRY(mm(s, L.gate, x + s0 * H, M, s->ws.rlogits, E));
-        UT_TRY(launch_route(m->ctx, s->ws.rlogits, L.bias, M, E, k, (int)c.n_group,
-                            (int)c.topk_group, c.norm_topk_prob, c.routed_scaling_factor,
-                            s->ws.rids, s->ws.rw));
+        const int64_t slots = moe_slots(M, k, E, -1);
+        ScratchLayout lay = moe_layout(M, k, slots, H, c.moe_intermediate_size, L.expert_fmt);
+        UT_TRY(launch_route_plan(m->ctx, s->ws.rlogits, L.bias, M, E, k, (int)c.n_group,
+                                 (int)c.topk_group, c.norm_topk_prob, c.routed_scaling_factor,
+                                 s->ws.rids, s->ws.rw, L.experts.gate_w,
+                                 moe_plan_view(s->ws.moe, lay), s->ws.err));
         MoeCall mc;
         mc.fmt = L.expert_fmt;
         mc.tbl = L.experts;
@@ -408,19 +449,23 @@ int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, int64_t rows
         mc.ids = s->ws.rids;
         mc.weights = s->ws.rw;
         mc.x = x + s0 * H;
+        XDigits xr = xdigits_rows(xd, s0);
+        if (L.expert_fmt != UT_FMT_F32) mc.x_digits = &xr;
         mc.out = out + s0 * H;
         mc.ldo = H;
         mc.accumulate = 0;
         mc.err_flag = s->ws.err;
+        mc.plan_ready = true;
         UT_TRY(moe_pass(m->ctx, mc, s->ws.moe));
     }
-    if (L.has_shared) UT_TRY(mlp_add(s, L.shared, x, rows, out));
+    if (L.has_shared) UT_TRY(mlp_add(s, L.shared, x, xd, rows, out));
     return UT_OK;
 }
 
-// mla_forward_cached, absorbed form (attention.rs:123-279).  x: normed rows.
-int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, int64_t rows, KvCache &kv,
-                    float *out) {
+// mla_forward_cached, absorbed form (attention.rs:123-279).  x: normed rows
+// with digits xd.
+int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, const XDigits &xd,
+                    int64_t rows, KvCache &kv, float *out) {
     ut_model *m = s->m;
     ut_ctx *ctx = m->ctx;
     const ut_model_config &c = m->c;
@@ -430,18 +475,19 @@ int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, int64_t rows
     const int64_t qh = nope + rope;
     const float scale = 1.0f / sqrtf((float)qh);  // config.rs:142-144
     const int64_t pos_base = kv.len;
+    UT_TRY(matmul_digits(ctx, L.kv_a, x, xd, rows, w.comp, Lr + rope, 0));
     if (L.lora) {
-        UT_TRY(mm(s, L.q_a, x, rows, w.qa, c.q_lora_rank));
-        UT_TRY(launch_rmsnorm(ctx, w.qa, c.q_lora_rank, L.q_a_norm, c.q_lora_rank, c.rms_norm_eps,
-                              rows, w.qa_n, c.q_lora_rank));
-        UT_TRY(mm(s, L.q_b, w.qa_n, rows, w.q, heads * qh));
+        UT_TRY(matmul_digits(ctx, L.q_a, x, xd, rows, w.qa, c.q_lora_rank, 0));
+        XDigits qd;
+        UT_TRY(norm_dig(s, w.qa, c.q_lora_rank, L.q_a_norm, c.q_lora_rank, rows, w.qa_n,
+                        c.q_lora_rank, w.digB, dig_flags({L.q_b}), &qd));
+        UT_TRY(matmul_digits(ctx, L.q_b, w.qa_n, qd, rows, w.q, heads * qh, 0));
     } else {
-        UT_TRY(mm(s, L.q_proj, x, rows, w.q, heads * qh));
+        UT_TRY(matmul_digits(ctx, L.q_proj, x, xd, rows, w.q, heads * qh, 0));
     }
     const int64_t half = rope / 2;
     UT_TRY(launch_rope(ctx, w.q + nope, rows, heads, heads * qh, qh, rope, pos_base, m->rope_table,
                        half));
-    UT_TRY(mm(s, L.kv_a, x, rows, w.comp, Lr + rope));
     UT_TRY(launch_rmsnorm(ctx, w.comp, Lr + rope, L.kv_a_norm, Lr, c.rms_norm_eps, rows,
                           kv.latent + pos_base * Lr, Lr));
     UT_CHECK_HIP(ctx, hipMemcpy2DAsync(kv.krot + pos_base * rope, rope * 4, w.comp + Lr,
@@ -451,8 +497,14 @@ int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, int64_t rows
                        m->rope_table, half));
     kv.len = pos_base + rows;
     UT_TRY(launch_absorb_q(ctx, L.kv_b, w.q, rows, heads, nope, rope, vh, w.qabs, w.qrope));
-    UT_TRY(launch_mla_attend(ctx, w.qabs, w.qrope, kv.latent, kv.krot, rows, heads, Lr, rope,
-                             pos_base, scale, w.clat, w.mla));
+    // query rows in groups of kMlaRowsPerCall (bounded scratch; a row's
+    // result does not depend on its group)
+    for (int64_t r0 = 0; r0 < rows; r0 += kMlaRowsPerCall) {
+        const int64_t rn = rows - r0 < kMlaRowsPerCall ? rows - r0 : kMlaRowsPerCall;
+        UT_TRY(launch_mla_attend(ctx, w.qabs + r0 * heads * Lr, w.qrope + r0 * heads * rope,
+                                 kv.latent, kv.krot, rn, heads, Lr, rope, pos_base + r0, scale,
+                                 w.clat + r0 * heads * Lr, w.mla));
+    }
     UT_TRY(launch_absorb_v(ctx, L.kv_b, w.clat, rows, heads, nope, vh, w.ctxv));
     return mm(s, L.o_proj, w.ctxv, rows, out, c.hidden_size);
 }
@@ -464,12 +516,20 @@ int32_t run_layer(ut_session *s, const LayerW &L, float *x, int64_t rows, KvCach
     const ut_model_config &c = m->c;
     const int64_t H = c.hidden_size;
     Workspace &w = s->ws;
-    UT_TRY(launch_rmsnorm(ctx, x, H, L.input_norm, H, c.rms_norm_eps, rows, w.normed, H));
-    UT_TRY(mla_forward(s, L, w.normed, rows, kv, w.attn));
+    XDigits xd;
+    UT_TRY(norm_dig(s, x, H, L.input_norm, H, rows, w.normed, H, w.digA,
+                    dig_flags({L.q_a, L.q_proj, L.kv_a}), &xd));
+    UT_TRY(mla_forward(s, L, w.normed, xd, rows, kv, w.attn));
     UT_TRY(launch_add(ctx, x, w.attn, rows * H));
-    UT_TRY(launch_rmsnorm(ctx, x, H, L.post_norm, H, c.rms_norm_eps, rows, w.normed, H));
-    if (L.dense) return mlp_add(s, L.mlp, w.normed, rows, x);
-    UT_TRY(moe_forward(s, L, w.normed, rows, w.moe_out));
+    int f = 0;
+    if (L.dense) f = dig_flags_fmt(L.mlp.fmt, H);
+    else {
+        f = dig_flags_fmt(L.expert_fmt, H);
+        if (L.has_shared) f |= dig_flags_fmt(L.shared.fmt, H);
+    }
+    UT_TRY(norm_dig(s, x, H, L.post_norm, H, rows, w.normed, H, w.digA, f, &xd));
+    if (L.dense) return mlp_add(s, L.mlp, w.normed, xd, rows, x);
+    UT_TRY(moe_forward(s, L, w.normed, xd, rows, w.moe_out));
     return launch_add(ctx, x, w.moe_out, rows * H);
 }
 
@@ -526,8 +586,10 @@ int32_t prefill_dev(ut_session *s, const int32_t *ids, int64_t n) {
                                          hipMemcpyDeviceToDevice, ctx->stream));
     s->pos += n;
     s->tokens.insert(s->tokens.end(), ids, ids + n);
-    UT_TRY(launch_rmsnorm(ctx, w.x, H, m->final_norm, H, c.rms_norm_eps, n, w.normed, H));
-    UT_TRY(mm(s, m->lm_head, w.normed, n, w.logits, V));
+    XDigits fd;
+    UT_TRY(norm_dig(s, w.x, H, m->final_norm, H, n, w.normed, H, w.digA, dig_flags({m->lm_head}),
+                    &fd));
+    UT_TRY(matmul_digits(ctx, m->lm_head, w.normed, fd, n, w.logits, V, 0));
     return launch_argmax(ctx, w.logits, n, V, V, w.am, w.argm);
 }
 
@@ -569,9 +631,10 @@ int32_t draft_rows(ut_session *s, const std::vector<int32_t> &next_tokens, const
     UT_TRY(launch_rmsnorm(ctx, hidden_rows, H, m->hnorm, H, c.rms_norm_eps, rows, w.cat + H, 2 * H));
     UT_TRY(mm(s, m->eh_proj, w.cat, rows, w.x, H));
     UT_TRY(run_layer(s, m->mtp_layer, w.x, rows, s->mtp_kv));
-    UT_TRY(launch_rmsnorm(ctx, w.x + (rows - 1) * H, H, m->mtp_norm, H, c.rms_norm_eps, 1,
-                          w.normed, H));
-    UT_TRY(mm(s, m->mtp_head, w.normed, 1, w.logits, V));
+    XDigits hd_;
+    UT_TRY(norm_dig(s, w.x + (rows - 1) * H, H, m->mtp_norm, H, 1, w.normed, H, w.digA,
+                    dig_flags({m->mtp_head}), &hd_));
+    UT_TRY(matmul_digits(ctx, m->mtp_head, w.normed, hd_, 1, w.logits, V, 0));
     UT_TRY(launch_argmax(ctx, w.logits, 1, V, V, w.am, w.argm));
     return read_argmax(s, 1, draft_out);
 }
@@ -748,7 +811,8 @@ int32_t ut_model_create(ut_ctx *ctx, const ut_model_config *cfg, ut_model **out)
     const ut_model_config &c = *cfg;
     // DeepseekConfig::validate essentials (config.rs:154-216)
     if (c.vocab_size <= 0 || c.hidden_size <= 0 || c.num_hidden_layers < 0 ||
-        c.num_attention_heads <= 0 || c.kv_lora_rank <= 0 || c.qk_rope_head_dim <= 0 ||
+        c.num_attention_heads <= 0 || c.kv_lora_rank <= 0 || c.kv_lora_rank % 4 != 0 ||
+        c.qk_rope_head_dim <= 0 ||
         c.qk_rope_head_dim % 2 != 0 || c.qk_nope_head_dim <= 0 || c.v_head_dim <= 0 ||
         c.max_position_embeddings <= 0 || c.num_experts_per_tok <= 0 ||
         c.num_experts_per_tok > 64 || c.n_group < 0 || c.n_group > 64 ||

@@ -38,6 +38,7 @@ struct MoeCall {
     int accumulate = 0;
     int extra_slot = -1;  // >= 0: expert id always appended as the last slot, added with weight 1
     int32_t *err_flag = nullptr;
+    bool plan_ready = false;  // the slot plan is already in the scratch (launch_route_plan)
 };
 
 struct ScratchLayout {
@@ -58,6 +59,13 @@ bool moe_shape_ok(int fmt, int64_t H, int64_t I);
 // scratch: device memory of moe_layout(...).total bytes for this call's
 // (M, k, slots); slots from moe_slots().
 int32_t moe_pass(ut_ctx *ctx, const MoeCall &c, void *scratch);
+// The plan buffers inside a pass's scratch.
+MoePlan moe_plan_view(void *scratch, const ScratchLayout &L);
+// Routes M <= 4 rows and writes the slot plan into `plan` in one launch.
+int32_t launch_route_plan(ut_ctx *ctx, const float *logits, const float *bias, int M, int64_t E,
+                          int32_t k, int32_t n_group, int32_t topk_group, int32_t norm,
+                          float scale, int32_t *ids, float *weights,
+                          const uint8_t *const *gate_tbl, MoePlan plan, int32_t *err_flag);
 
 int32_t launch_route(ut_ctx *ctx, const float *logits, const float *bias, int64_t rows,
                      int64_t E, int32_t k, int32_t n_group, int32_t topk_group, int32_t norm,

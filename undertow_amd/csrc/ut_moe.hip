@@ -27,19 +27,15 @@ __device__ __forceinline__ bool ranks_before(float a, int ia, float b, int ib) {
     return a > b || (a == b && ia < ib);
 }
 
-__global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
-                                               const float *__restrict__ bias, int E, int k,
-                                               int n_group, int topk_group, int norm,
-                                               float scale, int32_t *__restrict__ ids,
-                                               float *__restrict__ weights) {
-    extern __shared__ float sm[];
+// Routes one row with the whole workgroup.  sm: 2*E + n_group floats.
+__device__ void route_row(const float *__restrict__ lg, const float *__restrict__ bias, int E,
+                          int k, int n_group, int topk_group, int norm, float scale,
+                          int32_t *__restrict__ ids, float *__restrict__ weights, float *sm,
+                          int *s_ids, int *s_group_ok) {
     float *sc = sm;           // sigmoid scores
     float *corr = sm + E;     // corrected (selection) scores, then masked
     float *gsc = sm + 2 * E;  // group scores
-    __shared__ int s_ids[64];
-    __shared__ int s_group_ok[64];
-    const int row = blockIdx.x, tid = threadIdx.x;
-    const float *lg = logits + (int64_t)row * E;
+    const int tid = threadIdx.x;
     if (tid < 64) s_ids[tid] = 0;
     for (int e = tid; e < E; e += blockDim.x) {
         float s = 1.0f / (1.0f + expf(-lg[e]));  // sigmoid (undertow-quant/src/lib.rs:116)
@@ -93,37 +89,36 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
         denom = denom + 1e-20f;
         for (int j = 0; j < keff; j++) {
             float v = norm ? w[j] / denom : w[j];
-            ids[(int64_t)row * k + j] = s_ids[j];
-            weights[(int64_t)row * k + j] = __fmul_rn(v, scale);
+            ids[j] = s_ids[j];
+            weights[j] = __fmul_rn(v, scale);
         }
         for (int j = keff; j < k; j++) {  // k > E: no expert (contributes nothing)
-            ids[(int64_t)row * k + j] = -1;
-            weights[(int64_t)row * k + j] = 0.0f;
+            ids[j] = -1;
+            weights[j] = 0.0f;
         }
     }
+    __syncthreads();
 }
 
-int32_t launch_route(ut_ctx *ctx, const float *logits, const float *bias, int64_t rows,
-                     int64_t E, int32_t k, int32_t n_group, int32_t topk_group, int32_t norm,
-                     float scale, int32_t *ids, float *weights) {
-    if (rows <= 0) return UT_OK;
-    size_t shmem = (size_t)(2 * E + (n_group > 0 ? n_group : 1)) * sizeof(float);
-    int tok = timing_begin(ctx, "route");
-    hipLaunchKernelGGL(k_route, dim3((unsigned)rows), dim3(256), shmem, ctx->stream, logits, bias,
-                       (int)E, (int)k, (int)n_group, (int)topk_group, (int)norm, scale, ids,
-                       weights);
-    timing_end(ctx, tok);
-    return launch_check(ctx, "k_route");
+__global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
+                                               const float *__restrict__ bias, int E, int k,
+                                               int n_group, int topk_group, int norm,
+                                               float scale, int32_t *__restrict__ ids,
+                                               float *__restrict__ weights) {
+    extern __shared__ float sm[];
+    __shared__ int s_ids[64];
+    __shared__ int s_group_ok[64];
+    const int row = blockIdx.x;
+    route_row(logits + (int64_t)row * E, bias, E, k, n_group, topk_group, norm, scale,
+              ids + (int64_t)row * k, weights + (int64_t)row * k, sm, s_ids, s_group_ok);
 }
 
-// --------------------------------------------------------------- plan ---
 // Slots in first-appearance order over (row, choice) -- the order in which
 // moe_forward groups rows by expert (model.rs:219-233).  Invalid ids (out of
 // range or not loaded) set the sticky error flag and contribute nothing.
-__global__ void k_moe_plan(const int32_t *__restrict__ ids, int M, int k, int E,
-                           const uint8_t *const *__restrict__ gate_tbl, int extra_slot,
-                           MoePlan plan, int32_t *__restrict__ err_flag) {
-    if (threadIdx.x != 0) return;
+__device__ void make_plan(const int32_t *__restrict__ ids, int M, int k, int E,
+                          const uint8_t *const *__restrict__ gate_tbl, int extra_slot,
+                          MoePlan plan, int32_t *__restrict__ err_flag) {
     int U = 0;
     for (int s = 0; s < M; s++) {
         for (int c = 0; c < k; c++) {
@@ -141,6 +136,64 @@ __global__ void k_moe_plan(const int32_t *__restrict__ ids, int M, int k, int E,
     }
     if (extra_slot >= 0) plan.uniq[U++] = extra_slot;  // a dense MLP run as one more slot
     *plan.count = U;
+}
+
+// Routing of M <= 4 rows plus the slot plan in one workgroup (one launch on
+// the decode path instead of two).
+__global__ __launch_bounds__(256) void k_route_plan(const float *__restrict__ logits,
+                                                    const float *__restrict__ bias, int M, int E,
+                                                    int k, int n_group, int topk_group, int norm,
+                                                    float scale, int32_t *__restrict__ ids,
+                                                    float *__restrict__ weights,
+                                                    const uint8_t *const *__restrict__ gate_tbl,
+                                                    MoePlan plan, int32_t *__restrict__ err_flag) {
+    extern __shared__ float sm[];
+    __shared__ int s_ids[64];
+    __shared__ int s_group_ok[64];
+    __shared__ int32_t s_all[4 * 64];
+    for (int row = 0; row < M; row++) {
+        route_row(logits + (int64_t)row * E, bias, E, k, n_group, topk_group, norm, scale,
+                  ids + (int64_t)row * k, weights + (int64_t)row * k, sm, s_ids, s_group_ok);
+        if (threadIdx.x < k) s_all[row * k + threadIdx.x] = ids[(int64_t)row * k + threadIdx.x];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) make_plan(s_all, M, k, E, gate_tbl, -1, plan, err_flag);
+}
+
+__global__ void k_moe_plan(const int32_t *__restrict__ ids, int M, int k, int E,
+                           const uint8_t *const *__restrict__ gate_tbl, int extra_slot,
+                           MoePlan plan, int32_t *__restrict__ err_flag) {
+    if (threadIdx.x == 0) make_plan(ids, M, k, E, gate_tbl, extra_slot, plan, err_flag);
+}
+
+int32_t launch_route(ut_ctx *ctx, const float *logits, const float *bias, int64_t rows,
+                     int64_t E, int32_t k, int32_t n_group, int32_t topk_group, int32_t norm,
+                     float scale, int32_t *ids, float *weights) {
+    if (rows <= 0) return UT_OK;
+    size_t shmem = (size_t)(2 * E + (n_group > 0 ? n_group : 1)) * sizeof(float);
+    int tok = timing_begin(ctx, "route");
+    hipLaunchKernelGGL(k_route, dim3((unsigned)rows), dim3(256), shmem, ctx->stream, logits, bias,
+                       (int)E, (int)k, (int)n_group, (int)topk_group, (int)norm, scale, ids,
+                       weights);
+    timing_end(ctx, tok);
+    return launch_check(ctx, "k_route");
+}
+
+int32_t launch_route_plan(ut_ctx *ctx, const float *logits, const float *bias, int M, int64_t E,
+                          int32_t k, int32_t n_group, int32_t topk_group, int32_t norm,
+                          float scale, int32_t *ids, float *weights,
+                          const uint8_t *const *gate_tbl, MoePlan plan, int32_t *err_flag) {
+    if (M < 1 || M > 4 || k > 64) {
+        set_error(ctx, "route_plan: M=%d k=%d outside 1..4 / 1..64", M, k);
+        return UT_ERR_ARG;
+    }
+    size_t shmem = (size_t)(2 * E + (n_group > 0 ? n_group : 1)) * sizeof(float);
+    int tok = timing_begin(ctx, "route_plan");
+    hipLaunchKernelGGL(k_route_plan, dim3(1), dim3(256), shmem, ctx->stream, logits, bias, M,
+                       (int)E, (int)k, (int)n_group, (int)topk_group, (int)norm, scale, ids,
+                       weights, gate_tbl, plan, err_flag);
+    timing_end(ctx, tok);
+    return launch_check(ctx, "k_route_plan");
 }
 
 // --------------------------------------------------------- gate / up ---
@@ -303,15 +356,15 @@ ScratchLayout moe_layout(int64_t M, int64_t k, int64_t slots, int64_t H, int64_t
 template <int FMT, int M>
 static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L, char *base,
                           int64_t slots) {
-    MoePlan plan;
-    plan.count = (int32_t *)(base + L.count);
-    plan.uniq = (int32_t *)(base + L.uniq);
-    plan.choice_slot = (int32_t *)(base + L.choice);
-    int tok = timing_begin(ctx, "moe_plan");
-    hipLaunchKernelGGL(k_moe_plan, dim3(1), dim3(64), 0, ctx->stream, c.ids, M, c.k, (int)c.E,
-                       c.tbl.gate_w, c.extra_slot, plan, c.err_flag);
-    timing_end(ctx, tok);
-    UT_TRY(launch_check(ctx, "k_moe_plan"));
+    MoePlan plan = moe_plan_view(base, L);
+    int tok = -1;
+    if (!c.plan_ready) {
+        tok = timing_begin(ctx, "moe_plan");
+        hipLaunchKernelGGL(k_moe_plan, dim3(1), dim3(64), 0, ctx->stream, c.ids, M, c.k, (int)c.E,
+                           c.tbl.gate_w, c.extra_slot, plan, c.err_flag);
+        timing_end(ctx, tok);
+        UT_TRY(launch_check(ctx, "k_moe_plan"));
+    }
 
     XSrc xs{};
     const int32_t *xexps = nullptr;
@@ -402,6 +455,15 @@ static int32_t moe_pass_fmt(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &
     case 3: return moe_pass_t<FMT, 3>(ctx, c, L, base, slots);
     default: return moe_pass_t<FMT, 4>(ctx, c, L, base, slots);
     }
+}
+
+MoePlan moe_plan_view(void *scratch, const ScratchLayout &L) {
+    char *base = (char *)scratch;
+    MoePlan plan;
+    plan.count = (int32_t *)(base + L.count);
+    plan.uniq = (int32_t *)(base + L.uniq);
+    plan.choice_slot = (int32_t *)(base + L.choice);
+    return plan;
 }
 
 bool moe_shape_ok(int fmt, int64_t H, int64_t I) {

@@ -123,72 +123,163 @@ int32_t launch_add(ut_ctx *ctx, float *y, const float *x, int64_t n) {
     return launch_check(ctx, "k_add");
 }
 
-// qabs: one workgroup per (row, head), threads over the latent columns;
-// the nope rows of the head are added in order (add_scaled_row semantics).
-__global__ __launch_bounds__(256) void k_absorb_q(int32_t fmt, const uint8_t *__restrict__ w,
+// Four consecutive codes of a row as floats (int4: 2 bytes, int8: 4 bytes,
+// f32: 16 bytes).  col % 4 == 0.
+template <int FMT>
+__device__ __forceinline__ float4 codes4(const uint8_t *row, int64_t col) {
+    if constexpr (FMT == UT_FMT_F32) {
+        return *(const float4 *)(row + col * 4);
+    } else if constexpr (FMT == UT_FMT_INT8) {
+        const uint32_t w = *(const uint32_t *)(row + col);
+        return make_float4((float)(int8_t)(w & 0xff), (float)(int8_t)((w >> 8) & 0xff),
+                           (float)(int8_t)((w >> 16) & 0xff), (float)(int8_t)(w >> 24));
+    } else {
+        const uint32_t w = *(const uint16_t *)(row + col / 2);
+        auto nib = [](uint32_t v) { return (float)((int)(v ^ 8) - 8); };
+        return make_float4(nib(w & 0xf), nib((w >> 4) & 0xf), nib((w >> 8) & 0xf), nib((w >> 12) & 0xf));
+    }
+}
+
+// qabs: one workgroup per (head, group of up to 4 query rows); thread t owns
+// latent columns 4t..4t+3.  The head's nope rows are added in d order per
+// column (add_scaled_row semantics), with the weight loads of 16 rows
+// issued ahead of their use.
+template <int FMT, int RB>
+__global__ __launch_bounds__(128) void k_absorb_q(const uint8_t *__restrict__ w,
                                                   const float *__restrict__ scales,
                                                   int64_t row_bytes, int64_t L,
-                                                  const float *__restrict__ q, int64_t heads,
-                                                  int64_t nope, int64_t rope, int64_t kvh,
-                                                  float *__restrict__ qabs,
+                                                  const float *__restrict__ q, int64_t rows,
+                                                  int64_t heads, int64_t nope, int64_t rope,
+                                                  int64_t kvh, float *__restrict__ qabs,
                                                   float *__restrict__ qrope) {
-    const int64_t sh = blockIdx.x;  // s*heads + h
-    const int64_t h = sh % heads;
-    const float *qn = q + sh * (nope + rope);
-    for (int64_t i = threadIdx.x; i < L; i += 256) {
-        float acc = 0.0f;
-        for (int64_t d = 0; d < nope; d++) {
-            const int64_t row = h * kvh + d;
-            const float f = fmt == UT_FMT_F32 ? qn[d] : __fmul_rn(qn[d], scales[row]);
-            acc = __fadd_rn(acc, __fmul_rn(f, code_at(fmt, w + row * row_bytes, i)));
+    const int64_t h = blockIdx.x, r0 = (int64_t)blockIdx.y * RB;
+    const int64_t qh = nope + rope;
+    const int64_t col = 512 * (int64_t)blockIdx.z + 4 * (int64_t)threadIdx.x;
+    if (col < L) {
+        float4 acc[RB];
+#pragma unroll
+        for (int r = 0; r < RB; r++) acc[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+        constexpr int U = 16;
+        for (int64_t d0 = 0; d0 < nope; d0 += U) {
+            float4 c[U];
+#pragma unroll
+            for (int u = 0; u < U; u++)
+                if (d0 + u < nope) c[u] = codes4<FMT>(w + (h * kvh + d0 + u) * row_bytes, col);
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int64_t d = d0 + u;
+                if (d >= nope) break;
+                const float sc = FMT == UT_FMT_F32 ? 1.0f : scales[h * kvh + d];
+#pragma unroll
+                for (int r = 0; r < RB; r++) {
+                    if (r0 + r >= rows) break;
+                    const float qn = q[((r0 + r) * heads + h) * qh + d];
+                    const float f = FMT == UT_FMT_F32 ? qn : __fmul_rn(qn, sc);
+                    acc[r].x = __fadd_rn(acc[r].x, __fmul_rn(f, c[u].x));
+                    acc[r].y = __fadd_rn(acc[r].y, __fmul_rn(f, c[u].y));
+                    acc[r].z = __fadd_rn(acc[r].z, __fmul_rn(f, c[u].z));
+                    acc[r].w = __fadd_rn(acc[r].w, __fmul_rn(f, c[u].w));
+                }
+            }
         }
-        qabs[sh * L + i] = acc;
+#pragma unroll
+        for (int r = 0; r < RB; r++)
+            if (r0 + r < rows) *(float4 *)(qabs + ((r0 + r) * heads + h) * L + col) = acc[r];
     }
-    for (int64_t i = threadIdx.x; i < rope; i += 256) qrope[sh * rope + i] = qn[nope + i];
+    if (blockIdx.z == 0) {
+        for (int64_t i = threadIdx.x; i < RB * rope; i += blockDim.x) {
+            const int64_t r = r0 + i / rope, j = i % rope;
+            if (r < rows) qrope[(r * heads + h) * rope + j] = q[(r * heads + h) * qh + nope + j];
+        }
+    }
 }
 
 int32_t launch_absorb_q(ut_ctx *ctx, const ut_qtensor *kv_b, const float *q, int64_t rows,
                         int64_t heads, int64_t nope, int64_t rope, int64_t vh, float *qabs,
                         float *qrope) {
     if (rows <= 0) return UT_OK;
+    const int64_t L = kv_b->in_dim;
+    if (L % 4 != 0) {
+        set_error(ctx, "absorb: kv_lora_rank %lld must be a multiple of 4", (long long)L);
+        return UT_ERR_SHAPE;
+    }
+    constexpr int RB = 4;
+    // 128 threads x 4 columns per workgroup column block
+    const unsigned threads = (unsigned)(L >= 512 ? 128 : ((L / 4) + 63) / 64 * 64);
+    dim3 grid((unsigned)heads, (unsigned)((rows + RB - 1) / RB), (unsigned)((L + 511) / 512));
+    const uint8_t *w = (const uint8_t *)kv_b->payload;
+    const int64_t kvh = nope + vh;
     int tok = timing_begin(ctx, "absorb_q");
-    hipLaunchKernelGGL(k_absorb_q, dim3((unsigned)(rows * heads)), dim3(256), 0, ctx->stream,
-                       kv_b->fmt, (const uint8_t *)kv_b->payload, kv_b->scales, kv_b->row_bytes,
-                       kv_b->in_dim, q, heads, nope, rope, nope + vh, qabs, qrope);
+    switch (kv_b->fmt) {
+    case UT_FMT_INT8: hipLaunchKernelGGL((k_absorb_q<UT_FMT_INT8, RB>), grid, dim3(threads), 0, ctx->stream, w, kv_b->scales, kv_b->row_bytes, L, q, rows, heads, nope, rope, kvh, qabs, qrope); break;
+    case UT_FMT_INT4: hipLaunchKernelGGL((k_absorb_q<UT_FMT_INT4, RB>), grid, dim3(threads), 0, ctx->stream, w, kv_b->scales, kv_b->row_bytes, L, q, rows, heads, nope, rope, kvh, qabs, qrope); break;
+    default: hipLaunchKernelGGL((k_absorb_q<UT_FMT_F32, RB>), grid, dim3(threads), 0, ctx->stream, w, kv_b->scales, kv_b->row_bytes, L, q, rows, heads, nope, rope, kvh, qabs, qrope); break;
+    }
     timing_end(ctx, tok);
     return launch_check(ctx, "k_absorb_q");
 }
 
-// ctx values: one wave per (row, head, output j); lanes split the latent
-// columns, then a fixed butterfly.
-__global__ __launch_bounds__(256) void k_absorb_v(int32_t fmt, const uint8_t *__restrict__ w,
+// ctx values: one workgroup per (head, 16 output rows j, group of up to 4
+// query rows); 16 sub-lanes per row each take L/16 columns in 4-column
+// pieces, then a fixed butterfly.  The value of (row r, output j) is read
+// from sub-lane r, whatever the number of query rows.
+template <int FMT, int RB>
+__global__ __launch_bounds__(256) void k_absorb_v(const uint8_t *__restrict__ w,
                                                   const float *__restrict__ scales,
                                                   int64_t row_bytes, int64_t L,
-                                                  const float *__restrict__ clat, int64_t heads,
-                                                  int64_t nope, int64_t vh,
+                                                  const float *__restrict__ clat, int64_t rows,
+                                                  int64_t heads, int64_t nope, int64_t vh,
                                                   float *__restrict__ out) {
-    const int64_t sh = blockIdx.x;
-    const int64_t h = sh % heads, s = sh / heads;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const float *x = clat + sh * L;
-    for (int64_t j = wave; j < vh; j += 4) {
-        const int64_t row = h * (nope + vh) + nope + j;
-        const uint8_t *wr = w + row * row_bytes;
-        float acc = 0.0f;
-        for (int64_t i = lane; i < L; i += 64) acc = __builtin_fmaf(x[i], code_at(fmt, wr, i), acc);
-        for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
-        acc = __shfl(acc, 0, 64);
-        if (lane == 0) out[s * heads * vh + h * vh + j] = fmt == UT_FMT_F32 ? acc : __fmul_rn(acc, scales[row]);
+    const int64_t h = blockIdx.x, r0 = (int64_t)blockIdx.z * RB;
+    const int jl = threadIdx.x >> 4, s = threadIdx.x & 15;
+    const int64_t j = (int64_t)blockIdx.y * 16 + jl;
+    const int64_t jc = j < vh ? j : vh - 1;
+    const int64_t row = h * (nope + vh) + nope + jc;
+    const uint8_t *wr = w + row * row_bytes;
+    float acc[RB];
+#pragma unroll
+    for (int r = 0; r < RB; r++) acc[r] = 0.0f;
+    for (int64_t c = 4 * s; c < L; c += 64) {
+        const float4 cw = codes4<FMT>(wr, c);
+#pragma unroll
+        for (int r = 0; r < RB; r++) {
+            const int64_t rr = r0 + r < rows ? r0 + r : rows - 1;
+            const float4 xv = *(const float4 *)(clat + (rr * heads + h) * L + c);
+            float a = acc[r];
+            a = __builtin_fmaf(xv.x, cw.x, a);
+            a = __builtin_fmaf(xv.y, cw.y, a);
+            a = __builtin_fmaf(xv.z, cw.z, a);
+            a = __builtin_fmaf(xv.w, cw.w, a);
+            acc[r] = a;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RB; r++) {
+        float v = acc[r];
+#pragma unroll
+        for (int off = 8; off >= 1; off >>= 1) v += __shfl_xor(v, off, 16);
+        if (s == r && j < vh && r0 + r < rows)
+            out[(r0 + r) * heads * vh + h * vh + j] = FMT == UT_FMT_F32 ? v : __fmul_rn(v, scales[row]);
     }
 }
 
 int32_t launch_absorb_v(ut_ctx *ctx, const ut_qtensor *kv_b, const float *clat, int64_t rows,
                         int64_t heads, int64_t nope, int64_t vh, float *out) {
     if (rows <= 0) return UT_OK;
+    const int64_t L = kv_b->in_dim;
+    if (L % 4 != 0) {
+        set_error(ctx, "absorb: kv_lora_rank %lld must be a multiple of 4", (long long)L);
+        return UT_ERR_SHAPE;
+    }
+    constexpr int RB = 4;
+    dim3 grid((unsigned)heads, (unsigned)((vh + 15) / 16), (unsigned)((rows + RB - 1) / RB));
+    const uint8_t *w = (const uint8_t *)kv_b->payload;
     int tok = timing_begin(ctx, "absorb_v");
-    hipLaunchKernelGGL(k_absorb_v, dim3((unsigned)(rows * heads)), dim3(256), 0, ctx->stream,
-                       kv_b->fmt, (const uint8_t *)kv_b->payload, kv_b->scales, kv_b->row_bytes,
-                       kv_b->in_dim, clat, heads, nope, vh, out);
+    switch (kv_b->fmt) {
+    case UT_FMT_INT8: hipLaunchKernelGGL((k_absorb_v<UT_FMT_INT8, RB>), grid, dim3(256), 0, ctx->stream, w, kv_b->scales, kv_b->row_bytes, L, clat, rows, heads, nope, vh, out); break;
+    case UT_FMT_INT4: hipLaunchKernelGGL((k_absorb_v<UT_FMT_INT4, RB>), grid, dim3(256), 0, ctx->stream, w, kv_b->scales, kv_b->row_bytes, L, clat, rows, heads, nope, vh, out); break;
+    default: hipLaunchKernelGGL((k_absorb_v<UT_FMT_F32, RB>), grid, dim3(256), 0, ctx->stream, w, kv_b->scales, kv_b->row_bytes, L, clat, rows, heads, nope, vh, out); break;
+    }
     timing_end(ctx, tok);
     return launch_check(ctx, "k_absorb_v");
 }
