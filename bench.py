@@ -203,6 +203,8 @@ def main():
     ap.add_argument("--mtp", default="c1,c4", help="comma list of c1,c4 or 'none'")
     ap.add_argument("--variants", action="store_true", default=True)
     ap.add_argument("--no-variants", dest="variants", action="store_false")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run a plain 1 GiB device copy (counter scaling for rocprofv3 --pmc)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -233,6 +235,17 @@ def main():
         variants["int8_M1"] = r
         log(f"config 2 int8 M=1: {r['gbs']:.1f} GB/s")
         del tbl8
+        torch.cuda.empty_cache()
+
+    if args.copy_probe:
+        n = 1 << 30
+        a = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        log(f"copy probe: 3 x {n} bytes")
+        del a, b
         torch.cuda.empty_cache()
 
     mtp = {}
