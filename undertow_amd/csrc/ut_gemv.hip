@@ -63,23 +63,23 @@ struct RowDigArgs {
     int32_t *exps;
     uint32_t *dig4, *dig8;
     int32_t *xt;
+    // optional slot plan built by the launch's last workgroup
+    const int32_t *plan_ids;
+    int plan_M, plan_k, plan_E;
+    const uint8_t *const *gate_tbl;
+    MoePlan plan;
+    int32_t *err_flag;
 };
-
-template <typename T, typename Op>
-__device__ __forceinline__ T block_reduce(T v, Op op, T *red4) {
-    for (int off = 32; off >= 1; off >>= 1) v = op(v, __shfl_xor(v, off, 64));
-    if ((threadIdx.x & 63) == 0) red4[threadIdx.x >> 6] = v;
-    __syncthreads();
-    T r = op(op(red4[0], red4[1]), op(red4[2], red4[3]));
-    __syncthreads();
-    return r;
-}
 
 __global__ __launch_bounds__(256) void k_rowdig(RowDigArgs a) {
     extern __shared__ float row[];
     __shared__ double redd[4];
     __shared__ uint32_t redu[4];
     const int64_t m = blockIdx.x;
+    if (a.plan_ids && blockIdx.x == gridDim.x - 1) {
+        make_plan(a.plan_ids, a.plan_M, a.plan_k, a.plan_E, a.gate_tbl, -1, a.plan, a.err_flag);
+        return;
+    }
     if (a.slot_count && (int)(m / a.rows_per_slot) >= *a.slot_count) return;
     const int tid = threadIdx.x;
     const int64_t K = a.K;
@@ -88,6 +88,7 @@ __global__ __launch_bounds__(256) void k_rowdig(RowDigArgs a) {
     float r = 1.0f;
     if (a.norm_w) {
         double acc = 0.0;
+#pragma unroll 8
         for (int64_t i = tid; i < K; i += 256) {
             const double v = (double)xr[i];
             acc += v * v;
@@ -99,6 +100,7 @@ __global__ __launch_bounds__(256) void k_rowdig(RowDigArgs a) {
         return a.norm_w ? __fmul_rn(__fmul_rn(xr[i], r), a.norm_w[i]) : xr[i];
     };
     uint32_t mx = 0;
+#pragma unroll 8
     for (int64_t i = tid; i < K; i += 256) {
         const float v = val(i);
         if (staged) row[i] = v;
@@ -163,7 +165,8 @@ static int32_t launch_rowdig(ut_ctx *ctx, const RowDigArgs &a, int64_t M, const 
     if (M <= 0) return UT_OK;
     const size_t shmem = a.K <= kRowLds ? (size_t)a.K * 4 : 0;
     int tok = timing_begin(ctx, name);
-    hipLaunchKernelGGL(k_rowdig, dim3((unsigned)M), dim3(256), shmem, ctx->stream, a);
+    hipLaunchKernelGGL(k_rowdig, dim3((unsigned)(M + (a.plan_ids ? 1 : 0))), dim3(256), shmem,
+                       ctx->stream, a);
     timing_end(ctx, tok);
     return launch_check(ctx, "k_rowdig");
 }
@@ -195,6 +198,27 @@ int32_t launch_digitize_slots(ut_ctx *ctx, const float *x, int64_t ldx, int64_t 
     a.dig8 = (flags & XD_DIG8) ? xd.dig8 : nullptr;
     a.xt = (flags & XD_XT) ? xd.xt : nullptr;
     return launch_rowdig(ctx, a, M, "digitize");
+}
+
+int32_t launch_digitize_plan(ut_ctx *ctx, const float *x, int64_t M, int64_t K, XDigits xd,
+                             int flags, const int32_t *ids, int k, int64_t E,
+                             const uint8_t *const *gate_tbl, MoePlan plan, int32_t *err_flag) {
+    RowDigArgs a{};
+    a.x = x;
+    a.ldx = K;
+    a.K = K;
+    a.exps = xd.exps;
+    a.dig4 = (flags & XD_DIG4) ? xd.dig4 : nullptr;
+    a.dig8 = (flags & XD_DIG8) ? xd.dig8 : nullptr;
+    a.xt = (flags & XD_XT) ? xd.xt : nullptr;
+    a.plan_ids = ids;
+    a.plan_M = (int)M;
+    a.plan_k = k;
+    a.plan_E = (int)E;
+    a.gate_tbl = gate_tbl;
+    a.plan = plan;
+    a.err_flag = err_flag;
+    return launch_rowdig(ctx, a, M, "digitize_plan");
 }
 
 int32_t launch_rmsnorm_digitize(ut_ctx *ctx, const float *x, int64_t ldx, int64_t M, int64_t K,

@@ -61,13 +61,37 @@ __host__ __device__ constexpr int gemv_chunk_cols() {
     return cols / T::kStepCols * T::kStepCols;
 }
 
-// Activations of one GEMV: digits (int formats) or f32 values.
+// Activations of one GEMV: digits (int formats) or f32 values.  For int
+// formats with dig == nullptr, xf is digitised while it is staged, with
+// x~ = rint(x * 2^sh[m]) (sh[m] = 22 - E of the row; INT32_MIN: non-finite).
 struct XSrc {
     const uint32_t *dig;  // [M][planes][KW] words (int formats)
     int64_t KW;           // words per plane row
     const float *xf;      // [M][ldx] (f32)
     int64_t ldx;
+    int32_t sh[4];        // staging-time digitisation shifts (dig == nullptr)
 };
+
+// Balanced digits of 8 (int4) or 4 (int8) columns, one word per plane.
+template <int FMT>
+__device__ __forceinline__ void digit_words(const float *v, int n, int32_t sh,
+                                            uint32_t *w /* [planes] */) {
+    constexpr int PL = FMT == UT_FMT_INT4 ? 6 : 3;
+    constexpr int B = FMT == UT_FMT_INT4 ? 4 : 8;
+    constexpr int32_t HALF = 1 << (B - 1), MASK = (1 << B) - 1;
+#pragma unroll
+    for (int p = 0; p < PL; p++) w[p] = 0;
+#pragma unroll
+    for (int j = 0; j < n; j++) {
+        int32_t q = sh == INT32_MIN ? 0 : (int32_t)rintf(ldexpf(v[j], sh));
+#pragma unroll
+        for (int p = 0; p < PL; p++) {
+            const int32_t d = ((q + HALF) & MASK) - HALF;  // balanced digit
+            q = (q - d) >> B;
+            w[p] |= (uint32_t)(d & MASK) << (B * j);
+        }
+    }
+}
 
 __device__ inline int64_t shfl_xor_i64(int64_t v, int off) {
     int lo = __shfl_xor((int)(uint32_t)(uint64_t)v, off, 16);
@@ -129,13 +153,34 @@ __device__ __forceinline__ void gemv_core(const uint8_t *const rows[R], int64_t 
                 float4 v = *(const float4 *)(x.xf + m * x.ldx + kc + 4 * c);
                 *(float4 *)(lds + m * KC + 4 * c) = v;
             }
-        } else {
+        } else if (x.dig) {
             const int n4 = kcn / T::kColsPerWord / 4;  // uint4 per plane row
             const int64_t w0 = kc / T::kColsPerWord;
             for (int i = tid; i < M * PL * n4; i += kGemvThreads) {
                 int mp = i / n4, c = i - mp * n4;
                 uint4 v = *(const uint4 *)(x.dig + (int64_t)mp * x.KW + w0 + 4 * c);
                 *(uint4 *)(lds + mp * LW + 4 * c) = v;
+            }
+        } else {
+            // digitise f32 activations into the LDS planes
+            constexpr int CPW = T::kColsPerWord;
+            const int ng = kcn / CPW;  // words per plane row in the chunk
+            for (int i = tid; i < M * ng; i += kGemvThreads) {
+                const int m = i / ng, g = i - m * ng;
+                const float *src = x.xf + m * x.ldx + kc + g * CPW;
+                float v[CPW];
+                if constexpr (CPW == 8) {
+                    const float4 a = *(const float4 *)src, b = *(const float4 *)(src + 4);
+                    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+                    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+                } else {
+                    const float4 a = *(const float4 *)src;
+                    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+                }
+                uint32_t w[PL];
+                digit_words<FMT>(v, CPW, x.sh[m], w);
+#pragma unroll
+                for (int p = 0; p < PL; p++) lds[(m * PL + p) * LW + g] = w[p];
             }
         }
         __syncthreads();
@@ -237,6 +282,16 @@ __device__ __forceinline__ void gemv_core(const uint8_t *const rows[R], int64_t 
                 res.F[r][m] = 0.0f;
             }
         }
+}
+
+template <typename T, typename Op>
+__device__ __forceinline__ T block_reduce(T v, Op op, T *red4) {
+    for (int off = 32; off >= 1; off >>= 1) v = op(v, __shfl_xor(v, off, 64));
+    if ((threadIdx.x & 63) == 0) red4[threadIdx.x >> 6] = v;
+    __syncthreads();
+    T r = op(op(red4[0], red4[1]), op(red4[2], red4[3]));
+    __syncthreads();
+    return r;
 }
 
 // Converts an exact integer total to the reference's f32 row value:

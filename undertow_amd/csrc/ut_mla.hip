@@ -58,6 +58,7 @@ __global__ __launch_bounds__(256) void k_mla_split(const float *__restrict__ qab
         if (live) {
             // score = sum_i q_i*lat_i + sum_i qr_i*krot_i, sequential adds
             const float *lr = latent + pos * L;
+#pragma unroll 8
             for (int d = 0; d < L; d += 4) {
                 const float4 kv = *(const float4 *)(lr + d);
 #pragma unroll
@@ -72,6 +73,7 @@ __global__ __launch_bounds__(256) void k_mla_split(const float *__restrict__ qab
                 }
             }
             const float *kr = krot + pos * P;
+#pragma unroll 8
             for (int d = 0; d < P; d++) {
                 const float kv = kr[d];
 #pragma unroll
@@ -103,6 +105,7 @@ __global__ __launch_bounds__(256) void k_mla_split(const float *__restrict__ qab
         float o[HG];
 #pragma unroll
         for (int hh = 0; hh < HG; hh++) o[hh] = 0.0f;
+#pragma unroll 16
         for (int64_t t = 0; t < tn; t++) {
             const float kv = latent[(t0 + t) * L + d];
 #pragma unroll
@@ -123,12 +126,14 @@ __global__ __launch_bounds__(256) void k_mla_combine(const float *__restrict__ p
     const int64_t n_ctx = pos_base + r + 1;
     const int ns = (int)((n_ctx + kMlaSlice - 1) / kMlaSlice);
     float M = -INFINITY;
+#pragma unroll 8
     for (int j = 0; j < ns; j++) M = fmaxf(M, part_m[qi * nsplit + j]);
     float Lsum = 0.0f;
     for (int j = 0; j < ns; j++) Lsum = __fadd_rn(Lsum, __fmul_rn(part_l[qi * nsplit + j], expf(part_m[qi * nsplit + j] - M)));
     const float inv = 1.0f / Lsum;
     for (int d = threadIdx.x; d < L; d += 256) {
         float acc = 0.0f;
+#pragma unroll 8
         for (int j = 0; j < ns; j++)
             acc = __builtin_fmaf(part_o[(qi * nsplit + j) * L + d], expf(part_m[qi * nsplit + j] - M), acc);
         clat[qi * L + d] = __fmul_rn(acc, inv);

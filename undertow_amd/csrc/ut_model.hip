@@ -72,6 +72,7 @@ struct ut_model {
     float2 *rope_table = nullptr;  // [max_pos][rope/2]
     int32_t *zeros = nullptr;      // [4] expert id 0 (MLP as a one-slot table)
     float *ones = nullptr;         // [4] weight 1
+    MoePlan mlp_plan{};            // the fixed one-slot plan of an MLP
     bool finalized = false;
     std::vector<void *> device_allocs;
     int64_t device_bytes = 0;
@@ -392,9 +393,11 @@ int32_t norm_dig(ut_session *s, const float *x, int64_t ldx, const float *w, int
 }
 
 // An MLP (dense FFN or shared expert) over rows, added into out
-// (MlpWeights::forward_add, model.rs:43-58).  xd: digits of x.
+// (MlpWeights::forward_add, model.rs:43-58).  xd: digits of x.  With init,
+// out = out + (init + mlp(x)) instead (the shared expert added to the routed
+// sum, then the residual add, in the reference's order).
 int32_t mlp_add(ut_session *s, const MlpW &w, const float *x, const XDigits &xd, int64_t rows,
-                float *out) {
+                float *out, const float *init = nullptr) {
     ut_model *m = s->m;
     for (int64_t s0 = 0; s0 < rows; s0 += 4) {
         MoeCall c;
@@ -414,14 +417,16 @@ int32_t mlp_add(ut_session *s, const MlpW &w, const float *x, const XDigits &xd,
         c.ldo = c.H;
         c.accumulate = 1;
         c.err_flag = s->ws.err;
+        c.plan = &m->mlp_plan;
+        c.init = init ? init + s0 * c.H : nullptr;
         UT_TRY(moe_pass(m->ctx, c, s->ws.moe));
     }
     return UT_OK;
 }
 
-// moe_forward (model.rs:195-286): router, routed experts in choice order,
-// then the shared expert, into out (overwritten).  x: normed rows (f32, for
-// the f32 router gate) with digits xd.
+// The routed part of moe_forward (model.rs:195-281): router, routed experts
+// in choice order, into out (overwritten).  x: normed rows (f32, for the f32
+// router gate) with digits xd.
 int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigits &xd,
                     int64_t rows, float *out) {
     ut_model *m = s->m;
@@ -458,12 +463,11 @@ int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
         mc.plan_ready = true;
         UT_TRY(moe_pass(m->ctx, mc, s->ws.moe));
     }
-    if (L.has_shared) UT_TRY(mlp_add(s, L.shared, x, xd, rows, out));
     return UT_OK;
 }
 
-// mla_forward_cached, absorbed form (attention.rs:123-279).  x: normed rows
-// with digits xd.
+// mla_forward_cached, absorbed form (attention.rs:123-279), added into out
+// (the residual).  x: normed rows with digits xd.
 int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, const XDigits &xd,
                     int64_t rows, KvCache &kv, float *out) {
     ut_model *m = s->m;
@@ -485,18 +489,11 @@ int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
     } else {
         UT_TRY(matmul_digits(ctx, L.q_proj, x, xd, rows, w.q, heads * qh, 0));
     }
-    const int64_t half = rope / 2;
-    UT_TRY(launch_rope(ctx, w.q + nope, rows, heads, heads * qh, qh, rope, pos_base, m->rope_table,
-                       half));
-    UT_TRY(launch_rmsnorm(ctx, w.comp, Lr + rope, L.kv_a_norm, Lr, c.rms_norm_eps, rows,
-                          kv.latent + pos_base * Lr, Lr));
-    UT_CHECK_HIP(ctx, hipMemcpy2DAsync(kv.krot + pos_base * rope, rope * 4, w.comp + Lr,
-                                       (Lr + rope) * 4, rope * 4, rows, hipMemcpyDeviceToDevice,
-                                       ctx->stream));
-    UT_TRY(launch_rope(ctx, kv.krot + pos_base * rope, rows, 1, rope, rope, rope, pos_base,
-                       m->rope_table, half));
+    UT_TRY(launch_kv_append(ctx, w.comp, rows, Lr, rope, L.kv_a_norm, c.rms_norm_eps, kv.latent,
+                            kv.krot, pos_base, m->rope_table));
     kv.len = pos_base + rows;
-    UT_TRY(launch_absorb_q(ctx, L.kv_b, w.q, rows, heads, nope, rope, vh, w.qabs, w.qrope));
+    UT_TRY(launch_absorb_q(ctx, L.kv_b, w.q, rows, heads, nope, rope, vh, w.qabs, w.qrope,
+                           pos_base, m->rope_table));
     // query rows in groups of kMlaRowsPerCall (bounded scratch; a row's
     // result does not depend on its group)
     for (int64_t r0 = 0; r0 < rows; r0 += kMlaRowsPerCall) {
@@ -506,7 +503,8 @@ int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
                                  w.clat + r0 * heads * Lr, w.mla));
     }
     UT_TRY(launch_absorb_v(ctx, L.kv_b, w.clat, rows, heads, nope, vh, w.ctxv));
-    return mm(s, L.o_proj, w.ctxv, rows, out, c.hidden_size);
+    // x += o_proj(ctx) (the residual add of model.rs:478-480 in the epilogue)
+    return mm(s, L.o_proj, w.ctxv, rows, out, c.hidden_size, 1);
 }
 
 // run_layer (model.rs:127-183) / the per-layer body of prefill (:470-526).
@@ -519,8 +517,7 @@ int32_t run_layer(ut_session *s, const LayerW &L, float *x, int64_t rows, KvCach
     XDigits xd;
     UT_TRY(norm_dig(s, x, H, L.input_norm, H, rows, w.normed, H, w.digA,
                     dig_flags({L.q_a, L.q_proj, L.kv_a}), &xd));
-    UT_TRY(mla_forward(s, L, w.normed, xd, rows, kv, w.attn));
-    UT_TRY(launch_add(ctx, x, w.attn, rows * H));
+    UT_TRY(mla_forward(s, L, w.normed, xd, rows, kv, x));
     int f = 0;
     if (L.dense) f = dig_flags_fmt(L.mlp.fmt, H);
     else {
@@ -530,6 +527,8 @@ int32_t run_layer(ut_session *s, const LayerW &L, float *x, int64_t rows, KvCach
     UT_TRY(norm_dig(s, x, H, L.post_norm, H, rows, w.normed, H, w.digA, f, &xd));
     if (L.dense) return mlp_add(s, L.mlp, w.normed, xd, rows, x);
     UT_TRY(moe_forward(s, L, w.normed, xd, rows, w.moe_out));
+    // x += (routed + shared) (model.rs:282-284 then the residual add)
+    if (L.has_shared) return mlp_add(s, L.shared, w.normed, xd, rows, x, w.moe_out);
     return launch_add(ctx, x, w.moe_out, rows * H);
 }
 
@@ -918,6 +917,14 @@ int32_t ut_model_finalize(ut_model *m) {
     UT_CHECK_HIP(ctx, hipMemcpy(o, os, 16, hipMemcpyHostToDevice));
     m->zeros = (int32_t *)z;
     m->ones = (float *)o;
+    // fixed plan of an MLP run as a one-expert block: count 1, slot 0 = expert 0
+    void *pl = nullptr;
+    UT_TRY(dev_alloc(m, 64, &pl));
+    const int32_t plan_init[16] = {1, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    UT_CHECK_HIP(ctx, hipMemcpy(pl, plan_init, 64, hipMemcpyHostToDevice));
+    m->mlp_plan.count = (int32_t *)pl;
+    m->mlp_plan.uniq = (int32_t *)pl + 4;
+    m->mlp_plan.choice_slot = (int32_t *)pl + 8;
     m->finalized = true;
     return UT_OK;
 }

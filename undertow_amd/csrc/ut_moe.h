@@ -39,6 +39,8 @@ struct MoeCall {
     int extra_slot = -1;  // >= 0: expert id always appended as the last slot, added with weight 1
     int32_t *err_flag = nullptr;
     bool plan_ready = false;  // the slot plan is already in the scratch (launch_route_plan)
+    const MoePlan *plan = nullptr;  // a fixed plan elsewhere (one-slot MLPs)
+    const float *init = nullptr;    // combine starts from init[M, ldo] instead of zero
 };
 
 struct ScratchLayout {
@@ -47,6 +49,44 @@ struct ScratchLayout {
     int xflags = 0, hflags = 0;
     int64_t ntiles = 0;
 };
+
+// Slots in first-appearance order over (row, choice) -- the order in which
+// moe_forward groups rows by expert (model.rs:219-233).  Invalid ids (out of
+// range or not loaded) set the sticky error flag and contribute nothing.
+// Whole-workgroup function: ids are read once in parallel, the assignment
+// runs in LDS, the plan is written out in parallel.  n = M*k <= 256.
+__device__ inline void make_plan(const int32_t *ids, int M, int k, int E,
+                          const uint8_t *const *__restrict__ gate_tbl, int extra_slot,
+                          MoePlan plan, int32_t *__restrict__ err_flag) {
+    __shared__ int s_e[256], s_slot[256], s_uniq[257], s_U;
+    const int n = M * k, tid = threadIdx.x;
+    if (tid < n) {
+        const int e = ids[tid];
+        const bool ok = e >= 0 && e < E && gate_tbl[e] != nullptr;
+        if (!ok && e != -1 && err_flag) *err_flag = 1;
+        s_e[tid] = ok ? e : -1;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int U = 0;
+        for (int i = 0; i < n; i++) {
+            const int e = s_e[i];
+            int slot = -1;
+            if (e >= 0) {
+                for (int u = 0; u < U; u++)
+                    if (s_uniq[u] == e) { slot = u; break; }
+                if (slot < 0) { slot = U; s_uniq[U++] = e; }
+            }
+            s_slot[i] = slot;
+        }
+        if (extra_slot >= 0) s_uniq[U++] = extra_slot;  // a dense MLP run as one more slot
+        s_U = U;
+    }
+    __syncthreads();
+    if (tid < n) plan.choice_slot[tid] = s_slot[tid];
+    if (tid < s_U) plan.uniq[tid] = s_uniq[tid];
+    if (tid == 0) *plan.count = s_U;
+}
 
 inline int64_t moe_slots(int M, int64_t k, int64_t E, int extra) {
     int64_t s = (int64_t)M * k;
@@ -73,6 +113,13 @@ int32_t launch_route(ut_ctx *ctx, const float *logits, const float *bias, int64_
 
 // Digitise rows of x in slot groups of rows_per_slot rows; groups at or past
 // *slot_count are skipped.
+// Digitise x [M, K] and, in one extra workgroup of the same launch, build
+// the slot plan of (ids, M, k) -- the two independent set-up steps of an
+// expert pass.
+int32_t launch_digitize_plan(ut_ctx *ctx, const float *x, int64_t M, int64_t K, XDigits xd,
+                             int flags, const int32_t *ids, int k, int64_t E,
+                             const uint8_t *const *gate_tbl, MoePlan plan, int32_t *err_flag);
+
 int32_t launch_digitize_slots(ut_ctx *ctx, const float *x, int64_t ldx, int64_t M, int64_t K,
                               const uint32_t *rowmax_parts, int32_t nparts, XDigits xd,
                               int flags, const int32_t *slot_count, int rows_per_slot);

@@ -10,8 +10,8 @@
 //   k_moe_gate_up  grid (I/16, slots): gate and up rows of one expert in the
 //                  same lanes, h = silu(g)*u written per (slot, row), plus
 //                  per-workgroup max|h| partials
-//   k_digitize     digits of h per (slot, row)
-//   k_moe_down     grid (H/64 or H/32, slots): d = down(h) per (slot, row)
+//   k_moe_down     grid (H/64 or H/32, slots): d = down(h) per (slot, row),
+//                  h digitised while it is staged (exponent from the partials)
 //   k_moe_combine  out[s] = sum_c w[s,c]*d[slot(s,c), s] in router order
 // Every expert's weights are read once per pass whatever rows chose it;
 // the row dimension rides along in the same instructions.
@@ -50,10 +50,12 @@ __device__ void route_row(const float *__restrict__ lg, const float *__restrict_
         for (int g = tid; g < n_group; g += blockDim.x) {
             const float *v = corr + g * gs;
             int b0 = 0;
+#pragma unroll 8
             for (int i = 1; i < gs; i++) if (v[i] > v[b0]) b0 = i;
             float s = 0.0f + v[b0];
             if (gs > 1) {
                 int b1 = b0 == 0 ? 1 : 0;
+#pragma unroll 8
                 for (int i = 0; i < gs; i++)
                     if (i != b0 && ranks_before(v[i], i, v[b1], b1)) b1 = i;
                 s = s + v[b1];
@@ -78,23 +80,29 @@ __device__ void route_row(const float *__restrict__ lg, const float *__restrict_
     for (int e = tid; e < E; e += blockDim.x) {
         const float v = corr[e];
         int rank = 0;
+#pragma unroll 16
         for (int j = 0; j < E; j++) rank += ranks_before(corr[j], j, v, e);
         if (rank < keff) s_ids[rank] = e;
     }
     __syncthreads();
+    // weights = sigmoid of the chosen, normalised by their sequential sum
+    // (+1e-20) in choice order, then scaled
+    __shared__ float s_denom;
     if (tid == 0) {
-        float w[64];
         float denom = 0.0f;
-        for (int j = 0; j < keff; j++) { w[j] = sc[s_ids[j]]; denom = denom + w[j]; }
-        denom = denom + 1e-20f;
-        for (int j = 0; j < keff; j++) {
-            float v = norm ? w[j] / denom : w[j];
-            ids[j] = s_ids[j];
-            weights[j] = __fmul_rn(v, scale);
-        }
-        for (int j = keff; j < k; j++) {  // k > E: no expert (contributes nothing)
-            ids[j] = -1;
-            weights[j] = 0.0f;
+        for (int j = 0; j < keff; j++) denom = denom + sc[s_ids[j]];
+        s_denom = denom + 1e-20f;
+    }
+    __syncthreads();
+    if (tid < k) {
+        if (tid < keff) {
+            const float w = sc[s_ids[tid]];
+            const float v = norm ? w / s_denom : w;
+            ids[tid] = s_ids[tid];
+            weights[tid] = __fmul_rn(v, scale);
+        } else {  // k > E: no expert (contributes nothing)
+            ids[tid] = -1;
+            weights[tid] = 0.0f;
         }
     }
     __syncthreads();
@@ -111,31 +119,6 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
     const int row = blockIdx.x;
     route_row(logits + (int64_t)row * E, bias, E, k, n_group, topk_group, norm, scale,
               ids + (int64_t)row * k, weights + (int64_t)row * k, sm, s_ids, s_group_ok);
-}
-
-// Slots in first-appearance order over (row, choice) -- the order in which
-// moe_forward groups rows by expert (model.rs:219-233).  Invalid ids (out of
-// range or not loaded) set the sticky error flag and contribute nothing.
-__device__ void make_plan(const int32_t *__restrict__ ids, int M, int k, int E,
-                          const uint8_t *const *__restrict__ gate_tbl, int extra_slot,
-                          MoePlan plan, int32_t *__restrict__ err_flag) {
-    int U = 0;
-    for (int s = 0; s < M; s++) {
-        for (int c = 0; c < k; c++) {
-            int e = ids[s * k + c];
-            int slot = -1;
-            if (e < 0 || e >= E || gate_tbl[e] == nullptr) {
-                if (e != -1 && err_flag) *err_flag = 1;
-            } else {
-                for (int u = 0; u < U; u++)
-                    if (plan.uniq[u] == e) { slot = u; break; }
-                if (slot < 0) { slot = U; plan.uniq[U++] = e; }
-            }
-            plan.choice_slot[s * k + c] = slot;
-        }
-    }
-    if (extra_slot >= 0) plan.uniq[U++] = extra_slot;  // a dense MLP run as one more slot
-    *plan.count = U;
 }
 
 // Routing of M <= 4 rows plus the slot plan in one workgroup (one launch on
@@ -157,13 +140,13 @@ __global__ __launch_bounds__(256) void k_route_plan(const float *__restrict__ lo
         if (threadIdx.x < k) s_all[row * k + threadIdx.x] = ids[(int64_t)row * k + threadIdx.x];
     }
     __syncthreads();
-    if (threadIdx.x == 0) make_plan(s_all, M, k, E, gate_tbl, -1, plan, err_flag);
+    make_plan(s_all, M, k, E, gate_tbl, -1, plan, err_flag);
 }
 
-__global__ void k_moe_plan(const int32_t *__restrict__ ids, int M, int k, int E,
+__global__ __launch_bounds__(256) void k_moe_plan(const int32_t *__restrict__ ids, int M, int k, int E,
                            const uint8_t *const *__restrict__ gate_tbl, int extra_slot,
                            MoePlan plan, int32_t *__restrict__ err_flag) {
-    if (threadIdx.x == 0) make_plan(ids, M, k, E, gate_tbl, extra_slot, plan, err_flag);
+    make_plan(ids, M, k, E, gate_tbl, extra_slot, plan, err_flag);
 }
 
 int32_t launch_route(ut_ctx *ctx, const float *logits, const float *bias, int64_t rows,
@@ -258,9 +241,10 @@ struct DownArgs {
     const int32_t *uniq;
     const int32_t *count;
     int64_t H, I, row_bytes;  // down is [H, I]
-    XSrc x;                   // digits of h: slot u's rows start at u*M
-    int64_t x_slot_stride;    // words (or floats) between slots
-    const int32_t *exps;      // [slots*M]
+    XSrc x;                   // h (f32, digitised while staged): slot u's rows start at u*M
+    int64_t x_slot_stride;    // floats between slots
+    const uint32_t *hmax_parts;  // [slots*M][nparts] max|h| bits from the gate/up kernel
+    int nparts;
     float *d;                 // [slots][M][H]
 };
 
@@ -285,8 +269,31 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_down(DownArgs a) {
         rows[r] = dw + o * a.row_bytes;
     }
     XSrc xs = a.x;
-    if constexpr (FMT == UT_FMT_F32) xs.xf = a.x.xf + u * a.x_slot_stride;
-    else xs.dig = a.x.dig + u * a.x_slot_stride;
+    xs.xf = a.x.xf + u * a.x_slot_stride;
+    xs.dig = nullptr;
+    int32_t exl[M];
+    if constexpr (FMT != UT_FMT_F32) {
+        // the row exponent of h from the gate/up workgroups' partial maxima
+        __shared__ uint32_t red4[4];
+        __shared__ int32_t s_sh[4];
+        for (int m = 0; m < M; m++) {
+            uint32_t mx = 0;
+            for (int i = tid; i < a.nparts; i += kGemvThreads)
+                mx = max(mx, a.hmax_parts[((int64_t)u * M + m) * a.nparts + i]);
+            mx = block_reduce(mx, [](uint32_t p, uint32_t q) { return p > q ? p : q; }, red4);
+            if (tid == 0) {
+                int E = 0;
+                if (mx < 0x7f800000u && mx != 0) (void)frexpf(__uint_as_float(mx), &E);
+                s_sh[m] = mx >= 0x7f800000u ? INT32_MIN : 22 - E;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            xs.sh[m] = s_sh[m];
+            exl[m] = s_sh[m] == INT32_MIN ? INT32_MIN : -s_sh[m];
+        }
+    }
     CoreOut<FMT, M, R> res;
     gemv_core<FMT, M, R>(rows, a.I, xs, lds, res);
 #pragma unroll
@@ -295,7 +302,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_down(DownArgs a) {
         for (int m = 0; m < M; m++) {
             const int64_t o = row0 + r;
             if (s == 4 * r + m && o < a.H) {
-                float v = core_value<FMT, M, R>(res, r, m, a.exps + u * M, dsc, o);
+                float v = core_value<FMT, M, R>(res, r, m, exl, dsc, o);
                 a.d[((int64_t)u * M + m) * a.H + o] = v;
             }
         }
@@ -304,16 +311,19 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_down(DownArgs a) {
 // ------------------------------------------------------------ combine ---
 // out[s, o] = sum_c w[s,c] * d[slot(s,c), s, o], in router choice order from
 // zero (model.rs:268-281: moe_out starts zeroed; the reference adds
-// w*d per choice).  extra >= 0: then += d[extra, s, o] (a dense MLP slot,
-// MlpWeights::forward_add, model.rs:282-284).  accumulate: out += result.
+// w*d per choice) or from init[s, o].  extra >= 0: then += d[extra, s, o]
+// (a dense MLP slot, MlpWeights::forward_add, model.rs:282-284).
+// accumulate: out += result.
 __global__ void k_moe_combine(const int32_t *__restrict__ choice_slot,
                               const float *__restrict__ weights, const float *__restrict__ d,
                               int M, int k, int64_t H, const int32_t *__restrict__ count,
-                              int extra, float *__restrict__ out, int64_t ldo, int accumulate) {
+                              int extra, const float *__restrict__ init, float *__restrict__ out,
+                              int64_t ldo, int accumulate) {
     const int s = blockIdx.y;
     const int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (o >= H) return;
-    float acc = 0.0f;
+    float acc = init ? init[s * ldo + o] : 0.0f;
+#pragma unroll 8
     for (int c = 0; c < k; c++) {
         int slot = choice_slot[s * k + c];
         if (slot < 0) continue;
@@ -356,16 +366,9 @@ ScratchLayout moe_layout(int64_t M, int64_t k, int64_t slots, int64_t H, int64_t
 template <int FMT, int M>
 static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L, char *base,
                           int64_t slots) {
-    MoePlan plan = moe_plan_view(base, L);
+    MoePlan plan = c.plan ? *c.plan : moe_plan_view(base, L);
+    const bool need_plan = !c.plan_ready && !c.plan;
     int tok = -1;
-    if (!c.plan_ready) {
-        tok = timing_begin(ctx, "moe_plan");
-        hipLaunchKernelGGL(k_moe_plan, dim3(1), dim3(64), 0, ctx->stream, c.ids, M, c.k, (int)c.E,
-                           c.tbl.gate_w, c.extra_slot, plan, c.err_flag);
-        timing_end(ctx, tok);
-        UT_TRY(launch_check(ctx, "k_moe_plan"));
-    }
-
     XSrc xs{};
     const int32_t *xexps = nullptr;
     if constexpr (FMT == UT_FMT_F32) {
@@ -373,11 +376,25 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
         xs.ldx = c.H;
     } else {
         XDigits xd = xdigits_view(base + L.xd, M, c.H, L.xflags);
-        if (c.x_digits) xd = *c.x_digits;  // caller already digitised x
-        else UT_TRY(launch_digitize(ctx, c.x, c.H, M, c.H, nullptr, xd, L.xflags));
+        if (c.x_digits) {
+            xd = *c.x_digits;  // caller already digitised x
+        } else if (need_plan && c.extra_slot < 0) {
+            UT_TRY(launch_digitize_plan(ctx, c.x, M, c.H, xd, L.xflags, c.ids, c.k, c.E,
+                                        c.tbl.gate_w, plan, c.err_flag));
+        } else {
+            UT_TRY(launch_digitize(ctx, c.x, c.H, M, c.H, nullptr, xd, L.xflags));
+        }
         xs.dig = FMT == UT_FMT_INT4 ? xd.dig4 : xd.dig8;
         xs.KW = (c.H + FmtTraits<FMT>::kColsPerWord - 1) / FmtTraits<FMT>::kColsPerWord;
         xexps = xd.exps;
+    }
+    const bool planned = FMT != UT_FMT_F32 && !c.x_digits && need_plan && c.extra_slot < 0;
+    if (need_plan && !planned) {
+        tok = timing_begin(ctx, "moe_plan");
+        hipLaunchKernelGGL(k_moe_plan, dim3(1), dim3(256), 0, ctx->stream, c.ids, M, c.k, (int)c.E,
+                           c.tbl.gate_w, c.extra_slot, plan, c.err_flag);
+        timing_end(ctx, tok);
+        UT_TRY(launch_check(ctx, "k_moe_plan"));
     }
     float *h = (float *)(base + L.h);
     uint32_t *hmax = (uint32_t *)(base + L.hmax);
@@ -401,23 +418,9 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
         UT_TRY(launch_check(ctx, "k_moe_gate_up"));
     }
     XSrc hs{};
-    const int32_t *hexps = nullptr;
-    int64_t hstride = 0;
-    if constexpr (FMT == UT_FMT_F32) {
-        hs.xf = h;
-        hs.ldx = c.I;
-        hstride = M * c.I;
-    } else {
-        XDigits hd = xdigits_view(base + L.hd, slots * M, c.I, L.hflags);
-        UT_TRY(launch_digitize_slots(ctx, h, c.I, slots * M, c.I, hmax, (int)L.ntiles, hd,
-                                     L.hflags, plan.count, M));
-        constexpr int PL = FmtTraits<FMT>::kPlanes;
-        const int64_t KW = (c.I + FmtTraits<FMT>::kColsPerWord - 1) / FmtTraits<FMT>::kColsPerWord;
-        hs.dig = FMT == UT_FMT_INT4 ? hd.dig4 : hd.dig8;
-        hs.KW = KW;
-        hstride = (int64_t)M * PL * KW;
-        hexps = hd.exps;
-    }
+    hs.xf = h;
+    hs.ldx = c.I;
+    const int64_t hstride = (int64_t)M * c.I;
     float *d = (float *)(base + L.d);
     {
         DownArgs a;
@@ -429,7 +432,8 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
         a.row_bytes = payload_bytes(FMT, 1, c.I);
         a.x = hs;
         a.x_slot_stride = hstride;
-        a.exps = hexps;
+        a.hmax_parts = hmax;
+        a.nparts = (int)L.ntiles;
         a.d = d;
         tok = timing_begin(ctx, FMT == UT_FMT_INT4 ? "moe_down_int4" : FMT == UT_FMT_INT8 ? "moe_down_int8" : "moe_down_f32");
         constexpr int DR = 16 * down_rows<M>();
@@ -441,7 +445,7 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
     tok = timing_begin(ctx, "moe_combine");
     hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((c.H + 255) / 256), (unsigned)M), dim3(256),
                        0, ctx->stream, plan.choice_slot, c.weights, d, M, c.k, c.H, plan.count,
-                       c.extra_slot >= 0 ? 1 : 0, c.out, c.ldo, c.accumulate);
+                       c.extra_slot >= 0 ? 1 : 0, c.init, c.out, c.ldo, c.accumulate);
     timing_end(ctx, tok);
     return launch_check(ctx, "k_moe_combine");
 }
@@ -601,7 +605,8 @@ void ut_expert_table_free(ut_expert_table *t) {
 int32_t ut_moe_experts(ut_ctx *ctx, const ut_expert_table *tbl, const int32_t *ids_dev,
                        const float *weights_dev, int64_t rows, int32_t top_k, const float *x_dev,
                        float *out_dev) {
-    if (!ctx || !tbl || !ids_dev || !weights_dev || !x_dev || !out_dev || rows < 0 || top_k <= 0) {
+    if (!ctx || !tbl || !ids_dev || !weights_dev || !x_dev || !out_dev || rows < 0 || top_k <= 0 ||
+        top_k > 64) {
         set_error(ctx, "ut_moe_experts: bad argument");
         return UT_ERR_ARG;
     }

@@ -23,10 +23,15 @@ int32_t launch_rope(ut_ctx *ctx, float *v, int64_t rows, int64_t heads, int64_t 
 int32_t launch_add(ut_ctx *ctx, float *y, const float *x, int64_t n);
 // Absorbed query (attention.rs:204-213): for each (s, h)
 //   qabs[s,h,:] = sum_d (q[s,h,d]*scale[h*kvh+d]) * W[h*kvh+d, :]  (d < nope,
-//   adds in d order) and q_rope[s,h,:] = q[s,h,nope:nope+rope].
+//   adds in d order) and q_rope[s,h,:] = rope_interleave(q[s,h,nope:], pos_base+s).
 int32_t launch_absorb_q(ut_ctx *ctx, const ut_qtensor *kv_b, const float *q, int64_t rows,
                         int64_t heads, int64_t nope, int64_t rope, int64_t vh, float *qabs,
-                        float *qrope);
+                        float *qrope, int64_t pos_base, const float2 *table);
+// Cache append (attention.rs:168-186) for rows at positions pos_base..:
+// latent = rmsnorm(comp[:L], w), krot = rope_interleave(comp[L:L+P], pos).
+int32_t launch_kv_append(ut_ctx *ctx, const float *comp, int64_t rows, int64_t L, int64_t P,
+                         const float *w, float eps, float *latent, float *krot, int64_t pos_base,
+                         const float2 *table);
 // Absorbed value (attention.rs:235, QTensor::matvec_rows): for each (s, h)
 //   ctx[s, h*vh + j] = (sum_i clat[s,h,i] * W[h*kvh+nope+j, i]) * scale.
 int32_t launch_absorb_v(ut_ctx *ctx, const ut_qtensor *kv_b, const float *clat, int64_t rows,

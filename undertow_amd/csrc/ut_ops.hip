@@ -23,6 +23,7 @@ __global__ void k_embed(int32_t fmt, const uint8_t *__restrict__ payload,
     const uint8_t *row = payload + id * row_bytes;
     // add_scaled_row(id, 1.0) into zeros: f = 1*scale; 0 + f*q
     const float f = fmt == UT_FMT_F32 ? 1.0f : __fmul_rn(1.0f, scales[id]);
+#pragma unroll 8
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < H;
          i += (int64_t)gridDim.x * blockDim.x)
         out[s * ldo + i] = __fadd_rn(0.0f, __fmul_rn(f, code_at(fmt, row, i)));
@@ -48,6 +49,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, in
     const float *xr = x + s * ldx;
     __shared__ double red[4];
     double acc = 0.0;
+#pragma unroll 8
     for (int64_t i = threadIdx.x; i < n; i += 256) {
         double v = (double)xr[i];
         acc += v * v;
@@ -57,6 +59,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, in
     __syncthreads();
     const double ms = ((red[0] + red[1]) + (red[2] + red[3])) / (double)n;
     const float r = 1.0f / sqrtf(__fadd_rn((float)ms, eps));
+#pragma unroll 8
     for (int64_t i = threadIdx.x; i < n; i += 256)
         out[s * ldo + i] = __fmul_rn(__fmul_rn(xr[i], r), w[i]);
 }
@@ -108,6 +111,7 @@ int32_t launch_rope(ut_ctx *ctx, float *v, int64_t rows, int64_t heads, int64_t 
 }
 
 __global__ void k_add(float *__restrict__ y, const float *__restrict__ x, int64_t n) {
+#pragma unroll 8
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x)
         y[i] = __fadd_rn(y[i], x[i]);
@@ -121,6 +125,49 @@ int32_t launch_add(ut_ctx *ctx, float *y, const float *x, int64_t n) {
     hipLaunchKernelGGL(k_add, dim3(blocks), dim3(256), 0, ctx->stream, y, x, n);
     timing_end(ctx, tok);
     return launch_check(ctx, "k_add");
+}
+
+// Cache append (attention.rs:168-186): latent[pos] = rmsnorm(comp[:L], w),
+// krot[pos] = rope_interleave(comp[L:L+P], pos), one workgroup per row.
+__global__ __launch_bounds__(256) void k_kv_append(const float *__restrict__ comp, int64_t L,
+                                                   int64_t P, const float *__restrict__ w,
+                                                   float eps, float *__restrict__ latent,
+                                                   float *__restrict__ krot, int64_t pos_base,
+                                                   const float2 *__restrict__ table) {
+    const int64_t s = blockIdx.x, pos = pos_base + s;
+    const float *c = comp + s * (L + P);
+    __shared__ double red[4];
+    double acc = 0.0;
+    for (int64_t i = threadIdx.x; i < L; i += 256) {
+        const double v = (double)c[i];
+        acc += v * v;
+    }
+    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    const double ms = ((red[0] + red[1]) + (red[2] + red[3])) / (double)L;
+    const float r = 1.0f / sqrtf(__fadd_rn((float)ms, eps));
+    for (int64_t i = threadIdx.x; i < L; i += 256)
+        latent[pos * L + i] = __fmul_rn(__fmul_rn(c[i], r), w[i]);
+    const int64_t half = P / 2;
+    for (int64_t jj = threadIdx.x; jj < P; jj += 256) {
+        const int64_t j = jj < half ? jj : jj - half;
+        const float a = c[L + 2 * j], b = c[L + 2 * j + 1];
+        const float2 cs = table[pos * half + j];
+        krot[pos * P + jj] = jj < half ? __fsub_rn(__fmul_rn(a, cs.x), __fmul_rn(b, cs.y))
+                                       : __fadd_rn(__fmul_rn(b, cs.x), __fmul_rn(a, cs.y));
+    }
+}
+
+int32_t launch_kv_append(ut_ctx *ctx, const float *comp, int64_t rows, int64_t L, int64_t P,
+                         const float *w, float eps, float *latent, float *krot, int64_t pos_base,
+                         const float2 *table) {
+    if (rows <= 0) return UT_OK;
+    int tok = timing_begin(ctx, "kv_append");
+    hipLaunchKernelGGL(k_kv_append, dim3((unsigned)rows), dim3(256), 0, ctx->stream, comp, L, P, w,
+                       eps, latent, krot, pos_base, table);
+    timing_end(ctx, tok);
+    return launch_check(ctx, "k_kv_append");
 }
 
 // Four consecutive codes of a row as floats (int4: 2 bytes, int8: 4 bytes,
@@ -151,7 +198,8 @@ __global__ __launch_bounds__(128) void k_absorb_q(const uint8_t *__restrict__ w,
                                                   const float *__restrict__ q, int64_t rows,
                                                   int64_t heads, int64_t nope, int64_t rope,
                                                   int64_t kvh, float *__restrict__ qabs,
-                                                  float *__restrict__ qrope) {
+                                                  float *__restrict__ qrope, int64_t pos_base,
+                                                  const float2 *__restrict__ table) {
     const int64_t h = blockIdx.x, r0 = (int64_t)blockIdx.y * RB;
     const int64_t qh = nope + rope;
     const int64_t col = 512 * (int64_t)blockIdx.z + 4 * (int64_t)threadIdx.x;
@@ -187,16 +235,25 @@ __global__ __launch_bounds__(128) void k_absorb_q(const uint8_t *__restrict__ w,
             if (r0 + r < rows) *(float4 *)(qabs + ((r0 + r) * heads + h) * L + col) = acc[r];
     }
     if (blockIdx.z == 0) {
+        // q_rope = rope_interleave(q[nope:], pos_base + r) (attention.rs:106-118,156-166)
+        const int64_t half = rope / 2;
         for (int64_t i = threadIdx.x; i < RB * rope; i += blockDim.x) {
-            const int64_t r = r0 + i / rope, j = i % rope;
-            if (r < rows) qrope[(r * heads + h) * rope + j] = q[(r * heads + h) * qh + nope + j];
+            const int64_t r = r0 + i / rope, jj = i % rope;
+            if (r >= rows) continue;
+            const float *in = q + (r * heads + h) * qh + nope;
+            const int64_t j = jj < half ? jj : jj - half;
+            const float a = in[2 * j], b = in[2 * j + 1];
+            const float2 cs = table[(pos_base + r) * half + j];
+            qrope[(r * heads + h) * rope + jj] =
+                jj < half ? __fsub_rn(__fmul_rn(a, cs.x), __fmul_rn(b, cs.y))
+                          : __fadd_rn(__fmul_rn(b, cs.x), __fmul_rn(a, cs.y));
         }
     }
 }
 
 int32_t launch_absorb_q(ut_ctx *ctx, const ut_qtensor *kv_b, const float *q, int64_t rows,
                         int64_t heads, int64_t nope, int64_t rope, int64_t vh, float *qabs,
-                        float *qrope) {
+                        float *qrope, int64_t pos_base, const float2 *table) {
     if (rows <= 0) return UT_OK;
     const int64_t L = kv_b->in_dim;
     if (L % 4 != 0) {
@@ -211,9 +268,9 @@ int32_t launch_absorb_q(ut_ctx *ctx, const ut_qtensor *kv_b, const float *q, int
     const int64_t kvh = nope + vh;
     int tok = timing_begin(ctx, "absorb_q");
     switch (kv_b->fmt) {
-    case UT_FMT_INT8: hipLaunchKernelGGL((k_absorb_q<UT_FMT_INT8, RB>), grid, dim3(threads), 0, ctx->stream, w, kv_b->scales, kv_b->row_bytes, L, q, rows, heads, nope, rope, kvh, qabs, qrope); break;
-    case UT_FMT_INT4: hipLaunchKernelGGL((k_absorb_q<UT_FMT_INT4, RB>), grid, dim3(threads), 0, ctx->stream, w, kv_b->scales, kv_b->row_bytes, L, q, rows, heads, nope, rope, kvh, qabs, qrope); break;
-    default: hipLaunchKernelGGL((k_absorb_q<UT_FMT_F32, RB>), grid, dim3(threads), 0, ctx->stream, w, kv_b->scales, kv_b->row_bytes, L, q, rows, heads, nope, rope, kvh, qabs, qrope); break;
+    case UT_FMT_INT8: hipLaunchKernelGGL((k_absorb_q<UT_FMT_INT8, RB>), grid, dim3(threads), 0, ctx->stream, w, kv_b->scales, kv_b->row_bytes, L, q, rows, heads, nope, rope, kvh, qabs, qrope, pos_base, table); break;
+    case UT_FMT_INT4: hipLaunchKernelGGL((k_absorb_q<UT_FMT_INT4, RB>), grid, dim3(threads), 0, ctx->stream, w, kv_b->scales, kv_b->row_bytes, L, q, rows, heads, nope, rope, kvh, qabs, qrope, pos_base, table); break;
+    default: hipLaunchKernelGGL((k_absorb_q<UT_FMT_F32, RB>), grid, dim3(threads), 0, ctx->stream, w, kv_b->scales, kv_b->row_bytes, L, q, rows, heads, nope, rope, kvh, qabs, qrope, pos_base, table); break;
     }
     timing_end(ctx, tok);
     return launch_check(ctx, "k_absorb_q");
@@ -239,6 +296,7 @@ __global__ __launch_bounds__(256) void k_absorb_v(const uint8_t *__restrict__ w,
     float acc[RB];
 #pragma unroll
     for (int r = 0; r < RB; r++) acc[r] = 0.0f;
+#pragma unroll 8
     for (int64_t c = 4 * s; c < L; c += 64) {
         const float4 cw = codes4<FMT>(wr, c);
 #pragma unroll

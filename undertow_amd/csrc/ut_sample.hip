@@ -53,6 +53,7 @@ __global__ __launch_bounds__(256) void k_argmax_partial(const float *__restrict_
     const float *xr = x + row * ldx;
     const int64_t lo = (int64_t)blockIdx.x * chunk, hi = lo + chunk < V ? lo + chunk : V;
     Best b{0.0f, -1};
+#pragma unroll 8
     for (int64_t i = lo + threadIdx.x; i < hi; i += blockDim.x) {
         float v = xr[i];
         if (v == v && (b.i < 0 || v > b.v)) { b.v = v; b.i = (int32_t)i; }
