@@ -125,16 +125,14 @@ __global__ __launch_bounds__(256) void k_rowdig(RowDigArgs a) {
     if (a.dig4) {
         const int64_t K8 = (K + 7) / 8;
         for (int64_t c = tid; c < K8; c += 256) {
-            uint32_t w[6] = {0, 0, 0, 0, 0, 0};
-            for (int j = 0; j < 8; j++) {
-                int32_t v = xq(8 * c + j);
+            float v[8];
 #pragma unroll
-                for (int p = 0; p < 6; p++) {
-                    int32_t d = ((v + 8) & 15) - 8;  // balanced digit in [-8, 7]
-                    v = (v - d) >> 4;
-                    w[p] |= (uint32_t)(d & 15) << (4 * j);
-                }
+            for (int j = 0; j < 8; j++) {
+                const int64_t k = 8 * c + j;
+                v[j] = k < K ? (staged ? row[k] : val(k)) : 0.0f;
             }
+            uint32_t w[6];
+            digit_words<UT_FMT_INT4>(v, 8, bad ? INT32_MIN : sh, w);
 #pragma unroll
             for (int p = 0; p < 6; p++) a.dig4[(m * 6 + p) * K8 + c] = w[p];
         }
@@ -142,16 +140,14 @@ __global__ __launch_bounds__(256) void k_rowdig(RowDigArgs a) {
     if (a.dig8) {
         const int64_t K4 = (K + 3) / 4;
         for (int64_t c = tid; c < K4; c += 256) {
-            uint32_t w[3] = {0, 0, 0};
-            for (int j = 0; j < 4; j++) {
-                int32_t v = xq(4 * c + j);
+            float v[4];
 #pragma unroll
-                for (int p = 0; p < 3; p++) {
-                    int32_t d = ((v + 128) & 255) - 128;  // balanced digit in [-128, 127]
-                    v = (v - d) >> 8;
-                    w[p] |= (uint32_t)(d & 255) << (8 * j);
-                }
+            for (int j = 0; j < 4; j++) {
+                const int64_t k = 4 * c + j;
+                v[j] = k < K ? (staged ? row[k] : val(k)) : 0.0f;
             }
+            uint32_t w[3];
+            digit_words<UT_FMT_INT8>(v, 4, bad ? INT32_MIN : sh, w);
 #pragma unroll
             for (int p = 0; p < 3; p++) a.dig8[(m * 3 + p) * K4 + c] = w[p];
         }

@@ -73,24 +73,29 @@ struct XSrc {
 };
 
 // Balanced digits of 8 (int4) or 4 (int8) columns, one word per plane.
+// With u = x~ + 0x888888 (int4; 0x808080 for int8) every digit of u is the
+// balanced digit plus 8 (128), so the balanced digit's two's-complement
+// field is the plain field of u with its top bit flipped: one add per
+// column, then a shift / mask per plane.
 template <int FMT>
 __device__ __forceinline__ void digit_words(const float *v, int n, int32_t sh,
                                             uint32_t *w /* [planes] */) {
     constexpr int PL = FMT == UT_FMT_INT4 ? 6 : 3;
     constexpr int B = FMT == UT_FMT_INT4 ? 4 : 8;
-    constexpr int32_t HALF = 1 << (B - 1), MASK = (1 << B) - 1;
+    constexpr uint32_t OFF = FMT == UT_FMT_INT4 ? 0x888888u : 0x808080u;
+    constexpr uint32_t MASK = (1u << B) - 1;
+    constexpr uint32_t FLIP = FMT == UT_FMT_INT4 ? 0x88888888u : 0x80808080u;
 #pragma unroll
     for (int p = 0; p < PL; p++) w[p] = 0;
 #pragma unroll
     for (int j = 0; j < n; j++) {
-        int32_t q = sh == INT32_MIN ? 0 : (int32_t)rintf(ldexpf(v[j], sh));
+        const int32_t q = sh == INT32_MIN ? 0 : (int32_t)rintf(ldexpf(v[j], sh));
+        const uint32_t u = (uint32_t)q + OFF;
 #pragma unroll
-        for (int p = 0; p < PL; p++) {
-            const int32_t d = ((q + HALF) & MASK) - HALF;  // balanced digit
-            q = (q - d) >> B;
-            w[p] |= (uint32_t)(d & MASK) << (B * j);
-        }
+        for (int p = 0; p < PL; p++) w[p] |= ((u >> (B * p)) & MASK) << (B * j);
     }
+#pragma unroll
+    for (int p = 0; p < PL; p++) w[p] ^= FLIP & (n * B >= 32 ? 0xffffffffu : ((1u << (n * B)) - 1));
 }
 
 __device__ inline int64_t shfl_xor_i64(int64_t v, int off) {

@@ -50,15 +50,22 @@ __device__ void route_row(const float *__restrict__ lg, const float *__restrict_
         for (int g = tid; g < n_group; g += blockDim.x) {
             const float *v = corr + g * gs;
             int b0 = 0;
+            float v0 = v[0];
 #pragma unroll 8
-            for (int i = 1; i < gs; i++) if (v[i] > v[b0]) b0 = i;
-            float s = 0.0f + v[b0];
+            for (int i = 1; i < gs; i++) {
+                const float vi = v[i];
+                if (vi > v0) { b0 = i; v0 = vi; }
+            }
+            float s = 0.0f + v0;
             if (gs > 1) {
                 int b1 = b0 == 0 ? 1 : 0;
+                float v1 = v[b1];
 #pragma unroll 8
-                for (int i = 0; i < gs; i++)
-                    if (i != b0 && ranks_before(v[i], i, v[b1], b1)) b1 = i;
-                s = s + v[b1];
+                for (int i = 0; i < gs; i++) {
+                    const float vi = v[i];
+                    if (i != b0 && ranks_before(vi, i, v1, b1)) { b1 = i; v1 = vi; }
+                }
+                s = s + v1;
             }
             gsc[g] = s;
         }
