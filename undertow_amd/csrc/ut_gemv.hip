@@ -157,12 +157,153 @@ __global__ __launch_bounds__(256) void k_rowdig(RowDigArgs a) {
     }
 }
 
+// The same work with the row held in registers: thread t owns the 8-column
+// groups t, t + T, ... (GPT of them), all loads of the row are issued before
+// the first use, and every digit word is formed from the owner's registers.
+// One global round trip per row instead of one per 256 columns.
+template <typename T, typename Op>
+__device__ __forceinline__ T wide_reduce(T v, Op op, T *red /* [16] */) {
+    for (int off = 32; off >= 1; off >>= 1) v = op(v, __shfl_xor(v, off, 64));
+    const int nw = (blockDim.x + 63) >> 6;
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    T r = red[0];
+    for (int w = 1; w < nw; w++) r = op(r, red[w]);
+    __syncthreads();
+    return r;
+}
+
+template <int GPT>
+__global__ __launch_bounds__(1024) void k_rowdig_reg(RowDigArgs a) {
+    __shared__ double redd[16];
+    __shared__ uint32_t redu[16];
+    const int64_t m = blockIdx.x;
+    if (a.plan_ids && blockIdx.x == gridDim.x - 1) {
+        make_plan(a.plan_ids, a.plan_M, a.plan_k, a.plan_E, a.gate_tbl, -1, a.plan, a.err_flag);
+        return;
+    }
+    if (a.slot_count && (int)(m / a.rows_per_slot) >= *a.slot_count) return;
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const int64_t K = a.K;
+    const float *xr = a.x + m * a.ldx;
+    const bool vec = ((uintptr_t)xr & 15) == 0 &&
+                     (!a.norm_w || ((uintptr_t)a.norm_w & 15) == 0);
+    auto load8 = [&](const float *src, int64_t c, float (&v)[8]) {
+        const int64_t k0 = 8 * c;
+        if (vec && k0 + 8 <= K) {
+            const float4 p = *(const float4 *)(src + k0), q = *(const float4 *)(src + k0 + 4);
+            v[0] = p.x; v[1] = p.y; v[2] = p.z; v[3] = p.w;
+            v[4] = q.x; v[5] = q.y; v[6] = q.z; v[7] = q.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = k0 + j < K ? src[k0 + j] : 0.0f;
+        }
+    };
+    const int64_t NG = (K + 7) / 8;
+    float v[GPT][8], wv[GPT][8];
+#pragma unroll
+    for (int g = 0; g < GPT; g++) {
+        const int64_t c = tid + (int64_t)g * nt;
+        if (c < NG) {
+            load8(xr, c, v[g]);
+            if (a.norm_w) load8(a.norm_w, c, wv[g]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[g][j] = 0.0f, wv[g][j] = 0.0f;
+        }
+    }
+    if (a.norm_w) {
+        double acc = 0.0;
+#pragma unroll
+        for (int g = 0; g < GPT; g++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) acc += (double)v[g][j] * (double)v[g][j];
+        acc = wide_reduce(acc, [](double p, double q) { return p + q; }, redd);
+        const float r = 1.0f / sqrtf(__fadd_rn((float)(acc / (double)K), a.eps));
+#pragma unroll
+        for (int g = 0; g < GPT; g++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[g][j] = __fmul_rn(__fmul_rn(v[g][j], r), wv[g][j]);
+    }
+    uint32_t mx = 0;
+#pragma unroll
+    for (int g = 0; g < GPT; g++) {
+        const int64_t c = tid + (int64_t)g * nt;
+        if (c >= NG) continue;
+#pragma unroll
+        for (int j = 0; j < 8; j++) mx = max(mx, __float_as_uint(fabsf(v[g][j])));
+        if (a.out) {
+            float *o = a.out + m * a.ldo + 8 * c;
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (8 * c + j < K) o[j] = v[g][j];
+        }
+    }
+    if (a.rowmax) {
+        mx = 0;
+        for (int i = tid; i < a.nparts; i += nt) mx = max(mx, a.rowmax[m * a.nparts + i]);
+    }
+    mx = wide_reduce(mx, [](uint32_t p, uint32_t q) { return p > q ? p : q; }, redu);
+    // non-finite rows (|x| bits >= +inf) produce NaN outputs downstream
+    const bool bad = mx >= 0x7f800000u;
+    int E = 0;
+    if (!bad && mx != 0) (void)frexpf(__uint_as_float(mx), &E);
+    const int sh = bad ? INT32_MIN : 22 - E;
+    if (tid == 0) a.exps[m] = bad ? INT32_MIN : E - 22;
+    const int64_t K8 = NG, K4 = (K + 3) / 4;
+#pragma unroll
+    for (int g = 0; g < GPT; g++) {
+        const int64_t c = tid + (int64_t)g * nt;
+        if (c >= NG) continue;
+        if (a.dig4) {
+            uint32_t w[6];
+            digit_words<UT_FMT_INT4>(v[g], 8, sh, w);
+#pragma unroll
+            for (int p = 0; p < 6; p++) a.dig4[(m * 6 + p) * K8 + c] = w[p];
+        }
+        if (a.dig8) {
+            uint32_t w[3];
+            digit_words<UT_FMT_INT8>(v[g], 4, sh, w);
+#pragma unroll
+            for (int p = 0; p < 3; p++) a.dig8[(m * 3 + p) * K4 + 2 * c] = w[p];
+            if (2 * c + 1 < K4) {
+                digit_words<UT_FMT_INT8>(v[g] + 4, 4, sh, w);
+#pragma unroll
+                for (int p = 0; p < 3; p++) a.dig8[(m * 3 + p) * K4 + 2 * c + 1] = w[p];
+            }
+        }
+        if (a.xt) {
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (8 * c + j < K)
+                    a.xt[m * K + 8 * c + j] =
+                        bad ? 0 : (int32_t)rintf(ldexpf(v[g][j], sh));
+        }
+    }
+}
+
+constexpr int64_t kRowRegCols = 4 * 8 * 1024;  // widest row the register kernel takes
+
 static int32_t launch_rowdig(ut_ctx *ctx, const RowDigArgs &a, int64_t M, const char *name) {
     if (M <= 0) return UT_OK;
-    const size_t shmem = a.K <= kRowLds ? (size_t)a.K * 4 : 0;
+    const dim3 grid((unsigned)(M + (a.plan_ids ? 1 : 0)));
     int tok = timing_begin(ctx, name);
-    hipLaunchKernelGGL(k_rowdig, dim3((unsigned)(M + (a.plan_ids ? 1 : 0))), dim3(256), shmem,
-                       ctx->stream, a);
+    if (a.K <= kRowRegCols) {
+        const int64_t NG = (a.K + 7) / 8;
+        const int gpt = NG <= 1024 ? 1 : NG <= 2048 ? 2 : 4;
+        int64_t nt = (NG + gpt - 1) / gpt;
+        nt = (nt + 63) / 64 * 64;
+        // the plan workgroup needs at least the threads make_plan assumes
+        if (a.plan_ids && nt < 256) nt = 256;
+        switch (gpt) {
+        case 1: hipLaunchKernelGGL(k_rowdig_reg<1>, grid, dim3((unsigned)nt), 0, ctx->stream, a); break;
+        case 2: hipLaunchKernelGGL(k_rowdig_reg<2>, grid, dim3((unsigned)nt), 0, ctx->stream, a); break;
+        default: hipLaunchKernelGGL(k_rowdig_reg<4>, grid, dim3((unsigned)nt), 0, ctx->stream, a); break;
+        }
+    } else {
+        const size_t shmem = a.K <= kRowLds ? (size_t)a.K * 4 : 0;
+        hipLaunchKernelGGL(k_rowdig, grid, dim3(256), shmem, ctx->stream, a);
+    }
     timing_end(ctx, tok);
     return launch_check(ctx, "k_rowdig");
 }
@@ -245,6 +386,11 @@ struct PlainArgs {
     float *out;
     int64_t ldo;
     int accumulate;
+    // split-K over blockIdx.z (ks > 1): columns [z*kslice, (z+1)*kslice),
+    // partial totals to part[(z*M + m)*O + row]; k_gemv_splitk_sum finishes
+    int ks;
+    int64_t kslice;
+    int64_t *part;
 };
 
 // 16*R output rows per workgroup (R = 4 rows per lane at M <= 2, else 2):
@@ -264,6 +410,20 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
         rows[r] = a.w + row * a.row_bytes;
     }
     CoreOut<FMT, M, R> res;
+    if (a.ks > 1) {
+        const int64_t kb = (int64_t)blockIdx.z * a.kslice;
+        gemv_core<FMT, M, R>(rows, a.K, a.x, lds, res, kb, kb + a.kslice);
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                const int64_t row = row0 + r;
+                if (s == 4 * r + m && row < a.O)
+                    a.part[((int64_t)blockIdx.z * M + m) * a.O + row] =
+                        FMT == UT_FMT_F32 ? (int64_t)__float_as_uint(res.F[r][m]) : res.S[r][m];
+            }
+        return;
+    }
     gemv_core<FMT, M, R>(rows, a.K, a.x, lds, res);
 #pragma unroll
     for (int r = 0; r < R; r++)
@@ -276,6 +436,34 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
                 *o = a.accumulate ? __fadd_rn(*o, v) : v;
             }
         }
+}
+
+// Sums the split-K partials of (m, row) in z order (integers exactly, f32
+// in that fixed order) and applies the row epilogue.
+template <int FMT>
+__global__ __launch_bounds__(256) void k_gemv_splitk_sum(const int64_t *__restrict__ part, int ks,
+                                                         int64_t O, int M,
+                                                         const int32_t *__restrict__ exps,
+                                                         const float *__restrict__ scales,
+                                                         float *__restrict__ out, int64_t ldo,
+                                                         int accumulate) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= O * M) return;
+    const int64_t m = i / O, row = i - m * O;
+    const int64_t zs = (int64_t)M * O;
+    float v;
+    if constexpr (FMT == UT_FMT_F32) {
+        v = __uint_as_float((uint32_t)part[i]);
+#pragma unroll 16
+        for (int z = 1; z < ks; z++) v = __fadd_rn(v, __uint_as_float((uint32_t)part[z * zs + i]));
+    } else {
+        int64_t S = part[i];
+#pragma unroll 16
+        for (int z = 1; z < ks; z++) S += part[z * zs + i];
+        v = int_total_to_f32(S, exps[m], scales[row]);
+    }
+    float *o = out + m * ldo + row;
+    *o = accumulate ? __fadd_rn(*o, v) : v;
 }
 
 // ------------------------------------------------------ generic GEMV ---
@@ -337,6 +525,35 @@ static bool fast_ok(const ut_qtensor *w) {
     return w->in_dim % 4 == 0;
 }
 
+// Split of K for a weight of O rows and K columns.  Weights with fewer
+// than 256 tiles of 64 rows cannot keep the chip's loads in flight, so
+// their K range is split over blockIdx.z (each split at least two steps
+// wide) and a second launch sums the partials.  The split depends on the
+// weight's shape only, so an f32 row's summation order is the same for
+// every M.
+constexpr int64_t kSplitTargetWGs = 1024;
+
+static void splitk_plan(int32_t fmt, int64_t O, int64_t K, int *ks_out, int64_t *kslice_out) {
+    const int64_t step = fmt == UT_FMT_INT4 ? FmtTraits<UT_FMT_INT4>::kStepCols
+                         : fmt == UT_FMT_INT8 ? FmtTraits<UT_FMT_INT8>::kStepCols
+                                              : FmtTraits<UT_FMT_F32>::kStepCols;
+    const int64_t tiles64 = (O + 63) / 64;
+    int64_t ks = tiles64 >= 256 ? 1 : (kSplitTargetWGs + tiles64 - 1) / tiles64;
+    const int64_t max_ks = K / (2 * step);
+    if (ks > max_ks) ks = max_ks;
+    // partials of the widest case (M = 4) must fit
+    while (ks > 1 && ks * 4 * O * 8 > kSplitKPartBytes) ks--;
+    if (ks <= 1) {
+        *ks_out = 1;
+        *kslice_out = K;
+        return;
+    }
+    int64_t kslice = (K + ks - 1) / ks;
+    kslice = (kslice + step - 1) / step * step;
+    *ks_out = (int)((K + kslice - 1) / kslice);
+    *kslice_out = kslice;
+}
+
 template <int FMT>
 static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrows) {
     const ut_qtensor *w = ga.w;
@@ -365,8 +582,11 @@ static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrow
         a.x.ldx = 0;
         a.exps = ga.xd.exps + m0;
     }
+    splitk_plan(FMT, w->out_dim, w->in_dim, &a.ks, &a.kslice);
+    a.part = nullptr;
+    if (a.ks > 1) UT_TRY(splitk_buffer(ctx, &a.part));
     const int rows_per_wg = 16 * (mrows <= 2 ? 4 : 2);
-    dim3 grid((unsigned)((w->out_dim + rows_per_wg - 1) / rows_per_wg));
+    dim3 grid((unsigned)((w->out_dim + rows_per_wg - 1) / rows_per_wg), 1, (unsigned)a.ks);
     const char *name = FMT == UT_FMT_INT4 ? "gemv_int4" : FMT == UT_FMT_INT8 ? "gemv_int8" : "gemv_f32";
     int tok = timing_begin(ctx, name);
     switch (mrows) {
@@ -374,6 +594,13 @@ static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrow
     case 2: hipLaunchKernelGGL((k_gemv<FMT, 2>), grid, dim3(kGemvThreads), 0, ctx->stream, a); break;
     case 3: hipLaunchKernelGGL((k_gemv<FMT, 3>), grid, dim3(kGemvThreads), 0, ctx->stream, a); break;
     default: hipLaunchKernelGGL((k_gemv<FMT, 4>), grid, dim3(kGemvThreads), 0, ctx->stream, a); break;
+    }
+    if (a.ks > 1) {
+        UT_TRY(launch_check(ctx, name));
+        const int64_t n = w->out_dim * mrows;
+        hipLaunchKernelGGL(k_gemv_splitk_sum<FMT>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                           ctx->stream, a.part, a.ks, w->out_dim, mrows, a.exps, a.scales, a.out,
+                           a.ldo, a.accumulate);
     }
     timing_end(ctx, tok);
     return launch_check(ctx, name);

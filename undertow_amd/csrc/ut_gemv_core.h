@@ -121,7 +121,8 @@ template <int FMT, int M, int R = kGemvRows> struct CoreOut {
 // does not drain the memory pipe.
 template <int FMT, int M, int R = kGemvRows>
 __device__ __forceinline__ void gemv_core(const uint8_t *const rows[R], int64_t K, const XSrc &x,
-                                          uint32_t *lds, CoreOut<FMT, M, R> &res) {
+                                          uint32_t *lds, CoreOut<FMT, M, R> &res,
+                                          int64_t k_begin = 0, int64_t k_end = -1) {
     using T = FmtTraits<FMT>;
     constexpr int KC = gemv_chunk_cols<FMT, M>();
     constexpr int PL = T::kPlanes;
@@ -234,34 +235,37 @@ __device__ __forceinline__ void gemv_core(const uint8_t *const rows[R], int64_t 
         }
     };
 
-    const int64_t nsteps = (K + STEP - 1) / STEP;
-    const int64_t lane_col = (int64_t)s * LANE_COLS;
+    // columns [k_begin, k_end) (k_begin a multiple of STEP); K bounds loads
+    const int64_t kend = k_end < 0 || k_end > K ? K : k_end;
+    const int64_t nsteps = kend > k_begin ? (kend - k_begin + STEP - 1) / STEP : 0;
+    const int64_t lane_col = k_begin + (int64_t)s * LANE_COLS;
     uint4 wa[R], wb[R];
-    load(wa, lane_col);
-    load(wb, lane_col + STEP);
-    int64_t kc = 0, chunk_end = 0;
+    auto loadk = [&](uint4 (&w)[R], int64_t col) { if (col < kend) load(w, col); };
+    loadk(wa, lane_col);
+    loadk(wb, lane_col + STEP);
+    int64_t kc = k_begin, chunk_end = k_begin;
     for (int64_t t = 0; t < nsteps; t += 2) {
         // step t (buffer a)
-        if (t * STEP >= chunk_end) {
-            kc = t * STEP;
-            const int kcn = (int)((K - kc) < KC ? (K - kc) : KC);
+        if (k_begin + t * STEP >= chunk_end) {
+            kc = k_begin + t * STEP;
+            const int kcn = (int)((kend - kc) < KC ? (kend - kc) : KC);
             chunk_end = kc + kcn;
             stage(kc, kcn);
         }
         const int64_t ca = t * STEP + lane_col;
-        if (ca < K) compute(wa, (int)(ca - kc));
-        load(wa, ca + 2 * STEP);
+        if (ca < kend) compute(wa, (int)(ca - kc));
+        loadk(wa, ca + 2 * STEP);
         // step t+1 (buffer b)
         if (t + 1 < nsteps) {
-            if ((t + 1) * STEP >= chunk_end) {
-                kc = (t + 1) * STEP;
-                const int kcn = (int)((K - kc) < KC ? (K - kc) : KC);
+            if (k_begin + (t + 1) * STEP >= chunk_end) {
+                kc = k_begin + (t + 1) * STEP;
+                const int kcn = (int)((kend - kc) < KC ? (kend - kc) : KC);
                 chunk_end = kc + kcn;
                 stage(kc, kcn);
             }
             const int64_t cb = (t + 1) * STEP + lane_col;
-            if (cb < K) compute(wb, (int)(cb - kc));
-            load(wb, cb + 2 * STEP);
+            if (cb < kend) compute(wb, (int)(cb - kc));
+            loadk(wb, cb + 2 * STEP);
         }
     }
 

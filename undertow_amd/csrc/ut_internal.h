@@ -70,6 +70,8 @@ struct ut_ctx {
     // Sticky device-side error flag (invalid expert ids), reported by the
     // next ut_ctx_synchronize().
     int32_t *dev_err = nullptr;
+    // Split-K GEMV partial totals (allocated on first use).
+    void *splitk = nullptr;
     // Handle lifetime: models hold a reference on their context and
     // sessions on their model, so the handles may be released in any order.
     int refs = 1;
@@ -108,6 +110,10 @@ void ctx_retain(ut_ctx *ctx);
 void ctx_release(ut_ctx *ctx);
 // The context's device error flag (allocated on first use) and its check.
 int32_t device_error_flag(ut_ctx *ctx, int32_t **flag);
+// Split-K partials buffer of the context (kSplitKPartBytes), allocated on
+// first use.
+constexpr int64_t kSplitKPartBytes = int64_t(8) << 20;
+int32_t splitk_buffer(ut_ctx *ctx, int64_t **part);
 int32_t check_device_error(ut_ctx *ctx);
 
 int64_t payload_bytes(int32_t fmt, int64_t out_dim, int64_t in_dim);

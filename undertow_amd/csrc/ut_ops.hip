@@ -251,6 +251,93 @@ __global__ __launch_bounds__(128) void k_absorb_q(const uint8_t *__restrict__ w,
     }
 }
 
+// The same product with the head's nope rows staged in LDS first: a
+// workgroup takes one head, one block of CB latent columns and up to 4
+// query rows.  All of the block's weight bytes are requested at once
+// (16-byte loads, a few per thread), then thread t adds the nope rows of
+// column t in d order from LDS.  f[r][d] = q*scale is formed once in LDS.
+template <int FMT, int RB, int CB>
+__global__ __launch_bounds__(CB) void k_absorb_q_lds(const uint8_t *__restrict__ w,
+                                                     const float *__restrict__ scales,
+                                                     int64_t row_bytes, int64_t L,
+                                                     const float *__restrict__ q, int64_t rows,
+                                                     int64_t heads, int nope, int64_t rope,
+                                                     int64_t kvh, float *__restrict__ qabs,
+                                                     float *__restrict__ qrope, int64_t pos_base,
+                                                     const float2 *__restrict__ table) {
+    constexpr int BPC2 = FMT == UT_FMT_INT4 ? 1 : FMT == UT_FMT_INT8 ? 2 : 8;  // 2*bytes/col
+    constexpr int ROWB = CB * BPC2 / 2;  // staged bytes per nope row
+    constexpr int PIECES = ROWB / 16;
+    extern __shared__ __attribute__((aligned(16))) uint8_t sm_abs[];
+    uint8_t *codes = sm_abs;                                   // [nope][ROWB]
+    float *f = (float *)(sm_abs + (size_t)nope * ROWB);       // [RB][nope]
+    const int64_t h = blockIdx.x, r0 = (int64_t)blockIdx.z * RB;
+    const int64_t qh = nope + rope;
+    const int tid = threadIdx.x;
+    const int64_t cb0 = (int64_t)blockIdx.y * CB;
+    const uint8_t *wh = w + (h * kvh) * row_bytes + cb0 * BPC2 / 2;
+    for (int i = tid; i < nope * PIECES; i += CB) {
+        const int d = i / PIECES, pc = i - d * PIECES;
+        *(uint4 *)(codes + d * ROWB + 16 * pc) = *(const uint4 *)(wh + d * row_bytes + 16 * pc);
+    }
+    for (int i = tid; i < RB * nope; i += CB) {
+        const int r = i / nope, d = i - r * nope;
+        const int64_t rr = r0 + r < rows ? r0 + r : rows - 1;
+        const float qn = q[(rr * heads + h) * qh + d];
+        f[i] = FMT == UT_FMT_F32 ? qn : __fmul_rn(qn, scales[h * kvh + d]);
+    }
+    __syncthreads();
+    float acc[RB];
+#pragma unroll
+    for (int r = 0; r < RB; r++) acc[r] = 0.0f;
+#pragma unroll 8
+    for (int d = 0; d < nope; d++) {
+        float c;
+        if constexpr (FMT == UT_FMT_F32) {
+            c = *(const float *)(codes + d * ROWB + 4 * tid);
+        } else if constexpr (FMT == UT_FMT_INT8) {
+            c = (float)(int8_t)codes[d * ROWB + tid];
+        } else {
+            const uint32_t b = codes[d * ROWB + (tid >> 1)];
+            c = (float)((int)(((b >> (4 * (tid & 1))) & 0xf) ^ 8) - 8);
+        }
+#pragma unroll
+        for (int r = 0; r < RB; r++) acc[r] = __fadd_rn(acc[r], __fmul_rn(f[r * nope + d], c));
+    }
+#pragma unroll
+    for (int r = 0; r < RB; r++)
+        if (r0 + r < rows) qabs[((r0 + r) * heads + h) * L + cb0 + tid] = acc[r];
+    if (blockIdx.y == 0) {
+        // q_rope = rope_interleave(q[nope:], pos_base + r) (attention.rs:106-118,156-166)
+        const int64_t half = rope / 2;
+        for (int64_t i = tid; i < RB * rope; i += CB) {
+            const int64_t r = r0 + i / rope, jj = i % rope;
+            if (r >= rows) continue;
+            const float *in = q + (r * heads + h) * qh + nope;
+            const int64_t j = jj < half ? jj : jj - half;
+            const float a = in[2 * j], b = in[2 * j + 1];
+            const float2 cs = table[(pos_base + r) * half + j];
+            qrope[(r * heads + h) * rope + jj] =
+                jj < half ? __fsub_rn(__fmul_rn(a, cs.x), __fmul_rn(b, cs.y))
+                          : __fadd_rn(__fmul_rn(b, cs.x), __fmul_rn(a, cs.y));
+        }
+    }
+}
+
+template <int FMT, int RB, int CB>
+static void absorb_q_lds_launch(ut_ctx *ctx, const ut_qtensor *kv_b, const float *q, int64_t rows,
+                                int64_t heads, int64_t nope, int64_t rope, int64_t kvh,
+                                float *qabs, float *qrope, int64_t pos_base,
+                                const float2 *table) {
+    const int64_t L = kv_b->in_dim;
+    constexpr int BPC2 = FMT == UT_FMT_INT4 ? 1 : FMT == UT_FMT_INT8 ? 2 : 8;
+    const size_t shmem = (size_t)nope * (CB * BPC2 / 2) + (size_t)RB * nope * 4;
+    dim3 grid((unsigned)heads, (unsigned)(L / CB), (unsigned)((rows + RB - 1) / RB));
+    hipLaunchKernelGGL((k_absorb_q_lds<FMT, RB, CB>), grid, dim3(CB), shmem, ctx->stream,
+                       (const uint8_t *)kv_b->payload, kv_b->scales, kv_b->row_bytes, L, q, rows,
+                       heads, (int)nope, rope, kvh, qabs, qrope, pos_base, table);
+}
+
 int32_t launch_absorb_q(ut_ctx *ctx, const ut_qtensor *kv_b, const float *q, int64_t rows,
                         int64_t heads, int64_t nope, int64_t rope, int64_t vh, float *qabs,
                         float *qrope, int64_t pos_base, const float2 *table) {
@@ -261,11 +348,33 @@ int32_t launch_absorb_q(ut_ctx *ctx, const ut_qtensor *kv_b, const float *q, int
         return UT_ERR_SHAPE;
     }
     constexpr int RB = 4;
+    const int64_t kvh = nope + vh;
+    // LDS-staged kernel: 128- (or 64-) column blocks, 16-byte aligned rows,
+    // the block's nope rows within 64 KiB of LDS
+    const int bpc2 = kv_b->fmt == UT_FMT_INT4 ? 1 : kv_b->fmt == UT_FMT_INT8 ? 2 : 8;
+    const int cb = L % 128 == 0 ? 128 : L % 64 == 0 ? 64 : 0;
+    if (cb && (cb * bpc2 / 2) % 16 == 0 && kv_b->row_bytes % 16 == 0 &&
+        ((uintptr_t)kv_b->payload & 15) == 0 &&
+        (size_t)nope * (cb * bpc2 / 2) + RB * nope * 4 <= 64 * 1024) {
+        int tok = timing_begin(ctx, "absorb_q");
+#define UT_ABSQ(F, C) absorb_q_lds_launch<F, RB, C>(ctx, kv_b, q, rows, heads, nope, rope, kvh, qabs, qrope, pos_base, table)
+        if (cb == 128) {
+            if (kv_b->fmt == UT_FMT_INT8) UT_ABSQ(UT_FMT_INT8, 128);
+            else if (kv_b->fmt == UT_FMT_INT4) UT_ABSQ(UT_FMT_INT4, 128);
+            else UT_ABSQ(UT_FMT_F32, 128);
+        } else {
+            if (kv_b->fmt == UT_FMT_INT8) UT_ABSQ(UT_FMT_INT8, 64);
+            else if (kv_b->fmt == UT_FMT_INT4) UT_ABSQ(UT_FMT_INT4, 64);
+            else UT_ABSQ(UT_FMT_F32, 64);
+        }
+#undef UT_ABSQ
+        timing_end(ctx, tok);
+        return launch_check(ctx, "k_absorb_q_lds");
+    }
     // 128 threads x 4 columns per workgroup column block
     const unsigned threads = (unsigned)(L >= 512 ? 128 : ((L / 4) + 63) / 64 * 64);
     dim3 grid((unsigned)heads, (unsigned)((rows + RB - 1) / RB), (unsigned)((L + 511) / 512));
     const uint8_t *w = (const uint8_t *)kv_b->payload;
-    const int64_t kvh = nope + vh;
     int tok = timing_begin(ctx, "absorb_q");
     switch (kv_b->fmt) {
     case UT_FMT_INT8: hipLaunchKernelGGL((k_absorb_q<UT_FMT_INT8, RB>), grid, dim3(threads), 0, ctx->stream, w, kv_b->scales, kv_b->row_bytes, L, q, rows, heads, nope, rope, kvh, qabs, qrope, pos_base, table); break;

@@ -133,6 +133,19 @@ int32_t device_error_flag(ut_ctx *ctx, int32_t **flag) {
     return UT_OK;
 }
 
+int32_t splitk_buffer(ut_ctx *ctx, int64_t **part) {
+    if (!ctx->splitk) {
+        if (hipMalloc(&ctx->splitk, kSplitKPartBytes) != hipSuccess) {
+            (void)hipGetLastError();
+            ctx->splitk = nullptr;
+            set_error(ctx, "split-K buffer allocation failed");
+            return UT_ERR_OOM;
+        }
+    }
+    *part = (int64_t *)ctx->splitk;
+    return UT_OK;
+}
+
 int32_t check_device_error(ut_ctx *ctx) {
     if (!ctx->dev_err) return UT_OK;
     int32_t f = 0;
@@ -247,6 +260,7 @@ void ut::ctx_release(ut_ctx *ctx) {
     }
     if (ctx->scratch.ptr) (void)hipFree(ctx->scratch.ptr);
     if (ctx->dev_err) (void)hipFree(ctx->dev_err);
+    if (ctx->splitk) (void)hipFree(ctx->splitk);
     if (ctx->pinned) (void)hipHostFree(ctx->pinned);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
