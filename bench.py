@@ -20,6 +20,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -194,6 +195,20 @@ def mtp_bench(U, ctx, cfg, prompt_len, new_tokens, depths, seed, expert_fmt, den
     return res
 
 
+def committed_traffic() -> float | None:
+    """HBM bytes per `k_moe_gate_up<int4,1>` launch, from the committed
+    counter summary: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes over
+    this script's headline leg, each scaled by what the counter reads for a
+    plain copy of known size (--copy-probe).  None when it is absent."""
+    p = ROOT / "profiles" / "k_moe_gate_up_int4_c2_m1.md"
+    try:
+        text = p.read_text()
+    except OSError:
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.]+)\s*$", text, re.M)
+    return float(m.group(1)) if m else None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -287,7 +302,9 @@ def main():
                      "achieved": round(head["gate_up_gbs"], 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(head["gate_up_gbs"] / HBM_PEAK_GBS, 4),
                      "avg_launch_us": round(gu_us, 3), "bytes_per_launch": head["gate_up_bytes"],
-                     "traffic": None},
+                     "traffic": committed_traffic(),
+                     "traffic_source": "profiles/k_moe_gate_up_int4_c2_m1.md (FETCH_SIZE x2.0 + "
+                                       "WRITE_SIZE x1.0 per dispatch, copy-scaled)"},
         "kernels": {"gate_up_us": round(gu_us, 3), "down_us": round(head["down_us"], 3),
                     "down_gbs": round(head["down_gbs"], 1),
                     "all_kernels_us_per_step": round(head["kernels_us_per_step"], 3)},
