@@ -184,7 +184,10 @@ __device__ __forceinline__ void gemv_core(const uint8_t *const rows[R], int64_t 
                     v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
                 }
                 uint32_t w[PL];
-                digit_words<FMT>(v, CPW, x.sh[m], w);
+                // select, not index: a runtime index into x.sh would move the
+                // whole argument struct to scratch memory
+                const int32_t shm = m == 0 ? x.sh[0] : m == 1 ? x.sh[1] : m == 2 ? x.sh[2] : x.sh[3];
+                digit_words<FMT>(v, CPW, shm, w);
 #pragma unroll
                 for (int p = 0; p < PL; p++) lds[(m * PL + p) * LW + g] = w[p];
             }
