@@ -118,6 +118,68 @@ def expert_block_bench(U, ctx, torch, tbl, cfg, M, steps, warmup, fmt_bits, seed
     }
 
 
+# ------------------------------------------------------- MLA attention --
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def mla_bench(U, ctx, torch, steps, warmup, Ts=(1024, 4096, 32768), Rs=(1, 2, 4)):
+    """Config 3: absorbed-MLA decode attention at DeepSeek-V3 shape (128
+    heads, latent 512 + rope 64, scale 1/sqrt(192)) over an N(0,1) f32 cache,
+    R query rows with row s seeing T - R + 1 + s positions.  Algorithmic
+    FLOPs 2*128*(576+512) per (row, position); bytes = the f32 cache rows
+    read (T*576*4).  Kernel times are HIP events around each launch on the
+    stream the kernels run on."""
+    H, L, P = 128, 512, 64
+    scale = float(1.0 / np.sqrt(192.0))
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(3)
+    Tmax = max(Ts)
+    lat = torch.randn(Tmax, L, device="cuda:0", generator=g)
+    kr = torch.randn(Tmax, P, device="cuda:0", generator=g)
+    res = {}
+    for R in Rs:
+        qabs = torch.randn(R, H, L, device="cuda:0", generator=g)
+        qr = torch.randn(R, H, P, device="cuda:0", generator=g)
+        out = torch.empty(R, H, L, device="cuda:0")
+        for T in Ts:
+            pb = T - R
+            for _ in range(warmup):
+                U.mla_attend(ctx, qabs, qr, lat, kr, pb, scale, out=out)
+            ctx.synchronize()
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0.record()
+            for _ in range(steps):
+                U.mla_attend(ctx, qabs, qr, lat, kr, pb, scale, out=out)
+            t1.record()
+            ctx.synchronize()
+            us = t0.elapsed_time(t1) / steps * 1e3
+            ctx.enable_timing(True)
+            for _ in range(steps):
+                U.mla_attend(ctx, qabs, qr, lat, kr, pb, scale, out=out)
+            ctx.synchronize()
+            n1, ms1 = ctx.kernel_time("mla_mfma")
+            n2, ms2 = ctx.kernel_time("mla_combine")
+            ctx.enable_timing(False)
+            flops = 2 * H * (L + P + L) * (R * T - R * (R - 1) // 2)
+            nbytes = T * (L + P) * 4
+            k_us = ms1 / max(n1, 1) * 1e3
+            res[f"R{R}_T{T}"] = {
+                "us_per_call": round(us, 2),
+                "mfma_kernel_us": round(k_us, 2),
+                "combine_us": round(ms2 / max(n2, 1) * 1e3, 2),
+                "gflop": round(flops / 1e9, 3),
+                "tflops_call": round(flops / (us * 1e-6) / 1e12, 1),
+                "mfma_util_call": round(flops / (us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+                "mfma_util_kernel": round(flops / (k_us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)
+                if n1 else None,
+                "cache_gbs_call": round(nbytes / (us * 1e-6) / 1e9, 1),
+                "hbm_frac_call": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            }
+            log(f"config 3 MLA R={R} T={T}: {json.dumps(res[f'R{R}_T{T}'])}")
+    del lat, kr
+    return res
+
+
 # --------------------------------------------------------- CPU baseline --
 def cpu_baseline(cfg, seconds=10.0):
     """The reference CPU expert block (AVX-512/AVX2 restatement of
@@ -218,6 +280,9 @@ def main():
     ap.add_argument("--mtp", default="c1,c4", help="comma list of c1,c4 or 'none'")
     ap.add_argument("--variants", action="store_true", default=True)
     ap.add_argument("--no-variants", dest="variants", action="store_false")
+    ap.add_argument("--mla", action="store_true", default=True,
+                    help="config 3 MLA attention leg (default on)")
+    ap.add_argument("--no-mla", dest="mla", action="store_false")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 1 GiB device copy (counter scaling for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -261,6 +326,12 @@ def main():
         torch.cuda.synchronize()
         log(f"copy probe: 3 x {n} bytes")
         del a, b
+        torch.cuda.empty_cache()
+
+    mla = {}
+    if args.mla:
+        log("config 3 MLA decode attention")
+        mla = mla_bench(U, ctx, torch, args.steps, args.warmup)
         torch.cuda.empty_cache()
 
     mtp = {}
@@ -310,6 +381,7 @@ def main():
                     "all_kernels_us_per_step": round(head["kernels_us_per_step"], 3)},
         "variants": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                      for k, v in variants.items()},
+        "mla": mla,
         "mtp": mtp,
         "cpu_baseline": cpu,
     }

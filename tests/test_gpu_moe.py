@@ -171,8 +171,13 @@ def test_moe_bad_expert_is_reported(ctx):
 # --------------------------------------------------------------- attention
 @pytest.mark.parametrize("R,H,L,P,T", [(1, 4, 64, 16, 5), (2, 4, 64, 16, 40), (4, 8, 16, 8, 300),
                                        (2, 128, 512, 64, 1024), (1, 128, 512, 64, 600),
-                                       (3, 6, 32, 8, 17)])
+                                       (3, 6, 32, 8, 17), (4, 128, 512, 64, 4096),
+                                       (2, 128, 512, 64, 9000), (1, 128, 512, 64, 33)])
 def test_mla_attend_matches_oracle(ctx, R, H, L, P, T):
+    """DeepSeek-V3 shapes (128 heads, 512 + 64) run on the bf16 matrix cores
+    with each f32 operand split into bf16 hi + lo parts (products keep about
+    16 significant bits): bar 1e-4 of the largest output, against 1e-5 for
+    the f32 kernel that adds in the reference's order."""
     import undertow_amd as U
     rng = np.random.default_rng(R * 100 + T)
     qabs = rng.standard_normal((R, H, L)).astype(np.float32)
@@ -183,7 +188,9 @@ def test_mla_attend_matches_oracle(ctx, R, H, L, P, T):
     scale = float(1 / np.sqrt(192.0))
     got = host(U.mla_attend(ctx, dev(qabs), dev(qr), dev(lat), dev(kr), pos_base, scale))
     want = O.mla_attend(qabs, qr, lat, kr, pos_base, scale)
-    assert np.abs(got - want).max() <= 1e-5 * max(1.0, np.abs(want).max())
+    mfma = H % 32 == 0 and L == 512 and P == 64
+    tol = (1e-4 if mfma else 1e-5) * max(1.0, np.abs(want).max())
+    assert np.abs(got - want).max() <= tol, np.abs(got - want).max()
     # row independence: row s alone at pos_base + s sees the same context
     for s in range(R):
         one = host(U.mla_attend(ctx, dev(qabs[s:s + 1]), dev(qr[s:s + 1]), dev(lat), dev(kr),

@@ -140,16 +140,352 @@ __global__ __launch_bounds__(256) void k_mla_combine(const float *__restrict__ p
     }
 }
 
-size_t mla_scratch_bytes(int64_t R, int64_t H, int64_t L, int64_t T) {
+// ------------------------------------------------------ MFMA variant ---
+// For DeepSeek-V3-like shapes (heads % 32 == 0, L % 128 == 0,
+// (L + P) % 64 == 0) the score and context contractions run on the bf16
+// matrix cores.  Each f32 operand x is split into x_hi = bf16(x) and
+// x_lo = bf16(x - x_hi), and a product is taken as hi*hi + hi*lo + lo*hi
+// (f32 accumulation), which keeps about 16 significant bits per product
+// term instead of bf16's 8.
+//
+// Work split.  A column is one (query row r, head h) pair, c = r*H + h; a
+// workgroup takes 32 columns (all of one query row, since H % 32 == 0) and
+// one slice of positions, 32 positions per tile:
+//   scores  S^T[pos x col] = K[pos x (L+P)] . Q^T[(L+P) x col]
+//           (v_mfma_f32_32x32x16_bf16, A = cache rows straight from global
+//           memory, B = the workgroup's queries held in registers); wave w
+//           reduces over dims [w*D/4, (w+1)*D/4) and the four partial tiles
+//           are summed through LDS in wave order;
+//   softmax online over the slice's tiles (running max m and sum l per
+//           column, exp with the fast exponential);
+//   context O^T[L x col] += V^T[L x pos] . P[pos x col] with V = the latent
+//           rows; wave w owns dims [w*L/4, (w+1)*L/4) in 32-row m-tiles.
+// The slice writes (m, l, O) to the partial buffers, k_mla_combine_mfma
+// merges the slices.  The slice length depends only on the row's context
+// length, so a row's result is the same whichever rows share the call.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+constexpr int kMfmaTile = 32;
+
+__host__ __device__ inline int64_t mla_mfma_slice(int64_t n_ctx) {
+    int64_t q = n_ctx / 64, s = 1;
+    while (s * 2 <= q) s *= 2;
+    return s < 32 ? 32 : s > 256 ? 256 : s;
+}
+
+__device__ __forceinline__ void split8(const float (&x)[8], bf16x8_t &hi, bf16x8_t &lo) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const __bf16 h = (__bf16)x[j];
+        hi[j] = h;
+        lo[j] = (__bf16)__fsub_rn(x[j], (float)h);
+    }
+}
+
+__device__ __forceinline__ void load8(const float *p, float (&x)[8]) {
+    const float4 a = *(const float4 *)p, b = *(const float4 *)(p + 4);
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+    x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+}
+
+struct MlaMfmaArgs {
+    const float *qabs, *qrope, *latent, *krot;
+    int H, L, P, RH;
+    int64_t pos_base;
+    float scale;
+    int groups, nslice;  // column groups of 32, slices in the grid
+    float *part_m, *part_l, *part_o;  // [j][col], [j][col], [j][L][col]
+};
+
+// KS: k-steps (16 dims) per wave for the scores, (L+P) = 64*KS;
+// MT: 32-dim m-tiles per wave for the context, L = 128*MT.
+//
+// Per 32-position tile: the cache rows of the tile are in registers (score
+// operand layout, loaded during the previous tile), the score MFMAs run,
+// the latent part is written to LDS transposed ([dim][position], bf16 hi
+// and lo) for the context operand, and the next tile's loads are issued
+// into the same registers while the softmax and context MFMAs run.
+constexpr int kVPitch = kMfmaTile + 8;  // bf16 per LDS row of the transposed tile
+
+template <int KS, int MT>
+__global__ __launch_bounds__(256) void k_mla_mfma(MlaMfmaArgs a) {
+    constexpr int LMAX = 128 * MT;
+    __shared__ float sS[4][kMfmaTile][kMfmaTile + 1];
+    __shared__ __attribute__((aligned(16))) __bf16 sVh[LMAX * kVPitch];
+    __shared__ __attribute__((aligned(16))) __bf16 sVl[LMAX * kVPitch];
+    // XCD-aware order: the column groups of one slice share blockIdx % 8
+    const int b = blockIdx.x, x8 = b & 7, q = b >> 3;
+    const int group = q % a.groups;
+    const int slice = (q / a.groups) * 8 + x8;
+    const int c0 = group * 32;
+    const int r = c0 / a.H;
+    const int64_t n_ctx = a.pos_base + r + 1;
+    const int64_t slen = mla_mfma_slice(n_ctx);
+    const int64_t p0 = (int64_t)slice * slen;
+    if (slice >= a.nslice || p0 >= n_ctx) return;  // uniform per workgroup
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, half = l >> 5, n = l & 31;
+    const int L = a.L, P = a.P;
+    const int col = c0 + n;
+    const int dbase = w * (16 * KS);  // first score dim of this wave
+
+    // queries of this lane's column, dims dbase + 16*ks + 8*half + [0, 8)
+    bf16x8_t qh[KS], ql[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) {
+        const int d0 = dbase + 16 * ks + 8 * half;
+        float v[8];
+        load8(d0 < L ? a.qabs + (int64_t)col * L + d0 : a.qrope + (int64_t)col * P + (d0 - L), v);
+        split8(v, qh[ks], ql[ks]);
+    }
+    f32x16_t o[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) o[mt][i] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+    const int64_t tend = p0 + slen < n_ctx ? p0 + slen : n_ctx;
+    const int64_t last = n_ctx - 1;
+
+    // cache rows of a tile in the score operand layout (lane: position n)
+    float kv[KS][8];
+    auto load_tile = [&](int64_t t0) {
+        const int64_t pos = t0 + n <= last ? t0 + n : last;
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            const int d0 = dbase + 16 * ks + 8 * half;
+            load8(d0 < L ? a.latent + pos * L + d0 : a.krot + pos * P + (d0 - L), kv[ks]);
+        }
+    };
+    load_tile(p0);
+
+    for (int64_t t0 = p0; t0 < tend; t0 += kMfmaTile) {
+        // ---- partial scores over this wave's dims; latent dims to LDS
+        f32x16_t sc;
+#pragma unroll
+        for (int i = 0; i < 16; i++) sc[i] = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            bf16x8_t kh, kl;
+            split8(kv[ks], kh, kl);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, qh[ks], sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, ql[ks], sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kl, qh[ks], sc, 0, 0, 0);
+            const int d0 = dbase + 16 * ks + 8 * half;
+            if (d0 < L) {
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    sVh[(d0 + j) * kVPitch + n] = kh[j];
+                    sVl[(d0 + j) * kVPitch + n] = kl[j];
+                }
+            }
+        }
+        // ---- the next tile's loads overlap the softmax and context below
+        if (t0 + kMfmaTile < tend) load_tile(t0 + kMfmaTile);
+        // ---- sum the four waves' partial tiles in wave order
+        // C layout: register i holds position row (i/4)*8 + half*4 + i%4, column n
+#pragma unroll
+        for (int i = 0; i < 16; i++) sS[w][(i >> 2) * 8 + half * 4 + (i & 3)][n] = sc[i];
+        __syncthreads();
+        float p[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int pr = (i >> 2) * 8 + half * 4 + (i & 3);
+            float v = __fadd_rn(__fadd_rn(__fadd_rn(sS[0][pr][n], sS[1][pr][n]), sS[2][pr][n]), sS[3][pr][n]);
+            p[i] = t0 + pr < n_ctx ? __fmul_rn(v, a.scale) : -INFINITY;
+        }
+        // ---- online softmax per column (lanes n and n + 32 share a column)
+        float mt_ = p[0];
+#pragma unroll
+        for (int i = 1; i < 16; i++) mt_ = fmaxf(mt_, p[i]);
+        mt_ = fmaxf(mt_, __shfl_xor(mt_, 32, 64));
+        const float m_new = fmaxf(m_run, mt_);  // finite: position t0 is live
+        const float alpha = __expf(m_run - m_new);
+        float ls = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            p[i] = __expf(p[i] - m_new);
+            ls += p[i];
+        }
+        ls += __shfl_xor(ls, 32, 64);
+        l_run = l_run * alpha + ls;
+        m_run = m_new;
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) o[mt][i] *= alpha;
+        // ---- P as the B operand: lane (half, n) needs positions 16*ks + 8*half + [0, 8)
+        bf16x8_t ph[2], pl[2];
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            float snd[4], rcv[4], pk[8];
+#pragma unroll
+            for (int i = 0; i < 4; i++) snd[i] = half ? p[8 * ks + i] : p[8 * ks + 4 + i];
+#pragma unroll
+            for (int i = 0; i < 4; i++) rcv[i] = __shfl_xor(snd[i], 32, 64);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                pk[i] = half ? rcv[i] : p[8 * ks + i];
+                pk[4 + i] = half ? p[8 * ks + 4 + i] : rcv[i];
+            }
+            split8(pk, ph[ks], pl[ks]);
+        }
+        // ---- context: A = V^T from LDS (lane: dim, 8 consecutive positions)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            const int dim = w * (32 * MT) + 32 * mt + n;
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                const int off = dim * kVPitch + 16 * ks + 8 * half;
+                const bf16x8_t vh = *(const bf16x8_t *)&sVh[off];
+                const bf16x8_t vl = *(const bf16x8_t *)&sVl[off];
+                o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh, ph[ks], o[mt], 0, 0, 0);
+                o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh, pl[ks], o[mt], 0, 0, 0);
+                o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vl, ph[ks], o[mt], 0, 0, 0);
+            }
+        }
+        __syncthreads();  // sS and sV are rewritten by the next tile
+    }
+    // ---- slice partials: O^T register i is dim w*32*MT + 32*mt + (i/4)*8 + half*4 + i%4
+    const int64_t RH = a.RH;
+    if (w == 0 && half == 0) {
+        a.part_m[(int64_t)slice * RH + col] = m_run;
+        a.part_l[(int64_t)slice * RH + col] = l_run;
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int dim = w * (32 * MT) + 32 * mt + (i >> 2) * 8 + half * 4 + (i & 3);
+            a.part_o[((int64_t)slice * L + dim) * RH + col] = o[mt][i];
+        }
+}
+
+// Merges the slices: M = max m_j, Ls = sum l_j e^(m_j - M),
+// clat = sum_j o_j e^(m_j - M) / Ls.  A workgroup takes 32 columns x 8 dims;
+// thread (col, t) first takes slices j = t, t+8, ... for the max and the
+// weights (kept in LDS; partial sums reduced in t order), then dim t over
+// all slices.  Every sum runs in a fixed order.
+constexpr int kMlaMaxSlices = 256;
+
+__global__ __launch_bounds__(256) void k_mla_combine_mfma(const float *__restrict__ part_m,
+                                                          const float *__restrict__ part_l,
+                                                          const float *__restrict__ part_o,
+                                                          int RH, int H, int L, int64_t pos_base,
+                                                          float *__restrict__ clat) {
+    __shared__ float sw[kMlaMaxSlices][33];
+    __shared__ float red[8][33];
+    __shared__ float sM[32], sInv[32];
+    const int tid = threadIdx.x, tx = tid & 31, ty = tid >> 5;
+    const int col = blockIdx.x * 32 + tx;
+    const int d = blockIdx.y * 8 + ty;
+    const int64_t n_ctx = pos_base + col / H + 1;
+    const int64_t slen = mla_mfma_slice(n_ctx);
+    const int ns = (int)((n_ctx + slen - 1) / slen);
+    float mx = -INFINITY;
+    for (int j = ty; j < ns; j += 8) mx = fmaxf(mx, part_m[(int64_t)j * RH + col]);
+    red[ty][tx] = mx;
+    __syncthreads();
+    if (ty == 0) {
+        float M = red[0][tx];
+#pragma unroll
+        for (int t = 1; t < 8; t++) M = fmaxf(M, red[t][tx]);
+        sM[tx] = M;
+    }
+    __syncthreads();
+    const float M = sM[tx];
+    float ls = 0.0f;
+    for (int j = ty; j < ns; j += 8) {
+        const float e = __expf(part_m[(int64_t)j * RH + col] - M);
+        sw[j][tx] = e;
+        ls = __fadd_rn(ls, __fmul_rn(part_l[(int64_t)j * RH + col], e));
+    }
+    __syncthreads();
+    red[ty][tx] = ls;
+    __syncthreads();
+    if (ty == 0) {
+        float t = red[0][tx];
+#pragma unroll
+        for (int u = 1; u < 8; u++) t = __fadd_rn(t, red[u][tx]);
+        sInv[tx] = 1.0f / t;
+    }
+    __syncthreads();
+    const float *po = part_o + (int64_t)d * RH + col;
+    const int64_t js = (int64_t)L * RH;
+    float acc0 = 0.0f, acc1 = 0.0f;
+    int j = 0;
+#pragma unroll 4
+    for (; j + 1 < ns; j += 2) {
+        acc0 = __builtin_fmaf(po[(int64_t)j * js], sw[j][tx], acc0);
+        acc1 = __builtin_fmaf(po[(int64_t)(j + 1) * js], sw[j + 1][tx], acc1);
+    }
+    if (j < ns) acc0 = __builtin_fmaf(po[(int64_t)j * js], sw[j][tx], acc0);
+    clat[(int64_t)col * L + d] = __fmul_rn(__fadd_rn(acc0, acc1), sInv[tx]);
+}
+
+// Largest slice count over the rows' context lengths n <= T.
+static int64_t mla_mfma_nslice(int64_t T) {
+    int64_t best = (T + mla_mfma_slice(T) - 1) / mla_mfma_slice(T);
+    for (int64_t b = 64; b <= T; b *= 2) {  // just below each slice-length step
+        const int64_t n = b * 64 - 1;
+        if (n > T) break;
+        const int64_t s = mla_mfma_slice(n), c = (n + s - 1) / s;
+        if (c > best) best = c;
+    }
+    return best;
+}
+
+static bool mla_mfma_ok(int64_t H, int64_t L, int64_t P, int64_t T) {
+    return H % 32 == 0 && L % 128 == 0 && (L + P) % 64 == 0 && L % 16 == 0 &&
+           (L / 128 == 4 && (L + P) / 64 == 9) &&  // instantiated: DeepSeek-V3 MLA (512 + 64)
+           mla_mfma_nslice(T) <= kMlaMaxSlices;
+}
+
+static size_t mla_mfma_scratch_bytes(int64_t R, int64_t H, int64_t L, int64_t T) {
+    const size_t ns = (size_t)mla_mfma_nslice(T), RH = (size_t)(R * H);
+    return ((ns * RH * 4 + 255) & ~size_t(255)) * 2 + ((ns * L * RH * 4 + 255) & ~size_t(255));
+}
+
+static size_t mla_split_scratch_bytes(int64_t R, int64_t H, int64_t L, int64_t T) {
     int64_t ns = (T + kMlaSlice - 1) / kMlaSlice;
     size_t n = (size_t)R * H * ns;
-    return ((n * 4 + 255) & ~size_t(255)) * 2 + ((n * L * 4 + 255) & ~size_t(255));
+    size_t b = ((n * 4 + 255) & ~size_t(255)) * 2 + ((n * L * 4 + 255) & ~size_t(255));
+    return b;
+}
+
+size_t mla_scratch_bytes(int64_t R, int64_t H, int64_t L, int64_t P, int64_t T) {
+    return mla_mfma_ok(H, L, P, T) ? mla_mfma_scratch_bytes(R, H, L, T)
+                                : mla_split_scratch_bytes(R, H, L, T);
 }
 
 int32_t launch_mla_attend(ut_ctx *ctx, const float *qabs, const float *qrope, const float *latent,
                           const float *krot, int64_t R, int64_t H, int64_t L, int64_t P,
                           int64_t pos_base, float scale, float *clat, void *scratch) {
     const int64_t T = pos_base + R;  // positions any row can see
+    if (mla_mfma_ok(H, L, P, T)) {
+        const int64_t RH = R * H, ns = mla_mfma_nslice(T);
+        MlaMfmaArgs a;
+        a.qabs = qabs; a.qrope = qrope; a.latent = latent; a.krot = krot;
+        a.H = (int)H; a.L = (int)L; a.P = (int)P; a.RH = (int)RH;
+        a.pos_base = pos_base;
+        a.scale = scale;
+        a.groups = (int)(RH / 32);
+        a.nslice = (int)ns;
+        a.part_m = (float *)scratch;
+        a.part_l = (float *)((char *)scratch + ((ns * RH * 4 + 255) & ~int64_t(255)));
+        a.part_o = (float *)((char *)a.part_l + ((ns * RH * 4 + 255) & ~int64_t(255)));
+        const int64_t nwg = (int64_t)a.groups * ((ns + 7) / 8 * 8);
+        int tok = timing_begin(ctx, "mla_mfma");
+        hipLaunchKernelGGL((k_mla_mfma<9, 4>), dim3((unsigned)nwg), dim3(256), 0, ctx->stream, a);
+        timing_end(ctx, tok);
+        UT_TRY(launch_check(ctx, "k_mla_mfma"));
+        tok = timing_begin(ctx, "mla_combine");
+        hipLaunchKernelGGL(k_mla_combine_mfma, dim3((unsigned)(RH / 32), (unsigned)(L / 8)),
+                           dim3(256), 0, ctx->stream, a.part_m, a.part_l, a.part_o, (int)RH, (int)H,
+                           (int)L, pos_base, clat);
+        timing_end(ctx, tok);
+        return launch_check(ctx, "k_mla_combine_mfma");
+    }
     const int nsplit = (int)((T + kMlaSlice - 1) / kMlaSlice);
     const size_t n = (size_t)R * H * nsplit;
     float *pm = (float *)scratch;
@@ -197,7 +533,7 @@ extern "C" int32_t ut_mla_attend(ut_ctx *ctx, const float *qabs_dev, const float
         return UT_ERR_ARG;
     }
     ScratchPlan plan;
-    plan.add(mla_scratch_bytes(R, H, L, pos_base + R));
+    plan.add(mla_scratch_bytes(R, H, L, P, pos_base + R));
     std::vector<void *> ptrs;
     UT_TRY(scratch_acquire(ctx, plan, ptrs));
     return launch_mla_attend(ctx, qabs_dev, q_rope_dev, latent_dev, krot_dev, R, H, L, P, pos_base,

@@ -313,6 +313,13 @@ int32_t ws_reserve(ut_session *s, int64_t rows) {
         size_t b = moe_layout(4, 1, 1, H, max_inter(m), f).total;
         if (b > moe_bytes) moe_bytes = b;
     }
+    // routed experts with the shared expert beside them in the same launches
+    for (int fa : {UT_FMT_INT4, UT_FMT_INT8})
+        for (int fb : {UT_FMT_INT4, UT_FMT_INT8}) {
+            size_t b = moe_layout(4, k, slots_routed, H, c.moe_intermediate_size, fa).total +
+                       moe_layout(4, 1, 1, H, max_inter(m), fb).total;
+            if (b > moe_bytes) moe_bytes = b;
+        }
     ScratchPlan plan;
     auto F = [&](int64_t n) { return plan.add((size_t)n * 4); };
     size_t ix = F(R * H), inorm = F(R * H), iattn = F(R * H), imoe = F(R * H);
@@ -326,7 +333,7 @@ int32_t ws_reserve(ut_session *s, int64_t rows) {
     size_t idA = plan.add(matmul_digit_bytes(R, kmax));
     size_t idB = plan.add(matmul_digit_bytes(R, kmax));
     size_t imoes = plan.add(moe_bytes);
-    size_t imla = plan.add(mla_scratch_bytes(R < kMlaRowsPerCall ? R : kMlaRowsPerCall, heads, Lr, s->cap));
+    size_t imla = plan.add(mla_scratch_bytes(R < kMlaRowsPerCall ? R : kMlaRowsPerCall, heads, Lr, c.qk_rope_head_dim, s->cap));
     size_t iarg = plan.add(argmax_scratch_bytes(R, c.vocab_size) + 256);
     size_t total = 0;
     for (size_t b : plan.sizes) total += b;
@@ -428,7 +435,7 @@ int32_t mlp_add(ut_session *s, const MlpW &w, const float *x, const XDigits &xd,
 // in choice order, into out (overwritten).  x: normed rows (f32, for the f32
 // router gate) with digits xd.
 int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigits &xd,
-                    int64_t rows, float *out) {
+                    int64_t rows, float *out, int accumulate = 0, const MlpW *shared = nullptr) {
     ut_model *m = s->m;
     const ut_model_config &c = m->c;
     const int64_t H = c.hidden_size, E = c.n_routed_experts;
@@ -458,9 +465,18 @@ int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
         if (L.expert_fmt != UT_FMT_F32) mc.x_digits = &xr;
         mc.out = out + s0 * H;
         mc.ldo = H;
-        mc.accumulate = 0;
+        mc.accumulate = accumulate;
         mc.err_flag = s->ws.err;
         mc.plan_ready = true;
+        MoeCall sc;
+        if (shared) {
+            sc.fmt = shared->fmt;
+            sc.tbl = shared->ptrs;
+            sc.I = shared->inter;
+            sc.plan = &m->mlp_plan;
+            mc.shared = &sc;
+            mc.shared_scratch = (char *)s->ws.moe + lay.total;
+        }
         UT_TRY(moe_pass(m->ctx, mc, s->ws.moe));
     }
     return UT_OK;
@@ -526,10 +542,12 @@ int32_t run_layer(ut_session *s, const LayerW &L, float *x, int64_t rows, KvCach
     }
     UT_TRY(norm_dig(s, x, H, L.post_norm, H, rows, w.normed, H, w.digA, f, &xd));
     if (L.dense) return mlp_add(s, L.mlp, w.normed, xd, rows, x);
-    UT_TRY(moe_forward(s, L, w.normed, xd, rows, w.moe_out));
     // x += (routed + shared) (model.rs:282-284 then the residual add)
-    if (L.has_shared) return mlp_add(s, L.shared, w.normed, xd, rows, x, w.moe_out);
-    return launch_add(ctx, x, w.moe_out, rows * H);
+    if (L.has_shared && moe_dual_ok(L.expert_fmt, L.shared.fmt))
+        return moe_forward(s, L, w.normed, xd, rows, x, 1, &L.shared);
+    if (!L.has_shared) return moe_forward(s, L, w.normed, xd, rows, x, 1);
+    UT_TRY(moe_forward(s, L, w.normed, xd, rows, w.moe_out));
+    return mlp_add(s, L.shared, w.normed, xd, rows, x, w.moe_out);
 }
 
 int32_t check_flags(ut_session *s) {

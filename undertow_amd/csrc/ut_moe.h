@@ -41,6 +41,13 @@ struct MoeCall {
     bool plan_ready = false;  // the slot plan is already in the scratch (launch_route_plan)
     const MoePlan *plan = nullptr;  // a fixed plan elsewhere (one-slot MLPs)
     const float *init = nullptr;    // combine starts from init[M, ldo] instead of zero
+    // Optional one-slot MLP (a shared expert, format int4 or int8 like the
+    // routed experts) run in the same gate/up and down launches as the
+    // routed experts and added after the routed sum.  Its fmt, tbl, I and
+    // plan are used; it needs x_digits holding both formats' digits and its
+    // own scratch of moe_layout(M, 1, 1, H, I, fmt).total bytes.
+    const MoeCall *shared = nullptr;
+    void *shared_scratch = nullptr;
 };
 
 struct ScratchLayout {
@@ -96,6 +103,11 @@ inline int64_t moe_slots(int M, int64_t k, int64_t E, int extra) {
 ScratchLayout moe_layout(int64_t M, int64_t k, int64_t slots, int64_t H, int64_t I, int fmt);
 size_t moe_scratch_bytes(int64_t M, int64_t k, int64_t slots, int64_t H, int64_t I, int fmt);
 bool moe_shape_ok(int fmt, int64_t H, int64_t I);
+// Whether routed experts of format fa and a shared MLP of format fb can run
+// in the same launches.
+inline bool moe_dual_ok(int fa, int fb) {
+    return (fa == UT_FMT_INT4 || fa == UT_FMT_INT8) && (fb == UT_FMT_INT4 || fb == UT_FMT_INT8);
+}
 // scratch: device memory of moe_layout(...).total bytes for this call's
 // (M, k, slots); slots from moe_slots().
 int32_t moe_pass(ut_ctx *ctx, const MoeCall &c, void *scratch);

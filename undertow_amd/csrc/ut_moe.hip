@@ -203,17 +203,15 @@ struct GateUpArgs {
 // w*4 + g; row slot 0 reads gate row o, slot 1 up row o, so both land in the
 // same lanes and h = silu(g)*u is formed in registers.
 template <int FMT, int M>
-__global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up(GateUpArgs a) {
-    const int u = blockIdx.y;
-    if (u >= *a.count) return;
-    __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
-    __shared__ uint32_t wg_max[4];
+__device__ __forceinline__ void gate_up_body(const GateUpArgs &a, int u, int tile, uint32_t *lds,
+                                             uint32_t *wg_max) {
+    if (u >= *a.count || tile >= a.ntiles) return;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
     if (tid < 4) wg_max[tid] = 0;
     const int e = a.uniq[u];
     const uint8_t *gw = a.tbl.gate_w[e], *uw = a.tbl.up_w[e];
     const float *gsc = a.tbl.gate_s[e], *usc = a.tbl.up_s[e];
-    const int64_t o = (int64_t)blockIdx.x * kGateUpRowsPerWG + wave * 4 + g;
+    const int64_t o = (int64_t)tile * kGateUpRowsPerWG + wave * 4 + g;
     const int64_t oc = o < a.I ? o : a.I - 1;
     const uint8_t *rows[2] = {gw + oc * a.row_bytes, uw + oc * a.row_bytes};
     CoreOut<FMT, M, 2> res;
@@ -239,7 +237,24 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up(GateUpArgs a) {
         }
     }
     __syncthreads();
-    if (tid < M) a.hmax_parts[((int64_t)u * M + tid) * a.ntiles + blockIdx.x] = wg_max[tid];
+    if (tid < M) a.hmax_parts[((int64_t)u * M + tid) * a.ntiles + tile] = wg_max[tid];
+}
+
+template <int FMT, int M>
+__global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up(GateUpArgs a) {
+    __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
+    __shared__ uint32_t wg_max[4];
+    gate_up_body<FMT, M>(a, blockIdx.y, blockIdx.x, lds, wg_max);
+}
+
+// Routed experts (format FA, slots 0..gridDim.y-2) and one shared MLP
+// (format FB, the last grid row) in one launch.
+template <int FA, int FB, int M>
+__global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up_dual(GateUpArgs a, GateUpArgs b) {
+    __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
+    __shared__ uint32_t wg_max[4];
+    if (blockIdx.y + 1 < gridDim.y) gate_up_body<FA, M>(a, blockIdx.y, blockIdx.x, lds, wg_max);
+    else gate_up_body<FB, M>(b, 0, blockIdx.x, lds, wg_max);
 }
 
 // --------------------------------------------------------------- down ---
@@ -259,16 +274,14 @@ struct DownArgs {
 template <int M> constexpr int down_rows() { return M <= 2 ? 4 : 2; }
 
 template <int FMT, int M>
-__global__ __launch_bounds__(kGemvThreads) void k_moe_down(DownArgs a) {
+__device__ __forceinline__ void down_body(const DownArgs &a, int u, int tile, uint32_t *lds) {
     constexpr int R = down_rows<M>();
-    const int u = blockIdx.y;
     if (u >= *a.count) return;
-    __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
     const int e = a.uniq[u];
     const uint8_t *dw = a.tbl.down_w[e];
     const float *dsc = a.tbl.down_s[e];
-    const int64_t row0 = (int64_t)blockIdx.x * (16 * R) + wave * (4 * R) + g * R;
+    const int64_t row0 = (int64_t)tile * (16 * R) + wave * (4 * R) + g * R;
     const uint8_t *rows[R];
 #pragma unroll
     for (int r = 0; r < R; r++) {
@@ -315,6 +328,19 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_down(DownArgs a) {
         }
 }
 
+template <int FMT, int M>
+__global__ __launch_bounds__(kGemvThreads) void k_moe_down(DownArgs a) {
+    __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
+    down_body<FMT, M>(a, blockIdx.y, blockIdx.x, lds);
+}
+
+template <int FA, int FB, int M>
+__global__ __launch_bounds__(kGemvThreads) void k_moe_down_dual(DownArgs a, DownArgs b) {
+    __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
+    if (blockIdx.y + 1 < gridDim.y) down_body<FA, M>(a, blockIdx.y, blockIdx.x, lds);
+    else down_body<FB, M>(b, 0, blockIdx.x, lds);
+}
+
 // ------------------------------------------------------------ combine ---
 // out[s, o] = sum_c w[s,c] * d[slot(s,c), s, o], in router choice order from
 // zero (model.rs:268-281: moe_out starts zeroed; the reference adds
@@ -324,7 +350,8 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_down(DownArgs a) {
 __global__ void k_moe_combine(const int32_t *__restrict__ choice_slot,
                               const float *__restrict__ weights, const float *__restrict__ d,
                               int M, int k, int64_t H, const int32_t *__restrict__ count,
-                              int extra, const float *__restrict__ init, float *__restrict__ out,
+                              int extra, const float *__restrict__ dshared,
+                              const float *__restrict__ init, float *__restrict__ out,
                               int64_t ldo, int accumulate) {
     const int s = blockIdx.y;
     const int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -340,6 +367,9 @@ __global__ void k_moe_combine(const int32_t *__restrict__ choice_slot,
         int slot = *count - 1;
         acc = __fadd_rn(acc, d[((int64_t)slot * M + s) * H + o]);
     }
+    // a shared MLP run beside the routed experts (MlpWeights::forward_add
+    // after the routed sum, model.rs:282-284)
+    if (dshared) acc = __fadd_rn(acc, dshared[(int64_t)s * H + o]);
     float *po = out + s * ldo + o;
     *po = accumulate ? __fadd_rn(*po, acc) : acc;
 }
@@ -368,6 +398,41 @@ ScratchLayout moe_layout(int64_t M, int64_t k, int64_t slots, int64_t H, int64_t
     L.hflags = hflags;
     L.ntiles = ntiles;
     return L;
+}
+
+template <int FA, int M>
+static void launch_gate_up(ut_ctx *ctx, const GateUpArgs &a, int64_t slots, const GateUpArgs *b,
+                           int fb) {
+    if (!b) {
+        hipLaunchKernelGGL((k_moe_gate_up<FA, M>), dim3((unsigned)a.ntiles, (unsigned)slots),
+                           dim3(kGemvThreads), 0, ctx->stream, a);
+        return;
+    }
+    if constexpr (FA != UT_FMT_F32) {
+        const dim3 grid((unsigned)(a.ntiles > b->ntiles ? a.ntiles : b->ntiles), (unsigned)(slots + 1));
+        if (fb == UT_FMT_INT4)
+            hipLaunchKernelGGL((k_moe_gate_up_dual<FA, UT_FMT_INT4, M>), grid, dim3(kGemvThreads), 0, ctx->stream, a, *b);
+        else
+            hipLaunchKernelGGL((k_moe_gate_up_dual<FA, UT_FMT_INT8, M>), grid, dim3(kGemvThreads), 0, ctx->stream, a, *b);
+    }
+}
+
+template <int FA, int M>
+static void launch_down(ut_ctx *ctx, const DownArgs &a, int64_t slots, const DownArgs *b, int fb) {
+    constexpr int DR = 16 * down_rows<M>();
+    const unsigned gx = (unsigned)((a.H + DR - 1) / DR);
+    if (!b) {
+        hipLaunchKernelGGL((k_moe_down<FA, M>), dim3(gx, (unsigned)slots), dim3(kGemvThreads), 0,
+                           ctx->stream, a);
+        return;
+    }
+    if constexpr (FA != UT_FMT_F32) {
+        const dim3 grid(gx, (unsigned)(slots + 1));
+        if (fb == UT_FMT_INT4)
+            hipLaunchKernelGGL((k_moe_down_dual<FA, UT_FMT_INT4, M>), grid, dim3(kGemvThreads), 0, ctx->stream, a, *b);
+        else
+            hipLaunchKernelGGL((k_moe_down_dual<FA, UT_FMT_INT8, M>), grid, dim3(kGemvThreads), 0, ctx->stream, a, *b);
+    }
 }
 
 template <int FMT, int M>
@@ -405,6 +470,13 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
     }
     float *h = (float *)(base + L.h);
     uint32_t *hmax = (uint32_t *)(base + L.hmax);
+    // the shared MLP's buffers (c.shared)
+    ScratchLayout SL;
+    char *sbase = (char *)c.shared_scratch;
+    if (c.shared) SL = moe_layout(M, 1, 1, c.H, c.shared->I, c.shared->fmt);
+    GateUpArgs gb{};
+    DownArgs db{};
+    float *dshared = nullptr;
     {
         GateUpArgs a;
         a.tbl = c.tbl;
@@ -418,9 +490,23 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
         a.h = h;
         a.hmax_parts = hmax;
         a.ntiles = (int)L.ntiles;
+        if (c.shared) {
+            const MoeCall &sc = *c.shared;
+            gb.tbl = sc.tbl;
+            gb.uniq = sc.plan->uniq;
+            gb.count = sc.plan->count;
+            gb.H = c.H;
+            gb.I = sc.I;
+            gb.row_bytes = payload_bytes(sc.fmt, 1, c.H);
+            gb.x.dig = sc.fmt == UT_FMT_INT4 ? c.x_digits->dig4 : c.x_digits->dig8;
+            gb.x.KW = sc.fmt == UT_FMT_INT4 ? (c.H + 7) / 8 : (c.H + 3) / 4;
+            gb.exps = c.x_digits->exps;
+            gb.h = (float *)(sbase + SL.h);
+            gb.hmax_parts = (uint32_t *)(sbase + SL.hmax);
+            gb.ntiles = (int)SL.ntiles;
+        }
         tok = timing_begin(ctx, FMT == UT_FMT_INT4 ? "moe_gate_up_int4" : FMT == UT_FMT_INT8 ? "moe_gate_up_int8" : "moe_gate_up_f32");
-        hipLaunchKernelGGL((k_moe_gate_up<FMT, M>), dim3((unsigned)L.ntiles, (unsigned)slots),
-                           dim3(kGemvThreads), 0, ctx->stream, a);
+        launch_gate_up<FMT, M>(ctx, a, slots, c.shared ? &gb : nullptr, c.shared ? c.shared->fmt : 0);
         timing_end(ctx, tok);
         UT_TRY(launch_check(ctx, "k_moe_gate_up"));
     }
@@ -442,17 +528,31 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
         a.hmax_parts = hmax;
         a.nparts = (int)L.ntiles;
         a.d = d;
+        if (c.shared) {
+            const MoeCall &sc = *c.shared;
+            db.tbl = sc.tbl;
+            db.uniq = sc.plan->uniq;
+            db.count = sc.plan->count;
+            db.H = c.H;
+            db.I = sc.I;
+            db.row_bytes = payload_bytes(sc.fmt, 1, sc.I);
+            db.x = XSrc{};
+            db.x.xf = gb.h;
+            db.x.ldx = sc.I;
+            db.x_slot_stride = (int64_t)M * sc.I;
+            db.hmax_parts = gb.hmax_parts;
+            db.nparts = gb.ntiles;
+            db.d = dshared = (float *)(sbase + SL.d);
+        }
         tok = timing_begin(ctx, FMT == UT_FMT_INT4 ? "moe_down_int4" : FMT == UT_FMT_INT8 ? "moe_down_int8" : "moe_down_f32");
-        constexpr int DR = 16 * down_rows<M>();
-        hipLaunchKernelGGL((k_moe_down<FMT, M>), dim3((unsigned)((c.H + DR - 1) / DR), (unsigned)slots),
-                           dim3(kGemvThreads), 0, ctx->stream, a);
+        launch_down<FMT, M>(ctx, a, slots, c.shared ? &db : nullptr, c.shared ? c.shared->fmt : 0);
         timing_end(ctx, tok);
         UT_TRY(launch_check(ctx, "k_moe_down"));
     }
     tok = timing_begin(ctx, "moe_combine");
     hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((c.H + 255) / 256), (unsigned)M), dim3(256),
                        0, ctx->stream, plan.choice_slot, c.weights, d, M, c.k, c.H, plan.count,
-                       c.extra_slot >= 0 ? 1 : 0, c.init, c.out, c.ldo, c.accumulate);
+                       c.extra_slot >= 0 ? 1 : 0, dshared, c.init, c.out, c.ldo, c.accumulate);
     timing_end(ctx, tok);
     return launch_check(ctx, "k_moe_combine");
 }
@@ -487,6 +587,19 @@ int32_t moe_pass(ut_ctx *ctx, const MoeCall &c, void *scratch) {
     if (c.M < 1 || c.M > 4) {
         set_error(ctx, "moe_pass: M=%d outside 1..4", c.M);
         return UT_ERR_ARG;
+    }
+    if (c.shared) {
+        const MoeCall &sc = *c.shared;
+        const int need = (sc.fmt == UT_FMT_INT4 ? XD_DIG4 : XD_DIG8) |
+                         (c.fmt == UT_FMT_INT4 ? XD_DIG4 : XD_DIG8);
+        const bool have = c.x_digits && (!(need & XD_DIG4) || c.x_digits->dig4) &&
+                          (!(need & XD_DIG8) || c.x_digits->dig8);
+        if (!moe_dual_ok(c.fmt, sc.fmt) || !sc.plan || !c.shared_scratch || !have ||
+            !moe_shape_ok(sc.fmt, c.H, sc.I) || c.extra_slot >= 0) {
+            set_error(ctx, "moe_pass: shared MLP (format %d) cannot run beside format %d experts",
+                      sc.fmt, c.fmt);
+            return UT_ERR_ARG;
+        }
     }
     if (!moe_shape_ok(c.fmt, c.H, c.I)) {
         set_error(ctx, "moe: hidden %lld / inter %lld not supported for format %d", (long long)c.H,

@@ -303,11 +303,14 @@ def argmax_rows(ctx: Context, logits):
     return idx
 
 
-def mla_attend(ctx: Context, qabs, q_rope, latent, krot, pos_base: int, scale: float):
+def mla_attend(ctx: Context, qabs, q_rope, latent, krot, pos_base: int, scale: float, out=None):
     torch = _torch()
     R, H, L = qabs.shape
     P = q_rope.shape[2]
-    out = torch.empty((R, H, L), dtype=torch.float32, device=qabs.device)
+    if out is None:
+        out = torch.empty((R, H, L), dtype=torch.float32, device=qabs.device)
+    elif tuple(out.shape) != (R, H, L) or out.dtype != torch.float32 or not out.is_contiguous():
+        raise ShapeError(f"mla_attend: out must be a contiguous float32 [{R}, {H}, {L}] tensor")
     ctx.check(lib().ut_mla_attend(ctx.handle, _ptr(qabs), _ptr(q_rope), _ptr(latent), _ptr(krot),
                                   R, H, L, P, pos_base, scale, _ptr(out)))
     return out
