@@ -167,6 +167,20 @@ int32_t ut_mla_attend(ut_ctx *ctx, const float *qabs_dev, const float *q_rope_de
                       const float *latent_dev, const float *krot_dev, int64_t R, int64_t H,
                       int64_t L, int64_t P, int64_t pos_base, float scale, float *clat_dev);
 
+/* The same attention over a cache kept on the device in the split form the
+ * bf16 matrix-core kernel reads (LayerKvCache, attention.rs:76-94, held as
+ * [T][2][L+P] bf16: per position the hi parts of [latent | krot], then the lo
+ * parts, x = hi + lo to about 2^-17 |x|; the bytes of the f32 cache).
+ * ut_mla_cache_split converts T f32 positions into that form (kc_dev holds
+ * T * 2 * (L+P) bf16, 16-byte aligned); ut_mla_attend_split then attends
+ * without converting.  Shapes: H % 32 == 0, L == 512, P == 64 (DeepSeek-V3);
+ * others return UT_ERR_SHAPE. */
+int32_t ut_mla_cache_split(ut_ctx *ctx, const float *latent_dev, const float *krot_dev, int64_t T,
+                           int64_t L, int64_t P, void *kc_dev);
+int32_t ut_mla_attend_split(ut_ctx *ctx, const float *qabs_dev, const float *q_rope_dev,
+                            const void *kc_dev, int64_t R, int64_t H, int64_t L, int64_t P,
+                            int64_t pos_base, float scale, float *clat_dev);
+
 /* ---------------------------------------------------------------- model */
 /* DeepseekConfig fields the forward pass reads (adapters/undertow-deepseek-
  * moe/src/config.rs:30-85).  q_lora_rank == 0 selects the direct q_proj. */

@@ -191,8 +191,42 @@ def test_mla_attend_matches_oracle(ctx, R, H, L, P, T):
     mfma = H % 32 == 0 and L == 512 and P == 64
     tol = (1e-4 if mfma else 1e-5) * max(1.0, np.abs(want).max())
     assert np.abs(got - want).max() <= tol, np.abs(got - want).max()
+    if mfma:
+        # the split-cache entry (cache converted once) gives the same bits
+        kc = U.mla_cache_split(ctx, dev(lat), dev(kr))
+        got2 = host(U.mla_attend_split(ctx, dev(qabs), dev(qr), kc, pos_base, scale))
+        assert np.array_equal(got2, got)
     # row independence: row s alone at pos_base + s sees the same context
     for s in range(R):
         one = host(U.mla_attend(ctx, dev(qabs[s:s + 1]), dev(qr[s:s + 1]), dev(lat), dev(kr),
                                 pos_base + s, scale))
         assert np.array_equal(one[0], got[s])
+
+
+def test_mla_split_cache_round_trip(ctx):
+    """hi + lo of the split cache reproduces the f32 cache to 2^-16 relative
+    (hi = bf16(x) rounded to nearest, lo = bf16(x - hi))."""
+    import torch
+    import undertow_amd as U
+    rng = np.random.default_rng(5)
+    T, L, P = 37, 512, 64
+    lat = (rng.standard_normal((T, L)) * np.exp(rng.uniform(-20, 20, (T, 1)))).astype(np.float32)
+    kr = rng.standard_normal((T, P)).astype(np.float32)
+    kc = U.mla_cache_split(ctx, dev(lat), dev(kr))
+    bits = host(kc).astype(np.uint16).astype(np.uint32) << 16
+    parts = bits.view(np.float32).astype(np.float64)  # [T, 2, L+P]
+    x = np.concatenate([lat, kr], 1).astype(np.float64)
+    hi, lo = parts[:, 0], parts[:, 1]
+    # hi is x rounded to bf16 (8 significant bits)
+    assert np.all(np.abs(hi - x) <= np.abs(x) * 2.0 ** -8)
+    assert np.all(np.abs(hi + lo - x) <= np.abs(x) * 2.0 ** -16)
+
+
+def test_mla_attend_split_rejects_other_shapes(ctx):
+    import undertow_amd as U
+    q = dev(np.zeros((1, 4, 64), np.float32))
+    qr = dev(np.zeros((1, 4, 16), np.float32))
+    kc = U.mla_cache_split(ctx, dev(np.zeros((8, 64), np.float32)), dev(np.zeros((8, 16), np.float32)))
+    with pytest.raises(U.UtError) as ei:
+        U.mla_attend_split(ctx, q, qr, kc, 4, 0.1)
+    assert ei.value.code == U.runtime.UT_ERR_SHAPE

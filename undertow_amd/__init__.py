@@ -5,5 +5,6 @@ in ``include/undertow_hip.h``); this package is its host-side binding.
 """
 from .runtime import (  # noqa: F401
     EXPORTED, F32, INFER, INT4, INT8, LIB_PATH, Context, ContextOverflow, ExpertTable, Model,
-    ModelConfig, QTensor, Session, ShapeError, UtError, argmax_rows, lib, mla_attend, route,
+    ModelConfig, QTensor, Session, ShapeError, UtError, argmax_rows, lib, mla_attend,
+    mla_attend_split, mla_cache_split, route,
 )

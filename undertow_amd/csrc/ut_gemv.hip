@@ -6,6 +6,11 @@
 #include "ut_gemv_core.h"
 #include "ut_moe.h"
 
+// Weight steps in flight per lane in the plain GEMV (see gemv_core).
+#ifndef UT_GEMV_DEPTH
+#define UT_GEMV_DEPTH 2
+#endif
+
 namespace ut {
 
 // ------------------------------------------------------- digitisation ---
@@ -412,7 +417,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
     CoreOut<FMT, M, R> res;
     if (a.ks > 1) {
         const int64_t kb = (int64_t)blockIdx.z * a.kslice;
-        gemv_core<FMT, M, R>(rows, a.K, a.x, lds, res, kb, kb + a.kslice);
+        gemv_core<FMT, M, R, UT_GEMV_DEPTH>(rows, a.K, a.x, lds, res, kb, kb + a.kslice);
 #pragma unroll
         for (int r = 0; r < R; r++)
 #pragma unroll
@@ -424,7 +429,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
             }
         return;
     }
-    gemv_core<FMT, M, R>(rows, a.K, a.x, lds, res);
+    gemv_core<FMT, M, R, UT_GEMV_DEPTH>(rows, a.K, a.x, lds, res);
 #pragma unroll
     for (int r = 0; r < R; r++)
 #pragma unroll

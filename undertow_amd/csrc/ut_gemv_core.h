@@ -98,6 +98,27 @@ __device__ __forceinline__ void digit_words(const float *v, int n, int32_t sh,
     for (int p = 0; p < PL; p++) w[p] ^= FLIP & (n * B >= 32 ? 0xffffffffu : ((1u << (n * B)) - 1));
 }
 
+// Loads through global-address-space pointers: the row pointers come from
+// device-side expert tables, so the compiler cannot infer their address
+// space and would otherwise emit flat loads (which also hold the LDS
+// counter and force conservative waits).
+// (Loaded as native vectors: a class type's copy constructor would take the
+// address back to the generic space.)
+typedef unsigned int ut_u32x4 __attribute__((ext_vector_type(4)));
+typedef float ut_f32x4 __attribute__((ext_vector_type(4)));
+template <typename T> __device__ __forceinline__ T ld_global(const void *p);
+template <> __device__ __forceinline__ uint4 ld_global<uint4>(const void *p) {
+    const ut_u32x4 v = *(const __attribute__((address_space(1))) ut_u32x4 *)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float ld_global_f32(const float *p) {
+    return *(const __attribute__((address_space(1))) float *)p;
+}
+template <> __device__ __forceinline__ float4 ld_global<float4>(const void *p) {
+    const ut_f32x4 v = *(const __attribute__((address_space(1))) ut_f32x4 *)p;
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
 __device__ inline int64_t shfl_xor_i64(int64_t v, int off) {
     int lo = __shfl_xor((int)(uint32_t)(uint64_t)v, off, 16);
     int hi = __shfl_xor((int)(uint32_t)((uint64_t)v >> 32), off, 16);
@@ -115,11 +136,11 @@ template <int FMT, int M, int R = kGemvRows> struct CoreOut {
 // K: columns (the caller's contract: int4 K % 32 == 0, int8 K % 16 == 0,
 // f32 K % 4 == 0, rows 16-byte aligned).
 //
-// The K loop is software-pipelined two steps deep: the weights of steps
-// t+1 and t+2 are in flight while step t computes, and the first loads are
-// issued before the first activation chunk is staged, so the LDS barrier
-// does not drain the memory pipe.
-template <int FMT, int M, int R = kGemvRows>
+// The K loop is software-pipelined DEPTH steps deep: the weights of the
+// next DEPTH-1 steps are in flight while a step computes, and the first
+// loads are issued before the first activation chunk is staged, so the LDS
+// barrier does not drain the memory pipe.
+template <int FMT, int M, int R = kGemvRows, int DEPTH = 2>
 __device__ __forceinline__ void gemv_core(const uint8_t *const rows[R], int64_t K, const XSrc &x,
                                           uint32_t *lds, CoreOut<FMT, M, R> &res,
                                           int64_t k_begin = 0, int64_t k_end = -1) {
@@ -147,7 +168,7 @@ __device__ __forceinline__ void gemv_core(const uint8_t *const rows[R], int64_t 
         if (col < K) {
             const int64_t boff = col * T::kBytesPerCol2 / 2;
 #pragma unroll
-            for (int r = 0; r < R; r++) w[r] = *(const uint4 *)(rows[r] + boff);
+            for (int r = 0; r < R; r++) w[r] = ld_global<uint4>(rows[r] + boff);
         }
     };
     auto stage = [&](int64_t kc, int kcn) {
@@ -156,7 +177,7 @@ __device__ __forceinline__ void gemv_core(const uint8_t *const rows[R], int64_t 
             const int n4 = kcn / 4;  // float4 per row
             for (int i = tid; i < M * n4; i += kGemvThreads) {
                 int m = i / n4, c = i - m * n4;
-                float4 v = *(const float4 *)(x.xf + m * x.ldx + kc + 4 * c);
+                float4 v = ld_global<float4>(x.xf + m * x.ldx + kc + 4 * c);
                 *(float4 *)(lds + m * KC + 4 * c) = v;
             }
         } else if (x.dig) {
@@ -164,7 +185,7 @@ __device__ __forceinline__ void gemv_core(const uint8_t *const rows[R], int64_t 
             const int64_t w0 = kc / T::kColsPerWord;
             for (int i = tid; i < M * PL * n4; i += kGemvThreads) {
                 int mp = i / n4, c = i - mp * n4;
-                uint4 v = *(const uint4 *)(x.dig + (int64_t)mp * x.KW + w0 + 4 * c);
+                uint4 v = ld_global<uint4>(x.dig + (int64_t)mp * x.KW + w0 + 4 * c);
                 *(uint4 *)(lds + mp * LW + 4 * c) = v;
             }
         } else {
@@ -176,11 +197,11 @@ __device__ __forceinline__ void gemv_core(const uint8_t *const rows[R], int64_t 
                 const float *src = x.xf + m * x.ldx + kc + g * CPW;
                 float v[CPW];
                 if constexpr (CPW == 8) {
-                    const float4 a = *(const float4 *)src, b = *(const float4 *)(src + 4);
+                    const float4 a = ld_global<float4>(src), b = ld_global<float4>(src + 4);
                     v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
                     v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
                 } else {
-                    const float4 a = *(const float4 *)src;
+                    const float4 a = ld_global<float4>(src);
                     v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
                 }
                 uint32_t w[PL];
@@ -238,37 +259,31 @@ __device__ __forceinline__ void gemv_core(const uint8_t *const rows[R], int64_t 
         }
     };
 
-    // columns [k_begin, k_end) (k_begin a multiple of STEP); K bounds loads
+    // columns [k_begin, k_end) (k_begin a multiple of STEP); K bounds loads.
+    // DEPTH steps of weights are in flight per lane: step t computes while
+    // steps t+1 .. t+DEPTH-1 are loading.
     const int64_t kend = k_end < 0 || k_end > K ? K : k_end;
     const int64_t nsteps = kend > k_begin ? (kend - k_begin + STEP - 1) / STEP : 0;
     const int64_t lane_col = k_begin + (int64_t)s * LANE_COLS;
-    uint4 wa[R], wb[R];
+    uint4 wq[DEPTH][R];
     auto loadk = [&](uint4 (&w)[R], int64_t col) { if (col < kend) load(w, col); };
-    loadk(wa, lane_col);
-    loadk(wb, lane_col + STEP);
+#pragma unroll
+    for (int u = 0; u < DEPTH; u++) loadk(wq[u], lane_col + u * STEP);
     int64_t kc = k_begin, chunk_end = k_begin;
-    for (int64_t t = 0; t < nsteps; t += 2) {
-        // step t (buffer a)
-        if (k_begin + t * STEP >= chunk_end) {
-            kc = k_begin + t * STEP;
-            const int kcn = (int)((kend - kc) < KC ? (kend - kc) : KC);
-            chunk_end = kc + kcn;
-            stage(kc, kcn);
-        }
-        const int64_t ca = t * STEP + lane_col;
-        if (ca < kend) compute(wa, (int)(ca - kc));
-        loadk(wa, ca + 2 * STEP);
-        // step t+1 (buffer b)
-        if (t + 1 < nsteps) {
-            if (k_begin + (t + 1) * STEP >= chunk_end) {
-                kc = k_begin + (t + 1) * STEP;
-                const int kcn = (int)((kend - kc) < KC ? (kend - kc) : KC);
-                chunk_end = kc + kcn;
-                stage(kc, kcn);
+    for (int64_t t = 0; t < nsteps; t += DEPTH) {
+#pragma unroll
+        for (int u = 0; u < DEPTH; u++) {
+            if (t + u < nsteps) {
+                if (k_begin + (t + u) * STEP >= chunk_end) {
+                    kc = k_begin + (t + u) * STEP;
+                    const int kcn = (int)((kend - kc) < KC ? (kend - kc) : KC);
+                    chunk_end = kc + kcn;
+                    stage(kc, kcn);
+                }
+                const int64_t cu = (t + u) * STEP + lane_col;
+                if (cu < kend) compute(wq[u], (int)(cu - kc));
+                loadk(wq[u], cu + DEPTH * STEP);
             }
-            const int64_t cb = (t + 1) * STEP + lane_col;
-            if (cb < kend) compute(wb, (int)(cb - kc));
-            loadk(wb, cb + 2 * STEP);
         }
     }
 
@@ -321,7 +336,7 @@ __device__ __forceinline__ float core_value(const CoreOut<FMT, M, R> &res, int r
                                             const int32_t *exps, const float *scales,
                                             int64_t row) {
     if constexpr (FMT == UT_FMT_F32) return res.F[r][m];
-    else return int_total_to_f32(res.S[r][m], exps[m], scales[row]);
+    else return int_total_to_f32(res.S[r][m], exps[m], ld_global_f32(scales + row));
 }
 
 }  // namespace ut

@@ -190,7 +190,8 @@ __device__ __forceinline__ void load8(const float *p, float (&x)[8]) {
 }
 
 struct MlaMfmaArgs {
-    const float *qabs, *qrope, *latent, *krot;
+    const float *qabs, *qrope;
+    const __bf16 *kc;  // [T][2][L+P]: bf16 hi plane then lo plane per position
     int H, L, P, RH;
     int64_t pos_base;
     float scale;
@@ -201,16 +202,17 @@ struct MlaMfmaArgs {
 // KS: k-steps (16 dims) per wave for the scores, (L+P) = 64*KS;
 // MT: 32-dim m-tiles per wave for the context, L = 128*MT.
 //
-// Per 32-position tile: the cache rows of the tile are in registers (score
-// operand layout, loaded during the previous tile), the score MFMAs run,
-// the latent part is written to LDS transposed ([dim][position], bf16 hi
-// and lo) for the context operand, and the next tile's loads are issued
-// into the same registers while the softmax and context MFMAs run.
+// Per 32-position tile: the tile's cache rows are in registers in the score
+// operand layout (bf16 hi and lo, loaded during the previous tile, while the
+// next tile loads into a second register set); the score MFMAs run; the
+// latent part is written to LDS transposed ([dim][position]) for the
+// context operand; then the softmax and context MFMAs.
 constexpr int kVPitch = kMfmaTile + 8;  // bf16 per LDS row of the transposed tile
 
 template <int KS, int MT>
 __global__ __launch_bounds__(256) void k_mla_mfma(MlaMfmaArgs a) {
     constexpr int LMAX = 128 * MT;
+    constexpr int D = 64 * KS;
     __shared__ float sS[4][kMfmaTile][kMfmaTile + 1];
     __shared__ __attribute__((aligned(16))) __bf16 sVh[LMAX * kVPitch];
     __shared__ __attribute__((aligned(16))) __bf16 sVl[LMAX * kVPitch];
@@ -227,13 +229,13 @@ __global__ __launch_bounds__(256) void k_mla_mfma(MlaMfmaArgs a) {
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, half = l >> 5, n = l & 31;
     const int L = a.L, P = a.P;
     const int col = c0 + n;
-    const int dbase = w * (16 * KS);  // first score dim of this wave
+    const int dlane = w * (16 * KS) + 8 * half;  // this lane's first score dim
 
-    // queries of this lane's column, dims dbase + 16*ks + 8*half + [0, 8)
+    // queries of this lane's column, dims dlane + 16*ks + [0, 8)
     bf16x8_t qh[KS], ql[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ks++) {
-        const int d0 = dbase + 16 * ks + 8 * half;
+        const int d0 = dlane + 16 * ks;
         float v[8];
         load8(d0 < L ? a.qabs + (int64_t)col * L + d0 : a.qrope + (int64_t)col * P + (d0 - L), v);
         split8(v, qh[ks], ql[ks]);
@@ -245,54 +247,56 @@ __global__ __launch_bounds__(256) void k_mla_mfma(MlaMfmaArgs a) {
         for (int i = 0; i < 16; i++) o[mt][i] = 0.0f;
     float m_run = -INFINITY, l_run = 0.0f;
     const int64_t tend = p0 + slen < n_ctx ? p0 + slen : n_ctx;
-    const int64_t last = n_ctx - 1;
+    const uint32_t last = (uint32_t)(n_ctx - 1);
 
-    // cache rows of a tile in the score operand layout (lane: position n)
-    float kv[KS][8];
-    auto load_tile = [&](int64_t t0) {
-        const int64_t pos = t0 + n <= last ? t0 + n : last;
+    // the tile's cache rows in the score operand layout (lane: position n);
+    // two register sets: tile t computes while tile t+1 loads
+    bf16x8_t kh[KS], kl[KS], nh[KS], nl[KS];
+    auto load_tile = [&](uint32_t t0, bf16x8_t (&h)[KS], bf16x8_t (&lo)[KS]) {
+        const uint32_t pos = t0 + n <= last ? t0 + n : last;
+        const __bf16 *row = a.kc + (size_t)pos * (2 * D) + dlane;
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
-            const int d0 = dbase + 16 * ks + 8 * half;
-            load8(d0 < L ? a.latent + pos * L + d0 : a.krot + pos * P + (d0 - L), kv[ks]);
+            h[ks] = *(const bf16x8_t *)(row + 16 * ks);
+            lo[ks] = *(const bf16x8_t *)(row + D + 16 * ks);
         }
     };
-    load_tile(p0);
+    load_tile((uint32_t)p0, kh, kl);
 
     for (int64_t t0 = p0; t0 < tend; t0 += kMfmaTile) {
+        // ---- the next tile's loads overlap this whole tile
+        const bool more = t0 + kMfmaTile < tend;
+        if (more) load_tile((uint32_t)(t0 + kMfmaTile), nh, nl);
         // ---- partial scores over this wave's dims; latent dims to LDS
         f32x16_t sc;
 #pragma unroll
         for (int i = 0; i < 16; i++) sc[i] = 0.0f;
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
-            bf16x8_t kh, kl;
-            split8(kv[ks], kh, kl);
-            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, qh[ks], sc, 0, 0, 0);
-            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, ql[ks], sc, 0, 0, 0);
-            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kl, qh[ks], sc, 0, 0, 0);
-            const int d0 = dbase + 16 * ks + 8 * half;
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh[ks], qh[ks], sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh[ks], ql[ks], sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kl[ks], qh[ks], sc, 0, 0, 0);
+            const int d0 = dlane + 16 * ks;
             if (d0 < L) {
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
-                    sVh[(d0 + j) * kVPitch + n] = kh[j];
-                    sVl[(d0 + j) * kVPitch + n] = kl[j];
+                    sVh[(d0 + j) * kVPitch + n] = kh[ks][j];
+                    sVl[(d0 + j) * kVPitch + n] = kl[ks][j];
                 }
             }
         }
-        // ---- the next tile's loads overlap the softmax and context below
-        if (t0 + kMfmaTile < tend) load_tile(t0 + kMfmaTile);
         // ---- sum the four waves' partial tiles in wave order
         // C layout: register i holds position row (i/4)*8 + half*4 + i%4, column n
 #pragma unroll
         for (int i = 0; i < 16; i++) sS[w][(i >> 2) * 8 + half * 4 + (i & 3)][n] = sc[i];
         __syncthreads();
         float p[16];
+        const int64_t live = n_ctx - t0;  // rows pr < live are inside the context
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const int pr = (i >> 2) * 8 + half * 4 + (i & 3);
             float v = __fadd_rn(__fadd_rn(__fadd_rn(sS[0][pr][n], sS[1][pr][n]), sS[2][pr][n]), sS[3][pr][n]);
-            p[i] = t0 + pr < n_ctx ? __fmul_rn(v, a.scale) : -INFINITY;
+            p[i] = pr < live ? __fmul_rn(v, a.scale) : -INFINITY;
         }
         // ---- online softmax per column (lanes n and n + 32 share a column)
         float mt_ = p[0];
@@ -300,7 +304,16 @@ __global__ __launch_bounds__(256) void k_mla_mfma(MlaMfmaArgs a) {
         for (int i = 1; i < 16; i++) mt_ = fmaxf(mt_, p[i]);
         mt_ = fmaxf(mt_, __shfl_xor(mt_, 32, 64));
         const float m_new = fmaxf(m_run, mt_);  // finite: position t0 is live
-        const float alpha = __expf(m_run - m_new);
+        // the context only needs rescaling when a column's maximum moved
+        // (alpha is exactly 1 otherwise)
+        if (__any(m_new != m_run)) {
+            const float alpha = __expf(m_run - m_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) o[mt][i] *= alpha;
+        }
         float ls = 0.0f;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
@@ -308,12 +321,8 @@ __global__ __launch_bounds__(256) void k_mla_mfma(MlaMfmaArgs a) {
             ls += p[i];
         }
         ls += __shfl_xor(ls, 32, 64);
-        l_run = l_run * alpha + ls;
+        l_run += ls;
         m_run = m_new;
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-            for (int i = 0; i < 16; i++) o[mt][i] *= alpha;
         // ---- P as the B operand: lane (half, n) needs positions 16*ks + 8*half + [0, 8)
         bf16x8_t ph[2], pl[2];
 #pragma unroll
@@ -345,6 +354,13 @@ __global__ __launch_bounds__(256) void k_mla_mfma(MlaMfmaArgs a) {
             }
         }
         __syncthreads();  // sS and sV are rewritten by the next tile
+        if (more) {
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                kh[ks] = nh[ks];
+                kl[ks] = nl[ks];
+            }
+        }
     }
     // ---- slice partials: O^T register i is dim w*32*MT + 32*mt + (i/4)*8 + half*4 + i%4
     const int64_t RH = a.RH;
@@ -352,13 +368,29 @@ __global__ __launch_bounds__(256) void k_mla_mfma(MlaMfmaArgs a) {
         a.part_m[(int64_t)slice * RH + col] = m_run;
         a.part_l[(int64_t)slice * RH + col] = l_run;
     }
+    float *po = a.part_o + ((int64_t)slice * L + w * (32 * MT) + half * 4) * RH + col;
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int dim = w * (32 * MT) + 32 * mt + (i >> 2) * 8 + half * 4 + (i & 3);
-            a.part_o[((int64_t)slice * L + dim) * RH + col] = o[mt][i];
-        }
+        for (int i = 0; i < 16; i++)
+            po[(int64_t)(32 * mt + (i >> 2) * 8 + (i & 3)) * RH] = o[mt][i];
+}
+
+// The cache in the MFMA kernel's form: per position the bf16 hi parts of
+// [latent | k_rot] then the lo parts, x = hi + lo + O(2^-17 |x|).
+__global__ __launch_bounds__(256) void k_mla_cache_split(const float *__restrict__ latent,
+                                                         const float *__restrict__ krot, int L,
+                                                         int P, int64_t T,
+                                                         __bf16 *__restrict__ kc) {
+    const int D = L + P;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= T * D) return;
+    const int64_t pos = i / D;
+    const int d = (int)(i - pos * D);
+    const float x = d < L ? latent[pos * L + d] : krot[pos * P + (d - L)];
+    const __bf16 h = (__bf16)x;
+    kc[pos * 2 * D + d] = h;
+    kc[pos * 2 * D + D + d] = (__bf16)__fsub_rn(x, (float)h);
 }
 
 // Merges the slices: M = max m_j, Ls = sum l_j e^(m_j - M),
@@ -436,10 +468,11 @@ static int64_t mla_mfma_nslice(int64_t T) {
 }
 
 static bool mla_mfma_ok(int64_t H, int64_t L, int64_t P, int64_t T) {
-    return H % 32 == 0 && L % 128 == 0 && (L + P) % 64 == 0 && L % 16 == 0 &&
-           (L / 128 == 4 && (L + P) / 64 == 9) &&  // instantiated: DeepSeek-V3 MLA (512 + 64)
-           mla_mfma_nslice(T) <= kMlaMaxSlices;
+    // instantiated for the DeepSeek-V3 MLA shape: latent 512 + rope 64
+    return H % 32 == 0 && L == 512 && P == 64 && mla_mfma_nslice(T) <= kMlaMaxSlices;
 }
+
+bool mla_kc_ok(int64_t H, int64_t L, int64_t P, int64_t T) { return mla_mfma_ok(H, L, P, T); }
 
 static size_t mla_mfma_scratch_bytes(int64_t R, int64_t H, int64_t L, int64_t T) {
     const size_t ns = (size_t)mla_mfma_nslice(T), RH = (size_t)(R * H);
@@ -454,8 +487,58 @@ static size_t mla_split_scratch_bytes(int64_t R, int64_t H, int64_t L, int64_t T
 }
 
 size_t mla_scratch_bytes(int64_t R, int64_t H, int64_t L, int64_t P, int64_t T) {
-    return mla_mfma_ok(H, L, P, T) ? mla_mfma_scratch_bytes(R, H, L, T)
-                                : mla_split_scratch_bytes(R, H, L, T);
+    // the f32 entry also holds the split cache (T x (L+P) x 4 bytes)
+    return mla_mfma_ok(H, L, P, T)
+               ? mla_mfma_scratch_bytes(R, H, L, T) + (size_t)T * (L + P) * 4 + 256
+               : mla_split_scratch_bytes(R, H, L, T);
+}
+
+size_t mla_kc_scratch_bytes(int64_t R, int64_t H, int64_t L, int64_t T) {
+    return mla_mfma_scratch_bytes(R, H, L, T);
+}
+
+int32_t launch_mla_cache_split(ut_ctx *ctx, const float *latent, const float *krot, int64_t T,
+                               int64_t L, int64_t P, __bf16 *kc) {
+    if (T <= 0) return UT_OK;
+    const int64_t n = T * (L + P);
+    int tok = timing_begin(ctx, "mla_cache_split");
+    hipLaunchKernelGGL(k_mla_cache_split, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       ctx->stream, latent, krot, (int)L, (int)P, T, kc);
+    timing_end(ctx, tok);
+    return launch_check(ctx, "k_mla_cache_split");
+}
+
+int32_t launch_mla_attend_kc(ut_ctx *ctx, const float *qabs, const float *qrope, const __bf16 *kc,
+                             int64_t R, int64_t H, int64_t L, int64_t P, int64_t pos_base,
+                             float scale, float *clat, void *scratch) {
+    const int64_t T = pos_base + R;
+    if (!mla_mfma_ok(H, L, P, T) || ((uintptr_t)kc & 15) != 0) {
+        set_error(ctx, "mla: split-cache attention needs 32k heads, latent 512 + rope 64, a "
+                       "16-byte aligned cache and at most %d slices", kMlaMaxSlices);
+        return UT_ERR_SHAPE;
+    }
+    const int64_t RH = R * H, ns = mla_mfma_nslice(T);
+    MlaMfmaArgs a;
+    a.qabs = qabs; a.qrope = qrope; a.kc = kc;
+    a.H = (int)H; a.L = (int)L; a.P = (int)P; a.RH = (int)RH;
+    a.pos_base = pos_base;
+    a.scale = scale;
+    a.groups = (int)(RH / 32);
+    a.nslice = (int)ns;
+    a.part_m = (float *)scratch;
+    a.part_l = (float *)((char *)scratch + ((ns * RH * 4 + 255) & ~int64_t(255)));
+    a.part_o = (float *)((char *)a.part_l + ((ns * RH * 4 + 255) & ~int64_t(255)));
+    const int64_t nwg = (int64_t)a.groups * ((ns + 7) / 8 * 8);
+    int tok = timing_begin(ctx, "mla_mfma");
+    hipLaunchKernelGGL((k_mla_mfma<9, 4>), dim3((unsigned)nwg), dim3(256), 0, ctx->stream, a);
+    timing_end(ctx, tok);
+    UT_TRY(launch_check(ctx, "k_mla_mfma"));
+    tok = timing_begin(ctx, "mla_combine");
+    hipLaunchKernelGGL(k_mla_combine_mfma, dim3((unsigned)(RH / 32), (unsigned)(L / 8)),
+                       dim3(256), 0, ctx->stream, a.part_m, a.part_l, a.part_o, (int)RH, (int)H,
+                       (int)L, pos_base, clat);
+    timing_end(ctx, tok);
+    return launch_check(ctx, "k_mla_combine_mfma");
 }
 
 int32_t launch_mla_attend(ut_ctx *ctx, const float *qabs, const float *qrope, const float *latent,
@@ -463,28 +546,11 @@ int32_t launch_mla_attend(ut_ctx *ctx, const float *qabs, const float *qrope, co
                           int64_t pos_base, float scale, float *clat, void *scratch) {
     const int64_t T = pos_base + R;  // positions any row can see
     if (mla_mfma_ok(H, L, P, T)) {
-        const int64_t RH = R * H, ns = mla_mfma_nslice(T);
-        MlaMfmaArgs a;
-        a.qabs = qabs; a.qrope = qrope; a.latent = latent; a.krot = krot;
-        a.H = (int)H; a.L = (int)L; a.P = (int)P; a.RH = (int)RH;
-        a.pos_base = pos_base;
-        a.scale = scale;
-        a.groups = (int)(RH / 32);
-        a.nslice = (int)ns;
-        a.part_m = (float *)scratch;
-        a.part_l = (float *)((char *)scratch + ((ns * RH * 4 + 255) & ~int64_t(255)));
-        a.part_o = (float *)((char *)a.part_l + ((ns * RH * 4 + 255) & ~int64_t(255)));
-        const int64_t nwg = (int64_t)a.groups * ((ns + 7) / 8 * 8);
-        int tok = timing_begin(ctx, "mla_mfma");
-        hipLaunchKernelGGL((k_mla_mfma<9, 4>), dim3((unsigned)nwg), dim3(256), 0, ctx->stream, a);
-        timing_end(ctx, tok);
-        UT_TRY(launch_check(ctx, "k_mla_mfma"));
-        tok = timing_begin(ctx, "mla_combine");
-        hipLaunchKernelGGL(k_mla_combine_mfma, dim3((unsigned)(RH / 32), (unsigned)(L / 8)),
-                           dim3(256), 0, ctx->stream, a.part_m, a.part_l, a.part_o, (int)RH, (int)H,
-                           (int)L, pos_base, clat);
-        timing_end(ctx, tok);
-        return launch_check(ctx, "k_mla_combine_mfma");
+        // the f32 cache is split into the MFMA form in scratch first
+        __bf16 *kc = (__bf16 *)((char *)scratch + mla_mfma_scratch_bytes(R, H, L, T));
+        UT_TRY(launch_mla_cache_split(ctx, latent, krot, T, L, P, kc));
+        return launch_mla_attend_kc(ctx, qabs, qrope, kc, R, H, L, P, pos_base, scale, clat,
+                                    scratch);
     }
     const int nsplit = (int)((T + kMlaSlice - 1) / kMlaSlice);
     const size_t n = (size_t)R * H * nsplit;
@@ -538,4 +604,38 @@ extern "C" int32_t ut_mla_attend(ut_ctx *ctx, const float *qabs_dev, const float
     UT_TRY(scratch_acquire(ctx, plan, ptrs));
     return launch_mla_attend(ctx, qabs_dev, q_rope_dev, latent_dev, krot_dev, R, H, L, P, pos_base,
                              scale, clat_dev, ptrs[0]);
+}
+
+extern "C" int32_t ut_mla_cache_split(ut_ctx *ctx, const float *latent_dev, const float *krot_dev,
+                                      int64_t T, int64_t L, int64_t P, void *kc_dev) {
+    if (!ctx || !latent_dev || !krot_dev || !kc_dev || T < 0 || L <= 0 || P <= 0) {
+        set_error(ctx, "ut_mla_cache_split: bad argument");
+        return UT_ERR_ARG;
+    }
+    if (((uintptr_t)kc_dev & 15) != 0) {
+        set_error(ctx, "ut_mla_cache_split: kc must be 16-byte aligned");
+        return UT_ERR_ARG;
+    }
+    return launch_mla_cache_split(ctx, latent_dev, krot_dev, T, L, P, (__bf16 *)kc_dev);
+}
+
+extern "C" int32_t ut_mla_attend_split(ut_ctx *ctx, const float *qabs_dev, const float *q_rope_dev,
+                                       const void *kc_dev, int64_t R, int64_t H, int64_t L,
+                                       int64_t P, int64_t pos_base, float scale, float *clat_dev) {
+    if (!ctx || !qabs_dev || !q_rope_dev || !kc_dev || !clat_dev || R <= 0 || H <= 0 || L <= 0 ||
+        P <= 0 || pos_base < 0) {
+        set_error(ctx, "ut_mla_attend_split: bad argument");
+        return UT_ERR_ARG;
+    }
+    if (!mla_kc_ok(H, L, P, pos_base + R)) {
+        set_error(ctx, "ut_mla_attend_split: shape (H %lld, L %lld, P %lld, T %lld) not supported",
+                  (long long)H, (long long)L, (long long)P, (long long)(pos_base + R));
+        return UT_ERR_SHAPE;
+    }
+    ScratchPlan plan;
+    plan.add(mla_kc_scratch_bytes(R, H, L, pos_base + R));
+    std::vector<void *> ptrs;
+    UT_TRY(scratch_acquire(ctx, plan, ptrs));
+    return launch_mla_attend_kc(ctx, qabs_dev, q_rope_dev, (const __bf16 *)kc_dev, R, H, L, P,
+                                pos_base, scale, clat_dev, ptrs[0]);
 }

@@ -55,6 +55,7 @@ struct LayerW {
 struct KvCache {
     float *latent = nullptr;  // [cap, kv_lora]
     float *krot = nullptr;    // [cap, rope]
+    __bf16 *kc = nullptr;     // split bf16 form [cap][2][kv_lora + rope] (MFMA attention)
     int64_t len = 0;
 };
 
@@ -506,7 +507,7 @@ int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
         UT_TRY(matmul_digits(ctx, L.q_proj, x, xd, rows, w.q, heads * qh, 0));
     }
     UT_TRY(launch_kv_append(ctx, w.comp, rows, Lr, rope, L.kv_a_norm, c.rms_norm_eps, kv.latent,
-                            kv.krot, pos_base, m->rope_table));
+                            kv.krot, kv.kc, pos_base, m->rope_table));
     kv.len = pos_base + rows;
     UT_TRY(launch_absorb_q(ctx, L.kv_b, w.q, rows, heads, nope, rope, vh, w.qabs, w.qrope,
                            pos_base, m->rope_table));
@@ -514,9 +515,14 @@ int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
     // result does not depend on its group)
     for (int64_t r0 = 0; r0 < rows; r0 += kMlaRowsPerCall) {
         const int64_t rn = rows - r0 < kMlaRowsPerCall ? rows - r0 : kMlaRowsPerCall;
-        UT_TRY(launch_mla_attend(ctx, w.qabs + r0 * heads * Lr, w.qrope + r0 * heads * rope,
-                                 kv.latent, kv.krot, rn, heads, Lr, rope, pos_base + r0, scale,
-                                 w.clat + r0 * heads * Lr, w.mla));
+        if (kv.kc)
+            UT_TRY(launch_mla_attend_kc(ctx, w.qabs + r0 * heads * Lr, w.qrope + r0 * heads * rope,
+                                        kv.kc, rn, heads, Lr, rope, pos_base + r0, scale,
+                                        w.clat + r0 * heads * Lr, w.mla));
+        else
+            UT_TRY(launch_mla_attend(ctx, w.qabs + r0 * heads * Lr, w.qrope + r0 * heads * rope,
+                                     kv.latent, kv.krot, rn, heads, Lr, rope, pos_base + r0, scale,
+                                     w.clat + r0 * heads * Lr, w.mla));
     }
     UT_TRY(launch_absorb_v(ctx, L.kv_b, w.clat, rows, heads, nope, vh, w.ctxv));
     // x += o_proj(ctx) (the residual add of model.rs:478-480 in the epilogue)
@@ -990,9 +996,13 @@ int32_t ut_session_create(ut_model *m, int32_t path, ut_session **out) {
     }
     char *p = (char *)s->kv_alloc;
     s->kv.resize((size_t)c.num_hidden_layers);
+    // DeepSeek-V3-shaped attention keeps the cache in the MFMA kernel's
+    // split bf16 form (the same bytes as the f32 cache)
+    const bool split = mla_kc_ok(c.num_attention_heads, c.kv_lora_rank, c.qk_rope_head_dim, s->cap);
     auto carve = [&](KvCache &kv) {
         kv.latent = (float *)p;
         kv.krot = (float *)(p + (size_t)s->cap * c.kv_lora_rank * 4);
+        kv.kc = split ? (__bf16 *)p : nullptr;
         kv.len = 0;
         p += per;
     };

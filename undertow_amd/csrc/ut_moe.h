@@ -6,6 +6,7 @@
 namespace ut {
 
 constexpr int kGateUpRowsPerWG = 16;  // h rows per gate/up workgroup
+constexpr int kDownMaxSplit = 8;      // K splits of a one-slot MLP's down projection
 
 // Device arrays of per-expert pointers (indexed by expert id).
 struct ExpertPtrs {
@@ -52,7 +53,7 @@ struct MoeCall {
 
 struct ScratchLayout {
     size_t total = 0;
-    size_t count = 0, uniq = 0, choice = 0, xd = 0, h = 0, hmax = 0, hd = 0, d = 0;
+    size_t count = 0, uniq = 0, choice = 0, xd = 0, h = 0, hmax = 0, hd = 0, d = 0, dpart = 0;
     int xflags = 0, hflags = 0;
     int64_t ntiles = 0;
 };
@@ -65,7 +66,7 @@ struct ScratchLayout {
 __device__ inline void make_plan(const int32_t *ids, int M, int k, int E,
                           const uint8_t *const *__restrict__ gate_tbl, int extra_slot,
                           MoePlan plan, int32_t *__restrict__ err_flag) {
-    __shared__ int s_e[256], s_slot[256], s_uniq[257], s_U;
+    __shared__ int s_e[256], s_first[256];
     const int n = M * k, tid = threadIdx.x;
     if (tid < n) {
         const int e = ids[tid];
@@ -74,25 +75,34 @@ __device__ inline void make_plan(const int32_t *ids, int M, int k, int E,
         s_e[tid] = ok ? e : -1;
     }
     __syncthreads();
-    if (tid == 0) {
-        int U = 0;
-        for (int i = 0; i < n; i++) {
-            const int e = s_e[i];
-            int slot = -1;
-            if (e >= 0) {
-                for (int u = 0; u < U; u++)
-                    if (s_uniq[u] == e) { slot = u; break; }
-                if (slot < 0) { slot = U; s_uniq[U++] = e; }
-            }
-            s_slot[i] = slot;
+    // entry i opens a slot when its expert does not appear before it
+    int e = -1, j0 = -1;
+    if (tid < n) {
+        e = s_e[tid];
+        if (e >= 0) {
+            j0 = tid;
+            for (int j = 0; j < tid; j++)
+                if (s_e[j] == e) { j0 = j; break; }
         }
-        if (extra_slot >= 0) s_uniq[U++] = extra_slot;  // a dense MLP run as one more slot
-        s_U = U;
+        s_first[tid] = e >= 0 && j0 == tid;
     }
     __syncthreads();
-    if (tid < n) plan.choice_slot[tid] = s_slot[tid];
-    if (tid < s_U) plan.uniq[tid] = s_uniq[tid];
-    if (tid == 0) *plan.count = s_U;
+    if (tid < n) {
+        // slot = number of slot openings before the expert's first entry
+        int slot = -1;
+        if (e >= 0) {
+            slot = 0;
+            for (int j = 0; j < j0; j++) slot += s_first[j];
+            if (j0 == tid) plan.uniq[slot] = e;
+        }
+        plan.choice_slot[tid] = slot;
+    }
+    if (tid == 0) {
+        int U = 0;
+        for (int j = 0; j < n; j++) U += s_first[j];
+        if (extra_slot >= 0) plan.uniq[U++] = extra_slot;  // a dense MLP run as one more slot
+        *plan.count = U;
+    }
 }
 
 inline int64_t moe_slots(int M, int64_t k, int64_t E, int extra) {

@@ -18,6 +18,14 @@
 #include "ut_gemv_core.h"
 #include "ut_moe.h"
 
+// Weight steps in flight per lane in the expert kernels (see gemv_core).
+#ifndef UT_GATE_UP_DEPTH
+#define UT_GATE_UP_DEPTH 2
+#endif
+#ifndef UT_DOWN_DEPTH
+#define UT_DOWN_DEPTH 2
+#endif
+
 namespace ut {
 
 // ------------------------------------------------------------- router ---
@@ -28,10 +36,12 @@ __device__ __forceinline__ bool ranks_before(float a, int ia, float b, int ib) {
 }
 
 // Routes one row with the whole workgroup.  sm: 2*E + n_group floats.
-__device__ void route_row(const float *__restrict__ lg, const float *__restrict__ bias, int E,
-                          int k, int n_group, int topk_group, int norm, float scale,
-                          int32_t *__restrict__ ids, float *__restrict__ weights, float *sm,
-                          int *s_ids, int *s_group_ok) {
+__device__ __forceinline__ void route_row(const float *__restrict__ lg,
+                                          const float *__restrict__ bias, int E, int k,
+                                          int n_group, int topk_group, int norm, float scale,
+                                          int32_t *__restrict__ ids, float *__restrict__ weights,
+                                          float *sm, int *s_ids, int *s_group_ok) {
+    __shared__ float s_w[64];  // sigmoid of the chosen, in choice order
     float *sc = sm;           // sigmoid scores
     float *corr = sm + E;     // corrected (selection) scores, then masked
     float *gsc = sm + 2 * E;  // group scores
@@ -89,22 +99,21 @@ __device__ void route_row(const float *__restrict__ lg, const float *__restrict_
         int rank = 0;
 #pragma unroll 16
         for (int j = 0; j < E; j++) rank += ranks_before(corr[j], j, v, e);
-        if (rank < keff) s_ids[rank] = e;
+        if (rank < keff) {
+            s_ids[rank] = e;
+            s_w[rank] = sc[e];
+        }
     }
     __syncthreads();
     // weights = sigmoid of the chosen, normalised by their sequential sum
     // (+1e-20) in choice order, then scaled
-    __shared__ float s_denom;
-    if (tid == 0) {
-        float denom = 0.0f;
-        for (int j = 0; j < keff; j++) denom = denom + sc[s_ids[j]];
-        s_denom = denom + 1e-20f;
-    }
-    __syncthreads();
     if (tid < k) {
         if (tid < keff) {
-            const float w = sc[s_ids[tid]];
-            const float v = norm ? w / s_denom : w;
+            float denom = 0.0f;
+            for (int j = 0; j < keff; j++) denom = denom + s_w[j];
+            denom = denom + 1e-20f;
+            const float w = s_w[tid];
+            const float v = norm ? w / denom : w;
             ids[tid] = s_ids[tid];
             weights[tid] = __fmul_rn(v, scale);
         } else {  // k > E: no expert (contributes nothing)
@@ -144,7 +153,9 @@ __global__ __launch_bounds__(256) void k_route_plan(const float *__restrict__ lo
     for (int row = 0; row < M; row++) {
         route_row(logits + (int64_t)row * E, bias, E, k, n_group, topk_group, norm, scale,
                   ids + (int64_t)row * k, weights + (int64_t)row * k, sm, s_ids, s_group_ok);
-        if (threadIdx.x < k) s_all[row * k + threadIdx.x] = ids[(int64_t)row * k + threadIdx.x];
+        // the chosen ids from LDS (route_row ends with a barrier)
+        if (threadIdx.x < k) s_all[row * k + threadIdx.x] = threadIdx.x < (k < E ? k : E) ? s_ids[threadIdx.x] : -1;
+        __syncthreads();
     }
     __syncthreads();
     make_plan(s_all, M, k, E, gate_tbl, -1, plan, err_flag);
@@ -215,7 +226,7 @@ __device__ __forceinline__ void gate_up_body(const GateUpArgs &a, int u, int til
     const int64_t oc = o < a.I ? o : a.I - 1;
     const uint8_t *rows[2] = {gw + oc * a.row_bytes, uw + oc * a.row_bytes};
     CoreOut<FMT, M, 2> res;
-    gemv_core<FMT, M, 2>(rows, a.H, a.x, lds, res);
+    gemv_core<FMT, M, 2, UT_GATE_UP_DEPTH>(rows, a.H, a.x, lds, res);
 #pragma unroll
     for (int m = 0; m < M; m++) {
         // f32: the gate value lives on sub-lane m, the up value on 4 + m
@@ -226,8 +237,8 @@ __device__ __forceinline__ void gate_up_body(const GateUpArgs &a, int u, int til
         }
         if (s == m && o < a.I) {
             if constexpr (FMT != UT_FMT_F32) {
-                gv = int_total_to_f32(res.S[0][m], a.exps[m], gsc[o]);
-                uv = int_total_to_f32(res.S[1][m], a.exps[m], usc[o]);
+                gv = int_total_to_f32(res.S[0][m], a.exps[m], ld_global_f32(gsc + o));
+                uv = int_total_to_f32(res.S[1][m], a.exps[m], ld_global_f32(usc + o));
             }
             // silu(g) * u (undertow-quant/src/lib.rs:121; model.rs:241-247)
             float sg = gv / (1.0f + expf(-gv));
@@ -268,7 +279,27 @@ struct DownArgs {
     const uint32_t *hmax_parts;  // [slots*M][nparts] max|h| bits from the gate/up kernel
     int nparts;
     float *d;                 // [slots][M][H]
+    // split-K over blockIdx.z (ks > 1, one-slot MLPs): columns
+    // [z*kslice, (z+1)*kslice), exact partial totals to part[z][slot][M][H]
+    // (f32 weights: the partial's bits), finished by k_moe_down_finish
+    int ks = 1;
+    int64_t kslice = 0;
+    int64_t *part = nullptr;
 };
+
+// The digitisation shift of h row (u, m): 22 - E with max|h| < 2^E, from the
+// gate/up workgroups' partial maxima (INT32_MIN: non-finite row).  Whole
+// workgroup; red4: 4 words of LDS.
+__device__ __forceinline__ int32_t h_shift(const uint32_t *hmax_parts, int nparts, int64_t row,
+                                           uint32_t *red4) {
+    uint32_t mx = 0;
+    for (int i = threadIdx.x; i < nparts; i += kGemvThreads)
+        mx = max(mx, hmax_parts[row * nparts + i]);
+    mx = block_reduce(mx, [](uint32_t p, uint32_t q) { return p > q ? p : q; }, red4);
+    int E = 0;
+    if (mx < 0x7f800000u && mx != 0) (void)frexpf(__uint_as_float(mx), &E);
+    return mx >= 0x7f800000u ? INT32_MIN : 22 - E;
+}
 
 // Rows per lane: 4 at M <= 2 (more activation reuse), 2 above (registers).
 template <int M> constexpr int down_rows() { return M <= 2 ? 4 : 2; }
@@ -295,27 +326,30 @@ __device__ __forceinline__ void down_body(const DownArgs &a, int u, int tile, ui
     if constexpr (FMT != UT_FMT_F32) {
         // the row exponent of h from the gate/up workgroups' partial maxima
         __shared__ uint32_t red4[4];
-        __shared__ int32_t s_sh[4];
-        for (int m = 0; m < M; m++) {
-            uint32_t mx = 0;
-            for (int i = tid; i < a.nparts; i += kGemvThreads)
-                mx = max(mx, a.hmax_parts[((int64_t)u * M + m) * a.nparts + i]);
-            mx = block_reduce(mx, [](uint32_t p, uint32_t q) { return p > q ? p : q; }, red4);
-            if (tid == 0) {
-                int E = 0;
-                if (mx < 0x7f800000u && mx != 0) (void)frexpf(__uint_as_float(mx), &E);
-                s_sh[m] = mx >= 0x7f800000u ? INT32_MIN : 22 - E;
-            }
-        }
-        __syncthreads();
 #pragma unroll
         for (int m = 0; m < M; m++) {
-            xs.sh[m] = s_sh[m];
-            exl[m] = s_sh[m] == INT32_MIN ? INT32_MIN : -s_sh[m];
+            const int32_t sh = h_shift(a.hmax_parts, a.nparts, (int64_t)u * M + m, red4);
+            xs.sh[m] = sh;
+            exl[m] = sh == INT32_MIN ? INT32_MIN : -sh;
         }
     }
     CoreOut<FMT, M, R> res;
-    gemv_core<FMT, M, R>(rows, a.I, xs, lds, res);
+    if (a.ks > 1) {
+        const int64_t kb = (int64_t)blockIdx.z * a.kslice;
+        gemv_core<FMT, M, R, UT_DOWN_DEPTH>(rows, a.I, xs, lds, res, kb, kb + a.kslice);
+        const int64_t slots = gridDim.y;
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                const int64_t o = row0 + r;
+                if (s == 4 * r + m && o < a.H)
+                    a.part[(((int64_t)blockIdx.z * slots + u) * M + m) * a.H + o] =
+                        FMT == UT_FMT_F32 ? (int64_t)__float_as_uint(res.F[r][m]) : res.S[r][m];
+            }
+        return;
+    }
+    gemv_core<FMT, M, R, UT_DOWN_DEPTH>(rows, a.I, xs, lds, res);
 #pragma unroll
     for (int r = 0; r < R; r++)
 #pragma unroll
@@ -332,6 +366,36 @@ template <int FMT, int M>
 __global__ __launch_bounds__(kGemvThreads) void k_moe_down(DownArgs a) {
     __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
     down_body<FMT, M>(a, blockIdx.y, blockIdx.x, lds);
+}
+
+// Sums the split-K partials of down (slot u, row m) in z order (integers
+// exactly, f32 in that fixed order) and applies the row epilogue into d.
+// Grid (H / 256, slots * M).
+template <int FMT>
+__global__ __launch_bounds__(kGemvThreads) void k_moe_down_finish(DownArgs a, int M) {
+    __shared__ uint32_t red4[4];
+    const int u = blockIdx.y / M, m = blockIdx.y - u * M;
+    if (u >= *a.count) return;
+    int32_t exl = 0;
+    if constexpr (FMT != UT_FMT_F32) {
+        const int32_t sh = h_shift(a.hmax_parts, a.nparts, (int64_t)u * M + m, red4);
+        exl = sh == INT32_MIN ? INT32_MIN : -sh;
+    }
+    const int64_t o = (int64_t)blockIdx.x * kGemvThreads + threadIdx.x;
+    if (o >= a.H) return;
+    const int64_t slots = gridDim.y / M;
+    const int64_t zs = slots * M * a.H;
+    const int64_t i = ((int64_t)u * M + m) * a.H + o;
+    float v;
+    if constexpr (FMT == UT_FMT_F32) {
+        v = __uint_as_float((uint32_t)a.part[i]);
+        for (int z = 1; z < a.ks; z++) v = __fadd_rn(v, __uint_as_float((uint32_t)a.part[z * zs + i]));
+    } else {
+        int64_t S = a.part[i];
+        for (int z = 1; z < a.ks; z++) S += a.part[z * zs + i];
+        v = int_total_to_f32(S, exl, ld_global_f32(a.tbl.down_s[a.uniq[u]] + o));
+    }
+    a.d[i] = v;
 }
 
 template <int FA, int FB, int M>
@@ -394,6 +458,7 @@ ScratchLayout moe_layout(int64_t M, int64_t k, int64_t slots, int64_t H, int64_t
     L.hmax = take((size_t)slots * M * ntiles * 4);
     L.hd = take(fmt == UT_FMT_F32 ? 0 : xdigits_bytes(slots * M, I, hflags));
     L.d = take((size_t)slots * M * H * 4);
+    L.dpart = take(slots == 1 ? (size_t)kDownMaxSplit * M * H * 8 : 0);
     L.xflags = xflags;
     L.hflags = hflags;
     L.ntiles = ntiles;
@@ -422,8 +487,13 @@ static void launch_down(ut_ctx *ctx, const DownArgs &a, int64_t slots, const Dow
     constexpr int DR = 16 * down_rows<M>();
     const unsigned gx = (unsigned)((a.H + DR - 1) / DR);
     if (!b) {
-        hipLaunchKernelGGL((k_moe_down<FA, M>), dim3(gx, (unsigned)slots), dim3(kGemvThreads), 0,
-                           ctx->stream, a);
+        hipLaunchKernelGGL((k_moe_down<FA, M>), dim3(gx, (unsigned)slots, (unsigned)a.ks),
+                           dim3(kGemvThreads), 0, ctx->stream, a);
+        if (a.ks > 1)
+            hipLaunchKernelGGL((k_moe_down_finish<FA>),
+                               dim3((unsigned)((a.H + kGemvThreads - 1) / kGemvThreads),
+                                    (unsigned)(slots * M)),
+                               dim3(kGemvThreads), 0, ctx->stream, a, M);
         return;
     }
     if constexpr (FA != UT_FMT_F32) {
@@ -528,6 +598,22 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
         a.hmax_parts = hmax;
         a.nparts = (int)L.ntiles;
         a.d = d;
+        // a one-slot MLP (dense FFN, lone shared expert) has too few down
+        // tiles to fill the chip: split its K range (M-independent choice)
+        if (slots == 1 && !c.shared) {
+            constexpr int64_t step = FmtTraits<FMT>::kStepCols;
+            const int64_t tiles64 = (c.H + 63) / 64;
+            int64_t ks = tiles64 >= 256 ? 1 : (512 + tiles64 - 1) / tiles64;
+            if (ks > kDownMaxSplit) ks = kDownMaxSplit;
+            if (ks > c.I / (2 * step)) ks = c.I / (2 * step);
+            if (ks > 1) {
+                int64_t kslice = (c.I + ks - 1) / ks;
+                kslice = (kslice + step - 1) / step * step;
+                a.ks = (int)((c.I + kslice - 1) / kslice);
+                a.kslice = kslice;
+                a.part = (int64_t *)(base + L.dpart);
+            }
+        }
         if (c.shared) {
             const MoeCall &sc = *c.shared;
             db.tbl = sc.tbl;

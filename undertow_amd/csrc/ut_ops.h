@@ -28,10 +28,12 @@ int32_t launch_absorb_q(ut_ctx *ctx, const ut_qtensor *kv_b, const float *q, int
                         int64_t heads, int64_t nope, int64_t rope, int64_t vh, float *qabs,
                         float *qrope, int64_t pos_base, const float2 *table);
 // Cache append (attention.rs:168-186) for rows at positions pos_base..:
-// latent = rmsnorm(comp[:L], w), krot = rope_interleave(comp[L:L+P], pos).
+// latent = rmsnorm(comp[:L], w), krot = rope_interleave(comp[L:L+P], pos),
+// stored as f32 (latent, krot) or, with kc, in the MFMA attention's split
+// bf16 form (per position: hi parts of [latent | krot], then lo parts).
 int32_t launch_kv_append(ut_ctx *ctx, const float *comp, int64_t rows, int64_t L, int64_t P,
-                         const float *w, float eps, float *latent, float *krot, int64_t pos_base,
-                         const float2 *table);
+                         const float *w, float eps, float *latent, float *krot, __bf16 *kc,
+                         int64_t pos_base, const float2 *table);
 // Absorbed value (attention.rs:235, QTensor::matvec_rows): for each (s, h)
 //   ctx[s, h*vh + j] = (sum_i clat[s,h,i] * W[h*kvh+nope+j, i]) * scale.
 int32_t launch_absorb_v(ut_ctx *ctx, const ut_qtensor *kv_b, const float *clat, int64_t rows,

@@ -15,13 +15,16 @@ missing library raises ``RuntimeError``.
 from __future__ import annotations
 
 import ctypes as C
+import os
 from pathlib import Path
 from typing import Optional
 
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-LIB_PATH = HERE / "lib" / "libundertow_hip.so"
+# UNDERTOW_HIP_LIB selects another build of the library (e.g. a variant
+# compiled with different pipeline depths); the in-tree build by default.
+LIB_PATH = Path(os.environ.get("UNDERTOW_HIP_LIB", str(HERE / "lib" / "libundertow_hip.so")))
 
 F32, INT8, INT4, INFER = 0, 1, 2, -1
 
@@ -83,6 +86,8 @@ _SIGS = [
     ("ut_moe_experts", _i32, [_vp, _vp, _vp, _vp, _i64, _i32, _vp, _vp]),
     ("ut_argmax_rows", _i32, [_vp, _vp, _i64, _i64, _vp]),
     ("ut_mla_attend", _i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _vp]),
+    ("ut_mla_cache_split", _i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    ("ut_mla_attend_split", _i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _vp]),
     ("ut_model_create", _i32, [_vp, _vp, C.POINTER(_vp)]),
     ("ut_model_set_tensor", _i32, [_vp, C.c_char_p, _i32, _vp, _i64, _vp, _i64, _i64]),
     ("ut_model_finalize", _i32, [_vp]),
@@ -313,6 +318,30 @@ def mla_attend(ctx: Context, qabs, q_rope, latent, krot, pos_base: int, scale: f
         raise ShapeError(f"mla_attend: out must be a contiguous float32 [{R}, {H}, {L}] tensor")
     ctx.check(lib().ut_mla_attend(ctx.handle, _ptr(qabs), _ptr(q_rope), _ptr(latent), _ptr(krot),
                                   R, H, L, P, pos_base, scale, _ptr(out)))
+    return out
+
+
+def mla_cache_split(ctx: Context, latent, krot):
+    """The cache [T, L] + [T, P] (f32) in the split bf16 form of the MFMA
+    attention kernel: an int16 tensor [T, 2, L + P] (hi parts, then lo)."""
+    torch = _torch()
+    T, L = latent.shape
+    P = krot.shape[1]
+    kc = torch.empty((T, 2, L + P), dtype=torch.int16, device=latent.device)
+    ctx.check(lib().ut_mla_cache_split(ctx.handle, _ptr(latent), _ptr(krot), T, L, P, _ptr(kc)))
+    return kc
+
+
+def mla_attend_split(ctx: Context, qabs, q_rope, kc, pos_base: int, scale: float, out=None):
+    torch = _torch()
+    R, H, L = qabs.shape
+    P = q_rope.shape[2]
+    if kc.shape[-1] != L + P:
+        raise ShapeError(f"mla_attend_split: cache width {kc.shape[-1]} != {L} + {P}")
+    if out is None:
+        out = torch.empty((R, H, L), dtype=torch.float32, device=qabs.device)
+    ctx.check(lib().ut_mla_attend_split(ctx.handle, _ptr(qabs), _ptr(q_rope), _ptr(kc), R, H, L, P,
+                                        pos_base, scale, _ptr(out)))
     return out
 
 
