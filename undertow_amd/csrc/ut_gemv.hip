@@ -8,7 +8,7 @@
 
 // Weight steps in flight per lane in the plain GEMV (see gemv_core).
 #ifndef UT_GEMV_DEPTH
-#define UT_GEMV_DEPTH 2
+#define UT_GEMV_DEPTH 1
 #endif
 
 namespace ut {
@@ -382,14 +382,17 @@ int32_t launch_rmsnorm_digitize(ut_ctx *ctx, const float *x, int64_t ldx, int64_
 }
 
 // --------------------------------------------------------- fast GEMV ---
+// Rows [0, O1) come from weight w, rows [O1, O) from w2 (same format, K and
+// row bytes), written to out / out2: two projections of one activation
+// (e.g. kv_a and q_a) in one launch.
 struct PlainArgs {
-    const uint8_t *w;
-    const float *scales;
-    int64_t O, K, row_bytes;
+    const uint8_t *w, *w2;
+    const float *scales, *scales2;
+    int64_t O, O1, K, row_bytes;
     XSrc x;
     const int32_t *exps;
-    float *out;
-    int64_t ldo;
+    float *out, *out2;
+    int64_t ldo, ldo2;
     int accumulate;
     // split-K over blockIdx.z (ks > 1): columns [z*kslice, (z+1)*kslice),
     // partial totals to part[(z*M + m)*O + row]; k_gemv_splitk_sum finishes
@@ -397,6 +400,16 @@ struct PlainArgs {
     int64_t kslice;
     int64_t *part;
 };
+
+__device__ __forceinline__ const uint8_t *plain_row(const PlainArgs &a, int64_t row) {
+    return row < a.O1 ? a.w + row * a.row_bytes : a.w2 + (row - a.O1) * a.row_bytes;
+}
+__device__ __forceinline__ float plain_scale(const PlainArgs &a, int64_t row) {
+    return ld_global_f32(row < a.O1 ? a.scales + row : a.scales2 + (row - a.O1));
+}
+__device__ __forceinline__ float *plain_out(const PlainArgs &a, int64_t m, int64_t row) {
+    return row < a.O1 ? a.out + m * a.ldo + row : a.out2 + m * a.ldo2 + (row - a.O1);
+}
 
 // 16*R output rows per workgroup (R = 4 rows per lane at M <= 2, else 2):
 // wave w, row group g, slot r -> row blockIdx.x*16R + w*4R + g*R + r.
@@ -410,10 +423,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
     const int64_t row0 = (int64_t)blockIdx.x * (16 * R) + wave * (4 * R) + g * R;
     const uint8_t *rows[R];
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-        int64_t row = row0 + r < a.O ? row0 + r : a.O - 1;
-        rows[r] = a.w + row * a.row_bytes;
-    }
+    for (int r = 0; r < R; r++) rows[r] = plain_row(a, row0 + r < a.O ? row0 + r : a.O - 1);
     CoreOut<FMT, M, R> res;
     if (a.ks > 1) {
         const int64_t kb = (int64_t)blockIdx.z * a.kslice;
@@ -436,39 +446,45 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
         for (int m = 0; m < M; m++) {
             const int64_t row = row0 + r;
             if (s == 4 * r + m && row < a.O) {
-                float v = core_value<FMT, M, R>(res, r, m, a.exps, a.scales, row);
-                float *o = a.out + m * a.ldo + row;
+                const float v = FMT == UT_FMT_F32
+                                    ? res.F[r][m]
+                                    : int_total_to_f32(res.S[r][m], a.exps[m], plain_scale(a, row));
+                float *o = plain_out(a, m, row);
                 *o = a.accumulate ? __fadd_rn(*o, v) : v;
             }
         }
 }
 
-// Sums the split-K partials of (m, row) in z order (integers exactly, f32
-// in that fixed order) and applies the row epilogue.
+// The value of (m, row) from split-K partials [ks][M][O]: summed in z order
+// (integers exactly, f32 in that fixed order) with the row epilogue.
 template <int FMT>
-__global__ __launch_bounds__(256) void k_gemv_splitk_sum(const int64_t *__restrict__ part, int ks,
-                                                         int64_t O, int M,
-                                                         const int32_t *__restrict__ exps,
-                                                         const float *__restrict__ scales,
-                                                         float *__restrict__ out, int64_t ldo,
-                                                         int accumulate) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= O * M) return;
-    const int64_t m = i / O, row = i - m * O;
-    const int64_t zs = (int64_t)M * O;
-    float v;
+__device__ __forceinline__ float splitk_value(const int64_t *__restrict__ part, int ks, int64_t O,
+                                              int M, int64_t m, int64_t row, int32_t exp,
+                                              float scale) {
+    const int64_t zs = (int64_t)M * O, i = m * O + row;
     if constexpr (FMT == UT_FMT_F32) {
-        v = __uint_as_float((uint32_t)part[i]);
+        float v = __uint_as_float((uint32_t)part[i]);
 #pragma unroll 16
         for (int z = 1; z < ks; z++) v = __fadd_rn(v, __uint_as_float((uint32_t)part[z * zs + i]));
+        return v;
     } else {
         int64_t S = part[i];
 #pragma unroll 16
         for (int z = 1; z < ks; z++) S += part[z * zs + i];
-        v = int_total_to_f32(S, exps[m], scales[row]);
+        return int_total_to_f32(S, exp, scale);
     }
-    float *o = out + m * ldo + row;
-    *o = accumulate ? __fadd_rn(*o, v) : v;
+}
+
+template <int FMT>
+__global__ __launch_bounds__(256) void k_gemv_splitk_sum(PlainArgs a, int M) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= a.O * M) return;
+    const int64_t m = i / a.O, row = i - m * a.O;
+    const float v = splitk_value<FMT>(a.part, a.ks, a.O, M, m, row,
+                                      FMT == UT_FMT_F32 ? 0 : a.exps[m],
+                                      FMT == UT_FMT_F32 ? 0.0f : plain_scale(a, row));
+    float *o = plain_out(a, m, row);
+    *o = a.accumulate ? __fadd_rn(*o, v) : v;
 }
 
 // ------------------------------------------------------ generic GEMV ---
@@ -523,6 +539,9 @@ __global__ __launch_bounds__(64) void k_gemv_generic(int32_t fmt, const uint8_t 
 static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 // Whether the fast kernel takes this weight (16-byte aligned rows).
+static bool fast_ok(const ut_qtensor *w);
+bool gemv_fast_ok(const ut_qtensor *w) { return fast_ok(w); }
+
 static bool fast_ok(const ut_qtensor *w) {
     if (!aligned16(w->payload)) return false;
     if (w->fmt == UT_FMT_INT4) return w->in_dim % 32 == 0;
@@ -561,15 +580,20 @@ static void splitk_plan(int32_t fmt, int64_t O, int64_t K, int *ks_out, int64_t 
 
 template <int FMT>
 static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrows) {
-    const ut_qtensor *w = ga.w;
+    const ut_qtensor *w = ga.w, *w2 = ga.w2;
     PlainArgs a;
     a.w = (const uint8_t *)w->payload;
     a.scales = w->scales;
-    a.O = w->out_dim;
+    a.O1 = w->out_dim;
+    a.w2 = w2 ? (const uint8_t *)w2->payload : a.w;
+    a.scales2 = w2 ? w2->scales : a.scales;
+    a.O = w->out_dim + (w2 ? w2->out_dim : 0);
     a.K = w->in_dim;
     a.row_bytes = w->row_bytes;
     a.out = ga.out + m0 * ga.ldo;
     a.ldo = ga.ldo;
+    a.out2 = w2 ? ga.out2 + m0 * ga.ldo2 : a.out;
+    a.ldo2 = w2 ? ga.ldo2 : a.ldo;
     a.accumulate = ga.accumulate;
     if constexpr (FMT == UT_FMT_F32) {
         a.x.xf = ga.xf + m0 * w->in_dim;
@@ -587,11 +611,11 @@ static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrow
         a.x.ldx = 0;
         a.exps = ga.xd.exps + m0;
     }
-    splitk_plan(FMT, w->out_dim, w->in_dim, &a.ks, &a.kslice);
+    splitk_plan(FMT, a.O, w->in_dim, &a.ks, &a.kslice);
     a.part = nullptr;
     if (a.ks > 1) UT_TRY(splitk_buffer(ctx, &a.part));
     const int rows_per_wg = 16 * (mrows <= 2 ? 4 : 2);
-    dim3 grid((unsigned)((w->out_dim + rows_per_wg - 1) / rows_per_wg), 1, (unsigned)a.ks);
+    dim3 grid((unsigned)((a.O + rows_per_wg - 1) / rows_per_wg), 1, (unsigned)a.ks);
     const char *name = FMT == UT_FMT_INT4 ? "gemv_int4" : FMT == UT_FMT_INT8 ? "gemv_int8" : "gemv_f32";
     int tok = timing_begin(ctx, name);
     switch (mrows) {
@@ -602,10 +626,16 @@ static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrow
     }
     if (a.ks > 1) {
         UT_TRY(launch_check(ctx, name));
-        const int64_t n = w->out_dim * mrows;
-        hipLaunchKernelGGL(k_gemv_splitk_sum<FMT>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
-                           ctx->stream, a.part, a.ks, w->out_dim, mrows, a.exps, a.scales, a.out,
-                           a.ldo, a.accumulate);
+        if (ga.defer) {
+            // the consumer sums the partials (only one chunk of rows)
+            ga.defer->part = a.part;
+            ga.defer->ks = a.ks;
+            ga.defer->O = a.O;
+        } else {
+            const int64_t n = a.O * mrows;
+            hipLaunchKernelGGL(k_gemv_splitk_sum<FMT>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                               ctx->stream, a, mrows);
+        }
     }
     timing_end(ctx, tok);
     return launch_check(ctx, name);
@@ -613,7 +643,18 @@ static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrow
 
 int32_t gemv(ut_ctx *ctx, const GemvArgs &ga) {
     const ut_qtensor *w = ga.w;
+    if (ga.defer) ga.defer->ks = 1;
     if (ga.M <= 0) return UT_OK;
+    if (ga.w2 && (ga.w2->fmt != w->fmt || ga.w2->in_dim != w->in_dim ||
+                  ga.w2->row_bytes != w->row_bytes || !fast_ok(ga.w2) || !fast_ok(w) ||
+                  (w->fmt == UT_FMT_F32 && !aligned16(ga.xf)))) {
+        set_error(ctx, "gemv: the two weights must share format, K and row layout");
+        return UT_ERR_ARG;
+    }
+    if (ga.defer && ga.M > 4) {
+        set_error(ctx, "gemv: deferred split-K sums take at most 4 rows");
+        return UT_ERR_ARG;
+    }
     if (fast_ok(w) && (w->fmt == UT_FMT_F32 ? aligned16(ga.xf) && (w->in_dim % 4 == 0) : true)) {
         for (int64_t m0 = 0; m0 < ga.M; m0 += 4) {
             int mrows = (int)((ga.M - m0) < 4 ? (ga.M - m0) : 4);

@@ -111,6 +111,18 @@ template <> __device__ __forceinline__ uint4 ld_global<uint4>(const void *p) {
     const ut_u32x4 v = *(const __attribute__((address_space(1))) ut_u32x4 *)p;
     return make_uint4(v.x, v.y, v.z, v.w);
 }
+// Streamed weights (read once per pass): non-temporal loads.
+#ifndef UT_WEIGHT_NT
+#define UT_WEIGHT_NT 1
+#endif
+__device__ __forceinline__ uint4 ld_weights(const void *p) {
+#if UT_WEIGHT_NT
+    const ut_u32x4 v = __builtin_nontemporal_load((const __attribute__((address_space(1))) ut_u32x4 *)p);
+#else
+    const ut_u32x4 v = *(const __attribute__((address_space(1))) ut_u32x4 *)p;
+#endif
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
 __device__ __forceinline__ float ld_global_f32(const float *p) {
     return *(const __attribute__((address_space(1))) float *)p;
 }
@@ -168,7 +180,7 @@ __device__ __forceinline__ void gemv_core(const uint8_t *const rows[R], int64_t 
         if (col < K) {
             const int64_t boff = col * T::kBytesPerCol2 / 2;
 #pragma unroll
-            for (int r = 0; r < R; r++) w[r] = ld_global<uint4>(rows[r] + boff);
+            for (int r = 0; r < R; r++) w[r] = ld_weights(rows[r] + boff);
         }
     };
     auto stage = [&](int64_t kc, int kcn) {

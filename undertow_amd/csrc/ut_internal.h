@@ -177,6 +177,15 @@ int xdigit_flags_for(int32_t fmt, int64_t K);
 // ---------------------------------------------------------- GEMV core ---
 // out[m, o] (row stride ldo) for one quantized matrix, all rows o < O.
 // x is given digitised (int formats) or as f32 (fmt F32).
+// Split-K partials handed to the consumer instead of a sum launch: ks > 1
+// means part[z][M][O] holds int64 totals (f32 weights: the float's bits)
+// that the consumer sums in z order; ks == 1 means out was written.
+struct SplitKPartials {
+    int64_t *part = nullptr;
+    int ks = 1;
+    int64_t O = 0;
+};
+
 struct GemvArgs {
     const ut_qtensor *w = nullptr;
     const float *xf = nullptr;  // f32 activations [M, K] (F32 weights)
@@ -185,8 +194,16 @@ struct GemvArgs {
     float *out = nullptr;
     int64_t ldo = 0;
     int accumulate = 0;         // out += result instead of out = result
+    // optional second weight (same format, K and row bytes) -> out2[M, ldo2]
+    const ut_qtensor *w2 = nullptr;
+    float *out2 = nullptr;
+    int64_t ldo2 = 0;
+    // optional: leave split-K partials to the consumer (M <= 4, fast path)
+    SplitKPartials *defer = nullptr;
 };
 int32_t gemv(ut_ctx *ctx, const GemvArgs &a);
+// Whether the fast (digit / vector) GEMV takes this weight.
+bool gemv_fast_ok(const ut_qtensor *w);
 
 // out[M, ldo] (+)= x[M, K] * w^T with x f32 on device: digitises x into
 // digit_scratch (matmul_digit_bytes(M, K) bytes) when w is quantized.

@@ -443,11 +443,27 @@ int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
     const int k = (int)c.num_experts_per_tok;
     for (int64_t s0 = 0; s0 < rows; s0 += 4) {
         const int M = (int)(rows - s0 < 4 ? rows - s0 : 4);
-        // f32 gate matmul (lib.rs:128), then route (router.rs:58) + slot plan
-        UT_TRY(mm(s, L.gate, x + s0 * H, M, s->ws.rlogits, E));
+        // f32 gate matmul (lib.rs:128), then route (router.rs:58) + slot plan;
+        // a split gate GEMV leaves its partials to the router launch
+        SplitKPartials gparts;
+        {
+            GemvArgs ga;
+            ga.w = L.gate;
+            ga.xf = x + s0 * H;
+            ga.M = M;
+            ga.out = s->ws.rlogits;
+            ga.ldo = E;
+            ga.defer = &gparts;
+            if (L.gate->fmt != UT_FMT_F32) {
+                UT_TRY(mm(s, L.gate, x + s0 * H, M, s->ws.rlogits, E));
+                gparts = SplitKPartials{};
+            } else {
+                UT_TRY(gemv(m->ctx, ga));
+            }
+        }
         const int64_t slots = moe_slots(M, k, E, -1);
         ScratchLayout lay = moe_layout(M, k, slots, H, c.moe_intermediate_size, L.expert_fmt);
-        UT_TRY(launch_route_plan(m->ctx, s->ws.rlogits, L.bias, M, E, k, (int)c.n_group,
+        UT_TRY(launch_route_plan(m->ctx, s->ws.rlogits, &gparts, L.bias, M, E, k, (int)c.n_group,
                                  (int)c.topk_group, c.norm_topk_prob, c.routed_scaling_factor,
                                  s->ws.rids, s->ws.rw, L.experts.gate_w,
                                  moe_plan_view(s->ws.moe, lay), s->ws.err));
@@ -496,9 +512,27 @@ int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
     const int64_t qh = nope + rope;
     const float scale = 1.0f / sqrtf((float)qh);  // config.rs:142-144
     const int64_t pos_base = kv.len;
-    UT_TRY(matmul_digits(ctx, L.kv_a, x, xd, rows, w.comp, Lr + rope, 0));
+    const bool pair = L.lora && L.kv_a->fmt == L.q_a->fmt && L.kv_a->fmt != UT_FMT_F32 &&
+                      L.kv_a->in_dim == L.q_a->in_dim && L.kv_a->row_bytes == L.q_a->row_bytes &&
+                      gemv_fast_ok(L.kv_a) && gemv_fast_ok(L.q_a);
+    if (pair) {
+        // kv_a and q_a read the same normed row: one launch for both
+        GemvArgs ga;
+        ga.w = L.kv_a;
+        ga.xf = x;
+        ga.xd = xd;
+        ga.M = rows;
+        ga.out = w.comp;
+        ga.ldo = Lr + rope;
+        ga.w2 = L.q_a;
+        ga.out2 = w.qa;
+        ga.ldo2 = c.q_lora_rank;
+        UT_TRY(gemv(ctx, ga));
+    } else {
+        UT_TRY(matmul_digits(ctx, L.kv_a, x, xd, rows, w.comp, Lr + rope, 0));
+    }
     if (L.lora) {
-        UT_TRY(matmul_digits(ctx, L.q_a, x, xd, rows, w.qa, c.q_lora_rank, 0));
+        if (!pair) UT_TRY(matmul_digits(ctx, L.q_a, x, xd, rows, w.qa, c.q_lora_rank, 0));
         XDigits qd;
         UT_TRY(norm_dig(s, w.qa, c.q_lora_rank, L.q_a_norm, c.q_lora_rank, rows, w.qa_n,
                         c.q_lora_rank, w.digB, dig_flags({L.q_b}), &qd));

@@ -124,10 +124,13 @@ int32_t moe_pass(ut_ctx *ctx, const MoeCall &c, void *scratch);
 // The plan buffers inside a pass's scratch.
 MoePlan moe_plan_view(void *scratch, const ScratchLayout &L);
 // Routes M <= 4 rows and writes the slot plan into `plan` in one launch.
-int32_t launch_route_plan(ut_ctx *ctx, const float *logits, const float *bias, int M, int64_t E,
-                          int32_t k, int32_t n_group, int32_t topk_group, int32_t norm,
-                          float scale, int32_t *ids, float *weights,
-                          const uint8_t *const *gate_tbl, MoePlan plan, int32_t *err_flag);
+// parts (optional): the gate GEMV's deferred split-K partials, summed here
+// instead of logits being read.
+int32_t launch_route_plan(ut_ctx *ctx, const float *logits, const SplitKPartials *parts,
+                          const float *bias, int M, int64_t E, int32_t k, int32_t n_group,
+                          int32_t topk_group, int32_t norm, float scale, int32_t *ids,
+                          float *weights, const uint8_t *const *gate_tbl, MoePlan plan,
+                          int32_t *err_flag);
 
 int32_t launch_route(ut_ctx *ctx, const float *logits, const float *bias, int64_t rows,
                      int64_t E, int32_t k, int32_t n_group, int32_t topk_group, int32_t norm,

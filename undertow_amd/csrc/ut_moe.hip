@@ -20,10 +20,10 @@
 
 // Weight steps in flight per lane in the expert kernels (see gemv_core).
 #ifndef UT_GATE_UP_DEPTH
-#define UT_GATE_UP_DEPTH 2
+#define UT_GATE_UP_DEPTH 1
 #endif
 #ifndef UT_DOWN_DEPTH
-#define UT_DOWN_DEPTH 2
+#define UT_DOWN_DEPTH 1
 #endif
 
 namespace ut {
@@ -139,19 +139,36 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
 
 // Routing of M <= 4 rows plus the slot plan in one workgroup (one launch on
 // the decode path instead of two).
+// logits: [M, E], or (part != nullptr) the gate GEMV's split-K partials
+// [ks][M][E] (f32 bits), summed here in z order as the GEMV's own sum
+// launch would.
 __global__ __launch_bounds__(256) void k_route_plan(const float *__restrict__ logits,
+                                                    const int64_t *__restrict__ part, int ks,
                                                     const float *__restrict__ bias, int M, int E,
                                                     int k, int n_group, int topk_group, int norm,
                                                     float scale, int32_t *__restrict__ ids,
                                                     float *__restrict__ weights,
                                                     const uint8_t *const *__restrict__ gate_tbl,
                                                     MoePlan plan, int32_t *__restrict__ err_flag) {
-    extern __shared__ float sm[];
+    extern __shared__ float sm[];  // [2E + n_group] route scratch, then [M][E] logits
     __shared__ int s_ids[64];
     __shared__ int s_group_ok[64];
     __shared__ int32_t s_all[4 * 64];
+    float *s_lg = sm + 2 * E + (n_group > 0 ? n_group : 1);
+    for (int i = threadIdx.x; i < M * E; i += blockDim.x) {
+        float v;
+        if (part) {
+            v = __uint_as_float((uint32_t)part[i]);
+#pragma unroll 16
+            for (int z = 1; z < ks; z++) v = __fadd_rn(v, __uint_as_float((uint32_t)part[(int64_t)z * M * E + i]));
+        } else {
+            v = logits[i];
+        }
+        s_lg[i] = v;
+    }
+    __syncthreads();
     for (int row = 0; row < M; row++) {
-        route_row(logits + (int64_t)row * E, bias, E, k, n_group, topk_group, norm, scale,
+        route_row(s_lg + row * E, bias, E, k, n_group, topk_group, norm, scale,
                   ids + (int64_t)row * k, weights + (int64_t)row * k, sm, s_ids, s_group_ok);
         // the chosen ids from LDS (route_row ends with a barrier)
         if (threadIdx.x < k) s_all[row * k + threadIdx.x] = threadIdx.x < (k < E ? k : E) ? s_ids[threadIdx.x] : -1;
@@ -180,17 +197,25 @@ int32_t launch_route(ut_ctx *ctx, const float *logits, const float *bias, int64_
     return launch_check(ctx, "k_route");
 }
 
-int32_t launch_route_plan(ut_ctx *ctx, const float *logits, const float *bias, int M, int64_t E,
-                          int32_t k, int32_t n_group, int32_t topk_group, int32_t norm,
-                          float scale, int32_t *ids, float *weights,
-                          const uint8_t *const *gate_tbl, MoePlan plan, int32_t *err_flag) {
+int32_t launch_route_plan(ut_ctx *ctx, const float *logits, const SplitKPartials *parts,
+                          const float *bias, int M, int64_t E, int32_t k, int32_t n_group,
+                          int32_t topk_group, int32_t norm, float scale, int32_t *ids,
+                          float *weights, const uint8_t *const *gate_tbl, MoePlan plan,
+                          int32_t *err_flag) {
     if (M < 1 || M > 4 || k > 64) {
         set_error(ctx, "route_plan: M=%d k=%d outside 1..4 / 1..64", M, k);
         return UT_ERR_ARG;
     }
-    size_t shmem = (size_t)(2 * E + (n_group > 0 ? n_group : 1)) * sizeof(float);
+    const bool split = parts && parts->ks > 1;
+    if (split && parts->O != E) {
+        set_error(ctx, "route_plan: partials of %lld rows for %lld experts", (long long)parts->O,
+                  (long long)E);
+        return UT_ERR_ARG;
+    }
+    size_t shmem = (size_t)(2 * E + (n_group > 0 ? n_group : 1) + M * E) * sizeof(float);
     int tok = timing_begin(ctx, "route_plan");
-    hipLaunchKernelGGL(k_route_plan, dim3(1), dim3(256), shmem, ctx->stream, logits, bias, M,
+    hipLaunchKernelGGL(k_route_plan, dim3(1), dim3(256), shmem, ctx->stream, logits,
+                       split ? (const int64_t *)parts->part : nullptr, split ? parts->ks : 1, bias, M,
                        (int)E, (int)k, (int)n_group, (int)topk_group, (int)norm, scale, ids,
                        weights, gate_tbl, plan, err_flag);
     timing_end(ctx, tok);
