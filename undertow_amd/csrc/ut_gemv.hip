@@ -71,7 +71,7 @@ struct RowDigArgs {
     // optional slot plan built by the launch's last workgroup
     const int32_t *plan_ids;
     int plan_M, plan_k, plan_E;
-    const uint8_t *const *gate_tbl;
+    const void *const *tbl;  // [6][E] expert pointer table
     MoePlan plan;
     int32_t *err_flag;
 };
@@ -82,7 +82,7 @@ __global__ __launch_bounds__(256) void k_rowdig(RowDigArgs a) {
     __shared__ uint32_t redu[4];
     const int64_t m = blockIdx.x;
     if (a.plan_ids && blockIdx.x == gridDim.x - 1) {
-        make_plan(a.plan_ids, a.plan_M, a.plan_k, a.plan_E, a.gate_tbl, -1, a.plan, a.err_flag);
+        make_plan(a.plan_ids, a.plan_M, a.plan_k, a.plan_E, a.tbl, -1, a.plan, a.err_flag);
         return;
     }
     if (a.slot_count && (int)(m / a.rows_per_slot) >= *a.slot_count) return;
@@ -184,7 +184,7 @@ __global__ __launch_bounds__(1024) void k_rowdig_reg(RowDigArgs a) {
     __shared__ uint32_t redu[16];
     const int64_t m = blockIdx.x;
     if (a.plan_ids && blockIdx.x == gridDim.x - 1) {
-        make_plan(a.plan_ids, a.plan_M, a.plan_k, a.plan_E, a.gate_tbl, -1, a.plan, a.err_flag);
+        make_plan(a.plan_ids, a.plan_M, a.plan_k, a.plan_E, a.tbl, -1, a.plan, a.err_flag);
         return;
     }
     if (a.slot_count && (int)(m / a.rows_per_slot) >= *a.slot_count) return;
@@ -344,7 +344,7 @@ int32_t launch_digitize_slots(ut_ctx *ctx, const float *x, int64_t ldx, int64_t 
 
 int32_t launch_digitize_plan(ut_ctx *ctx, const float *x, int64_t M, int64_t K, XDigits xd,
                              int flags, const int32_t *ids, int k, int64_t E,
-                             const uint8_t *const *gate_tbl, MoePlan plan, int32_t *err_flag) {
+                             const void *const *tbl, MoePlan plan, int32_t *err_flag) {
     RowDigArgs a{};
     a.x = x;
     a.ldx = K;
@@ -357,7 +357,7 @@ int32_t launch_digitize_plan(ut_ctx *ctx, const float *x, int64_t M, int64_t K, 
     a.plan_M = (int)M;
     a.plan_k = k;
     a.plan_E = (int)E;
-    a.gate_tbl = gate_tbl;
+    a.tbl = tbl;
     a.plan = plan;
     a.err_flag = err_flag;
     return launch_rowdig(ctx, a, M, "digitize_plan");

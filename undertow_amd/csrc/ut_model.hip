@@ -93,6 +93,7 @@ struct Workspace {
     float *logits = nullptr, *emb = nullptr, *cat = nullptr;
     float *rlogits = nullptr, *rw = nullptr;
     int32_t *rids = nullptr, *ids = nullptr, *am = nullptr, *err = nullptr;
+    int32_t *vids = nullptr;  // verify ids [next, drafts...] assembled on the device
     void *digits = nullptr, *moe = nullptr, *mla = nullptr, *argm = nullptr;
     void *digA = nullptr, *digB = nullptr;  // activation digits shared by consumers
 };
@@ -111,11 +112,17 @@ struct ut_session {
     void *kv_alloc = nullptr;
     Workspace ws;
     int64_t cap = 0;
+    // host staging of the generation loops (pinned): [0, kPinIds) ids going
+    // up, then readback slots; `ready` marks the end of the last readback
+    int32_t *pin = nullptr;
+    hipEvent_t ready = nullptr;
 };
 
 namespace {
 
 constexpr int64_t kMlaRowsPerCall = 16;
+constexpr int64_t kPinIds = 16384;   // ints of the upload slot (the last 8: verify ids)
+constexpr int64_t kPinBack = 64;     // ints of the readback slot (argmax rows, drafts, flag)
 
 int64_t hd(const ut_model *m) { return m->c.hidden_size; }
 
@@ -330,6 +337,7 @@ int32_t ws_reserve(ut_session *s, int64_t rows) {
     size_t iclat = F(R * heads * Lr), ictx = F(R * heads * c.v_head_dim);
     size_t ilog = F(R * c.vocab_size), iemb = F(R * H), icat = F(R * 2 * H);
     size_t irl = F(4 * E), irw = F(4 * k), irid = F(4 * k), iids = F(R), iam = F(R), ierr = F(1);
+    size_t ivids = F(8);
     size_t idig = plan.add(matmul_digit_bytes(R, kmax));
     size_t idA = plan.add(matmul_digit_bytes(R, kmax));
     size_t idB = plan.add(matmul_digit_bytes(R, kmax));
@@ -360,6 +368,7 @@ int32_t ws_reserve(ut_session *s, int64_t rows) {
     w.logits = (float *)p[ilog]; w.emb = (float *)p[iemb]; w.cat = (float *)p[icat];
     w.rlogits = (float *)p[irl]; w.rw = (float *)p[irw]; w.rids = (int32_t *)p[irid];
     w.ids = (int32_t *)p[iids]; w.am = (int32_t *)p[iam]; w.err = (int32_t *)p[ierr];
+    w.vids = (int32_t *)p[ivids];
     w.digits = p[idig]; w.moe = p[imoes]; w.mla = p[imla]; w.argm = p[iarg];
     w.digA = p[idA]; w.digB = p[idB];
     w.rows = R;
@@ -425,7 +434,9 @@ int32_t mlp_add(ut_session *s, const MlpW &w, const float *x, const XDigits &xd,
         c.ldo = c.H;
         c.accumulate = 1;
         c.err_flag = s->ws.err;
-        c.plan = &m->mlp_plan;
+        MoePlan mp = m->mlp_plan;
+        mp.sp = (const void **)w.dev;  // the MLP's 6 weight pointers are its slot 0
+        c.plan = &mp;
         c.init = init ? init + s0 * c.H : nullptr;
         UT_TRY(moe_pass(m->ctx, c, s->ws.moe));
     }
@@ -465,7 +476,7 @@ int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
         ScratchLayout lay = moe_layout(M, k, slots, H, c.moe_intermediate_size, L.expert_fmt);
         UT_TRY(launch_route_plan(m->ctx, s->ws.rlogits, &gparts, L.bias, M, E, k, (int)c.n_group,
                                  (int)c.topk_group, c.norm_topk_prob, c.routed_scaling_factor,
-                                 s->ws.rids, s->ws.rw, L.experts.gate_w,
+                                 s->ws.rids, s->ws.rw, (const void *const *)L.experts.gate_w,
                                  moe_plan_view(s->ws.moe, lay), s->ws.err));
         MoeCall mc;
         mc.fmt = L.expert_fmt;
@@ -486,11 +497,13 @@ int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
         mc.err_flag = s->ws.err;
         mc.plan_ready = true;
         MoeCall sc;
+        MoePlan sp_plan = m->mlp_plan;
         if (shared) {
             sc.fmt = shared->fmt;
             sc.tbl = shared->ptrs;
             sc.I = shared->inter;
-            sc.plan = &m->mlp_plan;
+            sp_plan.sp = (const void **)shared->dev;  // slot 0 = the shared expert
+            sc.plan = &sp_plan;
             mc.shared = &sc;
             mc.shared_scratch = (char *)s->ws.moe + lay.total;
         }
@@ -614,7 +627,10 @@ int32_t upload_ids(ut_session *s, const int32_t *ids, int64_t n) {
 }
 
 // InferenceSession::prefill (model.rs:447-547) into ws.logits / ws.am.
-int32_t prefill_dev(ut_session *s, const int32_t *ids, int64_t n) {
+// ids_dev: the token ids are already on the device (an earlier argmax:
+// always in the vocabulary); they are not checked, uploaded or recorded in
+// s->tokens (the caller records them once it has read them back).
+int32_t prefill_dev(ut_session *s, const int32_t *ids, int64_t n, const int32_t *ids_dev = nullptr) {
     ut_model *m = s->m;
     ut_ctx *ctx = m->ctx;
     const ut_model_config &c = m->c;
@@ -627,22 +643,30 @@ int32_t prefill_dev(ut_session *s, const int32_t *ids, int64_t n) {
                   (long long)s->cap);
         return UT_ERR_CONTEXT_OVERFLOW;
     }
-    for (int64_t i = 0; i < n; i++)
-        if (ids[i] < 0 || ids[i] >= c.vocab_size) {
-            set_error(ctx, "token id %d out of vocab (%lld)", ids[i], (long long)c.vocab_size);
-            return UT_ERR_BAD_TOKEN;
+    if (ids_dev) {
+        // device ids point into the workspace: it must not move
+        if (n > s->ws.rows) {
+            set_error(ctx, "device-fed prefill of %lld rows exceeds the workspace", (long long)n);
+            return UT_ERR_STATE;
         }
-    UT_TRY(ws_reserve(s, n));
+    } else {
+        for (int64_t i = 0; i < n; i++)
+            if (ids[i] < 0 || ids[i] >= c.vocab_size) {
+                set_error(ctx, "token id %d out of vocab (%lld)", ids[i], (long long)c.vocab_size);
+                return UT_ERR_BAD_TOKEN;
+            }
+        UT_TRY(ws_reserve(s, n));
+    }
     Workspace &w = s->ws;
     const int64_t H = c.hidden_size, V = c.vocab_size;
-    UT_TRY(upload_ids(s, ids, n));
-    UT_TRY(launch_embed(ctx, m->embed, w.ids, n, w.x, H));
+    if (!ids_dev) UT_TRY(upload_ids(s, ids, n));
+    UT_TRY(launch_embed(ctx, m->embed, ids_dev ? ids_dev : w.ids, n, w.x, H));
     for (size_t li = 0; li < m->layers.size(); li++) UT_TRY(run_layer(s, m->layers[li], w.x, n, s->kv[li]));
     if (m->has_mtp)
         UT_CHECK_HIP(ctx, hipMemcpyAsync(s->hidden + s->pos * H, w.x, (size_t)n * H * 4,
                                          hipMemcpyDeviceToDevice, ctx->stream));
     s->pos += n;
-    s->tokens.insert(s->tokens.end(), ids, ids + n);
+    if (!ids_dev) s->tokens.insert(s->tokens.end(), ids, ids + n);
     XDigits fd;
     UT_TRY(norm_dig(s, w.x, H, m->final_norm, H, n, w.normed, H, w.digA, dig_flags({m->lm_head}),
                     &fd));
@@ -661,6 +685,51 @@ int32_t read_argmax(ut_session *s, int64_t n, int32_t *out) {
     return UT_OK;
 }
 
+// Asynchronous readback for the generation loops: n ints from dev, then the
+// sticky error flag, into the session's pinned readback slot; `ready` is
+// recorded behind them, so later launches need not wait for the host.
+int32_t readback_enqueue(ut_session *s, const int32_t *dev, int64_t n, int64_t slot_off = 0) {
+    ut_ctx *ctx = s->m->ctx;
+    int32_t *back = s->pin + kPinIds;
+    if (slot_off + n + 1 > kPinBack) {
+        set_error(ctx, "readback of %lld ints exceeds the staging slot", (long long)n);
+        return UT_ERR_ARG;
+    }
+    UT_CHECK_HIP(ctx, hipMemcpyAsync(back + slot_off, dev, (size_t)n * 4, hipMemcpyDeviceToHost, ctx->stream));
+    UT_CHECK_HIP(ctx, hipMemcpyAsync(back + kPinBack - 1, s->ws.err, 4, hipMemcpyDeviceToHost, ctx->stream));
+    UT_CHECK_HIP(ctx, hipEventRecord(s->ready, ctx->stream));
+    return UT_OK;
+}
+
+// Waits for the last readback; out <- the ints at slot_off.
+int32_t readback_wait(ut_session *s, int64_t n, int32_t *out, int64_t slot_off = 0) {
+    ut_ctx *ctx = s->m->ctx;
+    UT_CHECK_HIP(ctx, hipEventSynchronize(s->ready));
+    const int32_t *back = s->pin + kPinIds;
+    if (back[kPinBack - 1]) {
+        set_error(ctx, "a routed expert id was out of range or not loaded");
+        return UT_ERR_BAD_EXPERT;
+    }
+    memcpy(out, back + slot_off, (size_t)n * 4);
+    return UT_OK;
+}
+
+// Host ids to a device buffer through the pinned upload slot.  The caller
+// guarantees that the slot's previous upload has completed (the generation
+// loops read back, and so wait, after every step).
+// Uploads queued in one step use disjoint offsets of the slot.
+int32_t upload_slot(ut_session *s, int32_t *dev, const int32_t *ids, int64_t n, int64_t off = 0) {
+    ut_ctx *ctx = s->m->ctx;
+    if (off + n > kPinIds) {
+        set_error(ctx, "upload of %lld ids exceeds the staging slot", (long long)n);
+        return UT_ERR_ARG;
+    }
+    memcpy(s->pin + off, ids, (size_t)n * 4);
+    UT_CHECK_HIP(ctx, hipMemcpyAsync(dev, s->pin + off, (size_t)n * 4, hipMemcpyHostToDevice,
+                                     ctx->stream));
+    return UT_OK;
+}
+
 void truncate_session(ut_session *s, int64_t len) {
     // model.rs:556-564, LayerKvCache::truncate (attention.rs:89-93)
     for (auto &kv : s->kv)
@@ -669,21 +738,35 @@ void truncate_session(ut_session *s, int64_t len) {
     if ((int64_t)s->tokens.size() > s->pos) s->tokens.resize((size_t)s->pos);
 }
 
-// draft_logits (mtp.rs:74-133): feed positions fed..pos-1 to the MTP layer,
-// return the argmax of the head's logits for the last one.  chain_hidden:
-// when non-null, run one more chained draft row on (emb(next), hidden =
-// chain_hidden) at position pos (depth > 1; the caller rolls the MTP cache
-// back afterwards).
-int32_t draft_rows(ut_session *s, const std::vector<int32_t> &next_tokens, const float *hidden_rows,
-                   int64_t rows, int32_t *draft_out) {
+// draft_logits (mtp.rs:74-133): feed positions fed..pos-1 to the MTP layer
+// and take the argmax of the head's logits for the last one.
+// draft_logits on device ids: row ids come from the host (host_ids, rows of
+// them) or, for a chained draft, from ws.vids[in_slot] (one row); the draft
+// id goes to ws.vids[out_slot] without a host round trip.
+int32_t draft_rows_dev(ut_session *s, const int32_t *host_ids, int in_slot,
+                       const float *hidden_rows, int64_t rows, int out_slot) {
     ut_model *m = s->m;
     ut_ctx *ctx = m->ctx;
     const ut_model_config &c = m->c;
     Workspace &w = s->ws;
     const int64_t H = c.hidden_size, V = c.vocab_size;
-    UT_TRY(ws_reserve(s, rows));
-    UT_TRY(upload_ids(s, next_tokens.data(), rows));
-    UT_TRY(launch_embed(ctx, m->embed, w.ids, rows, w.emb, H));
+    if (rows > w.rows) UT_TRY(ws_reserve(s, rows));
+    const int32_t *ids = in_slot >= 0 ? w.vids + in_slot : nullptr;
+    int32_t *draft_dev = w.vids + out_slot;
+    if (in_slot < 0) {
+        if (rows > kPinIds - 8) {
+            set_error(ctx, "MTP draft over %lld positions exceeds the staging slot", (long long)rows);
+            return UT_ERR_ARG;
+        }
+        for (int64_t i = 0; i < rows; i++)
+            if (host_ids[i] < 0 || host_ids[i] >= V) {
+                set_error(ctx, "token id %d out of vocab (%lld)", host_ids[i], (long long)V);
+                return UT_ERR_BAD_TOKEN;
+            }
+        UT_TRY(upload_slot(s, w.ids, host_ids, rows));
+        ids = w.ids;
+    }
+    UT_TRY(launch_embed(ctx, m->embed, ids, rows, w.emb, H));
     UT_TRY(launch_rmsnorm(ctx, w.emb, H, m->enorm, H, c.rms_norm_eps, rows, w.cat, 2 * H));
     UT_TRY(launch_rmsnorm(ctx, hidden_rows, H, m->hnorm, H, c.rms_norm_eps, rows, w.cat + H, 2 * H));
     UT_TRY(mm(s, m->eh_proj, w.cat, rows, w.x, H));
@@ -692,8 +775,7 @@ int32_t draft_rows(ut_session *s, const std::vector<int32_t> &next_tokens, const
     UT_TRY(norm_dig(s, w.x + (rows - 1) * H, H, m->mtp_norm, H, 1, w.normed, H, w.digA,
                     dig_flags({m->mtp_head}), &hd_));
     UT_TRY(matmul_digits(ctx, m->mtp_head, w.normed, hd_, 1, w.logits, V, 0));
-    UT_TRY(launch_argmax(ctx, w.logits, 1, V, V, w.am, w.argm));
-    return read_argmax(s, 1, draft_out);
+    return launch_argmax(ctx, w.logits, 1, V, V, draft_dev, w.argm);
 }
 
 // ---------------------------------------------------------- synthesis ---
@@ -1045,6 +1127,13 @@ int32_t ut_session_create(ut_model *m, int32_t path, ut_session **out) {
         carve(s->mtp_kv);
         s->hidden = (float *)p;
     }
+    if (hipHostMalloc((void **)&s->pin, (size_t)(kPinIds + kPinBack) * 4, hipHostMallocDefault) != hipSuccess ||
+        hipEventCreateWithFlags(&s->ready, hipEventDisableTiming) != hipSuccess) {
+        (void)hipGetLastError();
+        set_error(m->ctx, "session staging allocation failed");
+        ut_session_free(s);
+        return UT_ERR_OOM;
+    }
     int32_t rc = ws_reserve(s, 4);
     if (rc) {
         ut_session_free(s);
@@ -1060,6 +1149,8 @@ void ut_session_free(ut_session *s) {
     (void)hipStreamSynchronize(s->m->ctx->stream);
     if (s->ws.base) (void)hipFree(s->ws.base);
     if (s->kv_alloc) (void)hipFree(s->kv_alloc);
+    if (s->pin) (void)hipHostFree(s->pin);
+    if (s->ready) (void)hipEventDestroy(s->ready);
     ut_model *m = s->m;
     delete s;
     ut_model_free(m);  // drops the session's reference
@@ -1091,7 +1182,9 @@ int64_t ut_session_position(const ut_session *s) { return s ? s->pos : UT_ERR_AR
 
 int64_t ut_generate_greedy(ut_model *m, const int32_t *prompt, int64_t n, int64_t max_new,
                            int32_t *out) {
-    // undertow_core::generate, greedy (core/model.rs:139-185)
+    // undertow_core::generate, greedy (core/model.rs:139-185).  Each step is
+    // fed the previous step's argmax on the device, and the next step is
+    // queued before the host waits for the current token.
     if (!m || !prompt || (max_new > 0 && !out) || max_new < 0) return UT_ERR_ARG;
     ut_session *s = nullptr;
     UT_TRY(ut_session_create(m, 0, &s));
@@ -1099,23 +1192,46 @@ int64_t ut_generate_greedy(ut_model *m, const int32_t *prompt, int64_t n, int64_
     int32_t rc = prefill_dev(s, prompt, n);
     if (rc == UT_OK) rc = read_argmax(s, n, am.data());
     if (rc) { ut_session_free(s); return rc; }
-    int32_t next = am[(size_t)n - 1];
     int64_t produced = 0;
-    while (produced < max_new) {
-        out[produced++] = next;
-        if (produced == max_new) break;
-        rc = prefill_dev(s, &next, 1);
-        if (rc == UT_ERR_CONTEXT_OVERFLOW) break;  // clean stop at the context end
-        if (rc == UT_OK) rc = read_argmax(s, 1, &next);
-        if (rc) { ut_session_free(s); return rc; }
+    if (max_new == 0) { ut_session_free(s); return 0; }
+    int32_t tok = am[(size_t)n - 1];
+    out[produced++] = tok;
+    bool queued = false;  // a step whose output token is not read yet
+    if (produced < max_new) {
+        rc = prefill_dev(s, nullptr, 1, s->ws.am + (n - 1));
+        if (rc == UT_OK) {
+            s->tokens.push_back(tok);
+            queued = true;
+        } else if (rc == UT_ERR_CONTEXT_OVERFLOW) {
+            rc = UT_OK;  // clean stop at the context end
+        }
+    }
+    while (queued && rc == UT_OK) {
+        rc = readback_enqueue(s, s->ws.am, 1);
+        if (rc) break;
+        bool next_queued = false;
+        if (produced + 1 < max_new) {
+            // fed from ws.am[0], which this step overwrites only after reading it
+            const int32_t r2 = prefill_dev(s, nullptr, 1, s->ws.am);
+            if (r2 == UT_OK) next_queued = true;
+            else if (r2 != UT_ERR_CONTEXT_OVERFLOW) { rc = r2; break; }
+        }
+        rc = readback_wait(s, 1, &tok);
+        if (rc) break;
+        out[produced++] = tok;
+        if (next_queued) s->tokens.push_back(tok);  // the id the queued step was fed
+        queued = next_queued;
     }
     ut_session_free(s);
-    return produced;
+    return rc ? rc : produced;
 }
 
 int64_t ut_generate_mtp(ut_model *m, const int32_t *prompt, int64_t n, int64_t max_new,
                         int32_t depth, int32_t *out, int64_t *drafted, int64_t *accepted) {
-    // speculative_loop (mtp.rs:263-314) with the native draft head
+    // speculative_loop (mtp.rs:263-314) with the native draft head.  Drafts
+    // stay on the device (ws.vids[1..depth]) and feed the verify launch
+    // directly; the host reads the verify argmax and the drafts once per
+    // step, for the accept decision.
     if (!m || !prompt || (max_new > 0 && !out) || max_new < 0) return UT_ERR_ARG;
     if (depth < 1 || depth > 3) {
         set_error(m->ctx, "MTP depth %d outside 1..3", depth);
@@ -1138,7 +1254,7 @@ int64_t ut_generate_mtp(ut_model *m, const int32_t *prompt, int64_t n, int64_t m
     if (rc) { ut_session_free(s); return rc; }
     int32_t next = am[(size_t)n - 1];
     int64_t produced = 0, nd = 0, na = 0;
-    std::vector<int32_t> toks, drafts;
+    std::vector<int32_t> toks, drafts((size_t)depth);
     for (;;) {
         out[produced++] = next;
         if (produced >= max_new) break;
@@ -1146,11 +1262,9 @@ int64_t ut_generate_mtp(ut_model *m, const int32_t *prompt, int64_t n, int64_t m
         const int64_t pos = s->pos, fed = s->mtp_fed, pending = pos - fed;
         toks.clear();
         for (int64_t i = fed; i < pos; i++) toks.push_back(i + 1 < pos ? s->tokens[(size_t)i + 1] : next);
-        int32_t d = 0;
-        rc = draft_rows(s, toks, s->hidden + fed * H, pending, &d);
+        rc = draft_rows_dev(s, toks.data(), -1, s->hidden + fed * H, pending, 1);
         if (rc) break;
         s->mtp_fed = pos;
-        drafts.assign(1, d);
         // ---- chained drafts (depth > 1): MTP layer on its own last hidden state
         for (int32_t j = 1; j < depth && rc == UT_OK; j++) {
             // the MTP layer's output row for the last fed position is in ws.x
@@ -1158,21 +1272,25 @@ int64_t ut_generate_mtp(ut_model *m, const int32_t *prompt, int64_t n, int64_t m
             const int64_t last = (j == 1 ? pending : 1) - 1;
             UT_CHECK_HIP(ctx, hipMemcpyAsync(s->ws.attn, s->ws.x + last * H, (size_t)H * 4,
                                              hipMemcpyDeviceToDevice, ctx->stream));
-            toks.assign(1, drafts.back());
-            rc = draft_rows(s, toks, s->ws.attn, 1, &d);
-            drafts.push_back(d);
+            rc = draft_rows_dev(s, nullptr, j, s->ws.attn, 1, 1 + j);
         }
         s->mtp_kv.len = s->mtp_fed;  // speculative MTP rows are never kept
         if (rc) break;
-        nd += (int64_t)drafts.size();
-        // ---- verify [next, d1..dk] in one prefill
+        nd += depth;
+        // ---- verify [next, d1..dk] in one prefill, ids assembled on the device
         const int64_t pos_before = s->pos;
-        toks.assign(1, next);
-        toks.insert(toks.end(), drafts.begin(), drafts.end());
-        rc = prefill_dev(s, toks.data(), (int64_t)toks.size());
-        if (rc == UT_ERR_CONTEXT_OVERFLOW) { rc = UT_OK; break; }
-        if (rc == UT_OK) rc = read_argmax(s, (int64_t)toks.size(), am.data());
+        rc = upload_slot(s, s->ws.vids, &next, 1, kPinIds - 8);
         if (rc) break;
+        rc = prefill_dev(s, nullptr, depth + 1, s->ws.vids);
+        if (rc == UT_ERR_CONTEXT_OVERFLOW) { rc = UT_OK; break; }
+        if (rc) break;
+        rc = readback_enqueue(s, s->ws.vids + 1, depth, depth + 1);
+        if (rc == UT_OK) rc = readback_enqueue(s, s->ws.am, depth + 1, 0);
+        if (rc == UT_OK) rc = readback_wait(s, depth + 1, am.data(), 0);
+        if (rc) break;
+        memcpy(drafts.data(), s->pin + kPinIds + depth + 1, (size_t)depth * 4);
+        s->tokens.push_back(next);
+        s->tokens.insert(s->tokens.end(), drafts.begin(), drafts.end());
         int64_t a = 0;
         bool full = false;
         while (a < (int64_t)drafts.size() && am[(size_t)a] == drafts[(size_t)a]) {

@@ -22,7 +22,15 @@ struct MoePlan {
     int32_t *count;        // number of slots used
     int32_t *uniq;         // [slots] expert id per slot
     int32_t *choice_slot;  // [M*k] slot of each (row, choice), -1 when invalid
+    // [slots][6] the slot's weight pointers (gate, up, down payloads, then
+    // their scales), resolved once so the expert kernels start with a
+    // single dependent load
+    const void **sp;
 };
+
+// Pointer i (0..5: gate, up, down payloads; gate, up, down scales) of
+// expert e in a [6][E] device pointer table.
+enum { kSpGate = 0, kSpUp = 1, kSpDown = 2, kSpGateS = 3, kSpUpS = 4, kSpDownS = 5 };
 
 // One pass of the expert block over M <= 4 rows (all on device).
 struct MoeCall {
@@ -53,7 +61,7 @@ struct MoeCall {
 
 struct ScratchLayout {
     size_t total = 0;
-    size_t count = 0, uniq = 0, choice = 0, xd = 0, h = 0, hmax = 0, hd = 0, d = 0, dpart = 0;
+    size_t count = 0, uniq = 0, choice = 0, sp = 0, xd = 0, h = 0, hmax = 0, hd = 0, d = 0, dpart = 0;
     int xflags = 0, hflags = 0;
     int64_t ntiles = 0;
 };
@@ -63,9 +71,11 @@ struct ScratchLayout {
 // range or not loaded) set the sticky error flag and contribute nothing.
 // Whole-workgroup function: ids are read once in parallel, the assignment
 // runs in LDS, the plan is written out in parallel.  n = M*k <= 256.
+// tbl: the [6][E] pointer table (ExpertPtrs laid out from gate_w).
 __device__ inline void make_plan(const int32_t *ids, int M, int k, int E,
-                          const uint8_t *const *__restrict__ gate_tbl, int extra_slot,
+                          const void *const *__restrict__ tbl, int extra_slot,
                           MoePlan plan, int32_t *__restrict__ err_flag) {
+    const void *const *gate_tbl = tbl;
     __shared__ int s_e[256], s_first[256];
     const int n = M * k, tid = threadIdx.x;
     if (tid < n) {
@@ -93,14 +103,21 @@ __device__ inline void make_plan(const int32_t *ids, int M, int k, int E,
         if (e >= 0) {
             slot = 0;
             for (int j = 0; j < j0; j++) slot += s_first[j];
-            if (j0 == tid) plan.uniq[slot] = e;
+            if (j0 == tid) {
+                plan.uniq[slot] = e;
+#pragma unroll
+                for (int i = 0; i < 6; i++) plan.sp[slot * 6 + i] = tbl[(int64_t)i * E + e];
+            }
         }
         plan.choice_slot[tid] = slot;
     }
     if (tid == 0) {
         int U = 0;
         for (int j = 0; j < n; j++) U += s_first[j];
-        if (extra_slot >= 0) plan.uniq[U++] = extra_slot;  // a dense MLP run as one more slot
+        if (extra_slot >= 0) {  // a dense MLP run as one more slot
+            for (int i = 0; i < 6; i++) plan.sp[U * 6 + i] = tbl[(int64_t)i * E + extra_slot];
+            plan.uniq[U++] = extra_slot;
+        }
         *plan.count = U;
     }
 }
@@ -129,7 +146,7 @@ MoePlan moe_plan_view(void *scratch, const ScratchLayout &L);
 int32_t launch_route_plan(ut_ctx *ctx, const float *logits, const SplitKPartials *parts,
                           const float *bias, int M, int64_t E, int32_t k, int32_t n_group,
                           int32_t topk_group, int32_t norm, float scale, int32_t *ids,
-                          float *weights, const uint8_t *const *gate_tbl, MoePlan plan,
+                          float *weights, const void *const *tbl, MoePlan plan,
                           int32_t *err_flag);
 
 int32_t launch_route(ut_ctx *ctx, const float *logits, const float *bias, int64_t rows,
@@ -143,7 +160,7 @@ int32_t launch_route(ut_ctx *ctx, const float *logits, const float *bias, int64_
 // expert pass.
 int32_t launch_digitize_plan(ut_ctx *ctx, const float *x, int64_t M, int64_t K, XDigits xd,
                              int flags, const int32_t *ids, int k, int64_t E,
-                             const uint8_t *const *gate_tbl, MoePlan plan, int32_t *err_flag);
+                             const void *const *tbl, MoePlan plan, int32_t *err_flag);
 
 int32_t launch_digitize_slots(ut_ctx *ctx, const float *x, int64_t ldx, int64_t M, int64_t K,
                               const uint32_t *rowmax_parts, int32_t nparts, XDigits xd,

@@ -148,7 +148,7 @@ __global__ __launch_bounds__(256) void k_route_plan(const float *__restrict__ lo
                                                     int k, int n_group, int topk_group, int norm,
                                                     float scale, int32_t *__restrict__ ids,
                                                     float *__restrict__ weights,
-                                                    const uint8_t *const *__restrict__ gate_tbl,
+                                                    const void *const *__restrict__ tbl,
                                                     MoePlan plan, int32_t *__restrict__ err_flag) {
     extern __shared__ float sm[];  // [2E + n_group] route scratch, then [M][E] logits
     __shared__ int s_ids[64];
@@ -175,13 +175,13 @@ __global__ __launch_bounds__(256) void k_route_plan(const float *__restrict__ lo
         __syncthreads();
     }
     __syncthreads();
-    make_plan(s_all, M, k, E, gate_tbl, -1, plan, err_flag);
+    make_plan(s_all, M, k, E, tbl, -1, plan, err_flag);
 }
 
 __global__ __launch_bounds__(256) void k_moe_plan(const int32_t *__restrict__ ids, int M, int k, int E,
-                           const uint8_t *const *__restrict__ gate_tbl, int extra_slot,
+                           const void *const *__restrict__ tbl, int extra_slot,
                            MoePlan plan, int32_t *__restrict__ err_flag) {
-    make_plan(ids, M, k, E, gate_tbl, extra_slot, plan, err_flag);
+    make_plan(ids, M, k, E, tbl, extra_slot, plan, err_flag);
 }
 
 int32_t launch_route(ut_ctx *ctx, const float *logits, const float *bias, int64_t rows,
@@ -200,7 +200,7 @@ int32_t launch_route(ut_ctx *ctx, const float *logits, const float *bias, int64_
 int32_t launch_route_plan(ut_ctx *ctx, const float *logits, const SplitKPartials *parts,
                           const float *bias, int M, int64_t E, int32_t k, int32_t n_group,
                           int32_t topk_group, int32_t norm, float scale, int32_t *ids,
-                          float *weights, const uint8_t *const *gate_tbl, MoePlan plan,
+                          float *weights, const void *const *tbl, MoePlan plan,
                           int32_t *err_flag) {
     if (M < 1 || M > 4 || k > 64) {
         set_error(ctx, "route_plan: M=%d k=%d outside 1..4 / 1..64", M, k);
@@ -217,7 +217,7 @@ int32_t launch_route_plan(ut_ctx *ctx, const float *logits, const SplitKPartials
     hipLaunchKernelGGL(k_route_plan, dim3(1), dim3(256), shmem, ctx->stream, logits,
                        split ? (const int64_t *)parts->part : nullptr, split ? parts->ks : 1, bias, M,
                        (int)E, (int)k, (int)n_group, (int)topk_group, (int)norm, scale, ids,
-                       weights, gate_tbl, plan, err_flag);
+                       weights, tbl, plan, err_flag);
     timing_end(ctx, tok);
     return launch_check(ctx, "k_route_plan");
 }
@@ -225,6 +225,7 @@ int32_t launch_route_plan(ut_ctx *ctx, const float *logits, const SplitKPartials
 // --------------------------------------------------------- gate / up ---
 struct GateUpArgs {
     ExpertPtrs tbl;
+    const void *const *sp;  // the plan's per-slot weight pointers
     const int32_t *uniq;
     const int32_t *count;
     int64_t H, I, row_bytes;  // gate/up are [I, H]
@@ -241,12 +242,13 @@ struct GateUpArgs {
 template <int FMT, int M>
 __device__ __forceinline__ void gate_up_body(const GateUpArgs &a, int u, int tile, uint32_t *lds,
                                              uint32_t *wg_max) {
-    if (u >= *a.count || tile >= a.ntiles) return;
+    // the slot count and the slot's pointers load in parallel
+    const int cnt = *a.count;
+    const uint8_t *gw = (const uint8_t *)a.sp[u * 6 + kSpGate], *uw = (const uint8_t *)a.sp[u * 6 + kSpUp];
+    const float *gsc = (const float *)a.sp[u * 6 + kSpGateS], *usc = (const float *)a.sp[u * 6 + kSpUpS];
+    if (u >= cnt || tile >= a.ntiles) return;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
     if (tid < 4) wg_max[tid] = 0;
-    const int e = a.uniq[u];
-    const uint8_t *gw = a.tbl.gate_w[e], *uw = a.tbl.up_w[e];
-    const float *gsc = a.tbl.gate_s[e], *usc = a.tbl.up_s[e];
     const int64_t o = (int64_t)tile * kGateUpRowsPerWG + wave * 4 + g;
     const int64_t oc = o < a.I ? o : a.I - 1;
     const uint8_t *rows[2] = {gw + oc * a.row_bytes, uw + oc * a.row_bytes};
@@ -296,6 +298,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up_dual(GateUpArgs a,
 // --------------------------------------------------------------- down ---
 struct DownArgs {
     ExpertPtrs tbl;
+    const void *const *sp;  // the plan's per-slot weight pointers
     const int32_t *uniq;
     const int32_t *count;
     int64_t H, I, row_bytes;  // down is [H, I]
@@ -332,11 +335,11 @@ template <int M> constexpr int down_rows() { return M <= 2 ? 4 : 2; }
 template <int FMT, int M>
 __device__ __forceinline__ void down_body(const DownArgs &a, int u, int tile, uint32_t *lds) {
     constexpr int R = down_rows<M>();
-    if (u >= *a.count) return;
+    const int cnt = *a.count;
+    const uint8_t *dw = (const uint8_t *)a.sp[u * 6 + kSpDown];
+    const float *dsc = (const float *)a.sp[u * 6 + kSpDownS];
+    if (u >= cnt) return;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
-    const int e = a.uniq[u];
-    const uint8_t *dw = a.tbl.down_w[e];
-    const float *dsc = a.tbl.down_s[e];
     const int64_t row0 = (int64_t)tile * (16 * R) + wave * (4 * R) + g * R;
     const uint8_t *rows[R];
 #pragma unroll
@@ -418,7 +421,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_down_finish(DownArgs a, in
     } else {
         int64_t S = a.part[i];
         for (int z = 1; z < a.ks; z++) S += a.part[z * zs + i];
-        v = int_total_to_f32(S, exl, ld_global_f32(a.tbl.down_s[a.uniq[u]] + o));
+        v = int_total_to_f32(S, exl, ld_global_f32((const float *)a.sp[u * 6 + kSpDownS] + o));
     }
     a.d[i] = v;
 }
@@ -478,6 +481,7 @@ ScratchLayout moe_layout(int64_t M, int64_t k, int64_t slots, int64_t H, int64_t
     L.count = take(4);
     L.uniq = take((size_t)slots * 4);
     L.choice = take((size_t)M * k * 4);
+    L.sp = take((size_t)slots * 6 * sizeof(void *));
     L.xd = take(fmt == UT_FMT_F32 ? 0 : xdigits_bytes(M, H, xflags));
     L.h = take((size_t)slots * M * I * 4);
     L.hmax = take((size_t)slots * M * ntiles * 4);
@@ -547,7 +551,7 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
             xd = *c.x_digits;  // caller already digitised x
         } else if (need_plan && c.extra_slot < 0) {
             UT_TRY(launch_digitize_plan(ctx, c.x, M, c.H, xd, L.xflags, c.ids, c.k, c.E,
-                                        c.tbl.gate_w, plan, c.err_flag));
+                                        (const void *const *)c.tbl.gate_w, plan, c.err_flag));
         } else {
             UT_TRY(launch_digitize(ctx, c.x, c.H, M, c.H, nullptr, xd, L.xflags));
         }
@@ -559,7 +563,7 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
     if (need_plan && !planned) {
         tok = timing_begin(ctx, "moe_plan");
         hipLaunchKernelGGL(k_moe_plan, dim3(1), dim3(256), 0, ctx->stream, c.ids, M, c.k, (int)c.E,
-                           c.tbl.gate_w, c.extra_slot, plan, c.err_flag);
+                           (const void *const *)c.tbl.gate_w, c.extra_slot, plan, c.err_flag);
         timing_end(ctx, tok);
         UT_TRY(launch_check(ctx, "k_moe_plan"));
     }
@@ -575,6 +579,7 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
     {
         GateUpArgs a;
         a.tbl = c.tbl;
+        a.sp = plan.sp;
         a.uniq = plan.uniq;
         a.count = plan.count;
         a.H = c.H;
@@ -588,6 +593,7 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
         if (c.shared) {
             const MoeCall &sc = *c.shared;
             gb.tbl = sc.tbl;
+            gb.sp = sc.plan->sp;
             gb.uniq = sc.plan->uniq;
             gb.count = sc.plan->count;
             gb.H = c.H;
@@ -613,6 +619,7 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
     {
         DownArgs a;
         a.tbl = c.tbl;
+        a.sp = plan.sp;
         a.uniq = plan.uniq;
         a.count = plan.count;
         a.H = c.H;
@@ -642,6 +649,7 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
         if (c.shared) {
             const MoeCall &sc = *c.shared;
             db.tbl = sc.tbl;
+            db.sp = sc.plan->sp;
             db.uniq = sc.plan->uniq;
             db.count = sc.plan->count;
             db.H = c.H;
@@ -685,6 +693,7 @@ MoePlan moe_plan_view(void *scratch, const ScratchLayout &L) {
     plan.count = (int32_t *)(base + L.count);
     plan.uniq = (int32_t *)(base + L.uniq);
     plan.choice_slot = (int32_t *)(base + L.choice);
+    plan.sp = (const void **)(base + L.sp);
     return plan;
 }
 
