@@ -322,6 +322,13 @@ def main():
         del tbl8
         torch.cuda.empty_cache()
 
+    # measured read ceiling (non-temporal 16-byte loads over 4 GiB)
+    buf = torch.empty(1 << 30, dtype=torch.int32, device="cuda:0").fill_(1)
+    read_ceiling = ctx.probe_read_bandwidth(buf, reps=10)
+    del buf
+    torch.cuda.empty_cache()
+    log(f"HBM read ceiling (plain read kernel): {read_ceiling:.0f} GB/s")
+
     if args.copy_probe:
         n = 1 << 30
         a = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
@@ -378,6 +385,8 @@ def main():
                      "achieved": round(head["gate_up_gbs"], 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(head["gate_up_gbs"] / HBM_PEAK_GBS, 4),
                      "avg_launch_us": round(gu_us, 3), "bytes_per_launch": head["gate_up_bytes"],
+                     "frac_of_measured_read_ceiling": round(head["gate_up_gbs"] / read_ceiling, 4),
+                     "measured_read_ceiling": round(read_ceiling, 1),
                      "traffic": committed_traffic(),
                      "traffic_source": "profiles/k_moe_gate_up_int4_c2_m1.md (FETCH_SIZE x2.0 + "
                                        "WRITE_SIZE x1.0 per dispatch, copy-scaled)"},

@@ -82,6 +82,14 @@ int32_t     ut_ctx_enable_timing(ut_ctx *ctx, int32_t on);
 int32_t     ut_ctx_kernel_time(ut_ctx *ctx, const char *prefix, int64_t *launches,
                                double *total_ms);
 
+/* Measurement helper (no counterpart in the reference; for roofline
+ * calibration): streams `bytes` of device memory at buf_dev with
+ * non-temporal 16-byte loads, `reps` times on the context's stream, and
+ * returns the read rate in GB/s.  bytes must be a positive multiple of 16
+ * and buf_dev 16-byte aligned. */
+int32_t     ut_probe_read_bandwidth(ut_ctx *ctx, const void *buf_dev, int64_t bytes, int32_t reps,
+                                    double *gbs);
+
 /* --------------------------------------------------------------- QTensor */
 /* QTensor::from_quantized (undertow-quant/src/qtensor.rs:85-138) /
  * read_qtensor (undertow-io/src/reader.rs:403-444): copies the payload

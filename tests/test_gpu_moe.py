@@ -139,17 +139,19 @@ def test_moe_experts_f32_weights(ctx):
     assert np.abs(got - want).max() <= 1e-5 * max(1.0, np.abs(want).max())
 
 
-def test_moe_experts_deepseek_shape(ctx):
-    """hidden 7168, inter 2048, top-8 of 16 loaded experts."""
+@pytest.mark.parametrize("fmt,Ms", [(INT4, (1, 2, 4)), (INT8, (1,))])
+def test_moe_experts_deepseek_shape(ctx, fmt, Ms):
+    """hidden 7168, inter 2048, top-8 of 16 loaded experts
+    (M = 1 takes the streaming gate/up kernel)."""
     rng = np.random.default_rng(1234)
     E, H, I, k = 16, 7168, 2048, 8
-    tbl, host_w = make_experts(ctx, rng, INT4, E, H, I)
-    for M in (1, 2, 4):
+    tbl, host_w = make_experts(ctx, rng, fmt, E, H, I)
+    for M in Ms:
         ids = np.stack([rng.permutation(E)[:k] for _ in range(M)]).astype(np.int32)
         w = rng.random((M, k)).astype(np.float32)
         x = rng.standard_normal((M, H)).astype(np.float32)
         got = host(tbl.moe_experts(dev(ids), dev(w), dev(x)))
-        want = oracle_moe(INT4, H, I, host_w, ids, w, x)
+        want = oracle_moe(fmt, H, I, host_w, ids, w, x)
         tol = 1e-4 * np.maximum(np.abs(want), 1.0)
         assert (np.abs(got - want) <= tol).all(), (M, np.abs(got - want).max())
 

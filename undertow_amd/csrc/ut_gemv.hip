@@ -6,10 +6,6 @@
 #include "ut_gemv_core.h"
 #include "ut_moe.h"
 
-// Weight steps in flight per lane in the plain GEMV (see gemv_core).
-#ifndef UT_GEMV_DEPTH
-#define UT_GEMV_DEPTH 1
-#endif
 
 namespace ut {
 
@@ -427,7 +423,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
     CoreOut<FMT, M, R> res;
     if (a.ks > 1) {
         const int64_t kb = (int64_t)blockIdx.z * a.kslice;
-        gemv_core<FMT, M, R, UT_GEMV_DEPTH>(rows, a.K, a.x, lds, res, kb, kb + a.kslice);
+        gemv_core<FMT, M, R, gemv_depth<M>()>(rows, a.K, a.x, lds, res, kb, kb + a.kslice);
 #pragma unroll
         for (int r = 0; r < R; r++)
 #pragma unroll
@@ -439,7 +435,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
             }
         return;
     }
-    gemv_core<FMT, M, R, UT_GEMV_DEPTH>(rows, a.K, a.x, lds, res);
+    gemv_core<FMT, M, R, gemv_depth<M>()>(rows, a.K, a.x, lds, res);
 #pragma unroll
     for (int r = 0; r < R; r++)
 #pragma unroll

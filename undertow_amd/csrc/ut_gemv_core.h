@@ -52,6 +52,18 @@ template <> struct FmtTraits<UT_FMT_F32> {
     static constexpr int kBytesPerCol2 = 8;
 };
 
+// Weight steps in flight per lane (the software-pipeline depth of
+// gemv_core): two for one activation row; more rows keep one, since their
+// accumulators leave no registers for a second step (measured on the
+// expert and dense shapes).  UT_GEMV_DEPTH overrides it for experiments.
+template <int M> __host__ __device__ constexpr int gemv_depth() {
+#ifdef UT_GEMV_DEPTH
+    return UT_GEMV_DEPTH;
+#else
+    return M == 1 ? 2 : 1;
+#endif
+}
+
 // Columns of one staged chunk: as many as fit kLdsWords for M rows.
 template <int FMT, int M>
 __host__ __device__ constexpr int gemv_chunk_cols() {
@@ -144,90 +156,180 @@ template <int FMT, int M, int R = kGemvRows> struct CoreOut {
     float F[R][M];
 };
 
-// rows[r]: byte pointer of row r (already clamped to a valid row).
-// K: columns (the caller's contract: int4 K % 32 == 0, int8 K % 16 == 0,
-// f32 K % 4 == 0, rows 16-byte aligned).
-//
-// The K loop is software-pipelined DEPTH steps deep: the weights of the
-// next DEPTH-1 steps are in flight while a step computes, and the first
-// loads are issued before the first activation chunk is staged, so the LDS
-// barrier does not drain the memory pipe.
-template <int FMT, int M, int R = kGemvRows, int DEPTH = 2>
-__device__ __forceinline__ void gemv_core(const uint8_t *const rows[R], int64_t K, const XSrc &x,
-                                          uint32_t *lds, CoreOut<FMT, M, R> &res,
-                                          int64_t k_begin = 0, int64_t k_end = -1) {
+// The pieces of the GEMV lane work, shared by the tiled kernels and the
+// streaming expert kernel:
+//   gemv_stage    stages columns [kc, kc+kcn) of the activations in LDS
+//                 (whole workgroup; barriers on both sides);
+//   GemvAcc       per-lane accumulators: compute() takes one step of R
+//                 weight rows (16 bytes each) against the staged chunk,
+//                 finish() reduces across the 16 sub-lanes of the row group.
+template <int FMT, int M>
+__device__ __forceinline__ void gemv_stage(const XSrc &x, uint32_t *lds, int64_t kc, int kcn) {
     using T = FmtTraits<FMT>;
     constexpr int KC = gemv_chunk_cols<FMT, M>();
     constexpr int PL = T::kPlanes;
-    constexpr int STEP = T::kStepCols;                 // columns per step (16 sub-lanes)
-    constexpr int LANE_COLS = STEP / 16;               // columns per lane per step
-    constexpr int LW = KC / T::kColsPerWord;           // LDS words per plane row
+    constexpr int LW = KC / T::kColsPerWord;  // LDS words per plane row
     const int tid = threadIdx.x;
-    const int s = tid & 15;
-
-    int32_t acc[R][M][PL];
-    float facc[R][M];
-#pragma unroll
-    for (int r = 0; r < R; r++)
-#pragma unroll
-        for (int m = 0; m < M; m++) {
-            facc[r][m] = 0.0f;
-#pragma unroll
-            for (int p = 0; p < PL; p++) acc[r][m][p] = 0;
+    __syncthreads();
+    if constexpr (FMT == UT_FMT_F32) {
+        const int n4 = kcn / 4;  // float4 per row
+        for (int i = tid; i < M * n4; i += kGemvThreads) {
+            int m = i / n4, c = i - m * n4;
+            float4 v = ld_global<float4>(x.xf + m * x.ldx + kc + 4 * c);
+            *(float4 *)(lds + m * KC + 4 * c) = v;
         }
-
-    auto load = [&](uint4 (&w)[R], int64_t col) {
-        if (col < K) {
-            const int64_t boff = col * T::kBytesPerCol2 / 2;
-#pragma unroll
-            for (int r = 0; r < R; r++) w[r] = ld_weights(rows[r] + boff);
+    } else if (x.dig) {
+        const int n4 = kcn / T::kColsPerWord / 4;  // uint4 per plane row
+        const int64_t w0 = kc / T::kColsPerWord;
+        for (int i = tid; i < M * PL * n4; i += kGemvThreads) {
+            int mp = i / n4, c = i - mp * n4;
+            uint4 v = ld_global<uint4>(x.dig + (int64_t)mp * x.KW + w0 + 4 * c);
+            *(uint4 *)(lds + mp * LW + 4 * c) = v;
         }
-    };
-    auto stage = [&](int64_t kc, int kcn) {
+    } else {
+        // digitise f32 activations into the LDS planes
+        constexpr int CPW = T::kColsPerWord;
+        const int ng = kcn / CPW;  // words per plane row in the chunk
+        for (int i = tid; i < M * ng; i += kGemvThreads) {
+            const int m = i / ng, g = i - m * ng;
+            const float *src = x.xf + m * x.ldx + kc + g * CPW;
+            float v[CPW];
+            if constexpr (CPW == 8) {
+                const float4 a = ld_global<float4>(src), b = ld_global<float4>(src + 4);
+                v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+                v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+            } else {
+                const float4 a = ld_global<float4>(src);
+                v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+            }
+            uint32_t w[PL];
+            // select, not index: a runtime index into x.sh would move the
+            // whole argument struct to scratch memory
+            const int32_t shm = m == 0 ? x.sh[0] : m == 1 ? x.sh[1] : m == 2 ? x.sh[2] : x.sh[3];
+            digit_words<FMT>(v, CPW, shm, w);
+#pragma unroll
+            for (int p = 0; p < PL; p++) lds[(m * PL + p) * LW + g] = w[p];
+        }
+    }
+    __syncthreads();
+}
+
+// gemv_stage for a range that is one whole chunk, split around `issue`:
+// every thread first loads its share of the chunk into registers
+// (unconditionally, from a clamped index, so the wait counts stay exact),
+// then `issue()` starts the caller's first weight loads, then the shares
+// go to LDS.  The activation loads (L2 hits) are older than the weight
+// loads, so the LDS writes wait for them alone and the weights stay in
+// flight across the barrier.
+template <int FMT, int M, typename Issue>
+__device__ __forceinline__ void gemv_stage_once(const XSrc &x, uint32_t *lds, int64_t kc, int kcn,
+                                                Issue &&issue) {
+    using T = FmtTraits<FMT>;
+    constexpr int KC = gemv_chunk_cols<FMT, M>();
+    constexpr int PL = T::kPlanes;
+    constexpr int CPW = T::kColsPerWord;
+    constexpr int LW = KC / CPW;
+    const int tid = threadIdx.x;
+    if constexpr (FMT == UT_FMT_F32) {
+        constexpr int NI = (M * (KC / 4) + kGemvThreads - 1) / kGemvThreads;
+        const int n4 = kcn / 4, tot = M * n4;
+        float4 v[NI];
+#pragma unroll
+        for (int j = 0; j < NI; j++) {
+            const int i = tid + j * kGemvThreads, ic = i < tot ? i : tot - 1;
+            const int m = ic / n4, c = ic - m * n4;
+            v[j] = ld_global<float4>(x.xf + m * x.ldx + kc + 4 * c);
+        }
+        issue();
         __syncthreads();
-        if constexpr (FMT == UT_FMT_F32) {
-            const int n4 = kcn / 4;  // float4 per row
-            for (int i = tid; i < M * n4; i += kGemvThreads) {
-                int m = i / n4, c = i - m * n4;
-                float4 v = ld_global<float4>(x.xf + m * x.ldx + kc + 4 * c);
-                *(float4 *)(lds + m * KC + 4 * c) = v;
+#pragma unroll
+        for (int j = 0; j < NI; j++) {
+            const int i = tid + j * kGemvThreads;
+            if (i < tot) {
+                const int m = i / n4, c = i - m * n4;
+                *(float4 *)(lds + m * KC + 4 * c) = v[j];
             }
-        } else if (x.dig) {
-            const int n4 = kcn / T::kColsPerWord / 4;  // uint4 per plane row
-            const int64_t w0 = kc / T::kColsPerWord;
-            for (int i = tid; i < M * PL * n4; i += kGemvThreads) {
-                int mp = i / n4, c = i - mp * n4;
-                uint4 v = ld_global<uint4>(x.dig + (int64_t)mp * x.KW + w0 + 4 * c);
-                *(uint4 *)(lds + mp * LW + 4 * c) = v;
+        }
+    } else if (x.dig) {
+        constexpr int NI = (M * PL * (LW / 4) + kGemvThreads - 1) / kGemvThreads;
+        const int n4 = kcn / CPW / 4, tot = M * PL * n4;
+        const int64_t w0 = kc / CPW;
+        uint4 v[NI];
+#pragma unroll
+        for (int j = 0; j < NI; j++) {
+            const int i = tid + j * kGemvThreads, ic = i < tot ? i : tot - 1;
+            const int mp = ic / n4, c = ic - mp * n4;
+            v[j] = ld_global<uint4>(x.dig + (int64_t)mp * x.KW + w0 + 4 * c);
+        }
+        issue();
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < NI; j++) {
+            const int i = tid + j * kGemvThreads;
+            if (i < tot) {
+                const int mp = i / n4, c = i - mp * n4;
+                *(uint4 *)(lds + mp * LW + 4 * c) = v[j];
             }
-        } else {
-            // digitise f32 activations into the LDS planes
-            constexpr int CPW = T::kColsPerWord;
-            const int ng = kcn / CPW;  // words per plane row in the chunk
-            for (int i = tid; i < M * ng; i += kGemvThreads) {
+        }
+    } else {
+        // digitise f32 activations into the LDS planes
+        constexpr int NI = (M * LW + kGemvThreads - 1) / kGemvThreads;
+        constexpr int NV = CPW / 4;  // float4 per word group
+        const int ng = kcn / CPW, tot = M * ng;
+        float4 v[NI][NV];
+#pragma unroll
+        for (int j = 0; j < NI; j++) {
+            const int i = tid + j * kGemvThreads, ic = i < tot ? i : tot - 1;
+            const int m = ic / ng, g = ic - m * ng;
+            const float *src = x.xf + m * x.ldx + kc + g * CPW;
+#pragma unroll
+            for (int q = 0; q < NV; q++) v[j][q] = ld_global<float4>(src + 4 * q);
+        }
+        issue();
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < NI; j++) {
+            const int i = tid + j * kGemvThreads;
+            if (i < tot) {
                 const int m = i / ng, g = i - m * ng;
-                const float *src = x.xf + m * x.ldx + kc + g * CPW;
-                float v[CPW];
-                if constexpr (CPW == 8) {
-                    const float4 a = ld_global<float4>(src), b = ld_global<float4>(src + 4);
-                    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-                    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-                } else {
-                    const float4 a = ld_global<float4>(src);
-                    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+                float f[CPW];
+#pragma unroll
+                for (int q = 0; q < NV; q++) {
+                    f[4 * q] = v[j][q].x; f[4 * q + 1] = v[j][q].y;
+                    f[4 * q + 2] = v[j][q].z; f[4 * q + 3] = v[j][q].w;
                 }
                 uint32_t w[PL];
-                // select, not index: a runtime index into x.sh would move the
-                // whole argument struct to scratch memory
                 const int32_t shm = m == 0 ? x.sh[0] : m == 1 ? x.sh[1] : m == 2 ? x.sh[2] : x.sh[3];
-                digit_words<FMT>(v, CPW, shm, w);
+                digit_words<FMT>(f, CPW, shm, w);
 #pragma unroll
                 for (int p = 0; p < PL; p++) lds[(m * PL + p) * LW + g] = w[p];
             }
         }
-        __syncthreads();
-    };
-    auto compute = [&](const uint4 (&wv)[R], int c0) {  // c0: column within the chunk
+    }
+    __syncthreads();
+}
+
+template <int FMT, int M, int R> struct GemvAcc {
+    using T = FmtTraits<FMT>;
+    static constexpr int KC = gemv_chunk_cols<FMT, M>();
+    static constexpr int PL = T::kPlanes;
+    static constexpr int LW = KC / T::kColsPerWord;
+    int32_t acc[R][M][PL];
+    float facc[R][M];
+
+    __device__ __forceinline__ void zero() {
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                facc[r][m] = 0.0f;
+#pragma unroll
+                for (int p = 0; p < PL; p++) acc[r][m][p] = 0;
+            }
+    }
+
+    // c0: this lane's first column within the staged chunk
+    __device__ __forceinline__ void compute(const uint32_t *lds, const uint4 (&wv)[R], int c0) {
         if constexpr (FMT == UT_FMT_F32) {
 #pragma unroll
             for (int m = 0; m < M; m++) {
@@ -269,16 +371,105 @@ __device__ __forceinline__ void gemv_core(const uint8_t *const rows[R], int64_t 
                 }
             }
         }
-    };
+    }
 
+    // reduce across the 16 sub-lanes of the row group
+    __device__ __forceinline__ void finish(CoreOut<FMT, M, R> &res) const {
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                if constexpr (FMT == UT_FMT_F32) {
+                    float v = facc[r][m];
+#pragma unroll
+                    for (int off = 8; off >= 1; off >>= 1) v += __shfl_xor(v, off, 16);
+                    res.F[r][m] = v;
+                    res.S[r][m] = 0;
+                } else {
+                    constexpr int SH = FMT == UT_FMT_INT4 ? 4 : 8;
+                    int64_t t = 0;
+#pragma unroll
+                    for (int p = PL - 1; p >= 0; p--) t = t * (1 << SH) + (int64_t)acc[r][m][p];
+#pragma unroll
+                    for (int off = 8; off >= 1; off >>= 1) t += shfl_xor_i64(t, off);
+                    res.S[r][m] = t;
+                    res.F[r][m] = 0.0f;
+                }
+            }
+    }
+};
+
+// One step of R weight rows for this lane (16 bytes each, at column col).
+template <int FMT, int R>
+__device__ __forceinline__ void gemv_load(const uint8_t *const rows[R], int64_t col, uint4 (&w)[R]) {
+    const int64_t boff = col * FmtTraits<FMT>::kBytesPerCol2 / 2;
+#pragma unroll
+    for (int r = 0; r < R; r++) w[r] = ld_weights(rows[r] + boff);
+}
+
+// rows[r]: byte pointer of row r (already clamped to a valid row).
+// K: columns (the caller's contract: int4 K % 32 == 0, int8 K % 16 == 0,
+// f32 K % 4 == 0, rows 16-byte aligned).
+//
+// The K loop is software-pipelined DEPTH steps deep: the weights of the
+// next DEPTH-1 steps are in flight while a step computes, and the first
+// loads are issued before the first activation chunk is staged, so the LDS
+// barrier does not drain the memory pipe.
+//
+// When the whole column range is one LDS chunk of whole steps (the expert
+// and most dense shapes) the activations are staged once and the loop has
+// no staging branch and no per-lane bounds: straight-line code in which
+// the compiler's wait counts keep the DEPTH-1 younger steps in flight (a
+// staging branch inside the loop makes it drain every load first).
+template <int FMT, int M, int R = kGemvRows, int DEPTH = gemv_depth<M>()>
+__device__ __forceinline__ void gemv_core(const uint8_t *const rows[R], int64_t K, const XSrc &x,
+                                          uint32_t *lds, CoreOut<FMT, M, R> &res,
+                                          int64_t k_begin = 0, int64_t k_end = -1) {
+    using T = FmtTraits<FMT>;
+    constexpr int KC = gemv_chunk_cols<FMT, M>();
+    constexpr int STEP = T::kStepCols;    // columns per step (16 sub-lanes)
+    constexpr int LANE_COLS = STEP / 16;  // columns per lane per step
+    const int s = threadIdx.x & 15;
+    GemvAcc<FMT, M, R> A;
+    A.zero();
     // columns [k_begin, k_end) (k_begin a multiple of STEP); K bounds loads.
-    // DEPTH steps of weights are in flight per lane: step t computes while
-    // steps t+1 .. t+DEPTH-1 are loading.
     const int64_t kend = k_end < 0 || k_end > K ? K : k_end;
     const int64_t nsteps = kend > k_begin ? (kend - k_begin + STEP - 1) / STEP : 0;
     const int64_t lane_col = k_begin + (int64_t)s * LANE_COLS;
     uint4 wq[DEPTH][R];
-    auto loadk = [&](uint4 (&w)[R], int64_t col) { if (col < kend) load(w, col); };
+    auto loadk = [&](uint4 (&w)[R], int64_t col) { if (col < kend) gemv_load<FMT, R>(rows, col, w); };
+    if (nsteps > 0 && kend - k_begin <= KC && (kend - k_begin) % STEP == 0) {
+        // unconditional (clamped) first loads: a skipped load on any path
+        // into the loop would make the wait counts inside it conservative
+        gemv_stage_once<FMT, M>(x, lds, k_begin, (int)(kend - k_begin), [&]() {
+#pragma unroll
+            for (int u = 0; u < DEPTH; u++)
+                gemv_load<FMT, R>(rows, lane_col + (u < nsteps ? u : nsteps - 1) * STEP, wq[u]);
+        });
+        const int c0 = s * LANE_COLS;
+        int64_t t = 0;
+        for (; t + 2 * DEPTH <= nsteps; t += DEPTH) {
+#pragma unroll
+            for (int u = 0; u < DEPTH; u++) {
+                A.compute(lds, wq[u], (int)((t + u) * STEP) + c0);
+                gemv_load<FMT, R>(rows, lane_col + (t + u + DEPTH) * STEP, wq[u]);
+                // keep the scheduler from sinking the loads below the next
+                // step's compute (which would drain the pipe every DEPTH steps)
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        // the last DEPTH..2*DEPTH-1 steps (fewer when nsteps < DEPTH)
+#pragma unroll
+        for (int i = 0; i < 2 * DEPTH; i++) {
+            if (t + i < nsteps) {
+                A.compute(lds, wq[i % DEPTH], (int)((t + i) * STEP) + c0);
+                if (t + i + DEPTH < nsteps)
+                    gemv_load<FMT, R>(rows, lane_col + (t + i + DEPTH) * STEP, wq[i % DEPTH]);
+            }
+        }
+        A.finish(res);
+        return;
+    }
 #pragma unroll
     for (int u = 0; u < DEPTH; u++) loadk(wq[u], lane_col + u * STEP);
     int64_t kc = k_begin, chunk_end = k_begin;
@@ -286,41 +477,19 @@ __device__ __forceinline__ void gemv_core(const uint8_t *const rows[R], int64_t 
 #pragma unroll
         for (int u = 0; u < DEPTH; u++) {
             if (t + u < nsteps) {
+                const int64_t cu = (t + u) * STEP + lane_col;
                 if (k_begin + (t + u) * STEP >= chunk_end) {
                     kc = k_begin + (t + u) * STEP;
                     const int kcn = (int)((kend - kc) < KC ? (kend - kc) : KC);
                     chunk_end = kc + kcn;
-                    stage(kc, kcn);
+                    gemv_stage<FMT, M>(x, lds, kc, kcn);
                 }
-                const int64_t cu = (t + u) * STEP + lane_col;
-                if (cu < kend) compute(wq[u], (int)(cu - kc));
+                if (cu < kend) A.compute(lds, wq[u], (int)(cu - kc));
                 loadk(wq[u], cu + DEPTH * STEP);
             }
         }
     }
-
-    // ---- reduce across the 16 sub-lanes of the row group
-#pragma unroll
-    for (int r = 0; r < R; r++)
-#pragma unroll
-        for (int m = 0; m < M; m++) {
-            if constexpr (FMT == UT_FMT_F32) {
-                float v = facc[r][m];
-#pragma unroll
-                for (int off = 8; off >= 1; off >>= 1) v += __shfl_xor(v, off, 16);
-                res.F[r][m] = v;
-                res.S[r][m] = 0;
-            } else {
-                constexpr int SH = FMT == UT_FMT_INT4 ? 4 : 8;
-                int64_t t = 0;
-#pragma unroll
-                for (int p = PL - 1; p >= 0; p--) t = t * (1 << SH) + (int64_t)acc[r][m][p];
-#pragma unroll
-                for (int off = 8; off >= 1; off >>= 1) t += shfl_xor_i64(t, off);
-                res.S[r][m] = t;
-                res.F[r][m] = 0.0f;
-            }
-        }
+    A.finish(res);
 }
 
 template <typename T, typename Op>

@@ -18,13 +18,6 @@
 #include "ut_gemv_core.h"
 #include "ut_moe.h"
 
-// Weight steps in flight per lane in the expert kernels (see gemv_core).
-#ifndef UT_GATE_UP_DEPTH
-#define UT_GATE_UP_DEPTH 1
-#endif
-#ifndef UT_DOWN_DEPTH
-#define UT_DOWN_DEPTH 1
-#endif
 
 namespace ut {
 
@@ -253,7 +246,7 @@ __device__ __forceinline__ void gate_up_body(const GateUpArgs &a, int u, int til
     const int64_t oc = o < a.I ? o : a.I - 1;
     const uint8_t *rows[2] = {gw + oc * a.row_bytes, uw + oc * a.row_bytes};
     CoreOut<FMT, M, 2> res;
-    gemv_core<FMT, M, 2, UT_GATE_UP_DEPTH>(rows, a.H, a.x, lds, res);
+    gemv_core<FMT, M, 2, gemv_depth<M>()>(rows, a.H, a.x, lds, res);
 #pragma unroll
     for (int m = 0; m < M; m++) {
         // f32: the gate value lives on sub-lane m, the up value on 4 + m
@@ -364,7 +357,7 @@ __device__ __forceinline__ void down_body(const DownArgs &a, int u, int tile, ui
     CoreOut<FMT, M, R> res;
     if (a.ks > 1) {
         const int64_t kb = (int64_t)blockIdx.z * a.kslice;
-        gemv_core<FMT, M, R, UT_DOWN_DEPTH>(rows, a.I, xs, lds, res, kb, kb + a.kslice);
+        gemv_core<FMT, M, R, gemv_depth<M>()>(rows, a.I, xs, lds, res, kb, kb + a.kslice);
         const int64_t slots = gridDim.y;
 #pragma unroll
         for (int r = 0; r < R; r++)
@@ -377,7 +370,7 @@ __device__ __forceinline__ void down_body(const DownArgs &a, int u, int tile, ui
             }
         return;
     }
-    gemv_core<FMT, M, R, UT_DOWN_DEPTH>(rows, a.I, xs, lds, res);
+    gemv_core<FMT, M, R, gemv_depth<M>()>(rows, a.I, xs, lds, res);
 #pragma unroll
     for (int r = 0; r < R; r++)
 #pragma unroll
