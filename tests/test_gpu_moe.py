@@ -17,7 +17,9 @@ pytestmark = pytest.mark.gpu
 
 # ------------------------------------------------------------------ router
 @pytest.mark.parametrize("E,k,ng,tg", [(256, 8, 8, 4), (8, 2, 4, 2), (16, 4, 4, 2), (64, 6, 1, 1),
-                                       (8, 2, 1, 1), (4, 2, 4, 2)])
+                                       (8, 2, 1, 1), (4, 2, 4, 2), (512, 8, 8, 4), (1024, 8, 8, 4),
+                                       (160, 8, 5, 2), (100, 6, 4, 2), (128, 8, 16, 4),
+                                       (64, 8, 64, 8), (2048, 8, 8, 4), (96, 8, 3, 1)])
 @pytest.mark.parametrize("bias", [False, True])
 def test_route_matches_oracle(ctx, E, k, ng, tg, bias):
     import undertow_amd as U
@@ -50,6 +52,37 @@ def test_route_ties_pick_lowest_index(ctx):
     logits = np.zeros((1, 32), np.float32)
     ids, _ = U.route(ctx, dev(logits), None, 8, 1, 1, True, 1.0)
     assert host(ids)[0].tolist() == list(range(8))
+
+
+@pytest.mark.parametrize("E,ng,tg", [(256, 8, 4), (8, 4, 2), (1024, 8, 4)])
+def test_route_ties_across_groups(ctx, E, ng, tg):
+    """Equal group scores rank by group index; equal scores inside the
+    eligible groups by expert index; masked (-inf) experts never win over
+    eligible ones."""
+    import undertow_amd as U
+    rng = np.random.default_rng(E)
+    rows = [np.zeros(E, np.float32),
+            np.repeat(rng.standard_normal(E // 4).astype(np.float32), 4),
+            np.tile(np.array([1.0, 0.5, 0.5, 1.0], np.float32), E // 4)]
+    logits = np.stack(rows)
+    k = min(8, E)
+    ids, w = U.route(ctx, dev(logits), None, k, ng, tg, True, 1.0)
+    ids, w = host(ids), host(w)
+    for r in range(len(rows)):
+        oid, ow = O.route(logits[r], None, k, ng, tg, True, 1.0)
+        assert ids[r].tolist() == oid.tolist()
+        assert np.abs(w[r] - ow).max() <= 1e-6
+
+
+def test_route_k_above_expert_count(ctx):
+    """k > E: the E experts in order, then id -1 / weight 0 slots."""
+    import undertow_amd as U
+    logits = np.array([[0.5, -1.0, 2.0, 0.1]], np.float32)
+    ids, w = U.route(ctx, dev(logits), None, 6, 1, 1, True, 1.0)
+    ids, w = host(ids)[0], host(w)[0]
+    oid, ow = O.route(logits[0], None, 6, 1, 1, True, 1.0)
+    assert ids[:4].tolist() == oid[:4].tolist() and ids[4:].tolist() == [-1, -1]
+    assert np.abs(w[:4] - ow[:4]).max() <= 1e-6 and w[4:].tolist() == [0.0, 0.0]
 
 
 # ------------------------------------------------------------------ argmax

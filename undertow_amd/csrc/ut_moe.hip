@@ -117,6 +117,178 @@ __device__ __forceinline__ void route_row(const float *__restrict__ lg,
     __syncthreads();
 }
 
+// ------------------------------------------------------ wave router ---
+// The same routing by one wavefront: lane l holds experts
+// [l*KPL, l*KPL + KPL), and every selection is a cross-lane max of 64-bit
+// keys = order-preserving value bits above the complemented expert index,
+// so the largest key is the largest value with the lowest index (the
+// order of topk_indices, undertow-core/src/router.rs:136-163).  The group
+// scores come from max reductions over each group's run of lanes.  -0 is
+// keyed as +0 (the two compare equal in the reference).  Taken when
+// E <= 64*KPL and, with group limitation, E = n_group * gs with gs a
+// power-of-two multiple of KPL (gs/KPL <= 64 lanes per group).
+
+__device__ __forceinline__ uint32_t order_bits(float v) {
+    const uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float order_value(uint32_t h) {
+    return __uint_as_float((h & 0x80000000u) ? (h & 0x7fffffffu) : ~h);
+}
+__device__ __forceinline__ uint64_t route_key(float v, int e) {
+    return ((uint64_t)order_bits(v) << 32) | (uint64_t)(uint32_t)~(uint32_t)e;
+}
+
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xF, false);
+}
+// max over aligned runs of LG lanes, valid in the run's last lane (and in
+// every lane of the run for LG <= 16)
+template <int LG>
+__device__ __forceinline__ uint32_t run_max_u32(uint32_t v) {
+    if constexpr (LG >= 2) v = max(v, dpp_u32<0xB1>(v));        // quad_perm 1,0,3,2
+    if constexpr (LG >= 4) v = max(v, dpp_u32<0x4E>(v));        // quad_perm 2,3,0,1
+    if constexpr (LG >= 8) v = max(v, dpp_u32<0x141>(v));       // row_half_mirror
+    if constexpr (LG >= 16) v = max(v, dpp_u32<0x140>(v));      // row_mirror
+    if constexpr (LG >= 32) v = max(v, dpp_u32<0x142, 0xA>(v)); // row_bcast15
+    if constexpr (LG >= 64) v = max(v, dpp_u32<0x143, 0xC>(v)); // row_bcast31
+    return v;
+}
+// the run's maximum key in every lane of the run
+template <int LG>
+__device__ __forceinline__ uint64_t run_max_key(uint64_t k) {
+    const int lane = threadIdx.x & 63, last = lane | (LG - 1);
+    uint32_t hi = run_max_u32<LG>((uint32_t)(k >> 32));
+    if constexpr (LG == 64) hi = __builtin_amdgcn_readlane(hi, 63);
+    else if constexpr (LG == 32) hi = __shfl(hi, last, 64);
+    uint32_t lo = run_max_u32<LG>((uint32_t)(k >> 32) == hi ? (uint32_t)k : 0u);
+    if constexpr (LG == 64) lo = __builtin_amdgcn_readlane(lo, 63);
+    else if constexpr (LG == 32) lo = __shfl(lo, last, 64);
+    return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t run_max_key_rt(uint64_t k, int LG) {
+    switch (LG) {
+    case 1: return k;
+    case 2: return run_max_key<2>(k);
+    case 4: return run_max_key<4>(k);
+    case 8: return run_max_key<8>(k);
+    case 16: return run_max_key<16>(k);
+    case 32: return run_max_key<32>(k);
+    default: return run_max_key<64>(k);
+    }
+}
+
+static bool route_wave_ok(int64_t E, int n_group, int topk_group, int k, int *kpl) {
+    int p = E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : E <= 1024 ? 16 : 0;
+    if (!p || k > 64) return false;
+    *kpl = p;
+    if (!(n_group > 1 && topk_group < n_group)) return true;
+    if (E % n_group) return false;
+    const int64_t gs = E / n_group, lg = gs / p;
+    return gs % p == 0 && lg >= 1 && lg <= 64 && (lg & (lg - 1)) == 0;
+}
+
+// Routes one row with one wavefront (all 64 lanes active).  Lane r < k
+// returns choice r in *my_id / *my_w (id -1, weight 0 past E).
+template <int KPL>
+__device__ __forceinline__ void route_row_wave(const float *__restrict__ lg,
+                                               const float *__restrict__ bias, int E, int k,
+                                               int n_group, int topk_group, int norm, float scale,
+                                               int32_t *my_id, float *my_w) {
+    const int lane = threadIdx.x & 63;
+    float sc[KPL];
+    uint64_t key[KPL];
+#pragma unroll
+    for (int j = 0; j < KPL; j++) {
+        const int e = lane * KPL + j;
+        if (e < E) {
+            const float s = 1.0f / (1.0f + expf(-lg[e]));  // sigmoid (undertow-quant/src/lib.rs:116)
+            sc[j] = s;
+            key[j] = route_key(bias ? __fadd_rn(s, bias[e]) : s, e);
+        } else {
+            sc[j] = 0.0f;
+            key[j] = 0;  // below every expert's key
+        }
+    }
+    if (n_group > 1 && topk_group < n_group) {
+        const int gs = E / n_group, LG = gs / KPL;
+        uint64_t b = key[0];
+#pragma unroll
+        for (int j = 1; j < KPL; j++) b = key[j] > b ? key[j] : b;
+        const uint64_t m1 = run_max_key_rt(b, LG);
+        uint64_t b2 = 0;
+#pragma unroll
+        for (int j = 0; j < KPL; j++) b2 = key[j] != m1 && key[j] > b2 ? key[j] : b2;
+        const uint64_t m2 = run_max_key_rt(b2, LG);
+        // group score = sum of the group's top-2 in topk order
+        float gsum = 0.0f + order_value((uint32_t)(m1 >> 32));
+        if (gs > 1) gsum = gsum + order_value((uint32_t)(m2 >> 32));
+        const int g = lane / LG;
+        const uint64_t gk = route_key(gsum, g);
+        int rank = 0;
+        for (int g2 = 0; g2 < n_group; g2++) {
+            const int src = g2 * LG;
+            const uint64_t o = ((uint64_t)(uint32_t)__shfl((int)(gk >> 32), src, 64) << 32) |
+                               (uint32_t)__shfl((int)(uint32_t)gk, src, 64);
+            rank += o > gk;
+        }
+        if (rank >= topk_group) {
+#pragma unroll
+            for (int j = 0; j < KPL; j++)
+                if (lane * KPL + j < E) key[j] = route_key(-INFINITY, lane * KPL + j);
+        }
+    }
+    const int keff = k < E ? k : E;
+    float denom = 0.0f;
+    int32_t id = -1;
+    float wv = 0.0f;
+    for (int r = 0; r < keff; r++) {
+        uint64_t b = key[0];
+#pragma unroll
+        for (int j = 1; j < KPL; j++) b = key[j] > b ? key[j] : b;
+        const uint64_t win = run_max_key<64>(b);
+        const int e = (int)~(uint32_t)win;
+        float sv = 0.0f;
+#pragma unroll
+        for (int j = 0; j < KPL; j++) {
+            if (key[j] == win) key[j] = 0;
+            if (lane * KPL + j == e) sv = sc[j];
+        }
+        sv = __shfl(sv, e / KPL, 64);
+        denom = denom + sv;  // sequential sum in choice order
+        if (lane == r) { id = e; wv = sv; }
+    }
+    // weights = sigmoid of the chosen, normalised by their sum (+1e-20)
+    denom = denom + 1e-20f;
+    if (lane < k) {
+        if (lane < keff) {
+            *my_id = id;
+            *my_w = __fmul_rn(norm ? wv / denom : wv, scale);
+        } else {  // k > E: no expert (contributes nothing)
+            *my_id = -1;
+            *my_w = 0.0f;
+        }
+    }
+}
+
+template <int KPL>
+__global__ __launch_bounds__(64) void k_route_wave(const float *__restrict__ logits,
+                                                   const float *__restrict__ bias, int E, int k,
+                                                   int n_group, int topk_group, int norm,
+                                                   float scale, int32_t *__restrict__ ids,
+                                                   float *__restrict__ weights) {
+    const int row = blockIdx.x, lane = threadIdx.x;
+    int32_t id = -1;
+    float w = 0.0f;
+    route_row_wave<KPL>(logits + (int64_t)row * E, bias, E, k, n_group, topk_group, norm, scale,
+                        &id, &w);
+    if (lane < k) {
+        ids[(int64_t)row * k + lane] = id;
+        weights[(int64_t)row * k + lane] = w;
+    }
+}
+
 __global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
                                                const float *__restrict__ bias, int E, int k,
                                                int n_group, int topk_group, int norm,
@@ -171,6 +343,46 @@ __global__ __launch_bounds__(256) void k_route_plan(const float *__restrict__ lo
     make_plan(s_all, M, k, E, tbl, -1, plan, err_flag);
 }
 
+// k_route_plan with the wave router: wave r routes row r (M <= 4).
+template <int KPL>
+__global__ __launch_bounds__(256) void k_route_plan_wave(const float *__restrict__ logits,
+                                                         const int64_t *__restrict__ part, int ks,
+                                                         const float *__restrict__ bias, int M,
+                                                         int E, int k, int n_group, int topk_group,
+                                                         int norm, float scale,
+                                                         int32_t *__restrict__ ids,
+                                                         float *__restrict__ weights,
+                                                         const void *const *__restrict__ tbl,
+                                                         MoePlan plan, int32_t *__restrict__ err_flag) {
+    extern __shared__ float s_lg[];  // [M][E] logits
+    __shared__ int32_t s_all[4 * 64];
+    for (int i = threadIdx.x; i < M * E; i += blockDim.x) {
+        float v;
+        if (part) {
+            v = __uint_as_float((uint32_t)part[i]);
+#pragma unroll 16
+            for (int z = 1; z < ks; z++) v = __fadd_rn(v, __uint_as_float((uint32_t)part[(int64_t)z * M * E + i]));
+        } else {
+            v = logits[i];
+        }
+        s_lg[i] = v;
+    }
+    __syncthreads();
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (wave < M) {
+        int32_t id = -1;
+        float w = 0.0f;
+        route_row_wave<KPL>(s_lg + wave * E, bias, E, k, n_group, topk_group, norm, scale, &id, &w);
+        if (lane < k) {
+            ids[(int64_t)wave * k + lane] = id;
+            weights[(int64_t)wave * k + lane] = w;
+            s_all[wave * k + lane] = id;
+        }
+    }
+    __syncthreads();
+    make_plan(s_all, M, k, E, tbl, -1, plan, err_flag);
+}
+
 __global__ __launch_bounds__(256) void k_moe_plan(const int32_t *__restrict__ ids, int M, int k, int E,
                            const void *const *__restrict__ tbl, int extra_slot,
                            MoePlan plan, int32_t *__restrict__ err_flag) {
@@ -183,9 +395,25 @@ int32_t launch_route(ut_ctx *ctx, const float *logits, const float *bias, int64_
     if (rows <= 0) return UT_OK;
     size_t shmem = (size_t)(2 * E + (n_group > 0 ? n_group : 1)) * sizeof(float);
     int tok = timing_begin(ctx, "route");
-    hipLaunchKernelGGL(k_route, dim3((unsigned)rows), dim3(256), shmem, ctx->stream, logits, bias,
-                       (int)E, (int)k, (int)n_group, (int)topk_group, (int)norm, scale, ids,
-                       weights);
+    int kpl = 0;
+    if (route_wave_ok(E, n_group, topk_group, k, &kpl)) {
+#define UT_ROUTE_W(P)                                                                          \
+    hipLaunchKernelGGL(k_route_wave<P>, dim3((unsigned)rows), dim3(64), 0, ctx->stream, logits, \
+                       bias, (int)E, (int)k, (int)n_group, (int)topk_group, (int)norm, scale, ids, \
+                       weights)
+        switch (kpl) {
+        case 1: UT_ROUTE_W(1); break;
+        case 2: UT_ROUTE_W(2); break;
+        case 4: UT_ROUTE_W(4); break;
+        case 8: UT_ROUTE_W(8); break;
+        default: UT_ROUTE_W(16); break;
+        }
+#undef UT_ROUTE_W
+    } else {
+        hipLaunchKernelGGL(k_route, dim3((unsigned)rows), dim3(256), shmem, ctx->stream, logits, bias,
+                           (int)E, (int)k, (int)n_group, (int)topk_group, (int)norm, scale, ids,
+                           weights);
+    }
     timing_end(ctx, tok);
     return launch_check(ctx, "k_route");
 }
@@ -207,10 +435,27 @@ int32_t launch_route_plan(ut_ctx *ctx, const float *logits, const SplitKPartials
     }
     size_t shmem = (size_t)(2 * E + (n_group > 0 ? n_group : 1) + M * E) * sizeof(float);
     int tok = timing_begin(ctx, "route_plan");
-    hipLaunchKernelGGL(k_route_plan, dim3(1), dim3(256), shmem, ctx->stream, logits,
-                       split ? (const int64_t *)parts->part : nullptr, split ? parts->ks : 1, bias, M,
-                       (int)E, (int)k, (int)n_group, (int)topk_group, (int)norm, scale, ids,
-                       weights, tbl, plan, err_flag);
+    int kpl = 0;
+    if (route_wave_ok(E, n_group, topk_group, k, &kpl)) {
+#define UT_ROUTE_PW(P)                                                                           \
+    hipLaunchKernelGGL(k_route_plan_wave<P>, dim3(1), dim3(256), (size_t)M * E * sizeof(float),   \
+                       ctx->stream, logits, split ? (const int64_t *)parts->part : nullptr,      \
+                       split ? parts->ks : 1, bias, M, (int)E, (int)k, (int)n_group,              \
+                       (int)topk_group, (int)norm, scale, ids, weights, tbl, plan, err_flag)
+        switch (kpl) {
+        case 1: UT_ROUTE_PW(1); break;
+        case 2: UT_ROUTE_PW(2); break;
+        case 4: UT_ROUTE_PW(4); break;
+        case 8: UT_ROUTE_PW(8); break;
+        default: UT_ROUTE_PW(16); break;
+        }
+#undef UT_ROUTE_PW
+    } else {
+        hipLaunchKernelGGL(k_route_plan, dim3(1), dim3(256), shmem, ctx->stream, logits,
+                           split ? (const int64_t *)parts->part : nullptr, split ? parts->ks : 1, bias, M,
+                           (int)E, (int)k, (int)n_group, (int)topk_group, (int)norm, scale, ids,
+                           weights, tbl, plan, err_flag);
+    }
     timing_end(ctx, tok);
     return launch_check(ctx, "k_route_plan");
 }
