@@ -141,32 +141,42 @@ __global__ __launch_bounds__(256) void k_mla_combine(const float *__restrict__ p
 }
 
 // ------------------------------------------------------ MFMA variant ---
-// For DeepSeek-V3-like shapes (heads % 32 == 0, L % 128 == 0,
-// (L + P) % 64 == 0) the score and context contractions run on the bf16
-// matrix cores.  Each f32 operand x is split into x_hi = bf16(x) and
-// x_lo = bf16(x - x_hi), and a product is taken as hi*hi + hi*lo + lo*hi
-// (f32 accumulation), which keeps about 16 significant bits per product
-// term instead of bf16's 8.
+// For the DeepSeek-V3 shape (heads % 32 == 0, latent 512 + rope 64) the
+// score and context contractions run on the bf16 matrix cores.  Each f32
+// operand x is split into x_hi = bf16(x) and x_lo = bf16(x - x_hi), and a
+// product is taken as hi*hi + hi*lo + lo*hi (f32 accumulation), which keeps
+// about 16 significant bits per product term instead of bf16's 8.  The
+// cache is kept in that split form ([T][2][L+P] bf16: the hi plane, then
+// the lo plane of each position).
 //
 // Work split.  A column is one (query row r, head h) pair, c = r*H + h; a
-// workgroup takes 32 columns (all of one query row, since H % 32 == 0) and
-// one slice of positions, 32 positions per tile:
-//   scores  S^T[pos x col] = K[pos x (L+P)] . Q^T[(L+P) x col]
-//           (v_mfma_f32_32x32x16_bf16, A = cache rows straight from global
-//           memory, B = the workgroup's queries held in registers); wave w
-//           reduces over dims [w*D/4, (w+1)*D/4) and the four partial tiles
-//           are summed through LDS in wave order;
-//   softmax online over the slice's tiles (running max m and sum l per
-//           column, exp with the fast exponential);
-//   context O^T[L x col] += V^T[L x pos] . P[pos x col] with V = the latent
-//           rows; wave w owns dims [w*L/4, (w+1)*L/4) in 32-row m-tiles.
+// workgroup (k_mla_mfma16) takes 32 columns of one query row and one slice
+// of positions, 16 positions per tile:
+//   copy    the tile's 16 cache rows (36 KiB) go straight from global
+//           memory to LDS (global_load_lds), double-buffered: the next
+//           tile's copy is issued between this tile's score steps;
+//   scores  S^T[pos x col] = K[pos x (L+P)] . Q^T[(L+P) x col] with
+//           v_mfma_f32_16x16x32_bf16; wave w takes column block w&1 over
+//           dim half w>>1 (queries held in registers), the two halves are
+//           summed through LDS;
+//   softmax online, per column; the exponent offset moves only when a
+//           score exceeds it by more than kMlaHeadroom (so the context is
+//           rescaled on such jumps only);
+//   context O^T[L x col] += V^T[L x pos] . P[pos x col] with
+//           v_mfma_f32_32x32x16_bf16; wave w owns latent dims
+//           [128w, 128w + 128); V^T comes from the tile's rows in LDS by the
+//           transposing read (ds_read_b64_tr_b16: within each 16-lane group,
+//           lane j supplies 4 consecutive dims of row 4q + j/4 and lane i
+//           receives dim i of the group's 4 rows).
+// LDS rows keep their 16-byte chunks XOR-swizzled by a permutation of the
+// row's low 3 bits, which leaves both read patterns free of bank conflicts.
+// 76 KiB of LDS and < 256 registers per lane let two workgroups share a CU.
 // The slice writes (m, l, O) to the partial buffers, k_mla_combine_mfma
 // merges the slices.  The slice length depends only on the row's context
 // length, so a row's result is the same whichever rows share the call.
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-constexpr int kMfmaTile = 32;
 
 __host__ __device__ inline int64_t mla_mfma_slice(int64_t n_ctx) {
     int64_t q = n_ctx / 64, s = 1;
@@ -199,24 +209,45 @@ struct MlaMfmaArgs {
     float *part_m, *part_l, *part_o;  // [j][col], [j][col], [j][L][col]
 };
 
-// KS: k-steps (16 dims) per wave for the scores, (L+P) = 64*KS;
-// MT: 32-dim m-tiles per wave for the context, L = 128*MT.
-//
-// Per 32-position tile: the tile's cache rows are in registers in the score
-// operand layout (bf16 hi and lo, loaded during the previous tile, while the
-// next tile loads into a second register set); the score MFMAs run; the
-// latent part is written to LDS transposed ([dim][position]) for the
-// context operand; then the softmax and context MFMAs.
-constexpr int kVPitch = kMfmaTile + 8;  // bf16 per LDS row of the transposed tile
+constexpr int kRowChunks = 144;       // 16-byte chunks per position (576 hi + 576 lo)
+constexpr float kMlaHeadroom = 8.0f;  // nats a score may exceed the running offset
 
-template <int KS, int MT>
-__global__ __launch_bounds__(256) void k_mla_mfma(MlaMfmaArgs a) {
-    constexpr int LMAX = 128 * MT;
-    constexpr int D = 64 * KS;
-    __shared__ float sS[4][kMfmaTile][kMfmaTile + 1];
-    __shared__ __attribute__((aligned(16))) __bf16 sVh[LMAX * kVPitch];
-    __shared__ __attribute__((aligned(16))) __bf16 sVl[LMAX * kVPitch];
-    // XCD-aware order: the column groups of one slice share blockIdx % 8
+__device__ __forceinline__ int mla_swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+__device__ __forceinline__ int mla_slot(int r, int c) { return r * kRowChunks + (c ^ mla_swz(r)); }
+
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4_t;
+__device__ __forceinline__ bf16x8_t tr_pair(const uint8_t *lds_a, const uint8_t *lds_b) {
+    const bf16x4_t x = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+        (lds_bf16x4_t *)(__attribute__((address_space(3))) uint8_t *)lds_a);
+    const bf16x4_t y = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+        (lds_bf16x4_t *)(__attribute__((address_space(3))) uint8_t *)lds_b);
+    return __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// Lanes l and l ^ 32 combined without an LDS round trip: permlane32_swap
+// of (v, v) returns the low halves of both operands in one register and the
+// high halves in the other, so max / sum of the two is the pair's result in
+// every lane (and the same sum order in both lanes).
+__device__ __forceinline__ float pair_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __fadd_rn(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+constexpr int kTile16 = 16;
+constexpr int kTile16Bytes = kTile16 * kRowChunks * 16;  // 36864
+
+__global__ __launch_bounds__(256, 2) void k_mla_mfma16(MlaMfmaArgs a) {
+    constexpr int KS = 9, MT = 4, D = 576;
+    typedef __bf16 bf16x8l_t __attribute__((ext_vector_type(8)));
+    typedef float f32x4l_t __attribute__((ext_vector_type(4)));
+    __shared__ __attribute__((aligned(16))) uint8_t sT0[kTile16Bytes];
+    __shared__ __attribute__((aligned(16))) uint8_t sT1[kTile16Bytes];
+    __shared__ __attribute__((aligned(16))) float sS[2][32][kTile16];  // [dim half][column][position]
     const int b = blockIdx.x, x8 = b & 7, q = b >> 3;
     const int group = q % a.groups;
     const int slice = (q / a.groups) * 8 + x8;
@@ -226,20 +257,23 @@ __global__ __launch_bounds__(256) void k_mla_mfma(MlaMfmaArgs a) {
     const int64_t slen = mla_mfma_slice(n_ctx);
     const int64_t p0 = (int64_t)slice * slen;
     if (slice >= a.nslice || p0 >= n_ctx) return;  // uniform per workgroup
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, half = l >> 5, n = l & 31;
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+    const int cb = w & 1, dh = w >> 1;
     const int L = a.L, P = a.P;
-    const int col = c0 + n;
-    const int dlane = w * (16 * KS) + 8 * half;  // this lane's first score dim
-
-    // queries of this lane's column, dims dlane + 16*ks + [0, 8)
-    bf16x8_t qh[KS], ql[KS];
+    // score operand lanes: column 16*cb + (l & 15), dims 288*dh + 32*ks + 8*(l >> 4)
+    const int qcol = c0 + 16 * cb + (l & 15);
+    const int qd0 = 288 * dh + 8 * (l >> 4);
+    bf16x8l_t qh[KS], ql[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ks++) {
-        const int d0 = dlane + 16 * ks;
+        const int d0 = qd0 + 32 * ks;
         float v[8];
-        load8(d0 < L ? a.qabs + (int64_t)col * L + d0 : a.qrope + (int64_t)col * P + (d0 - L), v);
+        load8(d0 < L ? a.qabs + (int64_t)qcol * L + d0 : a.qrope + (int64_t)qcol * P + (d0 - L), v);
         split8(v, qh[ks], ql[ks]);
     }
+    // context lanes: column l & 31, positions 8*(l >> 5) + [0, 8)
+    const int n = l & 31, kh = l >> 5;
+    const int col = c0 + n;
     f32x16_t o[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
@@ -249,64 +283,67 @@ __global__ __launch_bounds__(256) void k_mla_mfma(MlaMfmaArgs a) {
     const int64_t tend = p0 + slen < n_ctx ? p0 + slen : n_ctx;
     const uint32_t last = (uint32_t)(n_ctx - 1);
 
-    // the tile's cache rows in the score operand layout (lane: position n);
-    // two register sets: tile t computes while tile t+1 loads
-    bf16x8_t kh[KS], kl[KS], nh[KS], nl[KS];
-    auto load_tile = [&](uint32_t t0, bf16x8_t (&h)[KS], bf16x8_t (&lo)[KS]) {
-        const uint32_t pos = t0 + n <= last ? t0 + n : last;
-        const __bf16 *row = a.kc + (size_t)pos * (2 * D) + dlane;
-#pragma unroll
-        for (int ks = 0; ks < KS; ks++) {
-            h[ks] = *(const bf16x8_t *)(row + 16 * ks);
-            lo[ks] = *(const bf16x8_t *)(row + D + 16 * ks);
-        }
+    // wave w copies slots [w*9*64, (w+1)*9*64) of a tile (part i: one 1 KiB run)
+    auto copy_part = [&](uint32_t t0, uint8_t *dst, int i) {
+        const int s0 = (w * 9 + i) * 64, sl = s0 + l;
+        const int rr = sl / kRowChunks, phy = sl - rr * kRowChunks;
+        const int c = phy ^ mla_swz(rr);
+        const uint32_t pos = t0 + rr <= last ? t0 + rr : last;
+        const __bf16 *src = a.kc + (size_t)pos * (2 * D) + c * 8;
+        __builtin_amdgcn_global_load_lds((const void *)src,
+                                         (__attribute__((address_space(3))) void *)(dst + s0 * 16),
+                                         16, 0, 0);
     };
-    load_tile((uint32_t)p0, kh, kl);
-
-    for (int64_t t0 = p0; t0 < tend; t0 += kMfmaTile) {
-        // ---- the next tile's loads overlap this whole tile
-        const bool more = t0 + kMfmaTile < tend;
-        if (more) load_tile((uint32_t)(t0 + kMfmaTile), nh, nl);
-        // ---- partial scores over this wave's dims; latent dims to LDS
-        f32x16_t sc;
 #pragma unroll
-        for (int i = 0; i < 16; i++) sc[i] = 0.0f;
+    for (int i = 0; i < 9; i++) copy_part((uint32_t)p0, sT0, i);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+
+    auto tile = [&](const uint8_t *T, uint8_t *Nx, int64_t t0) {
+        const bool more = t0 + kTile16 < tend;
+        const uint32_t tn = (uint32_t)(t0 + kTile16);
+        // ---- partial scores: 16 positions x this wave's 16 columns, its dim half
+        // three independent accumulator chains (hi*hi, hi*lo, lo*hi), summed
+        // at the end, keep the matrix pipe busy
+        f32x4l_t sa = {0.0f, 0.0f, 0.0f, 0.0f}, sb = sa, sd = sa;
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
-            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh[ks], qh[ks], sc, 0, 0, 0);
-            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh[ks], ql[ks], sc, 0, 0, 0);
-            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kl[ks], qh[ks], sc, 0, 0, 0);
-            const int d0 = dlane + 16 * ks;
-            if (d0 < L) {
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    sVh[(d0 + j) * kVPitch + n] = kh[ks][j];
-                    sVl[(d0 + j) * kVPitch + n] = kl[ks][j];
-                }
-            }
+            if (more) copy_part(tn, Nx, ks);
+            const int ch = 36 * dh + 4 * ks + (l >> 4);
+            const bf16x8l_t kh8 = *(const bf16x8l_t *)(T + mla_slot(l & 15, ch) * 16);
+            const bf16x8l_t kl8 = *(const bf16x8l_t *)(T + mla_slot(l & 15, 72 + ch) * 16);
+            sa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh8, qh[ks], sa, 0, 0, 0);
+            sb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh8, ql[ks], sb, 0, 0, 0);
+            sd = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl8, qh[ks], sd, 0, 0, 0);
         }
-        // ---- sum the four waves' partial tiles in wave order
-        // C layout: register i holds position row (i/4)*8 + half*4 + i%4, column n
+        f32x4l_t sc;
 #pragma unroll
-        for (int i = 0; i < 16; i++) sS[w][(i >> 2) * 8 + half * 4 + (i & 3)][n] = sc[i];
-        __syncthreads();
-        float p[16];
-        const int64_t live = n_ctx - t0;  // rows pr < live are inside the context
+        for (int i = 0; i < 4; i++) sc[i] = __fadd_rn(sa[i], __fadd_rn(sb[i], sd[i]));
+        // C layout: register i holds position 4*(l >> 4) + i, column l & 15
+        *(f32x4l_t *)&sS[dh][16 * cb + (l & 15)][4 * (l >> 4)] = sc;
+        // an LDS-only barrier (the fence of __syncthreads would also wait
+        // for the next tile's copy)
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        // ---- this lane's 8 positions of column n, dim halves summed in order
+        const f32x4l_t a0 = *(const f32x4l_t *)&sS[0][n][8 * kh];
+        const f32x4l_t a1 = *(const f32x4l_t *)&sS[0][n][8 * kh + 4];
+        const f32x4l_t b0 = *(const f32x4l_t *)&sS[1][n][8 * kh];
+        const f32x4l_t b1 = *(const f32x4l_t *)&sS[1][n][8 * kh + 4];
+        const int live = n_ctx - t0 < kTile16 ? (int)(n_ctx - t0) : kTile16;
+        float p[8];
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int pr = (i >> 2) * 8 + half * 4 + (i & 3);
-            float v = __fadd_rn(__fadd_rn(__fadd_rn(sS[0][pr][n], sS[1][pr][n]), sS[2][pr][n]), sS[3][pr][n]);
-            p[i] = pr < live ? __fmul_rn(v, a.scale) : -INFINITY;
+        for (int e = 0; e < 8; e++) {
+            const float v = __fadd_rn(e < 4 ? a0[e] : a1[e - 4], e < 4 ? b0[e] : b1[e - 4]);
+            p[e] = __fadd_rn(__fmul_rn(v, a.scale), 8 * kh + e < live ? 0.0f : -INFINITY);
         }
-        // ---- online softmax per column (lanes n and n + 32 share a column)
         float mt_ = p[0];
 #pragma unroll
-        for (int i = 1; i < 16; i++) mt_ = fmaxf(mt_, p[i]);
-        mt_ = fmaxf(mt_, __shfl_xor(mt_, 32, 64));
-        const float m_new = fmaxf(m_run, mt_);  // finite: position t0 is live
-        // the context only needs rescaling when a column's maximum moved
-        // (alpha is exactly 1 otherwise)
-        if (__any(m_new != m_run)) {
+        for (int e = 1; e < 8; e++) mt_ = fmaxf(mt_, p[e]);
+        mt_ = pair_max(mt_);
+        // the exponent offset moves only on a jump of more than kMlaHeadroom
+        const bool jump = mt_ > m_run + kMlaHeadroom;
+        const float m_new = jump ? mt_ : m_run;
+        if (__any(jump)) {
             const float alpha = __expf(m_run - m_new);
             l_run *= alpha;
 #pragma unroll
@@ -316,59 +353,44 @@ __global__ __launch_bounds__(256) void k_mla_mfma(MlaMfmaArgs a) {
         }
         float ls = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            p[i] = __expf(p[i] - m_new);
-            ls += p[i];
+        for (int e = 0; e < 8; e++) {
+            p[e] = __expf(p[e] - m_new);
+            ls += p[e];
         }
-        ls += __shfl_xor(ls, 32, 64);
+        ls = pair_sum(ls);
         l_run += ls;
         m_run = m_new;
-        // ---- P as the B operand: lane (half, n) needs positions 16*ks + 8*half + [0, 8)
-        bf16x8_t ph[2], pl[2];
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-            float snd[4], rcv[4], pk[8];
-#pragma unroll
-            for (int i = 0; i < 4; i++) snd[i] = half ? p[8 * ks + i] : p[8 * ks + 4 + i];
-#pragma unroll
-            for (int i = 0; i < 4; i++) rcv[i] = __shfl_xor(snd[i], 32, 64);
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                pk[i] = half ? rcv[i] : p[8 * ks + i];
-                pk[4 + i] = half ? p[8 * ks + 4 + i] : rcv[i];
-            }
-            split8(pk, ph[ks], pl[ks]);
-        }
-        // ---- context: A = V^T from LDS (lane: dim, 8 consecutive positions)
+        bf16x8_t ph, pl;
+        split8(p, ph, pl);
+        // ---- context over this wave's 128 latent dims (k = the 16 positions)
+        const int g = l >> 4, j = l & 15;
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
-            const int dim = w * (32 * MT) + 32 * mt + n;
-#pragma unroll
-            for (int ks = 0; ks < 2; ks++) {
-                const int off = dim * kVPitch + 16 * ks + 8 * half;
-                const bf16x8_t vh = *(const bf16x8_t *)&sVh[off];
-                const bf16x8_t vl = *(const bf16x8_t *)&sVl[off];
-                o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh, ph[ks], o[mt], 0, 0, 0);
-                o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh, pl[ks], o[mt], 0, 0, 0);
-                o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vl, ph[ks], o[mt], 0, 0, 0);
-            }
+            const int d0 = 128 * w + 32 * mt + 16 * (g & 1);
+            const int chunk = (d0 >> 3) + ((j & 3) >> 1), boff = 8 * (j & 1);
+            const int ra = 8 * kh + (j >> 2), rb = ra + 4;
+            const bf16x8_t vh = tr_pair(T + mla_slot(ra, chunk) * 16 + boff,
+                                        T + mla_slot(rb, chunk) * 16 + boff);
+            const bf16x8_t vl = tr_pair(T + mla_slot(ra, 72 + chunk) * 16 + boff,
+                                        T + mla_slot(rb, 72 + chunk) * 16 + boff);
+            o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh, ph, o[mt], 0, 0, 0);
+            o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh, pl, o[mt], 0, 0, 0);
+            o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vl, ph, o[mt], 0, 0, 0);
         }
-        __syncthreads();  // sS and sV are rewritten by the next tile
-        if (more) {
-#pragma unroll
-            for (int ks = 0; ks < KS; ks++) {
-                kh[ks] = nh[ks];
-                kl[ks] = nl[ks];
-            }
-        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    };
+    for (int64_t t0 = p0; t0 < tend; t0 += 2 * kTile16) {
+        tile(sT0, sT1, t0);
+        if (t0 + kTile16 < tend) tile(sT1, sT0, t0 + kTile16);
     }
-    // ---- slice partials: O^T register i is dim w*32*MT + 32*mt + (i/4)*8 + half*4 + i%4
+    // ---- slice partials: O^T register i is dim 128*w + 32*mt + (i/4)*8 + kh*4 + i%4
     const int64_t RH = a.RH;
-    if (w == 0 && half == 0) {
+    if (w == 0 && kh == 0) {
         a.part_m[(int64_t)slice * RH + col] = m_run;
         a.part_l[(int64_t)slice * RH + col] = l_run;
     }
-    float *po = a.part_o + ((int64_t)slice * L + w * (32 * MT) + half * 4) * RH + col;
+    float *po = a.part_o + ((int64_t)slice * L + 128 * w + kh * 4) * RH + col;
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
@@ -528,9 +550,10 @@ int32_t launch_mla_attend_kc(ut_ctx *ctx, const float *qabs, const float *qrope,
     a.part_m = (float *)scratch;
     a.part_l = (float *)((char *)scratch + ((ns * RH * 4 + 255) & ~int64_t(255)));
     a.part_o = (float *)((char *)a.part_l + ((ns * RH * 4 + 255) & ~int64_t(255)));
+    a.groups = (int)(RH / 32);  // 32 columns per workgroup
     const int64_t nwg = (int64_t)a.groups * ((ns + 7) / 8 * 8);
     int tok = timing_begin(ctx, "mla_mfma");
-    hipLaunchKernelGGL((k_mla_mfma<9, 4>), dim3((unsigned)nwg), dim3(256), 0, ctx->stream, a);
+    hipLaunchKernelGGL(k_mla_mfma16, dim3((unsigned)nwg), dim3(256), 0, ctx->stream, a);
     timing_end(ctx, tok);
     UT_TRY(launch_check(ctx, "k_mla_mfma"));
     tok = timing_begin(ctx, "mla_combine");
