@@ -11,7 +11,7 @@ import json
 import numpy as np
 import pytest
 
-from models import C1, checkpoint, gpu_model, prompt_ids
+from models import C1, C1_MLA, checkpoint, gpu_model, prompt_ids
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -75,6 +75,25 @@ def test_c1_greedy_stream_identical(c1):
     prompt = prompt_ids(16, C1["vocab_size"])
     want = om.greedy_decode(prompt, 64)[16:]
     assert m.generate_greedy(prompt, 64) == want
+
+
+@pytest.fixture(scope="module")
+def c1_mla(ctx):
+    ck = checkpoint(C1_MLA, fmt="int4")
+    return ck, gpu_model(ctx, ck), O.Model(ck)
+
+
+def test_c1_mla_shape_logits_and_stream(c1_mla):
+    """DeepSeek-V3 attention dims end to end: int8 kv_b absorbs, split-cache
+    matrix-core attention, against the oracle's sequential f32 loops."""
+    ck, m, om = c1_mla
+    prompt = prompt_ids(16, C1_MLA["vocab_size"])
+    got, want = m.forward(prompt), om.forward(prompt)
+    err = np.abs(got - want)
+    assert err.max() <= 1e-3 and err.mean() <= 1e-4, (err.max(), err.mean())
+    ok = gap_ok(want)
+    assert (got.argmax(1)[ok] == want.argmax(1)[ok]).all()
+    assert m.generate_greedy(prompt, 16) == om.greedy_decode(prompt, 16)[16:]
 
 
 def test_c1_mtp_matches_oracle_and_greedy(c1):

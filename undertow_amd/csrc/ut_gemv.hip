@@ -162,15 +162,55 @@ __global__ __launch_bounds__(256) void k_rowdig(RowDigArgs a) {
 // groups t, t + T, ... (GPT of them), all loads of the row are issued before
 // the first use, and every digit word is formed from the owner's registers.
 // One global round trip per row instead of one per 256 columns.
+//
+// Wave reductions by DPP moves (no LDS round trips): after the quad, half-row
+// and row mirror steps every lane holds its 16-lane row's value; the row
+// broadcasts then fold rows 0..3 into lane 63.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t v, uint32_t identity) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)identity, (int)v, CTRL, ROW_MASK, 0xF, false);
+}
+template <typename T> struct DppBits;
+template <> struct DppBits<uint32_t> {
+    template <int C, int RM> static __device__ __forceinline__ uint32_t mov(uint32_t v) { return dpp_mov<C, RM>(v, 0u); }
+    static __device__ __forceinline__ uint32_t lane63(uint32_t v) { return __builtin_amdgcn_readlane(v, 63); }
+};
+template <> struct DppBits<double> {
+    template <int C, int RM> static __device__ __forceinline__ double mov(double v) {
+        const uint64_t u = __double_as_longlong(v);
+        const uint32_t lo = dpp_mov<C, RM>((uint32_t)u, 0u), hi = dpp_mov<C, RM>((uint32_t)(u >> 32), 0u);
+        return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));  // identity 0.0
+    }
+    static __device__ __forceinline__ double lane63(double v) {
+        const uint64_t u = __double_as_longlong(v);
+        const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)u, 63), hi = __builtin_amdgcn_readlane((uint32_t)(u >> 32), 63);
+        return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+    }
+};
+// identity of op must be all-zero bits (sum of doubles, max of unsigned)
+template <typename T, typename Op>
+__device__ __forceinline__ T wave_reduce_dpp(T v, Op op) {
+    using B = DppBits<T>;
+    v = op(v, B::template mov<0xB1, 0xF>(v));   // quad_perm 1,0,3,2
+    v = op(v, B::template mov<0x4E, 0xF>(v));   // quad_perm 2,3,0,1
+    v = op(v, B::template mov<0x141, 0xF>(v));  // row_half_mirror
+    v = op(v, B::template mov<0x140, 0xF>(v));  // row_mirror
+    v = op(v, B::template mov<0x142, 0xA>(v));  // row_bcast15
+    v = op(v, B::template mov<0x143, 0xC>(v));  // row_bcast31
+    return B::lane63(v);
+}
+
 template <typename T, typename Op>
 __device__ __forceinline__ T wide_reduce(T v, Op op, T *red /* [16] */) {
-    for (int off = 32; off >= 1; off >>= 1) v = op(v, __shfl_xor(v, off, 64));
+    v = wave_reduce_dpp(v, op);
     const int nw = (blockDim.x + 63) >> 6;
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
+    // LDS-only barriers: the fence of __syncthreads would also wait for the
+    // caller's outstanding global stores
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     T r = red[0];
     for (int w = 1; w < nw; w++) r = op(r, red[w]);
-    __syncthreads();
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     return r;
 }
 
@@ -233,18 +273,24 @@ __global__ __launch_bounds__(1024) void k_rowdig_reg(RowDigArgs a) {
         if (c >= NG) continue;
 #pragma unroll
         for (int j = 0; j < 8; j++) mx = max(mx, __float_as_uint(fabsf(v[g][j])));
-        if (a.out) {
-            float *o = a.out + m * a.ldo + 8 * c;
-#pragma unroll
-            for (int j = 0; j < 8; j++)
-                if (8 * c + j < K) o[j] = v[g][j];
-        }
     }
     if (a.rowmax) {
         mx = 0;
         for (int i = tid; i < a.nparts; i += nt) mx = max(mx, a.rowmax[m * a.nparts + i]);
     }
     mx = wide_reduce(mx, [](uint32_t p, uint32_t q) { return p > q ? p : q; }, redu);
+    // every store comes after the last barrier, so no barrier waits for them
+    if (a.out) {
+#pragma unroll
+        for (int g = 0; g < GPT; g++) {
+            const int64_t c = tid + (int64_t)g * nt;
+            if (c >= NG) continue;
+            float *o = a.out + m * a.ldo + 8 * c;
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (8 * c + j < K) o[j] = v[g][j];
+        }
+    }
     // non-finite rows (|x| bits >= +inf) produce NaN outputs downstream
     const bool bad = mx >= 0x7f800000u;
     int E = 0;

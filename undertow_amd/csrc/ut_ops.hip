@@ -373,7 +373,14 @@ int32_t launch_absorb_q(ut_ctx *ctx, const ut_qtensor *kv_b, const float *q, int
         ((uintptr_t)kv_b->payload & 15) == 0 &&
         (size_t)nope * (cb * bpc2 / 2) + RB * nope * 4 <= 64 * 1024) {
         int tok = timing_begin(ctx, "absorb_q");
-#define UT_ABSQ(F, C) absorb_q_lds_launch<F, RB, C>(ctx, kv_b, q, rows, heads, nope, rope, kvh, qabs, qrope, pos_base, table)
+        // query rows per pass: as many as are there, up to RB (the rows ride
+        // along in the same loop; a single decode row does a quarter of the work)
+#define UT_ABSQ(F, C)                                                                                   \
+    do {                                                                                                \
+        if (rows == 1) absorb_q_lds_launch<F, 1, C>(ctx, kv_b, q, rows, heads, nope, rope, kvh, qabs, qrope, pos_base, table); \
+        else if (rows == 2) absorb_q_lds_launch<F, 2, C>(ctx, kv_b, q, rows, heads, nope, rope, kvh, qabs, qrope, pos_base, table); \
+        else absorb_q_lds_launch<F, RB, C>(ctx, kv_b, q, rows, heads, nope, rope, kvh, qabs, qrope, pos_base, table); \
+    } while (0)
         if (cb == 128) {
             if (kv_b->fmt == UT_FMT_INT8) UT_ABSQ(UT_FMT_INT8, 128);
             else if (kv_b->fmt == UT_FMT_INT4) UT_ABSQ(UT_FMT_INT4, 128);
@@ -446,6 +453,48 @@ __global__ __launch_bounds__(256) void k_absorb_v(const uint8_t *__restrict__ w,
     }
 }
 
+// int8 weights, latent width 512: 32 lanes per output row, lane k takes
+// columns 16k..16k+15 with one 16-byte code load, then a butterfly over the
+// 32 lanes; a workgroup covers 8 output rows of one head.
+template <int RB>
+__global__ __launch_bounds__(256) void k_absorb_v_i8(const uint8_t *__restrict__ w,
+                                                     const float *__restrict__ scales,
+                                                     int64_t row_bytes,
+                                                     const float *__restrict__ clat, int64_t rows,
+                                                     int64_t heads, int64_t nope, int64_t vh,
+                                                     float *__restrict__ out) {
+    constexpr int L = 512;
+    const int64_t h = blockIdx.x, r0 = (int64_t)blockIdx.z * RB;
+    const int jl = threadIdx.x >> 5, k = threadIdx.x & 31;
+    const int64_t j = (int64_t)blockIdx.y * 8 + jl;
+    const int64_t jc = j < vh ? j : vh - 1;
+    const int64_t row = h * (nope + vh) + nope + jc;
+    const uint4 cw = *(const uint4 *)(w + row * row_bytes + 16 * k);
+    float acc[RB];
+#pragma unroll
+    for (int r = 0; r < RB; r++) {
+        const int64_t rr = r0 + r < rows ? r0 + r : rows - 1;
+        const float *xr = clat + (rr * heads + h) * L + 16 * k;
+        float a = 0.0f;
+#pragma unroll
+        for (int q4 = 0; q4 < 4; q4++) {
+            const float4 xv = *(const float4 *)(xr + 4 * q4);
+            const uint32_t word = q4 == 0 ? cw.x : q4 == 1 ? cw.y : q4 == 2 ? cw.z : cw.w;
+            a = __builtin_fmaf(xv.x, (float)(int8_t)(word), a);
+            a = __builtin_fmaf(xv.y, (float)(int8_t)(word >> 8), a);
+            a = __builtin_fmaf(xv.z, (float)(int8_t)(word >> 16), a);
+            a = __builtin_fmaf(xv.w, (float)(int8_t)(word >> 24), a);
+        }
+#pragma unroll
+        for (int off = 16; off >= 1; off >>= 1) a += __shfl_xor(a, off, 32);
+        acc[r] = a;
+    }
+#pragma unroll
+    for (int r = 0; r < RB; r++)
+        if (k == r && j < vh && r0 + r < rows)
+            out[(r0 + r) * heads * vh + h * vh + j] = __fmul_rn(acc[r], scales[row]);
+}
+
 int32_t launch_absorb_v(ut_ctx *ctx, const ut_qtensor *kv_b, const float *clat, int64_t rows,
                         int64_t heads, int64_t nope, int64_t vh, float *out) {
     if (rows <= 0) return UT_OK;
@@ -455,8 +504,24 @@ int32_t launch_absorb_v(ut_ctx *ctx, const ut_qtensor *kv_b, const float *clat, 
         return UT_ERR_SHAPE;
     }
     constexpr int RB = 4;
-    dim3 grid((unsigned)heads, (unsigned)((vh + 15) / 16), (unsigned)((rows + RB - 1) / RB));
     const uint8_t *w = (const uint8_t *)kv_b->payload;
+    if (kv_b->fmt == UT_FMT_INT8 && L == 512 && kv_b->row_bytes % 16 == 0 &&
+        ((uintptr_t)w & 15) == 0) {
+        int tok = timing_begin(ctx, "absorb_v");
+        const dim3 g8((unsigned)heads, (unsigned)((vh + 7) / 8), (unsigned)((rows + RB - 1) / RB));
+        if (rows == 1)
+            hipLaunchKernelGGL((k_absorb_v_i8<1>), g8, dim3(256), 0, ctx->stream, w, kv_b->scales,
+                               kv_b->row_bytes, clat, rows, heads, nope, vh, out);
+        else if (rows == 2)
+            hipLaunchKernelGGL((k_absorb_v_i8<2>), g8, dim3(256), 0, ctx->stream, w, kv_b->scales,
+                               kv_b->row_bytes, clat, rows, heads, nope, vh, out);
+        else
+            hipLaunchKernelGGL((k_absorb_v_i8<RB>), g8, dim3(256), 0, ctx->stream, w, kv_b->scales,
+                               kv_b->row_bytes, clat, rows, heads, nope, vh, out);
+        timing_end(ctx, tok);
+        return launch_check(ctx, "k_absorb_v_i8");
+    }
+    dim3 grid((unsigned)heads, (unsigned)((vh + 15) / 16), (unsigned)((rows + RB - 1) / RB));
     int tok = timing_begin(ctx, "absorb_v");
     switch (kv_b->fmt) {
     case UT_FMT_INT8: hipLaunchKernelGGL((k_absorb_v<UT_FMT_INT8, RB>), grid, dim3(256), 0, ctx->stream, w, kv_b->scales, kv_b->row_bytes, L, clat, rows, heads, nope, vh, out); break;
