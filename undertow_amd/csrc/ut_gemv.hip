@@ -5,6 +5,7 @@
 // kernel for shapes the fast one does not take.
 #include "ut_gemv_core.h"
 #include "ut_moe.h"
+#include "ut_ops.h"
 
 
 namespace ut {
@@ -215,6 +216,11 @@ __device__ __forceinline__ T wide_reduce(T v, Op op, T *red /* [16] */) {
 }
 
 template <int GPT>
+__device__ __forceinline__ void rowdig_body(const RowDigArgs &a, int64_t m, float (&v)[GPT][8],
+                                            const float (&wv)[GPT][8], double *redd,
+                                            uint32_t *redu);
+
+template <int GPT>
 __global__ __launch_bounds__(1024) void k_rowdig_reg(RowDigArgs a) {
     __shared__ double redd[16];
     __shared__ uint32_t redu[16];
@@ -253,6 +259,18 @@ __global__ __launch_bounds__(1024) void k_rowdig_reg(RowDigArgs a) {
             for (int j = 0; j < 8; j++) v[g][j] = 0.0f, wv[g][j] = 0.0f;
         }
     }
+    rowdig_body<GPT>(a, m, v, wv, redd, redu);
+}
+
+// The part of the row digitiser after the row is in registers: thread tid
+// owns the 8-column groups tid + g*blockDim.x (v zero past K), wv the norm
+// weights of the same columns (read when a.norm_w is set).
+template <int GPT>
+__device__ __forceinline__ void rowdig_body(const RowDigArgs &a, int64_t m, float (&v)[GPT][8],
+                                            const float (&wv)[GPT][8], double *redd,
+                                            uint32_t *redu) {
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const int64_t K = a.K, NG = (K + 7) / 8;
     if (a.norm_w) {
         double acc = 0.0;
 #pragma unroll
@@ -330,6 +348,122 @@ __global__ __launch_bounds__(1024) void k_rowdig_reg(RowDigArgs a) {
 }
 
 constexpr int64_t kRowRegCols = 4 * 8 * 1024;  // widest row the register kernel takes
+
+// After the kv_a / q_a pair GEMV's split-K pass (kv_a rows first, then
+// q_a): workgroup m < M sums row m's q_a partials, rms-normalises and
+// digitises them for q_b (the row digitiser's body); workgroup M + m sums
+// row m's kv_a partials into LDS and appends them to the cache.  The
+// partials are exact integer totals, so these sums equal the split-K sum
+// kernel's values bit for bit; one launch replaces three.
+struct MlaPreArgs {
+    const int64_t *part;
+    int ks;
+    int64_t O, O1;  // pair rows, kv_a rows
+    const int32_t *exps;
+    const float *kv_scales, *q_scales;
+    int M;
+    RowDigArgs qa;  // K = q_lora_rank, norm_w = q_a_norm
+    int64_t L, P;
+    const float *kv_norm;
+    float *latent, *krot;
+    __bf16 *kc;
+    int64_t pos_base;
+    const float2 *table;
+};
+
+// Exact sum over the ks partials of element i (z-stride zs), 16 loads in
+// flight per call.
+__device__ __forceinline__ int64_t splitk_total(const int64_t *__restrict__ part, int ks,
+                                                int64_t zs, int64_t i) {
+    int64_t S = 0;
+    for (int z0 = 0; z0 < ks; z0 += 16) {
+        int64_t t[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) t[u] = z0 + u < ks ? part[(z0 + u) * zs + i] : 0;
+#pragma unroll
+        for (int u = 0; u < 16; u++) S += t[u];
+    }
+    return S;
+}
+
+__global__ __launch_bounds__(1024) void k_mla_pre(MlaPreArgs a) {
+    __shared__ double redd[16];
+    __shared__ uint32_t redu[16];
+    __shared__ double red4[16];
+    __shared__ float sc[kMlaPreMaxComp > 2048 ? kMlaPreMaxComp : 2048];
+    const int tid = threadIdx.x;
+    const int64_t zs = (int64_t)a.M * a.O;
+    const bool qrow = (int)blockIdx.x < a.M;
+    const int64_t m = qrow ? blockIdx.x : blockIdx.x - a.M;
+    // the row's values into LDS (every thread, coalesced partial reads)
+    const int64_t n = qrow ? a.qa.K : a.O1, off = m * a.O + (qrow ? a.O1 : 0);
+    const float *scl = qrow ? a.q_scales : a.kv_scales;
+    for (int64_t i = tid; i < n; i += blockDim.x)
+        sc[i] = int_total_to_f32(splitk_total(a.part, a.ks, zs, off + i), a.exps[m], ld_global_f32(scl + i));
+    __syncthreads();
+    if (qrow) {
+        const int64_t K = a.qa.K, NG = (K + 7) / 8;
+        float v[1][8], wv[1][8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int64_t col = 8 * tid + j;
+            const bool in = tid < NG && col < K;
+            v[0][j] = in ? sc[col] : 0.0f;
+            wv[0][j] = in ? a.qa.norm_w[col] : 0.0f;
+        }
+        rowdig_body<1>(a.qa, m, v, wv, redd, redu);
+    } else {
+        kv_append_row(sc, a.L, a.P, a.kv_norm, a.qa.eps, a.latent, a.krot, a.kc, a.pos_base + m,
+                      a.table, red4);
+    }
+}
+
+bool mla_pre_ok(int64_t M, int64_t q_lora, int64_t L, int64_t P) {
+    return M >= 1 && M <= 4 && q_lora <= 8 * 256 && L + P <= kMlaPreMaxComp;
+}
+
+int32_t launch_mla_pre(ut_ctx *ctx, const SplitKPartials &pp, int64_t O1, const int32_t *exps,
+                       const float *kv_scales, const float *q_scales, int64_t M, int64_t q_lora,
+                       const float *q_norm, float eps, float *qa_n, const XDigits &qd, int flags,
+                       int64_t L, int64_t P, const float *kv_norm, float *latent, float *krot,
+                       __bf16 *kc, int64_t pos_base, const float2 *table) {
+    if (!mla_pre_ok(M, q_lora, L, P) || pp.ks < 1 || !pp.part || O1 != L + P) {
+        set_error(ctx, "mla_pre: unsupported shape");
+        return UT_ERR_ARG;
+    }
+    MlaPreArgs a{};
+    a.part = pp.part;
+    a.ks = pp.ks;
+    a.O = pp.O;
+    a.O1 = O1;
+    a.exps = exps;
+    a.kv_scales = kv_scales;
+    a.q_scales = q_scales;
+    a.M = (int)M;
+    a.qa.K = q_lora;
+    a.qa.norm_w = q_norm;
+    a.qa.eps = eps;
+    a.qa.out = qa_n;
+    a.qa.ldo = q_lora;
+    a.qa.exps = qd.exps;
+    a.qa.dig4 = (flags & XD_DIG4) ? qd.dig4 : nullptr;
+    a.qa.dig8 = (flags & XD_DIG8) ? qd.dig8 : nullptr;
+    a.qa.xt = (flags & XD_XT) ? qd.xt : nullptr;
+    a.L = L;
+    a.P = P;
+    a.kv_norm = kv_norm;
+    a.latent = latent;
+    a.krot = krot;
+    a.kc = kc;
+    a.pos_base = pos_base;
+    a.table = table;
+    int tok = timing_begin(ctx, "mla_pre");
+    hipLaunchKernelGGL(k_mla_pre, dim3((unsigned)(2 * M)), dim3(1024), 0, ctx->stream, a);
+    timing_end(ctx, tok);
+    return launch_check(ctx, "k_mla_pre");
+}
+
+
 
 static int32_t launch_rowdig(ut_ctx *ctx, const RowDigArgs &a, int64_t M, const char *name) {
     if (M <= 0) return UT_OK;
@@ -681,6 +815,89 @@ static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrow
     }
     timing_end(ctx, tok);
     return launch_check(ctx, name);
+}
+
+// f32 weights with few output rows (the router gate: 256 x 7168): one
+// workgroup per output row for all M <= 4 activation rows; thread t takes
+// the float4 columns 4t + 1024j (every weight load in flight at once), the
+// per-thread FMA chains are summed by DPP within each wave and then over the
+// four waves in order.  No split-K partials, so the router reads the logits
+// directly.
+template <> struct DppBits<float> {
+    template <int C, int RM> static __device__ __forceinline__ float mov(float v) {
+        return __uint_as_float(dpp_mov<C, RM>(__float_as_uint(v), 0u));
+    }
+    static __device__ __forceinline__ float lane63(float v) {
+        return __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 63));
+    }
+};
+
+template <int M, int NJ>
+__global__ __launch_bounds__(256) void k_rowdot_f32(const float *__restrict__ w, int64_t K,
+                                                    const float *__restrict__ x, int64_t ldx,
+                                                    float *__restrict__ out, int64_t ldo) {
+    __shared__ float red[4][M];
+    const int64_t row = blockIdx.x;
+    const int tid = threadIdx.x;
+    const float *wr = w + row * K;
+    float4 wv[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int64_t c = 4 * tid + 1024 * j;
+        wv[j] = c < K ? ld_global<float4>(wr + c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    float acc[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+        float a = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const int64_t c = 4 * tid + 1024 * j;
+            if (c < K) {
+                const float4 xv = ld_global<float4>(x + m * ldx + c);
+                a = __builtin_fmaf(wv[j].x, xv.x, a);
+                a = __builtin_fmaf(wv[j].y, xv.y, a);
+                a = __builtin_fmaf(wv[j].z, xv.z, a);
+                a = __builtin_fmaf(wv[j].w, xv.w, a);
+            }
+        }
+        acc[m] = wave_reduce_dpp(a, [](float p, float q) { return p + q; });
+    }
+    if ((tid & 63) == 0)
+#pragma unroll
+        for (int m = 0; m < M; m++) red[tid >> 6][m] = acc[m];
+    __syncthreads();
+    if (tid < M) out[tid * ldo + row] = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
+}
+
+bool rowdot_f32_ok(const ut_qtensor *w, int64_t M) {
+    return w->fmt == UT_FMT_F32 && M >= 1 && M <= 4 && w->in_dim % 4 == 0 &&
+           w->in_dim <= 8 * 1024 && w->out_dim <= 4096 && ((uintptr_t)w->payload & 15) == 0;
+}
+
+int32_t launch_rowdot_f32(ut_ctx *ctx, const ut_qtensor *w, const float *x, int64_t M,
+                          float *out, int64_t ldo) {
+    if (!rowdot_f32_ok(w, M) || ((uintptr_t)x & 15) != 0) {
+        set_error(ctx, "rowdot_f32: unsupported shape or alignment");
+        return UT_ERR_ARG;
+    }
+    const int64_t K = w->in_dim;
+    const int nj = (int)((K + 1023) / 1024);
+    int tok = timing_begin(ctx, "rowdot_f32");
+    const dim3 grid((unsigned)w->out_dim);
+    const float *wp = (const float *)w->payload;
+#define UT_RD(MM, NJ) hipLaunchKernelGGL((k_rowdot_f32<MM, NJ>), grid, dim3(256), 0, ctx->stream, wp, K, x, K, out, ldo)
+#define UT_RDM(MM) do { if (nj <= 2) UT_RD(MM, 2); else if (nj <= 4) UT_RD(MM, 4); else UT_RD(MM, 8); } while (0)
+    switch (M) {
+    case 1: UT_RDM(1); break;
+    case 2: UT_RDM(2); break;
+    case 3: UT_RDM(3); break;
+    default: UT_RDM(4); break;
+    }
+#undef UT_RDM
+#undef UT_RD
+    timing_end(ctx, tok);
+    return launch_check(ctx, "k_rowdot_f32");
 }
 
 int32_t gemv(ut_ctx *ctx, const GemvArgs &ga) {

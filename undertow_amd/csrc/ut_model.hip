@@ -468,6 +468,9 @@ int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
             if (L.gate->fmt != UT_FMT_F32) {
                 UT_TRY(mm(s, L.gate, x + s0 * H, M, s->ws.rlogits, E));
                 gparts = SplitKPartials{};
+            } else if (rowdot_f32_ok(L.gate, M) && ((uintptr_t)(x + s0 * H) & 15) == 0) {
+                UT_TRY(launch_rowdot_f32(m->ctx, L.gate, x + s0 * H, M, s->ws.rlogits, E));
+                gparts = SplitKPartials{};
             } else {
                 UT_TRY(gemv(m->ctx, ga));
             }
@@ -528,6 +531,10 @@ int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
     const bool pair = L.lora && L.kv_a->fmt == L.q_a->fmt && L.kv_a->fmt != UT_FMT_F32 &&
                       L.kv_a->in_dim == L.q_a->in_dim && L.kv_a->row_bytes == L.q_a->row_bytes &&
                       gemv_fast_ok(L.kv_a) && gemv_fast_ok(L.q_a);
+    // with the pair's split-K partials deferred, one launch finishes both
+    // outputs: q_a's norm + digits and kv_a's cache append
+    const bool fused = pair && mla_pre_ok(rows, c.q_lora_rank, Lr, rope);
+    SplitKPartials pp;
     if (pair) {
         // kv_a and q_a read the same normed row: one launch for both
         GemvArgs ga;
@@ -540,21 +547,31 @@ int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
         ga.w2 = L.q_a;
         ga.out2 = w.qa;
         ga.ldo2 = c.q_lora_rank;
+        if (fused) ga.defer = &pp;
         UT_TRY(gemv(ctx, ga));
     } else {
         UT_TRY(matmul_digits(ctx, L.kv_a, x, xd, rows, w.comp, Lr + rope, 0));
     }
-    if (L.lora) {
-        if (!pair) UT_TRY(matmul_digits(ctx, L.q_a, x, xd, rows, w.qa, c.q_lora_rank, 0));
-        XDigits qd;
-        UT_TRY(norm_dig(s, w.qa, c.q_lora_rank, L.q_a_norm, c.q_lora_rank, rows, w.qa_n,
-                        c.q_lora_rank, w.digB, dig_flags({L.q_b}), &qd));
+    if (fused && pp.ks > 1) {
+        const int qf = dig_flags({L.q_b});
+        const XDigits qd = xdigits_view(w.digB, rows, c.q_lora_rank, qf);
+        UT_TRY(launch_mla_pre(ctx, pp, Lr + rope, xd.exps, L.kv_a->scales, L.q_a->scales, rows,
+                              c.q_lora_rank, L.q_a_norm, c.rms_norm_eps, w.qa_n, qd, qf, Lr, rope,
+                              L.kv_a_norm, kv.latent, kv.krot, kv.kc, pos_base, m->rope_table));
         UT_TRY(matmul_digits(ctx, L.q_b, w.qa_n, qd, rows, w.q, heads * qh, 0));
     } else {
-        UT_TRY(matmul_digits(ctx, L.q_proj, x, xd, rows, w.q, heads * qh, 0));
+        if (L.lora) {
+            if (!pair) UT_TRY(matmul_digits(ctx, L.q_a, x, xd, rows, w.qa, c.q_lora_rank, 0));
+            XDigits qd;
+            UT_TRY(norm_dig(s, w.qa, c.q_lora_rank, L.q_a_norm, c.q_lora_rank, rows, w.qa_n,
+                            c.q_lora_rank, w.digB, dig_flags({L.q_b}), &qd));
+            UT_TRY(matmul_digits(ctx, L.q_b, w.qa_n, qd, rows, w.q, heads * qh, 0));
+        } else {
+            UT_TRY(matmul_digits(ctx, L.q_proj, x, xd, rows, w.q, heads * qh, 0));
+        }
+        UT_TRY(launch_kv_append(ctx, w.comp, rows, Lr, rope, L.kv_a_norm, c.rms_norm_eps,
+                                kv.latent, kv.krot, kv.kc, pos_base, m->rope_table));
     }
-    UT_TRY(launch_kv_append(ctx, w.comp, rows, Lr, rope, L.kv_a_norm, c.rms_norm_eps, kv.latent,
-                            kv.krot, kv.kc, pos_base, m->rope_table));
     kv.len = pos_base + rows;
     UT_TRY(launch_absorb_q(ctx, L.kv_b, w.q, rows, heads, nope, rope, vh, w.qabs, w.qrope,
                            pos_base, m->rope_table));
@@ -586,13 +603,13 @@ int32_t run_layer(ut_session *s, const LayerW &L, float *x, int64_t rows, KvCach
     XDigits xd;
     UT_TRY(norm_dig(s, x, H, L.input_norm, H, rows, w.normed, H, w.digA,
                     dig_flags({L.q_a, L.q_proj, L.kv_a}), &xd));
-    UT_TRY(mla_forward(s, L, w.normed, xd, rows, kv, x));
     int f = 0;
     if (L.dense) f = dig_flags_fmt(L.mlp.fmt, H);
     else {
         f = dig_flags_fmt(L.expert_fmt, H);
         if (L.has_shared) f |= dig_flags_fmt(L.shared.fmt, H);
     }
+    UT_TRY(mla_forward(s, L, w.normed, xd, rows, kv, x));
     UT_TRY(norm_dig(s, x, H, L.post_norm, H, rows, w.normed, H, w.digA, f, &xd));
     if (L.dense) return mlp_add(s, L.mlp, w.normed, xd, rows, x);
     // x += (routed + shared) (model.rs:282-284 then the residual add)

@@ -5,6 +5,62 @@
 
 namespace ut {
 
+// One cache append (attention.rs:168-186): latent[pos] = rmsnorm(c[:L], w),
+// krot[pos] = rope_interleave(c[L:L+P], pos), by the whole workgroup (up to
+// 1024 threads; red: one double per wave).
+// kc != nullptr: the cache is kept in the split bf16 form of the MFMA
+// attention kernel (per position: hi parts of [latent | k_rot], then lo).
+// c may point to global or shared memory.  red: 4 doubles of shared memory.
+__device__ __forceinline__ void kv_store(float *__restrict__ plain, int64_t pi,
+                                         __bf16 *__restrict__ kc, int64_t ki, int64_t D, float v) {
+    if (kc) {
+        const __bf16 h = (__bf16)v;
+        kc[ki] = h;
+        kc[ki + D] = (__bf16)__fsub_rn(v, (float)h);
+    } else {
+        plain[pi] = v;
+    }
+}
+
+__device__ __forceinline__ void kv_append_row(const float *c, int64_t L, int64_t P,
+                                              const float *__restrict__ w, float eps,
+                                              float *__restrict__ latent, float *__restrict__ krot,
+                                              __bf16 *__restrict__ kc, int64_t pos,
+                                              const float2 *__restrict__ table, double *red) {
+    const int nt = blockDim.x, nw = nt >> 6;
+    double acc = 0.0;
+    for (int64_t i = threadIdx.x; i < L; i += nt) {
+        const double v = (double)c[i];
+        acc += v * v;
+    }
+    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    // waves summed pairwise in a fixed tree ((0+1)+(2+3)) + ... for 4 waves
+    double ms = 0.0;
+    for (int q = 0; q < nw; q += 4) {
+        double t = red[q];
+        if (q + 1 < nw) t += red[q + 1];
+        double t2 = q + 2 < nw ? red[q + 2] : 0.0;
+        if (q + 3 < nw) t2 += red[q + 3];
+        ms += t + t2;
+    }
+    ms /= (double)L;
+    const float r = 1.0f / sqrtf(__fadd_rn((float)ms, eps));
+    const int64_t D = L + P, kb = pos * 2 * D;
+    for (int64_t i = threadIdx.x; i < L; i += nt)
+        kv_store(latent, pos * L + i, kc, kb + i, D, __fmul_rn(__fmul_rn(c[i], r), w[i]));
+    const int64_t half = P / 2;
+    for (int64_t jj = threadIdx.x; jj < P; jj += nt) {
+        const int64_t j = jj < half ? jj : jj - half;
+        const float a = c[L + 2 * j], b = c[L + 2 * j + 1];
+        const float2 cs = table[pos * half + j];
+        kv_store(krot, pos * P + jj, kc, kb + L + jj, D,
+                 jj < half ? __fsub_rn(__fmul_rn(a, cs.x), __fmul_rn(b, cs.y))
+                           : __fadd_rn(__fmul_rn(b, cs.x), __fmul_rn(a, cs.y)));
+    }
+}
+
 // Embedding rows (model.rs:119-122): out[s] = 0 + (1*scale[id])*q[id] (f32
 // tables copied).  ids: device int32 [rows].
 int32_t launch_embed(ut_ctx *ctx, const ut_qtensor *emb, const int32_t *ids, int64_t rows,

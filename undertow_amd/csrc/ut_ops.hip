@@ -127,52 +127,16 @@ int32_t launch_add(ut_ctx *ctx, float *y, const float *x, int64_t n) {
     return launch_check(ctx, "k_add");
 }
 
-// Cache append (attention.rs:168-186): latent[pos] = rmsnorm(comp[:L], w),
-// krot[pos] = rope_interleave(comp[L:L+P], pos), one workgroup per row.
-// kc != nullptr: the cache is kept in the split bf16 form of the MFMA
-// attention kernel (per position: hi parts of [latent | k_rot], then lo).
-__device__ __forceinline__ void kv_store(float *__restrict__ plain, int64_t pi,
-                                         __bf16 *__restrict__ kc, int64_t ki, int64_t D, float v) {
-    if (kc) {
-        const __bf16 h = (__bf16)v;
-        kc[ki] = h;
-        kc[ki + D] = (__bf16)__fsub_rn(v, (float)h);
-    } else {
-        plain[pi] = v;
-    }
-}
-
+// Cache append, one workgroup per row (kv_append_row).
 __global__ __launch_bounds__(256) void k_kv_append(const float *__restrict__ comp, int64_t L,
                                                    int64_t P, const float *__restrict__ w,
                                                    float eps, float *__restrict__ latent,
                                                    float *__restrict__ krot, __bf16 *__restrict__ kc,
                                                    int64_t pos_base,
                                                    const float2 *__restrict__ table) {
-    const int64_t s = blockIdx.x, pos = pos_base + s;
-    const float *c = comp + s * (L + P);
     __shared__ double red[4];
-    double acc = 0.0;
-    for (int64_t i = threadIdx.x; i < L; i += 256) {
-        const double v = (double)c[i];
-        acc += v * v;
-    }
-    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
-    __syncthreads();
-    const double ms = ((red[0] + red[1]) + (red[2] + red[3])) / (double)L;
-    const float r = 1.0f / sqrtf(__fadd_rn((float)ms, eps));
-    const int64_t D = L + P, kb = pos * 2 * D;
-    for (int64_t i = threadIdx.x; i < L; i += 256)
-        kv_store(latent, pos * L + i, kc, kb + i, D, __fmul_rn(__fmul_rn(c[i], r), w[i]));
-    const int64_t half = P / 2;
-    for (int64_t jj = threadIdx.x; jj < P; jj += 256) {
-        const int64_t j = jj < half ? jj : jj - half;
-        const float a = c[L + 2 * j], b = c[L + 2 * j + 1];
-        const float2 cs = table[pos * half + j];
-        kv_store(krot, pos * P + jj, kc, kb + L + jj, D,
-                 jj < half ? __fsub_rn(__fmul_rn(a, cs.x), __fmul_rn(b, cs.y))
-                           : __fadd_rn(__fmul_rn(b, cs.x), __fmul_rn(a, cs.y)));
-    }
+    const int64_t s = blockIdx.x;
+    kv_append_row(comp + s * (L + P), L, P, w, eps, latent, krot, kc, pos_base + s, table, red);
 }
 
 int32_t launch_kv_append(ut_ctx *ctx, const float *comp, int64_t rows, int64_t L, int64_t P,
