@@ -164,43 +164,6 @@ __global__ __launch_bounds__(256) void k_rowdig(RowDigArgs a) {
 // the first use, and every digit word is formed from the owner's registers.
 // One global round trip per row instead of one per 256 columns.
 //
-// Wave reductions by DPP moves (no LDS round trips): after the quad, half-row
-// and row mirror steps every lane holds its 16-lane row's value; the row
-// broadcasts then fold rows 0..3 into lane 63.
-template <int CTRL, int ROW_MASK = 0xF>
-__device__ __forceinline__ uint32_t dpp_mov(uint32_t v, uint32_t identity) {
-    return (uint32_t)__builtin_amdgcn_update_dpp((int)identity, (int)v, CTRL, ROW_MASK, 0xF, false);
-}
-template <typename T> struct DppBits;
-template <> struct DppBits<uint32_t> {
-    template <int C, int RM> static __device__ __forceinline__ uint32_t mov(uint32_t v) { return dpp_mov<C, RM>(v, 0u); }
-    static __device__ __forceinline__ uint32_t lane63(uint32_t v) { return __builtin_amdgcn_readlane(v, 63); }
-};
-template <> struct DppBits<double> {
-    template <int C, int RM> static __device__ __forceinline__ double mov(double v) {
-        const uint64_t u = __double_as_longlong(v);
-        const uint32_t lo = dpp_mov<C, RM>((uint32_t)u, 0u), hi = dpp_mov<C, RM>((uint32_t)(u >> 32), 0u);
-        return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));  // identity 0.0
-    }
-    static __device__ __forceinline__ double lane63(double v) {
-        const uint64_t u = __double_as_longlong(v);
-        const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)u, 63), hi = __builtin_amdgcn_readlane((uint32_t)(u >> 32), 63);
-        return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
-    }
-};
-// identity of op must be all-zero bits (sum of doubles, max of unsigned)
-template <typename T, typename Op>
-__device__ __forceinline__ T wave_reduce_dpp(T v, Op op) {
-    using B = DppBits<T>;
-    v = op(v, B::template mov<0xB1, 0xF>(v));   // quad_perm 1,0,3,2
-    v = op(v, B::template mov<0x4E, 0xF>(v));   // quad_perm 2,3,0,1
-    v = op(v, B::template mov<0x141, 0xF>(v));  // row_half_mirror
-    v = op(v, B::template mov<0x140, 0xF>(v));  // row_mirror
-    v = op(v, B::template mov<0x142, 0xA>(v));  // row_bcast15
-    v = op(v, B::template mov<0x143, 0xC>(v));  // row_bcast31
-    return B::lane63(v);
-}
-
 template <typename T, typename Op>
 __device__ __forceinline__ T wide_reduce(T v, Op op, T *red /* [16] */) {
     v = wave_reduce_dpp(v, op);
@@ -575,6 +538,10 @@ struct PlainArgs {
     int ks;
     int64_t kslice;
     int64_t *part;
+    // x.dig == nullptr for int weights: the row shifts come from partial
+    // maxima xmax [M][nxmax]; workgroup 0 records the exponents in exps
+    const uint32_t *xmax;
+    int nxmax;
 };
 
 __device__ __forceinline__ const uint8_t *plain_row(const PlainArgs &a, int64_t row) {
@@ -600,10 +567,30 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
     const uint8_t *rows[R];
 #pragma unroll
     for (int r = 0; r < R; r++) rows[r] = plain_row(a, row0 + r < a.O ? row0 + r : a.O - 1);
+    XSrc xs = a.x;
+    int32_t exl[M];
+    if constexpr (FMT != UT_FMT_F32) {
+        if (a.xmax) {
+            __shared__ uint32_t redm[4 * M];
+            int32_t sh[M];
+            rowmax_shifts<M>(a.xmax, a.nxmax, sh, redm);
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                xs.sh[m] = sh[m];
+                exl[m] = sh[m] == INT32_MIN ? INT32_MIN : -sh[m];
+            }
+            if (blockIdx.x == 0 && blockIdx.z == 0 && tid < M)
+                const_cast<int32_t *>(a.exps)[tid] = tid == 0 ? exl[0] : tid == 1 ? exl[M > 1 ? 1 : 0]
+                                                    : tid == 2 ? exl[M > 2 ? 2 : 0] : exl[M > 3 ? 3 : 0];
+        } else {
+#pragma unroll
+            for (int m = 0; m < M; m++) exl[m] = a.exps[m];
+        }
+    }
     CoreOut<FMT, M, R> res;
     if (a.ks > 1) {
         const int64_t kb = (int64_t)blockIdx.z * a.kslice;
-        gemv_core<FMT, M, R, gemv_depth<M>()>(rows, a.K, a.x, lds, res, kb, kb + a.kslice);
+        gemv_core<FMT, M, R, gemv_depth<M>()>(rows, a.K, xs, lds, res, kb, kb + a.kslice);
 #pragma unroll
         for (int r = 0; r < R; r++)
 #pragma unroll
@@ -615,7 +602,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
             }
         return;
     }
-    gemv_core<FMT, M, R, gemv_depth<M>()>(rows, a.K, a.x, lds, res);
+    gemv_core<FMT, M, R, gemv_depth<M>()>(rows, a.K, xs, lds, res);
 #pragma unroll
     for (int r = 0; r < R; r++)
 #pragma unroll
@@ -624,7 +611,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
             if (s == 4 * r + m && row < a.O) {
                 const float v = FMT == UT_FMT_F32
                                     ? res.F[r][m]
-                                    : int_total_to_f32(res.S[r][m], a.exps[m], plain_scale(a, row));
+                                    : int_total_to_f32(res.S[r][m], exl[m], plain_scale(a, row));
                 float *o = plain_out(a, m, row);
                 *o = a.accumulate ? __fadd_rn(*o, v) : v;
             }
@@ -781,12 +768,23 @@ static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrow
     } else {
         constexpr int PL = FmtTraits<FMT>::kPlanes;
         const int64_t KW = (w->in_dim + FmtTraits<FMT>::kColsPerWord - 1) / FmtTraits<FMT>::kColsPerWord;
-        a.x.dig = (FMT == UT_FMT_INT4 ? ga.xd.dig4 : ga.xd.dig8) + m0 * PL * KW;
-        a.x.KW = KW;
-        a.x.xf = nullptr;
-        a.x.ldx = 0;
-        a.exps = ga.xd.exps + m0;
+        if (ga.xmax) {
+            a.x.dig = nullptr;
+            a.x.KW = KW;
+            a.x.xf = ga.xf + m0 * w->in_dim;
+            a.x.ldx = w->in_dim;
+            a.exps = ga.exps_out + m0;
+            if (!aligned16(a.x.xf)) return UT_ERR_ARG;
+        } else {
+            a.x.dig = (FMT == UT_FMT_INT4 ? ga.xd.dig4 : ga.xd.dig8) + m0 * PL * KW;
+            a.x.KW = KW;
+            a.x.xf = nullptr;
+            a.x.ldx = 0;
+            a.exps = ga.xd.exps + m0;
+        }
     }
+    a.xmax = FMT != UT_FMT_F32 && ga.xmax ? ga.xmax + m0 * ga.nxmax : nullptr;
+    a.nxmax = ga.nxmax;
     splitk_plan(FMT, a.O, w->in_dim, &a.ks, &a.kslice);
     a.part = nullptr;
     if (a.ks > 1) UT_TRY(splitk_buffer(ctx, &a.part));
@@ -823,14 +821,6 @@ static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrow
 // per-thread FMA chains are summed by DPP within each wave and then over the
 // four waves in order.  No split-K partials, so the router reads the logits
 // directly.
-template <> struct DppBits<float> {
-    template <int C, int RM> static __device__ __forceinline__ float mov(float v) {
-        return __uint_as_float(dpp_mov<C, RM>(__float_as_uint(v), 0u));
-    }
-    static __device__ __forceinline__ float lane63(float v) {
-        return __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 63));
-    }
-};
 
 template <int M, int NJ>
 __global__ __launch_bounds__(256) void k_rowdot_f32(const float *__restrict__ w, int64_t K,

@@ -502,6 +502,98 @@ __device__ __forceinline__ T block_reduce(T v, Op op, T *red4) {
     return r;
 }
 
+// Wave reductions by DPP moves (no LDS round trips): after the quad, half-row
+// and row mirror steps every lane holds its 16-lane row's value; the row
+// broadcasts then fold rows 0..3 into lane 63.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t v, uint32_t identity) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)identity, (int)v, CTRL, ROW_MASK, 0xF, false);
+}
+template <typename T> struct DppBits;
+template <> struct DppBits<uint32_t> {
+    template <int C, int RM> static __device__ __forceinline__ uint32_t mov(uint32_t v) { return dpp_mov<C, RM>(v, 0u); }
+    static __device__ __forceinline__ uint32_t lane63(uint32_t v) { return __builtin_amdgcn_readlane(v, 63); }
+};
+template <> struct DppBits<double> {
+    template <int C, int RM> static __device__ __forceinline__ double mov(double v) {
+        const uint64_t u = __double_as_longlong(v);
+        const uint32_t lo = dpp_mov<C, RM>((uint32_t)u, 0u), hi = dpp_mov<C, RM>((uint32_t)(u >> 32), 0u);
+        return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));  // identity 0.0
+    }
+    static __device__ __forceinline__ double lane63(double v) {
+        const uint64_t u = __double_as_longlong(v);
+        const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)u, 63), hi = __builtin_amdgcn_readlane((uint32_t)(u >> 32), 63);
+        return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+    }
+};
+// identity of op must be all-zero bits (sum of doubles, max of unsigned)
+template <typename T, typename Op>
+__device__ __forceinline__ T wave_reduce_dpp(T v, Op op) {
+    using B = DppBits<T>;
+    v = op(v, B::template mov<0xB1, 0xF>(v));   // quad_perm 1,0,3,2
+    v = op(v, B::template mov<0x4E, 0xF>(v));   // quad_perm 2,3,0,1
+    v = op(v, B::template mov<0x141, 0xF>(v));  // row_half_mirror
+    v = op(v, B::template mov<0x140, 0xF>(v));  // row_mirror
+    v = op(v, B::template mov<0x142, 0xA>(v));  // row_bcast15
+    v = op(v, B::template mov<0x143, 0xC>(v));  // row_bcast31
+    return B::lane63(v);
+}
+
+template <> struct DppBits<float> {
+    template <int C, int RM> static __device__ __forceinline__ float mov(float v) {
+        return __uint_as_float(dpp_mov<C, RM>(__float_as_uint(v), 0u));
+    }
+    static __device__ __forceinline__ float lane63(float v) {
+        return __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 63));
+    }
+};
+
+// The digitisation shifts of M activation rows from partial maxima of |x|
+// (float bits, nparts per row): 22 - E with max < 2^E, INT32_MIN for a
+// non-finite row.  Whole workgroup of kGemvThreads; red: 4*M words of LDS.
+// 16-byte loads when nparts % 4 == 0 (16-byte aligned rows), DPP wave
+// maxima, LDS-only barriers.
+template <int M>
+__device__ __forceinline__ void rowmax_shifts(const uint32_t *parts, int nparts,
+                                              int32_t (&sh)[M], uint32_t *red) {
+    uint32_t mx[M];
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+        const uint32_t *pr = parts + (int64_t)m * nparts;
+        uint32_t v = 0;
+        if ((nparts & 3) == 0) {
+            for (int i = 4 * tid; i < nparts; i += 4 * kGemvThreads) {
+                const ut_u32x4 q = *(const ut_u32x4 *)(pr + i);
+                v = max(v, max(max(q[0], q[1]), max(q[2], q[3])));
+            }
+        } else {
+            for (int i = tid; i < nparts; i += kGemvThreads) v = max(v, pr[i]);
+        }
+        mx[m] = wave_reduce_dpp(v, [](uint32_t p, uint32_t q) { return p > q ? p : q; });
+    }
+    if ((tid & 63) == 0)
+#pragma unroll
+        for (int m = 0; m < M; m++) red[(tid >> 6) * M + m] = mx[m];
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+        const uint32_t r = max(max(red[m], red[M + m]), max(red[2 * M + m], red[3 * M + m]));
+        int E = 0;
+        if (r < 0x7f800000u && r != 0) (void)frexpf(__uint_as_float(r), &E);
+        sh[m] = r >= 0x7f800000u ? INT32_MIN : 22 - E;
+    }
+    // red may be reused right away by the caller
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+__device__ __forceinline__ int32_t rowmax_shift(const uint32_t *parts, int nparts, int64_t row,
+                                                uint32_t *red4) {
+    int32_t sh[1];
+    rowmax_shifts<1>(parts + row * nparts, nparts, sh, red4);
+    return sh[0];
+}
+
 // Converts an exact integer total to the reference's f32 row value:
 // fl(fl(S * 2^e) * scale).  e == INT32_MIN marks a non-finite activation row.
 __device__ __forceinline__ float int_total_to_f32(int64_t S, int32_t e, float scale) {

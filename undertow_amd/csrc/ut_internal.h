@@ -200,6 +200,12 @@ struct GemvArgs {
     int64_t ldo2 = 0;
     // optional: leave split-K partials to the consumer (M <= 4, fast path)
     SplitKPartials *defer = nullptr;
+    // optional (int weights, fast path): digitise xf while staging, with the
+    // row shift from partial maxima of |x| (float bits, [M][nxmax]) written
+    // by the producer; the rows' exponents go to exps_out [M]
+    const uint32_t *xmax = nullptr;
+    int nxmax = 0;
+    int32_t *exps_out = nullptr;
 };
 int32_t gemv(ut_ctx *ctx, const GemvArgs &a);
 // The kv_a / q_a pair GEMV's deferred split-K partials (kv_a rows first)

@@ -94,6 +94,8 @@ struct Workspace {
     float *rlogits = nullptr, *rw = nullptr;
     int32_t *rids = nullptr, *ids = nullptr, *am = nullptr, *err = nullptr;
     int32_t *vids = nullptr;  // verify ids [next, drafts...] assembled on the device
+    uint32_t *vmax = nullptr;  // partial maxima of |ctx| per row (absorb_v -> o_proj)
+    int32_t *vexps = nullptr;  // o_proj activation exponents per row
     void *digits = nullptr, *moe = nullptr, *mla = nullptr, *argm = nullptr;
     void *digA = nullptr, *digB = nullptr;  // activation digits shared by consumers
 };
@@ -338,6 +340,7 @@ int32_t ws_reserve(ut_session *s, int64_t rows) {
     size_t ilog = F(R * c.vocab_size), iemb = F(R * H), icat = F(R * 2 * H);
     size_t irl = F(4 * E), irw = F(4 * k), irid = F(4 * k), iids = F(R), iam = F(R), ierr = F(1);
     size_t ivids = F(8);
+    size_t ivmax = F(R * heads * ((c.v_head_dim + 7) / 8)), ivexp = F(R);
     size_t idig = plan.add(matmul_digit_bytes(R, kmax));
     size_t idA = plan.add(matmul_digit_bytes(R, kmax));
     size_t idB = plan.add(matmul_digit_bytes(R, kmax));
@@ -369,6 +372,7 @@ int32_t ws_reserve(ut_session *s, int64_t rows) {
     w.rlogits = (float *)p[irl]; w.rw = (float *)p[irw]; w.rids = (int32_t *)p[irid];
     w.ids = (int32_t *)p[iids]; w.am = (int32_t *)p[iam]; w.err = (int32_t *)p[ierr];
     w.vids = (int32_t *)p[ivids];
+    w.vmax = (uint32_t *)p[ivmax]; w.vexps = (int32_t *)p[ivexp];
     w.digits = p[idig]; w.moe = p[imoes]; w.mla = p[imla]; w.argm = p[iarg];
     w.digA = p[idA]; w.digB = p[idB];
     w.rows = R;
@@ -588,9 +592,25 @@ int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
                                      kv.latent, kv.krot, rn, heads, Lr, rope, pos_base + r0, scale,
                                      w.clat + r0 * heads * Lr, w.mla));
     }
-    UT_TRY(launch_absorb_v(ctx, L.kv_b, w.clat, rows, heads, nope, vh, w.ctxv));
-    // x += o_proj(ctx) (the residual add of model.rs:478-480 in the epilogue)
-    return mm(s, L.o_proj, w.ctxv, rows, out, c.hidden_size, 1);
+    // x += o_proj(ctx) (the residual add of model.rs:478-480 in the epilogue);
+    // with absorb_v's row maxima the o_proj GEMV digitises ctx itself while
+    // staging (no separate digitising launch; the same digits)
+    const bool vm = absorb_v_max_ok(L.kv_b) && L.o_proj->fmt != UT_FMT_F32 &&
+                    gemv_fast_ok(L.o_proj) && rows <= 4;
+    UT_TRY(launch_absorb_v(ctx, L.kv_b, w.clat, rows, heads, nope, vh, w.ctxv,
+                           vm ? w.vmax : nullptr));
+    if (!vm) return mm(s, L.o_proj, w.ctxv, rows, out, c.hidden_size, 1);
+    GemvArgs ga;
+    ga.w = L.o_proj;
+    ga.M = rows;
+    ga.xf = w.ctxv;
+    ga.out = out;
+    ga.ldo = c.hidden_size;
+    ga.accumulate = 1;
+    ga.xmax = w.vmax;
+    ga.nxmax = (int)(heads * ((vh + 7) / 8));
+    ga.exps_out = w.vexps;
+    return gemv(ctx, ga);
 }
 
 // run_layer (model.rs:127-183) / the per-layer body of prefill (:470-526).

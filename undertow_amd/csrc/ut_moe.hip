@@ -558,13 +558,7 @@ struct DownArgs {
 // workgroup; red4: 4 words of LDS.
 __device__ __forceinline__ int32_t h_shift(const uint32_t *hmax_parts, int nparts, int64_t row,
                                            uint32_t *red4) {
-    uint32_t mx = 0;
-    for (int i = threadIdx.x; i < nparts; i += kGemvThreads)
-        mx = max(mx, hmax_parts[row * nparts + i]);
-    mx = block_reduce(mx, [](uint32_t p, uint32_t q) { return p > q ? p : q; }, red4);
-    int E = 0;
-    if (mx < 0x7f800000u && mx != 0) (void)frexpf(__uint_as_float(mx), &E);
-    return mx >= 0x7f800000u ? INT32_MIN : 22 - E;
+    return rowmax_shift(hmax_parts, nparts, row, red4);
 }
 
 // Rows per lane: 4 at M <= 2 (more activation reuse), 2 above (registers).

@@ -420,13 +420,17 @@ __global__ __launch_bounds__(256) void k_absorb_v(const uint8_t *__restrict__ w,
 // int8 weights, latent width 512: 32 lanes per output row, lane k takes
 // columns 16k..16k+15 with one 16-byte code load, then a butterfly over the
 // 32 lanes; a workgroup covers 8 output rows of one head.
+// vmax (optional): per row, this workgroup's max |out| (float bits) at
+// [row][h * gridDim.y + blockIdx.y], for a consumer that digitises the row.
 template <int RB>
 __global__ __launch_bounds__(256) void k_absorb_v_i8(const uint8_t *__restrict__ w,
                                                      const float *__restrict__ scales,
                                                      int64_t row_bytes,
                                                      const float *__restrict__ clat, int64_t rows,
                                                      int64_t heads, int64_t nope, int64_t vh,
-                                                     float *__restrict__ out) {
+                                                     float *__restrict__ out,
+                                                     uint32_t *__restrict__ vmax) {
+    __shared__ uint32_t smax[RB][8];
     constexpr int L = 512;
     const int64_t h = blockIdx.x, r0 = (int64_t)blockIdx.z * RB;
     const int jl = threadIdx.x >> 5, k = threadIdx.x & 31;
@@ -454,13 +458,34 @@ __global__ __launch_bounds__(256) void k_absorb_v_i8(const uint8_t *__restrict__
         acc[r] = a;
     }
 #pragma unroll
-    for (int r = 0; r < RB; r++)
-        if (k == r && j < vh && r0 + r < rows)
-            out[(r0 + r) * heads * vh + h * vh + j] = __fmul_rn(acc[r], scales[row]);
+    for (int r = 0; r < RB; r++) {
+        const float v = __fmul_rn(acc[r], scales[row]);
+        if (k == r) smax[r][jl] = j < vh ? __float_as_uint(fabsf(v)) : 0u;
+        if (k == r && j < vh && r0 + r < rows) out[(r0 + r) * heads * vh + h * vh + j] = v;
+    }
+    if (vmax) {
+        __syncthreads();
+        if (threadIdx.x < RB && r0 + threadIdx.x < rows) {
+            uint32_t mx = smax[threadIdx.x][0];
+#pragma unroll
+            for (int q = 1; q < 8; q++) mx = max(mx, smax[threadIdx.x][q]);
+            const int64_t nparts = heads * (int64_t)gridDim.y;
+            vmax[(r0 + threadIdx.x) * nparts + h * gridDim.y + blockIdx.y] = mx;
+        }
+    }
+}
+
+bool absorb_v_max_ok(const ut_qtensor *kv_b) {
+    return kv_b->fmt == UT_FMT_INT8 && kv_b->in_dim == 512 && kv_b->row_bytes % 16 == 0 &&
+           ((uintptr_t)kv_b->payload & 15) == 0;
 }
 
 int32_t launch_absorb_v(ut_ctx *ctx, const ut_qtensor *kv_b, const float *clat, int64_t rows,
-                        int64_t heads, int64_t nope, int64_t vh, float *out) {
+                        int64_t heads, int64_t nope, int64_t vh, float *out, uint32_t *vmax) {
+    if (vmax && !absorb_v_max_ok(kv_b)) {
+        set_error(ctx, "absorb_v: row maxima need the int8 512-wide kernel");
+        return UT_ERR_ARG;
+    }
     if (rows <= 0) return UT_OK;
     const int64_t L = kv_b->in_dim;
     if (L % 4 != 0) {
@@ -475,13 +500,13 @@ int32_t launch_absorb_v(ut_ctx *ctx, const ut_qtensor *kv_b, const float *clat, 
         const dim3 g8((unsigned)heads, (unsigned)((vh + 7) / 8), (unsigned)((rows + RB - 1) / RB));
         if (rows == 1)
             hipLaunchKernelGGL((k_absorb_v_i8<1>), g8, dim3(256), 0, ctx->stream, w, kv_b->scales,
-                               kv_b->row_bytes, clat, rows, heads, nope, vh, out);
+                               kv_b->row_bytes, clat, rows, heads, nope, vh, out, vmax);
         else if (rows == 2)
             hipLaunchKernelGGL((k_absorb_v_i8<2>), g8, dim3(256), 0, ctx->stream, w, kv_b->scales,
-                               kv_b->row_bytes, clat, rows, heads, nope, vh, out);
+                               kv_b->row_bytes, clat, rows, heads, nope, vh, out, vmax);
         else
             hipLaunchKernelGGL((k_absorb_v_i8<RB>), g8, dim3(256), 0, ctx->stream, w, kv_b->scales,
-                               kv_b->row_bytes, clat, rows, heads, nope, vh, out);
+                               kv_b->row_bytes, clat, rows, heads, nope, vh, out, vmax);
         timing_end(ctx, tok);
         return launch_check(ctx, "k_absorb_v_i8");
     }
