@@ -418,8 +418,9 @@ int32_t norm_dig(ut_session *s, const float *x, int64_t ldx, const float *w, int
 // out = out + (init + mlp(x)) instead (the shared expert added to the routed
 // sum, then the residual add, in the reference's order).
 int32_t mlp_add(ut_session *s, const MlpW &w, const float *x, const XDigits &xd, int64_t rows,
-                float *out, const float *init = nullptr) {
+                float *out, const float *init = nullptr, const NormNext *next = nullptr) {
     ut_model *m = s->m;
+    if (next && rows > 4) return UT_ERR_ARG;  // x and xd would be overwritten mid-loop
     for (int64_t s0 = 0; s0 < rows; s0 += 4) {
         MoeCall c;
         c.fmt = w.fmt;
@@ -442,6 +443,7 @@ int32_t mlp_add(ut_session *s, const MlpW &w, const float *x, const XDigits &xd,
         mp.sp = (const void **)w.dev;  // the MLP's 6 weight pointers are its slot 0
         c.plan = &mp;
         c.init = init ? init + s0 * c.H : nullptr;
+        c.next = next;
         UT_TRY(moe_pass(m->ctx, c, s->ws.moe));
     }
     return UT_OK;
@@ -451,9 +453,11 @@ int32_t mlp_add(ut_session *s, const MlpW &w, const float *x, const XDigits &xd,
 // in choice order, into out (overwritten).  x: normed rows (f32, for the f32
 // router gate) with digits xd.
 int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigits &xd,
-                    int64_t rows, float *out, int accumulate = 0, const MlpW *shared = nullptr) {
+                    int64_t rows, float *out, int accumulate = 0, const MlpW *shared = nullptr,
+                    const NormNext *next = nullptr) {
     ut_model *m = s->m;
     const ut_model_config &c = m->c;
+    if (next && rows > 4) return UT_ERR_ARG;  // x and xd would be overwritten mid-loop
     const int64_t H = c.hidden_size, E = c.n_routed_experts;
     const int k = (int)c.num_experts_per_tok;
     for (int64_t s0 = 0; s0 < rows; s0 += 4) {
@@ -514,6 +518,7 @@ int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
             mc.shared = &sc;
             mc.shared_scratch = (char *)s->ws.moe + lay.total;
         }
+        mc.next = next;
         UT_TRY(moe_pass(m->ctx, mc, s->ws.moe));
     }
     return UT_OK;
@@ -613,16 +618,42 @@ int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
     return gemv(ctx, ga);
 }
 
+// Whether the norm that follows a layer (the next layer's input norm, the
+// final norm) can run inside the layer's last combine: every consumer of the
+// layer's own normed rows has run by then, and rows fit one combine.
+bool fuse_next_ok(const ut_model *m, int64_t rows) {
+    return rows <= 4 && moe_combine_norm_ok(m->c.hidden_size);
+}
+
+// The fused norm's arguments: rmsnorm with norm_w into ws.normed and the
+// digit forms `flags` into ws.digA; *xd gets the view the consumers read.
+NormNext next_norm(ut_session *s, const float *norm_w, int flags, int64_t rows, XDigits *xd) {
+    const int64_t H = s->m->c.hidden_size;
+    NormNext nx;
+    nx.norm_w = norm_w;
+    nx.eps = s->m->c.rms_norm_eps;
+    nx.normed = s->ws.normed;
+    nx.ldn = H;
+    nx.flags = flags;
+    nx.nd = *xd = xdigits_view(s->ws.digA, rows, H, flags);
+    return nx;
+}
+
+int input_flags(const LayerW &L) { return dig_flags({L.q_a, L.q_proj, L.kv_a}); }
+
 // run_layer (model.rs:127-183) / the per-layer body of prefill (:470-526).
-int32_t run_layer(ut_session *s, const LayerW &L, float *x, int64_t rows, KvCache &kv) {
+// pre: the input norm already ran (its rows in ws.normed, digits *pre).
+// next: the following norm, run by the layer's last combine.
+int32_t run_layer(ut_session *s, const LayerW &L, float *x, int64_t rows, KvCache &kv,
+                  const XDigits *pre = nullptr, const NormNext *next = nullptr) {
     ut_model *m = s->m;
     ut_ctx *ctx = m->ctx;
     const ut_model_config &c = m->c;
     const int64_t H = c.hidden_size;
     Workspace &w = s->ws;
     XDigits xd;
-    UT_TRY(norm_dig(s, x, H, L.input_norm, H, rows, w.normed, H, w.digA,
-                    dig_flags({L.q_a, L.q_proj, L.kv_a}), &xd));
+    if (pre) xd = *pre;
+    else UT_TRY(norm_dig(s, x, H, L.input_norm, H, rows, w.normed, H, w.digA, input_flags(L), &xd));
     int f = 0;
     if (L.dense) f = dig_flags_fmt(L.mlp.fmt, H);
     else {
@@ -631,13 +662,13 @@ int32_t run_layer(ut_session *s, const LayerW &L, float *x, int64_t rows, KvCach
     }
     UT_TRY(mla_forward(s, L, w.normed, xd, rows, kv, x));
     UT_TRY(norm_dig(s, x, H, L.post_norm, H, rows, w.normed, H, w.digA, f, &xd));
-    if (L.dense) return mlp_add(s, L.mlp, w.normed, xd, rows, x);
+    if (L.dense) return mlp_add(s, L.mlp, w.normed, xd, rows, x, nullptr, next);
     // x += (routed + shared) (model.rs:282-284 then the residual add)
     if (L.has_shared && moe_dual_ok(L.expert_fmt, L.shared.fmt))
-        return moe_forward(s, L, w.normed, xd, rows, x, 1, &L.shared);
-    if (!L.has_shared) return moe_forward(s, L, w.normed, xd, rows, x, 1);
+        return moe_forward(s, L, w.normed, xd, rows, x, 1, &L.shared, next);
+    if (!L.has_shared) return moe_forward(s, L, w.normed, xd, rows, x, 1, nullptr, next);
     UT_TRY(moe_forward(s, L, w.normed, xd, rows, w.moe_out));
-    return mlp_add(s, L.shared, w.normed, xd, rows, x, w.moe_out);
+    return mlp_add(s, L.shared, w.normed, xd, rows, x, w.moe_out, next);
 }
 
 int32_t check_flags(ut_session *s) {
@@ -698,15 +729,30 @@ int32_t prefill_dev(ut_session *s, const int32_t *ids, int64_t n, const int32_t 
     const int64_t H = c.hidden_size, V = c.vocab_size;
     if (!ids_dev) UT_TRY(upload_ids(s, ids, n));
     UT_TRY(launch_embed(ctx, m->embed, ids_dev ? ids_dev : w.ids, n, w.x, H));
-    for (size_t li = 0; li < m->layers.size(); li++) UT_TRY(run_layer(s, m->layers[li], w.x, n, s->kv[li]));
+    // each layer's last combine runs the norm that follows it when the rows
+    // fit one combine (decode and verify steps)
+    const bool fuse = fuse_next_ok(m, n);
+    XDigits cur, nxt;
+    const size_t nl = m->layers.size();
+    for (size_t li = 0; li < nl; li++) {
+        NormNext nx;
+        if (fuse)
+            nx = li + 1 < nl ? next_norm(s, m->layers[li + 1].input_norm,
+                                         input_flags(m->layers[li + 1]), n, &nxt)
+                             : next_norm(s, m->final_norm, dig_flags({m->lm_head}), n, &nxt);
+        UT_TRY(run_layer(s, m->layers[li], w.x, n, s->kv[li], fuse && li > 0 ? &cur : nullptr,
+                         fuse ? &nx : nullptr));
+        cur = nxt;
+    }
     if (m->has_mtp)
         UT_CHECK_HIP(ctx, hipMemcpyAsync(s->hidden + s->pos * H, w.x, (size_t)n * H * 4,
                                          hipMemcpyDeviceToDevice, ctx->stream));
     s->pos += n;
     if (!ids_dev) s->tokens.insert(s->tokens.end(), ids, ids + n);
-    XDigits fd;
-    UT_TRY(norm_dig(s, w.x, H, m->final_norm, H, n, w.normed, H, w.digA, dig_flags({m->lm_head}),
-                    &fd));
+    XDigits fd = cur;
+    if (!fuse || nl == 0)
+        UT_TRY(norm_dig(s, w.x, H, m->final_norm, H, n, w.normed, H, w.digA,
+                        dig_flags({m->lm_head}), &fd));
     UT_TRY(matmul_digits(ctx, m->lm_head, w.normed, fd, n, w.logits, V, 0));
     return launch_argmax(ctx, w.logits, n, V, V, w.am, w.argm);
 }
@@ -807,11 +853,21 @@ int32_t draft_rows_dev(ut_session *s, const int32_t *host_ids, int in_slot,
     UT_TRY(launch_rmsnorm(ctx, w.emb, H, m->enorm, H, c.rms_norm_eps, rows, w.cat, 2 * H));
     UT_TRY(launch_rmsnorm(ctx, hidden_rows, H, m->hnorm, H, c.rms_norm_eps, rows, w.cat + H, 2 * H));
     UT_TRY(mm(s, m->eh_proj, w.cat, rows, w.x, H));
-    UT_TRY(run_layer(s, m->mtp_layer, w.x, rows, s->mtp_kv));
     XDigits hd_;
-    UT_TRY(norm_dig(s, w.x + (rows - 1) * H, H, m->mtp_norm, H, 1, w.normed, H, w.digA,
-                    dig_flags({m->mtp_head}), &hd_));
-    UT_TRY(matmul_digits(ctx, m->mtp_head, w.normed, hd_, 1, w.logits, V, 0));
+    const float *hn = w.normed;
+    if (fuse_next_ok(m, rows)) {
+        // the layer's last combine normalises every row; the head reads the last
+        XDigits all;
+        const NormNext nx = next_norm(s, m->mtp_norm, dig_flags({m->mtp_head}), rows, &all);
+        UT_TRY(run_layer(s, m->mtp_layer, w.x, rows, s->mtp_kv, nullptr, &nx));
+        hd_ = xdigits_rows(all, rows - 1);
+        hn = w.normed + (rows - 1) * H;
+    } else {
+        UT_TRY(run_layer(s, m->mtp_layer, w.x, rows, s->mtp_kv));
+        UT_TRY(norm_dig(s, w.x + (rows - 1) * H, H, m->mtp_norm, H, 1, w.normed, H, w.digA,
+                        dig_flags({m->mtp_head}), &hd_));
+    }
+    UT_TRY(matmul_digits(ctx, m->mtp_head, hn, hd_, 1, w.logits, V, 0));
     return launch_argmax(ctx, w.logits, 1, V, V, draft_dev, w.argm);
 }
 

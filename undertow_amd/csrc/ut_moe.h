@@ -33,6 +33,18 @@ struct MoePlan {
 enum { kSpGate = 0, kSpUp = 1, kSpDown = 2, kSpGateS = 3, kSpUpS = 4, kSpDownS = 5 };
 
 // One pass of the expert block over M <= 4 rows (all on device).
+// The next input norm, run by the launch that finishes a residual row:
+// normed = rmsnorm(out row, norm_w) (f32, row stride ldn) and its digit
+// forms (flags) in nd, rows counted from the call's first row.
+struct NormNext {
+    const float *norm_w = nullptr;
+    float eps = 0.0f;
+    float *normed = nullptr;
+    int64_t ldn = 0;
+    XDigits nd;
+    int flags = 0;
+};
+
 struct MoeCall {
     int fmt = UT_FMT_INT4;
     ExpertPtrs tbl;
@@ -57,7 +69,11 @@ struct MoeCall {
     // own scratch of moe_layout(M, 1, 1, H, I, fmt).total bytes.
     const MoeCall *shared = nullptr;
     void *shared_scratch = nullptr;
+    // optional: the combine also rms-normalises and digitises the finished
+    // rows of out (one launch instead of two; H <= 8192, H % 8 == 0)
+    const NormNext *next = nullptr;
 };
+bool moe_combine_norm_ok(int64_t H);
 
 struct ScratchLayout {
     size_t total = 0;

@@ -17,6 +17,7 @@
 // the row dimension rides along in the same instructions.
 #include "ut_gemv_core.h"
 #include "ut_moe.h"
+#include "ut_rowdig.h"
 
 
 namespace ut {
@@ -698,6 +699,68 @@ __global__ void k_moe_combine(const int32_t *__restrict__ choice_slot,
     *po = accumulate ? __fadd_rn(*po, acc) : acc;
 }
 
+// The same combine for one row per workgroup (thread t: columns 8t..8t+7,
+// each computed exactly as k_moe_combine does), then the finished row
+// rms-normalised and digitised by the row digitiser's body (nd: K = H).
+__global__ __launch_bounds__(1024) void k_moe_combine_norm(
+    const int32_t *__restrict__ choice_slot, const float *__restrict__ weights,
+    const float *__restrict__ d, int M, int k, int64_t H, const int32_t *__restrict__ count,
+    int extra, const float *__restrict__ dshared, const float *__restrict__ init,
+    float *__restrict__ out, int64_t ldo, int accumulate, RowDigArgs nd) {
+    __shared__ double redd[16];
+    __shared__ uint32_t redu[16];
+    const int s = blockIdx.x, tid = threadIdx.x;
+    const int64_t c0 = 8 * (int64_t)tid;
+    float v[1][8], wv[1][8];
+    auto ld8 = [](const float *p, float (&r)[8]) {
+        const float4 a = *(const float4 *)p, b = *(const float4 *)(p + 4);
+        r[0] = a.x; r[1] = a.y; r[2] = a.z; r[3] = a.w;
+        r[4] = b.x; r[5] = b.y; r[6] = b.z; r[7] = b.w;
+    };
+    if (c0 < H) {
+        float acc[8], t[8];
+        if (init) ld8(init + s * ldo + c0, acc);
+        else
+#pragma unroll
+            for (int j = 0; j < 8; j++) acc[j] = 0.0f;
+        for (int c = 0; c < k; c++) {
+            const int slot = choice_slot[s * k + c];
+            if (slot < 0) continue;
+            const float wc = weights[s * k + c];
+            ld8(d + ((int64_t)slot * M + s) * H + c0, t);
+#pragma unroll
+            for (int j = 0; j < 8; j++) acc[j] = __fadd_rn(acc[j], __fmul_rn(wc, t[j]));
+        }
+        if (extra) {
+            ld8(d + ((int64_t)(*count - 1) * M + s) * H + c0, t);
+#pragma unroll
+            for (int j = 0; j < 8; j++) acc[j] = __fadd_rn(acc[j], t[j]);
+        }
+        if (dshared) {
+            ld8(dshared + (int64_t)s * H + c0, t);
+#pragma unroll
+            for (int j = 0; j < 8; j++) acc[j] = __fadd_rn(acc[j], t[j]);
+        }
+        float *po = out + s * ldo + c0;
+        if (accumulate) {
+            ld8(po, t);
+#pragma unroll
+            for (int j = 0; j < 8; j++) acc[j] = __fadd_rn(t[j], acc[j]);
+        }
+        *(float4 *)po = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        *(float4 *)(po + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+        ld8(nd.norm_w + c0, wv[0]);
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[0][j] = acc[j];
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[0][j] = 0.0f, wv[0][j] = 0.0f;
+    }
+    rowdig_body<1>(nd, s, v, wv, redd, redu);
+}
+
+bool moe_combine_norm_ok(int64_t H) { return H % 8 == 0 && H <= 8 * 1024; }
+
 // ------------------------------------------------------------- driver ---
 size_t moe_scratch_bytes(int64_t M, int64_t k, int64_t slots, int64_t H, int64_t I, int fmt) {
     ScratchLayout L = moe_layout(M, k, slots, H, I, fmt);
@@ -899,6 +962,33 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
         launch_down<FMT, M>(ctx, a, slots, c.shared ? &db : nullptr, c.shared ? c.shared->fmt : 0);
         timing_end(ctx, tok);
         UT_TRY(launch_check(ctx, "k_moe_down"));
+    }
+    if (c.next) {
+        if (!moe_combine_norm_ok(c.H) || ((uintptr_t)c.out & 15) != 0 || c.ldo % 4 != 0 ||
+            (c.init && ((uintptr_t)c.init & 15) != 0) || !c.next->norm_w || !c.next->nd.exps) {
+            set_error(ctx, "moe_pass: fused next norm needs H %% 8 == 0, H <= 8192 and 16-byte "
+                           "aligned rows (H=%lld)", (long long)c.H);
+            return UT_ERR_ARG;
+        }
+        const NormNext &nx = *c.next;
+        RowDigArgs nd{};
+        nd.K = c.H;
+        nd.norm_w = nx.norm_w;
+        nd.eps = nx.eps;
+        nd.out = nx.normed;
+        nd.ldo = nx.ldn;
+        nd.exps = nx.nd.exps;
+        nd.dig4 = (nx.flags & XD_DIG4) ? nx.nd.dig4 : nullptr;
+        nd.dig8 = (nx.flags & XD_DIG8) ? nx.nd.dig8 : nullptr;
+        nd.xt = (nx.flags & XD_XT) ? nx.nd.xt : nullptr;
+        tok = timing_begin(ctx, "moe_combine_norm");
+        const unsigned threads = (unsigned)((c.H / 8 + 63) / 64 * 64);
+        hipLaunchKernelGGL(k_moe_combine_norm, dim3((unsigned)M), dim3(threads), 0, ctx->stream,
+                           plan.choice_slot, c.weights, d, M, c.k, c.H, plan.count,
+                           c.extra_slot >= 0 ? 1 : 0, dshared, c.init, c.out, c.ldo, c.accumulate,
+                           nd);
+        timing_end(ctx, tok);
+        return launch_check(ctx, "k_moe_combine_norm");
     }
     tok = timing_begin(ctx, "moe_combine");
     hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((c.H + 255) / 256), (unsigned)M), dim3(256),
