@@ -187,15 +187,22 @@ def test_moe_experts_deepseek_shape(ctx, fmt, Ms):
         want = oracle_moe(fmt, H, I, host_w, ids, w, x)
         tol = 1e-4 * np.maximum(np.abs(want), 1.0)
         assert (np.abs(got - want) <= tol).all(), (M, np.abs(got - want).max())
+        # a one-row call (the gate/up launch plans and digitises x itself)
+        # gives the multi-row call's row bit for bit
+        if M > 1:
+            for s in range(M):
+                one = host(tbl.moe_experts(dev(ids[s:s + 1]), dev(w[s:s + 1]), dev(x[s:s + 1])))
+                assert np.array_equal(one[0], got[s]), (M, s)
 
 
-def test_moe_bad_expert_is_reported(ctx):
+@pytest.mark.parametrize("H", [64, 256])  # 256: the gate/up launch resolves the plan
+def test_moe_bad_expert_is_reported(ctx, H):
     import undertow_amd as U
     rng = np.random.default_rng(3)
-    tbl, _ = make_experts(ctx, rng, INT8, 4, 64, 32)
+    tbl, _ = make_experts(ctx, rng, INT8, 4, H, 32)
     ids = np.array([[1, 9]], np.int32)
     out = tbl.moe_experts(dev(ids), dev(np.ones((1, 2), np.float32)),
-                          dev(np.ones((1, 64), np.float32)))
+                          dev(np.ones((1, H), np.float32)))
     with pytest.raises(U.UtError) as ei:
         ctx.synchronize()
     assert ei.value.code == U.runtime.UT_ERR_BAD_EXPERT

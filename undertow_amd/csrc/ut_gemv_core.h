@@ -82,7 +82,15 @@ struct XSrc {
     const float *xf;      // [M][ldx] (f32)
     int64_t ldx;
     int32_t sh[4];        // staging-time digitisation shifts (dig == nullptr)
+    // dig == nullptr: the shifts come from the staged rows' own max|x|
+    // (single-chunk staging only) instead of sh
+    int self_max = 0;
 };
+
+typedef unsigned int ut_u32x4 __attribute__((ext_vector_type(4)));
+template <int M>
+__device__ __forceinline__ void rowmax_reduce(const ut_u32x4 (&q)[M], int32_t (&sh)[M],
+                                              uint32_t *red);
 
 // Balanced digits of 8 (int4) or 4 (int8) columns, one word per plane.
 // With u = x~ + 0x888888 (int4; 0x808080 for int8) every digit of u is the
@@ -116,7 +124,6 @@ __device__ __forceinline__ void digit_words(const float *v, int n, int32_t sh,
 // counter and force conservative waits).
 // (Loaded as native vectors: a class type's copy constructor would take the
 // address back to the generic space.)
-typedef unsigned int ut_u32x4 __attribute__((ext_vector_type(4)));
 typedef float ut_f32x4 __attribute__((ext_vector_type(4)));
 template <typename T> __device__ __forceinline__ T ld_global(const void *p);
 template <> __device__ __forceinline__ uint4 ld_global<uint4>(const void *p) {
@@ -221,9 +228,19 @@ __device__ __forceinline__ void gemv_stage(const XSrc &x, uint32_t *lds, int64_t
 // go to LDS.  The activation loads (L2 hits) are older than the weight
 // loads, so the LDS writes wait for them alone and the weights stay in
 // flight across the barrier.
-template <int FMT, int M, typename Issue>
+// The digitise branch calls prep(sh) after issue() and before the
+// barrier: a caller whose digitisation shifts are still being reduced
+// finishes them there, with the weights already in flight.
+struct NoPrep {
+    __device__ void operator()(int32_t (&)[4]) const {}
+};
+struct NoMid {
+    __device__ void operator()() const {}
+};
+
+template <int FMT, int M, typename Issue, typename Prep = NoPrep>
 __device__ __forceinline__ void gemv_stage_once(const XSrc &x, uint32_t *lds, int64_t kc, int kcn,
-                                                Issue &&issue) {
+                                                Issue &&issue, Prep &&prep = Prep{}) {
     using T = FmtTraits<FMT>;
     constexpr int KC = gemv_chunk_cols<FMT, M>();
     constexpr int PL = T::kPlanes;
@@ -286,6 +303,36 @@ __device__ __forceinline__ void gemv_stage_once(const XSrc &x, uint32_t *lds, in
             for (int q = 0; q < NV; q++) v[j][q] = ld_global<float4>(src + 4 * q);
         }
         issue();
+        // prep's waits stay behind every load above
+        __builtin_amdgcn_sched_barrier(0);
+        int32_t shl[4] = {x.sh[0], x.sh[1], x.sh[2], x.sh[3]};
+        if (x.self_max) {
+            // max|x| of each row over the whole staged range (kcn = the
+            // row's columns): the row digitiser's exponent rule
+            ut_u32x4 q[M];
+#pragma unroll
+            for (int m = 0; m < M; m++) q[m] = ut_u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int j = 0; j < NI; j++) {
+                const int i = tid + j * kGemvThreads;
+                const int mi = i < tot ? i / ng : -1;
+                uint32_t b = 0;
+#pragma unroll
+                for (int q4 = 0; q4 < NV; q4++) {
+                    b = max(b, max(max(__float_as_uint(fabsf(v[j][q4].x)), __float_as_uint(fabsf(v[j][q4].y))),
+                                   max(__float_as_uint(fabsf(v[j][q4].z)), __float_as_uint(fabsf(v[j][q4].w)))));
+                }
+#pragma unroll
+                for (int m = 0; m < M; m++)
+                    if (mi == m) q[m][0] = max(q[m][0], b);
+            }
+            __shared__ uint32_t red[4 * M];
+            int32_t sh[M];
+            rowmax_reduce<M>(q, sh, red);
+#pragma unroll
+            for (int m = 0; m < M; m++) shl[m] = sh[m];
+        }
+        prep(shl);
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < NI; j++) {
@@ -299,7 +346,7 @@ __device__ __forceinline__ void gemv_stage_once(const XSrc &x, uint32_t *lds, in
                     f[4 * q + 2] = v[j][q].z; f[4 * q + 3] = v[j][q].w;
                 }
                 uint32_t w[PL];
-                const int32_t shm = m == 0 ? x.sh[0] : m == 1 ? x.sh[1] : m == 2 ? x.sh[2] : x.sh[3];
+                const int32_t shm = m == 0 ? shl[0] : m == 1 ? shl[1] : m == 2 ? shl[2] : shl[3];
                 digit_words<FMT>(f, CPW, shm, w);
 #pragma unroll
                 for (int p = 0; p < PL; p++) lds[(m * PL + p) * LW + g] = w[p];
@@ -421,10 +468,26 @@ __device__ __forceinline__ void gemv_load(const uint8_t *const rows[R], int64_t 
 // no staging branch and no per-lane bounds: straight-line code in which
 // the compiler's wait counts keep the DEPTH-1 younger steps in flight (a
 // staging branch inside the loop makes it drain every load first).
-template <int FMT, int M, int R = kGemvRows, int DEPTH = gemv_depth<M>()>
+// Whether gemv_core stages the columns [k_begin, kend) once (the
+// straight-line path, the only one that calls prep).
+template <int FMT, int M>
+__device__ __forceinline__ bool gemv_one_chunk(int64_t k_begin, int64_t kend) {
+    constexpr int KC = gemv_chunk_cols<FMT, M>();
+    constexpr int STEP = FmtTraits<FMT>::kStepCols;
+    return kend > k_begin && kend - k_begin <= KC && (kend - k_begin) % STEP == 0;
+}
+
+//
+// prep: see gemv_stage_once (single-chunk path with f32 activations only;
+// the caller must not rely on it elsewhere).  mid: runs on the single-chunk
+// path after the activation loads are issued and before the first weight
+// loads, which read rows[] only then (so mid may still fill rows in).
+template <int FMT, int M, int R = kGemvRows, int DEPTH = gemv_depth<M>(), typename Prep = NoPrep,
+          typename Mid = NoMid>
 __device__ __forceinline__ void gemv_core(const uint8_t *const rows[R], int64_t K, const XSrc &x,
                                           uint32_t *lds, CoreOut<FMT, M, R> &res,
-                                          int64_t k_begin = 0, int64_t k_end = -1) {
+                                          int64_t k_begin = 0, int64_t k_end = -1,
+                                          Prep &&prep = Prep{}, Mid &&mid = Mid{}) {
     using T = FmtTraits<FMT>;
     constexpr int KC = gemv_chunk_cols<FMT, M>();
     constexpr int STEP = T::kStepCols;    // columns per step (16 sub-lanes)
@@ -438,14 +501,15 @@ __device__ __forceinline__ void gemv_core(const uint8_t *const rows[R], int64_t 
     const int64_t lane_col = k_begin + (int64_t)s * LANE_COLS;
     uint4 wq[DEPTH][R];
     auto loadk = [&](uint4 (&w)[R], int64_t col) { if (col < kend) gemv_load<FMT, R>(rows, col, w); };
-    if (nsteps > 0 && kend - k_begin <= KC && (kend - k_begin) % STEP == 0) {
+    if (gemv_one_chunk<FMT, M>(k_begin, kend)) {
         // unconditional (clamped) first loads: a skipped load on any path
         // into the loop would make the wait counts inside it conservative
         gemv_stage_once<FMT, M>(x, lds, k_begin, (int)(kend - k_begin), [&]() {
+            mid();
 #pragma unroll
             for (int u = 0; u < DEPTH; u++)
                 gemv_load<FMT, R>(rows, lane_col + (u < nsteps ? u : nsteps - 1) * STEP, wq[u]);
-        });
+        }, prep);
         const int c0 = s * LANE_COLS;
         int64_t t = 0;
         for (; t + 2 * DEPTH <= nsteps; t += DEPTH) {
@@ -553,25 +617,44 @@ template <> struct DppBits<float> {
 // non-finite row.  Whole workgroup of kGemvThreads; red: 4*M words of LDS.
 // 16-byte loads when nparts % 4 == 0 (16-byte aligned rows), DPP wave
 // maxima, LDS-only barriers.
+// This thread's share of the partial maxima: rowmax_load issues the loads
+// (one 16-byte load per thread per row when nparts % 4 == 0 and
+// nparts <= 4 * kGemvThreads; threads past the end re-read the row's first
+// four, which leaves the maximum unchanged) without waiting for them, so a
+// caller can put them ahead of other loads; rowmax_reduce finishes the
+// shifts.
 template <int M>
-__device__ __forceinline__ void rowmax_shifts(const uint32_t *parts, int nparts,
-                                              int32_t (&sh)[M], uint32_t *red) {
-    uint32_t mx[M];
+__device__ __forceinline__ void rowmax_load(const uint32_t *parts, int nparts, ut_u32x4 (&q)[M]) {
     const int tid = threadIdx.x;
 #pragma unroll
     for (int m = 0; m < M; m++) {
         const uint32_t *pr = parts + (int64_t)m * nparts;
+        if ((nparts & 3) == 0 && nparts <= 4 * kGemvThreads) {
+            q[m] = *(const ut_u32x4 *)(pr + (4 * tid < nparts ? 4 * tid : 0));
+            continue;
+        }
         uint32_t v = 0;
         if ((nparts & 3) == 0) {
             for (int i = 4 * tid; i < nparts; i += 4 * kGemvThreads) {
-                const ut_u32x4 q = *(const ut_u32x4 *)(pr + i);
-                v = max(v, max(max(q[0], q[1]), max(q[2], q[3])));
+                const ut_u32x4 w = *(const ut_u32x4 *)(pr + i);
+                v = max(v, max(max(w[0], w[1]), max(w[2], w[3])));
             }
         } else {
             for (int i = tid; i < nparts; i += kGemvThreads) v = max(v, pr[i]);
         }
-        mx[m] = wave_reduce_dpp(v, [](uint32_t p, uint32_t q) { return p > q ? p : q; });
+        q[m] = ut_u32x4{v, v, v, v};
     }
+}
+
+template <int M>
+__device__ __forceinline__ void rowmax_reduce(const ut_u32x4 (&q)[M], int32_t (&sh)[M],
+                                              uint32_t *red) {
+    uint32_t mx[M];
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int m = 0; m < M; m++)
+        mx[m] = wave_reduce_dpp(max(max(q[m][0], q[m][1]), max(q[m][2], q[m][3])),
+                                [](uint32_t p, uint32_t q) { return p > q ? p : q; });
     if ((tid & 63) == 0)
 #pragma unroll
         for (int m = 0; m < M; m++) red[(tid >> 6) * M + m] = mx[m];
@@ -585,6 +668,14 @@ __device__ __forceinline__ void rowmax_shifts(const uint32_t *parts, int nparts,
     }
     // red may be reused right away by the caller
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+template <int M>
+__device__ __forceinline__ void rowmax_shifts(const uint32_t *parts, int nparts,
+                                              int32_t (&sh)[M], uint32_t *red) {
+    ut_u32x4 q[M];
+    rowmax_load<M>(parts, nparts, q);
+    rowmax_reduce<M>(q, sh, red);
 }
 
 __device__ __forceinline__ int32_t rowmax_shift(const uint32_t *parts, int nparts, int64_t row,

@@ -473,7 +473,71 @@ struct GateUpArgs {
     float *h;                 // [slots][M][I]
     uint32_t *hmax_parts;     // [slots][M][ntiles] float bits
     int ntiles;
+    // optional (plan_ids set; one row, k <= 64): every wave resolves its
+    // slot from the expert ids itself and workgroup (0, 0) writes the plan
+    // for the later launches, so no plan launch runs first; x is then f32
+    // with self_max
+    const int32_t *plan_ids = nullptr;
+    int plan_M = 0, plan_k = 0;
+    int64_t E = 0;
+    const void *const *ptbl = nullptr;  // [6][E] pointer table
+    MoePlan plan{};
+    int32_t *err_flag = nullptr;
 };
+
+// The slot plan of make_plan for one activation row (n = k <= 64 entries),
+// resolved by each wave on its own (lane j holds entry j; no LDS, no
+// barrier): returns the slot count and lane `slot u's first entry`'s
+// pointers in p6 (unset when u >= count).  The writer wave also writes the
+// plan and the invalid-id flag exactly as make_plan does.  id: this lane's
+// entry (-1 past n), loaded by the caller ahead of other loads.
+__device__ inline int plan_slot_wave(int id, int n, int64_t E, const void *const *__restrict__ tbl,
+                                     int u, bool writer, MoePlan plan,
+                                     int32_t *__restrict__ err_flag, const void *(&p6)[6]) {
+    const int lane = threadIdx.x & 63;
+    const bool inr = lane < n && id >= 0 && id < E;
+    const int64_t ec = inr ? id : 0;
+    const void *p[6];
+#pragma unroll
+    for (int i = 0; i < 6; i++) p[i] = tbl[(int64_t)i * E + ec];
+    const bool ok = inr && p[kSpGate] != nullptr;
+    const int e = ok ? id : -1;
+    // j0: the entry's first appearance (the reference groups rows by expert
+    // in first-appearance order, model.rs:219-233)
+    int j0 = lane;
+    for (int i = 0; i < n; i++) {
+        const int ei = __builtin_amdgcn_readlane(e, i);
+        if (i < j0 && ei == e) j0 = i;
+    }
+    const bool first = ok && j0 == lane;
+    const uint64_t fm = __ballot(first);
+    const int slot = ok ? __popcll(fm & ((1ull << j0) - 1)) : -1;
+    const int cnt = __popcll(fm);
+    const uint64_t um = __ballot(first && slot == u);
+    if (um) {
+        const int L = __ffsll((unsigned long long)um) - 1;
+#pragma unroll
+        for (int i = 0; i < 6; i++) {
+            const uint64_t v = (uint64_t)p[i];
+            const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, L);
+            const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), L);
+            p6[i] = (const void *)(((uint64_t)hi << 32) | lo);
+        }
+    }
+    if (writer) {
+        if (lane < n) {
+            if (!ok && id != -1 && err_flag) *err_flag = 1;
+            plan.choice_slot[lane] = slot;
+            if (first) {
+                plan.uniq[slot] = e;
+#pragma unroll
+                for (int i = 0; i < 6; i++) plan.sp[slot * 6 + i] = p[i];
+            }
+        }
+        if (lane == 0) *plan.count = cnt;
+    }
+    return cnt;
+}
 
 // 16 h-rows per workgroup: wave w, row group g -> h row o = tile*16 +
 // w*4 + g; row slot 0 reads gate row o, slot 1 up row o, so both land in the
@@ -481,18 +545,54 @@ struct GateUpArgs {
 template <int FMT, int M>
 __device__ __forceinline__ void gate_up_body(const GateUpArgs &a, int u, int tile, uint32_t *lds,
                                              uint32_t *wg_max) {
-    // the slot count and the slot's pointers load in parallel
-    const int cnt = *a.count;
-    const uint8_t *gw = (const uint8_t *)a.sp[u * 6 + kSpGate], *uw = (const uint8_t *)a.sp[u * 6 + kSpUp];
-    const float *gsc = (const float *)a.sp[u * 6 + kSpGateS], *usc = (const float *)a.sp[u * 6 + kSpUpS];
-    if (u >= cnt || tile >= a.ntiles) return;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
-    if (tid < 4) wg_max[tid] = 0;
     const int64_t o = (int64_t)tile * kGateUpRowsPerWG + wave * 4 + g;
     const int64_t oc = o < a.I ? o : a.I - 1;
-    const uint8_t *rows[2] = {gw + oc * a.row_bytes, uw + oc * a.row_bytes};
+    const uint8_t *rows[2];
+    const float *gsc = nullptr, *usc = nullptr;
+    int cnt = 0;
+    if (tid < 4) wg_max[tid] = 0;  // published by the core's barriers
     CoreOut<FMT, M, 2> res;
-    gemv_core<FMT, M, 2, gemv_depth<M>()>(rows, a.H, a.x, lds, res);
+    // x's exponents: given, or (self_max) found while x is staged
+    int32_t exl[M];
+    auto prep = [&](int32_t (&shl)[4]) {
+#pragma unroll
+        for (int m = 0; m < M; m++) exl[m] = shl[m] == INT32_MIN ? INT32_MIN : -shl[m];
+    };
+    if (a.plan_ids) {
+        // one activation row: this wave resolves the slot from the ids
+        // (loaded ahead of x) while x's loads are in flight; a slot past the
+        // count streams x itself in place of weights (valid memory of at
+        // least a row's bytes) and stores nothing
+        if (!gemv_one_chunk<FMT, M>(0, a.H)) return;  // the host's condition for plan_ids
+        const int id = lane < a.plan_k ? a.plan_ids[lane] : -1;
+        auto mid = [&]() {
+            const void *p6[6];
+            cnt = plan_slot_wave(id, a.plan_k, a.E, a.ptbl, u, u == 0 && tile == 0 && wave == 0,
+                                 a.plan, a.err_flag, p6);
+            const bool live = u < cnt;
+            rows[0] = live ? (const uint8_t *)p6[kSpGate] + oc * a.row_bytes : (const uint8_t *)a.x.xf;
+            rows[1] = live ? (const uint8_t *)p6[kSpUp] + oc * a.row_bytes : (const uint8_t *)a.x.xf;
+            gsc = live ? (const float *)p6[kSpGateS] : nullptr;
+            usc = live ? (const float *)p6[kSpUpS] : nullptr;
+        };
+        gemv_core<FMT, M, 2, gemv_depth<M>()>(rows, a.H, a.x, lds, res, 0, -1, prep, mid);
+        if (u >= cnt || tile >= a.ntiles) return;
+    } else {
+        // the slot count and the slot's pointers load in parallel
+        cnt = *a.count;
+        const uint8_t *gw = (const uint8_t *)a.sp[u * 6 + kSpGate];
+        const uint8_t *uw = (const uint8_t *)a.sp[u * 6 + kSpUp];
+        gsc = (const float *)a.sp[u * 6 + kSpGateS];
+        usc = (const float *)a.sp[u * 6 + kSpUpS];
+        if (u >= cnt || tile >= a.ntiles) return;
+        rows[0] = gw + oc * a.row_bytes;
+        rows[1] = uw + oc * a.row_bytes;
+        if constexpr (FMT != UT_FMT_F32)
+#pragma unroll
+            for (int m = 0; m < M; m++) exl[m] = a.exps[m];
+        gemv_core<FMT, M, 2, gemv_depth<M>()>(rows, a.H, a.x, lds, res, 0, -1, prep);
+    }
 #pragma unroll
     for (int m = 0; m < M; m++) {
         // f32: the gate value lives on sub-lane m, the up value on 4 + m
@@ -503,8 +603,8 @@ __device__ __forceinline__ void gate_up_body(const GateUpArgs &a, int u, int til
         }
         if (s == m && o < a.I) {
             if constexpr (FMT != UT_FMT_F32) {
-                gv = int_total_to_f32(res.S[0][m], a.exps[m], ld_global_f32(gsc + o));
-                uv = int_total_to_f32(res.S[1][m], a.exps[m], ld_global_f32(usc + o));
+                gv = int_total_to_f32(res.S[0][m], exl[m], ld_global_f32(gsc + o));
+                uv = int_total_to_f32(res.S[1][m], exl[m], ld_global_f32(usc + o));
             }
             // silu(g) * u (undertow-quant/src/lib.rs:121; model.rs:241-247)
             float sg = gv / (1.0f + expf(-gv));
@@ -565,6 +665,15 @@ __device__ __forceinline__ int32_t h_shift(const uint32_t *hmax_parts, int npart
 // Rows per lane: 4 at M <= 2 (more activation reuse), 2 above (registers).
 template <int M> constexpr int down_rows() { return M <= 2 ? 4 : 2; }
 
+// Weight steps in flight in down.
+template <int M> constexpr int down_depth() {
+#ifdef UT_DOWN_DEPTH
+    return M == 1 ? UT_DOWN_DEPTH : gemv_depth<M>();
+#else
+    return gemv_depth<M>();
+#endif
+}
+
 template <int FMT, int M>
 __device__ __forceinline__ void down_body(const DownArgs &a, int u, int tile, uint32_t *lds) {
     constexpr int R = down_rows<M>();
@@ -584,20 +693,40 @@ __device__ __forceinline__ void down_body(const DownArgs &a, int u, int tile, ui
     xs.xf = a.x.xf + u * a.x_slot_stride;
     xs.dig = nullptr;
     int32_t exl[M];
+    const int64_t kb = a.ks > 1 ? (int64_t)blockIdx.z * a.kslice : 0;
+    const int64_t ke = a.ks > 1 ? (kb + a.kslice < a.I ? kb + a.kslice : a.I) : a.I;
+    // the row exponents of h from the gate/up workgroups' partial maxima:
+    // their loads go out first; on the one-chunk path the reduction runs
+    // inside the staging, after the first weight loads (prep)
+    __shared__ uint32_t red[4 * M];
+    ut_u32x4 pv[M];
+    const bool late = FMT != UT_FMT_F32 && gemv_one_chunk<FMT, M>(kb, ke);
     if constexpr (FMT != UT_FMT_F32) {
-        // the row exponent of h from the gate/up workgroups' partial maxima
-        __shared__ uint32_t red4[4];
+        rowmax_load<M>(a.hmax_parts + (int64_t)u * M * a.nparts, a.nparts, pv);
+        if (!late) {
+            int32_t sh[M];
+            rowmax_reduce<M>(pv, sh, red);
 #pragma unroll
-        for (int m = 0; m < M; m++) {
-            const int32_t sh = h_shift(a.hmax_parts, a.nparts, (int64_t)u * M + m, red4);
-            xs.sh[m] = sh;
-            exl[m] = sh == INT32_MIN ? INT32_MIN : -sh;
+            for (int m = 0; m < M; m++) {
+                xs.sh[m] = sh[m];
+                exl[m] = sh[m] == INT32_MIN ? INT32_MIN : -sh[m];
+            }
         }
     }
+    auto prep = [&](int32_t (&shl)[4]) {
+        if constexpr (FMT != UT_FMT_F32) {
+            int32_t sh[M];
+            rowmax_reduce<M>(pv, sh, red);
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                shl[m] = sh[m];
+                exl[m] = sh[m] == INT32_MIN ? INT32_MIN : -sh[m];
+            }
+        }
+    };
     CoreOut<FMT, M, R> res;
     if (a.ks > 1) {
-        const int64_t kb = (int64_t)blockIdx.z * a.kslice;
-        gemv_core<FMT, M, R, gemv_depth<M>()>(rows, a.I, xs, lds, res, kb, kb + a.kslice);
+        gemv_core<FMT, M, R, down_depth<M>()>(rows, a.I, xs, lds, res, kb, ke, prep);
         const int64_t slots = gridDim.y;
 #pragma unroll
         for (int r = 0; r < R; r++)
@@ -610,7 +739,7 @@ __device__ __forceinline__ void down_body(const DownArgs &a, int u, int tile, ui
             }
         return;
     }
-    gemv_core<FMT, M, R, gemv_depth<M>()>(rows, a.I, xs, lds, res);
+    gemv_core<FMT, M, R, down_depth<M>()>(rows, a.I, xs, lds, res, 0, -1, prep);
 #pragma unroll
     for (int r = 0; r < R; r++)
 #pragma unroll
@@ -837,9 +966,19 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
     int tok = -1;
     XSrc xs{};
     const int32_t *xexps = nullptr;
+    // expert ids given and x not digitised: the gate/up workgroups resolve
+    // the plan and digitise x themselves (x staged whole, as f32)
+    constexpr int64_t KC = gemv_chunk_cols<FMT, M>();
+    const bool self_plan = FMT != UT_FMT_F32 && !c.x_digits && need_plan && c.extra_slot < 0 &&
+                           !c.shared && c.H <= KC && c.H % FmtTraits<FMT>::kStepCols == 0 &&
+                           M == 1 && c.k <= 64;
     if constexpr (FMT == UT_FMT_F32) {
         xs.xf = c.x;
         xs.ldx = c.H;
+    } else if (self_plan) {
+        xs.xf = c.x;
+        xs.ldx = c.H;
+        xs.self_max = 1;
     } else {
         XDigits xd = xdigits_view(base + L.xd, M, c.H, L.xflags);
         if (c.x_digits) {
@@ -854,6 +993,7 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
         xs.KW = (c.H + FmtTraits<FMT>::kColsPerWord - 1) / FmtTraits<FMT>::kColsPerWord;
         xexps = xd.exps;
     }
+    // the digitiser (or, with self_plan, the gate/up launch) writes the plan
     const bool planned = FMT != UT_FMT_F32 && !c.x_digits && need_plan && c.extra_slot < 0;
     if (need_plan && !planned) {
         tok = timing_begin(ctx, "moe_plan");
@@ -885,6 +1025,15 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
         a.h = h;
         a.hmax_parts = hmax;
         a.ntiles = (int)L.ntiles;
+        if (self_plan) {
+            a.plan_ids = c.ids;
+            a.plan_M = M;
+            a.plan_k = c.k;
+            a.E = c.E;
+            a.ptbl = (const void *const *)c.tbl.gate_w;
+            a.plan = plan;
+            a.err_flag = c.err_flag;
+        }
         if (c.shared) {
             const MoeCall &sc = *c.shared;
             gb.tbl = sc.tbl;
