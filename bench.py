@@ -7,7 +7,10 @@ N(0,1) router logits, M=1 token row) -- in achieved algorithmic HBM GB/s.
 A step = route (sigmoid, group limit, top-k) + gate/up + SiLU*mul + down +
 choice-order combine, with fresh routing logits every step over the 5.6 GB
 expert pool (so the 256 MB MALL does not hold the working set).  Inputs are
-resident in HBM before the timed region.
+resident in HBM before the timed region.  The K timed steps are queued
+behind a GPU-side wait (outside the timed region) so the events bracket the
+GPU work, not Python's launch rate; the host-paced figure (each step
+launched as the host reaches it) is reported beside it.
 
 Also reported: M=2/4 and int8 variants, the roofline of the dominant kernel
 (fused gate/up, timed with HIP events on the stream it runs on), the
@@ -59,6 +62,11 @@ def build_experts(U, ctx, torch, n, hidden, inter, fmt, seed):
     return tbl
 
 
+# GPU-side wait before a queued timed region: ~10 ms of shader clock, far
+# longer than enqueueing a few hundred launches
+QUEUE_WAIT_CYCLES = 25_000_000
+
+
 def expert_block_bench(U, ctx, torch, tbl, cfg, M, steps, warmup, fmt_bits, seed):
     """Time `steps` expert-block passes; returns dict with GB/s and kernel times."""
     from undertow_amd.configs import expert_bytes, gate_up_bytes
@@ -85,12 +93,31 @@ def expert_block_bench(U, ctx, torch, tbl, cfg, M, steps, warmup, fmt_bits, seed
         step(i)
     ctx.synchronize()
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ts = torch.cuda.Event(enable_timing=True)
+    # host-paced: each step launched as the host reaches it
     t0.record()
     for i in range(warmup, n):
         step(i)
     t1.record()
     ctx.synchronize()
+    host_paced_ms = t0.elapsed_time(t1) / steps
+    # queued: a GPU-side wait (outside the timed region) lets the host
+    # enqueue all `steps` launches first, so the events bracket the GPU work
+    # alone; the wait is checked to have outlasted the host's enqueueing
+    ts.record()
+    torch.cuda._sleep(QUEUE_WAIT_CYCLES)
+    t0.record()
+    h0 = time.perf_counter()
+    for i in range(warmup, n):
+        step(i)
+    enqueue_ms = (time.perf_counter() - h0) * 1e3
+    t1.record()
+    ctx.synchronize()
+    wait_ms = ts.elapsed_time(t0)
     ms = t0.elapsed_time(t1) / steps
+    if enqueue_ms >= wait_ms:  # the GPU caught up with the host: host-paced after all
+        log(f"queue wait {wait_ms:.2f} ms shorter than enqueueing {enqueue_ms:.2f} ms")
+        ms = max(ms, host_paced_ms)
     ids = ids_all[warmup:].cpu().numpy()
     uniq = [len(np.unique(ids[s])) for s in range(steps)]
     u_mean = float(np.mean(uniq))
@@ -110,6 +137,7 @@ def expert_block_bench(U, ctx, torch, tbl, cfg, M, steps, warmup, fmt_bits, seed
     dn_bytes = u_mean * (H * ((I * fmt_bits + 7) // 8) + H * 4) + u_mean * M * I * 4
     return {
         "M": M, "unique_experts_mean": u_mean, "ms_per_step": ms,
+        "host_paced_ms_per_step": host_paced_ms,
         "bytes_per_step": bytes_step, "gbs": bytes_step / (ms * 1e-3) / 1e9,
         "gate_up_us": gms / max(gl, 1) * 1e3, "gate_up_bytes": gu_bytes,
         "gate_up_gbs": gu_bytes / (gms / max(gl, 1) * 1e-3) / 1e9,
@@ -370,6 +398,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(head["ms_per_step"], 5),
+        "host_paced_ms_per_step": round(head["host_paced_ms_per_step"], 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -479,9 +479,9 @@ __device__ __forceinline__ bool gemv_one_chunk(int64_t k_begin, int64_t kend) {
 
 //
 // prep: see gemv_stage_once (single-chunk path with f32 activations only;
-// the caller must not rely on it elsewhere).  mid: runs on the single-chunk
-// path after the activation loads are issued and before the first weight
-// loads, which read rows[] only then (so mid may still fill rows in).
+// the caller must not rely on it elsewhere).  mid: runs before the first
+// weight loads, which read rows[] only then (so mid may still fill rows
+// in); on the single-chunk path after the activation loads are issued.
 template <int FMT, int M, int R = kGemvRows, int DEPTH = gemv_depth<M>(), typename Prep = NoPrep,
           typename Mid = NoMid>
 __device__ __forceinline__ void gemv_core(const uint8_t *const rows[R], int64_t K, const XSrc &x,
@@ -534,6 +534,7 @@ __device__ __forceinline__ void gemv_core(const uint8_t *const rows[R], int64_t 
         A.finish(res);
         return;
     }
+    mid();
 #pragma unroll
     for (int u = 0; u < DEPTH; u++) loadk(wq[u], lane_col + u * STEP);
     int64_t kc = k_begin, chunk_end = k_begin;

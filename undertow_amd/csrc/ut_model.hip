@@ -485,10 +485,20 @@ int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
         }
         const int64_t slots = moe_slots(M, k, E, -1);
         ScratchLayout lay = moe_layout(M, k, slots, H, c.moe_intermediate_size, L.expert_fmt);
-        UT_TRY(launch_route_plan(m->ctx, s->ws.rlogits, &gparts, L.bias, M, E, k, (int)c.n_group,
-                                 (int)c.topk_group, c.norm_topk_prob, c.routed_scaling_factor,
-                                 s->ws.rids, s->ws.rw, (const void *const *)L.experts.gate_w,
-                                 moe_plan_view(s->ws.moe, lay), s->ws.err));
+        // with the logits whole and few choices the expert launch builds the
+        // slot plan itself (route alone here); else route + plan in one launch
+        const bool gate_plans = gparts.ks <= 1 && (int64_t)M * k <= 64 &&
+                                L.expert_fmt != UT_FMT_F32;
+        if (gate_plans)
+            UT_TRY(launch_route(m->ctx, s->ws.rlogits, L.bias, M, E, k, (int)c.n_group,
+                                (int)c.topk_group, c.norm_topk_prob, c.routed_scaling_factor,
+                                s->ws.rids, s->ws.rw));
+        else
+            UT_TRY(launch_route_plan(m->ctx, s->ws.rlogits, &gparts, L.bias, M, E, k,
+                                     (int)c.n_group, (int)c.topk_group, c.norm_topk_prob,
+                                     c.routed_scaling_factor, s->ws.rids, s->ws.rw,
+                                     (const void *const *)L.experts.gate_w,
+                                     moe_plan_view(s->ws.moe, lay), s->ws.err));
         MoeCall mc;
         mc.fmt = L.expert_fmt;
         mc.tbl = L.experts;
@@ -506,7 +516,7 @@ int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
         mc.ldo = H;
         mc.accumulate = accumulate;
         mc.err_flag = s->ws.err;
-        mc.plan_ready = true;
+        mc.plan_ready = !gate_plans;
         MoeCall sc;
         MoePlan sp_plan = m->mlp_plan;
         if (shared) {

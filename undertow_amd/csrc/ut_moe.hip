@@ -473,10 +473,9 @@ struct GateUpArgs {
     float *h;                 // [slots][M][I]
     uint32_t *hmax_parts;     // [slots][M][ntiles] float bits
     int ntiles;
-    // optional (plan_ids set; one row, k <= 64): every wave resolves its
-    // slot from the expert ids itself and workgroup (0, 0) writes the plan
-    // for the later launches, so no plan launch runs first; x is then f32
-    // with self_max
+    // optional (plan_ids set; M * k <= 64): every wave resolves its slot
+    // from the expert ids itself and workgroup (0, 0) writes the plan for
+    // the later launches, so no plan launch runs first
     const int32_t *plan_ids = nullptr;
     int plan_M = 0, plan_k = 0;
     int64_t E = 0;
@@ -553,26 +552,32 @@ __device__ __forceinline__ void gate_up_body(const GateUpArgs &a, int u, int til
     int cnt = 0;
     if (tid < 4) wg_max[tid] = 0;  // published by the core's barriers
     CoreOut<FMT, M, 2> res;
-    // x's exponents: given, or (self_max) found while x is staged
+    // x's exponents: given, or (self_max) found while x is staged (prep)
     int32_t exl[M];
+    if constexpr (FMT != UT_FMT_F32)
+        if (!a.x.self_max)
+#pragma unroll
+            for (int m = 0; m < M; m++) exl[m] = a.exps[m];
     auto prep = [&](int32_t (&shl)[4]) {
 #pragma unroll
         for (int m = 0; m < M; m++) exl[m] = shl[m] == INT32_MIN ? INT32_MIN : -shl[m];
     };
     if (a.plan_ids) {
-        // one activation row: this wave resolves the slot from the ids
-        // (loaded ahead of x) while x's loads are in flight; a slot past the
-        // count streams x itself in place of weights (valid memory of at
-        // least a row's bytes) and stores nothing
-        if (!gemv_one_chunk<FMT, M>(0, a.H)) return;  // the host's condition for plan_ids
-        const int id = lane < a.plan_k ? a.plan_ids[lane] : -1;
+        // this wave resolves the slot from the ids (loaded ahead of x) while
+        // x's loads are in flight; a slot past the count streams x itself in
+        // place of weights (valid memory of at least a row's bytes: f32 x,
+        // or its digit planes) and stores nothing
+        if (tile >= a.ntiles) return;
+        const int n = a.plan_M * a.plan_k;
+        const int id = lane < n ? a.plan_ids[lane] : -1;
+        const uint8_t *dummy = a.x.xf ? (const uint8_t *)a.x.xf : (const uint8_t *)a.x.dig;
         auto mid = [&]() {
             const void *p6[6];
-            cnt = plan_slot_wave(id, a.plan_k, a.E, a.ptbl, u, u == 0 && tile == 0 && wave == 0,
-                                 a.plan, a.err_flag, p6);
+            cnt = plan_slot_wave(id, n, a.E, a.ptbl, u, u == 0 && tile == 0 && wave == 0, a.plan,
+                                 a.err_flag, p6);
             const bool live = u < cnt;
-            rows[0] = live ? (const uint8_t *)p6[kSpGate] + oc * a.row_bytes : (const uint8_t *)a.x.xf;
-            rows[1] = live ? (const uint8_t *)p6[kSpUp] + oc * a.row_bytes : (const uint8_t *)a.x.xf;
+            rows[0] = live ? (const uint8_t *)p6[kSpGate] + oc * a.row_bytes : dummy;
+            rows[1] = live ? (const uint8_t *)p6[kSpUp] + oc * a.row_bytes : dummy;
             gsc = live ? (const float *)p6[kSpGateS] : nullptr;
             usc = live ? (const float *)p6[kSpUpS] : nullptr;
         };
@@ -588,9 +593,6 @@ __device__ __forceinline__ void gate_up_body(const GateUpArgs &a, int u, int til
         if (u >= cnt || tile >= a.ntiles) return;
         rows[0] = gw + oc * a.row_bytes;
         rows[1] = uw + oc * a.row_bytes;
-        if constexpr (FMT != UT_FMT_F32)
-#pragma unroll
-            for (int m = 0; m < M; m++) exl[m] = a.exps[m];
         gemv_core<FMT, M, 2, gemv_depth<M>()>(rows, a.H, a.x, lds, res, 0, -1, prep);
     }
 #pragma unroll
@@ -828,6 +830,93 @@ __global__ void k_moe_combine(const int32_t *__restrict__ choice_slot,
     *po = accumulate ? __fadd_rn(*po, acc) : acc;
 }
 
+// NC consecutive columns c0.. of row s of k_moe_combine's result, with
+// every load issued before the first sum (1 <= k <= 8: the choices' rows
+// load in one round trip; an invalid choice reads slot 0's row and is
+// skipped), and the sums in k_moe_combine's order.  16-byte aligned rows.
+template <int NC>
+__device__ __forceinline__ void combine_cols(const int32_t *__restrict__ choice_slot,
+                                             const float *__restrict__ weights,
+                                             const float *__restrict__ d, int M, int k, int64_t H,
+                                             const int32_t *__restrict__ count, int extra,
+                                             const float *__restrict__ dshared,
+                                             const float *__restrict__ init, const float *prev,
+                                             int s, int64_t c0, float (&acc)[NC]) {
+    constexpr int KF = 8;
+    auto ldv = [](const float *p, float (&r)[NC]) {
+#pragma unroll
+        for (int q = 0; q < NC / 4; q++) {
+            const float4 v = *(const float4 *)(p + 4 * q);
+            r[4 * q] = v.x; r[4 * q + 1] = v.y; r[4 * q + 2] = v.z; r[4 * q + 3] = v.w;
+        }
+    };
+    const bool fast = k >= 1 && k <= KF;
+    int slot[KF];
+    float wc[KF], dv[KF][NC], ex[NC], sh[NC], pv[NC];
+    if (fast) {
+        // straight-line loads (choices past k repeat the last one, unused)
+#pragma unroll
+        for (int c = 0; c < KF; c++) {
+            const int cc = c < k ? c : k - 1;
+            slot[c] = choice_slot[s * k + cc];
+            wc[c] = weights[s * k + cc];
+        }
+#pragma unroll
+        for (int c = 0; c < KF; c++)
+            ldv(d + ((int64_t)(slot[c] > 0 ? slot[c] : 0) * M + s) * H + c0, dv[c]);
+    }
+    if (init) ldv(init, acc);
+    else
+#pragma unroll
+        for (int j = 0; j < NC; j++) acc[j] = 0.0f;
+    if (extra) ldv(d + ((int64_t)(*count - 1) * M + s) * H + c0, ex);
+    if (dshared) ldv(dshared + (int64_t)s * H + c0, sh);
+    if (prev) ldv(prev, pv);
+    if (fast) {
+#pragma unroll
+        for (int c = 0; c < KF; c++)
+            if (c < k && slot[c] >= 0)
+#pragma unroll
+                for (int j = 0; j < NC; j++) acc[j] = __fadd_rn(acc[j], __fmul_rn(wc[c], dv[c][j]));
+    } else {
+        for (int c = 0; c < k; c++) {
+            const int sl = choice_slot[s * k + c];
+            if (sl < 0) continue;
+            float t[NC];
+            ldv(d + ((int64_t)sl * M + s) * H + c0, t);
+            const float w = weights[s * k + c];
+#pragma unroll
+            for (int j = 0; j < NC; j++) acc[j] = __fadd_rn(acc[j], __fmul_rn(w, t[j]));
+        }
+    }
+    if (extra)
+#pragma unroll
+        for (int j = 0; j < NC; j++) acc[j] = __fadd_rn(acc[j], ex[j]);
+    if (dshared)
+#pragma unroll
+        for (int j = 0; j < NC; j++) acc[j] = __fadd_rn(acc[j], sh[j]);
+    if (prev)
+#pragma unroll
+        for (int j = 0; j < NC; j++) acc[j] = __fadd_rn(pv[j], acc[j]);
+}
+
+// k_moe_combine with four columns per thread (H % 4 == 0, 16-byte aligned
+// rows).
+__global__ __launch_bounds__(256) void k_moe_combine4(
+    const int32_t *__restrict__ choice_slot, const float *__restrict__ weights,
+    const float *__restrict__ d, int M, int k, int64_t H, const int32_t *__restrict__ count,
+    int extra, const float *__restrict__ dshared, const float *__restrict__ init,
+    float *__restrict__ out, int64_t ldo, int accumulate) {
+    const int s = blockIdx.y;
+    const int64_t c0 = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+    if (c0 >= H) return;
+    float *po = out + s * ldo + c0;
+    float acc[4];
+    combine_cols<4>(choice_slot, weights, d, M, k, H, count, extra, dshared,
+                    init ? init + s * ldo + c0 : nullptr, accumulate ? po : nullptr, s, c0, acc);
+    *(float4 *)po = make_float4(acc[0], acc[1], acc[2], acc[3]);
+}
+
 // The same combine for one row per workgroup (thread t: columns 8t..8t+7,
 // each computed exactly as k_moe_combine does), then the finished row
 // rms-normalised and digitised by the row digitiser's body (nd: K = H).
@@ -841,44 +930,16 @@ __global__ __launch_bounds__(1024) void k_moe_combine_norm(
     const int s = blockIdx.x, tid = threadIdx.x;
     const int64_t c0 = 8 * (int64_t)tid;
     float v[1][8], wv[1][8];
-    auto ld8 = [](const float *p, float (&r)[8]) {
-        const float4 a = *(const float4 *)p, b = *(const float4 *)(p + 4);
-        r[0] = a.x; r[1] = a.y; r[2] = a.z; r[3] = a.w;
-        r[4] = b.x; r[5] = b.y; r[6] = b.z; r[7] = b.w;
-    };
     if (c0 < H) {
-        float acc[8], t[8];
-        if (init) ld8(init + s * ldo + c0, acc);
-        else
-#pragma unroll
-            for (int j = 0; j < 8; j++) acc[j] = 0.0f;
-        for (int c = 0; c < k; c++) {
-            const int slot = choice_slot[s * k + c];
-            if (slot < 0) continue;
-            const float wc = weights[s * k + c];
-            ld8(d + ((int64_t)slot * M + s) * H + c0, t);
-#pragma unroll
-            for (int j = 0; j < 8; j++) acc[j] = __fadd_rn(acc[j], __fmul_rn(wc, t[j]));
-        }
-        if (extra) {
-            ld8(d + ((int64_t)(*count - 1) * M + s) * H + c0, t);
-#pragma unroll
-            for (int j = 0; j < 8; j++) acc[j] = __fadd_rn(acc[j], t[j]);
-        }
-        if (dshared) {
-            ld8(dshared + (int64_t)s * H + c0, t);
-#pragma unroll
-            for (int j = 0; j < 8; j++) acc[j] = __fadd_rn(acc[j], t[j]);
-        }
         float *po = out + s * ldo + c0;
-        if (accumulate) {
-            ld8(po, t);
-#pragma unroll
-            for (int j = 0; j < 8; j++) acc[j] = __fadd_rn(t[j], acc[j]);
-        }
+        const float4 w0 = *(const float4 *)(nd.norm_w + c0), w1 = *(const float4 *)(nd.norm_w + c0 + 4);
+        float acc[8];
+        combine_cols<8>(choice_slot, weights, d, M, k, H, count, extra, dshared,
+                        init ? init + s * ldo + c0 : nullptr, accumulate ? po : nullptr, s, c0, acc);
         *(float4 *)po = make_float4(acc[0], acc[1], acc[2], acc[3]);
         *(float4 *)(po + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
-        ld8(nd.norm_w + c0, wv[0]);
+        wv[0][0] = w0.x; wv[0][1] = w0.y; wv[0][2] = w0.z; wv[0][3] = w0.w;
+        wv[0][4] = w1.x; wv[0][5] = w1.y; wv[0][6] = w1.z; wv[0][7] = w1.w;
 #pragma unroll
         for (int j = 0; j < 8; j++) v[0][j] = acc[j];
     } else {
@@ -966,12 +1027,14 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
     int tok = -1;
     XSrc xs{};
     const int32_t *xexps = nullptr;
-    // expert ids given and x not digitised: the gate/up workgroups resolve
-    // the plan and digitise x themselves (x staged whole, as f32)
+    // expert ids given: the gate/up workgroups resolve the plan themselves
+    // (gate_plan); with x not digitised, one row and x staged whole, they
+    // digitise x too (self_plan, x as f32)
     constexpr int64_t KC = gemv_chunk_cols<FMT, M>();
-    const bool self_plan = FMT != UT_FMT_F32 && !c.x_digits && need_plan && c.extra_slot < 0 &&
-                           !c.shared && c.H <= KC && c.H % FmtTraits<FMT>::kStepCols == 0 &&
-                           M == 1 && c.k <= 64;
+    const bool gate_plan = FMT != UT_FMT_F32 && need_plan && c.extra_slot < 0 &&
+                           (int64_t)M * c.k <= 64;
+    const bool self_plan = gate_plan && !c.x_digits && !c.shared && c.H <= KC &&
+                           c.H % FmtTraits<FMT>::kStepCols == 0 && M == 1;
     if constexpr (FMT == UT_FMT_F32) {
         xs.xf = c.x;
         xs.ldx = c.H;
@@ -993,8 +1056,9 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
         xs.KW = (c.H + FmtTraits<FMT>::kColsPerWord - 1) / FmtTraits<FMT>::kColsPerWord;
         xexps = xd.exps;
     }
-    // the digitiser (or, with self_plan, the gate/up launch) writes the plan
-    const bool planned = FMT != UT_FMT_F32 && !c.x_digits && need_plan && c.extra_slot < 0;
+    // the gate/up launch (gate_plan) or the digitiser writes the plan
+    const bool planned =
+        gate_plan || (FMT != UT_FMT_F32 && !c.x_digits && need_plan && c.extra_slot < 0);
     if (need_plan && !planned) {
         tok = timing_begin(ctx, "moe_plan");
         hipLaunchKernelGGL(k_moe_plan, dim3(1), dim3(256), 0, ctx->stream, c.ids, M, c.k, (int)c.E,
@@ -1025,7 +1089,7 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
         a.h = h;
         a.hmax_parts = hmax;
         a.ntiles = (int)L.ntiles;
-        if (self_plan) {
+        if (gate_plan && (self_plan || c.x_digits)) {
             a.plan_ids = c.ids;
             a.plan_M = M;
             a.plan_k = c.k;
@@ -1140,9 +1204,17 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
         return launch_check(ctx, "k_moe_combine_norm");
     }
     tok = timing_begin(ctx, "moe_combine");
-    hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((c.H + 255) / 256), (unsigned)M), dim3(256),
-                       0, ctx->stream, plan.choice_slot, c.weights, d, M, c.k, c.H, plan.count,
-                       c.extra_slot >= 0 ? 1 : 0, dshared, c.init, c.out, c.ldo, c.accumulate);
+    if (c.H % 4 == 0 && c.ldo % 4 == 0 && ((uintptr_t)c.out & 15) == 0 &&
+        (!c.init || ((uintptr_t)c.init & 15) == 0))
+        hipLaunchKernelGGL(k_moe_combine4, dim3((unsigned)((c.H / 4 + 255) / 256), (unsigned)M),
+                           dim3(256), 0, ctx->stream, plan.choice_slot, c.weights, d, M, c.k, c.H,
+                           plan.count, c.extra_slot >= 0 ? 1 : 0, dshared, c.init, c.out, c.ldo,
+                           c.accumulate);
+    else
+        hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((c.H + 255) / 256), (unsigned)M),
+                           dim3(256), 0, ctx->stream, plan.choice_slot, c.weights, d, M, c.k, c.H,
+                           plan.count, c.extra_slot >= 0 ? 1 : 0, dshared, c.init, c.out, c.ldo,
+                           c.accumulate);
     timing_end(ctx, tok);
     return launch_check(ctx, "k_moe_combine");
 }
