@@ -122,8 +122,10 @@ def expert_block_bench(U, ctx, torch, tbl, cfg, M, steps, warmup, fmt_bits, seed
     uniq = [len(np.unique(ids[s])) for s in range(steps)]
     u_mean = float(np.mean(uniq))
     bytes_step = u_mean * expert_bytes(H, I, fmt_bits) + 2 * M * H * 4
-    # per-kernel durations (events around each launch) in a second pass
+    # per-kernel durations (events around each launch) in a second pass,
+    # queued behind a GPU-side wait like the timed region
     ctx.enable_timing(True)
+    torch.cuda._sleep(QUEUE_WAIT_CYCLES)
     for i in range(warmup, n):
         step(i)
     ctx.synchronize()
@@ -143,6 +145,7 @@ def expert_block_bench(U, ctx, torch, tbl, cfg, M, steps, warmup, fmt_bits, seed
         "gate_up_gbs": gu_bytes / (gms / max(gl, 1) * 1e-3) / 1e9,
         "down_us": dms / max(dl, 1) * 1e3, "down_gbs": dn_bytes / (dms / max(dl, 1) * 1e-3) / 1e9,
         "kernels_us_per_step": tms / steps * 1e3,
+        "launches_per_step": tl / steps,
     }
 
 
@@ -421,7 +424,13 @@ def main():
                                        "WRITE_SIZE x1.0 per dispatch, copy-scaled)"},
         "kernels": {"gate_up_us": round(gu_us, 3), "down_us": round(head["down_us"], 3),
                     "down_gbs": round(head["down_gbs"], 1),
-                    "all_kernels_us_per_step": round(head["kernels_us_per_step"], 3)},
+                    "all_kernels_us_per_step": round(head["kernels_us_per_step"], 3),
+                    "launches_per_step": head["launches_per_step"],
+                    # what the bracketing events add to each launch: the
+                    # bracketed durations' sum less the queued step time
+                    "event_overhead_us_per_launch": round(
+                        (head["kernels_us_per_step"] - head["ms_per_step"] * 1e3)
+                        / max(head["launches_per_step"], 1), 3)},
         "variants": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                      for k, v in variants.items()},
         "mla": mla,

@@ -272,3 +272,21 @@ def test_mla_attend_split_rejects_other_shapes(ctx):
     with pytest.raises(U.UtError) as ei:
         U.mla_attend_split(ctx, q, qr, kc, 4, 0.1)
     assert ei.value.code == U.runtime.UT_ERR_SHAPE
+
+
+
+def test_kernel_timing(ctx):
+    """Bench tooling: per-launch event timing."""
+    rng = np.random.default_rng(5)
+    tbl, _ = make_experts(ctx, rng, INT8, 4, 256, 32)
+    ids = dev(np.array([[0, 2]], np.int32))
+    w = dev(np.ones((1, 2), np.float32))
+    x = dev(rng.standard_normal((1, 256)).astype(np.float32))
+    ctx.enable_timing(True)
+    for _ in range(3):
+        tbl.moe_experts(ids, w, x)
+    ctx.synchronize()
+    n, ms = ctx.kernel_time("moe_gate_up")
+    nd, msd = ctx.kernel_time("moe_down")
+    ctx.enable_timing(False)
+    assert n == 3 and nd == 3 and ms > 0 and msd > 0
