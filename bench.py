@@ -62,9 +62,22 @@ def build_experts(U, ctx, torch, n, hidden, inter, fmt, seed):
     return tbl
 
 
-# GPU-side wait before a queued timed region: ~10 ms of shader clock, far
-# longer than enqueueing a few hundred launches
-QUEUE_WAIT_CYCLES = 25_000_000
+_CYCLES_PER_MS = None
+
+
+def gpu_wait(torch, ms: float) -> None:
+    """Hold the current stream for about `ms` (a spin kernel), so launches
+    queued behind it start back to back."""
+    global _CYCLES_PER_MS
+    if _CYCLES_PER_MS is None:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(1_000_000)  # warm
+        e0.record()
+        torch.cuda._sleep(4_000_000)
+        e1.record()
+        torch.cuda.synchronize()
+        _CYCLES_PER_MS = 4_000_000 / max(e0.elapsed_time(e1), 1e-3)
+    torch.cuda._sleep(int(ms * _CYCLES_PER_MS))
 
 
 def expert_block_bench(U, ctx, torch, tbl, cfg, M, steps, warmup, fmt_bits, seed):
@@ -96,16 +109,20 @@ def expert_block_bench(U, ctx, torch, tbl, cfg, M, steps, warmup, fmt_bits, seed
     ts = torch.cuda.Event(enable_timing=True)
     # host-paced: each step launched as the host reaches it
     t0.record()
+    h0 = time.perf_counter()
     for i in range(warmup, n):
         step(i)
+    host_ms = (time.perf_counter() - h0) * 1e3
     t1.record()
     ctx.synchronize()
     host_paced_ms = t0.elapsed_time(t1) / steps
-    # queued: a GPU-side wait (outside the timed region) lets the host
-    # enqueue all `steps` launches first, so the events bracket the GPU work
-    # alone; the wait is checked to have outlasted the host's enqueueing
+    # queued: a GPU-side wait (outside the timed region, three times the
+    # host's enqueueing time) lets the host enqueue all `steps` launches
+    # first, so the events bracket the GPU work alone; the wait is checked to
+    # have outlasted the enqueueing
+    wait_for = max(5.0, 3.0 * host_ms)
     ts.record()
-    torch.cuda._sleep(QUEUE_WAIT_CYCLES)
+    gpu_wait(torch, wait_for)
     t0.record()
     h0 = time.perf_counter()
     for i in range(warmup, n):
@@ -125,7 +142,7 @@ def expert_block_bench(U, ctx, torch, tbl, cfg, M, steps, warmup, fmt_bits, seed
     # per-kernel durations (events around each launch) in a second pass,
     # queued behind a GPU-side wait like the timed region
     ctx.enable_timing(True)
-    torch.cuda._sleep(QUEUE_WAIT_CYCLES)
+    gpu_wait(torch, wait_for * 3.0)  # events make enqueueing slower
     for i in range(warmup, n):
         step(i)
     ctx.synchronize()

@@ -432,9 +432,13 @@ __device__ __forceinline__ float *plain_out(const PlainArgs &a, int64_t m, int64
     return row < a.O1 ? a.out + m * a.ldo + row : a.out2 + m * a.ldo2 + (row - a.O1);
 }
 
-// 16*R output rows per workgroup (R = 4 rows per lane at M <= 2, else 2):
-// wave w, row group g, slot r -> row blockIdx.x*16R + w*4R + g*R + r.
-template <int M> constexpr int plain_rows() { return M <= 2 ? 4 : 2; }
+// 16*R output rows per workgroup (R = 2 rows per lane at M = 1 -- registers
+// for four workgroups per CU and every weight step of a short row in flight
+// -- 4 at M = 2 (activation reuse), else 2): wave w, row group g, slot r ->
+// row blockIdx.x*16R + w*4R + g*R + r.
+template <int M> constexpr int plain_rows() { return M == 2 ? 4 : 2; }
+template <int M> constexpr int plain_depth() { return M == 1 ? 4 : gemv_depth<M>(); }
+__host__ __device__ constexpr int plain_rows_rt(int M) { return 16 * (M == 2 ? 4 : 2); }
 
 template <int FMT, int M>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
@@ -447,28 +451,42 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
     for (int r = 0; r < R; r++) rows[r] = plain_row(a, row0 + r < a.O ? row0 + r : a.O - 1);
     XSrc xs = a.x;
     int32_t exl[M];
+    const int64_t kb = a.ks > 1 ? (int64_t)blockIdx.z * a.kslice : 0;
+    const int64_t ke = a.ks > 1 ? (kb + a.kslice < a.K ? kb + a.kslice : a.K) : a.K;
+    // x's row shifts from the producer's partial maxima (xmax): their loads
+    // go out first; on the one-chunk path the reduction runs inside the
+    // staging, after the first weight loads (prep)
+    __shared__ uint32_t redm[4 * M];
+    ut_u32x4 pv[M];
+    const bool late = FMT != UT_FMT_F32 && a.xmax && gemv_one_chunk<FMT, M>(kb, ke);
+    auto shifts = [&](int32_t (&shl)[4]) {
+        int32_t sh[M];
+        rowmax_reduce<M>(pv, sh, redm);
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            shl[m] = sh[m];
+            exl[m] = sh[m] == INT32_MIN ? INT32_MIN : -sh[m];
+        }
+        if (blockIdx.x == 0 && blockIdx.z == 0 && tid < M)
+            const_cast<int32_t *>(a.exps)[tid] = tid == 0 ? exl[0] : tid == 1 ? exl[M > 1 ? 1 : 0]
+                                                : tid == 2 ? exl[M > 2 ? 2 : 0] : exl[M > 3 ? 3 : 0];
+    };
     if constexpr (FMT != UT_FMT_F32) {
         if (a.xmax) {
-            __shared__ uint32_t redm[4 * M];
-            int32_t sh[M];
-            rowmax_shifts<M>(a.xmax, a.nxmax, sh, redm);
-#pragma unroll
-            for (int m = 0; m < M; m++) {
-                xs.sh[m] = sh[m];
-                exl[m] = sh[m] == INT32_MIN ? INT32_MIN : -sh[m];
-            }
-            if (blockIdx.x == 0 && blockIdx.z == 0 && tid < M)
-                const_cast<int32_t *>(a.exps)[tid] = tid == 0 ? exl[0] : tid == 1 ? exl[M > 1 ? 1 : 0]
-                                                    : tid == 2 ? exl[M > 2 ? 2 : 0] : exl[M > 3 ? 3 : 0];
+            rowmax_load<M>(a.xmax, a.nxmax, pv);
+            if (!late) shifts(xs.sh);
         } else {
 #pragma unroll
             for (int m = 0; m < M; m++) exl[m] = a.exps[m];
         }
     }
+    auto prep = [&](int32_t (&shl)[4]) {
+        if constexpr (FMT != UT_FMT_F32)
+            if (late) shifts(shl);
+    };
     CoreOut<FMT, M, R> res;
     if (a.ks > 1) {
-        const int64_t kb = (int64_t)blockIdx.z * a.kslice;
-        gemv_core<FMT, M, R, gemv_depth<M>()>(rows, a.K, xs, lds, res, kb, kb + a.kslice);
+        gemv_core<FMT, M, R, plain_depth<M>()>(rows, a.K, xs, lds, res, kb, ke, prep);
 #pragma unroll
         for (int r = 0; r < R; r++)
 #pragma unroll
@@ -480,7 +498,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
             }
         return;
     }
-    gemv_core<FMT, M, R, gemv_depth<M>()>(rows, a.K, xs, lds, res);
+    gemv_core<FMT, M, R, plain_depth<M>()>(rows, a.K, xs, lds, res, 0, -1, prep);
 #pragma unroll
     for (int r = 0; r < R; r++)
 #pragma unroll
@@ -597,13 +615,28 @@ static bool fast_ok(const ut_qtensor *w) {
 // weight's shape only, so an f32 row's summation order is the same for
 // every M.
 constexpr int64_t kSplitTargetWGs = 1024;
+constexpr int64_t kSplitMinTiles = 256;  // integer formats: at least this many tiles -> no split
 
-static void splitk_plan(int32_t fmt, int64_t O, int64_t K, int *ks_out, int64_t *kslice_out) {
+// resident: workgroups of the launch's kernel the chip holds at once.
+static void splitk_plan(int32_t fmt, int64_t O, int64_t K, int rows_per_wg, int64_t resident,
+                        int *ks_out, int64_t *kslice_out) {
     const int64_t step = fmt == UT_FMT_INT4 ? FmtTraits<UT_FMT_INT4>::kStepCols
                          : fmt == UT_FMT_INT8 ? FmtTraits<UT_FMT_INT8>::kStepCols
                                               : FmtTraits<UT_FMT_F32>::kStepCols;
-    const int64_t tiles64 = (O + 63) / 64;
-    int64_t ks = tiles64 >= 256 ? 1 : (kSplitTargetWGs + tiles64 - 1) / tiles64;
+    int64_t ks;
+    if (fmt == UT_FMT_F32) {
+        // f32 partials are summed in z order, so their split must not depend
+        // on the row count: 64-row tiles, about kSplitTargetWGs workgroups
+        const int64_t tiles64 = (O + 63) / 64;
+        ks = tiles64 >= 256 ? 1 : (kSplitTargetWGs + tiles64 - 1) / tiles64;
+    } else {
+        // integer partials are exact, so the launch's own tiles decide: as
+        // many splits as fit the chip in one wave of workgroups (a second,
+        // partial wave would only add a tail)
+        const int64_t tiles = (O + rows_per_wg - 1) / rows_per_wg;
+        ks = tiles >= kSplitMinTiles ? 1 : resident / tiles;
+        if (ks < 1) ks = 1;
+    }
     const int64_t max_ks = K / (2 * step);
     if (ks > max_ks) ks = max_ks;
     // partials of the widest case (M = 4) must fit
@@ -617,6 +650,31 @@ static void splitk_plan(int32_t fmt, int64_t O, int64_t K, int *ks_out, int64_t 
     kslice = (kslice + step - 1) / step * step;
     *ks_out = (int)((K + kslice - 1) / kslice);
     *kslice_out = kslice;
+}
+
+// Workgroups of k_gemv<FMT, M> resident on the whole chip (occupancy query,
+// once per instantiation).
+template <int FMT, int M> static int64_t gemv_resident_m(ut_ctx *ctx) {
+    static int per_cu = 0;
+    if (per_cu == 0) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, (const void *)k_gemv<FMT, M>,
+                                                         kGemvThreads, 0) != hipSuccess ||
+            n < 1) {
+            (void)hipGetLastError();
+            n = 2;
+        }
+        per_cu = n;
+    }
+    return (int64_t)per_cu * ctx->multiprocessors;
+}
+template <int FMT> static int64_t gemv_resident(ut_ctx *ctx, int mrows) {
+    switch (mrows) {
+    case 1: return gemv_resident_m<FMT, 1>(ctx);
+    case 2: return gemv_resident_m<FMT, 2>(ctx);
+    case 3: return gemv_resident_m<FMT, 3>(ctx);
+    default: return gemv_resident_m<FMT, 4>(ctx);
+    }
 }
 
 template <int FMT>
@@ -663,10 +721,11 @@ static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrow
     }
     a.xmax = FMT != UT_FMT_F32 && ga.xmax ? ga.xmax + m0 * ga.nxmax : nullptr;
     a.nxmax = ga.nxmax;
-    splitk_plan(FMT, a.O, w->in_dim, &a.ks, &a.kslice);
+    const int rows_per_wg = plain_rows_rt(mrows);
+    splitk_plan(FMT, a.O, w->in_dim, rows_per_wg, gemv_resident<FMT>(ctx, mrows), &a.ks,
+                &a.kslice);
     a.part = nullptr;
     if (a.ks > 1) UT_TRY(splitk_buffer(ctx, &a.part));
-    const int rows_per_wg = 16 * (mrows <= 2 ? 4 : 2);
     dim3 grid((unsigned)((a.O + rows_per_wg - 1) / rows_per_wg), 1, (unsigned)a.ks);
     const char *name = FMT == UT_FMT_INT4 ? "gemv_int4" : FMT == UT_FMT_INT8 ? "gemv_int8" : "gemv_f32";
     int tok = timing_begin(ctx, name);

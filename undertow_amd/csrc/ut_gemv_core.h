@@ -64,12 +64,15 @@ template <int M> __host__ __device__ constexpr int gemv_depth() {
 #endif
 }
 
-// Columns of one staged chunk: as many as fit kLdsWords for M rows.
-template <int FMT, int M>
+// Columns of one staged chunk: as many as fit kLdsWords for M rows, or at
+// most CAP (> 0) when the caller's K is known to be short (fewer staging
+// registers per thread).
+template <int FMT, int M, int CAP = 0>
 __host__ __device__ constexpr int gemv_chunk_cols() {
     using T = FmtTraits<FMT>;
     // words per column per row = planes / cols_per_word
     int cols = kLdsWords * T::kColsPerWord / (M * T::kPlanes);
+    if (CAP > 0 && CAP < cols) cols = CAP;
     return cols / T::kStepCols * T::kStepCols;
 }
 
@@ -170,10 +173,9 @@ template <int FMT, int M, int R = kGemvRows> struct CoreOut {
 //   GemvAcc       per-lane accumulators: compute() takes one step of R
 //                 weight rows (16 bytes each) against the staged chunk,
 //                 finish() reduces across the 16 sub-lanes of the row group.
-template <int FMT, int M>
+template <int FMT, int M, int KC = gemv_chunk_cols<FMT, M>()>
 __device__ __forceinline__ void gemv_stage(const XSrc &x, uint32_t *lds, int64_t kc, int kcn) {
     using T = FmtTraits<FMT>;
-    constexpr int KC = gemv_chunk_cols<FMT, M>();
     constexpr int PL = T::kPlanes;
     constexpr int LW = KC / T::kColsPerWord;  // LDS words per plane row
     const int tid = threadIdx.x;
@@ -210,9 +212,12 @@ __device__ __forceinline__ void gemv_stage(const XSrc &x, uint32_t *lds, int64_t
                 v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
             }
             uint32_t w[PL];
-            // select, not index: a runtime index into x.sh would move the
-            // whole argument struct to scratch memory
-            const int32_t shm = m == 0 ? x.sh[0] : m == 1 ? x.sh[1] : m == 2 ? x.sh[2] : x.sh[3];
+            // select among opaque copies, not index: a runtime index into
+            // x.sh (which the compiler rebuilds from a plain select chain)
+            // would move the argument struct to scratch memory
+            int32_t s0 = x.sh[0], s1 = x.sh[1], s2 = x.sh[2], s3 = x.sh[3];
+            asm volatile("" : "+v"(s0), "+v"(s1), "+v"(s2), "+v"(s3));
+            const int32_t shm = m == 0 ? s0 : m == 1 ? s1 : m == 2 ? s2 : s3;
             digit_words<FMT>(v, CPW, shm, w);
 #pragma unroll
             for (int p = 0; p < PL; p++) lds[(m * PL + p) * LW + g] = w[p];
@@ -238,11 +243,10 @@ struct NoMid {
     __device__ void operator()() const {}
 };
 
-template <int FMT, int M, typename Issue, typename Prep = NoPrep>
+template <int FMT, int M, int KC, typename Issue, typename Prep = NoPrep>
 __device__ __forceinline__ void gemv_stage_once(const XSrc &x, uint32_t *lds, int64_t kc, int kcn,
                                                 Issue &&issue, Prep &&prep = Prep{}) {
     using T = FmtTraits<FMT>;
-    constexpr int KC = gemv_chunk_cols<FMT, M>();
     constexpr int PL = T::kPlanes;
     constexpr int CPW = T::kColsPerWord;
     constexpr int LW = KC / CPW;
@@ -356,9 +360,9 @@ __device__ __forceinline__ void gemv_stage_once(const XSrc &x, uint32_t *lds, in
     __syncthreads();
 }
 
-template <int FMT, int M, int R> struct GemvAcc {
+template <int FMT, int M, int R, int KC_ = gemv_chunk_cols<FMT, M>()> struct GemvAcc {
     using T = FmtTraits<FMT>;
-    static constexpr int KC = gemv_chunk_cols<FMT, M>();
+    static constexpr int KC = KC_;
     static constexpr int PL = T::kPlanes;
     static constexpr int LW = KC / T::kColsPerWord;
     int32_t acc[R][M][PL];
@@ -470,9 +474,8 @@ __device__ __forceinline__ void gemv_load(const uint8_t *const rows[R], int64_t 
 // staging branch inside the loop makes it drain every load first).
 // Whether gemv_core stages the columns [k_begin, kend) once (the
 // straight-line path, the only one that calls prep).
-template <int FMT, int M>
+template <int FMT, int M, int KC = gemv_chunk_cols<FMT, M>()>
 __device__ __forceinline__ bool gemv_one_chunk(int64_t k_begin, int64_t kend) {
-    constexpr int KC = gemv_chunk_cols<FMT, M>();
     constexpr int STEP = FmtTraits<FMT>::kStepCols;
     return kend > k_begin && kend - k_begin <= KC && (kend - k_begin) % STEP == 0;
 }
@@ -482,18 +485,18 @@ __device__ __forceinline__ bool gemv_one_chunk(int64_t k_begin, int64_t kend) {
 // the caller must not rely on it elsewhere).  mid: runs before the first
 // weight loads, which read rows[] only then (so mid may still fill rows
 // in); on the single-chunk path after the activation loads are issued.
-template <int FMT, int M, int R = kGemvRows, int DEPTH = gemv_depth<M>(), typename Prep = NoPrep,
-          typename Mid = NoMid>
+// KC: the staged chunk's columns (gemv_chunk_cols, possibly capped).
+template <int FMT, int M, int R = kGemvRows, int DEPTH = gemv_depth<M>(),
+          int KC = gemv_chunk_cols<FMT, M>(), typename Prep = NoPrep, typename Mid = NoMid>
 __device__ __forceinline__ void gemv_core(const uint8_t *const rows[R], int64_t K, const XSrc &x,
                                           uint32_t *lds, CoreOut<FMT, M, R> &res,
                                           int64_t k_begin = 0, int64_t k_end = -1,
                                           Prep &&prep = Prep{}, Mid &&mid = Mid{}) {
     using T = FmtTraits<FMT>;
-    constexpr int KC = gemv_chunk_cols<FMT, M>();
     constexpr int STEP = T::kStepCols;    // columns per step (16 sub-lanes)
     constexpr int LANE_COLS = STEP / 16;  // columns per lane per step
     const int s = threadIdx.x & 15;
-    GemvAcc<FMT, M, R> A;
+    GemvAcc<FMT, M, R, KC> A;
     A.zero();
     // columns [k_begin, k_end) (k_begin a multiple of STEP); K bounds loads.
     const int64_t kend = k_end < 0 || k_end > K ? K : k_end;
@@ -501,10 +504,10 @@ __device__ __forceinline__ void gemv_core(const uint8_t *const rows[R], int64_t 
     const int64_t lane_col = k_begin + (int64_t)s * LANE_COLS;
     uint4 wq[DEPTH][R];
     auto loadk = [&](uint4 (&w)[R], int64_t col) { if (col < kend) gemv_load<FMT, R>(rows, col, w); };
-    if (gemv_one_chunk<FMT, M>(k_begin, kend)) {
+    if (gemv_one_chunk<FMT, M, KC>(k_begin, kend)) {
         // unconditional (clamped) first loads: a skipped load on any path
         // into the loop would make the wait counts inside it conservative
-        gemv_stage_once<FMT, M>(x, lds, k_begin, (int)(kend - k_begin), [&]() {
+        gemv_stage_once<FMT, M, KC>(x, lds, k_begin, (int)(kend - k_begin), [&]() {
             mid();
 #pragma unroll
             for (int u = 0; u < DEPTH; u++)
@@ -547,7 +550,7 @@ __device__ __forceinline__ void gemv_core(const uint8_t *const rows[R], int64_t 
                     kc = k_begin + (t + u) * STEP;
                     const int kcn = (int)((kend - kc) < KC ? (kend - kc) : KC);
                     chunk_end = kc + kcn;
-                    gemv_stage<FMT, M>(x, lds, kc, kcn);
+                    gemv_stage<FMT, M, KC>(x, lds, kc, kcn);
                 }
                 if (cu < kend) A.compute(lds, wq[u], (int)(cu - kc));
                 loadk(wq[u], cu + DEPTH * STEP);

@@ -6,7 +6,7 @@
 namespace ut {
 
 constexpr int kGateUpRowsPerWG = 16;  // h rows per gate/up workgroup
-constexpr int kDownMaxSplit = 8;      // K splits of a one-slot MLP's down projection
+constexpr int kDownMaxSplit = 16;     // K splits of a one-slot MLP's down projection
 
 // Device arrays of per-expert pointers (indexed by expert id).
 struct ExpertPtrs {

@@ -664,17 +664,19 @@ __device__ __forceinline__ int32_t h_shift(const uint32_t *hmax_parts, int npart
     return rowmax_shift(hmax_parts, nparts, row, red4);
 }
 
-// Rows per lane: 4 at M <= 2 (more activation reuse), 2 above (registers).
-template <int M> constexpr int down_rows() { return M <= 2 ? 4 : 2; }
+// Rows per lane: 2 at M = 1 (registers for four workgroups per CU and
+// every weight step in flight), 4 at M = 2 (more activation reuse), 2 above
+// (registers).
+template <int M> constexpr int down_rows() { return M == 2 ? 4 : 2; }
 
-// Weight steps in flight in down.
-template <int M> constexpr int down_depth() {
-#ifdef UT_DOWN_DEPTH
-    return M == 1 ? UT_DOWN_DEPTH : gemv_depth<M>();
-#else
-    return gemv_depth<M>();
-#endif
-}
+// Staged columns of down's h: inter sizes up to 2048 stage once (fewer
+// staging registers, so more workgroups fit a CU); longer K is staged in
+// chunks, or split (one-slot MLPs, kslice <= this).
+template <int FMT, int M> constexpr int down_kc() { return gemv_chunk_cols<FMT, M, 2048>(); }
+
+// Weight steps in flight in down: at M = 1 four (all of a 2048-column
+// int4 row), else the core's default.
+template <int M> constexpr int down_depth() { return M == 1 ? 4 : gemv_depth<M>(); }
 
 template <int FMT, int M>
 __device__ __forceinline__ void down_body(const DownArgs &a, int u, int tile, uint32_t *lds) {
@@ -702,7 +704,8 @@ __device__ __forceinline__ void down_body(const DownArgs &a, int u, int tile, ui
     // inside the staging, after the first weight loads (prep)
     __shared__ uint32_t red[4 * M];
     ut_u32x4 pv[M];
-    const bool late = FMT != UT_FMT_F32 && gemv_one_chunk<FMT, M>(kb, ke);
+    constexpr int KC = down_kc<FMT, M>();
+    const bool late = FMT != UT_FMT_F32 && gemv_one_chunk<FMT, M, KC>(kb, ke);
     if constexpr (FMT != UT_FMT_F32) {
         rowmax_load<M>(a.hmax_parts + (int64_t)u * M * a.nparts, a.nparts, pv);
         if (!late) {
@@ -728,7 +731,7 @@ __device__ __forceinline__ void down_body(const DownArgs &a, int u, int tile, ui
     };
     CoreOut<FMT, M, R> res;
     if (a.ks > 1) {
-        gemv_core<FMT, M, R, down_depth<M>()>(rows, a.I, xs, lds, res, kb, ke, prep);
+        gemv_core<FMT, M, R, down_depth<M>(), KC>(rows, a.I, xs, lds, res, kb, ke, prep);
         const int64_t slots = gridDim.y;
 #pragma unroll
         for (int r = 0; r < R; r++)
@@ -741,7 +744,7 @@ __device__ __forceinline__ void down_body(const DownArgs &a, int u, int tile, ui
             }
         return;
     }
-    gemv_core<FMT, M, R, down_depth<M>()>(rows, a.I, xs, lds, res, 0, -1, prep);
+    gemv_core<FMT, M, R, down_depth<M>(), KC>(rows, a.I, xs, lds, res, 0, -1, prep);
 #pragma unroll
     for (int r = 0; r < R; r++)
 #pragma unroll
@@ -1144,6 +1147,10 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
             constexpr int64_t step = FmtTraits<FMT>::kStepCols;
             const int64_t tiles64 = (c.H + 63) / 64;
             int64_t ks = tiles64 >= 256 ? 1 : (512 + tiles64 - 1) / tiles64;
+            // integer formats (exact partial totals, so any split gives the
+            // same result): slices short enough to stage once
+            constexpr int64_t kcd = down_kc<FMT, M>();
+            if (FMT != UT_FMT_F32 && ks > 1 && (c.I + ks - 1) / ks > kcd) ks = (c.I + kcd - 1) / kcd;
             if (ks > kDownMaxSplit) ks = kDownMaxSplit;
             if (ks > c.I / (2 * step)) ks = c.I / (2 * step);
             if (ks > 1) {
