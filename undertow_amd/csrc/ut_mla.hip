@@ -178,9 +178,13 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 
+// Slice length of a row that sees n_ctx positions: about n_ctx/64 in whole
+// 16-position tiles, at least 32 and at most 256 (so at most 64 slices up
+// to 16384 positions, n_ctx/256 beyond).  A function of n_ctx alone, so a
+// row's result does not depend on which rows share the call; no power-of-two
+// steps, so neighbouring context lengths get similar slice counts.
 __host__ __device__ inline int64_t mla_mfma_slice(int64_t n_ctx) {
-    int64_t q = n_ctx / 64, s = 1;
-    while (s * 2 <= q) s *= 2;
+    const int64_t s = (n_ctx + 1023) / 1024 * 16;
     return s < 32 ? 32 : s > 256 ? 256 : s;
 }
 
@@ -422,71 +426,113 @@ __global__ __launch_bounds__(256) void k_mla_cache_split(const float *__restrict
 // all slices.  Every sum runs in a fixed order.
 constexpr int kMlaMaxSlices = 256;
 
-__global__ __launch_bounds__(256) void k_mla_combine_mfma(const float *__restrict__ part_m,
-                                                          const float *__restrict__ part_l,
-                                                          const float *__restrict__ part_o,
-                                                          int RH, int H, int L, int64_t pos_base,
-                                                          float *__restrict__ clat) {
-    __shared__ float sw[kMlaMaxSlices][33];
-    __shared__ float red[8][33];
+// A workgroup merges 32 columns x 8 latent dims.  Every load is issued at
+// the start (one memory round trip): thread (tx, tyz) holds the slice
+// statistics m, l of column tx for slices tyz + 32k; thread (c4, dy, part)
+// holds four adjacent columns of dim dy (16-byte loads) for one sixteenth
+// of the slices.  The sixteen part sums are added in part order through
+// LDS, so every output's sum has a fixed order.
+constexpr int kCombineParts = 16;
+constexpr int kCombineStat = kMlaMaxSlices / 32;                          // m, l per thread
+constexpr int kCombineSlices = (kMlaMaxSlices + kCombineParts - 1) / kCombineParts;  // per part
+
+__global__ __launch_bounds__(1024) void k_mla_combine_mfma(const float *__restrict__ part_m,
+                                                           const float *__restrict__ part_l,
+                                                           const float *__restrict__ part_o,
+                                                           int RH, int H, int L, int64_t pos_base,
+                                                           float *__restrict__ clat) {
+    __shared__ __attribute__((aligned(16))) float sw[kMlaMaxSlices][32];
+    __shared__ float red[32][33];
     __shared__ float sM[32], sInv[32];
-    const int tid = threadIdx.x, tx = tid & 31, ty = tid >> 5;
+    __shared__ __attribute__((aligned(16))) float sq[kCombineParts][8][32];
+    const int tid = threadIdx.x;
+    const int tx = tid & 31, tyz = tid >> 5;
     const int col = blockIdx.x * 32 + tx;
-    const int d = blockIdx.y * 8 + ty;
+    // the slice count is the same for the workgroup's 32 columns (one query
+    // row: 32 | H)
     const int64_t n_ctx = pos_base + col / H + 1;
     const int64_t slen = mla_mfma_slice(n_ctx);
     const int ns = (int)((n_ctx + slen - 1) / slen);
-    float mx = -INFINITY;
-    for (int j = ty; j < ns; j += 8) mx = fmaxf(mx, part_m[(int64_t)j * RH + col]);
-    red[ty][tx] = mx;
-    __syncthreads();
-    if (ty == 0) {
-        float M = red[0][tx];
+    // merge-pass loads: columns 4*c4.., dim dy, slices [j0, j1)
+    const int c4 = tid & 7, dy = (tid >> 3) & 7, part = tid >> 6;
+    const int q = (ns + kCombineParts - 1) / kCombineParts;
+    const int j0 = part * q, j1 = j0 + q < ns ? j0 + q : ns;
+    const float *po = part_o + (int64_t)(blockIdx.y * 8 + dy) * RH + blockIdx.x * 32 + 4 * c4;
+    const int64_t js = (int64_t)L * RH;
+    float4 v[kCombineSlices];
 #pragma unroll
-        for (int t = 1; t < 8; t++) M = fmaxf(M, red[t][tx]);
+    for (int u = 0; u < kCombineSlices; u++)
+        if (u < q) {
+            const int j = j0 + u < j1 ? j0 + u : (j1 > 0 ? j1 - 1 : 0);
+            v[u] = *(const float4 *)(po + (int64_t)j * js);
+        }
+    // statistics loads
+    float pm[kCombineStat], pl[kCombineStat];
+#pragma unroll
+    for (int k = 0; k < kCombineStat; k++) {
+        const int j = tyz + 32 * k;
+        if (j < ns) {
+            pm[k] = part_m[(int64_t)j * RH + col];
+            pl[k] = part_l[(int64_t)j * RH + col];
+        }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kCombineStat; k++)
+        if (tyz + 32 * k < ns) mx = fmaxf(mx, pm[k]);
+    red[tyz][tx] = mx;
+    __syncthreads();
+    if (tyz == 0) {
+        float M = red[0][tx];
+        for (int t = 1; t < 32; t++) M = fmaxf(M, red[t][tx]);
         sM[tx] = M;
     }
     __syncthreads();
     const float M = sM[tx];
     float ls = 0.0f;
-    for (int j = ty; j < ns; j += 8) {
-        const float e = __expf(part_m[(int64_t)j * RH + col] - M);
-        sw[j][tx] = e;
-        ls = __fadd_rn(ls, __fmul_rn(part_l[(int64_t)j * RH + col], e));
-    }
-    __syncthreads();
-    red[ty][tx] = ls;
-    __syncthreads();
-    if (ty == 0) {
-        float t = red[0][tx];
 #pragma unroll
-        for (int u = 1; u < 8; u++) t = __fadd_rn(t, red[u][tx]);
-        sInv[tx] = 1.0f / t;
+    for (int k = 0; k < kCombineStat; k++) {
+        const int j = tyz + 32 * k;
+        if (j < ns) {
+            const float e = __expf(pm[k] - M);
+            sw[j][tx] = e;
+            ls = __fadd_rn(ls, __fmul_rn(pl[k], e));
+        }
     }
+    red[tyz][tx] = ls;
+    __syncthreads();  // sw and red complete
+    if (tyz == 0) {
+        float t = red[0][tx];
+        for (int u = 1; u < 32; u++) t = __fadd_rn(t, red[u][tx]);
+        sInv[tx] = 1.0f / t;  // read after the barrier below
+    }
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int u = 0; u < kCombineSlices; u++)
+        if (j0 + u < j1) {
+            const float4 w = *(const float4 *)&sw[j0 + u][4 * c4];
+            acc.x = __builtin_fmaf(v[u].x, w.x, acc.x);
+            acc.y = __builtin_fmaf(v[u].y, w.y, acc.y);
+            acc.z = __builtin_fmaf(v[u].z, w.z, acc.z);
+            acc.w = __builtin_fmaf(v[u].w, w.w, acc.w);
+        }
+    *(float4 *)&sq[part][dy][4 * c4] = acc;
     __syncthreads();
-    const float *po = part_o + (int64_t)d * RH + col;
-    const int64_t js = (int64_t)L * RH;
-    float acc0 = 0.0f, acc1 = 0.0f;
-    int j = 0;
-#pragma unroll 4
-    for (; j + 1 < ns; j += 2) {
-        acc0 = __builtin_fmaf(po[(int64_t)j * js], sw[j][tx], acc0);
-        acc1 = __builtin_fmaf(po[(int64_t)(j + 1) * js], sw[j + 1][tx], acc1);
+    if (tid < 256) {
+        const int oc = tid & 31, od = tid >> 5;  // output column, dim
+        float t = sq[0][od][oc];
+#pragma unroll
+        for (int u = 1; u < kCombineParts; u++) t = __fadd_rn(t, sq[u][od][oc]);
+        clat[(int64_t)(blockIdx.x * 32 + oc) * L + blockIdx.y * 8 + od] = __fmul_rn(t, sInv[oc]);
     }
-    if (j < ns) acc0 = __builtin_fmaf(po[(int64_t)j * js], sw[j][tx], acc0);
-    clat[(int64_t)col * L + d] = __fmul_rn(__fadd_rn(acc0, acc1), sInv[tx]);
 }
 
-// Largest slice count over the rows' context lengths n <= T.
+// Largest slice count over the rows' context lengths n <= T (an upper
+// bound: slices past a row's count exit at once).
 static int64_t mla_mfma_nslice(int64_t T) {
-    int64_t best = (T + mla_mfma_slice(T) - 1) / mla_mfma_slice(T);
-    for (int64_t b = 64; b <= T; b *= 2) {  // just below each slice-length step
-        const int64_t n = b * 64 - 1;
-        if (n > T) break;
-        const int64_t s = mla_mfma_slice(n), c = (n + s - 1) / s;
-        if (c > best) best = c;
-    }
-    return best;
+    if (T <= 2048) return (T + 31) / 32;  // 32-position slices
+    if (T <= 16384) return 64;            // length >= n/64
+    return (T + 255) / 256;               // 256-position slices
 }
 
 static bool mla_mfma_ok(int64_t H, int64_t L, int64_t P, int64_t T) {
@@ -558,8 +604,8 @@ int32_t launch_mla_attend_kc(ut_ctx *ctx, const float *qabs, const float *qrope,
     UT_TRY(launch_check(ctx, "k_mla_mfma"));
     tok = timing_begin(ctx, "mla_combine");
     hipLaunchKernelGGL(k_mla_combine_mfma, dim3((unsigned)(RH / 32), (unsigned)(L / 8)),
-                       dim3(256), 0, ctx->stream, a.part_m, a.part_l, a.part_o, (int)RH, (int)H,
-                       (int)L, pos_base, clat);
+                       dim3(1024), 0, ctx->stream, a.part_m, a.part_l, a.part_o,
+                       (int)RH, (int)H, (int)L, pos_base, clat);
     timing_end(ctx, tok);
     return launch_check(ctx, "k_mla_combine_mfma");
 }
