@@ -546,6 +546,54 @@ __global__ __launch_bounds__(256) void k_gemv_splitk_sum(PlainArgs a, int M) {
     *o = a.accumulate ? __fadd_rn(*o, v) : v;
 }
 
+// The split-K sum for one row per workgroup (thread t: rows 8t..8t+7 of the
+// output, each finished exactly as k_gemv_splitk_sum does), then the
+// finished row rms-normalised and digitised by the row digitiser's body
+// (nd: K = O).  Integer formats, one weight (O1 == O), O % 8 == 0.
+template <int FMT>
+__global__ __launch_bounds__(1024) void k_splitk_sum_norm(PlainArgs a, int M, RowDigArgs nd) {
+    __shared__ double redd[16];
+    __shared__ uint32_t redu[16];
+    const int m = blockIdx.x, tid = threadIdx.x;
+    const int64_t c0 = 8 * (int64_t)tid;
+    float v[1][8], wv[1][8];
+    if (c0 < a.O) {
+        const int64_t zs = (int64_t)M * a.O;
+        const int64_t *p = a.part + m * a.O + c0;
+        int64_t S[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) S[j] = p[j];
+#pragma unroll 4
+        for (int z = 1; z < a.ks; z++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) S[j] += p[z * zs + j];
+        float *po = a.out + m * a.ldo + c0;
+        const float4 s0 = *(const float4 *)(a.scales + c0), s1 = *(const float4 *)(a.scales + c0 + 4);
+        const float sc[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+        const float4 w0 = *(const float4 *)(nd.norm_w + c0), w1 = *(const float4 *)(nd.norm_w + c0 + 4);
+        float old[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (a.accumulate) {
+            const float4 o0 = *(const float4 *)po, o1 = *(const float4 *)(po + 4);
+            old[0] = o0.x; old[1] = o0.y; old[2] = o0.z; old[3] = o0.w;
+            old[4] = o1.x; old[5] = o1.y; old[6] = o1.z; old[7] = o1.w;
+        }
+        const int32_t e = a.exps[m];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float x = int_total_to_f32(S[j], e, sc[j]);
+            v[0][j] = a.accumulate ? __fadd_rn(old[j], x) : x;
+        }
+        *(float4 *)po = make_float4(v[0][0], v[0][1], v[0][2], v[0][3]);
+        *(float4 *)(po + 4) = make_float4(v[0][4], v[0][5], v[0][6], v[0][7]);
+        wv[0][0] = w0.x; wv[0][1] = w0.y; wv[0][2] = w0.z; wv[0][3] = w0.w;
+        wv[0][4] = w1.x; wv[0][5] = w1.y; wv[0][6] = w1.z; wv[0][7] = w1.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[0][j] = 0.0f, wv[0][j] = 0.0f;
+    }
+    rowdig_body<1>(nd, m, v, wv, redd, redu);
+}
+
 // ------------------------------------------------------ generic GEMV ---
 // One wave per output row; any K and alignment.  Integer formats sum
 // x~ * q exactly (so the result equals the fast kernel's bit for bit);
@@ -737,11 +785,31 @@ static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrow
     }
     if (a.ks > 1) {
         UT_TRY(launch_check(ctx, name));
+        const bool fuse_next = FMT != UT_FMT_F32 && ga.next && !ga.defer && !w2 && m0 == 0 &&
+                               mrows == ga.M && a.O % 8 == 0 && a.O <= 8 * 1024 &&
+                               aligned16(a.out) && a.ldo % 4 == 0 && aligned16(a.scales) &&
+                               aligned16(ga.next->norm_w) && ga.next->nd.exps;
         if (ga.defer) {
             // the consumer sums the partials (only one chunk of rows)
             ga.defer->part = a.part;
             ga.defer->ks = a.ks;
             ga.defer->O = a.O;
+        } else if (fuse_next) {
+            const NormNext &nx = *ga.next;
+            RowDigArgs nd{};
+            nd.K = a.O;
+            nd.norm_w = nx.norm_w;
+            nd.eps = nx.eps;
+            nd.out = nx.normed;
+            nd.ldo = nx.ldn;
+            nd.exps = nx.nd.exps;
+            nd.dig4 = (nx.flags & XD_DIG4) ? nx.nd.dig4 : nullptr;
+            nd.dig8 = (nx.flags & XD_DIG8) ? nx.nd.dig8 : nullptr;
+            nd.xt = (nx.flags & XD_XT) ? nx.nd.xt : nullptr;
+            const unsigned threads = (unsigned)((a.O / 8 + 63) / 64 * 64);
+            hipLaunchKernelGGL(k_splitk_sum_norm<FMT>, dim3((unsigned)mrows), dim3(threads), 0,
+                               ctx->stream, a, mrows, nd);
+            if (ga.next_done) *ga.next_done = true;
         } else {
             const int64_t n = a.O * mrows;
             hipLaunchKernelGGL(k_gemv_splitk_sum<FMT>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
@@ -830,6 +898,7 @@ int32_t launch_rowdot_f32(ut_ctx *ctx, const ut_qtensor *w, const float *x, int6
 int32_t gemv(ut_ctx *ctx, const GemvArgs &ga) {
     const ut_qtensor *w = ga.w;
     if (ga.defer) ga.defer->ks = 1;
+    if (ga.next_done) *ga.next_done = false;
     if (ga.M <= 0) return UT_OK;
     if (ga.w2 && (ga.w2->fmt != w->fmt || ga.w2->in_dim != w->in_dim ||
                   ga.w2->row_bytes != w->row_bytes || !fast_ok(ga.w2) || !fast_ok(w) ||

@@ -206,6 +206,11 @@ struct GemvArgs {
     const uint32_t *xmax = nullptr;
     int nxmax = 0;
     int32_t *exps_out = nullptr;
+    // optional (M <= 4, one weight, no defer): when the GEMV splits K, its
+    // partial sum also runs this rmsnorm+digitise on the finished rows (one
+    // launch instead of two); *next_done reports whether it did
+    const struct NormNext *next = nullptr;
+    bool *next_done = nullptr;
 };
 int32_t gemv(ut_ctx *ctx, const GemvArgs &a);
 // The kv_a / q_a pair GEMV's deferred split-K partials (kv_a rows first)

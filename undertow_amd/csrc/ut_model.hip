@@ -537,7 +537,9 @@ int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
 // mla_forward_cached, absorbed form (attention.rs:123-279), added into out
 // (the residual).  x: normed rows with digits xd.
 int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, const XDigits &xd,
-                    int64_t rows, KvCache &kv, float *out) {
+                    int64_t rows, KvCache &kv, float *out, const NormNext *post = nullptr,
+                    bool *post_done = nullptr) {
+    if (post_done) *post_done = false;
     ut_model *m = s->m;
     ut_ctx *ctx = m->ctx;
     const ut_model_config &c = m->c;
@@ -625,6 +627,9 @@ int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
     ga.xmax = w.vmax;
     ga.nxmax = (int)(heads * ((vh + 7) / 8));
     ga.exps_out = w.vexps;
+    // the post-attention norm runs in o_proj's partial sum when K is split
+    ga.next = post;
+    ga.next_done = post_done;
     return gemv(ctx, ga);
 }
 
@@ -670,8 +675,15 @@ int32_t run_layer(ut_session *s, const LayerW &L, float *x, int64_t rows, KvCach
         f = dig_flags_fmt(L.expert_fmt, H);
         if (L.has_shared) f |= dig_flags_fmt(L.shared.fmt, H);
     }
-    UT_TRY(mla_forward(s, L, w.normed, xd, rows, kv, x));
-    UT_TRY(norm_dig(s, x, H, L.post_norm, H, rows, w.normed, H, w.digA, f, &xd));
+    // the post-attention norm, run inside o_proj's split-K sum where it can
+    // be (every reader of the layer's normed input has run by then)
+    XDigits pd;
+    const NormNext post = next_norm(s, L.post_norm, f, rows, &pd);
+    bool post_done = false;
+    UT_TRY(mla_forward(s, L, w.normed, xd, rows, kv, x, fuse_next_ok(m, rows) ? &post : nullptr,
+                       &post_done));
+    if (post_done) xd = pd;
+    else UT_TRY(norm_dig(s, x, H, L.post_norm, H, rows, w.normed, H, w.digA, f, &xd));
     if (L.dense) return mlp_add(s, L.mlp, w.normed, xd, rows, x, nullptr, next);
     // x += (routed + shared) (model.rs:282-284 then the residual add)
     if (L.has_shared && moe_dual_ok(L.expert_fmt, L.shared.fmt))
