@@ -432,13 +432,14 @@ __device__ __forceinline__ float *plain_out(const PlainArgs &a, int64_t m, int64
     return row < a.O1 ? a.out + m * a.ldo + row : a.out2 + m * a.ldo2 + (row - a.O1);
 }
 
-// 16*R output rows per workgroup (R = 2 rows per lane at M = 1 -- registers
-// for four workgroups per CU and every weight step of a short row in flight
-// -- 4 at M = 2 (activation reuse), else 2): wave w, row group g, slot r ->
-// row blockIdx.x*16R + w*4R + g*R + r.
-template <int M> constexpr int plain_rows() { return M == 2 ? 4 : 2; }
-template <int M> constexpr int plain_depth() { return M == 1 ? 4 : gemv_depth<M>(); }
-__host__ __device__ constexpr int plain_rows_rt(int M) { return 16 * (M == 2 ? 4 : 2); }
+// 32 output rows per workgroup (R = 2 rows per lane: registers for three or
+// four workgroups per CU; four rows per lane at M = 2 held two or three and
+// measured slower): wave w, row group g, slot r -> row blockIdx.x*16R +
+// w*4R + g*R + r.  Weight steps in flight: every step of a short row at
+// M = 1, two at M = 2, the core's default above.
+template <int M> constexpr int plain_rows() { return 2; }
+template <int M> constexpr int plain_depth() { return M == 1 ? 4 : M == 2 ? 2 : gemv_depth<M>(); }
+__host__ __device__ constexpr int plain_rows_rt(int) { return 16 * 2; }
 
 template <int FMT, int M>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
@@ -583,15 +584,14 @@ __global__ __launch_bounds__(1024) void k_splitk_sum_norm(PlainArgs a, int M, Ro
             const float x = int_total_to_f32(S[j], e, sc[j]);
             v[0][j] = a.accumulate ? __fadd_rn(old[j], x) : x;
         }
-        *(float4 *)po = make_float4(v[0][0], v[0][1], v[0][2], v[0][3]);
-        *(float4 *)(po + 4) = make_float4(v[0][4], v[0][5], v[0][6], v[0][7]);
         wv[0][0] = w0.x; wv[0][1] = w0.y; wv[0][2] = w0.z; wv[0][3] = w0.w;
         wv[0][4] = w1.x; wv[0][5] = w1.y; wv[0][6] = w1.z; wv[0][7] = w1.w;
     } else {
 #pragma unroll
         for (int j = 0; j < 8; j++) v[0][j] = 0.0f, wv[0][j] = 0.0f;
     }
-    rowdig_body<1>(nd, m, v, wv, redd, redu);
+    // the finished row goes to out after the reductions (nd.raw)
+    rowdig_body<1, true>(nd, m, v, wv, redd, redu);
 }
 
 // ------------------------------------------------------ generic GEMV ---
@@ -657,11 +657,12 @@ static bool fast_ok(const ut_qtensor *w) {
 }
 
 // Split of K for a weight of O rows and K columns.  Weights with fewer
-// than 256 tiles of 64 rows cannot keep the chip's loads in flight, so
-// their K range is split over blockIdx.z (each split at least two steps
-// wide) and a second launch sums the partials.  The split depends on the
-// weight's shape only, so an f32 row's summation order is the same for
-// every M.
+// than 256 row tiles cannot keep the chip's loads in flight, so their K
+// range is split over blockIdx.z (each split at least two steps wide) and a
+// second launch sums the partials.  f32 splits depend on the weight's shape
+// only (64-row tiles, about kSplitTargetWGs workgroups), so an f32 row's
+// summation order is the same for every M; integer partials are exact, so
+// their split follows the launch's own tiles and occupancy.
 constexpr int64_t kSplitTargetWGs = 1024;
 constexpr int64_t kSplitMinTiles = 256;  // integer formats: at least this many tiles -> no split
 
@@ -806,6 +807,8 @@ static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrow
             nd.dig4 = (nx.flags & XD_DIG4) ? nx.nd.dig4 : nullptr;
             nd.dig8 = (nx.flags & XD_DIG8) ? nx.nd.dig8 : nullptr;
             nd.xt = (nx.flags & XD_XT) ? nx.nd.xt : nullptr;
+            nd.raw = a.out;
+            nd.ldr = a.ldo;
             const unsigned threads = (unsigned)((a.O / 8 + 63) / 64 * 64);
             hipLaunchKernelGGL(k_splitk_sum_norm<FMT>, dim3((unsigned)mrows), dim3(threads), 0,
                                ctx->stream, a, mrows, nd);

@@ -10,7 +10,7 @@
 //   k_moe_gate_up  grid (I/16, slots): gate and up rows of one expert in the
 //                  same lanes, h = silu(g)*u written per (slot, row), plus
 //                  per-workgroup max|h| partials
-//   k_moe_down     grid (H/64 or H/32, slots): d = down(h) per (slot, row),
+//   k_moe_down     grid (H/32, slots): d = down(h) per (slot, row),
 //                  h digitised while it is staged (exponent from the partials)
 //   k_moe_combine  out[s] = sum_c w[s,c]*d[slot(s,c), s] in router order
 // Every expert's weights are read once per pass whatever rows chose it;
@@ -664,10 +664,10 @@ __device__ __forceinline__ int32_t h_shift(const uint32_t *hmax_parts, int npart
     return rowmax_shift(hmax_parts, nparts, row, red4);
 }
 
-// Rows per lane: 2 at M = 1 (registers for four workgroups per CU and
-// every weight step in flight), 4 at M = 2 (more activation reuse), 2 above
-// (registers).
-template <int M> constexpr int down_rows() { return M == 2 ? 4 : 2; }
+// Rows per lane: 2 (registers for three or four workgroups per CU; at M = 1
+// also every weight step in flight; four rows per lane at M = 2 held two
+// workgroups per CU and measured slower).
+template <int M> constexpr int down_rows() { return 2; }
 
 // Staged columns of down's h: inter sizes up to 2048 stage once (fewer
 // staging registers, so more workgroups fit a CU); longer K is staged in
@@ -675,8 +675,8 @@ template <int M> constexpr int down_rows() { return M == 2 ? 4 : 2; }
 template <int FMT, int M> constexpr int down_kc() { return gemv_chunk_cols<FMT, M, 2048>(); }
 
 // Weight steps in flight in down: at M = 1 four (all of a 2048-column
-// int4 row), else the core's default.
-template <int M> constexpr int down_depth() { return M == 1 ? 4 : gemv_depth<M>(); }
+// int4 row), two at M = 2, else the core's default.
+template <int M> constexpr int down_depth() { return M == 1 ? 4 : M == 2 ? 2 : gemv_depth<M>(); }
 
 template <int FMT, int M>
 __device__ __forceinline__ void down_body(const DownArgs &a, int u, int tile, uint32_t *lds) {
@@ -939,8 +939,6 @@ __global__ __launch_bounds__(1024) void k_moe_combine_norm(
         float acc[8];
         combine_cols<8>(choice_slot, weights, d, M, k, H, count, extra, dshared,
                         init ? init + s * ldo + c0 : nullptr, accumulate ? po : nullptr, s, c0, acc);
-        *(float4 *)po = make_float4(acc[0], acc[1], acc[2], acc[3]);
-        *(float4 *)(po + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
         wv[0][0] = w0.x; wv[0][1] = w0.y; wv[0][2] = w0.z; wv[0][3] = w0.w;
         wv[0][4] = w1.x; wv[0][5] = w1.y; wv[0][6] = w1.z; wv[0][7] = w1.w;
 #pragma unroll
@@ -949,7 +947,8 @@ __global__ __launch_bounds__(1024) void k_moe_combine_norm(
 #pragma unroll
         for (int j = 0; j < 8; j++) v[0][j] = 0.0f, wv[0][j] = 0.0f;
     }
-    rowdig_body<1>(nd, s, v, wv, redd, redu);
+    // the combined row goes to out after the reductions (nd.raw)
+    rowdig_body<1, true>(nd, s, v, wv, redd, redu);
 }
 
 bool moe_combine_norm_ok(int64_t H) { return H % 8 == 0 && H <= 8 * 1024; }
@@ -1201,6 +1200,8 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
         nd.dig4 = (nx.flags & XD_DIG4) ? nx.nd.dig4 : nullptr;
         nd.dig8 = (nx.flags & XD_DIG8) ? nx.nd.dig8 : nullptr;
         nd.xt = (nx.flags & XD_XT) ? nx.nd.xt : nullptr;
+        nd.raw = c.out;
+        nd.ldr = c.ldo;
         tok = timing_begin(ctx, "moe_combine_norm");
         const unsigned threads = (unsigned)((c.H / 8 + 63) / 64 * 64);
         hipLaunchKernelGGL(k_moe_combine_norm, dim3((unsigned)M), dim3(threads), 0, ctx->stream,

@@ -35,6 +35,10 @@ struct RowDigArgs {
     const void *const *tbl;  // [6][E] expert pointer table
     MoePlan plan;
     int32_t *err_flag;
+    // rowdig_body<GPT, true>: the incoming (un-normalised) row is stored
+    // here (row stride ldr) after the reductions
+    float *raw;
+    int64_t ldr;
 };
 
 template <typename T, typename Op>
@@ -53,13 +57,22 @@ __device__ __forceinline__ T wide_reduce(T v, Op op, T *red /* [16] */) {
 
 // The part of the row digitiser after the row is in registers: thread tid
 // owns the 8-column groups tid + g*blockDim.x (v zero past K), wv the norm
-// weights of the same columns (read when a.norm_w is set).
-template <int GPT>
+// weights of the same columns (read when a.norm_w is set).  RAW: also store
+// the incoming row to a.raw -- after the reductions, so that their barriers
+// do not wait for the stores (a producer that finishes the row hands it
+// over here instead of storing it first).
+template <int GPT, bool RAW = false>
 __device__ __forceinline__ void rowdig_body(const RowDigArgs &a, int64_t m, float (&v)[GPT][8],
                                             const float (&wv)[GPT][8], double *redd,
                                             uint32_t *redu) {
     const int tid = threadIdx.x, nt = blockDim.x;
     const int64_t K = a.K, NG = (K + 7) / 8;
+    float rv[RAW ? GPT : 1][8];
+    if constexpr (RAW)
+#pragma unroll
+        for (int g = 0; g < GPT; g++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) rv[g][j] = v[g][j];
     if (a.norm_w) {
         double acc = 0.0;
 #pragma unroll
@@ -87,6 +100,16 @@ __device__ __forceinline__ void rowdig_body(const RowDigArgs &a, int64_t m, floa
     }
     mx = wide_reduce(mx, [](uint32_t p, uint32_t q) { return p > q ? p : q; }, redu);
     // every store comes after the last barrier, so no barrier waits for them
+    if constexpr (RAW) {
+#pragma unroll
+        for (int g = 0; g < GPT; g++) {
+            const int64_t c = tid + (int64_t)g * nt;
+            if (8 * c + 8 > K) continue;  // callers with RAW take whole groups
+            float *o = a.raw + m * a.ldr + 8 * c;
+            *(float4 *)o = make_float4(rv[g][0], rv[g][1], rv[g][2], rv[g][3]);
+            *(float4 *)(o + 4) = make_float4(rv[g][4], rv[g][5], rv[g][6], rv[g][7]);
+        }
+    }
     if (a.out) {
 #pragma unroll
         for (int g = 0; g < GPT; g++) {
