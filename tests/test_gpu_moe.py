@@ -159,6 +159,25 @@ def test_moe_experts_small(ctx, fmt, M):
         assert np.array_equal(one[0], got[s])
 
 
+@pytest.mark.parametrize("M", [1, 3, 7])
+def test_moe_experts_many_choices(ctx, M):
+    """k = 10 choices (the combine's general path past 8) and M*k > 64 at
+    M = 7 (the plan built before gate/up instead of inside it)."""
+    rng = np.random.default_rng(70 + M)
+    E, H, I, k = 16, 512, 64, 10
+    tbl, host_w = make_experts(ctx, rng, INT4, E, H, I)
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(M)]).astype(np.int32)
+    w = rng.random((M, k)).astype(np.float32)
+    x = rng.standard_normal((M, H)).astype(np.float32)
+    got = host(tbl.moe_experts(dev(ids), dev(w), dev(x)))
+    want = oracle_moe(INT4, H, I, host_w, ids, w, x)
+    tol = 1e-4 * np.maximum(np.abs(want), 1.0)
+    assert (np.abs(got - want) <= tol).all(), np.abs(got - want).max()
+    for s_ in range(M):
+        one = host(tbl.moe_experts(dev(ids[s_:s_ + 1]), dev(w[s_:s_ + 1]), dev(x[s_:s_ + 1])))
+        assert np.array_equal(one[0], got[s_])
+
+
 def test_moe_experts_f32_weights(ctx):
     import undertow_amd as U
     rng = np.random.default_rng(9)
