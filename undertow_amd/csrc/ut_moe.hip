@@ -629,11 +629,13 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up(GateUpArgs a) {
 // Routed experts (format FA, slots 0..gridDim.y-2) and one shared MLP
 // (format FB, the last grid row) in one launch.
 template <int FA, int FB, int M>
-// At one row, registers for five workgroups per CU: the routed and shared
-// experts' 9 x 128 workgroups are then all resident at once (four per CU
-// left 128 for a second pass: 32.6 -> 29.9 us); the plain kernel's 1,024
-// need only four and run faster without the bound's spills.
-__global__ __launch_bounds__(kGemvThreads, M == 1 ? 5 : 1) void k_moe_gate_up_dual(GateUpArgs a, GateUpArgs b) {
+// At one and two rows, registers for five workgroups per CU (a few spilled
+// values): at one row the routed and shared experts' 9 x 128 workgroups are
+// then all resident at once (four per CU left 128 for a second pass:
+// 32.6 -> 29.9 us), at two rows the 17 x 128 take 1.7 passes instead of 2.1
+// (66.9 -> 63.4 us).  The plain kernel's 1,024 workgroups at one row need
+// only four per CU and run faster without the bound's spills.
+__global__ __launch_bounds__(kGemvThreads, M <= 2 ? 5 : 1) void k_moe_gate_up_dual(GateUpArgs a, GateUpArgs b) {
     __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
     __shared__ uint32_t wg_max[4];
     if (blockIdx.y + 1 < gridDim.y) gate_up_body<FA, M>(a, blockIdx.y, blockIdx.x, lds, wg_max);
