@@ -11,7 +11,7 @@ import json
 import numpy as np
 import pytest
 
-from models import C1, C1_MLA, checkpoint, gpu_model, prompt_ids
+from models import C1, C1_E256, C1_MLA, checkpoint, gpu_model, prompt_ids
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -94,6 +94,28 @@ def test_c1_mla_shape_logits_and_stream(c1_mla):
     ok = gap_ok(want)
     assert (got.argmax(1)[ok] == want.argmax(1)[ok]).all()
     assert m.generate_greedy(prompt, 16) == om.greedy_decode(prompt, 16)[16:]
+
+
+@pytest.fixture(scope="module")
+def c1_e256(ctx):
+    ck = checkpoint(C1_E256, fmt="int4")
+    return ck, gpu_model(ctx, ck), O.Model(ck)
+
+
+def test_c1_deepseek_router_logits_stream_and_mtp(c1_e256):
+    """256 experts, 8 groups, top-8: prefill (4-row chunks), decode (1 row)
+    and MTP verify (2 rows) route inside the expert launch."""
+    ck, m, om = c1_e256
+    prompt = prompt_ids(16, C1_E256["vocab_size"])
+    got, want = m.forward(prompt), om.forward(prompt)
+    err = np.abs(got - want)
+    assert err.max() <= 1e-3 and err.mean() <= 1e-4, (err.max(), err.mean())
+    ok = gap_ok(want)
+    assert (got.argmax(1)[ok] == want.argmax(1)[ok]).all()
+    stream = om.greedy_decode(prompt, 32)[16:]
+    assert m.generate_greedy(prompt, 32) == stream
+    toks, drafted, accepted = m.generate_mtp(prompt, 32, depth=1)
+    assert toks == stream and drafted > 0
 
 
 def test_c1_mtp_matches_oracle_and_greedy(c1):

@@ -485,15 +485,12 @@ int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
         }
         const int64_t slots = moe_slots(M, k, E, -1);
         ScratchLayout lay = moe_layout(M, k, slots, H, c.moe_intermediate_size, L.expert_fmt);
-        // with the logits whole and few choices the expert launch builds the
-        // slot plan itself (route alone here); else route + plan in one launch
+        // with the logits whole and few choices the expert launch routes and
+        // builds the slot plan itself (moe_pass); else route + plan in one
+        // launch here
         const bool gate_plans = gparts.ks <= 1 && (int64_t)M * k <= 64 &&
                                 L.expert_fmt != UT_FMT_F32;
-        if (gate_plans)
-            UT_TRY(launch_route(m->ctx, s->ws.rlogits, L.bias, M, E, k, (int)c.n_group,
-                                (int)c.topk_group, c.norm_topk_prob, c.routed_scaling_factor,
-                                s->ws.rids, s->ws.rw));
-        else
+        if (!gate_plans)
             UT_TRY(launch_route_plan(m->ctx, s->ws.rlogits, &gparts, L.bias, M, E, k,
                                      (int)c.n_group, (int)c.topk_group, c.norm_topk_prob,
                                      c.routed_scaling_factor, s->ws.rids, s->ws.rw,
@@ -517,6 +514,16 @@ int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
         mc.accumulate = accumulate;
         mc.err_flag = s->ws.err;
         mc.plan_ready = !gate_plans;
+        if (gate_plans) {
+            mc.route_logits = s->ws.rlogits;
+            mc.route_bias = L.bias;
+            mc.route_ng = (int)c.n_group;
+            mc.route_tg = (int)c.topk_group;
+            mc.route_norm = c.norm_topk_prob;
+            mc.route_scale = c.routed_scaling_factor;
+            mc.route_ids = s->ws.rids;
+            mc.route_w = s->ws.rw;
+        }
         MoeCall sc;
         MoePlan sp_plan = m->mlp_plan;
         if (shared) {

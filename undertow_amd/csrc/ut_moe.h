@@ -72,6 +72,16 @@ struct MoeCall {
     // optional: the combine also rms-normalises and digitises the finished
     // rows of out (one launch instead of two; H <= 8192, H % 8 == 0)
     const NormNext *next = nullptr;
+    // optional: route too (k_route_wave's semantics) from the router logits
+    // [M, E]; the choices land in route_ids / route_w (which ids / weights
+    // must name).  Done inside the gate/up launch where it can be, else by a
+    // route launch first.
+    const float *route_logits = nullptr;
+    const float *route_bias = nullptr;
+    int route_ng = 1, route_tg = 1, route_norm = 0;
+    float route_scale = 1.0f;
+    int32_t *route_ids = nullptr;
+    float *route_w = nullptr;
 };
 bool moe_combine_norm_ok(int64_t H);
 

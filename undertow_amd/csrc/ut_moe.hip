@@ -192,11 +192,44 @@ static bool route_wave_ok(int64_t E, int n_group, int topk_group, int k, int *kp
 
 // Routes one row with one wavefront (all 64 lanes active).  Lane r < k
 // returns choice r in *my_id / *my_w (id -1, weight 0 past E).
+// This lane's logits and biases (experts lane*KPL + j), loaded ahead of the
+// routing so a caller can overlap the loads with other work.
+template <int KPL>
+__device__ __forceinline__ void route_load(const float *__restrict__ lg,
+                                           const float *__restrict__ bias, int E,
+                                           float (&lv)[KPL], float (&bv)[KPL]) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < KPL; j++) {
+        const int e = lane * KPL + j;
+        lv[j] = e < E ? lg[e] : 0.0f;
+        bv[j] = e < E && bias ? bias[e] : 0.0f;
+    }
+}
+
+template <int KPL>
+__device__ __forceinline__ void route_row_wave_v(const float (&lv)[KPL], const float (&bv)[KPL],
+                                                 bool has_bias, int E, int k, int n_group,
+                                                 int topk_group, int norm, float scale,
+                                                 int32_t *my_id, float *my_w);
+
 template <int KPL>
 __device__ __forceinline__ void route_row_wave(const float *__restrict__ lg,
                                                const float *__restrict__ bias, int E, int k,
                                                int n_group, int topk_group, int norm, float scale,
                                                int32_t *my_id, float *my_w) {
+    float lv[KPL], bv[KPL];
+    route_load<KPL>(lg, bias, E, lv, bv);
+    route_row_wave_v<KPL>(lv, bv, bias != nullptr, E, k, n_group, topk_group, norm, scale, my_id,
+                          my_w);
+}
+
+// The wave router on loaded logits (route_load).
+template <int KPL>
+__device__ __forceinline__ void route_row_wave_v(const float (&lv)[KPL], const float (&bv)[KPL],
+                                                 bool has_bias, int E, int k, int n_group,
+                                                 int topk_group, int norm, float scale,
+                                                 int32_t *my_id, float *my_w) {
     const int lane = threadIdx.x & 63;
     float sc[KPL];
     uint64_t key[KPL];
@@ -204,9 +237,9 @@ __device__ __forceinline__ void route_row_wave(const float *__restrict__ lg,
     for (int j = 0; j < KPL; j++) {
         const int e = lane * KPL + j;
         if (e < E) {
-            const float s = 1.0f / (1.0f + expf(-lg[e]));  // sigmoid (undertow-quant/src/lib.rs:116)
+            const float s = 1.0f / (1.0f + expf(-lv[j]));  // sigmoid (undertow-quant/src/lib.rs:116)
             sc[j] = s;
-            key[j] = route_key(bias ? __fadd_rn(s, bias[e]) : s, e);
+            key[j] = route_key(has_bias ? __fadd_rn(s, bv[j]) : s, e);
         } else {
             sc[j] = 0.0f;
             key[j] = 0;  // below every expert's key
@@ -482,6 +515,15 @@ struct GateUpArgs {
     const void *const *ptbl = nullptr;  // [6][E] pointer table
     MoePlan plan{};
     int32_t *err_flag = nullptr;
+    // optional (one row, with plan_ids' conditions, E/64 = 4 keys per
+    // lane): the waves route the row from the logits first; workgroup
+    // (0, 0) writes the choices to route_ids / route_w
+    const float *route_lg = nullptr;
+    const float *route_bias = nullptr;
+    int route_ng = 1, route_tg = 1, route_norm = 0;
+    float route_scale = 1.0f;
+    int32_t *route_ids = nullptr;
+    float *route_w = nullptr;
 };
 
 // The slot plan of make_plan for one activation row (n = k <= 64 entries),
@@ -569,9 +611,31 @@ __device__ __forceinline__ void gate_up_body(const GateUpArgs &a, int u, int til
         // or its digit planes) and stores nothing
         if (tile >= a.ntiles) return;
         const int n = a.plan_M * a.plan_k;
-        const int id = lane < n ? a.plan_ids[lane] : -1;
+        int id = (M > 1 || !a.route_lg) && lane < n ? a.plan_ids[lane] : -1;
         const uint8_t *dummy = a.x.xf ? (const uint8_t *)a.x.xf : (const uint8_t *)a.x.dig;
         auto mid = [&]() {
+            if constexpr (M == 1) if (a.route_lg) {
+                // wave m routes row m; the choices go round through LDS
+                __shared__ int32_t s_rid[64];
+                __shared__ float s_rw[64];
+                if (wave < a.plan_M) {
+                    int32_t rid = -1;
+                    float rw = 0.0f;
+                    route_row_wave<4>(a.route_lg + (int64_t)wave * a.E, a.route_bias, (int)a.E,
+                                      a.plan_k, a.route_ng, a.route_tg, a.route_norm,
+                                      a.route_scale, &rid, &rw);
+                    if (lane < a.plan_k) {
+                        s_rid[wave * a.plan_k + lane] = rid;
+                        s_rw[wave * a.plan_k + lane] = rw;
+                    }
+                }
+                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                id = lane < n ? s_rid[lane] : -1;
+                if (u == 0 && tile == 0 && wave == 0 && lane < n) {
+                    a.route_ids[lane] = id;
+                    a.route_w[lane] = s_rw[lane];
+                }
+            }
             const void *p6[6];
             cnt = plan_slot_wave(id, n, a.E, a.ptbl, u, u == 0 && tile == 0 && wave == 0, a.plan,
                                  a.err_flag, p6);
@@ -1043,6 +1107,16 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
                            (int64_t)M * c.k <= 64;
     const bool self_plan = gate_plan && !c.x_digits && !c.shared && c.H <= KC &&
                            c.H % FmtTraits<FMT>::kStepCols == 0 && M == 1;
+    const bool gate_plans_here = gate_plan && (self_plan || c.x_digits);
+    // routing inside gate/up: one row (at two rows the routing's registers
+    // and latency in the prologue cost the expert launch more than the
+    // route launch it saves), the wave router with four keys per lane
+    int kpl = 0;
+    const bool route_here = c.route_logits && gate_plans_here && M == 1 &&
+                            route_wave_ok(c.E, c.route_ng, c.route_tg, c.k, &kpl) && kpl == 4;
+    if (c.route_logits && !route_here)
+        UT_TRY(launch_route(ctx, c.route_logits, c.route_bias, M, c.E, c.k, c.route_ng, c.route_tg,
+                            c.route_norm, c.route_scale, c.route_ids, c.route_w));
     if constexpr (FMT == UT_FMT_F32) {
         xs.xf = c.x;
         xs.ldx = c.H;
@@ -1097,7 +1171,7 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
         a.h = h;
         a.hmax_parts = hmax;
         a.ntiles = (int)L.ntiles;
-        if (gate_plan && (self_plan || c.x_digits)) {
+        if (gate_plans_here) {
             a.plan_ids = c.ids;
             a.plan_M = M;
             a.plan_k = c.k;
@@ -1105,6 +1179,16 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
             a.ptbl = (const void *const *)c.tbl.gate_w;
             a.plan = plan;
             a.err_flag = c.err_flag;
+        }
+        if (gate_plans_here && route_here) {
+            a.route_lg = c.route_logits;
+            a.route_bias = c.route_bias;
+            a.route_ng = c.route_ng;
+            a.route_tg = c.route_tg;
+            a.route_norm = c.route_norm;
+            a.route_scale = c.route_scale;
+            a.route_ids = c.route_ids;
+            a.route_w = c.route_w;
         }
         if (c.shared) {
             const MoeCall &sc = *c.shared;
