@@ -3,16 +3,20 @@
 // sigmoid router (router.rs:58-113, undertow-core/src/router.rs:136-163).
 //
 // One pass over M <= 4 token rows:
-//   k_route        one workgroup per row: sigmoid, bias, group limitation,
+//   k_route_wave   one wavefront per row: sigmoid, bias, group limitation,
 //                  top-k by rank (value desc, lowest index first), weights
-//   k_moe_plan     unique experts in first-appearance order -> slots
-//   k_digitize     activation digits of x (shared by every expert)
+//                  (k_route: the workgroup form for other expert counts)
+//   slot plan      unique experts in first-appearance order -> slots; built
+//                  by every gate/up wave itself when M*k <= 64 (else by
+//                  k_moe_plan, k_route_plan_wave or the digitiser)
 //   k_moe_gate_up  grid (I/16, slots): gate and up rows of one expert in the
 //                  same lanes, h = silu(g)*u written per (slot, row), plus
-//                  per-workgroup max|h| partials
+//                  per-workgroup max|h| partials; at one row it may also
+//                  route the row and digitise x while staging it
 //   k_moe_down     grid (H/32, slots): d = down(h) per (slot, row),
 //                  h digitised while it is staged (exponent from the partials)
-//   k_moe_combine  out[s] = sum_c w[s,c]*d[slot(s,c), s] in router order
+//   k_moe_combine4 out[s] = sum_c w[s,c]*d[slot(s,c), s] in router order
+//                  (k_moe_combine_norm: also the next rmsnorm + digits)
 // Every expert's weights are read once per pass whatever rows chose it;
 // the row dimension rides along in the same instructions.
 #include "ut_gemv_core.h"
