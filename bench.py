@@ -80,7 +80,7 @@ def gpu_wait(torch, ms: float) -> None:
     torch.cuda._sleep(int(ms * _CYCLES_PER_MS))
 
 
-def expert_block_bench(U, ctx, torch, tbl, cfg, M, steps, warmup, fmt_bits, seed):
+def expert_block_bench(U, ctx, torch, tbl, cfg, M, steps, warmup, fmt_bits, seed, fused=True):
     """Time `steps` expert-block passes; returns dict with GB/s and kernel times."""
     from undertow_amd.configs import expert_bytes, gate_up_bytes
     E, H, I, k = cfg["n_experts"], cfg["hidden"], cfg["inter"], cfg["top_k"]
@@ -95,12 +95,21 @@ def expert_block_bench(U, ctx, torch, tbl, cfg, M, steps, warmup, fmt_bits, seed
     lib = U.lib()
 
     def step(i):
-        ctx.check(lib.ut_route(ctx.handle, logits[i].data_ptr(), None, M, E, k, cfg["n_group"],
-                               cfg["topk_group"], cfg["norm_topk_prob"],
-                               cfg["routed_scaling_factor"], ids_all[i].data_ptr(),
-                               w_all[i].data_ptr()))
-        ctx.check(lib.ut_moe_experts(ctx.handle, tbl._h, ids_all[i].data_ptr(),
-                                     w_all[i].data_ptr(), M, k, x.data_ptr(), out.data_ptr()))
+        if not fused:
+            ctx.check(lib.ut_route(ctx.handle, logits[i].data_ptr(), None, M, E, k,
+                                   cfg["n_group"], cfg["topk_group"], cfg["norm_topk_prob"],
+                                   cfg["routed_scaling_factor"], ids_all[i].data_ptr(),
+                                   w_all[i].data_ptr()))
+            ctx.check(lib.ut_moe_experts(ctx.handle, tbl._h, ids_all[i].data_ptr(),
+                                         w_all[i].data_ptr(), M, k, x.data_ptr(), out.data_ptr()))
+            return
+        # route + routed experts (moe_forward's body, model.rs:210-281) in
+        # one call; at one row the routing runs inside the gate/up launch
+        ctx.check(lib.ut_moe_route_experts(ctx.handle, tbl._h, logits[i].data_ptr(), None, M, k,
+                                           cfg["n_group"], cfg["topk_group"],
+                                           cfg["norm_topk_prob"], cfg["routed_scaling_factor"],
+                                           x.data_ptr(), out.data_ptr(), ids_all[i].data_ptr(),
+                                           w_all[i].data_ptr()))
 
     for i in range(warmup):
         step(i)
@@ -356,6 +365,11 @@ def main():
     log(f"config 2 int4 M=1: {head['gbs']:.1f} GB/s/step, gate_up {head['gate_up_gbs']:.1f} GB/s")
     variants = {}
     if args.variants:
+        r = expert_block_bench(U, ctx, torch, tbl4, C2, 1, args.steps, args.warmup, 4, 11,
+                               fused=False)
+        variants["int4_M1_route_then_experts"] = r
+        log(f"config 2 int4 M=1, ut_route then ut_moe_experts: {r['gbs']:.1f} GB/s, "
+            f"gate_up {r['gate_up_gbs']:.1f} GB/s")
         for M in (2, 4):
             r = expert_block_bench(U, ctx, torch, tbl4, C2, M, args.steps, args.warmup, 4, 11 + M)
             variants[f"int4_M{M}"] = r

@@ -158,6 +158,20 @@ int32_t ut_moe_experts(ut_ctx *ctx, const ut_expert_table *tbl, const int32_t *i
                        const float *weights_dev, int64_t rows, int32_t top_k, const float *x_dev,
                        float *out_dev);
 
+/* Route then run the routed experts, as moe_forward does per row
+ * (adapters/undertow-deepseek-moe/src/model.rs:210-281: route at :210-216,
+ * then the expert body): the choices of ut_route over logits_dev [rows, E]
+ * (E = the table's expert count; same arguments and semantics) are written
+ * to ids_dev / weights_dev [rows, top_k], and out_dev is ut_moe_experts'
+ * result for them.  Results are identical to ut_route followed by
+ * ut_moe_experts; at one row with the one-wave router's shapes the routing
+ * runs inside the expert launch. */
+int32_t ut_moe_route_experts(ut_ctx *ctx, const ut_expert_table *tbl, const float *logits_dev,
+                             const float *bias_dev, int64_t rows, int32_t top_k, int32_t n_group,
+                             int32_t topk_group, int32_t norm_topk_prob,
+                             float routed_scaling_factor, const float *x_dev, float *out_dev,
+                             int32_t *ids_dev, float *weights_dev);
+
 /* ------------------------------------------------------ sample / verify */
 /* argmax (undertow-core/src/sample.rs:353-361) per row: first index of the
  * maximum; NaN never wins; returns 0 when row[0] is NaN. */

@@ -214,6 +214,54 @@ def test_moe_experts_deepseek_shape(ctx, fmt, Ms):
                 assert np.array_equal(one[0], got[s]), (M, s)
 
 
+@pytest.mark.parametrize("fmt,H,I,Ms", [(INT4, 512, 256, (1, 2, 3, 5)), (INT8, 512, 128, (1, 2)),
+                                         (INT4, 7168, 2048, (1, 2))])
+@pytest.mark.parametrize("bias", [False, True])
+def test_moe_route_experts_matches_route_then_experts(ctx, fmt, H, I, Ms, bias):
+    """ut_moe_route_experts (routing inside the gate/up launch at one row
+    with DeepSeek-V3's router: 256 experts, 8 groups, top-4 groups, top-8)
+    gives ut_route's choices and ut_moe_experts' output bit for bit, and
+    the oracle's within the expert bar.  The 256-entry table reuses 16
+    distinct weight sets (each id is still its own slot)."""
+    import undertow_amd as U
+    rng = np.random.default_rng(500 + H + fmt + bias)
+    E, k, ng, tg = 256, 8, 8, 4
+    n_w = 16
+    tbl = U.ExpertTable(ctx, E, H, I)
+    host_w = []
+    qts = []
+    for j in range(n_w):
+        g = rand_qtensor(rng, fmt, I, H)
+        u = rand_qtensor(rng, fmt, I, H)
+        d = rand_qtensor(rng, fmt, H, I)
+        qts.append((U.QTensor(ctx, fmt, *g, I, H), U.QTensor(ctx, fmt, *u, I, H),
+                    U.QTensor(ctx, fmt, *d, H, I)))
+        host_w.append((g, u, d))
+    for e in range(E):
+        tbl.set(e, *qts[e % n_w])
+    b = (rng.standard_normal(E) * 0.1).astype(np.float32) if bias else None
+    for M in Ms:
+        logits = rng.standard_normal((M, E)).astype(np.float32)
+        x = rng.standard_normal((M, H)).astype(np.float32)
+        out, ids, w = tbl.moe_route_experts(dev(logits), None if b is None else dev(b), dev(x),
+                                            k, ng, tg, True, 2.5)
+        rid, rw = U.route(ctx, dev(logits), None if b is None else dev(b), k, ng, tg, True, 2.5)
+        ref = tbl.moe_experts(rid, rw, dev(x))
+        assert np.array_equal(host(ids), host(rid)), M
+        assert np.array_equal(host(w), host(rw)), M
+        assert np.array_equal(host(out), host(ref)), M
+        hid, hw = host(ids), host(w)
+        for r in range(M):
+            oid, ow = O.route(logits[r], b, k, ng, tg, True, 2.5)
+            assert hid[r].tolist() == oid.tolist(), (M, r)
+            assert np.abs(hw[r] - ow).max() <= 1e-6, (M, r)
+        # id e holds weight set e % 16 (the oracle computes each choice on
+        # its own, so two ids sharing a set stay two choices)
+        want = oracle_moe(fmt, H, I, host_w, (hid % n_w).astype(np.int32), hw, x)
+        tol = 1e-4 * np.maximum(np.abs(want), 1.0)
+        assert (np.abs(host(out) - want) <= tol).all(), (M, np.abs(host(out) - want).max())
+
+
 @pytest.mark.parametrize("H", [64, 256])  # 256: the gate/up launch resolves the plan
 def test_moe_bad_expert_is_reported(ctx, H):
     import undertow_amd as U

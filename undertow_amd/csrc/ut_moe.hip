@@ -1528,4 +1528,61 @@ int32_t ut_moe_experts(ut_ctx *ctx, const ut_expert_table *tbl, const int32_t *i
     return UT_OK;
 }
 
+int32_t ut_moe_route_experts(ut_ctx *ctx, const ut_expert_table *tbl, const float *logits_dev,
+                             const float *bias_dev, int64_t rows, int32_t top_k, int32_t n_group,
+                             int32_t topk_group, int32_t norm_topk_prob,
+                             float routed_scaling_factor, const float *x_dev, float *out_dev,
+                             int32_t *ids_dev, float *weights_dev) {
+    if (!ctx || !tbl || !logits_dev || !ids_dev || !weights_dev || !x_dev || !out_dev || rows < 0 ||
+        top_k <= 0 || top_k > 64 || n_group < 0 || n_group > 64 || topk_group < 0) {
+        set_error(ctx, "ut_moe_route_experts: bad argument (top_k must be 1..64, n_group <= 64)");
+        return UT_ERR_ARG;
+    }
+    if (tbl->n > 4096) {
+        set_error(ctx, "ut_moe_route_experts: n_experts %lld > 4096", (long long)tbl->n);
+        return UT_ERR_ARG;
+    }
+    if (tbl->fmt < 0) {
+        set_error(ctx, "ut_moe_route_experts: empty expert table");
+        return UT_ERR_BAD_EXPERT;
+    }
+    if (rows == 0) return UT_OK;
+    const int64_t maxM = 4;
+    const int64_t slots = moe_slots((int)maxM, top_k, tbl->n, -1);
+    ScratchPlan plan;
+    plan.add(moe_layout(maxM, top_k, slots, tbl->hidden, tbl->inter, tbl->fmt).total);
+    std::vector<void *> ptrs;
+    UT_TRY(scratch_acquire(ctx, plan, ptrs));
+    int32_t *flag = nullptr;
+    UT_TRY(device_error_flag(ctx, &flag));
+    for (int64_t s0 = 0; s0 < rows; s0 += maxM) {
+        MoeCall c;
+        c.fmt = tbl->fmt;
+        c.tbl = tbl->ptrs;
+        c.E = tbl->n;
+        c.H = tbl->hidden;
+        c.I = tbl->inter;
+        c.M = (int)((rows - s0) < maxM ? (rows - s0) : maxM);
+        c.k = top_k;
+        // the choices: routed inside the gate/up launch where that applies
+        // (one row, the one-wave router), else by a route launch first
+        c.route_logits = logits_dev + s0 * tbl->n;
+        c.route_bias = bias_dev;
+        c.route_ng = n_group;
+        c.route_tg = topk_group;
+        c.route_norm = norm_topk_prob;
+        c.route_scale = routed_scaling_factor;
+        c.route_ids = ids_dev + s0 * top_k;
+        c.route_w = weights_dev + s0 * top_k;
+        c.ids = c.route_ids;
+        c.weights = c.route_w;
+        c.x = x_dev + s0 * tbl->hidden;
+        c.out = out_dev + s0 * tbl->hidden;
+        c.ldo = tbl->hidden;
+        c.err_flag = flag;
+        UT_TRY(moe_pass(ctx, c, ptrs[0]));
+    }
+    return UT_OK;
+}
+
 }  // extern "C"

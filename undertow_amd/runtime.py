@@ -85,6 +85,8 @@ _SIGS = [
     ("ut_expert_table_set", _i32, [_vp, _i64, _vp, _vp, _vp]),
     ("ut_expert_table_free", None, [_vp]),
     ("ut_moe_experts", _i32, [_vp, _vp, _vp, _vp, _i64, _i32, _vp, _vp]),
+    ("ut_moe_route_experts", _i32, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _f32, _vp,
+                                    _vp, _vp, _vp]),
     ("ut_argmax_rows", _i32, [_vp, _vp, _i64, _i64, _vp]),
     ("ut_mla_attend", _i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _vp]),
     ("ut_mla_cache_split", _i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
@@ -380,6 +382,21 @@ class ExpertTable:
         self.ctx.check(lib().ut_moe_experts(self.ctx.handle, self._h, _ptr(ids), _ptr(weights),
                                             rows, k, _ptr(x), _ptr(out)))
         return out
+
+    def moe_route_experts(self, logits, bias, x, k, n_group, topk_group, norm_topk_prob,
+                          routed_scaling_factor):
+        """Route (ut_route's semantics) and run the experts in one call;
+        returns (out, ids, weights)."""
+        torch = _torch()
+        rows = x.shape[0]
+        out = torch.empty_like(x)
+        ids = torch.empty((rows, k), dtype=torch.int32, device=x.device)
+        w = torch.empty((rows, k), dtype=torch.float32, device=x.device)
+        self.ctx.check(lib().ut_moe_route_experts(
+            self.ctx.handle, self._h, _ptr(logits), _ptr(bias) if bias is not None else None, rows,
+            k, n_group, topk_group, int(norm_topk_prob), routed_scaling_factor, _ptr(x), _ptr(out),
+            _ptr(ids), _ptr(w)))
+        return out, ids, w
 
 
 class Model:
