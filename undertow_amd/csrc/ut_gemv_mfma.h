@@ -1,0 +1,169 @@
+// ut_gemv_mfma.h -- int4 skinny GEMV for 2..5 activation rows on the matrix
+// cores (v_mfma_i32_16x16x64_i8), the same exact-integer totals as the
+// dot-product core in ut_gemv_core.h.
+//
+// Why: with M activation rows the dot-product core reads 6*M digit words
+// from LDS and issues 24*M dot instructions per 16 weight bytes and row;
+// past two rows its accumulators (6 planes x M x rows per lane) leave room
+// for one weight step in flight, and the GEMV is latency-bound far below
+// the HBM rate.  On the matrix core one wave computes 16 weight rows
+// against N = 3*M columns (three base-256 digit planes per activation row)
+// with a 4-register accumulator, so the weight pipe can be kept deep.
+//
+// Work split of a wave: 16 weight rows (row i = lane & 15 is the A-operand
+// row this lane loads); lane group kg = lane >> 4 owns, per 128-column
+// step, the 32 columns [128j + 32kg, +32): one 16-byte load of packed int4,
+// unpacked to two 16-byte A operands of sign-extended bytes.  The byte
+// order inside an operand is a permutation of those columns (per 8-column
+// group: the even columns, then the odd ones, which is what masking the
+// low and high nibbles of a packed word gives); the staged activation
+// digits use the same permutation, and since A and B share the K order of
+// each lane group and byte, the products pair the same columns.
+//
+// Activations: x~ = rint(x * 2^sh) as in the dot-product core (the same
+// shift, so the same integer), written as three balanced base-256 digit
+// planes; plane row n = 3m + p holds the digits of activation row m.
+// Totals: S = sum_p 256^p * C[row][3m + p], exact in int64 (|C| < 2^31:
+// K * 8 * 128 <= 2^31 for K <= 2^21).
+#pragma once
+
+#include "ut_gemv_core.h"
+
+namespace ut {
+
+typedef int ut_i32x4 __attribute__((ext_vector_type(4)));
+
+// Staged digit row pitch: the chunk's columns plus 16 bytes, so the 16
+// plane rows a lane group reads sit in distinct LDS banks.
+template <int KC> __host__ __device__ constexpr int mfma_row_bytes() { return KC + 16; }
+template <int M, int KC> __host__ __device__ constexpr int mfma_lds_words() {
+    return 3 * M * mfma_row_bytes<KC>() / 4;
+}
+constexpr int kMfmaStepCols = 128;  // columns per step (4 lane groups x 32)
+
+// Sign-extended bytes of the 4 nibbles (bits 0-3 of each byte) of t, where
+// t holds each nibble with its top bit flipped: ((u ^ 8) + 120) ^ 128 is u's
+// two's-complement value for a nibble u, and no byte carries.
+__device__ __forceinline__ int mfma_sext4(uint32_t t) {
+    return (int)(((t & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u);
+}
+
+// Stage the columns [kc, kc + kcn) (kcn <= KC, a multiple of 8) of M f32
+// activation rows (row m at xf + m*ldx) as digit planes in the permuted
+// column order.  issue() runs after the activation loads are issued (the
+// caller's first weight loads); prep(sh) fills the per-row shifts
+// (INT32_MIN: non-finite row, zero digits).
+template <int M, int KC, typename Issue, typename Prep>
+__device__ __forceinline__ void mfma_stage_f32(const float *xf, int64_t ldx, int64_t kc, int kcn,
+                                               uint8_t *lds, Issue &&issue, Prep &&prep) {
+    constexpr int NI = (M * (KC / 8) + kGemvThreads - 1) / kGemvThreads;
+    constexpr int RB = mfma_row_bytes<KC>();
+    const int NG = kcn / 8, TOT = M * NG;
+    const int tid = threadIdx.x;
+    float4 v[NI][2];
+#pragma unroll
+    for (int j = 0; j < NI; j++) {
+        const int i = tid + j * kGemvThreads, ic = i < TOT ? i : TOT - 1;
+        const int m = ic / NG, g = ic - m * NG;
+        const float *src = xf + m * ldx + kc + 8 * g;
+        v[j][0] = ld_global<float4>(src);
+        v[j][1] = ld_global<float4>(src + 4);
+    }
+    issue();
+    __builtin_amdgcn_sched_barrier(0);
+    int32_t shl[4] = {0, 0, 0, 0};
+    prep(shl);
+#pragma unroll
+    for (int j = 0; j < NI; j++) {
+        const int i = tid + j * kGemvThreads;
+        if (i < TOT) {
+            const int m = i / NG, g = i - m * NG;
+            const int32_t sh = m == 0 ? shl[0] : m == 1 ? shl[1] : m == 2 ? shl[2] : shl[3];
+            const float ev[4] = {v[j][0].x, v[j][0].z, v[j][1].x, v[j][1].z};
+            const float od[4] = {v[j][0].y, v[j][0].w, v[j][1].y, v[j][1].w};
+            uint32_t we[3], wo[3];
+            digit_words<UT_FMT_INT8>(ev, 4, sh, we);
+            digit_words<UT_FMT_INT8>(od, 4, sh, wo);
+#pragma unroll
+            for (int p = 0; p < 3; p++)
+                *(uint2 *)(lds + (3 * m + p) * RB + 8 * g) = make_uint2(we[p], wo[p]);
+        }
+    }
+    __syncthreads();
+}
+
+// One wave: 16 rows x M activation rows over the columns [0, K) staged
+// whole (K <= KC, K % 128 == 0).  arow: this lane's A row (row lane & 15
+// of the wave's 16, clamped to a valid row).  DEPTH steps of weights in
+// flight.  The total for (wave row 4g + r, activation row m) lands in
+// res.S[r][m] of sub-lane 4r + m of lane group g (the dot-product core's
+// convention with 4 rows per lane).
+template <int M, int DEPTH, int KC, typename Prep>
+__device__ __forceinline__ void mfma_gemv_i4_f32x(const uint8_t *arow, int64_t K, const float *xf,
+                                                  int64_t ldx, uint8_t *lds,
+                                                  CoreOut<UT_FMT_INT4, M, 4> &res, Prep &&prep) {
+    static_assert(M >= 1 && M <= 4, "three digit planes per row, 16 columns");
+    constexpr int RB = mfma_row_bytes<KC>();
+    const int lane = threadIdx.x & 63, n = lane & 15, kg = lane >> 4;
+    const int nsteps = (int)(K / kMfmaStepCols);
+    const uint8_t *ap = arow + 16 * kg;  // step j: bytes [64j + 16kg, +16)
+    uint4 wq[DEPTH];
+    mfma_stage_f32<M, KC>(xf, ldx, 0, (int)K, lds, [&]() {
+#pragma unroll
+        for (int u = 0; u < DEPTH; u++) wq[u] = ld_weights(ap + 64 * (u < nsteps ? u : nsteps - 1));
+    }, prep);
+    const bool bn = n < 3 * M;
+    const uint8_t *bp = lds + (bn ? n : 0) * RB + 32 * kg;
+    ut_i32x4 acc = {0, 0, 0, 0};
+    auto step = [&](const uint4 &w, int j) {
+        const uint32_t X = 0x88888888u;
+        const uint32_t a0 = w.x ^ X, a1 = w.y ^ X, a2 = w.z ^ X, a3 = w.w ^ X;
+        const ut_i32x4 A0 = {mfma_sext4(a0), mfma_sext4(a0 >> 4), mfma_sext4(a1), mfma_sext4(a1 >> 4)};
+        const ut_i32x4 A1 = {mfma_sext4(a2), mfma_sext4(a2 >> 4), mfma_sext4(a3), mfma_sext4(a3 >> 4)};
+        uint4 b0 = *(const uint4 *)(bp + kMfmaStepCols * j);
+        uint4 b1 = *(const uint4 *)(bp + kMfmaStepCols * j + 16);
+        if (!bn) b0 = b1 = make_uint4(0u, 0u, 0u, 0u);
+        const ut_i32x4 B0 = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w};
+        const ut_i32x4 B1 = {(int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, acc, 0, 0, 0);
+    };
+    int t = 0;
+    for (; t + 2 * DEPTH <= nsteps; t += DEPTH) {
+#pragma unroll
+        for (int u = 0; u < DEPTH; u++) {
+            step(wq[u], t + u);
+            wq[u] = ld_weights(ap + 64 * (t + u + DEPTH));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 2 * DEPTH; i++) {
+        if (t + i < nsteps) {
+            step(wq[i % DEPTH], t + i);
+            if (t + i + DEPTH < nsteps) wq[i % DEPTH] = ld_weights(ap + 64 * (t + i + DEPTH));
+        }
+    }
+    // acc[q] = C[4kg + q][n]: sub-lane s = 4r + m of group kg collects
+    // row 4kg + r's planes 3m, 3m+1, 3m+2 from sub-lanes 3m + p
+    const int r_me = n >> 2, m_me = n & 3;
+    int64_t S = 0;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+#pragma unroll
+        for (int p = 0; p < 3; p++) {
+            const int src = (lane & 48) | (3 * m_me + p);
+            const int v = __shfl(acc[q], src, 64);
+            if (q == r_me) S += (int64_t)v * (int64_t)(1 << (8 * p));
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            res.S[r][m] = S;
+            res.F[r][m] = 0.0f;
+        }
+}
+
+}  // namespace ut

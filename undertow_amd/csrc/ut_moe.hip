@@ -21,6 +21,7 @@
 // the row dimension rides along in the same instructions.
 #include "ut_gemv_core.h"
 #include "ut_moe.h"
+#include "ut_gemv_mfma.h"
 #include "ut_rowdig.h"
 
 
@@ -831,6 +832,54 @@ __device__ __forceinline__ void down_body(const DownArgs &a, int u, int tile, ui
         }
 }
 
+// Down on the matrix cores (int4, 2..4 rows, the inter size staged whole:
+// I <= 2048, I % 128 == 0, no split): each wave 16 rows, the workgroup 64;
+// the same totals and epilogue as down_body.
+template <int M> constexpr int down_mfma_depth() { return 8; }
+constexpr int kDownMfmaKC = 2048;
+inline bool down_mfma_ok(int fmt, int M, int64_t I, int ks) {
+    return fmt == UT_FMT_INT4 && M >= 2 && M <= 4 && ks == 1 && I <= kDownMfmaKC &&
+           I % kMfmaStepCols == 0;
+}
+
+template <int M>
+__global__ __launch_bounds__(kGemvThreads) void k_moe_down_mfma(DownArgs a) {
+    __shared__ __attribute__((aligned(16))) uint32_t lds[mfma_lds_words<M, kDownMfmaKC>()];
+    __shared__ uint32_t red[4 * M];
+    const int u = blockIdx.y;
+    if (u >= *a.count) return;
+    const uint8_t *dw = (const uint8_t *)a.sp[u * 6 + kSpDown];
+    const float *dsc = (const float *)a.sp[u * 6 + kSpDownS];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
+    const int64_t wrow0 = (int64_t)blockIdx.x * 64 + wave * 16;
+    const int64_t ar = wrow0 + s < a.H ? wrow0 + s : a.H - 1;
+    ut_u32x4 pv[M];
+    rowmax_load<M>(a.hmax_parts + (int64_t)u * M * a.nparts, a.nparts, pv);
+    int32_t exl[M];
+    auto prep = [&](int32_t (&shl)[4]) {
+        int32_t sh[M];
+        rowmax_reduce<M>(pv, sh, red);
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            shl[m] = sh[m];
+            exl[m] = sh[m] == INT32_MIN ? INT32_MIN : -sh[m];
+        }
+    };
+    CoreOut<UT_FMT_INT4, M, 4> res;
+    mfma_gemv_i4_f32x<M, down_mfma_depth<M>(), kDownMfmaKC>(
+        dw + ar * a.row_bytes, a.I, a.x.xf + u * a.x_slot_stride, a.x.ldx, (uint8_t *)lds, res,
+        prep);
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            const int64_t o = wrow0 + 4 * g + r;
+            if (s == 4 * r + m && o < a.H)
+                a.d[((int64_t)u * M + m) * a.H + o] =
+                    core_value<UT_FMT_INT4, M, 4>(res, r, m, exl, dsc, o);
+        }
+}
+
 template <int FMT, int M>
 __global__ __launch_bounds__(kGemvThreads) void k_moe_down(DownArgs a) {
     __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
@@ -1076,6 +1125,13 @@ template <int FA, int M>
 static void launch_down(ut_ctx *ctx, const DownArgs &a, int64_t slots, const DownArgs *b, int fb) {
     constexpr int DR = 16 * down_rows<M>();
     const unsigned gx = (unsigned)((a.H + DR - 1) / DR);
+    if constexpr (FA == UT_FMT_INT4 && M >= 2 && M <= 4) {
+        if (!b && down_mfma_ok(FA, M, a.I, a.ks)) {
+            hipLaunchKernelGGL((k_moe_down_mfma<M>), dim3((unsigned)((a.H + 63) / 64), (unsigned)slots),
+                               dim3(kGemvThreads), 0, ctx->stream, a);
+            return;
+        }
+    }
     if (!b) {
         hipLaunchKernelGGL((k_moe_down<FA, M>), dim3(gx, (unsigned)slots, (unsigned)a.ks),
                            dim3(kGemvThreads), 0, ctx->stream, a);
