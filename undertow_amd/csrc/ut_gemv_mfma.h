@@ -166,4 +166,119 @@ __device__ __forceinline__ void mfma_gemv_i4_f32x(const uint8_t *arow, int64_t K
         }
 }
 
+// The same GEMV over a long K staged in chunks of KC columns (K % 512 ==
+// 0; every chunk but the last a multiple of 4 steps): f32 activations with
+// given shifts sh[m] (INT32_MIN: zero digits).  The next chunk's
+// activations load into registers while the current one computes, and the
+// weight loads run on across chunk boundaries (the barriers between
+// chunks wait for LDS only).
+template <int M, int KC>
+__device__ __forceinline__ void mfma_gemv_i4_chunks(const uint8_t *arow, int64_t K,
+                                                    const float *xf, int64_t ldx,
+                                                    const int32_t (&sh)[M], uint8_t *lds,
+                                                    CoreOut<UT_FMT_INT4, M, 4> &res) {
+    static_assert(M >= 1 && M <= 4, "three digit planes per row, 16 columns");
+    static_assert(KC % (4 * kMfmaStepCols) == 0, "chunks of whole step groups");
+    constexpr int DEPTH = 4;
+    constexpr int RB = mfma_row_bytes<KC>();
+    constexpr int NI = (M * (KC / 8) + kGemvThreads - 1) / kGemvThreads;
+    const int tid = threadIdx.x, lane = tid & 63, n = lane & 15, kg = lane >> 4;
+    const int nsteps = (int)(K / kMfmaStepCols);
+    const uint8_t *ap = arow + 16 * kg;
+    float4 xv[NI][2];
+    auto xload = [&](int64_t kc) {
+        const int kcn = (int)(K - kc < KC ? K - kc : KC), NG = kcn / 8, TOT = M * NG;
+#pragma unroll
+        for (int j = 0; j < NI; j++) {
+            const int i = tid + j * kGemvThreads, ic = i < TOT ? i : TOT - 1;
+            const int m = ic / NG, g = ic - m * NG;
+            const float *src = xf + m * ldx + kc + 8 * g;
+            xv[j][0] = ld_global<float4>(src);
+            xv[j][1] = ld_global<float4>(src + 4);
+        }
+    };
+    auto xstore = [&](int64_t kc) {
+        const int kcn = (int)(K - kc < KC ? K - kc : KC), NG = kcn / 8, TOT = M * NG;
+#pragma unroll
+        for (int j = 0; j < NI; j++) {
+            const int i = tid + j * kGemvThreads;
+            if (i < TOT) {
+                const int m = i / NG, g = i - m * NG;
+                const int32_t s = m == 0 ? sh[0] : m == 1 ? sh[M > 1 ? 1 : 0]
+                                : m == 2 ? sh[M > 2 ? 2 : 0] : sh[M > 3 ? 3 : 0];
+                const float ev[4] = {xv[j][0].x, xv[j][0].z, xv[j][1].x, xv[j][1].z};
+                const float od[4] = {xv[j][0].y, xv[j][0].w, xv[j][1].y, xv[j][1].w};
+                uint32_t we[3], wo[3];
+                digit_words<UT_FMT_INT8>(ev, 4, s, we);
+                digit_words<UT_FMT_INT8>(od, 4, s, wo);
+#pragma unroll
+                for (int p = 0; p < 3; p++)
+                    *(uint2 *)(lds + (3 * m + p) * RB + 8 * g) = make_uint2(we[p], wo[p]);
+            }
+        }
+    };
+    auto lds_barrier = []() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+    xload(0);
+    uint4 wq[DEPTH];
+#pragma unroll
+    for (int u = 0; u < DEPTH; u++) wq[u] = ld_weights(ap + 64 * u);
+    xstore(0);
+    lds_barrier();
+    const bool bn = n < 3 * M;
+    const uint8_t *bp = lds + (bn ? n : 0) * RB + 32 * kg;
+    ut_i32x4 acc = {0, 0, 0, 0};
+    int j0 = 0;  // global step of the chunk's first step
+    for (int64_t kc = 0; kc < K; kc += KC) {
+        const bool more = kc + KC < K;
+        if (more) xload(kc + KC);
+        const int csteps = (int)((K - kc < KC ? K - kc : KC) / kMfmaStepCols);
+        for (int t = 0; t < csteps; t += DEPTH) {
+#pragma unroll
+            for (int u = 0; u < DEPTH; u++) {
+                const uint4 w = wq[u];
+                const int jn = j0 + t + u + DEPTH;
+                wq[u] = ld_weights(ap + 64 * (jn < nsteps ? jn : nsteps - 1));
+                const uint32_t X = 0x88888888u;
+                const uint32_t a0 = w.x ^ X, a1 = w.y ^ X, a2 = w.z ^ X, a3 = w.w ^ X;
+                const ut_i32x4 A0 = {mfma_sext4(a0), mfma_sext4(a0 >> 4), mfma_sext4(a1),
+                                     mfma_sext4(a1 >> 4)};
+                const ut_i32x4 A1 = {mfma_sext4(a2), mfma_sext4(a2 >> 4), mfma_sext4(a3),
+                                     mfma_sext4(a3 >> 4)};
+                uint4 b0 = *(const uint4 *)(bp + kMfmaStepCols * (t + u));
+                uint4 b1 = *(const uint4 *)(bp + kMfmaStepCols * (t + u) + 16);
+                if (!bn) b0 = b1 = make_uint4(0u, 0u, 0u, 0u);
+                const ut_i32x4 B0 = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w};
+                const ut_i32x4 B1 = {(int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, acc, 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        j0 += csteps;
+        if (more) {
+            lds_barrier();  // every wave is done with this chunk
+            xstore(kc + KC);
+            lds_barrier();
+        }
+    }
+    const int r_me = n >> 2, m_me = n & 3;
+    int64_t S = 0;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+#pragma unroll
+        for (int p = 0; p < 3; p++) {
+            const int src = (lane & 48) | (3 * m_me + p);
+            const int v = __shfl(acc[q], src, 64);
+            if (q == r_me) S += (int64_t)v * (int64_t)(1 << (8 * p));
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            res.S[r][m] = S;
+            res.F[r][m] = 0.0f;
+        }
+}
+
 }  // namespace ut

@@ -508,6 +508,7 @@ struct GateUpArgs {
     int64_t H, I, row_bytes;  // gate/up are [I, H]
     XSrc x;                   // digits (or f32) of x, shared by all slots
     const int32_t *exps;
+    const float *mfma_xf = nullptr;  // k_moe_gate_up_mfma: x as f32 [M][H] (digitised by exps)
     float *h;                 // [slots][M][I]
     uint32_t *hmax_parts;     // [slots][M][ntiles] float bits
     int ntiles;
@@ -695,6 +696,69 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up(GateUpArgs a) {
     gate_up_body<FMT, M>(a, blockIdx.y, blockIdx.x, lds, wg_max);
 }
 
+// Gate/up on the matrix cores (int4, 2..4 rows, plan ready, H % 512 == 0):
+// each wave 8 h rows (A rows 0-7 the gate rows, 8-15 the up rows), the
+// workgroup 32 (two of the plain kernel's 16-row tiles: both partial-max
+// slots get the workgroup's maximum).  x is digitised while staged, by the
+// digitiser's exponents, into the same integers as its digit planes.
+template <int M> constexpr int gate_up_mfma_kc() { return M == 2 ? 4096 : 2048; }
+inline bool gate_up_mfma_ok(int fmt, int M, int64_t H) {
+    return fmt == UT_FMT_INT4 && M >= 2 && M <= 4 && H % 512 == 0;
+}
+
+template <int M>
+__global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up_mfma(GateUpArgs a) {
+    constexpr int KC = gate_up_mfma_kc<M>();
+    __shared__ __attribute__((aligned(16))) uint32_t lds[mfma_lds_words<M, KC>()];
+    __shared__ uint32_t wg_max[4];
+    const int u = blockIdx.y, tile = blockIdx.x;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
+    const int cnt = *a.count;
+    const uint8_t *gw = (const uint8_t *)a.sp[u * 6 + kSpGate];
+    const uint8_t *uw = (const uint8_t *)a.sp[u * 6 + kSpUp];
+    const float *gsc = (const float *)a.sp[u * 6 + kSpGateS];
+    const float *usc = (const float *)a.sp[u * 6 + kSpUpS];
+    if (u >= cnt) return;
+    if (tid < 4) wg_max[tid] = 0;
+    const int64_t o0 = (int64_t)tile * 32 + wave * 8;
+    const int ai = s & 7;  // this lane's A row: gate (s < 8) or up row o0 + ai
+    const int64_t ao = o0 + ai < a.I ? o0 + ai : a.I - 1;
+    const uint8_t *arow = (s < 8 ? gw : uw) + ao * a.row_bytes;
+    int32_t exl[M], sh[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+        exl[m] = a.exps[m];
+        sh[m] = exl[m] == INT32_MIN ? INT32_MIN : -exl[m];
+    }
+    CoreOut<UT_FMT_INT4, M, 4> res;
+    mfma_gemv_i4_chunks<M, KC>(arow, a.H, a.mfma_xf, a.H, sh, (uint8_t *)lds, res);
+    // lanes 0-31 hold the gate totals of rows 4g + r (g < 2), lanes 32-63
+    // the up totals of the same rows
+    const int64_t S = res.S[0][0];
+    const int lo = (int)(uint32_t)S, hi = (int)(uint32_t)((uint64_t)S >> 32);
+    const int ulo = __shfl(lo, lane + 32 < 64 ? lane + 32 : lane, 64);
+    const int uhi = __shfl(hi, lane + 32 < 64 ? lane + 32 : lane, 64);
+    const int r = s >> 2, m = s & 3;
+    const int64_t o = o0 + 4 * g + r;
+    if (g < 2 && m < M && o < a.I) {
+        const int32_t e = m == 0 ? exl[0] : m == 1 ? exl[M > 1 ? 1 : 0]
+                        : m == 2 ? exl[M > 2 ? 2 : 0] : exl[M > 3 ? 3 : 0];
+        const int64_t US = (int64_t)(((uint64_t)(uint32_t)uhi << 32) | (uint32_t)ulo);
+        const float gv = int_total_to_f32(S, e, ld_global_f32(gsc + o));
+        const float uv = int_total_to_f32(US, e, ld_global_f32(usc + o));
+        // silu(g) * u (undertow-quant/src/lib.rs:121; model.rs:241-247)
+        const float sg = gv / (1.0f + expf(-gv));
+        const float hv = __fmul_rn(sg, uv);
+        a.h[((int64_t)u * M + m) * a.I + o] = hv;
+        atomicMax(&wg_max[m], __float_as_uint(fabsf(hv)));
+    }
+    __syncthreads();
+    if (tid < 2 * M) {
+        const int mm = tid >> 1, part = 2 * tile + (tid & 1);
+        if (part < a.ntiles) a.hmax_parts[((int64_t)u * M + mm) * a.ntiles + part] = wg_max[mm];
+    }
+}
+
 // Routed experts (format FA, slots 0..gridDim.y-2) and one shared MLP
 // (format FB, the last grid row) in one launch.
 template <int FA, int FB, int M>
@@ -835,11 +899,18 @@ __device__ __forceinline__ void down_body(const DownArgs &a, int u, int tile, ui
 // Down on the matrix cores (int4, 2..4 rows, the inter size staged whole:
 // I <= 2048, I % 128 == 0, no split): each wave 16 rows, the workgroup 64;
 // the same totals and epilogue as down_body.
-template <int M> constexpr int down_mfma_depth() { return 8; }
+// UT_DOWN_MFMA_MIN_M: the fewest rows that take it (experiments).
+#ifndef UT_DOWN_MFMA_MIN_M
+#define UT_DOWN_MFMA_MIN_M 2
+#endif
+#ifndef UT_DOWN_MFMA_DEPTH
+#define UT_DOWN_MFMA_DEPTH 4
+#endif
+template <int M> constexpr int down_mfma_depth() { return UT_DOWN_MFMA_DEPTH; }
 constexpr int kDownMfmaKC = 2048;
 inline bool down_mfma_ok(int fmt, int M, int64_t I, int ks) {
-    return fmt == UT_FMT_INT4 && M >= 2 && M <= 4 && ks == 1 && I <= kDownMfmaKC &&
-           I % kMfmaStepCols == 0;
+    return fmt == UT_FMT_INT4 && M >= UT_DOWN_MFMA_MIN_M && M <= 4 && ks == 1 &&
+           I <= kDownMfmaKC && I % kMfmaStepCols == 0;
 }
 
 template <int M>
@@ -1107,6 +1178,14 @@ ScratchLayout moe_layout(int64_t M, int64_t k, int64_t slots, int64_t H, int64_t
 template <int FA, int M>
 static void launch_gate_up(ut_ctx *ctx, const GateUpArgs &a, int64_t slots, const GateUpArgs *b,
                            int fb) {
+    if constexpr (FA == UT_FMT_INT4 && M >= 2 && M <= 4) {
+        if (!b && a.mfma_xf) {
+            hipLaunchKernelGGL((k_moe_gate_up_mfma<M>),
+                               dim3((unsigned)((a.I + 31) / 32), (unsigned)slots),
+                               dim3(kGemvThreads), 0, ctx->stream, a);
+            return;
+        }
+    }
     if (!b) {
         hipLaunchKernelGGL((k_moe_gate_up<FA, M>), dim3((unsigned)a.ntiles, (unsigned)slots),
                            dim3(kGemvThreads), 0, ctx->stream, a);
@@ -1125,7 +1204,7 @@ template <int FA, int M>
 static void launch_down(ut_ctx *ctx, const DownArgs &a, int64_t slots, const DownArgs *b, int fb) {
     constexpr int DR = 16 * down_rows<M>();
     const unsigned gx = (unsigned)((a.H + DR - 1) / DR);
-    if constexpr (FA == UT_FMT_INT4 && M >= 2 && M <= 4) {
+    if constexpr (FA == UT_FMT_INT4 && M >= UT_DOWN_MFMA_MIN_M && M <= 4) {
         if (!b && down_mfma_ok(FA, M, a.I, a.ks)) {
             hipLaunchKernelGGL((k_moe_down_mfma<M>), dim3((unsigned)((a.H + 63) / 64), (unsigned)slots),
                                dim3(kGemvThreads), 0, ctx->stream, a);
@@ -1228,6 +1307,11 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
         a.row_bytes = payload_bytes(FMT, 1, c.H);
         a.x = xs;
         a.exps = xexps;
+        // x digitised in this pass from c.x (so c.x is what the digits
+        // hold): the matrix-core kernel stages c.x itself
+        if (gate_up_mfma_ok(FMT, M, c.H) && !c.x_digits && !gate_plans_here && !c.shared &&
+            xs.dig && xexps && L.ntiles == (c.I + kGateUpRowsPerWG - 1) / kGateUpRowsPerWG)
+            a.mfma_xf = c.x;
         a.h = h;
         a.hmax_parts = hmax;
         a.ntiles = (int)L.ntiles;
