@@ -96,6 +96,18 @@ def test_c1_mla_shape_logits_and_stream(c1_mla):
     assert m.generate_greedy(prompt, 16) == om.greedy_decode(prompt, 16)[16:]
 
 
+@pytest.mark.parametrize("depth", [1, 2, 3])
+def test_c1_mla_mtp_verify_rows(c1_mla, depth):
+    """Verify steps of 2, 3 and 4 rows at hidden 1024 (the matrix-core
+    expert kernels take 3 and 4 rows, beside the shared expert's own
+    launches): the MTP stream equals greedy decode and the oracle's."""
+    ck, m, om = c1_mla
+    prompt = prompt_ids(16, C1_MLA["vocab_size"])
+    toks, drafted, accepted = m.generate_mtp(prompt, 16, depth=depth)
+    assert toks == m.generate_greedy(prompt, 16) == om.greedy_decode(prompt, 16)[16:]
+    assert drafted > 0 and 0 <= accepted <= drafted
+
+
 @pytest.fixture(scope="module")
 def c1_e256(ctx):
     ck = checkpoint(C1_E256, fmt="int4")

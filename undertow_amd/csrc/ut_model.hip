@@ -488,8 +488,11 @@ int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
         // with the logits whole and few choices the expert launch routes and
         // builds the slot plan itself (moe_pass); else route + plan in one
         // launch here
+        // (three or more rows with int4 experts go to the matrix-core expert
+        // kernels, which take the plan ready-made)
+        const bool mfma_rows = M >= 3 && gate_up_mfma_ok(L.expert_fmt, M, H);
         const bool gate_plans = gparts.ks <= 1 && (int64_t)M * k <= 64 &&
-                                L.expert_fmt != UT_FMT_F32;
+                                L.expert_fmt != UT_FMT_F32 && !mfma_rows;
         if (!gate_plans)
             UT_TRY(launch_route_plan(m->ctx, s->ws.rlogits, &gparts, L.bias, M, E, k,
                                      (int)c.n_group, (int)c.topk_group, c.norm_topk_prob,
@@ -509,6 +512,7 @@ int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
         mc.x = x + s0 * H;
         XDigits xr = xdigits_rows(xd, s0);
         if (L.expert_fmt != UT_FMT_F32) mc.x_digits = &xr;
+        mc.x_matches_digits = true;  // xd digitised exactly these rows of x
         mc.out = out + s0 * H;
         mc.ldo = H;
         mc.accumulate = accumulate;

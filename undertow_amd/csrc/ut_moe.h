@@ -60,6 +60,9 @@ struct MoeCall {
     int extra_slot = -1;  // >= 0: expert id always appended as the last slot, added with weight 1
     int32_t *err_flag = nullptr;
     bool plan_ready = false;  // the slot plan is already in the scratch (launch_route_plan)
+    // x (f32) holds exactly the values x_digits were made from (the
+    // matrix-core expert kernels then stage x themselves)
+    bool x_matches_digits = false;
     const MoePlan *plan = nullptr;  // a fixed plan elsewhere (one-slot MLPs)
     const float *init = nullptr;    // combine starts from init[M, ldo] instead of zero
     // Optional one-slot MLP (a shared expert, format int4 or int8 like the
@@ -84,6 +87,11 @@ struct MoeCall {
     float *route_w = nullptr;
 };
 bool moe_combine_norm_ok(int64_t H);
+// Whether the matrix-core gate/up takes an expert pass of M rows (int4,
+// 2..4 rows, hidden a multiple of 512).
+inline bool gate_up_mfma_ok(int fmt, int M, int64_t H) {
+    return fmt == UT_FMT_INT4 && M >= 2 && M <= 4 && H % 512 == 0;
+}
 
 struct ScratchLayout {
     size_t total = 0;

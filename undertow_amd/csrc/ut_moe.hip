@@ -702,9 +702,6 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up(GateUpArgs a) {
 // slots get the workgroup's maximum).  x is digitised while staged, by the
 // digitiser's exponents, into the same integers as its digit planes.
 template <int M> constexpr int gate_up_mfma_kc() { return M == 2 ? 4096 : 2048; }
-inline bool gate_up_mfma_ok(int fmt, int M, int64_t H) {
-    return fmt == UT_FMT_INT4 && M >= 2 && M <= 4 && H % 512 == 0;
-}
 
 template <int M>
 __global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up_mfma(GateUpArgs a) {
@@ -1179,10 +1176,19 @@ template <int FA, int M>
 static void launch_gate_up(ut_ctx *ctx, const GateUpArgs &a, int64_t slots, const GateUpArgs *b,
                            int fb) {
     if constexpr (FA == UT_FMT_INT4 && M >= 2 && M <= 4) {
-        if (!b && a.mfma_xf) {
+        if (a.mfma_xf) {
             hipLaunchKernelGGL((k_moe_gate_up_mfma<M>),
                                dim3((unsigned)((a.I + 31) / 32), (unsigned)slots),
                                dim3(kGemvThreads), 0, ctx->stream, a);
+            // a shared MLP beside it: its own launch
+            if (b) {
+                if (fb == UT_FMT_INT4)
+                    hipLaunchKernelGGL((k_moe_gate_up<UT_FMT_INT4, M>), dim3((unsigned)b->ntiles, 1u),
+                                       dim3(kGemvThreads), 0, ctx->stream, *b);
+                else
+                    hipLaunchKernelGGL((k_moe_gate_up<UT_FMT_INT8, M>), dim3((unsigned)b->ntiles, 1u),
+                                       dim3(kGemvThreads), 0, ctx->stream, *b);
+            }
             return;
         }
     }
@@ -1205,9 +1211,18 @@ static void launch_down(ut_ctx *ctx, const DownArgs &a, int64_t slots, const Dow
     constexpr int DR = 16 * down_rows<M>();
     const unsigned gx = (unsigned)((a.H + DR - 1) / DR);
     if constexpr (FA == UT_FMT_INT4 && M >= UT_DOWN_MFMA_MIN_M && M <= 4) {
-        if (!b && down_mfma_ok(FA, M, a.I, a.ks)) {
+        if ((!b || M >= 3) && down_mfma_ok(FA, M, a.I, a.ks)) {
             hipLaunchKernelGGL((k_moe_down_mfma<M>), dim3((unsigned)((a.H + 63) / 64), (unsigned)slots),
                                dim3(kGemvThreads), 0, ctx->stream, a);
+            // a shared MLP beside it (one slot, no split): its own launch
+            if (b) {
+                constexpr int DRB = 16 * down_rows<M>();
+                const dim3 gb((unsigned)((b->H + DRB - 1) / DRB), 1u, 1u);
+                if (fb == UT_FMT_INT4)
+                    hipLaunchKernelGGL((k_moe_down<UT_FMT_INT4, M>), gb, dim3(kGemvThreads), 0, ctx->stream, *b);
+                else
+                    hipLaunchKernelGGL((k_moe_down<UT_FMT_INT8, M>), gb, dim3(kGemvThreads), 0, ctx->stream, *b);
+            }
             return;
         }
     }
@@ -1242,8 +1257,15 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
     // (gate_plan); with x not digitised, one row and x staged whole, they
     // digitise x too (self_plan, x as f32)
     constexpr int64_t KC = gemv_chunk_cols<FMT, M>();
+    // the matrix-core gate/up (int4, 2..4 rows): x as f32 with the
+    // digitiser's exponents, the slot plan made before the launch; beside a
+    // shared expert from three rows on (at two the fused routed + shared
+    // launch of the dot-product kernels is faster)
+    const bool use_mfma = gate_up_mfma_ok(FMT, M, c.H) && c.extra_slot < 0 &&
+                          (!c.x_digits || c.x_matches_digits) && (!c.shared || M >= 3) &&
+                          L.ntiles == (c.I + kGateUpRowsPerWG - 1) / kGateUpRowsPerWG;
     const bool gate_plan = FMT != UT_FMT_F32 && need_plan && c.extra_slot < 0 &&
-                           (int64_t)M * c.k <= 64;
+                           (int64_t)M * c.k <= 64 && !use_mfma;
     const bool self_plan = gate_plan && !c.x_digits && !c.shared && c.H <= KC &&
                            c.H % FmtTraits<FMT>::kStepCols == 0 && M == 1;
     const bool gate_plans_here = gate_plan && (self_plan || c.x_digits);
@@ -1309,9 +1331,7 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
         a.exps = xexps;
         // x digitised in this pass from c.x (so c.x is what the digits
         // hold): the matrix-core kernel stages c.x itself
-        if (gate_up_mfma_ok(FMT, M, c.H) && !c.x_digits && !gate_plans_here && !c.shared &&
-            xs.dig && xexps && L.ntiles == (c.I + kGateUpRowsPerWG - 1) / kGateUpRowsPerWG)
-            a.mfma_xf = c.x;
+        if (use_mfma && xs.dig && xexps) a.mfma_xf = c.x;
         a.h = h;
         a.hmax_parts = hmax;
         a.ntiles = (int)L.ntiles;
