@@ -15,6 +15,9 @@
 //                  route the row and digitise x while staging it
 //   k_moe_down     grid (H/32, slots): d = down(h) per (slot, row),
 //                  h digitised while it is staged (exponent from the partials)
+//   k_moe_gate_up_mfma / k_moe_down_mfma  the same two stages on the
+//                  matrix cores for int4 experts at 2..4 rows (ut_gemv_mfma.h),
+//                  bit-identical results
 //   k_moe_combine4 out[s] = sum_c w[s,c]*d[slot(s,c), s] in router order
 //                  (k_moe_combine_norm: also the next rmsnorm + digits)
 // Every expert's weights are read once per pass whatever rows chose it;
