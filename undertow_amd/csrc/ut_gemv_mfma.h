@@ -92,60 +92,12 @@ __device__ __forceinline__ void mfma_stage_f32(const float *xf, int64_t ldx, int
     __syncthreads();
 }
 
-// One wave: 16 rows x M activation rows over the columns [0, K) staged
-// whole (K <= KC, K % 128 == 0).  arow: this lane's A row (row lane & 15
-// of the wave's 16, clamped to a valid row).  DEPTH steps of weights in
-// flight.  The total for (wave row 4g + r, activation row m) lands in
-// res.S[r][m] of sub-lane 4r + m of lane group g (the dot-product core's
-// convention with 4 rows per lane).
-template <int M, int DEPTH, int KC, typename Prep>
-__device__ __forceinline__ void mfma_gemv_i4_f32x(const uint8_t *arow, int64_t K, const float *xf,
-                                                  int64_t ldx, uint8_t *lds,
-                                                  CoreOut<UT_FMT_INT4, M, 4> &res, Prep &&prep) {
-    static_assert(M >= 1 && M <= 4, "three digit planes per row, 16 columns");
-    constexpr int RB = mfma_row_bytes<KC>();
-    const int lane = threadIdx.x & 63, n = lane & 15, kg = lane >> 4;
-    const int nsteps = (int)(K / kMfmaStepCols);
-    const uint8_t *ap = arow + 16 * kg;  // step j: bytes [64j + 16kg, +16)
-    uint4 wq[DEPTH];
-    mfma_stage_f32<M, KC>(xf, ldx, 0, (int)K, lds, [&]() {
-#pragma unroll
-        for (int u = 0; u < DEPTH; u++) wq[u] = ld_weights(ap + 64 * (u < nsteps ? u : nsteps - 1));
-    }, prep);
-    const bool bn = n < 3 * M;
-    const uint8_t *bp = lds + (bn ? n : 0) * RB + 32 * kg;
-    ut_i32x4 acc = {0, 0, 0, 0};
-    auto step = [&](const uint4 &w, int j) {
-        const uint32_t X = 0x88888888u;
-        const uint32_t a0 = w.x ^ X, a1 = w.y ^ X, a2 = w.z ^ X, a3 = w.w ^ X;
-        const ut_i32x4 A0 = {mfma_sext4(a0), mfma_sext4(a0 >> 4), mfma_sext4(a1), mfma_sext4(a1 >> 4)};
-        const ut_i32x4 A1 = {mfma_sext4(a2), mfma_sext4(a2 >> 4), mfma_sext4(a3), mfma_sext4(a3 >> 4)};
-        uint4 b0 = *(const uint4 *)(bp + kMfmaStepCols * j);
-        uint4 b1 = *(const uint4 *)(bp + kMfmaStepCols * j + 16);
-        if (!bn) b0 = b1 = make_uint4(0u, 0u, 0u, 0u);
-        const ut_i32x4 B0 = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w};
-        const ut_i32x4 B1 = {(int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
-        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, acc, 0, 0, 0);
-    };
-    int t = 0;
-    for (; t + 2 * DEPTH <= nsteps; t += DEPTH) {
-#pragma unroll
-        for (int u = 0; u < DEPTH; u++) {
-            step(wq[u], t + u);
-            wq[u] = ld_weights(ap + 64 * (t + u + DEPTH));
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < 2 * DEPTH; i++) {
-        if (t + i < nsteps) {
-            step(wq[i % DEPTH], t + i);
-            if (t + i + DEPTH < nsteps) wq[i % DEPTH] = ld_weights(ap + 64 * (t + i + DEPTH));
-        }
-    }
-    // acc[q] = C[4kg + q][n]: sub-lane s = 4r + m of group kg collects
-    // row 4kg + r's planes 3m, 3m+1, 3m+2 from sub-lanes 3m + p
+// acc[q] = C[4kg + q][n] (lane group kg, sub-lane n): sub-lane s = 4r + m
+// of group kg collects row 4kg + r's planes 3m, 3m+1, 3m+2 from sub-lanes
+// 3m + p into res.S[r][m].
+template <int M>
+__device__ __forceinline__ void mfma_collect(const ut_i32x4 &acc, CoreOut<UT_FMT_INT4, M, 4> &res) {
+    const int lane = threadIdx.x & 63, n = lane & 15;
     const int r_me = n >> 2, m_me = n & 3;
     int64_t S = 0;
 #pragma unroll
@@ -164,6 +116,77 @@ __device__ __forceinline__ void mfma_gemv_i4_f32x(const uint8_t *arow, int64_t K
             res.S[r][m] = S;
             res.F[r][m] = 0.0f;
         }
+}
+
+// One wave: TW tiles of 16 rows (one A operand each, sharing the B
+// operand) x M activation rows over the columns [0, K) staged
+// whole (K <= KC, K % 128 == 0).  arow[w]: this lane's A row of tile w
+// (row lane & 15 of the tile's 16, clamped to a valid row).  DEPTH steps of weights in
+// flight.  The total for (wave row 4g + r, activation row m) lands in
+// res.S[r][m] of sub-lane 4r + m of lane group g (the dot-product core's
+// convention with 4 rows per lane).
+template <int M, int DEPTH, int KC, int TW, typename Prep>
+__device__ __forceinline__ void mfma_gemv_i4_f32x(const uint8_t *const (&arow)[TW], int64_t K,
+                                                  const float *xf, int64_t ldx, uint8_t *lds,
+                                                  CoreOut<UT_FMT_INT4, M, 4> (&res)[TW],
+                                                  Prep &&prep) {
+    static_assert(M >= 1 && M <= 4, "three digit planes per row, 16 columns");
+    constexpr int RB = mfma_row_bytes<KC>();
+    const int lane = threadIdx.x & 63, n = lane & 15, kg = lane >> 4;
+    const int nsteps = (int)(K / kMfmaStepCols);
+    const uint8_t *ap[TW];  // step j: bytes [64j + 16kg, +16)
+#pragma unroll
+    for (int w = 0; w < TW; w++) ap[w] = arow[w] + 16 * kg;
+    uint4 wq[DEPTH][TW];
+    mfma_stage_f32<M, KC>(xf, ldx, 0, (int)K, lds, [&]() {
+#pragma unroll
+        for (int u = 0; u < DEPTH; u++)
+#pragma unroll
+            for (int w = 0; w < TW; w++) wq[u][w] = ld_weights(ap[w] + 64 * (u < nsteps ? u : nsteps - 1));
+    }, prep);
+    const bool bn = n < 3 * M;
+    const uint8_t *bp = lds + (bn ? n : 0) * RB + 32 * kg;
+    ut_i32x4 acc[TW];
+#pragma unroll
+    for (int w = 0; w < TW; w++) acc[w] = ut_i32x4{0, 0, 0, 0};
+    auto step = [&](const uint4 (&wv)[TW], int j) {
+        uint4 b0 = *(const uint4 *)(bp + kMfmaStepCols * j);
+        uint4 b1 = *(const uint4 *)(bp + kMfmaStepCols * j + 16);
+        if (!bn) b0 = b1 = make_uint4(0u, 0u, 0u, 0u);
+        const ut_i32x4 B0 = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w};
+        const ut_i32x4 B1 = {(int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+#pragma unroll
+        for (int w = 0; w < TW; w++) {
+            const uint32_t X = 0x88888888u;
+            const uint32_t a0 = wv[w].x ^ X, a1 = wv[w].y ^ X, a2 = wv[w].z ^ X, a3 = wv[w].w ^ X;
+            const ut_i32x4 A0 = {mfma_sext4(a0), mfma_sext4(a0 >> 4), mfma_sext4(a1), mfma_sext4(a1 >> 4)};
+            const ut_i32x4 A1 = {mfma_sext4(a2), mfma_sext4(a2 >> 4), mfma_sext4(a3), mfma_sext4(a3 >> 4)};
+            acc[w] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, acc[w], 0, 0, 0);
+            acc[w] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, acc[w], 0, 0, 0);
+        }
+    };
+    auto load = [&](uint4 (&wv)[TW], int j) {
+#pragma unroll
+        for (int w = 0; w < TW; w++) wv[w] = ld_weights(ap[w] + 64 * j);
+    };
+    int t = 0;
+    for (; t + 2 * DEPTH <= nsteps; t += DEPTH) {
+#pragma unroll
+        for (int u = 0; u < DEPTH; u++) {
+            step(wq[u], t + u);
+            load(wq[u], t + u + DEPTH);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 2 * DEPTH; i++) {
+        if (t + i < nsteps) {
+            step(wq[i % DEPTH], t + i);
+            if (t + i + DEPTH < nsteps) load(wq[i % DEPTH], t + i + DEPTH);
+        }
+    }
+#pragma unroll
+    for (int w = 0; w < TW; w++) mfma_collect<M>(acc[w], res[w]);
 }
 
 // The same GEMV over a long K staged in chunks of KC columns (K % 512 ==

@@ -897,7 +897,8 @@ __device__ __forceinline__ void down_body(const DownArgs &a, int u, int tile, ui
 }
 
 // Down on the matrix cores (int4, 2..4 rows, the inter size staged whole:
-// I <= 2048, I % 128 == 0, no split): each wave 16 rows, the workgroup 64;
+// I <= 2048, I % 128 == 0, no split): each wave TW x 16 rows, the
+// workgroup 64 TW;
 // the same totals and epilogue as down_body.
 // UT_DOWN_MFMA_MIN_M: the fewest rows that take it (experiments).
 #ifndef UT_DOWN_MFMA_MIN_M
@@ -907,6 +908,13 @@ __device__ __forceinline__ void down_body(const DownArgs &a, int u, int tile, ui
 #define UT_DOWN_MFMA_DEPTH 4
 #endif
 template <int M> constexpr int down_mfma_depth() { return UT_DOWN_MFMA_DEPTH; }
+// 16-row tiles per wave (one staged h for TW x 16 rows): two from three
+// rows on (C2 down at four rows 69.3 -> 67.0 us), one at two rows (two
+// measured 29.2 -> 32.7 us there)
+#ifndef UT_DOWN_MFMA_TW
+#define UT_DOWN_MFMA_TW (M >= 3 ? 2 : 1)
+#endif
+template <int M> constexpr int down_mfma_tw() { return UT_DOWN_MFMA_TW; }
 constexpr int kDownMfmaKC = 2048;
 inline bool down_mfma_ok(int fmt, int M, int64_t I, int ks) {
     return fmt == UT_FMT_INT4 && M >= UT_DOWN_MFMA_MIN_M && M <= 4 && ks == 1 &&
@@ -922,8 +930,14 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_down_mfma(DownArgs a) {
     const uint8_t *dw = (const uint8_t *)a.sp[u * 6 + kSpDown];
     const float *dsc = (const float *)a.sp[u * 6 + kSpDownS];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
-    const int64_t wrow0 = (int64_t)blockIdx.x * 64 + wave * 16;
-    const int64_t ar = wrow0 + s < a.H ? wrow0 + s : a.H - 1;
+    constexpr int TW = down_mfma_tw<M>();
+    const int64_t wrow0 = (int64_t)blockIdx.x * (64 * TW) + wave * (16 * TW);
+    const uint8_t *arow[TW];
+#pragma unroll
+    for (int w = 0; w < TW; w++) {
+        const int64_t ar = wrow0 + 16 * w + s < a.H ? wrow0 + 16 * w + s : a.H - 1;
+        arow[w] = dw + ar * a.row_bytes;
+    }
     ut_u32x4 pv[M];
     rowmax_load<M>(a.hmax_parts + (int64_t)u * M * a.nparts, a.nparts, pv);
     int32_t exl[M];
@@ -936,19 +950,20 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_down_mfma(DownArgs a) {
             exl[m] = sh[m] == INT32_MIN ? INT32_MIN : -sh[m];
         }
     };
-    CoreOut<UT_FMT_INT4, M, 4> res;
-    mfma_gemv_i4_f32x<M, down_mfma_depth<M>(), kDownMfmaKC>(
-        dw + ar * a.row_bytes, a.I, a.x.xf + u * a.x_slot_stride, a.x.ldx, (uint8_t *)lds, res,
-        prep);
+    CoreOut<UT_FMT_INT4, M, 4> res[TW];
+    mfma_gemv_i4_f32x<M, down_mfma_depth<M>(), kDownMfmaKC, TW>(
+        arow, a.I, a.x.xf + u * a.x_slot_stride, a.x.ldx, (uint8_t *)lds, res, prep);
 #pragma unroll
-    for (int r = 0; r < 4; r++)
+    for (int w = 0; w < TW; w++)
 #pragma unroll
-        for (int m = 0; m < M; m++) {
-            const int64_t o = wrow0 + 4 * g + r;
-            if (s == 4 * r + m && o < a.H)
-                a.d[((int64_t)u * M + m) * a.H + o] =
-                    core_value<UT_FMT_INT4, M, 4>(res, r, m, exl, dsc, o);
-        }
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                const int64_t o = wrow0 + 16 * w + 4 * g + r;
+                if (s == 4 * r + m && o < a.H)
+                    a.d[((int64_t)u * M + m) * a.H + o] =
+                        core_value<UT_FMT_INT4, M, 4>(res[w], r, m, exl, dsc, o);
+            }
 }
 
 template <int FMT, int M>
@@ -1215,7 +1230,8 @@ static void launch_down(ut_ctx *ctx, const DownArgs &a, int64_t slots, const Dow
     const unsigned gx = (unsigned)((a.H + DR - 1) / DR);
     if constexpr (FA == UT_FMT_INT4 && M >= UT_DOWN_MFMA_MIN_M && M <= 4) {
         if ((!b || M >= 3) && down_mfma_ok(FA, M, a.I, a.ks)) {
-            hipLaunchKernelGGL((k_moe_down_mfma<M>), dim3((unsigned)((a.H + 63) / 64), (unsigned)slots),
+            constexpr int WR = 64 * down_mfma_tw<M>();
+            hipLaunchKernelGGL((k_moe_down_mfma<M>), dim3((unsigned)((a.H + WR - 1) / WR), (unsigned)slots),
                                dim3(kGemvThreads), 0, ctx->stream, a);
             // a shared MLP beside it (one slot, no split): its own launch
             if (b) {
