@@ -333,6 +333,45 @@ def committed_traffic() -> float | None:
     return float(m.group(1)) if m else None
 
 
+def profile_decode(cfg_name: str, prompt_len: int, tokens: int, seed: int = 42) -> None:
+    """Decode-step driver for kernel traces (run it under rocprofv3): the
+    synthetic model on device, a uniform-random prompt, then `tokens`
+    one-row decode steps and `tokens // 2` two-row verify steps (the MTP
+    verify width at depth 1), the phases separated by an idle second so a
+    kernel trace splits cleanly at the gaps.  Prints the host-timed ms per
+    step of each phase."""
+    import torch
+    import undertow_amd as U
+    from undertow_amd.configs import C1, C4
+
+    cfg = {"c1": C1, "c4": C4}[cfg_name]
+    ctx = U.Context(0)
+    m = U.Model(ctx, cfg)
+    m.synthesize(seed, 0.02, U.INT4, U.INT8)
+    rng = np.random.default_rng(1)
+    prompt = rng.integers(0, cfg["vocab_size"], prompt_len).tolist()
+    s = m.session()
+    s.prefill(prompt, want_logits=False)
+    nxt = s.last_argmax[-1]
+    torch.cuda.synchronize()
+    time.sleep(1.0)
+    t0 = time.perf_counter()
+    for _ in range(tokens):
+        s.prefill([nxt], want_logits=False)
+        nxt = s.last_argmax[-1]
+    t1 = time.perf_counter()
+    print(f"decode {tokens} tokens: {(t1 - t0) / tokens * 1e3:.3f} ms/token", flush=True)
+    torch.cuda.synchronize()
+    time.sleep(1.0)
+    n = max(tokens // 2, 1)
+    t0 = time.perf_counter()
+    for _ in range(n):
+        s.prefill([nxt, nxt], want_logits=False)
+        nxt = s.last_argmax[-1]
+    t1 = time.perf_counter()
+    print(f"verify (2 rows) {n} steps: {(t1 - t0) / n * 1e3:.3f} ms/step", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -347,11 +386,19 @@ def main():
     ap.add_argument("--no-mla", dest="mla", action="store_false")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 1 GiB device copy (counter scaling for rocprofv3 --pmc)")
+    ap.add_argument("--profile-decode", choices=["c1", "c4"], default=None,
+                    help="only run the decode-step driver for kernel traces (no JSON line)")
+    ap.add_argument("--prompt", type=int, default=512, help="prompt length for --profile-decode")
+    ap.add_argument("--tokens", type=int, default=32, help="decode steps for --profile-decode")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1"}))
+        print(json.dumps({"error": "this build measures one GPU only (every GPU box here has "
+                                   "one); run with --gpus 1"}))
         sys.exit(2)
+    if args.profile_decode:
+        profile_decode(args.profile_decode, args.prompt, args.tokens)
+        return
 
     import torch
     import undertow_amd as U

@@ -120,6 +120,13 @@ int32_t ut_qtensor_matmul(ut_ctx *ctx, const ut_qtensor *qt, float *out_dev, int
 /* QTensor::add_scaled_row (qtensor.rs:516-543): acc[i] += (factor*scale[row])*q[row,i]. */
 int32_t ut_qtensor_add_scaled_row(ut_ctx *ctx, const ut_qtensor *qt, int64_t row, float factor,
                                   float *acc_dev);
+/* QTensor::matvec_rows (qtensor.rs:548-586): out[j] = scale[row0+j] *
+ * sum_i x[i]*q[row0+j, i] for j in [0, nrows), x [in_dim] and out [nrows]
+ * f32 on the device.  x_len / out_len are element counts, checked like the
+ * reference's assert!s (UT_ERR_SHAPE, also when row0 + nrows > out_dim). */
+int32_t ut_qtensor_matvec_rows(ut_ctx *ctx, const ut_qtensor *qt, int64_t row0, int64_t nrows,
+                               const float *x_dev, int64_t x_len, float *out_dev,
+                               int64_t out_len);
 
 /* ---------------------------------------------------------------- router */
 /* RouterAdapter::route (undertow-core/src/adapter.rs:99-114) as
@@ -258,24 +265,64 @@ int32_t ut_session_prefill(ut_session *s, const int32_t *ids, int64_t n, float *
 int32_t ut_session_truncate(ut_session *s, int64_t len);
 int64_t ut_session_position(const ut_session *s);
 
+/* DeepseekMoeModel::stop_ids (adapters/undertow-deepseek-moe/src/
+ * loader.rs:304-309, model.rs:93): the checkpoint's stop tokens (config
+ * eos ids plus generation_config's), which every generation call below
+ * honours.  Empty until set. */
+int32_t ut_model_set_stop_ids(ut_model *m, const int32_t *ids, int64_t n);
+
+/* on_token of undertow_core::generate (undertow-core/src/model.rs:139-166)
+ * and of the speculative loops (mtp.rs:194-257, 263-314): called with each
+ * emitted token in order; return 0 to end the stream after it. */
+typedef int32_t (*ut_token_fn)(void *user, int32_t token);
+/* draft_fn of speculative_loop (mtp.rs:263-314): `tokens` are the
+ * session's consumed tokens [n_tokens] (prompt plus verified tokens), `next`
+ * the emitted token not consumed yet.  Writes `depth` draft ids (the
+ * reference drafts one); returns 0, or a negative status that ends the
+ * loop with that status. */
+typedef int32_t (*ut_draft_fn)(void *user, const int32_t *tokens, int64_t n_tokens, int32_t next,
+                               int32_t depth, int32_t *drafts);
+
 /* undertow_core::generate with a greedy sampler (undertow-core/src/
- * model.rs:139-185) on a fresh session: writes up to max_new tokens to
- * out, returns the count (< max_new when the context is full) or a
- * negative status. */
+ * model.rs:139-166; greedy_decode :168-185) on a fresh session: emits up to
+ * max_new tokens into out and to on_token (may be NULL), stopping after a
+ * stop token (the model's stop ids or extra_stop_ids, emitted and counted)
+ * or when on_token returns 0.  Returns the count (short of max_new also when
+ * the context is full) or a negative status. */
+int64_t ut_generate(ut_model *m, const int32_t *prompt, int64_t n, int64_t max_new,
+                    const int32_t *extra_stop_ids, int64_t n_extra, ut_token_fn on_token,
+                    void *user, int32_t *out);
+/* ut_generate without extra stop ids or callback. */
 int64_t ut_generate_greedy(ut_model *m, const int32_t *prompt, int64_t n, int64_t max_new,
                            int32_t *out);
-/* generate_greedy_mtp -> speculative_loop (adapters/undertow-deepseek-moe/
- * src/mtp.rs:176-191,263-314) with the native MTP head (draft_logits,
- * mtp.rs:74-133).  depth 1 is the reference: draft one token, verify
- * [next, draft] as a 2-row prefill, accept iff argmax(row 0) == draft.
- * depth 2..3 (no reference counterpart) chains the MTP module on its own
- * last hidden state, verifies depth+1 rows and accepts the longest matching
- * prefix; the main KV rolls back to the last verified position and the MTP
- * module is only fed verified positions, so the output always equals
- * ut_generate_greedy.  Returns the produced count; drafted / accepted
- * count draft tokens. */
+/* speculative_loop (adapters/undertow-deepseek-moe/src/mtp.rs:263-314) and
+ * generate_greedy_mtp (:176-191).  Drafts come from draft_fn, or from the
+ * native MTP head (draft_logits, mtp.rs:74-133) when draft_fn is NULL.
+ * depth 1 is the reference: draft one token, verify [next, draft] as a
+ * 2-row prefill, accept iff argmax(row 0) == draft, else roll the draft's
+ * KV position back.  depth 2..3 (no reference counterpart) drafts 2-3
+ * tokens (the native head chains the MTP module on its own last output
+ * row), verifies depth+1 rows and accepts the longest matching prefix; the
+ * main KV rolls back to the last verified position and the MTP module is
+ * only fed verified positions, so the output always equals ut_generate's.
+ * Stop ids, on_token and max_new end the stream as in ut_generate, also in
+ * the middle of an accepted run.  Returns the produced count; drafted /
+ * accepted count draft tokens (MtpStats). */
+int64_t ut_speculative_loop(ut_model *m, const int32_t *prompt, int64_t n, int64_t max_new,
+                            int32_t depth, const int32_t *extra_stop_ids, int64_t n_extra,
+                            ut_token_fn on_token, void *user, ut_draft_fn draft_fn,
+                            void *draft_user, int32_t *out, int64_t *drafted, int64_t *accepted);
+/* ut_speculative_loop with the native MTP head, no extra stop ids or callback. */
 int64_t ut_generate_mtp(ut_model *m, const int32_t *prompt, int64_t n, int64_t max_new,
                         int32_t depth, int32_t *out, int64_t *drafted, int64_t *accepted);
+/* draft_logits (mtp.rs:74-133) on the session's MTP state: feeds the
+ * positions not yet fed to the MTP layer (t_next = the following consumed
+ * token, next_token for the last) and writes the head's logits [vocab] for
+ * the last one (logits_host may be NULL) and their argmax (draft_host may
+ * be NULL).  UT_ERR_STATE when the model has no MTP head or nothing is
+ * pending. */
+int32_t ut_session_draft_logits(ut_session *s, int32_t next_token, float *logits_host,
+                                int32_t *draft_host);
 
 #ifdef __cplusplus
 }

@@ -125,6 +125,25 @@ def lib():
         L.uto_generate_mtp.restype = C.c_int64
         L.uto_generate_mtp.argtypes = [C.c_void_p, _i32p, C.c_int64, C.c_int64, _i32p,
                                        C.POINTER(C.c_int64), C.POINTER(C.c_int64)]
+        L.uto_ckpt_new.restype = C.c_void_p
+        L.uto_ckpt_new.argtypes = []
+        L.uto_ckpt_add.argtypes = [C.c_void_p, C.c_char_p, C.c_int32, C.c_int32, C.c_int64,
+                                   C.c_int64, C.c_void_p, C.c_int64, C.c_void_p]
+        L.uto_ckpt_synthesize.restype = C.c_void_p
+        L.uto_ckpt_synthesize.argtypes = [C.POINTER(Spec), C.c_uint64, C.c_float, C.c_int, C.c_int]
+        L.uto_generate_greedy.restype = C.c_int64
+        L.uto_generate_greedy.argtypes = [C.c_void_p, _i32p, C.c_int64, C.c_int64, C.c_void_p,
+                                          C.c_int64, C.c_void_p, C.c_void_p, _i32p]
+        L.uto_speculative_loop.restype = C.c_int64
+        L.uto_speculative_loop.argtypes = [C.c_void_p, _i32p, C.c_int64, C.c_int64, C.c_int32,
+                                           C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p,
+                                           C.c_void_p, C.c_void_p, _i32p, C.POINTER(C.c_int64),
+                                           C.POINTER(C.c_int64)]
+        L.uto_mtp_state_new.restype = C.c_void_p
+        L.uto_mtp_state_new.argtypes = []
+        L.uto_mtp_state_free.argtypes = [C.c_void_p]
+        L.uto_draft_logits.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, _f32p,
+                                       C.c_void_p]
         _lib = L
     return _lib
 
@@ -298,12 +317,56 @@ def default_spec(**overrides) -> Spec:
     return s
 
 
+TOKEN_FN = C.CFUNCTYPE(C.c_int32, C.c_void_p, C.c_int32)
+DRAFT_FN = C.CFUNCTYPE(C.c_int32, C.c_void_p, C.POINTER(C.c_int32), C.c_int64, C.c_int32,
+                       C.c_int32, C.POINTER(C.c_int32))
+
+
 class Checkpoint:
     """A generated (optionally converted) checkpoint held by the C oracle."""
 
-    def __init__(self, spec: Spec):
+    def __init__(self, spec: Spec, _handle=None):
         self.spec = spec
-        self._h = lib().uto_generate(C.byref(spec))
+        self._h = _handle if _handle is not None else lib().uto_generate(C.byref(spec))
+
+    @classmethod
+    def synthesize(cls, spec: Spec, seed: int, std: float, expert_fmt: int,
+                   dense_fmt: int) -> "Checkpoint":
+        """Seeded weights at large widths in converted form (uto_ckpt_synthesize)."""
+        return cls(spec, lib().uto_ckpt_synthesize(C.byref(spec), seed, std, expert_fmt, dense_fmt))
+
+    @classmethod
+    def from_tensors(cls, spec: Spec, tensors) -> "Checkpoint":
+        """A checkpoint of (name, fmt, shape, payload, scales) tuples."""
+        L = lib()
+        h = L.uto_ckpt_new()
+        ck = cls(spec, h)
+        for name, fmt, shape, payload, scales in tensors:
+            payload = np.ascontiguousarray(payload)
+            sc = None if scales is None else np.ascontiguousarray(scales, np.float32)
+            d1 = shape[1] if len(shape) == 2 else 1
+            rc = L.uto_ckpt_add(h, name.encode(), fmt, len(shape), shape[0], d1,
+                                payload.ctypes.data, payload.nbytes,
+                                None if sc is None else sc.ctypes.data)
+            if rc != 0:
+                raise ValueError(f"uto_ckpt_add({name}) failed")
+        return ck
+
+    def raw_tensors(self):
+        """Yield (name, fmt, shape, payload address, nbytes, scales address|None)
+        without copying (valid while the checkpoint lives)."""
+        L = lib()
+        name = C.create_string_buffer(256)
+        fmt = C.c_int32()
+        shape = (C.c_int64 * 2)()
+        ndim = C.c_int32()
+        nb = C.c_int64()
+        for i in range(L.uto_ckpt_count(self._h)):
+            L.uto_ckpt_info(self._h, i, name, 256, C.byref(fmt), shape, C.byref(ndim))
+            p = L.uto_ckpt_payload(self._h, i, C.byref(nb))
+            shp = (shape[0], shape[1]) if ndim.value == 2 else (shape[0],)
+            sp = L.uto_ckpt_scales(self._h, i) if fmt.value != F32 else None
+            yield name.value.decode(), fmt.value, shp, p, nb.value, sp
 
     def __del__(self):
         if getattr(self, "_h", None):
@@ -361,11 +424,58 @@ class Model:
 
     def greedy_decode(self, prompt, max_new: int) -> list:
         p = np.asarray(prompt, np.int32)
-        out = np.zeros(max_new, np.int32)
+        out = np.zeros(max(max_new, 1), np.int32)
         n = lib().uto_greedy_decode(self._h, p, p.size, max_new, out)
         if n < 0:
             raise RuntimeError(f"greedy_decode error {n}")
         return list(prompt) + out[:n].tolist()
+
+    def generate(self, prompt, max_new: int, stop_ids=(), on_token=None) -> list:
+        """core::generate, greedy, with stop ids and on_token -> new tokens."""
+        p = np.asarray(prompt, np.int32)
+        out = np.zeros(max(max_new, 1), np.int32)
+        st = np.ascontiguousarray(stop_ids, np.int32)
+        cb = TOKEN_FN(lambda _u, t: int(bool(on_token(t)))) if on_token else None
+        n = lib().uto_generate_greedy(self._h, p, p.size, max_new,
+                                      st.ctypes.data if st.size else None, st.size,
+                                      C.cast(cb, C.c_void_p) if cb else None, None, out)
+        if n < 0:
+            raise RuntimeError(f"generate error {n}")
+        return out[:n].tolist()
+
+    def speculative_loop(self, prompt, max_new: int, depth: int = 1, draft_fn=None,
+                         stop_ids=(), on_token=None):
+        """speculative_loop (mtp.rs:263-314): draft_fn(tokens, next, depth)
+        -> `depth` ids, or None for the native MTP head.
+        Returns (tokens, drafted, accepted)."""
+        p = np.asarray(prompt, np.int32)
+        out = np.zeros(max(max_new, 1), np.int32)
+        st = np.ascontiguousarray(stop_ids, np.int32)
+        tcb = TOKEN_FN(lambda _u, t: int(bool(on_token(t)))) if on_token else None
+        err = []
+
+        def _draft(_u, toks, n, nxt, dep, dst):
+            try:
+                ids = list(draft_fn([toks[i] for i in range(n)], nxt, dep))
+                for i in range(dep):
+                    dst[i] = int(ids[i])
+                return 0
+            except Exception as e:
+                err.append(e)
+                return -6
+
+        dcb = DRAFT_FN(_draft) if draft_fn else None
+        d, a = C.c_int64(), C.c_int64()
+        n = lib().uto_speculative_loop(self._h, p, p.size, max_new, depth,
+                                       st.ctypes.data if st.size else None, st.size,
+                                       C.cast(tcb, C.c_void_p) if tcb else None, None,
+                                       C.cast(dcb, C.c_void_p) if dcb else None, None, out,
+                                       C.byref(d), C.byref(a))
+        if err:
+            raise err[0]
+        if n < 0:
+            raise RuntimeError(f"speculative_loop error {n}")
+        return out[:n].tolist(), d.value, a.value
 
     def generate_mtp(self, prompt, max_new: int):
         p = np.asarray(prompt, np.int32)
@@ -387,6 +497,9 @@ class Session:
         self._h = lib().uto_session_new(model._h, path)
 
     def __del__(self):
+        if getattr(self, "_mtp", None):
+            lib().uto_mtp_state_free(self._mtp)
+            self._mtp = None
         if getattr(self, "_h", None):
             lib().uto_session_free(self._h)
             self._h = None
@@ -404,6 +517,20 @@ class Session:
 
     def decode(self, tok: int) -> np.ndarray:
         return self.prefill([tok])[0]
+
+    def draft_logits(self, next_token: int):
+        """draft_logits (mtp.rs:74-133) on this session's MtpState ->
+        (logits [vocab], last MTP-layer output row [hidden])."""
+        if getattr(self, "_mtp", None) is None:
+            self._mtp = lib().uto_mtp_state_new()
+        V, Hd = self.model.spec.vocab_size, self.model.spec.hidden_size
+        logits = np.zeros(V, np.float32)
+        row = np.zeros(Hd, np.float32)
+        rc = lib().uto_draft_logits(self.model._h, self._h, self._mtp, next_token, logits,
+                                    row.ctypes.data)
+        if rc != 0:
+            raise RuntimeError(f"draft_logits error {rc}")
+        return logits, row
 
     def truncate(self, n: int) -> None:
         lib().uto_session_truncate(self._h, n)

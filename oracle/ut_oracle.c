@@ -8,12 +8,14 @@
  * -ffp-contract=off flag matters: the Rust reference never fuses a*b+c, so a
  * contracted build would not be the same arithmetic.
  */
+#define _DEFAULT_SOURCE /* madvise */
 #include "ut_oracle.h"
 
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <sys/mman.h>
 
 #if defined(__FP_FAST_FMAF) && !defined(UTO_ALLOW_FMA)
 /* An FMA-contracting build would not restate the reference's arithmetic. */
@@ -165,9 +167,13 @@ void uto_dequantize(int fmt, const void *payload, const float *scales,
 void uto_matmul(int fmt, const void *payload, const float *scales,
                 int64_t out_dim, int64_t in_dim, const float *x, int64_t seq,
                 float *out) {
+    /* Rows are independent and each keeps its sequential order, so the
+     * thread split changes no value (the reference's rayon row split,
+     * qtensor.rs:274-309). */
     for (int64_t s = 0; s < seq; s++) {
         const float *xs = x + s * in_dim;
         float *os = out + s * out_dim;
+#pragma omp parallel for schedule(static) if (out_dim * in_dim >= (1 << 18))
         for (int64_t o = 0; o < out_dim; o++) {
             float acc = 0.0f;
             if (fmt == UTO_F32) {
@@ -435,12 +441,15 @@ void uto_moe_experts(int fmt, int64_t hidden, int64_t inter,
 void uto_mla_attend(const float *qabs, const float *q_rope, const float *latent,
                     const float *krot, int64_t R, int64_t H, int64_t L,
                     int64_t P, int64_t pos_base, float scale, float *clat) {
-    /* attention.rs:214-234 */
+    /* attention.rs:214-234; the (row, head) pairs are independent (the
+     * reference runs them as rayon tasks, attention.rs:202), each in its
+     * sequential order */
     int64_t nmax = pos_base + R;
-    float *scores = (float *)xcalloc((size_t)nmax, 4);
+#pragma omp parallel for collapse(2) schedule(dynamic) if (R * H * nmax >= (1 << 14))
     for (int64_t s = 0; s < R; s++) {
-        int64_t n_ctx = pos_base + s + 1;
         for (int64_t h = 0; h < H; h++) {
+            float *scores = (float *)xcalloc((size_t)nmax, 4);
+            int64_t n_ctx = pos_base + s + 1;
             const float *qa = qabs + (s * H + h) * L;
             const float *qr = q_rope + (s * H + h) * P;
             for (int64_t t = 0; t < n_ctx; t++) {
@@ -459,9 +468,9 @@ void uto_mla_attend(const float *qabs, const float *q_rope, const float *latent,
                 float a = scores[t];
                 for (int64_t i = 0; i < L; i++) cl[i] += a * lat[i];
             }
+            free(scores);
         }
     }
-    free(scores);
 }
 
 /* ============================================================ checkpoint */
@@ -510,6 +519,23 @@ void uto_spec_default(uto_spec *s) {
     s->max_position_embeddings = 4096;
 }
 
+static uto_tensor *ck_push_empty(uto_ckpt *c, const char *name, int ndim, int64_t d0,
+                                 int64_t d1) {
+    if (c->n == c->cap) {
+        c->cap = c->cap ? c->cap * 2 : 256;
+        c->t = (uto_tensor *)realloc(c->t, (size_t)c->cap * sizeof(uto_tensor));
+        if (!c->t) abort();
+    }
+    uto_tensor *t = &c->t[c->n++];
+    memset(t, 0, sizeof(*t));
+    snprintf(t->name, sizeof(t->name), "%s", name);
+    t->ndim = ndim;
+    t->shape[0] = d0;
+    t->shape[1] = ndim == 2 ? d1 : 1;
+    t->fmt = UTO_F32;
+    return t;
+}
+
 static uto_tensor *ck_push(uto_ckpt *c, const char *name, int ndim, int64_t d0,
                            int64_t d1) {
     if (c->n == c->cap) {
@@ -530,10 +556,15 @@ static uto_tensor *ck_push(uto_ckpt *c, const char *name, int ndim, int64_t d0,
     return t;
 }
 
-typedef struct { uto_ckpt *c; uto_pcg32 rng; float std; } gen_state;
+typedef struct { uto_ckpt *c; uto_pcg32 rng; float std; int skip_mats; } gen_state;
 
 static void g_mat(gen_state *g, const char *name, int64_t d0, int64_t d1) {
-    /* Gen::mat (oracle.rs:126-132): normal() * std, row-major. */
+    /* Gen::mat (oracle.rs:126-132): normal() * std, row-major.  skip_mats:
+     * leave the matrix for uto_ckpt_synthesize to fill. */
+    if (g->skip_mats) {
+        ck_push_empty(g->c, name, 2, d0, d1);
+        return;
+    }
     uto_tensor *t = ck_push(g->c, name, 2, d0, d1);
     float *d = (float *)t->payload;
     for (int64_t i = 0; i < d0 * d1; i++) d[i] = uto_pcg32_normal(&g->rng) * g->std;
@@ -592,12 +623,13 @@ static void g_moe(gen_state *g, const uto_spec *s, int64_t li) {
     }
 }
 
-uto_ckpt *uto_generate(const uto_spec *s) {
+static uto_ckpt *generate(const uto_spec *s, int skip_mats) {
     /* generate_oracle (oracle.rs:150-310), tensor order preserved. */
     uto_ckpt *c = (uto_ckpt *)xcalloc(1, sizeof(uto_ckpt));
     gen_state g;
     g.c = c;
     g.std = s->init_std;
+    g.skip_mats = skip_mats;
     uto_pcg32_init(&g.rng, s->seed, 54);
     char nm[160];
     int64_t hd = s->hidden_size;
@@ -626,6 +658,8 @@ uto_ckpt *uto_generate(const uto_spec *s) {
     }
     return c;
 }
+
+uto_ckpt *uto_generate(const uto_spec *s) { return generate(s, 0); }
 
 void uto_ckpt_free(uto_ckpt *c) {
     if (!c) return;
@@ -808,6 +842,119 @@ const void *uto_ckpt_payload(const uto_ckpt *c, int64_t i, int64_t *nbytes) {
 const float *uto_ckpt_scales(const uto_ckpt *c, int64_t i) {
     if (i < 0 || i >= c->n) return NULL;
     return c->t[i].scales;
+}
+
+uto_ckpt *uto_ckpt_new(void) { return (uto_ckpt *)xcalloc(1, sizeof(uto_ckpt)); }
+
+int uto_ckpt_add(uto_ckpt *c, const char *name, int32_t fmt, int32_t ndim, int64_t d0, int64_t d1,
+                 const void *payload, int64_t nbytes, const float *scales) {
+    if (ndim != 1 && ndim != 2) return -1;
+    if (ndim == 1 && fmt != UTO_F32) return -1;
+    if (nbytes != uto_payload_bytes(fmt, d0, ndim == 2 ? d1 : 1)) return -1;
+    if (fmt != UTO_F32 && !scales) return -1;
+    uto_tensor *t = ck_push(c, name, ndim, d0, d1);
+    free(t->payload);
+    t->payload = xcalloc((size_t)nbytes, 1);
+    memcpy(t->payload, payload, (size_t)nbytes);
+    t->nbytes = nbytes;
+    t->fmt = fmt;
+    if (fmt != UTO_F32) {
+        t->scales = (float *)xcalloc((size_t)d0, 4);
+        memcpy(t->scales, scales, (size_t)d0 * 4);
+    }
+    return 0;
+}
+
+/* ----------------------------------------------------- synthetic weights */
+/* Test inputs at DeepSeek-V3 width, where generate_oracle's Irwin-Hall
+ * stream would take minutes: each element is a pure function of (seed,
+ * tensor ordinal, element index) through splitmix64, so rows fill in
+ * parallel.  The distributions are the benchmark's: quantized codes uniform
+ * over the format's range, per-row scales |N(0,std)|/qmax, f32 matrices
+ * N(0,std), norms 1 +- 0.1, the bias ramp of oracle.rs:205-209. */
+static uint64_t splitmix(uint64_t x) {
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+
+static float syn_u01(uint64_t key, uint64_t i) {
+    return (float)((splitmix(key ^ splitmix(i)) >> 40) + 0.5) * (1.0f / 16777216.0f);
+}
+
+static float syn_normal(uint64_t key, uint64_t i) {
+    /* Box-Muller over two uniforms of the element's stream */
+    float u1 = syn_u01(key, 2 * i), u2 = syn_u01(key, 2 * i + 1);
+    return sqrtf(-2.0f * logf(u1)) * cosf(6.2831853f * u2);
+}
+
+/* Buffers of many megabytes on transparent huge pages where the kernel
+ * offers them (a fault per 2 MiB instead of per 4 KiB); every byte is
+ * written by the caller. */
+static void *big_alloc(size_t n) {
+    const size_t huge = (size_t)2 << 20;
+    if (n < huge) return xcalloc(n, 1);
+    size_t sz = (n + huge - 1) / huge * huge;
+    void *p = aligned_alloc(huge, sz);
+    if (!p) { fprintf(stderr, "ut_oracle: out of memory\n"); abort(); }
+#ifdef MADV_HUGEPAGE
+    madvise(p, sz, MADV_HUGEPAGE);
+#endif
+    return p;
+}
+
+static void syn_tensor(uto_tensor *t, uint64_t key, int fmt, float std) {
+    int64_t o = t->shape[0], in = t->ndim == 2 ? t->shape[1] : 1;
+    if (fmt == UTO_F32) {
+        free(t->payload);
+        t->nbytes = o * in * 4;
+        t->payload = big_alloc((size_t)t->nbytes);
+        float *d = (float *)t->payload;
+#pragma omp parallel for schedule(static)
+        for (int64_t r = 0; r < o; r++)
+            for (int64_t i = 0; i < in; i++) d[r * in + i] = syn_normal(key, (uint64_t)(r * in + i)) * std;
+        return;
+    }
+    int64_t nb = uto_payload_bytes(fmt, o, in), rb = nb / o;
+    uint8_t *p = (uint8_t *)big_alloc((size_t)nb);
+    float *sc = (float *)xcalloc((size_t)o, 4);
+    float qmax = fmt == UTO_INT4 ? 7.0f : 127.0f;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < o; r++) {
+        uint8_t *row = p + r * rb;
+        for (int64_t b = 0; b < rb; b += 8) {
+            uint64_t v = splitmix(key ^ splitmix((uint64_t)(r * rb + b) | (1ull << 62)));
+            for (int64_t j = 0; j < 8 && b + j < rb; j++) {
+                uint8_t byte = (uint8_t)(v >> (8 * j));
+                if (fmt == UTO_INT8) byte = (uint8_t)(int8_t)((int)(byte % 255u) - 127);
+                row[b + j] = byte;
+            }
+        }
+        if (fmt == UTO_INT4 && in % 2 == 1) row[rb - 1] &= 0x0F;
+        sc[r] = fabsf(syn_normal(key ^ 0x5ca1e5ull, (uint64_t)r)) * std / qmax;
+    }
+    free(t->payload);
+    t->payload = p;
+    t->nbytes = nb;
+    t->scales = sc;
+    t->fmt = fmt;
+}
+
+uto_ckpt *uto_ckpt_synthesize(const uto_spec *s, uint64_t seed, float std, int expert_fmt,
+                              int dense_fmt) {
+    /* uto_generate's tensor list (norms and bias as generated), every
+     * matrix filled by syn_tensor in the format the converter would give it
+     * (classify_tensor: experts expert_fmt, dense dense_fmt, router gate f32) */
+    uto_ckpt *c = generate(s, 1);
+    for (int64_t i = 0; i < c->n; i++) {
+        uto_tensor *t = &c->t[i];
+        if (t->ndim != 2) continue;
+        int d = classify(t->name);
+        int fmt = d == 2 ? expert_fmt : (d == 1 ? dense_fmt : UTO_F32);
+        syn_tensor(t, splitmix(seed ^ splitmix((uint64_t)i + 1)), fmt, std);
+    }
+    return c;
 }
 
 /* ================================================================= model */
@@ -1173,18 +1320,17 @@ int uto_session_prefill(uto_session *s, const int32_t *ids, int64_t n, float *lo
     for (int64_t li = 0; li < c->num_hidden_layers; li++)
         run_layer(c, &m->layers[li], x, n, &s->kv[li], s->path);
     s->pos += n;
-    if (m->has_mtp) {
-        if (s->pos > s->hcap) {
-            int64_t nc = s->hcap ? s->hcap : 64;
-            while (nc < s->pos) nc *= 2;
-            s->tokens = (int32_t *)realloc(s->tokens, (size_t)nc * 4);
-            s->hidden = (float *)realloc(s->hidden, (size_t)(nc * hd) * 4);
-            if (!s->tokens || !s->hidden) abort();
-            s->hcap = nc;
-        }
-        memcpy(s->tokens + s->pos - n, ids, (size_t)n * 4);
-        memcpy(s->hidden + (s->pos - n) * hd, x, (size_t)(n * hd) * 4);
+    /* session.tokens always; session.hidden (the MTP head's input) with MTP */
+    if (s->pos > s->hcap) {
+        int64_t nc = s->hcap ? s->hcap : 64;
+        while (nc < s->pos) nc *= 2;
+        s->tokens = (int32_t *)realloc(s->tokens, (size_t)nc * 4);
+        if (m->has_mtp) s->hidden = (float *)realloc(s->hidden, (size_t)(nc * hd) * 4);
+        if (!s->tokens || (m->has_mtp && !s->hidden)) abort();
+        s->hcap = nc;
     }
+    memcpy(s->tokens + s->pos - n, ids, (size_t)n * 4);
+    if (m->has_mtp) memcpy(s->hidden + (s->pos - n) * hd, x, (size_t)(n * hd) * 4);
     float *normed = (float *)xcalloc((size_t)hd, 4);
     for (int64_t i = 0; i < n; i++) {
         uto_rmsnorm(normed, x + i * hd, m->final_norm, hd, c->rms_norm_eps);
@@ -1203,8 +1349,33 @@ void uto_session_truncate(uto_session *s, int64_t len) {
 
 int64_t uto_session_position(const uto_session *s) { return s->pos; }
 
-int64_t uto_greedy_decode(uto_model *m, const int32_t *prompt, int64_t n, int64_t max_new, int32_t *out) {
-    /* core/model.rs:139-185 with a greedy sampler (argmax); no stop ids. */
+/* ================================================== generation loops ==== */
+/* The emit rule of undertow_core::generate (core/model.rs:139-166) and the
+ * speculative loops (mtp.rs:194-257, 263-314): emit, report to on_token,
+ * end after a stop token (emitted and counted), when on_token returns 0, or
+ * at max_new tokens. */
+typedef struct {
+    const int32_t *stops;
+    int64_t n_stops;
+    uto_token_fn on_token;
+    void *user;
+    int32_t *out;
+    int64_t max_new, produced;
+} emit_state;
+
+static int emit(emit_state *e, int32_t tok) {
+    e->out[e->produced++] = tok;
+    int keep = e->on_token ? e->on_token(e->user, tok) != 0 : 1;
+    int stop = 0;
+    for (int64_t i = 0; i < e->n_stops; i++)
+        if (e->stops[i] == tok) stop = 1;
+    return stop || !keep || e->produced >= e->max_new;
+}
+
+int64_t uto_generate_greedy(uto_model *m, const int32_t *prompt, int64_t n, int64_t max_new,
+                            const int32_t *stops, int64_t n_stops, uto_token_fn on_token,
+                            void *user, int32_t *out) {
+    /* core/model.rs:139-166 with a greedy sampler (argmax). */
     int64_t V = m->c.vocab_size;
     uto_session *s = uto_session_new(m, 0);
     float *logits = (float *)xcalloc((size_t)(n * V), 4);
@@ -1212,80 +1383,148 @@ int64_t uto_greedy_decode(uto_model *m, const int32_t *prompt, int64_t n, int64_
     if (rc) { free(logits); uto_session_free(s); return rc; }
     float *last = (float *)xcalloc((size_t)V, 4);
     memcpy(last, logits + (n - 1) * V, (size_t)V * 4);
-    int64_t produced = 0;
-    while (produced < max_new) {
+    emit_state e = {stops, n_stops, on_token, user, out, max_new, 0};
+    while (e.produced < max_new) {
         int32_t next = (int32_t)uto_argmax(last, V);
-        out[produced++] = next;
-        if (produced == max_new) break;
+        if (emit(&e, next)) break;
         if (uto_session_prefill(s, &next, 1, last) == -2) break;
     }
     free(last); free(logits); uto_session_free(s);
-    return produced;
+    return e.produced;
 }
 
-/* MtpState + draft_logits (mtp.rs:48-133). */
-typedef struct { kv_cache kv; int64_t fed; } mtp_state;
+int64_t uto_greedy_decode(uto_model *m, const int32_t *prompt, int64_t n, int64_t max_new, int32_t *out) {
+    /* greedy_decode (core/model.rs:168-185) without stop ids. */
+    return uto_generate_greedy(m, prompt, n, max_new, NULL, 0, NULL, NULL, out);
+}
 
-static void draft_logits(uto_model *m, uto_session *sess, mtp_state *st, int32_t next_token, float *logits) {
+/* MtpState (mtp.rs:48-55): the MTP layer's own KV and the fed count. */
+struct uto_mtp_state { kv_cache kv; int64_t fed; };
+
+uto_mtp_state *uto_mtp_state_new(void) { return (uto_mtp_state *)xcalloc(1, sizeof(uto_mtp_state)); }
+
+void uto_mtp_state_free(uto_mtp_state *st) {
+    if (!st) return;
+    free(st->kv.latent); free(st->kv.k_rot); free(st);
+}
+
+/* The MTP module over `rows` inputs: x_j = eh_proj(concat(enorm(embed(t_j)),
+ * hnorm(h_j))), the MTP layer on its own KV, then the head over the last
+ * row (mtp.rs:84-131).  last_out (may be NULL) gets the layer's output row
+ * for the last input, before the head's norm. */
+static void mtp_rows(uto_model *m, uto_mtp_state *st, const int32_t *t_next, const float *hidden,
+                     int64_t rows, float *logits, float *last_out) {
     const uto_spec *c = &m->c;
-    int64_t hd = c->hidden_size, pos = sess->pos, pending = pos - st->fed;
-    float *xs = (float *)xcalloc((size_t)(pending * hd), 4);
+    int64_t hd = c->hidden_size;
+    float *xs = (float *)xcalloc((size_t)(rows * hd), 4);
     float *emb = (float *)xcalloc((size_t)hd, 4), *cat = (float *)xcalloc((size_t)(2 * hd), 4);
-    for (int64_t j = 0, i = st->fed; i < pos; i++, j++) {
-        int32_t t_next = i + 1 < pos ? sess->tokens[i + 1] : next_token;
-        embed_row(m, t_next, emb);
+    for (int64_t j = 0; j < rows; j++) {
+        embed_row(m, t_next[j], emb);
         uto_rmsnorm(cat, emb, m->enorm, hd, c->rms_norm_eps);
-        uto_rmsnorm(cat + hd, sess->hidden + i * hd, m->hnorm, hd, c->rms_norm_eps);
+        uto_rmsnorm(cat + hd, hidden + j * hd, m->hnorm, hd, c->rms_norm_eps);
         qt_matmul(&m->eh_proj, cat, 1, xs + j * hd);
     }
-    run_layer(c, &m->mtp_layer, xs, pending, &st->kv, 0);
-    st->fed = pos;
+    run_layer(c, &m->mtp_layer, xs, rows, &st->kv, 0);
+    if (last_out) memcpy(last_out, xs + (rows - 1) * hd, (size_t)hd * 4);
     float *normed = (float *)xcalloc((size_t)hd, 4);
-    uto_rmsnorm(normed, xs + (pending - 1) * hd, m->mtp_norm, hd, c->rms_norm_eps);
+    uto_rmsnorm(normed, xs + (rows - 1) * hd, m->mtp_norm, hd, c->rms_norm_eps);
     qt_matmul(&m->mtp_head, normed, 1, logits);
     free(normed); free(emb); free(cat); free(xs);
 }
 
-int64_t uto_generate_mtp(uto_model *m, const int32_t *prompt, int64_t n, int64_t max_new, int32_t *out,
-                         int64_t *drafted, int64_t *accepted) {
-    /* speculative_loop (mtp.rs:263-314) driven by the native draft head; the
-     * greedy sampler path of speculative_loop_with_sampler (mtp.rs:194-257)
-     * reduces to the same decisions (one-hot p and q). */
+int uto_draft_logits(uto_model *m, uto_session *sess, uto_mtp_state *st, int32_t next_token,
+                     float *logits, float *last_out) {
+    /* draft_logits (mtp.rs:74-133): pending positions fed..pos-1, t_next =
+     * the following consumed token, next_token for the last. */
     if (!m->has_mtp) return -4;
-    int64_t V = m->c.vocab_size;
+    int64_t pos = sess->pos, pending = pos - st->fed;
+    if (pending <= 0) return -5;
+    int32_t *t_next = (int32_t *)xcalloc((size_t)pending, 4);
+    for (int64_t j = 0, i = st->fed; i < pos; i++, j++)
+        t_next[j] = i + 1 < pos ? sess->tokens[i + 1] : next_token;
+    mtp_rows(m, st, t_next, sess->hidden + st->fed * m->c.hidden_size, pending, logits, last_out);
+    st->fed = pos;
+    free(t_next);
+    return 0;
+}
+
+int64_t uto_speculative_loop(uto_model *m, const int32_t *prompt, int64_t n, int64_t max_new,
+                             int32_t depth, const int32_t *stops, int64_t n_stops,
+                             uto_token_fn on_token, void *user, uto_draft_fn draft_fn,
+                             void *draft_user, int32_t *out, int64_t *drafted, int64_t *accepted) {
+    /* speculative_loop (mtp.rs:263-314); the greedy path of
+     * speculative_loop_with_sampler (mtp.rs:194-257) makes the same
+     * decisions (one-hot p and q).  depth 1 is the reference.  depth 2..3
+     * (an extension): the native head chains the MTP layer on its own output
+     * row for the last fed position with the previous draft's embedding
+     * (rows never kept: the MTP KV returns to the fed length), the verify
+     * prefill takes [next, d1..dk] and the longest prefix of drafts equal to
+     * the verify argmax rows is accepted. */
+    if (drafted) *drafted = 0;
+    if (accepted) *accepted = 0;
+    if (depth < 1 || depth > 3) return -1;
+    if (!draft_fn && !m->has_mtp) return -4;
+    int64_t V = m->c.vocab_size, hd = m->c.hidden_size;
     uto_session *s = uto_session_new(m, 0);
-    mtp_state st;
-    memset(&st, 0, sizeof st);
+    uto_mtp_state *st = uto_mtp_state_new();
     float *logits = (float *)xcalloc((size_t)(n * V), 4);
     int rc = uto_session_prefill(s, prompt, n, logits);
-    if (rc) { free(logits); uto_session_free(s); return rc; }
+    if (rc) { free(logits); uto_mtp_state_free(st); uto_session_free(s); return rc; }
     int32_t next = (int32_t)uto_argmax(logits + (n - 1) * V, V);
-    float *dl = (float *)xcalloc((size_t)V, 4), *ver = (float *)xcalloc((size_t)(2 * V), 4);
-    int64_t produced = 0, nd = 0, na = 0;
+    float *dl = (float *)xcalloc((size_t)V, 4), *ver = (float *)xcalloc((size_t)((depth + 1) * V), 4);
+    float *row = (float *)xcalloc((size_t)hd, 4), *row2 = (float *)xcalloc((size_t)hd, 4);
+    int32_t d[3], vid[4];
+    int64_t nd = 0, na = 0;
+    emit_state e = {stops, n_stops, on_token, user, out, max_new, 0};
+    int64_t result = 0;
+    if (max_new == 0) goto done;
     for (;;) {
-        out[produced++] = next;
-        if (produced >= max_new) break;
-        draft_logits(m, s, &st, next, dl);
-        int32_t dr = (int32_t)uto_argmax(dl, V);
-        nd++;
-        int64_t pos_before = s->pos;
-        int32_t pair[2] = {next, dr};
-        if (uto_session_prefill(s, pair, 2, ver) == -2) break;
-        int32_t verified = (int32_t)uto_argmax(ver, V);
-        if (verified == dr) {
-            na++;
-            out[produced++] = dr;
-            if (produced >= max_new) break;
-            next = (int32_t)uto_argmax(ver + V, V);
+        if (emit(&e, next)) break;
+        if (draft_fn) {
+            int32_t r = draft_fn(draft_user, s->tokens, s->pos, next, depth, d);
+            if (r < 0) { result = r; goto done; }
+            for (int i = 0; i < depth; i++)
+                if (d[i] < 0 || d[i] >= V) { result = -3; goto done; }
         } else {
-            uto_session_truncate(s, pos_before + 1);
-            next = verified;
+            uto_draft_logits(m, s, st, next, dl, row);
+            d[0] = (int32_t)uto_argmax(dl, V);
+            int64_t kv_len = st->kv.len;
+            for (int j = 1; j < depth; j++) {
+                mtp_rows(m, st, &d[j - 1], row, 1, dl, row2);
+                memcpy(row, row2, (size_t)hd * 4);
+                d[j] = (int32_t)uto_argmax(dl, V);
+            }
+            st->kv.len = kv_len;
         }
+        nd += depth;
+        int64_t pos_before = s->pos;
+        vid[0] = next;
+        for (int i = 0; i < depth; i++) vid[i + 1] = d[i];
+        if (uto_session_prefill(s, vid, depth + 1, ver) == -2) break;
+        int64_t a = 0;
+        int end = 0;
+        while (a < depth && (int32_t)uto_argmax(ver + a * V, V) == d[a]) {
+            a++;
+            na++;
+            if (emit(&e, d[a - 1])) { end = 1; break; }
+        }
+        if (end) break;
+        next = (int32_t)uto_argmax(ver + a * V, V);
+        if (a < depth) uto_session_truncate(s, pos_before + 1 + a);
     }
+    result = e.produced;
+done:
     if (drafted) *drafted = nd;
     if (accepted) *accepted = na;
-    free(dl); free(ver); free(logits);
-    free(st.kv.latent); free(st.kv.k_rot);
+    free(dl); free(ver); free(logits); free(row); free(row2);
+    uto_mtp_state_free(st);
     uto_session_free(s);
-    return produced;
+    return result;
+}
+
+int64_t uto_generate_mtp(uto_model *m, const int32_t *prompt, int64_t n, int64_t max_new, int32_t *out,
+                         int64_t *drafted, int64_t *accepted) {
+    /* generate_greedy_mtp (mtp.rs:176-191) without stop ids: depth 1. */
+    return uto_speculative_loop(m, prompt, n, max_new, 1, NULL, 0, NULL, NULL, NULL, NULL, out,
+                                drafted, accepted);
 }

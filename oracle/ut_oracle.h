@@ -157,6 +157,19 @@ int       uto_ckpt_info(const uto_ckpt *c, int64_t i, char *name, int64_t name_c
 /* Payload bytes (f32 data, int8 codes, packed int4) and scales pointers. */
 const void  *uto_ckpt_payload(const uto_ckpt *c, int64_t i, int64_t *nbytes);
 const float *uto_ckpt_scales(const uto_ckpt *c, int64_t i);
+/* An empty checkpoint, and a copy of one tensor added to it (1-D f32 or
+ * 2-D [d0, d1] in fmt; nbytes must equal payload_bytes, scales [d0] for the
+ * integer formats).  Returns 0 or -1.  For hand-built test models. */
+uto_ckpt *uto_ckpt_new(void);
+int       uto_ckpt_add(uto_ckpt *c, const char *name, int32_t fmt, int32_t ndim, int64_t d0,
+                       int64_t d1, const void *payload, int64_t nbytes, const float *scales);
+/* Test inputs at DeepSeek-V3 width: uto_generate's tensor list with every
+ * matrix filled from a counter-based generator (fast, parallel) in the
+ * format classify_tensor gives it: codes uniform over the format's range,
+ * per-row scales |N(0,std)|/qmax, f32 matrices N(0,std).  Not the
+ * reference's generator; a source of seeded weights only. */
+uto_ckpt *uto_ckpt_synthesize(const uto_spec *s, uint64_t seed, float std, int expert_fmt,
+                              int dense_fmt);
 
 typedef struct uto_model uto_model;
 typedef struct uto_session uto_session;
@@ -171,12 +184,42 @@ void         uto_session_free(uto_session *s);
 int     uto_session_prefill(uto_session *s, const int32_t *ids, int64_t n, float *logits);
 void    uto_session_truncate(uto_session *s, int64_t len);
 int64_t uto_session_position(const uto_session *s);
-/* undertow_core::greedy_decode (undertow-core/src/model.rs:139-185); writes
- * the new tokens, returns their count or a negative error. */
+/* on_token (core/model.rs:139-166, mtp.rs:194-314): return 0 to stop. */
+typedef int32_t (*uto_token_fn)(void *user, int32_t token);
+/* draft_fn of speculative_loop (mtp.rs:263-314): consumed tokens [n], the
+ * emitted not-yet-consumed `next`; writes `depth` drafts; < 0 aborts. */
+typedef int32_t (*uto_draft_fn)(void *user, const int32_t *tokens, int64_t n, int32_t next,
+                                int32_t depth, int32_t *drafts);
+/* undertow_core::generate with a greedy sampler (core/model.rs:139-166):
+ * stops after a token in stops[] (emitted and counted), when on_token
+ * (may be NULL) returns 0, at max_new, or at the context end.  Returns the
+ * count or a negative error. */
+int64_t uto_generate_greedy(uto_model *m, const int32_t *prompt, int64_t n, int64_t max_new,
+                            const int32_t *stops, int64_t n_stops, uto_token_fn on_token,
+                            void *user, int32_t *out);
+/* greedy_decode (core/model.rs:168-185) without stop ids. */
 int64_t uto_greedy_decode(uto_model *m, const int32_t *prompt, int64_t n,
                           int64_t max_new, int32_t *out);
-/* generate_greedy_mtp -> speculative_loop greedy (mtp.rs:74-133,176-191,
- * 263-314).  Returns produced count; drafted/accepted via pointers. */
+/* MtpState (mtp.rs:48-55) and draft_logits (mtp.rs:74-133): feeds the
+ * session's pending positions to the MTP layer and writes the head's
+ * logits [vocab] for the last; last_out (may be NULL) gets that position's
+ * MTP-layer output row (before the head's norm).  Returns 0, -4 without an
+ * MTP head, -5 with nothing pending. */
+typedef struct uto_mtp_state uto_mtp_state;
+uto_mtp_state *uto_mtp_state_new(void);
+void           uto_mtp_state_free(uto_mtp_state *st);
+int            uto_draft_logits(uto_model *m, uto_session *s, uto_mtp_state *st,
+                                int32_t next_token, float *logits, float *last_out);
+/* speculative_loop (mtp.rs:263-314) at depth 1 (the reference) to 3 (an
+ * extension: native drafts chain the MTP layer on its own last output row,
+ * depth+1 verify rows, longest matching prefix accepted, rollback to the
+ * last verified position).  draft_fn NULL: the native MTP head.  Stop and
+ * callback rules of uto_generate_greedy.  Returns the produced count. */
+int64_t uto_speculative_loop(uto_model *m, const int32_t *prompt, int64_t n, int64_t max_new,
+                             int32_t depth, const int32_t *stops, int64_t n_stops,
+                             uto_token_fn on_token, void *user, uto_draft_fn draft_fn,
+                             void *draft_user, int32_t *out, int64_t *drafted, int64_t *accepted);
+/* generate_greedy_mtp (mtp.rs:176-191) without stop ids: depth 1. */
 int64_t uto_generate_mtp(uto_model *m, const int32_t *prompt, int64_t n,
                          int64_t max_new, int32_t *out, int64_t *drafted,
                          int64_t *accepted);

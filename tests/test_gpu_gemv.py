@@ -144,3 +144,55 @@ def test_shape_mismatch_raises(ctx):
         U.QTensor(ctx, INT4, payload[:, :-1], scales, 8, 64)  # payload size mismatch
     q = U.QTensor(ctx, U.INFER, payload, scales, 8, 64)
     assert q.format == INT4
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("o,i,row0,nrows", [(16, 256, 3, 9), (7, 130, 0, 7), (32768, 512, 128, 128),
+                                            (32768, 512, 32640, 128), (2048, 7168, 1000, 37)])
+def test_matvec_rows_matches_oracle(ctx, fmt, o, i, row0, nrows):
+    """QTensor::matvec_rows (qtensor.rs:548-586), e.g. one head's V block of
+    kv_b at DeepSeek-V3 shape (128 heads x (128 + 128) rows x 512)."""
+    import torch
+    rng = np.random.default_rng(o + i + row0 + fmt)
+    payload, scales = rand_qtensor(rng, fmt, o, i)
+    qt = upload(ctx, fmt, payload, scales, o, i)
+    x = rng.standard_normal(i).astype(np.float32)
+    out = torch.full((nrows,), float("nan"), device="cuda:0")
+    qt.matvec_rows(row0, nrows, dev(x), out)
+    got = host(out)
+    want = O.matvec_rows(fmt, payload, scales, o, i, row0, nrows, x)
+    tol = 1e-4 * np.maximum(np.abs(want), 1.0)
+    assert (np.abs(got - want) <= tol).all(), np.abs(got - want).max()
+    if fmt != F32:
+        # the same rows of the whole-matrix GEMV, bit for bit
+        full = run_matmul(ctx, qt, x[None, :])[0]
+        assert np.array_equal(got, full[row0:row0 + nrows])
+
+
+def test_matvec_rows_shape_errors(ctx):
+    import torch
+    import undertow_amd as U
+    rng = np.random.default_rng(1)
+    payload, scales = rand_qtensor(rng, INT8, 16, 32)
+    qt = upload(ctx, INT8, payload, scales, 16, 32)
+    x = dev(rng.standard_normal(32).astype(np.float32))
+    with pytest.raises(U.ShapeError):
+        qt.matvec_rows(10, 7, x, torch.empty(7, device="cuda:0"))
+    with pytest.raises(U.ShapeError):
+        qt.matvec_rows(0, 4, x, torch.empty(5, device="cuda:0"))
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("o,i,row,factor", [(16, 256, 5, 0.75), (7, 131, 6, -1.5), (512, 7168, 300, 3.0)])
+def test_add_scaled_row_matches_oracle(ctx, fmt, o, i, row, factor):
+    """QTensor::add_scaled_row (qtensor.rs:516-543): acc += (factor*scale)*q,
+    bit-exact (one rounding per element, as the reference)."""
+    rng = np.random.default_rng(o + i + row + fmt)
+    payload, scales = rand_qtensor(rng, fmt, o, i)
+    qt = upload(ctx, fmt, payload, scales, o, i)
+    acc0 = rng.standard_normal(i).astype(np.float32)
+    acc = dev(acc0)
+    qt.add_scaled_row(row, factor, acc)
+    got = host(acc)
+    want = O.add_scaled_row(fmt, payload, scales, o, i, row, factor, acc0)
+    assert np.array_equal(got, want), np.abs(got - want).max()

@@ -312,6 +312,38 @@ def test_mla_attend_matches_oracle(ctx, R, H, L, P, T):
         assert np.array_equal(one[0], got[s])
 
 
+HEADS_CHECKED = [0, 1, 31, 32, 63, 64, 100, 127]
+
+
+@pytest.mark.parametrize("R,T", [(1, 32768), (2, 32768), (4, 32768), (4, 16400), (3, 16385)])
+def test_mla_long_context_matches_oracle(ctx, R, T):
+    """Config 3's longest context: past 16384 positions the matrix-core
+    kernel takes 256-position slices and (T+255)/256 of them per row.  All
+    128 heads run on the GPU; the oracle's sequential loops check eight of
+    them (its (row, head) pairs are independent)."""
+    import undertow_amd as U
+    H, L, P = 128, 512, 64
+    rng = np.random.default_rng(R * 7 + T)
+    qabs = rng.standard_normal((R, H, L)).astype(np.float32)
+    qr = rng.standard_normal((R, H, P)).astype(np.float32)
+    lat = rng.standard_normal((T, L)).astype(np.float32)
+    kr = rng.standard_normal((T, P)).astype(np.float32)
+    pos_base = T - R
+    scale = float(1 / np.sqrt(192.0))
+    kc = U.mla_cache_split(ctx, dev(lat), dev(kr))
+    got = host(U.mla_attend_split(ctx, dev(qabs), dev(qr), kc, pos_base, scale))
+    hs = HEADS_CHECKED
+    want = O.mla_attend(np.ascontiguousarray(qabs[:, hs]), np.ascontiguousarray(qr[:, hs]), lat, kr,
+                        pos_base, scale)
+    tol = 1e-4 * max(1.0, np.abs(want).max())
+    assert np.abs(got[:, hs] - want).max() <= tol, np.abs(got[:, hs] - want).max()
+    assert np.isfinite(got).all()
+    for s in range(R):
+        one = host(U.mla_attend_split(ctx, dev(qabs[s:s + 1]), dev(qr[s:s + 1]), kc, pos_base + s,
+                                      scale))
+        assert np.array_equal(one[0], got[s])
+
+
 def test_mla_split_cache_round_trip(ctx):
     """hi + lo of the split cache reproduces the f32 cache to 2^-16 relative
     (hi = bf16(x) rounded to nearest, lo = bf16(x - hi))."""

@@ -1021,3 +1021,36 @@ extern "C" int32_t ut_qtensor_matmul(ut_ctx *ctx, const ut_qtensor *qt, float *o
     UT_TRY(launch_digitize(ctx, x_dev, qt->in_dim, seq, qt->in_dim, nullptr, ga.xd, flags));
     return gemv(ctx, ga);
 }
+
+// QTensor::matvec_rows (qtensor.rs:548-586): the GEMV of one activation
+// vector against the contiguous row block [row0, row0 + nrows), through a
+// view of those rows (payload and scales offset, nothing copied).  For the
+// integer formats each row's value is the one ut_qtensor_matmul gives for
+// that row (exact integer sums); an f32 block may split K differently from
+// the whole matrix, so its rows agree to rounding.
+extern "C" int32_t ut_qtensor_matvec_rows(ut_ctx *ctx, const ut_qtensor *qt, int64_t row0,
+                                          int64_t nrows, const float *x_dev, int64_t x_len,
+                                          float *out_dev, int64_t out_len) {
+    if (!ctx || !qt || !x_dev || (!out_dev && nrows > 0) || row0 < 0 || nrows < 0) {
+        set_error(ctx, "ut_qtensor_matvec_rows: bad argument");
+        return UT_ERR_ARG;
+    }
+    // the reference's assert!/assert_eq!s (qtensor.rs:549-552)
+    if (row0 + nrows > qt->out_dim) {
+        set_error(ctx, "rows [%lld, %lld) exceed out_dim %lld", (long long)row0,
+                  (long long)(row0 + nrows), (long long)qt->out_dim);
+        return UT_ERR_SHAPE;
+    }
+    if (x_len != qt->in_dim || out_len != nrows) {
+        set_error(ctx, "matvec_rows shapes: x %lld (in %lld), out %lld (rows %lld)",
+                  (long long)x_len, (long long)qt->in_dim, (long long)out_len, (long long)nrows);
+        return UT_ERR_SHAPE;
+    }
+    if (nrows == 0) return UT_OK;
+    ut_qtensor view = *qt;
+    view.owns = false;
+    view.out_dim = nrows;
+    view.payload = (uint8_t *)qt->payload + row0 * qt->row_bytes;
+    view.scales = qt->scales ? qt->scales + row0 : nullptr;
+    return ut_qtensor_matmul(ctx, &view, out_dev, nrows, x_dev, qt->in_dim, 1);
+}

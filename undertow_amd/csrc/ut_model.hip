@@ -75,6 +75,7 @@ struct ut_model {
     float *ones = nullptr;         // [4] weight 1
     MoePlan mlp_plan{};            // the fixed one-slot plan of an MLP
     bool finalized = false;
+    std::vector<int32_t> stop_ids;  // the checkpoint's stop tokens (DeepseekMoeModel::stop_ids)
     std::vector<void *> device_allocs;
     int64_t device_bytes = 0;
     int device = 0;
@@ -870,16 +871,16 @@ int32_t draft_rows_dev(ut_session *s, const int32_t *host_ids, int in_slot,
     const int32_t *ids = in_slot >= 0 ? w.vids + in_slot : nullptr;
     int32_t *draft_dev = w.vids + out_slot;
     if (in_slot < 0) {
-        if (rows > kPinIds - 8) {
-            set_error(ctx, "MTP draft over %lld positions exceeds the staging slot", (long long)rows);
-            return UT_ERR_ARG;
-        }
         for (int64_t i = 0; i < rows; i++)
             if (host_ids[i] < 0 || host_ids[i] >= V) {
                 set_error(ctx, "token id %d out of vocab (%lld)", host_ids[i], (long long)V);
                 return UT_ERR_BAD_TOKEN;
             }
-        UT_TRY(upload_slot(s, w.ids, host_ids, rows));
+        // a short feed goes through the session's pinned slot (no wait); a
+        // long one (the first draft after a long prompt) through a pinned
+        // buffer of its size, ordered behind the stream
+        if (rows <= kPinIds - 8) UT_TRY(upload_slot(s, w.ids, host_ids, rows));
+        else UT_TRY(upload_ids(s, host_ids, rows));
         ids = w.ids;
     }
     UT_TRY(launch_embed(ctx, m->embed, ids, rows, w.emb, H));
@@ -1064,6 +1065,186 @@ int32_t synthesize_all(ut_model *m, uint64_t seed, float std, int expert_fmt, in
     }
     UT_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
     return UT_OK;
+}
+
+// ----------------------------------------------------- generation loops ---
+// The emit rule shared by undertow_core::generate (core/model.rs:139-166)
+// and the speculative loops (mtp.rs:194-257, 263-314): every emitted token
+// goes to out and to on_token, and the stream ends after a stop token (the
+// model's stop ids or the call's extra ids; the stop token is emitted and
+// counted), when on_token returns 0, or at max_new tokens.
+struct Emit {
+    const ut_model *m;
+    const int32_t *extra;
+    int64_t n_extra;
+    ut_token_fn on_token;
+    void *user;
+    int32_t *out;
+    int64_t max_new;
+    int64_t produced = 0;
+
+    bool is_stop(int32_t tok) const {
+        for (int32_t id : m->stop_ids)
+            if (id == tok) return true;
+        for (int64_t i = 0; i < n_extra; i++)
+            if (extra[i] == tok) return true;
+        return false;
+    }
+    // emits tok; true when the stream ends with it
+    bool push(int32_t tok) {
+        out[produced++] = tok;
+        const bool keep = on_token ? on_token(user, tok) != 0 : true;
+        return is_stop(tok) || !keep || produced >= max_new;
+    }
+};
+
+// Greedy generation on a fresh session.  Each step is fed the previous
+// step's argmax on the device, and the next step is queued before the host
+// waits for the current token (a step queued past the stream's end is
+// discarded with the session).
+int64_t gen_greedy(ut_model *m, const int32_t *prompt, int64_t n, Emit &em) {
+    ut_session *s = nullptr;
+    UT_TRY(ut_session_create(m, 0, &s));
+    std::vector<int32_t> am((size_t)(n > 0 ? n : 1));
+    int32_t rc = prefill_dev(s, prompt, n);
+    if (rc == UT_OK) rc = read_argmax(s, n, am.data());
+    if (rc || em.max_new == 0) {
+        ut_session_free(s);
+        return rc;
+    }
+    int32_t tok = am[(size_t)n - 1];
+    bool queued = false;  // a step whose output token is not read yet
+    if (!em.push(tok)) {
+        rc = prefill_dev(s, nullptr, 1, s->ws.am + (n - 1));
+        if (rc == UT_OK) {
+            s->tokens.push_back(tok);
+            queued = true;
+        } else if (rc == UT_ERR_CONTEXT_OVERFLOW) {
+            rc = UT_OK;  // end of stream at the context end (core/model.rs:158-161)
+        }
+    }
+    while (queued && rc == UT_OK) {
+        rc = readback_enqueue(s, s->ws.am, 1);
+        if (rc) break;
+        bool next_queued = false;
+        if (em.produced + 1 < em.max_new) {
+            // fed from ws.am[0], which this step overwrites only after reading it
+            const int32_t r2 = prefill_dev(s, nullptr, 1, s->ws.am);
+            if (r2 == UT_OK) next_queued = true;
+            else if (r2 != UT_ERR_CONTEXT_OVERFLOW) { rc = r2; break; }
+        }
+        rc = readback_wait(s, 1, &tok);
+        if (rc) break;
+        if (em.push(tok)) break;
+        if (next_queued) s->tokens.push_back(tok);  // the id the queued step was fed
+        queued = next_queued;
+    }
+    ut_session_free(s);
+    return rc ? rc : em.produced;
+}
+
+// speculative_loop (mtp.rs:263-314) at depth 1..3.  Drafts come from the
+// native MTP head (draft_fn == nullptr: draft_logits, mtp.rs:74-133, chained
+// on its own output row for depth > 1) or from the caller's draft_fn.  One
+// verify prefill of [next, d1..dk]; the longest prefix of drafts equal to
+// the verify argmax rows is accepted; the main KV rolls back to the last
+// verified position.
+int64_t gen_spec(ut_model *m, const int32_t *prompt, int64_t n, int32_t depth, ut_draft_fn draft_fn,
+                 void *draft_user, Emit &em, int64_t *drafted, int64_t *accepted) {
+    ut_ctx *ctx = m->ctx;
+    const int64_t H = m->c.hidden_size, V = m->c.vocab_size;
+    ut_session *s = nullptr;
+    UT_TRY(ut_session_create(m, 0, &s));
+    std::vector<int32_t> am((size_t)(n > depth + 1 ? n : depth + 1));
+    int32_t rc = prefill_dev(s, prompt, n);
+    if (rc == UT_OK) rc = read_argmax(s, n, am.data());
+    if (rc || em.max_new == 0) {
+        ut_session_free(s);
+        return rc;
+    }
+    int32_t next = am[(size_t)n - 1];
+    int64_t nd = 0, na = 0;
+    std::vector<int32_t> toks, drafts((size_t)depth), vid((size_t)depth + 1);
+    for (;;) {
+        if (em.push(next)) break;
+        const int64_t pos_before = s->pos;
+        if (draft_fn) {
+            // draft_fn(&session, next) (mtp.rs:263-314): the consumed tokens
+            // and the emitted, not yet consumed `next`
+            const int32_t r = draft_fn(draft_user, s->tokens.data(), (int64_t)s->tokens.size(),
+                                       next, depth, drafts.data());
+            if (r < 0) {
+                set_error(ctx, "draft callback returned %d", r);
+                rc = r;
+                break;
+            }
+            for (int32_t d : drafts)
+                if (d < 0 || d >= V) {
+                    set_error(ctx, "draft id %d out of vocab (%lld)", d, (long long)V);
+                    rc = UT_ERR_BAD_TOKEN;
+                }
+            if (rc) break;
+            vid[0] = next;
+            std::copy(drafts.begin(), drafts.end(), vid.begin() + 1);
+            // the workspace holds at least four rows; vids must not move
+            rc = ws_reserve(s, depth + 1);
+            if (rc == UT_OK) rc = upload_slot(s, s->ws.vids, vid.data(), depth + 1, kPinIds - 8);
+            if (rc) break;
+        } else {
+            // ---- draft: feed verified positions fed..pos-1 (mtp.rs:84-121)
+            const int64_t pos = s->pos, fed = s->mtp_fed, pending = pos - fed;
+            toks.clear();
+            for (int64_t i = fed; i < pos; i++) toks.push_back(i + 1 < pos ? s->tokens[(size_t)i + 1] : next);
+            rc = draft_rows_dev(s, toks.data(), -1, s->hidden + fed * H, pending, 1);
+            if (rc) break;
+            s->mtp_fed = pos;
+            // ---- chained drafts (depth > 1): MTP layer on its own last output row
+            for (int32_t j = 1; j < depth && rc == UT_OK; j++) {
+                // the MTP layer's output row for the last fed position is in ws.x
+                // (staged in ws.attn, which is free between layers)
+                const int64_t last = (j == 1 ? pending : 1) - 1;
+                rc = hipMemcpyAsync(s->ws.attn, s->ws.x + last * H, (size_t)H * 4,
+                                    hipMemcpyDeviceToDevice, ctx->stream) == hipSuccess
+                         ? UT_OK : UT_ERR_HIP;
+                if (rc == UT_OK) rc = draft_rows_dev(s, nullptr, j, s->ws.attn, 1, 1 + j);
+            }
+            s->mtp_kv.len = s->mtp_fed;  // speculative MTP rows are never kept
+            if (rc) break;
+            rc = upload_slot(s, s->ws.vids, &next, 1, kPinIds - 8);
+            if (rc) break;
+        }
+        nd += depth;
+        // ---- verify [next, d1..dk] in one prefill, ids assembled on the device
+        rc = prefill_dev(s, nullptr, depth + 1, s->ws.vids);
+        if (rc == UT_ERR_CONTEXT_OVERFLOW) {
+            // no room for the verify rows: end the stream cleanly (mtp.rs:283-289;
+            // the draft stays counted, as stats.drafted was bumped before)
+            rc = UT_OK;
+            break;
+        }
+        if (rc) break;
+        if (!draft_fn) rc = readback_enqueue(s, s->ws.vids + 1, depth, depth + 1);
+        if (rc == UT_OK) rc = readback_enqueue(s, s->ws.am, depth + 1, 0);
+        if (rc == UT_OK) rc = readback_wait(s, depth + 1, am.data(), 0);
+        if (rc) break;
+        if (!draft_fn) memcpy(drafts.data(), s->pin + kPinIds + depth + 1, (size_t)depth * 4);
+        s->tokens.push_back(next);
+        s->tokens.insert(s->tokens.end(), drafts.begin(), drafts.end());
+        int64_t a = 0;
+        bool end = false;
+        while (a < depth && am[(size_t)a] == drafts[(size_t)a]) {
+            a++;
+            na++;
+            if (em.push(drafts[(size_t)a - 1])) { end = true; break; }
+        }
+        if (end) break;
+        next = am[(size_t)a];
+        if (a < depth) truncate_session(s, pos_before + 1 + a);
+    }
+    if (drafted) *drafted = nd;
+    if (accepted) *accepted = na;
+    ut_session_free(s);
+    return rc ? rc : em.produced;
 }
 
 }  // namespace
@@ -1306,133 +1487,91 @@ int32_t ut_session_truncate(ut_session *s, int64_t len) {
 
 int64_t ut_session_position(const ut_session *s) { return s ? s->pos : UT_ERR_ARG; }
 
-int64_t ut_generate_greedy(ut_model *m, const int32_t *prompt, int64_t n, int64_t max_new,
-                           int32_t *out) {
-    // undertow_core::generate, greedy (core/model.rs:139-185).  Each step is
-    // fed the previous step's argmax on the device, and the next step is
-    // queued before the host waits for the current token.
-    if (!m || !prompt || (max_new > 0 && !out) || max_new < 0) return UT_ERR_ARG;
-    ut_session *s = nullptr;
-    UT_TRY(ut_session_create(m, 0, &s));
-    std::vector<int32_t> am((size_t)n);
-    int32_t rc = prefill_dev(s, prompt, n);
-    if (rc == UT_OK) rc = read_argmax(s, n, am.data());
-    if (rc) { ut_session_free(s); return rc; }
-    int64_t produced = 0;
-    if (max_new == 0) { ut_session_free(s); return 0; }
-    int32_t tok = am[(size_t)n - 1];
-    out[produced++] = tok;
-    bool queued = false;  // a step whose output token is not read yet
-    if (produced < max_new) {
-        rc = prefill_dev(s, nullptr, 1, s->ws.am + (n - 1));
-        if (rc == UT_OK) {
-            s->tokens.push_back(tok);
-            queued = true;
-        } else if (rc == UT_ERR_CONTEXT_OVERFLOW) {
-            rc = UT_OK;  // clean stop at the context end
-        }
-    }
-    while (queued && rc == UT_OK) {
-        rc = readback_enqueue(s, s->ws.am, 1);
-        if (rc) break;
-        bool next_queued = false;
-        if (produced + 1 < max_new) {
-            // fed from ws.am[0], which this step overwrites only after reading it
-            const int32_t r2 = prefill_dev(s, nullptr, 1, s->ws.am);
-            if (r2 == UT_OK) next_queued = true;
-            else if (r2 != UT_ERR_CONTEXT_OVERFLOW) { rc = r2; break; }
-        }
-        rc = readback_wait(s, 1, &tok);
-        if (rc) break;
-        out[produced++] = tok;
-        if (next_queued) s->tokens.push_back(tok);  // the id the queued step was fed
-        queued = next_queued;
-    }
-    ut_session_free(s);
-    return rc ? rc : produced;
+int32_t ut_model_set_stop_ids(ut_model *m, const int32_t *ids, int64_t n) {
+    // DeepseekMoeModel::stop_ids (adapters/undertow-deepseek-moe/src/
+    // loader.rs:304-309): the config's eos ids plus generation_config's
+    if (!m || n < 0 || (n > 0 && !ids)) return UT_ERR_ARG;
+    m->stop_ids.assign(ids, ids + n);
+    return UT_OK;
 }
 
-int64_t ut_generate_mtp(ut_model *m, const int32_t *prompt, int64_t n, int64_t max_new,
-                        int32_t depth, int32_t *out, int64_t *drafted, int64_t *accepted) {
-    // speculative_loop (mtp.rs:263-314) with the native draft head.  Drafts
-    // stay on the device (ws.vids[1..depth]) and feed the verify launch
-    // directly; the host reads the verify argmax and the drafts once per
-    // step, for the accept decision.
-    if (!m || !prompt || (max_new > 0 && !out) || max_new < 0) return UT_ERR_ARG;
+int64_t ut_generate(ut_model *m, const int32_t *prompt, int64_t n, int64_t max_new,
+                    const int32_t *extra_stop_ids, int64_t n_extra, ut_token_fn on_token,
+                    void *user, int32_t *out) {
+    if (!m || !prompt || (max_new > 0 && !out) || max_new < 0 || n_extra < 0 ||
+        (n_extra > 0 && !extra_stop_ids))
+        return UT_ERR_ARG;
+    Emit em{m, extra_stop_ids, n_extra, on_token, user, out, max_new};
+    return gen_greedy(m, prompt, n, em);
+}
+
+int64_t ut_generate_greedy(ut_model *m, const int32_t *prompt, int64_t n, int64_t max_new,
+                           int32_t *out) {
+    return ut_generate(m, prompt, n, max_new, nullptr, 0, nullptr, nullptr, out);
+}
+
+int64_t ut_speculative_loop(ut_model *m, const int32_t *prompt, int64_t n, int64_t max_new,
+                            int32_t depth, const int32_t *extra_stop_ids, int64_t n_extra,
+                            ut_token_fn on_token, void *user, ut_draft_fn draft_fn,
+                            void *draft_user, int32_t *out, int64_t *drafted, int64_t *accepted) {
+    if (drafted) *drafted = 0;
+    if (accepted) *accepted = 0;
+    if (!m || !prompt || (max_new > 0 && !out) || max_new < 0 || n_extra < 0 ||
+        (n_extra > 0 && !extra_stop_ids))
+        return UT_ERR_ARG;
     if (depth < 1 || depth > 3) {
         set_error(m->ctx, "MTP depth %d outside 1..3", depth);
         return UT_ERR_ARG;
     }
-    if (!m->has_mtp) {
+    if (!draft_fn && !m->has_mtp) {
         set_error(m->ctx, "model has no MTP head; use plain generation");
         return UT_ERR_STATE;
     }
-    if (drafted) *drafted = 0;
-    if (accepted) *accepted = 0;
-    if (max_new == 0) return 0;
+    Emit em{m, extra_stop_ids, n_extra, on_token, user, out, max_new};
+    return gen_spec(m, prompt, n, depth, draft_fn, draft_user, em, drafted, accepted);
+}
+
+int64_t ut_generate_mtp(ut_model *m, const int32_t *prompt, int64_t n, int64_t max_new,
+                        int32_t depth, int32_t *out, int64_t *drafted, int64_t *accepted) {
+    return ut_speculative_loop(m, prompt, n, max_new, depth, nullptr, 0, nullptr, nullptr, nullptr,
+                               nullptr, out, drafted, accepted);
+}
+
+int32_t ut_session_draft_logits(ut_session *s, int32_t next_token, float *logits_host,
+                                int32_t *draft_host) {
+    // draft_logits (mtp.rs:74-133) on the session's own MTP state: feeds
+    // positions fed..pos-1 (t_next = the following consumed token, or
+    // next_token for the last) and returns the head's logits for the last
+    if (!s) return UT_ERR_ARG;
+    ut_model *m = s->m;
     ut_ctx *ctx = m->ctx;
-    const int64_t H = m->c.hidden_size;
-    ut_session *s = nullptr;
-    UT_TRY(ut_session_create(m, 0, &s));
-    std::vector<int32_t> am((size_t)(n > depth + 1 ? n : depth + 1));
-    int32_t rc = prefill_dev(s, prompt, n);
-    if (rc == UT_OK) rc = read_argmax(s, n, am.data());
-    if (rc) { ut_session_free(s); return rc; }
-    int32_t next = am[(size_t)n - 1];
-    int64_t produced = 0, nd = 0, na = 0;
-    std::vector<int32_t> toks, drafts((size_t)depth);
-    for (;;) {
-        out[produced++] = next;
-        if (produced >= max_new) break;
-        // ---- draft: feed verified positions fed..pos-1 (mtp.rs:84-121)
-        const int64_t pos = s->pos, fed = s->mtp_fed, pending = pos - fed;
-        toks.clear();
-        for (int64_t i = fed; i < pos; i++) toks.push_back(i + 1 < pos ? s->tokens[(size_t)i + 1] : next);
-        rc = draft_rows_dev(s, toks.data(), -1, s->hidden + fed * H, pending, 1);
-        if (rc) break;
-        s->mtp_fed = pos;
-        // ---- chained drafts (depth > 1): MTP layer on its own last hidden state
-        for (int32_t j = 1; j < depth && rc == UT_OK; j++) {
-            // the MTP layer's output row for the last fed position is in ws.x
-            // (hidden input staged in ws.attn, which is free between layers)
-            const int64_t last = (j == 1 ? pending : 1) - 1;
-            UT_CHECK_HIP(ctx, hipMemcpyAsync(s->ws.attn, s->ws.x + last * H, (size_t)H * 4,
-                                             hipMemcpyDeviceToDevice, ctx->stream));
-            rc = draft_rows_dev(s, nullptr, j, s->ws.attn, 1, 1 + j);
-        }
-        s->mtp_kv.len = s->mtp_fed;  // speculative MTP rows are never kept
-        if (rc) break;
-        nd += depth;
-        // ---- verify [next, d1..dk] in one prefill, ids assembled on the device
-        const int64_t pos_before = s->pos;
-        rc = upload_slot(s, s->ws.vids, &next, 1, kPinIds - 8);
-        if (rc) break;
-        rc = prefill_dev(s, nullptr, depth + 1, s->ws.vids);
-        if (rc == UT_ERR_CONTEXT_OVERFLOW) { rc = UT_OK; break; }
-        if (rc) break;
-        rc = readback_enqueue(s, s->ws.vids + 1, depth, depth + 1);
-        if (rc == UT_OK) rc = readback_enqueue(s, s->ws.am, depth + 1, 0);
-        if (rc == UT_OK) rc = readback_wait(s, depth + 1, am.data(), 0);
-        if (rc) break;
-        memcpy(drafts.data(), s->pin + kPinIds + depth + 1, (size_t)depth * 4);
-        s->tokens.push_back(next);
-        s->tokens.insert(s->tokens.end(), drafts.begin(), drafts.end());
-        int64_t a = 0;
-        bool full = false;
-        while (a < (int64_t)drafts.size() && am[(size_t)a] == drafts[(size_t)a]) {
-            a++;
-            na++;
-            out[produced++] = drafts[(size_t)a - 1];
-            if (produced >= max_new) { full = true; break; }
-        }
-        if (full) break;
-        next = am[(size_t)a];
-        if (a < (int64_t)drafts.size()) truncate_session(s, pos_before + 1 + a);
+    const int64_t H = m->c.hidden_size, V = m->c.vocab_size;
+    if (!m->has_mtp) {
+        set_error(ctx, "model has no MTP head");
+        return UT_ERR_STATE;
     }
-    if (drafted) *drafted = nd;
-    if (accepted) *accepted = na;
-    ut_session_free(s);
-    return rc ? rc : produced;
+    if (next_token < 0 || next_token >= V) {
+        set_error(ctx, "token id %d out of vocab (%lld)", next_token, (long long)V);
+        return UT_ERR_BAD_TOKEN;
+    }
+    const int64_t pos = s->pos, fed = s->mtp_fed;
+    if (pos <= fed) {
+        set_error(ctx, "draft with nothing pending (position %lld, fed %lld)", (long long)pos,
+                  (long long)fed);
+        return UT_ERR_STATE;
+    }
+    std::vector<int32_t> toks;
+    for (int64_t i = fed; i < pos; i++) toks.push_back(i + 1 < pos ? s->tokens[(size_t)i + 1] : next_token);
+    UT_TRY(draft_rows_dev(s, toks.data(), -1, s->hidden + fed * H, pos - fed, 1));
+    s->mtp_fed = pos;
+    if (logits_host)
+        UT_CHECK_HIP(ctx, hipMemcpyAsync(logits_host, s->ws.logits, (size_t)V * 4,
+                                         hipMemcpyDeviceToHost, ctx->stream));
+    int32_t d = 0;
+    UT_TRY(readback_enqueue(s, s->ws.vids + 1, 1));
+    UT_TRY(readback_wait(s, 1, &d));
+    if (draft_host) *draft_host = d;
+    return UT_OK;
 }
 
 int32_t ut_model_synthesize(ut_model *m, uint64_t seed, float init_std, int32_t expert_fmt,

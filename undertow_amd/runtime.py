@@ -15,16 +15,14 @@ missing library raises ``RuntimeError``.
 from __future__ import annotations
 
 import ctypes as C
-import os
 from pathlib import Path
 from typing import Optional
 
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-# UNDERTOW_HIP_LIB selects another build of the library (e.g. a variant
-# compiled with different pipeline depths); the in-tree build by default.
-LIB_PATH = Path(os.environ.get("UNDERTOW_HIP_LIB", str(HERE / "lib" / "libundertow_hip.so")))
+# Always the in-tree build (undertow_amd/_build.py writes it).
+LIB_PATH = HERE / "lib" / "libundertow_hip.so"
 
 F32, INT8, INT4, INFER = 0, 1, 2, -1
 
@@ -80,6 +78,7 @@ _SIGS = [
     ("ut_qtensor_dequantize", _i32, [_vp, _vp, _vp]),
     ("ut_qtensor_matmul", _i32, [_vp, _vp, _vp, _i64, _vp, _i64, _i64]),
     ("ut_qtensor_add_scaled_row", _i32, [_vp, _vp, _i64, _f32, _vp]),
+    ("ut_qtensor_matvec_rows", _i32, [_vp, _vp, _i64, _i64, _vp, _i64, _vp, _i64]),
     ("ut_route", _i32, [_vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _i32, _f32, _vp, _vp]),
     ("ut_expert_table_create", _i32, [_vp, _i64, _i64, _i64, C.POINTER(_vp)]),
     ("ut_expert_table_set", _i32, [_vp, _i64, _vp, _vp, _vp]),
@@ -102,9 +101,18 @@ _SIGS = [
     ("ut_session_prefill", _i32, [_vp, _vp, _i64, _vp, _vp]),
     ("ut_session_truncate", _i32, [_vp, _i64]),
     ("ut_session_position", _i64, [_vp]),
+    ("ut_model_set_stop_ids", _i32, [_vp, _vp, _i64]),
+    ("ut_generate", _i64, [_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp]),
     ("ut_generate_greedy", _i64, [_vp, _vp, _i64, _i64, _vp]),
+    ("ut_speculative_loop", _i64, [_vp, _vp, _i64, _i64, _i32, _vp, _i64, _vp, _vp, _vp, _vp, _vp,
+                                   C.POINTER(_i64), C.POINTER(_i64)]),
     ("ut_generate_mtp", _i64, [_vp, _vp, _i64, _i64, _i32, _vp, C.POINTER(_i64), C.POINTER(_i64)]),
+    ("ut_session_draft_logits", _i32, [_vp, _i32, _vp, _vp]),
 ]
+
+# on_token / draft_fn callbacks of the generation loops (ut_token_fn, ut_draft_fn)
+TOKEN_FN = C.CFUNCTYPE(_i32, _vp, _i32)
+DRAFT_FN = C.CFUNCTYPE(_i32, _vp, C.POINTER(_i32), _i64, _i32, _i32, C.POINTER(_i32))
 
 EXPORTED = [s[0] for s in _SIGS]
 
@@ -296,6 +304,11 @@ class QTensor:
         self.ctx.check(lib().ut_qtensor_add_scaled_row(self.ctx.handle, self._h, row, factor,
                                                        _ptr(acc)))
 
+    def matvec_rows(self, row0: int, nrows: int, x, out) -> None:
+        """QTensor::matvec_rows: out [nrows] <- rows [row0, row0+nrows) . x [in_dim]."""
+        self.ctx.check(lib().ut_qtensor_matvec_rows(self.ctx.handle, self._h, row0, nrows,
+                                                    _ptr(x), x.numel(), _ptr(out), out.numel()))
+
 
 def route(ctx: Context, logits, bias, top_k: int, n_group: int, topk_group: int,
           norm_topk_prob: bool, routed_scaling_factor: float):
@@ -445,12 +458,64 @@ class Model:
     def forward(self, ids) -> np.ndarray:
         return self.session().prefill(ids)
 
+    def set_stop_ids(self, ids) -> None:
+        """DeepseekMoeModel::stop_ids (loader.rs:304-309)."""
+        a = np.ascontiguousarray(ids, np.int32)
+        self.ctx.check(lib().ut_model_set_stop_ids(self._h, a.ctypes.data if a.size else None,
+                                                   a.size))
+
     def generate_greedy(self, prompt, max_new: int) -> list:
         p = np.ascontiguousarray(prompt, np.int32)
         out = np.zeros(max(max_new, 1), np.int32)
         n = lib().ut_generate_greedy(self._h, p.ctypes.data, p.size, max_new, out.ctypes.data)
         self.ctx.check(int(n))
         return out[:n].tolist()
+
+    def generate(self, prompt, max_new: int, extra_stop_ids=(), on_token=None) -> list:
+        """undertow_core::generate, greedy: stops after a stop id (emitted),
+        when on_token(id) returns False, or at max_new tokens."""
+        p = np.ascontiguousarray(prompt, np.int32)
+        out = np.zeros(max(max_new, 1), np.int32)
+        st = np.ascontiguousarray(extra_stop_ids, np.int32)
+        cb = TOKEN_FN(lambda _u, t: int(bool(on_token(t)))) if on_token else None
+        n = lib().ut_generate(self._h, p.ctypes.data, p.size, max_new,
+                              st.ctypes.data if st.size else None, st.size,
+                              C.cast(cb, _vp) if cb else None, None, out.ctypes.data)
+        self.ctx.check(int(n))
+        return out[:n].tolist()
+
+    def speculative_loop(self, prompt, max_new: int, depth: int = 1, draft_fn=None,
+                         extra_stop_ids=(), on_token=None):
+        """speculative_loop (mtp.rs:263-314).  draft_fn(tokens, next, depth)
+        -> list of `depth` ids; None drafts with the native MTP head.
+        Returns (tokens, drafted, accepted)."""
+        p = np.ascontiguousarray(prompt, np.int32)
+        out = np.zeros(max(max_new, 1), np.int32)
+        st = np.ascontiguousarray(extra_stop_ids, np.int32)
+        tcb = TOKEN_FN(lambda _u, t: int(bool(on_token(t)))) if on_token else None
+        err = []
+
+        def _draft(_u, toks, n, nxt, dep, dst):
+            try:
+                ids = list(draft_fn([toks[i] for i in range(n)], nxt, dep))
+                for i in range(dep):
+                    dst[i] = int(ids[i])
+                return 0
+            except Exception as e:  # surfaced after the call
+                err.append(e)
+                return UT_ERR_STATE
+
+        dcb = DRAFT_FN(_draft) if draft_fn else None
+        d, a = _i64(), _i64()
+        n = lib().ut_speculative_loop(self._h, p.ctypes.data, p.size, max_new, depth,
+                                      st.ctypes.data if st.size else None, st.size,
+                                      C.cast(tcb, _vp) if tcb else None, None,
+                                      C.cast(dcb, _vp) if dcb else None, None,
+                                      out.ctypes.data, C.byref(d), C.byref(a))
+        if err:
+            raise err[0]
+        self.ctx.check(int(n))
+        return out[:n].tolist(), d.value, a.value
 
     def generate_mtp(self, prompt, max_new: int, depth: int = 1):
         p = np.ascontiguousarray(prompt, np.int32)
@@ -494,6 +559,16 @@ class Session:
 
     def decode(self, tok: int):
         return self.prefill([tok])[0]
+
+    def draft_logits(self, next_token: int):
+        """draft_logits (mtp.rs:74-133) on this session's MTP state ->
+        (logits [vocab], draft id)."""
+        V = self.model.cfg["vocab_size"]
+        logits = np.zeros(V, np.float32)
+        d = _i32()
+        self.model.ctx.check(lib().ut_session_draft_logits(self._h, next_token,
+                                                           logits.ctypes.data, C.byref(d)))
+        return logits, d.value
 
     def truncate(self, n: int) -> None:
         self.model.ctx.check(lib().ut_session_truncate(self._h, n))
