@@ -165,6 +165,20 @@ int32_t ut_moe_experts(ut_ctx *ctx, const ut_expert_table *tbl, const int32_t *i
                        const float *weights_dev, int64_t rows, int32_t top_k, const float *x_dev,
                        float *out_dev);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops and harnesses that
+ * forbid hipMalloc): ut_moe_experts with the same arguments and results,
+ * allocating nothing.  Its working memory (slot plan, h, digits, down
+ * outputs) is a fixed 32 MiB array per device in the library's code
+ * object, looked up when the context is created; calls whose working set
+ * exceeds it (about top_k * 4 rows * (hidden + inter) * 4 bytes, e.g.
+ * top_k 64 at hidden 7168) return UT_ERR_ARG.  Every call on one GPU shares
+ * that array, so calls that overlap on a GPU (other streams or contexts)
+ * race; calls in stream order do not. */
+int32_t ut_moe_experts_noalloc(ut_ctx *ctx, const ut_expert_table *tbl, const int32_t *ids_dev,
+                               const float *weights_dev, int64_t rows, int32_t top_k,
+                               const float *x_dev, float *out_dev);
+
 /* Route then run the routed experts, as moe_forward does per row
  * (adapters/undertow-deepseek-moe/src/model.rs:210-281: route at :210-216,
  * then the expert body): the choices of ut_route over logits_dev [rows, E]

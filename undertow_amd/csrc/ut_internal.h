@@ -72,6 +72,10 @@ struct ut_ctx {
     int32_t *dev_err = nullptr;
     // Split-K GEMV partial totals (allocated on first use).
     void *splitk = nullptr;
+    // Device address of this device's copy of the expert block's fixed
+    // working array (ut_moe_experts_noalloc), from hipGetSymbolAddress at
+    // context creation.
+    void *noalloc_scratch = nullptr;
     // Handle lifetime: models hold a reference on their context and
     // sessions on their model, so the handles may be released in any order.
     int refs = 1;
@@ -108,8 +112,12 @@ void timing_end(ut_ctx *ctx, int token);
 int32_t launch_check(ut_ctx *ctx, const char *name);
 void ctx_retain(ut_ctx *ctx);
 void ctx_release(ut_ctx *ctx);
-// The context's device error flag (allocated on first use) and its check.
+// The context's device error flag (allocated when the context is created)
+// and its check.
 int32_t device_error_flag(ut_ctx *ctx, int32_t **flag);
+// Looks up this device's copy of the expert block's fixed working array
+// (hipGetSymbolAddress, the device current) into ctx->noalloc_scratch.
+int32_t moe_noalloc_scratch_init(ut_ctx *ctx);
 // Split-K partials buffer of the context (kSplitKPartBytes), allocated on
 // first use.
 constexpr int64_t kSplitKPartBytes = int64_t(8) << 20;

@@ -1666,27 +1666,16 @@ void ut_expert_table_free(ut_expert_table *t) {
     delete t;
 }
 
-int32_t ut_moe_experts(ut_ctx *ctx, const ut_expert_table *tbl, const int32_t *ids_dev,
-                       const float *weights_dev, int64_t rows, int32_t top_k, const float *x_dev,
-                       float *out_dev) {
-    if (!ctx || !tbl || !ids_dev || !weights_dev || !x_dev || !out_dev || rows < 0 || top_k <= 0 ||
-        top_k > 64) {
-        set_error(ctx, "ut_moe_experts: bad argument");
-        return UT_ERR_ARG;
-    }
-    if (tbl->fmt < 0) {
-        set_error(ctx, "ut_moe_experts: empty expert table");
-        return UT_ERR_BAD_EXPERT;
-    }
-    if (rows == 0) return UT_OK;
+}  // extern "C"
+
+namespace {
+
+// The routed-expert block over rows already routed, in passes of up to four
+// rows, with `scratch` (moe_layout's bytes at four rows) as working memory.
+int32_t moe_experts_rows(ut_ctx *ctx, const ut_expert_table *tbl, const int32_t *ids_dev,
+                         const float *weights_dev, int64_t rows, int32_t top_k, const float *x_dev,
+                         float *out_dev, void *scratch, int32_t *flag) {
     const int64_t maxM = 4;
-    const int64_t slots = moe_slots((int)maxM, top_k, tbl->n, -1);
-    ScratchPlan plan;
-    plan.add(moe_layout(maxM, top_k, slots, tbl->hidden, tbl->inter, tbl->fmt).total);
-    std::vector<void *> ptrs;
-    UT_TRY(scratch_acquire(ctx, plan, ptrs));
-    int32_t *flag = nullptr;
-    UT_TRY(device_error_flag(ctx, &flag));
     for (int64_t s0 = 0; s0 < rows; s0 += maxM) {
         MoeCall c;
         c.fmt = tbl->fmt;
@@ -1702,9 +1691,95 @@ int32_t ut_moe_experts(ut_ctx *ctx, const ut_expert_table *tbl, const int32_t *i
         c.out = out_dev + s0 * tbl->hidden;
         c.ldo = tbl->hidden;
         c.err_flag = flag;
-        UT_TRY(moe_pass(ctx, c, ptrs[0]));
+        UT_TRY(moe_pass(ctx, c, scratch));
     }
     return UT_OK;
+}
+
+int32_t moe_experts_check(ut_ctx *ctx, const char *fn, const ut_expert_table *tbl,
+                          const int32_t *ids_dev, const float *weights_dev, int64_t rows,
+                          int32_t top_k, const float *x_dev, float *out_dev) {
+    if (!ctx || !tbl || !ids_dev || !weights_dev || !x_dev || !out_dev || rows < 0 || top_k <= 0 ||
+        top_k > 64) {
+        set_error(ctx, "%s: bad argument", fn);
+        return UT_ERR_ARG;
+    }
+    if (tbl->fmt < 0) {
+        set_error(ctx, "%s: empty expert table", fn);
+        return UT_ERR_BAD_EXPERT;
+    }
+    return UT_OK;
+}
+
+}  // namespace
+
+// Working memory of ut_moe_experts_noalloc: a fixed array in the code
+// object, one copy per device (each GPU the library runs on holds it until
+// the process ends).  Host code never names it: kernels get the address
+// that hipGetSymbolAddress returned for the device (ctx->noalloc_scratch).
+constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) unsigned char noalloc_scratch[kNoAllocScratchBytes];
+
+int32_t ut::moe_noalloc_scratch_init(ut_ctx *ctx) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(noalloc_scratch));
+    if (e != hipSuccess || !p) {
+        (void)hipGetLastError();
+        set_error(ctx, "hipGetSymbolAddress of the expert block's working array failed: %s",
+                  hipGetErrorString(e));
+        return UT_ERR_HIP;
+    }
+    ctx->noalloc_scratch = p;
+    return UT_OK;
+}
+
+extern "C" {
+
+int32_t ut_moe_experts(ut_ctx *ctx, const ut_expert_table *tbl, const int32_t *ids_dev,
+                       const float *weights_dev, int64_t rows, int32_t top_k, const float *x_dev,
+                       float *out_dev) {
+    UT_TRY(moe_experts_check(ctx, "ut_moe_experts", tbl, ids_dev, weights_dev, rows, top_k, x_dev,
+                             out_dev));
+    if (rows == 0) return UT_OK;
+    const int64_t maxM = 4;
+    const int64_t slots = moe_slots((int)maxM, top_k, tbl->n, -1);
+    ScratchPlan plan;
+    plan.add(moe_layout(maxM, top_k, slots, tbl->hidden, tbl->inter, tbl->fmt).total);
+    std::vector<void *> ptrs;
+    UT_TRY(scratch_acquire(ctx, plan, ptrs));
+    int32_t *flag = nullptr;
+    UT_TRY(device_error_flag(ctx, &flag));
+    return moe_experts_rows(ctx, tbl, ids_dev, weights_dev, rows, top_k, x_dev, out_dev, ptrs[0],
+                            flag);
+}
+
+int32_t ut_moe_experts_noalloc(ut_ctx *ctx, const ut_expert_table *tbl, const int32_t *ids_dev,
+                               const float *weights_dev, int64_t rows, int32_t top_k,
+                               const float *x_dev, float *out_dev) {
+    // ut_moe_experts without any allocation: the same kernels over the
+    // device's fixed working array.  Every byte a pass reads from it was
+    // written earlier in the same pass (slot plan, h and its partial maxima,
+    // digits, down outputs), so nothing needs clearing between calls.
+    UT_TRY(moe_experts_check(ctx, "ut_moe_experts_noalloc", tbl, ids_dev, weights_dev, rows,
+                             top_k, x_dev, out_dev));
+    if (!ctx->noalloc_scratch || !ctx->dev_err) {
+        set_error(ctx, "ut_moe_experts_noalloc: context set-up incomplete");
+        return UT_ERR_STATE;
+    }
+    const int64_t maxM = 4;
+    const int64_t slots = moe_slots((int)maxM, top_k, tbl->n, -1);
+    const size_t need = moe_layout(maxM, top_k, slots, tbl->hidden, tbl->inter, tbl->fmt).total;
+    if (need > kNoAllocScratchBytes) {
+        set_error(ctx,
+                  "ut_moe_experts_noalloc: working set of %zu bytes (top_k %d, hidden %lld, "
+                  "inter %lld) exceeds the fixed %zu-byte array; use ut_moe_experts",
+                  need, top_k, (long long)tbl->hidden, (long long)tbl->inter,
+                  kNoAllocScratchBytes);
+        return UT_ERR_ARG;
+    }
+    if (rows == 0) return UT_OK;
+    return moe_experts_rows(ctx, tbl, ids_dev, weights_dev, rows, top_k, x_dev, out_dev,
+                            ctx->noalloc_scratch, ctx->dev_err);
 }
 
 int32_t ut_moe_route_experts(ut_ctx *ctx, const ut_expert_table *tbl, const float *logits_dev,

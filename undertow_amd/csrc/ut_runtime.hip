@@ -263,6 +263,15 @@ int32_t ut_ctx_create(int32_t device, ut_ctx **out) {
     c->stream = c->own_stream;
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, device) == hipSuccess) c->multiprocessors = prop.multiProcessorCount;
+    // set-up that later calls must not repeat (ut_moe_experts_noalloc
+    // allocates nothing): the error flag and the fixed working array's address
+    int32_t *flag = nullptr;
+    int32_t rc = device_error_flag(c, &flag);
+    if (rc == UT_OK) rc = moe_noalloc_scratch_init(c);
+    if (rc != UT_OK) {
+        ctx_release(c);
+        return rc;
+    }
     *out = c;
     return UT_OK;
 }

@@ -84,6 +84,7 @@ _SIGS = [
     ("ut_expert_table_set", _i32, [_vp, _i64, _vp, _vp, _vp]),
     ("ut_expert_table_free", None, [_vp]),
     ("ut_moe_experts", _i32, [_vp, _vp, _vp, _vp, _i64, _i32, _vp, _vp]),
+    ("ut_moe_experts_noalloc", _i32, [_vp, _vp, _vp, _vp, _i64, _i32, _vp, _vp]),
     ("ut_moe_route_experts", _i32, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _f32, _vp,
                                     _vp, _vp, _vp]),
     ("ut_argmax_rows", _i32, [_vp, _vp, _i64, _i64, _vp]),
@@ -395,6 +396,12 @@ class ExpertTable:
         self.ctx.check(lib().ut_moe_experts(self.ctx.handle, self._h, _ptr(ids), _ptr(weights),
                                             rows, k, _ptr(x), _ptr(out)))
         return out
+
+    def moe_experts_noalloc(self, ids, weights, x, out) -> None:
+        """ut_moe_experts into a caller's `out`, allocating nothing."""
+        rows, k = ids.shape
+        self.ctx.check(lib().ut_moe_experts_noalloc(self.ctx.handle, self._h, _ptr(ids),
+                                                    _ptr(weights), rows, k, _ptr(x), _ptr(out)))
 
     def moe_route_experts(self, logits, bias, x, k, n_group, topk_group, norm_topk_prob,
                           routed_scaling_factor):
