@@ -243,16 +243,43 @@ def mla_bench(U, ctx, torch, steps, warmup, Ts=(1024, 4096, 32768), Rs=(1, 2, 4)
 
 
 # --------------------------------------------------------- CPU baseline --
-def cpu_baseline(cfg, seconds=10.0):
+def host_cpu() -> dict:
+    """The host the CPU legs run on: model name, ISA flags, cores."""
+    info = {"model": None, "flags": [], "nproc": os.cpu_count(),
+            "affinity": len(os.sched_getaffinity(0))}
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name") and info["model"] is None:
+                info["model"] = line.split(":", 1)[1].strip()
+            if line.startswith("flags"):
+                fl = set(line.split(":", 1)[1].split())
+                info["flags"] = [f for f in ("avx2", "fma", "avx512f", "avx512bw", "avx512_vnni")
+                                 if f in fl]
+                break
+    except OSError:
+        pass
+    return info
+
+
+def _timed(fn, min_s: float, min_reps: int = 3):
+    fn()
+    reps, t0 = 0, time.perf_counter()
+    while reps < min_reps or time.perf_counter() - t0 < min_s:
+        fn()
+        reps += 1
+    return (time.perf_counter() - t0) / reps, reps
+
+
+def cpu_baseline_c2(cfg, seconds):
     """The reference CPU expert block (AVX-512/AVX2 restatement of
     avx512::matmul_i4 with the rayon split, oracle/cpu_baseline.c) on the
-    host's cores, M=1, on a 16-expert host pool with the same algorithmic
-    bytes per step."""
+    host's cores, M=1, over a 128-expert int4 host pool (2.8 GB, beyond any
+    host cache), the same algorithmic bytes per step as the GPU leg."""
     from oracle import oracle as O
     from undertow_amd.configs import expert_bytes
     L = O.cpu_baseline_lib()
     H, I, k = cfg["hidden"], cfg["inter"], cfg["top_k"]
-    n = 16
+    n = 128
     rng = np.random.default_rng(5)
     gq = rng.integers(0, 256, (n, I, H // 2), dtype=np.uint8)
     uq = rng.integers(0, 256, (n, I, H // 2), dtype=np.uint8)
@@ -271,18 +298,102 @@ def cpu_baseline(cfg, seconds=10.0):
         L.ucb_moe_experts(2, H, I, vp(gq), vp(gs), vp(uq), vp(us), vp(dq), vp(ds), 1, k, ids, w,
                           x.reshape(-1), out.reshape(-1), threads)
 
-    step()
-    t0 = time.perf_counter()
-    steps = 0
-    while time.perf_counter() - t0 < seconds or steps < 5:
-        step()
-        steps += 1
-    dt = (time.perf_counter() - t0) / steps
+    dt, steps = _timed(step, seconds, 5)
     isa = {2: "avx512", 1: "avx2", 0: "scalar"}.get(int(L.ucb_isa()), "?")
     return {"value": k * expert_bytes(H, I, 4) / dt / 1e9, "unit": "GB/s", "cores": threads,
-            "kind": "port",
-            "sample": f"{steps} steps of the config-2 expert block at M=1 (top-8 over a 16-expert "
-                      f"int4 host pool, {isa}, {threads} threads), {dt * 1e3:.2f} ms/step"}
+            "kind": "port", "isa": isa, "ms_per_step": dt * 1e3,
+            "sample": f"{steps} steps of the config-2 expert block at M=1 (top-8 over a 128-expert "
+                      f"int4 host pool of 2.8 GB, {isa}, {threads} threads), {dt * 1e3:.2f} ms/step"}
+
+
+def cpu_baseline_c3(seconds_each, Ts=(1024, 4096, 32768), Rs=(1, 2, 4)):
+    """Config 3 on the host: the absorbed MLA loops (attention.rs:202-236),
+    one task per (row, head) over the host's cores, 128 heads, latent 512 +
+    rope 64, at every (R, T)."""
+    from oracle import oracle as O
+    L = O.cpu_baseline_lib()
+    H, Ld, P = 128, 512, 64
+    rng = np.random.default_rng(3)
+    Tmax = max(Ts)
+    lat = rng.standard_normal((Tmax, Ld)).astype(np.float32)
+    kr = rng.standard_normal((Tmax, P)).astype(np.float32)
+    threads = int(L.ucb_max_threads())
+    res = {}
+    for R in Rs:
+        qabs = rng.standard_normal((R, H, Ld)).astype(np.float32)
+        qr = rng.standard_normal((R, H, P)).astype(np.float32)
+        out = np.zeros((R, H, Ld), np.float32)
+        for T in Ts:
+            def call():
+                L.ucb_mla_attend(qabs.reshape(-1), qr.reshape(-1), lat.reshape(-1), kr.reshape(-1),
+                                 R, H, Ld, P, T - R, 0.0721688, out.reshape(-1), threads)
+            dt, reps = _timed(call, seconds_each, 2)
+            flops = 2 * H * (Ld + P + Ld) * (R * T - R * (R - 1) // 2)
+            res[f"R{R}_T{T}"] = {"us_per_call": round(dt * 1e6, 1), "reps": reps,
+                                 "gflops": round(flops / dt / 1e9, 2)}
+    return {"unit": "us per call", "cores": threads, "kind": "port", "configs": res}
+
+
+def cpu_baseline_model(name, cfg, prompt_len, new_tokens, depths, experts=None):
+    """Configs 1 and 4 end to end on the host: the oracle's model code over
+    the restated dispatched kernels (libcpu_model.so: QTensor::matmul on
+    AVX-512/AVX2 with the rayon split, attention tasks per (row, head)),
+    greedy and MTP decode tok/s at batch 1, prefill excluded."""
+    from oracle import oracle as O
+    CM = O.cpu_model_lib()
+    over = dict(cfg, init_std=0.02)
+    if experts:
+        over.update(n_routed_experts=experts)
+    sp = O.default_spec(**over)
+    t0 = time.perf_counter()
+    if name == "c1":
+        ck = O.Checkpoint(sp, L=CM)  # the reference's own generator, then converted
+        ck.convert(O.INT4, O.INT8)
+    else:
+        ck = O.Checkpoint.synthesize(sp, 4242, 0.02, O.INT4, O.INT8, L=CM)
+    t_make = time.perf_counter() - t0
+    m = O.Model(ck)
+    rng = np.random.default_rng(42)
+    prompt = rng.integers(0, cfg["vocab_size"], prompt_len).tolist()
+    t0 = time.perf_counter()
+    m.session().prefill(prompt)
+    t_prefill = time.perf_counter() - t0
+    res = {"prompt": prompt_len, "new_tokens": new_tokens, "make_s": round(t_make, 2),
+           "prefill_s": round(t_prefill, 3), "cores": int(O.cpu_baseline_lib().ucb_max_threads()),
+           "kind": "port"}
+    t0 = time.perf_counter()
+    toks = m.generate(prompt, new_tokens)
+    dt = time.perf_counter() - t0 - t_prefill
+    res["greedy_tok_s"] = round(len(toks) / dt, 3)
+    for d in depths:
+        t0 = time.perf_counter()
+        mt, drafted, accepted = m.speculative_loop(prompt, new_tokens, depth=d)
+        dt = time.perf_counter() - t0 - t_prefill
+        res[f"mtp{d}"] = {"tok_s": round(len(mt) / dt, 3), "drafted": drafted,
+                          "accepted": accepted, "lossless": mt == toks}
+    if experts:
+        res["note"] = (f"{experts}-expert pool per layer: the per-token weight bytes are the "
+                       f"config's (top-{cfg['num_experts_per_tok']} per layer), the pool is "
+                       f"bounded to keep host synthesis short")
+    return res
+
+
+def cpu_baseline(cfg2, seconds=10.0):
+    host = host_cpu()
+    log(f"CPU baseline host: {host}")
+    head = cpu_baseline_c2(cfg2, seconds)
+    log(f"CPU config 2: {head['value']:.1f} GB/s")
+    head["host"] = host
+    legs = {}
+    legs["c3"] = cpu_baseline_c3(1.0)
+    log(f"CPU config 3: {json.dumps(legs['c3'])}")
+    from undertow_amd.configs import C1, C4
+    legs["c1"] = cpu_baseline_model("c1", C1, 16, 64, (1,))
+    log(f"CPU config 1: {json.dumps(legs['c1'])}")
+    legs["c4"] = cpu_baseline_model("c4", C4, 32, 8, (1,), experts=32)
+    log(f"CPU config 4: {json.dumps(legs['c4'])}")
+    head["legs"] = legs
+    return head
 
 
 # ------------------------------------------------------------------ MTP --

@@ -107,6 +107,22 @@ int32_t ut_qtensor_format(const ut_qtensor *qt);
 int64_t ut_qtensor_out_dim(const ut_qtensor *qt);
 int64_t ut_qtensor_in_dim(const ut_qtensor *qt);
 int64_t ut_qtensor_nbytes(const ut_qtensor *qt);
+/* QTensor::quantize (undertow-quant/src/qtensor.rs:142-213) on the device:
+ * the f32 matrix w_dev [out_dim, in_dim] becomes a new QTensor of format
+ * fmt with per-row s = max|w|/qmax (qmax 127 / 7) and codes
+ * round(w/s) (half away from zero) clamped to +-qmax; a row of zeros keeps
+ * s = 0.  Bit-exact with the reference.  A non-finite weight is the
+ * reference's Err: UT_ERR_FORMAT, the message naming its flat index, row
+ * and column (the smallest such index). */
+int32_t ut_qtensor_quantize(ut_ctx *ctx, int32_t fmt, const float *w_dev, int64_t out_dim,
+                            int64_t in_dim, ut_qtensor **out);
+/* The QTensor's stored data read back to the host, as TensorEntry::
+ * from_qtensor reads a QTensor's payload and scales to write them
+ * (undertow-io/src/writer.rs:35-64): payload_host gets payload_len bytes
+ * (must equal QuantFormat::payload_bytes), scales_host out_dim floats
+ * (NULL for f32 tensors).  Synchronises the context's stream. */
+int32_t ut_qtensor_download(ut_ctx *ctx, const ut_qtensor *qt, void *payload_host,
+                            int64_t payload_len, float *scales_host);
 /* QTensor::dequantize (qtensor.rs:265-272): out[o,i] = fl(scale[o]*q[o,i])
  * (bit-exact), f32 tensors copied.  out_dev holds out_dim*in_dim floats. */
 int32_t ut_qtensor_dequantize(ut_ctx *ctx, const ut_qtensor *qt, float *out_dev);

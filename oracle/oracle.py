@@ -60,15 +60,32 @@ class Spec(C.Structure):
 
 _lib = None
 _cb = None
+_cm = None
 
 
 def lib():
+    """The scalar restatement (the parity checker)."""
     global _lib
     if _lib is None:
-        path = LIB_DIR / "liboracle.so"
-        if not path.exists():
-            build()
-        L = C.CDLL(str(path))
+        _lib = _load("liboracle.so")
+    return _lib
+
+
+def cpu_model_lib():
+    """The same model code over the restated dispatched SIMD kernels
+    (libcpu_model.so): the timed CPU baseline, never a parity checker."""
+    global _cm
+    if _cm is None:
+        _cm = _load("libcpu_model.so")
+    return _cm
+
+
+def _load(name):
+    path = LIB_DIR / name
+    if not path.exists():
+        build()
+    L = C.CDLL(str(path))
+    if True:
         L.uto_pcg32_fill.argtypes = [C.c_uint64, C.c_uint64, C.c_int, C.c_float, _f32p, C.c_int64]
         L.uto_payload_bytes.restype = C.c_int64
         L.uto_payload_bytes.argtypes = [C.c_int, C.c_int64, C.c_int64]
@@ -144,8 +161,7 @@ def lib():
         L.uto_mtp_state_free.argtypes = [C.c_void_p]
         L.uto_draft_logits.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, _f32p,
                                        C.c_void_p]
-        _lib = L
-    return _lib
+    return L
 
 
 def cpu_baseline_lib():
@@ -325,15 +341,17 @@ DRAFT_FN = C.CFUNCTYPE(C.c_int32, C.c_void_p, C.POINTER(C.c_int32), C.c_int64, C
 class Checkpoint:
     """A generated (optionally converted) checkpoint held by the C oracle."""
 
-    def __init__(self, spec: Spec, _handle=None):
+    def __init__(self, spec: Spec, _handle=None, L=None):
+        self.L = L or lib()
         self.spec = spec
-        self._h = _handle if _handle is not None else lib().uto_generate(C.byref(spec))
+        self._h = _handle if _handle is not None else self.L.uto_generate(C.byref(spec))
 
     @classmethod
     def synthesize(cls, spec: Spec, seed: int, std: float, expert_fmt: int,
-                   dense_fmt: int) -> "Checkpoint":
+                   dense_fmt: int, L=None) -> "Checkpoint":
         """Seeded weights at large widths in converted form (uto_ckpt_synthesize)."""
-        return cls(spec, lib().uto_ckpt_synthesize(C.byref(spec), seed, std, expert_fmt, dense_fmt))
+        L = L or lib()
+        return cls(spec, L.uto_ckpt_synthesize(C.byref(spec), seed, std, expert_fmt, dense_fmt), L)
 
     @classmethod
     def from_tensors(cls, spec: Spec, tensors) -> "Checkpoint":
@@ -355,7 +373,7 @@ class Checkpoint:
     def raw_tensors(self):
         """Yield (name, fmt, shape, payload address, nbytes, scales address|None)
         without copying (valid while the checkpoint lives)."""
-        L = lib()
+        L = self.L
         name = C.create_string_buffer(256)
         fmt = C.c_int32()
         shape = (C.c_int64 * 2)()
@@ -370,22 +388,22 @@ class Checkpoint:
 
     def __del__(self):
         if getattr(self, "_h", None):
-            lib().uto_ckpt_free(self._h)
+            self.L.uto_ckpt_free(self._h)
             self._h = None
 
     def safetensors_bytes(self) -> bytes:
-        n = lib().uto_ckpt_safetensors(self._h, None, 0)
+        n = self.L.uto_ckpt_safetensors(self._h, None, 0)
         buf = (C.c_uint8 * n)()
-        lib().uto_ckpt_safetensors(self._h, buf, n)
+        self.L.uto_ckpt_safetensors(self._h, buf, n)
         return bytes(buf)
 
     def convert(self, expert_fmt: int, dense_fmt: int) -> None:
-        if lib().uto_ckpt_convert(self._h, expert_fmt, dense_fmt) != 0:
+        if self.L.uto_ckpt_convert(self._h, expert_fmt, dense_fmt) != 0:
             raise ValueError("conversion failed (non-finite weight)")
 
     def tensors(self):
         """Yield (name, fmt, shape, payload ndarray, scales ndarray|None)."""
-        L = lib()
+        L = self.L
         name = C.create_string_buffer(256)
         fmt = C.c_int32()
         shape = (C.c_int64 * 2)()
@@ -407,13 +425,14 @@ class Model:
     def __init__(self, ckpt: Checkpoint):
         self.ckpt = ckpt  # keeps the tensors alive
         self.spec = ckpt.spec
-        self._h = lib().uto_model_new(ckpt._h, C.byref(ckpt.spec))
+        self.L = ckpt.L  # the library the checkpoint was made with
+        self._h = self.L.uto_model_new(ckpt._h, C.byref(ckpt.spec))
         if not self._h:
             raise ValueError("oracle model build failed")
 
     def __del__(self):
         if getattr(self, "_h", None):
-            lib().uto_model_free(self._h)
+            self.L.uto_model_free(self._h)
             self._h = None
 
     def session(self, path: int = 0) -> "Session":
@@ -425,7 +444,7 @@ class Model:
     def greedy_decode(self, prompt, max_new: int) -> list:
         p = np.asarray(prompt, np.int32)
         out = np.zeros(max(max_new, 1), np.int32)
-        n = lib().uto_greedy_decode(self._h, p, p.size, max_new, out)
+        n = self.L.uto_greedy_decode(self._h, p, p.size, max_new, out)
         if n < 0:
             raise RuntimeError(f"greedy_decode error {n}")
         return list(prompt) + out[:n].tolist()
@@ -436,7 +455,7 @@ class Model:
         out = np.zeros(max(max_new, 1), np.int32)
         st = np.ascontiguousarray(stop_ids, np.int32)
         cb = TOKEN_FN(lambda _u, t: int(bool(on_token(t)))) if on_token else None
-        n = lib().uto_generate_greedy(self._h, p, p.size, max_new,
+        n = self.L.uto_generate_greedy(self._h, p, p.size, max_new,
                                       st.ctypes.data if st.size else None, st.size,
                                       C.cast(cb, C.c_void_p) if cb else None, None, out)
         if n < 0:
@@ -466,7 +485,7 @@ class Model:
 
         dcb = DRAFT_FN(_draft) if draft_fn else None
         d, a = C.c_int64(), C.c_int64()
-        n = lib().uto_speculative_loop(self._h, p, p.size, max_new, depth,
+        n = self.L.uto_speculative_loop(self._h, p, p.size, max_new, depth,
                                        st.ctypes.data if st.size else None, st.size,
                                        C.cast(tcb, C.c_void_p) if tcb else None, None,
                                        C.cast(dcb, C.c_void_p) if dcb else None, None, out,
@@ -481,7 +500,7 @@ class Model:
         p = np.asarray(prompt, np.int32)
         out = np.zeros(max_new, np.int32)
         d, a = C.c_int64(), C.c_int64()
-        n = lib().uto_generate_mtp(self._h, p, p.size, max_new, out, C.byref(d), C.byref(a))
+        n = self.L.uto_generate_mtp(self._h, p, p.size, max_new, out, C.byref(d), C.byref(a))
         if n < 0:
             raise RuntimeError(f"generate_mtp error {n}")
         return out[:n].tolist(), d.value, a.value
@@ -494,21 +513,22 @@ class ContextOverflow(RuntimeError):
 class Session:
     def __init__(self, model: Model, path: int = 0):
         self.model = model
-        self._h = lib().uto_session_new(model._h, path)
+        self.L = model.L
+        self._h = self.L.uto_session_new(model._h, path)
 
     def __del__(self):
         if getattr(self, "_mtp", None):
-            lib().uto_mtp_state_free(self._mtp)
+            self.L.uto_mtp_state_free(self._mtp)
             self._mtp = None
         if getattr(self, "_h", None):
-            lib().uto_session_free(self._h)
+            self.L.uto_session_free(self._h)
             self._h = None
 
     def prefill(self, ids) -> np.ndarray:
         ids = np.asarray(ids, np.int32)
         V = self.model.spec.vocab_size
         out = np.zeros((ids.size, V), np.float32)
-        rc = lib().uto_session_prefill(self._h, ids, ids.size, _vp(out))
+        rc = self.L.uto_session_prefill(self._h, ids, ids.size, _vp(out))
         if rc == -2:
             raise ContextOverflow("context overflow")
         if rc != 0:
@@ -522,19 +542,19 @@ class Session:
         """draft_logits (mtp.rs:74-133) on this session's MtpState ->
         (logits [vocab], last MTP-layer output row [hidden])."""
         if getattr(self, "_mtp", None) is None:
-            self._mtp = lib().uto_mtp_state_new()
+            self._mtp = self.L.uto_mtp_state_new()
         V, Hd = self.model.spec.vocab_size, self.model.spec.hidden_size
         logits = np.zeros(V, np.float32)
         row = np.zeros(Hd, np.float32)
-        rc = lib().uto_draft_logits(self.model._h, self._h, self._mtp, next_token, logits,
+        rc = self.L.uto_draft_logits(self.model._h, self._h, self._mtp, next_token, logits,
                                     row.ctypes.data)
         if rc != 0:
             raise RuntimeError(f"draft_logits error {rc}")
         return logits, row
 
     def truncate(self, n: int) -> None:
-        lib().uto_session_truncate(self._h, n)
+        self.L.uto_session_truncate(self._h, n)
 
     @property
     def position(self) -> int:
-        return int(lib().uto_session_position(self._h))
+        return int(self.L.uto_session_position(self._h))

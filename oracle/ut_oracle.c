@@ -164,9 +164,25 @@ void uto_dequantize(int fmt, const void *payload, const float *scales,
                            out + r * in_dim);
 }
 
+#ifdef UTO_SIMD_MATMUL
+/* The CPU baseline build (oracle/Makefile: libcpu_model.so): integer
+ * matmuls go to the restated dispatched kernels with the rayon row split
+ * (cpu_baseline.c: avx512.rs / avx2.rs, qtensor.rs:281-319), as the
+ * reference's QTensor::matmul dispatches them at run time.  The parity
+ * checker (liboracle.so) never defines this. */
+void ucb_matmul(int fmt, const void *payload, const float *scales, int64_t out_dim, int64_t in_dim,
+                const float *x, int64_t seq, float *out, int nthreads);
+#endif
+
 void uto_matmul(int fmt, const void *payload, const float *scales,
                 int64_t out_dim, int64_t in_dim, const float *x, int64_t seq,
                 float *out) {
+#ifdef UTO_SIMD_MATMUL
+    if (fmt != UTO_F32) {
+        ucb_matmul(fmt, payload, scales, out_dim, in_dim, x, seq, out, 0);
+        return;
+    }
+#endif
     /* Rows are independent and each keeps its sequential order, so the
      * thread split changes no value (the reference's rayon row split,
      * qtensor.rs:274-309). */
@@ -1163,9 +1179,13 @@ static void mla_forward(const uto_spec *c, const layer_w *w, const float *x, int
     float *ctx = (float *)xcalloc((size_t)(seq * h * vh), 4);
     float *scores = (float *)xcalloc((size_t)total, 4);
     if (absorbed) {
-        float *qabs = (float *)xcalloc((size_t)Lr, 4), *clat = (float *)xcalloc((size_t)Lr, 4);
+        /* one task per (row, head), as the reference's rayon tasks
+         * (attention.rs:202); each keeps its sequential order */
+#pragma omp parallel for collapse(2) schedule(dynamic) if (seq * h * total >= (1 << 12))
         for (int64_t s = 0; s < seq; s++) {
             for (int64_t hh = 0; hh < h; hh++) {
+                float *qabs = (float *)xcalloc((size_t)Lr, 4), *clat = (float *)xcalloc((size_t)Lr, 4);
+                float *scores = (float *)xcalloc((size_t)total, 4);
                 int64_t n_ctx = pos_base + s + 1;
                 const float *qn = q + s * h * qh + hh * qh, *qr = qn + nope;
                 int64_t rbase = hh * kvh;
@@ -1189,9 +1209,9 @@ static void mla_forward(const uto_spec *c, const layer_w *w, const float *x, int
                 }
                 uto_matvec_rows(w->kv_b.fmt, w->kv_b.p, w->kv_b.s, w->kv_b.out_dim, Lr,
                                 rbase + nope, vh, clat, ctx + (s * h + hh) * vh);
+                free(qabs); free(clat); free(scores);
             }
         }
-        free(qabs); free(clat);
     } else {
         float *kvr = (float *)xcalloc((size_t)(total * h * kvh), 4);
         qt_matmul(&w->kv_b, kv->latent, total, kvr);

@@ -196,3 +196,42 @@ def test_add_scaled_row_matches_oracle(ctx, fmt, o, i, row, factor):
     got = host(acc)
     want = O.add_scaled_row(fmt, payload, scales, o, i, row, factor, acc0)
     assert np.array_equal(got, want), np.abs(got - want).max()
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("o,i", [(1, 1), (5, 17), (7, 130), (64, 129), (2048, 7168), (300, 1000)])
+def test_quantize_bit_exact(ctx, fmt, o, i):
+    """QTensor::quantize (qtensor.rs:142-213) on the device: codes and scales
+    bit-identical to the oracle, including rows of zeros, rows whose ratios
+    land on .5 (round half away from zero) and the odd-column nibble."""
+    import undertow_amd as U
+    rng = np.random.default_rng(o * 31 + i + fmt)
+    w = (rng.standard_normal((o, i)) * rng.uniform(0.01, 3.0, (o, 1))).astype(np.float32)
+    if o > 2:
+        w[1] = 0.0
+        # exact half-way ratios: max 7 (or 127) -> s = 1, entries k + 0.5
+        qmax = 7.0 if fmt == INT4 else 127.0
+        w[2] = np.float32(0.5) + np.arange(i, dtype=np.float32) % 5 - 2
+        w[2, 0] = qmax
+    qt = U.QTensor.quantize(ctx, dev(w), fmt)
+    payload, scales = qt.download()
+    want_p, want_s = O.quantize(w, fmt)
+    assert np.array_equal(payload, np.ascontiguousarray(want_p).view(np.uint8).reshape(-1))
+    if fmt != F32:
+        assert np.array_equal(scales, want_s)
+    # and it feeds the GEMV like an uploaded tensor
+    x = rng.standard_normal((2, i)).astype(np.float32)
+    assert np.array_equal(run_matmul(ctx, qt, x),
+                          run_matmul(ctx, upload(ctx, fmt, want_p, want_s, o, i), x))
+
+
+def test_quantize_rejects_non_finite(ctx):
+    import undertow_amd as U
+    w = np.ones((4, 10), np.float32)
+    w[2, 7] = np.inf
+    w[3, 1] = np.nan
+    for fmt in (INT4, INT8, F32):
+        with pytest.raises(U.UtError) as ei:
+            U.QTensor.quantize(ctx, dev(w), fmt)
+        assert ei.value.code == U.runtime.UT_ERR_FORMAT
+        assert "flat index 27 (row 2, col 7)" in str(ei.value)

@@ -191,6 +191,57 @@ __global__ void k_dequantize(int32_t fmt, const uint8_t *__restrict__ payload,
     }
 }
 
+// QTensor::quantize (qtensor.rs:142-213), one workgroup per output row:
+// m = max|w| (a max: exact in any order), s = m/qmax, q = round(w/s) (half
+// away from zero) clamped to +-qmax; a row of zeros keeps s = 0 and zero
+// codes.  A non-finite weight lowers *bad to its flat index (the host
+// reports the smallest, as the reference's position() does).
+__global__ __launch_bounds__(256) void k_quantize(int32_t fmt, const float *__restrict__ w,
+                                                  int64_t in_dim, int64_t row_bytes,
+                                                  uint8_t *__restrict__ payload,
+                                                  float *__restrict__ scales,
+                                                  unsigned long long *__restrict__ bad) {
+    __shared__ float red[256];
+    const int tid = threadIdx.x;
+    const int64_t o = blockIdx.x;
+    const float *row = w + o * in_dim;
+    float m = 0.0f;
+    unsigned long long first = ~0ull;
+    for (int64_t i = tid; i < in_dim; i += 256) {
+        const float v = row[i];
+        if (!isfinite(v) && first == ~0ull) first = (unsigned long long)(o * in_dim + i);
+        m = fmaxf(m, fabsf(v));
+    }
+    if (first != ~0ull) atomicMin(bad, first);
+    if (fmt == UT_FMT_F32) return;  // the finiteness check only
+    red[tid] = m;
+    __syncthreads();
+    for (int st = 128; st > 0; st >>= 1) {
+        if (tid < st) red[tid] = fmaxf(red[tid], red[tid + st]);
+        __syncthreads();
+    }
+    m = red[0];
+    const float qmax = fmt == UT_FMT_INT4 ? 7.0f : 127.0f;
+    const float sc = m > 0.0f ? __fdiv_rn(m, qmax) : 0.0f;
+    if (tid == 0) scales[o] = sc;
+    auto code = [&](int64_t i) -> int {
+        if (!(m > 0.0f)) return 0;
+        float v = roundf(__fdiv_rn(row[i], sc));
+        v = fminf(fmaxf(v, -qmax), qmax);
+        return (int)v;
+    };
+    uint8_t *prow = payload + o * row_bytes;
+    if (fmt == UT_FMT_INT8) {
+        for (int64_t i = tid; i < in_dim; i += 256) prow[i] = (uint8_t)(int8_t)code(i);
+    } else {
+        for (int64_t b = tid; b < row_bytes; b += 256) {
+            const int lo = code(2 * b);
+            const int hi = 2 * b + 1 < in_dim ? code(2 * b + 1) : 0;
+            prow[b] = (uint8_t)((lo & 0xF) | ((hi & 0xF) << 4));
+        }
+    }
+}
+
 // QTensor::add_scaled_row (qtensor.rs:516-543): f = factor*scale[row];
 // acc[i] += f*q[row,i] (two roundings, no FMA, as the reference).
 __global__ void k_add_scaled_row(int32_t fmt, const uint8_t *__restrict__ payload,
@@ -469,6 +520,82 @@ int32_t ut_qtensor_dequantize(ut_ctx *ctx, const ut_qtensor *qt, float *out_dev)
         timing_end(ctx, tok);
         UT_TRY(launch_check(ctx, "k_dequantize"));
     }
+    return UT_OK;
+}
+
+int32_t ut_qtensor_quantize(ut_ctx *ctx, int32_t fmt, const float *w_dev, int64_t out_dim,
+                            int64_t in_dim, ut_qtensor **out) {
+    if (!ctx || !w_dev || !out || out_dim <= 0 || in_dim <= 0) return UT_ERR_ARG;
+    *out = nullptr;
+    if (fmt != UT_FMT_F32 && fmt != UT_FMT_INT8 && fmt != UT_FMT_INT4) {
+        set_error(ctx, "quantize: unknown format %d", fmt);
+        return UT_ERR_ARG;
+    }
+    ScratchPlan plan;
+    plan.add(8);
+    std::vector<void *> ptrs;
+    UT_TRY(scratch_acquire(ctx, plan, ptrs));
+    unsigned long long *bad = (unsigned long long *)ptrs[0];
+    UT_CHECK_HIP(ctx, hipMemsetAsync(bad, 0xFF, 8, ctx->stream));
+    ut_qtensor *q = new (std::nothrow) ut_qtensor();
+    if (!q) return UT_ERR_OOM;
+    q->fmt = fmt;
+    q->out_dim = out_dim;
+    q->in_dim = in_dim;
+    q->row_bytes = payload_bytes(fmt, 1, in_dim);
+    q->device = ctx->device;
+    const int64_t nb = payload_bytes(fmt, out_dim, in_dim);
+    if (hipMalloc(&q->payload, (size_t)nb) != hipSuccess ||
+        (fmt != UT_FMT_F32 && hipMalloc((void **)&q->scales, (size_t)out_dim * 4) != hipSuccess)) {
+        (void)hipGetLastError();
+        ut_qtensor_free(q);
+        set_error(ctx, "device allocation for a %lldx%lld tensor failed", (long long)out_dim,
+                  (long long)in_dim);
+        return UT_ERR_OOM;
+    }
+    hipLaunchKernelGGL(k_quantize, dim3((unsigned)out_dim), dim3(256), 0, ctx->stream, fmt, w_dev,
+                       in_dim, q->row_bytes, (uint8_t *)q->payload, q->scales, bad);
+    int32_t rc = launch_check(ctx, "k_quantize");
+    // f32: the data as given (QuantFormat::F32 keeps w)
+    if (rc == UT_OK && fmt == UT_FMT_F32 &&
+        hipMemcpyAsync(q->payload, w_dev, (size_t)nb, hipMemcpyDeviceToDevice, ctx->stream) !=
+            hipSuccess)
+        rc = UT_ERR_HIP;
+    unsigned long long first = ~0ull;
+    if (rc == UT_OK &&
+        hipMemcpyAsync(&first, bad, 8, hipMemcpyDeviceToHost, ctx->stream) != hipSuccess)
+        rc = UT_ERR_HIP;
+    if (rc == UT_OK && hipStreamSynchronize(ctx->stream) != hipSuccess) rc = UT_ERR_HIP;
+    if (rc == UT_OK && first != ~0ull) {
+        // the reference's Err (qtensor.rs:149-155)
+        set_error(ctx, "non-finite weight at flat index %llu (row %lld, col %lld)", first,
+                  (long long)(first / (unsigned long long)in_dim),
+                  (long long)(first % (unsigned long long)in_dim));
+        rc = UT_ERR_FORMAT;
+    }
+    if (rc != UT_OK) {
+        ut_qtensor_free(q);
+        return rc;
+    }
+    *out = q;
+    return UT_OK;
+}
+
+int32_t ut_qtensor_download(ut_ctx *ctx, const ut_qtensor *qt, void *payload_host,
+                            int64_t payload_len, float *scales_host) {
+    if (!ctx || !qt || !payload_host) return UT_ERR_ARG;
+    if (payload_len != payload_bytes(qt->fmt, qt->out_dim, qt->in_dim) ||
+        (qt->fmt != UT_FMT_F32 && !scales_host)) {
+        set_error(ctx, "download: payload of %lld bytes for a %lldx%lld tensor of format %d",
+                  (long long)payload_len, (long long)qt->out_dim, (long long)qt->in_dim, qt->fmt);
+        return UT_ERR_SHAPE;
+    }
+    UT_CHECK_HIP(ctx, hipMemcpyAsync(payload_host, qt->payload, (size_t)payload_len,
+                                     hipMemcpyDeviceToHost, ctx->stream));
+    if (qt->fmt != UT_FMT_F32)
+        UT_CHECK_HIP(ctx, hipMemcpyAsync(scales_host, qt->scales, (size_t)qt->out_dim * 4,
+                                         hipMemcpyDeviceToHost, ctx->stream));
+    UT_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
     return UT_OK;
 }
 

@@ -76,6 +76,8 @@ _SIGS = [
     ("ut_qtensor_in_dim", _i64, [_vp]),
     ("ut_qtensor_nbytes", _i64, [_vp]),
     ("ut_qtensor_dequantize", _i32, [_vp, _vp, _vp]),
+    ("ut_qtensor_quantize", _i32, [_vp, _i32, _vp, _i64, _i64, C.POINTER(_vp)]),
+    ("ut_qtensor_download", _i32, [_vp, _vp, _vp, _i64, _vp]),
     ("ut_qtensor_matmul", _i32, [_vp, _vp, _vp, _i64, _vp, _i64, _i64]),
     ("ut_qtensor_add_scaled_row", _i32, [_vp, _vp, _i64, _f32, _vp]),
     ("ut_qtensor_matvec_rows", _i32, [_vp, _vp, _i64, _i64, _vp, _i64, _vp, _i64]),
@@ -265,6 +267,27 @@ class QTensor:
         if h and _lib is not None:
             _lib.ut_qtensor_free(h)
             self._h = None
+
+    @classmethod
+    def quantize(cls, ctx: Context, w, fmt: int) -> "QTensor":
+        """QTensor::quantize (qtensor.rs:142-213) of a device f32 matrix [out, in]."""
+        out_dim, in_dim = w.shape
+        h = _vp()
+        ctx.check(lib().ut_qtensor_quantize(ctx.handle, fmt, _ptr(w), out_dim, in_dim, C.byref(h)))
+        q = cls.__new__(cls)
+        q._h = h
+        q.ctx = ctx
+        return q
+
+    def download(self):
+        """(payload uint8 array, scales float32 array | None) copied to the host."""
+        fmt, o, i = self.format, self.out_dim, self.in_dim
+        nb = self.nbytes - (0 if fmt == F32 else o * 4)
+        payload = np.zeros(nb, np.uint8)
+        scales = None if fmt == F32 else np.zeros(o, np.float32)
+        self.ctx.check(lib().ut_qtensor_download(self.ctx.handle, self._h, payload.ctypes.data, nb,
+                                                 None if scales is None else scales.ctypes.data))
+        return payload, scales
 
     @property
     def handle(self):
