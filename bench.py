@@ -497,6 +497,11 @@ def main():
     ap.add_argument("--no-mla", dest="mla", action="store_false")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 1 GiB device copy (counter scaling for rocprofv3 --pmc)")
+    ap.add_argument("--read-floor", action="store_true",
+                    help="only the single-launch read floor at the expert kernels' sizes "
+                         "(fresh windows of a 4 GiB buffer; for kernel traces)")
+    ap.add_argument("--mla-only", action="store_true",
+                    help="only the config 3 MLA leg (for counter passes; no JSON line)")
     ap.add_argument("--profile-decode", choices=["c1", "c4"], default=None,
                     help="only run the decode-step driver for kernel traces (no JSON line)")
     ap.add_argument("--prompt", type=int, default=512, help="prompt length for --profile-decode")
@@ -509,6 +514,24 @@ def main():
         sys.exit(2)
     if args.profile_decode:
         profile_decode(args.profile_decode, args.prompt, args.tokens)
+        return
+    if args.read_floor:
+        import torch
+        import undertow_amd as U
+        ctx = U.Context(0)
+        buf = torch.empty(1 << 30, dtype=torch.int32, device="cuda:0").fill_(1)
+        # the expert block's launches: down (8 experts), gate/up (8), both
+        for name, nb in (("down_8", 58_982_400), ("gate_up_8", 117_600_256),
+                         ("block_8", 176_582_656), ("window_1g", 1 << 30 >> 2)):
+            nb = nb // 256 * 256
+            g = ctx.probe_read_windows(buf, nb, reps=32)
+            print(json.dumps({"window": name, "bytes": nb, "gbs": round(g, 1),
+                              "us_per_launch": round(nb / g / 1e3, 2)}), flush=True)
+        return
+    if args.mla_only:
+        import torch
+        import undertow_amd as U
+        mla_bench(U, U.Context(0), torch, args.steps, args.warmup)
         return
 
     import torch

@@ -89,6 +89,13 @@ int32_t     ut_ctx_kernel_time(ut_ctx *ctx, const char *prefix, int64_t *launche
  * and buf_dev 16-byte aligned. */
 int32_t     ut_probe_read_bandwidth(ut_ctx *ctx, const void *buf_dev, int64_t bytes, int32_t reps,
                                     double *gbs);
+/* The same read kernel over `reps` consecutive windows of window_bytes in
+ * turn (wrapping within total_bytes >= 2 windows), one launch each, so that
+ * with total_bytes well above the 256 MB memory-side cache every launch
+ * reads data fresh from HBM: the single-launch read floor for a kernel of
+ * that size.  window_bytes a multiple of 256. */
+int32_t     ut_probe_read_windows(ut_ctx *ctx, const void *buf_dev, int64_t total_bytes,
+                                  int64_t window_bytes, int32_t reps, double *gbs);
 
 /* --------------------------------------------------------------- QTensor */
 /* QTensor::from_quantized (undertow-quant/src/qtensor.rs:85-138) /

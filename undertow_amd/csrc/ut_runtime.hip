@@ -410,6 +410,40 @@ int32_t ut_probe_read_bandwidth(ut_ctx *ctx, const void *buf_dev, int64_t bytes,
     return launch_check(ctx, "k_probe_read");
 }
 
+int32_t ut_probe_read_windows(ut_ctx *ctx, const void *buf_dev, int64_t total_bytes,
+                              int64_t window_bytes, int32_t reps, double *gbs) {
+    if (!ctx || !buf_dev || !gbs || window_bytes <= 0 || window_bytes % 256 != 0 ||
+        total_bytes < 2 * window_bytes || reps <= 0 || ((uintptr_t)buf_dev & 15) != 0) {
+        set_error(ctx, "ut_probe_read_windows: bad argument");
+        return UT_ERR_ARG;
+    }
+    int64_t *sink = nullptr;
+    UT_TRY(splitk_buffer(ctx, &sink));
+    hipEvent_t a = nullptr, b = nullptr;
+    UT_CHECK_HIP(ctx, hipEventCreate(&a));
+    UT_CHECK_HIP(ctx, hipEventCreate(&b));
+    const int64_t nwin = total_bytes / window_bytes, n = window_bytes / 16;
+    const unsigned wgs = (unsigned)ctx->multiprocessors;
+    const char *base = (const char *)buf_dev;
+    // warm-up on the last window; the timed launches then take windows 0, 1,
+    // ... in turn, each read once per pass over the buffer
+    hipLaunchKernelGGL(k_probe_read, dim3(wgs), dim3(256), 0, ctx->stream,
+                       (const ut_probe_u4 *)(base + (nwin - 1) * window_bytes), n, (unsigned *)sink);
+    UT_CHECK_HIP(ctx, hipEventRecord(a, ctx->stream));
+    for (int32_t r = 0; r < reps; r++)
+        hipLaunchKernelGGL(k_probe_read, dim3(wgs), dim3(256), 0, ctx->stream,
+                           (const ut_probe_u4 *)(base + (r % (nwin - 1)) * window_bytes), n,
+                           (unsigned *)sink);
+    UT_CHECK_HIP(ctx, hipEventRecord(b, ctx->stream));
+    UT_CHECK_HIP(ctx, hipEventSynchronize(b));
+    float ms = 0.0f;
+    UT_CHECK_HIP(ctx, hipEventElapsedTime(&ms, a, b));
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    *gbs = (double)window_bytes * reps / (ms * 1e-3) / 1e9;
+    return launch_check(ctx, "k_probe_read");
+}
+
 int32_t ut_ctx_kernel_time(ut_ctx *ctx, const char *prefix, int64_t *launches, double *total_ms) {
     if (!ctx || !prefix) return UT_ERR_ARG;
     UT_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));

@@ -69,6 +69,7 @@ _SIGS = [
     ("ut_ctx_enable_timing", _i32, [_vp, _i32]),
     ("ut_ctx_kernel_time", _i32, [_vp, C.c_char_p, C.POINTER(_i64), C.POINTER(C.c_double)]),
     ("ut_probe_read_bandwidth", _i32, [_vp, _vp, _i64, _i32, C.POINTER(C.c_double)]),
+    ("ut_probe_read_windows", _i32, [_vp, _vp, _i64, _i64, _i32, C.POINTER(C.c_double)]),
     ("ut_qtensor_upload", _i32, [_vp, _i32, _vp, _i64, _vp, _i64, _i64, _i64, C.POINTER(_vp)]),
     ("ut_qtensor_free", None, [_vp]),
     ("ut_qtensor_format", _i32, [_vp]),
@@ -228,6 +229,13 @@ class Context:
         g = C.c_double()
         self.check(lib().ut_probe_read_bandwidth(self._h, _ptr(buf), buf.numel() * buf.element_size(),
                                                  reps, C.byref(g)))
+        return g.value
+
+    def probe_read_windows(self, buf, window_bytes: int, reps: int = 16) -> float:
+        """GB/s of one read launch per fresh window_bytes window of `buf`."""
+        g = C.c_double()
+        self.check(lib().ut_probe_read_windows(self._h, _ptr(buf), buf.numel() * buf.element_size(),
+                                               window_bytes, reps, C.byref(g)))
         return g.value
 
     def kernel_time(self, prefix: str):
