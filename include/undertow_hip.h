@@ -44,7 +44,8 @@ enum {
     UT_ERR_CONTEXT_OVERFLOW = -7, /* EngineError::ContextOverflow */
     UT_ERR_BAD_TOKEN = -8,        /* token id >= vocab_size */
     UT_ERR_NOT_FOUND = -9,        /* a required tensor was never set */
-    UT_ERR_STATE = -10            /* call out of order (e.g. no MTP head) */
+    UT_ERR_STATE = -10,           /* call out of order (e.g. no MTP head) */
+    UT_ERR_IO = -11               /* EngineError::Io: a checkpoint file could not be read */
 };
 
 /* QuantFormat (undertow-quant/src/qtensor.rs:17-21).  UT_FMT_INFER asks
@@ -275,6 +276,21 @@ int32_t ut_model_create(ut_ctx *ctx, const ut_model_config *cfg, ut_model **out)
 int32_t ut_model_set_tensor(ut_model *m, const char *name, int32_t fmt, const void *payload,
                             int64_t nbytes, const float *scales, int64_t d0, int64_t d1);
 int32_t ut_model_finalize(ut_model *m);
+/* load_model_with's tensor reads (adapters/undertow-deepseek-moe/src/
+ * loader.rs:67-229 through read_qtensor and ShardedModelReader, undertow-io/
+ * src/reader.rs:78-143,300-444) straight into HBM, then finalize: opens
+ * dir/model.safetensors.index.json (or a single dir/model.safetensors),
+ * validates every shard header (known dtype, data_offsets consistent with
+ * shape and dtype, extents inside the file, header <= 100 MB), and streams
+ * each tensor the config needs into one device arena: pread into pinned
+ * staging buffers, two in flight, each drained by hipMemcpyAsync.
+ * Quantized weights are the converter's `<name>` U8 payload plus
+ * `<name>.scales` F32 [out_dim] (int8 or int4 from the payload size, as
+ * read_qtensor); plain tensors may be F32, BF16 or F16 (widened to f32).
+ * Errors: UT_ERR_IO (unreadable file), UT_ERR_FORMAT (bad header or
+ * payload size), UT_ERR_NOT_FOUND, UT_ERR_SHAPE.  bytes_read (may be NULL)
+ * gets the tensor bytes read from disk.  Needs a fresh model. */
+int32_t ut_model_load_dir(ut_model *m, const char *dir, int64_t *bytes_read);
 /* Benchmark support, no reference counterpart: fills every tensor of the
  * config on device from a counter-based generator (int4 experts and int8
  * dense matrices with codes uniform over the format's range and per-row

@@ -13,6 +13,7 @@
 #include "ut_mla.h"
 #include "ut_moe.h"
 #include "ut_ops.h"
+#include "ut_safetensors.h"
 #include "ut_sample.h"
 
 using namespace ut;
@@ -990,11 +991,10 @@ void synth_layer_list(const ut_model_config &c, int64_t li, bool dense, std::vec
     }
 }
 
-int32_t synthesize_all(ut_model *m, uint64_t seed, float std, int expert_fmt, int dense_fmt) {
-    const ut_model_config &c = m->c;
-    ut_ctx *ctx = m->ctx;
+// Every tensor the config needs, with its shape (the names load_model_with
+// reads, loader.rs:67-229).
+void model_tensor_list(const ut_model_config &c, std::vector<SynthItem> &items) {
     const int64_t H = c.hidden_size, L = c.num_hidden_layers;
-    std::vector<SynthItem> items;
     items.push_back({"model.embed_tokens.weight", 0, 1, c.vocab_size, H});
     for (int64_t li = 0; li < L; li++) synth_layer_list(c, li, li < c.first_k_dense_replace, items);
     items.push_back({"model.norm.weight", 1, 0, H, 1});
@@ -1008,6 +1008,13 @@ int32_t synthesize_all(ut_model *m, uint64_t seed, float std, int expert_fmt, in
         items.push_back({p + "shared_head.norm.weight", 1, 0, H, 1});
         items.push_back({p + "shared_head.head.weight", 0, 1, c.vocab_size, H});
     }
+}
+
+int32_t synthesize_all(ut_model *m, uint64_t seed, float std, int expert_fmt, int dense_fmt) {
+    const ut_model_config &c = m->c;
+    ut_ctx *ctx = m->ctx;
+    std::vector<SynthItem> items;
+    model_tensor_list(c, items);
     // one arena for everything, 256-byte aligned pieces
     auto al = [](int64_t b) { return (b + 255) & ~int64_t(255); };
     int64_t total = 0;
@@ -1249,6 +1256,245 @@ int64_t gen_spec(ut_model *m, const int32_t *prompt, int64_t n, int32_t depth, u
 
 }  // namespace
 
+// ------------------------------------------------------- shard loader ---
+// Host->device streaming through two pinned staging buffers: pread fills
+// one while the copy engine drains the other (hipMemcpyAsync on the
+// context's stream, an event per buffer marks when it may be refilled).
+struct Stager {
+    ut_ctx *ctx = nullptr;
+    static constexpr size_t kChunk = size_t(64) << 20;
+    void *pin[2] = {nullptr, nullptr};
+    hipEvent_t done[2] = {nullptr, nullptr};
+    bool pending[2] = {false, false};
+    int next = 0;
+    uint64_t bytes_read = 0;
+    std::vector<uint16_t> halves;
+
+    int32_t init(ut_ctx *c) {
+        ctx = c;
+        for (int i = 0; i < 2; i++) {
+            if (hipHostMalloc(&pin[i], kChunk, hipHostMallocDefault) != hipSuccess ||
+                hipEventCreateWithFlags(&done[i], hipEventDisableTiming) != hipSuccess) {
+                (void)hipGetLastError();
+                set_error(ctx, "pinned staging allocation failed");
+                return UT_ERR_OOM;
+            }
+        }
+        return UT_OK;
+    }
+    ~Stager() {
+        for (int i = 0; i < 2; i++) {
+            if (pending[i]) (void)hipEventSynchronize(done[i]);
+            if (pin[i]) (void)hipHostFree(pin[i]);
+            if (done[i]) (void)hipEventDestroy(done[i]);
+        }
+    }
+    int32_t take(void **buf) {
+        const int b = next;
+        next ^= 1;
+        if (pending[b]) UT_CHECK_HIP(ctx, hipEventSynchronize(done[b]));
+        pending[b] = false;
+        *buf = pin[b];
+        return b;
+    }
+    int32_t send(int b, void *dst, size_t n) {
+        UT_CHECK_HIP(ctx, hipMemcpyAsync(dst, pin[b], n, hipMemcpyHostToDevice, ctx->stream));
+        UT_CHECK_HIP(ctx, hipEventRecord(done[b], ctx->stream));
+        pending[b] = true;
+        return UT_OK;
+    }
+    // n bytes at offset of a shard to dst (device)
+    int32_t raw(const st::Shard &sh, uint64_t offset, uint64_t n, char *dst) {
+        for (uint64_t pos = 0; pos < n;) {
+            const size_t len = (size_t)std::min<uint64_t>(kChunk, n - pos);
+            void *buf = nullptr;
+            int b = take(&buf);
+            if (b < 0) return b;
+            std::string err;
+            if (!st::read_at(sh, buf, len, offset + pos, err)) {
+                set_error(ctx, "%s", err.c_str());
+                return UT_ERR_IO;
+            }
+            bytes_read += len;
+            UT_TRY(send(b, dst + pos, len));
+            pos += len;
+        }
+        return UT_OK;
+    }
+    // count 16-bit floats (bf16 or f16) at offset, widened exactly to f32 at dst
+    int32_t widen(const st::Shard &sh, uint64_t offset, uint64_t count, bool bf16, float *dst) {
+        const uint64_t per = kChunk / 4;
+        halves.resize((size_t)std::min<uint64_t>(per, count));
+        for (uint64_t pos = 0; pos < count;) {
+            const uint64_t cnt = std::min<uint64_t>(per, count - pos);
+            std::string err;
+            if (!st::read_at(sh, halves.data(), cnt * 2, offset + pos * 2, err)) {
+                set_error(ctx, "%s", err.c_str());
+                return UT_ERR_IO;
+            }
+            bytes_read += cnt * 2;
+            void *buf = nullptr;
+            int b = take(&buf);
+            uint32_t *o = (uint32_t *)buf;
+            for (uint64_t i = 0; i < cnt; i++) {
+                const uint32_t h = halves[(size_t)i];
+                if (bf16) {
+                    o[i] = h << 16;
+                } else {
+                    // IEEE binary16 -> binary32 (exact: every half is a float)
+                    const uint32_t sign = (h & 0x8000u) << 16, ex = (h >> 10) & 0x1F, man = h & 0x3FF;
+                    uint32_t v;
+                    if (ex == 0x1F) {
+                        v = sign | 0x7F800000u | (man << 13);
+                    } else if (ex != 0) {
+                        v = sign | ((ex + 112) << 23) | (man << 13);
+                    } else if (man == 0) {
+                        v = sign;
+                    } else {
+                        int e = -1;
+                        uint32_t m = man;
+                        do { e++; m <<= 1; } while (!(m & 0x400));
+                        v = sign | ((uint32_t)(112 - e) << 23) | ((m & 0x3FF) << 13);
+                    }
+                    o[i] = v;
+                }
+            }
+            UT_TRY(send(b, dst + pos, (size_t)cnt * 4));
+            pos += cnt;
+        }
+        return UT_OK;
+    }
+};
+
+// read_qtensor (undertow-io/src/reader.rs:403-444) and the vector reads of
+// load_model_with (loader.rs:67-229) for every tensor the config needs,
+// streamed into one device arena.  skip_experts: leave the routed experts
+// out (an expert store serves them).
+int32_t load_dir_all(ut_model *m, const char *dir, bool skip_experts, int64_t *bytes_read) {
+    ut_ctx *ctx = m->ctx;
+    st::Index idx;
+    std::string err;
+    if (!st::open_dir(dir, idx, err)) {
+        set_error(ctx, "%s", err.c_str());
+        return err.find("No such file") != std::string::npos ||
+                       err.find("Permission denied") != std::string::npos
+                   ? UT_ERR_IO
+                   : UT_ERR_FORMAT;
+    }
+    std::vector<SynthItem> items;
+    model_tensor_list(m->c, items);
+    struct Plan {
+        const SynthItem *it;
+        const st::Entry *data, *scales;
+        int fmt;
+        int64_t pb;
+    };
+    std::vector<Plan> plan;
+    auto al = [](int64_t b) { return (b + 255) & ~int64_t(255); };
+    int64_t total = 0;
+    for (auto &it : items) {
+        if (skip_experts && it.cls == 2) continue;
+        const st::Entry *e = idx.find(it.name);
+        if (!e) {
+            set_error(ctx, "tensor not found: %s", it.name.c_str());
+            return UT_ERR_NOT_FOUND;
+        }
+        Plan pl{&it, e, nullptr, UT_FMT_F32, 0};
+        const bool floaty = e->dtype == st::ST_F32 || e->dtype == st::ST_BF16 || e->dtype == st::ST_F16;
+        if (it.kind != 0) {
+            if (!floaty || e->shape.size() != 1 || e->shape[0] != it.d0) {
+                set_error(ctx, "shape mismatch for %s: expected [%lld]", it.name.c_str(), (long long)it.d0);
+                return UT_ERR_SHAPE;
+            }
+            pl.pb = it.d0 * 4;
+            total += al(pl.pb);
+        } else if ((pl.scales = idx.find(it.name + ".scales"))) {
+            const st::Entry *sc = pl.scales;
+            if (sc->dtype != st::ST_F32 || sc->shape.size() != 1 || sc->shape[0] != it.d0) {
+                set_error(ctx, "shape mismatch for %s.scales: expected [%lld]", it.name.c_str(),
+                          (long long)it.d0);
+                return UT_ERR_SHAPE;
+            }
+            if (e->dtype != st::ST_U8 && e->dtype != st::ST_I8) {
+                set_error(ctx, "%s: quantized payload must be U8", it.name.c_str());
+                return UT_ERR_FORMAT;
+            }
+            if ((int64_t)e->nbytes == payload_bytes(UT_FMT_INT8, it.d0, it.d1)) pl.fmt = UT_FMT_INT8;
+            else if ((int64_t)e->nbytes == payload_bytes(UT_FMT_INT4, it.d0, it.d1)) pl.fmt = UT_FMT_INT4;
+            else {
+                set_error(ctx, "%s: payload of %llu bytes matches neither int8 nor int4 for [%lld, %lld]",
+                          it.name.c_str(), (unsigned long long)e->nbytes, (long long)it.d0,
+                          (long long)it.d1);
+                return UT_ERR_FORMAT;
+            }
+            pl.pb = (int64_t)e->nbytes;
+            total += al(pl.pb) + al(it.d0 * 4);
+        } else {
+            if (!floaty || e->shape.size() != 2 || e->shape[0] != it.d0 || e->shape[1] != it.d1) {
+                set_error(ctx, "shape mismatch for %s: expected [%lld, %lld]", it.name.c_str(),
+                          (long long)it.d0, (long long)it.d1);
+                return UT_ERR_SHAPE;
+            }
+            pl.pb = it.d0 * it.d1 * 4;
+            total += al(pl.pb);
+        }
+        plan.push_back(pl);
+    }
+    Stager sg;
+    UT_TRY(sg.init(ctx));
+    void *arena = nullptr;
+    UT_TRY(dev_alloc(m, (size_t)total, &arena));
+    char *p = (char *)arena;
+    auto fill_f32 = [&](const st::Entry *e, float *dst) -> int32_t {
+        const st::Shard &sh = idx.shards[(size_t)e->shard];
+        if (e->dtype == st::ST_F32) return sg.raw(sh, e->offset, e->nbytes, (char *)dst);
+        return sg.widen(sh, e->offset, e->nbytes / 2, e->dtype == st::ST_BF16, dst);
+    };
+    for (auto &pl : plan) {
+        const SynthItem &it = *pl.it;
+        DevTensor t;
+        t.d0 = it.d0;
+        t.d1 = it.d1;
+        if (it.kind != 0) {
+            UT_TRY(fill_f32(pl.data, (float *)p));
+            t.vec = (float *)p;
+            p += al(pl.pb);
+        } else {
+            ut_qtensor *q = new (std::nothrow) ut_qtensor();
+            if (!q) return UT_ERR_OOM;
+            q->fmt = pl.fmt;
+            q->out_dim = it.d0;
+            q->in_dim = it.d1;
+            q->row_bytes = payload_bytes(pl.fmt, 1, it.d1);
+            q->owns = false;
+            q->device = m->device;
+            q->payload = p;
+            t.qt = q;
+            auto prev = m->tensors.find(it.name);
+            if (prev != m->tensors.end() && prev->second.qt) ut_qtensor_free(prev->second.qt);
+            m->tensors[it.name] = t;
+            if (pl.fmt == UT_FMT_F32) {
+                UT_TRY(fill_f32(pl.data, (float *)p));
+                p += al(pl.pb);
+            } else {
+                UT_TRY(sg.raw(idx.shards[(size_t)pl.data->shard], pl.data->offset, pl.data->nbytes, p));
+                p += al(pl.pb);
+                q->scales = (float *)p;
+                UT_TRY(sg.raw(idx.shards[(size_t)pl.scales->shard], pl.scales->offset,
+                              pl.scales->nbytes, p));
+                p += al(it.d0 * 4);
+            }
+            continue;
+        }
+        auto prev = m->tensors.find(it.name);
+        if (prev != m->tensors.end() && prev->second.qt) ut_qtensor_free(prev->second.qt);
+        m->tensors[it.name] = t;
+    }
+    UT_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (bytes_read) *bytes_read = (int64_t)sg.bytes_read;
+    return UT_OK;
+}
+
 extern "C" {
 
 int32_t ut_model_create(ut_ctx *ctx, const ut_model_config *cfg, ut_model **out) {
@@ -1313,6 +1559,16 @@ int32_t ut_model_set_tensor(ut_model *m, const char *name, int32_t fmt, const vo
         m->tensors.emplace(name, t);
     }
     return UT_OK;
+}
+
+int32_t ut_model_load_dir(ut_model *m, const char *dir, int64_t *bytes_read) {
+    if (!m || !dir) return UT_ERR_ARG;
+    if (m->finalized || !m->tensors.empty()) {
+        set_error(m->ctx, "ut_model_load_dir needs a fresh model");
+        return UT_ERR_STATE;
+    }
+    UT_TRY(load_dir_all(m, dir, false, bytes_read));
+    return ut_model_finalize(m);
 }
 
 int32_t ut_model_finalize(ut_model *m) {

@@ -37,6 +37,7 @@ UT_ERR_CONTEXT_OVERFLOW = -7
 UT_ERR_BAD_TOKEN = -8
 UT_ERR_NOT_FOUND = -9
 UT_ERR_STATE = -10
+UT_ERR_IO = -11
 
 
 class UtError(RuntimeError):
@@ -97,6 +98,7 @@ _SIGS = [
     ("ut_model_create", _i32, [_vp, _vp, C.POINTER(_vp)]),
     ("ut_model_set_tensor", _i32, [_vp, C.c_char_p, _i32, _vp, _i64, _vp, _i64, _i64]),
     ("ut_model_finalize", _i32, [_vp]),
+    ("ut_model_load_dir", _i32, [_vp, C.c_char_p, C.POINTER(_i64)]),
     ("ut_model_synthesize", _i32, [_vp, C.c_uint64, _f32, _i32, _i32]),
     ("ut_model_device_bytes", _i64, [_vp]),
     ("ut_model_free", None, [_vp]),
@@ -481,6 +483,13 @@ class Model:
 
     def finalize(self) -> None:
         self.ctx.check(lib().ut_model_finalize(self._h))
+
+    def load_dir(self, path) -> int:
+        """Stream a converted checkpoint directory into HBM and finalize;
+        returns the bytes read."""
+        n = _i64()
+        self.ctx.check(lib().ut_model_load_dir(self._h, str(path).encode(), C.byref(n)))
+        return n.value
 
     def synthesize(self, seed: int, init_std: float = 0.02, expert_fmt: int = INT4,
                    dense_fmt: int = INT8) -> None:
