@@ -291,6 +291,55 @@ int32_t ut_model_finalize(ut_model *m);
  * payload size), UT_ERR_NOT_FOUND, UT_ERR_SHAPE.  bytes_read (may be NULL)
  * gets the tensor bytes read from disk.  Needs a fresh model. */
 int32_t ut_model_load_dir(ut_model *m, const char *dir, int64_t *bytes_read);
+/* The HBM tier of the expert store: DiskExpertStore with an LRU or weighted
+ * ExpertCache (undertow-io/src/store.rs:46-249, undertow-core/src/cache.rs:
+ * 15-340) whose cache lives in device memory.  Routed experts stay in the
+ * backing source; a byte-budgeted pool of HBM slots holds the cached ones
+ * (one slot = one expert's gate, up and down payloads and scales), plus
+ * room for the experts of one step beyond the budget.  Each MoE step routes
+ * on the device, reads the choices back, loads missing experts into slots
+ * (evicting by the policy; pinned experts stay) and publishes the layer's
+ * pointer table before the expert launches: results are bit-identical to a
+ * resident model.  prefetch: at one-row decode, a pilot routing of the next
+ * MoE layer on the post-attention residual (pilot_prefetch, adapters/
+ * undertow-deepseek-moe/src/model.rs:290-318) loads its predicted experts
+ * during the current step. */
+typedef struct {
+    int64_t hbm_budget_bytes; /* cache_budget_bytes for routed experts */
+    int32_t policy;           /* CachePolicy: 0 LRU, 1 weighted (half-life 512 accesses) */
+    int32_t prefetch;         /* 1: pilot-router prefetch one layer ahead at decode */
+} ut_expert_store_config;
+/* StoreStatsSnapshot (undertow-core/src/store.rs). */
+typedef struct {
+    int64_t hits, misses, bytes_read, evictions, prefetch_issued, prefetch_dropped;
+    int64_t bytes_used, budget_bytes, pinned_experts;
+    double read_seconds;
+} ut_store_stats;
+/* load_model_with with StoreChoice::DiskStreaming (adapters/undertow-
+ * deepseek-moe/src/loader.rs:233-302): ut_model_load_dir for everything but
+ * the routed experts, which stay in dir's shards behind the HBM tier
+ * (pread into pinned staging on a miss, read_qtensor's layout). */
+int32_t ut_model_load_dir_tiered(ut_model *m, const char *dir, const ut_expert_store_config *cfg,
+                                 int64_t *bytes_read);
+/* Benchmark support, no reference counterpart: ut_model_synthesize with the
+ * routed experts behind the HBM tier, served from a pinned host pool of
+ * host_pool_experts seeded experts (key (layer, e) reads pool entry
+ * (layer * E + e) mod host_pool_experts). */
+int32_t ut_model_synthesize_tiered(ut_model *m, uint64_t seed, float init_std, int32_t expert_fmt,
+                                   int32_t dense_fmt, const ut_expert_store_config *cfg,
+                                   int64_t host_pool_experts);
+/* DiskExpertStore::pin_hottest (store.rs:146-166): loads and pins the
+ * (layer, expert) pairs in order (hottest first, as ExpertProfile::hottest)
+ * until budget_bytes are pinned or the cache's budget is full of pins;
+ * out-of-range pairs are skipped. */
+int32_t ut_model_pin_experts(ut_model *m, const int32_t *layer_expert, int64_t n,
+                             int64_t budget_bytes, int64_t *pinned_bytes);
+/* TieredStore::stats (store.rs:233-240).  UT_ERR_STATE without a store. */
+int32_t ut_model_store_stats(ut_model *m, ut_store_stats *out);
+/* TieredStore::usage (store.rs:222-231): per-expert get counts
+ * [num_hidden_layers (+1 with MTP)][n_routed_experts], the data of an
+ * ExpertProfile (undertow-core/src/profile.rs:18-100). */
+int32_t ut_model_expert_usage(ut_model *m, int64_t *counts, int64_t n);
 /* Benchmark support, no reference counterpart: fills every tensor of the
  * config on device from a counter-based generator (int4 experts and int8
  * dense matrices with codes uniform over the format's range and per-row

@@ -8,7 +8,7 @@ import struct
 import numpy as np
 import pytest
 
-from models import C1, checkpoint, gpu_model, prompt_ids
+from models import C1, checkpoint, gpu_model, prompt_ids, write_converted
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -18,30 +18,6 @@ def fresh_model(ctx, ck):
     import undertow_amd as U
     from models import CFG_KEYS
     return U.Model(ctx, {k: getattr(ck.spec, k) for k in CFG_KEYS})
-
-
-def write_converted(ck, d, expert_layers):
-    """The converter's layout (undertow-convert/src/lib.rs:273-345): routed
-    experts of layer L in experts-{L:05}.safetensors, the rest in
-    dense.safetensors, plus model.safetensors.index.json."""
-    groups = {}
-    for t in ck.tensors():
-        name = t[0]
-        shard = "dense.safetensors"
-        for L in expert_layers:
-            if name.startswith(f"model.layers.{L}.mlp.experts."):
-                shard = f"experts-{L:05d}.safetensors"
-        groups.setdefault(shard, []).append(t)
-    wm = {}
-    for shard, ts in groups.items():
-        sub = O.Checkpoint.from_tensors(ck.spec, ts)
-        (d / shard).write_bytes(sub.safetensors_bytes())
-        for name, fmt, shape, payload, scales in ts:
-            wm[name] = shard
-            if fmt != O.F32:
-                wm[name + ".scales"] = shard
-    (d / "model.safetensors.index.json").write_text(json.dumps({"metadata": {}, "weight_map": wm}))
-    return groups
 
 
 def write_safetensors(path, entries):

@@ -15,6 +15,7 @@
 #include "ut_ops.h"
 #include "ut_safetensors.h"
 #include "ut_sample.h"
+#include "ut_store.h"
 
 using namespace ut;
 
@@ -51,6 +52,7 @@ struct LayerW {
     void *experts_dev = nullptr;     // 6*E device pointers
     ExpertPtrs experts{};
     int expert_fmt = UT_FMT_F32;
+    int64_t index = 0;               // layer index (the MTP layer: num_hidden_layers)
 };
 
 struct KvCache {
@@ -77,6 +79,8 @@ struct ut_model {
     MoePlan mlp_plan{};            // the fixed one-slot plan of an MLP
     bool finalized = false;
     std::vector<int32_t> stop_ids;  // the checkpoint's stop tokens (DeepseekMoeModel::stop_ids)
+    ut::ExpertStore *store = nullptr;  // the HBM tier of routed experts, when not all resident
+    bool store_prefetch = false;       // pilot-router hints one layer ahead at decode
     std::vector<void *> device_allocs;
     int64_t device_bytes = 0;
     int device = 0;
@@ -257,7 +261,13 @@ int32_t load_layer(ut_model *m, int64_t li, bool dense, LayerW *L) {
     std::vector<const void *> vals((size_t)E * 6, nullptr);
     const int64_t I = c.moe_intermediate_size;
     int fmt = -1;
-    for (int64_t e = 0; e < E; e++) {
+    L->index = li;
+    if (m->store) {
+        // the store's slots fill the table as experts arrive (all null now)
+        fmt = m->store->fmt();
+        m->store->set_table(li, (void **)L->experts_dev);
+    }
+    for (int64_t e = 0; !m->store && e < E; e++) {
         const std::string ep = p + "mlp.experts." + std::to_string(e) + ".";
         const ut_qtensor *g, *u, *d;
         UT_TRY(get_qt(m, ep + "gate_proj.weight", I, H, &g));
@@ -454,6 +464,44 @@ int32_t mlp_add(ut_session *s, const MlpW &w, const float *x, const XDigits &xd,
 // The routed part of moe_forward (model.rs:195-281): router, routed experts
 // in choice order, into out (overwritten).  x: normed rows (f32, for the f32
 // router gate) with digits xd.
+// The routed experts of M rows through the HBM tier: the choices (and, at
+// one row with pilot hints on, the next MoE layer's predicted choices:
+// pilot_prefetch, model.rs:290-318, on the post-attention residual `resid`)
+// come back to the host in one round trip; missing experts are loaded into
+// slots and the layer's pointer table published, all in stream order.
+int32_t tiered_experts(ut_session *s, const LayerW &L, const float *resid, int64_t M) {
+    ut_model *m = s->m;
+    ut_ctx *ctx = m->ctx;
+    const ut_model_config &c = m->c;
+    const int64_t E = c.n_routed_experts, k = c.num_experts_per_tok, H = c.hidden_size;
+    const int64_t n = M * k;
+    const LayerW *nxt = nullptr;
+    if (m->store_prefetch && M == 1 && L.index + 1 < c.num_hidden_layers &&
+        !m->layers[(size_t)L.index + 1].dense)
+        nxt = &m->layers[(size_t)L.index + 1];
+    if (nxt) {
+        // row 1 of the workspace's router buffers is free at one row
+        UT_TRY(launch_rmsnorm(ctx, resid, H, nxt->post_norm, H, c.rms_norm_eps, 1, s->ws.emb, H));
+        UT_TRY(mm(s, nxt->gate, s->ws.emb, 1, s->ws.rlogits + E, E));
+        UT_TRY(launch_route(ctx, s->ws.rlogits + E, nxt->bias, 1, E, (int)k, (int)c.n_group,
+                            (int)c.topk_group, c.norm_topk_prob, c.routed_scaling_factor,
+                            s->ws.rids + k, s->ws.rw + k));
+    }
+    const int64_t nb = nxt ? n + k : n;
+    std::vector<int32_t> ids((size_t)nb);
+    // through the context's pinned buffer: the session's readback slot may
+    // hold a generation loop's token still to be read
+    void *pin = nullptr;
+    UT_TRY(pinned_acquire(ctx, (size_t)nb * 4, &pin));
+    UT_CHECK_HIP(ctx, hipMemcpyAsync(pin, s->ws.rids, (size_t)nb * 4, hipMemcpyDeviceToHost,
+                                     ctx->stream));
+    UT_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    memcpy(ids.data(), pin, (size_t)nb * 4);
+    UT_TRY(m->store->ensure(L.index, ids.data(), n));
+    if (nxt) UT_TRY(m->store->prefetch(nxt->index, ids.data() + n, k));
+    return UT_OK;
+}
+
 int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigits &xd,
                     int64_t rows, float *out, int accumulate = 0, const MlpW *shared = nullptr,
                     const NormNext *next = nullptr) {
@@ -474,7 +522,8 @@ int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
             ga.M = M;
             ga.out = s->ws.rlogits;
             ga.ldo = E;
-            ga.defer = &gparts;
+            // the tiered path routes in its own launch: logits finished here
+            ga.defer = m->store ? nullptr : &gparts;
             if (L.gate->fmt != UT_FMT_F32) {
                 UT_TRY(mm(s, L.gate, x + s0 * H, M, s->ws.rlogits, E));
                 gparts = SplitKPartials{};
@@ -487,15 +536,24 @@ int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
         }
         const int64_t slots = moe_slots(M, k, E, -1);
         ScratchLayout lay = moe_layout(M, k, slots, H, c.moe_intermediate_size, L.expert_fmt);
+        if (m->store) {
+            // the HBM tier: route, read the choices back, bring missing
+            // experts into their slots (TieredStore::get_expert), then the
+            // expert launches plan from the ids like a resident table
+            UT_TRY(launch_route(m->ctx, s->ws.rlogits, L.bias, M, E, k, (int)c.n_group,
+                                (int)c.topk_group, c.norm_topk_prob, c.routed_scaling_factor,
+                                s->ws.rids, s->ws.rw));
+            UT_TRY(tiered_experts(s, L, s->ws.x + s0 * H, M));
+        }
         // with the logits whole and few choices the expert launch routes and
         // builds the slot plan itself (moe_pass); else route + plan in one
         // launch here
         // (three or more rows with int4 experts go to the matrix-core expert
         // kernels, which take the plan ready-made)
         const bool mfma_rows = M >= 3 && gate_up_mfma_ok(L.expert_fmt, M, H);
-        const bool gate_plans = gparts.ks <= 1 && (int64_t)M * k <= 64 &&
+        const bool gate_plans = !m->store && gparts.ks <= 1 && (int64_t)M * k <= 64 &&
                                 L.expert_fmt != UT_FMT_F32 && !mfma_rows;
-        if (!gate_plans)
+        if (!gate_plans && !m->store)
             UT_TRY(launch_route_plan(m->ctx, s->ws.rlogits, &gparts, L.bias, M, E, k,
                                      (int)c.n_group, (int)c.topk_group, c.norm_topk_prob,
                                      c.routed_scaling_factor, s->ws.rids, s->ws.rw,
@@ -519,7 +577,7 @@ int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
         mc.ldo = H;
         mc.accumulate = accumulate;
         mc.err_flag = s->ws.err;
-        mc.plan_ready = !gate_plans;
+        mc.plan_ready = !gate_plans && !m->store;
         if (gate_plans) {
             mc.route_logits = s->ws.rlogits;
             mc.route_bias = L.bias;
@@ -1019,6 +1077,7 @@ int32_t synthesize_all(ut_model *m, uint64_t seed, float std, int expert_fmt, in
     auto al = [](int64_t b) { return (b + 255) & ~int64_t(255); };
     int64_t total = 0;
     for (auto &it : items) {
+        if (m->store && it.cls == 2) continue;  // routed experts live in the store
         if (it.kind != 0) { total += al(it.d0 * 4); continue; }
         int fmt = it.cls == 0 ? UT_FMT_F32 : it.cls == 1 ? dense_fmt : expert_fmt;
         total += al(payload_bytes(fmt, it.d0, it.d1)) + (fmt == UT_FMT_F32 ? 0 : al(it.d0 * 4));
@@ -1036,6 +1095,7 @@ int32_t synthesize_all(ut_model *m, uint64_t seed, float std, int expert_fmt, in
         return launch_check(ctx, "k_synth");
     };
     for (auto &it : items) {
+        if (m->store && it.cls == 2) continue;
         DevTensor t;
         t.d0 = it.d0;
         t.d1 = it.d1;
@@ -1571,6 +1631,131 @@ int32_t ut_model_load_dir(ut_model *m, const char *dir, int64_t *bytes_read) {
     return ut_model_finalize(m);
 }
 
+}  // extern "C"
+
+namespace {
+
+int32_t make_store(ut_model *m, int expert_fmt, const ut_expert_store_config *cfg) {
+    const ut_model_config &c = m->c;
+    if (cfg->hbm_budget_bytes < 0 || (cfg->policy != 0 && cfg->policy != 1)) {
+        set_error(m->ctx, "expert store: bad budget or policy");
+        return UT_ERR_ARG;
+    }
+    if (c.n_routed_experts <= 0) {
+        set_error(m->ctx, "expert store: the model has no routed experts");
+        return UT_ERR_ARG;
+    }
+    m->store = new (std::nothrow) ut::ExpertStore();
+    if (!m->store) return UT_ERR_OOM;
+    m->store_prefetch = cfg->prefetch != 0;
+    const int64_t layers = c.num_hidden_layers + (c.mtp ? 1 : 0);
+    return m->store->init(m->ctx, layers, c.n_routed_experts, c.hidden_size,
+                          c.moe_intermediate_size, expert_fmt, cfg->hbm_budget_bytes, cfg->policy,
+                          4 * c.num_experts_per_tok);
+}
+
+int32_t need_store(const ut_model *m) {
+    if (!m) return UT_ERR_ARG;
+    if (!m->store) {
+        set_error(m->ctx, "the model has no expert store (all experts resident)");
+        return UT_ERR_STATE;
+    }
+    return UT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t ut_model_load_dir_tiered(ut_model *m, const char *dir, const ut_expert_store_config *cfg,
+                                 int64_t *bytes_read) {
+    if (!m || !dir || !cfg) return UT_ERR_ARG;
+    if (m->finalized || !m->tensors.empty() || m->store) {
+        set_error(m->ctx, "ut_model_load_dir_tiered needs a fresh model");
+        return UT_ERR_STATE;
+    }
+    // the experts' format from the first routed expert's payload size
+    // (read_qtensor's inference, reader.rs:421-430)
+    int fmt = UT_FMT_F32;
+    {
+        ut::st::Index idx;
+        std::string err;
+        if (!ut::st::open_dir(dir, idx, err)) {
+            set_error(m->ctx, "%s", err.c_str());
+            return err.find("No such file") != std::string::npos ? UT_ERR_IO : UT_ERR_FORMAT;
+        }
+        const int64_t L0 = m->c.first_k_dense_replace < m->c.num_hidden_layers
+                               ? m->c.first_k_dense_replace : m->c.num_hidden_layers;
+        const std::string n = "model.layers." + std::to_string(L0) + ".mlp.experts.0.gate_proj.weight";
+        const ut::st::Entry *e = idx.find(n);
+        if (!e) {
+            set_error(m->ctx, "tensor not found: %s", n.c_str());
+            return UT_ERR_NOT_FOUND;
+        }
+        const int64_t I = m->c.moe_intermediate_size, H = m->c.hidden_size;
+        if (idx.find(n + ".scales"))
+            fmt = (int64_t)e->nbytes == payload_bytes(UT_FMT_INT8, I, H) ? UT_FMT_INT8 : UT_FMT_INT4;
+    }
+    UT_TRY(make_store(m, fmt, cfg));
+    UT_TRY(load_dir_all(m, dir, true, bytes_read));
+    UT_TRY(ut_model_finalize(m));
+    return m->store->attach_disk(dir);
+}
+
+int32_t ut_model_synthesize_tiered(ut_model *m, uint64_t seed, float init_std, int32_t expert_fmt,
+                                   int32_t dense_fmt, const ut_expert_store_config *cfg,
+                                   int64_t host_pool_experts) {
+    if (!m || !cfg || host_pool_experts <= 0) return UT_ERR_ARG;
+    if (m->finalized || !m->tensors.empty() || m->store) {
+        set_error(m->ctx, "ut_model_synthesize_tiered needs a fresh model");
+        return UT_ERR_STATE;
+    }
+    if ((expert_fmt != UT_FMT_INT4 && expert_fmt != UT_FMT_INT8) ||
+        (dense_fmt != UT_FMT_INT4 && dense_fmt != UT_FMT_INT8)) {
+        set_error(m->ctx, "synthesize: formats must be int4 or int8");
+        return UT_ERR_ARG;
+    }
+    UT_TRY(make_store(m, expert_fmt, cfg));
+    UT_TRY(synthesize_all(m, seed, init_std, expert_fmt, dense_fmt));
+    UT_TRY(ut_model_finalize(m));
+    return m->store->attach_host_pool(host_pool_experts, seed, init_std);
+}
+
+int32_t ut_model_pin_experts(ut_model *m, const int32_t *layer_expert, int64_t n,
+                             int64_t budget_bytes, int64_t *pinned_bytes) {
+    UT_TRY(need_store(m));
+    if (n < 0 || (n > 0 && !layer_expert) || budget_bytes < 0) return UT_ERR_ARG;
+    return m->store->pin(layer_expert, n, budget_bytes, pinned_bytes);
+}
+
+int32_t ut_model_store_stats(ut_model *m, ut_store_stats *out) {
+    UT_TRY(need_store(m));
+    if (!out) return UT_ERR_ARG;
+    const ut::StoreStats &st = m->store->stats();
+    out->hits = st.hits;
+    out->misses = st.misses;
+    out->bytes_read = st.bytes_read;
+    out->evictions = st.evictions;
+    out->prefetch_issued = st.prefetch_issued;
+    out->prefetch_dropped = st.prefetch_dropped;
+    out->bytes_used = st.bytes_used;
+    out->budget_bytes = st.budget_bytes;
+    out->pinned_experts = st.pinned;
+    out->read_seconds = st.read_seconds;
+    return UT_OK;
+}
+
+int32_t ut_model_expert_usage(ut_model *m, int64_t *counts, int64_t n) {
+    UT_TRY(need_store(m));
+    const std::vector<int64_t> &u = m->store->usage();
+    if (!counts || n != (int64_t)u.size()) {
+        set_error(m->ctx, "expert usage holds %lld counts", (long long)u.size());
+        return UT_ERR_SHAPE;
+    }
+    std::copy(u.begin(), u.end(), counts);
+    return UT_OK;
+}
+
 int32_t ut_model_finalize(ut_model *m) {
     if (!m) return UT_ERR_ARG;
     if (m->finalized) return UT_OK;
@@ -1641,6 +1826,7 @@ void ut_model_free(ut_model *m) {
     for (auto &kv : m->tensors)
         if (kv.second.qt) ut_qtensor_free(kv.second.qt);
     for (void *p : m->device_allocs) (void)hipFree(p);
+    delete m->store;
     ut_ctx *ctx = m->ctx;
     delete m;
     ctx_release(ctx);

@@ -99,6 +99,11 @@ _SIGS = [
     ("ut_model_set_tensor", _i32, [_vp, C.c_char_p, _i32, _vp, _i64, _vp, _i64, _i64]),
     ("ut_model_finalize", _i32, [_vp]),
     ("ut_model_load_dir", _i32, [_vp, C.c_char_p, C.POINTER(_i64)]),
+    ("ut_model_load_dir_tiered", _i32, [_vp, C.c_char_p, _vp, C.POINTER(_i64)]),
+    ("ut_model_synthesize_tiered", _i32, [_vp, C.c_uint64, _f32, _i32, _i32, _vp, _i64]),
+    ("ut_model_pin_experts", _i32, [_vp, _vp, _i64, _i64, C.POINTER(_i64)]),
+    ("ut_model_store_stats", _i32, [_vp, _vp]),
+    ("ut_model_expert_usage", _i32, [_vp, _vp, _i64]),
     ("ut_model_synthesize", _i32, [_vp, C.c_uint64, _f32, _i32, _i32]),
     ("ut_model_device_bytes", _i64, [_vp]),
     ("ut_model_free", None, [_vp]),
@@ -167,6 +172,70 @@ class ModelConfig(C.Structure):
         return c
 
 
+class StoreConfig(C.Structure):
+    """ut_expert_store_config: cache budget, CachePolicy, pilot prefetch."""
+    _fields_ = [("hbm_budget_bytes", _i64), ("policy", _i32), ("prefetch", _i32)]
+
+
+class StoreStats(C.Structure):
+    """ut_store_stats (StoreStatsSnapshot)."""
+    _fields_ = [("hits", _i64), ("misses", _i64), ("bytes_read", _i64), ("evictions", _i64),
+                ("prefetch_issued", _i64), ("prefetch_dropped", _i64), ("bytes_used", _i64),
+                ("budget_bytes", _i64), ("pinned_experts", _i64), ("read_seconds", C.c_double)]
+
+    def as_dict(self) -> dict:
+        return {k: getattr(self, k) for k, _ in self._fields_}
+
+
+LRU, WEIGHTED = 0, 1
+
+
+class ExpertProfile:
+    """ExpertProfile (undertow-core/src/profile.rs:18-100): a hot-expert
+    histogram as JSON {version, architecture, counts: [[layer, expert, count]]},
+    counts sorted by count descending, then layer, then expert."""
+
+    VERSION = 1
+
+    def __init__(self, architecture: str, counts):
+        self.version = self.VERSION
+        self.architecture = architecture
+        self.counts = sorted(((int(l), int(e), int(c)) for l, e, c in counts),
+                             key=lambda t: (-t[2], t[0], t[1]))
+
+    @classmethod
+    def from_usage(cls, architecture: str, usage) -> "ExpertProfile":
+        u = np.asarray(usage)
+        return cls(architecture, [(l, e, u[l, e]) for l in range(u.shape[0])
+                                  for e in range(u.shape[1]) if u[l, e] > 0])
+
+    def save(self, path) -> None:
+        import json
+        Path(path).write_text(json.dumps({"version": self.version, "architecture": self.architecture,
+                                          "counts": [list(t) for t in self.counts]}, indent=2))
+
+    @classmethod
+    def load(cls, path) -> "ExpertProfile":
+        import json
+        d = json.loads(Path(path).read_text())
+        if d.get("version") != cls.VERSION:
+            raise ValueError(f"{path}: profile version {d.get('version')} unsupported "
+                             f"(expected {cls.VERSION})")
+        return cls(d["architecture"], d["counts"])
+
+    def merge(self, other: "ExpertProfile") -> None:
+        if other.architecture != self.architecture:
+            raise ValueError(f"cannot merge profile for architecture '{other.architecture}' "
+                             f"into '{self.architecture}'")
+        acc = {}
+        for l, e, c in self.counts + other.counts:
+            acc[(l, e)] = acc.get((l, e), 0) + c
+        self.counts = ExpertProfile(self.architecture, [(l, e, c) for (l, e), c in acc.items()]).counts
+
+    def hottest(self):
+        return [(l, e) for l, e, _ in self.counts]
+
+
 def _ptr(t) -> Optional[int]:
     """Device address of a torch tensor (or None)."""
     if t is None:
@@ -183,6 +252,12 @@ class Context:
     """A ut_ctx bound to torch's current stream on `device`."""
 
     def __init__(self, device: int = 0, bind_torch_stream: bool = True):
+        s = None
+        if bind_torch_stream:
+            # torch's HIP runtime first: it does not come up in a process
+            # where another runtime initialised the device before it
+            torch = _torch()
+            s = torch.cuda.current_stream(device).cuda_stream  # 0: the null stream
         h = _vp()
         rc = lib().ut_ctx_create(device, C.byref(h))
         if rc != UT_OK:
@@ -191,8 +266,6 @@ class Context:
         self.device = device
         self.own_stream = lib().ut_ctx_stream(self._h)
         if bind_torch_stream:
-            torch = _torch()
-            s = torch.cuda.current_stream(device).cuda_stream  # 0: the null stream
             self.check(lib().ut_ctx_set_stream(self._h, s))
 
     def __del__(self):
@@ -483,6 +556,43 @@ class Model:
 
     def finalize(self) -> None:
         self.ctx.check(lib().ut_model_finalize(self._h))
+
+    def load_dir_tiered(self, path, hbm_budget_bytes: int, policy: int = LRU,
+                        prefetch: bool = False) -> int:
+        """Dense tensors into HBM, routed experts behind the HBM tier of the
+        expert store; returns the bytes read at load."""
+        cfg = StoreConfig(hbm_budget_bytes, policy, int(prefetch))
+        n = _i64()
+        self.ctx.check(lib().ut_model_load_dir_tiered(self._h, str(path).encode(), C.byref(cfg),
+                                                      C.byref(n)))
+        return n.value
+
+    def synthesize_tiered(self, seed: int, hbm_budget_bytes: int, host_pool_experts: int,
+                          init_std: float = 0.02, expert_fmt: int = INT4, dense_fmt: int = INT8,
+                          policy: int = LRU, prefetch: bool = False) -> None:
+        cfg = StoreConfig(hbm_budget_bytes, policy, int(prefetch))
+        self.ctx.check(lib().ut_model_synthesize_tiered(self._h, seed, init_std, expert_fmt,
+                                                        dense_fmt, C.byref(cfg), host_pool_experts))
+
+    def pin_experts(self, keys, budget_bytes: int) -> int:
+        """pin_hottest over (layer, expert) keys; returns the pinned bytes."""
+        a = np.ascontiguousarray(np.asarray(keys, np.int32).reshape(-1, 2))
+        n = _i64()
+        self.ctx.check(lib().ut_model_pin_experts(self._h, a.ctypes.data if a.size else None,
+                                                  a.shape[0], budget_bytes, C.byref(n)))
+        return n.value
+
+    def store_stats(self) -> dict:
+        st = StoreStats()
+        self.ctx.check(lib().ut_model_store_stats(self._h, C.byref(st)))
+        return st.as_dict()
+
+    def expert_usage(self) -> np.ndarray:
+        L = self.cfg["num_hidden_layers"] + (1 if self.cfg.get("mtp") else 0)
+        E = self.cfg["n_routed_experts"]
+        u = np.zeros((L, E), np.int64)
+        self.ctx.check(lib().ut_model_expert_usage(self._h, u.ctypes.data, u.size))
+        return u
 
     def load_dir(self, path) -> int:
         """Stream a converted checkpoint directory into HBM and finalize;
