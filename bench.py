@@ -430,6 +430,80 @@ def mtp_bench(U, ctx, cfg, prompt_len, new_tokens, depths, seed, expert_fmt, den
     return res
 
 
+def c5_bench(U, ctx, torch, prompt_len=2048, new_tokens=256, pin_frac=0.25, seed=42,
+             pool_experts=1024):
+    """Config 5: DeepSeek-V3 671B-shaped random-init model at full depth.
+    Dense and shared weights (about 18.5 GB int8) are synthesized in HBM; the
+    333 GB of int4 routed experts sit behind the expert store's HBM tier with
+    a budget of the HBM left over, filled from a pinned host pool of
+    `pool_experts` seeded experts (key (layer, e) reads entry
+    (layer * 256 + e) mod pool_experts: every miss moves a real 22 MB
+    expert over the host link).  The prompt's prefill records a routing
+    profile; its hottest quarter of all routed experts is pinned; then
+    greedy and MTP depth-1 decode of `new_tokens` tokens, timed from the
+    first emitted token (prefill excluded), with pilot-router prefetch."""
+    from undertow_amd.configs import C5
+    free, total = torch.cuda.mem_get_info()
+    E, nL = C5["n_routed_experts"], C5["num_hidden_layers"] + 1 - C5["first_k_dense_replace"]
+    budget = int(free - 26e9)
+    m = U.Model(ctx, C5)
+    t0 = time.perf_counter()
+    m.synthesize_tiered(seed, budget, pool_experts, prefetch=True)
+    ctx.synchronize()
+    t_make = time.perf_counter() - t0
+    rng = np.random.default_rng(seed)
+    prompt = rng.integers(0, C5["vocab_size"], prompt_len).tolist()
+    t0 = time.perf_counter()
+    s = m.session()
+    s.prefill(prompt, want_logits=False)
+    t_prefill = time.perf_counter() - t0
+    del s
+    log(f"config 5: made in {t_make:.1f} s (budget {budget / 1e9:.1f} GB), prompt prefill "
+        f"{t_prefill:.1f} s, store {json.dumps(m.store_stats())}")
+    usage = m.expert_usage()
+    prof = U.ExpertProfile.from_usage("deepseek_v3", usage)
+    n_pin = int(pin_frac * E * nL)
+    slot = 2 * C5["moe_intermediate_size"] * (C5["hidden_size"] // 2) + \
+        C5["hidden_size"] * (C5["moe_intermediate_size"] // 2) + \
+        (2 * C5["moe_intermediate_size"] + C5["hidden_size"]) * 4
+    pinned = m.pin_experts(prof.hottest()[:n_pin], n_pin * (slot + 2048))
+    res = {"prompt": prompt_len, "new_tokens": new_tokens, "make_s": round(t_make, 2),
+           "prefill_s": round(t_prefill, 2), "hbm_budget_gb": round(budget / 1e9, 1),
+           "expert_gb_total": round(E * nL * slot / 1e9, 1),
+           "pinned_gb": round(pinned / 1e9, 1), "host_pool_experts": pool_experts}
+
+    def timed(run):
+        stamps = []
+        st0 = m.store_stats()
+        toks = run(lambda t: stamps.append(time.perf_counter()) or True)
+        st1 = m.store_stats()
+        dt = stamps[-1] - stamps[0]
+        d = {k: st1[k] - st0[k] for k in ("hits", "misses", "bytes_read", "prefetch_issued")}
+        return toks, (len(stamps) - 1) / dt, dt, d
+
+    toks, tps, dt, d = timed(lambda cb: m.generate(prompt, new_tokens, on_token=cb))
+    res["greedy_tok_s"] = round(tps, 3)
+    res["greedy_store"] = dict(d, hit_rate=round(d["hits"] / max(d["hits"] + d["misses"], 1), 4),
+                               host_link_gbs=round(d["bytes_read"] / dt / 1e9, 2),
+                               gb_per_token=round(d["bytes_read"] / max(len(toks), 1) / 1e9, 3))
+    log(f"config 5 greedy: {res['greedy_tok_s']} tok/s, {json.dumps(res['greedy_store'])}")
+    out, drafted, accepted = [], 0, 0
+
+    def mtp_run(cb):
+        nonlocal drafted, accepted
+        t, drafted, accepted = m.speculative_loop(prompt, new_tokens, depth=1, on_token=cb)
+        return t
+
+    mt, tps, dt, d = timed(mtp_run)
+    res["mtp1"] = {"tok_s": round(tps, 3), "drafted": drafted, "accepted": accepted,
+                   "lossless": mt == toks,
+                   "store": dict(d, hit_rate=round(d["hits"] / max(d["hits"] + d["misses"], 1), 4),
+                                 host_link_gbs=round(d["bytes_read"] / dt / 1e9, 2))}
+    res["evictions"] = m.store_stats()["evictions"]
+    del m
+    return res
+
+
 def committed_traffic() -> float | None:
     """HBM bytes per `k_moe_gate_up<int4,1>` launch, from the committed
     counter summary: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes over
@@ -490,6 +564,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--mtp", default="c1,c4", help="comma list of c1,c4 or 'none'")
+    ap.add_argument("--c5", action="store_true", default=True,
+                    help="config 5 (full depth, experts behind the HBM tier; default on)")
+    ap.add_argument("--no-c5", dest="c5", action="store_false")
+    ap.add_argument("--c5-tokens", type=int, default=256)
+    ap.add_argument("--c5-prompt", type=int, default=2048)
+    ap.add_argument("--c5-only", action="store_true",
+                    help="only the config 5 leg (no JSON line)")
     ap.add_argument("--variants", action="store_true", default=True)
     ap.add_argument("--no-variants", dest="variants", action="store_false")
     ap.add_argument("--mla", action="store_true", default=True,
@@ -514,6 +595,12 @@ def main():
         sys.exit(2)
     if args.profile_decode:
         profile_decode(args.profile_decode, args.prompt, args.tokens)
+        return
+    if args.c5_only:
+        import torch
+        import undertow_amd as U
+        r = c5_bench(U, U.Context(0), torch, prompt_len=args.c5_prompt, new_tokens=args.c5_tokens)
+        print(json.dumps(r), flush=True)
         return
     if args.read_floor:
         import torch
@@ -599,6 +686,13 @@ def main():
         log(f"MTP {name}: {json.dumps(mtp[name])}")
         torch.cuda.empty_cache()
 
+    c5 = {}
+    if args.c5:
+        log("config 5: full depth, routed experts behind the expert store's HBM tier")
+        c5 = c5_bench(U, ctx, torch, prompt_len=args.c5_prompt, new_tokens=args.c5_tokens)
+        log(f"config 5: {json.dumps(c5)}")
+        torch.cuda.empty_cache()
+
     cpu = None
     if not args.skip_cpu:
         log("CPU baseline (reference CPU path restated, host cores)")
@@ -647,6 +741,7 @@ def main():
                      for k, v in variants.items()},
         "mla": mla,
         "mtp": mtp,
+        "c5": c5,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -120,3 +120,24 @@ def test_missing_expert_shard_is_reported(ctx, tmp_path):
     with pytest.raises(U.UtError) as ei:
         fresh(ctx, ck).load_dir_tiered(tmp_path, hbm_budget_bytes=1 << 20)
     assert ei.value.code == U.runtime.UT_ERR_IO
+
+
+def test_synthesized_model_with_a_host_pool(ctx):
+    """ut_model_synthesize_tiered: dense weights on the device, routed
+    experts from a pinned host pool behind a three-expert budget."""
+    import undertow_amd as U
+    cfg = dict(C1, num_hidden_layers=3)
+    ck = checkpoint(cfg, fmt="int4")
+    m = fresh(ctx, ck)
+    m.synthesize_tiered(7, hbm_budget_bytes=3 * expert_bytes(ck), host_pool_experts=5,
+                        prefetch=True)
+    prompt = prompt_ids(16, C1["vocab_size"])
+    toks = m.generate_greedy(prompt, 16)
+    assert len(toks) == 16
+    assert m.generate_mtp(prompt, 16, depth=1)[0] == toks
+    st = m.store_stats()
+    assert st["misses"] > 0 and st["hits"] > 0 and st["bytes_read"] > 0
+    usage = m.expert_usage()
+    assert usage.shape == (4, 8) and usage[0].sum() == 0 and usage[1:].sum() > 0
+    prof = U.ExpertProfile.from_usage("deepseek_moe", usage)
+    assert prof.counts[0][2] == usage.max()

@@ -21,6 +21,12 @@ C4 = dict(vocab_size=129280, hidden_size=7168, intermediate_size=18432,
           qk_rope_head_dim=64, v_head_dim=128, rms_norm_eps=1e-6, rope_theta=10000.0, mtp=1,
           max_position_embeddings=1024)
 
+# C5: DeepSeek-V3 671B's shape at full depth (61 layers, the first 3 dense),
+# context for a 2048-token prompt plus 256 new tokens.  Its routed experts
+# (59 MoE layers with the MTP module x 256 x 22 MB = 333 GB int4) exceed HBM
+# and run behind the expert store's HBM tier.
+C5 = dict(C4, num_hidden_layers=61, first_k_dense_replace=3, max_position_embeddings=2560)
+
 # C2: one routed-expert block at DeepSeek-V3 expert shape.
 C2 = dict(hidden=7168, inter=2048, n_experts=256, top_k=8, n_group=8, topk_group=4,
           norm_topk_prob=1, routed_scaling_factor=2.5)

@@ -90,6 +90,7 @@ private:
     void evict(int slot);
     void enforce_budget(const std::unordered_set<int64_t> &keep);
     double effective(const Slot &s) const;
+    void fill_pool(unsigned t, unsigned nt, int64_t pool_experts, uint64_t seed, float std, float qmax);
 
     ut_ctx *ctx_ = nullptr;
     int64_t L_ = 0, E_ = 0, H_ = 0, I_ = 0, capacity_ = 0;

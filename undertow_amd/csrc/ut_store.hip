@@ -3,6 +3,7 @@
 #include "ut_store.h"
 
 #include <chrono>
+#include <thread>
 #include <cmath>
 #include <cstring>
 
@@ -142,9 +143,24 @@ int32_t ExpertStore::attach_host_pool(int64_t pool_experts, uint64_t seed, float
     }
     host_pool_n_ = pool_experts;
     // seeded experts: codes uniform over the format's range, per-row scales
-    // |N(0, std)| / qmax (the synthetic benchmark's distributions)
+    // |N(0, std)| / qmax (the synthetic benchmark's distributions); every
+    // expert a pure function of (seed, index), filled by a few threads
     const float qmax = fmt_ == UT_FMT_INT4 ? 7.0f : 127.0f;
-    for (int64_t x = 0; x < pool_experts; x++) {
+    unsigned nt = std::thread::hardware_concurrency();
+    nt = nt < 1 ? 1 : (nt > 16 ? 16 : nt);
+    std::vector<std::thread> pool;
+    for (unsigned t = 0; t < nt; t++)
+        pool.emplace_back([this, t, nt, pool_experts, seed, std, qmax]() {
+            fill_pool(t, nt, pool_experts, seed, std, qmax);
+        });
+    for (auto &th : pool) th.join();
+    source_ = HOST_POOL;
+    return UT_OK;
+}
+
+void ExpertStore::fill_pool(unsigned t, unsigned nt, int64_t pool_experts, uint64_t seed, float std,
+                            float qmax) {
+    for (int64_t x = t; x < pool_experts; x += nt) {
         char *base = host_pool_ + x * slot_bytes_;
         for (int i = 0; i < 3; i++) {
             uint64_t *w = (uint64_t *)(base + off_[i]);
@@ -172,8 +188,6 @@ int32_t ExpertStore::attach_host_pool(int64_t pool_experts, uint64_t seed, float
             }
         }
     }
-    source_ = HOST_POOL;
-    return UT_OK;
 }
 
 double ExpertStore::effective(const Slot &s) const {
