@@ -461,9 +461,6 @@ int32_t mlp_add(ut_session *s, const MlpW &w, const float *x, const XDigits &xd,
     return UT_OK;
 }
 
-// The routed part of moe_forward (model.rs:195-281): router, routed experts
-// in choice order, into out (overwritten).  x: normed rows (f32, for the f32
-// router gate) with digits xd.
 // The routed experts of M rows through the HBM tier: the choices (and, at
 // one row with pilot hints on, the next MoE layer's predicted choices:
 // pilot_prefetch, model.rs:290-318, on the post-attention residual `resid`)
@@ -502,6 +499,9 @@ int32_t tiered_experts(ut_session *s, const LayerW &L, const float *resid, int64
     return UT_OK;
 }
 
+// The routed part of moe_forward (model.rs:195-281): router, routed experts
+// in choice order, into out (overwritten).  x: normed rows (f32, for the f32
+// router gate) with digits xd.
 int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigits &xd,
                     int64_t rows, float *out, int accumulate = 0, const MlpW *shared = nullptr,
                     const NormNext *next = nullptr) {
