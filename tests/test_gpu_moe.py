@@ -262,6 +262,38 @@ def test_moe_route_experts_matches_route_then_experts(ctx, fmt, H, I, Ms, bias):
         assert (np.abs(host(out) - want) <= tol).all(), (M, np.abs(host(out) - want).max())
 
 
+@pytest.mark.parametrize("fmt", [INT4, INT8])
+def test_moe_one_row_equals_two_rows_repeated(ctx, fmt):
+    """One row and two rows take different gate/up kernels (the one-row
+    kernel plans and digitises x itself).  Over many calls, with the routing
+    inside the call and without, the one-row result equals each row of the
+    two-row call on the duplicated row bit for bit, and the oracle within the
+    expert bar."""
+    import undertow_amd as U
+    rng = np.random.default_rng(77 + fmt)
+    E, H, I, k = 16, 1024, 512, 8
+    tbl, host_w = make_experts(ctx, rng, fmt, E, H, I)
+    for it in range(40):
+        ids = rng.permutation(E)[:k].astype(np.int32)[None]
+        w = rng.random((1, k)).astype(np.float32)
+        x = rng.standard_normal((1, H)).astype(np.float32)
+        one = host(tbl.moe_experts(dev(ids), dev(w), dev(x)))
+        two = host(tbl.moe_experts(dev(np.repeat(ids, 2, 0)), dev(np.repeat(w, 2, 0)),
+                                   dev(np.repeat(x, 2, 0))))
+        assert np.array_equal(one[0], two[0]) and np.array_equal(one[0], two[1]), it
+        if it % 10 == 0:
+            want = oracle_moe(fmt, H, I, host_w, ids, w, x)
+            assert (np.abs(one - want) <= 1e-4 * np.maximum(np.abs(want), 1.0)).all(), it
+    logits = rng.standard_normal((1, E)).astype(np.float32)
+    x = rng.standard_normal((1, H)).astype(np.float32)
+    for it in range(20):
+        out, ids, w = tbl.moe_route_experts(dev(logits), None, dev(x), k, 4, 2, True, 2.5)
+        ref = tbl.moe_experts(ids, w, dev(np.repeat(x, 1, 0)))
+        assert np.array_equal(host(out), host(ref)), it
+        logits = rng.standard_normal((1, E)).astype(np.float32)
+    ctx.synchronize()
+
+
 @pytest.mark.parametrize("H", [64, 256])  # 256: the gate/up launch resolves the plan
 def test_moe_bad_expert_is_reported(ctx, H):
     import undertow_amd as U
