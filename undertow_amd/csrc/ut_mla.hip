@@ -168,9 +168,16 @@ __global__ __launch_bounds__(256) void k_mla_combine(const float *__restrict__ p
 //           transposing read (ds_read_b64_tr_b16: within each 16-lane group,
 //           lane j supplies 4 consecutive dims of row 4q + j/4 and lane i
 //           receives dim i of the group's 4 rows).
-// LDS rows keep their 16-byte chunks XOR-swizzled by a permutation of the
-// row's low 3 bits, which leaves both read patterns free of bank conflicts.
-// 76 KiB of LDS and < 256 registers per lane let two workgroups share a CU.
+// LDS has 64 banks (256 bytes per pass: 16 lanes of a 16-byte read, 32
+// lanes of an 8-byte read).  Every 2,304-byte row starts at bank 0, so a
+// row's 16-byte chunks are XOR-swizzled by mla_swz(r), a 4-bit permutation
+// of the row index (chunk groups of 16 stay inside the 144-chunk row):
+// the score read's 16 lanes (rows 0-15, one chunk) get 16 distinct slots,
+// and the transposing read's 32 lanes (4 consecutive rows x 4 chunks of a
+// 4-aligned group) too, since rows 4k..4k+3 differ in the swizzle's high
+// two bits.  The score exchange rows are padded to 20 floats (80-byte
+// stride: 16 lanes at distinct 16-byte slots).
+// 77 KiB of LDS and < 256 registers per lane let two workgroups share a CU.
 // The slice writes (m, l, O) to the partial buffers, k_mla_combine_mfma
 // merges the slices.  The slice length depends only on the row's context
 // length, so a row's result is the same whichever rows share the call.
@@ -216,7 +223,7 @@ struct MlaMfmaArgs {
 constexpr int kRowChunks = 144;       // 16-byte chunks per position (576 hi + 576 lo)
 constexpr float kMlaHeadroom = 8.0f;  // nats a score may exceed the running offset
 
-__device__ __forceinline__ int mla_swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+__device__ __forceinline__ int mla_swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 __device__ __forceinline__ int mla_slot(int r, int c) { return r * kRowChunks + (c ^ mla_swz(r)); }
 
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
@@ -251,7 +258,8 @@ __global__ __launch_bounds__(256, 2) void k_mla_mfma16(MlaMfmaArgs a) {
     typedef float f32x4l_t __attribute__((ext_vector_type(4)));
     __shared__ __attribute__((aligned(16))) uint8_t sT0[kTile16Bytes];
     __shared__ __attribute__((aligned(16))) uint8_t sT1[kTile16Bytes];
-    __shared__ __attribute__((aligned(16))) float sS[2][32][kTile16];  // [dim half][column][position]
+    // [dim half][column][position], rows padded to 20 floats
+    __shared__ __attribute__((aligned(16))) float sS[2][32][kTile16 + 4];
     const int b = blockIdx.x, x8 = b & 7, q = b >> 3;
     const int group = q % a.groups;
     const int slice = (q / a.groups) * 8 + x8;
