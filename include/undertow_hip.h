@@ -141,6 +141,18 @@ int32_t ut_qtensor_dequantize(ut_ctx *ctx, const ut_qtensor *qt, float *out_dev)
  * (the reference's "threading never changes numerics"). */
 int32_t ut_qtensor_matmul(ut_ctx *ctx, const ut_qtensor *qt, float *out_dev, int64_t out_len,
                           const float *x_dev, int64_t x_len, int64_t seq);
+/* set_fast_int8 / fast_int8_enabled (undertow-quant/src/lib.rs:31-43): the
+ * opt-in fast path for int8 matmuls, per context here (the reference's
+ * switch is process-global).  While on, ut_qtensor_matmul and
+ * ut_qtensor_matvec_rows on int8 tensors quantise each activation row to i8
+ * with one scale (quantize_activations, lib.rs:46-59) and take the exact
+ * integer dot (avx512.rs:221-242, neon.rs:139-184):
+ * out = (acc as f32) * a_scale * scale[o].  It changes numerics (about 1e-2
+ * relative; the reference bounds it at 3% of the row magnitude) and is off
+ * by default.  The model's own projections and the expert block keep exact
+ * numerics. */
+int32_t ut_set_fast_int8(ut_ctx *ctx, int32_t enabled);
+int32_t ut_fast_int8_enabled(const ut_ctx *ctx);
 /* QTensor::add_scaled_row (qtensor.rs:516-543): acc[i] += (factor*scale[row])*q[row,i]. */
 int32_t ut_qtensor_add_scaled_row(ut_ctx *ctx, const ut_qtensor *qt, int64_t row, float factor,
                                   float *acc_dev);

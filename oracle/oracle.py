@@ -92,6 +92,9 @@ def _load(name):
         L.uto_quantize.argtypes = [C.c_int, _f32p, C.c_int64, C.c_int64, C.c_void_p, _f32p]
         L.uto_dequantize.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, _f32p]
         L.uto_matmul.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, _f32p, C.c_int64, _f32p]
+        L.uto_quantize_activations.argtypes = [_f32p, C.c_int64, C.c_void_p]
+        L.uto_quantize_activations.restype = C.c_float
+        L.uto_matmul_fast_i8.argtypes = [C.c_void_p, _f32p, C.c_int64, C.c_int64, _f32p, C.c_int64, _f32p]
         L.uto_add_scaled_row.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_float, _f32p]
         L.uto_matvec_rows.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_int64, _f32p, _f32p]
         L.uto_rmsnorm.argtypes = [_f32p, _f32p, _f32p, C.c_int64, C.c_float]
@@ -235,6 +238,26 @@ def matmul(fmt: int, payload: np.ndarray, scales, out_dim: int, in_dim: int, x: 
     sc = None if scales is None else np.ascontiguousarray(scales, np.float32)
     lib().uto_matmul(fmt, _vp(payload), None if sc is None else _vp(sc), out_dim, in_dim,
                      x.reshape(-1), seq, out)
+    return out.reshape(seq, out_dim)
+
+
+def quantize_activations(x: np.ndarray):
+    """lib.rs:46-59: (i8 codes, scale) of one activation row."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    q = np.zeros(x.size, np.int8)
+    s = lib().uto_quantize_activations(x, x.size, _vp(q))
+    return q, np.float32(s)
+
+
+def matmul_fast_i8(payload: np.ndarray, scales, out_dim: int, in_dim: int,
+                   x: np.ndarray) -> np.ndarray:
+    """The opt-in fast-int8 matmul (avx512.rs:221-242): x [seq, in] -> [seq, out]."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, in_dim)
+    seq = x.shape[0]
+    out = np.zeros(seq * out_dim, np.float32)
+    q = np.ascontiguousarray(payload).view(np.int8)
+    sc = np.ascontiguousarray(scales, np.float32)
+    lib().uto_matmul_fast_i8(_vp(q), sc, out_dim, in_dim, x.reshape(-1), seq, out)
     return out.reshape(seq, out_dim)
 
 

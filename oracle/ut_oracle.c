@@ -138,6 +138,51 @@ int uto_quantize(int fmt, const float *w, int64_t out_dim, int64_t in_dim,
     return 0;
 }
 
+/* lib.rs:46-59 */
+float uto_quantize_activations(const float *x, int64_t n, int8_t *out) {
+    float max = 0.0f;
+    for (int64_t i = 0; i < n; i++) {
+        /* f32::max returns the other operand when one is NaN */
+        const float a = fabsf(x[i]);
+        if (!(a <= max) && !isnan(a)) max = a;
+    }
+    if (max == 0.0f) {
+        memset(out, 0, (size_t)n);
+        return 0.0f;
+    }
+    const float scale = max / 127.0f;
+    const float inv = 127.0f / max;
+    for (int64_t i = 0; i < n; i++) {
+        float t = roundf(x[i] * inv);
+        /* clamp keeps NaN; `as i8` maps NaN to 0 */
+        if (isnan(t)) {
+            out[i] = 0;
+            continue;
+        }
+        t = t < -127.0f ? -127.0f : t > 127.0f ? 127.0f : t;
+        out[i] = (int8_t)t;
+    }
+    return scale;
+}
+
+/* avx512.rs:221-242: per row, the activations quantised once, then for
+ * every output row the exact integer dot (dot_i8_vnni's total - 128 * sum_b
+ * + tail is the plain sum of products) as f32 times a_scale times scale. */
+void uto_matmul_fast_i8(const int8_t *q, const float *scales, int64_t out_dim, int64_t in_dim,
+                        const float *x, int64_t seq, float *out) {
+    int8_t *qa = (int8_t *)malloc((size_t)(in_dim > 0 ? in_dim : 1));
+    for (int64_t s = 0; s < seq; s++) {
+        const float a_scale = uto_quantize_activations(x + s * in_dim, in_dim, qa);
+        for (int64_t o = 0; o < out_dim; o++) {
+            const int8_t *row = q + o * in_dim;
+            int32_t acc = 0;
+            for (int64_t i = 0; i < in_dim; i++) acc += (int32_t)qa[i] * (int32_t)row[i];
+            out[s * out_dim + o] = ((float)acc * a_scale) * scales[o];
+        }
+    }
+    free(qa);
+}
+
 void uto_add_scaled_row(int fmt, const void *payload, const float *scales,
                         int64_t out_dim, int64_t in_dim, int64_t row,
                         float factor, float *acc) {

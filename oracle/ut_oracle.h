@@ -63,6 +63,17 @@ void uto_dequantize(int fmt, const void *payload, const float *scales,
 void uto_matmul(int fmt, const void *payload, const float *scales,
                 int64_t out_dim, int64_t in_dim, const float *x, int64_t seq,
                 float *out);
+/* The opt-in fast-int8 path (undertow-quant/src/lib.rs:31-59): one
+ * activation row quantised symmetrically to i8 with one scale
+ * (quantize_activations: max = fold of max(|v|) from 0, which skips NaN;
+ * scale = max/127, inv = 127/max, q = round(v*inv) half away from zero,
+ * clamped to +-127, NaN -> 0; a zero row gives scale 0), then
+ * avx512::matmul_i8_vnni (avx512.rs:221-242) / neon::matmul_i8_sdot
+ * (neon.rs:139-184): out[s,o] = (acc as f32) * a_scale * scale[o] with acc
+ * the exact integer dot of the i8 activations and the i8 codes. */
+float uto_quantize_activations(const float *x, int64_t n, int8_t *out);
+void uto_matmul_fast_i8(const int8_t *q, const float *scales, int64_t out_dim, int64_t in_dim,
+                        const float *x, int64_t seq, float *out);
 /* QTensor::add_scaled_row (qtensor.rs:516-543). */
 void uto_add_scaled_row(int fmt, const void *payload, const float *scales,
                         int64_t out_dim, int64_t in_dim, int64_t row,

@@ -235,3 +235,65 @@ def test_quantize_rejects_non_finite(ctx):
             U.QTensor.quantize(ctx, dev(w), fmt)
         assert ei.value.code == U.runtime.UT_ERR_FORMAT
         assert "flat index 27 (row 2, col 7)" in str(ei.value)
+
+
+# ------------------------------------------------------------ fast int8
+@pytest.mark.parametrize("o,i,seq", [(4, 64, 2), (7, 130, 2), (3, 16, 2), (512, 7168, 3),
+                                     (129, 1000, 1), (2048, 2048, 4)])
+def test_fast_int8_matches_oracle(ctx, o, i, seq):
+    """set_fast_int8 (lib.rs:31-59, avx512.rs:221-242): bit for bit the
+    oracle's restatement, within the reference's 3 % of the row magnitude of
+    the exact path (neon.rs:257-278), and off again restores the exact
+    path."""
+    import torch
+    rng = np.random.default_rng(900 + o + i)
+    w = rng.uniform(-1.0, 1.0, (o, i)).astype(np.float32)
+    q, s = O.quantize(w, INT8)
+    qt = upload(ctx, INT8, q, s, o, i)
+    x = rng.uniform(-1.0, 1.0, (seq, i)).astype(np.float32)
+    exact = run_matmul(ctx, qt, x)
+    assert not ctx.fast_int8_enabled()
+    ctx.set_fast_int8(True)
+    try:
+        assert ctx.fast_int8_enabled()
+        got = run_matmul(ctx, qt, x)
+        # matvec_rows takes the same path
+        out = torch.full((o // 2 + 1,), float("nan"), device="cuda:0")
+        qt.matvec_rows(o // 3, o // 2 + 1, dev(x[0]), out)
+        rows = host(out)
+    finally:
+        ctx.set_fast_int8(False)
+    want = O.matmul_fast_i8(q, s, o, i, x)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(rows.view(np.uint32), want[0, o // 3:o // 3 + o // 2 + 1].view(np.uint32))
+    mag = np.maximum(np.abs(exact).max(axis=1, keepdims=True), 1e-3)
+    assert (np.abs(got - exact) <= 0.03 * mag).all()
+    assert np.array_equal(run_matmul(ctx, qt, x), exact)
+
+
+def test_fast_int8_edges_and_other_formats(ctx):
+    """Zero, NaN and infinite activation rows as the oracle has them; int4
+    and f32 tensors keep the exact path while the switch is on."""
+    rng = np.random.default_rng(44)
+    o, i = 8, 64
+    q = rng.integers(-127, 128, (o, i)).astype(np.int8).view(np.uint8)
+    s = (rng.random(o) * 0.1 + 0.01).astype(np.float32)
+    qt = upload(ctx, INT8, q, s, o, i)
+    x = rng.standard_normal((4, i)).astype(np.float32)
+    x[0] = 0.0
+    x[1, 5] = np.nan
+    x[2, 7] = np.inf
+    p4, s4 = rand_qtensor(rng, INT4, o, i)
+    qt4 = upload(ctx, INT4, p4, s4, o, i)
+    exact4 = run_matmul(ctx, qt4, x[3:])
+    ctx.set_fast_int8(True)
+    try:
+        got = run_matmul(ctx, qt, x)
+        got4 = run_matmul(ctx, qt4, x[3:])
+    finally:
+        ctx.set_fast_int8(False)
+    want = O.matmul_fast_i8(q, s, o, i, x)
+    assert np.array_equal(got[0], np.zeros(o, np.float32))
+    assert np.array_equal(got[[0, 1, 3]].view(np.uint32), want[[0, 1, 3]].view(np.uint32))
+    assert np.isnan(got[2]).all() and np.isnan(want[2]).all()
+    assert np.array_equal(got4, exact4)

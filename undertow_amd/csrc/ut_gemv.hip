@@ -983,6 +983,100 @@ int32_t matmul_dev(ut_ctx *ctx, const ut_qtensor *w, const float *x, int64_t M, 
 
 using namespace ut;
 
+// ------------------------------------------------------ fast int8 ---
+// The opt-in fast-int8 path (undertow-quant/src/lib.rs:31-59,
+// avx512.rs:221-242).  k_act_quant_i8: one workgroup per activation row,
+// quantize_activations: max = max|v| over the row skipping NaN (f32::max
+// keeps the non-NaN operand, fmaxf too), scale = max/127, inv = 127/max,
+// code = round(v*inv) half away from zero, clamped to +-127, NaN -> 0; a
+// zero row gets scale 0 and zero codes.  Rows of xq are kp bytes (zero
+// padded to 16).
+__global__ __launch_bounds__(256) void k_act_quant_i8(const float *__restrict__ x, int64_t K,
+                                                      int8_t *__restrict__ xq, int64_t kp,
+                                                      float *__restrict__ ascale) {
+    __shared__ float red[4];
+    const int64_t m = blockIdx.x;
+    const float *xr = x + m * K;
+    float mx = 0.0f;
+    for (int64_t i = threadIdx.x; i < K; i += 256) mx = fmaxf(mx, fabsf(xr[i]));
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const bool zero = mx == 0.0f;
+    const float inv = zero ? 0.0f : __fdiv_rn(127.0f, mx);
+    if (threadIdx.x == 0) ascale[m] = zero ? 0.0f : __fdiv_rn(mx, 127.0f);
+    int8_t *qr = xq + m * kp;
+    for (int64_t i = threadIdx.x; i < kp; i += 256) {
+        int q = 0;
+        if (i < K && !zero) {
+            const float t = roundf(__fmul_rn(xr[i], inv));
+            q = isnan(t) ? 0 : (int)fminf(fmaxf(t, -127.0f), 127.0f);
+        }
+        qr[i] = (int8_t)q;
+    }
+}
+
+// One wave per output row: the exact integer dot of the row's i8 codes and
+// the row's quantised activations (v_dot4 over 16-byte steps when K % 16 ==
+// 0, bytes otherwise), then (acc as f32) * a_scale * scale[o].  Grid
+// (ceil(O / 4), seq).
+__global__ __launch_bounds__(256) void k_gemv_fast_i8(const int8_t *__restrict__ w,
+                                                      const float *__restrict__ scales, int64_t O,
+                                                      int64_t K, const int8_t *__restrict__ xq,
+                                                      int64_t kp, const float *__restrict__ ascale,
+                                                      float *__restrict__ out, int64_t ldo) {
+    const int64_t o = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t m = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    if (o >= O) return;
+    const int8_t *wr = w + o * K;
+    const int8_t *xr = xq + m * kp;
+    int32_t acc = 0;
+    if ((K & 15) == 0) {
+        for (int64_t c = 16 * (int64_t)lane; c < K; c += 1024) {
+            const uint4 wv = ld_weights(wr + c);
+            const uint4 xv = *(const uint4 *)(xr + c);
+            acc = __builtin_amdgcn_sdot4((int)wv.x, (int)xv.x, acc, false);
+            acc = __builtin_amdgcn_sdot4((int)wv.y, (int)xv.y, acc, false);
+            acc = __builtin_amdgcn_sdot4((int)wv.z, (int)xv.z, acc, false);
+            acc = __builtin_amdgcn_sdot4((int)wv.w, (int)xv.w, acc, false);
+        }
+    } else {
+        for (int64_t c = lane; c < K; c += 64) acc += (int32_t)wr[c] * (int32_t)xr[c];
+    }
+    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if (lane == 0) out[m * ldo + o] = __fmul_rn(__fmul_rn((float)acc, ascale[m]), scales[o]);
+}
+
+static int32_t matmul_fast_i8(ut_ctx *ctx, const ut_qtensor *qt, float *out, const float *x,
+                              int64_t seq) {
+    const int64_t K = qt->in_dim, O = qt->out_dim, kp = (K + 15) / 16 * 16;
+    ScratchPlan plan;
+    plan.add((size_t)(seq * kp));
+    plan.add((size_t)seq * 4);
+    std::vector<void *> ptrs;
+    UT_TRY(scratch_acquire(ctx, plan, ptrs));
+    int8_t *xq = (int8_t *)ptrs[0];
+    float *as = (float *)ptrs[1];
+    int tok = timing_begin(ctx, "gemv_fast_i8");
+    hipLaunchKernelGGL(k_act_quant_i8, dim3((unsigned)seq), dim3(256), 0, ctx->stream, x, K, xq,
+                       kp, as);
+    hipLaunchKernelGGL(k_gemv_fast_i8, dim3((unsigned)((O + 3) / 4), (unsigned)seq), dim3(256), 0,
+                       ctx->stream, (const int8_t *)qt->payload, qt->scales, O, K, xq, kp, as, out,
+                       O);
+    timing_end(ctx, tok);
+    return launch_check(ctx, "k_gemv_fast_i8");
+}
+
+extern "C" int32_t ut_set_fast_int8(ut_ctx *ctx, int32_t enabled) {
+    if (!ctx) return UT_ERR_ARG;
+    ctx->fast_int8 = enabled != 0;
+    return UT_OK;
+}
+
+extern "C" int32_t ut_fast_int8_enabled(const ut_ctx *ctx) { return ctx && ctx->fast_int8 ? 1 : 0; }
+
 extern "C" int32_t ut_qtensor_matmul(ut_ctx *ctx, const ut_qtensor *qt, float *out_dev,
                                      int64_t out_len, const float *x_dev, int64_t x_len,
                                      int64_t seq) {
@@ -1002,6 +1096,8 @@ extern "C" int32_t ut_qtensor_matmul(ut_ctx *ctx, const ut_qtensor *qt, float *o
         return UT_ERR_SHAPE;
     }
     if (seq == 0) return UT_OK;
+    // Int8 { .. } if fast_int8_enabled() (qtensor.rs:385-398)
+    if (qt->fmt == UT_FMT_INT8 && ctx->fast_int8) return matmul_fast_i8(ctx, qt, out_dev, x_dev, seq);
     GemvArgs ga;
     ga.w = qt;
     ga.M = seq;

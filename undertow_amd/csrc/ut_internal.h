@@ -76,6 +76,8 @@ struct ut_ctx {
     // working array (ut_moe_experts_noalloc), from hipGetSymbolAddress at
     // context creation.
     void *noalloc_scratch = nullptr;
+    // The opt-in fast-int8 matmul (ut_set_fast_int8): off by default.
+    bool fast_int8 = false;
     // Handle lifetime: models hold a reference on their context and
     // sessions on their model, so the handles may be released in any order.
     int refs = 1;

@@ -82,6 +82,8 @@ _SIGS = [
     ("ut_qtensor_download", _i32, [_vp, _vp, _vp, _i64, _vp]),
     ("ut_qtensor_matmul", _i32, [_vp, _vp, _vp, _i64, _vp, _i64, _i64]),
     ("ut_qtensor_add_scaled_row", _i32, [_vp, _vp, _i64, _f32, _vp]),
+    ("ut_set_fast_int8", _i32, [_vp, _i32]),
+    ("ut_fast_int8_enabled", _i32, [_vp]),
     ("ut_qtensor_matvec_rows", _i32, [_vp, _vp, _i64, _i64, _vp, _i64, _vp, _i64]),
     ("ut_route", _i32, [_vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _i32, _f32, _vp, _vp]),
     ("ut_expert_table_create", _i32, [_vp, _i64, _i64, _i64, C.POINTER(_vp)]),
@@ -298,6 +300,14 @@ class Context:
 
     def enable_timing(self, on: bool) -> None:
         self.check(lib().ut_ctx_enable_timing(self._h, int(on)))
+
+    def set_fast_int8(self, enabled: bool) -> None:
+        """set_fast_int8 (undertow-quant/src/lib.rs:37-39), for this context:
+        int8 QTensor matmuls quantise their activations to i8."""
+        self.check(lib().ut_set_fast_int8(self._h, int(enabled)))
+
+    def fast_int8_enabled(self) -> bool:
+        return bool(lib().ut_fast_int8_enabled(self._h))
 
     def probe_read_bandwidth(self, buf, reps: int = 10) -> float:
         """GB/s of a plain non-temporal read of the device tensor `buf`."""
