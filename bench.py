@@ -429,6 +429,18 @@ def mtp_bench(U, ctx, cfg, prompt_len, new_tokens, depths, seed, expert_fmt, den
     greedy = m.generate_greedy(prompt, new_tokens)
     dt = time.perf_counter() - t0 - t_prefill
     res["greedy_tok_s"] = len(greedy) / dt
+    # the same decode with one-row steps replayed from a captured graph
+    before = m.graph_stats()
+    m.enable_graphs(True)
+    t0 = time.perf_counter()
+    greedy_g = m.generate_greedy(prompt, new_tokens)
+    dt = time.perf_counter() - t0 - t_prefill
+    m.enable_graphs(False)
+    after = m.graph_stats()
+    assert greedy_g == greedy, "graph replay output differs from the eager decode"
+    res["greedy_graph"] = {"tok_s": len(greedy_g) / dt,
+                           "replays": after["replays"] - before["replays"],
+                           "failures": after["failures"] - before["failures"]}
     for d in depths:
         t0 = time.perf_counter()
         toks, drafted, accepted = m.generate_mtp(prompt, new_tokens, depth=d)

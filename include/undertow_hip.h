@@ -385,6 +385,23 @@ int64_t ut_session_position(const ut_session *s);
  * honours.  Empty until set. */
 int32_t ut_model_set_stop_ids(ut_model *m, const int32_t *ids, int64_t n);
 
+/* No reference counterpart (the reference runs on the CPU): one-row decode
+ * steps of the greedy loop (ut_generate) replayed from a graph captured on
+ * the context's stream, instead of about 40-60 kernel launches per token
+ * from the host.  Every position-dependent kernel of the step reads the
+ * session's position from device memory, attention grids are sized for the
+ * session's capacity (workgroups past the context exit at once), and the
+ * step advances the position itself.  Outputs are identical to the eager
+ * launches.  A session captures on its second one-row step; if capturing
+ * fails (or the graph would hold anything but kernel launches) the session
+ * stays eager.  Not used with the expert tier or kernel timing on.  Off by
+ * default. */
+int32_t ut_model_enable_graphs(ut_model *m, int32_t on);
+/* Counts since the model was made: graphs captured, steps replayed from
+ * them, captures given up (each pointer may be NULL). */
+int32_t ut_model_graph_stats(const ut_model *m, int64_t *captures, int64_t *replays,
+                             int64_t *failures);
+
 /* on_token of undertow_core::generate (undertow-core/src/model.rs:139-166)
  * and of the speculative loops (mtp.rs:194-257, 263-314): called with each
  * emitted token in order; return 0 to end the stream after it. */

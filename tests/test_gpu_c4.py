@@ -56,6 +56,23 @@ def test_c4_greedy_stream_identical(c4):
     assert m.generate_greedy(prompt, NEW) == stream
 
 
+def test_c4_graph_replay_matches(c4):
+    """The captured one-row step at full width (fused q_a/kv_a finish,
+    matrix-core attention, routed + shared experts, the MTP hidden-state
+    copy) replays to the oracle's greedy stream."""
+    ck, m, om, prompt, stream = c4
+    before = m.graph_stats()
+    m.enable_graphs(True)
+    try:
+        got = m.generate_greedy(prompt, NEW)
+    finally:
+        m.enable_graphs(False)
+    after = m.graph_stats()
+    assert got == stream
+    assert after["failures"] == before["failures"]
+    assert after["replays"] - before["replays"] == NEW - 3
+
+
 def test_c4_incremental_equals_one_shot(c4):
     ck, m, om, prompt, stream = c4
     ids = prompt + stream[:6]

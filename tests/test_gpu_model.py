@@ -108,6 +108,36 @@ def test_c1_mla_mtp_verify_rows(c1_mla, depth):
     assert drafted > 0 and 0 <= accepted <= drafted
 
 
+@pytest.mark.parametrize("which", ["c1", "c1_mla"])
+def test_graph_replay_matches_eager(request, which):
+    """One-row greedy steps replayed from a captured graph (every position
+    read from device memory, attention grids sized for the capacity) give
+    the eager stream token for token, over 45 replays with the host's
+    readbacks and waits between them; a second call captures its own
+    session's graph.  c1 takes the f32 split-T attention, c1_mla the
+    matrix-core attention with the fused q_a/kv_a finish."""
+    ck, m, om = request.getfixturevalue(which)
+    cfg = C1 if which == "c1" else C1_MLA
+    prompt = prompt_ids(16, cfg["vocab_size"])
+    eager = m.generate_greedy(prompt, 48)
+    eager2 = m.generate_greedy(prompt[:9], 40)
+    before = m.graph_stats()
+    m.enable_graphs(True)
+    try:
+        g1 = m.generate_greedy(prompt, 48)
+        g2 = m.generate_greedy(prompt[:9], 40)
+    finally:
+        m.enable_graphs(False)
+    after = m.graph_stats()
+    assert g1 == eager
+    assert g2 == eager2
+    # the replays ran: one capture per call, every step from the third on
+    assert after["failures"] == before["failures"]
+    assert after["captures"] - before["captures"] == 2
+    assert after["replays"] - before["replays"] == (48 - 3) + (40 - 3)
+    assert eager == om.greedy_decode(prompt, 48)[16:]
+
+
 @pytest.fixture(scope="module")
 def c1_e256(ctx):
     ck = checkpoint(C1_E256, fmt="int4")

@@ -208,7 +208,7 @@ struct MlaPreArgs {
     const float *kv_norm;
     float *latent, *krot;
     __bf16 *kc;
-    int64_t pos_base;
+    PosRef pos;
     const float2 *table;
 };
 
@@ -254,7 +254,7 @@ __global__ __launch_bounds__(1024) void k_mla_pre(MlaPreArgs a) {
         }
         rowdig_body<1>(a.qa, m, v, wv, redd, redu);
     } else {
-        kv_append_row(sc, a.L, a.P, a.kv_norm, a.qa.eps, a.latent, a.krot, a.kc, a.pos_base + m,
+        kv_append_row(sc, a.L, a.P, a.kv_norm, a.qa.eps, a.latent, a.krot, a.kc, a.pos.get() + m,
                       a.table, red4);
     }
 }
@@ -296,7 +296,7 @@ int32_t launch_mla_pre(ut_ctx *ctx, const SplitKPartials &pp, int64_t O1, const 
     a.latent = latent;
     a.krot = krot;
     a.kc = kc;
-    a.pos_base = pos_base;
+    a.pos = pos_ref(ctx, pos_base);
     a.table = table;
     int tok = timing_begin(ctx, "mla_pre");
     hipLaunchKernelGGL(k_mla_pre, dim3((unsigned)(2 * M)), dim3(1024), 0, ctx->stream, a);

@@ -78,10 +78,43 @@ struct ut_ctx {
     void *noalloc_scratch = nullptr;
     // The opt-in fast-int8 matmul (ut_set_fast_int8): off by default.
     bool fast_int8 = false;
+    // While a session captures its decode step into a graph: the device word
+    // holding the step's position, the host position it held at capture
+    // (positions passed to launchers are taken relative to it) and the
+    // session's capacity (grids that depend on the context length are sized
+    // for it).  step_pos == nullptr: positions are host values.
+    const int64_t *step_pos = nullptr;
+    int64_t step_pos_host = 0, step_cap = 0;
     // Handle lifetime: models hold a reference on their context and
     // sessions on their model, so the handles may be released in any order.
     int refs = 1;
 };
+
+namespace ut {
+// A position handed to a kernel: a host value, or (in a captured decode
+// step) an offset from a device word read when the kernel runs, so each
+// replay of the step sees the session's current position.
+struct PosRef {
+    int64_t base = 0;
+    const int64_t *dev = nullptr;
+    __device__ __forceinline__ int64_t get() const { return dev ? base + *dev : base; }
+};
+inline PosRef pos_ref(const ut_ctx *ctx, int64_t pos) {
+    PosRef r;
+    if (ctx->step_pos) {
+        r.base = pos - ctx->step_pos_host;
+        r.dev = ctx->step_pos;
+    } else {
+        r.base = pos;
+    }
+    return r;
+}
+// The positions a launch can see at most: pos_end itself, or the capacity
+// while a decode step is captured.
+inline int64_t pos_extent(const ut_ctx *ctx, int64_t pos_end) {
+    return ctx->step_pos ? ctx->step_cap : pos_end;
+}
+}  // namespace ut
 
 struct ut_qtensor {
     int32_t fmt = UT_FMT_F32;

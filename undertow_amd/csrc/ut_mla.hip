@@ -28,7 +28,7 @@ __global__ __launch_bounds__(256) void k_mla_split(const float *__restrict__ qab
                                                    const float *__restrict__ qrope,
                                                    const float *__restrict__ latent,
                                                    const float *__restrict__ krot, int R, int H,
-                                                   int L, int P, int64_t pos_base, float scale,
+                                                   int L, int P, PosRef pos, float scale,
                                                    float *__restrict__ part_m,
                                                    float *__restrict__ part_l,
                                                    float *__restrict__ part_o, int nsplit) {
@@ -40,8 +40,11 @@ __global__ __launch_bounds__(256) void k_mla_split(const float *__restrict__ qab
     const int groups = H / HG;
     const int r = blockIdx.x / groups, h0 = (blockIdx.x % groups) * HG;
     const int j = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int64_t n_ctx = pos_base + r + 1;
+    const int64_t n_ctx = pos.get() + r + 1;
     const int64_t t0 = (int64_t)j * kMlaSlice;
+    // past the row's context (a grid sized for more positions): the combine
+    // reads only the row's own slices
+    if (t0 >= n_ctx) return;
     for (int i = tid; i < HG * QW; i += 256) {
         int hh = i / QW, d = i - hh * QW;
         int64_t qi = ((int64_t)r * H + h0 + hh);
@@ -119,11 +122,11 @@ __global__ __launch_bounds__(256) void k_mla_split(const float *__restrict__ qab
 __global__ __launch_bounds__(256) void k_mla_combine(const float *__restrict__ part_m,
                                                      const float *__restrict__ part_l,
                                                      const float *__restrict__ part_o, int L,
-                                                     int H, int64_t pos_base, int nsplit,
+                                                     int H, PosRef pos, int nsplit,
                                                      float *__restrict__ clat) {
     const int64_t qi = blockIdx.x;  // r*H + h
     const int r = (int)(qi / H);
-    const int64_t n_ctx = pos_base + r + 1;
+    const int64_t n_ctx = pos.get() + r + 1;
     const int ns = (int)((n_ctx + kMlaSlice - 1) / kMlaSlice);
     float M = -INFINITY;
 #pragma unroll 8
@@ -214,7 +217,7 @@ struct MlaMfmaArgs {
     const float *qabs, *qrope;
     const __bf16 *kc;  // [T][2][L+P]: bf16 hi plane then lo plane per position
     int H, L, P, RH;
-    int64_t pos_base;
+    PosRef pos;
     float scale;
     int groups, nslice;  // column groups of 32, slices in the grid
     float *part_m, *part_l, *part_o;  // [j][col], [j][col], [j][L][col]
@@ -265,7 +268,7 @@ __global__ __launch_bounds__(256, 2) void k_mla_mfma16(MlaMfmaArgs a) {
     const int slice = (q / a.groups) * 8 + x8;
     const int c0 = group * 32;
     const int r = c0 / a.H;
-    const int64_t n_ctx = a.pos_base + r + 1;
+    const int64_t n_ctx = a.pos.get() + r + 1;
     const int64_t slen = mla_mfma_slice(n_ctx);
     const int64_t p0 = (int64_t)slice * slen;
     if (slice >= a.nslice || p0 >= n_ctx) return;  // uniform per workgroup
@@ -447,7 +450,7 @@ constexpr int kCombineSlices = (kMlaMaxSlices + kCombineParts - 1) / kCombinePar
 __global__ __launch_bounds__(1024) void k_mla_combine_mfma(const float *__restrict__ part_m,
                                                            const float *__restrict__ part_l,
                                                            const float *__restrict__ part_o,
-                                                           int RH, int H, int L, int64_t pos_base,
+                                                           int RH, int H, int L, PosRef pos,
                                                            float *__restrict__ clat) {
     __shared__ __attribute__((aligned(16))) float sw[kMlaMaxSlices][32];
     __shared__ float red[32][33];
@@ -458,7 +461,7 @@ __global__ __launch_bounds__(1024) void k_mla_combine_mfma(const float *__restri
     const int col = blockIdx.x * 32 + tx;
     // the slice count is the same for the workgroup's 32 columns (one query
     // row: 32 | H)
-    const int64_t n_ctx = pos_base + col / H + 1;
+    const int64_t n_ctx = pos.get() + col / H + 1;
     const int64_t slen = mla_mfma_slice(n_ctx);
     const int ns = (int)((n_ctx + slen - 1) / slen);
     // merge-pass loads: columns 4*c4.., dim dy, slices [j0, j1)
@@ -587,7 +590,7 @@ int32_t launch_mla_cache_split(ut_ctx *ctx, const float *latent, const float *kr
 int32_t launch_mla_attend_kc(ut_ctx *ctx, const float *qabs, const float *qrope, const __bf16 *kc,
                              int64_t R, int64_t H, int64_t L, int64_t P, int64_t pos_base,
                              float scale, float *clat, void *scratch) {
-    const int64_t T = pos_base + R;
+    const int64_t T = pos_extent(ctx, pos_base + R);
     if (!mla_mfma_ok(H, L, P, T) || ((uintptr_t)kc & 15) != 0) {
         set_error(ctx, "mla: split-cache attention needs 32k heads, latent 512 + rope 64, a "
                        "16-byte aligned cache and at most %d slices", kMlaMaxSlices);
@@ -597,7 +600,7 @@ int32_t launch_mla_attend_kc(ut_ctx *ctx, const float *qabs, const float *qrope,
     MlaMfmaArgs a;
     a.qabs = qabs; a.qrope = qrope; a.kc = kc;
     a.H = (int)H; a.L = (int)L; a.P = (int)P; a.RH = (int)RH;
-    a.pos_base = pos_base;
+    a.pos = pos_ref(ctx, pos_base);
     a.scale = scale;
     a.groups = (int)(RH / 32);
     a.nslice = (int)ns;
@@ -613,7 +616,7 @@ int32_t launch_mla_attend_kc(ut_ctx *ctx, const float *qabs, const float *qrope,
     tok = timing_begin(ctx, "mla_combine");
     hipLaunchKernelGGL(k_mla_combine_mfma, dim3((unsigned)(RH / 32), (unsigned)(L / 8)),
                        dim3(1024), 0, ctx->stream, a.part_m, a.part_l, a.part_o,
-                       (int)RH, (int)H, (int)L, pos_base, clat);
+                       (int)RH, (int)H, (int)L, a.pos, clat);
     timing_end(ctx, tok);
     return launch_check(ctx, "k_mla_combine_mfma");
 }
@@ -621,7 +624,7 @@ int32_t launch_mla_attend_kc(ut_ctx *ctx, const float *qabs, const float *qrope,
 int32_t launch_mla_attend(ut_ctx *ctx, const float *qabs, const float *qrope, const float *latent,
                           const float *krot, int64_t R, int64_t H, int64_t L, int64_t P,
                           int64_t pos_base, float scale, float *clat, void *scratch) {
-    const int64_t T = pos_base + R;  // positions any row can see
+    const int64_t T = pos_extent(ctx, pos_base + R);  // positions any row can see
     if (mla_mfma_ok(H, L, P, T)) {
         // the f32 cache is split into the MFMA form in scratch first
         __bf16 *kc = (__bf16 *)((char *)scratch + mla_mfma_scratch_bytes(R, H, L, T));
@@ -646,18 +649,19 @@ int32_t launch_mla_attend(ut_ctx *ctx, const float *qabs, const float *qrope, co
         return UT_ERR_SHAPE;
     }
     dim3 grid((unsigned)(R * H / HG), (unsigned)nsplit);
+    const PosRef pr = pos_ref(ctx, pos_base);
     int tok = timing_begin(ctx, "mla_split");
     switch (HG) {
-    case 8: hipLaunchKernelGGL(k_mla_split<8>, grid, dim3(256), shmem, ctx->stream, qabs, qrope, latent, krot, (int)R, (int)H, (int)L, (int)P, pos_base, scale, pm, pl, po, nsplit); break;
-    case 4: hipLaunchKernelGGL(k_mla_split<4>, grid, dim3(256), shmem, ctx->stream, qabs, qrope, latent, krot, (int)R, (int)H, (int)L, (int)P, pos_base, scale, pm, pl, po, nsplit); break;
-    case 2: hipLaunchKernelGGL(k_mla_split<2>, grid, dim3(256), shmem, ctx->stream, qabs, qrope, latent, krot, (int)R, (int)H, (int)L, (int)P, pos_base, scale, pm, pl, po, nsplit); break;
-    default: hipLaunchKernelGGL(k_mla_split<1>, grid, dim3(256), shmem, ctx->stream, qabs, qrope, latent, krot, (int)R, (int)H, (int)L, (int)P, pos_base, scale, pm, pl, po, nsplit); break;
+    case 8: hipLaunchKernelGGL(k_mla_split<8>, grid, dim3(256), shmem, ctx->stream, qabs, qrope, latent, krot, (int)R, (int)H, (int)L, (int)P, pr, scale, pm, pl, po, nsplit); break;
+    case 4: hipLaunchKernelGGL(k_mla_split<4>, grid, dim3(256), shmem, ctx->stream, qabs, qrope, latent, krot, (int)R, (int)H, (int)L, (int)P, pr, scale, pm, pl, po, nsplit); break;
+    case 2: hipLaunchKernelGGL(k_mla_split<2>, grid, dim3(256), shmem, ctx->stream, qabs, qrope, latent, krot, (int)R, (int)H, (int)L, (int)P, pr, scale, pm, pl, po, nsplit); break;
+    default: hipLaunchKernelGGL(k_mla_split<1>, grid, dim3(256), shmem, ctx->stream, qabs, qrope, latent, krot, (int)R, (int)H, (int)L, (int)P, pr, scale, pm, pl, po, nsplit); break;
     }
     timing_end(ctx, tok);
     UT_TRY(launch_check(ctx, "k_mla_split"));
     tok = timing_begin(ctx, "mla_combine");
     hipLaunchKernelGGL(k_mla_combine, dim3((unsigned)(R * H)), dim3(256), 0, ctx->stream, pm, pl,
-                       po, (int)L, (int)H, pos_base, nsplit, clat);
+                       po, (int)L, (int)H, pr, nsplit, clat);
     timing_end(ctx, tok);
     return launch_check(ctx, "k_mla_combine");
 }

@@ -81,6 +81,8 @@ struct ut_model {
     std::vector<int32_t> stop_ids;  // the checkpoint's stop tokens (DeepseekMoeModel::stop_ids)
     ut::ExpertStore *store = nullptr;  // the HBM tier of routed experts, when not all resident
     bool store_prefetch = false;       // pilot-router hints one layer ahead at decode
+    bool graphs = false;               // one-row decode steps replayed from a captured graph
+    int64_t graph_captures = 0, graph_replays = 0, graph_failures = 0;
     std::vector<void *> device_allocs;
     int64_t device_bytes = 0;
     int device = 0;
@@ -124,6 +126,16 @@ struct ut_session {
     // up, then readback slots; `ready` marks the end of the last readback
     int32_t *pin = nullptr;
     hipEvent_t ready = nullptr;
+    // The one-row decode step as a captured graph (ut_model_enable_graphs):
+    // the device word holding the step's position, the position it will hold
+    // once the enqueued work has run (-1: unknown), the executable graph, the
+    // one-row steps run so far, and whether capturing failed (eager from
+    // then on).
+    int64_t *dpos = nullptr;
+    int64_t dpos_host = -1;
+    hipGraphExec_t g1 = nullptr;
+    int64_t m1_steps = 0;
+    bool graph_failed = false;
 };
 
 namespace {
@@ -365,6 +377,11 @@ int32_t ws_reserve(ut_session *s, int64_t rows) {
         UT_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
         UT_CHECK_HIP(ctx, hipFree(w.base));
         w.base = nullptr;
+    }
+    // a captured step names the old workspace
+    if (s->g1) {
+        (void)hipGraphExecDestroy(s->g1);
+        s->g1 = nullptr;
     }
     if (hipMalloc(&w.base, total) != hipSuccess) {
         (void)hipGetLastError();
@@ -837,9 +854,7 @@ int32_t prefill_dev(ut_session *s, const int32_t *ids, int64_t n, const int32_t 
                          fuse ? &nx : nullptr));
         cur = nxt;
     }
-    if (m->has_mtp)
-        UT_CHECK_HIP(ctx, hipMemcpyAsync(s->hidden + s->pos * H, w.x, (size_t)n * H * 4,
-                                         hipMemcpyDeviceToDevice, ctx->stream));
+    if (m->has_mtp) UT_TRY(launch_copy_rows_at(ctx, s->hidden, H, s->pos, w.x, n, H));
     s->pos += n;
     if (!ids_dev) s->tokens.insert(s->tokens.end(), ids, ids + n);
     XDigits fd = cur;
@@ -1169,6 +1184,114 @@ struct Emit {
 // step's argmax on the device, and the next step is queued before the host
 // waits for the current token (a step queued past the stream's end is
 // discarded with the session).
+// Whether one-row decode steps of this session may run from a captured
+// graph: asked for, not given up on, every launch of the step on the device
+// (no expert tier: it reads the routing back each layer), no kernel timing
+// (its events), and one eager one-row step run first (host-side one-time
+// set-up, such as occupancy queries, happens there).
+bool graph_ok(const ut_session *s) {
+    const ut_model *m = s->m;
+    return m->graphs && !s->graph_failed && !m->store && !m->ctx->timing && s->m1_steps >= 1;
+}
+
+// Captures the one-row step fed from ws.am[0] into s->g1.  The capture pass
+// runs the host side of the step (so the session's positions advance as if
+// it ran); every position-dependent launch reads the device word s->dpos,
+// and attention grids are sized for the capacity.  The graph must hold
+// kernel launches only.  The null stream cannot be captured: then the
+// launches are captured on the context's own stream (capturing runs
+// nothing) and the graph is launched on the context's stream.  On failure
+// the host positions are restored and UT_ERR_STATE returned (the caller
+// runs the step eagerly).
+int32_t capture_step(ut_session *s) {
+    ut_model *m = s->m;
+    ut_ctx *ctx = m->ctx;
+    const hipStream_t run_stream = ctx->stream;
+    ctx->stream = run_stream ? run_stream : ctx->own_stream;
+    const int64_t pos0 = s->pos;
+    std::vector<int64_t> lens;
+    for (auto &kv : s->kv) lens.push_back(kv.len);
+    ctx->step_pos = s->dpos;
+    ctx->step_pos_host = pos0;
+    ctx->step_cap = s->cap;
+    hipGraph_t graph = nullptr;
+    int32_t rc = UT_OK;
+    if (hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+        rc = UT_ERR_STATE;
+    } else {
+        rc = prefill_dev(s, nullptr, 1, s->ws.am);
+        if (rc == UT_OK) rc = launch_pos_add(ctx, s->dpos, 1);
+        if (hipStreamEndCapture(ctx->stream, &graph) != hipSuccess) rc = UT_ERR_STATE;
+    }
+    ctx->step_pos = nullptr;
+    ctx->stream = run_stream;
+    (void)hipGetLastError();
+    if (rc == UT_OK && graph) {
+        size_t nn = 0;
+        if (hipGraphGetNodes(graph, nullptr, &nn) != hipSuccess) rc = UT_ERR_STATE;
+        std::vector<hipGraphNode_t> nodes(nn);
+        if (rc == UT_OK && nn && hipGraphGetNodes(graph, nodes.data(), &nn) != hipSuccess)
+            rc = UT_ERR_STATE;
+        for (size_t i = 0; rc == UT_OK && i < nn; i++) {
+            hipGraphNodeType t;
+            if (hipGraphNodeGetType(nodes[i], &t) != hipSuccess || t != hipGraphNodeTypeKernel)
+                rc = UT_ERR_STATE;
+        }
+        if (rc == UT_OK && hipGraphInstantiate(&s->g1, graph, nullptr, nullptr, 0) != hipSuccess) {
+            s->g1 = nullptr;
+            rc = UT_ERR_STATE;
+        }
+    } else if (rc == UT_OK) {
+        rc = UT_ERR_STATE;
+    }
+    if (graph) (void)hipGraphDestroy(graph);
+    (void)hipGetLastError();
+    if (rc != UT_OK) {
+        s->pos = pos0;
+        for (size_t i = 0; i < lens.size(); i++) s->kv[i].len = lens[i];
+        return UT_ERR_STATE;
+    }
+    return UT_OK;
+}
+
+// One device-fed decode step (its token in ws.am[0]): replayed from the
+// captured graph when the session allows it, else launched eagerly.
+int32_t decode_step(ut_session *s) {
+    ut_model *m = s->m;
+    ut_ctx *ctx = m->ctx;
+    if (!graph_ok(s)) {
+        const int32_t rc = prefill_dev(s, nullptr, 1, s->ws.am);
+        if (rc == UT_OK) s->m1_steps++;
+        return rc;
+    }
+    if (s->pos + 1 > s->cap) {
+        set_error(ctx, "context overflow: %lld + 1 > %lld", (long long)s->pos, (long long)s->cap);
+        return UT_ERR_CONTEXT_OVERFLOW;
+    }
+    // the device position word must hold this step's position
+    if (s->dpos_host != s->pos) {
+        UT_TRY(launch_pos_set(ctx, s->dpos, s->pos));
+        s->dpos_host = s->pos;
+    }
+    if (!s->g1) {
+        if (capture_step(s) != UT_OK) {
+            s->graph_failed = true;
+            m->graph_failures++;
+            return decode_step(s);
+        }
+        m->graph_captures++;
+        // the capture pass advanced the host positions; now run the step
+    } else {
+        s->pos += 1;
+        for (auto &kv : s->kv) kv.len += 1;
+    }
+    UT_CHECK_HIP(ctx, hipGraphLaunch(s->g1, ctx->stream));
+    m->graph_replays++;
+    s->dpos_host += 1;
+    s->m1_steps++;
+    return UT_OK;
+}
+
 int64_t gen_greedy(ut_model *m, const int32_t *prompt, int64_t n, Emit &em) {
     ut_session *s = nullptr;
     UT_TRY(ut_session_create(m, 0, &s));
@@ -1196,7 +1319,7 @@ int64_t gen_greedy(ut_model *m, const int32_t *prompt, int64_t n, Emit &em) {
         bool next_queued = false;
         if (em.produced + 1 < em.max_new) {
             // fed from ws.am[0], which this step overwrites only after reading it
-            const int32_t r2 = prefill_dev(s, nullptr, 1, s->ws.am);
+            const int32_t r2 = decode_step(s);
             if (r2 == UT_OK) next_queued = true;
             else if (r2 != UT_ERR_CONTEXT_OVERFLOW) { rc = r2; break; }
         }
@@ -1853,7 +1976,7 @@ int32_t ut_session_create(ut_model *m, int32_t path, ut_session **out) {
     const int64_t nl = c.num_hidden_layers + (m->has_mtp ? 1 : 0);
     const size_t per = (size_t)s->cap * (c.kv_lora_rank + c.qk_rope_head_dim) * 4;
     const size_t hid = m->has_mtp ? (size_t)s->cap * c.hidden_size * 4 : 0;
-    if (hipMalloc(&s->kv_alloc, per * nl + hid + 256) != hipSuccess) {
+    if (hipMalloc(&s->kv_alloc, per * nl + hid + 512) != hipSuccess) {
         (void)hipGetLastError();
         set_error(m->ctx, "KV cache allocation failed");
         delete s;
@@ -1875,7 +1998,9 @@ int32_t ut_session_create(ut_model *m, int32_t path, ut_session **out) {
     if (m->has_mtp) {
         carve(s->mtp_kv);
         s->hidden = (float *)p;
+        p += hid;
     }
+    s->dpos = (int64_t *)((char *)s->kv_alloc + ((per * nl + hid + 255) & ~size_t(255)));
     if (hipHostMalloc((void **)&s->pin, (size_t)(kPinIds + kPinBack) * 4, hipHostMallocDefault) != hipSuccess ||
         hipEventCreateWithFlags(&s->ready, hipEventDisableTiming) != hipSuccess) {
         (void)hipGetLastError();
@@ -1896,6 +2021,7 @@ void ut_session_free(ut_session *s) {
     if (!s) return;
     (void)hipSetDevice(s->m->device);
     (void)hipStreamSynchronize(s->m->ctx->stream);
+    if (s->g1) (void)hipGraphExecDestroy(s->g1);
     if (s->ws.base) (void)hipFree(s->ws.base);
     if (s->kv_alloc) (void)hipFree(s->kv_alloc);
     if (s->pin) (void)hipHostFree(s->pin);
@@ -1934,6 +2060,21 @@ int32_t ut_model_set_stop_ids(ut_model *m, const int32_t *ids, int64_t n) {
     // loader.rs:304-309): the config's eos ids plus generation_config's
     if (!m || n < 0 || (n > 0 && !ids)) return UT_ERR_ARG;
     m->stop_ids.assign(ids, ids + n);
+    return UT_OK;
+}
+
+int32_t ut_model_enable_graphs(ut_model *m, int32_t on) {
+    if (!m) return UT_ERR_ARG;
+    m->graphs = on != 0;
+    return UT_OK;
+}
+
+int32_t ut_model_graph_stats(const ut_model *m, int64_t *captures, int64_t *replays,
+                             int64_t *failures) {
+    if (!m) return UT_ERR_ARG;
+    if (captures) *captures = m->graph_captures;
+    if (replays) *replays = m->graph_replays;
+    if (failures) *failures = m->graph_failures;
     return UT_OK;
 }
 

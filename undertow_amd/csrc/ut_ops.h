@@ -69,14 +69,15 @@ int32_t launch_embed(ut_ctx *ctx, const ut_qtensor *emb, const int32_t *ids, int
 // f64, r = 1/sqrt((float)ms + eps), out = (x*r)*w.
 int32_t launch_rmsnorm(ut_ctx *ctx, const float *x, int64_t ldx, const float *w, int64_t n,
                        float eps, int64_t rows, float *out, int64_t ldo);
-// rope_interleave (attention.rs:106-118) in place on `heads` slices of
-// `dim` floats per row: slice (s, h) at v + s*ld_row + h*ld_head, position
-// pos_base + s.  table: [positions][dim/2] (cos, sin) computed on the host.
-int32_t launch_rope(ut_ctx *ctx, float *v, int64_t rows, int64_t heads, int64_t ld_row,
-                    int64_t ld_head, int64_t dim, int64_t pos_base, const float2 *table,
-                    int64_t table_stride);
 // y += x (f32 adds), n elements.
 int32_t launch_add(ut_ctx *ctx, float *y, const float *x, int64_t n);
+// dst rows [pos, pos + rows) (stride ld) <- src [rows][H]; pos follows the
+// context's captured-step position when one is set.
+int32_t launch_copy_rows_at(ut_ctx *ctx, float *dst, int64_t ld, int64_t pos, const float *src,
+                            int64_t rows, int64_t H);
+// *p = v, and *p += n (a captured step's position word).
+int32_t launch_pos_set(ut_ctx *ctx, int64_t *p, int64_t v);
+int32_t launch_pos_add(ut_ctx *ctx, int64_t *p, int64_t n);
 // Absorbed query (attention.rs:204-213): for each (s, h)
 //   qabs[s,h,:] = sum_d (q[s,h,d]*scale[h*kvh+d]) * W[h*kvh+d, :]  (d < nope,
 //   adds in d order) and q_rope[s,h,:] = rope_interleave(q[s,h,nope:], pos_base+s).

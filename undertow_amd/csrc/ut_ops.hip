@@ -74,42 +74,6 @@ int32_t launch_rmsnorm(ut_ctx *ctx, const float *x, int64_t ldx, const float *w,
     return launch_check(ctx, "k_rmsnorm");
 }
 
-// One workgroup per (row, head) slice; the slice is read completely before
-// any element is written (the permutation moves pairs to split halves).
-__global__ void k_rope(float *__restrict__ v, int64_t heads, int64_t ld_row, int64_t ld_head,
-                       int64_t dim, int64_t pos_base, const float2 *__restrict__ table,
-                       int64_t table_stride) {
-    const int64_t s = blockIdx.x / heads, h = blockIdx.x % heads;
-    float *p = v + s * ld_row + h * ld_head;
-    const int64_t half = dim / 2;
-    const float2 *cs = table + (pos_base + s) * table_stride;
-    const int j = threadIdx.x;
-    float a = 0.0f, b = 0.0f;
-    if (j < half) { a = p[2 * j]; b = p[2 * j + 1]; }
-    __syncthreads();
-    if (j < half) {
-        const float c = cs[j].x, sn = cs[j].y;
-        p[j] = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, sn));
-        p[half + j] = __fadd_rn(__fmul_rn(b, c), __fmul_rn(a, sn));
-    }
-}
-
-int32_t launch_rope(ut_ctx *ctx, float *v, int64_t rows, int64_t heads, int64_t ld_row,
-                    int64_t ld_head, int64_t dim, int64_t pos_base, const float2 *table,
-                    int64_t table_stride) {
-    if (rows <= 0 || dim <= 0) return UT_OK;
-    if (dim / 2 > 1024) {
-        set_error(ctx, "rope dim %lld too large", (long long)dim);
-        return UT_ERR_SHAPE;
-    }
-    unsigned threads = (unsigned)(((dim / 2) + 63) / 64 * 64);
-    int tok = timing_begin(ctx, "rope");
-    hipLaunchKernelGGL(k_rope, dim3((unsigned)(rows * heads)), dim3(threads), 0, ctx->stream, v,
-                       heads, ld_row, ld_head, dim, pos_base, table, table_stride);
-    timing_end(ctx, tok);
-    return launch_check(ctx, "k_rope");
-}
-
 __global__ void k_add(float *__restrict__ y, const float *__restrict__ x, int64_t n) {
 #pragma unroll 8
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
@@ -127,16 +91,58 @@ int32_t launch_add(ut_ctx *ctx, float *y, const float *x, int64_t n) {
     return launch_check(ctx, "k_add");
 }
 
+// rows x H floats from src into dst rows pos.. (row stride ld): the
+// pre-norm hidden states the MTP head reads later.
+__global__ void k_copy_rows_at(float *__restrict__ dst, int64_t ld, PosRef pos,
+                               const float *__restrict__ src, int64_t H) {
+    float *d = dst + (pos.get() + blockIdx.y) * ld;
+    const float *s = src + (int64_t)blockIdx.y * H;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < H;
+         i += (int64_t)gridDim.x * blockDim.x)
+        d[i] = s[i];
+}
+
+int32_t launch_copy_rows_at(ut_ctx *ctx, float *dst, int64_t ld, int64_t pos, const float *src,
+                            int64_t rows, int64_t H) {
+    if (rows <= 0) return UT_OK;
+    unsigned bx = (unsigned)((H + 255) / 256);
+    if (bx > 32) bx = 32;
+    int tok = timing_begin(ctx, "copy_rows");
+    hipLaunchKernelGGL(k_copy_rows_at, dim3(bx, (unsigned)rows), dim3(256), 0, ctx->stream, dst, ld,
+                       pos_ref(ctx, pos), src, H);
+    timing_end(ctx, tok);
+    return launch_check(ctx, "k_copy_rows_at");
+}
+
+// The device position word of a captured decode step: set before a replay
+// when the host moved the position, advanced by the step itself.
+__global__ void k_pos_set(int64_t *p, int64_t v) {
+    if (threadIdx.x == 0) *p = v;
+}
+__global__ void k_pos_add(int64_t *p, int64_t n) {
+    if (threadIdx.x == 0) *p += n;
+}
+
+int32_t launch_pos_set(ut_ctx *ctx, int64_t *p, int64_t v) {
+    hipLaunchKernelGGL(k_pos_set, dim3(1), dim3(64), 0, ctx->stream, p, v);
+    return launch_check(ctx, "k_pos_set");
+}
+
+int32_t launch_pos_add(ut_ctx *ctx, int64_t *p, int64_t n) {
+    hipLaunchKernelGGL(k_pos_add, dim3(1), dim3(64), 0, ctx->stream, p, n);
+    return launch_check(ctx, "k_pos_add");
+}
+
 // Cache append, one workgroup per row (kv_append_row).
 __global__ __launch_bounds__(256) void k_kv_append(const float *__restrict__ comp, int64_t L,
                                                    int64_t P, const float *__restrict__ w,
                                                    float eps, float *__restrict__ latent,
                                                    float *__restrict__ krot, __bf16 *__restrict__ kc,
-                                                   int64_t pos_base,
+                                                   PosRef pos,
                                                    const float2 *__restrict__ table) {
     __shared__ double red[4];
     const int64_t s = blockIdx.x;
-    kv_append_row(comp + s * (L + P), L, P, w, eps, latent, krot, kc, pos_base + s, table, red);
+    kv_append_row(comp + s * (L + P), L, P, w, eps, latent, krot, kc, pos.get() + s, table, red);
 }
 
 int32_t launch_kv_append(ut_ctx *ctx, const float *comp, int64_t rows, int64_t L, int64_t P,
@@ -145,7 +151,7 @@ int32_t launch_kv_append(ut_ctx *ctx, const float *comp, int64_t rows, int64_t L
     if (rows <= 0) return UT_OK;
     int tok = timing_begin(ctx, "kv_append");
     hipLaunchKernelGGL(k_kv_append, dim3((unsigned)rows), dim3(256), 0, ctx->stream, comp, L, P, w,
-                       eps, latent, krot, kc, pos_base, table);
+                       eps, latent, krot, kc, pos_ref(ctx, pos_base), table);
     timing_end(ctx, tok);
     return launch_check(ctx, "k_kv_append");
 }
@@ -178,8 +184,9 @@ __global__ __launch_bounds__(128) void k_absorb_q(const uint8_t *__restrict__ w,
                                                   const float *__restrict__ q, int64_t rows,
                                                   int64_t heads, int64_t nope, int64_t rope,
                                                   int64_t kvh, float *__restrict__ qabs,
-                                                  float *__restrict__ qrope, int64_t pos_base,
+                                                  float *__restrict__ qrope, PosRef pos,
                                                   const float2 *__restrict__ table) {
+    const int64_t pos_base = pos.get();
     const int64_t h = blockIdx.x, r0 = (int64_t)blockIdx.y * RB;
     const int64_t qh = nope + rope;
     const int64_t col = 512 * (int64_t)blockIdx.z + 4 * (int64_t)threadIdx.x;
@@ -243,8 +250,9 @@ __global__ __launch_bounds__(CB) void k_absorb_q_lds(const uint8_t *__restrict__
                                                      const float *__restrict__ q, int64_t rows,
                                                      int64_t heads, int nope, int64_t rope,
                                                      int64_t kvh, float *__restrict__ qabs,
-                                                     float *__restrict__ qrope, int64_t pos_base,
+                                                     float *__restrict__ qrope, PosRef pos,
                                                      const float2 *__restrict__ table) {
+    const int64_t pos_base = pos.get();
     constexpr int BPC2 = FMT == UT_FMT_INT4 ? 1 : FMT == UT_FMT_INT8 ? 2 : 8;  // 2*bytes/col
     constexpr int ROWB = CB * BPC2 / 2;  // staged bytes per nope row
     constexpr int PIECES = ROWB / 16;
@@ -315,7 +323,7 @@ static void absorb_q_lds_launch(ut_ctx *ctx, const ut_qtensor *kv_b, const float
     dim3 grid((unsigned)heads, (unsigned)(L / CB), (unsigned)((rows + RB - 1) / RB));
     hipLaunchKernelGGL((k_absorb_q_lds<FMT, RB, CB>), grid, dim3(CB), shmem, ctx->stream,
                        (const uint8_t *)kv_b->payload, kv_b->scales, kv_b->row_bytes, L, q, rows,
-                       heads, (int)nope, rope, kvh, qabs, qrope, pos_base, table);
+                       heads, (int)nope, rope, kvh, qabs, qrope, pos_ref(ctx, pos_base), table);
 }
 
 int32_t launch_absorb_q(ut_ctx *ctx, const ut_qtensor *kv_b, const float *q, int64_t rows,
@@ -364,9 +372,9 @@ int32_t launch_absorb_q(ut_ctx *ctx, const ut_qtensor *kv_b, const float *q, int
     const uint8_t *w = (const uint8_t *)kv_b->payload;
     int tok = timing_begin(ctx, "absorb_q");
     switch (kv_b->fmt) {
-    case UT_FMT_INT8: hipLaunchKernelGGL((k_absorb_q<UT_FMT_INT8, RB>), grid, dim3(threads), 0, ctx->stream, w, kv_b->scales, kv_b->row_bytes, L, q, rows, heads, nope, rope, kvh, qabs, qrope, pos_base, table); break;
-    case UT_FMT_INT4: hipLaunchKernelGGL((k_absorb_q<UT_FMT_INT4, RB>), grid, dim3(threads), 0, ctx->stream, w, kv_b->scales, kv_b->row_bytes, L, q, rows, heads, nope, rope, kvh, qabs, qrope, pos_base, table); break;
-    default: hipLaunchKernelGGL((k_absorb_q<UT_FMT_F32, RB>), grid, dim3(threads), 0, ctx->stream, w, kv_b->scales, kv_b->row_bytes, L, q, rows, heads, nope, rope, kvh, qabs, qrope, pos_base, table); break;
+    case UT_FMT_INT8: hipLaunchKernelGGL((k_absorb_q<UT_FMT_INT8, RB>), grid, dim3(threads), 0, ctx->stream, w, kv_b->scales, kv_b->row_bytes, L, q, rows, heads, nope, rope, kvh, qabs, qrope, pos_ref(ctx, pos_base), table); break;
+    case UT_FMT_INT4: hipLaunchKernelGGL((k_absorb_q<UT_FMT_INT4, RB>), grid, dim3(threads), 0, ctx->stream, w, kv_b->scales, kv_b->row_bytes, L, q, rows, heads, nope, rope, kvh, qabs, qrope, pos_ref(ctx, pos_base), table); break;
+    default: hipLaunchKernelGGL((k_absorb_q<UT_FMT_F32, RB>), grid, dim3(threads), 0, ctx->stream, w, kv_b->scales, kv_b->row_bytes, L, q, rows, heads, nope, rope, kvh, qabs, qrope, pos_ref(ctx, pos_base), table); break;
     }
     timing_end(ctx, tok);
     return launch_check(ctx, "k_absorb_q");

@@ -115,6 +115,8 @@ _SIGS = [
     ("ut_session_truncate", _i32, [_vp, _i64]),
     ("ut_session_position", _i64, [_vp]),
     ("ut_model_set_stop_ids", _i32, [_vp, _vp, _i64]),
+    ("ut_model_enable_graphs", _i32, [_vp, _i32]),
+    ("ut_model_graph_stats", _i32, [_vp, _vp, _vp, _vp]),
     ("ut_generate", _i64, [_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp]),
     ("ut_generate_greedy", _i64, [_vp, _vp, _i64, _i64, _vp]),
     ("ut_speculative_loop", _i64, [_vp, _vp, _i64, _i64, _i32, _vp, _i64, _vp, _vp, _vp, _vp, _vp,
@@ -630,6 +632,15 @@ class Model:
         a = np.ascontiguousarray(ids, np.int32)
         self.ctx.check(lib().ut_model_set_stop_ids(self._h, a.ctypes.data if a.size else None,
                                                    a.size))
+
+    def enable_graphs(self, on: bool = True) -> None:
+        """One-row greedy decode steps replayed from a captured graph."""
+        self.ctx.check(lib().ut_model_enable_graphs(self._h, int(on)))
+
+    def graph_stats(self) -> dict:
+        c, r, f = C.c_int64(), C.c_int64(), C.c_int64()
+        self.ctx.check(lib().ut_model_graph_stats(self._h, C.byref(c), C.byref(r), C.byref(f)))
+        return {"captures": c.value, "replays": r.value, "failures": f.value}
 
     def generate_greedy(self, prompt, max_new: int) -> list:
         p = np.ascontiguousarray(prompt, np.int32)
