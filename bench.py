@@ -80,8 +80,10 @@ def gpu_wait(torch, ms: float) -> None:
     torch.cuda._sleep(int(ms * _CYCLES_PER_MS))
 
 
-def expert_block_bench(U, ctx, torch, tbl, cfg, M, steps, warmup, fmt_bits, seed, fused=True):
-    """Time `steps` expert-block passes; returns dict with GB/s and kernel times."""
+def expert_block_bench(U, ctx, torch, tbl, cfg, M, steps, warmup, fmt_bits, seed, fused=True,
+                       bf16x=False):
+    """Time `steps` expert-block passes; returns dict with GB/s and kernel times.
+    bf16x: the activations x are bf16 (the _bf16 entry points)."""
     from undertow_amd.configs import expert_bytes, gate_up_bytes
     E, H, I, k = cfg["n_experts"], cfg["hidden"], cfg["inter"], cfg["top_k"]
     g = torch.Generator(device="cuda:0")
@@ -89,6 +91,9 @@ def expert_block_bench(U, ctx, torch, tbl, cfg, M, steps, warmup, fmt_bits, seed
     n = steps + warmup
     logits = torch.randn(n, M, E, device="cuda:0", generator=g)
     x = torch.randn(M, H, device="cuda:0", generator=g)
+    if bf16x:
+        x = x.to(torch.bfloat16)
+    xb = x.element_size()
     ids_all = torch.empty(n, M, k, dtype=torch.int32, device="cuda:0")
     w_all = torch.empty(n, M, k, dtype=torch.float32, device="cuda:0")
     out = torch.empty(M, H, device="cuda:0")
@@ -100,16 +105,16 @@ def expert_block_bench(U, ctx, torch, tbl, cfg, M, steps, warmup, fmt_bits, seed
                                    cfg["n_group"], cfg["topk_group"], cfg["norm_topk_prob"],
                                    cfg["routed_scaling_factor"], ids_all[i].data_ptr(),
                                    w_all[i].data_ptr()))
-            ctx.check(lib.ut_moe_experts(ctx.handle, tbl._h, ids_all[i].data_ptr(),
-                                         w_all[i].data_ptr(), M, k, x.data_ptr(), out.data_ptr()))
+            fn = lib.ut_moe_experts_bf16 if bf16x else lib.ut_moe_experts
+            ctx.check(fn(ctx.handle, tbl._h, ids_all[i].data_ptr(), w_all[i].data_ptr(), M, k,
+                         x.data_ptr(), out.data_ptr()))
             return
         # route + routed experts (moe_forward's body, model.rs:210-281) in
         # one call; at one row the routing runs inside the gate/up launch
-        ctx.check(lib.ut_moe_route_experts(ctx.handle, tbl._h, logits[i].data_ptr(), None, M, k,
-                                           cfg["n_group"], cfg["topk_group"],
-                                           cfg["norm_topk_prob"], cfg["routed_scaling_factor"],
-                                           x.data_ptr(), out.data_ptr(), ids_all[i].data_ptr(),
-                                           w_all[i].data_ptr()))
+        fn = lib.ut_moe_route_experts_bf16 if bf16x else lib.ut_moe_route_experts
+        ctx.check(fn(ctx.handle, tbl._h, logits[i].data_ptr(), None, M, k, cfg["n_group"],
+                     cfg["topk_group"], cfg["norm_topk_prob"], cfg["routed_scaling_factor"],
+                     x.data_ptr(), out.data_ptr(), ids_all[i].data_ptr(), w_all[i].data_ptr()))
 
     for i in range(warmup):
         step(i)
@@ -147,7 +152,7 @@ def expert_block_bench(U, ctx, torch, tbl, cfg, M, steps, warmup, fmt_bits, seed
     ids = ids_all[warmup:].cpu().numpy()
     uniq = [len(np.unique(ids[s])) for s in range(steps)]
     u_mean = float(np.mean(uniq))
-    bytes_step = u_mean * expert_bytes(H, I, fmt_bits) + 2 * M * H * 4
+    bytes_step = u_mean * expert_bytes(H, I, fmt_bits) + M * H * (xb + 4)
     # per-kernel durations (events around each launch) in a second pass,
     # queued behind a GPU-side wait like the timed region
     ctx.enable_timing(True)
@@ -160,14 +165,14 @@ def expert_block_bench(U, ctx, torch, tbl, cfg, M, steps, warmup, fmt_bits, seed
     dl, dms = ctx.kernel_time(f"moe_down_{sfx}")
     tl, tms = ctx.kernel_time("")
     ctx.enable_timing(False)
-    gu_bytes = u_mean * gate_up_bytes(H, I, fmt_bits) + M * H * 4
+    gu_bytes = u_mean * gate_up_bytes(H, I, fmt_bits) + M * H * xb
     dn_bytes = u_mean * (H * ((I * fmt_bits + 7) // 8) + H * 4) + u_mean * M * I * 4
 
     def rate(nbytes, launches, total_ms):
         return nbytes / (total_ms / launches * 1e-3) / 1e9 if launches else None
 
     r = {
-        "M": M, "unique_experts_mean": u_mean, "ms_per_step": ms,
+        "M": M, "x_dtype": "bf16" if bf16x else "f32", "unique_experts_mean": u_mean, "ms_per_step": ms,
         "host_paced_ms_per_step": host_paced_ms,
         "bytes_per_step": bytes_step, "gbs": bytes_step / (ms * 1e-3) / 1e9,
         "kernels_us_per_step": tms / steps * 1e3,
@@ -674,6 +679,12 @@ def main():
             r = expert_block_bench(U, ctx, torch, tbl4, C2, M, args.steps, args.warmup, 4, 11 + M)
             variants[f"int4_M{M}"] = r
             log(f"config 2 int4 M={M}: {r['gbs']:.1f} GB/s")
+        # the bf16-activation variant of config 2
+        for M in (1, 4):
+            r = expert_block_bench(U, ctx, torch, tbl4, C2, M, args.steps, args.warmup, 4,
+                                   11 + M, bf16x=True)
+            variants[f"int4_M{M}_bf16x"] = r
+            log(f"config 2 int4 M={M}, bf16 activations: {r['gbs']:.1f} GB/s")
     del tbl4
     torch.cuda.empty_cache()
     if args.variants:

@@ -229,6 +229,24 @@ int32_t ut_moe_route_experts(ut_ctx *ctx, const ut_expert_table *tbl, const floa
                              float routed_scaling_factor, const float *x_dev, float *out_dev,
                              int32_t *ids_dev, float *weights_dev);
 
+/* bf16 activations: ut_moe_experts / ut_moe_route_experts with x_dev as
+ * bf16 bits [rows, hidden] (16-byte aligned, hidden % 8 == 0, else
+ * UT_ERR_ARG).  Each value is widened to f32 exactly, as the reference
+ * loads bf16 tensors (undertow-io/src/reader.rs:261-267 via
+ * half::bf16::to_f32), so out is bit-identical to the f32 entry point on
+ * the widened x.  At one row the gate/up launch reads the bf16 values
+ * itself (half the activation bytes); other shapes widen them in the
+ * working memory first. */
+int32_t ut_moe_experts_bf16(ut_ctx *ctx, const ut_expert_table *tbl, const int32_t *ids_dev,
+                            const float *weights_dev, int64_t rows, int32_t top_k,
+                            const uint16_t *x_dev, float *out_dev);
+int32_t ut_moe_route_experts_bf16(ut_ctx *ctx, const ut_expert_table *tbl,
+                                  const float *logits_dev, const float *bias_dev, int64_t rows,
+                                  int32_t top_k, int32_t n_group, int32_t topk_group,
+                                  int32_t norm_topk_prob, float routed_scaling_factor,
+                                  const uint16_t *x_dev, float *out_dev, int32_t *ids_dev,
+                                  float *weights_dev);
+
 /* ------------------------------------------------------ sample / verify */
 /* argmax (undertow-core/src/sample.rs:353-361) per row: first index of the
  * maximum; NaN never wins; returns 0 when row[0] is NaN. */

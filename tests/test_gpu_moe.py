@@ -294,6 +294,53 @@ def test_moe_one_row_equals_two_rows_repeated(ctx, fmt):
     ctx.synchronize()
 
 
+@pytest.mark.parametrize("fmt", [INT4, INT8])
+@pytest.mark.parametrize("H", [1024, 7168])
+def test_moe_bf16_activations_equal_widened_f32(ctx, fmt, H):
+    """bf16 activations (ut_moe_experts_bf16 / ut_moe_route_experts_bf16):
+    bit-identical to the f32 entry points on the exactly widened values, at
+    one row (the gate/up launch widens while staging), two to four rows
+    (widened first) and five (two passes); the oracle within the expert bar
+    on the widened x."""
+    import torch
+    rng = np.random.default_rng(91 + fmt + H)
+    E, I, k = 16, 512, 8
+    tbl, host_w = make_experts(ctx, rng, fmt, E, H, I)
+    for M in (1, 2, 3, 4, 5, 1):
+        ids = np.stack([rng.permutation(E)[:k] for _ in range(M)]).astype(np.int32)
+        w = rng.random((M, k)).astype(np.float32)
+        xb = dev(rng.standard_normal((M, H)).astype(np.float32)).to(torch.bfloat16)
+        xw = xb.float()
+        got = host(tbl.moe_experts(dev(ids), dev(w), xb))
+        ref = host(tbl.moe_experts(dev(ids), dev(w), xw))
+        assert np.array_equal(got, ref), M
+        want = oracle_moe(fmt, H, I, host_w, ids, w, host(xw))
+        assert (np.abs(got - want) <= 1e-4 * np.maximum(np.abs(want), 1.0)).all(), M
+        logits = dev(rng.standard_normal((M, E)).astype(np.float32))
+        out, rid, rw = tbl.moe_route_experts(logits, None, xb, k, 4, 2, True, 2.5)
+        out2, rid2, rw2 = tbl.moe_route_experts(logits, None, xw, k, 4, 2, True, 2.5)
+        assert np.array_equal(host(rid), host(rid2)) and np.array_equal(host(rw), host(rw2))
+        assert np.array_equal(host(out), host(out2)), M
+    ctx.synchronize()
+
+
+def test_moe_bf16_activations_checked(ctx):
+    """Misaligned bf16 rows and a hidden size that is not a multiple of 8
+    are refused on the host before any launch."""
+    import torch
+    import undertow_amd as U
+    rng = np.random.default_rng(5)
+    tbl, _ = make_experts(ctx, rng, INT8, 4, 256, 64)
+    ids, w = dev(np.array([[0, 1]], np.int32)), dev(np.ones((1, 2), np.float32))
+    buf = torch.zeros(257, dtype=torch.bfloat16, device="cuda:0")
+    with pytest.raises(U.UtError, match="alignment"):
+        tbl.moe_experts(ids, w, buf[1:].view(1, 256))
+    tbl2, _ = make_experts(ctx, rng, INT8, 2, 36, 16)
+    with pytest.raises(U.UtError, match="alignment"):
+        tbl2.moe_experts(ids, w, torch.zeros((1, 36), dtype=torch.bfloat16, device="cuda:0"))
+    ctx.synchronize()
+
+
 @pytest.mark.parametrize("H", [64, 256])  # 256: the gate/up launch resolves the plan
 def test_moe_bad_expert_is_reported(ctx, H):
     import undertow_amd as U

@@ -88,6 +88,9 @@ struct XSrc {
     // dig == nullptr: the shifts come from the staged rows' own max|x|
     // (single-chunk staging only) instead of sh
     int self_max = 0;
+    // bf16 activations [M][ldx] in place of xf (digitise-while-staging path
+    // only): widened to f32 exactly as they are staged
+    const uint16_t *xh = nullptr;
 };
 
 typedef unsigned int ut_u32x4 __attribute__((ext_vector_type(4)));
@@ -151,6 +154,11 @@ __device__ __forceinline__ float ld_global_f32(const float *p) {
 template <> __device__ __forceinline__ float4 ld_global<float4>(const void *p) {
     const ut_f32x4 v = *(const __attribute__((address_space(1))) ut_f32x4 *)p;
     return make_float4(v.x, v.y, v.z, v.w);
+}
+typedef unsigned int ut_u32x2 __attribute__((ext_vector_type(2)));
+template <> __device__ __forceinline__ uint2 ld_global<uint2>(const void *p) {
+    const ut_u32x2 v = *(const __attribute__((address_space(1))) ut_u32x2 *)p;
+    return make_uint2(v.x, v.y);
 }
 
 __device__ inline int64_t shfl_xor_i64(int64_t v, int off) {
@@ -302,9 +310,22 @@ __device__ __forceinline__ void gemv_stage_once(const XSrc &x, uint32_t *lds, in
         for (int j = 0; j < NI; j++) {
             const int i = tid + j * kGemvThreads, ic = i < tot ? i : tot - 1;
             const int m = ic / ng, g = ic - m * ng;
-            const float *src = x.xf + m * x.ldx + kc + g * CPW;
+            if (x.xh) {
+                const uint16_t *hs = x.xh + m * x.ldx + kc + g * CPW;
 #pragma unroll
-            for (int q = 0; q < NV; q++) v[j][q] = ld_global<float4>(src + 4 * q);
+                for (int q = 0; q < NV; q++) {
+                    // little-endian pairs: the low half is the even value
+                    const uint2 hv = ld_global<uint2>(hs + 4 * q);
+                    v[j][q] = make_float4(__uint_as_float(hv.x << 16),
+                                          __uint_as_float(hv.x & 0xffff0000u),
+                                          __uint_as_float(hv.y << 16),
+                                          __uint_as_float(hv.y & 0xffff0000u));
+                }
+            } else {
+                const float *src = x.xf + m * x.ldx + kc + g * CPW;
+#pragma unroll
+                for (int q = 0; q < NV; q++) v[j][q] = ld_global<float4>(src + 4 * q);
+            }
         }
         issue();
         // prep's waits stay behind every load above

@@ -53,6 +53,7 @@ struct MoeCall {
     const int32_t *ids = nullptr;      // [M, k]
     const float *weights = nullptr;    // [M, k]
     const float *x = nullptr;          // [M, H]
+    const uint16_t *xh = nullptr;      // [M, H] bf16 activations in place of x
     const XDigits *x_digits = nullptr; // optional: x already digitised
     float *out = nullptr;              // [M, ldo]
     int64_t ldo = 0;
@@ -96,6 +97,7 @@ inline bool gate_up_mfma_ok(int fmt, int M, int64_t H) {
 struct ScratchLayout {
     size_t total = 0;
     size_t count = 0, uniq = 0, choice = 0, sp = 0, xd = 0, h = 0, hmax = 0, hd = 0, d = 0, dpart = 0;
+    size_t xw = 0;  // bf16 activations widened to f32 (when not staged by gate/up)
     int xflags = 0, hflags = 0;
     int64_t ntiles = 0;
 };

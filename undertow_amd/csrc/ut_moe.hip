@@ -26,6 +26,7 @@
 #include "ut_moe.h"
 #include "ut_gemv_mfma.h"
 #include "ut_rowdig.h"
+#include "ut_ops.h"
 
 
 namespace ut {
@@ -621,7 +622,9 @@ __device__ __forceinline__ void gate_up_body(const GateUpArgs &a, int u, int til
         if (tile >= a.ntiles) return;
         const int n = a.plan_M * a.plan_k;
         int id = (M > 1 || !a.route_lg) && lane < n ? a.plan_ids[lane] : -1;
-        const uint8_t *dummy = a.x.xf ? (const uint8_t *)a.x.xf : (const uint8_t *)a.x.dig;
+        const uint8_t *dummy = a.x.xf   ? (const uint8_t *)a.x.xf
+                               : a.x.xh ? (const uint8_t *)a.x.xh
+                                        : (const uint8_t *)a.x.dig;
         auto mid = [&]() {
             if constexpr (M == 1) if (a.route_lg) {
                 // wave m routes row m; the choices go round through LDS
@@ -1184,6 +1187,7 @@ ScratchLayout moe_layout(int64_t M, int64_t k, int64_t slots, int64_t H, int64_t
     L.hd = take(fmt == UT_FMT_F32 ? 0 : xdigits_bytes(slots * M, I, hflags));
     L.d = take((size_t)slots * M * H * 4);
     L.dpart = take(slots == 1 ? (size_t)kDownMaxSplit * M * H * 8 : 0);
+    L.xw = take((size_t)M * H * 4);
     L.xflags = xflags;
     L.hflags = hflags;
     L.ntiles = ntiles;
@@ -1297,11 +1301,20 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
     if (c.route_logits && !route_here)
         UT_TRY(launch_route(ctx, c.route_logits, c.route_bias, M, c.E, c.k, c.route_ng, c.route_tg,
                             c.route_norm, c.route_scale, c.route_ids, c.route_w));
+    // bf16 activations: staged and widened by the gate/up launch itself
+    // when it digitises x (self_plan), else widened into the scratch first
+    const float *xin = c.x;
+    if (c.xh && !(self_plan && FMT != UT_FMT_F32)) {
+        float *xw = (float *)(base + L.xw);
+        UT_TRY(launch_bf16_to_f32(ctx, c.xh, (int64_t)M * c.H, xw));
+        xin = xw;
+    }
     if constexpr (FMT == UT_FMT_F32) {
-        xs.xf = c.x;
+        xs.xf = xin;
         xs.ldx = c.H;
     } else if (self_plan) {
-        xs.xf = c.x;
+        xs.xf = c.xh ? nullptr : xin;
+        xs.xh = c.xh;
         xs.ldx = c.H;
         xs.self_max = 1;
     } else {
@@ -1309,10 +1322,10 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
         if (c.x_digits) {
             xd = *c.x_digits;  // caller already digitised x
         } else if (need_plan && c.extra_slot < 0) {
-            UT_TRY(launch_digitize_plan(ctx, c.x, M, c.H, xd, L.xflags, c.ids, c.k, c.E,
+            UT_TRY(launch_digitize_plan(ctx, xin, M, c.H, xd, L.xflags, c.ids, c.k, c.E,
                                         (const void *const *)c.tbl.gate_w, plan, c.err_flag));
         } else {
-            UT_TRY(launch_digitize(ctx, c.x, c.H, M, c.H, nullptr, xd, L.xflags));
+            UT_TRY(launch_digitize(ctx, xin, c.H, M, c.H, nullptr, xd, L.xflags));
         }
         xs.dig = FMT == UT_FMT_INT4 ? xd.dig4 : xd.dig8;
         xs.KW = (c.H + FmtTraits<FMT>::kColsPerWord - 1) / FmtTraits<FMT>::kColsPerWord;
@@ -1350,7 +1363,7 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
         a.exps = xexps;
         // x digitised in this pass from c.x (so c.x is what the digits
         // hold): the matrix-core kernel stages c.x itself
-        if (use_mfma && xs.dig && xexps) a.mfma_xf = c.x;
+        if (use_mfma && xs.dig && xexps) a.mfma_xf = xin;
         a.h = h;
         a.hmax_parts = hmax;
         a.ntiles = (int)L.ntiles;
@@ -1674,7 +1687,8 @@ namespace {
 // rows, with `scratch` (moe_layout's bytes at four rows) as working memory.
 int32_t moe_experts_rows(ut_ctx *ctx, const ut_expert_table *tbl, const int32_t *ids_dev,
                          const float *weights_dev, int64_t rows, int32_t top_k, const float *x_dev,
-                         float *out_dev, void *scratch, int32_t *flag) {
+                         float *out_dev, void *scratch, int32_t *flag,
+                         const uint16_t *xh_dev = nullptr) {
     const int64_t maxM = 4;
     for (int64_t s0 = 0; s0 < rows; s0 += maxM) {
         MoeCall c;
@@ -1687,13 +1701,26 @@ int32_t moe_experts_rows(ut_ctx *ctx, const ut_expert_table *tbl, const int32_t 
         c.k = top_k;
         c.ids = ids_dev + s0 * top_k;
         c.weights = weights_dev + s0 * top_k;
-        c.x = x_dev + s0 * tbl->hidden;
+        if (xh_dev)
+            c.xh = xh_dev + s0 * tbl->hidden;
+        else
+            c.x = x_dev + s0 * tbl->hidden;
         c.out = out_dev + s0 * tbl->hidden;
         c.ldo = tbl->hidden;
         c.err_flag = flag;
         UT_TRY(moe_pass(ctx, c, scratch));
     }
     return UT_OK;
+}
+
+// bf16 activations are read 8 bytes (four values) at a time: 16-byte
+// aligned rows of a hidden size that is a multiple of 8.
+bool bf16_rows_ok(ut_ctx *ctx, const char *fn, const uint16_t *x, int64_t hidden) {
+    if (((uintptr_t)x & 15) || (hidden & 7)) {
+        set_error(ctx, "%s: bf16 activations need 16-byte alignment and hidden %% 8 == 0", fn);
+        return false;
+    }
+    return true;
 }
 
 int32_t moe_experts_check(ut_ctx *ctx, const char *fn, const ut_expert_table *tbl,
@@ -1782,24 +1809,32 @@ int32_t ut_moe_experts_noalloc(ut_ctx *ctx, const ut_expert_table *tbl, const in
                             ctx->noalloc_scratch, ctx->dev_err);
 }
 
-int32_t ut_moe_route_experts(ut_ctx *ctx, const ut_expert_table *tbl, const float *logits_dev,
-                             const float *bias_dev, int64_t rows, int32_t top_k, int32_t n_group,
-                             int32_t topk_group, int32_t norm_topk_prob,
-                             float routed_scaling_factor, const float *x_dev, float *out_dev,
-                             int32_t *ids_dev, float *weights_dev) {
-    if (!ctx || !tbl || !logits_dev || !ids_dev || !weights_dev || !x_dev || !out_dev || rows < 0 ||
-        top_k <= 0 || top_k > 64 || n_group < 0 || n_group > 64 || topk_group < 0) {
-        set_error(ctx, "ut_moe_route_experts: bad argument (top_k must be 1..64, n_group <= 64)");
+}  // extern "C"
+
+namespace {
+
+// ut_moe_route_experts over f32 (x_dev) or bf16 (xh_dev) activations.
+int32_t moe_route_experts_any(ut_ctx *ctx, const char *fn, const ut_expert_table *tbl,
+                              const float *logits_dev, const float *bias_dev, int64_t rows,
+                              int32_t top_k, int32_t n_group, int32_t topk_group,
+                              int32_t norm_topk_prob, float routed_scaling_factor,
+                              const float *x_dev, const uint16_t *xh_dev, float *out_dev,
+                              int32_t *ids_dev, float *weights_dev) {
+    if (!ctx || !tbl || !logits_dev || !ids_dev || !weights_dev || !(x_dev || xh_dev) ||
+        !out_dev || rows < 0 || top_k <= 0 || top_k > 64 || n_group < 0 || n_group > 64 ||
+        topk_group < 0) {
+        set_error(ctx, "%s: bad argument (top_k must be 1..64, n_group <= 64)", fn);
         return UT_ERR_ARG;
     }
     if (tbl->n > 4096) {
-        set_error(ctx, "ut_moe_route_experts: n_experts %lld > 4096", (long long)tbl->n);
+        set_error(ctx, "%s: n_experts %lld > 4096", fn, (long long)tbl->n);
         return UT_ERR_ARG;
     }
     if (tbl->fmt < 0) {
-        set_error(ctx, "ut_moe_route_experts: empty expert table");
+        set_error(ctx, "%s: empty expert table", fn);
         return UT_ERR_BAD_EXPERT;
     }
+    if (xh_dev && !bf16_rows_ok(ctx, fn, xh_dev, tbl->hidden)) return UT_ERR_ARG;
     if (rows == 0) return UT_OK;
     const int64_t maxM = 4;
     const int64_t slots = moe_slots((int)maxM, top_k, tbl->n, -1);
@@ -1830,13 +1865,71 @@ int32_t ut_moe_route_experts(ut_ctx *ctx, const ut_expert_table *tbl, const floa
         c.route_w = weights_dev + s0 * top_k;
         c.ids = c.route_ids;
         c.weights = c.route_w;
-        c.x = x_dev + s0 * tbl->hidden;
+        if (xh_dev)
+            c.xh = xh_dev + s0 * tbl->hidden;
+        else
+            c.x = x_dev + s0 * tbl->hidden;
         c.out = out_dev + s0 * tbl->hidden;
         c.ldo = tbl->hidden;
         c.err_flag = flag;
         UT_TRY(moe_pass(ctx, c, ptrs[0]));
     }
     return UT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t ut_moe_route_experts(ut_ctx *ctx, const ut_expert_table *tbl, const float *logits_dev,
+                             const float *bias_dev, int64_t rows, int32_t top_k, int32_t n_group,
+                             int32_t topk_group, int32_t norm_topk_prob,
+                             float routed_scaling_factor, const float *x_dev, float *out_dev,
+                             int32_t *ids_dev, float *weights_dev) {
+    if (!x_dev) {
+        set_error(ctx, "ut_moe_route_experts: bad argument");
+        return UT_ERR_ARG;
+    }
+    return moe_route_experts_any(ctx, "ut_moe_route_experts", tbl, logits_dev, bias_dev, rows,
+                                 top_k, n_group, topk_group, norm_topk_prob,
+                                 routed_scaling_factor, x_dev, nullptr, out_dev, ids_dev,
+                                 weights_dev);
+}
+
+int32_t ut_moe_route_experts_bf16(ut_ctx *ctx, const ut_expert_table *tbl,
+                                  const float *logits_dev, const float *bias_dev, int64_t rows,
+                                  int32_t top_k, int32_t n_group, int32_t topk_group,
+                                  int32_t norm_topk_prob, float routed_scaling_factor,
+                                  const uint16_t *x_dev, float *out_dev, int32_t *ids_dev,
+                                  float *weights_dev) {
+    if (!x_dev) {
+        set_error(ctx, "ut_moe_route_experts_bf16: bad argument");
+        return UT_ERR_ARG;
+    }
+    return moe_route_experts_any(ctx, "ut_moe_route_experts_bf16", tbl, logits_dev, bias_dev,
+                                 rows, top_k, n_group, topk_group, norm_topk_prob,
+                                 routed_scaling_factor, nullptr, x_dev, out_dev, ids_dev,
+                                 weights_dev);
+}
+
+int32_t ut_moe_experts_bf16(ut_ctx *ctx, const ut_expert_table *tbl, const int32_t *ids_dev,
+                            const float *weights_dev, int64_t rows, int32_t top_k,
+                            const uint16_t *x_dev, float *out_dev) {
+    const float *fake = (const float *)x_dev;  // the argument check's non-null test only
+    UT_TRY(moe_experts_check(ctx, "ut_moe_experts_bf16", tbl, ids_dev, weights_dev, rows, top_k,
+                             fake, out_dev));
+    if (!bf16_rows_ok(ctx, "ut_moe_experts_bf16", x_dev, tbl->hidden)) return UT_ERR_ARG;
+    if (rows == 0) return UT_OK;
+    const int64_t maxM = 4;
+    const int64_t slots = moe_slots((int)maxM, top_k, tbl->n, -1);
+    ScratchPlan plan;
+    plan.add(moe_layout(maxM, top_k, slots, tbl->hidden, tbl->inter, tbl->fmt).total);
+    std::vector<void *> ptrs;
+    UT_TRY(scratch_acquire(ctx, plan, ptrs));
+    int32_t *flag = nullptr;
+    UT_TRY(device_error_flag(ctx, &flag));
+    return moe_experts_rows(ctx, tbl, ids_dev, weights_dev, rows, top_k, nullptr, out_dev, ptrs[0],
+                            flag, x_dev);
 }
 
 }  // extern "C"

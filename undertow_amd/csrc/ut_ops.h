@@ -71,6 +71,8 @@ int32_t launch_rmsnorm(ut_ctx *ctx, const float *x, int64_t ldx, const float *w,
                        float eps, int64_t rows, float *out, int64_t ldo);
 // y += x (f32 adds), n elements.
 int32_t launch_add(ut_ctx *ctx, float *y, const float *x, int64_t n);
+// bf16 -> f32 (exact widening), n elements.
+int32_t launch_bf16_to_f32(ut_ctx *ctx, const uint16_t *x, int64_t n, float *y);
 // dst rows [pos, pos + rows) (stride ld) <- src [rows][H]; pos follows the
 // context's captured-step position when one is set.
 int32_t launch_copy_rows_at(ut_ctx *ctx, float *dst, int64_t ld, int64_t pos, const float *src,

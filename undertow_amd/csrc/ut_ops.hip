@@ -91,6 +91,22 @@ int32_t launch_add(ut_ctx *ctx, float *y, const float *x, int64_t n) {
     return launch_check(ctx, "k_add");
 }
 
+__global__ void k_bf16_to_f32(const uint16_t *__restrict__ x, int64_t n, float *__restrict__ y) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        y[i] = __uint_as_float((uint32_t)x[i] << 16);
+}
+
+int32_t launch_bf16_to_f32(ut_ctx *ctx, const uint16_t *x, int64_t n, float *y) {
+    if (n <= 0) return UT_OK;
+    unsigned blocks = (unsigned)((n + 255) / 256);
+    if (blocks > 1024) blocks = 1024;
+    int tok = timing_begin(ctx, "bf16_to_f32");
+    hipLaunchKernelGGL(k_bf16_to_f32, dim3(blocks), dim3(256), 0, ctx->stream, x, n, y);
+    timing_end(ctx, tok);
+    return launch_check(ctx, "k_bf16_to_f32");
+}
+
 // rows x H floats from src into dst rows pos.. (row stride ld): the
 // pre-norm hidden states the MTP head reads later.
 __global__ void k_copy_rows_at(float *__restrict__ dst, int64_t ld, PosRef pos,

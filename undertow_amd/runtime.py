@@ -93,6 +93,9 @@ _SIGS = [
     ("ut_moe_experts_noalloc", _i32, [_vp, _vp, _vp, _vp, _i64, _i32, _vp, _vp]),
     ("ut_moe_route_experts", _i32, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _f32, _vp,
                                     _vp, _vp, _vp]),
+    ("ut_moe_experts_bf16", _i32, [_vp, _vp, _vp, _vp, _i64, _i32, _vp, _vp]),
+    ("ut_moe_route_experts_bf16", _i32, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _f32,
+                                         _vp, _vp, _vp, _vp]),
     ("ut_argmax_rows", _i32, [_vp, _vp, _i64, _i64, _vp]),
     ("ut_mla_attend", _i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _vp]),
     ("ut_mla_cache_split", _i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
@@ -508,11 +511,14 @@ class ExpertTable:
         self._keep[e] = (gate, up, down)
 
     def moe_experts(self, ids, weights, x):
+        """The routed experts over f32 or bf16 activations x [rows, hidden];
+        the result is f32 either way."""
         torch = _torch()
         rows, k = ids.shape
-        out = torch.empty_like(x)
-        self.ctx.check(lib().ut_moe_experts(self.ctx.handle, self._h, _ptr(ids), _ptr(weights),
-                                            rows, k, _ptr(x), _ptr(out)))
+        out = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+        fn = lib().ut_moe_experts_bf16 if x.dtype == torch.bfloat16 else lib().ut_moe_experts
+        self.ctx.check(fn(self.ctx.handle, self._h, _ptr(ids), _ptr(weights), rows, k, _ptr(x),
+                          _ptr(out)))
         return out
 
     def moe_experts_noalloc(self, ids, weights, x, out) -> None:
@@ -524,13 +530,15 @@ class ExpertTable:
     def moe_route_experts(self, logits, bias, x, k, n_group, topk_group, norm_topk_prob,
                           routed_scaling_factor):
         """Route (ut_route's semantics) and run the experts in one call;
-        returns (out, ids, weights)."""
+        returns (out, ids, weights).  x may be f32 or bf16; out is f32."""
         torch = _torch()
         rows = x.shape[0]
-        out = torch.empty_like(x)
+        out = torch.empty(x.shape, dtype=torch.float32, device=x.device)
         ids = torch.empty((rows, k), dtype=torch.int32, device=x.device)
         w = torch.empty((rows, k), dtype=torch.float32, device=x.device)
-        self.ctx.check(lib().ut_moe_route_experts(
+        fn = (lib().ut_moe_route_experts_bf16 if x.dtype == torch.bfloat16
+              else lib().ut_moe_route_experts)
+        self.ctx.check(fn(
             self.ctx.handle, self._h, _ptr(logits), _ptr(bias) if bias is not None else None, rows,
             k, n_group, topk_group, int(norm_topk_prob), routed_scaling_factor, _ptr(x), _ptr(out),
             _ptr(ids), _ptr(w)))
