@@ -294,6 +294,49 @@ def test_moe_one_row_equals_two_rows_repeated(ctx, fmt):
     ctx.synchronize()
 
 
+@pytest.mark.parametrize("E,ng,tg", [(256, 8, 4), (256, 1, 1), (224, 7, 3), (256, 8, 8)])
+@pytest.mark.parametrize("bias", [False, True])
+def test_moe_route_experts_ties_match_route(ctx, E, ng, tg, bias):
+    """The one-row routing inside the gate/up launch (four keys per lane)
+    against ut_route's wave router on logits with many ties: values on a
+    coarse grid (equal sigmoids inside and across groups, tied group
+    scores), all-equal rows, and a NaN.  Ids, weights and outputs bit for
+    bit; ids also against the oracle."""
+    import undertow_amd as U
+    rng = np.random.default_rng(E + ng + bias)
+    H, I, k, n_w = 256, 64, 8, 8
+    tbl = U.ExpertTable(ctx, E, H, I)
+    qts = []
+    for j in range(n_w):
+        g, u, d = (rand_qtensor(rng, INT8, I, H), rand_qtensor(rng, INT8, I, H),
+                   rand_qtensor(rng, INT8, H, I))
+        qts.append((U.QTensor(ctx, INT8, *g, I, H), U.QTensor(ctx, INT8, *u, I, H),
+                    U.QTensor(ctx, INT8, *d, H, I)))
+    for e in range(E):
+        tbl.set(e, *qts[e % n_w])
+    b = (rng.integers(-2, 3, E) * 0.05).astype(np.float32) if bias else None
+    rows = [rng.integers(-3, 4, E).astype(np.float32) * 0.5 for _ in range(12)]
+    rows.append(np.zeros(E, np.float32))
+    rows.append(np.full(E, 2.0, np.float32))
+    nan_row = rng.integers(-3, 4, E).astype(np.float32)
+    nan_row[37] = np.nan
+    rows.append(nan_row)
+    x = dev(rng.standard_normal((1, H)).astype(np.float32))
+    for i, lg in enumerate(rows):
+        logits = dev(lg[None])
+        bd = None if b is None else dev(b)
+        out, ids, w = tbl.moe_route_experts(logits, bd, x, k, ng, tg, True, 2.5)
+        rid, rw = U.route(ctx, logits, bd, k, ng, tg, True, 2.5)
+        ref = tbl.moe_experts(rid, rw, x)
+        assert np.array_equal(host(ids), host(rid)), i
+        assert np.array_equal(host(w), host(rw), equal_nan=True), i
+        assert np.array_equal(host(out), host(ref), equal_nan=True), i
+        if not np.isnan(lg).any():
+            oid, _ = O.route(lg, b, k, ng, tg, True, 2.5)
+            assert host(ids)[0].tolist() == oid.tolist(), i
+    ctx.synchronize()
+
+
 @pytest.mark.parametrize("fmt", [INT4, INT8])
 @pytest.mark.parametrize("H", [1024, 7168])
 def test_moe_bf16_activations_equal_widened_f32(ctx, fmt, H):

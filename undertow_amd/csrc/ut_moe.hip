@@ -269,12 +269,14 @@ __device__ __forceinline__ void route_row_wave_v(const float (&lv)[KPL], const f
         if (gs > 1) gsum = gsum + order_value((uint32_t)(m2 >> 32));
         const int g = lane / LG;
         const uint64_t gk = route_key(gsum, g);
+        // group g2's key from its first lane (a wave-uniform lane: read
+        // lanes, no LDS permutes)
         int rank = 0;
         for (int g2 = 0; g2 < n_group; g2++) {
             const int src = g2 * LG;
-            const uint64_t o = ((uint64_t)(uint32_t)__shfl((int)(gk >> 32), src, 64) << 32) |
-                               (uint32_t)__shfl((int)(uint32_t)gk, src, 64);
-            rank += o > gk;
+            const uint32_t ohi = __builtin_amdgcn_readlane((uint32_t)(gk >> 32), src);
+            const uint32_t olo = __builtin_amdgcn_readlane((uint32_t)gk, src);
+            rank += (((uint64_t)ohi << 32) | olo) > gk;
         }
         if (rank >= topk_group) {
 #pragma unroll
@@ -282,23 +284,40 @@ __device__ __forceinline__ void route_row_wave_v(const float (&lv)[KPL], const f
                 if (lane * KPL + j < E) key[j] = route_key(-INFINITY, lane * KPL + j);
         }
     }
+    // the selections: the largest value bits over the wave, then the lowest
+    // index holding them -- the lowest lane with a match, its lowest j
+    // (e = lane*KPL + j) -- which is the largest 64-bit key without a second
+    // reduction.  A chosen key drops to 0, below every expert's value bits
+    // (-inf keys as 0x007fffff); only keys past E are 0, and at most E are
+    // chosen.
+    uint32_t hk[KPL];
+#pragma unroll
+    for (int j = 0; j < KPL; j++) hk[j] = (uint32_t)(key[j] >> 32);
     const int keff = k < E ? k : E;
     float denom = 0.0f;
     int32_t id = -1;
     float wv = 0.0f;
     for (int r = 0; r < keff; r++) {
-        uint64_t b = key[0];
+        uint32_t b = hk[0];
 #pragma unroll
-        for (int j = 1; j < KPL; j++) b = key[j] > b ? key[j] : b;
-        const uint64_t win = run_max_key<64>(b);
-        const int e = (int)~(uint32_t)win;
-        float sv = 0.0f;
+        for (int j = 1; j < KPL; j++) b = max(b, hk[j]);
+        const uint32_t mx = __builtin_amdgcn_readlane(run_max_u32<64>(b), 63);
+        int jf = -1;
+        float sj = 0.0f;
 #pragma unroll
-        for (int j = 0; j < KPL; j++) {
-            if (key[j] == win) key[j] = 0;
-            if (lane * KPL + j == e) sv = sc[j];
-        }
-        sv = __shfl(sv, e / KPL, 64);
+        for (int j = KPL - 1; j >= 0; j--)
+            if (hk[j] == mx) {
+                jf = j;
+                sj = sc[j];
+            }
+        const int L = __ffsll((unsigned long long)__ballot(jf >= 0)) - 1;
+        const int jw = __builtin_amdgcn_readlane(jf, L);
+        const int e = L * KPL + jw;
+        const float sv = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(sj), L));
+        if (lane == L)
+#pragma unroll
+            for (int j = 0; j < KPL; j++)
+                if (j == jw) hk[j] = 0;
         denom = denom + sv;  // sequential sum in choice order
         if (lane == r) { id = e; wv = sv; }
     }
