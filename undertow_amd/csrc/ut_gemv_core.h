@@ -507,8 +507,11 @@ __device__ __forceinline__ bool gemv_one_chunk(int64_t k_begin, int64_t kend) {
 // weight loads, which read rows[] only then (so mid may still fill rows
 // in); on the single-chunk path after the activation loads are issued.
 // KC: the staged chunk's columns (gemv_chunk_cols, possibly capped).
+// STAGED: the caller has already staged the one chunk into LDS (and passed
+// a workgroup barrier after it): straight to the weights.
 template <int FMT, int M, int R = kGemvRows, int DEPTH = gemv_depth<M>(),
-          int KC = gemv_chunk_cols<FMT, M>(), typename Prep = NoPrep, typename Mid = NoMid>
+          int KC = gemv_chunk_cols<FMT, M>(), bool STAGED = false, typename Prep = NoPrep,
+          typename Mid = NoMid>
 __device__ __forceinline__ void gemv_core(const uint8_t *const rows[R], int64_t K, const XSrc &x,
                                           uint32_t *lds, CoreOut<FMT, M, R> &res,
                                           int64_t k_begin = 0, int64_t k_end = -1,
@@ -528,12 +531,16 @@ __device__ __forceinline__ void gemv_core(const uint8_t *const rows[R], int64_t 
     if (gemv_one_chunk<FMT, M, KC>(k_begin, kend)) {
         // unconditional (clamped) first loads: a skipped load on any path
         // into the loop would make the wait counts inside it conservative
-        gemv_stage_once<FMT, M, KC>(x, lds, k_begin, (int)(kend - k_begin), [&]() {
+        auto first = [&]() {
             mid();
 #pragma unroll
             for (int u = 0; u < DEPTH; u++)
                 gemv_load<FMT, R>(rows, lane_col + (u < nsteps ? u : nsteps - 1) * STEP, wq[u]);
-        }, prep);
+        };
+        if constexpr (STAGED)
+            first();
+        else
+            gemv_stage_once<FMT, M, KC>(x, lds, k_begin, (int)(kend - k_begin), first, prep);
         const int c0 = s * LANE_COLS;
         int64_t t = 0;
         for (; t + 2 * DEPTH <= nsteps; t += DEPTH) {

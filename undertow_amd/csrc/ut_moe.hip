@@ -233,15 +233,14 @@ __device__ __forceinline__ void route_row_wave(const float *__restrict__ lg,
                           my_w);
 }
 
-// The wave router on loaded logits (route_load).
+// The wave router on loaded logits (route_load), in three phases for
+// callers that interleave them with other work: the keys (sigmoid, bias),
+// the group limitation, and the selections with their weights.
 template <int KPL>
-__device__ __forceinline__ void route_row_wave_v(const float (&lv)[KPL], const float (&bv)[KPL],
-                                                 bool has_bias, int E, int k, int n_group,
-                                                 int topk_group, int norm, float scale,
-                                                 int32_t *my_id, float *my_w) {
+__device__ __forceinline__ void route_phase_keys(const float (&lv)[KPL], const float (&bv)[KPL],
+                                                 bool has_bias, int E, float (&sc)[KPL],
+                                                 uint64_t (&key)[KPL]) {
     const int lane = threadIdx.x & 63;
-    float sc[KPL];
-    uint64_t key[KPL];
 #pragma unroll
     for (int j = 0; j < KPL; j++) {
         const int e = lane * KPL + j;
@@ -254,6 +253,12 @@ __device__ __forceinline__ void route_row_wave_v(const float (&lv)[KPL], const f
             key[j] = 0;  // below every expert's key
         }
     }
+}
+
+template <int KPL>
+__device__ __forceinline__ void route_phase_groups(uint64_t (&key)[KPL], int E, int n_group,
+                                                   int topk_group) {
+    const int lane = threadIdx.x & 63;
     if (n_group > 1 && topk_group < n_group) {
         const int gs = E / n_group, LG = gs / KPL;
         uint64_t b = key[0];
@@ -284,6 +289,14 @@ __device__ __forceinline__ void route_row_wave_v(const float (&lv)[KPL], const f
                 if (lane * KPL + j < E) key[j] = route_key(-INFINITY, lane * KPL + j);
         }
     }
+}
+
+template <int KPL>
+__device__ __forceinline__ void route_phase_select(const float (&sc)[KPL],
+                                                   const uint64_t (&key)[KPL], int E, int k,
+                                                   int norm, float scale, int32_t *my_id,
+                                                   float *my_w) {
+    const int lane = threadIdx.x & 63;
     // the selections: the largest value bits over the wave, then the lowest
     // index holding them -- the lowest lane with a match, its lowest j
     // (e = lane*KPL + j) -- which is the largest 64-bit key without a second
@@ -332,6 +345,18 @@ __device__ __forceinline__ void route_row_wave_v(const float (&lv)[KPL], const f
             *my_w = 0.0f;
         }
     }
+}
+
+template <int KPL>
+__device__ __forceinline__ void route_row_wave_v(const float (&lv)[KPL], const float (&bv)[KPL],
+                                                 bool has_bias, int E, int k, int n_group,
+                                                 int topk_group, int norm, float scale,
+                                                 int32_t *my_id, float *my_w) {
+    float sc[KPL];
+    uint64_t key[KPL];
+    route_phase_keys<KPL>(lv, bv, has_bias, E, sc, key);
+    route_phase_groups<KPL>(key, E, n_group, topk_group);
+    route_phase_select<KPL>(sc, key, E, k, norm, scale, my_id, my_w);
 }
 
 template <int KPL>
@@ -609,10 +634,219 @@ __device__ inline int plan_slot_wave(int id, int n, int64_t E, const void *const
     return cnt;
 }
 
+// plan_slot_wave for choices made in this launch whose gate and up weight
+// pointers came with them (gsel, usel: lane j < n holds entry j's), so the
+// slot's weights can be read at once; slot u's scale pointers are loaded by
+// expert id afterwards (read only after the weights).  The writer wave loads
+// all six pointers per entry for the plan, as plan_slot_wave.
+__device__ inline int plan_slot_wave_pf(int id, int n, int64_t E,
+                                        const void *const *__restrict__ tbl, uint64_t gsel,
+                                        uint64_t usel, int u, bool writer, MoePlan plan,
+                                        int32_t *__restrict__ err_flag, const void *(&p6)[6]) {
+    const int lane = threadIdx.x & 63;
+    const bool inr = lane < n && id >= 0 && id < E;
+    const bool ok = inr && gsel != 0;
+    const int e = ok ? id : -1;
+    // j0: the entry's first appearance (model.rs:219-233)
+    int j0 = lane;
+    for (int i = 0; i < n; i++) {
+        const int ei = __builtin_amdgcn_readlane(e, i);
+        if (i < j0 && ei == e) j0 = i;
+    }
+    const bool first = ok && j0 == lane;
+    const uint64_t fm = __ballot(first);
+    const int slot = ok ? __popcll(fm & ((1ull << j0) - 1)) : -1;
+    const int cnt = __popcll(fm);
+    const uint64_t um = __ballot(first && slot == u);
+    if (um) {
+        const int L = __ffsll((unsigned long long)um) - 1;
+        // halves as uint32_t: readlane returns int, which would sign-extend
+        const uint32_t glo = __builtin_amdgcn_readlane((uint32_t)gsel, L);
+        const uint32_t ghi = __builtin_amdgcn_readlane((uint32_t)(gsel >> 32), L);
+        const uint32_t ulo = __builtin_amdgcn_readlane((uint32_t)usel, L);
+        const uint32_t uhi = __builtin_amdgcn_readlane((uint32_t)(usel >> 32), L);
+        const int eu = __builtin_amdgcn_readlane(e, L);
+        p6[kSpGate] = (const void *)(((uint64_t)ghi << 32) | glo);
+        p6[kSpUp] = (const void *)(((uint64_t)uhi << 32) | ulo);
+        p6[kSpGateS] = tbl[(int64_t)kSpGateS * E + eu];
+        p6[kSpUpS] = tbl[(int64_t)kSpUpS * E + eu];
+    }
+    if (writer) {
+        if (lane < n) {
+            if (!ok && id != -1 && err_flag) *err_flag = 1;
+            plan.choice_slot[lane] = slot;
+            if (first) {
+                plan.uniq[slot] = e;
+#pragma unroll
+                for (int i = 0; i < 6; i++) plan.sp[slot * 6 + i] = tbl[(int64_t)i * E + e];
+            }
+        }
+        if (lane == 0) *plan.count = cnt;
+    }
+    return cnt;
+}
+
+// Gate/up at one row with the routing in this launch and x digitised here
+// (f32 or bf16 activations, one staged chunk): wave 0 routes the row while
+// waves 1-3 stage and digitise x, the router's phases falling between the
+// staging's two workgroup barriers -- the keys before the one after the
+// row-max partials, the group limitation and the selections before the
+// one after the digits.  Wave 0 loads the logits and its experts' gate/up
+// pointers first and hands the choices and their pointers over in LDS; the
+// first weight loads follow at once.  The same digits, exponent, choices
+// and results as the one-wave router in gemv_core's staging.  Returns the
+// slot count; rows, scale pointers, exponent and res are set for slot u.
+template <int FMT>
+__device__ __forceinline__ int gate_up_route_staged(const GateUpArgs &a, int u, int tile,
+                                                    int64_t oc, uint32_t *lds,
+                                                    const uint8_t *(&rows)[2], const float *&gsc,
+                                                    const float *&usc, int32_t &exl,
+                                                    CoreOut<FMT, 1, 2> &res) {
+    using T = FmtTraits<FMT>;
+    constexpr int KC = gemv_chunk_cols<FMT, 1>();
+    constexpr int CPW = T::kColsPerWord, PL = T::kPlanes, LW = KC / CPW, NV = CPW / 4;
+    constexpr int NS = kGemvThreads - 64;  // staging threads (waves 1-3)
+    constexpr int NI = (LW + NS - 1) / NS;
+    __shared__ uint32_t s_red[4];
+    __shared__ int32_t s_rid[64];
+    __shared__ uint64_t s_gp[64], s_up[64];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, t = tid - 64;
+    const int n = a.plan_k;  // one row
+    const int E = (int)a.E;
+    const int ng = (int)(a.H / CPW);  // word groups of the row
+    const bool writer = u == 0 && tile == 0 && wave == 0;
+    float lv[4], bv[4];
+    uint64_t pg[4], pu[4];
+    float4 v[NI][NV];
+    if (wave == 0) {
+        route_load<4>(a.route_lg, a.route_bias, E, lv, bv);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int e = lane * 4 + j;
+            pg[j] = e < E ? (uint64_t)a.ptbl[(int64_t)kSpGate * E + e] : 0;
+            pu[j] = e < E ? (uint64_t)a.ptbl[(int64_t)kSpUp * E + e] : 0;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < NI; j++) {
+            const int i = t + j * NS, ic = i < ng ? i : ng - 1;
+            if (a.x.xh) {
+                const uint16_t *hs = a.x.xh + (int64_t)ic * CPW;
+#pragma unroll
+                for (int q = 0; q < NV; q++) {
+                    // little-endian pairs: the low half is the even value
+                    const uint2 hv = ld_global<uint2>(hs + 4 * q);
+                    v[j][q] = make_float4(__uint_as_float(hv.x << 16),
+                                          __uint_as_float(hv.x & 0xffff0000u),
+                                          __uint_as_float(hv.y << 16),
+                                          __uint_as_float(hv.y & 0xffff0000u));
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < NV; q++)
+                    v[j][q] = ld_global<float4>(a.x.xf + (int64_t)ic * CPW + 4 * q);
+            }
+        }
+    }
+    // phase 1: the keys | max|x| partials
+    float rsc[4];
+    uint64_t rkey[4];
+    if (wave == 0) {
+        __builtin_amdgcn_s_setprio(3);
+        route_phase_keys<4>(lv, bv, a.route_bias != nullptr, E, rsc, rkey);
+        if (lane == 0) s_red[0] = 0;
+    } else {
+        uint32_t b = 0;
+#pragma unroll
+        for (int j = 0; j < NI; j++)
+            if (t + j * NS < ng)
+#pragma unroll
+                for (int q = 0; q < NV; q++)
+                    b = max(b, max(max(__float_as_uint(fabsf(v[j][q].x)),
+                                       __float_as_uint(fabsf(v[j][q].y))),
+                                   max(__float_as_uint(fabsf(v[j][q].z)),
+                                       __float_as_uint(fabsf(v[j][q].w)))));
+        b = wave_reduce_dpp(b, [](uint32_t p, uint32_t q) { return p > q ? p : q; });
+        if (lane == 0) s_red[wave] = b;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    // the row's exponent, as rowmax_reduce
+    const uint32_t r = max(max(s_red[0], s_red[1]), max(s_red[2], s_red[3]));
+    int Ex = 0;
+    if (r < 0x7f800000u && r != 0) (void)frexpf(__uint_as_float(r), &Ex);
+    const int32_t sh = r >= 0x7f800000u ? INT32_MIN : 22 - Ex;
+    exl = sh == INT32_MIN ? INT32_MIN : -sh;
+    // phase 2: group limitation and selections | digits
+    if (wave == 0) {
+        route_phase_groups<4>(rkey, E, a.route_ng, a.route_tg);
+        int32_t rid = -1;
+        float rw = 0.0f;
+        route_phase_select<4>(rsc, rkey, E, a.plan_k, a.route_norm, a.route_scale, &rid, &rw);
+        __builtin_amdgcn_s_setprio(0);
+        // each choice's gate/up pointers from the lane holding its expert
+        const bool inr = lane < n && rid >= 0 && rid < E;
+        const int src = inr ? rid >> 2 : 0, jj = inr ? rid & 3 : 0;
+        uint64_t gsel = 0, usel = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t glo = __shfl((uint32_t)pg[j], src, 64);
+            const uint32_t ghi = __shfl((uint32_t)(pg[j] >> 32), src, 64);
+            const uint32_t ulo = __shfl((uint32_t)pu[j], src, 64);
+            const uint32_t uhi = __shfl((uint32_t)(pu[j] >> 32), src, 64);
+            if (jj == j) {
+                gsel = ((uint64_t)ghi << 32) | glo;
+                usel = ((uint64_t)uhi << 32) | ulo;
+            }
+        }
+        if (lane < n) {
+            s_rid[lane] = rid;
+            s_gp[lane] = gsel;
+            s_up[lane] = usel;
+        }
+        if (writer && lane < n) {
+            a.route_ids[lane] = rid;
+            a.route_w[lane] = rw;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < NI; j++) {
+            const int i = t + j * NS;
+            if (i < ng) {
+                float f[CPW];
+#pragma unroll
+                for (int q = 0; q < NV; q++) {
+                    f[4 * q] = v[j][q].x; f[4 * q + 1] = v[j][q].y;
+                    f[4 * q + 2] = v[j][q].z; f[4 * q + 3] = v[j][q].w;
+                }
+                uint32_t w[PL];
+                digit_words<FMT>(f, CPW, sh, w);
+#pragma unroll
+                for (int p = 0; p < PL; p++) lds[p * LW + i] = w[p];
+            }
+        }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const int id = lane < n ? s_rid[lane] : -1;
+    const void *p6[6];
+    const int cnt = plan_slot_wave_pf(id, n, a.E, a.ptbl, lane < n ? s_gp[lane] : 0,
+                                      lane < n ? s_up[lane] : 0, u, writer, a.plan, a.err_flag,
+                                      p6);
+    const bool live = u < cnt;
+    const uint8_t *dummy = a.x.xf ? (const uint8_t *)a.x.xf : (const uint8_t *)a.x.xh;
+    rows[0] = live ? (const uint8_t *)p6[kSpGate] + oc * a.row_bytes : dummy;
+    rows[1] = live ? (const uint8_t *)p6[kSpUp] + oc * a.row_bytes : dummy;
+    gsc = live ? (const float *)p6[kSpGateS] : nullptr;
+    usc = live ? (const float *)p6[kSpUpS] : nullptr;
+    gemv_core<FMT, 1, 2, gemv_depth<1>(), KC, true>(rows, a.H, a.x, lds, res);
+    return cnt;
+}
+
 // 16 h-rows per workgroup: wave w, row group g -> h row o = tile*16 +
 // w*4 + g; row slot 0 reads gate row o, slot 1 up row o, so both land in the
 // same lanes and h = silu(g)*u is formed in registers.
-template <int FMT, int M>
+// STAGED_ROUTE: compile gate_up_route_staged in (launches whose one-row
+// routing may come with x to digitise).
+template <int FMT, int M, bool STAGED_ROUTE = true>
 __device__ __forceinline__ void gate_up_body(const GateUpArgs &a, int u, int tile, uint32_t *lds,
                                              uint32_t *wg_max) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
@@ -633,7 +867,16 @@ __device__ __forceinline__ void gate_up_body(const GateUpArgs &a, int u, int til
 #pragma unroll
         for (int m = 0; m < M; m++) exl[m] = shl[m] == INT32_MIN ? INT32_MIN : -shl[m];
     };
-    if (a.plan_ids) {
+    bool staged_route = false;
+    if constexpr (STAGED_ROUTE && M == 1 && FMT != UT_FMT_F32)
+        staged_route = a.plan_ids && a.route_lg && a.x.self_max && !a.x.dig;
+    if (staged_route) {
+        if constexpr (STAGED_ROUTE && M == 1 && FMT != UT_FMT_F32) {
+            if (tile >= a.ntiles) return;
+            cnt = gate_up_route_staged<FMT>(a, u, tile, oc, lds, rows, gsc, usc, exl[0], res);
+            if (u >= cnt) return;
+        }
+    } else if (a.plan_ids) {
         // this wave resolves the slot from the ids (loaded ahead of x) while
         // x's loads are in flight; a slot past the count streams x itself in
         // place of weights (valid memory of at least a row's bytes: f32 x,
@@ -793,8 +1036,11 @@ template <int FA, int FB, int M>
 __global__ __launch_bounds__(kGemvThreads, M <= 2 ? 5 : 1) void k_moe_gate_up_dual(GateUpArgs a, GateUpArgs b) {
     __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
     __shared__ uint32_t wg_max[4];
-    if (blockIdx.y + 1 < gridDim.y) gate_up_body<FA, M>(a, blockIdx.y, blockIdx.x, lds, wg_max);
-    else gate_up_body<FB, M>(b, 0, blockIdx.x, lds, wg_max);
+    // (the routed table's x comes digitised here: no staged routing)
+    if (blockIdx.y + 1 < gridDim.y)
+        gate_up_body<FA, M, false>(a, blockIdx.y, blockIdx.x, lds, wg_max);
+    else
+        gate_up_body<FB, M, false>(b, 0, blockIdx.x, lds, wg_max);
 }
 
 // --------------------------------------------------------------- down ---
