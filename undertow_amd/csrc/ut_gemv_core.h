@@ -111,6 +111,41 @@ __device__ __forceinline__ void digit_words(const float *v, int n, int32_t sh,
     constexpr uint32_t OFF = FMT == UT_FMT_INT4 ? 0x888888u : 0x808080u;
     constexpr uint32_t MASK = (1u << B) - 1;
     constexpr uint32_t FLIP = FMT == UT_FMT_INT4 ? 0x88888888u : 0x80808080u;
+    constexpr int KN = 32 / B;  // columns per full word
+    if (n == KN) {
+        // a full word: the planes are the transpose of the KN x KN matrix of
+        // B-bit fields (row j = u of column j, field p = digit p), built by
+        // swapping off-diagonal blocks of 1, 2 and 4 fields (int8: 1 and 2)
+        uint32_t u[KN];
+#pragma unroll
+        for (int j = 0; j < KN; j++) {
+            const int32_t q = sh == INT32_MIN ? 0 : (int32_t)rintf(ldexpf(v[j], sh));
+            u[j] = (uint32_t)q + OFF;
+        }
+        auto swap_blocks = [&](int i, int k, uint32_t m, int s) {
+            const uint32_t a = u[i], b = u[k];
+            u[i] = (a & m) | ((b << s) & ~m);
+            u[k] = ((a >> s) & m) | (b & ~m);
+        };
+        if constexpr (FMT == UT_FMT_INT4) {
+#pragma unroll
+            for (int i = 0; i < 8; i += 2) swap_blocks(i, i + 1, 0x0F0F0F0Fu, 4);
+            swap_blocks(0, 2, 0x00FF00FFu, 8);
+            swap_blocks(1, 3, 0x00FF00FFu, 8);
+            swap_blocks(4, 6, 0x00FF00FFu, 8);
+            swap_blocks(5, 7, 0x00FF00FFu, 8);
+#pragma unroll
+            for (int i = 0; i < 4; i++) swap_blocks(i, i + 4, 0x0000FFFFu, 16);
+        } else {
+            swap_blocks(0, 1, 0x00FF00FFu, 8);
+            swap_blocks(2, 3, 0x00FF00FFu, 8);
+            swap_blocks(0, 2, 0x0000FFFFu, 16);
+            swap_blocks(1, 3, 0x0000FFFFu, 16);
+        }
+#pragma unroll
+        for (int p = 0; p < PL; p++) w[p] = u[p] ^ FLIP;
+        return;
+    }
 #pragma unroll
     for (int p = 0; p < PL; p++) w[p] = 0;
 #pragma unroll
