@@ -117,10 +117,21 @@ __device__ __forceinline__ void digit_words(const float *v, int n, int32_t sh,
         // B-bit fields (row j = u of column j, field p = digit p), built by
         // swapping off-diagonal blocks of 1, 2 and 4 fields (int8: 1 and 2)
         uint32_t u[KN];
+        if (sh >= -126 && sh <= 127) {
+            // |x * 2^sh| <= 2^22, so x * 2^sh + 1.5 * 2^23 (one rounding, to
+            // nearest even) lies in [2^23, 2^24], where the ulp is 1: its
+            // bits are those of 1.5 * 2^23 plus rint(x * 2^sh)
+            const float scale = __uint_as_float((uint32_t)(sh + 127) << 23);
 #pragma unroll
-        for (int j = 0; j < KN; j++) {
-            const int32_t q = sh == INT32_MIN ? 0 : (int32_t)rintf(ldexpf(v[j], sh));
-            u[j] = (uint32_t)q + OFF;
+            for (int j = 0; j < KN; j++)
+                u[j] = __float_as_uint(__builtin_fmaf(v[j], scale, 12582912.0f)) +
+                       (OFF - 0x4B400000u);
+        } else {
+#pragma unroll
+            for (int j = 0; j < KN; j++) {
+                const int32_t q = sh == INT32_MIN ? 0 : (int32_t)rintf(ldexpf(v[j], sh));
+                u[j] = (uint32_t)q + OFF;
+            }
         }
         auto swap_blocks = [&](int i, int k, uint32_t m, int s) {
             const uint32_t a = u[i], b = u[k];
