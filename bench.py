@@ -453,6 +453,18 @@ def mtp_bench(U, ctx, cfg, prompt_len, new_tokens, depths, seed, expert_fmt, den
         assert toks == greedy, f"MTP depth {d} output differs from greedy"
         res[f"mtp{d}"] = {"tok_s": len(toks) / dt, "drafted": drafted, "accepted": accepted,
                           "acceptance": accepted / max(drafted, 1), "lossless": True}
+        # the same loop with its verify steps replayed from a captured graph
+        before = m.graph_stats()
+        m.enable_graphs(True)
+        t0 = time.perf_counter()
+        toks_g, _, _ = m.generate_mtp(prompt, new_tokens, depth=d)
+        dt = time.perf_counter() - t0 - t_prefill
+        m.enable_graphs(False)
+        after = m.graph_stats()
+        assert toks_g == greedy, f"MTP depth {d} graph replay output differs from greedy"
+        res[f"mtp{d}"]["graph"] = {"tok_s": len(toks_g) / dt,
+                                   "replays": after["replays"] - before["replays"],
+                                   "failures": after["failures"] - before["failures"]}
     del m
     return res
 

@@ -403,17 +403,19 @@ int64_t ut_session_position(const ut_session *s);
  * honours.  Empty until set. */
 int32_t ut_model_set_stop_ids(ut_model *m, const int32_t *ids, int64_t n);
 
-/* No reference counterpart (the reference runs on the CPU): one-row decode
- * steps of the greedy loop (ut_generate) replayed from a graph captured on
- * the context's stream, instead of about 40-60 kernel launches per token
- * from the host.  Every position-dependent kernel of the step reads the
- * session's position from device memory, attention grids are sized for the
+/* No reference counterpart (the reference runs on the CPU): the one-row
+ * decode steps of the greedy loop (ut_generate) and the verify steps of the
+ * MTP loop (ut_generate_mtp / ut_speculative_loop: depth + 1 rows) replayed
+ * from graphs captured on the context's stream, instead of about 40-60
+ * kernel launches per step from the host.  Every position-dependent kernel
+ * of a step reads the session's position from device memory (reset by one
+ * small launch after a rollback), attention grids are sized for the
  * session's capacity (workgroups past the context exit at once), and the
  * step advances the position itself.  Outputs are identical to the eager
- * launches.  A session captures on its second one-row step; if capturing
- * fails (or the graph would hold anything but kernel launches) the session
- * stays eager.  Not used with the expert tier or kernel timing on.  Off by
- * default. */
+ * launches.  A session captures on its second step of each shape; if
+ * capturing fails (or the graph would hold anything but kernel launches)
+ * the session stays eager.  Not used with the expert tier or kernel timing
+ * on.  Off by default. */
 int32_t ut_model_enable_graphs(ut_model *m, int32_t on);
 /* Counts since the model was made: graphs captured, steps replayed from
  * them, captures given up (each pointer may be NULL). */

@@ -147,6 +147,58 @@ def test_perfect_and_wrong_drafts_through_callback(c1, depth):
     assert got == greedy_sim(stream, depth, lambda r: r % (depth + 1), max_new)
 
 
+@pytest.mark.parametrize("depth", [1, 3])
+def test_verify_graph_replay_matches_eager(c1, ident, depth):
+    """The MTP verify step (depth + 1 rows fed from the device ids) replayed
+    from a captured graph, with the host's accept decision, rollbacks and
+    position resets between the replays: caller drafts (perfect, then wrong
+    at every position in turn) and native drafts on the identity module
+    (which accepts most of them) give the eager streams and counts."""
+    ck, m, om = c1
+    V = C1["vocab_size"]
+    prompt = prompt_ids(16, V)
+    stream = m.generate_greedy(prompt, 28)
+
+    def perfect(tokens, nxt, dep):
+        k = len(tokens) - len(prompt)
+        return stream[k + 1:k + 1 + dep]
+
+    def wrong_factory():
+        rounds = []
+
+        def draft(tokens, nxt, dep):
+            k = len(tokens) - len(prompt)
+            d = list(stream[k + 1:k + 1 + dep])
+            p = len(rounds) % (dep + 1)
+            rounds.append(p)
+            if p < dep:
+                d[p] = (d[p] + 1) % V
+            return d
+        return draft
+
+    ick, im, _ = ident
+    iprompt = prompt_ids(9, ick.spec.vocab_size, seed=4)
+    runs = [(m, lambda: m.speculative_loop(prompt, 24, depth=depth, draft_fn=perfect)),
+            (m, lambda: m.speculative_loop(prompt, 24, depth=depth, draft_fn=wrong_factory())),
+            (im, lambda: im.generate_mtp(iprompt, 20, depth=depth))]
+    eager = [f() for _, f in runs]
+    for mm, _ in runs:
+        mm.enable_graphs(True)
+    before = [mm.graph_stats() for mm, _ in runs]
+    try:
+        got = [f() for _, f in runs]
+    finally:
+        for mm, _ in runs:
+            mm.enable_graphs(False)
+    after = [mm.graph_stats() for mm, _ in runs]
+    assert got == eager
+    assert eager[2][2] > 0  # the identity module accepted native drafts
+    for b, a in zip(before, after):
+        assert a["failures"] == b["failures"]
+    assert after[0]["replays"] - before[0]["replays"] > 0
+    assert after[2]["replays"] - before[2]["replays"] > 0
+
+
 def test_stop_ids_and_on_token(c1):
     ck, m, om = c1
     prompt = prompt_ids(16, C1["vocab_size"])

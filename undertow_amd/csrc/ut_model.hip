@@ -135,6 +135,9 @@ struct ut_session {
     int64_t dpos_host = -1;
     hipGraphExec_t g1 = nullptr;
     int64_t m1_steps = 0;
+    // the MTP verify step (gv_rows rows fed from ws.vids), captured likewise
+    hipGraphExec_t gv = nullptr;
+    int64_t gv_rows = 0, v_steps = 0;
     bool graph_failed = false;
 };
 
@@ -379,6 +382,10 @@ int32_t ws_reserve(ut_session *s, int64_t rows) {
         w.base = nullptr;
     }
     // a captured step names the old workspace
+    if (s->gv) {
+        (void)hipGraphExecDestroy(s->gv);
+        s->gv = nullptr;
+    }
     if (s->g1) {
         (void)hipGraphExecDestroy(s->g1);
         s->g1 = nullptr;
@@ -1184,26 +1191,27 @@ struct Emit {
 // step's argmax on the device, and the next step is queued before the host
 // waits for the current token (a step queued past the stream's end is
 // discarded with the session).
-// Whether one-row decode steps of this session may run from a captured
-// graph: asked for, not given up on, every launch of the step on the device
-// (no expert tier: it reads the routing back each layer), no kernel timing
-// (its events), and one eager one-row step run first (host-side one-time
-// set-up, such as occupancy queries, happens there).
-bool graph_ok(const ut_session *s) {
+// Whether device-fed steps of this session may run from captured graphs:
+// asked for, not given up on, every launch of the step on the device (no
+// expert tier: it reads the routing back each layer), no kernel timing (its
+// events), and one eager step of the same shape run first (eager_steps:
+// host-side one-time set-up, such as occupancy queries and working-memory
+// growth, happens there).
+bool graph_ok(const ut_session *s, int64_t eager_steps) {
     const ut_model *m = s->m;
-    return m->graphs && !s->graph_failed && !m->store && !m->ctx->timing && s->m1_steps >= 1;
+    return m->graphs && !s->graph_failed && !m->store && !m->ctx->timing && eager_steps >= 1;
 }
 
-// Captures the one-row step fed from ws.am[0] into s->g1.  The capture pass
-// runs the host side of the step (so the session's positions advance as if
-// it ran); every position-dependent launch reads the device word s->dpos,
-// and attention grids are sized for the capacity.  The graph must hold
-// kernel launches only.  The null stream cannot be captured: then the
-// launches are captured on the context's own stream (capturing runs
-// nothing) and the graph is launched on the context's stream.  On failure
-// the host positions are restored and UT_ERR_STATE returned (the caller
-// runs the step eagerly).
-int32_t capture_step(ut_session *s) {
+// Captures the step of `rows` rows fed from the device ids at ids_dev (in
+// the workspace) into *exec.  The capture pass runs the host side of the
+// step (so the session's positions advance as if it ran); every
+// position-dependent launch reads the device word s->dpos, and attention
+// grids are sized for the capacity.  The graph must hold kernel launches
+// only.  The null stream cannot be captured: then the launches are captured
+// on the context's own stream (capturing runs nothing) and the graph is
+// launched on the context's stream.  On failure the host positions are
+// restored and UT_ERR_STATE returned (the caller runs the step eagerly).
+int32_t capture_rows(ut_session *s, int64_t rows, const int32_t *ids_dev, hipGraphExec_t *exec) {
     ut_model *m = s->m;
     ut_ctx *ctx = m->ctx;
     const hipStream_t run_stream = ctx->stream;
@@ -1219,8 +1227,8 @@ int32_t capture_step(ut_session *s) {
     if (hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal) != hipSuccess) {
         rc = UT_ERR_STATE;
     } else {
-        rc = prefill_dev(s, nullptr, 1, s->ws.am);
-        if (rc == UT_OK) rc = launch_pos_add(ctx, s->dpos, 1);
+        rc = prefill_dev(s, nullptr, rows, ids_dev);
+        if (rc == UT_OK) rc = launch_pos_add(ctx, s->dpos, rows);
         if (hipStreamEndCapture(ctx->stream, &graph) != hipSuccess) rc = UT_ERR_STATE;
     }
     ctx->step_pos = nullptr;
@@ -1237,8 +1245,8 @@ int32_t capture_step(ut_session *s) {
             if (hipGraphNodeGetType(nodes[i], &t) != hipSuccess || t != hipGraphNodeTypeKernel)
                 rc = UT_ERR_STATE;
         }
-        if (rc == UT_OK && hipGraphInstantiate(&s->g1, graph, nullptr, nullptr, 0) != hipSuccess) {
-            s->g1 = nullptr;
+        if (rc == UT_OK && hipGraphInstantiate(exec, graph, nullptr, nullptr, 0) != hipSuccess) {
+            *exec = nullptr;
             rc = UT_ERR_STATE;
         }
     } else if (rc == UT_OK) {
@@ -1254,18 +1262,21 @@ int32_t capture_step(ut_session *s) {
     return UT_OK;
 }
 
-// One device-fed decode step (its token in ws.am[0]): replayed from the
-// captured graph when the session allows it, else launched eagerly.
-int32_t decode_step(ut_session *s) {
+// One device-fed step of `rows` rows (ids at ids_dev): replayed from the
+// graph *g when the session allows it (captured on first use), else
+// launched eagerly.  eager_steps counts the steps of this shape.
+int32_t graph_step(ut_session *s, int64_t rows, const int32_t *ids_dev, hipGraphExec_t *g,
+                   int64_t *eager_steps) {
     ut_model *m = s->m;
     ut_ctx *ctx = m->ctx;
-    if (!graph_ok(s)) {
-        const int32_t rc = prefill_dev(s, nullptr, 1, s->ws.am);
-        if (rc == UT_OK) s->m1_steps++;
+    if (!graph_ok(s, *eager_steps)) {
+        const int32_t rc = prefill_dev(s, nullptr, rows, ids_dev);
+        if (rc == UT_OK) (*eager_steps)++;
         return rc;
     }
-    if (s->pos + 1 > s->cap) {
-        set_error(ctx, "context overflow: %lld + 1 > %lld", (long long)s->pos, (long long)s->cap);
+    if (s->pos + rows > s->cap) {
+        set_error(ctx, "context overflow: %lld + %lld > %lld", (long long)s->pos,
+                  (long long)rows, (long long)s->cap);
         return UT_ERR_CONTEXT_OVERFLOW;
     }
     // the device position word must hold this step's position
@@ -1273,23 +1284,37 @@ int32_t decode_step(ut_session *s) {
         UT_TRY(launch_pos_set(ctx, s->dpos, s->pos));
         s->dpos_host = s->pos;
     }
-    if (!s->g1) {
-        if (capture_step(s) != UT_OK) {
+    if (!*g) {
+        if (capture_rows(s, rows, ids_dev, g) != UT_OK) {
             s->graph_failed = true;
             m->graph_failures++;
-            return decode_step(s);
+            return graph_step(s, rows, ids_dev, g, eager_steps);
         }
         m->graph_captures++;
         // the capture pass advanced the host positions; now run the step
     } else {
-        s->pos += 1;
-        for (auto &kv : s->kv) kv.len += 1;
+        s->pos += rows;
+        for (auto &kv : s->kv) kv.len += rows;
     }
-    UT_CHECK_HIP(ctx, hipGraphLaunch(s->g1, ctx->stream));
+    UT_CHECK_HIP(ctx, hipGraphLaunch(*g, ctx->stream));
     m->graph_replays++;
-    s->dpos_host += 1;
-    s->m1_steps++;
+    s->dpos_host += rows;
+    (*eager_steps)++;
     return UT_OK;
+}
+
+// One device-fed decode step (its token in ws.am[0]).
+int32_t decode_step(ut_session *s) { return graph_step(s, 1, s->ws.am, &s->g1, &s->m1_steps); }
+
+// The MTP verify step: `rows` rows fed from ws.vids.
+int32_t verify_step(ut_session *s, int64_t rows) {
+    if (s->gv && s->gv_rows != rows) {
+        (void)hipGraphExecDestroy(s->gv);
+        s->gv = nullptr;
+        s->v_steps = 0;
+    }
+    s->gv_rows = rows;
+    return graph_step(s, rows, s->ws.vids, &s->gv, &s->v_steps);
 }
 
 int64_t gen_greedy(ut_model *m, const int32_t *prompt, int64_t n, Emit &em) {
@@ -1405,7 +1430,7 @@ int64_t gen_spec(ut_model *m, const int32_t *prompt, int64_t n, int32_t depth, u
         }
         nd += depth;
         // ---- verify [next, d1..dk] in one prefill, ids assembled on the device
-        rc = prefill_dev(s, nullptr, depth + 1, s->ws.vids);
+        rc = verify_step(s, depth + 1);
         if (rc == UT_ERR_CONTEXT_OVERFLOW) {
             // no room for the verify rows: end the stream cleanly (mtp.rs:283-289;
             // the draft stays counted, as stats.drafted was bumped before)
@@ -2022,6 +2047,7 @@ void ut_session_free(ut_session *s) {
     (void)hipSetDevice(s->m->device);
     (void)hipStreamSynchronize(s->m->ctx->stream);
     if (s->g1) (void)hipGraphExecDestroy(s->g1);
+    if (s->gv) (void)hipGraphExecDestroy(s->gv);
     if (s->ws.base) (void)hipFree(s->ws.base);
     if (s->kv_alloc) (void)hipFree(s->kv_alloc);
     if (s->pin) (void)hipHostFree(s->pin);

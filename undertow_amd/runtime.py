@@ -642,7 +642,8 @@ class Model:
                                                    a.size))
 
     def enable_graphs(self, on: bool = True) -> None:
-        """One-row greedy decode steps replayed from a captured graph."""
+        """Device-fed decode steps (one row) and MTP verify steps replayed
+        from graphs captured per session."""
         self.ctx.check(lib().ut_model_enable_graphs(self._h, int(on)))
 
     def graph_stats(self) -> dict:
