@@ -255,20 +255,26 @@ __device__ __forceinline__ void route_phase_keys(const float (&lv)[KPL], const f
     }
 }
 
-template <int KPL>
+// CLG > 0: the group's lane run known at compile time (CLG lanes, which the
+// caller checked); the same steps without the run-length switch.
+template <int KPL, int CLG = 0>
 __device__ __forceinline__ void route_phase_groups(uint64_t (&key)[KPL], int E, int n_group,
                                                    int topk_group) {
     const int lane = threadIdx.x & 63;
     if (n_group > 1 && topk_group < n_group) {
-        const int gs = E / n_group, LG = gs / KPL;
+        const int gs = E / n_group, LG = CLG > 0 ? CLG : gs / KPL;
         uint64_t b = key[0];
 #pragma unroll
         for (int j = 1; j < KPL; j++) b = key[j] > b ? key[j] : b;
-        const uint64_t m1 = run_max_key_rt(b, LG);
+        uint64_t m1;
+        if constexpr (CLG > 0) m1 = run_max_key<CLG>(b);
+        else m1 = run_max_key_rt(b, LG);
         uint64_t b2 = 0;
 #pragma unroll
         for (int j = 0; j < KPL; j++) b2 = key[j] != m1 && key[j] > b2 ? key[j] : b2;
-        const uint64_t m2 = run_max_key_rt(b2, LG);
+        uint64_t m2;
+        if constexpr (CLG > 0) m2 = run_max_key<CLG>(b2);
+        else m2 = run_max_key_rt(b2, LG);
         // group score = sum of the group's top-2 in topk order
         float gsum = 0.0f + order_value((uint32_t)(m1 >> 32));
         if (gs > 1) gsum = gsum + order_value((uint32_t)(m2 >> 32));
@@ -277,11 +283,20 @@ __device__ __forceinline__ void route_phase_groups(uint64_t (&key)[KPL], int E, 
         // group g2's key from its first lane (a wave-uniform lane: read
         // lanes, no LDS permutes)
         int rank = 0;
-        for (int g2 = 0; g2 < n_group; g2++) {
-            const int src = g2 * LG;
-            const uint32_t ohi = __builtin_amdgcn_readlane((uint32_t)(gk >> 32), src);
-            const uint32_t olo = __builtin_amdgcn_readlane((uint32_t)gk, src);
-            rank += (((uint64_t)ohi << 32) | olo) > gk;
+        if constexpr (CLG > 0) {
+#pragma unroll
+            for (int g2 = 0; g2 < 64 / CLG; g2++) {
+                const uint32_t ohi = __builtin_amdgcn_readlane((uint32_t)(gk >> 32), g2 * CLG);
+                const uint32_t olo = __builtin_amdgcn_readlane((uint32_t)gk, g2 * CLG);
+                rank += g2 < n_group && (((uint64_t)ohi << 32) | olo) > gk;
+            }
+        } else {
+            for (int g2 = 0; g2 < n_group; g2++) {
+                const int src = g2 * LG;
+                const uint32_t ohi = __builtin_amdgcn_readlane((uint32_t)(gk >> 32), src);
+                const uint32_t olo = __builtin_amdgcn_readlane((uint32_t)gk, src);
+                rank += (((uint64_t)ohi << 32) | olo) > gk;
+            }
         }
         if (rank >= topk_group) {
 #pragma unroll
@@ -778,7 +793,11 @@ __device__ __forceinline__ int gate_up_route_staged(const GateUpArgs &a, int u, 
     exl = sh == INT32_MIN ? INT32_MIN : -sh;
     // phase 2: group limitation and selections | digits
     if (wave == 0) {
-        route_phase_groups<4>(rkey, E, a.route_ng, a.route_tg);
+        // DeepSeek-V3's 8 groups of 32 experts: 8-lane runs at compile time
+        if (a.route_ng > 0 && E == 32 * a.route_ng)
+            route_phase_groups<4, 8>(rkey, E, a.route_ng, a.route_tg);
+        else
+            route_phase_groups<4>(rkey, E, a.route_ng, a.route_tg);
         int32_t rid = -1;
         float rw = 0.0f;
         route_phase_select<4>(rsc, rkey, E, a.plan_k, a.route_norm, a.route_scale, &rid, &rw);
