@@ -270,7 +270,7 @@ int32_t ut_mla_attend(ut_ctx *ctx, const float *qabs_dev, const float *q_rope_de
  * parts, x = hi + lo to about 2^-17 |x|; the bytes of the f32 cache).
  * ut_mla_cache_split converts T f32 positions into that form (kc_dev holds
  * T * 2 * (L+P) bf16, 16-byte aligned); ut_mla_attend_split then attends
- * without converting.  Shapes: H % 64 == 0, L == 512, P == 64 (DeepSeek-V3);
+ * without converting.  Shapes: H % 32 == 0, L == 512, P == 64 (DeepSeek-V3);
  * others return UT_ERR_SHAPE. */
 int32_t ut_mla_cache_split(ut_ctx *ctx, const float *latent_dev, const float *krot_dev, int64_t T,
                            int64_t L, int64_t P, void *kc_dev);

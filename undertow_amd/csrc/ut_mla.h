@@ -9,7 +9,7 @@ namespace ut {
 size_t mla_scratch_bytes(int64_t R, int64_t H, int64_t L, int64_t P, int64_t T);
 // The MFMA path over a cache kept in split form: per position the bf16 hi
 // parts of [latent | k_rot] then the lo parts (2 * (L + P) bf16, the bytes
-// of the f32 cache).  Taken for 64k heads, latent 512 and rope 64, up to a
+// of the f32 cache).  Taken for 32k heads, latent 512 and rope 64, up to a
 // context length T whose slice count fits the combine.
 bool mla_kc_ok(int64_t H, int64_t L, int64_t P, int64_t T);
 size_t mla_kc_scratch_bytes(int64_t R, int64_t H, int64_t L, int64_t T);

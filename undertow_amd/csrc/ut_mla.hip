@@ -144,7 +144,7 @@ __global__ __launch_bounds__(256) void k_mla_combine(const float *__restrict__ p
 }
 
 // ------------------------------------------------------ MFMA variant ---
-// For the DeepSeek-V3 shape (heads % 64 == 0, latent 512 + rope 64) the
+// For the DeepSeek-V3 shape (heads % 32 == 0, latent 512 + rope 64) the
 // score and context contractions run on the bf16 matrix cores.  Each f32
 // operand x is split into x_hi = bf16(x) and x_lo = bf16(x - x_hi), and a
 // product is taken as hi*hi + hi*lo + lo*hi (f32 accumulation), which keeps
@@ -153,35 +153,24 @@ __global__ __launch_bounds__(256) void k_mla_combine(const float *__restrict__ p
 // the lo plane of each position).
 //
 // Work split.  A column is one (query row r, head h) pair, c = r*H + h; a
-// workgroup (k_mla_mfma64: eight waves, one workgroup per CU) takes 64
-// columns of one query row and one slice of positions, 16 positions per
-// tile.  Each tile row is read from LDS as few times as the register budget
-// allows and each softmax weight is computed once, which roughly halves the
-// LDS traffic of a 32-column split; the loop is then bound by the latency of
-// its phases (two waves per SIMD, about 25% of the matrix pipe), not by the
-// throughput of one unit:
+// workgroup (k_mla_mfma16) takes 32 columns of one query row and one slice
+// of positions, 16 positions per tile:
 //   copy    the tile's 16 cache rows (36 KiB) go straight from global
 //           memory to LDS (global_load_lds), double-buffered: the next
 //           tile's copy is issued between this tile's score steps;
 //   scores  S^T[pos x col] = K[pos x (L+P)] . Q^T[(L+P) x col] with
-//           v_mfma_f32_16x16x32_bf16; wave w takes 32 columns (two 16-column
-//           blocks sharing each K read) over one dim quarter (5, 5, 4 and 4
-//           steps of 32 dims; queries held in registers), so the score dims
-//           are read twice per 64 columns; the quarters' partial scores go to
-//           LDS;
-//   softmax once per (column, position): thread t takes column t/8 and two
-//           of its positions, adds the quarters in order, and three DPP steps
-//           over its 8 lanes give the column's tile max and sum; the exponent
-//           offset moves only when a score exceeds it by more than
-//           kMlaHeadroom; the weights go to LDS as bf16 hi / lo planes, with
-//           each column's rescale factor (1 unless the offset moved);
+//           v_mfma_f32_16x16x32_bf16; wave w takes column block w&1 over
+//           dim half w>>1 (queries held in registers), the two halves are
+//           summed through LDS;
+//   softmax online, per column; the exponent offset moves only when a
+//           score exceeds it by more than kMlaHeadroom (so the context is
+//           rescaled on such jumps only);
 //   context O^T[L x col] += V^T[L x pos] . P[pos x col] with
-//           v_mfma_f32_32x32x16_bf16; wave w owns latent dims [64w, 64w + 64)
-//           of all 64 columns, so the latent part is read once per tile;
-//           V^T comes from the tile's rows by the transposing read
-//           (ds_read_b64_tr_b16: within each 16-lane group, lane j supplies 4
-//           consecutive dims of row 4q + j/4 and lane i receives dim i of the
-//           group's 4 rows).
+//           v_mfma_f32_32x32x16_bf16; wave w owns latent dims
+//           [128w, 128w + 128); V^T comes from the tile's rows in LDS by the
+//           transposing read (ds_read_b64_tr_b16: within each 16-lane group,
+//           lane j supplies 4 consecutive dims of row 4q + j/4 and lane i
+//           receives dim i of the group's 4 rows).
 // LDS has 64 banks (256 bytes per pass: 16 lanes of a 16-byte read, 32
 // lanes of an 8-byte read).  Every 2,304-byte row starts at bank 0, so a
 // row's 16-byte chunks are XOR-swizzled by mla_swz(r), a 4-bit permutation
@@ -190,16 +179,11 @@ __global__ __launch_bounds__(256) void k_mla_combine(const float *__restrict__ p
 // and the transposing read's 32 lanes (4 consecutive rows x 4 chunks of a
 // 4-aligned group) too, since rows 4k..4k+3 differ in the swizzle's high
 // two bits.  The score exchange rows are padded to 20 floats (80-byte
-// stride: 16 lanes at distinct 16-byte slots).  A weight plane is stored
-// per 8-position half as [half][column][8], the halves 1,152 bytes apart:
-// the 4-byte stores of a wave (8 columns x both halves) and the 16-byte
-// operand reads (16 consecutive columns of one half) both touch distinct
-// banks.
-// About 97 KiB of LDS and at most 256 registers per lane (two waves per
-// SIMD).  The slice writes (m, l, O) to the partial buffers,
-// k_mla_combine_mfma merges the slices.  The slice length depends only on
-// the row's context length, so a row's result is the same whichever rows
-// share the call.
+// stride: 16 lanes at distinct 16-byte slots).
+// 77 KiB of LDS and < 256 registers per lane let two workgroups share a CU.
+// The slice writes (m, l, O) to the partial buffers, k_mla_combine_mfma
+// merges the slices.  The slice length depends only on the row's context
+// length, so a row's result is the same whichever rows share the call.
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
@@ -235,7 +219,7 @@ struct MlaMfmaArgs {
     int H, L, P, RH;
     PosRef pos;
     float scale;
-    int groups, nslice;  // column groups of 64, slices in the grid
+    int groups, nslice;  // column groups of 32, slices in the grid
     float *part_m, *part_l, *part_o;  // [j][col], [j][col], [j][L][col]
 };
 
@@ -255,91 +239,68 @@ __device__ __forceinline__ bf16x8_t tr_pair(const uint8_t *lds_a, const uint8_t 
     return __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
+// Lanes l and l ^ 32 combined without an LDS round trip: permlane32_swap
+// of (v, v) returns the low halves of both operands in one register and the
+// high halves in the other, so max / sum of the two is the pair's result in
+// every lane (and the same sum order in both lanes).
+__device__ __forceinline__ float pair_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __fadd_rn(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 constexpr int kTile16 = 16;
 constexpr int kTile16Bytes = kTile16 * kRowChunks * 16;  // 36864
-constexpr int kMlaCols = 64;     // columns per workgroup
-constexpr int kPHalf = 1152;     // bytes per 8-position half of a weight plane (1 KiB + 128)
 
-// v over the 8-lane group of its lane (lanes 8k..8k+7): quad xor 1, quad
-// xor 2, then the half-row mirror; every lane of the group ends with the
-// same bits (op is commutative).
-template <int CTRL>
-__device__ __forceinline__ float dpp_f32(float v) {
-    return __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(
-        0, (int)__float_as_uint(v), CTRL, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float group8_max(float v) {
-    v = fmaxf(v, dpp_f32<0xB1>(v));
-    v = fmaxf(v, dpp_f32<0x4E>(v));
-    return fmaxf(v, dpp_f32<0x141>(v));
-}
-__device__ __forceinline__ float group8_sum(float v) {
-    v = __fadd_rn(v, dpp_f32<0xB1>(v));
-    v = __fadd_rn(v, dpp_f32<0x4E>(v));
-    return __fadd_rn(v, dpp_f32<0x141>(v));
-}
-
-__global__ __launch_bounds__(512, 1) void k_mla_mfma64(MlaMfmaArgs a) {
-    constexpr int NKS = 5, D = 576;
+__global__ __launch_bounds__(256, 2) void k_mla_mfma16(MlaMfmaArgs a) {
+    constexpr int KS = 9, MT = 4, D = 576;
+    typedef __bf16 bf16x8l_t __attribute__((ext_vector_type(8)));
     typedef float f32x4l_t __attribute__((ext_vector_type(4)));
     __shared__ __attribute__((aligned(16))) uint8_t sT0[kTile16Bytes];
     __shared__ __attribute__((aligned(16))) uint8_t sT1[kTile16Bytes];
-    // partial scores [dim quarter][column][position], rows padded to 20 floats
-    __shared__ __attribute__((aligned(16))) float sS[4][kMlaCols][kTile16 + 4];
-    // weights [hi | lo][position half][column][8 positions] as bf16
-    __shared__ __attribute__((aligned(16))) uint8_t sP[2][2][kPHalf];
-    __shared__ float sA[kMlaCols];  // each column's rescale factor for this tile
+    // [dim half][column][position], rows padded to 20 floats
+    __shared__ __attribute__((aligned(16))) float sS[2][32][kTile16 + 4];
     const int b = blockIdx.x, x8 = b & 7, q = b >> 3;
     const int group = q % a.groups;
     const int slice = (q / a.groups) * 8 + x8;
-    const int c0 = group * kMlaCols;
+    const int c0 = group * 32;
     const int r = c0 / a.H;
     const int64_t n_ctx = a.pos.get() + r + 1;
     const int64_t slen = mla_mfma_slice(n_ctx);
     const int64_t p0 = (int64_t)slice * slen;
     if (slice >= a.nslice || p0 >= n_ctx) return;  // uniform per workgroup
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+    const int cb = w & 1, dh = w >> 1;
     const int L = a.L, P = a.P;
-    // score role: dim quarter dq (32-dim steps ks0 .. ks0 + nks - 1) of the
-    // columns 32*ch + [0, 32), lanes as the 16x16x32 operands: column
-    // 16*bk + (l & 15), dims 32*step + 8*(l >> 4) + [0, 8)
-    const int dq = w >> 1, ch = w & 1;
-    const int nks = dq < 2 ? 5 : 4, ks0 = dq < 2 ? 5 * dq : 10 + 4 * (dq - 2);
-    bf16x8_t qh[NKS][2], ql[NKS][2];
+    // score operand lanes: column 16*cb + (l & 15), dims 288*dh + 32*ks + 8*(l >> 4)
+    const int qcol = c0 + 16 * cb + (l & 15);
+    const int qd0 = 288 * dh + 8 * (l >> 4);
+    bf16x8l_t qh[KS], ql[KS];
 #pragma unroll
-    for (int ks = 0; ks < NKS; ks++)
+    for (int ks = 0; ks < KS; ks++) {
+        const int d0 = qd0 + 32 * ks;
+        float v[8];
+        load8(d0 < L ? a.qabs + (int64_t)qcol * L + d0 : a.qrope + (int64_t)qcol * P + (d0 - L), v);
+        split8(v, qh[ks], ql[ks]);
+    }
+    // context lanes: column l & 31, positions 8*(l >> 5) + [0, 8)
+    const int n = l & 31, kh = l >> 5;
+    const int col = c0 + n;
+    f32x16_t o[MT];
 #pragma unroll
-        for (int bk = 0; bk < 2; bk++) {
-            float v[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-            if (ks < nks) {
-                const int qcol = c0 + 32 * ch + 16 * bk + (l & 15);
-                const int d0 = 32 * (ks0 + ks) + 8 * (l >> 4);
-                load8(d0 < L ? a.qabs + (int64_t)qcol * L + d0
-                             : a.qrope + (int64_t)qcol * P + (d0 - L), v);
-            }
-            split8(v, qh[ks][bk], ql[ks][bk]);
-        }
-    // softmax role: column sc, positions sp and sp + 1 of each tile
-    const int sc = tid >> 3, sp = 2 * (tid & 7);
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) o[mt][i] = 0.0f;
     float m_run = -INFINITY, l_run = 0.0f;
-    // context role: latent dims 64w + 32*db + [0, 32) of the columns
-    // 32*cb + (l & 31); weights k = positions 8*kh + [0, 8)
-    const int kh = l >> 5;
-    f32x16_t o[2][2];
-#pragma unroll
-    for (int db = 0; db < 2; db++)
-#pragma unroll
-        for (int cb = 0; cb < 2; cb++)
-#pragma unroll
-            for (int i = 0; i < 16; i++) o[db][cb][i] = 0.0f;
     const int64_t tend = p0 + slen < n_ctx ? p0 + slen : n_ctx;
     const uint32_t last = (uint32_t)(n_ctx - 1);
 
-    // a tile is 36 runs of 64 16-byte slots (1 KiB); wave w copies runs
-    // cp0 .. cp0 + nks - 1 (five each for waves 0-3, four each for 4-7)
-    const int cp0 = w < 4 ? 5 * w : 20 + 4 * (w - 4);
+    // wave w copies slots [w*9*64, (w+1)*9*64) of a tile (part i: one 1 KiB run)
     auto copy_part = [&](uint32_t t0, uint8_t *dst, int i) {
-        const int s0 = (cp0 + i) * 64, sl = s0 + l;
+        const int s0 = (w * 9 + i) * 64, sl = s0 + l;
         const int rr = sl / kRowChunks, phy = sl - rr * kRowChunks;
         const int c = phy ^ mla_swz(rr);
         const uint32_t pos = t0 + rr <= last ? t0 + rr : last;
@@ -349,114 +310,87 @@ __global__ __launch_bounds__(512, 1) void k_mla_mfma64(MlaMfmaArgs a) {
                                          16, 0, 0);
     };
 #pragma unroll
-    for (int i = 0; i < NKS; i++)
-        if (i < nks) copy_part((uint32_t)p0, sT0, i);
+    for (int i = 0; i < 9; i++) copy_part((uint32_t)p0, sT0, i);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
 
     auto tile = [&](const uint8_t *T, uint8_t *Nx, int64_t t0) {
         const bool more = t0 + kTile16 < tend;
         const uint32_t tn = (uint32_t)(t0 + kTile16);
-        // ---- partial scores: 16 positions x 32 columns over this wave's dim
-        // quarter; six independent accumulator chains (hi*hi, hi*lo, lo*hi
-        // per column block) keep the matrix pipe busy
-        f32x4l_t sa[2], sb[2], sd[2];
+        // ---- partial scores: 16 positions x this wave's 16 columns, its dim half
+        // three independent accumulator chains (hi*hi, hi*lo, lo*hi), summed
+        // at the end, keep the matrix pipe busy
+        f32x4l_t sa = {0.0f, 0.0f, 0.0f, 0.0f}, sb = sa, sd = sa;
 #pragma unroll
-        for (int bk = 0; bk < 2; bk++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) sa[bk][i] = sb[bk][i] = sd[bk][i] = 0.0f;
-#pragma unroll
-        for (int ks = 0; ks < NKS; ks++) {
-            if (ks < nks) {
-                if (more) copy_part(tn, Nx, ks);
-                const int cc = 4 * (ks0 + ks) + (l >> 4);
-                const bf16x8_t kh8 = *(const bf16x8_t *)(T + mla_slot(l & 15, cc) * 16);
-                const bf16x8_t kl8 = *(const bf16x8_t *)(T + mla_slot(l & 15, 72 + cc) * 16);
-#pragma unroll
-                for (int bk = 0; bk < 2; bk++) {
-                    sa[bk] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh8, qh[ks][bk], sa[bk], 0, 0, 0);
-                    sb[bk] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh8, ql[ks][bk], sb[bk], 0, 0, 0);
-                    sd[bk] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl8, qh[ks][bk], sd[bk], 0, 0, 0);
-                }
-            }
+        for (int ks = 0; ks < KS; ks++) {
+            if (more) copy_part(tn, Nx, ks);
+            const int ch = 36 * dh + 4 * ks + (l >> 4);
+            const bf16x8l_t kh8 = *(const bf16x8l_t *)(T + mla_slot(l & 15, ch) * 16);
+            const bf16x8l_t kl8 = *(const bf16x8l_t *)(T + mla_slot(l & 15, 72 + ch) * 16);
+            sa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh8, qh[ks], sa, 0, 0, 0);
+            sb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh8, ql[ks], sb, 0, 0, 0);
+            sd = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl8, qh[ks], sd, 0, 0, 0);
         }
+        f32x4l_t sc;
+#pragma unroll
+        for (int i = 0; i < 4; i++) sc[i] = __fadd_rn(sa[i], __fadd_rn(sb[i], sd[i]));
         // C layout: register i holds position 4*(l >> 4) + i, column l & 15
-#pragma unroll
-        for (int bk = 0; bk < 2; bk++) {
-            f32x4l_t s4;
-#pragma unroll
-            for (int i = 0; i < 4; i++) s4[i] = __fadd_rn(sa[bk][i], __fadd_rn(sb[bk][i], sd[bk][i]));
-            *(f32x4l_t *)&sS[dq][32 * ch + 16 * bk + (l & 15)][4 * (l >> 4)] = s4;
-        }
-        // LDS-only barriers (the fence of __syncthreads would also wait for
-        // the next tile's copy)
+        *(f32x4l_t *)&sS[dh][16 * cb + (l & 15)][4 * (l >> 4)] = sc;
+        // an LDS-only barrier (the fence of __syncthreads would also wait
+        // for the next tile's copy)
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        // ---- softmax of column sc at positions sp, sp + 1: quarters in order
+        // ---- this lane's 8 positions of column n, dim halves summed in order
+        const f32x4l_t a0 = *(const f32x4l_t *)&sS[0][n][8 * kh];
+        const f32x4l_t a1 = *(const f32x4l_t *)&sS[0][n][8 * kh + 4];
+        const f32x4l_t b0 = *(const f32x4l_t *)&sS[1][n][8 * kh];
+        const f32x4l_t b1 = *(const f32x4l_t *)&sS[1][n][8 * kh + 4];
         const int live = n_ctx - t0 < kTile16 ? (int)(n_ctx - t0) : kTile16;
-        float p[2];
-        {
-            const float2 q0 = *(const float2 *)&sS[0][sc][sp], q1 = *(const float2 *)&sS[1][sc][sp];
-            const float2 q2 = *(const float2 *)&sS[2][sc][sp], q3 = *(const float2 *)&sS[3][sc][sp];
-            const float v0 = __fadd_rn(__fadd_rn(__fadd_rn(q0.x, q1.x), q2.x), q3.x);
-            const float v1 = __fadd_rn(__fadd_rn(__fadd_rn(q0.y, q1.y), q2.y), q3.y);
-            p[0] = __fadd_rn(__fmul_rn(v0, a.scale), sp < live ? 0.0f : -INFINITY);
-            p[1] = __fadd_rn(__fmul_rn(v1, a.scale), sp + 1 < live ? 0.0f : -INFINITY);
+        float p[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float v = __fadd_rn(e < 4 ? a0[e] : a1[e - 4], e < 4 ? b0[e] : b1[e - 4]);
+            p[e] = __fadd_rn(__fmul_rn(v, a.scale), 8 * kh + e < live ? 0.0f : -INFINITY);
         }
-        const float mt_ = group8_max(fmaxf(p[0], p[1]));
+        float mt_ = p[0];
+#pragma unroll
+        for (int e = 1; e < 8; e++) mt_ = fmaxf(mt_, p[e]);
+        mt_ = pair_max(mt_);
         // the exponent offset moves only on a jump of more than kMlaHeadroom
         const bool jump = mt_ > m_run + kMlaHeadroom;
         const float m_new = jump ? mt_ : m_run;
-        const float alpha = jump ? __expf(m_run - m_new) : 1.0f;
-        l_run *= alpha;
-        p[0] = __expf(p[0] - m_new);
-        p[1] = __expf(p[1] - m_new);
-        l_run = __fadd_rn(l_run, group8_sum(__fadd_rn(p[0], p[1])));
+        if (__any(jump)) {
+            const float alpha = __expf(m_run - m_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) o[mt][i] *= alpha;
+        }
+        float ls = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            p[e] = __expf(p[e] - m_new);
+            ls += p[e];
+        }
+        ls = pair_sum(ls);
+        l_run += ls;
         m_run = m_new;
-        {
-            const __bf16 h0 = (__bf16)p[0], h1 = (__bf16)p[1];
-            const __bf16 e0 = (__bf16)__fsub_rn(p[0], (float)h0);
-            const __bf16 e1 = (__bf16)__fsub_rn(p[1], (float)h1);
-            const int off = (sp >> 3) * kPHalf + sc * 16 + 2 * (sp & 7);
-            *(uint32_t *)(sP[0][0] + off) = (uint32_t)__builtin_bit_cast(uint16_t, h0) |
-                                            ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-            *(uint32_t *)(sP[1][0] + off) = (uint32_t)__builtin_bit_cast(uint16_t, e0) |
-                                            ((uint32_t)__builtin_bit_cast(uint16_t, e1) << 16);
-        }
-        if ((tid & 7) == 0) sA[sc] = alpha;
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        // ---- context over this wave's 64 latent dims (k = the 16 positions)
-        const float a0 = sA[l & 31], a1 = sA[32 + (l & 31)];
-        if (__any(a0 != 1.0f || a1 != 1.0f)) {
-#pragma unroll
-            for (int db = 0; db < 2; db++)
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    o[db][0][i] *= a0;
-                    o[db][1][i] *= a1;
-                }
-        }
-        bf16x8_t ph[2], pl[2];
-#pragma unroll
-        for (int cb = 0; cb < 2; cb++) {
-            ph[cb] = *(const bf16x8_t *)(sP[0][kh] + (32 * cb + (l & 31)) * 16);
-            pl[cb] = *(const bf16x8_t *)(sP[1][kh] + (32 * cb + (l & 31)) * 16);
-        }
+        bf16x8_t ph, pl;
+        split8(p, ph, pl);
+        // ---- context over this wave's 128 latent dims (k = the 16 positions)
         const int g = l >> 4, j = l & 15;
 #pragma unroll
-        for (int db = 0; db < 2; db++) {
-            const int d0 = 64 * w + 32 * db + 16 * (g & 1);
+        for (int mt = 0; mt < MT; mt++) {
+            const int d0 = 128 * w + 32 * mt + 16 * (g & 1);
             const int chunk = (d0 >> 3) + ((j & 3) >> 1), boff = 8 * (j & 1);
             const int ra = 8 * kh + (j >> 2), rb = ra + 4;
             const bf16x8_t vh = tr_pair(T + mla_slot(ra, chunk) * 16 + boff,
                                         T + mla_slot(rb, chunk) * 16 + boff);
             const bf16x8_t vl = tr_pair(T + mla_slot(ra, 72 + chunk) * 16 + boff,
                                         T + mla_slot(rb, 72 + chunk) * 16 + boff);
-#pragma unroll
-            for (int cb = 0; cb < 2; cb++) {
-                o[db][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh, ph[cb], o[db][cb], 0, 0, 0);
-                o[db][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh, pl[cb], o[db][cb], 0, 0, 0);
-                o[db][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vl, ph[cb], o[db][cb], 0, 0, 0);
-            }
+            o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh, ph, o[mt], 0, 0, 0);
+            o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh, pl, o[mt], 0, 0, 0);
+            o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vl, ph, o[mt], 0, 0, 0);
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
@@ -465,22 +399,18 @@ __global__ __launch_bounds__(512, 1) void k_mla_mfma64(MlaMfmaArgs a) {
         tile(sT0, sT1, t0);
         if (t0 + kTile16 < tend) tile(sT1, sT0, t0 + kTile16);
     }
-    // ---- slice partials: O^T register i of block (db, cb) is dim
-    // 64w + 32*db + (i/4)*8 + kh*4 + i%4 of column 32*cb + (l & 31)
+    // ---- slice partials: O^T register i is dim 128*w + 32*mt + (i/4)*8 + kh*4 + i%4
     const int64_t RH = a.RH;
-    if ((tid & 7) == 0) {
-        a.part_m[(int64_t)slice * RH + c0 + sc] = m_run;
-        a.part_l[(int64_t)slice * RH + c0 + sc] = l_run;
+    if (w == 0 && kh == 0) {
+        a.part_m[(int64_t)slice * RH + col] = m_run;
+        a.part_l[(int64_t)slice * RH + col] = l_run;
     }
+    float *po = a.part_o + ((int64_t)slice * L + 128 * w + kh * 4) * RH + col;
 #pragma unroll
-    for (int db = 0; db < 2; db++)
+    for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-        for (int cb = 0; cb < 2; cb++) {
-            float *po = a.part_o + ((int64_t)slice * L + 64 * w + 32 * db + kh * 4) * RH + c0 +
-                        32 * cb + (l & 31);
-#pragma unroll
-            for (int i = 0; i < 16; i++) po[(int64_t)((i >> 2) * 8 + (i & 3)) * RH] = o[db][cb][i];
-        }
+        for (int i = 0; i < 16; i++)
+            po[(int64_t)(32 * mt + (i >> 2) * 8 + (i & 3)) * RH] = o[mt][i];
 }
 
 // The cache in the MFMA kernel's form: per position the bf16 hi parts of
@@ -618,7 +548,7 @@ static int64_t mla_mfma_nslice(int64_t T) {
 
 static bool mla_mfma_ok(int64_t H, int64_t L, int64_t P, int64_t T) {
     // instantiated for the DeepSeek-V3 MLA shape: latent 512 + rope 64
-    return H % kMlaCols == 0 && L == 512 && P == 64 && mla_mfma_nslice(T) <= kMlaMaxSlices;
+    return H % 32 == 0 && L == 512 && P == 64 && mla_mfma_nslice(T) <= kMlaMaxSlices;
 }
 
 bool mla_kc_ok(int64_t H, int64_t L, int64_t P, int64_t T) { return mla_mfma_ok(H, L, P, T); }
@@ -662,7 +592,7 @@ int32_t launch_mla_attend_kc(ut_ctx *ctx, const float *qabs, const float *qrope,
                              float scale, float *clat, void *scratch) {
     const int64_t T = pos_extent(ctx, pos_base + R);
     if (!mla_mfma_ok(H, L, P, T) || ((uintptr_t)kc & 15) != 0) {
-        set_error(ctx, "mla: split-cache attention needs 64k heads, latent 512 + rope 64, a "
+        set_error(ctx, "mla: split-cache attention needs 32k heads, latent 512 + rope 64, a "
                        "16-byte aligned cache and at most %d slices", kMlaMaxSlices);
         return UT_ERR_SHAPE;
     }
@@ -672,16 +602,15 @@ int32_t launch_mla_attend_kc(ut_ctx *ctx, const float *qabs, const float *qrope,
     a.H = (int)H; a.L = (int)L; a.P = (int)P; a.RH = (int)RH;
     a.pos = pos_ref(ctx, pos_base);
     a.scale = scale;
-    a.groups = (int)(RH / kMlaCols);  // 64 columns (of one query row) per workgroup
+    a.groups = (int)(RH / 32);
     a.nslice = (int)ns;
     a.part_m = (float *)scratch;
     a.part_l = (float *)((char *)scratch + ((ns * RH * 4 + 255) & ~int64_t(255)));
     a.part_o = (float *)((char *)a.part_l + ((ns * RH * 4 + 255) & ~int64_t(255)));
-    // workgroups b and b + 8 (same XCD) share a slice: its cache rows are
-    // read from HBM once per XCD
+    a.groups = (int)(RH / 32);  // 32 columns per workgroup
     const int64_t nwg = (int64_t)a.groups * ((ns + 7) / 8 * 8);
     int tok = timing_begin(ctx, "mla_mfma");
-    hipLaunchKernelGGL(k_mla_mfma64, dim3((unsigned)nwg), dim3(512), 0, ctx->stream, a);
+    hipLaunchKernelGGL(k_mla_mfma16, dim3((unsigned)nwg), dim3(256), 0, ctx->stream, a);
     timing_end(ctx, tok);
     UT_TRY(launch_check(ctx, "k_mla_mfma"));
     tok = timing_begin(ctx, "mla_combine");
