@@ -178,6 +178,28 @@ def test_moe_experts_many_choices(ctx, M):
         assert np.array_equal(one[0], got[s_])
 
 
+@pytest.mark.parametrize("E,ids", [(4, [2, 2, 0, 3, 0, 1]), (8, [5, 5, 1, 5]), (8, [6, 1, 4, 2])])
+def test_moe_one_row_repeated_ids(ctx, E, ids):
+    """Repeated expert ids in one row, and more choices than experts: the
+    plan gives such choices a shared slot, each choice still adds its own
+    weight times that slot's row in choice order.  The row equals the
+    oracle's and, bit for bit, the same row inside a two-row call."""
+    rng = np.random.default_rng(len(ids) * 10 + E)
+    H, I = 256, 128
+    tbl, host_w = make_experts(ctx, rng, INT4, E, H, I)
+    k = len(ids)
+    idm = np.array([ids], np.int32)
+    w = rng.random((1, k)).astype(np.float32)
+    x = rng.standard_normal((1, H)).astype(np.float32)
+    got = host(tbl.moe_experts(dev(idm), dev(w), dev(x)))
+    want = oracle_moe(INT4, H, I, host_w, idm, w, x)
+    tol = 1e-4 * np.maximum(np.abs(want), 1.0)
+    assert (np.abs(got - want) <= tol).all(), np.abs(got - want).max()
+    two = host(tbl.moe_experts(dev(np.repeat(idm, 2, 0)), dev(np.repeat(w, 2, 0)),
+                               dev(np.repeat(x, 2, 0))))
+    assert np.array_equal(two[0], got[0]) and np.array_equal(two[1], got[0])
+
+
 def test_moe_experts_f32_weights(ctx):
     import undertow_amd as U
     rng = np.random.default_rng(9)
