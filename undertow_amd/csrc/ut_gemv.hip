@@ -777,12 +777,13 @@ static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrow
     // 25.3 us and its split sum from 12.0 to 10.2 us)
     const int64_t resident = gemv_resident<FMT>(ctx, mrows) / (a.xmax ? 2 : 1);
     splitk_plan(FMT, a.O, w->in_dim, rows_per_wg, resident, &a.ks, &a.kslice);
-    if (FMT != UT_FMT_F32 && a.ks > 1) {
-        // a split launch takes enough splits for its K slice to be staged in
+    if (FMT != UT_FMT_F32) {
+        // every launch takes enough splits for its K slice to be staged in
         // one chunk at its row count: a second chunk drains the weight stream
         // behind a staging round (o_proj at DeepSeek-V3 width, two rows: 2
         // splits of 8,192 columns against 4 of 4,096 took the GEMV from 37.3
-        // to 26.7 us for 1.9 us more in its split sum)
+        // to 26.7 us for 1.9 us more in its split sum; at four rows the
+        // occupancy rule alone left it unsplit, eight 2,048-column chunks)
         const int64_t kc = mrows == 1   ? gemv_chunk_cols<FMT, 1>()
                            : mrows == 2 ? gemv_chunk_cols<FMT, 2>()
                            : mrows == 3 ? gemv_chunk_cols<FMT, 3>()

@@ -154,8 +154,8 @@ int32_t device_error_flag(ut_ctx *ctx, int32_t **flag);
 // (hipGetSymbolAddress, the device current) into ctx->noalloc_scratch.
 int32_t moe_noalloc_scratch_init(ut_ctx *ctx);
 // Split-K partials buffer of the context (kSplitKPartBytes), allocated on
-// first use.
-constexpr int64_t kSplitKPartBytes = int64_t(8) << 20;
+// first use: four rows of the LM head's logits (129,280) over four splits.
+constexpr int64_t kSplitKPartBytes = int64_t(32) << 20;
 int32_t splitk_buffer(ut_ctx *ctx, int64_t **part);
 int32_t check_device_error(ut_ctx *ctx);
 
