@@ -991,11 +991,9 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up(GateUpArgs a) {
 template <int M> constexpr int gate_up_mfma_kc() { return M == 2 ? 4096 : 2048; }
 
 template <int M>
-__global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up_mfma(GateUpArgs a) {
+__device__ __forceinline__ void gate_up_mfma_body(const GateUpArgs &a, int u, int tile,
+                                                  uint32_t *lds, uint32_t *wg_max) {
     constexpr int KC = gate_up_mfma_kc<M>();
-    __shared__ __attribute__((aligned(16))) uint32_t lds[mfma_lds_words<M, KC>()];
-    __shared__ uint32_t wg_max[4];
-    const int u = blockIdx.y, tile = blockIdx.x;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
     const int cnt = *a.count;
     const uint8_t *gw = (const uint8_t *)a.sp[u * 6 + kSpGate];
@@ -1040,6 +1038,30 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up_mfma(GateUpArgs a)
     if (tid < 2 * M) {
         const int mm = tid >> 1, part = 2 * tile + (tid & 1);
         if (part < a.ntiles) a.hmax_parts[((int64_t)u * M + mm) * a.ntiles + part] = wg_max[mm];
+    }
+}
+
+template <int M>
+__global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up_mfma(GateUpArgs a) {
+    __shared__ __attribute__((aligned(16))) uint32_t lds[mfma_lds_words<M, gate_up_mfma_kc<M>()>()];
+    __shared__ uint32_t wg_max[4];
+    gate_up_mfma_body<M>(a, blockIdx.y, blockIdx.x, lds, wg_max);
+}
+
+// The routed experts on the matrix cores (slots 0..gridDim.y-2, 32-row
+// tiles) and a shared MLP of format FB (the last grid row, the plain
+// kernel's 16-row tiles) in one launch, so the shared MLP's few workgroups
+// run beside the routed ones instead of after them.
+constexpr int cmax_words(int p, int q) { return p > q ? p : q; }
+template <int M, int FB>
+__global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up_mfma_dual(GateUpArgs a, GateUpArgs b) {
+    __shared__ __attribute__((aligned(16)))
+    uint32_t lds[cmax_words(mfma_lds_words<M, gate_up_mfma_kc<M>()>(), kLdsWords)];
+    __shared__ uint32_t wg_max[4];
+    if (blockIdx.y + 1 < gridDim.y) {
+        if ((int64_t)blockIdx.x * 32 < a.I) gate_up_mfma_body<M>(a, blockIdx.y, blockIdx.x, lds, wg_max);
+    } else {
+        gate_up_body<FB, M, false>(b, 0, blockIdx.x, lds, wg_max);
     }
 }
 
@@ -1483,18 +1505,20 @@ static void launch_gate_up(ut_ctx *ctx, const GateUpArgs &a, int64_t slots, cons
                            int fb) {
     if constexpr (FA == UT_FMT_INT4 && M >= 2 && M <= 4) {
         if (a.mfma_xf) {
-            hipLaunchKernelGGL((k_moe_gate_up_mfma<M>),
-                               dim3((unsigned)((a.I + 31) / 32), (unsigned)slots),
-                               dim3(kGemvThreads), 0, ctx->stream, a);
-            // a shared MLP beside it: its own launch
-            if (b) {
-                if (fb == UT_FMT_INT4)
-                    hipLaunchKernelGGL((k_moe_gate_up<UT_FMT_INT4, M>), dim3((unsigned)b->ntiles, 1u),
-                                       dim3(kGemvThreads), 0, ctx->stream, *b);
-                else
-                    hipLaunchKernelGGL((k_moe_gate_up<UT_FMT_INT8, M>), dim3((unsigned)b->ntiles, 1u),
-                                       dim3(kGemvThreads), 0, ctx->stream, *b);
+            const unsigned gx = (unsigned)((a.I + 31) / 32);
+            if (!b) {
+                hipLaunchKernelGGL((k_moe_gate_up_mfma<M>), dim3(gx, (unsigned)slots),
+                                   dim3(kGemvThreads), 0, ctx->stream, a);
+                return;
             }
+            // a shared MLP beside it: the last grid row
+            const dim3 grid(gx > (unsigned)b->ntiles ? gx : (unsigned)b->ntiles, (unsigned)(slots + 1));
+            if (fb == UT_FMT_INT4)
+                hipLaunchKernelGGL((k_moe_gate_up_mfma_dual<M, UT_FMT_INT4>), grid,
+                                   dim3(kGemvThreads), 0, ctx->stream, a, *b);
+            else
+                hipLaunchKernelGGL((k_moe_gate_up_mfma_dual<M, UT_FMT_INT8>), grid,
+                                   dim3(kGemvThreads), 0, ctx->stream, a, *b);
             return;
         }
     }
