@@ -1231,16 +1231,14 @@ inline bool down_mfma_ok(int fmt, int M, int64_t I, int ks) {
 }
 
 template <int M>
-__global__ __launch_bounds__(kGemvThreads) void k_moe_down_mfma(DownArgs a) {
-    __shared__ __attribute__((aligned(16))) uint32_t lds[mfma_lds_words<M, kDownMfmaKC>()];
-    __shared__ uint32_t red[4 * M];
-    const int u = blockIdx.y;
+__device__ __forceinline__ void down_mfma_body(const DownArgs &a, int u, int tile, uint32_t *lds,
+                                               uint32_t *red) {
     if (u >= *a.count) return;
     const uint8_t *dw = (const uint8_t *)a.sp[u * 6 + kSpDown];
     const float *dsc = (const float *)a.sp[u * 6 + kSpDownS];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
     constexpr int TW = down_mfma_tw<M>();
-    const int64_t wrow0 = (int64_t)blockIdx.x * (64 * TW) + wave * (16 * TW);
+    const int64_t wrow0 = (int64_t)tile * (64 * TW) + wave * (16 * TW);
     const uint8_t *arow[TW];
 #pragma unroll
     for (int w = 0; w < TW; w++) {
@@ -1273,6 +1271,28 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_down_mfma(DownArgs a) {
                     a.d[((int64_t)u * M + m) * a.H + o] =
                         core_value<UT_FMT_INT4, M, 4>(res[w], r, m, exl, dsc, o);
             }
+}
+
+template <int M>
+__global__ __launch_bounds__(kGemvThreads) void k_moe_down_mfma(DownArgs a) {
+    __shared__ __attribute__((aligned(16))) uint32_t lds[mfma_lds_words<M, kDownMfmaKC>()];
+    __shared__ uint32_t red[4 * M];
+    down_mfma_body<M>(a, blockIdx.y, blockIdx.x, lds, red);
+}
+
+// The routed experts' down on the matrix cores and a shared MLP's down
+// (format FB, one slot, no split) in one launch: a flat grid of gxm tiles
+// per routed slot (slot-major, as k_moe_down_mfma's grid), then the shared
+// MLP's gxb tiles, which run beside the routed ones instead of after them.
+template <int M, int FB>
+__global__ __launch_bounds__(kGemvThreads) void k_moe_down_mfma_dual(DownArgs a, DownArgs b, int gxm,
+                                                                    int nrouted) {
+    __shared__ __attribute__((aligned(16)))
+    uint32_t lds[cmax_words(mfma_lds_words<M, kDownMfmaKC>(), kLdsWords)];
+    __shared__ uint32_t red[4 * M];
+    const int i = blockIdx.x;
+    if (i < nrouted) down_mfma_body<M>(a, i / gxm, i % gxm, lds, red);
+    else down_body<FB, M>(b, 0, i - nrouted, lds);
 }
 
 template <int FMT, int M>
@@ -1543,17 +1563,22 @@ static void launch_down(ut_ctx *ctx, const DownArgs &a, int64_t slots, const Dow
     if constexpr (FA == UT_FMT_INT4 && M >= UT_DOWN_MFMA_MIN_M && M <= 4) {
         if ((!b || M >= 3) && down_mfma_ok(FA, M, a.I, a.ks)) {
             constexpr int WR = 64 * down_mfma_tw<M>();
-            hipLaunchKernelGGL((k_moe_down_mfma<M>), dim3((unsigned)((a.H + WR - 1) / WR), (unsigned)slots),
-                               dim3(kGemvThreads), 0, ctx->stream, a);
-            // a shared MLP beside it (one slot, no split): its own launch
-            if (b) {
-                constexpr int DRB = 16 * down_rows<M>();
-                const dim3 gb((unsigned)((b->H + DRB - 1) / DRB), 1u, 1u);
-                if (fb == UT_FMT_INT4)
-                    hipLaunchKernelGGL((k_moe_down<UT_FMT_INT4, M>), gb, dim3(kGemvThreads), 0, ctx->stream, *b);
-                else
-                    hipLaunchKernelGGL((k_moe_down<UT_FMT_INT8, M>), gb, dim3(kGemvThreads), 0, ctx->stream, *b);
+            const int gxm = (int)((a.H + WR - 1) / WR);
+            if (!b) {
+                hipLaunchKernelGGL((k_moe_down_mfma<M>), dim3((unsigned)gxm, (unsigned)slots),
+                                   dim3(kGemvThreads), 0, ctx->stream, a);
+                return;
             }
+            // a shared MLP beside it (one slot, no split): the grid's last tiles
+            constexpr int DRB = 16 * down_rows<M>();
+            const int nrouted = gxm * (int)slots;
+            const unsigned n = (unsigned)(nrouted + (b->H + DRB - 1) / DRB);
+            if (fb == UT_FMT_INT4)
+                hipLaunchKernelGGL((k_moe_down_mfma_dual<M, UT_FMT_INT4>), dim3(n), dim3(kGemvThreads), 0,
+                                   ctx->stream, a, *b, gxm, nrouted);
+            else
+                hipLaunchKernelGGL((k_moe_down_mfma_dual<M, UT_FMT_INT8>), dim3(n), dim3(kGemvThreads), 0,
+                                   ctx->stream, a, *b, gxm, nrouted);
             return;
         }
     }
