@@ -1561,7 +1561,7 @@ static void launch_down(ut_ctx *ctx, const DownArgs &a, int64_t slots, const Dow
     constexpr int DR = 16 * down_rows<M>();
     const unsigned gx = (unsigned)((a.H + DR - 1) / DR);
     if constexpr (FA == UT_FMT_INT4 && M >= UT_DOWN_MFMA_MIN_M && M <= 4) {
-        if ((!b || M >= 3) && down_mfma_ok(FA, M, a.I, a.ks)) {
+        if (down_mfma_ok(FA, M, a.I, a.ks)) {
             constexpr int WR = 64 * down_mfma_tw<M>();
             const int gxm = (int)((a.H + WR - 1) / WR);
             if (!b) {
@@ -1614,11 +1614,11 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
     // digitise x too (self_plan, x as f32)
     constexpr int64_t KC = gemv_chunk_cols<FMT, M>();
     // the matrix-core gate/up (int4, 2..4 rows): x as f32 with the
-    // digitiser's exponents, the slot plan made before the launch; beside a
-    // shared expert from three rows on (at two the fused routed + shared
-    // launch of the dot-product kernels is faster)
+    // digitiser's exponents, the slot plan made before the launch, a shared
+    // expert in the same launches (config-4 verify of two rows: 1,027 ->
+    // 1,003 us of GPU time against the dot-product dual kernels)
     const bool use_mfma = gate_up_mfma_ok(FMT, M, c.H) && c.extra_slot < 0 &&
-                          (!c.x_digits || c.x_matches_digits) && (!c.shared || M >= 3) &&
+                          (!c.x_digits || c.x_matches_digits) &&
                           L.ntiles == (c.I + kGateUpRowsPerWG - 1) / kGateUpRowsPerWG;
     const bool gate_plan = FMT != UT_FMT_F32 && need_plan && c.extra_slot < 0 &&
                            (int64_t)M * c.k <= 64 && !use_mfma;
