@@ -570,10 +570,10 @@ def committed_traffic(kernel: str) -> tuple[float | None, str | None]:
 def profile_decode(cfg_name: str, prompt_len: int, tokens: int, seed: int = 42) -> None:
     """Decode-step driver for kernel traces (run it under rocprofv3): the
     synthetic model on device, a uniform-random prompt, then `tokens`
-    one-row decode steps and `tokens // 2` two-row verify steps (the MTP
-    verify width at depth 1), the phases separated by an idle second so a
-    kernel trace splits cleanly at the gaps.  Prints the host-timed ms per
-    step of each phase."""
+    one-row decode steps, `tokens // 2` two-row and `tokens // 2` four-row
+    verify steps (the MTP verify widths at depth 1 and 3), the phases
+    separated by an idle second so a kernel trace splits cleanly at the
+    gaps.  Prints the host-timed ms per step of each phase."""
     import torch
     import undertow_amd as U
     from undertow_amd.configs import C1, C4
@@ -598,12 +598,15 @@ def profile_decode(cfg_name: str, prompt_len: int, tokens: int, seed: int = 42) 
     torch.cuda.synchronize()
     time.sleep(1.0)
     n = max(tokens // 2, 1)
-    t0 = time.perf_counter()
-    for _ in range(n):
-        s.prefill([nxt, nxt], want_logits=False)
-        nxt = s.last_argmax[-1]
-    t1 = time.perf_counter()
-    print(f"verify (2 rows) {n} steps: {(t1 - t0) / n * 1e3:.3f} ms/step", flush=True)
+    for rows in (2, 4):  # the MTP depth-1 and depth-3 verify widths
+        torch.cuda.synchronize()
+        time.sleep(1.0)
+        t0 = time.perf_counter()
+        for _ in range(n):
+            s.prefill([nxt] * rows, want_logits=False)
+            nxt = s.last_argmax[-1]
+        t1 = time.perf_counter()
+        print(f"verify ({rows} rows) {n} steps: {(t1 - t0) / n * 1e3:.3f} ms/step", flush=True)
 
 
 def main():
