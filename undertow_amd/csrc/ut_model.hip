@@ -138,6 +138,9 @@ struct ut_session {
     // the MTP verify step (gv_rows rows fed from ws.vids), captured likewise
     hipGraphExec_t gv = nullptr;
     int64_t gv_rows = 0, v_steps = 0;
+    // the MTP head's feed after a verify, one graph per fed row count 1..4
+    hipGraphExec_t gd[4] = {nullptr, nullptr, nullptr, nullptr};
+    int64_t d_steps[4] = {0, 0, 0, 0};
     bool graph_failed = false;
 };
 
@@ -382,6 +385,11 @@ int32_t ws_reserve(ut_session *s, int64_t rows) {
         w.base = nullptr;
     }
     // a captured step names the old workspace
+    for (auto &g : s->gd)
+        if (g) {
+            (void)hipGraphExecDestroy(g);
+            g = nullptr;
+        }
     if (s->gv) {
         (void)hipGraphExecDestroy(s->gv);
         s->gv = nullptr;
@@ -939,19 +947,21 @@ void truncate_session(ut_session *s, int64_t len) {
 // draft_logits (mtp.rs:74-133): feed positions fed..pos-1 to the MTP layer
 // and take the argmax of the head's logits for the last one.
 // draft_logits on device ids: row ids come from the host (host_ids, rows of
-// them) or, for a chained draft, from ws.vids[in_slot] (one row); the draft
-// id goes to ws.vids[out_slot] without a host round trip.
+// them), from dev_ids (rows of them, on the device), or, for a chained
+// draft, from ws.vids[in_slot] (one row); the draft id goes to
+// ws.vids[out_slot] without a host round trip.
 int32_t draft_rows_dev(ut_session *s, const int32_t *host_ids, int in_slot,
-                       const float *hidden_rows, int64_t rows, int out_slot) {
+                       const float *hidden_rows, int64_t rows, int out_slot,
+                       const int32_t *dev_ids = nullptr) {
     ut_model *m = s->m;
     ut_ctx *ctx = m->ctx;
     const ut_model_config &c = m->c;
     Workspace &w = s->ws;
     const int64_t H = c.hidden_size, V = c.vocab_size;
     if (rows > w.rows) UT_TRY(ws_reserve(s, rows));
-    const int32_t *ids = in_slot >= 0 ? w.vids + in_slot : nullptr;
+    const int32_t *ids = dev_ids ? dev_ids : in_slot >= 0 ? w.vids + in_slot : nullptr;
     int32_t *draft_dev = w.vids + out_slot;
-    if (in_slot < 0) {
+    if (!dev_ids && in_slot < 0) {
         for (int64_t i = 0; i < rows; i++)
             if (host_ids[i] < 0 || host_ids[i] >= V) {
                 set_error(ctx, "token id %d out of vocab (%lld)", host_ids[i], (long long)V);
@@ -1202,21 +1212,21 @@ bool graph_ok(const ut_session *s, int64_t eager_steps) {
     return m->graphs && !s->graph_failed && !m->store && !m->ctx->timing && eager_steps >= 1;
 }
 
-// Captures the step of `rows` rows fed from the device ids at ids_dev (in
-// the workspace) into *exec.  The capture pass runs the host side of the
-// step (so the session's positions advance as if it ran); every
-// position-dependent launch reads the device word s->dpos, and attention
-// grids are sized for the capacity.  The graph must hold kernel launches
+// Captures the launches of body() (a step of the session) into *exec.  The
+// capture pass runs the host side of the step (so the session's positions
+// advance as if it ran); every position-dependent launch reads the device
+// word s->dpos, and attention grids are sized for the capacity.  The graph must hold kernel launches
 // only.  The null stream cannot be captured: then the launches are captured
 // on the context's own stream (capturing runs nothing) and the graph is
 // launched on the context's stream.  On failure the host positions are
 // restored and UT_ERR_STATE returned (the caller runs the step eagerly).
-int32_t capture_rows(ut_session *s, int64_t rows, const int32_t *ids_dev, hipGraphExec_t *exec) {
+template <typename Body>
+int32_t capture_body(ut_session *s, Body body, hipGraphExec_t *exec) {
     ut_model *m = s->m;
     ut_ctx *ctx = m->ctx;
     const hipStream_t run_stream = ctx->stream;
     ctx->stream = run_stream ? run_stream : ctx->own_stream;
-    const int64_t pos0 = s->pos;
+    const int64_t pos0 = s->pos, mtp_len0 = s->mtp_kv.len;
     std::vector<int64_t> lens;
     for (auto &kv : s->kv) lens.push_back(kv.len);
     ctx->step_pos = s->dpos;
@@ -1227,8 +1237,7 @@ int32_t capture_rows(ut_session *s, int64_t rows, const int32_t *ids_dev, hipGra
     if (hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal) != hipSuccess) {
         rc = UT_ERR_STATE;
     } else {
-        rc = prefill_dev(s, nullptr, rows, ids_dev);
-        if (rc == UT_OK) rc = launch_pos_add(ctx, s->dpos, rows);
+        rc = body();
         if (hipStreamEndCapture(ctx->stream, &graph) != hipSuccess) rc = UT_ERR_STATE;
     }
     ctx->step_pos = nullptr;
@@ -1257,9 +1266,17 @@ int32_t capture_rows(ut_session *s, int64_t rows, const int32_t *ids_dev, hipGra
     if (rc != UT_OK) {
         s->pos = pos0;
         for (size_t i = 0; i < lens.size(); i++) s->kv[i].len = lens[i];
+        s->mtp_kv.len = mtp_len0;
         return UT_ERR_STATE;
     }
     return UT_OK;
+}
+
+int32_t capture_rows(ut_session *s, int64_t rows, const int32_t *ids_dev, hipGraphExec_t *exec) {
+    return capture_body(s, [&]() -> int32_t {
+        UT_TRY(prefill_dev(s, nullptr, rows, ids_dev));
+        return launch_pos_add(s->m->ctx, s->dpos, rows);
+    }, exec);
 }
 
 // One device-fed step of `rows` rows (ids at ids_dev): replayed from the
@@ -1315,6 +1332,51 @@ int32_t verify_step(ut_session *s, int64_t rows) {
     }
     s->gv_rows = rows;
     return graph_step(s, rows, s->ws.vids, &s->gv, &s->v_steps);
+}
+
+// The MTP head's feed after a verify that accepted `pending - 1` drafts
+// (mtp.rs:84-121): the ids of positions fed..pos-1 gathered on the device
+// from the verify's ids and argmax rows, the main model's hidden rows at
+// those positions read at the device position word, then the MTP layer and
+// head on them (the draft into ws.vids[1]).  Replayed from a graph per row
+// count when the session allows it, like the verify step.
+int32_t draft_feed(ut_session *s, int64_t pending) {
+    ut_model *m = s->m;
+    ut_ctx *ctx = m->ctx;
+    const int64_t H = m->c.hidden_size, fed = s->mtp_fed;
+    auto body = [&]() -> int32_t {
+        Workspace &w = s->ws;
+        UT_TRY(launch_feed_ids(ctx, w.ids, w.vids, w.am, (int)pending - 1));
+        UT_TRY(launch_copy_rows_from(ctx, w.attn, s->hidden, H, fed, pending, H));
+        return draft_rows_dev(s, nullptr, -1, w.attn, pending, 1, w.ids);
+    };
+    hipGraphExec_t *g = &s->gd[pending - 1];
+    int64_t *steps = &s->d_steps[pending - 1];
+    if (!graph_ok(s, *steps)) {
+        UT_TRY(body());
+        (*steps)++;
+        return UT_OK;
+    }
+    // the device position word must hold the main position
+    if (s->dpos_host != s->pos) {
+        UT_TRY(launch_pos_set(ctx, s->dpos, s->pos));
+        s->dpos_host = s->pos;
+    }
+    if (!*g) {
+        if (capture_body(s, body, g) != UT_OK) {
+            s->graph_failed = true;
+            m->graph_failures++;
+            return draft_feed(s, pending);
+        }
+        m->graph_captures++;
+        // the capture pass advanced the host's MTP cache length; now run it
+    } else {
+        s->mtp_kv.len += pending;
+    }
+    UT_CHECK_HIP(ctx, hipGraphLaunch(*g, ctx->stream));
+    m->graph_replays++;
+    (*steps)++;
+    return UT_OK;
 }
 
 int64_t gen_greedy(ut_model *m, const int32_t *prompt, int64_t n, Emit &em) {
@@ -1379,6 +1441,7 @@ int64_t gen_spec(ut_model *m, const int32_t *prompt, int64_t n, int32_t depth, u
     }
     int32_t next = am[(size_t)n - 1];
     int64_t nd = 0, na = 0;
+    bool verified = false;  // a verify ran in this loop (its ids and argmax rows are on the device)
     std::vector<int32_t> toks, drafts((size_t)depth), vid((size_t)depth + 1);
     for (;;) {
         if (em.push(next)) break;
@@ -1406,11 +1469,18 @@ int64_t gen_spec(ut_model *m, const int32_t *prompt, int64_t n, int32_t depth, u
             if (rc == UT_OK) rc = upload_slot(s, s->ws.vids, vid.data(), depth + 1, kPinIds - 8);
             if (rc) break;
         } else {
-            // ---- draft: feed verified positions fed..pos-1 (mtp.rs:84-121)
+            // ---- draft: feed verified positions fed..pos-1 (mtp.rs:84-121);
+            // after a verify their ids are the accepted drafts and `next`,
+            // which the device holds (draft_feed), else they come from the host
             const int64_t pos = s->pos, fed = s->mtp_fed, pending = pos - fed;
-            toks.clear();
-            for (int64_t i = fed; i < pos; i++) toks.push_back(i + 1 < pos ? s->tokens[(size_t)i + 1] : next);
-            rc = draft_rows_dev(s, toks.data(), -1, s->hidden + fed * H, pending, 1);
+            if (verified && pending >= 1 && pending <= depth + 1) {
+                rc = draft_feed(s, pending);
+            } else {
+                toks.clear();
+                for (int64_t i = fed; i < pos; i++)
+                    toks.push_back(i + 1 < pos ? s->tokens[(size_t)i + 1] : next);
+                rc = draft_rows_dev(s, toks.data(), -1, s->hidden + fed * H, pending, 1);
+            }
             if (rc) break;
             s->mtp_fed = pos;
             // ---- chained drafts (depth > 1): MTP layer on its own last output row
@@ -1442,6 +1512,7 @@ int64_t gen_spec(ut_model *m, const int32_t *prompt, int64_t n, int32_t depth, u
         if (rc == UT_OK) rc = readback_enqueue(s, s->ws.am, depth + 1, 0);
         if (rc == UT_OK) rc = readback_wait(s, depth + 1, am.data(), 0);
         if (rc) break;
+        verified = true;
         if (!draft_fn) memcpy(drafts.data(), s->pin + kPinIds + depth + 1, (size_t)depth * 4);
         s->tokens.push_back(next);
         s->tokens.insert(s->tokens.end(), drafts.begin(), drafts.end());
@@ -2048,6 +2119,8 @@ void ut_session_free(ut_session *s) {
     (void)hipStreamSynchronize(s->m->ctx->stream);
     if (s->g1) (void)hipGraphExecDestroy(s->g1);
     if (s->gv) (void)hipGraphExecDestroy(s->gv);
+    for (auto g : s->gd)
+        if (g) (void)hipGraphExecDestroy(g);
     if (s->ws.base) (void)hipFree(s->ws.base);
     if (s->kv_alloc) (void)hipFree(s->kv_alloc);
     if (s->pin) (void)hipHostFree(s->pin);

@@ -77,6 +77,11 @@ int32_t launch_bf16_to_f32(ut_ctx *ctx, const uint16_t *x, int64_t n, float *y);
 // context's captured-step position when one is set.
 int32_t launch_copy_rows_at(ut_ctx *ctx, float *dst, int64_t ld, int64_t pos, const float *src,
                             int64_t rows, int64_t H);
+// dst [rows][H] <- src rows [pos, pos + rows) (stride ld); pos as above.
+int32_t launch_copy_rows_from(ut_ctx *ctx, float *dst, const float *src, int64_t ld, int64_t pos,
+                              int64_t rows, int64_t H);
+// The MTP feed's ids after a verify that accepted a drafts: vids[1..a], am[a].
+int32_t launch_feed_ids(ut_ctx *ctx, int32_t *dst, const int32_t *vids, const int32_t *am, int a);
 // *p = v, and *p += n (a captured step's position word).
 int32_t launch_pos_set(ut_ctx *ctx, int64_t *p, int64_t v);
 int32_t launch_pos_add(ut_ctx *ctx, int64_t *p, int64_t n);

@@ -130,6 +130,44 @@ int32_t launch_copy_rows_at(ut_ctx *ctx, float *dst, int64_t ld, int64_t pos, co
     return launch_check(ctx, "k_copy_rows_at");
 }
 
+// Rows [pos, pos + rows) of src (row stride ld) into dst (rows x H): the
+// MTP feed's hidden rows, read at a position the device word may hold.
+__global__ void k_copy_rows_from(float *__restrict__ dst, const float *__restrict__ src, int64_t ld,
+                                 PosRef pos, int64_t H) {
+    const float *s = src + (pos.get() + blockIdx.y) * ld;
+    float *d = dst + (int64_t)blockIdx.y * H;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < H;
+         i += (int64_t)gridDim.x * blockDim.x)
+        d[i] = s[i];
+}
+
+int32_t launch_copy_rows_from(ut_ctx *ctx, float *dst, const float *src, int64_t ld, int64_t pos,
+                              int64_t rows, int64_t H) {
+    if (rows <= 0) return UT_OK;
+    unsigned bx = (unsigned)((H + 255) / 256);
+    if (bx > 32) bx = 32;
+    int tok = timing_begin(ctx, "copy_rows");
+    hipLaunchKernelGGL(k_copy_rows_from, dim3(bx, (unsigned)rows), dim3(256), 0, ctx->stream, dst,
+                       src, ld, pos_ref(ctx, pos), H);
+    timing_end(ctx, tok);
+    return launch_check(ctx, "k_copy_rows_from");
+}
+
+// The MTP feed's token ids after a verify of [next, d1..dk] that accepted
+// `a` drafts (mtp.rs:84-121): the accepted drafts d1..da (vids[1..a]) and
+// the verify's argmax row a (the next token), a + 1 ids into dst.
+__global__ void k_feed_ids(int32_t *__restrict__ dst, const int32_t *__restrict__ vids,
+                           const int32_t *__restrict__ am, int a) {
+    const int i = threadIdx.x;
+    if (i < a) dst[i] = vids[1 + i];
+    else if (i == a) dst[i] = am[a];
+}
+
+int32_t launch_feed_ids(ut_ctx *ctx, int32_t *dst, const int32_t *vids, const int32_t *am, int a) {
+    hipLaunchKernelGGL(k_feed_ids, dim3(1), dim3(64), 0, ctx->stream, dst, vids, am, a);
+    return launch_check(ctx, "k_feed_ids");
+}
+
 // The device position word of a captured decode step: set before a replay
 // when the host moved the position, advanced by the step itself.
 __global__ void k_pos_set(int64_t *p, int64_t v) {
