@@ -465,6 +465,25 @@ def mtp_bench(U, ctx, cfg, prompt_len, new_tokens, depths, seed, expert_fmt, den
         res[f"mtp{d}"]["graph"] = {"tok_s": len(toks_g) / dt,
                                    "replays": after["replays"] - before["replays"],
                                    "failures": after["failures"] - before["failures"]}
+        # The accept path's rate: caller drafts (speculative_loop's draft_fn,
+        # mtp.rs:263-314) equal to the greedy continuation, so every draft is
+        # accepted (the perfect-draft case of pipeline.rs:343-393). Random-init
+        # weights give the native head about zero acceptance, so this is the
+        # figure that shows what an accepted draft is worth on this step.
+        tail = greedy + [0] * (d + 1)
+
+        def perfect(tokens, nxt, dep, _n=len(prompt)):
+            e = len(tokens) - _n + 1
+            return tail[e:e + dep]
+
+        t0 = time.perf_counter()
+        toks_p, drafted_p, accepted_p = m.speculative_loop(prompt, new_tokens, depth=d,
+                                                           draft_fn=perfect)
+        dt = time.perf_counter() - t0 - t_prefill
+        assert toks_p == greedy, f"MTP depth {d} with perfect drafts differs from greedy"
+        res[f"mtp{d}"]["perfect_drafts"] = {"tok_s": len(toks_p) / dt, "drafted": drafted_p,
+                                            "accepted": accepted_p,
+                                            "acceptance": accepted_p / max(drafted_p, 1)}
     del m
     return res
 
