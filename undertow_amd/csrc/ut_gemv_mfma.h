@@ -195,11 +195,13 @@ __device__ __forceinline__ void mfma_gemv_i4_f32x(const uint8_t *const (&arow)[T
 // activations load into registers while the current one computes, and the
 // weight loads run on across chunk boundaries (the barriers between
 // chunks wait for LDS only).
-template <int M, int KC>
-__device__ __forceinline__ void mfma_gemv_i4_chunks(const uint8_t *arow, int64_t K,
+// TW tiles of 16 rows per wave (arow[w]: this lane's A row of tile w) share
+// each staged chunk.
+template <int M, int KC, int TW>
+__device__ __forceinline__ void mfma_gemv_i4_chunks(const uint8_t *const (&arow)[TW], int64_t K,
                                                     const float *xf, int64_t ldx,
                                                     const int32_t (&sh)[M], uint8_t *lds,
-                                                    CoreOut<UT_FMT_INT4, M, 4> &res) {
+                                                    CoreOut<UT_FMT_INT4, M, 4> (&res)[TW]) {
     static_assert(M >= 1 && M <= 4, "three digit planes per row, 16 columns");
     static_assert(KC % (4 * kMfmaStepCols) == 0, "chunks of whole step groups");
     // weight steps in flight: two at two rows (54.5 against 58.5 us for
@@ -209,7 +211,9 @@ __device__ __forceinline__ void mfma_gemv_i4_chunks(const uint8_t *arow, int64_t
     constexpr int NI = (M * (KC / 8) + kGemvThreads - 1) / kGemvThreads;
     const int tid = threadIdx.x, lane = tid & 63, n = lane & 15, kg = lane >> 4;
     const int nsteps = (int)(K / kMfmaStepCols);
-    const uint8_t *ap = arow + 16 * kg;
+    const uint8_t *ap[TW];
+#pragma unroll
+    for (int w = 0; w < TW; w++) ap[w] = arow[w] + 16 * kg;
     float4 xv[NI][2];
     auto xload = [&](int64_t kc) {
         const int kcn = (int)(K - kc < KC ? K - kc : KC), NG = kcn / 8, TOT = M * NG;
@@ -244,14 +248,18 @@ __device__ __forceinline__ void mfma_gemv_i4_chunks(const uint8_t *arow, int64_t
     };
     auto lds_barrier = []() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
     xload(0);
-    uint4 wq[DEPTH];
+    uint4 wq[DEPTH][TW];
 #pragma unroll
-    for (int u = 0; u < DEPTH; u++) wq[u] = ld_weights(ap + 64 * u);
+    for (int u = 0; u < DEPTH; u++)
+#pragma unroll
+        for (int w = 0; w < TW; w++) wq[u][w] = ld_weights(ap[w] + 64 * u);
     xstore(0);
     lds_barrier();
     const bool bn = n < 3 * M;
     const uint8_t *bp = lds + (bn ? n : 0) * RB + 32 * kg;
-    ut_i32x4 acc = {0, 0, 0, 0};
+    ut_i32x4 acc[TW];
+#pragma unroll
+    for (int w = 0; w < TW; w++) acc[w] = ut_i32x4{0, 0, 0, 0};
     int j0 = 0;  // global step of the chunk's first step
     for (int64_t kc = 0; kc < K; kc += KC) {
         const bool more = kc + KC < K;
@@ -260,22 +268,25 @@ __device__ __forceinline__ void mfma_gemv_i4_chunks(const uint8_t *arow, int64_t
         for (int t = 0; t < csteps; t += DEPTH) {
 #pragma unroll
             for (int u = 0; u < DEPTH; u++) {
-                const uint4 w = wq[u];
                 const int jn = j0 + t + u + DEPTH;
-                wq[u] = ld_weights(ap + 64 * (jn < nsteps ? jn : nsteps - 1));
-                const uint32_t X = 0x88888888u;
-                const uint32_t a0 = w.x ^ X, a1 = w.y ^ X, a2 = w.z ^ X, a3 = w.w ^ X;
-                const ut_i32x4 A0 = {mfma_sext4(a0), mfma_sext4(a0 >> 4), mfma_sext4(a1),
-                                     mfma_sext4(a1 >> 4)};
-                const ut_i32x4 A1 = {mfma_sext4(a2), mfma_sext4(a2 >> 4), mfma_sext4(a3),
-                                     mfma_sext4(a3 >> 4)};
                 uint4 b0 = *(const uint4 *)(bp + kMfmaStepCols * (t + u));
                 uint4 b1 = *(const uint4 *)(bp + kMfmaStepCols * (t + u) + 16);
                 if (!bn) b0 = b1 = make_uint4(0u, 0u, 0u, 0u);
                 const ut_i32x4 B0 = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w};
                 const ut_i32x4 B1 = {(int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
-                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, acc, 0, 0, 0);
+#pragma unroll
+                for (int w = 0; w < TW; w++) {
+                    const uint4 wv = wq[u][w];
+                    wq[u][w] = ld_weights(ap[w] + 64 * (jn < nsteps ? jn : nsteps - 1));
+                    const uint32_t X = 0x88888888u;
+                    const uint32_t a0 = wv.x ^ X, a1 = wv.y ^ X, a2 = wv.z ^ X, a3 = wv.w ^ X;
+                    const ut_i32x4 A0 = {mfma_sext4(a0), mfma_sext4(a0 >> 4), mfma_sext4(a1),
+                                         mfma_sext4(a1 >> 4)};
+                    const ut_i32x4 A1 = {mfma_sext4(a2), mfma_sext4(a2 >> 4), mfma_sext4(a3),
+                                         mfma_sext4(a3 >> 4)};
+                    acc[w] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, acc[w], 0, 0, 0);
+                    acc[w] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, acc[w], 0, 0, 0);
+                }
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -286,24 +297,8 @@ __device__ __forceinline__ void mfma_gemv_i4_chunks(const uint8_t *arow, int64_t
             lds_barrier();
         }
     }
-    const int r_me = n >> 2, m_me = n & 3;
-    int64_t S = 0;
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-#pragma unroll
-        for (int p = 0; p < 3; p++) {
-            const int src = (lane & 48) | (3 * m_me + p);
-            const int v = __shfl(acc[q], src, 64);
-            if (q == r_me) S += (int64_t)v * (int64_t)(1 << (8 * p));
-        }
-    }
-#pragma unroll
-    for (int r = 0; r < 4; r++)
-#pragma unroll
-        for (int m = 0; m < M; m++) {
-            res.S[r][m] = S;
-            res.F[r][m] = 0.0f;
-        }
+    for (int w = 0; w < TW; w++) mfma_collect<M>(acc[w], res[w]);
 }
 
 }  // namespace ut

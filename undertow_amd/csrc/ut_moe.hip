@@ -984,16 +984,20 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up(GateUpArgs a) {
 }
 
 // Gate/up on the matrix cores (int4, 2..4 rows, plan ready, H % 512 == 0):
-// each wave 8 h rows (A rows 0-7 the gate rows, 8-15 the up rows), the
-// workgroup 32 (two of the plain kernel's 16-row tiles: both partial-max
-// slots get the workgroup's maximum).  x is digitised while staged, by the
-// digitiser's exponents, into the same integers as its digit planes.
+// each wave TW tiles of 8 h rows (A rows 0-7 the gate rows, 8-15 the up
+// rows of one tile), the workgroup 32 * TW rows (2 * TW of the plain
+// kernel's 16-row tiles: every partial-max slot gets the workgroup's
+// maximum).  x is digitised while staged, by the digitiser's exponents,
+// into the same integers as its digit planes; the wave's tiles share each
+// staged chunk, so TW = 2 halves the activation staging per weight byte.
 template <int M> constexpr int gate_up_mfma_kc() { return M == 2 ? 4096 : 2048; }
+template <int M> constexpr int gate_up_mfma_tw() { return M >= 3 ? 2 : 1; }
+template <int M> constexpr int gate_up_mfma_rows() { return 32 * gate_up_mfma_tw<M>(); }
 
 template <int M>
 __device__ __forceinline__ void gate_up_mfma_body(const GateUpArgs &a, int u, int tile,
                                                   uint32_t *lds, uint32_t *wg_max) {
-    constexpr int KC = gate_up_mfma_kc<M>();
+    constexpr int KC = gate_up_mfma_kc<M>(), TW = gate_up_mfma_tw<M>();
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
     const int cnt = *a.count;
     const uint8_t *gw = (const uint8_t *)a.sp[u * 6 + kSpGate];
@@ -1002,41 +1006,48 @@ __device__ __forceinline__ void gate_up_mfma_body(const GateUpArgs &a, int u, in
     const float *usc = (const float *)a.sp[u * 6 + kSpUpS];
     if (u >= cnt) return;
     if (tid < 4) wg_max[tid] = 0;
-    const int64_t o0 = (int64_t)tile * 32 + wave * 8;
-    const int ai = s & 7;  // this lane's A row: gate (s < 8) or up row o0 + ai
-    const int64_t ao = o0 + ai < a.I ? o0 + ai : a.I - 1;
-    const uint8_t *arow = (s < 8 ? gw : uw) + ao * a.row_bytes;
+    const int64_t o0 = (int64_t)tile * (32 * TW) + wave * (8 * TW);  // tile w: rows o0 + 8w ..
+    const int ai = s & 7;  // this lane's A row: gate (s < 8) or up row o0 + 8w + ai
+    const uint8_t *arow[TW];
+#pragma unroll
+    for (int w = 0; w < TW; w++) {
+        const int64_t ao = o0 + 8 * w + ai < a.I ? o0 + 8 * w + ai : a.I - 1;
+        arow[w] = (s < 8 ? gw : uw) + ao * a.row_bytes;
+    }
     int32_t exl[M], sh[M];
 #pragma unroll
     for (int m = 0; m < M; m++) {
         exl[m] = a.exps[m];
         sh[m] = exl[m] == INT32_MIN ? INT32_MIN : -exl[m];
     }
-    CoreOut<UT_FMT_INT4, M, 4> res;
-    mfma_gemv_i4_chunks<M, KC>(arow, a.H, a.mfma_xf, a.H, sh, (uint8_t *)lds, res);
-    // lanes 0-31 hold the gate totals of rows 4g + r (g < 2), lanes 32-63
-    // the up totals of the same rows
-    const int64_t S = res.S[0][0];
-    const int lo = (int)(uint32_t)S, hi = (int)(uint32_t)((uint64_t)S >> 32);
-    const int ulo = __shfl(lo, lane + 32 < 64 ? lane + 32 : lane, 64);
-    const int uhi = __shfl(hi, lane + 32 < 64 ? lane + 32 : lane, 64);
+    CoreOut<UT_FMT_INT4, M, 4> res[TW];
+    mfma_gemv_i4_chunks<M, KC, TW>(arow, a.H, a.mfma_xf, a.H, sh, (uint8_t *)lds, res);
+    // per tile: lanes 0-31 hold the gate totals of rows 4g + r (g < 2),
+    // lanes 32-63 the up totals of the same rows
     const int r = s >> 2, m = s & 3;
-    const int64_t o = o0 + 4 * g + r;
-    if (g < 2 && m < M && o < a.I) {
-        const int32_t e = m == 0 ? exl[0] : m == 1 ? exl[M > 1 ? 1 : 0]
-                        : m == 2 ? exl[M > 2 ? 2 : 0] : exl[M > 3 ? 3 : 0];
-        const int64_t US = (int64_t)(((uint64_t)(uint32_t)uhi << 32) | (uint32_t)ulo);
-        const float gv = int_total_to_f32(S, e, ld_global_f32(gsc + o));
-        const float uv = int_total_to_f32(US, e, ld_global_f32(usc + o));
-        // silu(g) * u (undertow-quant/src/lib.rs:121; model.rs:241-247)
-        const float sg = gv / (1.0f + expf(-gv));
-        const float hv = __fmul_rn(sg, uv);
-        a.h[((int64_t)u * M + m) * a.I + o] = hv;
-        atomicMax(&wg_max[m], __float_as_uint(fabsf(hv)));
+    const int32_t e = m == 0 ? exl[0] : m == 1 ? exl[M > 1 ? 1 : 0]
+                    : m == 2 ? exl[M > 2 ? 2 : 0] : exl[M > 3 ? 3 : 0];
+#pragma unroll
+    for (int w = 0; w < TW; w++) {
+        const int64_t S = res[w].S[0][0];
+        const int lo = (int)(uint32_t)S, hi = (int)(uint32_t)((uint64_t)S >> 32);
+        const int ulo = __shfl(lo, lane + 32 < 64 ? lane + 32 : lane, 64);
+        const int uhi = __shfl(hi, lane + 32 < 64 ? lane + 32 : lane, 64);
+        const int64_t o = o0 + 8 * w + 4 * g + r;
+        if (g < 2 && m < M && o < a.I) {
+            const int64_t US = (int64_t)(((uint64_t)(uint32_t)uhi << 32) | (uint32_t)ulo);
+            const float gv = int_total_to_f32(S, e, ld_global_f32(gsc + o));
+            const float uv = int_total_to_f32(US, e, ld_global_f32(usc + o));
+            // silu(g) * u (undertow-quant/src/lib.rs:121; model.rs:241-247)
+            const float sg = gv / (1.0f + expf(-gv));
+            const float hv = __fmul_rn(sg, uv);
+            a.h[((int64_t)u * M + m) * a.I + o] = hv;
+            atomicMax(&wg_max[m], __float_as_uint(fabsf(hv)));
+        }
     }
     __syncthreads();
-    if (tid < 2 * M) {
-        const int mm = tid >> 1, part = 2 * tile + (tid & 1);
+    if (tid < 2 * TW * M) {
+        const int mm = tid / (2 * TW), part = 2 * TW * tile + tid % (2 * TW);
         if (part < a.ntiles) a.hmax_parts[((int64_t)u * M + mm) * a.ntiles + part] = wg_max[mm];
     }
 }
@@ -1059,7 +1070,8 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up_mfma_dual(GateUpAr
     uint32_t lds[cmax_words(mfma_lds_words<M, gate_up_mfma_kc<M>()>(), kLdsWords)];
     __shared__ uint32_t wg_max[4];
     if (blockIdx.y + 1 < gridDim.y) {
-        if ((int64_t)blockIdx.x * 32 < a.I) gate_up_mfma_body<M>(a, blockIdx.y, blockIdx.x, lds, wg_max);
+        if ((int64_t)blockIdx.x * gate_up_mfma_rows<M>() < a.I)
+            gate_up_mfma_body<M>(a, blockIdx.y, blockIdx.x, lds, wg_max);
     } else {
         gate_up_body<FB, M, false>(b, 0, blockIdx.x, lds, wg_max);
     }
@@ -1525,7 +1537,7 @@ static void launch_gate_up(ut_ctx *ctx, const GateUpArgs &a, int64_t slots, cons
                            int fb) {
     if constexpr (FA == UT_FMT_INT4 && M >= 2 && M <= 4) {
         if (a.mfma_xf) {
-            const unsigned gx = (unsigned)((a.I + 31) / 32);
+            const unsigned gx = (unsigned)((a.I + gate_up_mfma_rows<M>() - 1) / gate_up_mfma_rows<M>());
             if (!b) {
                 hipLaunchKernelGGL((k_moe_gate_up_mfma<M>), dim3(gx, (unsigned)slots),
                                    dim3(kGemvThreads), 0, ctx->stream, a);
