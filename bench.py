@@ -484,6 +484,19 @@ def mtp_bench(U, ctx, cfg, prompt_len, new_tokens, depths, seed, expert_fmt, den
         res[f"mtp{d}"]["perfect_drafts"] = {"tok_s": len(toks_p) / dt, "drafted": drafted_p,
                                             "accepted": accepted_p,
                                             "acceptance": accepted_p / max(drafted_p, 1)}
+        # the same with the verify steps replayed from captured graphs
+        before = m.graph_stats()
+        m.enable_graphs(True)
+        t0 = time.perf_counter()
+        toks_pg, _, accepted_pg = m.speculative_loop(prompt, new_tokens, depth=d, draft_fn=perfect)
+        dt = time.perf_counter() - t0 - t_prefill
+        m.enable_graphs(False)
+        after = m.graph_stats()
+        assert toks_pg == greedy and accepted_pg == accepted_p, \
+            f"MTP depth {d} with perfect drafts under graph replay differs"
+        res[f"mtp{d}"]["perfect_drafts"]["graph"] = {
+            "tok_s": len(toks_pg) / dt, "replays": after["replays"] - before["replays"],
+            "failures": after["failures"] - before["failures"]}
     del m
     return res
 
