@@ -991,13 +991,17 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up(GateUpArgs a) {
 // into the same integers as its digit planes; the wave's tiles share each
 // staged chunk, so TW = 2 halves the activation staging per weight byte.
 template <int M> constexpr int gate_up_mfma_kc() { return M == 2 ? 4096 : 2048; }
-template <int M> constexpr int gate_up_mfma_tw() { return M >= 3 ? 2 : 1; }
-template <int M> constexpr int gate_up_mfma_rows() { return 32 * gate_up_mfma_tw<M>(); }
+// Tiles per wave: two from two rows on when the routed experts have the
+// launch to themselves; beside a shared MLP (whose 16-row tiles set the
+// grid) two rows keep one, so that the routed workgroups stay many enough
+// to spread evenly over the CUs.
+template <int M, bool DUAL> constexpr int gate_up_mfma_tw() { return M >= (DUAL ? 3 : 2) ? 2 : 1; }
+template <int M, bool DUAL> constexpr int gate_up_mfma_rows() { return 32 * gate_up_mfma_tw<M, DUAL>(); }
 
-template <int M>
+template <int M, int TW>
 __device__ __forceinline__ void gate_up_mfma_body(const GateUpArgs &a, int u, int tile,
                                                   uint32_t *lds, uint32_t *wg_max) {
-    constexpr int KC = gate_up_mfma_kc<M>(), TW = gate_up_mfma_tw<M>();
+    constexpr int KC = gate_up_mfma_kc<M>();
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
     const int cnt = *a.count;
     const uint8_t *gw = (const uint8_t *)a.sp[u * 6 + kSpGate];
@@ -1056,7 +1060,7 @@ template <int M>
 __global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up_mfma(GateUpArgs a) {
     __shared__ __attribute__((aligned(16))) uint32_t lds[mfma_lds_words<M, gate_up_mfma_kc<M>()>()];
     __shared__ uint32_t wg_max[4];
-    gate_up_mfma_body<M>(a, blockIdx.y, blockIdx.x, lds, wg_max);
+    gate_up_mfma_body<M, gate_up_mfma_tw<M, false>()>(a, blockIdx.y, blockIdx.x, lds, wg_max);
 }
 
 // The routed experts on the matrix cores (slots 0..gridDim.y-2, 32-row
@@ -1070,8 +1074,8 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up_mfma_dual(GateUpAr
     uint32_t lds[cmax_words(mfma_lds_words<M, gate_up_mfma_kc<M>()>(), kLdsWords)];
     __shared__ uint32_t wg_max[4];
     if (blockIdx.y + 1 < gridDim.y) {
-        if ((int64_t)blockIdx.x * gate_up_mfma_rows<M>() < a.I)
-            gate_up_mfma_body<M>(a, blockIdx.y, blockIdx.x, lds, wg_max);
+        if ((int64_t)blockIdx.x * gate_up_mfma_rows<M, true>() < a.I)
+            gate_up_mfma_body<M, gate_up_mfma_tw<M, true>()>(a, blockIdx.y, blockIdx.x, lds, wg_max);
     } else {
         gate_up_body<FB, M, false>(b, 0, blockIdx.x, lds, wg_max);
     }
@@ -1537,13 +1541,16 @@ static void launch_gate_up(ut_ctx *ctx, const GateUpArgs &a, int64_t slots, cons
                            int fb) {
     if constexpr (FA == UT_FMT_INT4 && M >= 2 && M <= 4) {
         if (a.mfma_xf) {
-            const unsigned gx = (unsigned)((a.I + gate_up_mfma_rows<M>() - 1) / gate_up_mfma_rows<M>());
             if (!b) {
+                constexpr int R = gate_up_mfma_rows<M, false>();
+                const unsigned gx = (unsigned)((a.I + R - 1) / R);
                 hipLaunchKernelGGL((k_moe_gate_up_mfma<M>), dim3(gx, (unsigned)slots),
                                    dim3(kGemvThreads), 0, ctx->stream, a);
                 return;
             }
             // a shared MLP beside it: the last grid row
+            constexpr int R = gate_up_mfma_rows<M, true>();
+            const unsigned gx = (unsigned)((a.I + R - 1) / R);
             const dim3 grid(gx > (unsigned)b->ntiles ? gx : (unsigned)b->ntiles, (unsigned)(slots + 1));
             if (fb == UT_FMT_INT4)
                 hipLaunchKernelGGL((k_moe_gate_up_mfma_dual<M, UT_FMT_INT4>), grid,
