@@ -991,11 +991,11 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up(GateUpArgs a) {
 // into the same integers as its digit planes; the wave's tiles share each
 // staged chunk, so TW = 2 halves the activation staging per weight byte.
 template <int M> constexpr int gate_up_mfma_kc() { return M == 2 ? 4096 : 2048; }
-// Tiles per wave: two from two rows on when the routed experts have the
-// launch to themselves; beside a shared MLP (whose 16-row tiles set the
-// grid) two rows keep one, so that the routed workgroups stay many enough
-// to spread evenly over the CUs.
-template <int M, bool DUAL> constexpr int gate_up_mfma_tw() { return M >= (DUAL ? 3 : 2) ? 2 : 1; }
+// Tiles per wave: two when the routed experts have the launch to
+// themselves; beside a shared MLP (whose 16-row tiles set the grid) one, so
+// that the routed workgroups stay many enough to spread evenly over the CUs
+// (two made the four-row launch 61.9 -> 73.1 us at DeepSeek-V3 width).
+template <int M, bool DUAL> constexpr int gate_up_mfma_tw() { return !DUAL && M >= 2 ? 2 : 1; }
 template <int M, bool DUAL> constexpr int gate_up_mfma_rows() { return 32 * gate_up_mfma_tw<M, DUAL>(); }
 
 template <int M, int TW>
