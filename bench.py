@@ -501,29 +501,80 @@ def mtp_bench(U, ctx, cfg, prompt_len, new_tokens, depths, seed, expert_fmt, den
     return res
 
 
-def c5_bench(U, ctx, torch, prompt_len=2048, new_tokens=256, pin_frac=0.25, seed=42,
-             pool_experts=1024):
+def c5_bench(U, ctx, torch, prompt_len=2048, new_tokens=256, pin_frac=0.25, cache_frac=0.10,
+             seed=42, pool_experts=1024):
     """Config 5: DeepSeek-V3 671B-shaped random-init model at full depth.
     Dense and shared weights (about 18.5 GB int8) are synthesized in HBM; the
-    333 GB of int4 routed experts sit behind the expert store's HBM tier with
-    a budget of the HBM left over, filled from a pinned host pool of
-    `pool_experts` seeded experts (key (layer, e) reads entry
-    (layer * 256 + e) mod pool_experts: every miss moves a real 22 MB
-    expert over the host link).  The prompt's prefill records a routing
-    profile; its hottest quarter of all routed experts is pinned; then
-    greedy and MTP depth-1 decode of `new_tokens` tokens, timed from the
-    first emitted token (prefill excluded), with pilot-router prefetch."""
+    333 GB of int4 routed experts sit behind the expert store's HBM tier,
+    filled from a pinned host pool of `pool_experts` seeded experts (key
+    (layer, e) reads entry (layer * 256 + e) mod pool_experts: every miss
+    moves a real 22 MB expert over the host link).  Two stores:
+
+    - `hbm_rest`: the budget is the HBM left over (about 281 GB).  The
+      prompt's prefill records a routing profile, its hottest quarter of all
+      routed experts is pinned, then greedy and MTP depth-1 decode of
+      `new_tokens` tokens, timed from the first emitted token (prefill
+      excluded), with pilot-router prefetch;
+    - `streaming`: a budget below the prompt's working set, so the decode
+      streams its misses over the host link.  Random-init routing is
+      concentrated (the 2048-token prompt touches about a third of the
+      14,848 experts), so the BASELINE layout taken over all experts (the
+      hottest quarter pinned plus a cache) would hold the whole working
+      set; here the hottest `pin_frac` of the experts the profile saw are
+      pinned, plus a cache of `cache_frac` of all routed experts.  The same
+      greedy and MTP-1 runs, with hit rate and host-link rate."""
     from undertow_amd.configs import C5
-    free, total = torch.cuda.mem_get_info()
     E, nL = C5["n_routed_experts"], C5["num_hidden_layers"] + 1 - C5["first_k_dense_replace"]
+    slot = 2 * C5["moe_intermediate_size"] * (C5["hidden_size"] // 2) + \
+        C5["hidden_size"] * (C5["moe_intermediate_size"] // 2) + \
+        (2 * C5["moe_intermediate_size"] + C5["hidden_size"]) * 4
+    n_pin = int(pin_frac * E * nL)
+    rng = np.random.default_rng(seed)
+    prompt = rng.integers(0, C5["vocab_size"], prompt_len).tolist()
+    res = {"prompt": prompt_len, "new_tokens": new_tokens, "host_pool_experts": pool_experts,
+           "expert_gb_total": round(E * nL * slot / 1e9, 1), "slot_bytes": slot}
+
+    def store_delta(st0, st1, dt, ntok):
+        d = {k: st1[k] - st0[k] for k in ("hits", "misses", "bytes_read", "prefetch_issued",
+                                          "evictions")}
+        return dict(d, hit_rate=round(d["hits"] / max(d["hits"] + d["misses"], 1), 4),
+                    host_link_gbs=round(d["bytes_read"] / dt / 1e9, 2),
+                    gb_per_token=round(d["bytes_read"] / max(ntok, 1) / 1e9, 3))
+
+    def decode_runs(m, tag):
+        out = {}
+
+        def timed(run):
+            stamps = []
+            st0 = m.store_stats()
+            toks = run(lambda t: stamps.append(time.perf_counter()) or True)
+            st1 = m.store_stats()
+            dt = stamps[-1] - stamps[0]
+            return toks, (len(stamps) - 1) / dt, store_delta(st0, st1, dt, len(toks))
+
+        toks, tps, d = timed(lambda cb: m.generate(prompt, new_tokens, on_token=cb))
+        out["greedy_tok_s"] = round(tps, 3)
+        out["greedy_store"] = d
+        log(f"config 5 {tag} greedy: {out['greedy_tok_s']} tok/s, {json.dumps(d)}")
+        counts = {}
+
+        def mtp_run(cb):
+            t, counts["drafted"], counts["accepted"] = m.speculative_loop(
+                prompt, new_tokens, depth=1, on_token=cb)
+            return t
+
+        mt, tps, d = timed(mtp_run)
+        out["mtp1"] = {"tok_s": round(tps, 3), **counts, "lossless": mt == toks, "store": d}
+        log(f"config 5 {tag} MTP-1: {json.dumps(out['mtp1'])}")
+        return out
+
+    free, total = torch.cuda.mem_get_info()
     budget = int(free - 26e9)
     m = U.Model(ctx, C5)
     t0 = time.perf_counter()
     m.synthesize_tiered(seed, budget, pool_experts, prefetch=True)
     ctx.synchronize()
     t_make = time.perf_counter() - t0
-    rng = np.random.default_rng(seed)
-    prompt = rng.integers(0, C5["vocab_size"], prompt_len).tolist()
     t0 = time.perf_counter()
     s = m.session()
     s.prefill(prompt, want_logits=False)
@@ -533,45 +584,43 @@ def c5_bench(U, ctx, torch, prompt_len=2048, new_tokens=256, pin_frac=0.25, seed
         f"{t_prefill:.1f} s, store {json.dumps(m.store_stats())}")
     usage = m.expert_usage()
     prof = U.ExpertProfile.from_usage("deepseek_v3", usage)
-    n_pin = int(pin_frac * E * nL)
-    slot = 2 * C5["moe_intermediate_size"] * (C5["hidden_size"] // 2) + \
-        C5["hidden_size"] * (C5["moe_intermediate_size"] // 2) + \
-        (2 * C5["moe_intermediate_size"] + C5["hidden_size"]) * 4
-    pinned = m.pin_experts(prof.hottest()[:n_pin], n_pin * (slot + 2048))
-    res = {"prompt": prompt_len, "new_tokens": new_tokens, "make_s": round(t_make, 2),
-           "prefill_s": round(t_prefill, 2), "hbm_budget_gb": round(budget / 1e9, 1),
-           "expert_gb_total": round(E * nL * slot / 1e9, 1),
-           "pinned_gb": round(pinned / 1e9, 1), "host_pool_experts": pool_experts}
-
-    def timed(run):
-        stamps = []
-        st0 = m.store_stats()
-        toks = run(lambda t: stamps.append(time.perf_counter()) or True)
-        st1 = m.store_stats()
-        dt = stamps[-1] - stamps[0]
-        d = {k: st1[k] - st0[k] for k in ("hits", "misses", "bytes_read", "prefetch_issued")}
-        return toks, (len(stamps) - 1) / dt, dt, d
-
-    toks, tps, dt, d = timed(lambda cb: m.generate(prompt, new_tokens, on_token=cb))
-    res["greedy_tok_s"] = round(tps, 3)
-    res["greedy_store"] = dict(d, hit_rate=round(d["hits"] / max(d["hits"] + d["misses"], 1), 4),
-                               host_link_gbs=round(d["bytes_read"] / dt / 1e9, 2),
-                               gb_per_token=round(d["bytes_read"] / max(len(toks), 1) / 1e9, 3))
-    log(f"config 5 greedy: {res['greedy_tok_s']} tok/s, {json.dumps(res['greedy_store'])}")
-    out, drafted, accepted = [], 0, 0
-
-    def mtp_run(cb):
-        nonlocal drafted, accepted
-        t, drafted, accepted = m.speculative_loop(prompt, new_tokens, depth=1, on_token=cb)
-        return t
-
-    mt, tps, dt, d = timed(mtp_run)
-    res["mtp1"] = {"tok_s": round(tps, 3), "drafted": drafted, "accepted": accepted,
-                   "lossless": mt == toks,
-                   "store": dict(d, hit_rate=round(d["hits"] / max(d["hits"] + d["misses"], 1), 4),
-                                 host_link_gbs=round(d["bytes_read"] / dt / 1e9, 2))}
-    res["evictions"] = m.store_stats()["evictions"]
+    hot = prof.hottest()
+    pinned = m.pin_experts(hot[:n_pin], n_pin * slot)
+    r = {"hbm_budget_gb": round(budget / 1e9, 1), "make_s": round(t_make, 2),
+         "prefill_s": round(t_prefill, 2), "pinned_gb": round(pinned / 1e9, 1),
+         "profiled_experts": len(hot)}
+    r.update(decode_runs(m, "hbm_rest"))
+    r["evictions"] = m.store_stats()["evictions"]
+    res["hbm_rest"] = r
     del m
+    torch.cuda.empty_cache()
+
+    # the streaming store: the hottest pin_frac of the profiled experts
+    # pinned plus a cache of cache_frac of all experts; the prompt is
+    # prefilled through it too
+    n_pin = int(pin_frac * len(hot))
+    n_cache = int(cache_frac * E * nL)
+    sbudget = (n_pin + n_cache) * slot
+    m = U.Model(ctx, C5)
+    m.synthesize_tiered(seed, sbudget, pool_experts, prefetch=True)
+    t0 = time.perf_counter()
+    pinned = m.pin_experts(hot[:n_pin], n_pin * slot)
+    t_pin = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    s = m.session()
+    s.prefill(prompt, want_logits=False)
+    t_prefill = time.perf_counter() - t0
+    del s
+    log(f"config 5 streaming: budget {sbudget / 1e9:.1f} GB, pinned {pinned / 1e9:.1f} GB in "
+        f"{t_pin:.1f} s, prefill {t_prefill:.1f} s")
+    r = {"hbm_budget_gb": round(sbudget / 1e9, 1), "pinned_experts": n_pin,
+         "cache_experts": n_cache, "pinned_gb": round(pinned / 1e9, 1),
+         "cache_gb": round(n_cache * slot / 1e9, 1), "pin_s": round(t_pin, 2),
+         "prefill_s": round(t_prefill, 2)}
+    r.update(decode_runs(m, "streaming"))
+    res["streaming"] = r
+    del m
+    torch.cuda.empty_cache()
     return res
 
 
@@ -610,10 +659,16 @@ def profile_decode(cfg_name: str, prompt_len: int, tokens: int, seed: int = 42) 
     import undertow_amd as U
     from undertow_amd.configs import C1, C4
 
-    cfg = {"c1": C1, "c4": C4}[cfg_name]
+    from undertow_amd.configs import C5
+    cfg = {"c1": C1, "c4": C4, "c5": C5}[cfg_name]
     ctx = U.Context(0)
     m = U.Model(ctx, cfg)
-    m.synthesize(seed, 0.02, U.INT4, U.INT8)
+    if cfg_name == "c5":
+        # full depth behind a 40 GB expert tier fed from a 1,024-expert
+        # pinned host pool: decode steps read routes back and copy misses
+        m.synthesize_tiered(seed, 40 << 30, 1024, prefetch=True)
+    else:
+        m.synthesize(seed, 0.02, U.INT4, U.INT8)
     rng = np.random.default_rng(1)
     prompt = rng.integers(0, cfg["vocab_size"], prompt_len).tolist()
     s = m.session()
@@ -667,7 +722,7 @@ def main():
                          "(fresh windows of a 4 GiB buffer; for kernel traces)")
     ap.add_argument("--mla-only", action="store_true",
                     help="only the config 3 MLA leg (for counter passes; no JSON line)")
-    ap.add_argument("--profile-decode", choices=["c1", "c4"], default=None,
+    ap.add_argument("--profile-decode", choices=["c1", "c4", "c5"], default=None,
                     help="only run the decode-step driver for kernel traces (no JSON line)")
     ap.add_argument("--prompt", type=int, default=512, help="prompt length for --profile-decode")
     ap.add_argument("--tokens", type=int, default=32, help="decode steps for --profile-decode")

@@ -209,8 +209,11 @@ int32_t ut_moe_experts(ut_ctx *ctx, const ut_expert_table *tbl, const int32_t *i
  * object, looked up when the context is created; calls whose working set
  * exceeds it (about top_k * 4 rows * (hidden + inter) * 4 bytes, e.g.
  * top_k 64 at hidden 7168) return UT_ERR_ARG.  Every call on one GPU shares
- * that array, so calls that overlap on a GPU (other streams or contexts)
- * race; calls in stream order do not. */
+ * that array: the first context to call owns it until it is destroyed, and
+ * calls from any other context on that GPU return UT_ERR_STATE.  The
+ * owner's calls are ordered on its stream; a caller that runs them on
+ * several streams itself (ut_ctx_set_stream between overlapping calls
+ * synchronises) must not let two overlap. */
 int32_t ut_moe_experts_noalloc(ut_ctx *ctx, const ut_expert_table *tbl, const int32_t *ids_dev,
                                const float *weights_dev, int64_t rows, int32_t top_k,
                                const float *x_dev, float *out_dev);

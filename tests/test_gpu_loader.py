@@ -126,3 +126,39 @@ def test_bad_checkpoints_are_rejected(ctx, tmp_path):
     with pytest.raises(U.UtError) as ei:
         fresh_model(ctx, ck).load_dir(tmp_path)
     assert ei.value.code == U.runtime.UT_ERR_FORMAT
+
+
+def test_bf16_scales_and_any_payload_dtype(ctx, tmp_path):
+    """read_qtensor (reader.rs:403-444) takes the payload raw whatever its
+    dtype and reads `.scales` through read_f32, which widens BF16 / F16: a
+    converted checkpoint with 16-bit scales and I8 payloads loads, resident
+    and behind the HBM tier, as the same model with the widened scales."""
+    import torch
+    ck = checkpoint(C1, fmt="int4")
+    entries, ref = [], fresh_model(ctx, ck)
+    for i, (name, fmt, shape, payload, scales) in enumerate(ck.tensors()):
+        if fmt == O.F32:
+            entries.append((name, "F32", shape, payload.tobytes()))
+            ref.set_tensor(name, fmt, payload, None, shape)
+            continue
+        if i % 2:
+            t = torch.from_numpy(np.ascontiguousarray(scales, np.float32)).to(torch.bfloat16)
+            raw, wide, dt = t.view(torch.int16).numpy().tobytes(), t.float().numpy(), "BF16"
+        else:
+            h = np.asarray(scales, np.float32).astype(np.float16)
+            raw, wide, dt = h.tobytes(), h.astype(np.float32), "F16"
+        entries.append((name, "I8" if i % 3 == 0 else "U8", (payload.size,), payload.tobytes()))
+        entries.append((name + ".scales", dt, (shape[0],), raw))
+        ref.set_tensor(name, fmt, payload, wide, shape)
+    ref.finalize()
+    write_safetensors(tmp_path / "model.safetensors", entries)
+    ids = prompt_ids(12, ck.spec.vocab_size)
+    want = ref.forward(ids)
+    m = fresh_model(ctx, ck)
+    m.load_dir(tmp_path)
+    assert np.array_equal(m.forward(ids), want)
+    H, I = ck.spec.hidden_size, ck.spec.moe_intermediate_size
+    tiered = fresh_model(ctx, ck)
+    tiered.load_dir_tiered(tmp_path, hbm_budget_bytes=2 * (2 * I * (H // 2) + H * (I // 2) + (2 * I + H) * 4))
+    assert np.array_equal(tiered.forward(ids), want)
+    assert tiered.store_stats()["misses"] > 0

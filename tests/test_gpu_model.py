@@ -235,3 +235,25 @@ def test_handles_release_in_any_order():
     logits = s.prefill([1, 2, 3])  # model and context are still alive
     assert np.isfinite(logits).all()
     s._release()
+
+
+@pytest.mark.parametrize("inter", [96, 160])
+def test_shared_mlp_beside_matrix_core_experts_row_tail(ctx, inter):
+    """Hidden 512 with expert widths of 96 and 160 (I % 64 == 32): prefill
+    chunks and MTP verify steps of 2-4 rows run the routed experts on the
+    matrix cores with the shared MLP in the same launches, whose last
+    workgroups end past I.  Logits within the model bar of the oracle and
+    MTP depth 1-3 equal to greedy."""
+    cfg = dict(C1, hidden_size=512, moe_intermediate_size=inter)
+    ck = checkpoint(cfg, fmt="int4")
+    m, om = gpu_model(ctx, ck), O.Model(ck)
+    prompt = prompt_ids(11, C1["vocab_size"], seed=3)
+    got, want = m.forward(prompt), om.forward(prompt)
+    err = np.abs(got - want)
+    assert err.max() <= 1e-3 and err.mean() <= 1e-4, (err.max(), err.mean())
+    ok = gap_ok(want)
+    assert (got.argmax(1)[ok] == want.argmax(1)[ok]).all()
+    greedy = m.generate_greedy(prompt, 12)
+    assert greedy == om.greedy_decode(prompt, 12)[len(prompt):]
+    for depth in (1, 2, 3):
+        assert m.generate_mtp(prompt, 12, depth=depth)[0] == greedy, depth

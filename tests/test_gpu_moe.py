@@ -533,3 +533,27 @@ def test_kernel_timing(ctx):
     nd, msd = ctx.kernel_time("moe_down")
     ctx.enable_timing(False)
     assert n == 3 and nd == 3 and ms > 0 and msd > 0
+
+
+@pytest.mark.parametrize("I", [96, 160])
+def test_moe_matrix_core_gate_up_row_tail(ctx, I):
+    """The matrix-core gate/up takes 64 h rows per workgroup at 2-4 rows
+    when the routed experts have the launch to themselves; with I % 64 == 32
+    the last workgroup's second tile lies past I and its waves clamp their
+    rows.  Every row equals the one-row call (the dot-product kernels) bit
+    for bit and the oracle within the expert bar."""
+    rng = np.random.default_rng(I)
+    E, H, k = 8, 512, 4
+    tbl, host_w = make_experts(ctx, rng, INT4, E, H, I)
+    for M in (2, 3, 4):
+        ids = np.stack([rng.permutation(E)[:k] for _ in range(M)]).astype(np.int32)
+        w = rng.random((M, k)).astype(np.float32)
+        x = rng.standard_normal((M, H)).astype(np.float32)
+        got = host(tbl.moe_experts(dev(ids), dev(w), dev(x)))
+        assert np.isfinite(got).all(), M
+        want = oracle_moe(INT4, H, I, host_w, ids, w, x)
+        tol = 1e-4 * np.maximum(np.abs(want), 1.0)
+        assert (np.abs(got - want) <= tol).all(), (M, np.abs(got - want).max())
+        for s in range(M):
+            one = host(tbl.moe_experts(dev(ids[s:s + 1]), dev(w[s:s + 1]), dev(x[s:s + 1])))
+            assert np.array_equal(one[0], got[s]), (M, s)

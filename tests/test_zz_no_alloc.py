@@ -59,3 +59,26 @@ def test_noalloc_rejects_working_sets_beyond_its_array(ctx):
         tbl.moe_experts_noalloc(ids, w, x, out)
     assert ei.value.code == U.runtime.UT_ERR_ARG
     assert "exceeds" in str(ei.value)
+
+
+def test_noalloc_refuses_a_second_context_on_the_device(ctx):
+    """The array is one per device: the first context that calls owns it, a
+    second context on the same GPU is refused rather than racing on it, and
+    the owner keeps working."""
+    import torch
+    import undertow_amd as U
+    rng = np.random.default_rng(5)
+    tbl = make_table(ctx, rng, 8, 512, 256)
+    ids = dev(np.stack([rng.permutation(8)[:2] for _ in range(2)]).astype(np.int32))
+    w, x = dev(rng.random((2, 2)).astype(np.float32)), dev(rng.standard_normal((2, 512)).astype(np.float32))
+    out = torch.empty((2, 512), device="cuda:0")
+    tbl.moe_experts_noalloc(ids, w, x, out)  # ctx owns the device's array
+    other = U.Context(0)
+    tbl2 = make_table(other, rng, 8, 512, 256)
+    with pytest.raises(U.UtError) as ei:
+        tbl2.moe_experts_noalloc(ids, w, x, out)
+    assert ei.value.code == U.runtime.UT_ERR_STATE
+    del tbl2, other
+    want = host(tbl.moe_experts(ids, w, x))
+    tbl.moe_experts_noalloc(ids, w, x, out)
+    assert np.array_equal(host(out), want)

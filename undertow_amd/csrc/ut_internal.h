@@ -153,6 +153,8 @@ int32_t device_error_flag(ut_ctx *ctx, int32_t **flag);
 // Looks up this device's copy of the expert block's fixed working array
 // (hipGetSymbolAddress, the device current) into ctx->noalloc_scratch.
 int32_t moe_noalloc_scratch_init(ut_ctx *ctx);
+// Gives up the context's claim on its device's working array (at destroy).
+void moe_noalloc_release(const ut_ctx *ctx);
 // Split-K partials buffer of the context (kSplitKPartBytes), allocated on
 // first use: four rows of the LM head's logits (129,280) over four splits.
 constexpr int64_t kSplitKPartBytes = int64_t(32) << 20;

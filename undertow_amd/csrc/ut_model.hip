@@ -1614,30 +1614,8 @@ struct Stager {
             bytes_read += cnt * 2;
             void *buf = nullptr;
             int b = take(&buf);
-            uint32_t *o = (uint32_t *)buf;
-            for (uint64_t i = 0; i < cnt; i++) {
-                const uint32_t h = halves[(size_t)i];
-                if (bf16) {
-                    o[i] = h << 16;
-                } else {
-                    // IEEE binary16 -> binary32 (exact: every half is a float)
-                    const uint32_t sign = (h & 0x8000u) << 16, ex = (h >> 10) & 0x1F, man = h & 0x3FF;
-                    uint32_t v;
-                    if (ex == 0x1F) {
-                        v = sign | 0x7F800000u | (man << 13);
-                    } else if (ex != 0) {
-                        v = sign | ((ex + 112) << 23) | (man << 13);
-                    } else if (man == 0) {
-                        v = sign;
-                    } else {
-                        int e = -1;
-                        uint32_t m = man;
-                        do { e++; m <<= 1; } while (!(m & 0x400));
-                        v = sign | ((uint32_t)(112 - e) << 23) | ((m & 0x3FF) << 13);
-                    }
-                    o[i] = v;
-                }
-            }
+            if (b < 0) return b;
+            st::widen_halves(halves.data(), cnt, bf16, (uint32_t *)buf);
             UT_TRY(send(b, dst + pos, (size_t)cnt * 4));
             pos += cnt;
         }
@@ -1688,15 +1666,20 @@ int32_t load_dir_all(ut_model *m, const char *dir, bool skip_experts, int64_t *b
             pl.pb = it.d0 * 4;
             total += al(pl.pb);
         } else if ((pl.scales = idx.find(it.name + ".scales"))) {
+            // read_qtensor (reader.rs:410-430): the payload is read raw
+            // whatever its dtype and its format inferred from the byte count;
+            // the scales are read as f32 (F32, or BF16 / F16 widened exactly)
             const st::Entry *sc = pl.scales;
-            if (sc->dtype != st::ST_F32 || sc->shape.size() != 1 || sc->shape[0] != it.d0) {
+            const bool sc_floaty =
+                sc->dtype == st::ST_F32 || sc->dtype == st::ST_BF16 || sc->dtype == st::ST_F16;
+            if (!sc_floaty) {
+                set_error(ctx, "%s.scales: cannot convert the tensor to f32", it.name.c_str());
+                return UT_ERR_FORMAT;
+            }
+            if (sc->shape.size() != 1 || sc->shape[0] != it.d0) {
                 set_error(ctx, "shape mismatch for %s.scales: expected [%lld]", it.name.c_str(),
                           (long long)it.d0);
                 return UT_ERR_SHAPE;
-            }
-            if (e->dtype != st::ST_U8 && e->dtype != st::ST_I8) {
-                set_error(ctx, "%s: quantized payload must be U8", it.name.c_str());
-                return UT_ERR_FORMAT;
             }
             if ((int64_t)e->nbytes == payload_bytes(UT_FMT_INT8, it.d0, it.d1)) pl.fmt = UT_FMT_INT8;
             else if ((int64_t)e->nbytes == payload_bytes(UT_FMT_INT4, it.d0, it.d1)) pl.fmt = UT_FMT_INT4;
@@ -1759,8 +1742,7 @@ int32_t load_dir_all(ut_model *m, const char *dir, bool skip_experts, int64_t *b
                 UT_TRY(sg.raw(idx.shards[(size_t)pl.data->shard], pl.data->offset, pl.data->nbytes, p));
                 p += al(pl.pb);
                 q->scales = (float *)p;
-                UT_TRY(sg.raw(idx.shards[(size_t)pl.scales->shard], pl.scales->offset,
-                              pl.scales->nbytes, p));
+                UT_TRY(fill_f32(pl.scales, (float *)p));
                 p += al(it.d0 * 4);
             }
             continue;

@@ -22,6 +22,7 @@
 //                  (k_moe_combine_norm: also the next rmsnorm + digits)
 // Every expert's weights are read once per pass whatever rows chose it;
 // the row dimension rides along in the same instructions.
+#include <mutex>
 #include "ut_gemv_core.h"
 #include "ut_moe.h"
 #include "ut_gemv_mfma.h"
@@ -2099,6 +2100,36 @@ int32_t moe_experts_check(ut_ctx *ctx, const char *fn, const ut_expert_table *tb
 constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;
 static __device__ __align__(256) unsigned char noalloc_scratch[kNoAllocScratchBytes];
 
+// The context that owns each device's array: the first to call
+// ut_moe_experts_noalloc on that device, until it is destroyed.  Calls from
+// any other context on the device are refused (UT_ERR_STATE) instead of
+// racing on the array; one context orders its calls on its stream.
+namespace {
+constexpr int kNoAllocMaxDevices = 64;
+std::mutex g_noalloc_mu;
+const ut_ctx *g_noalloc_owner[kNoAllocMaxDevices] = {};
+
+int32_t noalloc_claim(ut_ctx *ctx) {
+    if (ctx->device < 0 || ctx->device >= kNoAllocMaxDevices) return UT_ERR_ARG;
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    const ut_ctx *&o = g_noalloc_owner[ctx->device];
+    if (!o) o = ctx;
+    if (o != ctx) {
+        set_error(ctx, "ut_moe_experts_noalloc: device %d's working array belongs to another "
+                       "context; calls from two contexts would race on it",
+                  ctx->device);
+        return UT_ERR_STATE;
+    }
+    return UT_OK;
+}
+}  // namespace
+
+void ut::moe_noalloc_release(const ut_ctx *ctx) {
+    if (ctx->device < 0 || ctx->device >= kNoAllocMaxDevices) return;
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    if (g_noalloc_owner[ctx->device] == ctx) g_noalloc_owner[ctx->device] = nullptr;
+}
+
 int32_t ut::moe_noalloc_scratch_init(ut_ctx *ctx) {
     void *p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(noalloc_scratch));
@@ -2156,6 +2187,7 @@ int32_t ut_moe_experts_noalloc(ut_ctx *ctx, const ut_expert_table *tbl, const in
                   kNoAllocScratchBytes);
         return UT_ERR_ARG;
     }
+    UT_TRY(noalloc_claim(ctx));
     if (rows == 0) return UT_OK;
     return moe_experts_rows(ctx, tbl, ids_dev, weights_dev, rows, top_k, x_dev, out_dev,
                             ctx->noalloc_scratch, ctx->dev_err);

@@ -337,6 +337,7 @@ void ut::ctx_release(ut_ctx *ctx) {
     if (!ctx || --ctx->refs > 0) return;
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
+    moe_noalloc_release(ctx);
     for (auto &p : ctx->pending) {
         (void)hipEventDestroy(p.start);
         (void)hipEventDestroy(p.stop);

@@ -5,7 +5,7 @@
 // expert of a layer, `dense.safetensors` with the rest, and
 // `model.safetensors.index.json` mapping tensor names to shard files; or a
 // single `model.safetensors`.  Quantized weights are `<name>` (U8 payload)
-// plus `<name>.scales` (F32, one per output row).
+// plus `<name>.scales` (one per output row: F32, or BF16 / F16 read as f32).
 //
 // Headers are untrusted input, validated as undertow-io's parse_header does
 // (undertow-io/src/reader.rs:78-143): every entry needs a known dtype, a
@@ -76,6 +76,15 @@ bool open_dir(const std::string &dir, Index &idx, std::string &err);
 
 // pread of [offset, offset + n) from a shard, retried until complete.
 bool read_at(const Shard &s, void *dst, uint64_t n, uint64_t offset, std::string &err);
+
+// decode_f32 of a 16-bit float run (reader.rs:256-276): n bf16 or f16
+// values widened exactly to f32 bits (every half is a float).
+void widen_halves(const uint16_t *src, uint64_t n, bool bf16, uint32_t *dst);
+
+// A tensor's elements as f32 into dst (F32 read as is, BF16 / F16 widened),
+// staging halves through `tmp`; false (err set) for other dtypes.
+bool read_f32_at(const Shard &s, const Entry &e, float *dst, std::vector<uint16_t> &tmp,
+                 std::string &err);
 
 }  // namespace st
 }  // namespace ut

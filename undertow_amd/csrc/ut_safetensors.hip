@@ -353,6 +353,46 @@ bool read_at(const Shard &s, void *dst, uint64_t n, uint64_t offset, std::string
     return true;
 }
 
+void widen_halves(const uint16_t *src, uint64_t n, bool bf16, uint32_t *dst) {
+    for (uint64_t i = 0; i < n; i++) {
+        const uint32_t h = src[i];
+        if (bf16) {
+            dst[i] = h << 16;
+            continue;
+        }
+        // IEEE binary16 -> binary32
+        const uint32_t sign = (h & 0x8000u) << 16, ex = (h >> 10) & 0x1F, man = h & 0x3FF;
+        uint32_t v;
+        if (ex == 0x1F) {
+            v = sign | 0x7F800000u | (man << 13);
+        } else if (ex != 0) {
+            v = sign | ((ex + 112) << 23) | (man << 13);
+        } else if (man == 0) {
+            v = sign;
+        } else {
+            int e = -1;
+            uint32_t m = man;
+            do { e++; m <<= 1; } while (!(m & 0x400));
+            v = sign | ((uint32_t)(112 - e) << 23) | ((m & 0x3FF) << 13);
+        }
+        dst[i] = v;
+    }
+}
+
+bool read_f32_at(const Shard &s, const Entry &e, float *dst, std::vector<uint16_t> &tmp,
+                 std::string &err) {
+    if (e.dtype == ST_F32) return read_at(s, dst, e.nbytes, e.offset, err);
+    if (e.dtype != ST_BF16 && e.dtype != ST_F16) {
+        err = s.path + ": cannot convert the tensor to f32";
+        return false;
+    }
+    const uint64_t n = e.nbytes / 2;
+    tmp.resize((size_t)n);
+    if (!read_at(s, tmp.data(), e.nbytes, e.offset, err)) return false;
+    widen_halves(tmp.data(), n, e.dtype == ST_BF16, (uint32_t *)dst);
+    return true;
+}
+
 Index::~Index() {
     for (auto &s : shards)
         if (s.fd >= 0) ::close(s.fd);

@@ -110,6 +110,7 @@ private:
     std::vector<char> dirty_;
     // sources
     st::Index idx_;
+    std::vector<uint16_t> halves_;  // 16-bit scales before widening
     void *stage_[2] = {nullptr, nullptr};
     hipEvent_t stage_done_[2] = {nullptr, nullptr};
     bool stage_busy_[2] = {false, false};

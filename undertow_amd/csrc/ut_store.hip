@@ -107,10 +107,16 @@ int32_t ExpertStore::attach_disk(const std::string &dir) {
                     return UT_ERR_NOT_FOUND;
                 }
                 const int64_t out = i == 2 ? H_ : I_;
-                const bool ok = fmt_ == UT_FMT_F32
-                                    ? (p->dtype == st::ST_F32 && (int64_t)p->nbytes == len_[i])
-                                    : (s && s->dtype == st::ST_F32 && (int64_t)s->nbytes == out * 4 &&
-                                       (int64_t)p->nbytes == len_[i]);
+                // read_qtensor (reader.rs:410-430): a quantized payload is
+                // taken raw by its byte count, its scales as f32 (F32, or
+                // BF16 / F16 widened when loaded)
+                const bool ok =
+                    fmt_ == UT_FMT_F32
+                        ? (p->dtype == st::ST_F32 && (int64_t)p->nbytes == len_[i])
+                        : (s && s->shape.size() == 1 && s->shape[0] == out &&
+                           (s->dtype == st::ST_F32 || s->dtype == st::ST_BF16 ||
+                            s->dtype == st::ST_F16) &&
+                           (int64_t)p->nbytes == len_[i]);
                 if (!ok) {
                     set_error(ctx_, "%s: not a %s expert of [%lld, %lld] (all routed experts of a "
                                     "store share one format)",
@@ -274,8 +280,8 @@ int32_t ExpertStore::load_into(int slot, int64_t layer, int64_t e) {
             }
             if (fmt_ != UT_FMT_F32) {
                 const st::Entry *sc = idx_.find(n + ".scales");
-                if (!sc || !st::read_at(idx_.shards[(size_t)sc->shard], stg + off_[3 + i],
-                                        sc->nbytes, sc->offset, err)) {
+                if (!sc || !st::read_f32_at(idx_.shards[(size_t)sc->shard], *sc,
+                                            (float *)(stg + off_[3 + i]), halves_, err)) {
                     set_error(ctx_, "%s", sc ? err.c_str() : ("tensor not found: " + n + ".scales").c_str());
                     return sc ? UT_ERR_IO : UT_ERR_NOT_FOUND;
                 }
