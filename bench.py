@@ -412,6 +412,81 @@ def cpu_baseline(cfg2, seconds=10.0):
 
 
 # ------------------------------------------------------------------ MTP --
+def model_step_bytes(cfg, rows, unique, ctx_len, expert_bits=4, dense_bits=8, mtp=False):
+    """Algorithmic HBM bytes of one forward step of `rows` token rows over the
+    main model (and, with mtp, of one MTP-head row): every weight the step
+    reads once (int8 dense matrices with f32 row scales, int4 routed
+    experts, f32 router gates and norms), `unique` routed experts per MoE
+    layer, the compressed KV cache of every layer read once (split bf16 hi/lo
+    rows, 2,304 B per position at latent 512 + rope 64), and the activations
+    ignored (a few hundred KB)."""
+    H, V, L = cfg["hidden_size"], cfg["vocab_size"], cfg["num_hidden_layers"]
+    heads, nope, rope, vh = (cfg["num_attention_heads"], cfg["qk_nope_head_dim"],
+                             cfg["qk_rope_head_dim"], cfg["v_head_dim"])
+    ql, kl, I, Id = cfg["q_lora_rank"], cfg["kv_lora_rank"], cfg["moe_intermediate_size"], \
+        cfg["intermediate_size"]
+    E = cfg["n_routed_experts"]
+
+    def mat(o, i, bits):
+        return o * ((i * bits + 7) // 8) + (o * 4 if bits < 32 else 0)
+
+    attn = (mat(ql, H, dense_bits) + mat(kl + rope, H, dense_bits) +
+            mat(heads * (nope + rope), ql, dense_bits) + mat(heads * (nope + vh), kl, dense_bits) +
+            mat(H, heads * vh, dense_bits) + 4 * (2 * H + ql + kl))
+    kv = ctx_len * (kl + rope) * 4
+    expert = 2 * mat(I, H, expert_bits) + mat(H, I, expert_bits)
+    Is = I * cfg["n_shared_experts"]
+    shared = 2 * mat(Is, H, dense_bits) + mat(H, Is, dense_bits) if Is else 0
+    moe = unique * expert + shared + mat(E, H, 32) + 4 * E
+    dense = 2 * mat(Id, H, dense_bits) + mat(H, Id, dense_bits)
+    nd = cfg["first_k_dense_replace"]
+    main = L * (attn + kv) + nd * dense + (L - nd) * moe + mat(V, H, dense_bits) + 4 * H
+    if not mtp:
+        return main
+    head = mat(H, 2 * H, dense_bits) + 4 * 2 * H + attn + kv + moe + mat(V, H, dense_bits) + 4 * H
+    return head
+
+
+def model_roofline(m, cfg, prompt, new_tokens, greedy_tok_s, steps=16):
+    """HBM roofline of the DeepSeek-V3-width model's steps: a one-row decode
+    step (from the greedy rate: the loop queues each step before reading the
+    last token back, so it runs at the GPU's pace) and isolated two- and
+    four-row verify steps (host-timed, one readback per step).  Algorithmic
+    bytes per model_step_bytes at the run's mean context; one row routes to
+    exactly top_k experts per MoE layer, R rows to between top_k and
+    R * top_k of them, so the verify figures take top_k (a floor on the
+    bytes, hence on the achieved rate) and also give the ceiling."""
+    k = cfg["num_experts_per_tok"]
+    T = len(prompt) + new_tokens // 2
+    b1 = model_step_bytes(cfg, 1, k, T)
+    us1 = 1e6 / greedy_tok_s
+    out = {"peak_gbs": HBM_PEAK_GBS, "unit": "GB/s",
+           "decode": {"bytes": b1, "us_per_step": round(us1, 1),
+                      "achieved": round(b1 / us1 / 1e3, 1),
+                      "frac": round(b1 / us1 / 1e3 / HBM_PEAK_GBS, 4)}}
+    s = m.session()
+    s.prefill(prompt, want_logits=False)
+    nxt = s.last_argmax[-1]
+    for rows in (2, 4):
+        s.prefill([nxt] * rows, want_logits=False)  # warm-up of this shape
+        nxt = s.last_argmax[-1]
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            s.prefill([nxt] * rows, want_logits=False)
+            nxt = s.last_argmax[-1]
+        us = (time.perf_counter() - t0) / steps * 1e6
+        T = s.position
+        lo = model_step_bytes(cfg, rows, k, T)
+        hi = model_step_bytes(cfg, rows, min(rows * k, cfg["n_routed_experts"]), T)
+        out[f"verify{rows}"] = {"bytes_floor": lo, "bytes_ceiling": hi, "us_per_step": round(us, 1),
+                                "achieved_floor": round(lo / us / 1e3, 1),
+                                "frac_floor": round(lo / us / 1e3 / HBM_PEAK_GBS, 4),
+                                "frac_ceiling": round(hi / us / 1e3 / HBM_PEAK_GBS, 4)}
+    del s
+    out["mtp_head_bytes"] = model_step_bytes(cfg, 1, k, T, mtp=True)
+    return out
+
+
 def mtp_bench(U, ctx, cfg, prompt_len, new_tokens, depths, seed, expert_fmt, dense_fmt):
     m = U.Model(ctx, cfg)
     t0 = time.perf_counter()
@@ -434,6 +509,8 @@ def mtp_bench(U, ctx, cfg, prompt_len, new_tokens, depths, seed, expert_fmt, den
     greedy = m.generate_greedy(prompt, new_tokens)
     dt = time.perf_counter() - t0 - t_prefill
     res["greedy_tok_s"] = len(greedy) / dt
+    if cfg["hidden_size"] >= 4096 and cfg["n_routed_experts"] >= 64:
+        res["roofline"] = model_roofline(m, cfg, prompt, new_tokens, res["greedy_tok_s"])
     # the same decode with one-row steps replayed from a captured graph
     before = m.graph_stats()
     m.enable_graphs(True)

@@ -382,6 +382,16 @@ int32_t ut_model_expert_usage(ut_model *m, int64_t *counts, int64_t n);
 int32_t ut_model_synthesize(ut_model *m, uint64_t seed, float init_std, int32_t expert_fmt,
                             int32_t dense_fmt);
 int64_t ut_model_device_bytes(const ut_model *m);
+/* LoadOptions::kv_budget_bytes (undertow-core/src/model.rs:36-61) and the
+ * effective context it gives (adapters/undertow-deepseek-moe/src/
+ * loader.rs:311-325, Model::max_context at model.rs:362-364): per position
+ * num_hidden_layers * (kv_lora_rank + qk_rope_head_dim) * 4 bytes plus,
+ * with an MTP head, hidden_size * 4 + 8; the context is
+ * min(max_position_embeddings, max(budget / that, 1)).  Sessions created
+ * afterwards hold that many positions and report UT_ERR_CONTEXT_OVERFLOW
+ * beyond it.  A negative budget removes the bound; 0 is UT_ERR_ARG. */
+int32_t ut_model_set_kv_budget(ut_model *m, int64_t kv_budget_bytes);
+int64_t ut_model_max_context(const ut_model *m);
 void    ut_model_free(ut_model *m);
 
 /* InferenceSession (model.rs:407-564).  path: 0 = Auto, 1 = Absorbed,
@@ -389,6 +399,15 @@ void    ut_model_free(ut_model *m);
  * form for every path (the reference's two paths agree to < 1e-4,
  * attention.rs:362-422). */
 int32_t ut_session_create(ut_model *m, int32_t path, ut_session **out);
+/* A session whose work runs on `ctx` (its stream, scratch and staging), a
+ * context on the model's device other than the model's own, so that
+ * sessions on several threads share one model without sharing a stream:
+ * the reference's Session per thread over an Arc'd model
+ * (undertow-bench/tests/pipeline.rs:226-249).  ctx NULL: the model's.
+ * The session holds a reference to ctx until it is freed.  A model whose
+ * routed experts sit behind the HBM tier serves sessions on its own
+ * context only (UT_ERR_STATE). */
+int32_t ut_session_create_on(ut_model *m, ut_ctx *ctx, int32_t path, ut_session **out);
 void    ut_session_free(ut_session *s);
 /* InferenceSession::prefill (model.rs:447-547): runs ids[0..n) through the
  * model, extends the KV cache.  logits_host [n, vocab] may be NULL;

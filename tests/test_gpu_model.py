@@ -257,3 +257,78 @@ def test_shared_mlp_beside_matrix_core_experts_row_tail(ctx, inter):
     assert greedy == om.greedy_decode(prompt, 12)[len(prompt):]
     for depth in (1, 2, 3):
         assert m.generate_mtp(prompt, 12, depth=depth)[0] == greedy, depth
+
+
+def test_concurrent_sessions_are_isolated(ctx, ref):
+    """Sessions on four threads, each on its own context (stream, scratch,
+    staging), share one resident model and run three forwards each with
+    logits bit-identical to a forward on the model's own context
+    (undertow-bench/tests/pipeline.rs:226-249)."""
+    import threading
+    import undertow_amd as U
+    ck = checkpoint(C1, fmt="int4")
+    m = gpu_model(ctx, ck)
+    ids = [t % C1["vocab_size"] for t in ref["full_ids"]] + prompt_ids(12, C1["vocab_size"])
+    want = m.forward(ids)
+    ctxs = [U.Context(0, bind_torch_stream=False) for _ in range(4)]
+    errors = []
+
+    def worker(c):
+        try:
+            for _ in range(3):
+                got = m.session(ctx=c).prefill(ids)
+                if not np.array_equal(got, want):
+                    errors.append(float(np.abs(got - want).max()))
+        except Exception as e:  # reported below, on the main thread
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=worker, args=(c,)) for c in ctxs]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+
+
+def test_kv_budget_lowers_effective_context(ctx):
+    """LoadOptions::kv_budget_bytes shrinks the usable context
+    (loader.rs:311-325); a forward past the lowered bound is a typed
+    overflow naming it, and forwards within it work
+    (undertow-bench/tests/pipeline.rs:463-483)."""
+    import undertow_amd as U
+    ck = checkpoint(C1, fmt="int4")
+    m = gpu_model(ctx, ck)
+    full = m.max_context
+    assert full == ck.spec.max_position_embeddings
+    m.set_kv_budget(16 * 1024)
+    s = ck.spec
+    per = s.num_hidden_layers * (s.kv_lora_rank + s.qk_rope_head_dim) * 4 + s.hidden_size * 4 + 8
+    eff = m.max_context
+    assert eff == min(full, max(16 * 1024 // per, 1)) and eff < full
+    long = [i % s.vocab_size for i in range(eff + 1)]
+    with pytest.raises(U.ContextOverflow) as ei:
+        m.forward(long)
+    assert ei.value.code == U.runtime.UT_ERR_CONTEXT_OVERFLOW and f"> {eff}" in str(ei.value)
+    a = m.forward(long[:min(eff, 8)])
+    m.set_kv_budget(None)
+    assert m.max_context == full
+    assert np.array_equal(a, m.forward(long[:min(eff, 8)]))
+    # a greedy stream stops at the lowered window
+    m.set_kv_budget(16 * 1024)
+    assert len(m.generate_greedy(long[:eff - 2], 50)) <= 3
+    with pytest.raises(U.UtError):
+        m.set_kv_budget(0)
+
+
+@pytest.mark.parametrize("fmt,floor,min_prefix", [("int8", 0.85, 6), ("int4", 0.55, 3)])
+def test_quantized_agreement_floors(ctx, ref, fmt, floor, min_prefix):
+    """pipeline.rs:137-177 on the GPU: the converted oracle-tiny fixture
+    keeps the reference's teacher-forcing agreement and greedy-prefix
+    floors against the transformers golden."""
+    from test_oracle_quant_agreement import agreement
+    m = gpu_model(ctx, checkpoint(fmt=fmt))
+    max_new = len(ref["full_ids"]) - len(ref["prompt_ids"])
+    rate, prefix = agreement(ref, m.forward(ref["full_ids"]),
+                             m.generate_greedy(ref["prompt_ids"], max_new))
+    assert rate >= floor, (fmt, rate)
+    assert prefix >= min_prefix, (fmt, prefix)

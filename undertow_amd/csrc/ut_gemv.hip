@@ -3,6 +3,7 @@
 // avx512.rs:197-267): activation digitisation, the fast skinny GEMV
 // (int4 / int8 / f32 weights, 1..4 activation rows per pass) and a generic
 // kernel for shapes the fast one does not take.
+#include <atomic>
 #include "ut_gemv_core.h"
 #include "ut_moe.h"
 #include "ut_ops.h"
@@ -704,18 +705,19 @@ static void splitk_plan(int32_t fmt, int64_t O, int64_t K, int rows_per_wg, int6
 // Workgroups of k_gemv<FMT, M> resident on the whole chip (occupancy query,
 // once per instantiation).
 template <int FMT, int M> static int64_t gemv_resident_m(ut_ctx *ctx) {
-    static int per_cu = 0;
-    if (per_cu == 0) {
-        int n = 0;
+    // sessions on several threads may ask at once: the same answer either way
+    static std::atomic<int> per_cu{0};
+    int n = per_cu.load(std::memory_order_relaxed);
+    if (n == 0) {
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, (const void *)k_gemv<FMT, M>,
                                                          kGemvThreads, 0) != hipSuccess ||
             n < 1) {
             (void)hipGetLastError();
             n = 2;
         }
-        per_cu = n;
+        per_cu.store(n, std::memory_order_relaxed);
     }
-    return (int64_t)per_cu * ctx->multiprocessors;
+    return (int64_t)n * ctx->multiprocessors;
 }
 template <int FMT> static int64_t gemv_resident(ut_ctx *ctx, int mrows) {
     switch (mrows) {

@@ -87,6 +87,9 @@ struct ut_model {
     int64_t device_bytes = 0;
     int device = 0;
     int refs = 1;  // the creator + one per live session
+    // a session KV budget in bytes (LoadOptions::kv_budget_bytes), -1: none;
+    // it lowers the positions a session may hold (ut_model_max_context)
+    int64_t kv_budget = -1;
 };
 
 namespace {
@@ -112,6 +115,9 @@ struct Workspace {
 
 struct ut_session {
     ut_model *m = nullptr;
+    // the context (stream, scratch, pinned staging) the session's work runs
+    // on: the model's, or one of the caller's on the same device
+    ut_ctx *ctx = nullptr;
     int32_t path = 0;
     int64_t pos = 0;
     std::vector<KvCache> kv;
@@ -334,7 +340,7 @@ int32_t ws_reserve(ut_session *s, int64_t rows) {
     if (rows <= w.rows) return UT_OK;
     ut_model *m = s->m;
     const ut_model_config &c = m->c;
-    ut_ctx *ctx = m->ctx;
+    ut_ctx *ctx = s->ctx;
     const int64_t H = c.hidden_size, heads = c.num_attention_heads;
     const int64_t qh = c.qk_nope_head_dim + c.qk_rope_head_dim, Lr = c.kv_lora_rank;
     const int64_t R = rows < 4 ? 4 : rows;
@@ -427,7 +433,7 @@ int32_t ws_reserve(ut_session *s, int64_t rows) {
 // ------------------------------------------------------------ forward ---
 int32_t mm(ut_session *s, const ut_qtensor *w, const float *x, int64_t M, float *out, int64_t ldo,
            int accumulate = 0) {
-    return matmul_dev(s->m->ctx, w, x, M, out, ldo, accumulate, s->ws.digits);
+    return matmul_dev(s->ctx, w, x, M, out, ldo, accumulate, s->ws.digits);
 }
 
 // Digit forms the given weights need from one shared activation.
@@ -453,7 +459,7 @@ int32_t norm_dig(ut_session *s, const float *x, int64_t ldx, const float *w, int
                  int64_t rows, float *out, int64_t ldo, void *buf, int flags, XDigits *xd) {
     const ut_model_config &c = s->m->c;
     *xd = xdigits_view(buf, rows, n, flags);
-    return launch_rmsnorm_digitize(s->m->ctx, x, ldx, rows, n, w, c.rms_norm_eps, out, ldo, *xd,
+    return launch_rmsnorm_digitize(s->ctx, x, ldx, rows, n, w, c.rms_norm_eps, out, ldo, *xd,
                                    flags);
 }
 
@@ -488,7 +494,7 @@ int32_t mlp_add(ut_session *s, const MlpW &w, const float *x, const XDigits &xd,
         c.plan = &mp;
         c.init = init ? init + s0 * c.H : nullptr;
         c.next = next;
-        UT_TRY(moe_pass(m->ctx, c, s->ws.moe));
+        UT_TRY(moe_pass(s->ctx, c, s->ws.moe));
     }
     return UT_OK;
 }
@@ -500,7 +506,7 @@ int32_t mlp_add(ut_session *s, const MlpW &w, const float *x, const XDigits &xd,
 // slots and the layer's pointer table published, all in stream order.
 int32_t tiered_experts(ut_session *s, const LayerW &L, const float *resid, int64_t M) {
     ut_model *m = s->m;
-    ut_ctx *ctx = m->ctx;
+    ut_ctx *ctx = s->ctx;
     const ut_model_config &c = m->c;
     const int64_t E = c.n_routed_experts, k = c.num_experts_per_tok, H = c.hidden_size;
     const int64_t n = M * k;
@@ -560,10 +566,10 @@ int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
                 UT_TRY(mm(s, L.gate, x + s0 * H, M, s->ws.rlogits, E));
                 gparts = SplitKPartials{};
             } else if (rowdot_f32_ok(L.gate, M) && ((uintptr_t)(x + s0 * H) & 15) == 0) {
-                UT_TRY(launch_rowdot_f32(m->ctx, L.gate, x + s0 * H, M, s->ws.rlogits, E));
+                UT_TRY(launch_rowdot_f32(s->ctx, L.gate, x + s0 * H, M, s->ws.rlogits, E));
                 gparts = SplitKPartials{};
             } else {
-                UT_TRY(gemv(m->ctx, ga));
+                UT_TRY(gemv(s->ctx, ga));
             }
         }
         const int64_t slots = moe_slots(M, k, E, -1);
@@ -572,7 +578,7 @@ int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
             // the HBM tier: route, read the choices back, bring missing
             // experts into their slots (TieredStore::get_expert), then the
             // expert launches plan from the ids like a resident table
-            UT_TRY(launch_route(m->ctx, s->ws.rlogits, L.bias, M, E, k, (int)c.n_group,
+            UT_TRY(launch_route(s->ctx, s->ws.rlogits, L.bias, M, E, k, (int)c.n_group,
                                 (int)c.topk_group, c.norm_topk_prob, c.routed_scaling_factor,
                                 s->ws.rids, s->ws.rw));
             UT_TRY(tiered_experts(s, L, s->ws.x + s0 * H, M));
@@ -586,7 +592,7 @@ int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
         const bool gate_plans = !m->store && gparts.ks <= 1 && (int64_t)M * k <= 64 &&
                                 L.expert_fmt != UT_FMT_F32 && !mfma_rows;
         if (!gate_plans && !m->store)
-            UT_TRY(launch_route_plan(m->ctx, s->ws.rlogits, &gparts, L.bias, M, E, k,
+            UT_TRY(launch_route_plan(s->ctx, s->ws.rlogits, &gparts, L.bias, M, E, k,
                                      (int)c.n_group, (int)c.topk_group, c.norm_topk_prob,
                                      c.routed_scaling_factor, s->ws.rids, s->ws.rw,
                                      (const void *const *)L.experts.gate_w,
@@ -632,7 +638,7 @@ int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
             mc.shared_scratch = (char *)s->ws.moe + lay.total;
         }
         mc.next = next;
-        UT_TRY(moe_pass(m->ctx, mc, s->ws.moe));
+        UT_TRY(moe_pass(s->ctx, mc, s->ws.moe));
     }
     return UT_OK;
 }
@@ -644,7 +650,7 @@ int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
                     bool *post_done = nullptr) {
     if (post_done) *post_done = false;
     ut_model *m = s->m;
-    ut_ctx *ctx = m->ctx;
+    ut_ctx *ctx = s->ctx;
     const ut_model_config &c = m->c;
     Workspace &w = s->ws;
     const int64_t heads = c.num_attention_heads, nope = c.qk_nope_head_dim,
@@ -765,7 +771,7 @@ int input_flags(const LayerW &L) { return dig_flags({L.q_a, L.q_proj, L.kv_a}); 
 int32_t run_layer(ut_session *s, const LayerW &L, float *x, int64_t rows, KvCache &kv,
                   const XDigits *pre = nullptr, const NormNext *next = nullptr) {
     ut_model *m = s->m;
-    ut_ctx *ctx = m->ctx;
+    ut_ctx *ctx = s->ctx;
     const ut_model_config &c = m->c;
     const int64_t H = c.hidden_size;
     Workspace &w = s->ws;
@@ -798,7 +804,7 @@ int32_t run_layer(ut_session *s, const LayerW &L, float *x, int64_t rows, KvCach
 
 int32_t check_flags(ut_session *s) {
     // called after a stream sync: the sticky expert-id error flag
-    ut_ctx *ctx = s->m->ctx;
+    ut_ctx *ctx = s->ctx;
     int32_t f = 0;
     UT_CHECK_HIP(ctx, hipMemcpy(&f, s->ws.err, 4, hipMemcpyDeviceToHost));
     if (f) {
@@ -809,7 +815,7 @@ int32_t check_flags(ut_session *s) {
 }
 
 int32_t upload_ids(ut_session *s, const int32_t *ids, int64_t n) {
-    ut_ctx *ctx = s->m->ctx;
+    ut_ctx *ctx = s->ctx;
     void *pin = nullptr;
     UT_TRY(pinned_acquire(ctx, (size_t)n * 4, &pin));
     // the pinned buffer may still feed an earlier copy: order behind the stream
@@ -825,7 +831,7 @@ int32_t upload_ids(ut_session *s, const int32_t *ids, int64_t n) {
 // s->tokens (the caller records them once it has read them back).
 int32_t prefill_dev(ut_session *s, const int32_t *ids, int64_t n, const int32_t *ids_dev = nullptr) {
     ut_model *m = s->m;
-    ut_ctx *ctx = m->ctx;
+    ut_ctx *ctx = s->ctx;
     const ut_model_config &c = m->c;
     if (n <= 0) {
         set_error(ctx, "empty prompt");
@@ -881,7 +887,7 @@ int32_t prefill_dev(ut_session *s, const int32_t *ids, int64_t n, const int32_t 
 }
 
 int32_t read_argmax(ut_session *s, int64_t n, int32_t *out) {
-    ut_ctx *ctx = s->m->ctx;
+    ut_ctx *ctx = s->ctx;
     void *pin = nullptr;
     UT_TRY(pinned_acquire(ctx, (size_t)n * 4, &pin));
     UT_CHECK_HIP(ctx, hipMemcpyAsync(pin, s->ws.am, (size_t)n * 4, hipMemcpyDeviceToHost, ctx->stream));
@@ -895,7 +901,7 @@ int32_t read_argmax(ut_session *s, int64_t n, int32_t *out) {
 // sticky error flag, into the session's pinned readback slot; `ready` is
 // recorded behind them, so later launches need not wait for the host.
 int32_t readback_enqueue(ut_session *s, const int32_t *dev, int64_t n, int64_t slot_off = 0) {
-    ut_ctx *ctx = s->m->ctx;
+    ut_ctx *ctx = s->ctx;
     int32_t *back = s->pin + kPinIds;
     if (slot_off + n + 1 > kPinBack) {
         set_error(ctx, "readback of %lld ints exceeds the staging slot", (long long)n);
@@ -909,7 +915,7 @@ int32_t readback_enqueue(ut_session *s, const int32_t *dev, int64_t n, int64_t s
 
 // Waits for the last readback; out <- the ints at slot_off.
 int32_t readback_wait(ut_session *s, int64_t n, int32_t *out, int64_t slot_off = 0) {
-    ut_ctx *ctx = s->m->ctx;
+    ut_ctx *ctx = s->ctx;
     UT_CHECK_HIP(ctx, hipEventSynchronize(s->ready));
     const int32_t *back = s->pin + kPinIds;
     if (back[kPinBack - 1]) {
@@ -925,7 +931,7 @@ int32_t readback_wait(ut_session *s, int64_t n, int32_t *out, int64_t slot_off =
 // loops read back, and so wait, after every step).
 // Uploads queued in one step use disjoint offsets of the slot.
 int32_t upload_slot(ut_session *s, int32_t *dev, const int32_t *ids, int64_t n, int64_t off = 0) {
-    ut_ctx *ctx = s->m->ctx;
+    ut_ctx *ctx = s->ctx;
     if (off + n > kPinIds) {
         set_error(ctx, "upload of %lld ids exceeds the staging slot", (long long)n);
         return UT_ERR_ARG;
@@ -954,7 +960,7 @@ int32_t draft_rows_dev(ut_session *s, const int32_t *host_ids, int in_slot,
                        const float *hidden_rows, int64_t rows, int out_slot,
                        const int32_t *dev_ids = nullptr) {
     ut_model *m = s->m;
-    ut_ctx *ctx = m->ctx;
+    ut_ctx *ctx = s->ctx;
     const ut_model_config &c = m->c;
     Workspace &w = s->ws;
     const int64_t H = c.hidden_size, V = c.vocab_size;
@@ -1209,7 +1215,7 @@ struct Emit {
 // growth, happens there).
 bool graph_ok(const ut_session *s, int64_t eager_steps) {
     const ut_model *m = s->m;
-    return m->graphs && !s->graph_failed && !m->store && !m->ctx->timing && eager_steps >= 1;
+    return m->graphs && !s->graph_failed && !m->store && !s->ctx->timing && eager_steps >= 1;
 }
 
 // Captures the launches of body() (a step of the session) into *exec.  The
@@ -1223,7 +1229,7 @@ bool graph_ok(const ut_session *s, int64_t eager_steps) {
 template <typename Body>
 int32_t capture_body(ut_session *s, Body body, hipGraphExec_t *exec) {
     ut_model *m = s->m;
-    ut_ctx *ctx = m->ctx;
+    ut_ctx *ctx = s->ctx;
     const hipStream_t run_stream = ctx->stream;
     ctx->stream = run_stream ? run_stream : ctx->own_stream;
     const int64_t pos0 = s->pos, mtp_len0 = s->mtp_kv.len;
@@ -1275,7 +1281,7 @@ int32_t capture_body(ut_session *s, Body body, hipGraphExec_t *exec) {
 int32_t capture_rows(ut_session *s, int64_t rows, const int32_t *ids_dev, hipGraphExec_t *exec) {
     return capture_body(s, [&]() -> int32_t {
         UT_TRY(prefill_dev(s, nullptr, rows, ids_dev));
-        return launch_pos_add(s->m->ctx, s->dpos, rows);
+        return launch_pos_add(s->ctx, s->dpos, rows);
     }, exec);
 }
 
@@ -1285,7 +1291,7 @@ int32_t capture_rows(ut_session *s, int64_t rows, const int32_t *ids_dev, hipGra
 int32_t graph_step(ut_session *s, int64_t rows, const int32_t *ids_dev, hipGraphExec_t *g,
                    int64_t *eager_steps) {
     ut_model *m = s->m;
-    ut_ctx *ctx = m->ctx;
+    ut_ctx *ctx = s->ctx;
     if (!graph_ok(s, *eager_steps)) {
         const int32_t rc = prefill_dev(s, nullptr, rows, ids_dev);
         if (rc == UT_OK) (*eager_steps)++;
@@ -1342,7 +1348,7 @@ int32_t verify_step(ut_session *s, int64_t rows) {
 // count when the session allows it, like the verify step.
 int32_t draft_feed(ut_session *s, int64_t pending) {
     ut_model *m = s->m;
-    ut_ctx *ctx = m->ctx;
+    ut_ctx *ctx = s->ctx;
     const int64_t H = m->c.hidden_size, fed = s->mtp_fed;
     auto body = [&]() -> int32_t {
         Workspace &w = s->ws;
@@ -2033,23 +2039,65 @@ void ut_model_free(ut_model *m) {
     ctx_release(ctx);
 }
 
+int32_t ut_model_set_kv_budget(ut_model *m, int64_t kv_budget_bytes) {
+    if (!m) return UT_ERR_ARG;
+    if (kv_budget_bytes == 0) {
+        set_error(m->ctx, "KV budget of 0 bytes");
+        return UT_ERR_ARG;
+    }
+    m->kv_budget = kv_budget_bytes < 0 ? -1 : kv_budget_bytes;
+    return UT_OK;
+}
+
+int64_t ut_model_max_context(const ut_model *m) {
+    if (!m) return UT_ERR_ARG;
+    const ut_model_config &c = m->c;
+    if (m->kv_budget < 0) return c.max_position_embeddings;
+    // loader.rs:311-325: per position the compressed latents of every main
+    // layer, plus (with the MTP head) the saved hidden state and token id
+    const int64_t per = c.num_hidden_layers * (c.kv_lora_rank + c.qk_rope_head_dim) * 4 +
+                        (m->has_mtp ? c.hidden_size * 4 + 8 : 0);
+    int64_t eff = m->kv_budget / (per > 0 ? per : 1);
+    if (eff < 1) eff = 1;
+    return eff < c.max_position_embeddings ? eff : c.max_position_embeddings;
+}
+
 int32_t ut_session_create(ut_model *m, int32_t path, ut_session **out) {
+    return ut_session_create_on(m, nullptr, path, out);
+}
+
+int32_t ut_session_create_on(ut_model *m, ut_ctx *sctx, int32_t path, ut_session **out) {
     if (!m || !out) return UT_ERR_ARG;
     *out = nullptr;
+    ut_ctx *ctx = sctx ? sctx : m->ctx;
     if (!m->finalized) {
-        set_error(m->ctx, "model not finalized");
+        set_error(ctx, "model not finalized");
         return UT_ERR_STATE;
     }
     if (path < 0 || path > 2) {
-        set_error(m->ctx, "bad attention path %d", path);
+        set_error(ctx, "bad attention path %d", path);
         return UT_ERR_ARG;
+    }
+    if (ctx != m->ctx) {
+        if (ctx->device != m->device) {
+            set_error(ctx, "session context on device %d, model on device %d", ctx->device,
+                      m->device);
+            return UT_ERR_ARG;
+        }
+        // the HBM tier's slots and tables change in the model's stream order
+        if (m->store) {
+            set_error(ctx, "sessions on another context need all routed experts resident");
+            return UT_ERR_STATE;
+        }
     }
     ut_session *s = new (std::nothrow) ut_session();
     if (!s) return UT_ERR_OOM;
     s->m = m;
+    s->ctx = ctx;
     m->refs++;
+    if (ctx != m->ctx) ctx_retain(ctx);
     s->path = path;
-    s->cap = m->c.max_position_embeddings;
+    s->cap = ut_model_max_context(m);
     const ut_model_config &c = m->c;
     const int64_t nl = c.num_hidden_layers + (m->has_mtp ? 1 : 0);
     const size_t per = (size_t)s->cap * (c.kv_lora_rank + c.qk_rope_head_dim) * 4;
@@ -2098,7 +2146,7 @@ int32_t ut_session_create(ut_model *m, int32_t path, ut_session **out) {
 void ut_session_free(ut_session *s) {
     if (!s) return;
     (void)hipSetDevice(s->m->device);
-    (void)hipStreamSynchronize(s->m->ctx->stream);
+    (void)hipStreamSynchronize(s->ctx->stream);
     if (s->g1) (void)hipGraphExecDestroy(s->g1);
     if (s->gv) (void)hipGraphExecDestroy(s->gv);
     for (auto g : s->gd)
@@ -2108,14 +2156,16 @@ void ut_session_free(ut_session *s) {
     if (s->pin) (void)hipHostFree(s->pin);
     if (s->ready) (void)hipEventDestroy(s->ready);
     ut_model *m = s->m;
+    ut_ctx *own = s->ctx != m->ctx ? s->ctx : nullptr;
     delete s;
+    if (own) ctx_release(own);
     ut_model_free(m);  // drops the session's reference
 }
 
 int32_t ut_session_prefill(ut_session *s, const int32_t *ids, int64_t n, float *logits_host,
                            int32_t *argmax_host) {
     if (!s || (!ids && n > 0)) return UT_ERR_ARG;
-    ut_ctx *ctx = s->m->ctx;
+    ut_ctx *ctx = s->ctx;
     UT_TRY(prefill_dev(s, ids, n));
     if (logits_host) {
         UT_CHECK_HIP(ctx, hipMemcpyAsync(logits_host, s->ws.logits,
@@ -2208,7 +2258,7 @@ int32_t ut_session_draft_logits(ut_session *s, int32_t next_token, float *logits
     // next_token for the last) and returns the head's logits for the last
     if (!s) return UT_ERR_ARG;
     ut_model *m = s->m;
-    ut_ctx *ctx = m->ctx;
+    ut_ctx *ctx = s->ctx;
     const int64_t H = m->c.hidden_size, V = m->c.vocab_size;
     if (!m->has_mtp) {
         set_error(ctx, "model has no MTP head");

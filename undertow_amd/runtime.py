@@ -113,6 +113,9 @@ _SIGS = [
     ("ut_model_device_bytes", _i64, [_vp]),
     ("ut_model_free", None, [_vp]),
     ("ut_session_create", _i32, [_vp, _i32, C.POINTER(_vp)]),
+    ("ut_session_create_on", _i32, [_vp, _vp, _i32, C.POINTER(_vp)]),
+    ("ut_model_set_kv_budget", _i32, [_vp, _i64]),
+    ("ut_model_max_context", _i64, [_vp]),
     ("ut_session_free", None, [_vp]),
     ("ut_session_prefill", _i32, [_vp, _vp, _i64, _vp, _vp]),
     ("ut_session_truncate", _i32, [_vp, _i64]),
@@ -625,12 +628,22 @@ class Model:
                    dense_fmt: int = INT8) -> None:
         self.ctx.check(lib().ut_model_synthesize(self._h, seed, init_std, expert_fmt, dense_fmt))
 
+    def set_kv_budget(self, kv_budget_bytes: Optional[int]) -> None:
+        """LoadOptions::kv_budget_bytes: lowers the context sessions hold
+        (None removes the bound)."""
+        self.ctx.check(lib().ut_model_set_kv_budget(self._h, -1 if kv_budget_bytes is None
+                                                    else kv_budget_bytes))
+
+    @property
+    def max_context(self) -> int:
+        return int(lib().ut_model_max_context(self._h))
+
     @property
     def device_bytes(self) -> int:
         return lib().ut_model_device_bytes(self._h)
 
-    def session(self, path: int = 0) -> "Session":
-        return Session(self, path)
+    def session(self, path: int = 0, ctx: Optional[Context] = None) -> "Session":
+        return Session(self, path, ctx)
 
     def forward(self, ids) -> np.ndarray:
         return self.session().prefill(ids)
@@ -717,10 +730,15 @@ class Model:
 class Session:
     """InferenceSession (model.rs:407-564) on device."""
 
-    def __init__(self, model: Model, path: int = 0):
+    def __init__(self, model: Model, path: int = 0, ctx: Optional[Context] = None):
+        """ctx: run the session's work on this context (its own stream)
+        instead of the model's, so sessions on several threads can share
+        one model."""
         self.model = model
+        self.ctx = ctx or model.ctx
         h = _vp()
-        model.ctx.check(lib().ut_session_create(model._h, path, C.byref(h)))
+        self.ctx.check(lib().ut_session_create_on(model._h, None if ctx is None else ctx.handle,
+                                                  path, C.byref(h)))
         self._h = h
 
     def _release(self):
@@ -740,7 +758,7 @@ class Session:
         rc = lib().ut_session_prefill(self._h, ids.ctypes.data, ids.size,
                                       None if logits is None else logits.ctypes.data,
                                       am.ctypes.data)
-        self.model.ctx.check(rc)
+        self.ctx.check(rc)
         self.last_argmax = am[:ids.size].tolist()
         return logits
 
@@ -753,12 +771,12 @@ class Session:
         V = self.model.cfg["vocab_size"]
         logits = np.zeros(V, np.float32)
         d = _i32()
-        self.model.ctx.check(lib().ut_session_draft_logits(self._h, next_token,
-                                                           logits.ctypes.data, C.byref(d)))
+        self.ctx.check(lib().ut_session_draft_logits(self._h, next_token,
+                                                     logits.ctypes.data, C.byref(d)))
         return logits, d.value
 
     def truncate(self, n: int) -> None:
-        self.model.ctx.check(lib().ut_session_truncate(self._h, n))
+        self.ctx.check(lib().ut_session_truncate(self._h, n))
 
     @property
     def position(self) -> int:
