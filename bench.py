@@ -575,7 +575,43 @@ def mtp_bench(U, ctx, cfg, prompt_len, new_tokens, depths, seed, expert_fmt, den
             "tok_s": len(toks_pg) / dt, "replays": after["replays"] - before["replays"],
             "failures": after["failures"] - before["failures"]}
     del m
+    if cfg["hidden_size"] >= 4096 and cfg.get("mtp"):
+        res["restating_head"] = restating_head_bench(U, ctx, cfg, prompt, new_tokens, depths, seed,
+                                                     expert_fmt, dense_fmt)
     return res
+
+
+def restating_head_bench(U, ctx, cfg, prompt, new_tokens, depths, seed, expert_fmt, dense_fmt):
+    """The native draft head at non-zero acceptance: the same config
+    synthesized with an MTP module that restates its first MoE layer
+    (ut_model_synthesize_ex, UT_SYNTH_MTP_RESTATES; the other layers'
+    residual writes damped), so the native head's drafts mostly match the
+    verified tokens, as a trained head's do.  The same weight bytes per
+    step as the plain model; greedy and MTP depth 1/3 rates (prefill
+    excluded), acceptance, and the lossless check."""
+    m = U.Model(ctx, cfg)
+    m.synthesize(seed, 0.02, expert_fmt, dense_fmt, mtp_restates=True)
+    s = m.session()
+    s.prefill(prompt, want_logits=False)
+    del s
+    t0 = time.perf_counter()
+    s = m.session()
+    s.prefill(prompt, want_logits=False)
+    t_prefill = time.perf_counter() - t0
+    del s
+    t0 = time.perf_counter()
+    greedy = m.generate_greedy(prompt, new_tokens)
+    out = {"greedy_tok_s": len(greedy) / (time.perf_counter() - t0 - t_prefill)}
+    for d in depths:
+        t0 = time.perf_counter()
+        toks, drafted, accepted = m.generate_mtp(prompt, new_tokens, depth=d)
+        dt = time.perf_counter() - t0 - t_prefill
+        assert toks == greedy, f"restating head: MTP depth {d} output differs from greedy"
+        out[f"mtp{d}"] = {"tok_s": len(toks) / dt, "drafted": drafted, "accepted": accepted,
+                          "acceptance": accepted / max(drafted, 1), "lossless": True,
+                          "speedup_vs_greedy": len(toks) / dt / out["greedy_tok_s"]}
+    del m
+    return out
 
 
 def c5_bench(U, ctx, torch, prompt_len=2048, new_tokens=256, pin_frac=0.25, cache_frac=0.10,
@@ -725,7 +761,8 @@ def committed_traffic(kernel: str) -> tuple[float | None, str | None]:
                                "dispatch, copy-scaled)")
 
 
-def profile_decode(cfg_name: str, prompt_len: int, tokens: int, seed: int = 42) -> None:
+def profile_decode(cfg_name: str, prompt_len: int, tokens: int, seed: int = 42,
+                   restating: bool = False) -> None:
     """Decode-step driver for kernel traces (run it under rocprofv3): the
     synthetic model on device, a uniform-random prompt, then `tokens`
     one-row decode steps, `tokens // 2` two-row and `tokens // 2` four-row
@@ -745,7 +782,7 @@ def profile_decode(cfg_name: str, prompt_len: int, tokens: int, seed: int = 42) 
         # pinned host pool: decode steps read routes back and copy misses
         m.synthesize_tiered(seed, 40 << 30, 1024, prefetch=True)
     else:
-        m.synthesize(seed, 0.02, U.INT4, U.INT8)
+        m.synthesize(seed, 0.02, U.INT4, U.INT8, mtp_restates=restating)
     rng = np.random.default_rng(1)
     prompt = rng.integers(0, cfg["vocab_size"], prompt_len).tolist()
     s = m.session()
@@ -771,6 +808,17 @@ def profile_decode(cfg_name: str, prompt_len: int, tokens: int, seed: int = 42) 
             nxt = s.last_argmax[-1]
         t1 = time.perf_counter()
         print(f"verify ({rows} rows) {n} steps: {(t1 - t0) / n * 1e3:.3f} ms/step", flush=True)
+    if restating:
+        # the MTP depth-1 loop with a head that accepts its drafts: verify
+        # steps of two rows and the MTP head's feed of the verified rows
+        del s
+        torch.cuda.synchronize()
+        time.sleep(1.0)
+        t0 = time.perf_counter()
+        toks, drafted, accepted = m.generate_mtp(prompt, tokens, depth=1)
+        t1 = time.perf_counter()
+        print(f"MTP depth 1: {len(toks)} tokens in {(t1 - t0) * 1e3:.1f} ms (prefill included), "
+              f"{accepted}/{drafted} drafts accepted", flush=True)
 
 
 def main():
@@ -802,6 +850,9 @@ def main():
     ap.add_argument("--profile-decode", choices=["c1", "c4", "c5"], default=None,
                     help="only run the decode-step driver for kernel traces (no JSON line)")
     ap.add_argument("--prompt", type=int, default=512, help="prompt length for --profile-decode")
+    ap.add_argument("--restating", action="store_true",
+                    help="--profile-decode: a model whose MTP head restates a layer, plus an "
+                         "MTP depth-1 phase")
     ap.add_argument("--tokens", type=int, default=32, help="decode steps for --profile-decode")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -810,7 +861,7 @@ def main():
                                    "one); run with --gpus 1"}))
         sys.exit(2)
     if args.profile_decode:
-        profile_decode(args.profile_decode, args.prompt, args.tokens)
+        profile_decode(args.profile_decode, args.prompt, args.tokens, restating=args.restating)
         return
     if args.c5_only:
         import torch

@@ -381,6 +381,20 @@ int32_t ut_model_expert_usage(ut_model *m, int64_t *counts, int64_t n);
  * UT_FMT_INT8. */
 int32_t ut_model_synthesize(ut_model *m, uint64_t seed, float init_std, int32_t expert_fmt,
                             int32_t dense_fmt);
+/* Benchmark support, no reference counterpart: ut_model_synthesize with
+ * construction flags.  UT_SYNTH_MTP_RESTATES builds a model whose MTP head
+ * predicts like the main model, as a trained head does (random weights
+ * otherwise accept almost no drafts): the MTP module's layer restates the
+ * first MoE layer (the same bytes) and its head and head norm the lm_head
+ * and final norm; the other layers' residual writes (o_proj and the down
+ * projections) get scales 2^-10 of the synthesized ones; embedding rows
+ * get unit RMS and eh_proj = [I | 0], so the MTP module sees the next
+ * token's embedding as the main model does.  The weight bytes and shapes
+ * are the config's.  Needs an MTP module, int8 dense weights and at least
+ * one MoE layer (else UT_ERR_ARG). */
+enum { UT_SYNTH_MTP_RESTATES = 1 };
+int32_t ut_model_synthesize_ex(ut_model *m, uint64_t seed, float init_std, int32_t expert_fmt,
+                               int32_t dense_fmt, int32_t flags);
 int64_t ut_model_device_bytes(const ut_model *m);
 /* LoadOptions::kv_budget_bytes (undertow-core/src/model.rs:36-61) and the
  * effective context it gives (adapters/undertow-deepseek-moe/src/

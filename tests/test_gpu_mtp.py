@@ -256,3 +256,41 @@ def test_long_prompt_first_draft(ctx):
     toks, drafted, _ = m.generate_mtp(prompt, 4, depth=1)
     assert drafted > 0
     assert toks == m.generate_greedy(prompt, 4)
+
+
+def _device_cfg(overrides):
+    from undertow_amd.configs import C1 as DC1
+    return dict(DC1, **overrides)
+
+
+@pytest.mark.parametrize("over", [dict(num_hidden_layers=3),
+                                  dict(num_hidden_layers=2, hidden_size=1024, num_attention_heads=128,
+                                       kv_lora_rank=512, qk_nope_head_dim=128, qk_rope_head_dim=64,
+                                       v_head_dim=128)],
+                         ids=["c1_3layers", "mla_2layers"])
+def test_restating_mtp_head_accepts_and_stays_lossless(ctx, over):
+    """ut_model_synthesize_ex(UT_SYNTH_MTP_RESTATES): the MTP module restates
+    the first MoE layer and the other layers' residual writes are damped,
+    so the native head's drafts mostly match the verified tokens.  Greedy
+    and MTP depth 1-3 emit the same stream (the verify keeps speculation
+    lossless whatever the head predicts), the accept counts are consistent,
+    and depth 1 accepts most drafts.  The flags are validated."""
+    import undertow_amd as U
+    cfg = _device_cfg(over)
+    m = U.Model(ctx, cfg)
+    m.synthesize(31, 0.02, U.INT4, U.INT8, mtp_restates=True)
+    prompt = prompt_ids(24, cfg["vocab_size"], seed=8)
+    greedy = m.generate_greedy(prompt, 48)
+    for depth in (1, 2, 3):
+        toks, drafted, accepted = m.generate_mtp(prompt, 48, depth=depth)
+        assert toks == greedy, depth
+        assert 0 <= accepted <= drafted and drafted > 0
+        if depth == 1:
+            assert accepted / drafted > 0.5, (accepted, drafted)
+    plain = U.Model(ctx, cfg)
+    plain.synthesize(31, 0.02, U.INT4, U.INT8)
+    _, pd, pa = plain.generate_mtp(prompt, 48, depth=1)
+    assert pa < accepted or pa / pd < 0.5
+    bad = U.Model(ctx, cfg)
+    with pytest.raises(U.UtError):
+        bad.synthesize(31, 0.02, U.INT4, U.INT4, mtp_restates=True)

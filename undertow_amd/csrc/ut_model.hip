@@ -1106,11 +1106,80 @@ void model_tensor_list(const ut_model_config &c, std::vector<SynthItem> &items) 
     }
 }
 
-int32_t synthesize_all(ut_model *m, uint64_t seed, float std, int expert_fmt, int dense_fmt) {
+// Rows of an int8 embedding rescaled to unit RMS: scale[r] =
+// 1 / sqrt(mean(code^2)) over the row's codes (the integer sum is exact).
+__global__ __launch_bounds__(256) void k_unit_rms_scales(const int8_t *__restrict__ q, int64_t K,
+                                                         float *__restrict__ scales) {
+    __shared__ int64_t red[4];
+    const int64_t r = blockIdx.x;
+    int64_t acc = 0;
+    for (int64_t i = threadIdx.x; i < K; i += 256) {
+        const int v = q[r * K + i];
+        acc += v * v;
+    }
+    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int64_t t = red[0] + red[1] + red[2] + red[3];
+        scales[r] = t > 0 ? 1.0f / sqrtf((float)((double)t / (double)K)) : 1.0f;
+    }
+}
+
+// int8 [H, 2H] = [I | 0]: code 127 on the left block's diagonal.
+__global__ void k_eye_left_i8(int8_t *__restrict__ q, int64_t H) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < H * 2 * H;
+         i += (int64_t)gridDim.x * blockDim.x)
+        q[i] = (i / (2 * H)) == (i % (2 * H)) ? (int8_t)127 : (int8_t)0;
+}
+
+__global__ void k_fill_f32(float *__restrict__ p, int64_t n, float v) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+// flags & UT_SYNTH_MTP_RESTATES: the construction of ut_model_synthesize_ex
+// (the MTP module restates the first MoE layer; the other layers' residual
+// writes damped by 2^-10; unit-RMS embedding rows; eh_proj = [I | 0]).
+int32_t synthesize_all(ut_model *m, uint64_t seed, float std, int expert_fmt, int dense_fmt,
+                       int flags = 0) {
     const ut_model_config &c = m->c;
     ut_ctx *ctx = m->ctx;
     std::vector<SynthItem> items;
     model_tensor_list(c, items);
+    const bool restate = (flags & UT_SYNTH_MTP_RESTATES) != 0;
+    const int64_t src_layer = c.first_k_dense_replace;  // the MoE layer the MTP module restates
+    const std::string mtp_pre = "model.layers." + std::to_string(c.num_hidden_layers) + ".";
+    const std::string src_pre = "model.layers." + std::to_string(src_layer) + ".";
+    // the fills' keys by tensor name: a restating MTP tensor reuses its
+    // source's keys, so the generator writes the same bytes
+    std::unordered_map<std::string, std::pair<uint64_t, uint64_t>> keys;
+    auto source_of = [&](const std::string &name) -> std::string {
+        if (!restate) return std::string();
+        if (name == mtp_pre + "shared_head.norm.weight") return "model.norm.weight";
+        if (name == mtp_pre + "shared_head.head.weight") return "lm_head.weight";
+        if (name.compare(0, mtp_pre.size(), mtp_pre) != 0) return std::string();
+        const std::string rest = name.substr(mtp_pre.size());
+        if (rest == "enorm.weight" || rest == "hnorm.weight" || rest == "eh_proj.weight")
+            return std::string();
+        return src_pre + rest;
+    };
+    // a residual write of a layer other than the restated one (o_proj, and
+    // the down projections of the dense FFN, routed and shared experts)
+    auto damped = [&](const std::string &name) -> bool {
+        if (!restate || name.compare(0, 13, "model.layers.") != 0) return false;
+        if (name.compare(0, src_pre.size(), src_pre) == 0 ||
+            name.compare(0, mtp_pre.size(), mtp_pre) == 0)
+            return false;
+        const size_t n = name.size();
+        auto ends = [&](const char *t) {
+            const size_t k = strlen(t);
+            return n >= k && name.compare(n - k, k, t) == 0;
+        };
+        return ends("self_attn.o_proj.weight") || ends("down_proj.weight");
+    };
+    constexpr float kDamp = 1.0f / 1024.0f;
     // one arena for everything, 256-byte aligned pieces
     auto al = [](int64_t b) { return (b + 255) & ~int64_t(255); };
     int64_t total = 0;
@@ -1124,21 +1193,42 @@ int32_t synthesize_all(ut_model *m, uint64_t seed, float std, int expert_fmt, in
     UT_TRY(dev_alloc(m, (size_t)total, &arena));
     char *p = (char *)arena;
     uint64_t idx = 0;
+    uint64_t forced = 0;  // nonzero: the key of the next fill (a restated tensor's)
+    uint64_t last_key = 0;
     auto fill = [&](void *dst, int64_t n, int kind, float a, float b) -> int32_t {
-        const uint64_t key = mix_host(seed, idx++);
+        const uint64_t key = forced ? forced : mix_host(seed, idx);
+        idx++;
+        forced = 0;
+        last_key = key;
         int64_t blocks = (n + 255) / 256;
         if (blocks > 16384) blocks = 16384;
         hipLaunchKernelGGL(k_synth, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, dst, n,
                            kind, key, a, b);
         return launch_check(ctx, "k_synth");
     };
+    auto grid = [](int64_t n) { return (unsigned)std::min<int64_t>((n + 255) / 256, 16384); };
     for (auto &it : items) {
         if (m->store && it.cls == 2) continue;
         DevTensor t;
         t.d0 = it.d0;
         t.d1 = it.d1;
+        const std::string src = source_of(it.name);
+        const auto ks = src.empty() ? keys.end() : keys.find(src);
+        if (!src.empty() && ks == keys.end()) {
+            set_error(ctx, "synthesize: %s has no source %s", it.name.c_str(), src.c_str());
+            return UT_ERR_STATE;
+        }
         if (it.kind != 0) {
-            UT_TRY(fill(p, it.d0, it.kind == 1 ? 4 : 5, 0.0f, 0.0f));
+            if (restate && it.name == mtp_pre + "enorm.weight") {
+                hipLaunchKernelGGL(k_fill_f32, dim3(grid(it.d0)), dim3(256), 0, ctx->stream,
+                                   (float *)p, it.d0, 1.0f);
+                UT_TRY(launch_check(ctx, "k_fill_f32"));
+                idx++;
+            } else {
+                if (ks != keys.end()) forced = ks->second.first;
+                UT_TRY(fill(p, it.d0, it.kind == 1 ? 4 : 5, 0.0f, 0.0f));
+            }
+            keys[it.name] = {last_key, 0};
             t.vec = (float *)p;
             p += al(it.d0 * 4);
         } else {
@@ -1153,17 +1243,47 @@ int32_t synthesize_all(ut_model *m, uint64_t seed, float std, int expert_fmt, in
             q->device = m->device;
             q->payload = p;
             const int64_t pb = payload_bytes(fmt, it.d0, it.d1);
-            if (fmt == UT_FMT_F32) {
+            const bool eye = restate && it.name == mtp_pre + "eh_proj.weight" && fmt == UT_FMT_INT8;
+            const bool unit_rows = restate && it.name == "model.embed_tokens.weight" &&
+                                   fmt == UT_FMT_INT8;
+            uint64_t pkey = 0;
+            if (ks != keys.end()) forced = ks->second.first;
+            if (eye) {
+                hipLaunchKernelGGL(k_eye_left_i8, dim3(grid(pb)), dim3(256), 0, ctx->stream,
+                                   (int8_t *)p, it.d0);
+                UT_TRY(launch_check(ctx, "k_eye_left_i8"));
+                idx++;
+            } else if (fmt == UT_FMT_F32) {
                 UT_TRY(fill(p, it.d0 * it.d1, 3, std, 1.0f));
+                pkey = last_key;
             } else {
                 UT_TRY(fill(p, pb, fmt == UT_FMT_INT4 ? 0 : 1, 0.0f, 0.0f));
+                pkey = last_key;
             }
+            char *payload = p;
             p += al(pb);
+            uint64_t skey = 0;
             if (fmt != UT_FMT_F32) {
                 q->scales = (float *)p;
-                UT_TRY(fill(p, it.d0, 2, std, fmt == UT_FMT_INT4 ? 7.0f : 127.0f));
+                if (eye) {
+                    hipLaunchKernelGGL(k_fill_f32, dim3(grid(it.d0)), dim3(256), 0, ctx->stream,
+                                       (float *)p, it.d0, 1.0f / 127.0f);
+                    UT_TRY(launch_check(ctx, "k_fill_f32"));
+                    idx++;
+                } else if (unit_rows) {
+                    hipLaunchKernelGGL(k_unit_rms_scales, dim3((unsigned)it.d0), dim3(256), 0,
+                                       ctx->stream, (const int8_t *)payload, it.d1, (float *)p);
+                    UT_TRY(launch_check(ctx, "k_unit_rms_scales"));
+                    idx++;
+                } else {
+                    if (ks != keys.end()) forced = ks->second.second;
+                    UT_TRY(fill(p, it.d0, 2, damped(it.name) ? std * kDamp : std,
+                                fmt == UT_FMT_INT4 ? 7.0f : 127.0f));
+                    skey = last_key;
+                }
                 p += al(it.d0 * 4);
             }
+            keys[it.name] = {pkey, skey};
             t.qt = q;
         }
         m->tensors.emplace(it.name, t);
@@ -2290,7 +2410,23 @@ int32_t ut_session_draft_logits(ut_session *s, int32_t next_token, float *logits
 
 int32_t ut_model_synthesize(ut_model *m, uint64_t seed, float init_std, int32_t expert_fmt,
                             int32_t dense_fmt) {
+    return ut_model_synthesize_ex(m, seed, init_std, expert_fmt, dense_fmt, 0);
+}
+
+int32_t ut_model_synthesize_ex(ut_model *m, uint64_t seed, float init_std, int32_t expert_fmt,
+                               int32_t dense_fmt, int32_t flags) {
     if (!m) return UT_ERR_ARG;
+    if (flags & ~UT_SYNTH_MTP_RESTATES) {
+        set_error(m->ctx, "synthesize: unknown flags 0x%x", (unsigned)flags);
+        return UT_ERR_ARG;
+    }
+    if ((flags & UT_SYNTH_MTP_RESTATES) &&
+        (!m->c.mtp || dense_fmt != UT_FMT_INT8 ||
+         m->c.first_k_dense_replace >= m->c.num_hidden_layers)) {
+        set_error(m->ctx, "synthesize: a restating MTP module needs an MTP module, int8 dense "
+                          "weights and a MoE layer");
+        return UT_ERR_ARG;
+    }
     if (m->finalized || !m->tensors.empty()) {
         set_error(m->ctx, "ut_model_synthesize needs a fresh model");
         return UT_ERR_STATE;
@@ -2300,7 +2436,7 @@ int32_t ut_model_synthesize(ut_model *m, uint64_t seed, float init_std, int32_t 
         set_error(m->ctx, "synthesize: formats must be int4 or int8");
         return UT_ERR_ARG;
     }
-    UT_TRY(synthesize_all(m, seed, init_std, expert_fmt, dense_fmt));
+    UT_TRY(synthesize_all(m, seed, init_std, expert_fmt, dense_fmt, flags));
     return ut_model_finalize(m);
 }
 

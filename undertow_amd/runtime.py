@@ -114,6 +114,7 @@ _SIGS = [
     ("ut_model_free", None, [_vp]),
     ("ut_session_create", _i32, [_vp, _i32, C.POINTER(_vp)]),
     ("ut_session_create_on", _i32, [_vp, _vp, _i32, C.POINTER(_vp)]),
+    ("ut_model_synthesize_ex", _i32, [_vp, C.c_uint64, _f32, _i32, _i32, _i32]),
     ("ut_model_set_kv_budget", _i32, [_vp, _i64]),
     ("ut_model_max_context", _i64, [_vp]),
     ("ut_session_free", None, [_vp]),
@@ -198,6 +199,7 @@ class StoreStats(C.Structure):
 
 
 LRU, WEIGHTED = 0, 1
+SYNTH_MTP_RESTATES = 1  # ut_model_synthesize_ex: the MTP module restates a layer
 
 
 class ExpertProfile:
@@ -625,8 +627,11 @@ class Model:
         return n.value
 
     def synthesize(self, seed: int, init_std: float = 0.02, expert_fmt: int = INT4,
-                   dense_fmt: int = INT8) -> None:
-        self.ctx.check(lib().ut_model_synthesize(self._h, seed, init_std, expert_fmt, dense_fmt))
+                   dense_fmt: int = INT8, mtp_restates: bool = False) -> None:
+        """Seeded random weights made on the device; mtp_restates: the MTP
+        module restates the first MoE layer (a head that accepts drafts)."""
+        self.ctx.check(lib().ut_model_synthesize_ex(self._h, seed, init_std, expert_fmt, dense_fmt,
+                                                    SYNTH_MTP_RESTATES if mtp_restates else 0))
 
     def set_kv_budget(self, kv_budget_bytes: Optional[int]) -> None:
         """LoadOptions::kv_budget_bytes: lowers the context sessions hold
