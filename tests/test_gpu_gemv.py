@@ -59,7 +59,8 @@ def test_matmul_matches_oracle(ctx, fmt, o, i):
 
 
 @pytest.mark.parametrize("fmt", FMTS)
-@pytest.mark.parametrize("o,i", [(2048, 7168), (7168, 2048), (130, 64), (5, 17), (256, 7168)])
+@pytest.mark.parametrize("o,i", [(2048, 7168), (7168, 2048), (130, 64), (5, 17), (256, 7168),
+                                 (7168, 16384), (1000, 192)])
 def test_rows_do_not_depend_on_seq(ctx, fmt, o, i):
     rng = np.random.default_rng(7)
     payload, scales = rand_qtensor(rng, fmt, o, i)

@@ -5,6 +5,7 @@
 // kernel for shapes the fast one does not take.
 #include <atomic>
 #include "ut_gemv_core.h"
+#include "ut_gemv_mfma.h"
 #include "ut_moe.h"
 #include "ut_ops.h"
 #include "ut_rowdig.h"
@@ -516,6 +517,77 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
         }
 }
 
+// int8 weights at 3..4 activation rows on the matrix cores
+// (mfma_gemv_i8): 64 * TW output rows per workgroup, wave w's TW tiles of
+// 16 rows at blockIdx.x * 64TW + 16TW w + 16t; the same split-K partials,
+// epilogue and partial-maxima path (F32X: x digitised while staged) as
+// k_gemv, and the same totals, so the outputs are bit-identical to its.
+// UT_GEMV_I8_MFMA_MIN_M: the fewest rows that take it.
+#ifndef UT_GEMV_I8_MFMA_MIN_M
+#define UT_GEMV_I8_MFMA_MIN_M 3
+#endif
+template <int M> constexpr int gemv_i8_mfma_tw() { return 1; }
+template <int M> constexpr int gemv_i8_mfma_kc() { return M <= 2 ? 4096 : 2048; }
+template <int M> constexpr int gemv_i8_mfma_depth() { return 4; }
+
+template <int M, bool F32X>
+__global__ __launch_bounds__(kGemvThreads) void k_gemv_mfma_i8(PlainArgs a) {
+    constexpr int TW = gemv_i8_mfma_tw<M>(), KC = gemv_i8_mfma_kc<M>();
+    __shared__ __attribute__((aligned(16))) uint8_t lds[mfma_i8_lds_bytes<M, KC>()];
+    __shared__ uint32_t redm[4 * M];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
+    const int64_t rowbase = (int64_t)blockIdx.x * (64 * TW) + wave * (16 * TW);
+    const uint8_t *arow[TW];
+#pragma unroll
+    for (int w = 0; w < TW; w++) {
+        const int64_t r = rowbase + 16 * w + s;
+        arow[w] = plain_row(a, r < a.O ? r : a.O - 1);
+    }
+    const int64_t kb = a.ks > 1 ? (int64_t)blockIdx.z * a.kslice : 0;
+    const int64_t ke = a.ks > 1 ? (kb + a.kslice < a.K ? kb + a.kslice : a.K) : a.K;
+    int32_t exl[M];
+    ut_u32x4 pv[M];
+    if constexpr (F32X) {
+        rowmax_load<M>(a.xmax, a.nxmax, pv);
+    } else {
+#pragma unroll
+        for (int m = 0; m < M; m++) exl[m] = a.exps[m];
+    }
+    auto prep = [&](int32_t (&shl)[4]) {
+        if constexpr (F32X) {
+            int32_t sh[M];
+            rowmax_reduce<M>(pv, sh, redm);
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                shl[m] = sh[m];
+                exl[m] = sh[m] == INT32_MIN ? INT32_MIN : -sh[m];
+            }
+            if (blockIdx.x == 0 && blockIdx.z == 0 && tid < M)
+                const_cast<int32_t *>(a.exps)[tid] = tid == 0 ? exl[0] : tid == 1 ? exl[M > 1 ? 1 : 0]
+                                                    : tid == 2 ? exl[M > 2 ? 2 : 0] : exl[M > 3 ? 3 : 0];
+        }
+    };
+    CoreOut<UT_FMT_INT4, M, 4> res[TW];
+    mfma_gemv_i8<M, KC, TW, gemv_i8_mfma_depth<M>(), F32X>(arow, kb, ke, a.x.dig, a.x.KW, a.x.xf,
+                                                        a.x.ldx, lds, res, prep);
+#pragma unroll
+    for (int w = 0; w < TW; w++)
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                const int64_t row = rowbase + 16 * w + 4 * g + r;
+                if (s != 4 * r + m || row >= a.O) continue;
+                if (a.ks > 1) {
+                    a.part[((int64_t)blockIdx.z * M + m) * a.O + row] = res[w].S[r][m];
+                } else {
+                    const float v = int_total_to_f32(res[w].S[r][m], exl[m], plain_scale(a, row));
+                    float *o = plain_out(a, m, row);
+                    *o = a.accumulate ? __fadd_rn(*o, v) : v;
+                }
+            }
+}
+
 // The value of (m, row) from split-K partials [ks][M][O]: summed in z order
 // (integers exactly, f32 in that fixed order) with the row epilogue.
 template <int FMT>
@@ -728,6 +800,95 @@ template <int FMT> static int64_t gemv_resident(ut_ctx *ctx, int mrows) {
     }
 }
 
+// After a split-K GEMV launch: the consumer sums the partials (defer), or
+// the sum runs fused with the next rmsnorm + digitise, or alone.
+template <int FMT>
+static int32_t splitk_finish(ut_ctx *ctx, const GemvArgs &ga, const PlainArgs &a, int64_t m0,
+                             int mrows, const char *name) {
+    UT_TRY(launch_check(ctx, name));
+    const ut_qtensor *w2 = ga.w2;
+    const bool fuse_next = FMT != UT_FMT_F32 && ga.next && !ga.defer && !w2 && m0 == 0 &&
+                           mrows == ga.M && a.O % 8 == 0 && a.O <= 8 * 1024 &&
+                           aligned16(a.out) && a.ldo % 4 == 0 && aligned16(a.scales) &&
+                           aligned16(ga.next->norm_w) && ga.next->nd.exps;
+    if (ga.defer) {
+        // the consumer sums the partials (only one chunk of rows)
+        ga.defer->part = a.part;
+        ga.defer->ks = a.ks;
+        ga.defer->O = a.O;
+    } else if (fuse_next) {
+        const NormNext &nx = *ga.next;
+        RowDigArgs nd{};
+        nd.K = a.O;
+        nd.norm_w = nx.norm_w;
+        nd.eps = nx.eps;
+        nd.out = nx.normed;
+        nd.ldo = nx.ldn;
+        nd.exps = nx.nd.exps;
+        nd.dig4 = (nx.flags & XD_DIG4) ? nx.nd.dig4 : nullptr;
+        nd.dig8 = (nx.flags & XD_DIG8) ? nx.nd.dig8 : nullptr;
+        nd.xt = (nx.flags & XD_XT) ? nx.nd.xt : nullptr;
+        nd.raw = a.out;
+        nd.ldr = a.ldo;
+        const unsigned threads = (unsigned)((a.O / 8 + 63) / 64 * 64);
+        hipLaunchKernelGGL(k_splitk_sum_norm<FMT>, dim3((unsigned)mrows), dim3(threads), 0,
+                           ctx->stream, a, mrows, nd);
+        if (ga.next_done) *ga.next_done = true;
+    } else {
+        const int64_t n = a.O * mrows;
+        hipLaunchKernelGGL(k_gemv_splitk_sum<FMT>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                           ctx->stream, a, mrows);
+    }
+    return UT_OK;
+}
+
+// Workgroups of k_gemv_mfma_i8<M, F32X> resident on the chip.
+template <int M, bool F32X> static int64_t gemv_i8_mfma_resident(ut_ctx *ctx) {
+    static std::atomic<int> per_cu{0};
+    int n = per_cu.load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, (const void *)k_gemv_mfma_i8<M, F32X>,
+                                                         kGemvThreads, 0) != hipSuccess ||
+            n < 1) {
+            (void)hipGetLastError();
+            n = 2;
+        }
+        per_cu.store(n, std::memory_order_relaxed);
+    }
+    return (int64_t)n * ctx->multiprocessors;
+}
+
+template <int M, bool F32X>
+static int32_t launch_i8_mfma_m(ut_ctx *ctx, const GemvArgs &ga, PlainArgs a, int64_t m0) {
+    constexpr int rows_per_wg = 64 * gemv_i8_mfma_tw<M>();
+    // a launch that reduces the producer's partial maxima pays that in every
+    // workgroup: half as many splits, as for k_gemv
+    const int64_t resident = gemv_i8_mfma_resident<M, F32X>(ctx) / (F32X ? 2 : 1);
+    splitk_plan(UT_FMT_INT8, a.O, a.K, rows_per_wg, resident, &a.ks, &a.kslice);
+    a.part = nullptr;
+    if (a.ks > 1) UT_TRY(splitk_buffer(ctx, &a.part));
+    const dim3 grid((unsigned)((a.O + rows_per_wg - 1) / rows_per_wg), 1, (unsigned)a.ks);
+    const char *name = "gemv_int8_mfma";
+    int tok = timing_begin(ctx, name);
+    hipLaunchKernelGGL((k_gemv_mfma_i8<M, F32X>), grid, dim3(kGemvThreads), 0, ctx->stream, a);
+    if (a.ks > 1) UT_TRY(splitk_finish<UT_FMT_INT8>(ctx, ga, a, m0, M, name));
+    timing_end(ctx, tok);
+    return launch_check(ctx, name);
+}
+
+static int32_t launch_gemv_i8_mfma(ut_ctx *ctx, const GemvArgs &ga, const PlainArgs &a, int64_t m0,
+                                   int mrows) {
+    const bool f32x = a.xmax != nullptr;
+    switch (mrows) {
+    case 3: return f32x ? launch_i8_mfma_m<3, true>(ctx, ga, a, m0) : launch_i8_mfma_m<3, false>(ctx, ga, a, m0);
+    case 4: return f32x ? launch_i8_mfma_m<4, true>(ctx, ga, a, m0) : launch_i8_mfma_m<4, false>(ctx, ga, a, m0);
+#if UT_GEMV_I8_MFMA_MIN_M <= 2
+    case 2: return f32x ? launch_i8_mfma_m<2, true>(ctx, ga, a, m0) : launch_i8_mfma_m<2, false>(ctx, ga, a, m0);
+#endif
+    default: return UT_ERR_ARG;
+    }
+}
+
 template <int FMT>
 static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrows) {
     const ut_qtensor *w = ga.w, *w2 = ga.w2;
@@ -772,6 +933,12 @@ static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrow
     }
     a.xmax = FMT != UT_FMT_F32 && ga.xmax ? ga.xmax + m0 * ga.nxmax : nullptr;
     a.nxmax = ga.nxmax;
+    // int8 at 3..4 rows: the matrix-core kernel (64-row tiles, steps of 64
+    // columns), the same partials and epilogue
+    const bool i8_mfma = FMT == UT_FMT_INT8 && mrows >= UT_GEMV_I8_MFMA_MIN_M && mrows <= 4 &&
+                         w->in_dim % kMfmaI8StepCols == 0 &&
+                         (a.xmax || ((uintptr_t)a.x.dig & 15) == 0);
+    if (i8_mfma) return launch_gemv_i8_mfma(ctx, ga, a, m0, mrows);
     const int rows_per_wg = plain_rows_rt(mrows);
     // a launch that reduces the producer's partial maxima while staging
     // pays that in every workgroup: half as many splits (o_proj at
@@ -810,41 +977,7 @@ static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrow
     case 3: hipLaunchKernelGGL((k_gemv<FMT, 3>), grid, dim3(kGemvThreads), 0, ctx->stream, a); break;
     default: hipLaunchKernelGGL((k_gemv<FMT, 4>), grid, dim3(kGemvThreads), 0, ctx->stream, a); break;
     }
-    if (a.ks > 1) {
-        UT_TRY(launch_check(ctx, name));
-        const bool fuse_next = FMT != UT_FMT_F32 && ga.next && !ga.defer && !w2 && m0 == 0 &&
-                               mrows == ga.M && a.O % 8 == 0 && a.O <= 8 * 1024 &&
-                               aligned16(a.out) && a.ldo % 4 == 0 && aligned16(a.scales) &&
-                               aligned16(ga.next->norm_w) && ga.next->nd.exps;
-        if (ga.defer) {
-            // the consumer sums the partials (only one chunk of rows)
-            ga.defer->part = a.part;
-            ga.defer->ks = a.ks;
-            ga.defer->O = a.O;
-        } else if (fuse_next) {
-            const NormNext &nx = *ga.next;
-            RowDigArgs nd{};
-            nd.K = a.O;
-            nd.norm_w = nx.norm_w;
-            nd.eps = nx.eps;
-            nd.out = nx.normed;
-            nd.ldo = nx.ldn;
-            nd.exps = nx.nd.exps;
-            nd.dig4 = (nx.flags & XD_DIG4) ? nx.nd.dig4 : nullptr;
-            nd.dig8 = (nx.flags & XD_DIG8) ? nx.nd.dig8 : nullptr;
-            nd.xt = (nx.flags & XD_XT) ? nx.nd.xt : nullptr;
-            nd.raw = a.out;
-            nd.ldr = a.ldo;
-            const unsigned threads = (unsigned)((a.O / 8 + 63) / 64 * 64);
-            hipLaunchKernelGGL(k_splitk_sum_norm<FMT>, dim3((unsigned)mrows), dim3(threads), 0,
-                               ctx->stream, a, mrows, nd);
-            if (ga.next_done) *ga.next_done = true;
-        } else {
-            const int64_t n = a.O * mrows;
-            hipLaunchKernelGGL(k_gemv_splitk_sum<FMT>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
-                               ctx->stream, a, mrows);
-        }
-    }
+    if (a.ks > 1) UT_TRY(splitk_finish<FMT>(ctx, ga, a, m0, mrows, name));
     timing_end(ctx, tok);
     return launch_check(ctx, name);
 }

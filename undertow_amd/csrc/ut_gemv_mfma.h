@@ -301,4 +301,167 @@ __device__ __forceinline__ void mfma_gemv_i4_chunks(const uint8_t *const (&arow)
     for (int w = 0; w < TW; w++) mfma_collect<M>(acc[w], res[w]);
 }
 
+// ---------------------------------------------------------------- int8 ---
+// int8 weights on the matrix cores (the dense GEMVs of 3-4-row verify steps
+// and prefill chunks: the dot-product core issues 12 dot instructions per 4
+// weight bytes there and is VALU-bound).  One v_mfma_i32_16x16x64_i8 per
+// 64-column step and 16-row tile: A is the weights' own bytes (lane
+// (i, kg) loads 16 bytes of row i at columns [64j + 16kg, +16)), B the
+// activations' three balanced base-256 digit planes per row (plane row
+// n = 3m + p, the same columns, natural order), so the totals equal the
+// dot-product core's bit for bit.  Columns [kb, ke) (multiples of 64) in
+// staged chunks of KC; the next chunk's activations load into registers
+// while the current one computes, and the weight loads run on across the
+// chunk barriers.  Activations come as digit planes (dig: [M][3][KW]
+// words, the row digitiser's form) or, with F32X, as f32 rows digitised
+// while staged with the shifts prep() fills (INT32_MIN: zero digits).
+template <int M, int KC> __host__ __device__ constexpr int mfma_i8_lds_bytes() {
+    return 3 * M * mfma_row_bytes<KC>();
+}
+constexpr int kMfmaI8StepCols = 64;
+
+template <int M, int KC, int TW, int DEPTH, bool F32X, typename Prep>
+__device__ __forceinline__ void mfma_gemv_i8(const uint8_t *const (&arow)[TW], int64_t kb,
+                                             int64_t ke, const uint32_t *dig, int64_t KW,
+                                             const float *xf, int64_t ldx, uint8_t *lds,
+                                             CoreOut<UT_FMT_INT4, M, 4> (&res)[TW], Prep &&prep) {
+    static_assert(M >= 1 && M <= 4, "three digit planes per row, 16 columns");
+    static_assert(KC % (4 * kMfmaI8StepCols) == 0, "chunks of whole step groups");
+    constexpr int RB = mfma_row_bytes<KC>();
+    // staging work items per chunk: 16-byte pieces of the 3M plane rows, or
+    // 4-column groups of the M f32 rows
+    constexpr int ITEMS = F32X ? M * (KC / 4) : 3 * M * (KC / 16);
+    constexpr int NI = (ITEMS + kGemvThreads - 1) / kGemvThreads;
+    const int tid = threadIdx.x, lane = tid & 63, n = lane & 15, kg = lane >> 4;
+    const int nsteps = (int)((ke - kb) / kMfmaI8StepCols);
+    const uint8_t *ap[TW];
+#pragma unroll
+    for (int w = 0; w < TW; w++) ap[w] = arow[w] + kb + 16 * kg;
+    uint4 xr[NI];
+    int32_t shl[4] = {0, 0, 0, 0};
+    auto xload = [&](int64_t kc) {
+        const int kcn = (int)(ke - kb - kc < KC ? ke - kb - kc : KC);
+        if constexpr (F32X) {
+            const int NG = kcn / 4, TOT = M * NG;
+#pragma unroll
+            for (int j = 0; j < NI; j++) {
+                const int i = tid + j * kGemvThreads, ic = i < TOT ? i : TOT - 1;
+                const int m = ic / NG, g = ic - m * NG;
+                const float4 v = ld_global<float4>(xf + m * ldx + kb + kc + 4 * g);
+                xr[j] = make_uint4(__float_as_uint(v.x), __float_as_uint(v.y),
+                                   __float_as_uint(v.z), __float_as_uint(v.w));
+            }
+        } else {
+            const int NQ = kcn / 16, TOT = 3 * M * NQ;
+#pragma unroll
+            for (int j = 0; j < NI; j++) {
+                const int i = tid + j * kGemvThreads, ic = i < TOT ? i : TOT - 1;
+                const int r = ic / NQ, q = ic - r * NQ;
+                xr[j] = ld_global<uint4>((const uint8_t *)(dig + r * KW) + kb + kc + 16 * q);
+            }
+        }
+    };
+    auto xstore = [&](int64_t kc) {
+        const int kcn = (int)(ke - kb - kc < KC ? ke - kb - kc : KC);
+        if constexpr (F32X) {
+            const int NG = kcn / 4, TOT = M * NG;
+#pragma unroll
+            for (int j = 0; j < NI; j++) {
+                const int i = tid + j * kGemvThreads;
+                if (i < TOT) {
+                    const int m = i / NG, g = i - m * NG;
+                    const int32_t sh = m == 0 ? shl[0] : m == 1 ? shl[1] : m == 2 ? shl[2] : shl[3];
+                    const float v[4] = {__uint_as_float(xr[j].x), __uint_as_float(xr[j].y),
+                                        __uint_as_float(xr[j].z), __uint_as_float(xr[j].w)};
+                    uint32_t wd[3];
+                    digit_words<UT_FMT_INT8>(v, 4, sh, wd);
+#pragma unroll
+                    for (int p = 0; p < 3; p++) *(uint32_t *)(lds + (3 * m + p) * RB + 4 * g) = wd[p];
+                }
+            }
+        } else {
+            const int NQ = kcn / 16, TOT = 3 * M * NQ;
+#pragma unroll
+            for (int j = 0; j < NI; j++) {
+                const int i = tid + j * kGemvThreads;
+                if (i < TOT) {
+                    const int r = i / NQ, q = i - r * NQ;
+                    *(uint4 *)(lds + r * RB + 16 * q) = xr[j];
+                }
+            }
+        }
+    };
+    auto lds_barrier = []() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+    xload(0);
+    uint4 wq[DEPTH][TW];
+#pragma unroll
+    for (int u = 0; u < DEPTH; u++)
+#pragma unroll
+        for (int w = 0; w < TW; w++)
+            wq[u][w] = ld_weights(ap[w] + kMfmaI8StepCols * (u < nsteps ? u : nsteps - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    prep(shl);
+    xstore(0);
+    lds_barrier();
+    const bool bn = n < 3 * M;
+    const uint8_t *bp = lds + (bn ? n : 0) * RB + 16 * kg;
+    ut_i32x4 acc[TW];
+#pragma unroll
+    for (int w = 0; w < TW; w++) acc[w] = ut_i32x4{0, 0, 0, 0};
+    int j0 = 0;  // the chunk's first step
+    for (int64_t kc = 0; kc < ke - kb; kc += KC) {
+        const bool more = kc + KC < ke - kb;
+        if (more) xload(kc + KC);
+        const int csteps = (int)((ke - kb - kc < KC ? ke - kb - kc : KC) / kMfmaI8StepCols);
+        int t = 0;
+        for (; t + DEPTH <= csteps; t += DEPTH) {
+#pragma unroll
+            for (int u = 0; u < DEPTH; u++) {
+                const int jn = j0 + t + u + DEPTH;
+                uint4 b = *(const uint4 *)(bp + kMfmaI8StepCols * (t + u));
+                if (!bn) b = make_uint4(0u, 0u, 0u, 0u);
+                const ut_i32x4 B = {(int)b.x, (int)b.y, (int)b.z, (int)b.w};
+#pragma unroll
+                for (int w = 0; w < TW; w++) {
+                    const uint4 wv = wq[u][w];
+                    wq[u][w] = ld_weights(ap[w] + kMfmaI8StepCols * (jn < nsteps ? jn : nsteps - 1));
+                    const ut_i32x4 A = {(int)wv.x, (int)wv.y, (int)wv.z, (int)wv.w};
+                    acc[w] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, acc[w], 0, 0, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        // a chunk whose step count is not a multiple of DEPTH: the ring of
+        // loads in flight keeps its order (step t + u holds slot (t + u) % DEPTH)
+        for (; t < csteps; t++) {
+            const int u = (j0 + t) % DEPTH;
+            const int jn = j0 + t + DEPTH;
+            uint4 b = *(const uint4 *)(bp + kMfmaI8StepCols * t);
+            if (!bn) b = make_uint4(0u, 0u, 0u, 0u);
+            const ut_i32x4 B = {(int)b.x, (int)b.y, (int)b.z, (int)b.w};
+#pragma unroll
+            for (int w = 0; w < TW; w++) {
+                uint4 wv;
+#pragma unroll
+                for (int v = 0; v < DEPTH; v++)
+                    if (v == u) wv = wq[v][w];
+                const uint4 nx = ld_weights(ap[w] + kMfmaI8StepCols * (jn < nsteps ? jn : nsteps - 1));
+#pragma unroll
+                for (int v = 0; v < DEPTH; v++)
+                    if (v == u) wq[v][w] = nx;
+                const ut_i32x4 A = {(int)wv.x, (int)wv.y, (int)wv.z, (int)wv.w};
+                acc[w] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, acc[w], 0, 0, 0);
+            }
+        }
+        j0 += csteps;
+        if (more) {
+            lds_barrier();  // every wave is done with this chunk
+            xstore(kc + KC);
+            lds_barrier();
+        }
+    }
+#pragma unroll
+    for (int w = 0; w < TW; w++) mfma_collect<M>(acc[w], res[w]);
+}
+
 }  // namespace ut
