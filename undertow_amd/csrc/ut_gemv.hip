@@ -526,23 +526,39 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
 #ifndef UT_GEMV_I8_MFMA_MIN_M
 #define UT_GEMV_I8_MFMA_MIN_M 3
 #endif
-template <int M> constexpr int gemv_i8_mfma_tw() { return 1; }
-template <int M> constexpr int gemv_i8_mfma_kc() { return M <= 2 ? 4096 : 2048; }
-template <int M> constexpr int gemv_i8_mfma_depth() { return 4; }
+#ifndef UT_GEMV_I8_MFMA_TW
+#define UT_GEMV_I8_MFMA_TW 1
+#endif
+#ifndef UT_GEMV_I8_MFMA_DEPTH
+#define UT_GEMV_I8_MFMA_DEPTH 2
+#endif
+#ifndef UT_GEMV_I8_MFMA_SPLIT_FILL
+#define UT_GEMV_I8_MFMA_SPLIT_FILL 0
+#endif
+#ifndef UT_GEMV_I8_MFMA_KC4
+#define UT_GEMV_I8_MFMA_KC4 2048
+#endif
+template <int M> constexpr int gemv_i8_mfma_tw() { return UT_GEMV_I8_MFMA_TW; }
+template <int M> constexpr int gemv_i8_mfma_kc() { return M <= 2 ? 4096 : UT_GEMV_I8_MFMA_KC4; }
+template <int M> constexpr int gemv_i8_mfma_depth() { return UT_GEMV_I8_MFMA_DEPTH; }
 
 template <int M, bool F32X>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv_mfma_i8(PlainArgs a) {
     constexpr int TW = gemv_i8_mfma_tw<M>(), KC = gemv_i8_mfma_kc<M>();
     __shared__ __attribute__((aligned(16))) uint8_t lds[mfma_i8_lds_bytes<M, KC>()];
+    __shared__ __attribute__((aligned(16))) uint8_t wareas[4 * TW * kMfmaI8WaveAreaBytes];
     __shared__ uint32_t redm[4 * M];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
     const int64_t rowbase = (int64_t)blockIdx.x * (64 * TW) + wave * (16 * TW);
-    const uint8_t *arow[TW];
+    // load rows: tile w, instruction r -> row 4r + lane / 16 of the tile
+    const uint8_t *lrows[TW][4];
 #pragma unroll
-    for (int w = 0; w < TW; w++) {
-        const int64_t r = rowbase + 16 * w + s;
-        arow[w] = plain_row(a, r < a.O ? r : a.O - 1);
-    }
+    for (int w = 0; w < TW; w++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int64_t row = rowbase + 16 * w + 4 * r + g;
+            lrows[w][r] = plain_row(a, row < a.O ? row : a.O - 1);
+        }
     const int64_t kb = a.ks > 1 ? (int64_t)blockIdx.z * a.kslice : 0;
     const int64_t ke = a.ks > 1 ? (kb + a.kslice < a.K ? kb + a.kslice : a.K) : a.K;
     int32_t exl[M];
@@ -568,8 +584,9 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_mfma_i8(PlainArgs a) {
         }
     };
     CoreOut<UT_FMT_INT4, M, 4> res[TW];
-    mfma_gemv_i8<M, KC, TW, gemv_i8_mfma_depth<M>(), F32X>(arow, kb, ke, a.x.dig, a.x.KW, a.x.xf,
-                                                        a.x.ldx, lds, res, prep);
+    mfma_gemv_i8<M, KC, TW, gemv_i8_mfma_depth<M>(), F32X>(
+        lrows, kb, ke, a.x.dig, a.x.KW, a.x.xf, a.x.ldx, lds,
+        wareas + wave * TW * kMfmaI8WaveAreaBytes, res, prep);
 #pragma unroll
     for (int w = 0; w < TW; w++)
 #pragma unroll
@@ -865,6 +882,20 @@ static int32_t launch_i8_mfma_m(ut_ctx *ctx, const GemvArgs &ga, PlainArgs a, in
     // workgroup: half as many splits, as for k_gemv
     const int64_t resident = gemv_i8_mfma_resident<M, F32X>(ctx) / (F32X ? 2 : 1);
     splitk_plan(UT_FMT_INT8, a.O, a.K, rows_per_wg, resident, &a.ks, &a.kslice);
+#if UT_GEMV_I8_MFMA_SPLIT_FILL
+    {
+        // split until the launch fills the chip's resident workgroups once
+        const int64_t tiles = (a.O + rows_per_wg - 1) / rows_per_wg;
+        int64_t ks = resident / tiles;
+        const int64_t step = kMfmaI8SegCols;
+        if (ks > a.K / (2 * step)) ks = a.K / (2 * step);
+        while (ks > 1 && ks * 4 * a.O * 8 > kSplitKPartBytes) ks--;
+        if (ks > a.ks) {
+            a.kslice = ((a.K + ks - 1) / ks + step - 1) / step * step;
+            a.ks = (int)((a.K + a.kslice - 1) / a.kslice);
+        }
+    }
+#endif
     a.part = nullptr;
     if (a.ks > 1) UT_TRY(splitk_buffer(ctx, &a.part));
     const dim3 grid((unsigned)((a.O + rows_per_wg - 1) / rows_per_wg), 1, (unsigned)a.ks);
@@ -936,7 +967,7 @@ static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrow
     // int8 at 3..4 rows: the matrix-core kernel (64-row tiles, steps of 64
     // columns), the same partials and epilogue
     const bool i8_mfma = FMT == UT_FMT_INT8 && mrows >= UT_GEMV_I8_MFMA_MIN_M && mrows <= 4 &&
-                         w->in_dim % kMfmaI8StepCols == 0 &&
+                         w->in_dim % kMfmaI8SegCols == 0 &&
                          (a.xmax || ((uintptr_t)a.x.dig & 15) == 0);
     if (i8_mfma) return launch_gemv_i8_mfma(ctx, ga, a, m0, mrows);
     const int rows_per_wg = plain_rows_rt(mrows);

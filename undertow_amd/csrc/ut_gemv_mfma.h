@@ -305,38 +305,54 @@ __device__ __forceinline__ void mfma_gemv_i4_chunks(const uint8_t *const (&arow)
 // int8 weights on the matrix cores (the dense GEMVs of 3-4-row verify steps
 // and prefill chunks: the dot-product core issues 12 dot instructions per 4
 // weight bytes there and is VALU-bound).  One v_mfma_i32_16x16x64_i8 per
-// 64-column step and 16-row tile: A is the weights' own bytes (lane
-// (i, kg) loads 16 bytes of row i at columns [64j + 16kg, +16)), B the
+// 64-column step and 16-row tile: A is the weights' own bytes, B the
 // activations' three balanced base-256 digit planes per row (plane row
-// n = 3m + p, the same columns, natural order), so the totals equal the
-// dot-product core's bit for bit.  Columns [kb, ke) (multiples of 64) in
-// staged chunks of KC; the next chunk's activations load into registers
-// while the current one computes, and the weight loads run on across the
-// chunk barriers.  Activations come as digit planes (dig: [M][3][KW]
-// words, the row digitiser's form) or, with F32X, as f32 rows digitised
-// while staged with the shifts prep() fills (INT32_MIN: zero digits).
+// n = 3m + p, natural column order), so the totals equal the dot-product
+// core's bit for bit.
+//
+// Weight loads: the A operand gives a lane 16 bytes of one row (lane
+// (i, kg): row i, columns [64s + 16kg, +16) of step s), so loading it
+// directly asks for 64 bytes of each row per instruction, half a 128-byte
+// line, and every line twice.  Instead a wave loads a 256-column segment
+// of its 16 rows (four steps) as four instructions of 4 rows x 256
+// contiguous bytes (lane l: row 4r + l/16, bytes 16 (l % 16)), writes them
+// to a wave-private LDS area and reads the A operands back from it: with
+// the loads whole lines, lm_head-sized GEMVs at four rows went from 192 to
+// about 150 us in a timing-only probe of the access pattern.  The area's
+// 16-byte chunks are XOR-swizzled by the row (chunk c of row i at
+// 16 (c ^ i)), so the 16 rows a read touches sit in distinct banks.
+//
+// Columns [kb, ke) (multiples of 256) in staged chunks of KC for B; the
+// next chunk's activations load into registers while the current one
+// computes, and the weight loads run on across the chunk barriers.
+// Activations come as digit planes (dig: [M][3][KW] words, the row
+// digitiser's form) or, with F32X, as f32 rows digitised while staged with
+// the shifts prep() fills (INT32_MIN: zero digits).  rows[w][r]: this
+// lane's load row of tile w, instruction r (row 4r + lane/16 of the tile,
+// clamped to a valid row).  DS: 256-column segments in flight.
 template <int M, int KC> __host__ __device__ constexpr int mfma_i8_lds_bytes() {
     return 3 * M * mfma_row_bytes<KC>();
 }
 constexpr int kMfmaI8StepCols = 64;
+constexpr int kMfmaI8SegCols = 256;                // four steps
+constexpr int kMfmaI8WaveAreaBytes = 16 * 256;     // one segment of a 16-row tile
 
-template <int M, int KC, int TW, int DEPTH, bool F32X, typename Prep>
-__device__ __forceinline__ void mfma_gemv_i8(const uint8_t *const (&arow)[TW], int64_t kb,
+template <int M, int KC, int TW, int DS, bool F32X, typename Prep>
+__device__ __forceinline__ void mfma_gemv_i8(const uint8_t *const (&rows)[TW][4], int64_t kb,
                                              int64_t ke, const uint32_t *dig, int64_t KW,
                                              const float *xf, int64_t ldx, uint8_t *lds,
+                                             uint8_t *warea /* TW * kMfmaI8WaveAreaBytes */,
                                              CoreOut<UT_FMT_INT4, M, 4> (&res)[TW], Prep &&prep) {
     static_assert(M >= 1 && M <= 4, "three digit planes per row, 16 columns");
-    static_assert(KC % (4 * kMfmaI8StepCols) == 0, "chunks of whole step groups");
+    static_assert(KC % kMfmaI8SegCols == 0, "chunks of whole segments");
     constexpr int RB = mfma_row_bytes<KC>();
     // staging work items per chunk: 16-byte pieces of the 3M plane rows, or
     // 4-column groups of the M f32 rows
     constexpr int ITEMS = F32X ? M * (KC / 4) : 3 * M * (KC / 16);
     constexpr int NI = (ITEMS + kGemvThreads - 1) / kGemvThreads;
     const int tid = threadIdx.x, lane = tid & 63, n = lane & 15, kg = lane >> 4;
-    const int nsteps = (int)((ke - kb) / kMfmaI8StepCols);
-    const uint8_t *ap[TW];
-#pragma unroll
-    for (int w = 0; w < TW; w++) ap[w] = arow[w] + kb + 16 * kg;
+    const int nseg = (int)((ke - kb) / kMfmaI8SegCols);
+    const int64_t lo = kb + 16 * n;  // this lane's bytes within each loaded segment
     uint4 xr[NI];
     int32_t shl[4] = {0, 0, 0, 0};
     auto xload = [&](int64_t kc) {
@@ -392,68 +408,72 @@ __device__ __forceinline__ void mfma_gemv_i8(const uint8_t *const (&arow)[TW], i
         }
     };
     auto lds_barrier = []() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
-    xload(0);
-    uint4 wq[DEPTH][TW];
-#pragma unroll
-    for (int u = 0; u < DEPTH; u++)
+    // the segment in flight: wq[slot][w][r] = tile w's rows 4r + lane/16
+    uint4 wq[DS][TW][4];
+    auto seg_load = [&](uint4 (&d)[TW][4], int sg) {
+        const int64_t off = lo + (int64_t)kMfmaI8SegCols * (sg < nseg ? sg : nseg - 1);
 #pragma unroll
         for (int w = 0; w < TW; w++)
-            wq[u][w] = ld_weights(ap[w] + kMfmaI8StepCols * (u < nsteps ? u : nsteps - 1));
+#pragma unroll
+            for (int r = 0; r < 4; r++) d[w][r] = ld_weights(rows[w][r] + off);
+    };
+    xload(0);
+#pragma unroll
+    for (int u = 0; u < DS; u++) seg_load(wq[u], u);
     __builtin_amdgcn_sched_barrier(0);
     prep(shl);
     xstore(0);
     lds_barrier();
     const bool bn = n < 3 * M;
     const uint8_t *bp = lds + (bn ? n : 0) * RB + 16 * kg;
+    // A reads: row n, chunk 4s + kg at 16 ((4s + kg) ^ n); writes: row
+    // 4r + kg, chunk n at 16 (n ^ (4r + kg))
     ut_i32x4 acc[TW];
 #pragma unroll
     for (int w = 0; w < TW; w++) acc[w] = ut_i32x4{0, 0, 0, 0};
-    int j0 = 0;  // the chunk's first step
-    for (int64_t kc = 0; kc < ke - kb; kc += KC) {
-        const bool more = kc + KC < ke - kb;
-        if (more) xload(kc + KC);
-        const int csteps = (int)((ke - kb - kc < KC ? ke - kb - kc : KC) / kMfmaI8StepCols);
-        int t = 0;
-        for (; t + DEPTH <= csteps; t += DEPTH) {
+    auto segment = [&](uint4 (&d)[TW][4], int sg, int sl) {
 #pragma unroll
-            for (int u = 0; u < DEPTH; u++) {
-                const int jn = j0 + t + u + DEPTH;
-                uint4 b = *(const uint4 *)(bp + kMfmaI8StepCols * (t + u));
-                if (!bn) b = make_uint4(0u, 0u, 0u, 0u);
-                const ut_i32x4 B = {(int)b.x, (int)b.y, (int)b.z, (int)b.w};
+        for (int w = 0; w < TW; w++)
 #pragma unroll
-                for (int w = 0; w < TW; w++) {
-                    const uint4 wv = wq[u][w];
-                    wq[u][w] = ld_weights(ap[w] + kMfmaI8StepCols * (jn < nsteps ? jn : nsteps - 1));
-                    const ut_i32x4 A = {(int)wv.x, (int)wv.y, (int)wv.z, (int)wv.w};
-                    acc[w] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, acc[w], 0, 0, 0);
-                }
-                __builtin_amdgcn_sched_barrier(0);
+            for (int r = 0; r < 4; r++) {
+                const int row = 4 * r + kg;
+                *(uint4 *)(warea + w * kMfmaI8WaveAreaBytes + row * 256 + 16 * (n ^ row)) = d[w][r];
             }
-        }
-        // a chunk whose step count is not a multiple of DEPTH: the ring of
-        // loads in flight keeps its order (step t + u holds slot (t + u) % DEPTH)
-        for (; t < csteps; t++) {
-            const int u = (j0 + t) % DEPTH;
-            const int jn = j0 + t + DEPTH;
-            uint4 b = *(const uint4 *)(bp + kMfmaI8StepCols * t);
+        seg_load(d, sg + DS);
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            uint4 b = *(const uint4 *)(bp + kMfmaI8SegCols * sl + kMfmaI8StepCols * s);
             if (!bn) b = make_uint4(0u, 0u, 0u, 0u);
             const ut_i32x4 B = {(int)b.x, (int)b.y, (int)b.z, (int)b.w};
 #pragma unroll
             for (int w = 0; w < TW; w++) {
-                uint4 wv;
-#pragma unroll
-                for (int v = 0; v < DEPTH; v++)
-                    if (v == u) wv = wq[v][w];
-                const uint4 nx = ld_weights(ap[w] + kMfmaI8StepCols * (jn < nsteps ? jn : nsteps - 1));
-#pragma unroll
-                for (int v = 0; v < DEPTH; v++)
-                    if (v == u) wq[v][w] = nx;
-                const ut_i32x4 A = {(int)wv.x, (int)wv.y, (int)wv.z, (int)wv.w};
+                const uint4 av = *(const uint4 *)(warea + w * kMfmaI8WaveAreaBytes + n * 256 +
+                                                  16 * ((4 * s + kg) ^ n));
+                const ut_i32x4 A = {(int)av.x, (int)av.y, (int)av.z, (int)av.w};
                 acc[w] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, acc[w], 0, 0, 0);
             }
         }
-        j0 += csteps;
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    int g0 = 0;  // the chunk's first segment
+    for (int64_t kc = 0; kc < ke - kb; kc += KC) {
+        const bool more = kc + KC < ke - kb;
+        if (more) xload(kc + KC);
+        const int csegs = (int)((ke - kb - kc < KC ? ke - kb - kc : KC) / kMfmaI8SegCols);
+        int t = 0;
+        // every chunk but the last holds KC / 256 segments, a multiple of DS,
+        // so segment g sits in slot g % DS
+        for (; t + DS <= csegs; t += DS) {
+#pragma unroll
+            for (int u = 0; u < DS; u++) segment(wq[u], g0 + t + u, t + u);
+        }
+        for (; t < csegs; t++) {
+            const int u = (g0 + t) % DS;
+#pragma unroll
+            for (int v = 0; v < DS; v++)
+                if (v == u) segment(wq[v], g0 + t, t);
+        }
+        g0 += csegs;
         if (more) {
             lds_barrier();  // every wave is done with this chunk
             xstore(kc + KC);
