@@ -118,72 +118,118 @@ __device__ __forceinline__ void mfma_collect(const ut_i32x4 &acc, CoreOut<UT_FMT
         }
 }
 
-// One wave: TW tiles of 16 rows (one A operand each, sharing the B
-// operand) x M activation rows over the columns [0, K) staged
-// whole (K <= KC, K % 128 == 0).  arow[w]: this lane's A row of tile w
-// (row lane & 15 of the tile's 16, clamped to a valid row).  DEPTH steps of weights in
-// flight.  The total for (wave row 4g + r, activation row m) lands in
-// res.S[r][m] of sub-lane 4r + m of lane group g (the dot-product core's
-// convention with 4 rows per lane).
-template <int M, int DEPTH, int KC, int TW, typename Prep>
-__device__ __forceinline__ void mfma_gemv_i4_f32x(const uint8_t *const (&arow)[TW], int64_t K,
+// Weight loads of the int4 kernels.  The A operand gives a lane 16 bytes of
+// one row (lane (i, kg): row i, bytes [64j + 16kg, +16) of step j), so
+// loading it directly asks for 64 bytes of each row per instruction, half a
+// 128-byte line, and every line twice.  Instead a wave loads a 16-row tile
+// in 128-byte segments (two steps) as two instructions of 8 rows x 128
+// contiguous bytes (lane l: tile row 8r + l/8, bytes 16 (l % 8)), writes
+// them to a wave-private LDS area and reads the A operands back from it:
+// whole lines per request.  Area layout: rows 2q and 2q + 1 share 256
+// bytes, their 16-byte chunks XOR-swizzled by q, so the 16 rows one read
+// touches cover all 64 banks.  rows[w][r]: this lane's load row of tile w,
+// instruction r (tile row 8r + lane / 8), clamped to a valid row.
+constexpr int kI4SegBytes = 128;                    // two 128-column steps of a row
+constexpr int kI4WaveAreaBytes = 16 * kI4SegBytes;  // one segment of a 16-row tile
+__device__ __forceinline__ int i4_area_off(int row, int chunk) {
+    return (row >> 1) * 256 + (row & 1) * 128 + 16 * (chunk ^ ((row >> 1) & 7));
+}
+
+// Segment sg of tile w into registers (two 16-byte loads); a last segment
+// holding one step (odd nsteps) re-reads the first half for its second.
+template <int TW>
+__device__ __forceinline__ void i4_seg_load(uint4 (&d)[TW][2], const uint8_t *const (&rows)[TW][2],
+                                            int64_t kb, int sg, int nsteps) {
+    const int lane = threadIdx.x & 63, c = lane & 7;
+    const int nseg = (nsteps + 1) >> 1;
+    const int g = sg < nseg ? sg : nseg - 1;
+    const int cc = (2 * g + (c >> 2) < nsteps) ? c : c - 4;
+    const int64_t off = kb + (int64_t)kI4SegBytes * g + 16 * cc;
+#pragma unroll
+    for (int w = 0; w < TW; w++)
+#pragma unroll
+        for (int r = 0; r < 2; r++) d[w][r] = ld_weights(rows[w][r] + off);
+}
+
+template <int TW>
+__device__ __forceinline__ void i4_seg_store(const uint4 (&d)[TW][2], uint8_t *warea) {
+    const int lane = threadIdx.x & 63, c = lane & 7;
+#pragma unroll
+    for (int w = 0; w < TW; w++)
+#pragma unroll
+        for (int r = 0; r < 2; r++)
+            *(uint4 *)(warea + w * kI4WaveAreaBytes + i4_area_off(8 * r + (lane >> 3), c)) = d[w][r];
+}
+
+// The MFMA step s (0 or 1) of a staged segment for every tile: this lane's
+// A bytes (row lane % 16, chunk 4s + lane / 16) unpacked to two operands.
+template <int TW>
+__device__ __forceinline__ void i4_seg_mfma(const uint8_t *warea, int s, const ut_i32x4 &B0,
+                                            const ut_i32x4 &B1, ut_i32x4 (&acc)[TW]) {
+    const int lane = threadIdx.x & 63, n = lane & 15, kg = lane >> 4;
+#pragma unroll
+    for (int w = 0; w < TW; w++) {
+        const uint4 wv = *(const uint4 *)(warea + w * kI4WaveAreaBytes + i4_area_off(n, 4 * s + kg));
+        const uint32_t X = 0x88888888u;
+        const uint32_t a0 = wv.x ^ X, a1 = wv.y ^ X, a2 = wv.z ^ X, a3 = wv.w ^ X;
+        const ut_i32x4 A0 = {mfma_sext4(a0), mfma_sext4(a0 >> 4), mfma_sext4(a1), mfma_sext4(a1 >> 4)};
+        const ut_i32x4 A1 = {mfma_sext4(a2), mfma_sext4(a2 >> 4), mfma_sext4(a3), mfma_sext4(a3 >> 4)};
+        acc[w] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, acc[w], 0, 0, 0);
+        acc[w] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, acc[w], 0, 0, 0);
+    }
+}
+
+// One wave: TW tiles of 16 rows (sharing the B operand) x M activation rows
+// over the columns [0, K) staged whole (K <= KC, K % 128 == 0).  DS
+// segments (two steps each) of weights in flight.  The total for (wave row
+// 4g + r, activation row m) lands in res.S[r][m] of sub-lane 4r + m of
+// lane group g (the dot-product core's convention with 4 rows per lane).
+template <int M, int DS, int KC, int TW, typename Prep>
+__device__ __forceinline__ void mfma_gemv_i4_f32x(const uint8_t *const (&rows)[TW][2], int64_t K,
                                                   const float *xf, int64_t ldx, uint8_t *lds,
+                                                  uint8_t *warea,
                                                   CoreOut<UT_FMT_INT4, M, 4> (&res)[TW],
                                                   Prep &&prep) {
     static_assert(M >= 1 && M <= 4, "three digit planes per row, 16 columns");
     constexpr int RB = mfma_row_bytes<KC>();
     const int lane = threadIdx.x & 63, n = lane & 15, kg = lane >> 4;
-    const int nsteps = (int)(K / kMfmaStepCols);
-    const uint8_t *ap[TW];  // step j: bytes [64j + 16kg, +16)
-#pragma unroll
-    for (int w = 0; w < TW; w++) ap[w] = arow[w] + 16 * kg;
-    uint4 wq[DEPTH][TW];
+    const int nsteps = (int)(K / kMfmaStepCols), nseg = (nsteps + 1) >> 1;
+    uint4 wq[DS][TW][2];
     mfma_stage_f32<M, KC>(xf, ldx, 0, (int)K, lds, [&]() {
 #pragma unroll
-        for (int u = 0; u < DEPTH; u++)
-#pragma unroll
-            for (int w = 0; w < TW; w++) wq[u][w] = ld_weights(ap[w] + 64 * (u < nsteps ? u : nsteps - 1));
+        for (int u = 0; u < DS; u++) i4_seg_load<TW>(wq[u], rows, 0, u, nsteps);
     }, prep);
     const bool bn = n < 3 * M;
     const uint8_t *bp = lds + (bn ? n : 0) * RB + 32 * kg;
     ut_i32x4 acc[TW];
 #pragma unroll
     for (int w = 0; w < TW; w++) acc[w] = ut_i32x4{0, 0, 0, 0};
-    auto step = [&](const uint4 (&wv)[TW], int j) {
-        uint4 b0 = *(const uint4 *)(bp + kMfmaStepCols * j);
-        uint4 b1 = *(const uint4 *)(bp + kMfmaStepCols * j + 16);
-        if (!bn) b0 = b1 = make_uint4(0u, 0u, 0u, 0u);
-        const ut_i32x4 B0 = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w};
-        const ut_i32x4 B1 = {(int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+    auto segment = [&](uint4 (&d)[TW][2], int sg) {
+        i4_seg_store<TW>(d, warea);
+        i4_seg_load<TW>(d, rows, 0, sg + DS, nsteps);
 #pragma unroll
-        for (int w = 0; w < TW; w++) {
-            const uint32_t X = 0x88888888u;
-            const uint32_t a0 = wv[w].x ^ X, a1 = wv[w].y ^ X, a2 = wv[w].z ^ X, a3 = wv[w].w ^ X;
-            const ut_i32x4 A0 = {mfma_sext4(a0), mfma_sext4(a0 >> 4), mfma_sext4(a1), mfma_sext4(a1 >> 4)};
-            const ut_i32x4 A1 = {mfma_sext4(a2), mfma_sext4(a2 >> 4), mfma_sext4(a3), mfma_sext4(a3 >> 4)};
-            acc[w] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, acc[w], 0, 0, 0);
-            acc[w] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, acc[w], 0, 0, 0);
+        for (int s = 0; s < 2; s++) {
+            const int j = 2 * sg + s;
+            if (j >= nsteps) break;
+            uint4 b0 = *(const uint4 *)(bp + kMfmaStepCols * j);
+            uint4 b1 = *(const uint4 *)(bp + kMfmaStepCols * j + 16);
+            if (!bn) b0 = b1 = make_uint4(0u, 0u, 0u, 0u);
+            const ut_i32x4 B0 = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w};
+            const ut_i32x4 B1 = {(int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+            i4_seg_mfma<TW>(warea, s, B0, B1, acc);
         }
-    };
-    auto load = [&](uint4 (&wv)[TW], int j) {
-#pragma unroll
-        for (int w = 0; w < TW; w++) wv[w] = ld_weights(ap[w] + 64 * j);
+        __builtin_amdgcn_sched_barrier(0);
     };
     int t = 0;
-    for (; t + 2 * DEPTH <= nsteps; t += DEPTH) {
+    for (; t + DS <= nseg; t += DS) {
 #pragma unroll
-        for (int u = 0; u < DEPTH; u++) {
-            step(wq[u], t + u);
-            load(wq[u], t + u + DEPTH);
-            __builtin_amdgcn_sched_barrier(0);
-        }
+        for (int u = 0; u < DS; u++) segment(wq[u], t + u);
     }
+    for (; t < nseg; t++) {
+        const int u = t % DS;
 #pragma unroll
-    for (int i = 0; i < 2 * DEPTH; i++) {
-        if (t + i < nsteps) {
-            step(wq[i % DEPTH], t + i);
-            if (t + i + DEPTH < nsteps) load(wq[i % DEPTH], t + i + DEPTH);
-        }
+        for (int v = 0; v < DS; v++)
+            if (v == u) segment(wq[v], t);
     }
 #pragma unroll
     for (int w = 0; w < TW; w++) mfma_collect<M>(acc[w], res[w]);
@@ -195,25 +241,21 @@ __device__ __forceinline__ void mfma_gemv_i4_f32x(const uint8_t *const (&arow)[T
 // activations load into registers while the current one computes, and the
 // weight loads run on across chunk boundaries (the barriers between
 // chunks wait for LDS only).
-// TW tiles of 16 rows per wave (arow[w]: this lane's A row of tile w) share
-// each staged chunk.
+// TW tiles of 16 rows per wave share each staged chunk.
 template <int M, int KC, int TW>
-__device__ __forceinline__ void mfma_gemv_i4_chunks(const uint8_t *const (&arow)[TW], int64_t K,
+__device__ __forceinline__ void mfma_gemv_i4_chunks(const uint8_t *const (&rows)[TW][2], int64_t K,
                                                     const float *xf, int64_t ldx,
                                                     const int32_t (&sh)[M], uint8_t *lds,
+                                                    uint8_t *warea,
                                                     CoreOut<UT_FMT_INT4, M, 4> (&res)[TW]) {
     static_assert(M >= 1 && M <= 4, "three digit planes per row, 16 columns");
     static_assert(KC % (4 * kMfmaStepCols) == 0, "chunks of whole step groups");
-    // weight steps in flight: two at two rows (54.5 against 58.5 us for
-    // C2's gate/up), four beyond
-    constexpr int DEPTH = M == 2 ? 2 : 4;
+    // segments (two steps) of weights in flight: one at two rows, two beyond
+    constexpr int DS = M == 2 ? 1 : 2;
     constexpr int RB = mfma_row_bytes<KC>();
     constexpr int NI = (M * (KC / 8) + kGemvThreads - 1) / kGemvThreads;
     const int tid = threadIdx.x, lane = tid & 63, n = lane & 15, kg = lane >> 4;
     const int nsteps = (int)(K / kMfmaStepCols);
-    const uint8_t *ap[TW];
-#pragma unroll
-    for (int w = 0; w < TW; w++) ap[w] = arow[w] + 16 * kg;
     float4 xv[NI][2];
     auto xload = [&](int64_t kc) {
         const int kcn = (int)(K - kc < KC ? K - kc : KC), NG = kcn / 8, TOT = M * NG;
@@ -248,11 +290,9 @@ __device__ __forceinline__ void mfma_gemv_i4_chunks(const uint8_t *const (&arow)
     };
     auto lds_barrier = []() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
     xload(0);
-    uint4 wq[DEPTH][TW];
+    uint4 wq[DS][TW][2];
 #pragma unroll
-    for (int u = 0; u < DEPTH; u++)
-#pragma unroll
-        for (int w = 0; w < TW; w++) wq[u][w] = ld_weights(ap[w] + 64 * u);
+    for (int u = 0; u < DS; u++) i4_seg_load<TW>(wq[u], rows, 0, u, nsteps);
     xstore(0);
     lds_barrier();
     const bool bn = n < 3 * M;
@@ -260,37 +300,32 @@ __device__ __forceinline__ void mfma_gemv_i4_chunks(const uint8_t *const (&arow)
     ut_i32x4 acc[TW];
 #pragma unroll
     for (int w = 0; w < TW; w++) acc[w] = ut_i32x4{0, 0, 0, 0};
-    int j0 = 0;  // global step of the chunk's first step
+    auto segment = [&](uint4 (&d)[TW][2], int sg, int jl) {
+        i4_seg_store<TW>(d, warea);
+        i4_seg_load<TW>(d, rows, 0, sg + DS, nsteps);
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            uint4 b0 = *(const uint4 *)(bp + kMfmaStepCols * (jl + s));
+            uint4 b1 = *(const uint4 *)(bp + kMfmaStepCols * (jl + s) + 16);
+            if (!bn) b0 = b1 = make_uint4(0u, 0u, 0u, 0u);
+            const ut_i32x4 B0 = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w};
+            const ut_i32x4 B1 = {(int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+            i4_seg_mfma<TW>(warea, s, B0, B1, acc);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    int g0 = 0;  // global segment of the chunk's first
     for (int64_t kc = 0; kc < K; kc += KC) {
         const bool more = kc + KC < K;
         if (more) xload(kc + KC);
-        const int csteps = (int)((K - kc < KC ? K - kc : KC) / kMfmaStepCols);
-        for (int t = 0; t < csteps; t += DEPTH) {
+        // every chunk holds a multiple of 4 steps: whole segments, DS of them
+        // per round (DS <= 2), so segment g sits in slot g % DS
+        const int csegs = (int)((K - kc < KC ? K - kc : KC) / (2 * kMfmaStepCols));
+        for (int t = 0; t < csegs; t += DS) {
 #pragma unroll
-            for (int u = 0; u < DEPTH; u++) {
-                const int jn = j0 + t + u + DEPTH;
-                uint4 b0 = *(const uint4 *)(bp + kMfmaStepCols * (t + u));
-                uint4 b1 = *(const uint4 *)(bp + kMfmaStepCols * (t + u) + 16);
-                if (!bn) b0 = b1 = make_uint4(0u, 0u, 0u, 0u);
-                const ut_i32x4 B0 = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w};
-                const ut_i32x4 B1 = {(int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
-#pragma unroll
-                for (int w = 0; w < TW; w++) {
-                    const uint4 wv = wq[u][w];
-                    wq[u][w] = ld_weights(ap[w] + 64 * (jn < nsteps ? jn : nsteps - 1));
-                    const uint32_t X = 0x88888888u;
-                    const uint32_t a0 = wv.x ^ X, a1 = wv.y ^ X, a2 = wv.z ^ X, a3 = wv.w ^ X;
-                    const ut_i32x4 A0 = {mfma_sext4(a0), mfma_sext4(a0 >> 4), mfma_sext4(a1),
-                                         mfma_sext4(a1 >> 4)};
-                    const ut_i32x4 A1 = {mfma_sext4(a2), mfma_sext4(a2 >> 4), mfma_sext4(a3),
-                                         mfma_sext4(a3 >> 4)};
-                    acc[w] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, acc[w], 0, 0, 0);
-                    acc[w] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, acc[w], 0, 0, 0);
-                }
-                __builtin_amdgcn_sched_barrier(0);
-            }
+            for (int u = 0; u < DS; u++) segment(wq[u], g0 + t + u, 2 * (t + u));
         }
-        j0 += csteps;
+        g0 += csegs;
         if (more) {
             lds_barrier();  // every wave is done with this chunk
             xstore(kc + KC);

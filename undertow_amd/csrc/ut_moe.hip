@@ -998,6 +998,11 @@ template <int M> constexpr int gate_up_mfma_kc() { return M == 2 ? 4096 : 2048; 
 // (two made the four-row launch 61.9 -> 73.1 us at DeepSeek-V3 width).
 template <int M, bool DUAL> constexpr int gate_up_mfma_tw() { return !DUAL && M >= 2 ? 2 : 1; }
 template <int M, bool DUAL> constexpr int gate_up_mfma_rows() { return 32 * gate_up_mfma_tw<M, DUAL>(); }
+// LDS of the matrix-core gate/up: the staged x chunk, then each wave's
+// weight-transpose area
+template <int M, bool DUAL> constexpr int gate_up_mfma_lds_words() {
+    return mfma_lds_words<M, gate_up_mfma_kc<M>()>() + 4 * gate_up_mfma_tw<M, DUAL>() * kI4WaveAreaBytes / 4;
+}
 
 template <int M, int TW>
 __device__ __forceinline__ void gate_up_mfma_body(const GateUpArgs &a, int u, int tile,
@@ -1012,12 +1017,14 @@ __device__ __forceinline__ void gate_up_mfma_body(const GateUpArgs &a, int u, in
     if (u >= cnt) return;
     if (tid < 4) wg_max[tid] = 0;
     const int64_t o0 = (int64_t)tile * (32 * TW) + wave * (8 * TW);  // tile w: rows o0 + 8w ..
-    const int ai = s & 7;  // this lane's A row: gate (s < 8) or up row o0 + 8w + ai
-    const uint8_t *arow[TW];
+    // tile rows 0-7 are gate rows o0 + 8w .., rows 8-15 the same up rows;
+    // load instruction r takes tile row 8r + lane / 8: gate (r = 0) or up
+    const uint8_t *lrows[TW][2];
 #pragma unroll
     for (int w = 0; w < TW; w++) {
-        const int64_t ao = o0 + 8 * w + ai < a.I ? o0 + 8 * w + ai : a.I - 1;
-        arow[w] = (s < 8 ? gw : uw) + ao * a.row_bytes;
+        const int64_t o = o0 + 8 * w + (lane >> 3), ao = o < a.I ? o : a.I - 1;
+        lrows[w][0] = gw + ao * a.row_bytes;
+        lrows[w][1] = uw + ao * a.row_bytes;
     }
     int32_t exl[M], sh[M];
 #pragma unroll
@@ -1026,7 +1033,10 @@ __device__ __forceinline__ void gate_up_mfma_body(const GateUpArgs &a, int u, in
         sh[m] = exl[m] == INT32_MIN ? INT32_MIN : -exl[m];
     }
     CoreOut<UT_FMT_INT4, M, 4> res[TW];
-    mfma_gemv_i4_chunks<M, KC, TW>(arow, a.H, a.mfma_xf, a.H, sh, (uint8_t *)lds, res);
+    mfma_gemv_i4_chunks<M, KC, TW>(lrows, a.H, a.mfma_xf, a.H, sh, (uint8_t *)lds,
+                                   (uint8_t *)lds + 4 * mfma_lds_words<M, KC>() +
+                                       wave * TW * kI4WaveAreaBytes,
+                                   res);
     // per tile: lanes 0-31 hold the gate totals of rows 4g + r (g < 2),
     // lanes 32-63 the up totals of the same rows
     const int r = s >> 2, m = s & 3;
@@ -1059,7 +1069,7 @@ __device__ __forceinline__ void gate_up_mfma_body(const GateUpArgs &a, int u, in
 
 template <int M>
 __global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up_mfma(GateUpArgs a) {
-    __shared__ __attribute__((aligned(16))) uint32_t lds[mfma_lds_words<M, gate_up_mfma_kc<M>()>()];
+    __shared__ __attribute__((aligned(16))) uint32_t lds[gate_up_mfma_lds_words<M, false>()];
     __shared__ uint32_t wg_max[4];
     gate_up_mfma_body<M, gate_up_mfma_tw<M, false>()>(a, blockIdx.y, blockIdx.x, lds, wg_max);
 }
@@ -1072,7 +1082,7 @@ constexpr int cmax_words(int p, int q) { return p > q ? p : q; }
 template <int M, int FB>
 __global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up_mfma_dual(GateUpArgs a, GateUpArgs b) {
     __shared__ __attribute__((aligned(16)))
-    uint32_t lds[cmax_words(mfma_lds_words<M, gate_up_mfma_kc<M>()>(), kLdsWords)];
+    uint32_t lds[cmax_words(gate_up_mfma_lds_words<M, true>(), kLdsWords)];
     __shared__ uint32_t wg_max[4];
     if (blockIdx.y + 1 < gridDim.y) {
         if ((int64_t)blockIdx.x * gate_up_mfma_rows<M, true>() < a.I)
@@ -1256,12 +1266,15 @@ __device__ __forceinline__ void down_mfma_body(const DownArgs &a, int u, int til
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
     constexpr int TW = down_mfma_tw<M>();
     const int64_t wrow0 = (int64_t)tile * (64 * TW) + wave * (16 * TW);
-    const uint8_t *arow[TW];
+    // load instruction r of tile w takes tile row 8r + lane / 8
+    const uint8_t *lrows[TW][2];
 #pragma unroll
-    for (int w = 0; w < TW; w++) {
-        const int64_t ar = wrow0 + 16 * w + s < a.H ? wrow0 + 16 * w + s : a.H - 1;
-        arow[w] = dw + ar * a.row_bytes;
-    }
+    for (int w = 0; w < TW; w++)
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const int64_t o = wrow0 + 16 * w + 8 * r + (lane >> 3);
+            lrows[w][r] = dw + (o < a.H ? o : a.H - 1) * a.row_bytes;
+        }
     ut_u32x4 pv[M];
     rowmax_load<M>(a.hmax_parts + (int64_t)u * M * a.nparts, a.nparts, pv);
     int32_t exl[M];
@@ -1275,8 +1288,10 @@ __device__ __forceinline__ void down_mfma_body(const DownArgs &a, int u, int til
         }
     };
     CoreOut<UT_FMT_INT4, M, 4> res[TW];
-    mfma_gemv_i4_f32x<M, down_mfma_depth<M>(), kDownMfmaKC, TW>(
-        arow, a.I, a.x.xf + u * a.x_slot_stride, a.x.ldx, (uint8_t *)lds, res, prep);
+    mfma_gemv_i4_f32x<M, down_mfma_depth<M>() / 2, kDownMfmaKC, TW>(
+        lrows, a.I, a.x.xf + u * a.x_slot_stride, a.x.ldx, (uint8_t *)lds,
+        (uint8_t *)lds + 4 * mfma_lds_words<M, kDownMfmaKC>() + wave * TW * kI4WaveAreaBytes, res,
+        prep);
 #pragma unroll
     for (int w = 0; w < TW; w++)
 #pragma unroll
@@ -1290,9 +1305,15 @@ __device__ __forceinline__ void down_mfma_body(const DownArgs &a, int u, int til
             }
 }
 
+// LDS of the matrix-core down: the staged h, then each wave's
+// weight-transpose area
+template <int M> constexpr int down_mfma_lds_words() {
+    return mfma_lds_words<M, kDownMfmaKC>() + 4 * down_mfma_tw<M>() * kI4WaveAreaBytes / 4;
+}
+
 template <int M>
 __global__ __launch_bounds__(kGemvThreads) void k_moe_down_mfma(DownArgs a) {
-    __shared__ __attribute__((aligned(16))) uint32_t lds[mfma_lds_words<M, kDownMfmaKC>()];
+    __shared__ __attribute__((aligned(16))) uint32_t lds[down_mfma_lds_words<M>()];
     __shared__ uint32_t red[4 * M];
     down_mfma_body<M>(a, blockIdx.y, blockIdx.x, lds, red);
 }
@@ -1305,7 +1326,7 @@ template <int M, int FB>
 __global__ __launch_bounds__(kGemvThreads) void k_moe_down_mfma_dual(DownArgs a, DownArgs b, int gxm,
                                                                     int nrouted) {
     __shared__ __attribute__((aligned(16)))
-    uint32_t lds[cmax_words(mfma_lds_words<M, kDownMfmaKC>(), kLdsWords)];
+    uint32_t lds[cmax_words(down_mfma_lds_words<M>(), kLdsWords)];
     __shared__ uint32_t red[4 * M];
     const int i = blockIdx.x;
     if (i < nrouted) down_mfma_body<M>(a, i / gxm, i % gxm, lds, red);
