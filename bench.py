@@ -769,8 +769,12 @@ def committed_traffic(kernel: str) -> tuple[float | None, str | None]:
     m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.]+)\s*$", text, re.M)
     if not m:
         return None, None
-    return float(m.group(1)), (f"profiles/{name} (FETCH_SIZE x2.0 + WRITE_SIZE x0.5 per "
-                               "dispatch, copy-scaled)")
+    fs = re.search(r"^fetch_scale:\s*([0-9.]+)\s*$", text, re.M)
+    ws = re.search(r"^write_scale:\s*([0-9.]+)\s*$", text, re.M)
+    scales = (f"FETCH_SIZE x{fs.group(1)} + WRITE_SIZE x{ws.group(1)}" if fs and ws
+              else "FETCH_SIZE + WRITE_SIZE")
+    return float(m.group(1)), f"profiles/{name} ({scales} per dispatch, copy-scaled)"
+
 
 
 def profile_decode(cfg_name: str, prompt_len: int, tokens: int, seed: int = 42,
