@@ -95,6 +95,8 @@ def _load(name):
         L.uto_quantize_activations.argtypes = [_f32p, C.c_int64, C.c_void_p]
         L.uto_quantize_activations.restype = C.c_float
         L.uto_matmul_fast_i8.argtypes = [C.c_void_p, _f32p, C.c_int64, C.c_int64, _f32p, C.c_int64, _f32p]
+        L.uto_set_fast_int8.argtypes = [C.c_int]
+        L.uto_fast_int8_enabled.restype = C.c_int
         L.uto_add_scaled_row.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_float, _f32p]
         L.uto_matvec_rows.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_int64, _f32p, _f32p]
         L.uto_rmsnorm.argtypes = [_f32p, _f32p, _f32p, C.c_int64, C.c_float]
@@ -259,6 +261,16 @@ def matmul_fast_i8(payload: np.ndarray, scales, out_dim: int, in_dim: int,
     sc = np.ascontiguousarray(scales, np.float32)
     lib().uto_matmul_fast_i8(_vp(q), sc, out_dim, in_dim, x.reshape(-1), seq, out)
     return out.reshape(seq, out_dim)
+
+
+def set_fast_int8(enabled: bool) -> None:
+    """undertow_core::set_fast_int8 (undertow-quant/src/lib.rs:35-43): the
+    oracle's int8 matmuls take the fast path while set (process-global)."""
+    lib().uto_set_fast_int8(int(bool(enabled)))
+
+
+def fast_int8_enabled() -> bool:
+    return bool(lib().uto_fast_int8_enabled())
 
 
 def add_scaled_row(fmt, payload, scales, out_dim, in_dim, row, factor, acc):

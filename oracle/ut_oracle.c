@@ -219,9 +219,20 @@ void ucb_matmul(int fmt, const void *payload, const float *scales, int64_t out_d
                 const float *x, int64_t seq, float *out, int nthreads);
 #endif
 
+/* FAST_INT8 (undertow-quant/src/lib.rs:31-43): process-global, off by
+ * default; QTensor::matmul on Int8 takes the fast path while it is set
+ * (qtensor.rs:385-398). */
+static int g_fast_int8 = 0;
+void uto_set_fast_int8(int on) { g_fast_int8 = on != 0; }
+int uto_fast_int8_enabled(void) { return g_fast_int8; }
+
 void uto_matmul(int fmt, const void *payload, const float *scales,
                 int64_t out_dim, int64_t in_dim, const float *x, int64_t seq,
                 float *out) {
+    if (g_fast_int8 && fmt == UTO_INT8) {
+        uto_matmul_fast_i8((const int8_t *)payload, scales, out_dim, in_dim, x, seq, out);
+        return;
+    }
 #ifdef UTO_SIMD_MATMUL
     if (fmt != UTO_F32) {
         ucb_matmul(fmt, payload, scales, out_dim, in_dim, x, seq, out, 0);

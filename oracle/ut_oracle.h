@@ -72,6 +72,10 @@ void uto_matmul(int fmt, const void *payload, const float *scales,
  * (neon.rs:139-184): out[s,o] = (acc as f32) * a_scale * scale[o] with acc
  * the exact integer dot of the i8 activations and the i8 codes. */
 float uto_quantize_activations(const float *x, int64_t n, int8_t *out);
+/* set_fast_int8 / fast_int8_enabled (lib.rs:35-43): while set, uto_matmul
+ * on int8 weights is uto_matmul_fast_i8 (every int8 matmul of the model). */
+void uto_set_fast_int8(int on);
+int uto_fast_int8_enabled(void);
 void uto_matmul_fast_i8(const int8_t *q, const float *scales, int64_t out_dim, int64_t in_dim,
                         const float *x, int64_t seq, float *out);
 /* QTensor::add_scaled_row (qtensor.rs:516-543). */

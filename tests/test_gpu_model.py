@@ -332,3 +332,46 @@ def test_quantized_agreement_floors(ctx, ref, fmt, floor, min_prefix):
                              m.generate_greedy(ref["prompt_ids"], max_new))
     assert rate >= floor, (fmt, rate)
     assert prefix >= min_prefix, (fmt, prefix)
+
+
+@pytest.mark.parametrize("fmt,cfg", [("int8", None), ("int4", C1)], ids=["tiny_int8", "c1_int4"])
+def test_fast_int8_mode_in_the_model(ctx, ref, fmt, cfg):
+    """ut_set_fast_int8 reaches every int8 matmul of the model, as the
+    reference's process-global switch reaches every int8 QTensor::matmul
+    (undertow-quant/src/lib.rs:35-59, qtensor.rs:385-398).  This backend
+    runs the absorbed attention for every path, where kv_b goes through
+    matvec_rows / add_scaled_row (exact in the reference too), so the bar is
+    the oracle's absorbed path (session path 1) under its switch: logits
+    within the model bar, greedy decode identical.  The reference's quality
+    gate holds on the int8 fixture (undertow-bench/tests/fast_int8.rs:24-61:
+    teacher-forcing agreement >= 0.75), and switching off restores the exact
+    path bit for bit."""
+    ck = checkpoint(cfg, fmt=fmt)
+    m = gpu_model(ctx, ck)
+    om = O.Model(ck)
+    ids = ref["full_ids"] if cfg is None else prompt_ids(16, C1["vocab_size"])
+    exact = m.forward(ids)
+    ctx.set_fast_int8(True)
+    O.set_fast_int8(True)
+    try:
+        got = m.forward(ids)
+        want = om.session(path=1).prefill(ids)
+        prompt = ids[:12]
+        stream = m.generate_greedy(prompt, 12)
+        os_ = om.session(path=1)
+        nxt = int(os_.prefill(prompt)[-1].argmax())
+        ostream = [nxt]
+        while len(ostream) < 12:
+            nxt = int(os_.decode(nxt).argmax())
+            ostream.append(nxt)
+    finally:
+        ctx.set_fast_int8(False)
+        O.set_fast_int8(False)
+    err = np.abs(got - want)
+    assert err.max() <= 1e-3 and err.mean() <= 1e-4, (err.max(), err.mean())
+    assert stream == ostream
+    assert not np.array_equal(got, exact)
+    if cfg is None:
+        agree = np.mean([int(got[s].argmax()) == ref["tf_pred"][s] for s in range(len(ids))])
+        assert agree >= 0.75, agree
+    assert np.array_equal(m.forward(ids), exact)

@@ -1130,49 +1130,6 @@ size_t matmul_digit_bytes(int64_t M, int64_t K) {
     return xdigits_bytes(M, K, XD_DIG4 | XD_DIG8 | XD_XT);
 }
 
-int32_t matmul_digits(ut_ctx *ctx, const ut_qtensor *w, const float *x, const XDigits &xd,
-                      int64_t M, float *out, int64_t ldo, int accumulate) {
-    GemvArgs ga;
-    ga.w = w;
-    ga.M = M;
-    ga.out = out;
-    ga.ldo = ldo;
-    ga.accumulate = accumulate;
-    ga.xf = x;
-    ga.xd = xd;
-    if (w->fmt != UT_FMT_F32) {
-        const bool need4 = w->fmt == UT_FMT_INT4 && fast_ok(w), need8 = w->fmt == UT_FMT_INT8 && fast_ok(w);
-        if ((need4 && !xd.dig4) || (need8 && !xd.dig8) || (!fast_ok(w) && !xd.xt)) {
-            set_error(ctx, "matmul_digits: activation digits of the wrong form");
-            return UT_ERR_ARG;
-        }
-    }
-    return gemv(ctx, ga);
-}
-
-int32_t matmul_dev(ut_ctx *ctx, const ut_qtensor *w, const float *x, int64_t M, float *out,
-                   int64_t ldo, int accumulate, void *digit_scratch) {
-    if (M <= 0) return UT_OK;
-    GemvArgs ga;
-    ga.w = w;
-    ga.M = M;
-    ga.out = out;
-    ga.ldo = ldo;
-    ga.accumulate = accumulate;
-    if (w->fmt == UT_FMT_F32) {
-        ga.xf = x;
-        return gemv(ctx, ga);
-    }
-    int flags = fast_ok(w) ? xdigit_flags_for(w->fmt, w->in_dim) : XD_XT;
-    ga.xd = xdigits_view(digit_scratch, M, w->in_dim, flags);
-    UT_TRY(launch_digitize(ctx, x, w->in_dim, M, w->in_dim, nullptr, ga.xd, flags));
-    return gemv(ctx, ga);
-}
-
-}  // namespace ut
-
-using namespace ut;
-
 // ------------------------------------------------------ fast int8 ---
 // The opt-in fast-int8 path (undertow-quant/src/lib.rs:31-59,
 // avx512.rs:221-242).  k_act_quant_i8: one workgroup per activation row,
@@ -1215,7 +1172,8 @@ __global__ __launch_bounds__(256) void k_gemv_fast_i8(const int8_t *__restrict__
                                                       const float *__restrict__ scales, int64_t O,
                                                       int64_t K, const int8_t *__restrict__ xq,
                                                       int64_t kp, const float *__restrict__ ascale,
-                                                      float *__restrict__ out, int64_t ldo) {
+                                                      float *__restrict__ out, int64_t ldo,
+                                                      int accumulate) {
     const int64_t o = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int64_t m = blockIdx.y;
     const int lane = threadIdx.x & 63;
@@ -1236,11 +1194,15 @@ __global__ __launch_bounds__(256) void k_gemv_fast_i8(const int8_t *__restrict__
         for (int64_t c = lane; c < K; c += 64) acc += (int32_t)wr[c] * (int32_t)xr[c];
     }
     for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
-    if (lane == 0) out[m * ldo + o] = __fmul_rn(__fmul_rn((float)acc, ascale[m]), scales[o]);
+    if (lane == 0) {
+        const float v = __fmul_rn(__fmul_rn((float)acc, ascale[m]), scales[o]);
+        float *po = out + m * ldo + o;
+        *po = accumulate ? __fadd_rn(*po, v) : v;
+    }
 }
 
-static int32_t matmul_fast_i8(ut_ctx *ctx, const ut_qtensor *qt, float *out, const float *x,
-                              int64_t seq) {
+int32_t matmul_fast_i8(ut_ctx *ctx, const ut_qtensor *qt, float *out, int64_t ldo, int accumulate,
+                       const float *x, int64_t seq) {
     const int64_t K = qt->in_dim, O = qt->out_dim, kp = (K + 15) / 16 * 16;
     ScratchPlan plan;
     plan.add((size_t)(seq * kp));
@@ -1254,10 +1216,60 @@ static int32_t matmul_fast_i8(ut_ctx *ctx, const ut_qtensor *qt, float *out, con
                        kp, as);
     hipLaunchKernelGGL(k_gemv_fast_i8, dim3((unsigned)((O + 3) / 4), (unsigned)seq), dim3(256), 0,
                        ctx->stream, (const int8_t *)qt->payload, qt->scales, O, K, xq, kp, as, out,
-                       O);
+                       ldo, accumulate);
     timing_end(ctx, tok);
     return launch_check(ctx, "k_gemv_fast_i8");
 }
+
+
+int32_t matmul_digits(ut_ctx *ctx, const ut_qtensor *w, const float *x, const XDigits &xd,
+                      int64_t M, float *out, int64_t ldo, int accumulate) {
+    // the opt-in fast-int8 path replaces every int8 QTensor::matmul
+    // (qtensor.rs:385-398): activations quantised per row from x itself
+    if (ctx->fast_int8 && w->fmt == UT_FMT_INT8 && M > 0)
+        return matmul_fast_i8(ctx, w, out, ldo, accumulate, x, M);
+    GemvArgs ga;
+    ga.w = w;
+    ga.M = M;
+    ga.out = out;
+    ga.ldo = ldo;
+    ga.accumulate = accumulate;
+    ga.xf = x;
+    ga.xd = xd;
+    if (w->fmt != UT_FMT_F32) {
+        const bool need4 = w->fmt == UT_FMT_INT4 && fast_ok(w), need8 = w->fmt == UT_FMT_INT8 && fast_ok(w);
+        if ((need4 && !xd.dig4) || (need8 && !xd.dig8) || (!fast_ok(w) && !xd.xt)) {
+            set_error(ctx, "matmul_digits: activation digits of the wrong form");
+            return UT_ERR_ARG;
+        }
+    }
+    return gemv(ctx, ga);
+}
+
+int32_t matmul_dev(ut_ctx *ctx, const ut_qtensor *w, const float *x, int64_t M, float *out,
+                   int64_t ldo, int accumulate, void *digit_scratch) {
+    if (M <= 0) return UT_OK;
+    if (ctx->fast_int8 && w->fmt == UT_FMT_INT8)
+        return matmul_fast_i8(ctx, w, out, ldo, accumulate, x, M);
+    GemvArgs ga;
+    ga.w = w;
+    ga.M = M;
+    ga.out = out;
+    ga.ldo = ldo;
+    ga.accumulate = accumulate;
+    if (w->fmt == UT_FMT_F32) {
+        ga.xf = x;
+        return gemv(ctx, ga);
+    }
+    int flags = fast_ok(w) ? xdigit_flags_for(w->fmt, w->in_dim) : XD_XT;
+    ga.xd = xdigits_view(digit_scratch, M, w->in_dim, flags);
+    UT_TRY(launch_digitize(ctx, x, w->in_dim, M, w->in_dim, nullptr, ga.xd, flags));
+    return gemv(ctx, ga);
+}
+
+}  // namespace ut
+
+using namespace ut;
 
 extern "C" int32_t ut_set_fast_int8(ut_ctx *ctx, int32_t enabled) {
     if (!ctx) return UT_ERR_ARG;
@@ -1287,7 +1299,8 @@ extern "C" int32_t ut_qtensor_matmul(ut_ctx *ctx, const ut_qtensor *qt, float *o
     }
     if (seq == 0) return UT_OK;
     // Int8 { .. } if fast_int8_enabled() (qtensor.rs:385-398)
-    if (qt->fmt == UT_FMT_INT8 && ctx->fast_int8) return matmul_fast_i8(ctx, qt, out_dev, x_dev, seq);
+    if (qt->fmt == UT_FMT_INT8 && ctx->fast_int8)
+        return matmul_fast_i8(ctx, qt, out_dev, qt->out_dim, 0, x_dev, seq);
     GemvArgs ga;
     ga.w = qt;
     ga.M = seq;

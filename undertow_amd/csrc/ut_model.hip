@@ -51,6 +51,7 @@ struct LayerW {
     MlpW shared;
     void *experts_dev = nullptr;     // 6*E device pointers
     ExpertPtrs experts{};
+    std::vector<const ut_qtensor *> eqt;  // [E][3] gate, up, down (resident experts)
     int expert_fmt = UT_FMT_F32;
     int64_t index = 0;               // layer index (the MTP layer: num_hidden_layers)
 };
@@ -109,6 +110,7 @@ struct Workspace {
     int32_t *vexps = nullptr;  // o_proj activation exponents per row
     void *digits = nullptr, *moe = nullptr, *mla = nullptr, *argm = nullptr;
     void *digA = nullptr, *digB = nullptr;  // activation digits shared by consumers
+    float *fast = nullptr;  // the fast-int8 path's MLP rows
 };
 
 }  // namespace
@@ -298,6 +300,7 @@ int32_t load_layer(ut_model *m, int64_t li, bool dense, LayerW *L) {
         UT_TRY(get_qt(m, ep + "up_proj.weight", I, H, &u));
         UT_TRY(get_qt(m, ep + "down_proj.weight", H, I, &d));
         if (fmt < 0) fmt = g->fmt;
+        L->eqt.insert(L->eqt.end(), {g, u, d});
         if (g->fmt != fmt || u->fmt != fmt || d->fmt != fmt) {
             set_error(m->ctx, "layer %lld: experts must share one format", (long long)li);
             return UT_ERR_FORMAT;
@@ -383,6 +386,10 @@ int32_t ws_reserve(ut_session *s, int64_t rows) {
     size_t imoes = plan.add(moe_bytes);
     size_t imla = plan.add(mla_scratch_bytes(R < kMlaRowsPerCall ? R : kMlaRowsPerCall, heads, Lr, c.qk_rope_head_dim, s->cap));
     size_t iarg = plan.add(argmax_scratch_bytes(R, c.vocab_size) + 256);
+    // the fast-int8 path's MLP and expert rows (four rows at a time): gate,
+    // up, h [4][max inter], the choices' outputs [4][k][H] and a shared
+    // MLP's [4][H]
+    size_t ifast = F(3 * 4 * max_inter(m) + 4 * (k > 0 ? k : 1) * H + 4 * H);
     size_t total = 0;
     for (size_t b : plan.sizes) total += b;
     if (w.base) {
@@ -425,6 +432,7 @@ int32_t ws_reserve(ut_session *s, int64_t rows) {
     w.vmax = (uint32_t *)p[ivmax]; w.vexps = (int32_t *)p[ivexp];
     w.digits = p[idig]; w.moe = p[imoes]; w.mla = p[imla]; w.argm = p[iarg];
     w.digA = p[idA]; w.digB = p[idB];
+    w.fast = (float *)p[ifast];
     w.rows = R;
     UT_CHECK_HIP(ctx, hipMemsetAsync(w.err, 0, 4, ctx->stream));
     return UT_OK;
@@ -434,6 +442,80 @@ int32_t ws_reserve(ut_session *s, int64_t rows) {
 int32_t mm(ut_session *s, const ut_qtensor *w, const float *x, int64_t M, float *out, int64_t ldo,
            int accumulate = 0) {
     return matmul_dev(s->ctx, w, x, M, out, ldo, accumulate, s->ws.digits);
+}
+
+// The opt-in fast-int8 mode (ut_set_fast_int8 on the session's context,
+// undertow-quant/src/lib.rs:31-59): every int8 QTensor::matmul of the model
+// quantises its activations per row (matmul_dev / matmul_digits take the
+// fast kernel), so the fused launches that hand digits between kernels are
+// not used, and the MLPs and routed experts run as separate matmuls in the
+// reference's order.
+bool fast8(const ut_session *s) { return s->ctx->fast_int8; }
+
+// h = silu(g) * u (undertow-quant/src/lib.rs:121, model.rs:241-247)
+__global__ void k_silu_mul(const float *__restrict__ g, const float *__restrict__ u,
+                           float *__restrict__ h, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float gv = g[i];
+    h[i] = __fmul_rn(gv / (1.0f + expf(-gv)), u[i]);
+}
+
+// out[s] (+)= (init[s] +) y[s] per element: forward_add of an MLP, or with
+// init the shared expert added to the routed sum before the residual add
+__global__ void k_add_rows(float *__restrict__ out, int64_t ldo, const float *__restrict__ init,
+                           const float *__restrict__ y, int64_t n, int64_t rows) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n * rows) return;
+    const int64_t r = i / n, o = i - r * n;
+    const float t = init ? __fadd_rn(init[r * n + o], y[i]) : y[i];
+    float *po = out + r * ldo + o;
+    *po = __fadd_rn(*po, t);
+}
+
+// moe_forward's combine (model.rs:268-284) over per-choice outputs
+// d [rows][k][H]: sum = 0, sum += w[s,c] * d[s,c] in router order (choices
+// with a negative id skipped), then + shared[s] when given, then the
+// residual add out[s] += sum.
+__global__ void k_combine_rows(const float *__restrict__ d, const float *__restrict__ w,
+                               const int32_t *__restrict__ ids, int k, int64_t H,
+                               const float *__restrict__ shared, float *__restrict__ out,
+                               int64_t ldo) {
+    const int s = blockIdx.y;
+    const int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (o >= H) return;
+    float acc = 0.0f;
+    for (int c = 0; c < k; c++) {
+        if (ids[s * k + c] < 0) continue;
+        acc = __fadd_rn(acc, __fmul_rn(w[s * k + c], d[((int64_t)s * k + c) * H + o]));
+    }
+    if (shared) acc = __fadd_rn(acc, shared[(int64_t)s * H + o]);
+    float *po = out + (int64_t)s * ldo + o;
+    *po = __fadd_rn(*po, acc);
+}
+
+// An MLP over up to four rows as three matmuls (MlpWeights::forward_add,
+// model.rs:43-58): y = down(silu(gate x) * up x), then out += y, or with
+// init out += init + y.  y_out: also keep y there (the shared expert).
+int32_t mlp_rows_fast(ut_session *s, const MlpW &w, const float *x, int64_t rows, float *out,
+                      int64_t ldo, const float *init, float *y_out) {
+    ut_ctx *ctx = s->ctx;
+    const int64_t H = hd(s->m), I = w.inter, R = max_inter(s->m);
+    const int64_t k = s->m->c.num_experts_per_tok > 0 ? s->m->c.num_experts_per_tok : 1;
+    // ws.fast: g, u, h [4][R], then the choices' outputs [4][k][H], then y [4][H]
+    float *g = s->ws.fast, *u = g + 4 * R, *h = u + 4 * R, *y = h + 4 * R + 4 * k * H;
+    UT_TRY(mm(s, w.gate, x, rows, g, I));
+    UT_TRY(mm(s, w.up, x, rows, u, I));
+    const int64_t n = rows * I;
+    hipLaunchKernelGGL(k_silu_mul, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream, g, u,
+                       h, n);
+    UT_TRY(launch_check(ctx, "k_silu_mul"));
+    if (y_out) return mm(s, w.down, h, rows, y_out, H);
+    if (!init) return mm(s, w.down, h, rows, out, ldo, 1);
+    UT_TRY(mm(s, w.down, h, rows, y, H));
+    hipLaunchKernelGGL(k_add_rows, dim3((unsigned)((rows * H + 255) / 256)), dim3(256), 0,
+                       ctx->stream, out, ldo, init, y, H, rows);
+    return launch_check(ctx, "k_add_rows");
 }
 
 // Digit forms the given weights need from one shared activation.
@@ -471,6 +553,14 @@ int32_t mlp_add(ut_session *s, const MlpW &w, const float *x, const XDigits &xd,
                 float *out, const float *init = nullptr, const NormNext *next = nullptr) {
     ut_model *m = s->m;
     if (next && rows > 4) return UT_ERR_ARG;  // x and xd would be overwritten mid-loop
+    if (fast8(s)) {
+        if (next) return UT_ERR_ARG;  // the fused next norm is not used in this mode
+        const int64_t H = hd(m);
+        for (int64_t s0 = 0; s0 < rows; s0 += 4)
+            UT_TRY(mlp_rows_fast(s, w, x + s0 * H, rows - s0 < 4 ? rows - s0 : 4, out + s0 * H, H,
+                                 init ? init + s0 * H : nullptr, nullptr));
+        return UT_OK;
+    }
     for (int64_t s0 = 0; s0 < rows; s0 += 4) {
         MoeCall c;
         c.fmt = w.fmt;
@@ -643,6 +733,63 @@ int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
     return UT_OK;
 }
 
+// moe_forward in the fast-int8 mode (model.rs:195-286) over normed rows x,
+// added with the shared expert into out (the residual): the f32 router
+// gate and the router on the device, the choices read back, each choice's
+// expert MLP as three matmuls of its row (activations are quantised per
+// row, so a row's result does not depend on which rows share an expert),
+// then the combine in router order.
+int32_t moe_forward_fast(ut_session *s, const LayerW &L, const float *x, int64_t rows, float *out) {
+    ut_model *m = s->m;
+    ut_ctx *ctx = s->ctx;
+    const ut_model_config &c = m->c;
+    if (m->store || L.eqt.empty()) {
+        set_error(ctx, "the fast-int8 mode needs every routed expert resident");
+        return UT_ERR_STATE;
+    }
+    const int64_t H = c.hidden_size, E = c.n_routed_experts, I = c.moe_intermediate_size;
+    const int k = (int)c.num_experts_per_tok;
+    const int64_t R = max_inter(m);
+    float *d = s->ws.fast + 3 * 4 * R, *ysh = d + 4 * k * H;
+    for (int64_t s0 = 0; s0 < rows; s0 += 4) {
+        const int M = (int)(rows - s0 < 4 ? rows - s0 : 4);
+        UT_TRY(mm(s, L.gate, x + s0 * H, M, s->ws.rlogits, E));
+        UT_TRY(launch_route(ctx, s->ws.rlogits, L.bias, M, E, k, (int)c.n_group, (int)c.topk_group,
+                            c.norm_topk_prob, c.routed_scaling_factor, s->ws.rids, s->ws.rw));
+        std::vector<int32_t> ids((size_t)M * k);
+        void *pin = nullptr;
+        UT_TRY(pinned_acquire(ctx, ids.size() * 4, &pin));
+        UT_CHECK_HIP(ctx, hipMemcpyAsync(pin, s->ws.rids, ids.size() * 4, hipMemcpyDeviceToHost,
+                                         ctx->stream));
+        UT_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        memcpy(ids.data(), pin, ids.size() * 4);
+        for (int r = 0; r < M; r++)
+            for (int j = 0; j < k; j++) {
+                const int32_t e = ids[(size_t)r * k + j];
+                if (e < 0) continue;
+                if (e >= E) {
+                    set_error(ctx, "a routed expert id was out of range or not loaded");
+                    return UT_ERR_BAD_EXPERT;
+                }
+                MlpW ew;
+                ew.gate = L.eqt[(size_t)3 * e];
+                ew.up = L.eqt[(size_t)3 * e + 1];
+                ew.down = L.eqt[(size_t)3 * e + 2];
+                ew.fmt = ew.gate->fmt;
+                ew.inter = I;
+                UT_TRY(mlp_rows_fast(s, ew, x + (s0 + r) * H, 1, nullptr, 0, nullptr,
+                                     d + ((int64_t)r * k + j) * H));
+            }
+        if (L.has_shared)
+            UT_TRY(mlp_rows_fast(s, L.shared, x + s0 * H, M, nullptr, 0, nullptr, ysh));
+        hipLaunchKernelGGL(k_combine_rows, dim3((unsigned)((H + 255) / 256), (unsigned)M), dim3(256),
+                           0, ctx->stream, d, s->ws.rw, s->ws.rids, k, H,
+                           L.has_shared ? ysh : nullptr, out + s0 * H, H);
+        UT_TRY(launch_check(ctx, "k_combine_rows"));
+    }
+    return UT_OK;
+}
+
 // mla_forward_cached, absorbed form (attention.rs:123-279), added into out
 // (the residual).  x: normed rows with digits xd.
 int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, const XDigits &xd,
@@ -658,7 +805,7 @@ int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
     const int64_t qh = nope + rope;
     const float scale = 1.0f / sqrtf((float)qh);  // config.rs:142-144
     const int64_t pos_base = kv.len;
-    const bool pair = L.lora && L.kv_a->fmt == L.q_a->fmt && L.kv_a->fmt != UT_FMT_F32 &&
+    const bool pair = !fast8(s) && L.lora && L.kv_a->fmt == L.q_a->fmt && L.kv_a->fmt != UT_FMT_F32 &&
                       L.kv_a->in_dim == L.q_a->in_dim && L.kv_a->row_bytes == L.q_a->row_bytes &&
                       gemv_fast_ok(L.kv_a) && gemv_fast_ok(L.q_a);
     // with the pair's split-K partials deferred, one launch finishes both
@@ -721,7 +868,7 @@ int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
     // x += o_proj(ctx) (the residual add of model.rs:478-480 in the epilogue);
     // with absorb_v's row maxima the o_proj GEMV digitises ctx itself while
     // staging (no separate digitising launch; the same digits)
-    const bool vm = absorb_v_max_ok(L.kv_b) && L.o_proj->fmt != UT_FMT_F32 &&
+    const bool vm = !fast8(s) && absorb_v_max_ok(L.kv_b) && L.o_proj->fmt != UT_FMT_F32 &&
                     gemv_fast_ok(L.o_proj) && rows <= 4;
     UT_TRY(launch_absorb_v(ctx, L.kv_b, w.clat, rows, heads, nope, vh, w.ctxv,
                            vm ? w.vmax : nullptr));
@@ -745,8 +892,8 @@ int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
 // Whether the norm that follows a layer (the next layer's input norm, the
 // final norm) can run inside the layer's last combine: every consumer of the
 // layer's own normed rows has run by then, and rows fit one combine.
-bool fuse_next_ok(const ut_model *m, int64_t rows) {
-    return rows <= 4 && moe_combine_norm_ok(m->c.hidden_size);
+bool fuse_next_ok(const ut_session *s, int64_t rows) {
+    return rows <= 4 && moe_combine_norm_ok(s->m->c.hidden_size) && !fast8(s);
 }
 
 // The fused norm's arguments: rmsnorm with norm_w into ws.normed and the
@@ -789,11 +936,12 @@ int32_t run_layer(ut_session *s, const LayerW &L, float *x, int64_t rows, KvCach
     XDigits pd;
     const NormNext post = next_norm(s, L.post_norm, f, rows, &pd);
     bool post_done = false;
-    UT_TRY(mla_forward(s, L, w.normed, xd, rows, kv, x, fuse_next_ok(m, rows) ? &post : nullptr,
+    UT_TRY(mla_forward(s, L, w.normed, xd, rows, kv, x, fuse_next_ok(s, rows) ? &post : nullptr,
                        &post_done));
     if (post_done) xd = pd;
     else UT_TRY(norm_dig(s, x, H, L.post_norm, H, rows, w.normed, H, w.digA, f, &xd));
     if (L.dense) return mlp_add(s, L.mlp, w.normed, xd, rows, x, nullptr, next);
+    if (fast8(s)) return moe_forward_fast(s, L, w.normed, rows, x);
     // x += (routed + shared) (model.rs:282-284 then the residual add)
     if (L.has_shared && moe_dual_ok(L.expert_fmt, L.shared.fmt))
         return moe_forward(s, L, w.normed, xd, rows, x, 1, &L.shared, next);
@@ -862,7 +1010,7 @@ int32_t prefill_dev(ut_session *s, const int32_t *ids, int64_t n, const int32_t 
     UT_TRY(launch_embed(ctx, m->embed, ids_dev ? ids_dev : w.ids, n, w.x, H));
     // each layer's last combine runs the norm that follows it when the rows
     // fit one combine (decode and verify steps)
-    const bool fuse = fuse_next_ok(m, n);
+    const bool fuse = fuse_next_ok(s, n);
     XDigits cur, nxt;
     const size_t nl = m->layers.size();
     for (size_t li = 0; li < nl; li++) {
@@ -986,7 +1134,7 @@ int32_t draft_rows_dev(ut_session *s, const int32_t *host_ids, int in_slot,
     UT_TRY(mm(s, m->eh_proj, w.cat, rows, w.x, H));
     XDigits hd_;
     const float *hn = w.normed;
-    if (fuse_next_ok(m, rows)) {
+    if (fuse_next_ok(s, rows)) {
         // the layer's last combine normalises every row; the head reads the last
         XDigits all;
         const NormNext nx = next_norm(s, m->mtp_norm, dig_flags({m->mtp_head}), rows, &all);
@@ -1335,7 +1483,8 @@ struct Emit {
 // growth, happens there).
 bool graph_ok(const ut_session *s, int64_t eager_steps) {
     const ut_model *m = s->m;
-    return m->graphs && !s->graph_failed && !m->store && !s->ctx->timing && eager_steps >= 1;
+    return m->graphs && !s->graph_failed && !m->store && !s->ctx->timing && !fast8(s) &&
+           eager_steps >= 1;
 }
 
 // Captures the launches of body() (a step of the session) into *exec.  The
