@@ -19,6 +19,9 @@ OBJ = HERE / "lib" / "obj"
 LIB = HERE / "lib" / "libundertow_hip.so"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+# Tuning switches of the sources (``#ifndef UT_...`` macros), e.g.
+# UT_BUILD_DEFINES="-DUT_MOE_FOLD_COMBINE=1" to rebuild a measured variant.
+DEFINES = os.environ.get("UT_BUILD_DEFINES", "").split()
 ARCH = "gfx950"
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-ffp-contract=off",
@@ -29,7 +32,7 @@ FLAGS = [
 
 def _compile(src: Path) -> Path:
     obj = OBJ / (src.stem + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *FLAGS, *DEFINES, "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{r.stdout}\n{r.stderr}")
@@ -38,6 +41,9 @@ def _compile(src: Path) -> Path:
 
 def build(jobs: int = 8) -> Path:
     """Compile every HIP source and link the shared library (always rebuilds)."""
+    bad = [d for d in DEFINES if not d.startswith("-DUT_")]
+    if bad:
+        raise RuntimeError(f"UT_BUILD_DEFINES takes -DUT_* switches only, got {bad}")
     if not Path(HIPCC).exists() and shutil.which("hipcc") is None:
         raise RuntimeError("hipcc not found; cannot build the gfx950 backend")
     OBJ.mkdir(parents=True, exist_ok=True)

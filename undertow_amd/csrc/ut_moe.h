@@ -98,6 +98,7 @@ struct ScratchLayout {
     size_t total = 0;
     size_t count = 0, uniq = 0, choice = 0, sp = 0, xd = 0, h = 0, hmax = 0, hd = 0, d = 0, dpart = 0;
     size_t xw = 0;  // bf16 activations widened to f32 (when not staged by gate/up)
+    size_t arrive = 0;  // down's folded-combine arrival counters, one per 32 rows of H
     int xflags = 0, hflags = 0;
     int64_t ntiles = 0;
 };

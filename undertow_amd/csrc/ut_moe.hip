@@ -594,7 +594,18 @@ struct GateUpArgs {
     float route_scale = 1.0f;
     int32_t *route_ids = nullptr;
     float *route_w = nullptr;
+    // optional: zeroed by workgroup (0, 0) for the down launch that follows
+    // (its folded combine's arrival counters, CombineFold)
+    int32_t *arrive = nullptr;
+    int narrive = 0;
 };
+
+// Workgroup (0, 0) of a gate/up launch clears the next down launch's
+// arrival counters (stream order makes them zero when down starts).
+__device__ __forceinline__ void clear_arrivals(const GateUpArgs &a, int u, int tile) {
+    if (a.arrive && u == 0 && tile == 0)
+        for (int i = threadIdx.x; i < a.narrive; i += blockDim.x) a.arrive[i] = 0;
+}
 
 // The slot plan of make_plan for one activation row (n = k <= 64 entries),
 // resolved by each wave on its own (lane j holds entry j; no LDS, no
@@ -876,6 +887,7 @@ __device__ __forceinline__ void gate_up_body(const GateUpArgs &a, int u, int til
     const float *gsc = nullptr, *usc = nullptr;
     int cnt = 0;
     if (tid < 4) wg_max[tid] = 0;  // published by the core's barriers
+    clear_arrivals(a, u, tile);
     CoreOut<FMT, M, 2> res;
     // x's exponents: given, or (self_max) found while x is staged (prep)
     int32_t exl[M];
@@ -1014,6 +1026,7 @@ __device__ __forceinline__ void gate_up_mfma_body(const GateUpArgs &a, int u, in
     const uint8_t *uw = (const uint8_t *)a.sp[u * 6 + kSpUp];
     const float *gsc = (const float *)a.sp[u * 6 + kSpGateS];
     const float *usc = (const float *)a.sp[u * 6 + kSpUpS];
+    clear_arrivals(a, u, tile);
     if (u >= cnt) return;
     if (tid < 4) wg_max[tid] = 0;
     const int64_t o0 = (int64_t)tile * (32 * TW) + wave * (8 * TW);  // tile w: rows o0 + 8w ..
@@ -1112,6 +1125,29 @@ __global__ __launch_bounds__(kGemvThreads, M <= 2 ? 5 : 1) void k_moe_gate_up_du
 }
 
 // --------------------------------------------------------------- down ---
+// UT_MOE_FOLD_COMBINE=1: fold the routed combine into down (CombineFold)
+// instead of a combine launch after it.  Off: each workgroup's agent-scope
+// release writes back its XCD's L2, and at config 2's 1,792 down
+// workgroups that took down from 14.2 to 178 us per launch.
+#ifndef UT_MOE_FOLD_COMBINE
+#define UT_MOE_FOLD_COMBINE 0
+#endif
+// The routed experts' combine folded into down: each workgroup of a row
+// band (one per slot) releases its d rows and counts in at arrive[band];
+// the one that counts last adds the band's columns of out exactly as
+// k_moe_combine4 does (router choice order, the same init / extra /
+// shared / accumulate terms), so no combine launch follows.  The counters
+// are cleared by the gate/up launch before (GateUpArgs::arrive).
+struct CombineFold {
+    int32_t *arrive = nullptr;  // [bands]; nullptr: no fold
+    const int32_t *choice_slot = nullptr;
+    const float *weights = nullptr;
+    int k = 0, extra = 0, accumulate = 0;
+    const float *dshared = nullptr, *init = nullptr;
+    float *out = nullptr;
+    int64_t ldo = 0;
+};
+
 struct DownArgs {
     ExpertPtrs tbl;
     const void *const *sp;  // the plan's per-slot weight pointers
@@ -1129,7 +1165,11 @@ struct DownArgs {
     int ks = 1;
     int64_t kslice = 0;
     int64_t *part = nullptr;
+    CombineFold fold{};
 };
+
+template <int M>
+__device__ void fold_combine(const DownArgs &a, int band, int64_t c0, int ncols);
 
 // The digitisation shift of h row (u, m): 22 - E with max|h| < 2^E, from the
 // gate/up workgroups' partial maxima (INT32_MIN: non-finite row).  Whole
@@ -1316,6 +1356,8 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_down_mfma(DownArgs a) {
     __shared__ __attribute__((aligned(16))) uint32_t lds[down_mfma_lds_words<M>()];
     __shared__ uint32_t red[4 * M];
     down_mfma_body<M>(a, blockIdx.y, blockIdx.x, lds, red);
+    if (a.fold.arrive) fold_combine<M>(a, blockIdx.x, (int64_t)blockIdx.x * 64 * down_mfma_tw<M>(),
+                                       64 * down_mfma_tw<M>());
 }
 
 // The routed experts' down on the matrix cores and a shared MLP's down
@@ -1337,6 +1379,10 @@ template <int FMT, int M>
 __global__ __launch_bounds__(kGemvThreads) void k_moe_down(DownArgs a) {
     __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
     down_body<FMT, M>(a, blockIdx.y, blockIdx.x, lds);
+    if (a.fold.arrive) {
+        constexpr int DR = 16 * down_rows<M>();
+        fold_combine<M>(a, blockIdx.x, (int64_t)blockIdx.x * DR, DR);
+    }
 }
 
 // Sums the split-K partials of down (slot u, row m) in z order (integers
@@ -1496,6 +1542,33 @@ __global__ __launch_bounds__(256) void k_moe_combine4(
     *(float4 *)po = make_float4(acc[0], acc[1], acc[2], acc[3]);
 }
 
+// Down's folded combine (CombineFold): columns [c0, c0 + ncols) of every
+// row, by the band's last workgroup.  Every thread releases its own d
+// stores (agent scope: other XCDs' workgroups read them) before the count.
+template <int M>
+__device__ void fold_combine(const DownArgs &a, int band, int64_t c0, int ncols) {
+    __shared__ int s_last;
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) s_last = atomicAdd(a.fold.arrive + band, 1) == (int)gridDim.y - 1;
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    const CombineFold &f = a.fold;
+    const int per_row = ncols / 4;
+    for (int t = threadIdx.x; t < M * per_row; t += blockDim.x) {
+        const int s = t / per_row;
+        const int64_t c = c0 + 4 * (t - s * per_row);
+        if (c >= a.H) continue;
+        float *po = f.out + s * f.ldo + c;
+        float acc[4];
+        combine_cols<4>(f.choice_slot, f.weights, a.d, M, f.k, a.H, a.count, f.extra, f.dshared,
+                        f.init ? f.init + s * f.ldo + c : nullptr, f.accumulate ? po : nullptr, s,
+                        c, acc);
+        *(float4 *)po = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    }
+}
+
 // The same combine for one row per workgroup (thread t: columns 8t..8t+7,
 // each computed exactly as k_moe_combine does), then the finished row
 // rms-normalised and digitised by the row digitiser's body (nd: K = H).
@@ -1552,6 +1625,7 @@ ScratchLayout moe_layout(int64_t M, int64_t k, int64_t slots, int64_t H, int64_t
     L.d = take((size_t)slots * M * H * 4);
     L.dpart = take(slots == 1 ? (size_t)kDownMaxSplit * M * H * 8 : 0);
     L.xw = take((size_t)M * H * 4);
+    L.arrive = take((size_t)(H + 31) / 32 * 4);
     L.xflags = xflags;
     L.hflags = hflags;
     L.ntiles = ntiles;
@@ -1724,6 +1798,14 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
     GateUpArgs gb{};
     DownArgs db{};
     float *dshared = nullptr;
+    // the combine folded into the down launch (CombineFold): plain combine
+    // (no fused norm), the routed experts alone, no K split, rows as
+    // k_moe_combine4 takes them
+    const bool split_down = slots == 1 && !c.shared;
+    const bool fold = UT_MOE_FOLD_COMBINE && !c.next && !c.shared && !split_down && c.H % 4 == 0 &&
+                      c.ldo % 4 == 0 && ((uintptr_t)c.out & 15) == 0 &&
+                      (!c.init || ((uintptr_t)c.init & 15) == 0);
+    int32_t *arrive = fold ? (int32_t *)(base + L.arrive) : nullptr;
     {
         GateUpArgs a;
         a.tbl = c.tbl;
@@ -1760,6 +1842,8 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
             a.route_ids = c.route_ids;
             a.route_w = c.route_w;
         }
+        a.arrive = arrive;
+        a.narrive = (int)((c.H + 31) / 32);
         if (c.shared) {
             const MoeCall &sc = *c.shared;
             gb.tbl = sc.tbl;
@@ -1800,9 +1884,20 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
         a.hmax_parts = hmax;
         a.nparts = (int)L.ntiles;
         a.d = d;
+        if (fold) {
+            a.fold.arrive = arrive;
+            a.fold.choice_slot = plan.choice_slot;
+            a.fold.weights = c.weights;
+            a.fold.k = c.k;
+            a.fold.extra = c.extra_slot >= 0 ? 1 : 0;
+            a.fold.accumulate = c.accumulate;
+            a.fold.init = c.init;
+            a.fold.out = c.out;
+            a.fold.ldo = c.ldo;
+        }
         // a one-slot MLP (dense FFN, lone shared expert) has too few down
         // tiles to fill the chip: split its K range (M-independent choice)
-        if (slots == 1 && !c.shared) {
+        if (split_down) {
             constexpr int64_t step = FmtTraits<FMT>::kStepCols;
             const int64_t tiles64 = (c.H + 63) / 64;
             int64_t ks = tiles64 >= 256 ? 1 : (512 + tiles64 - 1) / tiles64;
@@ -1842,6 +1937,7 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
         timing_end(ctx, tok);
         UT_TRY(launch_check(ctx, "k_moe_down"));
     }
+    if (fold) return UT_OK;
     if (c.next) {
         if (!moe_combine_norm_ok(c.H) || ((uintptr_t)c.out & 15) != 0 || c.ldo % 4 != 0 ||
             (c.init && ((uintptr_t)c.init & 15) != 0) || !c.next->norm_w || !c.next->nd.exps) {
