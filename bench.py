@@ -935,9 +935,11 @@ def main():
     torch.cuda.empty_cache()
     if args.variants:
         tbl8 = build_experts(U, ctx, torch, C2["n_experts"], C2["hidden"], C2["inter"], U.INT8, 2)
-        r = expert_block_bench(U, ctx, torch, tbl8, C2, 1, args.steps, args.warmup, 8, 21)
-        variants["int8_M1"] = r
-        log(f"config 2 int8 M=1: {r['gbs']:.1f} GB/s")
+        # the int8 variant at the same shapes (kernels.rs:21-44)
+        for M in (1, 2, 4):
+            r = expert_block_bench(U, ctx, torch, tbl8, C2, M, args.steps, args.warmup, 8, 20 + M)
+            variants[f"int8_M{M}"] = r
+            log(f"config 2 int8 M={M}: {r['gbs']:.1f} GB/s")
         del tbl8
         torch.cuda.empty_cache()
 

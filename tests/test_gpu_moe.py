@@ -213,10 +213,34 @@ def test_moe_experts_f32_weights(ctx):
     assert np.abs(got - want).max() <= 1e-5 * max(1.0, np.abs(want).max())
 
 
-@pytest.mark.parametrize("fmt,Ms", [(INT4, (1, 2, 4)), (INT8, (1,))])
+@pytest.mark.parametrize("H,I", [(768, 512), (2560, 256), (512, 272)])
+def test_moe_int8_matrix_core_shapes(ctx, H, I):
+    """int8 experts at 2-4 rows take the matrix-core gate/up (H % 256 == 0)
+    and down (I % 256 == 0, I <= 2048); the shapes cover an odd segment
+    count (768: three 256-column segments), x staged in two chunks (2560 >
+    2048 columns), and a row tail with down on the dot-product kernel (272).
+    Rows equal one-row calls, which run the dot-product kernels, bit for bit."""
+    rng = np.random.default_rng(H + I)
+    E, k = 8, 3
+    tbl, host_w = make_experts(ctx, rng, INT8, E, H, I)
+    for M in (2, 3, 4):
+        ids = np.stack([rng.permutation(E)[:k] for _ in range(M)]).astype(np.int32)
+        w = rng.random((M, k)).astype(np.float32)
+        x = rng.standard_normal((M, H)).astype(np.float32)
+        got = host(tbl.moe_experts(dev(ids), dev(w), dev(x)))
+        want = oracle_moe(INT8, H, I, host_w, ids, w, x)
+        tol = 1e-4 * np.maximum(np.abs(want), 1.0)
+        assert (np.abs(got - want) <= tol).all(), (M, np.abs(got - want).max())
+        for s in range(M):
+            one = host(tbl.moe_experts(dev(ids[s:s + 1]), dev(w[s:s + 1]), dev(x[s:s + 1])))
+            assert np.array_equal(one[0], got[s]), (M, s)
+
+
+@pytest.mark.parametrize("fmt,Ms", [(INT4, (1, 2, 4)), (INT8, (1, 2, 3, 4))])
 def test_moe_experts_deepseek_shape(ctx, fmt, Ms):
     """hidden 7168, inter 2048, top-8 of 16 loaded experts
-    (M = 1 takes the streaming gate/up kernel)."""
+    (M = 1 takes the streaming gate/up kernel), int4 and the int8 variant at
+    the same shapes (undertow-quant/src/kernels.rs:21-44)."""
     rng = np.random.default_rng(1234)
     E, H, I, k = 16, 7168, 2048, 8
     tbl, host_w = make_experts(ctx, rng, fmt, E, H, I)

@@ -88,9 +88,18 @@ struct MoeCall {
     float *route_w = nullptr;
 };
 bool moe_combine_norm_ok(int64_t H);
-// Whether the matrix-core gate/up takes an expert pass of M rows (int4,
-// 2..4 rows, hidden a multiple of 512).
+// The fewest rows that take the int8 experts' matrix-core kernels (config
+// 2's int8 variant per step: two rows 4,760 -> 5,362 GB/s, four rows
+// 3,519 -> 5,321 GB/s against the dot-product kernels; one row stays on
+// those, 5,296 GB/s).
+#ifndef UT_MOE_I8_MFMA_MIN_M
+#define UT_MOE_I8_MFMA_MIN_M 2
+#endif
+// Whether the matrix-core gate/up takes an expert pass of M rows (int4:
+// 2..4 rows, hidden a multiple of 512; int8: UT_MOE_I8_MFMA_MIN_M..4 rows,
+// hidden a multiple of 256).
 inline bool gate_up_mfma_ok(int fmt, int M, int64_t H) {
+    if (fmt == UT_FMT_INT8) return M >= UT_MOE_I8_MFMA_MIN_M && M <= 4 && H % 256 == 0;
     return fmt == UT_FMT_INT4 && M >= 2 && M <= 4 && H % 512 == 0;
 }
 

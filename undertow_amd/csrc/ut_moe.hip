@@ -573,6 +573,7 @@ struct GateUpArgs {
     XSrc x;                   // digits (or f32) of x, shared by all slots
     const int32_t *exps;
     const float *mfma_xf = nullptr;  // k_moe_gate_up_mfma: x as f32 [M][H] (digitised by exps)
+    bool mfma8 = false;              // k_moe_gate_up_i8_mfma: int8 experts, x as digit planes
     float *h;                 // [slots][M][I]
     uint32_t *hmax_parts;     // [slots][M][ntiles] float bits
     int ntiles;
@@ -1087,6 +1088,87 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up_mfma(GateUpArgs a)
     gate_up_mfma_body<M, gate_up_mfma_tw<M, false>()>(a, blockIdx.y, blockIdx.x, lds, wg_max);
 }
 
+// Gate/up of int8 experts on the matrix cores (UT_MOE_I8_MFMA_MIN_M..4
+// rows, plan ready, x as the digitiser's three base-256 planes, H % 256 ==
+// 0): v_mfma_i32_16x16x64_i8 over the weights' own bytes (mfma_gemv_i8).
+// Each wave TW tiles of 8 h rows: load instructions 0-1 take the tile's
+// gate rows, 2-3 the same up rows, so the totals land as in the int4
+// kernel (lanes 0-31 gate, 32-63 up) and its epilogue applies unchanged.
+#ifndef UT_MOE_I8_MFMA_DEPTH
+#define UT_MOE_I8_MFMA_DEPTH 2
+#endif
+constexpr int kGateUpI8TW = 1;
+constexpr int kMoeI8KC = 2048;
+template <int M> constexpr int moe_i8_mfma_lds_bytes(int tw) {
+    return mfma_i8_lds_bytes<M, kMoeI8KC>() + 4 * tw * kMfmaI8WaveAreaBytes;
+}
+
+template <int M>
+__device__ __forceinline__ void gate_up_i8_mfma_body(const GateUpArgs &a, int u, int tile,
+                                                     uint8_t *lds, uint32_t *wg_max) {
+    constexpr int TW = kGateUpI8TW;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
+    const int cnt = *a.count;
+    const uint8_t *gw = (const uint8_t *)a.sp[u * 6 + kSpGate];
+    const uint8_t *uw = (const uint8_t *)a.sp[u * 6 + kSpUp];
+    const float *gsc = (const float *)a.sp[u * 6 + kSpGateS];
+    const float *usc = (const float *)a.sp[u * 6 + kSpUpS];
+    clear_arrivals(a, u, tile);
+    if (u >= cnt) return;
+    if (tid < 4) wg_max[tid] = 0;
+    const int64_t o0 = (int64_t)tile * (32 * TW) + wave * (8 * TW);
+    // instruction r takes tile row 4r + lane / 16: gate rows (r < 2) or up
+    const uint8_t *lrows[TW][4];
+#pragma unroll
+    for (int w = 0; w < TW; w++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int64_t o = o0 + 8 * w + 4 * (r & 1) + (lane >> 4), ao = o < a.I ? o : a.I - 1;
+            lrows[w][r] = (r < 2 ? gw : uw) + ao * a.row_bytes;
+        }
+    int32_t exl[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) exl[m] = a.exps[m];
+    CoreOut<UT_FMT_INT4, M, 4> res[TW];
+    mfma_gemv_i8<M, kMoeI8KC, TW, UT_MOE_I8_MFMA_DEPTH, false>(
+        lrows, 0, a.H, a.x.dig, a.x.KW, nullptr, 0, lds,
+        lds + mfma_i8_lds_bytes<M, kMoeI8KC>() + wave * TW * kMfmaI8WaveAreaBytes, res,
+        [](int32_t (&)[4]) {});
+    const int r = s >> 2, m = s & 3;
+    const int32_t e = m == 0 ? exl[0] : m == 1 ? exl[M > 1 ? 1 : 0]
+                    : m == 2 ? exl[M > 2 ? 2 : 0] : exl[M > 3 ? 3 : 0];
+#pragma unroll
+    for (int w = 0; w < TW; w++) {
+        const int64_t S = res[w].S[0][0];
+        const int lo = (int)(uint32_t)S, hi = (int)(uint32_t)((uint64_t)S >> 32);
+        const int ulo = __shfl(lo, lane + 32 < 64 ? lane + 32 : lane, 64);
+        const int uhi = __shfl(hi, lane + 32 < 64 ? lane + 32 : lane, 64);
+        const int64_t o = o0 + 8 * w + 4 * g + r;
+        if (g < 2 && m < M && o < a.I) {
+            const int64_t US = (int64_t)(((uint64_t)(uint32_t)uhi << 32) | (uint32_t)ulo);
+            const float gv = int_total_to_f32(S, e, ld_global_f32(gsc + o));
+            const float uv = int_total_to_f32(US, e, ld_global_f32(usc + o));
+            // silu(g) * u (undertow-quant/src/lib.rs:121; model.rs:241-247)
+            const float sg = gv / (1.0f + expf(-gv));
+            const float hv = __fmul_rn(sg, uv);
+            a.h[((int64_t)u * M + m) * a.I + o] = hv;
+            atomicMax(&wg_max[m], __float_as_uint(fabsf(hv)));
+        }
+    }
+    __syncthreads();
+    if (tid < 2 * TW * M) {
+        const int mm = tid / (2 * TW), part = 2 * TW * tile + tid % (2 * TW);
+        if (part < a.ntiles) a.hmax_parts[((int64_t)u * M + mm) * a.ntiles + part] = wg_max[mm];
+    }
+}
+
+template <int M>
+__global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up_i8_mfma(GateUpArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[moe_i8_mfma_lds_bytes<M>(kGateUpI8TW)];
+    __shared__ uint32_t wg_max[4];
+    gate_up_i8_mfma_body<M>(a, blockIdx.y, blockIdx.x, lds, wg_max);
+}
+
 // The routed experts on the matrix cores (slots 0..gridDim.y-2, 32-row
 // tiles) and a shared MLP of format FB (the last grid row, the plain
 // kernel's 16-row tiles) in one launch, so the shared MLP's few workgroups
@@ -1358,6 +1440,61 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_down_mfma(DownArgs a) {
     down_mfma_body<M>(a, blockIdx.y, blockIdx.x, lds, red);
     if (a.fold.arrive) fold_combine<M>(a, blockIdx.x, (int64_t)blockIdx.x * 64 * down_mfma_tw<M>(),
                                        64 * down_mfma_tw<M>());
+}
+
+// Down of int8 experts on the matrix cores (UT_MOE_I8_MFMA_MIN_M..4 rows,
+// I <= 2048 staged whole, I % 256 == 0, no split): h as f32 digitised while
+// staged by the gate/up workgroups' partial maxima, each wave one 16-row
+// tile, the workgroup 64 rows; the same totals and epilogue as down_body.
+inline bool down_i8_mfma_ok(int fmt, int M, int64_t I, int ks) {
+    return fmt == UT_FMT_INT8 && M >= UT_MOE_I8_MFMA_MIN_M && M <= 4 && ks == 1 &&
+           I <= kMoeI8KC && I % kMfmaI8SegCols == 0;
+}
+
+template <int M>
+__global__ __launch_bounds__(kGemvThreads) void k_moe_down_i8_mfma(DownArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[moe_i8_mfma_lds_bytes<M>(1)];
+    __shared__ uint32_t red[4 * M];
+    const int u = blockIdx.y, tile = blockIdx.x;
+    if (u < *a.count) {
+        const uint8_t *dw = (const uint8_t *)a.sp[u * 6 + kSpDown];
+        const float *dsc = (const float *)a.sp[u * 6 + kSpDownS];
+        const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
+        const int64_t wrow0 = (int64_t)tile * 64 + wave * 16;
+        // instruction r takes tile row 4r + lane / 16
+        const uint8_t *lrows[1][4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int64_t o = wrow0 + 4 * r + (lane >> 4);
+            lrows[0][r] = dw + (o < a.H ? o : a.H - 1) * a.row_bytes;
+        }
+        ut_u32x4 pv[M];
+        rowmax_load<M>(a.hmax_parts + (int64_t)u * M * a.nparts, a.nparts, pv);
+        int32_t exl[M];
+        auto prep = [&](int32_t (&shl)[4]) {
+            int32_t sh[M];
+            rowmax_reduce<M>(pv, sh, red);
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                shl[m] = sh[m];
+                exl[m] = sh[m] == INT32_MIN ? INT32_MIN : -sh[m];
+            }
+        };
+        CoreOut<UT_FMT_INT4, M, 4> res[1];
+        mfma_gemv_i8<M, kMoeI8KC, 1, UT_MOE_I8_MFMA_DEPTH, true>(
+            lrows, 0, a.I, nullptr, 0, a.x.xf + u * a.x_slot_stride, a.x.ldx, lds,
+            lds + mfma_i8_lds_bytes<M, kMoeI8KC>() + wave * kMfmaI8WaveAreaBytes, res, prep);
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                const int64_t o = wrow0 + 4 * g + r;
+                if (s == 4 * r + m && o < a.H)
+                    a.d[((int64_t)u * M + m) * a.H + o] =
+                        int_total_to_f32(res[0].S[r][m], exl[m], ld_global_f32(dsc + o));
+            }
+    }
+    if (a.fold.arrive) fold_combine<M>(a, blockIdx.x, (int64_t)blockIdx.x * 64, 64);
 }
 
 // The routed experts' down on the matrix cores and a shared MLP's down
@@ -1657,6 +1794,15 @@ static void launch_gate_up(ut_ctx *ctx, const GateUpArgs &a, int64_t slots, cons
             return;
         }
     }
+    if constexpr (FA == UT_FMT_INT8 && M >= 2 && M <= 4) {
+        if (a.mfma8 && !b) {
+            constexpr int R = 32 * kGateUpI8TW;
+            const unsigned gx = (unsigned)((a.I + R - 1) / R);
+            hipLaunchKernelGGL((k_moe_gate_up_i8_mfma<M>), dim3(gx, (unsigned)slots),
+                               dim3(kGemvThreads), 0, ctx->stream, a);
+            return;
+        }
+    }
     if (!b) {
         hipLaunchKernelGGL((k_moe_gate_up<FA, M>), dim3((unsigned)a.ntiles, (unsigned)slots),
                            dim3(kGemvThreads), 0, ctx->stream, a);
@@ -1694,6 +1840,14 @@ static void launch_down(ut_ctx *ctx, const DownArgs &a, int64_t slots, const Dow
             else
                 hipLaunchKernelGGL((k_moe_down_mfma_dual<M, UT_FMT_INT8>), dim3(n), dim3(kGemvThreads), 0,
                                    ctx->stream, a, *b, gxm, nrouted);
+            return;
+        }
+    }
+    if constexpr (FA == UT_FMT_INT8 && M >= 2 && M <= 4) {
+        if (!b && down_i8_mfma_ok(FA, M, a.I, a.ks)) {
+            hipLaunchKernelGGL((k_moe_down_i8_mfma<M>),
+                               dim3((unsigned)((a.H + 63) / 64), (unsigned)slots),
+                               dim3(kGemvThreads), 0, ctx->stream, a);
             return;
         }
     }
@@ -1819,7 +1973,10 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
         a.exps = xexps;
         // x digitised in this pass from c.x (so c.x is what the digits
         // hold): the matrix-core kernel stages c.x itself
-        if (use_mfma && xs.dig && xexps) a.mfma_xf = xin;
+        if (use_mfma && xs.dig && xexps) {
+            if (FMT == UT_FMT_INT4) a.mfma_xf = xin;
+            else a.mfma8 = true;
+        }
         a.h = h;
         a.hmax_parts = hmax;
         a.ntiles = (int)L.ntiles;
