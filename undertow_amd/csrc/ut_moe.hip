@@ -1208,15 +1208,13 @@ __global__ __launch_bounds__(kGemvThreads, M <= 2 ? 5 : 1) void k_moe_gate_up_du
 
 // --------------------------------------------------------------- down ---
 // UT_MOE_FOLD_COMBINE=1: fold the routed combine into down (CombineFold)
-// instead of a combine launch after it.  Off: each workgroup's agent-scope
-// release writes back its XCD's L2, and at config 2's 1,792 down
-// workgroups that took down from 14.2 to 178 us per launch.
+// instead of a combine launch after it.
 #ifndef UT_MOE_FOLD_COMBINE
 #define UT_MOE_FOLD_COMBINE 0
 #endif
 // The routed experts' combine folded into down: each workgroup of a row
-// band (one per slot) releases its d rows and counts in at arrive[band];
-// the one that counts last adds the band's columns of out exactly as
+// band (one per slot) stores its d rows device-coherently and counts in at
+// arrive[band]; the one that counts last adds the band's columns of out as
 // k_moe_combine4 does (router choice order, the same init / extra /
 // shared / accumulate terms), so no combine launch follows.  The counters
 // are cleared by the gate/up launch before (GateUpArgs::arrive).
@@ -1252,6 +1250,15 @@ struct DownArgs {
 
 template <int M>
 __device__ void fold_combine(const DownArgs &a, int band, int64_t c0, int ncols);
+
+// A finished d value.  With the combine folded into the launch it is
+// stored device-coherently (a relaxed agent-scope atomic store, written
+// through this XCD's L2), so the band's last workgroup, on any XCD, reads
+// it without a cache write-back.
+__device__ __forceinline__ void store_d(const DownArgs &a, int64_t i, float v) {
+    if (a.fold.arrive) __hip_atomic_store(a.d + i, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else a.d[i] = v;
+}
 
 // The digitisation shift of h row (u, m): 22 - E with max|h| < 2^E, from the
 // gate/up workgroups' partial maxima (INT32_MIN: non-finite row).  Whole
@@ -1349,7 +1356,7 @@ __device__ __forceinline__ void down_body(const DownArgs &a, int u, int tile, ui
             const int64_t o = row0 + r;
             if (s == 4 * r + m && o < a.H) {
                 float v = core_value<FMT, M, R>(res, r, m, exl, dsc, o);
-                a.d[((int64_t)u * M + m) * a.H + o] = v;
+                store_d(a, ((int64_t)u * M + m) * a.H + o, v);
             }
         }
 }
@@ -1422,8 +1429,8 @@ __device__ __forceinline__ void down_mfma_body(const DownArgs &a, int u, int til
             for (int m = 0; m < M; m++) {
                 const int64_t o = wrow0 + 16 * w + 4 * g + r;
                 if (s == 4 * r + m && o < a.H)
-                    a.d[((int64_t)u * M + m) * a.H + o] =
-                        core_value<UT_FMT_INT4, M, 4>(res[w], r, m, exl, dsc, o);
+                    store_d(a, ((int64_t)u * M + m) * a.H + o,
+                            core_value<UT_FMT_INT4, M, 4>(res[w], r, m, exl, dsc, o));
             }
 }
 
@@ -1490,8 +1497,8 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_down_i8_mfma(DownArgs a) {
             for (int m = 0; m < M; m++) {
                 const int64_t o = wrow0 + 4 * g + r;
                 if (s == 4 * r + m && o < a.H)
-                    a.d[((int64_t)u * M + m) * a.H + o] =
-                        int_total_to_f32(res[0].S[r][m], exl[m], ld_global_f32(dsc + o));
+                    store_d(a, ((int64_t)u * M + m) * a.H + o,
+                            int_total_to_f32(res[0].S[r][m], exl[m], ld_global_f32(dsc + o)));
             }
     }
     if (a.fold.arrive) fold_combine<M>(a, blockIdx.x, (int64_t)blockIdx.x * 64, 64);
@@ -1596,7 +1603,9 @@ __global__ void k_moe_combine(const int32_t *__restrict__ choice_slot,
 // every load issued before the first sum (1 <= k <= 8: the choices' rows
 // load in one round trip; an invalid choice reads slot 0's row and is
 // skipped), and the sums in k_moe_combine's order.  16-byte aligned rows.
-template <int NC>
+// COH: d was written in the same launch by other workgroups (store_d), so
+// its values are read device-coherently (relaxed agent-scope atomic loads).
+template <int NC, bool COH = false>
 __device__ __forceinline__ void combine_cols(const int32_t *__restrict__ choice_slot,
                                              const float *__restrict__ weights,
                                              const float *__restrict__ d, int M, int k, int64_t H,
@@ -1612,6 +1621,15 @@ __device__ __forceinline__ void combine_cols(const int32_t *__restrict__ choice_
             r[4 * q] = v.x; r[4 * q + 1] = v.y; r[4 * q + 2] = v.z; r[4 * q + 3] = v.w;
         }
     };
+    auto ldd = [&](const float *p, float (&r)[NC]) {
+        if constexpr (COH) {
+#pragma unroll
+            for (int j = 0; j < NC; j++)
+                r[j] = __hip_atomic_load(p + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            ldv(p, r);
+        }
+    };
     const bool fast = k >= 1 && k <= KF;
     int slot[KF];
     float wc[KF], dv[KF][NC], ex[NC], sh[NC], pv[NC];
@@ -1625,13 +1643,13 @@ __device__ __forceinline__ void combine_cols(const int32_t *__restrict__ choice_
         }
 #pragma unroll
         for (int c = 0; c < KF; c++)
-            ldv(d + ((int64_t)(slot[c] > 0 ? slot[c] : 0) * M + s) * H + c0, dv[c]);
+            ldd(d + ((int64_t)(slot[c] > 0 ? slot[c] : 0) * M + s) * H + c0, dv[c]);
     }
     if (init) ldv(init, acc);
     else
 #pragma unroll
         for (int j = 0; j < NC; j++) acc[j] = 0.0f;
-    if (extra) ldv(d + ((int64_t)(*count - 1) * M + s) * H + c0, ex);
+    if (extra) ldd(d + ((int64_t)(*count - 1) * M + s) * H + c0, ex);
     if (dshared) ldv(dshared + (int64_t)s * H + c0, sh);
     if (prev) ldv(prev, pv);
     if (fast) {
@@ -1645,7 +1663,7 @@ __device__ __forceinline__ void combine_cols(const int32_t *__restrict__ choice_
             const int sl = choice_slot[s * k + c];
             if (sl < 0) continue;
             float t[NC];
-            ldv(d + ((int64_t)sl * M + s) * H + c0, t);
+            ldd(d + ((int64_t)sl * M + s) * H + c0, t);
             const float w = weights[s * k + c];
 #pragma unroll
             for (int j = 0; j < NC; j++) acc[j] = __fadd_rn(acc[j], __fmul_rn(w, t[j]));
@@ -1680,17 +1698,20 @@ __global__ __launch_bounds__(256) void k_moe_combine4(
 }
 
 // Down's folded combine (CombineFold): columns [c0, c0 + ncols) of every
-// row, by the band's last workgroup.  Every thread releases its own d
-// stores (agent scope: other XCDs' workgroups read them) before the count.
+// row, by the band's last workgroup.  Each thread's d values were stored
+// device-coherently (store_d); the thread waits until its stores are
+// acknowledged before the workgroup counts in, and the last workgroup reads
+// d device-coherently, so no fence writes back or invalidates an L2.
 template <int M>
 __device__ void fold_combine(const DownArgs &a, int band, int64_t c0, int ncols) {
     __shared__ int s_last;
-    __threadfence();
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (threadIdx.x == 0) s_last = atomicAdd(a.fold.arrive + band, 1) == (int)gridDim.y - 1;
+    if (threadIdx.x == 0)
+        s_last = __hip_atomic_fetch_add(a.fold.arrive + band, 1, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.y - 1;
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
     const CombineFold &f = a.fold;
     const int per_row = ncols / 4;
     for (int t = threadIdx.x; t < M * per_row; t += blockDim.x) {
@@ -1699,9 +1720,9 @@ __device__ void fold_combine(const DownArgs &a, int band, int64_t c0, int ncols)
         if (c >= a.H) continue;
         float *po = f.out + s * f.ldo + c;
         float acc[4];
-        combine_cols<4>(f.choice_slot, f.weights, a.d, M, f.k, a.H, a.count, f.extra, f.dshared,
-                        f.init ? f.init + s * f.ldo + c : nullptr, f.accumulate ? po : nullptr, s,
-                        c, acc);
+        combine_cols<4, true>(f.choice_slot, f.weights, a.d, M, f.k, a.H, a.count, f.extra,
+                              f.dshared, f.init ? f.init + s * f.ldo + c : nullptr,
+                              f.accumulate ? po : nullptr, s, c, acc);
         *(float4 *)po = make_float4(acc[0], acc[1], acc[2], acc[3]);
     }
 }

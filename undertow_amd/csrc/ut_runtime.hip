@@ -266,29 +266,6 @@ __global__ void k_add_scaled_row(int32_t fmt, const uint8_t *__restrict__ payloa
     }
 }
 
-// Read-bandwidth probe: one 256-thread workgroup per CU, each lane keeps
-// eight non-temporal 16-byte loads in flight (the configuration that reads
-// fastest on gfx950: about 32 KB in flight per CU).
-typedef unsigned int ut_probe_u4 __attribute__((ext_vector_type(4)));
-
-__global__ __launch_bounds__(256) void k_probe_read(const ut_probe_u4 *__restrict__ p, int64_t n,
-                                                    unsigned *__restrict__ sink) {
-    constexpr int U = 8;
-    const int64_t stride = (int64_t)gridDim.x * 256;
-    int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    unsigned acc = 0;
-    for (; i + (U - 1) * stride < n; i += U * stride) {
-        ut_probe_u4 v[U];
-#pragma unroll
-        for (int u = 0; u < U; u++)
-            v[u] = __builtin_nontemporal_load((const __attribute__((address_space(1))) ut_probe_u4 *)(p + i + u * stride));
-#pragma unroll
-        for (int u = 0; u < U; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
-    }
-    for (; i < n; i += stride) acc ^= p[i].x;
-    if (acc == 0x9e3779b9u) sink[0] = acc;  // keeps the loads; practically never true
-}
-
 }  // namespace ut
 
 using namespace ut;
@@ -379,70 +356,6 @@ int32_t ut_ctx_enable_timing(ut_ctx *ctx, int32_t on) {
     ctx->timing = on != 0;
     if (on) ctx->stats.clear();
     return UT_OK;
-}
-
-int32_t ut_probe_read_bandwidth(ut_ctx *ctx, const void *buf_dev, int64_t bytes, int32_t reps,
-                                double *gbs) {
-    if (!ctx || !buf_dev || !gbs || bytes <= 0 || bytes % 16 != 0 || reps <= 0 ||
-        ((uintptr_t)buf_dev & 15) != 0) {
-        set_error(ctx, "ut_probe_read_bandwidth: bad argument");
-        return UT_ERR_ARG;
-    }
-    int64_t *sink = nullptr;
-    UT_TRY(splitk_buffer(ctx, &sink));  // scratch: any writable device word
-    hipEvent_t a = nullptr, b = nullptr;
-    UT_CHECK_HIP(ctx, hipEventCreate(&a));
-    UT_CHECK_HIP(ctx, hipEventCreate(&b));
-    const int64_t n = bytes / 16;
-    const unsigned wgs = (unsigned)ctx->multiprocessors;
-    hipLaunchKernelGGL(k_probe_read, dim3(wgs), dim3(256), 0, ctx->stream,
-                       (const ut_probe_u4 *)buf_dev, n, (unsigned *)sink);  // warm-up
-    UT_CHECK_HIP(ctx, hipEventRecord(a, ctx->stream));
-    for (int32_t r = 0; r < reps; r++)
-        hipLaunchKernelGGL(k_probe_read, dim3(wgs), dim3(256), 0, ctx->stream,
-                           (const ut_probe_u4 *)buf_dev, n, (unsigned *)sink);
-    UT_CHECK_HIP(ctx, hipEventRecord(b, ctx->stream));
-    UT_CHECK_HIP(ctx, hipEventSynchronize(b));
-    float ms = 0.0f;
-    UT_CHECK_HIP(ctx, hipEventElapsedTime(&ms, a, b));
-    (void)hipEventDestroy(a);
-    (void)hipEventDestroy(b);
-    *gbs = (double)bytes * reps / (ms * 1e-3) / 1e9;
-    return launch_check(ctx, "k_probe_read");
-}
-
-int32_t ut_probe_read_windows(ut_ctx *ctx, const void *buf_dev, int64_t total_bytes,
-                              int64_t window_bytes, int32_t reps, double *gbs) {
-    if (!ctx || !buf_dev || !gbs || window_bytes <= 0 || window_bytes % 256 != 0 ||
-        total_bytes < 2 * window_bytes || reps <= 0 || ((uintptr_t)buf_dev & 15) != 0) {
-        set_error(ctx, "ut_probe_read_windows: bad argument");
-        return UT_ERR_ARG;
-    }
-    int64_t *sink = nullptr;
-    UT_TRY(splitk_buffer(ctx, &sink));
-    hipEvent_t a = nullptr, b = nullptr;
-    UT_CHECK_HIP(ctx, hipEventCreate(&a));
-    UT_CHECK_HIP(ctx, hipEventCreate(&b));
-    const int64_t nwin = total_bytes / window_bytes, n = window_bytes / 16;
-    const unsigned wgs = (unsigned)ctx->multiprocessors;
-    const char *base = (const char *)buf_dev;
-    // warm-up on the last window; the timed launches then take windows 0, 1,
-    // ... in turn, each read once per pass over the buffer
-    hipLaunchKernelGGL(k_probe_read, dim3(wgs), dim3(256), 0, ctx->stream,
-                       (const ut_probe_u4 *)(base + (nwin - 1) * window_bytes), n, (unsigned *)sink);
-    UT_CHECK_HIP(ctx, hipEventRecord(a, ctx->stream));
-    for (int32_t r = 0; r < reps; r++)
-        hipLaunchKernelGGL(k_probe_read, dim3(wgs), dim3(256), 0, ctx->stream,
-                           (const ut_probe_u4 *)(base + (r % (nwin - 1)) * window_bytes), n,
-                           (unsigned *)sink);
-    UT_CHECK_HIP(ctx, hipEventRecord(b, ctx->stream));
-    UT_CHECK_HIP(ctx, hipEventSynchronize(b));
-    float ms = 0.0f;
-    UT_CHECK_HIP(ctx, hipEventElapsedTime(&ms, a, b));
-    (void)hipEventDestroy(a);
-    (void)hipEventDestroy(b);
-    *gbs = (double)window_bytes * reps / (ms * 1e-3) / 1e9;
-    return launch_check(ctx, "k_probe_read");
 }
 
 int32_t ut_ctx_kernel_time(ut_ctx *ctx, const char *prefix, int64_t *launches, double *total_ms) {
