@@ -530,6 +530,14 @@ int dig_flags(std::initializer_list<const ut_qtensor *> ws) {
     return f;
 }
 
+// Whether any of the weights reads its activation as f32 (f32 weights:
+// the integer formats read digits only).
+bool f32_reader(std::initializer_list<const ut_qtensor *> ws) {
+    for (const ut_qtensor *w : ws)
+        if (w && w->fmt == UT_FMT_F32) return true;
+    return false;
+}
+
 int dig_flags_fmt(int fmt, int64_t K) {
     if (fmt == UT_FMT_F32) return 0;
     return xdigit_flags_for(fmt, K);
@@ -833,7 +841,8 @@ int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
         const int qf = dig_flags({L.q_b});
         const XDigits qd = xdigits_view(w.digB, rows, c.q_lora_rank, qf);
         UT_TRY(launch_mla_pre(ctx, pp, Lr + rope, xd.exps, L.kv_a->scales, L.q_a->scales, rows,
-                              c.q_lora_rank, L.q_a_norm, c.rms_norm_eps, w.qa_n, qd, qf, Lr, rope,
+                              c.q_lora_rank, L.q_a_norm, c.rms_norm_eps,
+                              f32_reader({L.q_b}) ? w.qa_n : nullptr, qd, qf, Lr, rope,
                               L.kv_a_norm, kv.latent, kv.krot, kv.kc, pos_base, m->rope_table));
         UT_TRY(matmul_digits(ctx, L.q_b, w.qa_n, qd, rows, w.q, heads * qh, 0));
     } else {
@@ -896,14 +905,16 @@ bool fuse_next_ok(const ut_session *s, int64_t rows) {
     return rows <= 4 && moe_combine_norm_ok(s->m->c.hidden_size) && !fast8(s);
 }
 
-// The fused norm's arguments: rmsnorm with norm_w into ws.normed and the
-// digit forms `flags` into ws.digA; *xd gets the view the consumers read.
-NormNext next_norm(ut_session *s, const float *norm_w, int flags, int64_t rows, XDigits *xd) {
+// The fused norm's arguments: rmsnorm with norm_w into ws.normed (only when
+// a consumer reads the normed rows as f32: f32) and the digit forms `flags`
+// into ws.digA; *xd gets the view the consumers read.
+NormNext next_norm(ut_session *s, const float *norm_w, int flags, int64_t rows, XDigits *xd,
+                   bool f32 = true) {
     const int64_t H = s->m->c.hidden_size;
     NormNext nx;
     nx.norm_w = norm_w;
     nx.eps = s->m->c.rms_norm_eps;
-    nx.normed = s->ws.normed;
+    nx.normed = f32 ? s->ws.normed : nullptr;
     nx.ldn = H;
     nx.flags = flags;
     nx.nd = *xd = xdigits_view(s->ws.digA, rows, H, flags);
@@ -911,6 +922,7 @@ NormNext next_norm(ut_session *s, const float *norm_w, int flags, int64_t rows, 
 }
 
 int input_flags(const LayerW &L) { return dig_flags({L.q_a, L.q_proj, L.kv_a}); }
+bool input_f32(const LayerW &L) { return f32_reader({L.q_a, L.q_proj, L.kv_a}); }
 
 // run_layer (model.rs:127-183) / the per-layer body of prefill (:470-526).
 // pre: the input norm already ran (its rows in ws.normed, digits *pre).
@@ -1017,8 +1029,10 @@ int32_t prefill_dev(ut_session *s, const int32_t *ids, int64_t n, const int32_t 
         NormNext nx;
         if (fuse)
             nx = li + 1 < nl ? next_norm(s, m->layers[li + 1].input_norm,
-                                         input_flags(m->layers[li + 1]), n, &nxt)
-                             : next_norm(s, m->final_norm, dig_flags({m->lm_head}), n, &nxt);
+                                         input_flags(m->layers[li + 1]), n, &nxt,
+                                         input_f32(m->layers[li + 1]))
+                             : next_norm(s, m->final_norm, dig_flags({m->lm_head}), n, &nxt,
+                                         f32_reader({m->lm_head}));
         UT_TRY(run_layer(s, m->layers[li], w.x, n, s->kv[li], fuse && li > 0 ? &cur : nullptr,
                          fuse ? &nx : nullptr));
         cur = nxt;
@@ -1137,7 +1151,8 @@ int32_t draft_rows_dev(ut_session *s, const int32_t *host_ids, int in_slot,
     if (fuse_next_ok(s, rows)) {
         // the layer's last combine normalises every row; the head reads the last
         XDigits all;
-        const NormNext nx = next_norm(s, m->mtp_norm, dig_flags({m->mtp_head}), rows, &all);
+        const NormNext nx = next_norm(s, m->mtp_norm, dig_flags({m->mtp_head}), rows, &all,
+                                      f32_reader({m->mtp_head}));
         UT_TRY(run_layer(s, m->mtp_layer, w.x, rows, s->mtp_kv, nullptr, &nx));
         hd_ = xdigits_rows(all, rows - 1);
         hn = w.normed + (rows - 1) * H;

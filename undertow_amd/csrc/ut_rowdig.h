@@ -111,11 +111,18 @@ __device__ __forceinline__ void rowdig_body(const RowDigArgs &a, int64_t m, floa
         }
     }
     if (a.out) {
+        // whole 8-column groups of a 16-byte aligned row: two 16-byte stores
+        const bool ovec = ((uintptr_t)(a.out + m * a.ldo) & 15) == 0;
 #pragma unroll
         for (int g = 0; g < GPT; g++) {
             const int64_t c = tid + (int64_t)g * nt;
             if (c >= NG) continue;
             float *o = a.out + m * a.ldo + 8 * c;
+            if (ovec && 8 * c + 8 <= K) {
+                *(float4 *)o = make_float4(v[g][0], v[g][1], v[g][2], v[g][3]);
+                *(float4 *)(o + 4) = make_float4(v[g][4], v[g][5], v[g][6], v[g][7]);
+                continue;
+            }
 #pragma unroll
             for (int j = 0; j < 8; j++)
                 if (8 * c + j < K) o[j] = v[g][j];
@@ -141,12 +148,21 @@ __device__ __forceinline__ void rowdig_body(const RowDigArgs &a, int64_t m, floa
         if (a.dig8) {
             uint32_t w[3];
             digit_words<UT_FMT_INT8>(v[g], 4, sh, w);
+            if (2 * c + 1 < K4 && (K4 & 1) == 0 && ((uintptr_t)a.dig8 & 7) == 0) {
+                // both words of the group in one 8-byte store per plane
+                uint32_t w2[3];
+                digit_words<UT_FMT_INT8>(v[g] + 4, 4, sh, w2);
 #pragma unroll
-            for (int p = 0; p < 3; p++) a.dig8[(m * 3 + p) * K4 + 2 * c] = w[p];
-            if (2 * c + 1 < K4) {
-                digit_words<UT_FMT_INT8>(v[g] + 4, 4, sh, w);
+                for (int p = 0; p < 3; p++)
+                    *(uint2 *)(a.dig8 + (m * 3 + p) * K4 + 2 * c) = make_uint2(w[p], w2[p]);
+            } else {
 #pragma unroll
-                for (int p = 0; p < 3; p++) a.dig8[(m * 3 + p) * K4 + 2 * c + 1] = w[p];
+                for (int p = 0; p < 3; p++) a.dig8[(m * 3 + p) * K4 + 2 * c] = w[p];
+                if (2 * c + 1 < K4) {
+                    digit_words<UT_FMT_INT8>(v[g] + 4, 4, sh, w);
+#pragma unroll
+                    for (int p = 0; p < 3; p++) a.dig8[(m * 3 + p) * K4 + 2 * c + 1] = w[p];
+                }
             }
         }
         if (a.xt) {
