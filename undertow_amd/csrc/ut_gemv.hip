@@ -4,11 +4,13 @@
 // (int4 / int8 / f32 weights, 1..4 activation rows per pass) and a generic
 // kernel for shapes the fast one does not take.
 #include <atomic>
+#include "ut_argmax.h"
 #include "ut_gemv_core.h"
 #include "ut_gemv_mfma.h"
 #include "ut_moe.h"
 #include "ut_ops.h"
 #include "ut_rowdig.h"
+#include "ut_sample.h"
 
 
 namespace ut {
@@ -422,6 +424,9 @@ struct PlainArgs {
     // maxima xmax [M][nxmax]; workgroup 0 records the exponents in exps
     const uint32_t *xmax;
     int nxmax;
+    // optional: the launch that finishes the rows leaves argmax partials
+    // (k_gemv / k_gemv_mfma_i8 unsplit: one per workgroup; split: the sum's)
+    ArgmaxParts am;
 };
 
 __device__ __forceinline__ const uint8_t *plain_row(const PlainArgs &a, int64_t row) {
@@ -502,6 +507,9 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
         return;
     }
     gemv_core<FMT, M, R, plain_depth<M>()>(rows, a.K, xs, lds, res, 0, -1, prep);
+    Best bm[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) bm[m] = Best{0.0f, -1};
 #pragma unroll
     for (int r = 0; r < R; r++)
 #pragma unroll
@@ -512,9 +520,12 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
                                     ? res.F[r][m]
                                     : int_total_to_f32(res.S[r][m], exl[m], plain_scale(a, row));
                 float *o = plain_out(a, m, row);
-                *o = a.accumulate ? __fadd_rn(*o, v) : v;
+                const float nv = a.accumulate ? __fadd_rn(*o, v) : v;
+                *o = nv;
+                argmax_offer(bm[m], nv, row);
             }
         }
+    if (a.am.v) argmax_parts_store<M>(a.am, bm, blockIdx.x);
 }
 
 // int8 weights at 3..4 activation rows on the matrix cores
@@ -587,6 +598,9 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_mfma_i8(PlainArgs a) {
     mfma_gemv_i8<M, KC, TW, gemv_i8_mfma_depth<M>(), F32X>(
         lrows, kb, ke, a.x.dig, a.x.KW, a.x.xf, a.x.ldx, lds,
         wareas + wave * TW * kMfmaI8WaveAreaBytes, res, prep);
+    Best bm[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) bm[m] = Best{0.0f, -1};
 #pragma unroll
     for (int w = 0; w < TW; w++)
 #pragma unroll
@@ -600,9 +614,12 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_mfma_i8(PlainArgs a) {
                 } else {
                     const float v = int_total_to_f32(res[w].S[r][m], exl[m], plain_scale(a, row));
                     float *o = plain_out(a, m, row);
-                    *o = a.accumulate ? __fadd_rn(*o, v) : v;
+                    const float nv = a.accumulate ? __fadd_rn(*o, v) : v;
+                    *o = nv;
+                    argmax_offer(bm[m], nv, row);
                 }
             }
+    if (a.ks == 1 && a.am.v) argmax_parts_store<M>(a.am, bm, blockIdx.x);
 }
 
 // The value of (m, row) from split-K partials [ks][M][O]: summed in z order
@@ -635,6 +652,28 @@ __global__ __launch_bounds__(256) void k_gemv_splitk_sum(PlainArgs a, int M) {
                                       FMT == UT_FMT_F32 ? 0.0f : plain_scale(a, row));
     float *o = plain_out(a, m, row);
     *o = a.accumulate ? __fadd_rn(*o, v) : v;
+}
+
+// k_gemv_splitk_sum with argmax partials: grid (ceil(O / 256), M), so each
+// workgroup finishes 256 output rows of one activation row and leaves their
+// best candidate at a.am[m][blockIdx.x].
+template <int FMT>
+__global__ __launch_bounds__(256) void k_gemv_splitk_sum_am(PlainArgs a, int M) {
+    const int64_t m = blockIdx.y, row = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    Best bm[1] = {Best{0.0f, -1}};
+    if (row < a.O) {
+        const float v = splitk_value<FMT>(a.part, a.ks, a.O, M, m, row,
+                                          FMT == UT_FMT_F32 ? 0 : a.exps[m],
+                                          FMT == UT_FMT_F32 ? 0.0f : plain_scale(a, row));
+        float *o = plain_out(a, m, row);
+        const float nv = a.accumulate ? __fadd_rn(*o, v) : v;
+        *o = nv;
+        argmax_offer(bm[0], nv, row);
+    }
+    ArgmaxParts p = a.am;
+    p.v += m * p.stride;
+    p.i += m * p.stride;
+    argmax_parts_store<1>(p, bm, blockIdx.x);
 }
 
 // The split-K sum for one row per workgroup (thread t: rows 8t..8t+7 of the
@@ -851,12 +890,30 @@ static int32_t splitk_finish(ut_ctx *ctx, const GemvArgs &ga, const PlainArgs &a
         hipLaunchKernelGGL(k_splitk_sum_norm<FMT>, dim3((unsigned)mrows), dim3(threads), 0,
                            ctx->stream, a, mrows, nd);
         if (ga.next_done) *ga.next_done = true;
+    } else if (a.am.v) {
+        // argmax partials per 256 finished rows (a.am's stride was set so)
+        hipLaunchKernelGGL(k_gemv_splitk_sum_am<FMT>, dim3((unsigned)((a.O + 255) / 256), (unsigned)mrows),
+                           dim3(256), 0, ctx->stream, a, mrows);
     } else {
         const int64_t n = a.O * mrows;
         hipLaunchKernelGGL(k_gemv_splitk_sum<FMT>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
                            ctx->stream, a, mrows);
     }
     return UT_OK;
+}
+
+// The argmax partials' view for a launch of gx workgroups of rows_per_wg
+// output rows (ks > 1: the split sum's 256-row workgroups), when the caller
+// asked for them (ga.am_scratch) and the launch finishes every row of the
+// call: one chunk of rows, one weight, no deferred or fused consumer.
+static void argmax_plan(const GemvArgs &ga, PlainArgs &a, int64_t m0, int mrows, int64_t gx) {
+    a.am = ArgmaxParts{};
+    if (!ga.am_scratch || !ga.am_out || ga.w2 || ga.defer || ga.next || m0 != 0 || mrows != ga.M)
+        return;
+    const int64_t stride = a.ks > 1 ? (a.O + 255) / 256 : gx;
+    if (stride > argmax_gemv_parts_max(a.O)) return;
+    a.am = argmax_parts_view(ga.am_scratch, mrows, stride);
+    *ga.am_out = a.am;
 }
 
 // Workgroups of k_gemv_mfma_i8<M, F32X> resident on the chip.
@@ -899,6 +956,7 @@ static int32_t launch_i8_mfma_m(ut_ctx *ctx, const GemvArgs &ga, PlainArgs a, in
     a.part = nullptr;
     if (a.ks > 1) UT_TRY(splitk_buffer(ctx, &a.part));
     const dim3 grid((unsigned)((a.O + rows_per_wg - 1) / rows_per_wg), 1, (unsigned)a.ks);
+    argmax_plan(ga, a, m0, M, grid.x);
     const char *name = "gemv_int8_mfma";
     int tok = timing_begin(ctx, name);
     hipLaunchKernelGGL((k_gemv_mfma_i8<M, F32X>), grid, dim3(kGemvThreads), 0, ctx->stream, a);
@@ -1000,6 +1058,7 @@ static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrow
     a.part = nullptr;
     if (a.ks > 1) UT_TRY(splitk_buffer(ctx, &a.part));
     dim3 grid((unsigned)((a.O + rows_per_wg - 1) / rows_per_wg), 1, (unsigned)a.ks);
+    argmax_plan(ga, a, m0, mrows, grid.x);
     const char *name = FMT == UT_FMT_INT4 ? "gemv_int4" : FMT == UT_FMT_INT8 ? "gemv_int8" : "gemv_f32";
     int tok = timing_begin(ctx, name);
     switch (mrows) {
@@ -1091,6 +1150,7 @@ int32_t launch_rowdot_f32(ut_ctx *ctx, const ut_qtensor *w, const float *x, int6
 int32_t gemv(ut_ctx *ctx, const GemvArgs &ga) {
     const ut_qtensor *w = ga.w;
     if (ga.defer) ga.defer->ks = 1;
+    if (ga.am_out) *ga.am_out = ArgmaxParts{};
     if (ga.next_done) *ga.next_done = false;
     if (ga.M <= 0) return UT_OK;
     if (ga.w2 && (ga.w2->fmt != w->fmt || ga.w2->in_dim != w->in_dim ||
@@ -1244,6 +1304,34 @@ int32_t matmul_digits(ut_ctx *ctx, const ut_qtensor *w, const float *x, const XD
         }
     }
     return gemv(ctx, ga);
+}
+
+int32_t matmul_digits_argmax(ut_ctx *ctx, const ut_qtensor *w, const float *x, const XDigits &xd,
+                             int64_t M, float *out, int32_t *idx, void *am_scratch,
+                             const int32_t *err) {
+    ArgmaxParts am;
+    if (!(ctx->fast_int8 && w->fmt == UT_FMT_INT8) && w->fmt != UT_FMT_F32 && fast_ok(w) &&
+        M >= 1 && M <= 4) {
+        GemvArgs ga;
+        ga.w = w;
+        ga.M = M;
+        ga.out = out;
+        ga.ldo = w->out_dim;
+        ga.xf = x;
+        ga.xd = xd;
+        ga.am_scratch = am_scratch;
+        ga.am_out = &am;
+        const bool need4 = w->fmt == UT_FMT_INT4, need8 = w->fmt == UT_FMT_INT8;
+        if ((need4 && !xd.dig4) || (need8 && !xd.dig8)) {
+            set_error(ctx, "matmul_digits: activation digits of the wrong form");
+            return UT_ERR_ARG;
+        }
+        UT_TRY(gemv(ctx, ga));
+    } else {
+        UT_TRY(matmul_digits(ctx, w, x, xd, M, out, w->out_dim, 0));
+    }
+    if (am.v) return launch_argmax_final(ctx, out, M, w->out_dim, am, idx, err);
+    return launch_argmax(ctx, out, M, w->out_dim, w->out_dim, idx, am_scratch, err);
 }
 
 int32_t matmul_dev(ut_ctx *ctx, const ut_qtensor *w, const float *x, int64_t M, float *out,

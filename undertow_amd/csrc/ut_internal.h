@@ -231,6 +231,15 @@ struct SplitKPartials {
     int64_t O = 0;
 };
 
+// A GEMV epilogue's argmax partials (ut_argmax.h): workgroup j of the
+// producing launch writes the best (value, row) of activation row m among
+// the output rows it finished to v[m * stride + j], i[m * stride + j].
+struct ArgmaxParts {
+    float *v = nullptr;  // nullptr: no partials
+    int32_t *i = nullptr;
+    int64_t stride = 0;
+};
+
 struct GemvArgs {
     const ut_qtensor *w = nullptr;
     const float *xf = nullptr;  // f32 activations [M, K] (F32 weights)
@@ -256,6 +265,12 @@ struct GemvArgs {
     // launch instead of two); *next_done reports whether it did
     const struct NormNext *next = nullptr;
     bool *next_done = nullptr;
+    // optional (M <= 4, one weight, no defer, no next): the launch that
+    // finishes the output rows also leaves argmax partials per workgroup in
+    // am_scratch (argmax_scratch_bytes) and reports their view in *am_out
+    // (am_out->v == nullptr: it did not)
+    void *am_scratch = nullptr;
+    ArgmaxParts *am_out = nullptr;
 };
 int32_t gemv(ut_ctx *ctx, const GemvArgs &a);
 // The kv_a / q_a pair GEMV's deferred split-K partials (kv_a rows first)
@@ -282,6 +297,13 @@ size_t matmul_digit_bytes(int64_t M, int64_t K);
 // x is read only for f32 weights).
 int32_t matmul_digits(ut_ctx *ctx, const ut_qtensor *w, const float *x, const XDigits &xd,
                       int64_t M, float *out, int64_t ldo, int accumulate);
+// matmul_digits into out [M][out_dim], then idx [M] = each row's argmax;
+// the GEMV that finishes the rows leaves the argmax partials where it can
+// (am_scratch: argmax_scratch_bytes(M, out_dim)); err: the sticky error word
+// copied to idx[M].
+int32_t matmul_digits_argmax(ut_ctx *ctx, const ut_qtensor *w, const float *x, const XDigits &xd,
+                             int64_t M, float *out, int32_t *idx, void *am_scratch,
+                             const int32_t *err);
 int32_t matmul_dev(ut_ctx *ctx, const ut_qtensor *w, const float *x, int64_t M, float *out,
                    int64_t ldo, int accumulate, void *digit_scratch);
 

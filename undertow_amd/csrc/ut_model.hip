@@ -134,6 +134,9 @@ struct ut_session {
     // up, then readback slots; `ready` marks the end of the last readback
     int32_t *pin = nullptr;
     hipEvent_t ready = nullptr;
+    // where the last readback put the sticky error flag (an int of the
+    // readback slot: its last one, or just after the argmax rows)
+    int64_t err_slot = 63;
     // The one-row decode step as a captured graph (ut_model_enable_graphs):
     // the device word holding the step's position, the position it will hold
     // once the enqueued work has run (-1: unknown), the executable graph, the
@@ -377,7 +380,7 @@ int32_t ws_reserve(ut_session *s, int64_t rows) {
     size_t iqabs = F(R * heads * Lr), iqrope = F(R * heads * c.qk_rope_head_dim + 1);
     size_t iclat = F(R * heads * Lr), ictx = F(R * heads * c.v_head_dim);
     size_t ilog = F(R * c.vocab_size), iemb = F(R * H), icat = F(R * 2 * H);
-    size_t irl = F(4 * E), irw = F(4 * k), irid = F(4 * k), iids = F(R), iam = F(R), ierr = F(1);
+    size_t irl = F(4 * E), irw = F(4 * k), irid = F(4 * k), iids = F(R), iam = F(R + 1), ierr = F(1);
     size_t ivids = F(8);
     size_t ivmax = F(R * heads * ((c.v_head_dim + 7) / 8)), ivexp = F(R);
     size_t idig = plan.add(matmul_digit_bytes(R, kmax));
@@ -684,9 +687,9 @@ int32_t moe_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
         // with the logits whole and few choices the expert launch routes and
         // builds the slot plan itself (moe_pass); else route + plan in one
         // launch here
-        // (three or more rows with int4 experts go to the matrix-core expert
-        // kernels, which take the plan ready-made)
-        const bool mfma_rows = M >= 3 && gate_up_mfma_ok(L.expert_fmt, M, H);
+        // (two or more rows go to the matrix-core expert kernels, which take
+        // the plan ready-made: route and plan in one launch)
+        const bool mfma_rows = M >= 2 && gate_up_mfma_ok(L.expert_fmt, M, H);
         const bool gate_plans = !m->store && gparts.ks <= 1 && (int64_t)M * k <= 64 &&
                                 L.expert_fmt != UT_FMT_F32 && !mfma_rows;
         if (!gate_plans && !m->store)
@@ -1044,8 +1047,10 @@ int32_t prefill_dev(ut_session *s, const int32_t *ids, int64_t n, const int32_t 
     if (!fuse || nl == 0)
         UT_TRY(norm_dig(s, w.x, H, m->final_norm, H, n, w.normed, H, w.digA,
                         dig_flags({m->lm_head}), &fd));
+    // the argmax rows, then the sticky error word at am[n] (one readback)
+    if (n <= 4) return matmul_digits_argmax(ctx, m->lm_head, w.normed, fd, n, w.logits, w.am, w.argm, w.err);
     UT_TRY(matmul_digits(ctx, m->lm_head, w.normed, fd, n, w.logits, V, 0));
-    return launch_argmax(ctx, w.logits, n, V, V, w.am, w.argm);
+    return launch_argmax(ctx, w.logits, n, V, V, w.am, w.argm, w.err);
 }
 
 int32_t read_argmax(ut_session *s, int64_t n, int32_t *out) {
@@ -1059,19 +1064,30 @@ int32_t read_argmax(ut_session *s, int64_t n, int32_t *out) {
     return UT_OK;
 }
 
-// Asynchronous readback for the generation loops: n ints from dev, then the
-// sticky error flag, into the session's pinned readback slot; `ready` is
+// Asynchronous readback for the generation loops: n ints from dev and the
+// sticky error flag into the session's pinned readback slot; `ready` is
 // recorded behind them, so later launches need not wait for the host.
-int32_t readback_enqueue(ut_session *s, const int32_t *dev, int64_t n, int64_t slot_off = 0) {
+// How the flag comes back (err): RB_ERR_COPY in a copy of its own,
+// RB_ERR_INLINE as dev[n] (the argmax rows of prefill_dev carry it), RB_ERR_LATER
+// not with this readback (a later one of the same wait carries it).
+enum { RB_ERR_COPY, RB_ERR_INLINE, RB_ERR_LATER };
+int32_t readback_enqueue(ut_session *s, const int32_t *dev, int64_t n, int64_t slot_off = 0,
+                         int err = RB_ERR_COPY) {
     ut_ctx *ctx = s->ctx;
     int32_t *back = s->pin + kPinIds;
-    if (slot_off + n + 1 > kPinBack) {
+    if (slot_off + n + 1 > kPinBack - 1) {
         set_error(ctx, "readback of %lld ints exceeds the staging slot", (long long)n);
         return UT_ERR_ARG;
     }
-    UT_CHECK_HIP(ctx, hipMemcpyAsync(back + slot_off, dev, (size_t)n * 4, hipMemcpyDeviceToHost, ctx->stream));
-    UT_CHECK_HIP(ctx, hipMemcpyAsync(back + kPinBack - 1, s->ws.err, 4, hipMemcpyDeviceToHost, ctx->stream));
-    UT_CHECK_HIP(ctx, hipEventRecord(s->ready, ctx->stream));
+    const int64_t cnt = err == RB_ERR_INLINE ? n + 1 : n;
+    UT_CHECK_HIP(ctx, hipMemcpyAsync(back + slot_off, dev, (size_t)cnt * 4, hipMemcpyDeviceToHost, ctx->stream));
+    if (err == RB_ERR_COPY) {
+        UT_CHECK_HIP(ctx, hipMemcpyAsync(back + kPinBack - 1, s->ws.err, 4, hipMemcpyDeviceToHost, ctx->stream));
+        s->err_slot = kPinBack - 1;
+    } else if (err == RB_ERR_INLINE) {
+        s->err_slot = slot_off + n;
+    }
+    if (err != RB_ERR_LATER) UT_CHECK_HIP(ctx, hipEventRecord(s->ready, ctx->stream));
     return UT_OK;
 }
 
@@ -1080,7 +1096,7 @@ int32_t readback_wait(ut_session *s, int64_t n, int32_t *out, int64_t slot_off =
     ut_ctx *ctx = s->ctx;
     UT_CHECK_HIP(ctx, hipEventSynchronize(s->ready));
     const int32_t *back = s->pin + kPinIds;
-    if (back[kPinBack - 1]) {
+    if (back[s->err_slot]) {
         set_error(ctx, "a routed expert id was out of range or not loaded");
         return UT_ERR_BAD_EXPERT;
     }
@@ -1161,8 +1177,7 @@ int32_t draft_rows_dev(ut_session *s, const int32_t *host_ids, int in_slot,
         UT_TRY(norm_dig(s, w.x + (rows - 1) * H, H, m->mtp_norm, H, 1, w.normed, H, w.digA,
                         dig_flags({m->mtp_head}), &hd_));
     }
-    UT_TRY(matmul_digits(ctx, m->mtp_head, hn, hd_, 1, w.logits, V, 0));
-    return launch_argmax(ctx, w.logits, 1, V, V, draft_dev, w.argm);
+    return matmul_digits_argmax(ctx, m->mtp_head, hn, hd_, 1, w.logits, draft_dev, w.argm, nullptr);
 }
 
 // ---------------------------------------------------------- synthesis ---
@@ -1691,7 +1706,7 @@ int64_t gen_greedy(ut_model *m, const int32_t *prompt, int64_t n, Emit &em) {
         }
     }
     while (queued && rc == UT_OK) {
-        rc = readback_enqueue(s, s->ws.am, 1);
+        rc = readback_enqueue(s, s->ws.am, 1, 0, RB_ERR_INLINE);
         if (rc) break;
         bool next_queued = false;
         if (em.produced + 1 < em.max_new) {
@@ -1798,12 +1813,12 @@ int64_t gen_spec(ut_model *m, const int32_t *prompt, int64_t n, int32_t depth, u
             break;
         }
         if (rc) break;
-        if (!draft_fn) rc = readback_enqueue(s, s->ws.vids + 1, depth, depth + 1);
-        if (rc == UT_OK) rc = readback_enqueue(s, s->ws.am, depth + 1, 0);
+        if (!draft_fn) rc = readback_enqueue(s, s->ws.vids + 1, depth, depth + 2, RB_ERR_LATER);
+        if (rc == UT_OK) rc = readback_enqueue(s, s->ws.am, depth + 1, 0, RB_ERR_INLINE);
         if (rc == UT_OK) rc = readback_wait(s, depth + 1, am.data(), 0);
         if (rc) break;
         verified = true;
-        if (!draft_fn) memcpy(drafts.data(), s->pin + kPinIds + depth + 1, (size_t)depth * 4);
+        if (!draft_fn) memcpy(drafts.data(), s->pin + kPinIds + depth + 2, (size_t)depth * 4);
         s->tokens.push_back(next);
         s->tokens.insert(s->tokens.end(), drafts.begin(), drafts.end());
         int64_t a = 0;

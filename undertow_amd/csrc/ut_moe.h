@@ -118,9 +118,72 @@ struct ScratchLayout {
 // Whole-workgroup function: ids are read once in parallel, the assignment
 // runs in LDS, the plan is written out in parallel.  n = M*k <= 256.
 // tbl: the [6][E] pointer table (ExpertPtrs laid out from gate_w).
+// The slot plan of make_plan for one activation row (n = k <= 64 entries),
+// resolved by each wave on its own (lane j holds entry j; no LDS, no
+// barrier): returns the slot count and lane `slot u's first entry`'s
+// pointers in p6 (unset when u >= count).  The writer wave also writes the
+// plan and the invalid-id flag exactly as make_plan does.  id: this lane's
+// entry (-1 past n), loaded by the caller ahead of other loads.
+__device__ inline int plan_slot_wave(int id, int n, int64_t E, const void *const *__restrict__ tbl,
+                                     int u, bool writer, MoePlan plan,
+                                     int32_t *__restrict__ err_flag, const void *(&p6)[6]) {
+    const int lane = threadIdx.x & 63;
+    const bool inr = lane < n && id >= 0 && id < E;
+    const int64_t ec = inr ? id : 0;
+    const void *p[6];
+#pragma unroll
+    for (int i = 0; i < 6; i++) p[i] = tbl[(int64_t)i * E + ec];
+    const bool ok = inr && p[kSpGate] != nullptr;
+    const int e = ok ? id : -1;
+    // j0: the entry's first appearance (the reference groups rows by expert
+    // in first-appearance order, model.rs:219-233)
+    int j0 = lane;
+    for (int i = 0; i < n; i++) {
+        const int ei = __builtin_amdgcn_readlane(e, i);
+        if (i < j0 && ei == e) j0 = i;
+    }
+    const bool first = ok && j0 == lane;
+    const uint64_t fm = __ballot(first);
+    const int slot = ok ? __popcll(fm & ((1ull << j0) - 1)) : -1;
+    const int cnt = __popcll(fm);
+    const uint64_t um = __ballot(first && slot == u);
+    if (um) {
+        const int L = __ffsll((unsigned long long)um) - 1;
+#pragma unroll
+        for (int i = 0; i < 6; i++) {
+            const uint64_t v = (uint64_t)p[i];
+            const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, L);
+            const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), L);
+            p6[i] = (const void *)(((uint64_t)hi << 32) | lo);
+        }
+    }
+    if (writer) {
+        if (lane < n) {
+            if (!ok && id != -1 && err_flag) *err_flag = 1;
+            plan.choice_slot[lane] = slot;
+            if (first) {
+                plan.uniq[slot] = e;
+#pragma unroll
+                for (int i = 0; i < 6; i++) plan.sp[slot * 6 + i] = p[i];
+            }
+        }
+        if (lane == 0) *plan.count = cnt;
+    }
+    return cnt;
+}
+
 __device__ inline void make_plan(const int32_t *ids, int M, int k, int E,
                           const void *const *__restrict__ tbl, int extra_slot,
                           MoePlan plan, int32_t *__restrict__ err_flag) {
+    if (M * k <= 64 && extra_slot < 0) {
+        // up to 64 entries: wave 0 alone, one entry per lane (the same plan)
+        if ((threadIdx.x >> 6) == 0) {
+            const int lane = threadIdx.x & 63;
+            const void *p6[6];
+            plan_slot_wave(lane < M * k ? ids[lane] : -1, M * k, E, tbl, 0, true, plan, err_flag, p6);
+        }
+        return;
+    }
     const void *const *gate_tbl = tbl;
     __shared__ int s_e[256], s_first[256];
     const int n = M * k, tid = threadIdx.x;

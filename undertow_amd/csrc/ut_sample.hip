@@ -6,44 +6,11 @@
 // (vocab 129280 rows are read at full bandwidth), k_argmax_final reduces
 // the partials.  Ties keep the lowest index; the result does not depend
 // on the split.
+#include "ut_argmax.h"
 #include "ut_internal.h"
 #include "ut_sample.h"
 
 namespace ut {
-
-struct Best {
-    float v;
-    int32_t i;  // -1: no candidate
-};
-
-__device__ __forceinline__ Best better(Best a, Best b) {
-    if (a.i < 0) return b;
-    if (b.i < 0) return a;
-    if (b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
-    return a;
-}
-
-__device__ Best block_best(Best b) {
-    __shared__ float sv[16];
-    __shared__ int32_t si[16];
-    for (int off = 32; off >= 1; off >>= 1) {
-        Best o;
-        o.v = __shfl_xor(b.v, off, 64);
-        o.i = __shfl_xor(b.i, off, 64);
-        b = better(b, o);
-    }
-    const int wave = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
-    if ((threadIdx.x & 63) == 0) { sv[wave] = b.v; si[wave] = b.i; }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        Best r{0.0f, -1};
-        for (int w = 0; w < nw; w++) r = better(r, Best{sv[w], si[w]});
-        sv[0] = r.v;
-        si[0] = r.i;
-    }
-    __syncthreads();
-    return Best{sv[0], si[0]};
-}
 
 __global__ __launch_bounds__(256) void k_argmax_partial(const float *__restrict__ x, int64_t V,
                                                         int64_t ldx, int64_t chunk,
@@ -65,28 +32,62 @@ __global__ __launch_bounds__(256) void k_argmax_partial(const float *__restrict_
     }
 }
 
-__global__ __launch_bounds__(64) void k_argmax_final(const float *__restrict__ x, int64_t ldx,
-                                                     int nparts, const float *__restrict__ pv,
-                                                     const int32_t *__restrict__ pi,
-                                                     int32_t *__restrict__ idx) {
+// One workgroup per row: the best of the row's nparts partials, then the
+// row rule (index 0 when x[row][0] is NaN or nothing was a candidate).
+// err: also copies the sticky error word to idx[rows] (one readback for both).
+__global__ __launch_bounds__(256) void k_argmax_final(const float *__restrict__ x, int64_t ldx,
+                                                      int64_t nparts, const float *__restrict__ pv,
+                                                      const int32_t *__restrict__ pi,
+                                                      int32_t *__restrict__ idx,
+                                                      const int32_t *__restrict__ err) {
     const int64_t row = blockIdx.x;
     Best b{0.0f, -1};
-    for (int j = threadIdx.x; j < nparts; j += 64) b = better(b, Best{pv[row * nparts + j], pi[row * nparts + j]});
-    for (int off = 32; off >= 1; off >>= 1) {
-        Best o;
-        o.v = __shfl_xor(b.v, off, 64);
-        o.i = __shfl_xor(b.i, off, 64);
-        b = better(b, o);
+    // 16 partials per thread per round, every load of a round issued first
+    constexpr int U = 16;
+    for (int64_t j0 = 0; j0 < nparts; j0 += U * (int64_t)blockDim.x) {
+        Best c[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int64_t j = j0 + threadIdx.x + (int64_t)u * blockDim.x;
+            c[u] = j < nparts ? Best{pv[row * nparts + j], pi[row * nparts + j]} : Best{0.0f, -1};
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) b = better(b, c[u]);
     }
+    b = block_best(b);
     if (threadIdx.x == 0) {
-        float x0 = x[row * ldx];
+        const float x0 = x[row * ldx];
         idx[row] = (x0 != x0 || b.i < 0) ? 0 : b.i;
+        if (err && row == (int64_t)gridDim.x - 1) idx[gridDim.x] = *err;
     }
 }
 
 size_t argmax_scratch_bytes(int64_t rows, int64_t V) {
+    // the widest partial set: a GEMV epilogue's, one per 16 output rows
     int64_t parts = argmax_parts(V);
-    return (size_t)rows * parts * 8 + 256;
+    const int64_t gemv_parts = argmax_gemv_parts_max(V);
+    if (gemv_parts > parts) parts = gemv_parts;
+    return (size_t)rows * parts * 8 + 512;
+}
+
+int64_t argmax_gemv_parts_max(int64_t V) { return (V + 15) / 16; }
+
+ArgmaxParts argmax_parts_view(void *scratch, int64_t rows, int64_t stride) {
+    ArgmaxParts p;
+    p.v = (float *)scratch;
+    p.i = (int32_t *)((char *)scratch + ((rows * stride * 4 + 255) & ~int64_t(255)));
+    p.stride = stride;
+    return p;
+}
+
+int32_t launch_argmax_final(ut_ctx *ctx, const float *x, int64_t rows, int64_t ldx,
+                            const ArgmaxParts &p, int32_t *idx, const int32_t *err) {
+    if (rows <= 0) return UT_OK;
+    int tok = timing_begin(ctx, "argmax_final");
+    hipLaunchKernelGGL(k_argmax_final, dim3((unsigned)rows), dim3(256), 0, ctx->stream, x, ldx,
+                       p.stride, p.v, p.i, idx, err);
+    timing_end(ctx, tok);
+    return launch_check(ctx, "k_argmax_final");
 }
 
 int64_t argmax_parts(int64_t V) {
@@ -97,20 +98,17 @@ int64_t argmax_parts(int64_t V) {
 }
 
 int32_t launch_argmax(ut_ctx *ctx, const float *x, int64_t rows, int64_t V, int64_t ldx,
-                      int32_t *idx, void *scratch) {
+                      int32_t *idx, void *scratch, const int32_t *err) {
     if (rows <= 0) return UT_OK;
     const int64_t parts = argmax_parts(V);
     const int64_t chunk = (V + parts - 1) / parts;
-    float *pv = (float *)scratch;
-    int32_t *pi = (int32_t *)((char *)scratch + ((rows * parts * 4 + 255) & ~int64_t(255)));
+    const ArgmaxParts p = argmax_parts_view(scratch, rows, parts);
     int tok = timing_begin(ctx, "argmax");
     hipLaunchKernelGGL(k_argmax_partial, dim3((unsigned)parts, (unsigned)rows), dim3(256), 0,
-                       ctx->stream, x, V, ldx, chunk, pv, pi);
+                       ctx->stream, x, V, ldx, chunk, p.v, p.i);
     UT_TRY(launch_check(ctx, "k_argmax_partial"));
-    hipLaunchKernelGGL(k_argmax_final, dim3((unsigned)rows), dim3(64), 0, ctx->stream, x, ldx,
-                       (int)parts, pv, pi, idx);
     timing_end(ctx, tok);
-    return launch_check(ctx, "k_argmax_final");
+    return launch_argmax_final(ctx, x, rows, ldx, p, idx, err);
 }
 
 }  // namespace ut
