@@ -109,3 +109,20 @@ def test_c4_perfect_drafts(c4, depth):
     toks, drafted, accepted = m.speculative_loop(prompt, NEW, depth=depth, draft_fn=perfect)
     assert toks == stream
     assert drafted > 0 and accepted >= drafted - (depth - 1)
+
+
+@pytest.mark.parametrize("rows", [2, 4])
+def test_c4_decode_rows_equal_verify_rows(c4, rows):
+    """The design's MTP on == off guarantee at full width: a row's logits
+    from one-row decode steps equal, bit for bit, the same row's logits from
+    a verify step of `rows` rows (exact-integer GEMVs, row-independent
+    norms, attention slices and expert plans)."""
+    ck, m, om, prompt, stream = c4
+    feed = stream[:rows]
+    s = m.session()
+    s.prefill(prompt)
+    one = np.stack([s.decode(t) for t in feed])
+    v = m.session()
+    v.prefill(prompt)
+    many = v.prefill(feed)
+    assert np.array_equal(one, many)

@@ -208,6 +208,9 @@ struct MlaPreArgs {
     const float *kv_scales, *q_scales;
     int M;
     RowDigArgs qa;  // K = q_lora_rank, norm_w = q_a_norm
+    // set: q_a's rows go here as summed (un-normalised) and qa is unused
+    // (the q_b GEMV normalises them while staging)
+    float *qa_raw;
     int64_t L, P;
     const float *kv_norm;
     float *latent, *krot;
@@ -245,6 +248,10 @@ __global__ __launch_bounds__(1024) void k_mla_pre(MlaPreArgs a) {
     const float *scl = qrow ? a.q_scales : a.kv_scales;
     for (int64_t i = tid; i < n; i += blockDim.x)
         sc[i] = int_total_to_f32(splitk_total(a.part, a.ks, zs, off + i), a.exps[m], ld_global_f32(scl + i));
+    if (qrow && a.qa_raw) {
+        for (int64_t i = tid; i < n; i += blockDim.x) a.qa_raw[m * n + i] = sc[i];
+        return;
+    }
     __syncthreads();
     if (qrow) {
         const int64_t K = a.qa.K, NG = (K + 7) / 8;
@@ -271,7 +278,7 @@ int32_t launch_mla_pre(ut_ctx *ctx, const SplitKPartials &pp, int64_t O1, const 
                        const float *kv_scales, const float *q_scales, int64_t M, int64_t q_lora,
                        const float *q_norm, float eps, float *qa_n, const XDigits &qd, int flags,
                        int64_t L, int64_t P, const float *kv_norm, float *latent, float *krot,
-                       __bf16 *kc, int64_t pos_base, const float2 *table) {
+                       __bf16 *kc, int64_t pos_base, const float2 *table, float *qa_raw) {
     if (!mla_pre_ok(M, q_lora, L, P) || pp.ks < 1 || !pp.part || O1 != L + P) {
         set_error(ctx, "mla_pre: unsupported shape");
         return UT_ERR_ARG;
@@ -302,6 +309,7 @@ int32_t launch_mla_pre(ut_ctx *ctx, const SplitKPartials &pp, int64_t O1, const 
     a.kc = kc;
     a.pos = pos_ref(ctx, pos_base);
     a.table = table;
+    a.qa_raw = qa_raw;
     int tok = timing_begin(ctx, "mla_pre");
     hipLaunchKernelGGL(k_mla_pre, dim3((unsigned)(2 * M)), dim3(1024), 0, ctx->stream, a);
     timing_end(ctx, tok);
@@ -448,7 +456,9 @@ template <int M> constexpr int plain_rows() { return 2; }
 template <int M> constexpr int plain_depth() { return M == 1 ? 4 : M == 2 ? 2 : gemv_depth<M>(); }
 __host__ __device__ constexpr int plain_rows_rt(int) { return 16 * 2; }
 
-template <int FMT, int M>
+// NORM: x is one un-normalised row, normalised while staged (XSrc::nw).
+constexpr int kGemvNormCols = 2048;
+template <int FMT, int M, bool NORM = false>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
     constexpr int R = plain_rows<M>();
     __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
@@ -483,17 +493,20 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
         if (a.xmax) {
             rowmax_load<M>(a.xmax, a.nxmax, pv);
             if (!late) shifts(xs.sh);
-        } else {
+        } else if (!NORM) {
 #pragma unroll
             for (int m = 0; m < M; m++) exl[m] = a.exps[m];
         }
     }
     auto prep = [&](int32_t (&shl)[4]) {
-        if constexpr (FMT != UT_FMT_F32)
+        if constexpr (FMT != UT_FMT_F32) {
             if (late) shifts(shl);
+            // normalised while staged: the staging found the row's shift
+            if constexpr (NORM) exl[0] = shl[0] == INT32_MIN ? INT32_MIN : -shl[0];
+        }
     };
     CoreOut<FMT, M, R> res;
-    if (a.ks > 1) {
+    if (!NORM && a.ks > 1) {
         gemv_core<FMT, M, R, plain_depth<M>()>(rows, a.K, xs, lds, res, kb, ke, prep);
 #pragma unroll
         for (int r = 0; r < R; r++)
@@ -506,7 +519,11 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
             }
         return;
     }
-    gemv_core<FMT, M, R, plain_depth<M>()>(rows, a.K, xs, lds, res, 0, -1, prep);
+    // the normalising staging holds its row's groups in registers: rows of
+    // at most kGemvNormCols columns (one group per thread)
+    constexpr int KC = NORM ? gemv_chunk_cols<FMT, M, kGemvNormCols>() : gemv_chunk_cols<FMT, M>();
+    gemv_core<FMT, M, R, plain_depth<M>(), KC, false, decltype(prep) &, NoMid, NORM>(
+        rows, a.K, xs, lds, res, 0, -1, prep);
     Best bm[M];
 #pragma unroll
     for (int m = 0; m < M; m++) bm[m] = Best{0.0f, -1};
@@ -774,6 +791,18 @@ __global__ __launch_bounds__(64) void k_gemv_generic(int32_t fmt, const uint8_t 
 
 static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
+bool gemv_norm_ok(const ut_qtensor *w, int64_t M, const void *x, const void *norm_w) {
+    if (M != 1 || !w || (w->fmt != UT_FMT_INT8 && w->fmt != UT_FMT_INT4))
+        return false;
+    const int64_t K = w->in_dim;
+    const int64_t kc = w->fmt == UT_FMT_INT8 ? gemv_chunk_cols<UT_FMT_INT8, 1, kGemvNormCols>()
+                                             : gemv_chunk_cols<UT_FMT_INT4, 1, kGemvNormCols>();
+    const int64_t step = w->fmt == UT_FMT_INT8 ? FmtTraits<UT_FMT_INT8>::kStepCols
+                                               : FmtTraits<UT_FMT_INT4>::kStepCols;
+    return K <= kc && K % step == 0 && aligned16(x) && aligned16(norm_w) &&
+           aligned16(w->payload) && w->row_bytes % 16 == 0;
+}
+
 // Whether the fast kernel takes this weight (16-byte aligned rows).
 static bool fast_ok(const ut_qtensor *w);
 bool gemv_fast_ok(const ut_qtensor *w) { return fast_ok(w); }
@@ -1005,7 +1034,17 @@ static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrow
     } else {
         constexpr int PL = FmtTraits<FMT>::kPlanes;
         const int64_t KW = (w->in_dim + FmtTraits<FMT>::kColsPerWord - 1) / FmtTraits<FMT>::kColsPerWord;
-        if (ga.xmax) {
+        if (ga.norm_w) {
+            // one row, normalised and digitised while staged (gemv checked
+            // the shape: one chunk, no split)
+            a.x.dig = nullptr;
+            a.x.KW = KW;
+            a.x.xf = ga.xf;
+            a.x.ldx = w->in_dim;
+            a.x.nw = ga.norm_w;
+            a.x.neps = ga.norm_eps;
+            a.exps = nullptr;
+        } else if (ga.xmax) {
             a.x.dig = nullptr;
             a.x.KW = KW;
             a.x.xf = ga.xf + m0 * w->in_dim;
@@ -1024,7 +1063,7 @@ static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrow
     a.nxmax = ga.nxmax;
     // int8 at 3..4 rows: the matrix-core kernel (64-row tiles, steps of 64
     // columns), the same partials and epilogue
-    const bool i8_mfma = FMT == UT_FMT_INT8 && mrows >= UT_GEMV_I8_MFMA_MIN_M && mrows <= 4 &&
+    const bool i8_mfma = FMT == UT_FMT_INT8 && !ga.norm_w && mrows >= UT_GEMV_I8_MFMA_MIN_M && mrows <= 4 &&
                          w->in_dim % kMfmaI8SegCols == 0 &&
                          (a.xmax || ((uintptr_t)a.x.dig & 15) == 0);
     if (i8_mfma) return launch_gemv_i8_mfma(ctx, ga, a, m0, mrows);
@@ -1035,7 +1074,11 @@ static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrow
     // 25.3 us and its split sum from 12.0 to 10.2 us)
     const int64_t resident = gemv_resident<FMT>(ctx, mrows) / (a.xmax ? 2 : 1);
     splitk_plan(FMT, a.O, w->in_dim, rows_per_wg, resident, &a.ks, &a.kslice);
-    if (FMT != UT_FMT_F32) {
+    if (ga.norm_w) {
+        // the staging normalises whole rows: no K split
+        a.ks = 1;
+        a.kslice = w->in_dim;
+    } else if (FMT != UT_FMT_F32) {
         // every launch takes enough splits for its K slice to be staged in
         // one chunk at its row count: a second chunk drains the weight stream
         // behind a staging round (o_proj at DeepSeek-V3 width, two rows: 2
@@ -1061,6 +1104,13 @@ static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrow
     argmax_plan(ga, a, m0, mrows, grid.x);
     const char *name = FMT == UT_FMT_INT4 ? "gemv_int4" : FMT == UT_FMT_INT8 ? "gemv_int8" : "gemv_f32";
     int tok = timing_begin(ctx, name);
+    if constexpr (FMT != UT_FMT_F32) {
+        if (ga.norm_w) {
+            hipLaunchKernelGGL((k_gemv<FMT, 1, true>), grid, dim3(kGemvThreads), 0, ctx->stream, a);
+            timing_end(ctx, tok);
+            return launch_check(ctx, name);
+        }
+    }
     switch (mrows) {
     case 1: hipLaunchKernelGGL((k_gemv<FMT, 1>), grid, dim3(kGemvThreads), 0, ctx->stream, a); break;
     case 2: hipLaunchKernelGGL((k_gemv<FMT, 2>), grid, dim3(kGemvThreads), 0, ctx->stream, a); break;
@@ -1161,6 +1211,11 @@ int32_t gemv(ut_ctx *ctx, const GemvArgs &ga) {
     }
     if (ga.defer && ga.M > 4) {
         set_error(ctx, "gemv: deferred split-K sums take at most 4 rows");
+        return UT_ERR_ARG;
+    }
+    if (ga.norm_w && (ga.w2 || ga.defer || ga.next || ga.xmax || !gemv_norm_ok(w, ga.M, ga.xf, ga.norm_w))) {
+        set_error(ctx, "gemv: normalise-while-staging takes one row of at most 8192 columns "
+                       "(a multiple of the step) of an int4/int8 weight, 16-byte aligned");
         return UT_ERR_ARG;
     }
     if (fast_ok(w) && (w->fmt == UT_FMT_F32 ? aligned16(ga.xf) && (w->in_dim % 4 == 0) : true)) {

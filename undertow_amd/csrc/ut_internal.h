@@ -271,18 +271,28 @@ struct GemvArgs {
     // (am_out->v == nullptr: it did not)
     void *am_scratch = nullptr;
     ArgmaxParts *am_out = nullptr;
+    // optional (one row; gemv_norm_ok): xf is the un-normalised row, which
+    // the GEMV rms-normalises with norm_w (eps norm_eps) and digitises while
+    // staging it, with the row digitiser's arithmetic, so the outputs equal
+    // the GEMV of that digitiser's digits bit for bit
+    const float *norm_w = nullptr;
+    float norm_eps = 0.0f;
 };
+bool gemv_norm_ok(const ut_qtensor *w, int64_t M, const void *x, const void *norm_w);
 int32_t gemv(ut_ctx *ctx, const GemvArgs &a);
 // The kv_a / q_a pair GEMV's deferred split-K partials (kv_a rows first)
 // finished in one launch: q_a rows rms-normalised into qa_n and digitised
 // into qd (flags), kv_a rows appended to the cache (as launch_kv_append).
+// qa_raw set: q_a rows are only summed, into qa_raw, for a consumer that
+// normalises them itself (GemvArgs::norm_w).
 constexpr int64_t kMlaPreMaxComp = 1024;  // kv_lora_rank + qk_rope_head_dim bound
 bool mla_pre_ok(int64_t M, int64_t q_lora, int64_t L, int64_t P);
 int32_t launch_mla_pre(ut_ctx *ctx, const SplitKPartials &pp, int64_t O1, const int32_t *exps,
                        const float *kv_scales, const float *q_scales, int64_t M, int64_t q_lora,
                        const float *q_norm, float eps, float *qa_n, const XDigits &qd, int flags,
                        int64_t L, int64_t P, const float *kv_norm, float *latent, float *krot,
-                       __bf16 *kc, int64_t pos_base, const float2 *table);
+                       __bf16 *kc, int64_t pos_base, const float2 *table,
+                       float *qa_raw = nullptr);
 // f32 weights, M <= 4 rows, out [M][ldo]: one workgroup per output row
 bool rowdot_f32_ok(const ut_qtensor *w, int64_t M);
 int32_t launch_rowdot_f32(ut_ctx *ctx, const ut_qtensor *w, const float *x, int64_t M,

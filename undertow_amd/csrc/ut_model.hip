@@ -840,7 +840,25 @@ int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
     } else {
         UT_TRY(matmul_digits(ctx, L.kv_a, x, xd, rows, w.comp, Lr + rope, 0));
     }
-    if (fused && pp.ks > 1) {
+    // one row: q_b normalises q_a itself while staging it (the same digits
+    // as the row digitiser's), so mla_pre only sums q_a's partials
+    const bool qb_norm = fused && pp.ks > 1 && rows == 1 &&
+                         gemv_norm_ok(L.q_b, 1, w.qa, L.q_a_norm);
+    if (qb_norm) {
+        UT_TRY(launch_mla_pre(ctx, pp, Lr + rope, xd.exps, L.kv_a->scales, L.q_a->scales, rows,
+                              c.q_lora_rank, L.q_a_norm, c.rms_norm_eps, nullptr, XDigits{}, 0, Lr,
+                              rope, L.kv_a_norm, kv.latent, kv.krot, kv.kc, pos_base,
+                              m->rope_table, w.qa));
+        GemvArgs gq;
+        gq.w = L.q_b;
+        gq.M = 1;
+        gq.xf = w.qa;
+        gq.out = w.q;
+        gq.ldo = heads * qh;
+        gq.norm_w = L.q_a_norm;
+        gq.norm_eps = c.rms_norm_eps;
+        UT_TRY(gemv(ctx, gq));
+    } else if (fused && pp.ks > 1) {
         const int qf = dig_flags({L.q_b});
         const XDigits qd = xdigits_view(w.digB, rows, c.q_lora_rank, qf);
         UT_TRY(launch_mla_pre(ctx, pp, Lr + rope, xd.exps, L.kv_a->scales, L.q_a->scales, rows,
