@@ -435,6 +435,9 @@ struct PlainArgs {
     // optional: the launch that finishes the rows leaves argmax partials
     // (k_gemv / k_gemv_mfma_i8 unsplit: one per workgroup; split: the sum's)
     ArgmaxParts am;
+    // optional (k_gemv NORM): one more workgroup appends a finished kv_a
+    // row to the latent cache (kv_append_row) beside the GEMV's
+    KvAppendArgs kv;
 };
 
 __device__ __forceinline__ const uint8_t *plain_row(const PlainArgs &a, int64_t row) {
@@ -461,6 +464,15 @@ constexpr int kGemvNormCols = 2048;
 template <int FMT, int M, bool NORM = false>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
     constexpr int R = plain_rows<M>();
+    if constexpr (NORM) {
+        if (a.kv.comp && blockIdx.x == gridDim.x - 1) {
+            __shared__ double red4[4];
+            const KvAppendArgs &k = a.kv;
+            kv_append_row(k.comp, k.L, k.P, k.w, k.eps, k.latent, k.krot, k.kc, k.pos.get(),
+                          k.table, red4);
+            return;
+        }
+    }
     __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
     const int64_t row0 = (int64_t)blockIdx.x * (16 * R) + wave * (4 * R) + g * R;
@@ -637,6 +649,106 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_mfma_i8(PlainArgs a) {
                 }
             }
     if (a.ks == 1 && a.am.v) argmax_parts_store<M>(a.am, bm, blockIdx.x);
+}
+
+// int8 weights, one activation row (digit planes), rows whose K is
+// split inside the workgroup instead of across workgroups: a workgroup
+// takes 4 output rows, lane group g (16 lanes) of wave w the quarter w of
+// row g's columns, every 256-column step of the quarter in flight at once
+// (K <= 8192, K % 1024 == 0).  Per lane the exact plane sums of its 16
+// columns per step, the lane total S = sum_p acc_p 256^p in int64, summed
+// over the 16 lanes and then over the four quarters: the exact integer
+// total of the row, so the output equals the split-K GEMV's bit for bit,
+// and the rows come out finished (no partials, no sum launch).  Rows
+// [0, O1) of w, [O1, O) of w2 (PlainArgs), activations a.x.dig, exponent
+// a.exps[0].
+constexpr int kRowSplitMaxSteps = 8;
+__global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_rowsplit(PlainArgs a) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
+    const int64_t row = (int64_t)blockIdx.x * 4 + g;
+    const uint8_t *wr = plain_row(a, row < a.O ? row : a.O - 1);
+    const int64_t kq = a.K / 4;
+    const int nst = (int)(kq / 256);
+    const int64_t c0 = (int64_t)wave * kq + 16 * s;
+    uint4 w[kRowSplitMaxSteps];
+#pragma unroll
+    for (int u = 0; u < kRowSplitMaxSteps; u++)
+        if (u < nst) w[u] = ld_weights(wr + c0 + 256 * u);
+    const int32_t e = a.exps[0];
+    int32_t acc[3] = {0, 0, 0};
+#pragma unroll
+    for (int u = 0; u < kRowSplitMaxSteps; u++) {
+        if (u >= nst) continue;
+        const int64_t wd = (c0 + 256 * u) / 4;
+#pragma unroll
+        for (int p = 0; p < 3; p++) {
+            const uint4 xv = ld_global<uint4>(a.x.dig + (int64_t)p * a.x.KW + wd);
+            int t = acc[p];
+            t = __builtin_amdgcn_sdot4((int)w[u].x, (int)xv.x, t, false);
+            t = __builtin_amdgcn_sdot4((int)w[u].y, (int)xv.y, t, false);
+            t = __builtin_amdgcn_sdot4((int)w[u].z, (int)xv.z, t, false);
+            t = __builtin_amdgcn_sdot4((int)w[u].w, (int)xv.w, t, false);
+            acc[p] = t;
+        }
+    }
+    int64_t t = ((int64_t)acc[2] * 256 + acc[1]) * 256 + acc[0];
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) t += shfl_xor_i64(t, off);
+    __shared__ int64_t part[4][4];
+    if (s == 0) part[wave][g] = t;
+    __syncthreads();
+    const int64_t r = (int64_t)blockIdx.x * 4 + tid;
+    if (tid < 4 && r < a.O) {
+        const int64_t S = part[0][tid] + part[1][tid] + part[2][tid] + part[3][tid];
+        const float v = int_total_to_f32(S, e, plain_scale(a, r));
+        float *o = plain_out(a, 0, r);
+        *o = a.accumulate ? __fadd_rn(*o, v) : v;
+    }
+}
+
+static bool fast_ok(const ut_qtensor *w);
+
+bool gemv_rowsplit_ok(const GemvArgs &ga) {
+    const ut_qtensor *w = ga.w;
+    if (!w || w->fmt != UT_FMT_INT8 || ga.M != 1 || ga.defer || ga.next || ga.xmax ||
+        ga.norm_w || ga.am_scratch || !ga.xd.dig8 || !fast_ok(w))
+        return false;
+    if (ga.w2 && (ga.w2->fmt != w->fmt || ga.w2->in_dim != w->in_dim ||
+                  ga.w2->row_bytes != w->row_bytes || !fast_ok(ga.w2)))
+        return false;
+    const int64_t K = w->in_dim;
+    return K % 1024 == 0 && K / 1024 <= kRowSplitMaxSteps && ((uintptr_t)ga.xd.dig8 & 15) == 0;
+}
+
+int32_t launch_gemv_rowsplit(ut_ctx *ctx, const GemvArgs &ga) {
+    if (!gemv_rowsplit_ok(ga)) {
+        set_error(ctx, "gemv_rowsplit: one row of an int8 weight with K %% 1024 == 0, K <= 8192");
+        return UT_ERR_ARG;
+    }
+    const ut_qtensor *w = ga.w, *w2 = ga.w2;
+    PlainArgs a{};
+    a.w = (const uint8_t *)w->payload;
+    a.scales = w->scales;
+    a.O1 = w->out_dim;
+    a.w2 = w2 ? (const uint8_t *)w2->payload : a.w;
+    a.scales2 = w2 ? w2->scales : a.scales;
+    a.O = w->out_dim + (w2 ? w2->out_dim : 0);
+    a.K = w->in_dim;
+    a.row_bytes = w->row_bytes;
+    a.out = ga.out;
+    a.ldo = ga.ldo;
+    a.out2 = w2 ? ga.out2 : a.out;
+    a.ldo2 = w2 ? ga.ldo2 : a.ldo;
+    a.accumulate = ga.accumulate;
+    a.x.dig = ga.xd.dig8;
+    a.x.KW = (w->in_dim + 3) / 4;
+    a.exps = ga.xd.exps;
+    a.ks = 1;
+    int tok = timing_begin(ctx, "gemv_int8_rowsplit");
+    hipLaunchKernelGGL(k_gemv_i8_rowsplit, dim3((unsigned)((a.O + 3) / 4)), dim3(kGemvThreads), 0,
+                       ctx->stream, a);
+    timing_end(ctx, tok);
+    return launch_check(ctx, "k_gemv_i8_rowsplit");
 }
 
 // The value of (m, row) from split-K partials [ks][M][O]: summed in z order
@@ -1106,6 +1218,10 @@ static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrow
     int tok = timing_begin(ctx, name);
     if constexpr (FMT != UT_FMT_F32) {
         if (ga.norm_w) {
+            if (ga.kv) {
+                a.kv = *ga.kv;
+                grid.x += 1;  // the kv append's workgroup
+            }
             hipLaunchKernelGGL((k_gemv<FMT, 1, true>), grid, dim3(kGemvThreads), 0, ctx->stream, a);
             timing_end(ctx, tok);
             return launch_check(ctx, name);

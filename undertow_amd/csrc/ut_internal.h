@@ -231,6 +231,19 @@ struct SplitKPartials {
     int64_t O = 0;
 };
 
+// A kv_a row's cache append (kv_append_row) run by one workgroup of
+// another launch: comp = the finished [L + P] row.
+struct KvAppendArgs {
+    const float *comp = nullptr;  // nullptr: none
+    int64_t L = 0, P = 0;
+    const float *w = nullptr;
+    float eps = 0.0f;
+    float *latent = nullptr, *krot = nullptr;
+    __bf16 *kc = nullptr;
+    PosRef pos;
+    const float2 *table = nullptr;
+};
+
 // A GEMV epilogue's argmax partials (ut_argmax.h): workgroup j of the
 // producing launch writes the best (value, row) of activation row m among
 // the output rows it finished to v[m * stride + j], i[m * stride + j].
@@ -277,8 +290,14 @@ struct GemvArgs {
     // the GEMV of that digitiser's digits bit for bit
     const float *norm_w = nullptr;
     float norm_eps = 0.0f;
+    // optional with norm_w: the launch also appends this kv_a row
+    const KvAppendArgs *kv = nullptr;
 };
 bool gemv_norm_ok(const ut_qtensor *w, int64_t M, const void *x, const void *norm_w);
+// One row of an int8 weight (or the w/w2 pair) with every row finished in
+// its workgroup (K split inside it): no partials.  Checks gemv_rowsplit_ok.
+bool gemv_rowsplit_ok(const GemvArgs &ga);
+int32_t launch_gemv_rowsplit(ut_ctx *ctx, const GemvArgs &ga);
 int32_t gemv(ut_ctx *ctx, const GemvArgs &a);
 // The kv_a / q_a pair GEMV's deferred split-K partials (kv_a rows first)
 // finished in one launch: q_a rows rms-normalised into qa_n and digitised

@@ -823,7 +823,45 @@ int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
     // outputs: q_a's norm + digits and kv_a's cache append
     const bool fused = pair && mla_pre_ok(rows, c.q_lora_rank, Lr, rope);
     SplitKPartials pp;
-    if (pair) {
+    // one row: the pair's rows finished in their workgroups (K split inside
+    // them), q_b normalising q_a while staging it and, in one more
+    // workgroup of its launch, the kv append -- no mla_pre launch
+    GemvArgs pa;
+    pa.w = L.kv_a;
+    pa.xf = x;
+    pa.xd = xd;
+    pa.M = rows;
+    pa.out = w.comp;
+    pa.ldo = Lr + rope;
+    pa.w2 = L.q_a;
+    pa.out2 = w.qa;
+    pa.ldo2 = c.q_lora_rank;
+    const bool rowsplit = fused && rows == 1 && gemv_rowsplit_ok(pa) &&
+                          gemv_norm_ok(L.q_b, 1, w.qa, L.q_a_norm);
+    if (rowsplit) {
+        UT_TRY(launch_gemv_rowsplit(ctx, pa));
+        KvAppendArgs kva;
+        kva.comp = w.comp;
+        kva.L = Lr;
+        kva.P = rope;
+        kva.w = L.kv_a_norm;
+        kva.eps = c.rms_norm_eps;
+        kva.latent = kv.latent;
+        kva.krot = kv.krot;
+        kva.kc = kv.kc;
+        kva.pos = pos_ref(ctx, pos_base);
+        kva.table = m->rope_table;
+        GemvArgs gq;
+        gq.w = L.q_b;
+        gq.M = 1;
+        gq.xf = w.qa;
+        gq.out = w.q;
+        gq.ldo = heads * qh;
+        gq.norm_w = L.q_a_norm;
+        gq.norm_eps = c.rms_norm_eps;
+        gq.kv = &kva;
+        UT_TRY(gemv(ctx, gq));
+    } else if (pair) {
         // kv_a and q_a read the same normed row: one launch for both
         GemvArgs ga;
         ga.w = L.kv_a;
@@ -842,9 +880,11 @@ int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
     }
     // one row: q_b normalises q_a itself while staging it (the same digits
     // as the row digitiser's), so mla_pre only sums q_a's partials
-    const bool qb_norm = fused && pp.ks > 1 && rows == 1 &&
+    const bool qb_norm = !rowsplit && fused && pp.ks > 1 && rows == 1 &&
                          gemv_norm_ok(L.q_b, 1, w.qa, L.q_a_norm);
-    if (qb_norm) {
+    if (rowsplit) {
+        // done above
+    } else if (qb_norm) {
         UT_TRY(launch_mla_pre(ctx, pp, Lr + rope, xd.exps, L.kv_a->scales, L.q_a->scales, rows,
                               c.q_lora_rank, L.q_a_norm, c.rms_norm_eps, nullptr, XDigits{}, 0, Lr,
                               rope, L.kv_a_norm, kv.latent, kv.krot, kv.kc, pos_base,
