@@ -465,11 +465,13 @@ template <int FMT, int M, bool NORM = false>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
     constexpr int R = plain_rows<M>();
     if constexpr (NORM) {
-        if (a.kv.comp && blockIdx.x == gridDim.x - 1) {
+        // the last M workgroups append the M kv_a rows (row m at pos + m)
+        if (a.kv.comp && (int)blockIdx.x >= (int)gridDim.x - M) {
             __shared__ double red4[4];
             const KvAppendArgs &k = a.kv;
-            kv_append_row(k.comp, k.L, k.P, k.w, k.eps, k.latent, k.krot, k.kc, k.pos.get(),
-                          k.table, red4);
+            const int m = (int)blockIdx.x - ((int)gridDim.x - M);
+            kv_append_row(k.comp + m * (k.L + k.P), k.L, k.P, k.w, k.eps, k.latent, k.krot, k.kc,
+                          k.pos.get() + m, k.table, red4);
             return;
         }
     }
@@ -513,8 +515,11 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
     auto prep = [&](int32_t (&shl)[4]) {
         if constexpr (FMT != UT_FMT_F32) {
             if (late) shifts(shl);
-            // normalised while staged: the staging found the row's shift
-            if constexpr (NORM) exl[0] = shl[0] == INT32_MIN ? INT32_MIN : -shl[0];
+            // normalised while staged: the staging found the rows' shifts
+            if constexpr (NORM)
+#pragma unroll
+                for (int m = 0; m < M; m++)
+                    exl[m] = shl[m] == INT32_MIN ? INT32_MIN : -shl[m];
         }
     };
     CoreOut<FMT, M, R> res;
@@ -651,7 +656,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_mfma_i8(PlainArgs a) {
     if (a.ks == 1 && a.am.v) argmax_parts_store<M>(a.am, bm, blockIdx.x);
 }
 
-// int8 weights, one activation row (digit planes), rows whose K is
+// int8 weights, M <= 4 activation rows (digit planes), rows whose K is
 // split inside the workgroup instead of across workgroups: a workgroup
 // takes 4 output rows, lane group g (16 lanes) of wave w the quarter w of
 // row g's columns, every 256-column step of the quarter in flight at once
@@ -660,9 +665,10 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_mfma_i8(PlainArgs a) {
 // over the 16 lanes and then over the four quarters: the exact integer
 // total of the row, so the output equals the split-K GEMV's bit for bit,
 // and the rows come out finished (no partials, no sum launch).  Rows
-// [0, O1) of w, [O1, O) of w2 (PlainArgs), activations a.x.dig, exponent
-// a.exps[0].
+// [0, O1) of w, [O1, O) of w2 (PlainArgs), activations a.x.dig, exponents
+// a.exps[m].
 constexpr int kRowSplitMaxSteps = 8;
+template <int M>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_rowsplit(PlainArgs a) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
     const int64_t row = (int64_t)blockIdx.x * 4 + g;
@@ -674,34 +680,41 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_rowsplit(PlainArgs a) 
 #pragma unroll
     for (int u = 0; u < kRowSplitMaxSteps; u++)
         if (u < nst) w[u] = ld_weights(wr + c0 + 256 * u);
-    const int32_t e = a.exps[0];
-    int32_t acc[3] = {0, 0, 0};
+    int32_t acc[M][3];
+#pragma unroll
+    for (int m = 0; m < M; m++) acc[m][0] = acc[m][1] = acc[m][2] = 0;
 #pragma unroll
     for (int u = 0; u < kRowSplitMaxSteps; u++) {
         if (u >= nst) continue;
         const int64_t wd = (c0 + 256 * u) / 4;
 #pragma unroll
-        for (int p = 0; p < 3; p++) {
-            const uint4 xv = ld_global<uint4>(a.x.dig + (int64_t)p * a.x.KW + wd);
-            int t = acc[p];
-            t = __builtin_amdgcn_sdot4((int)w[u].x, (int)xv.x, t, false);
-            t = __builtin_amdgcn_sdot4((int)w[u].y, (int)xv.y, t, false);
-            t = __builtin_amdgcn_sdot4((int)w[u].z, (int)xv.z, t, false);
-            t = __builtin_amdgcn_sdot4((int)w[u].w, (int)xv.w, t, false);
-            acc[p] = t;
-        }
-    }
-    int64_t t = ((int64_t)acc[2] * 256 + acc[1]) * 256 + acc[0];
+        for (int m = 0; m < M; m++)
 #pragma unroll
-    for (int off = 8; off >= 1; off >>= 1) t += shfl_xor_i64(t, off);
-    __shared__ int64_t part[4][4];
-    if (s == 0) part[wave][g] = t;
+            for (int p = 0; p < 3; p++) {
+                const uint4 xv = ld_global<uint4>(a.x.dig + (int64_t)(m * 3 + p) * a.x.KW + wd);
+                int t = acc[m][p];
+                t = __builtin_amdgcn_sdot4((int)w[u].x, (int)xv.x, t, false);
+                t = __builtin_amdgcn_sdot4((int)w[u].y, (int)xv.y, t, false);
+                t = __builtin_amdgcn_sdot4((int)w[u].z, (int)xv.z, t, false);
+                t = __builtin_amdgcn_sdot4((int)w[u].w, (int)xv.w, t, false);
+                acc[m][p] = t;
+            }
+    }
+    __shared__ int64_t part[4][4][M];
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+        int64_t t = ((int64_t)acc[m][2] * 256 + acc[m][1]) * 256 + acc[m][0];
+#pragma unroll
+        for (int off = 8; off >= 1; off >>= 1) t += shfl_xor_i64(t, off);
+        if (s == 0) part[wave][g][m] = t;
+    }
     __syncthreads();
-    const int64_t r = (int64_t)blockIdx.x * 4 + tid;
-    if (tid < 4 && r < a.O) {
-        const int64_t S = part[0][tid] + part[1][tid] + part[2][tid] + part[3][tid];
-        const float v = int_total_to_f32(S, e, plain_scale(a, r));
-        float *o = plain_out(a, 0, r);
+    const int gr = tid & 3, m = tid >> 2;
+    const int64_t r = (int64_t)blockIdx.x * 4 + gr;
+    if (m < M && r < a.O) {
+        const int64_t S = part[0][gr][m] + part[1][gr][m] + part[2][gr][m] + part[3][gr][m];
+        const float v = int_total_to_f32(S, a.exps[m], plain_scale(a, r));
+        float *o = plain_out(a, m, r);
         *o = a.accumulate ? __fadd_rn(*o, v) : v;
     }
 }
@@ -710,7 +723,7 @@ static bool fast_ok(const ut_qtensor *w);
 
 bool gemv_rowsplit_ok(const GemvArgs &ga) {
     const ut_qtensor *w = ga.w;
-    if (!w || w->fmt != UT_FMT_INT8 || ga.M != 1 || ga.defer || ga.next || ga.xmax ||
+    if (!w || w->fmt != UT_FMT_INT8 || ga.M < 1 || ga.M > 2 || ga.defer || ga.next || ga.xmax ||
         ga.norm_w || ga.am_scratch || !ga.xd.dig8 || !fast_ok(w))
         return false;
     if (ga.w2 && (ga.w2->fmt != w->fmt || ga.w2->in_dim != w->in_dim ||
@@ -722,7 +735,8 @@ bool gemv_rowsplit_ok(const GemvArgs &ga) {
 
 int32_t launch_gemv_rowsplit(ut_ctx *ctx, const GemvArgs &ga) {
     if (!gemv_rowsplit_ok(ga)) {
-        set_error(ctx, "gemv_rowsplit: one row of an int8 weight with K %% 1024 == 0, K <= 8192");
+        set_error(ctx, "gemv_rowsplit: one or two rows of an int8 weight with K %% 1024 == 0, "
+                       "K <= 8192");
         return UT_ERR_ARG;
     }
     const ut_qtensor *w = ga.w, *w2 = ga.w2;
@@ -745,8 +759,11 @@ int32_t launch_gemv_rowsplit(ut_ctx *ctx, const GemvArgs &ga) {
     a.exps = ga.xd.exps;
     a.ks = 1;
     int tok = timing_begin(ctx, "gemv_int8_rowsplit");
-    hipLaunchKernelGGL(k_gemv_i8_rowsplit, dim3((unsigned)((a.O + 3) / 4)), dim3(kGemvThreads), 0,
-                       ctx->stream, a);
+    const dim3 grid((unsigned)((a.O + 3) / 4));
+    if (ga.M == 1)
+        hipLaunchKernelGGL(k_gemv_i8_rowsplit<1>, grid, dim3(kGemvThreads), 0, ctx->stream, a);
+    else
+        hipLaunchKernelGGL(k_gemv_i8_rowsplit<2>, grid, dim3(kGemvThreads), 0, ctx->stream, a);
     timing_end(ctx, tok);
     return launch_check(ctx, "k_gemv_i8_rowsplit");
 }
@@ -904,14 +921,14 @@ __global__ __launch_bounds__(64) void k_gemv_generic(int32_t fmt, const uint8_t 
 static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 bool gemv_norm_ok(const ut_qtensor *w, int64_t M, const void *x, const void *norm_w) {
-    if (M != 1 || !w || (w->fmt != UT_FMT_INT8 && w->fmt != UT_FMT_INT4))
+    if (M < 1 || M > 2 || !w || (w->fmt != UT_FMT_INT8 && w->fmt != UT_FMT_INT4))
         return false;
     const int64_t K = w->in_dim;
     const int64_t kc = w->fmt == UT_FMT_INT8 ? gemv_chunk_cols<UT_FMT_INT8, 1, kGemvNormCols>()
                                              : gemv_chunk_cols<UT_FMT_INT4, 1, kGemvNormCols>();
     const int64_t step = w->fmt == UT_FMT_INT8 ? FmtTraits<UT_FMT_INT8>::kStepCols
                                                : FmtTraits<UT_FMT_INT4>::kStepCols;
-    return K <= kc && K % step == 0 && aligned16(x) && aligned16(norm_w) &&
+    return K <= kc && K % step == 0 && K % 4 == 0 && aligned16(x) && aligned16(norm_w) &&
            aligned16(w->payload) && w->row_bytes % 16 == 0;
 }
 
@@ -1147,8 +1164,8 @@ static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrow
         constexpr int PL = FmtTraits<FMT>::kPlanes;
         const int64_t KW = (w->in_dim + FmtTraits<FMT>::kColsPerWord - 1) / FmtTraits<FMT>::kColsPerWord;
         if (ga.norm_w) {
-            // one row, normalised and digitised while staged (gemv checked
-            // the shape: one chunk, no split)
+            // one or two rows, normalised and digitised while staged (gemv
+            // checked the shape: one chunk, no split)
             a.x.dig = nullptr;
             a.x.KW = KW;
             a.x.xf = ga.xf;
@@ -1220,9 +1237,12 @@ static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrow
         if (ga.norm_w) {
             if (ga.kv) {
                 a.kv = *ga.kv;
-                grid.x += 1;  // the kv append's workgroup
+                grid.x += (unsigned)mrows;  // the kv appends' workgroups
             }
-            hipLaunchKernelGGL((k_gemv<FMT, 1, true>), grid, dim3(kGemvThreads), 0, ctx->stream, a);
+            if (mrows == 1)
+                hipLaunchKernelGGL((k_gemv<FMT, 1, true>), grid, dim3(kGemvThreads), 0, ctx->stream, a);
+            else
+                hipLaunchKernelGGL((k_gemv<FMT, 2, true>), grid, dim3(kGemvThreads), 0, ctx->stream, a);
             timing_end(ctx, tok);
             return launch_check(ctx, name);
         }
@@ -1330,8 +1350,8 @@ int32_t gemv(ut_ctx *ctx, const GemvArgs &ga) {
         return UT_ERR_ARG;
     }
     if (ga.norm_w && (ga.w2 || ga.defer || ga.next || ga.xmax || !gemv_norm_ok(w, ga.M, ga.xf, ga.norm_w))) {
-        set_error(ctx, "gemv: normalise-while-staging takes one row of at most 8192 columns "
-                       "(a multiple of the step) of an int4/int8 weight, 16-byte aligned");
+        set_error(ctx, "gemv: normalise-while-staging takes one or two rows of at most 2048 "
+                       "columns (a multiple of the step) of an int4/int8 weight, 16-byte aligned");
         return UT_ERR_ARG;
     }
     if (fast_ok(w) && (w->fmt == UT_FMT_F32 ? aligned16(ga.xf) && (w->in_dim % 4 == 0) : true)) {

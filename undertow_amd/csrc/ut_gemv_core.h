@@ -91,8 +91,8 @@ struct XSrc {
     // bf16 activations [M][ldx] in place of xf (digitise-while-staging path
     // only): widened to f32 exactly as they are staged
     const uint16_t *xh = nullptr;
-    // gemv_core<..., NORM = true> (one row, int formats, one whole chunk
-    // from column 0): xf is rms-normalised with these weights (eps neps)
+    // gemv_core<..., NORM = true> (int formats, one whole chunk from column
+    // 0): each row of xf is rms-normalised with these weights (eps neps)
     // while staged, by the row digitiser's rule and reduction order, and the
     // normalised row is digitised with its own exponent (reported through
     // prep)
@@ -306,18 +306,18 @@ struct NoMid {
 
 template <typename T, typename Op> __device__ __forceinline__ T wave_reduce_dpp(T v, Op op);
 
-// The normalising branch of gemv_stage_once (x.nw set, one row): thread t
-// holds the 8-column groups t + 256 j of the row.  The mean of squares is
-// taken in the row digitiser's order (rowdig_body with one group per
-// thread): each group's squares summed in f64 in column order, the groups
-// of a 64-lane wave by the DPP butterfly, the wave sums in wave order
-// (group c is lane c % 64 of wave c / 64 there, and lane t % 64 of wave
-// t / 64 + 4j here, so the sums are the same), then
-// r = 1/sqrt((float)(sum / K) + eps), v = (x * r) * w, the exponent from
-// max|v|, and v's digit words into the LDS planes.  Returns the shift.
-template <int FMT, int KC, typename Issue>
-__device__ __forceinline__ int32_t gemv_stage_norm(const XSrc &x, uint32_t *lds, int kcn,
-                                                   Issue &&issue) {
+// The normalising branch of gemv_stage_once (NORM: M <= 4 rows of x.xf,
+// row stride x.ldx): thread t holds the 8-column groups t + 256 j of each
+// row.  Each row's mean of squares is taken in the row digitiser's order
+// (rowdig_body with one group per thread): each group's squares summed in
+// f64 in column order, the groups of a 64-lane wave by the DPP butterfly,
+// the wave sums in wave order (group c is lane c % 64 of wave c / 64 there,
+// and lane t % 64 of wave t / 64 + 4j here, so the sums are the same), then
+// r = 1/sqrt((float)(sum / K) + eps), v = (x * r) * w, the row's exponent
+// from max|v|, and v's digit words into the LDS planes.  sh: the shifts.
+template <int FMT, int M, int KC, typename Issue>
+__device__ __forceinline__ void gemv_stage_norm(const XSrc &x, uint32_t *lds, int kcn,
+                                                Issue &&issue, int32_t (&sh)[4]) {
     using T = FmtTraits<FMT>;
     constexpr int PL = T::kPlanes;
     constexpr int LW = KC / T::kColsPerWord;
@@ -325,71 +325,86 @@ __device__ __forceinline__ int32_t gemv_stage_norm(const XSrc &x, uint32_t *lds,
     static_assert(4 * GMAX <= 16, "at most 16 virtual waves");
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int NG = kcn / 8;
-    float v[GMAX][8], wv[GMAX][8];
+    float v[M][GMAX][8], wv[GMAX][8];
 #pragma unroll
     for (int j = 0; j < GMAX; j++) {
         const int c = tid + j * kGemvThreads, cc = c < NG ? c : NG - 1;
-        const float4 a = ld_global<float4>(x.xf + 8 * cc), b = ld_global<float4>(x.xf + 8 * cc + 4);
-        const float4 p = ld_global<float4>(x.nw + 8 * cc), q = ld_global<float4>(x.nw + 8 * cc + 4);
         const bool in = c < NG;
-        v[j][0] = in ? a.x : 0.0f; v[j][1] = in ? a.y : 0.0f; v[j][2] = in ? a.z : 0.0f; v[j][3] = in ? a.w : 0.0f;
-        v[j][4] = in ? b.x : 0.0f; v[j][5] = in ? b.y : 0.0f; v[j][6] = in ? b.z : 0.0f; v[j][7] = in ? b.w : 0.0f;
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            const float *xr = x.xf + m * x.ldx + 8 * cc;
+            const float4 a = ld_global<float4>(xr), b = ld_global<float4>(xr + 4);
+            v[m][j][0] = in ? a.x : 0.0f; v[m][j][1] = in ? a.y : 0.0f;
+            v[m][j][2] = in ? a.z : 0.0f; v[m][j][3] = in ? a.w : 0.0f;
+            v[m][j][4] = in ? b.x : 0.0f; v[m][j][5] = in ? b.y : 0.0f;
+            v[m][j][6] = in ? b.z : 0.0f; v[m][j][7] = in ? b.w : 0.0f;
+        }
+        const float4 p = ld_global<float4>(x.nw + 8 * cc), q = ld_global<float4>(x.nw + 8 * cc + 4);
         wv[j][0] = p.x; wv[j][1] = p.y; wv[j][2] = p.z; wv[j][3] = p.w;
         wv[j][4] = q.x; wv[j][5] = q.y; wv[j][6] = q.z; wv[j][7] = q.w;
     }
     issue();
     __builtin_amdgcn_sched_barrier(0);
-    __shared__ double redd[16];
-    __shared__ uint32_t redu[4];
+    __shared__ double redd[M][16];
+    __shared__ uint32_t redu[M][4];
 #pragma unroll
-    for (int j = 0; j < GMAX; j++) {
-        double acc = 0.0;
+    for (int m = 0; m < M; m++)
 #pragma unroll
-        for (int q = 0; q < 8; q++) acc += (double)v[j][q] * (double)v[j][q];
-        acc = wave_reduce_dpp(acc, [](double p, double q) { return p + q; });
-        if (lane == 0) redd[wave + 4 * j] = acc;
-    }
-    for (int i = 4 * GMAX + tid; i < 16; i += kGemvThreads) redd[i] = 0.0;
+        for (int j = 0; j < GMAX; j++) {
+            double acc = 0.0;
+#pragma unroll
+            for (int q = 0; q < 8; q++) acc += (double)v[m][j][q] * (double)v[m][j][q];
+            acc = wave_reduce_dpp(acc, [](double p, double q) { return p + q; });
+            if (lane == 0) redd[m][wave + 4 * j] = acc;
+        }
+    for (int i = tid; i < M * 16; i += kGemvThreads)
+        if (i % 16 >= 4 * GMAX) redd[i / 16][i % 16] = 0.0;
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    double ss = redd[0];
-    for (int i = 1; i < 16; i++) ss += redd[i];
-    const float r = 1.0f / sqrtf(__fadd_rn((float)(ss / (double)kcn), x.neps));
-    uint32_t mx = 0;
 #pragma unroll
-    for (int j = 0; j < GMAX; j++) {
-        const bool in = tid + j * kGemvThreads < NG;
+    for (int m = 0; m < M; m++) {
+        double ss = redd[m][0];
+        for (int i = 1; i < 16; i++) ss += redd[m][i];
+        const float r = 1.0f / sqrtf(__fadd_rn((float)(ss / (double)kcn), x.neps));
+        uint32_t mx = 0;
 #pragma unroll
-        for (int q = 0; q < 8; q++) {
-            v[j][q] = __fmul_rn(__fmul_rn(v[j][q], r), wv[j][q]);
-            if (in) mx = max(mx, __float_as_uint(fabsf(v[j][q])));
+        for (int j = 0; j < GMAX; j++) {
+            const bool in = tid + j * kGemvThreads < NG;
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                v[m][j][q] = __fmul_rn(__fmul_rn(v[m][j][q], r), wv[j][q]);
+                if (in) mx = max(mx, __float_as_uint(fabsf(v[m][j][q])));
+            }
+        }
+        mx = wave_reduce_dpp(mx, [](uint32_t p, uint32_t q) { return p > q ? p : q; });
+        if (lane == 0) redu[m][wave] = mx;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+        const uint32_t mx = max(max(redu[m][0], redu[m][1]), max(redu[m][2], redu[m][3]));
+        const bool bad = mx >= 0x7f800000u;
+        int E = 0;
+        if (!bad && mx != 0) (void)frexpf(__uint_as_float(mx), &E);
+        sh[m] = bad ? INT32_MIN : 22 - E;
+#pragma unroll
+        for (int j = 0; j < GMAX; j++) {
+            const int c = tid + j * kGemvThreads;
+            if (c >= NG) continue;
+            if constexpr (FMT == UT_FMT_INT4) {
+                uint32_t w[PL];
+                digit_words<UT_FMT_INT4>(v[m][j], 8, sh[m], w);
+#pragma unroll
+                for (int p = 0; p < PL; p++) lds[(m * PL + p) * LW + c] = w[p];
+            } else {
+                uint32_t w[PL], w2[PL];
+                digit_words<UT_FMT_INT8>(v[m][j], 4, sh[m], w);
+                digit_words<UT_FMT_INT8>(v[m][j] + 4, 4, sh[m], w2);
+#pragma unroll
+                for (int p = 0; p < PL; p++)
+                    *(uint2 *)(lds + (m * PL + p) * LW + 2 * c) = make_uint2(w[p], w2[p]);
+            }
         }
     }
-    mx = wave_reduce_dpp(mx, [](uint32_t p, uint32_t q) { return p > q ? p : q; });
-    if (lane == 0) redu[wave] = mx;
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    mx = max(max(redu[0], redu[1]), max(redu[2], redu[3]));
-    const bool bad = mx >= 0x7f800000u;
-    int E = 0;
-    if (!bad && mx != 0) (void)frexpf(__uint_as_float(mx), &E);
-    const int32_t sh = bad ? INT32_MIN : 22 - E;
-#pragma unroll
-    for (int j = 0; j < GMAX; j++) {
-        const int c = tid + j * kGemvThreads;
-        if (c >= NG) continue;
-        if constexpr (FMT == UT_FMT_INT4) {
-            uint32_t w[PL];
-            digit_words<UT_FMT_INT4>(v[j], 8, sh, w);
-#pragma unroll
-            for (int p = 0; p < PL; p++) lds[p * LW + c] = w[p];
-        } else {
-            uint32_t w[PL], w2[PL];
-            digit_words<UT_FMT_INT8>(v[j], 4, sh, w);
-            digit_words<UT_FMT_INT8>(v[j] + 4, 4, sh, w2);
-#pragma unroll
-            for (int p = 0; p < PL; p++) *(uint2 *)(lds + p * LW + 2 * c) = make_uint2(w[p], w2[p]);
-        }
-    }
-    return sh;
 }
 
 template <int FMT, int M, int KC, bool NORM = false, typename Issue, typename Prep = NoPrep>
@@ -403,8 +418,9 @@ __device__ __forceinline__ void gemv_stage_once(const XSrc &x, uint32_t *lds, in
     // a separate instantiation: its registers would lower every other
     // kernel's occupancy
     if constexpr (NORM) {
-        static_assert(FMT != UT_FMT_F32 && M == 1, "normalising staging: one row, int formats");
-        int32_t shl[4] = {gemv_stage_norm<FMT, KC>(x, lds, kcn, issue), 0, 0, 0};
+        static_assert(FMT != UT_FMT_F32, "normalising staging: int formats");
+        int32_t shl[4] = {0, 0, 0, 0};
+        gemv_stage_norm<FMT, M, KC>(x, lds, kcn, issue, shl);
         prep(shl);
         __syncthreads();
         return;

@@ -823,9 +823,9 @@ int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
     // outputs: q_a's norm + digits and kv_a's cache append
     const bool fused = pair && mla_pre_ok(rows, c.q_lora_rank, Lr, rope);
     SplitKPartials pp;
-    // one row: the pair's rows finished in their workgroups (K split inside
-    // them), q_b normalising q_a while staging it and, in one more
-    // workgroup of its launch, the kv append -- no mla_pre launch
+    // one or two rows: the pair's rows finished in their workgroups (K split
+    // inside them), q_b normalising q_a while staging it and, in one more
+    // workgroup per row of its launch, the kv appends -- no mla_pre launch
     GemvArgs pa;
     pa.w = L.kv_a;
     pa.xf = x;
@@ -836,8 +836,8 @@ int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
     pa.w2 = L.q_a;
     pa.out2 = w.qa;
     pa.ldo2 = c.q_lora_rank;
-    const bool rowsplit = fused && rows == 1 && gemv_rowsplit_ok(pa) &&
-                          gemv_norm_ok(L.q_b, 1, w.qa, L.q_a_norm);
+    const bool rowsplit = fused && rows <= 2 && gemv_rowsplit_ok(pa) &&
+                          gemv_norm_ok(L.q_b, rows, w.qa, L.q_a_norm);
     if (rowsplit) {
         UT_TRY(launch_gemv_rowsplit(ctx, pa));
         KvAppendArgs kva;
@@ -853,7 +853,7 @@ int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
         kva.table = m->rope_table;
         GemvArgs gq;
         gq.w = L.q_b;
-        gq.M = 1;
+        gq.M = rows;
         gq.xf = w.qa;
         gq.out = w.q;
         gq.ldo = heads * qh;
