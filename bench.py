@@ -467,12 +467,17 @@ def model_roofline(m, cfg, prompt, new_tokens, greedy_tok_s, steps=16):
     s = m.session()
     s.prefill(prompt, want_logits=False)
     nxt = s.last_argmax[-1]
+    # verify rows are distinct tokens, as a verify step's drafts are (a
+    # repeated token would route every row to the same experts)
+    rng = np.random.default_rng(7)
     for rows in (2, 4):
-        s.prefill([nxt] * rows, want_logits=False)  # warm-up of this shape
+        s.prefill([nxt] + rng.integers(0, cfg["vocab_size"], rows - 1).tolist(),
+                  want_logits=False)  # warm-up of this shape
         nxt = s.last_argmax[-1]
         t0 = time.perf_counter()
         for _ in range(steps):
-            s.prefill([nxt] * rows, want_logits=False)
+            s.prefill([nxt] + rng.integers(0, cfg["vocab_size"], rows - 1).tolist(),
+                      want_logits=False)
             nxt = s.last_argmax[-1]
         us = (time.perf_counter() - t0) / steps * 1e6
         T = s.position
@@ -820,7 +825,9 @@ def profile_decode(cfg_name: str, prompt_len: int, tokens: int, seed: int = 42,
         time.sleep(1.0)
         t0 = time.perf_counter()
         for _ in range(n):
-            s.prefill([nxt] * rows, want_logits=False)
+            # distinct tokens per row, as a verify step's drafts are
+            s.prefill([nxt] + rng.integers(0, cfg["vocab_size"], rows - 1).tolist(),
+                      want_logits=False)
             nxt = s.last_argmax[-1]
         t1 = time.perf_counter()
         print(f"verify ({rows} rows) {n} steps: {(t1 - t0) / n * 1e3:.3f} ms/step", flush=True)

@@ -952,10 +952,17 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up(GateUpArgs a) {
 // staged chunk, so TW = 2 halves the activation staging per weight byte.
 template <int M> constexpr int gate_up_mfma_kc() { return M == 2 ? 4096 : 2048; }
 // Tiles per wave: two when the routed experts have the launch to
-// themselves; beside a shared MLP (whose 16-row tiles set the grid) one, so
-// that the routed workgroups stay many enough to spread evenly over the CUs
-// (two made the four-row launch 61.9 -> 73.1 us at DeepSeek-V3 width).
+// themselves; in the 2-D grid beside a shared MLP (whose 16-row tiles set
+// the grid) one.
 template <int M, bool DUAL> constexpr int gate_up_mfma_tw() { return !DUAL && M >= 2 ? 2 : 1; }
+// Tiles per wave of the routed experts beside a shared MLP on the flat grid
+// (k_moe_gate_up_mfma_dual_flat): two.  With verify rows of distinct tokens
+// (about 15 unique experts at two rows, 28 at four) the config-4 launch
+// took 52.9 -> 48.0 us at two rows and 87.5 -> 78.8 us at four against one
+// tile per wave (one on the flat grid: 52.5 / 86.5 us).
+#ifndef UT_GATE_UP_DUAL_TW
+#define UT_GATE_UP_DUAL_TW 2
+#endif
 template <int M, bool DUAL> constexpr int gate_up_mfma_rows() { return 32 * gate_up_mfma_tw<M, DUAL>(); }
 // LDS of the matrix-core gate/up: the staged x chunk, then each wave's
 // weight-transpose area
@@ -1131,6 +1138,23 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up_mfma_dual(GateUpAr
     } else {
         gate_up_body<FB, M, false>(b, 0, blockIdx.x, lds, wg_max);
     }
+}
+
+// The same pair of passes on a flat grid: gxm tiles of 32 * TW rows per
+// routed slot (slot-major, nrouted workgroups), then the shared MLP's
+// 16-row tiles, so no workgroup of the grid is empty when the routed tiles
+// are fewer than the shared MLP's.
+template <int M, int FB, int TW>
+__global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up_mfma_dual_flat(GateUpArgs a,
+                                                                             GateUpArgs b, int gxm,
+                                                                             int nrouted) {
+    __shared__ __attribute__((aligned(16)))
+    uint32_t lds[cmax_words(mfma_lds_words<M, gate_up_mfma_kc<M>()>() + TW * kI4WaveAreaBytes,
+                            kLdsWords)];
+    __shared__ uint32_t wg_max[4];
+    const int i = blockIdx.x;
+    if (i < nrouted) gate_up_mfma_body<M, TW>(a, i / gxm, i % gxm, lds, wg_max);
+    else gate_up_body<FB, M, false>(b, 0, i - nrouted, lds, wg_max);
 }
 
 // Routed experts (format FA, slots 0..gridDim.y-2) and one shared MLP
@@ -1748,16 +1772,19 @@ static void launch_gate_up(ut_ctx *ctx, const GateUpArgs &a, int64_t slots, cons
                                    dim3(kGemvThreads), 0, ctx->stream, a);
                 return;
             }
-            // a shared MLP beside it: the last grid row
-            constexpr int R = gate_up_mfma_rows<M, true>();
-            const unsigned gx = (unsigned)((a.I + R - 1) / R);
-            const dim3 grid(gx > (unsigned)b->ntiles ? gx : (unsigned)b->ntiles, (unsigned)(slots + 1));
+            // a shared MLP beside it: a flat grid, the routed slots' tiles
+            // (UT_GATE_UP_DUAL_TW per wave) and then the shared MLP's
+            constexpr int TW = UT_GATE_UP_DUAL_TW;
+            constexpr int R = 32 * TW;
+            const int gxm = (int)((a.I + R - 1) / R);
+            const int nrouted = gxm * (int)slots;
+            const dim3 grid((unsigned)(nrouted + b->ntiles));
             if (fb == UT_FMT_INT4)
-                hipLaunchKernelGGL((k_moe_gate_up_mfma_dual<M, UT_FMT_INT4>), grid,
-                                   dim3(kGemvThreads), 0, ctx->stream, a, *b);
+                hipLaunchKernelGGL((k_moe_gate_up_mfma_dual_flat<M, UT_FMT_INT4, TW>), grid,
+                                   dim3(kGemvThreads), 0, ctx->stream, a, *b, gxm, nrouted);
             else
-                hipLaunchKernelGGL((k_moe_gate_up_mfma_dual<M, UT_FMT_INT8>), grid,
-                                   dim3(kGemvThreads), 0, ctx->stream, a, *b);
+                hipLaunchKernelGGL((k_moe_gate_up_mfma_dual_flat<M, UT_FMT_INT8, TW>), grid,
+                                   dim3(kGemvThreads), 0, ctx->stream, a, *b, gxm, nrouted);
             return;
         }
     }
