@@ -443,16 +443,21 @@ constexpr int kMlaMaxSlices = 256;
 // holds four adjacent columns of dim dy (16-byte loads) for one sixteenth
 // of the slices.  The sixteen part sums are added in part order through
 // LDS, so every output's sum has a fixed order.
+// MAXS: the most slices the instantiation takes (the register arrays are
+// sized for it; with 64, two workgroups fit a CU instead of one).  Any
+// MAXS >= the rows' slice count runs the same operations in the same order.
 constexpr int kCombineParts = 16;
-constexpr int kCombineStat = kMlaMaxSlices / 32;                          // m, l per thread
-constexpr int kCombineSlices = (kMlaMaxSlices + kCombineParts - 1) / kCombineParts;  // per part
+constexpr int kCombineSmallSlices = 64;
 
+template <int MAXS>
 __global__ __launch_bounds__(1024) void k_mla_combine_mfma(const float *__restrict__ part_m,
                                                            const float *__restrict__ part_l,
                                                            const float *__restrict__ part_o,
                                                            int RH, int H, int L, PosRef pos,
                                                            float *__restrict__ clat) {
-    __shared__ __attribute__((aligned(16))) float sw[kMlaMaxSlices][32];
+    constexpr int kCombineStat = MAXS / 32;                                     // m, l per thread
+    constexpr int kCombineSlices = (MAXS + kCombineParts - 1) / kCombineParts;  // per part
+    __shared__ __attribute__((aligned(16))) float sw[MAXS][32];
     __shared__ float red[32][33];
     __shared__ float sM[32], sInv[32];
     __shared__ __attribute__((aligned(16))) float sq[kCombineParts][8][32];
@@ -614,9 +619,18 @@ int32_t launch_mla_attend_kc(ut_ctx *ctx, const float *qabs, const float *qrope,
     timing_end(ctx, tok);
     UT_TRY(launch_check(ctx, "k_mla_mfma"));
     tok = timing_begin(ctx, "mla_combine");
-    hipLaunchKernelGGL(k_mla_combine_mfma, dim3((unsigned)(RH / 32), (unsigned)(L / 8)),
-                       dim3(1024), 0, ctx->stream, a.part_m, a.part_l, a.part_o,
-                       (int)RH, (int)H, (int)L, a.pos, clat);
+    const dim3 cgrid((unsigned)(RH / 32), (unsigned)(L / 8));
+    if (a.nslice <= kCombineSmallSlices)
+        hipLaunchKernelGGL(k_mla_combine_mfma<kCombineSmallSlices>, cgrid, dim3(1024), 0,
+                           ctx->stream, a.part_m, a.part_l, a.part_o, (int)RH, (int)H, (int)L,
+                           a.pos, clat);
+    else if (a.nslice <= 2 * kCombineSmallSlices)
+        hipLaunchKernelGGL(k_mla_combine_mfma<2 * kCombineSmallSlices>, cgrid, dim3(1024), 0,
+                           ctx->stream, a.part_m, a.part_l, a.part_o, (int)RH, (int)H, (int)L,
+                           a.pos, clat);
+    else
+        hipLaunchKernelGGL(k_mla_combine_mfma<kMlaMaxSlices>, cgrid, dim3(1024), 0, ctx->stream,
+                           a.part_m, a.part_l, a.part_o, (int)RH, (int)H, (int)L, a.pos, clat);
     timing_end(ctx, tok);
     return launch_check(ctx, "k_mla_combine_mfma");
 }
