@@ -539,7 +539,11 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
     // the normalising staging holds its row's groups in registers: rows of
     // at most kGemvNormCols columns (one group per thread)
     constexpr int KC = NORM ? gemv_chunk_cols<FMT, M, kGemvNormCols>() : gemv_chunk_cols<FMT, M>();
-    gemv_core<FMT, M, R, plain_depth<M>(), KC, false, decltype(prep) &, NoMid, NORM>(
+    // one normalised row is short: six steps in flight (all of a 1,536-column
+    // int8 row, the q_a width: q_b 11.3 -> 10.9 us at config 4; at two rows
+    // six made it 12.7 -> 14.0 us)
+    constexpr int DEPTH = NORM && M == 1 ? 6 : plain_depth<M>();
+    gemv_core<FMT, M, R, DEPTH, KC, false, decltype(prep) &, NoMid, NORM>(
         rows, a.K, xs, lds, res, 0, -1, prep);
     Best bm[M];
 #pragma unroll
