@@ -405,7 +405,9 @@ def cpu_baseline(cfg2, seconds=10.0):
     from undertow_amd.configs import C1, C4
     legs["c1"] = cpu_baseline_model("c1", C1, 16, 64, (1,))
     log(f"CPU config 1: {json.dumps(legs['c1'])}")
-    legs["c4"] = cpu_baseline_model("c4", C4, 32, 8, (1,), experts=32)
+    # the GPU leg's prompt length (so attention reads the same context); 32
+    # tokens keep the leg near ten seconds of host time
+    legs["c4"] = cpu_baseline_model("c4", C4, 512, 32, (1,), experts=32)
     log(f"CPU config 4: {json.dumps(legs['c4'])}")
     head["legs"] = legs
     return head
