@@ -194,6 +194,71 @@ __global__ __launch_bounds__(1024) void k_rowdig_reg(RowDigArgs a) {
 
 constexpr int64_t kRowRegCols = 4 * 8 * 1024;  // widest row the register kernel takes
 
+// The embedding lookup and the first layer's input norm in one launch: row
+// m's values are k_embed's (0 + (1 * scale[id]) * q, the reference's
+// add_scaled_row into zeros), formed in the registers of the thread that
+// owns their 8-column group, then the row digitiser's body, which also
+// stores the looked-up row to a.raw (the residual stream).
+__global__ __launch_bounds__(1024) void k_rowdig_emb(RowDigArgs a, int32_t fmt,
+                                                     const uint8_t *__restrict__ payload,
+                                                     const float *__restrict__ scales,
+                                                     int64_t row_bytes,
+                                                     const int32_t *__restrict__ ids) {
+    __shared__ double redd[16];
+    __shared__ uint32_t redu[16];
+    const int64_t m = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int64_t NG = a.K / 8, c = tid;
+    const int64_t id = ids[m];
+    const uint8_t *row = payload + id * row_bytes;
+    const float f = fmt == UT_FMT_F32 ? 1.0f : __fmul_rn(1.0f, scales[id]);
+    float v[1][8], wv[1][8];
+    if (c < NG) {
+        const float4 w0 = *(const float4 *)(a.norm_w + 8 * c), w1 = *(const float4 *)(a.norm_w + 8 * c + 4);
+        wv[0][0] = w0.x; wv[0][1] = w0.y; wv[0][2] = w0.z; wv[0][3] = w0.w;
+        wv[0][4] = w1.x; wv[0][5] = w1.y; wv[0][6] = w1.z; wv[0][7] = w1.w;
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[0][j] = __fadd_rn(0.0f, __fmul_rn(f, code_at(fmt, row, 8 * c + j)));
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[0][j] = 0.0f, wv[0][j] = 0.0f;
+    }
+    rowdig_body<1, true>(a, m, v, wv, redd, redu);
+}
+
+bool embed_norm_ok(const ut_qtensor *emb, int64_t K, const float *x, const float *norm_w) {
+    return K % 8 == 0 && K <= 8 * 1024 && emb->in_dim == K && ((uintptr_t)x & 15) == 0 &&
+           ((uintptr_t)norm_w & 15) == 0;
+}
+
+int32_t launch_embed_norm(ut_ctx *ctx, const ut_qtensor *emb, const int32_t *ids, int64_t rows,
+                          float *x, int64_t ldx, const NormNext &nx) {
+    const int64_t K = emb->in_dim;
+    if (!embed_norm_ok(emb, K, x, nx.norm_w) || ldx % 4 != 0) {
+        set_error(ctx, "embed_norm: rows of a multiple of 8 columns, at most 8192, 16-byte aligned");
+        return UT_ERR_ARG;
+    }
+    if (rows <= 0) return UT_OK;
+    RowDigArgs a{};
+    a.K = K;
+    a.norm_w = nx.norm_w;
+    a.eps = nx.eps;
+    a.out = nx.normed;
+    a.ldo = nx.ldn;
+    a.exps = nx.nd.exps;
+    a.dig4 = (nx.flags & XD_DIG4) ? nx.nd.dig4 : nullptr;
+    a.dig8 = (nx.flags & XD_DIG8) ? nx.nd.dig8 : nullptr;
+    a.xt = (nx.flags & XD_XT) ? nx.nd.xt : nullptr;
+    a.raw = x;
+    a.ldr = ldx;
+    const unsigned threads = (unsigned)((K / 8 + 63) / 64 * 64);
+    int tok = timing_begin(ctx, "embed_norm");
+    hipLaunchKernelGGL(k_rowdig_emb, dim3((unsigned)rows), dim3(threads), 0, ctx->stream, a,
+                       emb->fmt, (const uint8_t *)emb->payload, emb->scales, emb->row_bytes, ids);
+    timing_end(ctx, tok);
+    return launch_check(ctx, "k_rowdig_emb");
+}
+
 // After the kv_a / q_a pair GEMV's split-K pass (kv_a rows first, then
 // q_a): workgroup m < M sums row m's q_a partials, rms-normalises and
 // digitises them for q_b (the row digitiser's body); workgroup M + m sums
@@ -1047,6 +1112,9 @@ static int32_t splitk_finish(ut_ctx *ctx, const GemvArgs &ga, const PlainArgs &a
         nd.dig8 = (nx.flags & XD_DIG8) ? nx.nd.dig8 : nullptr;
         nd.xt = (nx.flags & XD_XT) ? nx.nd.xt : nullptr;
         nd.raw = a.out;
+        nd.raw2 = nx.raw2;
+        nd.ldr2 = nx.ld2;
+        nd.pos2 = nx.pos2;
         nd.ldr = a.ldo;
         const unsigned threads = (unsigned)((a.O / 8 + 63) / 64 * 64);
         hipLaunchKernelGGL(k_splitk_sum_norm<FMT>, dim3((unsigned)mrows), dim3(threads), 0,

@@ -294,6 +294,13 @@ struct GemvArgs {
     const KvAppendArgs *kv = nullptr;
 };
 bool gemv_norm_ok(const ut_qtensor *w, int64_t M, const void *x, const void *norm_w);
+// The embedding lookup (launch_embed) and the norm that follows it
+// (rmsnorm + digits as NormNext asks) in one launch; x gets the looked-up
+// rows.  embed_norm_ok: rows of K % 8 == 0 columns, K <= 8192, aligned.
+struct NormNext;
+bool embed_norm_ok(const ut_qtensor *emb, int64_t K, const float *x, const float *norm_w);
+int32_t launch_embed_norm(ut_ctx *ctx, const ut_qtensor *emb, const int32_t *ids, int64_t rows,
+                          float *x, int64_t ldx, const NormNext &nx);
 // One row of an int8 weight (or the w/w2 pair) with every row finished in
 // its workgroup (K split inside it): no partials.  Checks gemv_rowsplit_ok.
 bool gemv_rowsplit_ok(const GemvArgs &ga);

@@ -1080,12 +1080,20 @@ int32_t prefill_dev(ut_session *s, const int32_t *ids, int64_t n, const int32_t 
     Workspace &w = s->ws;
     const int64_t H = c.hidden_size, V = c.vocab_size;
     if (!ids_dev) UT_TRY(upload_ids(s, ids, n));
-    UT_TRY(launch_embed(ctx, m->embed, ids_dev ? ids_dev : w.ids, n, w.x, H));
     // each layer's last combine runs the norm that follows it when the rows
-    // fit one combine (decode and verify steps)
+    // fit one combine (decode and verify steps); the first layer's input
+    // norm then runs in the embedding lookup's launch
     const bool fuse = fuse_next_ok(s, n);
     XDigits cur, nxt;
     const size_t nl = m->layers.size();
+    const bool emb_norm = fuse && nl > 0 && embed_norm_ok(m->embed, H, w.x, m->layers[0].input_norm);
+    if (emb_norm) {
+        const NormNext n0 = next_norm(s, m->layers[0].input_norm, input_flags(m->layers[0]), n,
+                                      &cur, input_f32(m->layers[0]));
+        UT_TRY(launch_embed_norm(ctx, m->embed, ids_dev ? ids_dev : w.ids, n, w.x, H, n0));
+    } else {
+        UT_TRY(launch_embed(ctx, m->embed, ids_dev ? ids_dev : w.ids, n, w.x, H));
+    }
     for (size_t li = 0; li < nl; li++) {
         NormNext nx;
         if (fuse)
@@ -1094,11 +1102,17 @@ int32_t prefill_dev(ut_session *s, const int32_t *ids, int64_t n, const int32_t 
                                          input_f32(m->layers[li + 1]))
                              : next_norm(s, m->final_norm, dig_flags({m->lm_head}), n, &nxt,
                                          f32_reader({m->lm_head}));
-        UT_TRY(run_layer(s, m->layers[li], w.x, n, s->kv[li], fuse && li > 0 ? &cur : nullptr,
-                         fuse ? &nx : nullptr));
+        if (fuse && li + 1 == nl && m->has_mtp) {
+            // the last combine also keeps the finished rows for the MTP head
+            nx.raw2 = s->hidden;
+            nx.ld2 = H;
+            nx.pos2 = pos_ref(ctx, s->pos);
+        }
+        UT_TRY(run_layer(s, m->layers[li], w.x, n, s->kv[li],
+                         fuse && (li > 0 || emb_norm) ? &cur : nullptr, fuse ? &nx : nullptr));
         cur = nxt;
     }
-    if (m->has_mtp) UT_TRY(launch_copy_rows_at(ctx, s->hidden, H, s->pos, w.x, n, H));
+    if (m->has_mtp && !(fuse && nl > 0)) UT_TRY(launch_copy_rows_at(ctx, s->hidden, H, s->pos, w.x, n, H));
     s->pos += n;
     if (!ids_dev) s->tokens.insert(s->tokens.end(), ids, ids + n);
     XDigits fd = cur;

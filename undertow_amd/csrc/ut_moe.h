@@ -43,6 +43,11 @@ struct NormNext {
     int64_t ldn = 0;
     XDigits nd;
     int flags = 0;
+    // optional: the finished (un-normalised) rows also go to raw2 at rows
+    // pos2, pos2 + 1, ... (stride ld2): the MTP head's hidden-state rows
+    float *raw2 = nullptr;
+    int64_t ld2 = 0;
+    PosRef pos2;
 };
 
 struct MoeCall {

@@ -2108,6 +2108,9 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
         nd.dig8 = (nx.flags & XD_DIG8) ? nx.nd.dig8 : nullptr;
         nd.xt = (nx.flags & XD_XT) ? nx.nd.xt : nullptr;
         nd.raw = c.out;
+        nd.raw2 = nx.raw2;
+        nd.ldr2 = nx.ld2;
+        nd.pos2 = nx.pos2;
         nd.ldr = c.ldo;
         tok = timing_begin(ctx, "moe_combine_norm");
         const unsigned threads = (unsigned)((c.H / 8 + 63) / 64 * 64);

@@ -5,6 +5,15 @@
 
 namespace ut {
 
+// Code i of a quantized row as a float (f32 rows: the value).
+__device__ __forceinline__ float code_at(int32_t fmt, const uint8_t *row, int64_t i) {
+    if (fmt == UT_FMT_F32) return ((const float *)row)[i];
+    if (fmt == UT_FMT_INT8) return (float)(int8_t)row[i];
+    uint8_t b = row[i >> 1];
+    int nib = (i & 1) ? (b >> 4) : (b & 0xF);
+    return (float)((nib ^ 8) - 8);
+}
+
 // One cache append (attention.rs:168-186): latent[pos] = rmsnorm(c[:L], w),
 // krot[pos] = rope_interleave(c[L:L+P], pos), by the whole workgroup (up to
 // 1024 threads; red: one double per wave).

@@ -7,13 +7,6 @@
 
 namespace ut {
 
-__device__ __forceinline__ float code_at(int32_t fmt, const uint8_t *row, int64_t i) {
-    if (fmt == UT_FMT_F32) return ((const float *)row)[i];
-    if (fmt == UT_FMT_INT8) return (float)(int8_t)row[i];
-    uint8_t b = row[i >> 1];
-    int nib = (i & 1) ? (b >> 4) : (b & 0xF);
-    return (float)((nib ^ 8) - 8);
-}
 
 __global__ void k_embed(int32_t fmt, const uint8_t *__restrict__ payload,
                         const float *__restrict__ scales, int64_t row_bytes, int64_t H,

@@ -39,6 +39,10 @@ struct RowDigArgs {
     // here (row stride ldr) after the reductions
     float *raw;
     int64_t ldr;
+    // and, when set, also at row pos2 + m of raw2 (stride ldr2)
+    float *raw2;
+    int64_t ldr2;
+    PosRef pos2;
 };
 
 template <typename T, typename Op>
@@ -101,6 +105,7 @@ __device__ __forceinline__ void rowdig_body(const RowDigArgs &a, int64_t m, floa
     mx = wide_reduce(mx, [](uint32_t p, uint32_t q) { return p > q ? p : q; }, redu);
     // every store comes after the last barrier, so no barrier waits for them
     if constexpr (RAW) {
+        float *r2 = a.raw2 ? a.raw2 + (a.pos2.get() + m) * a.ldr2 : nullptr;
 #pragma unroll
         for (int g = 0; g < GPT; g++) {
             const int64_t c = tid + (int64_t)g * nt;
@@ -108,6 +113,10 @@ __device__ __forceinline__ void rowdig_body(const RowDigArgs &a, int64_t m, floa
             float *o = a.raw + m * a.ldr + 8 * c;
             *(float4 *)o = make_float4(rv[g][0], rv[g][1], rv[g][2], rv[g][3]);
             *(float4 *)(o + 4) = make_float4(rv[g][4], rv[g][5], rv[g][6], rv[g][7]);
+            if (r2) {
+                *(float4 *)(r2 + 8 * c) = make_float4(rv[g][0], rv[g][1], rv[g][2], rv[g][3]);
+                *(float4 *)(r2 + 8 * c + 4) = make_float4(rv[g][4], rv[g][5], rv[g][6], rv[g][7]);
+            }
         }
     }
     if (a.out) {
