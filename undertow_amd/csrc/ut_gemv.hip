@@ -226,6 +226,87 @@ __global__ __launch_bounds__(1024) void k_rowdig_emb(RowDigArgs a, int32_t fmt,
     rowdig_body<1, true>(a, m, v, wv, redd, redu);
 }
 
+// The MTP module's input rows (mtp.rs: cat = [enorm(embed(id)) | hnorm(h)])
+// in one launch of two workgroups per row, one per half: the embedding row
+// as k_embed forms it (0 + (1 * scale[id]) * q), or the hidden row; each
+// rms-normalised (thread t sums its elements t, t + 1024, ... in f64, the
+// waves by the DPP butterfly and then in wave order), written to cat
+// [rows][2H], and the half's max|v| left as a partial maximum (float bits,
+// [rows][2]) from which eh_proj digitises the row while staging it.
+__global__ __launch_bounds__(1024) void k_mtp_input(int32_t fmt, const uint8_t *__restrict__ payload,
+                                                    const float *__restrict__ scales,
+                                                    int64_t row_bytes,
+                                                    const int32_t *__restrict__ ids,
+                                                    const float *__restrict__ hidden, int64_t H,
+                                                    const float *__restrict__ enorm,
+                                                    const float *__restrict__ hnorm, float eps,
+                                                    float *__restrict__ cat,
+                                                    uint32_t *__restrict__ vmax) {
+    __shared__ double redd[16];
+    __shared__ uint32_t redu[16];
+    constexpr int PT = 8;  // elements per thread (H <= 8192)
+    const int half = blockIdx.x;
+    const int64_t m = blockIdx.y;
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const float *w = half ? hnorm : enorm;
+    float v[PT];
+    double acc = 0.0;
+    if (half == 0) {
+        const int64_t id = ids[m];
+        const uint8_t *row = payload + id * row_bytes;
+        const float f = fmt == UT_FMT_F32 ? 1.0f : __fmul_rn(1.0f, scales[id]);
+#pragma unroll
+        for (int k = 0; k < PT; k++) {
+            const int64_t i = tid + (int64_t)k * nt;
+            v[k] = i < H ? __fadd_rn(0.0f, __fmul_rn(f, code_at(fmt, row, i))) : 0.0f;
+        }
+    } else {
+        const float *hr = hidden + m * H;
+#pragma unroll
+        for (int k = 0; k < PT; k++) {
+            const int64_t i = tid + (int64_t)k * nt;
+            v[k] = i < H ? hr[i] : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < PT; k++) acc += (double)v[k] * (double)v[k];
+    acc = wide_reduce(acc, [](double p, double q) { return p + q; }, redd);
+    const float r = 1.0f / sqrtf(__fadd_rn((float)(acc / (double)H), eps));
+    uint32_t mx = 0;
+    float *o = cat + m * 2 * H + half * H;
+#pragma unroll
+    for (int k = 0; k < PT; k++) {
+        const int64_t i = tid + (int64_t)k * nt;
+        if (i < H) {
+            const float x = __fmul_rn(__fmul_rn(v[k], r), w[i]);
+            o[i] = x;
+            mx = max(mx, __float_as_uint(fabsf(x)));
+        }
+    }
+    mx = wide_reduce(mx, [](uint32_t p, uint32_t q) { return p > q ? p : q; }, redu);
+    if (tid == 0) vmax[m * 2 + half] = mx;
+}
+
+bool mtp_input_ok(int64_t H) { return H % 4 == 0 && H <= 8 * 1024; }
+
+int32_t launch_mtp_input(ut_ctx *ctx, const ut_qtensor *emb, const int32_t *ids,
+                         const float *hidden, int64_t rows, int64_t H, const float *enorm,
+                         const float *hnorm, float eps, float *cat, uint32_t *vmax) {
+    if (!mtp_input_ok(H) || emb->in_dim != H) {
+        set_error(ctx, "mtp_input: hidden %lld unsupported", (long long)H);
+        return UT_ERR_ARG;
+    }
+    if (rows <= 0) return UT_OK;
+    int64_t nt = (H + 7) / 8;
+    nt = (nt + 63) / 64 * 64;
+    int tok = timing_begin(ctx, "mtp_input");
+    hipLaunchKernelGGL(k_mtp_input, dim3(2, (unsigned)rows), dim3((unsigned)nt), 0, ctx->stream,
+                       emb->fmt, (const uint8_t *)emb->payload, emb->scales, emb->row_bytes, ids,
+                       hidden, H, enorm, hnorm, eps, cat, vmax);
+    timing_end(ctx, tok);
+    return launch_check(ctx, "k_mtp_input");
+}
+
 bool embed_norm_ok(const ut_qtensor *emb, int64_t K, const float *x, const float *norm_w) {
     return K % 8 == 0 && K <= 8 * 1024 && emb->in_dim == K && ((uintptr_t)x & 15) == 0 &&
            ((uintptr_t)norm_w & 15) == 0;

@@ -298,6 +298,14 @@ bool gemv_norm_ok(const ut_qtensor *w, int64_t M, const void *x, const void *nor
 // (rmsnorm + digits as NormNext asks) in one launch; x gets the looked-up
 // rows.  embed_norm_ok: rows of K % 8 == 0 columns, K <= 8192, aligned.
 struct NormNext;
+// The MTP module's input rows [enorm(embed(ids)) | hnorm(hidden)] into
+// cat [rows][2H] in one launch, with each half's max|v| in vmax [rows][2]
+// (float bits) for a GEMV that digitises cat while staging it
+// (GemvArgs::xmax, nxmax = 2).
+bool mtp_input_ok(int64_t H);
+int32_t launch_mtp_input(ut_ctx *ctx, const ut_qtensor *emb, const int32_t *ids,
+                         const float *hidden, int64_t rows, int64_t H, const float *enorm,
+                         const float *hnorm, float eps, float *cat, uint32_t *vmax);
 bool embed_norm_ok(const ut_qtensor *emb, int64_t K, const float *x, const float *norm_w);
 int32_t launch_embed_norm(ut_ctx *ctx, const ut_qtensor *emb, const int32_t *ids, int64_t rows,
                           float *x, int64_t ldx, const NormNext &nx);

@@ -1230,10 +1230,28 @@ int32_t draft_rows_dev(ut_session *s, const int32_t *host_ids, int in_slot,
         else UT_TRY(upload_ids(s, host_ids, rows));
         ids = w.ids;
     }
-    UT_TRY(launch_embed(ctx, m->embed, ids, rows, w.emb, H));
-    UT_TRY(launch_rmsnorm(ctx, w.emb, H, m->enorm, H, c.rms_norm_eps, rows, w.cat, 2 * H));
-    UT_TRY(launch_rmsnorm(ctx, hidden_rows, H, m->hnorm, H, c.rms_norm_eps, rows, w.cat + H, 2 * H));
-    UT_TRY(mm(s, m->eh_proj, w.cat, rows, w.x, H));
+    if (!fast8(s) && m->eh_proj->fmt != UT_FMT_F32 && gemv_fast_ok(m->eh_proj) &&
+        mtp_input_ok(H) && rows <= 4) {
+        // the embedding and both norms in one launch, which leaves each
+        // half's max|v|; eh_proj digitises cat from them while staging it
+        UT_TRY(launch_mtp_input(ctx, m->embed, ids, hidden_rows, rows, H, m->enorm, m->hnorm,
+                                c.rms_norm_eps, w.cat, w.vmax));
+        GemvArgs ga;
+        ga.w = m->eh_proj;
+        ga.M = rows;
+        ga.xf = w.cat;
+        ga.out = w.x;
+        ga.ldo = H;
+        ga.xmax = w.vmax;
+        ga.nxmax = 2;
+        ga.exps_out = w.vexps;
+        UT_TRY(gemv(ctx, ga));
+    } else {
+        UT_TRY(launch_embed(ctx, m->embed, ids, rows, w.emb, H));
+        UT_TRY(launch_rmsnorm(ctx, w.emb, H, m->enorm, H, c.rms_norm_eps, rows, w.cat, 2 * H));
+        UT_TRY(launch_rmsnorm(ctx, hidden_rows, H, m->hnorm, H, c.rms_norm_eps, rows, w.cat + H, 2 * H));
+        UT_TRY(mm(s, m->eh_proj, w.cat, rows, w.x, H));
+    }
     XDigits hd_;
     const float *hn = w.normed;
     if (fuse_next_ok(s, rows)) {
