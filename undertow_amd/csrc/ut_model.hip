@@ -1230,6 +1230,9 @@ int32_t draft_rows_dev(ut_session *s, const int32_t *host_ids, int in_slot,
         else UT_TRY(upload_ids(s, host_ids, rows));
         ids = w.ids;
     }
+    NormNext pre_nx;
+    XDigits pre_xd;
+    bool pre_done = false;
     if (!fast8(s) && m->eh_proj->fmt != UT_FMT_F32 && gemv_fast_ok(m->eh_proj) &&
         mtp_input_ok(H) && rows <= 4) {
         // the embedding and both norms in one launch, which leaves each
@@ -1245,6 +1248,13 @@ int32_t draft_rows_dev(ut_session *s, const int32_t *host_ids, int in_slot,
         ga.xmax = w.vmax;
         ga.nxmax = 2;
         ga.exps_out = w.vexps;
+        // the MTP layer's input norm in eh_proj's split sum where it can run
+        if (fuse_next_ok(s, rows)) {
+            pre_nx = next_norm(s, m->mtp_layer.input_norm, input_flags(m->mtp_layer), rows, &pre_xd,
+                               input_f32(m->mtp_layer));
+            ga.next = &pre_nx;
+            ga.next_done = &pre_done;
+        }
         UT_TRY(gemv(ctx, ga));
     } else {
         UT_TRY(launch_embed(ctx, m->embed, ids, rows, w.emb, H));
@@ -1259,7 +1269,7 @@ int32_t draft_rows_dev(ut_session *s, const int32_t *host_ids, int in_slot,
         XDigits all;
         const NormNext nx = next_norm(s, m->mtp_norm, dig_flags({m->mtp_head}), rows, &all,
                                       f32_reader({m->mtp_head}));
-        UT_TRY(run_layer(s, m->mtp_layer, w.x, rows, s->mtp_kv, nullptr, &nx));
+        UT_TRY(run_layer(s, m->mtp_layer, w.x, rows, s->mtp_kv, pre_done ? &pre_xd : nullptr, &nx));
         hd_ = xdigits_rows(all, rows - 1);
         hn = w.normed + (rows - 1) * H;
     } else {
