@@ -437,102 +437,130 @@ __global__ __launch_bounds__(256) void k_mla_cache_split(const float *__restrict
 // all slices.  Every sum runs in a fixed order.
 constexpr int kMlaMaxSlices = 256;
 
-// A workgroup merges 32 columns x 8 latent dims.  Every load is issued at
-// the start (one memory round trip): thread (tx, tyz) holds the slice
-// statistics m, l of column tx for slices tyz + 32k; thread (c4, dy, part)
-// holds four adjacent columns of dim dy (16-byte loads) for one sixteenth
-// of the slices.  The sixteen part sums are added in part order through
-// LDS, so every output's sum has a fixed order.
+// A workgroup merges 32 columns x 8 latent dims, as 1,024 virtual threads
+// (NT threads, each standing for 1024 / NT of them).  Every load is issued
+// at the start (one memory round trip): virtual thread (tx, tyz) holds the
+// slice statistics m, l of column tx for slices tyz + 32k; virtual thread
+// (c4, dy, part) holds four adjacent columns of dim dy (16-byte loads) for
+// one sixteenth of the slices.  The 32 statistic sums and the sixteen part
+// sums are added in index order through LDS, so every output's sum has a
+// fixed order and NT does not change a bit of the result.
 // MAXS: the most slices the instantiation takes (the register arrays are
 // sized for it; with 64, two workgroups fit a CU instead of one).  Any
 // MAXS >= the rows' slice count runs the same operations in the same order.
+// NT < 1024 (fewer, busier threads) lets more rows' workgroups share a CU.
 constexpr int kCombineParts = 16;
 constexpr int kCombineSmallSlices = 64;
+constexpr int64_t kCombineOneWgPerCu = 256;  // workgroups: one per CU
+#ifndef UT_MLA_COMBINE_SMALL_NT
+#define UT_MLA_COMBINE_SMALL_NT 256
+#endif
 
-template <int MAXS>
-__global__ __launch_bounds__(1024) void k_mla_combine_mfma(const float *__restrict__ part_m,
-                                                           const float *__restrict__ part_l,
-                                                           const float *__restrict__ part_o,
-                                                           int RH, int H, int L, PosRef pos,
-                                                           float *__restrict__ clat) {
-    constexpr int kCombineStat = MAXS / 32;                                     // m, l per thread
+template <int MAXS, int NT>
+__global__ __launch_bounds__(NT) void k_mla_combine_mfma(const float *__restrict__ part_m,
+                                                         const float *__restrict__ part_l,
+                                                         const float *__restrict__ part_o,
+                                                         int RH, int H, int L, PosRef pos,
+                                                         float *__restrict__ clat) {
+    static_assert(NT % 64 == 0 && 1024 % NT == 0 && NT >= 256, "whole waves, 256 outputs");
+    constexpr int VT = 1024 / NT;                                               // virtual per thread
+    constexpr int kCombineStat = MAXS / 32;                                     // m, l per vthread
     constexpr int kCombineSlices = (MAXS + kCombineParts - 1) / kCombineParts;  // per part
     __shared__ __attribute__((aligned(16))) float sw[MAXS][32];
     __shared__ float red[32][33];
     __shared__ float sM[32], sInv[32];
     __shared__ __attribute__((aligned(16))) float sq[kCombineParts][8][32];
     const int tid = threadIdx.x;
-    const int tx = tid & 31, tyz = tid >> 5;
+    // virtual thread tid + NT i: tx and (c4, dy) are tid's, tyz and part step
+    const int tx = tid & 31, ty0 = tid >> 5;
     const int col = blockIdx.x * 32 + tx;
     // the slice count is the same for the workgroup's 32 columns (one query
     // row: 32 | H)
     const int64_t n_ctx = pos.get() + col / H + 1;
     const int64_t slen = mla_mfma_slice(n_ctx);
     const int ns = (int)((n_ctx + slen - 1) / slen);
-    // merge-pass loads: columns 4*c4.., dim dy, slices [j0, j1)
-    const int c4 = tid & 7, dy = (tid >> 3) & 7, part = tid >> 6;
+    // merge-pass loads: columns 4*c4.., dim dy, slices [j0, j1) of each part
+    const int c4 = tid & 7, dy = (tid >> 3) & 7, p0 = tid >> 6;
     const int q = (ns + kCombineParts - 1) / kCombineParts;
-    const int j0 = part * q, j1 = j0 + q < ns ? j0 + q : ns;
     const float *po = part_o + (int64_t)(blockIdx.y * 8 + dy) * RH + blockIdx.x * 32 + 4 * c4;
     const int64_t js = (int64_t)L * RH;
-    float4 v[kCombineSlices];
+    float4 v[VT][kCombineSlices];
 #pragma unroll
-    for (int u = 0; u < kCombineSlices; u++)
-        if (u < q) {
-            const int j = j0 + u < j1 ? j0 + u : (j1 > 0 ? j1 - 1 : 0);
-            v[u] = *(const float4 *)(po + (int64_t)j * js);
-        }
-    // statistics loads
-    float pm[kCombineStat], pl[kCombineStat];
+    for (int i = 0; i < VT; i++) {
+        const int j0 = (p0 + (NT / 64) * i) * q, j1 = j0 + q < ns ? j0 + q : ns;
 #pragma unroll
-    for (int k = 0; k < kCombineStat; k++) {
-        const int j = tyz + 32 * k;
-        if (j < ns) {
-            pm[k] = part_m[(int64_t)j * RH + col];
-            pl[k] = part_l[(int64_t)j * RH + col];
-        }
+        for (int u = 0; u < kCombineSlices; u++)
+            if (u < q) {
+                const int j = j0 + u < j1 ? j0 + u : (j1 > 0 ? j1 - 1 : 0);
+                v[i][u] = *(const float4 *)(po + (int64_t)j * js);
+            }
     }
-    float mx = -INFINITY;
+    // statistics loads
+    float pm[VT][kCombineStat], pl[VT][kCombineStat];
 #pragma unroll
-    for (int k = 0; k < kCombineStat; k++)
-        if (tyz + 32 * k < ns) mx = fmaxf(mx, pm[k]);
-    red[tyz][tx] = mx;
+    for (int i = 0; i < VT; i++)
+#pragma unroll
+        for (int k = 0; k < kCombineStat; k++) {
+            const int j = ty0 + (NT / 32) * i + 32 * k;
+            if (j < ns) {
+                pm[i][k] = part_m[(int64_t)j * RH + col];
+                pl[i][k] = part_l[(int64_t)j * RH + col];
+            }
+        }
+#pragma unroll
+    for (int i = 0; i < VT; i++) {
+        const int tyz = ty0 + (NT / 32) * i;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < kCombineStat; k++)
+            if (tyz + 32 * k < ns) mx = fmaxf(mx, pm[i][k]);
+        red[tyz][tx] = mx;
+    }
     __syncthreads();
-    if (tyz == 0) {
+    if (ty0 == 0) {
         float M = red[0][tx];
         for (int t = 1; t < 32; t++) M = fmaxf(M, red[t][tx]);
         sM[tx] = M;
     }
     __syncthreads();
     const float M = sM[tx];
-    float ls = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kCombineStat; k++) {
-        const int j = tyz + 32 * k;
-        if (j < ns) {
-            const float e = __expf(pm[k] - M);
-            sw[j][tx] = e;
-            ls = __fadd_rn(ls, __fmul_rn(pl[k], e));
+    for (int i = 0; i < VT; i++) {
+        const int tyz = ty0 + (NT / 32) * i;
+        float ls = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kCombineStat; k++) {
+            const int j = tyz + 32 * k;
+            if (j < ns) {
+                const float e = __expf(pm[i][k] - M);
+                sw[j][tx] = e;
+                ls = __fadd_rn(ls, __fmul_rn(pl[i][k], e));
+            }
         }
+        red[tyz][tx] = ls;
     }
-    red[tyz][tx] = ls;
     __syncthreads();  // sw and red complete
-    if (tyz == 0) {
+    if (ty0 == 0) {
         float t = red[0][tx];
         for (int u = 1; u < 32; u++) t = __fadd_rn(t, red[u][tx]);
         sInv[tx] = 1.0f / t;  // read after the barrier below
     }
-    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-    for (int u = 0; u < kCombineSlices; u++)
-        if (j0 + u < j1) {
-            const float4 w = *(const float4 *)&sw[j0 + u][4 * c4];
-            acc.x = __builtin_fmaf(v[u].x, w.x, acc.x);
-            acc.y = __builtin_fmaf(v[u].y, w.y, acc.y);
-            acc.z = __builtin_fmaf(v[u].z, w.z, acc.z);
-            acc.w = __builtin_fmaf(v[u].w, w.w, acc.w);
-        }
-    *(float4 *)&sq[part][dy][4 * c4] = acc;
+    for (int i = 0; i < VT; i++) {
+        const int part = p0 + (NT / 64) * i;
+        const int j0 = part * q, j1 = j0 + q < ns ? j0 + q : ns;
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int u = 0; u < kCombineSlices; u++)
+            if (j0 + u < j1) {
+                const float4 w = *(const float4 *)&sw[j0 + u][4 * c4];
+                acc.x = __builtin_fmaf(v[i][u].x, w.x, acc.x);
+                acc.y = __builtin_fmaf(v[i][u].y, w.y, acc.y);
+                acc.z = __builtin_fmaf(v[i][u].z, w.z, acc.z);
+                acc.w = __builtin_fmaf(v[i][u].w, w.w, acc.w);
+            }
+        *(float4 *)&sq[part][dy][4 * c4] = acc;
+    }
     __syncthreads();
     if (tid < 256) {
         const int oc = tid & 31, od = tid >> 5;  // output column, dim
@@ -620,17 +648,25 @@ int32_t launch_mla_attend_kc(ut_ctx *ctx, const float *qabs, const float *qrope,
     UT_TRY(launch_check(ctx, "k_mla_mfma"));
     tok = timing_begin(ctx, "mla_combine");
     const dim3 cgrid((unsigned)(RH / 32), (unsigned)(L / 8));
-    if (a.nslice <= kCombineSmallSlices)
-        hipLaunchKernelGGL(k_mla_combine_mfma<kCombineSmallSlices>, cgrid, dim3(1024), 0,
+    // up to 64 slices: 256-thread workgroups once the grid exceeds one per
+    // CU (config-4 verify of four rows: 15.2 -> 7.4 us per combine; at one
+    // row the 1,024-thread form is 0.2 us faster)
+    if (a.nslice <= kCombineSmallSlices && (int64_t)cgrid.x * cgrid.y > kCombineOneWgPerCu)
+        hipLaunchKernelGGL((k_mla_combine_mfma<kCombineSmallSlices, UT_MLA_COMBINE_SMALL_NT>), cgrid,
+                           dim3(UT_MLA_COMBINE_SMALL_NT), 0, ctx->stream, a.part_m, a.part_l,
+                           a.part_o, (int)RH, (int)H, (int)L, a.pos, clat);
+    else if (a.nslice <= kCombineSmallSlices)
+        hipLaunchKernelGGL((k_mla_combine_mfma<kCombineSmallSlices, 1024>), cgrid, dim3(1024), 0,
                            ctx->stream, a.part_m, a.part_l, a.part_o, (int)RH, (int)H, (int)L,
                            a.pos, clat);
     else if (a.nslice <= 2 * kCombineSmallSlices)
-        hipLaunchKernelGGL(k_mla_combine_mfma<2 * kCombineSmallSlices>, cgrid, dim3(1024), 0,
+        hipLaunchKernelGGL((k_mla_combine_mfma<2 * kCombineSmallSlices, 1024>), cgrid, dim3(1024), 0,
                            ctx->stream, a.part_m, a.part_l, a.part_o, (int)RH, (int)H, (int)L,
                            a.pos, clat);
     else
-        hipLaunchKernelGGL(k_mla_combine_mfma<kMlaMaxSlices>, cgrid, dim3(1024), 0, ctx->stream,
-                           a.part_m, a.part_l, a.part_o, (int)RH, (int)H, (int)L, a.pos, clat);
+        hipLaunchKernelGGL((k_mla_combine_mfma<kMlaMaxSlices, 1024>), cgrid, dim3(1024), 0,
+                           ctx->stream, a.part_m, a.part_l, a.part_o, (int)RH, (int)H, (int)L,
+                           a.pos, clat);
     timing_end(ctx, tok);
     return launch_check(ctx, "k_mla_combine_mfma");
 }

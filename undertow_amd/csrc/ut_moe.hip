@@ -1423,9 +1423,14 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_down_mfma(DownArgs a) {
 // I <= 2048 staged whole, I % 256 == 0, no split): h as f32 digitised while
 // staged by the gate/up workgroups' partial maxima, each wave one 16-row
 // tile, the workgroup 64 rows; the same totals and epilogue as down_body.
-inline bool down_i8_mfma_ok(int fmt, int M, int64_t I, int ks) {
-    return fmt == UT_FMT_INT8 && M >= UT_MOE_I8_MFMA_MIN_M && M <= 4 && ks == 1 &&
-           I <= kMoeI8KC && I % kMfmaI8SegCols == 0;
+// Whole 256-column segments in every K slice, each slice staged in one
+// chunk: the inter size whole (ks == 1) or split in slices of kslice
+// columns (a one-slot MLP's down, finished by k_moe_down_finish).
+inline bool down_i8_mfma_ok(int fmt, int M, int64_t I, int ks, int64_t kslice) {
+    if (fmt != UT_FMT_INT8 || M < UT_MOE_I8_MFMA_MIN_M || M > 4 || I % kMfmaI8SegCols != 0)
+        return false;
+    if (ks == 1) return I <= kMoeI8KC;
+    return kslice <= kMoeI8KC && kslice % kMfmaI8SegCols == 0;
 }
 
 template <int M>
@@ -1458,9 +1463,26 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_down_i8_mfma(DownArgs a) {
             }
         };
         CoreOut<UT_FMT_INT4, M, 4> res[1];
+        // split K (ks > 1): columns [z kslice, (z+1) kslice), exact partial
+        // totals to part[z][slot][M][H] as down_body writes them
+        const int64_t kb = a.ks > 1 ? (int64_t)blockIdx.z * a.kslice : 0;
+        const int64_t ke = a.ks > 1 ? (kb + a.kslice < a.I ? kb + a.kslice : a.I) : a.I;
         mfma_gemv_i8<M, kMoeI8KC, 1, UT_MOE_I8_MFMA_DEPTH, true>(
-            lrows, 0, a.I, nullptr, 0, a.x.xf + u * a.x_slot_stride, a.x.ldx, lds,
+            lrows, kb, ke, nullptr, 0, a.x.xf + u * a.x_slot_stride, a.x.ldx, lds,
             lds + mfma_i8_lds_bytes<M, kMoeI8KC>() + wave * kMfmaI8WaveAreaBytes, res, prep);
+        if (a.ks > 1) {
+            const int64_t slots = gridDim.y;
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+                for (int m = 0; m < M; m++) {
+                    const int64_t o = wrow0 + 4 * g + r;
+                    if (s == 4 * r + m && o < a.H)
+                        a.part[(((int64_t)blockIdx.z * slots + u) * M + m) * a.H + o] =
+                            res[0].S[r][m];
+                }
+            return;
+        }
 #pragma unroll
         for (int r = 0; r < 4; r++)
 #pragma unroll
@@ -1838,10 +1860,15 @@ static void launch_down(ut_ctx *ctx, const DownArgs &a, int64_t slots, const Dow
         }
     }
     if constexpr (FA == UT_FMT_INT8 && M >= 2 && M <= 4) {
-        if (!b && down_i8_mfma_ok(FA, M, a.I, a.ks)) {
+        if (!b && down_i8_mfma_ok(FA, M, a.I, a.ks, a.kslice)) {
             hipLaunchKernelGGL((k_moe_down_i8_mfma<M>),
-                               dim3((unsigned)((a.H + 63) / 64), (unsigned)slots),
+                               dim3((unsigned)((a.H + 63) / 64), (unsigned)slots, (unsigned)a.ks),
                                dim3(kGemvThreads), 0, ctx->stream, a);
+            if (a.ks > 1)
+                hipLaunchKernelGGL((k_moe_down_finish<FA>),
+                                   dim3((unsigned)((a.H + kGemvThreads - 1) / kGemvThreads),
+                                        (unsigned)(slots * M)),
+                                   dim3(kGemvThreads), 0, ctx->stream, a, M);
             return;
         }
     }
@@ -1879,9 +1906,11 @@ static int32_t moe_pass_t(ut_ctx *ctx, const MoeCall &c, const ScratchLayout &L,
     // the matrix-core gate/up (int4, 2..4 rows): x as f32 with the
     // digitiser's exponents, the slot plan made before the launch, a shared
     // expert in the same launches (config-4 verify of two rows: 1,027 ->
-    // 1,003 us of GPU time against the dot-product dual kernels)
+    // 1,003 us of GPU time against the dot-product dual kernels); the int8
+    // kernel reads x's digit planes only, so caller digits serve it as they
+    // are (a model's dense FFN at 2..4 rows)
     const bool use_mfma = gate_up_mfma_ok(FMT, M, c.H) && c.extra_slot < 0 &&
-                          (!c.x_digits || c.x_matches_digits) &&
+                          (FMT == UT_FMT_INT8 || !c.x_digits || c.x_matches_digits) &&
                           L.ntiles == (c.I + kGateUpRowsPerWG - 1) / kGateUpRowsPerWG;
     const bool gate_plan = FMT != UT_FMT_F32 && need_plan && c.extra_slot < 0 &&
                            (int64_t)M * c.k <= 64 && !use_mfma;
