@@ -1122,28 +1122,22 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up_i8_mfma(GateUpArgs
     gate_up_i8_mfma_body<M>(a, blockIdx.y, blockIdx.x, lds, wg_max);
 }
 
-// The routed experts on the matrix cores (slots 0..gridDim.y-2, 32-row
-// tiles) and a shared MLP of format FB (the last grid row, the plain
-// kernel's 16-row tiles) in one launch, so the shared MLP's few workgroups
-// run beside the routed ones instead of after them.
 constexpr int cmax_words(int p, int q) { return p > q ? p : q; }
-template <int M, int FB>
-__global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up_mfma_dual(GateUpArgs a, GateUpArgs b) {
-    __shared__ __attribute__((aligned(16)))
-    uint32_t lds[cmax_words(gate_up_mfma_lds_words<M, true>(), kLdsWords)];
-    __shared__ uint32_t wg_max[4];
-    if (blockIdx.y + 1 < gridDim.y) {
-        if ((int64_t)blockIdx.x * gate_up_mfma_rows<M, true>() < a.I)
-            gate_up_mfma_body<M, gate_up_mfma_tw<M, true>()>(a, blockIdx.y, blockIdx.x, lds, wg_max);
-    } else {
-        gate_up_body<FB, M, false>(b, 0, blockIdx.x, lds, wg_max);
-    }
-}
 
-// The same pair of passes on a flat grid: gxm tiles of 32 * TW rows per
-// routed slot (slot-major, nrouted workgroups), then the shared MLP's
-// 16-row tiles, so no workgroup of the grid is empty when the routed tiles
-// are fewer than the shared MLP's.
+// The routed experts on the matrix cores and a shared MLP of format FB in
+// one launch, so the shared MLP's few workgroups run beside the routed ones
+// instead of after them, on a flat grid: gxm tiles of 32 * TW rows per
+// routed slot (slot-major, nrouted workgroups) and the shared MLP's 16-row
+// tiles, so no workgroup of the grid is empty when the routed tiles are
+// fewer than the shared MLP's.
+// The shared MLP's workgroups first in the dual launches' grids (1), or
+// after the routed ones (0).  A shared int8 workgroup streams twice the
+// bytes of a routed int4 one; dispatched last, they ran on alone at the
+// launch's end: config-4 four-row verify gate/up 79.1 -> 68.4 us, two-row
+// 47.7 -> 44.8 us, one-row 30.9 -> 30.2 us.
+#ifndef UT_DUAL_SHARED_FIRST
+#define UT_DUAL_SHARED_FIRST 1
+#endif
 template <int M, int FB, int TW>
 __global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up_mfma_dual_flat(GateUpArgs a,
                                                                              GateUpArgs b, int gxm,
@@ -1152,13 +1146,16 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_gate_up_mfma_dual_flat(Gat
     uint32_t lds[cmax_words(mfma_lds_words<M, gate_up_mfma_kc<M>()>() + TW * kI4WaveAreaBytes,
                             kLdsWords)];
     __shared__ uint32_t wg_max[4];
-    const int i = blockIdx.x;
+    const int nb = gridDim.x - nrouted;
+    const int i = UT_DUAL_SHARED_FIRST ? (blockIdx.x < nb ? nrouted + blockIdx.x : blockIdx.x - nb)
+                                       : blockIdx.x;
     if (i < nrouted) gate_up_mfma_body<M, TW>(a, i / gxm, i % gxm, lds, wg_max);
     else gate_up_body<FB, M, false>(b, 0, i - nrouted, lds, wg_max);
 }
 
-// Routed experts (format FA, slots 0..gridDim.y-2) and one shared MLP
-// (format FB, the last grid row) in one launch.
+// Routed experts (format FA) and one shared MLP (format FB) in one launch:
+// grid rows are the routed slots and the shared MLP's row (the first with
+// UT_DUAL_SHARED_FIRST, else the last).
 template <int FA, int FB, int M>
 // At one and two rows, registers for five workgroups per CU (a few spilled
 // values): at one row the routed and shared experts' 9 x 128 workgroups are
@@ -1170,8 +1167,10 @@ __global__ __launch_bounds__(kGemvThreads, M <= 2 ? 5 : 1) void k_moe_gate_up_du
     __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
     __shared__ uint32_t wg_max[4];
     // (the routed table's x comes digitised here: no staged routing)
-    if (blockIdx.y + 1 < gridDim.y)
-        gate_up_body<FA, M, false>(a, blockIdx.y, blockIdx.x, lds, wg_max);
+    const int y = UT_DUAL_SHARED_FIRST ? (blockIdx.y == 0 ? gridDim.y - 1 : blockIdx.y - 1)
+                                       : blockIdx.y;
+    if (y + 1 < gridDim.y)
+        gate_up_body<FA, M, false>(a, y, blockIdx.x, lds, wg_max);
     else
         gate_up_body<FB, M, false>(b, 0, blockIdx.x, lds, wg_max);
 }
@@ -1498,15 +1497,18 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_down_i8_mfma(DownArgs a) {
 
 // The routed experts' down on the matrix cores and a shared MLP's down
 // (format FB, one slot, no split) in one launch: a flat grid of gxm tiles
-// per routed slot (slot-major, as k_moe_down_mfma's grid), then the shared
-// MLP's gxb tiles, which run beside the routed ones instead of after them.
+// per routed slot (slot-major, as k_moe_down_mfma's grid) and the shared
+// MLP's gxb tiles (first with UT_DUAL_SHARED_FIRST), which run beside the
+// routed ones instead of after them.
 template <int M, int FB>
 __global__ __launch_bounds__(kGemvThreads) void k_moe_down_mfma_dual(DownArgs a, DownArgs b, int gxm,
                                                                     int nrouted) {
     __shared__ __attribute__((aligned(16)))
     uint32_t lds[cmax_words(down_mfma_lds_words<M>(), kLdsWords)];
     __shared__ uint32_t red[4 * M];
-    const int i = blockIdx.x;
+    const int nb = gridDim.x - nrouted;
+    const int i = UT_DUAL_SHARED_FIRST ? (blockIdx.x < nb ? nrouted + blockIdx.x : blockIdx.x - nb)
+                                       : blockIdx.x;
     if (i < nrouted) down_mfma_body<M>(a, i / gxm, i % gxm, lds, red);
     else down_body<FB, M>(b, 0, i - nrouted, lds);
 }
@@ -1554,7 +1556,9 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_down_finish(DownArgs a, in
 template <int FA, int FB, int M>
 __global__ __launch_bounds__(kGemvThreads) void k_moe_down_dual(DownArgs a, DownArgs b) {
     __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
-    if (blockIdx.y + 1 < gridDim.y) down_body<FA, M>(a, blockIdx.y, blockIdx.x, lds);
+    const int y = UT_DUAL_SHARED_FIRST ? (blockIdx.y == 0 ? gridDim.y - 1 : blockIdx.y - 1)
+                                       : blockIdx.y;
+    if (y + 1 < gridDim.y) down_body<FA, M>(a, y, blockIdx.x, lds);
     else down_body<FB, M>(b, 0, blockIdx.x, lds);
 }
 
@@ -1846,7 +1850,7 @@ static void launch_down(ut_ctx *ctx, const DownArgs &a, int64_t slots, const Dow
                                    dim3(kGemvThreads), 0, ctx->stream, a);
                 return;
             }
-            // a shared MLP beside it (one slot, no split): the grid's last tiles
+            // a shared MLP beside it (one slot, no split): its tiles in the same grid
             constexpr int DRB = 16 * down_rows<M>();
             const int nrouted = gxm * (int)slots;
             const unsigned n = (unsigned)(nrouted + (b->H + DRB - 1) / DRB);
