@@ -606,24 +606,36 @@ template <int M> constexpr int plain_depth() { return M == 1 ? 4 : M == 2 ? 2 : 
 __host__ __device__ constexpr int plain_rows_rt(int) { return 16 * 2; }
 
 // NORM: x is one un-normalised row, normalised while staged (XSrc::nw).
+// The kv appends' workgroups first in the normalising GEMV's grid (config-4
+// one-row q_b 11.0 -> 10.3 us), or last.
+#ifndef UT_KV_APPEND_FIRST
+#define UT_KV_APPEND_FIRST 1
+#endif
 constexpr int kGemvNormCols = 2048;
 template <int FMT, int M, bool NORM = false>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
     constexpr int R = plain_rows<M>();
+    // bx: this workgroup's row tile
+    int bx = (int)blockIdx.x;
     if constexpr (NORM) {
-        // the last M workgroups append the M kv_a rows (row m at pos + m)
-        if (a.kv.comp && (int)blockIdx.x >= (int)gridDim.x - M) {
-            __shared__ double red4[4];
-            const KvAppendArgs &k = a.kv;
-            const int m = (int)blockIdx.x - ((int)gridDim.x - M);
-            kv_append_row(k.comp + m * (k.L + k.P), k.L, k.P, k.w, k.eps, k.latent, k.krot, k.kc,
-                          k.pos.get() + m, k.table, red4);
-            return;
+        // M more workgroups append the M kv_a rows (row m at pos + m): the
+        // grid's first (UT_KV_APPEND_FIRST), so their chain of reductions
+        // runs beside the tiles instead of after them, or its last
+        if (a.kv.comp) {
+            const int m = UT_KV_APPEND_FIRST ? bx : bx - ((int)gridDim.x - M);
+            if (m >= 0 && m < M) {
+                __shared__ double red4[4];
+                const KvAppendArgs &k = a.kv;
+                kv_append_row(k.comp + m * (k.L + k.P), k.L, k.P, k.w, k.eps, k.latent, k.krot,
+                              k.kc, k.pos.get() + m, k.table, red4);
+                return;
+            }
+            if (UT_KV_APPEND_FIRST) bx -= M;
         }
     }
     __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, s = lane & 15;
-    const int64_t row0 = (int64_t)blockIdx.x * (16 * R) + wave * (4 * R) + g * R;
+    const int64_t row0 = (int64_t)bx * (16 * R) + wave * (4 * R) + g * R;
     const uint8_t *rows[R];
 #pragma unroll
     for (int r = 0; r < R; r++) rows[r] = plain_row(a, row0 + r < a.O ? row0 + r : a.O - 1);
@@ -645,7 +657,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
             shl[m] = sh[m];
             exl[m] = sh[m] == INT32_MIN ? INT32_MIN : -sh[m];
         }
-        if (blockIdx.x == 0 && blockIdx.z == 0 && tid < M)
+        if (bx == 0 && blockIdx.z == 0 && tid < M)
             const_cast<int32_t *>(a.exps)[tid] = tid == 0 ? exl[0] : tid == 1 ? exl[M > 1 ? 1 : 0]
                                                 : tid == 2 ? exl[M > 2 ? 2 : 0] : exl[M > 3 ? 3 : 0];
     };
@@ -709,7 +721,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(PlainArgs a) {
                 argmax_offer(bm[m], nv, row);
             }
         }
-    if (a.am.v) argmax_parts_store<M>(a.am, bm, blockIdx.x);
+    if (a.am.v) argmax_parts_store<M>(a.am, bm, bx);
 }
 
 // int8 weights at 3..4 activation rows on the matrix cores
