@@ -126,3 +126,40 @@ def test_c4_decode_rows_equal_verify_rows(c4, rows):
     v.prefill(prompt)
     many = v.prefill(feed)
     assert np.array_equal(one, many)
+
+
+LONG = 72  # three 32-position attention slices per row at the end
+
+
+@pytest.fixture(scope="module")
+def c4_long(c4):
+    ck, m, om, prompt, stream = c4
+    long_prompt = prompt_ids(LONG, C4["vocab_size"], seed=22)
+    print("config 4: oracle forward and greedy stream of a 72-token prompt", flush=True)
+    want = om.forward(long_prompt)
+    lstream = om.greedy_decode(long_prompt, 8)[LONG:]
+    return long_prompt, want, lstream
+
+
+def test_c4_long_prompt_logits_match_oracle(c4, c4_long):
+    """Multi-slice attention in the model path (rows past 32 positions take
+    two and three slices, merged by the slice combine), prefill chunks of
+    four rows over a 72-token prompt."""
+    ck, m, om, prompt, stream = c4
+    long_prompt, want, lstream = c4_long
+    got = m.forward(long_prompt)
+    err = np.abs(got - want)
+    assert err.max() <= 1e-3 and err.mean() <= 1e-4, (err.max(), err.mean())
+    ok = gap_ok(want)
+    assert (got.argmax(1)[ok] == want.argmax(1)[ok]).all()
+
+
+def test_c4_long_prompt_streams(c4, c4_long):
+    """Greedy and MTP depth 1 / 3 after the 72-token prompt equal the
+    oracle's greedy stream."""
+    ck, m, om, prompt, stream = c4
+    long_prompt, want, lstream = c4_long
+    assert m.generate_greedy(long_prompt, 8) == lstream
+    for depth in (1, 3):
+        toks, drafted, accepted = m.generate_mtp(long_prompt, 8, depth=depth)
+        assert toks == lstream and drafted > 0
