@@ -1425,47 +1425,63 @@ static int32_t launch_fast(ut_ctx *ctx, const GemvArgs &ga, int64_t m0, int mrow
 
 // f32 weights with few output rows (the router gate: 256 x 7168): one
 // workgroup per output row for all M <= 4 activation rows; thread t takes
-// the float4 columns 4t + 1024j (every weight load in flight at once), the
-// per-thread FMA chains are summed by DPP within each wave and then over the
-// four waves in order.  No split-K partials, so the router reads the logits
-// directly.
-
-template <int M, int NJ>
+// the float4 columns 4t + 1024j (x's columns and the row's weights loaded
+// first, every load in flight at once; NJ exact for the row where it can
+// be: config-4 router at four rows 10.3 -> 5.4 us), the per-thread FMA
+// chains are summed by DPP within each wave and then over the four waves in
+// order.  EPW (output rows per workgroup, reusing x's registers) stays 1:
+// four rows per workgroup at four activation rows measured 7.0 us.  No
+// split-K partials, so the router reads the logits directly.
+template <int M, int NJ, int EPW>
 __global__ __launch_bounds__(256) void k_rowdot_f32(const float *__restrict__ w, int64_t K,
                                                     const float *__restrict__ x, int64_t ldx,
-                                                    float *__restrict__ out, int64_t ldo) {
-    __shared__ float red[4][M];
-    const int64_t row = blockIdx.x;
+                                                    float *__restrict__ out, int64_t ldo,
+                                                    int64_t O) {
+    __shared__ float red[EPW][4][M];
     const int tid = threadIdx.x;
-    const float *wr = w + row * K;
-    float4 wv[NJ];
+    float4 xv[M][NJ];
 #pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        const int64_t c = 4 * tid + 1024 * j;
-        wv[j] = c < K ? ld_global<float4>(wr + c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    }
-    float acc[M];
-#pragma unroll
-    for (int m = 0; m < M; m++) {
-        float a = 0.0f;
+    for (int m = 0; m < M; m++)
 #pragma unroll
         for (int j = 0; j < NJ; j++) {
             const int64_t c = 4 * tid + 1024 * j;
-            if (c < K) {
-                const float4 xv = ld_global<float4>(x + m * ldx + c);
-                a = __builtin_fmaf(wv[j].x, xv.x, a);
-                a = __builtin_fmaf(wv[j].y, xv.y, a);
-                a = __builtin_fmaf(wv[j].z, xv.z, a);
-                a = __builtin_fmaf(wv[j].w, xv.w, a);
-            }
+            xv[m][j] = c < K ? ld_global<float4>(x + m * ldx + c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
-        acc[m] = wave_reduce_dpp(a, [](float p, float q) { return p + q; });
-    }
-    if ((tid & 63) == 0)
+    float4 wv[EPW][NJ];
 #pragma unroll
-        for (int m = 0; m < M; m++) red[tid >> 6][m] = acc[m];
+    for (int e = 0; e < EPW; e++) {
+        const int64_t row0 = (int64_t)blockIdx.x * EPW + e;
+        const float *wr = w + (row0 < O ? row0 : O - 1) * K;
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const int64_t c = 4 * tid + 1024 * j;
+            wv[e][j] = c < K ? ld_global<float4>(wr + c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < EPW; e++)
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            float a = 0.0f;
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                const int64_t c = 4 * tid + 1024 * j;
+                if (c < K) {
+                    a = __builtin_fmaf(wv[e][j].x, xv[m][j].x, a);
+                    a = __builtin_fmaf(wv[e][j].y, xv[m][j].y, a);
+                    a = __builtin_fmaf(wv[e][j].z, xv[m][j].z, a);
+                    a = __builtin_fmaf(wv[e][j].w, xv[m][j].w, a);
+                }
+            }
+            a = wave_reduce_dpp(a, [](float p, float q) { return p + q; });
+            if ((tid & 63) == 0) red[e][tid >> 6][m] = a;
+        }
     __syncthreads();
-    if (tid < M) out[tid * ldo + row] = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
+    if (tid < EPW * M) {
+        const int e = tid / M, m = tid - e * M;
+        const int64_t row = (int64_t)blockIdx.x * EPW + e;
+        if (row < O) out[m * ldo + row] = ((red[e][0][m] + red[e][1][m]) + red[e][2][m]) + red[e][3][m];
+    }
 }
 
 bool rowdot_f32_ok(const ut_qtensor *w, int64_t M) {
@@ -1479,18 +1495,25 @@ int32_t launch_rowdot_f32(ut_ctx *ctx, const ut_qtensor *w, const float *x, int6
         set_error(ctx, "rowdot_f32: unsupported shape or alignment");
         return UT_ERR_ARG;
     }
-    const int64_t K = w->in_dim;
+    const int64_t K = w->in_dim, O = w->out_dim;
     const int nj = (int)((K + 1023) / 1024);
     int tok = timing_begin(ctx, "rowdot_f32");
-    const dim3 grid((unsigned)w->out_dim);
     const float *wp = (const float *)w->payload;
-#define UT_RD(MM, NJ) hipLaunchKernelGGL((k_rowdot_f32<MM, NJ>), grid, dim3(256), 0, ctx->stream, wp, K, x, K, out, ldo)
-#define UT_RDM(MM) do { if (nj <= 2) UT_RD(MM, 2); else if (nj <= 4) UT_RD(MM, 4); else UT_RD(MM, 8); } while (0)
+#define UT_RD(MM, NJ, EPW)                                                                  \
+    hipLaunchKernelGGL((k_rowdot_f32<MM, NJ, EPW>), dim3((unsigned)((O + EPW - 1) / EPW)), \
+                       dim3(256), 0, ctx->stream, wp, K, x, K, out, ldo, O)
+#define UT_RDM(MM, EPW)                                              \
+    do {                                                             \
+        if (nj <= 2) UT_RD(MM, 2, EPW);                              \
+        else if (nj <= 4) UT_RD(MM, 4, EPW);                         \
+        else if (nj == 7) UT_RD(MM, 7, EPW);                         \
+        else UT_RD(MM, 8, EPW);                                      \
+    } while (0)
     switch (M) {
-    case 1: UT_RDM(1); break;
-    case 2: UT_RDM(2); break;
-    case 3: UT_RDM(3); break;
-    default: UT_RDM(4); break;
+    case 1: UT_RDM(1, 1); break;
+    case 2: UT_RDM(2, 1); break;
+    case 3: UT_RDM(3, 1); break;
+    default: UT_RDM(4, 1); break;
     }
 #undef UT_RDM
 #undef UT_RD

@@ -382,7 +382,7 @@ int32_t ws_reserve(ut_session *s, int64_t rows) {
     size_t ilog = F(R * c.vocab_size), iemb = F(R * H), icat = F(R * 2 * H);
     size_t irl = F(4 * E), irw = F(4 * k), irid = F(4 * k), iids = F(R), iam = F(R + 1), ierr = F(1);
     size_t ivids = F(8);
-    size_t ivmax = F(R * heads * ((c.v_head_dim + 7) / 8)), ivexp = F(R);
+    size_t ivmax = F(R * absorb_v_parts(heads, c.v_head_dim)), ivexp = F(R);
     size_t idig = plan.add(matmul_digit_bytes(R, kmax));
     size_t idA = plan.add(matmul_digit_bytes(R, kmax));
     size_t idB = plan.add(matmul_digit_bytes(R, kmax));
@@ -951,7 +951,7 @@ int32_t mla_forward(ut_session *s, const LayerW &L, const float *x, const XDigit
     ga.ldo = c.hidden_size;
     ga.accumulate = 1;
     ga.xmax = w.vmax;
-    ga.nxmax = (int)(heads * ((vh + 7) / 8));
+    ga.nxmax = (int)absorb_v_parts(heads, vh);
     ga.exps_out = w.vexps;
     // the post-attention norm runs in o_proj's partial sum when K is split
     ga.next = post;

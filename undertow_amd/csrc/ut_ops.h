@@ -110,8 +110,10 @@ int32_t launch_kv_append(ut_ctx *ctx, const float *comp, int64_t rows, int64_t L
 // Absorbed value (attention.rs:235, QTensor::matvec_rows): for each (s, h)
 //   ctx[s, h*vh + j] = (sum_i clat[s,h,i] * W[h*kvh+nope+j, i]) * scale.
 // vmax (optional, absorb_v_max_ok weights): partial maxima of |ctx| per row,
-// [rows][heads * ceil(vh/8)] float bits, for the o_proj GEMV's digitising.
+// [rows][absorb_v_parts(heads, vh)] float bits, for the o_proj GEMV's
+// digitising.
 bool absorb_v_max_ok(const ut_qtensor *kv_b);
+int64_t absorb_v_parts(int64_t heads, int64_t vh);
 int32_t launch_absorb_v(ut_ctx *ctx, const ut_qtensor *kv_b, const float *clat, int64_t rows,
                         int64_t heads, int64_t nope, int64_t vh, float *out,
                         uint32_t *vmax = nullptr);
