@@ -380,6 +380,8 @@ __device__ __forceinline__ void mfma_gemv_i8(const uint8_t *const (&rows)[TW][4]
                                              CoreOut<UT_FMT_INT4, M, 4> (&res)[TW], Prep &&prep) {
     static_assert(M >= 1 && M <= 4, "three digit planes per row, 16 columns");
     static_assert(KC % kMfmaI8SegCols == 0, "chunks of whole segments");
+    // a segment's slot in flight is its index mod DS across chunks
+    static_assert((KC / kMfmaI8SegCols) % DS == 0, "DS divides a chunk's segments");
     constexpr int RB = mfma_row_bytes<KC>();
     // staging work items per chunk: 16-byte pieces of the 3M plane rows, or
     // 4-column groups of the M f32 rows
