@@ -601,11 +601,21 @@ struct GateUpArgs {
     int narrive = 0;
 };
 
+// UT_MOE_FOLD_COMBINE=1: fold the routed combine into down (CombineFold)
+// instead of a combine launch after it.
+#ifndef UT_MOE_FOLD_COMBINE
+#define UT_MOE_FOLD_COMBINE 0
+#endif
+// (the fold's device code is compiled in only with the switch on: its
+// argument loads and branches cost the default kernels registers)
+
 // Workgroup (0, 0) of a gate/up launch clears the next down launch's
 // arrival counters (stream order makes them zero when down starts).
 __device__ __forceinline__ void clear_arrivals(const GateUpArgs &a, int u, int tile) {
-    if (a.arrive && u == 0 && tile == 0)
-        for (int i = threadIdx.x; i < a.narrive; i += blockDim.x) a.arrive[i] = 0;
+    if constexpr (UT_MOE_FOLD_COMBINE) {
+        if (a.arrive && u == 0 && tile == 0)
+            for (int i = threadIdx.x; i < a.narrive; i += blockDim.x) a.arrive[i] = 0;
+    }
 }
 
 // plan_slot_wave for choices made in this launch whose gate and up weight
@@ -1176,11 +1186,6 @@ __global__ __launch_bounds__(kGemvThreads, M <= 2 ? 5 : 1) void k_moe_gate_up_du
 }
 
 // --------------------------------------------------------------- down ---
-// UT_MOE_FOLD_COMBINE=1: fold the routed combine into down (CombineFold)
-// instead of a combine launch after it.
-#ifndef UT_MOE_FOLD_COMBINE
-#define UT_MOE_FOLD_COMBINE 0
-#endif
 // The routed experts' combine folded into down: each workgroup of a row
 // band (one per slot) stores its d rows device-coherently and counts in at
 // arrive[band]; the one that counts last adds the band's columns of out as
@@ -1225,8 +1230,10 @@ __device__ void fold_combine(const DownArgs &a, int band, int64_t c0, int ncols)
 // through this XCD's L2), so the band's last workgroup, on any XCD, reads
 // it without a cache write-back.
 __device__ __forceinline__ void store_d(const DownArgs &a, int64_t i, float v) {
-    if (a.fold.arrive) __hip_atomic_store(a.d + i, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else a.d[i] = v;
+    if (UT_MOE_FOLD_COMBINE && a.fold.arrive)
+        __hip_atomic_store(a.d + i, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+        a.d[i] = v;
 }
 
 // The digitisation shift of h row (u, m): 22 - E with max|h| < 2^E, from the
@@ -1414,7 +1421,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_down_mfma(DownArgs a) {
     __shared__ __attribute__((aligned(16))) uint32_t lds[down_mfma_lds_words<M>()];
     __shared__ uint32_t red[4 * M];
     down_mfma_body<M>(a, blockIdx.y, blockIdx.x, lds, red);
-    if (a.fold.arrive) fold_combine<M>(a, blockIdx.x, (int64_t)blockIdx.x * 64 * down_mfma_tw<M>(),
+    if (UT_MOE_FOLD_COMBINE && a.fold.arrive) fold_combine<M>(a, blockIdx.x, (int64_t)blockIdx.x * 64 * down_mfma_tw<M>(),
                                        64 * down_mfma_tw<M>());
 }
 
@@ -1492,7 +1499,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_down_i8_mfma(DownArgs a) {
                             int_total_to_f32(res[0].S[r][m], exl[m], ld_global_f32(dsc + o)));
             }
     }
-    if (a.fold.arrive) fold_combine<M>(a, blockIdx.x, (int64_t)blockIdx.x * 64, 64);
+    if (UT_MOE_FOLD_COMBINE && a.fold.arrive) fold_combine<M>(a, blockIdx.x, (int64_t)blockIdx.x * 64, 64);
 }
 
 // The routed experts' down on the matrix cores and a shared MLP's down
@@ -1517,7 +1524,7 @@ template <int FMT, int M>
 __global__ __launch_bounds__(kGemvThreads) void k_moe_down(DownArgs a) {
     __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
     down_body<FMT, M>(a, blockIdx.y, blockIdx.x, lds);
-    if (a.fold.arrive) {
+    if (UT_MOE_FOLD_COMBINE && a.fold.arrive) {
         constexpr int DR = 16 * down_rows<M>();
         fold_combine<M>(a, blockIdx.x, (int64_t)blockIdx.x * DR, DR);
     }
