@@ -1687,7 +1687,7 @@ int32_t matmul_digits(ut_ctx *ctx, const ut_qtensor *w, const float *x, const XD
 
 int32_t matmul_digits_argmax(ut_ctx *ctx, const ut_qtensor *w, const float *x, const XDigits &xd,
                              int64_t M, float *out, int32_t *idx, void *am_scratch,
-                             const int32_t *err) {
+                             const int32_t *err, const int32_t *tail, int ntail) {
     ArgmaxParts am;
     if (!(ctx->fast_int8 && w->fmt == UT_FMT_INT8) && w->fmt != UT_FMT_F32 && fast_ok(w) &&
         M >= 1 && M <= 4) {
@@ -1709,8 +1709,8 @@ int32_t matmul_digits_argmax(ut_ctx *ctx, const ut_qtensor *w, const float *x, c
     } else {
         UT_TRY(matmul_digits(ctx, w, x, xd, M, out, w->out_dim, 0));
     }
-    if (am.v) return launch_argmax_final(ctx, out, M, w->out_dim, am, idx, err);
-    return launch_argmax(ctx, out, M, w->out_dim, w->out_dim, idx, am_scratch, err);
+    if (am.v) return launch_argmax_final(ctx, out, M, w->out_dim, am, idx, err, tail, ntail);
+    return launch_argmax(ctx, out, M, w->out_dim, w->out_dim, idx, am_scratch, err, tail, ntail);
 }
 
 int32_t matmul_dev(ut_ctx *ctx, const ut_qtensor *w, const float *x, int64_t M, float *out,

@@ -344,10 +344,10 @@ int32_t matmul_digits(ut_ctx *ctx, const ut_qtensor *w, const float *x, const XD
 // matmul_digits into out [M][out_dim], then idx [M] = each row's argmax;
 // the GEMV that finishes the rows leaves the argmax partials where it can
 // (am_scratch: argmax_scratch_bytes(M, out_dim)); err: the sticky error word
-// copied to idx[M].
+// copied to idx[M], and with it ntail ints of tail to idx[M + 1 ...].
 int32_t matmul_digits_argmax(ut_ctx *ctx, const ut_qtensor *w, const float *x, const XDigits &xd,
                              int64_t M, float *out, int32_t *idx, void *am_scratch,
-                             const int32_t *err);
+                             const int32_t *err, const int32_t *tail = nullptr, int ntail = 0);
 int32_t matmul_dev(ut_ctx *ctx, const ut_qtensor *w, const float *x, int64_t M, float *out,
                    int64_t ldo, int accumulate, void *digit_scratch);
 

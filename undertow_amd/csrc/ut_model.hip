@@ -380,7 +380,7 @@ int32_t ws_reserve(ut_session *s, int64_t rows) {
     size_t iqabs = F(R * heads * Lr), iqrope = F(R * heads * c.qk_rope_head_dim + 1);
     size_t iclat = F(R * heads * Lr), ictx = F(R * heads * c.v_head_dim);
     size_t ilog = F(R * c.vocab_size), iemb = F(R * H), icat = F(R * 2 * H);
-    size_t irl = F(4 * E), irw = F(4 * k), irid = F(4 * k), iids = F(R), iam = F(R + 1), ierr = F(1);
+    size_t irl = F(4 * E), irw = F(4 * k), irid = F(4 * k), iids = F(R), iam = F(2 * R + 1), ierr = F(1);
     size_t ivids = F(8);
     size_t ivmax = F(R * absorb_v_parts(heads, c.v_head_dim)), ivexp = F(R);
     size_t idig = plan.add(matmul_digit_bytes(R, kmax));
@@ -1119,10 +1119,16 @@ int32_t prefill_dev(ut_session *s, const int32_t *ids, int64_t n, const int32_t 
     if (!fuse || nl == 0)
         UT_TRY(norm_dig(s, w.x, H, m->final_norm, H, n, w.normed, H, w.digA,
                         dig_flags({m->lm_head}), &fd));
-    // the argmax rows, then the sticky error word at am[n] (one readback)
-    if (n <= 4) return matmul_digits_argmax(ctx, m->lm_head, w.normed, fd, n, w.logits, w.am, w.argm, w.err);
+    // the argmax rows, then the sticky error word at am[n] and, with device
+    // ids (a verify step), the rows' ids past the first (its drafts) at
+    // am[n + 1 ...]: one readback carries them all
+    const int32_t *tail = ids_dev ? ids_dev + 1 : nullptr;
+    const int ntail = ids_dev ? (int)(n - 1) : 0;
+    if (n <= 4)
+        return matmul_digits_argmax(ctx, m->lm_head, w.normed, fd, n, w.logits, w.am, w.argm,
+                                    w.err, tail, ntail);
     UT_TRY(matmul_digits(ctx, m->lm_head, w.normed, fd, n, w.logits, V, 0));
-    return launch_argmax(ctx, w.logits, n, V, V, w.am, w.argm, w.err);
+    return launch_argmax(ctx, w.logits, n, V, V, w.am, w.argm, w.err, tail, ntail);
 }
 
 int32_t read_argmax(ut_session *s, int64_t n, int32_t *out) {
@@ -1140,18 +1146,18 @@ int32_t read_argmax(ut_session *s, int64_t n, int32_t *out) {
 // sticky error flag into the session's pinned readback slot; `ready` is
 // recorded behind them, so later launches need not wait for the host.
 // How the flag comes back (err): RB_ERR_COPY in a copy of its own,
-// RB_ERR_INLINE as dev[n] (the argmax rows of prefill_dev carry it), RB_ERR_LATER
-// not with this readback (a later one of the same wait carries it).
-enum { RB_ERR_COPY, RB_ERR_INLINE, RB_ERR_LATER };
+// RB_ERR_INLINE as dev[n] (the argmax rows of prefill_dev carry it, and
+// after it a verify step's drafts: extra).
+enum { RB_ERR_COPY, RB_ERR_INLINE };
 int32_t readback_enqueue(ut_session *s, const int32_t *dev, int64_t n, int64_t slot_off = 0,
-                         int err = RB_ERR_COPY) {
+                         int err = RB_ERR_COPY, int64_t extra = 0) {
     ut_ctx *ctx = s->ctx;
     int32_t *back = s->pin + kPinIds;
-    if (slot_off + n + 1 > kPinBack - 1) {
-        set_error(ctx, "readback of %lld ints exceeds the staging slot", (long long)n);
+    if (slot_off + n + 1 + extra > kPinBack - 1) {
+        set_error(ctx, "readback of %lld ints exceeds the staging slot", (long long)(n + extra));
         return UT_ERR_ARG;
     }
-    const int64_t cnt = err == RB_ERR_INLINE ? n + 1 : n;
+    const int64_t cnt = (err == RB_ERR_INLINE ? n + 1 : n) + extra;
     UT_CHECK_HIP(ctx, hipMemcpyAsync(back + slot_off, dev, (size_t)cnt * 4, hipMemcpyDeviceToHost, ctx->stream));
     if (err == RB_ERR_COPY) {
         UT_CHECK_HIP(ctx, hipMemcpyAsync(back + kPinBack - 1, s->ws.err, 4, hipMemcpyDeviceToHost, ctx->stream));
@@ -1159,7 +1165,7 @@ int32_t readback_enqueue(ut_session *s, const int32_t *dev, int64_t n, int64_t s
     } else if (err == RB_ERR_INLINE) {
         s->err_slot = slot_off + n;
     }
-    if (err != RB_ERR_LATER) UT_CHECK_HIP(ctx, hipEventRecord(s->ready, ctx->stream));
+    UT_CHECK_HIP(ctx, hipEventRecord(s->ready, ctx->stream));
     return UT_OK;
 }
 
@@ -1913,8 +1919,9 @@ int64_t gen_spec(ut_model *m, const int32_t *prompt, int64_t n, int32_t depth, u
             break;
         }
         if (rc) break;
-        if (!draft_fn) rc = readback_enqueue(s, s->ws.vids + 1, depth, depth + 2, RB_ERR_LATER);
-        if (rc == UT_OK) rc = readback_enqueue(s, s->ws.am, depth + 1, 0, RB_ERR_INLINE);
+        // the verify's argmax rows, the flag and (after them, at depth + 2)
+        // its drafts in one copy
+        rc = readback_enqueue(s, s->ws.am, depth + 1, 0, RB_ERR_INLINE, draft_fn ? 0 : depth);
         if (rc == UT_OK) rc = readback_wait(s, depth + 1, am.data(), 0);
         if (rc) break;
         verified = true;

@@ -39,7 +39,8 @@ __global__ __launch_bounds__(256) void k_argmax_final(const float *__restrict__ 
                                                       int64_t nparts, const float *__restrict__ pv,
                                                       const int32_t *__restrict__ pi,
                                                       int32_t *__restrict__ idx,
-                                                      const int32_t *__restrict__ err) {
+                                                      const int32_t *__restrict__ err,
+                                                      const int32_t *__restrict__ tail, int ntail) {
     const int64_t row = blockIdx.x;
     Best b{0.0f, -1};
     // 16 partials per thread per round, every load of a round issued first
@@ -60,6 +61,10 @@ __global__ __launch_bounds__(256) void k_argmax_final(const float *__restrict__ 
         idx[row] = (x0 != x0 || b.i < 0) ? 0 : b.i;
         if (err && row == (int64_t)gridDim.x - 1) idx[gridDim.x] = *err;
     }
+    // after the error word, ntail ints of tail (a verify step's draft ids),
+    // so that one readback carries all three
+    if (err && tail && row == (int64_t)gridDim.x - 1 && (int)threadIdx.x < ntail)
+        idx[gridDim.x + 1 + threadIdx.x] = tail[threadIdx.x];
 }
 
 size_t argmax_scratch_bytes(int64_t rows, int64_t V) {
@@ -81,11 +86,16 @@ ArgmaxParts argmax_parts_view(void *scratch, int64_t rows, int64_t stride) {
 }
 
 int32_t launch_argmax_final(ut_ctx *ctx, const float *x, int64_t rows, int64_t ldx,
-                            const ArgmaxParts &p, int32_t *idx, const int32_t *err) {
+                            const ArgmaxParts &p, int32_t *idx, const int32_t *err,
+                            const int32_t *tail, int ntail) {
     if (rows <= 0) return UT_OK;
+    if (ntail < 0 || ntail > 256) {
+        set_error(ctx, "argmax: %d tail ints (at most 256)", ntail);
+        return UT_ERR_ARG;
+    }
     int tok = timing_begin(ctx, "argmax_final");
     hipLaunchKernelGGL(k_argmax_final, dim3((unsigned)rows), dim3(256), 0, ctx->stream, x, ldx,
-                       p.stride, p.v, p.i, idx, err);
+                       p.stride, p.v, p.i, idx, err, tail, ntail);
     timing_end(ctx, tok);
     return launch_check(ctx, "k_argmax_final");
 }
@@ -98,7 +108,8 @@ int64_t argmax_parts(int64_t V) {
 }
 
 int32_t launch_argmax(ut_ctx *ctx, const float *x, int64_t rows, int64_t V, int64_t ldx,
-                      int32_t *idx, void *scratch, const int32_t *err) {
+                      int32_t *idx, void *scratch, const int32_t *err, const int32_t *tail,
+                      int ntail) {
     if (rows <= 0) return UT_OK;
     const int64_t parts = argmax_parts(V);
     const int64_t chunk = (V + parts - 1) / parts;
@@ -108,7 +119,7 @@ int32_t launch_argmax(ut_ctx *ctx, const float *x, int64_t rows, int64_t V, int6
                        ctx->stream, x, V, ldx, chunk, p.v, p.i);
     UT_TRY(launch_check(ctx, "k_argmax_partial"));
     timing_end(ctx, tok);
-    return launch_argmax_final(ctx, x, rows, ldx, p, idx, err);
+    return launch_argmax_final(ctx, x, rows, ldx, p, idx, err, tail, ntail);
 }
 
 }  // namespace ut
