@@ -11,7 +11,7 @@ import json
 import numpy as np
 import pytest
 
-from models import C1, C1_E256, C1_MLA, checkpoint, gpu_model, prompt_ids
+from models import C1, C1_E256, C1_MLA, C1_MLA_V40, checkpoint, gpu_model, prompt_ids
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -106,6 +106,23 @@ def test_c1_mla_mtp_verify_rows(c1_mla, depth):
     toks, drafted, accepted = m.generate_mtp(prompt, 16, depth=depth)
     assert toks == m.generate_greedy(prompt, 16) == om.greedy_decode(prompt, 16)[16:]
     assert drafted > 0 and 0 <= accepted <= drafted
+
+
+def test_c1_mla_value_head_tail(ctx):
+    """A 40-dim value head (not a multiple of the absorbed V's 16 rows per
+    workgroup): logits against the oracle, and one-row decode, two- and
+    four-row verify streams equal to the oracle's greedy stream."""
+    ck = checkpoint(C1_MLA_V40, fmt="int4")
+    m, om = gpu_model(ctx, ck), O.Model(ck)
+    prompt = prompt_ids(16, C1_MLA_V40["vocab_size"], seed=5)
+    got, want = m.forward(prompt), om.forward(prompt)
+    err = np.abs(got - want)
+    assert err.max() <= 1e-3 and err.mean() <= 1e-4, (err.max(), err.mean())
+    stream = om.greedy_decode(prompt, 12)[16:]
+    assert m.generate_greedy(prompt, 12) == stream
+    for depth in (1, 3):
+        toks, drafted, accepted = m.generate_mtp(prompt, 12, depth=depth)
+        assert toks == stream and drafted > 0
 
 
 @pytest.mark.parametrize("which", ["c1", "c1_mla"])
