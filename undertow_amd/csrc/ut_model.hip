@@ -1896,13 +1896,11 @@ int64_t gen_spec(ut_model *m, const int32_t *prompt, int64_t n, int32_t depth, u
             s->mtp_fed = pos;
             // ---- chained drafts (depth > 1): MTP layer on its own last output row
             for (int32_t j = 1; j < depth && rc == UT_OK; j++) {
-                // the MTP layer's output row for the last fed position is in ws.x
-                // (staged in ws.attn, which is free between layers)
+                // the MTP layer's output row for the last fed position is in
+                // ws.x: the draft's first launch reads it (into its own input
+                // rows) before anything of the draft writes ws.x
                 const int64_t last = (j == 1 ? pending : 1) - 1;
-                rc = hipMemcpyAsync(s->ws.attn, s->ws.x + last * H, (size_t)H * 4,
-                                    hipMemcpyDeviceToDevice, ctx->stream) == hipSuccess
-                         ? UT_OK : UT_ERR_HIP;
-                if (rc == UT_OK) rc = draft_rows_dev(s, nullptr, j, s->ws.attn, 1, 1 + j);
+                rc = draft_rows_dev(s, nullptr, j, s->ws.x + last * H, 1, 1 + j);
             }
             s->mtp_kv.len = s->mtp_fed;  // speculative MTP rows are never kept
             if (rc) break;
