@@ -451,7 +451,6 @@ constexpr int kMlaMaxSlices = 256;
 // NT < 1024 (fewer, busier threads) lets more rows' workgroups share a CU.
 constexpr int kCombineParts = 16;
 constexpr int kCombineSmallSlices = 64;
-constexpr int64_t kCombineOneWgPerCu = 256;  // workgroups: one per CU
 #ifndef UT_MLA_COMBINE_SMALL_NT
 #define UT_MLA_COMBINE_SMALL_NT 256
 #endif
@@ -651,7 +650,7 @@ int32_t launch_mla_attend_kc(ut_ctx *ctx, const float *qabs, const float *qrope,
     // up to 64 slices: 256-thread workgroups once the grid exceeds one per
     // CU (config-4 verify of four rows: 15.2 -> 7.4 us per combine; at one
     // row the 1,024-thread form is 0.2 us faster)
-    if (a.nslice <= kCombineSmallSlices && (int64_t)cgrid.x * cgrid.y > kCombineOneWgPerCu)
+    if (a.nslice <= kCombineSmallSlices && (int64_t)cgrid.x * cgrid.y > ctx->multiprocessors)
         hipLaunchKernelGGL((k_mla_combine_mfma<kCombineSmallSlices, UT_MLA_COMBINE_SMALL_NT>), cgrid,
                            dim3(UT_MLA_COMBINE_SMALL_NT), 0, ctx->stream, a.part_m, a.part_l,
                            a.part_o, (int)RH, (int)H, (int)L, a.pos, clat);
