@@ -236,6 +236,28 @@ def test_moe_int8_matrix_core_shapes(ctx, H, I):
             assert np.array_equal(one[0], got[s]), (M, s)
 
 
+def test_moe_one_slot_int8_split_down(ctx):
+    """A one-slot int8 MLP (every row on one expert: the dense FFN's form)
+    at hidden 7168, inter 10240: at 2-4 rows gate/up runs on the matrix
+    cores and down splits K into five 2,048-column slices on the matrix
+    cores, whose exact partials the finish launch sums; each row equals a
+    one-row call (dot-product kernels) bit for bit, and the oracle."""
+    rng = np.random.default_rng(77)
+    E, H, I, k = 1, 7168, 10240, 1
+    tbl, host_w = make_experts(ctx, rng, INT8, E, H, I)
+    for M in (2, 3, 4):
+        ids = np.zeros((M, k), np.int32)
+        w = rng.random((M, k)).astype(np.float32)
+        x = rng.standard_normal((M, H)).astype(np.float32)
+        got = host(tbl.moe_experts(dev(ids), dev(w), dev(x)))
+        want = oracle_moe(INT8, H, I, host_w, ids, w, x)
+        tol = 1e-4 * np.maximum(np.abs(want), 1.0)
+        assert (np.abs(got - want) <= tol).all(), (M, np.abs(got - want).max())
+        for s in range(M):
+            one = host(tbl.moe_experts(dev(ids[s:s + 1]), dev(w[s:s + 1]), dev(x[s:s + 1])))
+            assert np.array_equal(one[0], got[s]), (M, s)
+
+
 @pytest.mark.parametrize("fmt,Ms", [(INT4, (1, 2, 4)), (INT8, (1, 2, 3, 4))])
 def test_moe_experts_deepseek_shape(ctx, fmt, Ms):
     """hidden 7168, inter 2048, top-8 of 16 loaded experts
