@@ -749,9 +749,9 @@ template <int M> constexpr int gemv_i8_mfma_tw() { return UT_GEMV_I8_MFMA_TW; }
 template <int M> constexpr int gemv_i8_mfma_kc() { return M <= 2 ? 4096 : UT_GEMV_I8_MFMA_KC4; }
 template <int M> constexpr int gemv_i8_mfma_depth() { return UT_GEMV_I8_MFMA_DEPTH; }
 
-template <int M, bool F32X>
+template <int M, bool F32X, int TW = gemv_i8_mfma_tw<M>()>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv_mfma_i8(PlainArgs a) {
-    constexpr int TW = gemv_i8_mfma_tw<M>(), KC = gemv_i8_mfma_kc<M>();
+    constexpr int KC = gemv_i8_mfma_kc<M>();
     __shared__ __attribute__((aligned(16))) uint8_t lds[mfma_i8_lds_bytes<M, KC>()];
     __shared__ __attribute__((aligned(16))) uint8_t wareas[4 * TW * kMfmaI8WaveAreaBytes];
     __shared__ uint32_t redm[4 * M];
@@ -1255,9 +1255,18 @@ template <int M, bool F32X> static int64_t gemv_i8_mfma_resident(ut_ctx *ctx) {
     return (int64_t)n * ctx->multiprocessors;
 }
 
-template <int M, bool F32X>
+// Weights of at least this many rows (the LM head) take two 16-row tiles
+// per wave: half the activation staging per weight byte (config-4 four-row
+// LM head 166.8 -> 161.3 us); the other launches keep one (fewer, fatter
+// workgroups measured slower there).
+constexpr int64_t kI8MfmaWideRows = 65536;
+
+template <int M, bool F32X, int TW = gemv_i8_mfma_tw<M>()>
 static int32_t launch_i8_mfma_m(ut_ctx *ctx, const GemvArgs &ga, PlainArgs a, int64_t m0) {
-    constexpr int rows_per_wg = 64 * gemv_i8_mfma_tw<M>();
+    if constexpr (!F32X && TW == 1) {
+        if (a.O >= kI8MfmaWideRows) return launch_i8_mfma_m<M, F32X, 2>(ctx, ga, a, m0);
+    }
+    constexpr int rows_per_wg = 64 * TW;
     // a launch that reduces the producer's partial maxima pays that in every
     // workgroup: half as many splits, as for k_gemv
     const int64_t resident = gemv_i8_mfma_resident<M, F32X>(ctx) / (F32X ? 2 : 1);
@@ -1282,7 +1291,7 @@ static int32_t launch_i8_mfma_m(ut_ctx *ctx, const GemvArgs &ga, PlainArgs a, in
     argmax_plan(ga, a, m0, M, grid.x);
     const char *name = "gemv_int8_mfma";
     int tok = timing_begin(ctx, name);
-    hipLaunchKernelGGL((k_gemv_mfma_i8<M, F32X>), grid, dim3(kGemvThreads), 0, ctx->stream, a);
+    hipLaunchKernelGGL((k_gemv_mfma_i8<M, F32X, TW>), grid, dim3(kGemvThreads), 0, ctx->stream, a);
     if (a.ks > 1) UT_TRY(splitk_finish<UT_FMT_INT8>(ctx, ga, a, m0, M, name));
     timing_end(ctx, tok);
     return launch_check(ctx, name);
