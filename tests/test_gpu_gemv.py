@@ -23,7 +23,8 @@ pytestmark = pytest.mark.gpu
 
 SHAPES = [(1, 1), (3, 16), (5, 17), (8, 64), (7, 130), (16, 256), (2, 31),  # avx512.rs:335-366
           (96, 256), (256, 512), (64, 128), (2048, 7168), (7168, 2048), (192, 96), (1536, 7168),
-          (256, 7168), (576, 7168), (96, 16384)]  # split-K shapes: router, kv_a, o_proj-like
+          (256, 7168), (576, 7168), (96, 16384),  # split-K shapes: router, kv_a, o_proj-like
+          (65600, 256)]  # >= 65,536 rows: int8 at 3-4 rows takes two tiles per wave, ragged last tile
 FMTS = [INT4, INT8, F32]
 
 
@@ -60,7 +61,7 @@ def test_matmul_matches_oracle(ctx, fmt, o, i):
 
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("o,i", [(2048, 7168), (7168, 2048), (130, 64), (5, 17), (256, 7168),
-                                 (7168, 16384), (1000, 192)])
+                                 (7168, 16384), (1000, 192), (65600, 256)])
 def test_rows_do_not_depend_on_seq(ctx, fmt, o, i):
     rng = np.random.default_rng(7)
     payload, scales = rand_qtensor(rng, fmt, o, i)
