@@ -508,7 +508,8 @@ HEADS_CHECKED = [0, 1, 31, 32, 63, 64, 100, 127]
 @pytest.mark.parametrize("R,T", [(1, 32768), (2, 32768), (4, 32768), (4, 16400), (3, 16385)])
 def test_mla_long_context_matches_oracle(ctx, R, T):
     """Config 3's longest context: past 16384 positions the matrix-core
-    kernel takes 256-position slices and (T+255)/256 of them per row.  All
+    kernel's slices grow past 256 positions (512 at 32768, 61 slices of 272
+    at 16400).  All
     128 heads run on the GPU; the oracle's sequential loops check eight of
     them (its (row, head) pairs are independent)."""
     import undertow_amd as U

@@ -189,13 +189,21 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 
 // Slice length of a row that sees n_ctx positions: about n_ctx/64 in whole
-// 16-position tiles, at least 32 and at most 256 (so at most 64 slices up
-// to 16384 positions, n_ctx/256 beyond).  A function of n_ctx alone, so a
-// row's result does not depend on which rows share the call; no power-of-two
-// steps, so neighbouring context lengths get similar slice counts.
+// 16-position tiles, at least 32 and at most UT_MLA_SLICE_CAP = 512 (so at
+// most 64 slices up to 32768 positions, n_ctx/512 beyond).  A function of
+// n_ctx alone, so a row's result does not depend on which rows share the
+// call; no power-of-two steps, so neighbouring context lengths get similar
+// slice counts.  The cap of 512 against 256 halves the slice partials past
+// 16384 positions: at T = 32768 two- and four-row calls went from 97.2 to
+// 88.0 us and from 179.3 to 154.6 us, one-row calls from 56.6 to 61.1 us
+// (256 workgroups, one per CU).  Verify rows outnumber single rows in
+// speculative decoding (every main-model layer of a round), so 512.
+#ifndef UT_MLA_SLICE_CAP
+#define UT_MLA_SLICE_CAP 512
+#endif
 __host__ __device__ inline int64_t mla_mfma_slice(int64_t n_ctx) {
     const int64_t s = (n_ctx + 1023) / 1024 * 16;
-    return s < 32 ? 32 : s > 256 ? 256 : s;
+    return s < 32 ? 32 : s > UT_MLA_SLICE_CAP ? UT_MLA_SLICE_CAP : s;
 }
 
 __device__ __forceinline__ void split8(const float (&x)[8], bf16x8_t &hi, bf16x8_t &lo) {
@@ -574,8 +582,8 @@ __global__ __launch_bounds__(NT) void k_mla_combine_mfma(const float *__restrict
 // bound: slices past a row's count exit at once).
 static int64_t mla_mfma_nslice(int64_t T) {
     if (T <= 2048) return (T + 31) / 32;  // 32-position slices
-    if (T <= 16384) return 64;            // length >= n/64
-    return (T + 255) / 256;               // 256-position slices
+    if (T <= 64 * UT_MLA_SLICE_CAP) return 64;  // length >= n/64
+    return (T + UT_MLA_SLICE_CAP - 1) / UT_MLA_SLICE_CAP;  // slices of the cap
 }
 
 static bool mla_mfma_ok(int64_t H, int64_t L, int64_t P, int64_t T) {
